@@ -1,0 +1,241 @@
+// C ABI of libgguf_hip (declared in include/gguf_hip.h).
+//
+// Every entry point validates its arguments before touching HIP, so the
+// error paths (unsupported type, block-size mismatch, byte-length mismatch,
+// null or misaligned pointers) behave identically with or without a GPU.
+// Error texts follow the reference's throws: gguf.ts:75-79,85-87,
+// gguf-dequant.ts:678-680,837, forward-pass.ts:1486-1489,1524.
+#include <stdarg.h>
+#include <stdio.h>
+
+#include "common.hpp"
+#include "gguf_hip.h"
+
+namespace {
+
+thread_local char g_err[512] = "";
+
+int fail(int code, const char *fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+int ok() {
+  g_err[0] = '\0';
+  return GGUF_HIP_OK;
+}
+
+// gguf.ts:39-73
+bool traits(int t, int *block, int *size) {
+  static const int tbl[][3] = {
+      {0, 1, 4},     {1, 1, 2},     {30, 1, 2},    {24, 1, 1},    {25, 1, 2},    {26, 1, 4},
+      {27, 1, 8},    {28, 1, 8},    {2, 32, 18},   {3, 32, 20},   {6, 32, 22},   {7, 32, 24},
+      {8, 32, 34},   {9, 32, 36},   {10, 256, 84}, {11, 256, 110}, {12, 256, 144}, {13, 256, 176},
+      {14, 256, 210}, {15, 256, 292}, {16, 256, 66}, {17, 256, 74}, {18, 256, 98},  {19, 256, 50},
+      {20, 32, 18},  {21, 256, 110}, {22, 256, 82}, {23, 256, 136}, {29, 256, 56}};
+  for (const auto &e : tbl)
+    if (e[0] == t) {
+      *block = e[1];
+      *size = e[2];
+      return true;
+    }
+  return false;
+}
+
+bool kernel_type(int t) { return t == GGUF_HIP_Q8_0 || t == GGUF_HIP_Q4_K || t == GGUF_HIP_Q6_K; }
+
+int check_type(int t) {
+  int b, s;
+  if (!traits(t, &b, &s)) return fail(GGUF_HIP_ERR_TYPE, "[GGUF] Unsupported ggml type %d", t);
+  if (!kernel_type(t))
+    return fail(GGUF_HIP_ERR_TYPE, "[gguf-hip] no kernel for ggml type %d", t);
+  return GGUF_HIP_OK;
+}
+
+int check_k(int t, int64_t k) {
+  int b, s;
+  traits(t, &b, &s);
+  if (k <= 0 || k % b != 0)
+    return fail(GGUF_HIP_ERR_SHAPE, "[GGUF] ne[0]=%lld not divisible by block size %d for type %d",
+                (long long)k, b, t);
+  if (k > (int64_t)1 << 30)
+    return fail(GGUF_HIP_ERR_SHAPE, "[gguf-hip] K=%lld too large", (long long)k);
+  return GGUF_HIP_OK;
+}
+
+int64_t tile_row_bytes(int t, int64_t k) {
+  int b, s;
+  traits(t, &b, &s);
+  const int64_t nb = k / b;
+  if (t == GGUF_HIP_Q4_K) return 144 * nb;
+  return (s * nb + 15) & ~(int64_t)15;
+}
+
+bool aligned(const void *p, uintptr_t a) { return ((uintptr_t)p % a) == 0; }
+
+int hip_status(hipError_t e, const char *what) {
+  if (e != hipSuccess)
+    return fail(GGUF_HIP_ERR_HIP, "[gguf-hip] %s: %s", what, hipGetErrorString(e));
+  return ok();
+}
+
+}  // namespace
+
+extern "C" {
+
+int gguf_hip_abi_version(void) { return GGUF_HIP_ABI_VERSION; }
+
+const char *gguf_hip_last_error(void) { return g_err; }
+
+int gguf_hip_type_traits(int ggml_type, int *block_elems, int *type_size) {
+  int b, s;
+  if (!traits(ggml_type, &b, &s))
+    return fail(GGUF_HIP_ERR_TYPE, "[GGUF] Unsupported ggml type %d", ggml_type);
+  if (block_elems) *block_elems = b;
+  if (type_size) *type_size = s;
+  return ok();
+}
+
+int64_t gguf_hip_raw_bytes(int ggml_type, int64_t n_rows, int64_t k) {
+  int b, s;
+  if (!traits(ggml_type, &b, &s))
+    return fail(GGUF_HIP_ERR_TYPE, "[GGUF] Unsupported ggml type %d", ggml_type);
+  if (k <= 0 || k % b != 0)
+    return fail(GGUF_HIP_ERR_SHAPE, "[GGUF] ne[0]=%lld not divisible by block size %d for type %d",
+                (long long)k, b, ggml_type);
+  if (n_rows < 0) return fail(GGUF_HIP_ERR_SHAPE, "[gguf-hip] negative row count");
+  ok();
+  return n_rows * (k / b) * s;
+}
+
+int64_t gguf_hip_tile_bytes(int ggml_type, int64_t n_rows, int64_t k) {
+  int rc = check_type(ggml_type);
+  if (rc) return rc;
+  if ((rc = check_k(ggml_type, k))) return rc;
+  if (n_rows < 0) return fail(GGUF_HIP_ERR_SHAPE, "[gguf-hip] negative row count");
+  ok();
+  return n_rows * tile_row_bytes(ggml_type, k);
+}
+
+int gguf_hip_repack(const void *raw, int64_t raw_bytes, int ggml_type, int64_t n_rows, int64_t k,
+                    void *tiles, int64_t tile_bytes, void *stream) {
+  int rc = check_type(ggml_type);
+  if (rc) return rc;
+  if ((rc = check_k(ggml_type, k))) return rc;
+  if (n_rows < 0) return fail(GGUF_HIP_ERR_SHAPE, "[gguf-hip] negative row count");
+  int b, s;
+  traits(ggml_type, &b, &s);
+  const int64_t want_raw = n_rows * (k / b) * s;
+  if (raw_bytes != want_raw)
+    return fail(GGUF_HIP_ERR_BYTES, "[repackGGUF] byteLength %lld != expected %lld",
+                (long long)raw_bytes, (long long)want_raw);
+  const int64_t trb = tile_row_bytes(ggml_type, k);
+  if (tile_bytes != n_rows * trb)
+    return fail(GGUF_HIP_ERR_BYTES, "[repackGGUF] output byteLength %lld != expected %lld",
+                (long long)tile_bytes, (long long)(n_rows * trb));
+  if (n_rows == 0) return ok();
+  if (!raw || !tiles) return fail(GGUF_HIP_ERR_NULL, "[gguf-hip] null pointer");
+  if (!aligned(tiles, 16))
+    return fail(GGUF_HIP_ERR_ALIGN, "[gguf-hip] tile buffer must be 16-byte aligned");
+  return hip_status(gguf::launch_repack((const uint8_t *)raw, ggml_type, n_rows, k,
+                                        (uint8_t *)tiles, trb, (hipStream_t)stream),
+                    "repack launch");
+}
+
+int gguf_hip_dequant(const void *tiles, int ggml_type, int64_t n_rows, int64_t k, float *out,
+                     int64_t ldo, void *stream) {
+  int rc = check_type(ggml_type);
+  if (rc) return rc;
+  if ((rc = check_k(ggml_type, k))) return rc;
+  if (n_rows < 0) return fail(GGUF_HIP_ERR_SHAPE, "[gguf-hip] negative row count");
+  if (n_rows > 1 && ldo < k) return fail(GGUF_HIP_ERR_SHAPE, "[gguf-hip] ldo < K");
+  if (n_rows == 0) return ok();
+  if (!tiles || !out) return fail(GGUF_HIP_ERR_NULL, "[gguf-hip] null pointer");
+  if (!aligned(tiles, 16))
+    return fail(GGUF_HIP_ERR_ALIGN, "[gguf-hip] tile buffer must be 16-byte aligned");
+  if (!aligned(out, 4)) return fail(GGUF_HIP_ERR_ALIGN, "[gguf-hip] output must be 4-byte aligned");
+  return hip_status(gguf::launch_dequant((const uint8_t *)tiles, ggml_type, n_rows, k,
+                                         tile_row_bytes(ggml_type, k), out, ldo,
+                                         (hipStream_t)stream),
+                    "dequant launch");
+}
+
+int gguf_hip_dequant_raw(const void *raw, int ggml_type, int64_t n_elems, float *out,
+                         void *stream) {
+  int rc = check_type(ggml_type);
+  if (rc) return rc;
+  int b, s;
+  traits(ggml_type, &b, &s);
+  if (n_elems < 0 || n_elems % b != 0)
+    return fail(GGUF_HIP_ERR_SHAPE, "[GGUF] n=%lld not divisible by %d", (long long)n_elems, b);
+  if (n_elems == 0) return ok();
+  if (!raw || !out) return fail(GGUF_HIP_ERR_NULL, "[gguf-hip] null pointer");
+  if (!aligned(out, 4)) return fail(GGUF_HIP_ERR_ALIGN, "[gguf-hip] output must be 4-byte aligned");
+  return hip_status(
+      gguf::launch_dequant_raw((const uint8_t *)raw, ggml_type, n_elems, out, (hipStream_t)stream),
+      "dequant_raw launch");
+}
+
+int gguf_hip_matmul_variant(const void *x, int x_type, int64_t ldx, const void *tiles,
+                            int ggml_type, int64_t n, int64_t k, float *y, int64_t ldy, int64_t m,
+                            int variant, void *stream) {
+  int rc = check_type(ggml_type);
+  if (rc) return rc;
+  if ((rc = check_k(ggml_type, k))) return rc;
+  if (x_type != GGUF_HIP_F32 && x_type != GGUF_HIP_F16)
+    return fail(GGUF_HIP_ERR_DTYPE, "[gguf-hip] activations must be f32 (0) or f16 (1), got %d",
+                x_type);
+  if (variant < GGUF_HIP_VARIANT_AUTO || variant > GGUF_HIP_VARIANT_GEMM)
+    return fail(GGUF_HIP_ERR_SHAPE, "[gguf-hip] unknown kernel variant %d", variant);
+  if (m < 0 || n < 0) return fail(GGUF_HIP_ERR_SHAPE, "[gguf-hip] negative M or N");
+  if (n > ((int64_t)1 << 30) || m > ((int64_t)1 << 30))
+    return fail(GGUF_HIP_ERR_SHAPE, "[gguf-hip] M or N too large");
+  if (m > 1 && ldx < k) return fail(GGUF_HIP_ERR_SHAPE, "[gguf-hip] ldx < K");
+  if (m > 1 && ldy < n) return fail(GGUF_HIP_ERR_SHAPE, "[gguf-hip] ldy < N");
+  if (variant == GGUF_HIP_VARIANT_SKINNY && m > 32)
+    return fail(GGUF_HIP_ERR_SHAPE, "[gguf-hip] skinny variant needs M <= 32, got %lld",
+                (long long)m);
+  if (m == 0 || n == 0) return ok();
+  if (!x || !tiles || !y) return fail(GGUF_HIP_ERR_NULL, "[gguf-hip] null pointer");
+  const int64_t esize = x_type == GGUF_HIP_F32 ? 4 : 2;
+  if (!aligned(tiles, 16))
+    return fail(GGUF_HIP_ERR_ALIGN, "[gguf-hip] weight buffer must be 16-byte aligned");
+  if (!aligned(x, 16) || (m > 1 && (ldx * esize) % 16 != 0))
+    return fail(GGUF_HIP_ERR_ALIGN, "[gguf-hip] activation rows must be 16-byte aligned");
+  if (!aligned(y, 4)) return fail(GGUF_HIP_ERR_ALIGN, "[gguf-hip] output must be 4-byte aligned");
+
+  const int64_t trb = tile_row_bytes(ggml_type, k);
+  const hipStream_t s = (hipStream_t)stream;
+  if (variant == GGUF_HIP_VARIANT_AUTO)
+    variant = m == 1 ? GGUF_HIP_VARIANT_GEMV
+                     : (m <= 32 ? GGUF_HIP_VARIANT_SKINNY : GGUF_HIP_VARIANT_GEMM);
+  hipError_t e = hipSuccess;
+  if (variant == GGUF_HIP_VARIANT_GEMV) {
+    const char *xb = (const char *)x;
+    for (int64_t m0 = 0; m0 < m && e == hipSuccess; m0 += 65535) {
+      const int64_t mc = (m - m0) < 65535 ? (m - m0) : 65535;
+      e = gguf::launch_gemv(xb + m0 * ldx * esize, x_type, ldx, (const uint8_t *)tiles, ggml_type,
+                            n, k, trb, y + m0 * ldy, ldy, mc, s);
+    }
+  } else {
+    const char *xb = (const char *)x;
+    const int64_t chunk = (int64_t)65535 * 32;  // grid.y cap at the smallest BM
+    for (int64_t m0 = 0; m0 < m && e == hipSuccess; m0 += chunk) {
+      const int64_t mc = (m - m0) < chunk ? (m - m0) : chunk;
+      e = gguf::launch_mfma(xb + m0 * ldx * esize, x_type, ldx, (const uint8_t *)tiles, ggml_type,
+                            n, k, trb, y + m0 * ldy, ldy, mc, variant == GGUF_HIP_VARIANT_SKINNY, s);
+    }
+  }
+  return hip_status(e, "matmul launch");
+}
+
+int gguf_hip_matmul(const void *x, int x_type, int64_t ldx, const void *tiles, int ggml_type,
+                    int64_t n, int64_t k, float *y, int64_t ldy, int64_t m, void *stream) {
+  return gguf_hip_matmul_variant(x, x_type, ldx, tiles, ggml_type, n, k, y, ldy, m,
+                                 GGUF_HIP_VARIANT_AUTO, stream);
+}
+
+}  // extern "C"

@@ -1,0 +1,125 @@
+"""GGML type ids, block traits and the HBM row layout of quantized weights.
+
+Type ids and (block elements, block bytes) follow the GGUF spec as the
+reference tabulates it in ``webgpu/src/model/gguf.ts:24-35`` (``GGML_TYPES``)
+and ``:39-73`` (``TYPE_TRAITS``); ``ggml_type_traits`` and
+``ggml_tensor_bytes`` mirror ``gguf.ts:75-92`` including their errors.
+
+The HBM row layout is this library's own (the reference pads blocks to 4-byte
+strides for WGSL, ``gguf-dequant.ts:655-672``; here rows are split into
+16-byte-aligned planes so kernels can issue 128-bit loads).  A weight of
+``N`` rows by ``K`` columns is stored as ``N`` consecutive rows of
+``tile_row_bytes(type, K)`` bytes each.  Row ``n`` holds the ``K/block``
+blocks of GGUF row ``n`` (row-major weight layout, ``matmul_gguf.wgsl:5-8``):
+
+* Q8_0 (32 elements / 34 B):  ``qs[K]`` int8 | ``d[K/32]`` f16 | pad to 16 B
+* Q4_K (256 elements / 144 B): the raw superblocks, unchanged
+  (``d, dmin`` f16 | ``scales[12]`` | ``qs[128]``); 144 is a multiple of 16
+* Q6_K (256 elements / 210 B): ``ql[K/2]`` | ``qh[K/4]`` | ``sc[K/16]`` int8 |
+  ``d[K/256]`` f16 | pad to 16 B; within each plane, superblock ``b`` owns
+  the bytes ``[b*128, b*128+128)`` of ``ql``, ``[b*64, ...)`` of ``qh``,
+  ``[b*16, ...)`` of ``sc`` — the byte order inside a superblock is GGUF's.
+
+Because rows are self-contained, row ranges of a weight are weights too:
+gate/up concatenation and row sharding are plain byte-range operations.
+"""
+
+from __future__ import annotations
+
+# gguf.ts:24-35
+GGML_TYPES = {
+    "F32": 0, "F16": 1,
+    "Q4_0": 2, "Q4_1": 3,
+    "Q5_0": 6, "Q5_1": 7,
+    "Q8_0": 8, "Q8_1": 9,
+    "Q2_K": 10, "Q3_K": 11, "Q4_K": 12, "Q5_K": 13, "Q6_K": 14, "Q8_K": 15,
+    "IQ2_XXS": 16, "IQ2_XS": 17, "IQ3_XXS": 18, "IQ1_S": 19, "IQ4_NL": 20,
+    "IQ3_S": 21, "IQ2_S": 22, "IQ4_XS": 23,
+    "I8": 24, "I16": 25, "I32": 26, "I64": 27, "F64": 28, "IQ1_M": 29,
+    "BF16": 30,
+}
+GGML_TYPE_NAMES = {v: k for k, v in GGML_TYPES.items()}
+
+F32 = GGML_TYPES["F32"]
+F16 = GGML_TYPES["F16"]
+Q8_0 = GGML_TYPES["Q8_0"]
+Q4_K = GGML_TYPES["Q4_K"]
+Q6_K = GGML_TYPES["Q6_K"]
+
+# gguf.ts:39-73 — [elements per block, bytes per block]
+_TYPE_TRAITS = {
+    0: (1, 4), 1: (1, 2), 30: (1, 2), 24: (1, 1), 25: (1, 2), 26: (1, 4),
+    27: (1, 8), 28: (1, 8),
+    2: (32, 18), 3: (32, 20), 6: (32, 22), 7: (32, 24), 8: (32, 34), 9: (32, 36),
+    10: (256, 84), 11: (256, 110), 12: (256, 144), 13: (256, 176), 14: (256, 210),
+    15: (256, 292),
+    16: (256, 66), 17: (256, 74), 18: (256, 98), 19: (256, 50), 20: (32, 18),
+    21: (256, 110), 22: (256, 82), 23: (256, 136), 29: (256, 56),
+}
+
+# Types the HIP kernels of this library decode.
+KERNEL_TYPES = (Q8_0, Q4_K, Q6_K)
+
+
+class GGMLTypeError(NotImplementedError):
+    """Unsupported ggml type (gguf.ts:75-79, gguf-dequant.ts:837,866)."""
+
+
+def ggml_type_traits(ggml_type: int) -> tuple[int, int, str]:
+    """``(block_size, type_size, name)``; raises for unknown types (gguf.ts:75-79)."""
+    t = _TYPE_TRAITS.get(int(ggml_type))
+    if t is None:
+        raise GGMLTypeError(f"[GGUF] Unsupported ggml type {ggml_type}")
+    return t[0], t[1], GGML_TYPE_NAMES[int(ggml_type)]
+
+
+def ggml_tensor_bytes(ggml_type: int, ne: list[int] | tuple[int, ...]) -> int:
+    """Raw GGUF bytes of a tensor with dims ``ne`` (innermost first), gguf.ts:82-92."""
+    block, tsize, _ = ggml_type_traits(ggml_type)
+    ne0 = int(ne[0]) if len(ne) else 1
+    if ne0 % block != 0:
+        raise ValueError(
+            f"[GGUF] ne[0]={ne0} not divisible by block size {block} for type {ggml_type}")
+    outer = 1
+    for d in ne[1:]:
+        outer *= int(d)
+    return (ne0 // block) * tsize * outer
+
+
+def _align16(x: int) -> int:
+    return (x + 15) & ~15
+
+
+def check_kernel_type(ggml_type: int) -> None:
+    if int(ggml_type) not in KERNEL_TYPES:
+        ggml_type_traits(ggml_type)  # unknown ids raise the gguf.ts error
+        raise GGMLTypeError(
+            f"[gguf-hip] no kernel for ggml type {ggml_type} "
+            f"({GGML_TYPE_NAMES.get(int(ggml_type), '?')})")
+
+
+def raw_row_bytes(ggml_type: int, k: int) -> int:
+    """GGUF bytes of one row of ``k`` elements."""
+    return ggml_tensor_bytes(ggml_type, [k])
+
+
+def tile_row_bytes(ggml_type: int, k: int) -> int:
+    """Bytes of one row of ``k`` elements in the HBM row layout (see module doc)."""
+    check_kernel_type(ggml_type)
+    block, tsize, _ = ggml_type_traits(ggml_type)
+    if k <= 0 or k % block != 0:
+        raise ValueError(f"[gguf-hip] K={k} not a positive multiple of block size {block}")
+    nb = k // block
+    if ggml_type == Q4_K:
+        return 144 * nb
+    return _align16(tsize * nb)
+
+
+def tile_plane_offsets(ggml_type: int, k: int) -> dict[str, int]:
+    """Byte offset of each plane inside one row of the HBM row layout."""
+    tile_row_bytes(ggml_type, k)
+    if ggml_type == Q8_0:
+        return {"qs": 0, "d": k}
+    if ggml_type == Q6_K:
+        return {"ql": 0, "qh": k // 2, "sc": k // 2 + k // 4, "d": k // 2 + k // 4 + k // 16}
+    return {"blocks": 0}

@@ -1,0 +1,162 @@
+"""Deterministic CPU quantizers that produce raw GGUF blocks (host-side input
+generation; the reference ships none — it only decodes).
+
+The decode side of each format is fixed by the reference
+(``webgpu/src/model/gguf-dequant.ts:152-166,169-176,255-281,369-399``); any
+block bytes are valid input to the kernels, so the quantizers only need to be
+deterministic and sensible.  They follow the packing conventions of
+llama.cpp's ``quantize_row_*_ref`` (6-bit scale/min packing of Q4_K, ql/qh
+split of Q6_K) with simpler scale searches:
+
+* Q8_0: ``d = max|w| / 127`` per 32 elements, stored as f16; ``q = rint(w / d)``.
+* Q4_K: per 32-element sub-block ``scale = (max - min(0, min)) / 15`` and
+  ``min = -min(0, min)``; per superblock ``d = max scale / 63``,
+  ``dmin = max min / 63`` (f16); 6-bit ``sc, m`` then 4-bit ``q``.
+* Q6_K: per 16-element sub-block ``scale = max|w| / 31``; ``d = max|scale| /
+  127`` (f16); int8 ``sc`` then ``q - 32`` in [-32, 31].
+
+All arithmetic is numpy f32; results depend only on the input values.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+
+from .ggml import Q4_K, Q6_K, Q8_0
+
+_CHUNK_ROWS = 4096
+
+
+def _f16(x: np.ndarray) -> np.ndarray:
+    return x.astype(np.float16)
+
+
+def _safe_div(a: np.ndarray, b: np.ndarray) -> np.ndarray:
+    out = np.zeros(np.broadcast(a, b).shape, np.float32)
+    np.divide(a, b, out=out, where=(b != 0))
+    return out
+
+
+def pack_q4_k_scales(sc: np.ndarray, m: np.ndarray) -> np.ndarray:
+    """Pack 8 six-bit (scale, min) pairs per superblock into 12 bytes.
+
+    ``sc``, ``m``: (..., 8) integers in [0, 63].  Slot j < 4 keeps the low six
+    bits of byte j (scale) and byte j + 4 (min); slot j >= 4 stores its low
+    nibbles in byte j + 4 and its top two bits in bits 6-7 of bytes j - 4
+    (scale) and j (min).
+    """
+    sc = np.asarray(sc, np.uint8)
+    m = np.asarray(m, np.uint8)
+    out = np.zeros(sc.shape[:-1] + (12,), np.uint8)
+    out[..., 0:4] = (sc[..., 0:4] & 63) | ((sc[..., 4:8] >> 4) << 6)
+    out[..., 4:8] = (m[..., 0:4] & 63) | ((m[..., 4:8] >> 4) << 6)
+    out[..., 8:12] = (sc[..., 4:8] & 0x0F) | ((m[..., 4:8] & 0x0F) << 4)
+    return out
+
+
+def pack_q6_k(q: np.ndarray) -> tuple[np.ndarray, np.ndarray]:
+    """Split unsigned 6-bit values (nb, 256) in element order into ``ql[128]``, ``qh[64]``.
+
+    Element ``128*h + 32*t + l`` (half h, quarter t, lane l < 32) puts its low
+    nibble in ``ql[64h + l]`` (t = 0 low, t = 2 high nibble) or
+    ``ql[64h + 32 + l]`` (t = 1 low, t = 3 high) and its top two bits in bits
+    ``2t..2t+1`` of ``qh[32h + l]``.
+    """
+    q = np.asarray(q, np.uint8).reshape(-1, 2, 4, 32)
+    lo = q & 0x0F
+    hi = q >> 4
+    ql = np.empty((q.shape[0], 2, 2, 32), np.uint8)
+    ql[:, :, 0, :] = lo[:, :, 0, :] | (lo[:, :, 2, :] << 4)
+    ql[:, :, 1, :] = lo[:, :, 1, :] | (lo[:, :, 3, :] << 4)
+    qh = hi[:, :, 0, :] | (hi[:, :, 1, :] << 2) | (hi[:, :, 2, :] << 4) | (hi[:, :, 3, :] << 6)
+    return ql.reshape(-1, 128), qh.reshape(-1, 64)
+
+
+def _quantize_q8_0(w: np.ndarray) -> np.ndarray:
+    blocks = w.reshape(-1, 32)
+    amax = np.abs(blocks).max(axis=1)
+    d = (amax / np.float32(127)).astype(np.float32)
+    inv = _safe_div(np.float32(1), d)
+    q = np.clip(np.rint(blocks * inv[:, None]), -127, 127).astype(np.int8)
+    out = np.empty((blocks.shape[0], 34), np.uint8)
+    out[:, 0:2] = _f16(d).view(np.uint8).reshape(-1, 2)
+    out[:, 2:34] = q.view(np.uint8)
+    return out.reshape(-1)
+
+
+def _quantize_q4_k(w: np.ndarray) -> np.ndarray:
+    sub = w.reshape(-1, 8, 32)
+    nb = sub.shape[0]
+    wmin = np.minimum(sub.min(axis=2), np.float32(0))
+    wmax = sub.max(axis=2)
+    scale = (wmax - wmin) / np.float32(15)
+    mins = -wmin
+    d16 = _f16(scale.max(axis=1) / np.float32(63))
+    dmin16 = _f16(mins.max(axis=1) / np.float32(63))
+    d = d16.astype(np.float32)[:, None]
+    dmin = dmin16.astype(np.float32)[:, None]
+    sc = np.clip(np.rint(_safe_div(scale, d)), 0, 63).astype(np.uint8)
+    m = np.clip(np.rint(_safe_div(mins, dmin)), 0, 63).astype(np.uint8)
+    d1 = (d * sc)[:, :, None]
+    m1 = (dmin * m)[:, :, None]
+    q = np.clip(np.rint(_safe_div(sub + m1, d1)), 0, 15).astype(np.uint8)   # (nb, 8, 32)
+    qs = q[:, 0::2, :] | (q[:, 1::2, :] << 4)                              # (nb, 4, 32)
+    out = np.empty((nb, 144), np.uint8)
+    out[:, 0:2] = d16.view(np.uint8).reshape(-1, 2)
+    out[:, 2:4] = dmin16.view(np.uint8).reshape(-1, 2)
+    out[:, 4:16] = pack_q4_k_scales(sc, m)
+    out[:, 16:144] = qs.reshape(nb, 128)
+    return out.reshape(-1)
+
+
+def _quantize_q6_k(w: np.ndarray) -> np.ndarray:
+    sub = w.reshape(-1, 16, 16)
+    nb = sub.shape[0]
+    scale = np.abs(sub).max(axis=2) / np.float32(31)                        # (nb, 16)
+    d16 = _f16(scale.max(axis=1) / np.float32(127))
+    d = d16.astype(np.float32)[:, None]
+    sc = np.clip(np.rint(_safe_div(scale, d)), -128, 127).astype(np.int8)
+    ds = (d * sc.astype(np.float32))[:, :, None]
+    q = np.clip(np.rint(_safe_div(sub, ds)), -32, 31).astype(np.int16) + 32   # 0..63
+    ql, qh = pack_q6_k(q.reshape(nb, 256))
+    out = np.empty((nb, 210), np.uint8)
+    out[:, 0:128] = ql
+    out[:, 128:192] = qh
+    out[:, 192:208] = sc.view(np.uint8)
+    out[:, 208:210] = d16.view(np.uint8).reshape(-1, 2)
+    return out.reshape(-1)
+
+
+_QUANTIZERS = {Q8_0: (32, 34, _quantize_q8_0), Q4_K: (256, 144, _quantize_q4_k),
+               Q6_K: (256, 210, _quantize_q6_k)}
+
+
+def quantize(w: np.ndarray, ggml_type: int) -> np.ndarray:
+    """Quantize a row-major f32 weight ``[N, K]`` to raw GGUF bytes (uint8, N*K/block*size)."""
+    if int(ggml_type) not in _QUANTIZERS:
+        raise NotImplementedError(f"[gguf-hip] no quantizer for ggml type {ggml_type}")
+    block, tsize, fn = _QUANTIZERS[int(ggml_type)]
+    w = np.asarray(w, np.float32)
+    if w.ndim == 1:
+        w = w.reshape(1, -1)
+    n, k = w.shape
+    if k % block:
+        raise ValueError(f"[gguf-hip] K={k} not divisible by block size {block}")
+    row_bytes = k // block * tsize
+    out = np.empty(n * row_bytes, np.uint8)
+    for r0 in range(0, n, _CHUNK_ROWS):
+        r1 = min(n, r0 + _CHUNK_ROWS)
+        out[r0 * row_bytes:r1 * row_bytes] = fn(np.ascontiguousarray(w[r0:r1]))
+    return out
+
+
+def synthetic_weight(n: int, k: int, seed: int, std: float = 0.02) -> np.ndarray:
+    """Seeded f32 weight ``[n, k]`` drawn from N(0, std^2)."""
+    rng = np.random.default_rng(seed)
+    return rng.standard_normal((n, k), dtype=np.float32) * np.float32(std)
+
+
+def synthetic_activations(m: int, k: int, seed: int, dtype=np.float32) -> np.ndarray:
+    """Seeded activations ``[m, k]`` ~ N(0, 1); fp16 ones are drawn in f32 then rounded."""
+    rng = np.random.default_rng(seed)
+    return rng.standard_normal((m, k), dtype=np.float32).astype(dtype)

@@ -1,0 +1,123 @@
+/*
+ * gguf_hip.h — C ABI of the MI355X (gfx950) GGUF dequant-matmul library.
+ *
+ * Drop-in for the quantized-projection path of the reference WebGPU engine:
+ *   dispatchMatmulGGUF(aBuf, gg, cBuf, M, N, K, label, io)
+ *       webgpu/src/engine/forward-pass.ts:1496-1544
+ *   repackGGUFForGPU(ggmlType, data, n)        webgpu/src/model/gguf-dequant.ts:809-840
+ *   dequantGGML(ggmlType, data, n)             webgpu/src/model/gguf-dequant.ts:844-868
+ *   ggmlTypeTraits / ggmlTensorBytes           webgpu/src/model/gguf.ts:75-92
+ *
+ * Conventions
+ *  - Plain pointers and sizes only.  Device pointers are HIP device memory;
+ *    `stream` is a hipStream_t (NULL = the legacy default stream).
+ *  - Every call validates its arguments before any HIP call and returns 0 on
+ *    success or a negative GGUF_HIP_ERR_* code; gguf_hip_last_error() then
+ *    describes the failure (thread-local string, valid until the next call on
+ *    that thread).  Validation failures therefore work without a GPU.
+ *  - Work is enqueued on `stream` and the calls return without a host sync,
+ *    like the reference's BatchedDispatcher (webgpu/src/engine/compute.ts:146-266).
+ *  - No call allocates device memory: weights, activations and outputs are
+ *    owned by the caller, as in the reference (forward-pass.ts:1140-1163).
+ *  - Weights live in the "HBM row layout": N rows of gguf_hip_tile_bytes(t,1,K)
+ *    bytes, rows 16-byte aligned; Q4_K rows are the raw GGUF superblocks, Q8_0
+ *    and Q6_K rows are split into 16-byte-aligned planes (qs|d for Q8_0,
+ *    ql|qh|sc|d for Q6_K).  gguf_hip_repack converts raw GGUF bytes.
+ */
+#ifndef GGUF_HIP_H
+#define GGUF_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define GGUF_HIP_ABI_VERSION 1
+
+/* ggml type ids (gguf.ts:24-35); activation dtypes reuse F32 / F16. */
+#define GGUF_HIP_F32 0
+#define GGUF_HIP_F16 1
+#define GGUF_HIP_Q8_0 8
+#define GGUF_HIP_Q4_K 12
+#define GGUF_HIP_Q6_K 14
+
+/* Error codes.  The Python host maps them onto the reference's throws:
+ * TYPE -> NotImplementedError ("no pipeline for ggml type", forward-pass.ts:1524;
+ *         "Unsupported ggml type", gguf.ts:75-79)
+ * SHAPE / NULL / ALIGN / DTYPE / BYTES -> ValueError
+ *         ("ne[0] not divisible by block size", gguf.ts:85-87;
+ *          "byteLength != expected", gguf-dequant.ts:678-680;
+ *          offsets must be aligned, forward-pass.ts:1486-1489)
+ * HIP -> RuntimeError. */
+#define GGUF_HIP_OK 0
+#define GGUF_HIP_ERR_TYPE (-1)
+#define GGUF_HIP_ERR_SHAPE (-2)
+#define GGUF_HIP_ERR_NULL (-3)
+#define GGUF_HIP_ERR_ALIGN (-4)
+#define GGUF_HIP_ERR_DTYPE (-5)
+#define GGUF_HIP_ERR_BYTES (-6)
+#define GGUF_HIP_ERR_HIP (-7)
+
+/* Kernel family for gguf_hip_matmul_variant. */
+#define GGUF_HIP_VARIANT_AUTO 0   /* GEMV for M == 1, skinny MFMA for M <= 32, GEMM above */
+#define GGUF_HIP_VARIANT_GEMV 1   /* VALU GEMV, one pass over the weights per activation row */
+#define GGUF_HIP_VARIANT_SKINNY 2 /* MFMA, all M <= 32 rows share one pass over the weights */
+#define GGUF_HIP_VARIANT_GEMM 3   /* MFMA GEMM with dequantized fp16 tiles staged in LDS */
+
+/* ABI version of the loaded library (GGUF_HIP_ABI_VERSION). */
+int gguf_hip_abi_version(void);
+
+/* Description of the last error on the calling thread ("" if none). */
+const char *gguf_hip_last_error(void);
+
+/* Elements and bytes per block of a ggml type; gguf.ts:75-79 (ggmlTypeTraits). */
+int gguf_hip_type_traits(int ggml_type, int *block_elems, int *type_size);
+
+/* Raw GGUF bytes of an [n_rows, k] tensor (gguf.ts:82-92, ggmlTensorBytes);
+ * negative error code on failure. */
+int64_t gguf_hip_raw_bytes(int ggml_type, int64_t n_rows, int64_t k);
+
+/* Bytes of an [n_rows, k] weight in the HBM row layout; replaces the
+ * GGUF_GPU_LAYOUT stride table (gguf-dequant.ts:655-672).  Negative on error. */
+int64_t gguf_hip_tile_bytes(int ggml_type, int64_t n_rows, int64_t k);
+
+/* Raw GGUF bytes (device, any alignment, exactly raw_bytes long) -> HBM row
+ * layout (device, 16-byte aligned, exactly tile_bytes long).  Replaces
+ * repackGGUFForGPU (gguf-dequant.ts:809-840) including its byte-length check
+ * (assertBytes, :678-680).  Pad bytes are written as zero. */
+int gguf_hip_repack(const void *raw, int64_t raw_bytes, int ggml_type, int64_t n_rows,
+                    int64_t k, void *tiles, int64_t tile_bytes, void *stream);
+
+/* Dequantize an [n_rows, k] weight in the HBM row layout to f32
+ * out[n * ldo + i].  Bit-exact to dequantGGML (gguf-dequant.ts:844-868). */
+int gguf_hip_dequant(const void *tiles, int ggml_type, int64_t n_rows, int64_t k, float *out,
+                     int64_t ldo, void *stream);
+
+/* Dequantize n_elems elements of raw GGUF bytes (device, any alignment) to
+ * f32 out[0..n_elems).  Same values as dequantGGML (gguf-dequant.ts:844-868);
+ * the reference uses it for the CPU embedding row-gather (forward-pass.ts:2171-2186). */
+int gguf_hip_dequant_raw(const void *raw, int ggml_type, int64_t n_elems, float *out,
+                         void *stream);
+
+/* y[m * ldy + n] = sum_k x[m * ldx + k] * dequant(W)[n, k] for m < M, n < N.
+ * x: f32 or f16 (x_type = GGUF_HIP_F32 / GGUF_HIP_F16), 16-byte aligned rows
+ * (ldx * sizeof(x) % 16 == 0).  W: HBM row layout, 16-byte aligned.
+ * y: f32, 4-byte aligned.  Accumulation in f32.  Replaces dispatchMatmulGGUF
+ * (forward-pass.ts:1496-1544); its io.aOffset / io.cOffset windows are plain
+ * pointer offsets here. */
+int gguf_hip_matmul(const void *x, int x_type, int64_t ldx, const void *tiles, int ggml_type,
+                    int64_t n, int64_t k, float *y, int64_t ldy, int64_t m, void *stream);
+
+/* gguf_hip_matmul with an explicit kernel family (GGUF_HIP_VARIANT_*), the
+ * analog of the reference's per-dispatch pipeline choice (forward-pass.ts:1501-1524).
+ * SKINNY requires M <= 32. */
+int gguf_hip_matmul_variant(const void *x, int x_type, int64_t ldx, const void *tiles,
+                            int ggml_type, int64_t n, int64_t k, float *y, int64_t ldy,
+                            int64_t m, int variant, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* GGUF_HIP_H */

@@ -1,0 +1,310 @@
+"""CPU oracle for the GGUF Q8_0 / Q4_K / Q6_K dequant-matmul path.
+
+TEST INFRASTRUCTURE ONLY.  This module is the checker: only ``tests/``,
+``__graft_entry__.smoke()`` and the ``cpu_baseline`` leg of ``bench.py`` may
+import it, and only to check or to time the CPU baseline.  The product path
+(the HIP library and its Python host code) never calls it.
+
+It restates the reference's CPU dequantization
+(``webgpu/src/model/gguf-dequant.ts``) twice:
+
+* ``*_loop`` functions follow the TypeScript loops line for line, computing in
+  Python floats (IEEE f64, like JavaScript numbers) and rounding once to f32
+  on store, as the reference's ``Float32Array`` store does.  Pure Python;
+  use them on small inputs only.
+* the vectorised numpy functions compute in f32.  They are bit-identical to
+  the loops because every product in these formats is exact in f32 (Q8_0
+  ``d*q`` needs <= 18 significant bits, Q6_K ``d*sc*q`` <= 23, Q4_K
+  ``d*sc*q`` <= 21 and ``dmin*m`` <= 17) and the only rounding left is the
+  final Q4_K subtraction, which f32 and f64-then-f32 both round correctly
+  (the exact difference is a multiple of 2**-24 below 2**27, so it fits in
+  f64's 53 bits).
+
+Parity pins (all in ``tests/test_oracle.py``):
+* the reference's gguf-py golden vectors (``webgpu/test-fixtures/gguf-*.json``
+  ``dequant_samples``: 1 Q8_0, 2 Q4_K, 3 Q6_K samples) — bit-exact;
+* exact rational arithmetic (``fractions.Fraction``) on random blocks;
+* an independently written encoder (the packing side of the 6-bit scale/min
+  and the Q6_K ql/qh split, in the package quantizer) round-tripping through
+  the decoders, exhaustively over each scale slot;
+* special values: d = 0, f16 subnormal and Inf/NaN scales, Q6_K sc = -128.
+``matmul_bt`` is pinned against numpy float64 products and linearity.
+"""
+
+from __future__ import annotations
+
+import math
+
+import numpy as np
+
+T_F32, T_F16, T_Q8_0, T_Q4_K, T_Q6_K, T_BF16 = 0, 1, 8, 12, 14, 30
+
+# ---------------------------------------------------------------------------
+# Literal restatement (pure Python, f64 arithmetic, f32 store)
+# ---------------------------------------------------------------------------
+
+
+def f16_to_f32(h: int) -> float:
+    """IEEE half bits -> value; gguf-dequant.ts:64-71."""
+    sign = -1.0 if (h & 0x8000) else 1.0
+    exp = (h >> 10) & 0x1F
+    frac = h & 0x3FF
+    if exp == 0:
+        return sign * frac * 2.0 ** -24
+    if exp == 0x1F:
+        return math.nan if frac else sign * math.inf
+    return sign * (1 + frac / 1024) * 2.0 ** (exp - 15)
+
+
+def _u16(b: bytes, off: int) -> int:
+    return b[off] | (b[off + 1] << 8)
+
+
+def _i8(v: int) -> int:
+    return v - 256 if v >= 128 else v
+
+
+def get_scale_min_k4(j: int, q: bytes, base: int) -> tuple[int, int]:
+    """6-bit (scale, min) pair ``j`` of a Q4_K superblock; gguf-dequant.ts:169-176."""
+    if j < 4:
+        return q[base + j] & 63, q[base + j + 4] & 63
+    sc = (q[base + j + 4] & 0x0F) | ((q[base + j - 4] >> 6) << 4)
+    m = (q[base + j + 4] >> 4) | ((q[base + j] >> 6) << 4)
+    return sc, m
+
+
+def dequant_q8_0_loop(data: bytes, n: int) -> np.ndarray:
+    """gguf-dequant.ts:152-166."""
+    if n % 32 != 0:
+        raise ValueError(f"[Q8_0] n={n} not divisible by 32")
+    out = np.zeros(n, np.float32)
+    for b in range(n // 32):
+        base = b * 34
+        d = f16_to_f32(_u16(data, base))
+        for i in range(32):
+            out[b * 32 + i] = d * _i8(data[base + 2 + i])
+    return out
+
+
+def dequant_q4_k_loop(data: bytes, n: int) -> np.ndarray:
+    """gguf-dequant.ts:255-281."""
+    if n % 256 != 0:
+        raise ValueError(f"[Q4_K] n={n} not divisible by 256")
+    out = np.zeros(n, np.float32)
+    for b in range(n // 256):
+        base = b * 144
+        d = f16_to_f32(_u16(data, base))
+        dmin = f16_to_f32(_u16(data, base + 2))
+        scales_base = base + 4
+        y = b * 256
+        qs = base + 16
+        is_ = 0
+        for _ in range(0, 256, 64):
+            sc1, m1 = get_scale_min_k4(is_ + 0, data, scales_base)
+            sc2, m2 = get_scale_min_k4(is_ + 1, data, scales_base)
+            d1, min1 = d * sc1, dmin * m1
+            d2, min2 = d * sc2, dmin * m2
+            for l in range(32):
+                out[y + l] = d1 * (data[qs + l] & 0x0F) - min1
+            for l in range(32):
+                out[y + 32 + l] = d2 * (data[qs + l] >> 4) - min2
+            y += 64
+            qs += 32
+            is_ += 2
+    return out
+
+
+def dequant_q6_k_loop(data: bytes, n: int) -> np.ndarray:
+    """gguf-dequant.ts:369-399."""
+    if n % 256 != 0:
+        raise ValueError(f"[Q6_K] n={n} not divisible by 256")
+    out = np.zeros(n, np.float32)
+    for b in range(n // 256):
+        base = b * 210
+        d = f16_to_f32(_u16(data, base + 208))
+        y, ql, qh, sc = b * 256, base, base + 128, base + 192
+        for _half in range(2):
+            for l in range(32):
+                is_ = l // 16
+                q1 = ((data[ql + l] & 0x0F) | (((data[qh + l] >> 0) & 3) << 4)) - 32
+                q2 = ((data[ql + l + 32] & 0x0F) | (((data[qh + l] >> 2) & 3) << 4)) - 32
+                q3 = ((data[ql + l] >> 4) | (((data[qh + l] >> 4) & 3) << 4)) - 32
+                q4 = ((data[ql + l + 32] >> 4) | (((data[qh + l] >> 6) & 3) << 4)) - 32
+                out[y + l] = d * _i8(data[sc + is_]) * q1
+                out[y + l + 32] = d * _i8(data[sc + is_ + 2]) * q2
+                out[y + l + 64] = d * _i8(data[sc + is_ + 4]) * q3
+                out[y + l + 96] = d * _i8(data[sc + is_ + 6]) * q4
+            y += 128
+            ql += 64
+            qh += 32
+            sc += 8
+    return out
+
+
+def dequant_ggml_loop(ggml_type: int, data: bytes, n: int) -> np.ndarray:
+    """Type switch of gguf-dequant.ts:844-868 (the in-scope types)."""
+    data = bytes(data)
+    if ggml_type == T_F32:
+        return np.frombuffer(data, "<f4", n).astype(np.float32)
+    if ggml_type == T_F16:
+        return np.array([f16_to_f32(_u16(data, 2 * i)) for i in range(n)], np.float32)
+    if ggml_type == T_BF16:
+        u = np.frombuffer(data, "<u2", n).astype(np.uint32) << 16
+        return u.view(np.float32).copy()
+    if ggml_type == T_Q8_0:
+        return dequant_q8_0_loop(data, n)
+    if ggml_type == T_Q4_K:
+        return dequant_q4_k_loop(data, n)
+    if ggml_type == T_Q6_K:
+        return dequant_q6_k_loop(data, n)
+    raise NotImplementedError(f"[GGUF-dequant] No CPU reference for ggml type {ggml_type}")
+
+
+# ---------------------------------------------------------------------------
+# Vectorised restatement (numpy, f32 arithmetic; bit-identical to the loops)
+# ---------------------------------------------------------------------------
+
+Q8_0_BLOCK = np.dtype([("d", "<f2"), ("qs", "i1", 32)])
+Q4_K_BLOCK = np.dtype([("d", "<f2"), ("dmin", "<f2"), ("scales", "u1", 12), ("qs", "u1", 128)])
+Q6_K_BLOCK = np.dtype([("ql", "u1", 128), ("qh", "u1", 64), ("sc", "i1", 16), ("d", "<f2")])
+assert Q8_0_BLOCK.itemsize == 34 and Q4_K_BLOCK.itemsize == 144 and Q6_K_BLOCK.itemsize == 210
+
+
+def _blocks(data, dtype: np.dtype, n: int, block: int, name: str) -> np.ndarray:
+    if n % block != 0:
+        raise ValueError(f"[{name}] n={n} not divisible by {block}")
+    buf = np.frombuffer(data, np.uint8) if not isinstance(data, np.ndarray) else data.reshape(-1)
+    nb = n // block
+    if buf.size < nb * dtype.itemsize:
+        raise ValueError(f"[{name}] byteLength {buf.size} < expected {nb * dtype.itemsize}")
+    return buf[: nb * dtype.itemsize].view(dtype)
+
+
+def q4_k_scale_min(scales: np.ndarray) -> tuple[np.ndarray, np.ndarray]:
+    """Vectorised get_scale_min_k4 for all j: ``scales`` (..., 12) u8 -> (sc, m) (..., 8)."""
+    s = scales.astype(np.uint8)
+    sc = np.empty(s.shape[:-1] + (8,), np.uint8)
+    m = np.empty_like(sc)
+    sc[..., :4] = s[..., 0:4] & 63
+    m[..., :4] = s[..., 4:8] & 63
+    sc[..., 4:] = (s[..., 8:12] & 0x0F) | ((s[..., 0:4] >> 6) << 4)
+    m[..., 4:] = (s[..., 8:12] >> 4) | ((s[..., 4:8] >> 6) << 4)
+    return sc, m
+
+
+def dequant_q8_0(data, n: int) -> np.ndarray:
+    blk = _blocks(data, Q8_0_BLOCK, n, 32, "Q8_0")
+    d = blk["d"].astype(np.float32)[:, None]
+    return (d * blk["qs"].astype(np.float32)).reshape(-1)
+
+
+def dequant_q4_k(data, n: int) -> np.ndarray:
+    blk = _blocks(data, Q4_K_BLOCK, n, 256, "Q4_K")
+    nb = blk.shape[0]
+    d = blk["d"].astype(np.float32)[:, None]
+    dmin = blk["dmin"].astype(np.float32)[:, None]
+    sc, m = q4_k_scale_min(blk["scales"])
+    d1 = (d * sc.astype(np.float32))[:, :, None]        # exact
+    m1 = (dmin * m.astype(np.float32))[:, :, None]      # exact
+    qs = blk["qs"].reshape(nb, 4, 1, 32)
+    q = np.concatenate([qs & 0x0F, qs >> 4], axis=2).reshape(nb, 8, 32)
+    return (d1 * q.astype(np.float32) - m1).reshape(-1)
+
+
+def q6_k_values(blk: np.ndarray) -> np.ndarray:
+    """Signed 6-bit values (q - 32) of Q6_K blocks in element order, shape (nb, 256)."""
+    nb = blk.shape[0]
+    ql = blk["ql"].reshape(nb, 2, 64).astype(np.int16)
+    qh = blk["qh"].reshape(nb, 2, 32).astype(np.int16)
+    lo, hi = ql[:, :, :32], ql[:, :, 32:]
+    q = np.stack([
+        (lo & 0x0F) | (((qh >> 0) & 3) << 4),
+        (hi & 0x0F) | (((qh >> 2) & 3) << 4),
+        (lo >> 4) | (((qh >> 4) & 3) << 4),
+        (hi >> 4) | (((qh >> 6) & 3) << 4),
+    ], axis=2)                                            # (nb, half, t, l)
+    return (q - 32).reshape(nb, 256)
+
+
+def dequant_q6_k(data, n: int) -> np.ndarray:
+    blk = _blocks(data, Q6_K_BLOCK, n, 256, "Q6_K")
+    nb = blk.shape[0]
+    d = blk["d"].astype(np.float32)[:, None]
+    # element e of a superblock uses scale index e // 16 (half*8 + 2t + l//16)
+    sc = np.repeat(blk["sc"].astype(np.float32), 16, axis=1)   # (nb, 256)
+    return ((d * sc) * q6_k_values(blk).astype(np.float32)).reshape(-1)
+
+
+def dequant_ggml(ggml_type: int, data, n: int) -> np.ndarray:
+    """Vectorised dequantization of raw GGUF bytes to f32 (gguf-dequant.ts:844-868)."""
+    if ggml_type == T_Q8_0:
+        return dequant_q8_0(data, n)
+    if ggml_type == T_Q4_K:
+        return dequant_q4_k(data, n)
+    if ggml_type == T_Q6_K:
+        return dequant_q6_k(data, n)
+    if ggml_type in (T_F32, T_F16, T_BF16):
+        return dequant_ggml_loop(ggml_type, bytes(np.frombuffer(data, np.uint8)), n)
+    raise NotImplementedError(f"[GGUF-dequant] No CPU reference for ggml type {ggml_type}")
+
+
+def dequant_rows(ggml_type: int, raw: np.ndarray, n_rows: int, k: int) -> np.ndarray:
+    """Dequantize a row-major [n_rows, k] weight from its raw GGUF bytes."""
+    return dequant_ggml(ggml_type, raw, n_rows * k).reshape(n_rows, k)
+
+
+# ---------------------------------------------------------------------------
+# Matmul reference and the parity gate
+# ---------------------------------------------------------------------------
+
+
+def matmul_bt(a: np.ndarray, w: np.ndarray) -> np.ndarray:
+    """``C[m, n] = sum_k a[m, k] * w[n, k]`` accumulated in f64 (kernel-tests.ts:98-110).
+
+    Returns the f64 result; the reference stores it to f32, ``.astype(np.float32)``.
+    """
+    return np.asarray(a, np.float64) @ np.asarray(w, np.float64).T
+
+
+def matmul_bt_abs(a: np.ndarray, w: np.ndarray) -> np.ndarray:
+    """``sum_k |a[m, k] * w[n, k]|`` — the scale of the per-element error bound."""
+    return np.abs(np.asarray(a, np.float64)) @ np.abs(np.asarray(w, np.float64)).T
+
+
+REL_TOL = 1e-3
+
+
+def parity_metrics(y, y_ref, sum_abs) -> dict:
+    """Both gates of the path: normwise and per-element relative error.
+
+    normwise  = ||y - y_ref||_2 / ||y_ref||_2                       (<= 1e-3)
+    elemwise  = max |y - y_ref| / sum_k |x_k w_nk|                  (<= 1e-3)
+    """
+    y = np.asarray(y, np.float64)
+    y_ref = np.asarray(y_ref, np.float64)
+    sum_abs = np.asarray(sum_abs, np.float64)
+    err = np.abs(y - y_ref)
+    denom = np.linalg.norm(y_ref)
+    normwise = float(np.linalg.norm(y - y_ref) / denom) if denom > 0 else float(np.linalg.norm(y - y_ref))
+    with np.errstate(divide="ignore", invalid="ignore"):
+        ratio = np.where(sum_abs > 0, err / sum_abs, np.where(err > 0, np.inf, 0.0))
+    finite = bool(np.all(np.isfinite(y)))
+    return {
+        "normwise": normwise,
+        "elemwise": float(ratio.max()) if ratio.size else 0.0,
+        "max_abs": float(err.max()) if err.size else 0.0,
+        "finite": finite,
+        "ok": finite and normwise <= REL_TOL and (float(ratio.max()) if ratio.size else 0.0) <= REL_TOL,
+    }
+
+
+def same_bits(a: np.ndarray, b: np.ndarray) -> bool:
+    """Bitwise f32 equality, NaN == NaN (any payload), +0 != -0."""
+    a = np.ascontiguousarray(a, np.float32).reshape(-1)
+    b = np.ascontiguousarray(b, np.float32).reshape(-1)
+    if a.shape != b.shape:
+        return False
+    na, nb_ = np.isnan(a), np.isnan(b)
+    if not np.array_equal(na, nb_):
+        return False
+    return bool(np.array_equal(a.view(np.uint32)[~na], b.view(np.uint32)[~nb_]))

@@ -1,0 +1,75 @@
+"""Write the golden fixtures used by the tests.
+
+1. ``gguf_dequant_samples.json`` — the gguf-py dequant samples that the
+   reference keeps in ``webgpu/test-fixtures/gguf-*.json`` (``dequant_samples``,
+   produced by ``webgpu/scripts/dump_gguf_fixture.py`` with llama.cpp's gguf-py),
+   reduced to the quantized types of this path (Q8_0, Q4_K, Q6_K) plus Q5_K.
+   Data only: raw block bytes and the expected f32 values.
+2. ``synthetic_small.npz`` — seeded synthetic blocks for each type, with the
+   oracle's dequantized values and f64 matmul results, so a change to the
+   oracle or to the quantizer shows up as a fixture mismatch.
+
+Run from the repository root:  python tests/golden/make_golden.py [reference_root]
+"""
+
+from __future__ import annotations
+
+import importlib
+import json
+import os
+import sys
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(os.path.dirname(HERE))
+KEEP_TYPES = {8, 12, 13, 14}
+FIXTURES = ["gguf-35b-a3b-q5ks.json", "gguf-9b-abliterated-q4km.json", "gguf-e4b-q4km.json"]
+
+
+def write_reference_samples(ref_root: str) -> None:
+    out = []
+    for name in FIXTURES:
+        path = os.path.join(ref_root, "webgpu", "test-fixtures", name)
+        with open(path, encoding="utf-8") as f:
+            fx = json.load(f)
+        for s in fx["dequant_samples"]:
+            if s["ggml_type"] in KEEP_TYPES:
+                out.append({
+                    "source": f"webgpu/test-fixtures/{name}",
+                    "tensor": s["tensor"],
+                    "ggml_type": s["ggml_type"],
+                    "n_elements": s["n_elements"],
+                    "bytes_hex": s["bytes_hex"],
+                    "expected_f32": s["expected_f32"],
+                })
+    with open(os.path.join(HERE, "gguf_dequant_samples.json"), "w", encoding="utf-8") as f:
+        json.dump({"samples": out}, f, indent=0)
+    print(f"wrote {len(out)} reference samples")
+
+
+def write_synthetic() -> None:
+    sys.path.insert(0, ROOT)
+    pkg = importlib.import_module("artifex-assistantv5_amd")
+    from oracle import gguf_ref
+
+    arrays = {}
+    for t, (n, k) in {8: (5, 96), 12: (3, 512), 14: (3, 512)}.items():
+        w = pkg.quantize.synthetic_weight(n, k, seed=1000 + t)
+        raw = pkg.quantize.quantize(w, t)
+        deq = gguf_ref.dequant_rows(t, raw, n, k)
+        x = pkg.quantize.synthetic_activations(2, k, seed=2000 + t)
+        arrays[f"t{t}_raw"] = raw
+        arrays[f"t{t}_shape"] = np.array([n, k])
+        arrays[f"t{t}_deq"] = deq
+        arrays[f"t{t}_x"] = x
+        arrays[f"t{t}_y"] = gguf_ref.matmul_bt(x, deq)
+    np.savez_compressed(os.path.join(HERE, "synthetic_small.npz"), **arrays)
+    print("wrote synthetic_small.npz")
+
+
+if __name__ == "__main__":
+    ref = sys.argv[1] if len(sys.argv) > 1 else "/root/reference"
+    if os.path.isdir(ref):
+        write_reference_samples(ref)
+    write_synthetic()

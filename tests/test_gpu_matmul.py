@@ -1,0 +1,194 @@
+"""GPU: dequant-matmul parity against the oracle.
+
+Gate (both must hold; written here and in oracle.gguf_ref.parity_metrics):
+    normwise  ||y - y_ref||_2 / ||y_ref||_2            <= 1e-3
+    elemwise  max |y - y_ref| / sum_k |x_k * w_nk|      <= 1e-3
+y_ref is the f64 product of the oracle's dequantized weights (bit-exact to
+gguf-dequant.ts) with the same activations.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+import tile_model
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-3
+GEMV, SKINNY, GEMM, AUTO = 1, 2, 3, 0
+
+
+def _check(ref, y, x, wdeq, label):
+    x64 = np.asarray(x, np.float64)
+    y_ref = ref.matmul_bt(x64, wdeq)
+    met = ref.parity_metrics(y, y_ref, ref.matmul_bt_abs(x64, wdeq))
+    assert met["ok"], (label, met)
+    return met
+
+
+def _case(pkg, t, n, k, seed):
+    w = pkg.quantize.synthetic_weight(n, k, seed=seed)
+    raw = pkg.quantize.quantize(w, t)
+    return raw, pkg.repack_gguf_for_gpu(t, raw, n, k)
+
+
+SMALL = [(1, 1, 256), (1, 70, 512), (3, 70, 512), (1, 257, 1280), (7, 9, 768), (17, 130, 512),
+         (32, 64, 1024), (33, 129, 512), (130, 200, 768)]
+
+
+@pytest.mark.parametrize("t", [8, 12, 14])
+@pytest.mark.parametrize("variant", [GEMV, SKINNY, GEMM, AUTO])
+@pytest.mark.parametrize("xdt", ["f32", "f16"])
+def test_small_shapes(pkg, ref, t, variant, xdt):
+    for i, (m, n, k) in enumerate(SMALL):
+        if variant == SKINNY and m > 32:
+            continue
+        raw, w = _case(pkg, t, n, k, seed=10 * t + i)
+        wdeq = ref.dequant_rows(t, raw, n, k)
+        x = pkg.quantize.synthetic_activations(m, k, seed=500 + i,
+                                               dtype=np.float32 if xdt == "f32" else np.float16)
+        xt = torch.from_numpy(x).cuda()
+        y = pkg.qlinear(xt, w, variant=variant).cpu().numpy()
+        _check(ref, y, x.astype(np.float32), wdeq, (t, variant, xdt, m, n, k))
+
+
+@pytest.mark.parametrize("t", [8])
+def test_q8_0_k_not_multiple_of_64(pkg, ref, t):
+    for variant in (GEMV, SKINNY, GEMM):
+        for m, n, k in [(1, 33, 96), (5, 40, 160), (40, 17, 32)]:
+            if variant == SKINNY and m > 32:
+                continue
+            raw, w = _case(pkg, t, n, k, seed=n + k)
+            x = pkg.quantize.synthetic_activations(m, k, seed=k)
+            y = pkg.qlinear(torch.from_numpy(x).cuda(), w, variant=variant).cpu().numpy()
+            _check(ref, y, x, ref.dequant_rows(t, raw, n, k), (variant, m, n, k))
+
+
+def test_reference_kernel_test_shapes(pkg, ref):
+    """kernel-tests.ts:910-927: M=3, N=70, K=512 per type, and N > 65535 (Q8_0, M=1, K=64)."""
+    for t in (8, 12, 14):
+        raw = tile_model.random_blocks(t, 70, 512, seed=t)
+        w = pkg.repack_gguf_for_gpu(t, raw, 70, 512)
+        a = (np.random.default_rng(t).random((3, 512), dtype=np.float32) * 0.5 - 0.25)
+        y = pkg.qlinear(torch.from_numpy(a).cuda(), w).cpu().numpy()
+        _check(ref, y, a, ref.dequant_rows(t, raw, 70, 512), t)
+    raw = tile_model.random_blocks(8, 65600, 64, seed=1)
+    w = pkg.repack_gguf_for_gpu(8, raw, 65600, 64)
+    a = np.random.default_rng(2).random((1, 64), dtype=np.float32) - 0.5
+    y = pkg.qlinear(torch.from_numpy(a).cuda(), w).cpu().numpy()
+    _check(ref, y, a, ref.dequant_rows(8, raw, 65600, 64), "wide")
+
+
+def test_no_writes_outside_output(pkg, ref):
+    t, m, n, k = 12, 5, 70, 512
+    raw, w = _case(pkg, t, n, k, seed=3)
+    x = torch.from_numpy(pkg.quantize.synthetic_activations(m, k, seed=4)).cuda()
+    for variant in (GEMV, SKINNY, GEMM):
+        big = torch.full((m + 2, n + 9), float("nan"), device="cuda")
+        out = big[1:1 + m, 3:3 + n]                      # strided window, ldy = n + 9
+        pkg.dispatch_matmul_gguf(x, w, out, m, n, k, "win", variant=variant)
+        b = big.cpu().numpy()
+        assert np.isnan(b[0]).all() and np.isnan(b[-1]).all()
+        assert np.isnan(b[:, :3]).all() and np.isnan(b[:, 3 + n:]).all()
+        assert np.isfinite(b[1:1 + m, 3:3 + n]).all()
+
+
+def test_io_offsets_window(pkg, ref):
+    t, m, n, k = 14, 2, 33, 512
+    raw, w = _case(pkg, t, n, k, seed=9)
+    x = pkg.quantize.synthetic_activations(m, k, seed=10)
+    a = torch.zeros(64 + m * k, device="cuda")
+    a[64:] = torch.from_numpy(x.reshape(-1)).cuda()
+    c = torch.zeros(16 + m * n, device="cuda")
+    pkg.dispatch_matmul_gguf(a, w, c, m, n, k, "io", io={"aOffset": 256, "cOffset": 64})
+    y = c[16:].view(m, n).cpu().numpy()
+    _check(ref, y, x, ref.dequant_rows(t, raw, n, k), "io")
+
+
+def test_projection_and_gate_up_fusion(pkg, ref):
+    t, k, ffn = 12, 512, 256
+    rg, wg = _case(pkg, t, ffn, k, seed=21)
+    ru, wu = _case(pkg, t, ffn, k, seed=22)
+    x = torch.from_numpy(pkg.quantize.synthetic_activations(1, k, seed=23)).cuda()
+    lw = pkg.LayerWeights(gate_gg=wg, up_gg=wu, gateUp_gg=pkg.concat_rows(wg, wu))
+    g = torch.empty(ffn, device="cuda")
+    u = torch.empty(ffn, device="cuda")
+    gu = torch.empty(2 * ffn, device="cuda")
+    pkg.dispatch_projection(x, lw, "gate", g, 1, ffn, k, "gate")
+    pkg.dispatch_projection(x, lw, "up", u, 1, ffn, k, "up")
+    pkg.dispatch_projection(x, lw, "gateUp", gu, 1, 2 * ffn, k, "gateUp")
+    # rows are reduced independently of their neighbours: the fused GEMV is byte-identical
+    assert torch.equal(gu, torch.cat([g, u]))
+    with pytest.raises(ValueError):
+        pkg.dispatch_projection(x, lw, "down", g, 1, ffn, k, "down")
+
+
+def test_errors_raise_like_reference(pkg):
+    raw, w = _case(pkg, 12, 8, 256, seed=1)
+    x = torch.zeros(1, 512, device="cuda")
+    with pytest.raises(ValueError):
+        pkg.qlinear(x, w)
+    with pytest.raises(ValueError):
+        pkg.dispatch_matmul_gguf(torch.zeros(256, device="cuda"), w, torch.zeros(8, device="cuda"),
+                                 1, 8, 512, "bad-k")
+    with pytest.raises(ValueError, match="byteLength"):
+        pkg.repack_gguf_for_gpu(12, raw[:-1], 8, 256)
+    with pytest.raises(NotImplementedError):
+        pkg.repack_gguf_for_gpu(13, raw, 8, 256)
+
+
+def test_deterministic(pkg):
+    raw, w = _case(pkg, 12, 4096, 4096, seed=2)
+    for m in (1, 8, 100):
+        x = torch.from_numpy(pkg.quantize.synthetic_activations(m, 4096, seed=m)).cuda()
+        assert torch.equal(pkg.qlinear(x, w), pkg.qlinear(x, w))
+
+
+# ---------------------------------------------------------------------------
+# full-size configurations (reference product in f64 on the GPU from the
+# GPU-dequantized weights, which test_gpu_dequant pins bit-exact to the oracle)
+# ---------------------------------------------------------------------------
+
+def _gpu_check(y, x, wdeq, label):
+    x64 = x.double()
+    w64 = wdeq.double()
+    y_ref = x64 @ w64.T
+    sa = x64.abs() @ w64.abs().T
+    err = (y.double() - y_ref).abs()
+    normwise = (torch.linalg.norm(y.double() - y_ref) / torch.linalg.norm(y_ref)).item()
+    elem = (err / sa).max().item()
+    assert torch.isfinite(y).all()
+    assert normwise <= TOL and elem <= TOL, (label, normwise, elem)
+
+
+FULL = [  # (type, M, N, K, x dtype)
+    (8, 1, 4096, 4096, torch.float32),
+    (12, 1, 14336, 4096, torch.float32), (12, 8, 14336, 4096, torch.float32),
+    (12, 32, 14336, 4096, torch.float32),
+    (12, 1, 4096, 14336, torch.float32), (12, 8, 4096, 14336, torch.float32),
+    (12, 32, 4096, 14336, torch.float32),
+    (14, 1, 151936, 4096, torch.float32),
+    (12, 512, 4096, 4096, torch.float16), (12, 2048, 14336, 4096, torch.float16),
+]
+
+
+@pytest.mark.parametrize("t,m,n,k,xdt", FULL)
+def test_full_size_configs(pkg, t, m, n, k, xdt):
+    g = torch.Generator(device="cuda").manual_seed(n + k + m)
+    if n * k <= 64 << 20:
+        wf = torch.randn(n, k, device="cuda", generator=g) * 0.02
+        raw = pkg.quantize.quantize(wf.cpu().numpy(), t)
+        w = pkg.repack_gguf_for_gpu(t, raw, n, k)
+    else:  # LM head: random blocks with finite scales, drawn on the device
+        block, size = tile_model.BLOCK[t]
+        rawd = torch.randint(0, 256, (n * k // block * size,), dtype=torch.uint8, device="cuda",
+                             generator=g)
+        blocks = rawd.view(-1, size)
+        for o in {8: [0], 12: [0, 2], 14: [208]}[t]:
+            v = (torch.rand(blocks.shape[0], device="cuda", generator=g) * 0.003 + 0.0005).half()
+            blocks[:, o:o + 2] = v.view(torch.uint8).view(-1, 2)
+        w = pkg.repack_gguf_for_gpu(t, rawd, n, k)
+    x = torch.randn(m, k, device="cuda", generator=g).to(xdt)
+    y = pkg.qlinear(x, w)
+    _gpu_check(y, x.float(), w.dequant().view(n, k), (t, m, n, k))

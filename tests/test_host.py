@@ -1,0 +1,85 @@
+"""Host-side logic (CPU only): type traits, layout math, quantizer, layout model."""
+
+import numpy as np
+import pytest
+
+import tile_model
+
+
+def test_type_traits_mirror_reference(pkg):
+    g = pkg.ggml
+    # gguf.ts:39-73
+    assert g.ggml_type_traits(8)[:2] == (32, 34)
+    assert g.ggml_type_traits(12)[:2] == (256, 144)
+    assert g.ggml_type_traits(14)[:2] == (256, 210)
+    assert g.ggml_type_traits(13)[:2] == (256, 176)
+    assert g.ggml_type_traits(30)[:2] == (1, 2)
+    with pytest.raises(NotImplementedError, match="Unsupported ggml type 99"):
+        g.ggml_type_traits(99)
+
+
+def test_tensor_bytes(pkg):
+    g = pkg.ggml
+    # gguf.ts:82-92: rowSize(ne0) x prod(outer)
+    assert g.ggml_tensor_bytes(12, [4096, 14336]) == 33_030_144
+    assert g.ggml_tensor_bytes(14, [4096, 151936]) == 510_504_960
+    assert g.ggml_tensor_bytes(8, [4096, 4096]) == 17_825_792
+    with pytest.raises(ValueError, match="not divisible by block size"):
+        g.ggml_tensor_bytes(12, [100, 3])
+
+
+@pytest.mark.parametrize("t", [8, 12, 14])
+@pytest.mark.parametrize("k", [256, 512, 768, 1280, 4096, 14336])
+def test_tile_row_bytes(pkg, t, k):
+    trb = pkg.tile_row_bytes(t, k)
+    assert trb == tile_model.tile_row_bytes(t, k)
+    assert trb % 16 == 0
+    assert trb - pkg.raw_row_bytes(t, k) < 16          # at most 15 pad bytes per row
+    if t == 12:
+        assert trb == pkg.raw_row_bytes(t, k)
+
+
+def test_tile_row_bytes_rejects(pkg):
+    with pytest.raises(ValueError):
+        pkg.tile_row_bytes(12, 100)
+    with pytest.raises(NotImplementedError):
+        pkg.tile_row_bytes(13, 256)            # Q5_K: known type, no kernel
+
+
+def test_plane_offsets(pkg):
+    assert pkg.ggml.tile_plane_offsets(8, 4096) == {"qs": 0, "d": 4096}
+    assert pkg.ggml.tile_plane_offsets(14, 4096) == {"ql": 0, "qh": 2048, "sc": 3072, "d": 3328}
+
+
+@pytest.mark.parametrize("t,k", [(8, 96), (8, 4096), (12, 512), (14, 768), (14, 4096)])
+def test_layout_model_roundtrip(ref, t, k):
+    raw = tile_model.random_blocks(t, 5, k, seed=t + k)
+    tiles = tile_model.to_tiles(t, raw, 5, k)
+    assert tiles.size == 5 * tile_model.tile_row_bytes(t, k)
+    back = tile_model.from_tiles(t, tiles, 5, k)
+    assert np.array_equal(back, raw)
+    assert ref.same_bits(ref.dequant_rows(t, back, 5, k), ref.dequant_rows(t, raw, 5, k))
+
+
+@pytest.mark.parametrize("t", [8, 12, 14])
+def test_quantize_deterministic_and_sized(pkg, t):
+    w = pkg.quantize.synthetic_weight(3, 512, seed=11)
+    a = pkg.quantize.quantize(w, t)
+    b = pkg.quantize.quantize(w.copy(), t)
+    assert np.array_equal(a, b)
+    assert a.size == pkg.ggml_tensor_bytes(t, [512, 3])
+
+
+def test_quantize_rejects(pkg):
+    with pytest.raises(ValueError):
+        pkg.quantize.quantize(np.zeros((2, 100), np.float32), 12)
+    with pytest.raises(NotImplementedError):
+        pkg.quantize.quantize(np.zeros((2, 256), np.float32), 13)
+
+
+def test_synthetic_inputs_seeded(pkg):
+    a = pkg.quantize.synthetic_activations(2, 64, seed=5)
+    b = pkg.quantize.synthetic_activations(2, 64, seed=5)
+    assert np.array_equal(a, b) and a.dtype == np.float32
+    h = pkg.quantize.synthetic_activations(2, 64, seed=5, dtype=np.float16)
+    assert h.dtype == np.float16 and np.array_equal(h, a.astype(np.float16))
