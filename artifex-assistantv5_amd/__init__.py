@@ -5,7 +5,7 @@ behind a C ABI, ``include/gguf_hip.h``).  The per-layer API mirrors the
 reference's WebGPU engine (``webgpu/src/engine/forward-pass.ts``):
 
 * ``GGUFWeight``            — a quantized matrix resident in HBM (forward-pass.ts:89-98)
-* ``repack_gguf_for_gpu``   — raw GGUF bytes -> HBM row layout (gguf-dequant.ts:809-840)
+* ``repack_gguf_for_gpu``   — raw GGUF bytes -> HBM row-tile layout (gguf-dequant.ts:809-840)
 * ``dispatch_matmul_gguf``  — ``C[M,N] = A[M,K] @ dequant(W)^T`` (forward-pass.ts:1496-1544)
 * ``dispatch_projection``   — per-layer projection lookup (forward-pass.ts:1576-1629)
 * ``dequant_ggml``          — dequantize to f32 on the GPU (gguf-dequant.ts:844-868)
@@ -17,7 +17,7 @@ on first use and a missing or unbuilt library raises immediately.
 
 from . import ggml, quantize  # noqa: F401
 from .ggml import (GGML_TYPES, GGMLTypeError, ggml_tensor_bytes, ggml_type_traits,  # noqa: F401
-                   raw_row_bytes, tile_row_bytes)
+                   raw_row_bytes, tile_row_bytes, tiled_bytes)
 from .linear import (GGUFWeight, LayerWeights, concat_rows, dequant_ggml,  # noqa: F401
                      dequant_raw, dispatch_matmul_gguf, dispatch_projection, qlinear,
                      repack_gguf_for_gpu)
@@ -27,5 +27,5 @@ __all__ = [
     "GGML_TYPES", "GGMLTypeError", "GGUFHipError", "GGUFWeight", "LayerWeights",
     "concat_rows", "dequant_ggml", "dequant_raw", "dispatch_matmul_gguf",
     "dispatch_projection", "ggml_tensor_bytes", "ggml_type_traits", "load_library",
-    "qlinear", "raw_row_bytes", "repack_gguf_for_gpu", "tile_row_bytes",
+    "qlinear", "raw_row_bytes", "repack_gguf_for_gpu", "tile_row_bytes", "tiled_bytes",
 ]

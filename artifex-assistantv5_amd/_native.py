@@ -17,10 +17,11 @@ from .ggml import GGMLTypeError
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libgguf_hip.so")
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 ERR_TYPE, ERR_SHAPE, ERR_NULL, ERR_ALIGN, ERR_DTYPE, ERR_BYTES, ERR_HIP = -1, -2, -3, -4, -5, -6, -7
-VARIANT_AUTO, VARIANT_GEMV, VARIANT_SKINNY, VARIANT_GEMM = 0, 1, 2, 3
+VARIANT_AUTO, VARIANT_DECODE, VARIANT_GEMM = 0, 1, 2
+DECODE_MAX_M = 32
 
 # Every symbol include/gguf_hip.h declares: name -> (restype, argtypes)
 _vp, _i32, _i64, _fp = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64, ctypes.c_void_p

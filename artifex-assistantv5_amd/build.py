@@ -19,11 +19,11 @@ ROOT = os.path.dirname(HERE)
 CSRC = os.path.join(HERE, "csrc")
 BUILD = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libgguf_hip.so")
-SOURCES = ["api.hip", "dequant.hip", "gemv.hip", "mfma.hip"]
+SOURCES = ["api.hip", "layout.hip", "decode.hip", "gemm.hip"]
 ARCH = "gfx950"
 
 HIPCC_FLAGS = [
-    f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC",
+    f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC", "-fvisibility=hidden",
     # no packed-fp32 (v_pk_*_f32) instructions anywhere in the device code
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-Wno-unused-result",
@@ -58,7 +58,13 @@ def build(verbose: bool = False) -> str:
     with concurrent.futures.ThreadPoolExecutor(max_workers=len(SOURCES)) as ex:
         objs = list(ex.map(lambda s: _compile(s, verbose), SOURCES))
     tmp = LIB + ".tmp"
-    cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-o", tmp]
+    # Export the C ABI only: kernel stubs and helpers bind locally, so two
+    # builds of the library in one process cannot interpose each other.
+    vers = os.path.join(BUILD, "exports.map")
+    with open(vers, "w", encoding="utf-8") as f:
+        f.write("{ global: gguf_hip_*; local: *; };\n")
+    cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", f"-Wl,--version-script={vers}",
+           *objs, "-o", tmp]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode:
         print(res.stdout + res.stderr, file=sys.stderr)

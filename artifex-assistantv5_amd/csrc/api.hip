@@ -66,12 +66,16 @@ int check_k(int t, int64_t k) {
   return GGUF_HIP_OK;
 }
 
-int64_t tile_row_bytes(int t, int64_t k) {
+// Bytes of one row's GGUF blocks; the row-tile layout stores rows in groups
+// of 16 (common.hpp), so a weight of n rows takes round_up(n, 16) rows.
+int64_t row_bytes(int t, int64_t k) {
   int b, s;
   traits(t, &b, &s);
-  const int64_t nb = k / b;
-  if (t == GGUF_HIP_Q4_K) return 144 * nb;
-  return (s * nb + 15) & ~(int64_t)15;
+  return (k / b) * s;
+}
+
+int64_t tiled_bytes(int t, int64_t n_rows, int64_t k) {
+  return ((n_rows + 15) / 16) * 16 * row_bytes(t, k);
 }
 
 bool aligned(const void *p, uintptr_t a) { return ((uintptr_t)p % a) == 0; }
@@ -117,7 +121,7 @@ int64_t gguf_hip_tile_bytes(int ggml_type, int64_t n_rows, int64_t k) {
   if ((rc = check_k(ggml_type, k))) return rc;
   if (n_rows < 0) return fail(GGUF_HIP_ERR_SHAPE, "[gguf-hip] negative row count");
   ok();
-  return n_rows * tile_row_bytes(ggml_type, k);
+  return tiled_bytes(ggml_type, n_rows, k);
 }
 
 int gguf_hip_repack(const void *raw, int64_t raw_bytes, int ggml_type, int64_t n_rows, int64_t k,
@@ -132,16 +136,16 @@ int gguf_hip_repack(const void *raw, int64_t raw_bytes, int ggml_type, int64_t n
   if (raw_bytes != want_raw)
     return fail(GGUF_HIP_ERR_BYTES, "[repackGGUF] byteLength %lld != expected %lld",
                 (long long)raw_bytes, (long long)want_raw);
-  const int64_t trb = tile_row_bytes(ggml_type, k);
-  if (tile_bytes != n_rows * trb)
+  const int64_t want_tiles = tiled_bytes(ggml_type, n_rows, k);
+  if (tile_bytes != want_tiles)
     return fail(GGUF_HIP_ERR_BYTES, "[repackGGUF] output byteLength %lld != expected %lld",
-                (long long)tile_bytes, (long long)(n_rows * trb));
+                (long long)tile_bytes, (long long)want_tiles);
   if (n_rows == 0) return ok();
   if (!raw || !tiles) return fail(GGUF_HIP_ERR_NULL, "[gguf-hip] null pointer");
   if (!aligned(tiles, 16))
     return fail(GGUF_HIP_ERR_ALIGN, "[gguf-hip] tile buffer must be 16-byte aligned");
   return hip_status(gguf::launch_repack((const uint8_t *)raw, ggml_type, n_rows, k,
-                                        (uint8_t *)tiles, trb, (hipStream_t)stream),
+                                        (uint8_t *)tiles, (hipStream_t)stream),
                     "repack launch");
 }
 
@@ -157,8 +161,7 @@ int gguf_hip_dequant(const void *tiles, int ggml_type, int64_t n_rows, int64_t k
   if (!aligned(tiles, 16))
     return fail(GGUF_HIP_ERR_ALIGN, "[gguf-hip] tile buffer must be 16-byte aligned");
   if (!aligned(out, 4)) return fail(GGUF_HIP_ERR_ALIGN, "[gguf-hip] output must be 4-byte aligned");
-  return hip_status(gguf::launch_dequant((const uint8_t *)tiles, ggml_type, n_rows, k,
-                                         tile_row_bytes(ggml_type, k), out, ldo,
+  return hip_status(gguf::launch_dequant((const uint8_t *)tiles, ggml_type, n_rows, k, out, ldo,
                                          (hipStream_t)stream),
                     "dequant launch");
 }
@@ -195,9 +198,6 @@ int gguf_hip_matmul_variant(const void *x, int x_type, int64_t ldx, const void *
     return fail(GGUF_HIP_ERR_SHAPE, "[gguf-hip] M or N too large");
   if (m > 1 && ldx < k) return fail(GGUF_HIP_ERR_SHAPE, "[gguf-hip] ldx < K");
   if (m > 1 && ldy < n) return fail(GGUF_HIP_ERR_SHAPE, "[gguf-hip] ldy < N");
-  if (variant == GGUF_HIP_VARIANT_SKINNY && m > 32)
-    return fail(GGUF_HIP_ERR_SHAPE, "[gguf-hip] skinny variant needs M <= 32, got %lld",
-                (long long)m);
   if (m == 0 || n == 0) return ok();
   if (!x || !tiles || !y) return fail(GGUF_HIP_ERR_NULL, "[gguf-hip] null pointer");
   const int64_t esize = x_type == GGUF_HIP_F32 ? 4 : 2;
@@ -207,28 +207,13 @@ int gguf_hip_matmul_variant(const void *x, int x_type, int64_t ldx, const void *
     return fail(GGUF_HIP_ERR_ALIGN, "[gguf-hip] activation rows must be 16-byte aligned");
   if (!aligned(y, 4)) return fail(GGUF_HIP_ERR_ALIGN, "[gguf-hip] output must be 4-byte aligned");
 
-  const int64_t trb = tile_row_bytes(ggml_type, k);
   const hipStream_t s = (hipStream_t)stream;
   if (variant == GGUF_HIP_VARIANT_AUTO)
-    variant = m == 1 ? GGUF_HIP_VARIANT_GEMV
-                     : (m <= 32 ? GGUF_HIP_VARIANT_SKINNY : GGUF_HIP_VARIANT_GEMM);
-  hipError_t e = hipSuccess;
-  if (variant == GGUF_HIP_VARIANT_GEMV) {
-    const char *xb = (const char *)x;
-    for (int64_t m0 = 0; m0 < m && e == hipSuccess; m0 += 65535) {
-      const int64_t mc = (m - m0) < 65535 ? (m - m0) : 65535;
-      e = gguf::launch_gemv(xb + m0 * ldx * esize, x_type, ldx, (const uint8_t *)tiles, ggml_type,
-                            n, k, trb, y + m0 * ldy, ldy, mc, s);
-    }
-  } else {
-    const char *xb = (const char *)x;
-    const int64_t chunk = (int64_t)65535 * 32;  // grid.y cap at the smallest BM
-    for (int64_t m0 = 0; m0 < m && e == hipSuccess; m0 += chunk) {
-      const int64_t mc = (m - m0) < chunk ? (m - m0) : chunk;
-      e = gguf::launch_mfma(xb + m0 * ldx * esize, x_type, ldx, (const uint8_t *)tiles, ggml_type,
-                            n, k, trb, y + m0 * ldy, ldy, mc, variant == GGUF_HIP_VARIANT_SKINNY, s);
-    }
-  }
+    variant = m <= GGUF_HIP_DECODE_MAX_M ? GGUF_HIP_VARIANT_DECODE : GGUF_HIP_VARIANT_GEMM;
+  const hipError_t e =
+      variant == GGUF_HIP_VARIANT_DECODE
+          ? gguf::launch_decode(x, x_type, ldx, (const uint8_t *)tiles, ggml_type, n, k, y, ldy, m, s)
+          : gguf::launch_gemm(x, x_type, ldx, (const uint8_t *)tiles, ggml_type, n, k, y, ldy, m, s);
   return hip_status(e, "matmul launch");
 }
 

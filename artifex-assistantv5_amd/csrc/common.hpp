@@ -1,5 +1,5 @@
-// Shared device helpers and the internal launcher interface of libgguf_hip.
-// gfx950 (CDNA4) only: wave64, MFMA, 160 KB LDS per CU.
+// Shared device helpers, the HBM row-tile layout and the internal launcher
+// interface of libgguf_hip.  gfx950 (CDNA4) only: wave64, MFMA, 160 KB LDS/CU.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -9,26 +9,65 @@ namespace gguf {
 
 typedef _Float16 half_t;
 typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
+typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
 typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
 typedef float float4_t __attribute__((ext_vector_type(4)));
 
 constexpr int kWave = 64;
 
+// ---------------------------------------------------------------------------
+// HBM row-tile layout.
+//
+// A weight of N rows x K columns is stored as ceil(N/16) row tiles of 16
+// consecutive rows (rows past N are zero).  A tile holds, for each "unit" of
+// the row (a 256-element superblock for Q4_K / Q6_K, a 32-element block for
+// Q8_0) in K order, one tile-unit of 16 * (GGUF block bytes): the 16 rows'
+// blocks interleaved at 16-byte (Q8_0 quant bytes: 8-byte) granularity so
+// that one wave-wide load reads contiguous memory and lane (r = lane & 15,
+// g = lane >> 4) receives exactly the bytes its MFMA operand needs:
+//
+//   Q4_K (2304 B)  [   0,  256) header of row r at 16 r: d, dmin, scales[12]
+//                  [ 256, 2304) piece (cp, g, r) at 256 + ((4 cp + g) * 16 + r) * 16:
+//                               qs[64 cp + 8 g, +8) | qs[64 cp + 32 + 8 g, +8)
+//   Q6_K (3360 B)  [   0, 3072) piece (v, g, r) at ((4 v + g) * 16 + r) * 16 holds
+//                               dwords 4v..4v+3 of the lane's 12 quant dwords;
+//                               for i = 2 hf + lh:  dword 3i   = ql[64 hf + 16 lh + 4 g, +4)
+//                                                   dword 3i+1 = ql[64 hf + 32 + 16 lh + 4 g, +4)
+//                                                   dword 3i+2 = qh[32 hf + 16 lh + 4 g, +4)
+//                  [3072, 3328) scales sc[16] of row r at 3072 + 16 r
+//                  [3328, 3360) d of row r at 3328 + 2 r
+//   Q8_0 ( 544 B)  [   0,   32) d of row r at 2 r
+//                  [  32,  544) piece (g, r) at 32 + (16 g + r) * 8: qs[8 g, +8)
+//
+// Byte offset of (tile t, unit u) = (t * units_per_row + u) * tile_unit_bytes.
+// No bytes are added: a tile is exactly 16 rows of GGUF blocks.
+// ---------------------------------------------------------------------------
+constexpr int kTileRows = 16;
+
+template <int TYPE>
+struct Fmt;
+template <>
+struct Fmt<12> {  // Q4_K
+  static constexpr int UE = 256, UB = 144, TU = 16 * 144;
+};
+template <>
+struct Fmt<14> {  // Q6_K
+  static constexpr int UE = 256, UB = 210, TU = 16 * 210;
+};
+template <>
+struct Fmt<8> {  // Q8_0
+  static constexpr int UE = 32, UB = 34, TU = 16 * 34;
+};
+
+__host__ __device__ inline int unit_elems(int type) { return type == 8 ? 32 : 256; }
+__host__ __device__ inline int unit_bytes(int type) {
+  return type == 8 ? 34 : (type == 12 ? 144 : 210);
+}
+
 // IEEE half bits -> f32 with the hardware converter (subnormals, Inf and NaN
 // preserved), the same mapping as f16ToF32 in gguf-dequant.ts:64-71.
 __device__ __forceinline__ float h2f(uint32_t bits16) {
   return (float)__builtin_bit_cast(half_t, (uint16_t)(bits16 & 0xFFFFu));
-}
-
-// The two halves of a 32-bit word as f16 values.  Used with masks that leave a
-// small unsigned integer q in each half: the half then holds q * 2^-24 (an f16
-// subnormal) exactly, and `(float)h.x * a` compiles to v_fma_mix_f32, which
-// converts the half and multiplies in one instruction.  The 2^24 factor is
-// folded into the per-block scale afterwards (an exact power of two).
-__device__ __forceinline__ half2_t as_h2(uint32_t w) { return __builtin_bit_cast(half2_t, w); }
-
-__device__ __forceinline__ float fmix(half_t q, float a, float acc) {
-  return __builtin_fmaf((float)q, a, acc);
 }
 
 // 6-bit (scale, min) pair j of a Q4_K superblock from its 12 scale bytes held
@@ -49,10 +88,25 @@ __device__ __forceinline__ void q4k_scale_min(int j, uint32_t s0, uint32_t s1, u
   }
 }
 
+// All eight 6-bit scales and mins of a Q4_K superblock, one per byte:
+// sc_lo = scales 0-3, sc_hi = scales 4-7, m_lo / m_hi likewise.
+__device__ __forceinline__ void q4k_scales_packed(uint32_t s0, uint32_t s1, uint32_t s2,
+                                                  uint32_t &sc_lo, uint32_t &sc_hi,
+                                                  uint32_t &m_lo, uint32_t &m_hi) {
+  sc_lo = s0 & 0x3F3F3F3Fu;
+  m_lo = s1 & 0x3F3F3F3Fu;
+  sc_hi = (s2 & 0x0F0F0F0Fu) | ((s0 >> 2) & 0x30303030u);
+  m_hi = ((s2 >> 4) & 0x0F0F0F0Fu) | ((s1 >> 2) & 0x30303030u);
+}
+
+__device__ __forceinline__ float ubyte(uint32_t w, int i) {
+  return (float)((w >> (8 * i)) & 0xFFu);
+}
+
 __device__ __forceinline__ uint4 ldg16(const void *p) { return *(const uint4 *)p; }
 
-// Streaming (read-once) 16-byte load of weight data: nontemporal so the
-// weight stream does not evict activations from L1/L2.
+// Streaming (read-once) 16-byte load of weight data: nontemporal, so the
+// weight stream does not evict the activations from the caches.
 __device__ __forceinline__ uint4 ldg16_stream(const void *p) {
   const uint4 *q = (const uint4 *)p;
   uint4 r;
@@ -60,6 +114,14 @@ __device__ __forceinline__ uint4 ldg16_stream(const void *p) {
   r.y = __builtin_nontemporal_load(&q->y);
   r.z = __builtin_nontemporal_load(&q->z);
   r.w = __builtin_nontemporal_load(&q->w);
+  return r;
+}
+
+__device__ __forceinline__ uint2 ldg8_stream(const void *p) {
+  const uint2 *q = (const uint2 *)p;
+  uint2 r;
+  r.x = __builtin_nontemporal_load(&q->x);
+  r.y = __builtin_nontemporal_load(&q->y);
   return r;
 }
 
@@ -72,16 +134,14 @@ __device__ __forceinline__ uint4 ldg16_stream(const void *p) {
 namespace gguf {
 
 hipError_t launch_repack(const uint8_t *raw, int type, int64_t n_rows, int64_t k, uint8_t *tiles,
-                         int64_t tile_row_bytes, hipStream_t s);
-hipError_t launch_dequant(const uint8_t *tiles, int type, int64_t n_rows, int64_t k,
-                          int64_t tile_row_bytes, float *out, int64_t ldo, hipStream_t s);
+                         hipStream_t s);
+hipError_t launch_dequant(const uint8_t *tiles, int type, int64_t n_rows, int64_t k, float *out,
+                          int64_t ldo, hipStream_t s);
 hipError_t launch_dequant_raw(const uint8_t *raw, int type, int64_t n_elems, float *out,
                               hipStream_t s);
-hipError_t launch_gemv(const void *x, int x_type, int64_t ldx, const uint8_t *tiles, int type,
-                       int64_t n, int64_t k, int64_t tile_row_bytes, float *y, int64_t ldy,
-                       int64_t m, hipStream_t s);
-hipError_t launch_mfma(const void *x, int x_type, int64_t ldx, const uint8_t *tiles, int type,
-                       int64_t n, int64_t k, int64_t tile_row_bytes, float *y, int64_t ldy,
-                       int64_t m, bool skinny, hipStream_t s);
+hipError_t launch_decode(const void *x, int x_type, int64_t ldx, const uint8_t *tiles, int type,
+                         int64_t n, int64_t k, float *y, int64_t ldy, int64_t m, hipStream_t s);
+hipError_t launch_gemm(const void *x, int x_type, int64_t ldx, const uint8_t *tiles, int type,
+                       int64_t n, int64_t k, float *y, int64_t ldy, int64_t m, hipStream_t s);
 
 }  // namespace gguf

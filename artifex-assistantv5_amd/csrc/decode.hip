@@ -1,0 +1,644 @@
+// MFMA decode kernel: y[m, n] = sum_k x[m, k] * dequant(W)[n, k] for up to
+// 32 activation rows, one pass over the weights, f32 result.
+//
+// Replaces the reference's decode GEMVs matmul_gguf_q8_0 /
+// matmul_gguf_q4_k_tiled_v4 / matmul_gguf_q6_k_tiled
+// (webgpu/src/shaders/matmul_gguf.wgsl:2102-2133, :3191-3245, :2406-2464),
+// and its batched decode, which re-reads the weights once per activation row
+// (grid.y = M, webgpu/src/engine/forward-pass.ts:1536-1539).
+//
+// Arithmetic.  The reference computes sum_k a_k * (d1 * q_k - min1) per unit
+// in f32.  Here the quantized codes q are fed to the matrix cores *exactly*:
+// a code masked into the low bits of an f16 is the subnormal q * 2^-24
+// (Q4_K high nibbles: 16 q * 2^-24; Q8_0: (q + 128) * 2^-24; Q6_K: the
+// unsigned 6-bit q + 32).  Activations are split into f16 hi + lo parts
+// (x = hi + lo to 22 significant bits; f16 activations are exact in hi
+// alone).  One v_mfma_f32_16x16x32_f16 (Q6_K: 16x16x16, one 16-element scale
+// group) then yields the exact-product, f32-accumulated dot of one scale
+// group of 16 weight rows with up to 16 activation rows, and the group's
+// scale, min and code offset are applied in f32 afterwards:
+//     acc += (d * sc * 2^24) * D  -  (dmin * m + offset * d * sc) * sum(x of group).
+// Nothing is rounded to f16 on the weight side, unlike an fp16 dequant-GEMM.
+//
+// Work split.  A workgroup is four waves; each wave owns one 16-row tile of
+// the weight (lane (r, g) = (lane & 15, lane >> 4) holds row r's operand
+// bytes, loaded from the row-tile layout as 1 KB-contiguous wave loads) and
+// every KS-th unit of K.  TS = 4 / KS tiles share a workgroup.  Activations
+// are staged per chunk of units into LDS (hi, lo, per-group sums), shared by
+// all waves.  Unit loads are double-buffered across chunks so the next
+// chunk's weight bytes are in flight while the current one is computed.  The
+// KS partial sums of a row are added in a fixed order (deterministic).
+#include "common.hpp"
+
+namespace gguf {
+
+namespace {
+
+constexpr float kTwo24 = 16777216.0f;  // 2^24
+constexpr float kTwo20 = 1048576.0f;   // 2^20
+constexpr int kXPad = 8;               // halves of padding per staged activation row
+
+template <int TYPE>
+struct Unit;
+template <>
+struct Unit<12> {  // header, qs pieces cp = 0, 1
+  uint4 h, a, b;
+};
+template <>
+struct Unit<14> {  // quant pieces v = 0..2, scales, d
+  uint4 p0, p1, p2, sc;
+  uint32_t d;
+};
+template <>
+struct Unit<8> {  // qs bytes 8g..8g+7, d
+  uint2 q;
+  uint32_t d;
+};
+
+// Scale group size (elements sharing one scale) and units in flight per wave.
+#ifndef GGUF_DECODE_P_Q4K
+#define GGUF_DECODE_P_Q4K 6
+#endif
+#ifndef GGUF_DECODE_P_Q6K
+#define GGUF_DECODE_P_Q6K 2
+#endif
+#ifndef GGUF_DECODE_P_Q8
+#define GGUF_DECODE_P_Q8 16
+#endif
+template <int TYPE>
+struct Dec;
+template <>
+struct Dec<12> {
+  static constexpr int GS = 32, P = GGUF_DECODE_P_Q4K;
+};
+template <>
+struct Dec<14> {
+  static constexpr int GS = 16, P = GGUF_DECODE_P_Q6K;
+};
+template <>
+struct Dec<8> {
+  static constexpr int GS = 32, P = GGUF_DECODE_P_Q8;
+};
+
+__device__ __forceinline__ void load_unit(const uint8_t *tu, int r, int g, Unit<12> &u) {
+  u.h = ldg16_stream(tu + 16 * r);
+  u.a = ldg16_stream(tu + 256 + (16 * g + r) * 16);
+  u.b = ldg16_stream(tu + 256 + (16 * (4 + g) + r) * 16);
+}
+__device__ __forceinline__ void load_unit(const uint8_t *tu, int r, int g, Unit<14> &u) {
+  u.p0 = ldg16_stream(tu + (16 * g + r) * 16);
+  u.p1 = ldg16_stream(tu + (16 * (4 + g) + r) * 16);
+  u.p2 = ldg16_stream(tu + (16 * (8 + g) + r) * 16);
+  u.sc = ldg16_stream(tu + 3072 + 16 * r);
+  u.d = *(const uint16_t *)(tu + 3328 + 2 * r);
+}
+__device__ __forceinline__ void load_unit(const uint8_t *tu, int r, int g, Unit<8> &u) {
+  u.q = ldg8_stream(tu + 32 + (16 * g + r) * 8);
+  u.d = *(const uint16_t *)(tu + 2 * r);
+}
+
+__device__ __forceinline__ half8_t as_h8(uint32_t a, uint32_t b, uint32_t c, uint32_t d) {
+  return __builtin_bit_cast(half8_t, make_uint4(a, b, c, d));
+}
+__device__ __forceinline__ half4_t as_h4(uint32_t a, uint32_t b) {
+  return __builtin_bit_cast(half4_t, make_uint2(a, b));
+}
+
+// Dynamic LDS of the decode kernel.  Stage records offsets into it (not
+// pointers), so every access below is an explicit ds_read / ds_write.
+extern __shared__ __align__(16) unsigned char g_lds[];
+
+struct Stage {
+  int xh, xl;  // half offsets of [M][ce + kXPad] hi and lo parts, quads in (0, 2, 1, 3) order
+  int xs;      // float offset of [ce / GS][MS] per-group sums of hi + lo, rows M..MS-1 zero
+  int zero;    // half offset of kZeroHalves zeros: the A operand of lanes that contribute nothing
+  int ld;      // ce + kXPad
+  int ms;      // 16 * MT
+};
+
+__device__ __forceinline__ half8_t lds_h8(int half_off) {
+  return *(const half8_t *)((const half_t *)g_lds + half_off);
+}
+__device__ __forceinline__ half4_t lds_h4(int half_off) {
+  return *(const half4_t *)((const half_t *)g_lds + half_off);
+}
+__device__ __forceinline__ float lds_f(int float_off) { return ((const float *)g_lds)[float_off]; }
+__device__ __forceinline__ float4 lds_f4(int float_off) {
+  return *(const float4 *)((const float *)g_lds + float_off);
+}
+
+// D = (hi + lo parts of A) x B; lanes with on == false read the zero operand.
+template <int PARTS>
+__device__ __forceinline__ float4_t mfma32(int ah, int al, int zero, half8_t b, bool on) {
+  float4_t d = {0.f, 0.f, 0.f, 0.f};
+  d = __builtin_amdgcn_mfma_f32_16x16x32_f16(lds_h8(on ? ah : zero), b, d, 0, 0, 0);
+  if (PARTS == 2) d = __builtin_amdgcn_mfma_f32_16x16x32_f16(lds_h8(on ? al : zero), b, d, 0, 0, 0);
+  return d;
+}
+
+template <int PARTS>
+__device__ __forceinline__ float4_t mfma16(int ah, int al, int zero, half4_t b, bool on) {
+  float4_t d = {0.f, 0.f, 0.f, 0.f};
+  d = __builtin_amdgcn_mfma_f32_16x16x16f16(lds_h4(on ? ah : zero), b, d, 0, 0, 0);
+  if (PARTS == 2) d = __builtin_amdgcn_mfma_f32_16x16x16f16(lds_h4(on ? al : zero), b, d, 0, 0, 0);
+  return d;
+}
+
+// acc[i] += s * D[i] - o * xs[i] for the MR activation rows a lane holds.
+template <int MR>
+__device__ __forceinline__ void apply(float (&acc)[4], const float4_t &D, float s, float o, int xs) {
+  if (MR == 1) {
+    acc[0] += s * D[0] - o * lds_f(xs);
+  } else {
+    const float4 v = lds_f4(xs);
+    acc[0] += s * D[0] - o * v.x;
+    acc[1] += s * D[1] - o * v.y;
+    acc[2] += s * D[2] - o * v.z;
+    acc[3] += s * D[3] - o * v.w;
+  }
+}
+
+// Shared-memory view of one staged chunk of activations.
+constexpr int kZeroHalves = 32;
+
+// ---------------------------------------------------------------------------
+// Single activation row (M = 1).  The 16 A rows of the MFMA are then free to
+// act as selectors: row 2j + p carries part p (hi / lo) of the activations of
+// scale group j and is zero in every MFMA that does not belong to group j, so
+// one accumulator chain over a unit's groups leaves group j's dot in rows
+// 2j, 2j + 1.  Lane (n, g) ends up holding the groups of "its" quarter and
+// applies their scales; a 4-lane sum per row finishes the unit.
+// ---------------------------------------------------------------------------
+
+// Q4_K: 8 sub-blocks, one chain; lane (n, g) keeps sub-blocks 2g (lo nibbles
+// of chunk g) and 2g + 1 (hi nibbles).
+template <int PARTS>
+__device__ __forceinline__ void unit_m1(const Unit<12> &u, const Stage &st, int ul, int lane,
+                                        float &acc) {
+  const int r = lane & 15, g = lane >> 4;
+  const int jo = r >> 1;
+  const bool live = PARTS == 2 || (r & 1) == 0;
+  const int own = (st.xh + (r & 1) * (st.xl - st.xh)) + 256 * ul + 8 * g;
+  const uint32_t w[8] = {u.a.x, u.a.y, u.a.z, u.a.w, u.b.x, u.b.y, u.b.z, u.b.w};
+  float4_t D = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+    const uint32_t wa = w[2 * c], wb = w[2 * c + 1];
+    const uint32_t wa8 = wa >> 8, wb8 = wb >> 8;
+    const half8_t blo = as_h8(wa & 0x000F000Fu, wa8 & 0x000F000Fu, wb & 0x000F000Fu, wb8 & 0x000F000Fu);
+    const half8_t bhi = as_h8(wa & 0x00F000F0u, wa8 & 0x00F000F0u, wb & 0x00F000F0u, wb8 & 0x00F000F0u);
+    const int pa = (live && jo == 2 * c) ? own + 64 * c : st.zero;
+    const int pb = (live && jo == 2 * c + 1) ? own + 64 * c + 32 : st.zero;
+    D = __builtin_amdgcn_mfma_f32_16x16x32_f16(lds_h8(pa), blo, D, 0, 0, 0);
+    D = __builtin_amdgcn_mfma_f32_16x16x32_f16(lds_h8(pb), bhi, D, 0, 0, 0);
+  }
+  // rows 4g + i: sub-block 2g (i = 0, 1) and 2g + 1 (i = 2, 3), part i & 1
+  const float dlo = D[0] + D[1], dhi = D[2] + D[3];
+  uint32_t sc_lo, sc_hi, m_lo, m_hi;
+  q4k_scales_packed(u.h.y, u.h.z, u.h.w, sc_lo, sc_hi, m_lo, m_hi);
+  const uint32_t scw = g < 2 ? sc_lo : sc_hi, mw = g < 2 ? m_lo : m_hi;
+  const int sh = 16 * (g & 1);
+  const float sc0 = (float)((scw >> sh) & 0xFFu), sc1 = (float)((scw >> (sh + 8)) & 0xFFu);
+  const float m0 = (float)((mw >> sh) & 0xFFu), m1 = (float)((mw >> (sh + 8)) & 0xFFu);
+  const int xs = st.xs + (ul * 8 + 2 * g) * st.ms;
+  const float d = h2f(u.h.x), dmin = h2f(u.h.x >> 16);
+  acc += (d * kTwo24) * (sc0 * dlo) + (d * kTwo20) * (sc1 * dhi) -
+         dmin * (m0 * lds_f(xs) + m1 * lds_f(xs + st.ms));
+}
+
+// Q6_K: 16 groups of 16 elements, two chains of 8 (halves hf = 0, 1); lane
+// (n, g) keeps groups 8 hf + 2 g + lh, lh = 0, 1.
+template <int PARTS>
+__device__ __forceinline__ void unit_m1(const Unit<14> &u, const Stage &st, int ul, int lane,
+                                        float &acc) {
+  const int r = lane & 15, g = lane >> 4;
+  const int so = r >> 1;
+  const bool live = PARTS == 2 || (r & 1) == 0;
+  const int own = (st.xh + (r & 1) * (st.xl - st.xh)) + 256 * ul + 4 * g;
+  const uint32_t dw[12] = {u.p0.x, u.p0.y, u.p0.z, u.p0.w, u.p1.x, u.p1.y,
+                           u.p1.z, u.p1.w, u.p2.x, u.p2.y, u.p2.z, u.p2.w};
+  const uint32_t scw[4] = {u.sc.x, u.sc.y, u.sc.z, u.sc.w};
+  const float d = h2f(u.d);
+  float sd = 0.f, sx = 0.f;
+#pragma unroll
+  for (int hf = 0; hf < 2; ++hf) {
+    float4_t D = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int lh = 0; lh < 2; ++lh) {
+      const int i = 2 * hf + lh;
+      const uint32_t qa = dw[3 * i], qb = dw[3 * i + 1], qh = dw[3 * i + 2];
+      const uint32_t v[4] = {(qa & 0x0F0F0F0Fu) | ((qh << 4) & 0x30303030u),
+                             (qb & 0x0F0F0F0Fu) | ((qh << 2) & 0x30303030u),
+                             ((qa >> 4) & 0x0F0F0F0Fu) | (qh & 0x30303030u),
+                             ((qb >> 4) & 0x0F0F0F0Fu) | ((qh >> 2) & 0x30303030u)};
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        const half4_t b = as_h4(v[t] & 0x00FF00FFu, (v[t] >> 8) & 0x00FF00FFu);
+        const int pa = (live && so == 2 * t + lh) ? own + 128 * hf + 32 * t + 16 * lh : st.zero;
+        D = __builtin_amdgcn_mfma_f32_16x16x16f16(lds_h4(pa), b, D, 0, 0, 0);
+      }
+    }
+    // rows 4g + i: group 8 hf + 2 g + (i >> 1), part i & 1
+    const uint32_t sw = scw[2 * hf + (g >> 1)];
+    const int sh = 16 * (g & 1);
+    const float s0 = (float)(int8_t)((sw >> sh) & 0xFFu), s1 = (float)(int8_t)((sw >> (sh + 8)) & 0xFFu);
+    const int xs = st.xs + (ul * 16 + 8 * hf + 2 * g) * st.ms;
+    sd += s0 * (D[0] + D[1]) + s1 * (D[2] + D[3]);
+    sx += s0 * lds_f(xs) + s1 * lds_f(xs + st.ms);
+  }
+  acc += (d * kTwo24) * sd - (d * 32.f) * sx;
+}
+
+// Q8_0: one block; rows 0 (hi) and 1 (lo) carry the activations, lanes g = 0
+// hold the result.
+template <int PARTS>
+__device__ __forceinline__ void unit_m1(const Unit<8> &u, const Stage &st, int ul, int lane,
+                                        float &acc) {
+  const int r = lane & 15, g = lane >> 4;
+  const bool live = r == 0 || (PARTS == 2 && r == 1);
+  const int pa = live ? st.xh + r * (st.xl - st.xh) + 32 * ul + 8 * g : st.zero;
+  const uint32_t u0 = u.q.x ^ 0x80808080u, u1 = u.q.y ^ 0x80808080u;
+  const half8_t b = as_h8(u0 & 0x00FF00FFu, (u0 >> 8) & 0x00FF00FFu, u1 & 0x00FF00FFu,
+                          (u1 >> 8) & 0x00FF00FFu);
+  float4_t D = {0.f, 0.f, 0.f, 0.f};
+  D = __builtin_amdgcn_mfma_f32_16x16x32_f16(lds_h8(pa), b, D, 0, 0, 0);
+  const float d = h2f(u.d);
+  const float v = (d * kTwo24) * (D[0] + D[1]) - (d * 128.f) * lds_f(st.xs + ul * st.ms);
+  acc += g == 0 ? v : 0.f;
+}
+
+// One unit of Q4_K: 8 sub-blocks x MT activation tiles.  Per activation row
+// the sub-block dots are folded as
+//   acc += d 2^24 sum_even sc_j D_j + d 2^20 sum_odd sc_j D_j - dmin sum_j m_j xs_j
+// (odd sub-blocks hold high nibbles, coded as 16 q).
+template <int PARTS, int MT, int MR>
+__device__ __forceinline__ void unit_compute(const Unit<12> &u, const Stage &st, int ul, int lane,
+                                             int M, float (&acc)[MT][4]) {
+  const int r = lane & 15, g = lane >> 4;
+  uint32_t sc_lo, sc_hi, m_lo, m_hi;
+  q4k_scales_packed(u.h.y, u.h.z, u.h.w, sc_lo, sc_hi, m_lo, m_hi);
+  const uint32_t w[8] = {u.a.x, u.a.y, u.a.z, u.a.w, u.b.x, u.b.y, u.b.z, u.b.w};
+  float se[MT][4], so[MT][4], sm[MT][4];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) se[mt][i] = so[mt][i] = sm[mt][i] = 0.f;
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+    const uint32_t wa = w[2 * c], wb = w[2 * c + 1];
+    const uint32_t wa8 = wa >> 8, wb8 = wb >> 8;
+    const half8_t blo = as_h8(wa & 0x000F000Fu, wa8 & 0x000F000Fu, wb & 0x000F000Fu, wb8 & 0x000F000Fu);
+    const half8_t bhi = as_h8(wa & 0x00F000F0u, wa8 & 0x00F000F0u, wb & 0x00F000F0u, wb8 & 0x00F000F0u);
+    const uint32_t scw = c < 2 ? sc_lo : sc_hi, mw = c < 2 ? m_lo : m_hi;
+    const int b0 = (2 * c) & 3, b1 = (2 * c + 1) & 3;
+    const float sc0 = ubyte(scw, b0), m0 = ubyte(mw, b0);
+    const float sc1 = ubyte(scw, b1), m1 = ubyte(mw, b1);
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      const int m = 16 * mt + r;
+      const bool on = m < M;
+      const int off = m * st.ld + 256 * ul + 64 * c + 8 * g;
+      const float4_t D0 = mfma32<PARTS>(st.xh + off, st.xl + off, st.zero, blo, on);
+      const float4_t D1 = mfma32<PARTS>(st.xh + off + 32, st.xl + off + 32, st.zero, bhi, on);
+      const int xs = st.xs + (ul * 8 + 2 * c) * st.ms + 16 * mt + 4 * g;
+      if (MR == 1) {
+        se[mt][0] += sc0 * D0[0];
+        so[mt][0] += sc1 * D1[0];
+        sm[mt][0] += m0 * lds_f(xs) + m1 * lds_f(xs + st.ms);
+      } else {
+        const float4 x0 = lds_f4(xs), x1 = lds_f4(xs + st.ms);
+        const float xv0[4] = {x0.x, x0.y, x0.z, x0.w}, xv1[4] = {x1.x, x1.y, x1.z, x1.w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          se[mt][i] += sc0 * D0[i];
+          so[mt][i] += sc1 * D1[i];
+          sm[mt][i] += m0 * xv0[i] + m1 * xv1[i];
+        }
+      }
+    }
+  }
+  const float d = h2f(u.h.x), dmin = h2f(u.h.x >> 16);
+  const float d24 = d * kTwo24, d20 = d * kTwo20;
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int i = 0; i < MR; ++i)
+      acc[mt][i] += d24 * se[mt][i] + d20 * so[mt][i] - dmin * sm[mt][i];
+}
+
+// One unit of Q6_K: 16 scale groups of 16 elements.
+template <int PARTS, int MT, int MR>
+__device__ __forceinline__ void unit_compute(const Unit<14> &u, const Stage &st, int ul, int lane,
+                                             int M, float (&acc)[MT][4]) {
+  const int r = lane & 15, g = lane >> 4;
+  const float d = h2f(u.d);
+  const float d24 = d * kTwo24, d32 = d * 32.f;
+  const uint32_t dw[12] = {u.p0.x, u.p0.y, u.p0.z, u.p0.w, u.p1.x, u.p1.y,
+                           u.p1.z, u.p1.w, u.p2.x, u.p2.y, u.p2.z, u.p2.w};
+  const uint32_t scw[4] = {u.sc.x, u.sc.y, u.sc.z, u.sc.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int hf = i >> 1, lh = i & 1;
+    const uint32_t qa = dw[3 * i], qb = dw[3 * i + 1], qh = dw[3 * i + 2];
+    const uint32_t v[4] = {(qa & 0x0F0F0F0Fu) | ((qh << 4) & 0x30303030u),
+                           (qb & 0x0F0F0F0Fu) | ((qh << 2) & 0x30303030u),
+                           ((qa >> 4) & 0x0F0F0F0Fu) | (qh & 0x30303030u),
+                           ((qb >> 4) & 0x0F0F0F0Fu) | ((qh >> 2) & 0x30303030u)};
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const half4_t b = as_h4(v[t] & 0x00FF00FFu, (v[t] >> 8) & 0x00FF00FFu);
+      const int s = 8 * hf + 2 * t + lh;
+      const float scf = (float)(int8_t)((scw[s >> 2] >> (8 * (s & 3))) & 0xFFu);
+      const float sd = d24 * scf, so = d32 * scf;
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        const int m = 16 * mt + r;
+        const int off = m * st.ld + 256 * ul + 128 * hf + 32 * t + 16 * lh + 4 * g;
+        const float4_t D = mfma16<PARTS>(st.xh + off, st.xl + off, st.zero, b, m < M);
+        apply<MR>(acc[mt], D, sd, so, st.xs + (ul * 16 + s) * st.ms + 16 * mt + 4 * g);
+      }
+    }
+  }
+}
+
+// One Q8_0 block.
+template <int PARTS, int MT, int MR>
+__device__ __forceinline__ void unit_compute(const Unit<8> &u, const Stage &st, int ul, int lane,
+                                             int M, float (&acc)[MT][4]) {
+  const int r = lane & 15, g = lane >> 4;
+  const uint32_t u0 = u.q.x ^ 0x80808080u, u1 = u.q.y ^ 0x80808080u;
+  const half8_t b = as_h8(u0 & 0x00FF00FFu, (u0 >> 8) & 0x00FF00FFu, u1 & 0x00FF00FFu,
+                          (u1 >> 8) & 0x00FF00FFu);
+  const float d = h2f(u.d);
+  const float sd = d * kTwo24, so = d * 128.f;
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) {
+    const int m = 16 * mt + r;
+    const int off = m * st.ld + 32 * ul + 8 * g;
+    const float4_t D = mfma32<PARTS>(st.xh + off, st.xl + off, st.zero, b, m < M);
+    apply<MR>(acc[mt], D, sd, so, st.xs + ul * st.ms + 16 * mt + 4 * g);
+  }
+}
+
+// Stage activations x[0:M, k0 : k0 + ce) into LDS (zeros past K).
+// Activation staging.  A chunk of M x ce activations is converted quad by
+// quad (4 consecutive elements per thread and step).  When a chunk has at most
+// 256 * kXQ quads, its loads are issued one chunk ahead into registers
+// (XPre) -- before the weight loads they would otherwise queue behind, since
+// the vector-memory counter retires loads in issue order.
+constexpr int kXQ = 4;
+
+struct XPre {
+  float v[kXQ][4];
+};
+
+template <typename XT>
+__device__ __forceinline__ void load_quad(const XT *__restrict__ x, int64_t ldx, int K, int k0,
+                                          int quads, int total, int q, float (&v)[4]) {
+  v[0] = v[1] = v[2] = v[3] = 0.f;
+  if (q < total) {
+    const int m = q / quads, e = 4 * (q - m * quads), k = k0 + e;
+    if (k < K) {
+      if constexpr (sizeof(XT) == 4) {
+        const float4 t = *(const float4 *)(x + (int64_t)m * ldx + k);
+        v[0] = t.x; v[1] = t.y; v[2] = t.z; v[3] = t.w;
+      } else {
+        const half4_t t = *(const half4_t *)(x + (int64_t)m * ldx + k);
+        v[0] = (float)t[0]; v[1] = (float)t[1]; v[2] = (float)t[2]; v[3] = (float)t[3];
+      }
+    }
+  }
+}
+
+// hi / lo parts (quad stored in (0, 2, 1, 3) order) and the group sums of hi + lo.
+// Groups never straddle a wave, so the shuffle reduction stays within one group.
+template <int PARTS, int GS>
+__device__ __forceinline__ void store_quad(int quads, int total, int q, const float (&v)[4],
+                                           const Stage &st) {
+  half_t hi[4], lo[4];
+  float s = 0.f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    hi[i] = (half_t)v[i];
+    lo[i] = (half_t)(v[i] - (float)hi[i]);
+    s += (float)hi[i] + (PARTS == 2 ? (float)lo[i] : 0.f);
+  }
+#pragma unroll
+  for (int mask = 1; mask < GS / 4; mask <<= 1) s += __shfl_xor(s, mask);
+  if (q < total) {
+    const int m = q / quads, e = 4 * (q - m * quads);
+    half_t *lh = (half_t *)g_lds;
+    *(half4_t *)(lh + st.xh + m * st.ld + e) = half4_t{hi[0], hi[2], hi[1], hi[3]};
+    if (PARTS == 2) *(half4_t *)(lh + st.xl + m * st.ld + e) = half4_t{lo[0], lo[2], lo[1], lo[3]};
+    if ((e & (GS - 1)) == 0) ((float *)g_lds)[st.xs + (e / GS) * st.ms + m] = s;
+  }
+}
+
+template <typename XT>
+__device__ __forceinline__ void prefetch_x(const XT *__restrict__ x, int64_t ldx, int M, int K,
+                                           int k0, int ce, XPre &p) {
+  const int quads = ce >> 2, total = M * quads;
+#pragma unroll
+  for (int it = 0; it < kXQ; ++it) load_quad<XT>(x, ldx, K, k0, quads, total, it * 256 + (int)threadIdx.x, p.v[it]);
+}
+
+// Stage chunk [k0, k0 + ce): from the prefetched registers when the chunk fits
+// them, else with synchronous loads.
+template <typename XT, int PARTS, int GS>
+__device__ __forceinline__ void stage_x(const XT *__restrict__ x, int64_t ldx, int M, int K,
+                                        int k0, int ce, const Stage &st, const XPre &p) {
+  const int quads = ce >> 2, total = M * quads;
+  if (total <= 256 * kXQ) {
+#pragma unroll
+    for (int it = 0; it < kXQ; ++it)
+      if (it * 256 < total) store_quad<PARTS, GS>(quads, total, it * 256 + (int)threadIdx.x, p.v[it], st);
+    return;
+  }
+  for (int q0 = 0; q0 < total; q0 += 256) {
+    float v[4];
+    load_quad<XT>(x, ldx, K, k0, quads, total, q0 + (int)threadIdx.x, v);
+    store_quad<PARTS, GS>(quads, total, q0 + (int)threadIdx.x, v, st);
+  }
+}
+
+template <int TYPE, typename XT, int MT, int MR>
+__global__ __launch_bounds__(256) void decode_kernel(const XT *__restrict__ x, int64_t ldx,
+                                                     const uint8_t *__restrict__ W, int N, int K,
+                                                     float *__restrict__ y, int64_t ldy, int M,
+                                                     int ks_n, int uc) {
+  constexpr int PARTS = sizeof(XT) == 4 ? 2 : 1;
+  constexpr int UE = Fmt<TYPE>::UE, TU = Fmt<TYPE>::TU, GS = Dec<TYPE>::GS;
+  constexpr int P = Dec<TYPE>::P;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int r = lane & 15, g = lane >> 4;
+  const int ts_n = 4 / ks_n;
+  const int ts = wave / ks_n, ks = wave - ts * ks_n;
+  const int ntiles = (N + 15) >> 4;
+  const int tile = blockIdx.x * ts_n + ts;
+  const bool active = tile < ntiles;
+  const int nu = K / UE;
+  const int cu = ks_n * uc;                    // units per staged chunk
+  const int ce = cu * UE;                      // elements per staged chunk
+  const int iters = (nu + ks_n - 1) / ks_n;    // loop trips, equal for every wave
+
+  // LDS: [hi][lo][group sums][reduction][zero]; hi/lo row blocks are multiples of 16 bytes
+  Stage st;
+  st.ld = ce + kXPad;
+  st.ms = 16 * MT;
+  st.xh = 0;
+  st.xl = M * st.ld;
+  st.xs = (st.xl + (PARTS == 2 ? M * st.ld : 0)) / 2;
+  const int red_off = st.xs + (ce / GS) * st.ms;   // floats: [4 waves][MT * 4][64]
+  st.zero = 2 * (red_off + 4 * MT * 4 * 64);
+  float *red = (float *)g_lds + red_off;
+
+  // rows M..ms-1 of the group sums and the zero operand stay zero throughout
+  for (int i = threadIdx.x; i < (ce / GS) * st.ms; i += 256) ((float *)g_lds)[st.xs + i] = 0.f;
+  if (threadIdx.x < kZeroHalves / 2) ((uint32_t *)((half_t *)g_lds + st.zero))[threadIdx.x] = 0u;
+
+  const uint8_t *wtile = W + (int64_t)(active ? tile : 0) * nu * TU;
+  float acc[MT][4];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) acc[mt][i] = 0.f;
+
+  // Trip i handles unit ks + ks_n * i; P units are in flight at any time.
+  // The first chunk's activations are requested ahead of the weights.
+  XPre xpre;
+  const bool xreg = M * (ce >> 2) <= 256 * kXQ;
+  if (xreg) prefetch_x<XT>(x, ldx, M, K, 0, ce, xpre);
+  Unit<TYPE> buf[P];
+#pragma unroll
+  for (int j = 0; j < P; ++j) {
+    const int u = ks + ks_n * j;
+    if (active && j < iters && u < nu) load_unit(wtile + (int64_t)u * TU, r, g, buf[j]);
+  }
+  for (int i0 = 0; i0 < iters; i0 += P) {
+#pragma unroll
+    for (int j = 0; j < P; ++j) {
+      const int i = i0 + j;
+      if (i < iters) {  // uniform over the workgroup
+        if (i % uc == 0) {
+          const int c = i / uc;
+          __syncthreads();  // the previous chunk is fully consumed
+          stage_x<XT, PARTS, GS>(x, ldx, M, K, c * ce, ce, st, xpre);
+          __syncthreads();
+          if (xreg && (c + 1) * uc < iters) prefetch_x<XT>(x, ldx, M, K, (c + 1) * ce, ce, xpre);
+        }
+        const int u = ks + ks_n * i;
+        if (active && u < nu) {
+          if constexpr (MT == 1 && MR == 1)
+            unit_m1<PARTS>(buf[j], st, ks + ks_n * (i % uc), lane, acc[0][0]);
+          else
+            unit_compute<PARTS, MT, MR>(buf[j], st, ks + ks_n * (i % uc), lane, M, acc);
+        }
+        const int un = u + ks_n * P;
+        if (active && i + P < iters && un < nu) load_unit(wtile + (int64_t)un * TU, r, g, buf[j]);
+      }
+    }
+  }
+
+  if constexpr (MT == 1 && MR == 1) {  // sum the four lane groups of each row
+    acc[0][0] += __shfl_xor(acc[0][0], 16);
+    acc[0][0] += __shfl_xor(acc[0][0], 32);
+  }
+
+  // fixed-order reduction of the ks_n partial sums of each tile
+  const int n = 16 * tile + r;
+  if (ks_n > 1) {
+    __syncthreads();
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int i = 0; i < MR; ++i) red[(wave * MT * 4 + mt * 4 + i) * 64 + lane] = acc[mt][i];
+    __syncthreads();
+    if (ks != 0) return;
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int i = 0; i < MR; ++i) {
+        float s = acc[mt][i];
+        for (int j = 1; j < ks_n; ++j) s += red[((wave + j) * MT * 4 + mt * 4 + i) * 64 + lane];
+        acc[mt][i] = s;
+      }
+  }
+  if (!active || n >= N) return;
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int i = 0; i < MR; ++i) {
+      const int m = 16 * mt + 4 * g + i;
+      if (m < M) y[(int64_t)m * ldy + n] = acc[mt][i];
+    }
+}
+
+#ifndef GGUF_DECODE_WAVES
+#define GGUF_DECODE_WAVES 2048  // target resident waves: 2 per SIMD on 256 CUs
+#endif
+
+template <int TYPE, typename XT, int MT, int MR>
+hipError_t launch_t(const XT *x, int64_t ldx, const uint8_t *W, int N, int K, float *y,
+                    int64_t ldy, int M, hipStream_t s) {
+  constexpr int PARTS = sizeof(XT) == 4 ? 2 : 1;
+  constexpr int UE = Fmt<TYPE>::UE, GS = Dec<TYPE>::GS;
+  const int ntiles = (N + 15) / 16;
+  const int nu = K / UE;
+  // K split: enough waves to fill the chip once, at least two units per wave
+  int ks = 1;
+  while (ks < 4 && ntiles * ks * 2 <= GGUF_DECODE_WAVES && nu >= 4 * ks) ks <<= 1;
+  // staged activations per chunk stay under 48 KB; for small M a chunk is at
+  // most 256 * kXQ quads so that it can be prefetched into registers
+  const int per_unit = M * UE * 2 * PARTS;
+  const int iters = (nu + ks - 1) / ks;
+  int uc = iters;
+  while (uc > 1 && ks * uc * per_unit > 48 * 1024) uc = (uc + 1) / 2;
+  if (M * ks * UE <= 4 * 256 * kXQ)
+    while (uc > 1 && M * ks * uc * UE > 4 * 256 * kXQ) uc = (uc + 1) / 2;
+  const int ce = ks * uc * UE;
+  const size_t lds = (size_t)M * (ce + kXPad) * 2 * PARTS + (size_t)(ce / GS) * 16 * MT * 4 +
+                     (size_t)4 * MT * 4 * 64 * 4 + kZeroHalves * 2;
+  const int ts = 4 / ks;
+  const dim3 grid((unsigned)((ntiles + ts - 1) / ts)), block(256);
+  hipLaunchKernelGGL((decode_kernel<TYPE, XT, MT, MR>), grid, block, lds, s, x, ldx, W, N, K, y,
+                     ldy, M, ks, uc);
+  return hipGetLastError();
+}
+
+template <int TYPE, typename XT>
+hipError_t launch_m(const XT *x, int64_t ldx, const uint8_t *W, int N, int K, float *y,
+                    int64_t ldy, int M, hipStream_t s) {
+  if (M == 1) return launch_t<TYPE, XT, 1, 1>(x, ldx, W, N, K, y, ldy, M, s);
+  if (M <= 16) return launch_t<TYPE, XT, 1, 4>(x, ldx, W, N, K, y, ldy, M, s);
+  return launch_t<TYPE, XT, 2, 4>(x, ldx, W, N, K, y, ldy, M, s);
+}
+
+template <typename XT>
+hipError_t launch_x(const XT *x, int64_t ldx, const uint8_t *W, int type, int N, int K, float *y,
+                    int64_t ldy, int M, hipStream_t s) {
+  if (type == 12) return launch_m<12, XT>(x, ldx, W, N, K, y, ldy, M, s);
+  if (type == 14) return launch_m<14, XT>(x, ldx, W, N, K, y, ldy, M, s);
+  return launch_m<8, XT>(x, ldx, W, N, K, y, ldy, M, s);
+}
+
+}  // namespace
+
+// Rows are processed in groups of at most 32 (one pass over the weights each).
+hipError_t launch_decode(const void *x, int x_type, int64_t ldx, const uint8_t *tiles, int type,
+                         int64_t n, int64_t k, float *y, int64_t ldy, int64_t m, hipStream_t s) {
+  const int esize = x_type == 0 ? 4 : 2;
+  hipError_t e = hipSuccess;
+  for (int64_t m0 = 0; m0 < m && e == hipSuccess; m0 += 32) {
+    const int mc = (int)((m - m0) < 32 ? (m - m0) : 32);
+    const char *xb = (const char *)x + m0 * ldx * esize;
+    if (x_type == 0)
+      e = launch_x<float>((const float *)xb, ldx, tiles, type, (int)n, (int)k, y + m0 * ldy, ldy,
+                          mc, s);
+    else
+      e = launch_x<half_t>((const half_t *)xb, ldx, tiles, type, (int)n, (int)k, y + m0 * ldy,
+                           ldy, mc, s);
+  }
+  return e;
+}
+
+}  // namespace gguf

@@ -1,0 +1,331 @@
+// Repack (raw GGUF bytes -> HBM row-tile layout) and dequantization to f32.
+//
+// Dequantization is bit-exact to the reference CPU dequant
+// (webgpu/src/model/gguf-dequant.ts:152-166 Q8_0, :255-281 Q4_K,
+// :369-399 Q6_K): every product in these formats is exact in f32, so the
+// only rounding is the final Q4_K subtraction, which f32 arithmetic (fused
+// or not) rounds exactly once, as the reference's f64-then-Float32Array does.
+// The row-tile layout itself is described in common.hpp.
+#include "common.hpp"
+
+namespace gguf {
+
+__device__ __forceinline__ uint32_t ld_u32_bytes(const uint8_t *p) {
+  return (uint32_t)p[0] | ((uint32_t)p[1] << 8) | ((uint32_t)p[2] << 16) | ((uint32_t)p[3] << 24);
+}
+__device__ __forceinline__ uint32_t ld_u16_bytes(const uint8_t *p) {
+  return (uint32_t)p[0] | ((uint32_t)p[1] << 8);
+}
+__device__ __forceinline__ uint2 ld_u64_bytes(const uint8_t *p) {
+  return make_uint2(ld_u32_bytes(p), ld_u32_bytes(p + 4));
+}
+
+// ---------------------------------------------------------------------------
+// Repack: one thread per (row n < 16 * tiles, unit u).  Rows past N write zeros.
+// ---------------------------------------------------------------------------
+template <int TYPE>
+__global__ __launch_bounds__(256) void repack_kernel(const uint8_t *__restrict__ raw, int64_t n_rows,
+                                                     int nu, int64_t n_pad,
+                                                     uint8_t *__restrict__ tiles) {
+  constexpr int UB = Fmt<TYPE>::UB, TU = Fmt<TYPE>::TU;
+  const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (gid >= n_pad * nu) return;
+  const int64_t n = gid / nu;
+  const int u = (int)(gid - n * nu);
+  const int r = (int)(n & 15);
+  uint8_t *tu = tiles + ((n >> 4) * nu + u) * (int64_t)TU;
+  if (n >= n_rows) {  // padding row of the last tile: every byte of its slots is zero
+    const uint4 z = make_uint4(0, 0, 0, 0);
+    if (TYPE == 12) {
+      *(uint4 *)(tu + 16 * r) = z;
+#pragma unroll
+      for (int p = 0; p < 8; ++p) *(uint4 *)(tu + 256 + (p * 16 + r) * 16) = z;
+    } else if (TYPE == 14) {
+#pragma unroll
+      for (int p = 0; p < 12; ++p) *(uint4 *)(tu + (p * 16 + r) * 16) = z;
+      *(uint4 *)(tu + 3072 + 16 * r) = z;
+      *(uint16_t *)(tu + 3328 + 2 * r) = 0;
+    } else {
+      *(uint16_t *)(tu + 2 * r) = 0;
+#pragma unroll
+      for (int g = 0; g < 4; ++g) *(uint2 *)(tu + 32 + (16 * g + r) * 8) = make_uint2(0, 0);
+    }
+    return;
+  }
+  const uint8_t *src = raw + (n * nu + u) * UB;
+  if (TYPE == 12) {
+    *(uint4 *)(tu + 16 * r) = make_uint4(ld_u32_bytes(src), ld_u32_bytes(src + 4),
+                                         ld_u32_bytes(src + 8), ld_u32_bytes(src + 12));
+    const uint8_t *qs = src + 16;
+#pragma unroll
+    for (int cp = 0; cp < 2; ++cp)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const uint2 a = ld_u64_bytes(qs + 64 * cp + 8 * g);
+        const uint2 b = ld_u64_bytes(qs + 64 * cp + 32 + 8 * g);
+        *(uint4 *)(tu + 256 + ((4 * cp + g) * 16 + r) * 16) = make_uint4(a.x, a.y, b.x, b.y);
+      }
+  } else if (TYPE == 14) {
+    const uint8_t *ql = src, *qh = src + 128;
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      uint32_t dw[12];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int hf = i >> 1, lh = i & 1;
+        dw[3 * i] = ld_u32_bytes(ql + 64 * hf + 16 * lh + 4 * g);
+        dw[3 * i + 1] = ld_u32_bytes(ql + 64 * hf + 32 + 16 * lh + 4 * g);
+        dw[3 * i + 2] = ld_u32_bytes(qh + 32 * hf + 16 * lh + 4 * g);
+      }
+#pragma unroll
+      for (int v = 0; v < 3; ++v)
+        *(uint4 *)(tu + ((4 * v + g) * 16 + r) * 16) =
+            make_uint4(dw[4 * v], dw[4 * v + 1], dw[4 * v + 2], dw[4 * v + 3]);
+    }
+    const uint8_t *sc = src + 192;
+    *(uint4 *)(tu + 3072 + 16 * r) = make_uint4(ld_u32_bytes(sc), ld_u32_bytes(sc + 4),
+                                                ld_u32_bytes(sc + 8), ld_u32_bytes(sc + 12));
+    *(uint16_t *)(tu + 3328 + 2 * r) = (uint16_t)ld_u16_bytes(src + 208);
+  } else {  // Q8_0
+    *(uint16_t *)(tu + 2 * r) = (uint16_t)ld_u16_bytes(src);
+#pragma unroll
+    for (int g = 0; g < 4; ++g) *(uint2 *)(tu + 32 + (16 * g + r) * 8) = ld_u64_bytes(src + 2 + 8 * g);
+  }
+}
+
+hipError_t launch_repack(const uint8_t *raw, int type, int64_t n_rows, int64_t k, uint8_t *tiles,
+                         hipStream_t s) {
+  const int nu = (int)(k / unit_elems(type));
+  const int64_t n_pad = (n_rows + 15) & ~(int64_t)15;
+  const int64_t total = n_pad * nu;
+  const dim3 grid((unsigned)((total + 255) / 256)), block(256);
+  if (type == 12)
+    hipLaunchKernelGGL(repack_kernel<12>, grid, block, 0, s, raw, n_rows, nu, n_pad, tiles);
+  else if (type == 14)
+    hipLaunchKernelGGL(repack_kernel<14>, grid, block, 0, s, raw, n_rows, nu, n_pad, tiles);
+  else
+    hipLaunchKernelGGL(repack_kernel<8>, grid, block, 0, s, raw, n_rows, nu, n_pad, tiles);
+  return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// Per-unit decoders shared by the tile and raw dequant kernels.
+// ---------------------------------------------------------------------------
+
+// Q4_K chunk c (32 qs bytes in q[0..7]) -> 32 values of sub-block 2c (lo) and
+// 32 of sub-block 2c + 1 (hi).
+__device__ __forceinline__ void q4k_decode_chunk(uint32_t hdr0, uint32_t s0, uint32_t s1,
+                                                 uint32_t s2, int c, const uint32_t q[8],
+                                                 float *lo, float *hi) {
+  const float d = h2f(hdr0), dmin = h2f(hdr0 >> 16);
+  uint32_t sc0, m0, sc1, m1;
+  q4k_scale_min(2 * c, s0, s1, s2, sc0, m0);
+  q4k_scale_min(2 * c + 1, s0, s1, s2, sc1, m1);
+  const float d1 = d * (float)sc0, min1 = dmin * (float)m0;
+  const float d2 = d * (float)sc1, min2 = dmin * (float)m1;
+#pragma unroll
+  for (int i = 0; i < 32; ++i) {
+    const uint32_t b = (q[i >> 2] >> (8 * (i & 3))) & 0xFFu;
+    lo[i] = d1 * (float)(b & 0x0Fu) - min1;
+    hi[i] = d2 * (float)(b >> 4) - min2;
+  }
+}
+
+// Q6_K 6-bit value (unsigned, q + 32) of element (hf, t, l) from the ql byte
+// ql[64 hf + 32 (t & 1) + l] and the qh byte qh[32 hf + l] (gguf-dequant.ts:369-399).
+__device__ __forceinline__ int q6k_value(uint32_t qlb, uint32_t qhb, int t) {
+  const uint32_t nib = (t >> 1) ? (qlb >> 4) : (qlb & 0x0Fu);
+  return (int)(nib | (((qhb >> (2 * t)) & 3u) << 4)) - 32;
+}
+
+// ---------------------------------------------------------------------------
+// Dequantization of the row-tile layout: out[n * ldo + k], rows n < N.
+// ---------------------------------------------------------------------------
+
+// Q4_K: one thread per (row, unit, chunk c).
+__global__ __launch_bounds__(256) void dequant_q4_k_kernel(const uint8_t *__restrict__ tiles,
+                                                           int64_t n_rows, int nu,
+                                                           float *__restrict__ out, int64_t ldo) {
+  const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (gid >= n_rows * nu * 4) return;
+  const int c = (int)(gid & 3);
+  const int64_t nuid = gid >> 2;
+  const int64_t n = nuid / nu;
+  const int u = (int)(nuid - n * nu);
+  const int r = (int)(n & 15);
+  const uint8_t *tu = tiles + ((n >> 4) * nu + u) * (int64_t)Fmt<12>::TU;
+  const uint4 hd = ldg16(tu + 16 * r);
+  const int cp = c >> 1, h = c & 1;
+  uint32_t q[8];
+#pragma unroll
+  for (int g = 0; g < 4; ++g) {
+    const uint4 p = ldg16(tu + 256 + ((4 * cp + g) * 16 + r) * 16);
+    q[2 * g] = h ? p.z : p.x;
+    q[2 * g + 1] = h ? p.w : p.y;
+  }
+  float lo[32], hi[32];
+  q4k_decode_chunk(hd.x, hd.y, hd.z, hd.w, c, q, lo, hi);
+  float *o = out + n * ldo + 256 * (int64_t)u + 64 * c;
+#pragma unroll
+  for (int i = 0; i < 32; ++i) {
+    o[i] = lo[i];
+    o[32 + i] = hi[i];
+  }
+}
+
+// Q6_K: one thread per (row, unit, half hf).
+__global__ __launch_bounds__(256) void dequant_q6_k_kernel(const uint8_t *__restrict__ tiles,
+                                                           int64_t n_rows, int nu,
+                                                           float *__restrict__ out, int64_t ldo) {
+  const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (gid >= n_rows * nu * 2) return;
+  const int hf = (int)(gid & 1);
+  const int64_t nuid = gid >> 1;
+  const int64_t n = nuid / nu;
+  const int u = (int)(nuid - n * nu);
+  const int r = (int)(n & 15);
+  const uint8_t *tu = tiles + ((n >> 4) * nu + u) * (int64_t)Fmt<14>::TU;
+  const float d = h2f(*(const uint16_t *)(tu + 3328 + 2 * r));
+  const int8_t *sc = (const int8_t *)(tu + 3072 + 16 * r);
+  float *o = out + n * ldo + 256 * (int64_t)u + 128 * hf;
+#pragma unroll
+  for (int g = 0; g < 4; ++g) {
+    uint32_t dw[12];
+#pragma unroll
+    for (int v = 0; v < 3; ++v) {
+      const uint4 p = ldg16(tu + ((4 * v + g) * 16 + r) * 16);
+      dw[4 * v] = p.x; dw[4 * v + 1] = p.y; dw[4 * v + 2] = p.z; dw[4 * v + 3] = p.w;
+    }
+#pragma unroll
+    for (int lh = 0; lh < 2; ++lh) {
+      const int i = 2 * hf + lh;
+      const uint32_t qa = dw[3 * i], qb = dw[3 * i + 1], qh = dw[3 * i + 2];
+#pragma unroll
+      for (int b = 0; b < 4; ++b) {
+        const int l = 16 * lh + 4 * g + b;
+        const uint32_t ab = (qa >> (8 * b)) & 0xFFu, bb = (qb >> (8 * b)) & 0xFFu;
+        const uint32_t hb = (qh >> (8 * b)) & 0xFFu;
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          const int q = q6k_value((t & 1) ? bb : ab, hb, t);
+          o[32 * t + l] = d * (float)sc[8 * hf + 2 * t + lh] * (float)q;
+        }
+      }
+    }
+  }
+}
+
+// Q8_0: one thread per (row, block).
+__global__ __launch_bounds__(256) void dequant_q8_0_kernel(const uint8_t *__restrict__ tiles,
+                                                           int64_t n_rows, int nu,
+                                                           float *__restrict__ out, int64_t ldo) {
+  const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (gid >= n_rows * nu) return;
+  const int64_t n = gid / nu;
+  const int u = (int)(gid - n * nu);
+  const int r = (int)(n & 15);
+  const uint8_t *tu = tiles + ((n >> 4) * nu + u) * (int64_t)Fmt<8>::TU;
+  const float d = h2f(*(const uint16_t *)(tu + 2 * r));
+  float *o = out + n * ldo + 32 * (int64_t)u;
+#pragma unroll
+  for (int g = 0; g < 4; ++g) {
+    const uint2 p = *(const uint2 *)(tu + 32 + (16 * g + r) * 8);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const uint32_t w = i < 4 ? p.x : p.y;
+      o[8 * g + i] = d * (float)(int8_t)((w >> (8 * (i & 3))) & 0xFFu);
+    }
+  }
+}
+
+hipError_t launch_dequant(const uint8_t *tiles, int type, int64_t n_rows, int64_t k, float *out,
+                          int64_t ldo, hipStream_t s) {
+  const int nu = (int)(k / unit_elems(type));
+  const int parts = type == 12 ? 4 : (type == 14 ? 2 : 1);
+  const int64_t total = n_rows * nu * parts;
+  const dim3 grid((unsigned)((total + 255) / 256)), block(256);
+  if (type == 12)
+    hipLaunchKernelGGL(dequant_q4_k_kernel, grid, block, 0, s, tiles, n_rows, nu, out, ldo);
+  else if (type == 14)
+    hipLaunchKernelGGL(dequant_q6_k_kernel, grid, block, 0, s, tiles, n_rows, nu, out, ldo);
+  else
+    hipLaunchKernelGGL(dequant_q8_0_kernel, grid, block, 0, s, tiles, n_rows, nu, out, ldo);
+  return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// Dequantization of raw GGUF bytes (any alignment: byte loads)
+// ---------------------------------------------------------------------------
+
+__global__ __launch_bounds__(256) void dequant_raw_q8_0_kernel(const uint8_t *__restrict__ raw,
+                                                               int64_t nb,
+                                                               float *__restrict__ out) {
+  const int64_t b = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (b >= nb) return;
+  const uint8_t *src = raw + b * 34;
+  const float d = h2f(ld_u16_bytes(src));
+  float *o = out + 32 * b;
+#pragma unroll
+  for (int i = 0; i < 32; ++i) o[i] = d * (float)(int8_t)src[2 + i];
+}
+
+__global__ __launch_bounds__(256) void dequant_raw_q4_k_kernel(const uint8_t *__restrict__ raw,
+                                                               int64_t nsb,
+                                                               float *__restrict__ out) {
+  const int64_t g = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (g >= nsb * 4) return;
+  const int c = (int)(g & 3);
+  const int64_t b = g >> 2;
+  const uint8_t *blk = raw + b * 144;
+  uint32_t q[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) q[i] = ld_u32_bytes(blk + 16 + 32 * c + 4 * i);
+  float lo[32], hi[32];
+  q4k_decode_chunk(ld_u32_bytes(blk), ld_u32_bytes(blk + 4), ld_u32_bytes(blk + 8),
+                   ld_u32_bytes(blk + 12), c, q, lo, hi);
+  float *o = out + 256 * b + 64 * c;
+#pragma unroll
+  for (int i = 0; i < 32; ++i) {
+    o[i] = lo[i];
+    o[32 + i] = hi[i];
+  }
+}
+
+__global__ __launch_bounds__(256) void dequant_raw_q6_k_kernel(const uint8_t *__restrict__ raw,
+                                                               int64_t nsb,
+                                                               float *__restrict__ out) {
+  const int64_t g = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (g >= nsb * 2) return;
+  const int hf = (int)(g & 1);
+  const int64_t b = g >> 1;
+  const uint8_t *blk = raw + b * 210;
+  const float d = h2f(ld_u16_bytes(blk + 208));
+  const int8_t *sc = (const int8_t *)(blk + 192);
+  float *o = out + 256 * b + 128 * hf;
+  for (int l = 0; l < 32; ++l) {
+    const uint32_t ab = blk[64 * hf + l], bb = blk[64 * hf + 32 + l], hb = blk[128 + 32 * hf + l];
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+      o[32 * t + l] = d * (float)sc[8 * hf + 2 * t + l / 16] * (float)q6k_value((t & 1) ? bb : ab, hb, t);
+  }
+}
+
+hipError_t launch_dequant_raw(const uint8_t *raw, int type, int64_t n_elems, float *out,
+                              hipStream_t s) {
+  if (type == 8) {
+    const int64_t nb = n_elems / 32;
+    hipLaunchKernelGGL(dequant_raw_q8_0_kernel, dim3((unsigned)((nb + 255) / 256)), dim3(256), 0,
+                       s, raw, nb, out);
+  } else if (type == 12) {
+    const int64_t nsb = n_elems / 256;
+    hipLaunchKernelGGL(dequant_raw_q4_k_kernel, dim3((unsigned)((nsb * 4 + 255) / 256)), dim3(256),
+                       0, s, raw, nsb, out);
+  } else {
+    const int64_t nsb = n_elems / 256;
+    hipLaunchKernelGGL(dequant_raw_q6_k_kernel, dim3((unsigned)((nsb * 2 + 255) / 256)), dim3(256),
+                       0, s, raw, nsb, out);
+  }
+  return hipGetLastError();
+}
+
+}  // namespace gguf

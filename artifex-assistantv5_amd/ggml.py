@@ -5,23 +5,21 @@ reference tabulates it in ``webgpu/src/model/gguf.ts:24-35`` (``GGML_TYPES``)
 and ``:39-73`` (``TYPE_TRAITS``); ``ggml_type_traits`` and
 ``ggml_tensor_bytes`` mirror ``gguf.ts:75-92`` including their errors.
 
-The HBM row layout is this library's own (the reference pads blocks to 4-byte
-strides for WGSL, ``gguf-dequant.ts:655-672``; here rows are split into
-16-byte-aligned planes so kernels can issue 128-bit loads).  A weight of
-``N`` rows by ``K`` columns is stored as ``N`` consecutive rows of
-``tile_row_bytes(type, K)`` bytes each.  Row ``n`` holds the ``K/block``
-blocks of GGUF row ``n`` (row-major weight layout, ``matmul_gguf.wgsl:5-8``):
+The row-tile layout is this library's own (the reference pads blocks to
+4-byte strides for WGSL, ``gguf-dequant.ts:655-672``).  Rows are grouped in
+tiles of 16 consecutive rows (row-major weight, ``matmul_gguf.wgsl:5-8``;
+the last tile is zero-padded).  For each unit of K -- a 256-element
+superblock (Q4_K, Q6_K) or a 32-element block (Q8_0) -- a tile stores the 16
+rows' GGUF blocks interleaved at 16-byte granularity (8 bytes for Q8_0
+quants), so that one wave-wide load of a matrix-core operand reads
+contiguous HBM.  No bytes are added: a weight of ``N`` rows takes
+``round_up(N, 16) * raw_row_bytes(type, K)`` bytes.  The byte order inside a
+tile-unit is defined in ``csrc/common.hpp`` (and modelled in
+``tests/tile_model.py``).
 
-* Q8_0 (32 elements / 34 B):  ``qs[K]`` int8 | ``d[K/32]`` f16 | pad to 16 B
-* Q4_K (256 elements / 144 B): the raw superblocks, unchanged
-  (``d, dmin`` f16 | ``scales[12]`` | ``qs[128]``); 144 is a multiple of 16
-* Q6_K (256 elements / 210 B): ``ql[K/2]`` | ``qh[K/4]`` | ``sc[K/16]`` int8 |
-  ``d[K/256]`` f16 | pad to 16 B; within each plane, superblock ``b`` owns
-  the bytes ``[b*128, b*128+128)`` of ``ql``, ``[b*64, ...)`` of ``qh``,
-  ``[b*16, ...)`` of ``sc`` — the byte order inside a superblock is GGUF's.
-
-Because rows are self-contained, row ranges of a weight are weights too:
-gate/up concatenation and row sharding are plain byte-range operations.
+Row ranges that start on a multiple of 16 are weights of their own (byte
+offset ``start * raw_row_bytes``): gate/up concatenation and row sharding
+stay byte-range operations.
 """
 
 from __future__ import annotations
@@ -86,10 +84,6 @@ def ggml_tensor_bytes(ggml_type: int, ne: list[int] | tuple[int, ...]) -> int:
     return (ne0 // block) * tsize * outer
 
 
-def _align16(x: int) -> int:
-    return (x + 15) & ~15
-
-
 def check_kernel_type(ggml_type: int) -> None:
     if int(ggml_type) not in KERNEL_TYPES:
         ggml_type_traits(ggml_type)  # unknown ids raise the gguf.ts error
@@ -103,23 +97,23 @@ def raw_row_bytes(ggml_type: int, k: int) -> int:
     return ggml_tensor_bytes(ggml_type, [k])
 
 
+TILE_ROWS = 16
+
+
 def tile_row_bytes(ggml_type: int, k: int) -> int:
-    """Bytes of one row of ``k`` elements in the HBM row layout (see module doc)."""
+    """Bytes per row in the row-tile layout (equal to the raw GGUF row bytes)."""
     check_kernel_type(ggml_type)
     block, tsize, _ = ggml_type_traits(ggml_type)
     if k <= 0 or k % block != 0:
         raise ValueError(f"[gguf-hip] K={k} not a positive multiple of block size {block}")
-    nb = k // block
-    if ggml_type == Q4_K:
-        return 144 * nb
-    return _align16(tsize * nb)
+    return tsize * (k // block)
 
 
-def tile_plane_offsets(ggml_type: int, k: int) -> dict[str, int]:
-    """Byte offset of each plane inside one row of the HBM row layout."""
-    tile_row_bytes(ggml_type, k)
-    if ggml_type == Q8_0:
-        return {"qs": 0, "d": k}
-    if ggml_type == Q6_K:
-        return {"ql": 0, "qh": k // 2, "sc": k // 2 + k // 4, "d": k // 2 + k // 4 + k // 16}
-    return {"blocks": 0}
+def tiled_rows(n: int) -> int:
+    """Rows a weight of ``n`` rows occupies (whole tiles of 16)."""
+    return -(-int(n) // TILE_ROWS) * TILE_ROWS
+
+
+def tiled_bytes(ggml_type: int, n: int, k: int) -> int:
+    """Bytes of an ``[n, k]`` weight in the row-tile layout."""
+    return tiled_rows(n) * tile_row_bytes(ggml_type, k)

@@ -24,8 +24,8 @@ import numpy as np
 import torch
 
 from . import _native
-from .ggml import (F16, F32, GGML_TYPE_NAMES, check_kernel_type, ggml_type_traits,
-                   raw_row_bytes, tile_row_bytes)
+from .ggml import (F16, F32, GGML_TYPE_NAMES, TILE_ROWS, check_kernel_type, ggml_type_traits,
+                   tile_row_bytes, tiled_bytes)
 
 _X_TYPES = {torch.float32: F32, torch.float16: F16}
 
@@ -55,8 +55,9 @@ def _as_device_u8(data, device) -> torch.Tensor:
 class GGUFWeight:
     """A quantized ``[n, k]`` matrix resident in HBM (forward-pass.ts:89-98).
 
-    ``data`` is a uint8 device tensor holding ``n`` rows in the HBM row layout
-    (``tile_row_bytes(ggml_type, k)`` bytes each) starting at ``byte_offset``.
+    ``data`` is a uint8 device tensor holding the weight in the row-tile
+    layout (``tiled_bytes(ggml_type, n, k)`` bytes: ``n`` rows rounded up to
+    whole 16-row tiles) starting at ``byte_offset``.
     """
 
     data: torch.Tensor
@@ -69,7 +70,7 @@ class GGUFWeight:
         check_kernel_type(self.ggml_type)
         if self.data.dtype != torch.uint8 or not self.data.is_cuda:
             raise ValueError("GGUFWeight.data must be a uint8 tensor on a HIP device")
-        need = self.byte_offset + self.n * self.row_bytes
+        need = self.byte_offset + tiled_bytes(self.ggml_type, self.n, self.k)
         if self.data.numel() < need:
             raise ValueError(f"GGUFWeight buffer holds {self.data.numel()} B, needs {need} B")
         if self.byte_offset % 16:
@@ -81,7 +82,7 @@ class GGUFWeight:
 
     @property
     def nbytes(self) -> int:
-        return self.n * self.row_bytes
+        return tiled_bytes(self.ggml_type, self.n, self.k)
 
     @property
     def type_name(self) -> str:
@@ -95,9 +96,15 @@ class GGUFWeight:
         return self.data.data_ptr() + self.byte_offset
 
     def rows(self, start: int, stop: int) -> "GGUFWeight":
-        """Row-range view ``[start, stop)`` sharing storage (rows are self-contained)."""
+        """Row-range view ``[start, stop)`` sharing storage.
+
+        ``start`` must be a multiple of 16 (a tile boundary).  A view whose
+        length is not a multiple of 16 keeps its last tile's trailing rows in
+        place; kernels compute but never store or return them."""
         if not 0 <= start <= stop <= self.n:
             raise ValueError(f"row range [{start}, {stop}) outside [0, {self.n})")
+        if start % TILE_ROWS:
+            raise ValueError(f"row range must start on a multiple of {TILE_ROWS}, got {start}")
         return GGUFWeight(self.data, self.ggml_type, stop - start, self.k,
                           self.byte_offset + start * self.row_bytes)
 
@@ -121,7 +128,7 @@ class LayerWeights:
 
 def repack_gguf_for_gpu(ggml_type: int, data, n: int, k: Optional[int] = None,
                         device=None) -> GGUFWeight:
-    """Raw GGUF bytes of an ``[n, k]`` tensor -> GGUFWeight in the HBM row layout.
+    """Raw GGUF bytes of an ``[n, k]`` tensor -> GGUFWeight in the row-tile layout.
 
     Mirrors repackGGUFForGPU (gguf-dequant.ts:809-840): ``repack(type, data, n)``
     with a single argument treats the data as one row of ``n`` elements; the
@@ -133,8 +140,7 @@ def repack_gguf_for_gpu(ggml_type: int, data, n: int, k: Optional[int] = None,
     check_kernel_type(ggml_type)
     raw = _as_device_u8(data, device)
     dev = raw.device
-    trb = tile_row_bytes(ggml_type, k)
-    out = torch.empty(n * trb, dtype=torch.uint8, device=dev)
+    out = torch.empty(tiled_bytes(ggml_type, n, k), dtype=torch.uint8, device=dev)
     with torch.cuda.device(dev):
         _native.check(lib.gguf_hip_repack(raw.data_ptr(), raw.numel(), ggml_type, n, k,
                                           out.data_ptr(), out.numel(), _stream(dev)), lib)
@@ -142,13 +148,20 @@ def repack_gguf_for_gpu(ggml_type: int, data, n: int, k: Optional[int] = None,
 
 
 def concat_rows(*weights: GGUFWeight) -> GGUFWeight:
-    """Row-concatenate weights of one type and K (gate+up fusion, forward-pass.ts:740-791)."""
+    """Row-concatenate weights of one type and K (gate+up fusion, forward-pass.ts:740-791).
+
+    Every weight but the last must have a multiple of 16 rows, so that the
+    parts' tiles line up."""
     if not weights:
         raise ValueError("concat_rows needs at least one weight")
     t, k = weights[0].ggml_type, weights[0].k
     for w in weights:
         if w.ggml_type != t or w.k != k:
             raise ValueError("concat_rows: weights must share ggml type and K")
+    for w in weights[:-1]:
+        if w.n % TILE_ROWS:
+            raise ValueError(f"concat_rows: all but the last weight need a multiple of "
+                             f"{TILE_ROWS} rows, got {w.n}")
     parts = [w.data[w.byte_offset:w.byte_offset + w.nbytes] for w in weights]
     return GGUFWeight(torch.cat(parts), t, sum(w.n for w in weights), k)
 
@@ -156,7 +169,7 @@ def concat_rows(*weights: GGUFWeight) -> GGUFWeight:
 def dequant_ggml(ggml_type: int, data, n: int) -> torch.Tensor:
     """Dequantize ``n`` elements to f32 on the GPU (gguf-dequant.ts:844-868).
 
-    ``data`` is a GGUFWeight (HBM row layout) or raw GGUF bytes (device or host).
+    ``data`` is a GGUFWeight (row-tile layout) or raw GGUF bytes (device or host).
     """
     lib = _native.load_library()
     check_kernel_type(ggml_type)

@@ -19,10 +19,16 @@
  *    like the reference's BatchedDispatcher (webgpu/src/engine/compute.ts:146-266).
  *  - No call allocates device memory: weights, activations and outputs are
  *    owned by the caller, as in the reference (forward-pass.ts:1140-1163).
- *  - Weights live in the "HBM row layout": N rows of gguf_hip_tile_bytes(t,1,K)
- *    bytes, rows 16-byte aligned; Q4_K rows are the raw GGUF superblocks, Q8_0
- *    and Q6_K rows are split into 16-byte-aligned planes (qs|d for Q8_0,
- *    ql|qh|sc|d for Q6_K).  gguf_hip_repack converts raw GGUF bytes.
+ *  - Weights live in the "row-tile layout": rows are grouped in tiles of 16
+ *    (the last tile zero-padded); for each 256-element superblock (Q4_K, Q6_K)
+ *    or 32-element block (Q8_0) of K, a tile stores the 16 rows' GGUF blocks
+ *    interleaved at 16-byte granularity (8 bytes for Q8_0 quants), so that
+ *    one wave-wide load of a matrix-core operand reads contiguous HBM.  The
+ *    byte count is exactly round_up(N, 16) rows of GGUF blocks
+ *    (gguf_hip_tile_bytes); the interleave is defined in csrc/common.hpp of
+ *    the library.  gguf_hip_repack converts raw GGUF bytes.  Row ranges that
+ *    start on a multiple of 16 are weights of their own (byte offset
+ *    start * row_bytes), which is how gate+up fusion concatenates weights.
  */
 #ifndef GGUF_HIP_H
 #define GGUF_HIP_H
@@ -33,7 +39,11 @@
 extern "C" {
 #endif
 
-#define GGUF_HIP_ABI_VERSION 1
+/* The library is built with hidden visibility; only the entry points below
+ * are exported (kernels and helpers cannot be interposed across libraries). */
+#pragma GCC visibility push(default)
+
+#define GGUF_HIP_ABI_VERSION 2
 
 /* ggml type ids (gguf.ts:24-35); activation dtypes reuse F32 / F16. */
 #define GGUF_HIP_F32 0
@@ -60,10 +70,13 @@ extern "C" {
 #define GGUF_HIP_ERR_HIP (-7)
 
 /* Kernel family for gguf_hip_matmul_variant. */
-#define GGUF_HIP_VARIANT_AUTO 0   /* GEMV for M == 1, skinny MFMA for M <= 32, GEMM above */
-#define GGUF_HIP_VARIANT_GEMV 1   /* VALU GEMV, one pass over the weights per activation row */
-#define GGUF_HIP_VARIANT_SKINNY 2 /* MFMA, all M <= 32 rows share one pass over the weights */
-#define GGUF_HIP_VARIANT_GEMM 3   /* MFMA GEMM with dequantized fp16 tiles staged in LDS */
+#define GGUF_HIP_VARIANT_AUTO 0   /* DECODE for M <= GGUF_HIP_DECODE_MAX_M, GEMM above */
+#define GGUF_HIP_VARIANT_DECODE 1 /* matrix-core decode: exact quant codes x split f16
+                                     activations, f32 scales; one pass over the weights
+                                     per 32 activation rows (any M) */
+#define GGUF_HIP_VARIANT_GEMM 2   /* MFMA GEMM with dequantized fp16 weight tiles and fp16
+                                     activations staged in LDS (prefill) */
+#define GGUF_HIP_DECODE_MAX_M 32
 
 /* ABI version of the loaded library (GGUF_HIP_ABI_VERSION). */
 int gguf_hip_abi_version(void);
@@ -78,18 +91,19 @@ int gguf_hip_type_traits(int ggml_type, int *block_elems, int *type_size);
  * negative error code on failure. */
 int64_t gguf_hip_raw_bytes(int ggml_type, int64_t n_rows, int64_t k);
 
-/* Bytes of an [n_rows, k] weight in the HBM row layout; replaces the
- * GGUF_GPU_LAYOUT stride table (gguf-dequant.ts:655-672).  Negative on error. */
+/* Bytes of an [n_rows, k] weight in the row-tile layout, round_up(n_rows, 16)
+ * rows of GGUF blocks; replaces the GGUF_GPU_LAYOUT stride table
+ * (gguf-dequant.ts:655-672).  Negative on error. */
 int64_t gguf_hip_tile_bytes(int ggml_type, int64_t n_rows, int64_t k);
 
-/* Raw GGUF bytes (device, any alignment, exactly raw_bytes long) -> HBM row
+/* Raw GGUF bytes (device, any alignment, exactly raw_bytes long) -> row-tile
  * layout (device, 16-byte aligned, exactly tile_bytes long).  Replaces
  * repackGGUFForGPU (gguf-dequant.ts:809-840) including its byte-length check
- * (assertBytes, :678-680).  Pad bytes are written as zero. */
+ * (assertBytes, :678-680).  Padding rows of the last tile are written as zero. */
 int gguf_hip_repack(const void *raw, int64_t raw_bytes, int ggml_type, int64_t n_rows,
                     int64_t k, void *tiles, int64_t tile_bytes, void *stream);
 
-/* Dequantize an [n_rows, k] weight in the HBM row layout to f32
+/* Dequantize an [n_rows, k] weight in the row-tile layout to f32
  * out[n * ldo + i].  Bit-exact to dequantGGML (gguf-dequant.ts:844-868). */
 int gguf_hip_dequant(const void *tiles, int ggml_type, int64_t n_rows, int64_t k, float *out,
                      int64_t ldo, void *stream);
@@ -102,7 +116,8 @@ int gguf_hip_dequant_raw(const void *raw, int ggml_type, int64_t n_elems, float 
 
 /* y[m * ldy + n] = sum_k x[m * ldx + k] * dequant(W)[n, k] for m < M, n < N.
  * x: f32 or f16 (x_type = GGUF_HIP_F32 / GGUF_HIP_F16), 16-byte aligned rows
- * (ldx * sizeof(x) % 16 == 0).  W: HBM row layout, 16-byte aligned.
+ * (ldx * sizeof(x) % 16 == 0), finite and within the f16 range (|x| < 65504).
+ * W: row-tile layout, 16-byte aligned.
  * y: f32, 4-byte aligned.  Accumulation in f32.  Replaces dispatchMatmulGGUF
  * (forward-pass.ts:1496-1544); its io.aOffset / io.cOffset windows are plain
  * pointer offsets here. */
@@ -110,11 +125,12 @@ int gguf_hip_matmul(const void *x, int x_type, int64_t ldx, const void *tiles, i
                     int64_t n, int64_t k, float *y, int64_t ldy, int64_t m, void *stream);
 
 /* gguf_hip_matmul with an explicit kernel family (GGUF_HIP_VARIANT_*), the
- * analog of the reference's per-dispatch pipeline choice (forward-pass.ts:1501-1524).
- * SKINNY requires M <= 32. */
+ * analog of the reference's per-dispatch pipeline choice (forward-pass.ts:1501-1524). */
 int gguf_hip_matmul_variant(const void *x, int x_type, int64_t ldx, const void *tiles,
                             int ggml_type, int64_t n, int64_t k, float *y, int64_t ldy,
                             int64_t m, int variant, void *stream);
+
+#pragma GCC visibility pop
 
 #ifdef __cplusplus
 }

@@ -60,13 +60,14 @@ def test_constants_match_header(native):
     assert d["GGUF_HIP_ERR_DTYPE"] == native.ERR_DTYPE
     assert d["GGUF_HIP_ERR_BYTES"] == native.ERR_BYTES
     assert d["GGUF_HIP_ERR_HIP"] == native.ERR_HIP
-    assert d["GGUF_HIP_VARIANT_SKINNY"] == native.VARIANT_SKINNY
+    assert d["GGUF_HIP_VARIANT_DECODE"] == native.VARIANT_DECODE
     assert d["GGUF_HIP_VARIANT_GEMM"] == native.VARIANT_GEMM
+    assert d["GGUF_HIP_DECODE_MAX_M"] == native.DECODE_MAX_M
     assert (d["GGUF_HIP_Q8_0"], d["GGUF_HIP_Q4_K"], d["GGUF_HIP_Q6_K"]) == (8, 12, 14)
 
 
 def test_abi_version(lib):
-    assert lib.gguf_hip_abi_version() == 1
+    assert lib.gguf_hip_abi_version() == 2
 
 
 def test_type_traits(lib, native):
@@ -80,7 +81,8 @@ def test_type_traits(lib, native):
 def test_byte_queries_agree_with_python(lib, pkg):
     for t in (8, 12, 14):
         for k in (256, 512, 1024, 4096, 14336):
-            assert lib.gguf_hip_tile_bytes(t, 7, k) == 7 * pkg.tile_row_bytes(t, k)
+            assert lib.gguf_hip_tile_bytes(t, 7, k) == 16 * pkg.tile_row_bytes(t, k)
+            assert lib.gguf_hip_tile_bytes(t, 33, k) == pkg.tiled_bytes(t, 33, k)
             assert lib.gguf_hip_raw_bytes(t, 7, k) == pkg.ggml_tensor_bytes(t, [k, 7])
     assert lib.gguf_hip_tile_bytes(13, 1, 256) == -1   # Q5_K: known type, no kernel
     assert lib.gguf_hip_tile_bytes(8, 1, 48) == -2
@@ -88,14 +90,15 @@ def test_byte_queries_agree_with_python(lib, pkg):
 
 def test_repack_errors(lib, native):
     raw_bytes = 2 * 144
+    tiled = 16 * raw_bytes                 # one row occupies a whole 16-row tile
     # byte length mismatch (assertBytes, gguf-dequant.ts:678-680)
-    assert lib.gguf_hip_repack(None, raw_bytes - 1, 12, 1, 512, None, 288, None) == native.ERR_BYTES
+    assert lib.gguf_hip_repack(None, raw_bytes - 1, 12, 1, 512, None, tiled, None) == native.ERR_BYTES
     assert "byteLength 287 != expected 288" in native.last_error(lib)
-    assert lib.gguf_hip_repack(None, raw_bytes, 12, 1, 512, None, 100, None) == native.ERR_BYTES
-    assert lib.gguf_hip_repack(None, raw_bytes, 12, 1, 512, None, 288, None) == native.ERR_NULL
-    assert lib.gguf_hip_repack(0x1000, raw_bytes, 12, 1, 512, 0x1008, 288, None) == native.ERR_ALIGN
-    assert lib.gguf_hip_repack(0x1000, 10, 99, 1, 512, 0x1000, 288, None) == native.ERR_TYPE
-    assert lib.gguf_hip_repack(0x1000, 10, 12, 1, 300, 0x1000, 288, None) == native.ERR_SHAPE
+    assert lib.gguf_hip_repack(None, raw_bytes, 12, 1, 512, None, 288, None) == native.ERR_BYTES
+    assert lib.gguf_hip_repack(None, raw_bytes, 12, 1, 512, None, tiled, None) == native.ERR_NULL
+    assert lib.gguf_hip_repack(0x1000, raw_bytes, 12, 1, 512, 0x1008, tiled, None) == native.ERR_ALIGN
+    assert lib.gguf_hip_repack(0x1000, 10, 99, 1, 512, 0x1000, tiled, None) == native.ERR_TYPE
+    assert lib.gguf_hip_repack(0x1000, 10, 12, 1, 300, 0x1000, tiled, None) == native.ERR_SHAPE
     assert lib.gguf_hip_repack(None, 0, 12, 0, 512, None, 0, None) == 0     # empty: no-op
 
 
@@ -117,9 +120,9 @@ def test_matmul_errors(lib, native):
     mm = lib.gguf_hip_matmul_variant
     x, w, y = 0x10000, 0x20000, 0x30000
     assert mm(x, 2, 512, w, 12, 8, 512, y, 8, 1, 0, None) == native.ERR_DTYPE
-    assert mm(x, 0, 512, w, 12, 8, 512, y, 8, 33, 2, None) == native.ERR_SHAPE   # skinny M>32
-    assert "M <= 32" in native.last_error(lib)
     assert mm(x, 0, 512, w, 12, 8, 512, y, 8, 1, 9, None) == native.ERR_SHAPE    # bad variant
+    assert "unknown kernel variant 9" in native.last_error(lib)
+    assert mm(x, 0, 512, w, 12, 8, 512, y, 8, 1, -1, None) == native.ERR_SHAPE
     assert mm(x, 0, 512, w, 11, 8, 512, y, 8, 1, 0, None) == native.ERR_TYPE     # Q3_K
     assert mm(x, 0, 512, w, 12, 8, 500, y, 8, 1, 0, None) == native.ERR_SHAPE
     assert mm(None, 0, 512, w, 12, 8, 512, y, 8, 1, 0, None) == native.ERR_NULL

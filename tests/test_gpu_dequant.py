@@ -58,14 +58,19 @@ def test_repack_from_unaligned_raw(pkg, ref, t):
                          ref.dequant_rows(t, raw, n, k).reshape(-1))
 
 
-def test_row_views_and_concat(pkg, ref):
-    t, k = 12, 512
-    raw = tile_model.random_blocks(t, 10, k, seed=5)
-    w = pkg.repack_gguf_for_gpu(t, raw, 10, k)
-    want = ref.dequant_rows(t, raw, 10, k)
-    assert ref.same_bits(w.rows(3, 7).dequant().cpu().numpy(), want[3:7])
-    cat = pkg.concat_rows(w.rows(0, 4), w.rows(4, 10))
+@pytest.mark.parametrize("t", [8, 12, 14])
+def test_row_views_and_concat(pkg, ref, t):
+    k = 512
+    raw = tile_model.random_blocks(t, 40, k, seed=5)
+    w = pkg.repack_gguf_for_gpu(t, raw, 40, k)
+    want = ref.dequant_rows(t, raw, 40, k)
+    assert ref.same_bits(w.rows(16, 37).dequant().cpu().numpy(), want[16:37])
+    cat = pkg.concat_rows(w.rows(0, 16), w.rows(16, 40))
     assert ref.same_bits(cat.dequant().cpu().numpy(), want)
+    with pytest.raises(ValueError):
+        w.rows(3, 7)                                   # views start on a tile boundary
+    with pytest.raises(ValueError):
+        pkg.concat_rows(w.rows(0, 20), w.rows(32, 40))  # inner parts are whole tiles
 
 
 @pytest.mark.parametrize("t,n,k", [(12, 14336, 4096), (12, 4096, 14336), (14, 4096, 14336),

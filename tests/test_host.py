@@ -32,11 +32,11 @@ def test_tensor_bytes(pkg):
 @pytest.mark.parametrize("k", [256, 512, 768, 1280, 4096, 14336])
 def test_tile_row_bytes(pkg, t, k):
     trb = pkg.tile_row_bytes(t, k)
-    assert trb == tile_model.tile_row_bytes(t, k)
-    assert trb % 16 == 0
-    assert trb - pkg.raw_row_bytes(t, k) < 16          # at most 15 pad bytes per row
-    if t == 12:
-        assert trb == pkg.raw_row_bytes(t, k)
+    assert trb == tile_model.tile_row_bytes(t, k) == pkg.raw_row_bytes(t, k)
+    for n in (1, 15, 16, 17, 14336):
+        assert pkg.tiled_bytes(t, n, k) == tile_model.tiled_bytes(t, n, k)
+        assert pkg.tiled_bytes(t, n, k) == -(-n // 16) * 16 * trb
+        assert (16 * trb) % 16 == 0                       # every tile starts 16-byte aligned
 
 
 def test_tile_row_bytes_rejects(pkg):
@@ -46,18 +46,29 @@ def test_tile_row_bytes_rejects(pkg):
         pkg.tile_row_bytes(13, 256)            # Q5_K: known type, no kernel
 
 
-def test_plane_offsets(pkg):
-    assert pkg.ggml.tile_plane_offsets(8, 4096) == {"qs": 0, "d": 4096}
-    assert pkg.ggml.tile_plane_offsets(14, 4096) == {"ql": 0, "qh": 2048, "sc": 3072, "d": 3328}
+def test_layout_model_is_a_permutation_of_each_tile_unit():
+    for t in (8, 12, 14):
+        block, ub = tile_model.BLOCK[t]
+        pos = tile_model._unit_maps(t)          # asserts the map is a bijection
+        assert pos.shape == (16, ub)
+    # header / d of row r sits at a fixed place (what the kernels read directly)
+    assert tile_model._unit_maps(12)[5, 0] == 80
+    assert tile_model._unit_maps(14)[3, 208] == 3328 + 6
+    assert tile_model._unit_maps(8)[7, 0] == 14
 
 
 @pytest.mark.parametrize("t,k", [(8, 96), (8, 4096), (12, 512), (14, 768), (14, 4096)])
-def test_layout_model_roundtrip(ref, t, k):
-    raw = tile_model.random_blocks(t, 5, k, seed=t + k)
-    tiles = tile_model.to_tiles(t, raw, 5, k)
-    assert tiles.size == 5 * tile_model.tile_row_bytes(t, k)
-    back = tile_model.from_tiles(t, tiles, 5, k)
+@pytest.mark.parametrize("n", [5, 16, 37])
+def test_layout_model_roundtrip(ref, t, k, n):
+    raw = tile_model.random_blocks(t, n, k, seed=t + k)
+    tiles = tile_model.to_tiles(t, raw, n, k)
+    assert tiles.size == tile_model.tiled_bytes(t, n, k)
+    back = tile_model.from_tiles(t, tiles, n, k)
     assert np.array_equal(back, raw)
+    # padding rows of the last tile are zero
+    pad = tile_model.tiled_rows(n) - n
+    full = tile_model.from_tiles(t, tiles, n + pad, k)
+    assert not full[raw.size:].any()
     assert ref.same_bits(ref.dequant_rows(t, back, 5, k), ref.dequant_rows(t, raw, 5, k))
 
 

@@ -1,60 +1,93 @@
-"""numpy model of the HBM row layout (test helper; the layout is defined in
-``artifex-assistantv5_amd/ggml.py`` and ``include/gguf_hip.h``)."""
+"""numpy model of the HBM row-tile layout (test helper; the layout is defined
+in ``artifex-assistantv5_amd/csrc/common.hpp`` and ``include/gguf_hip.h``).
+
+Rows are grouped in tiles of 16; per unit of K (Q4_K / Q6_K superblock, Q8_0
+block) a tile stores the 16 rows' GGUF blocks interleaved:
+
+* Q4_K: [header of row r at 16 r] then piece (cp, g, r) at 256 + ((4 cp + g) 16 + r) 16
+  = qs[64 cp + 8 g, +8) | qs[64 cp + 32 + 8 g, +8)
+* Q6_K: piece (v, g, r) at ((4 v + g) 16 + r) 16 = the lane's quant dwords 4v..4v+3,
+  dword 3i = ql[64 hf + 16 lh + 4 g, +4), 3i+1 = ql[64 hf + 32 + 16 lh + 4 g, +4),
+  3i+2 = qh[32 hf + 16 lh + 4 g, +4) for i = 2 hf + lh; scales at 3072 + 16 r; d at 3328 + 2 r
+* Q8_0: d at 2 r, then piece (g, r) at 32 + (16 g + r) 8 = qs[8 g, +8)
+"""
 
 import numpy as np
 
 BLOCK = {8: (32, 34), 12: (256, 144), 14: (256, 210)}
 
 
-def _align16(x):
-    return (x + 15) & ~15
-
-
 def tile_row_bytes(t, k):
     block, size = BLOCK[t]
-    nb = k // block
-    return 144 * nb if t == 12 else _align16(size * nb)
+    return size * (k // block)
+
+
+def tiled_rows(n):
+    return -(-n // 16) * 16
+
+
+def tiled_bytes(t, n, k):
+    return tiled_rows(n) * tile_row_bytes(t, k)
+
+
+def _unit_maps(t):
+    """(dst, src) byte index arrays: tile-unit byte dst[i] = row r's block byte src[i], as
+    arrays of shape (16, UB) giving the tile-unit offset of each (row, block byte)."""
+    block, ub = BLOCK[t]
+    pos = np.zeros((16, ub), np.int64)
+    for r in range(16):
+        if t == 12:
+            pos[r, 0:16] = 16 * r + np.arange(16)
+            for cp in range(2):
+                for g in range(4):
+                    base = 256 + ((4 * cp + g) * 16 + r) * 16
+                    pos[r, 16 + 64 * cp + 8 * g + np.arange(8)] = base + np.arange(8)
+                    pos[r, 16 + 64 * cp + 32 + 8 * g + np.arange(8)] = base + 8 + np.arange(8)
+        elif t == 14:
+            for g in range(4):
+                for i in range(4):
+                    hf, lh = i >> 1, i & 1
+                    srcs = [64 * hf + 16 * lh + 4 * g, 64 * hf + 32 + 16 * lh + 4 * g,
+                            128 + 32 * hf + 16 * lh + 4 * g]
+                    for j, src in enumerate(srcs):
+                        dwi = 3 * i + j
+                        base = ((4 * (dwi // 4) + g) * 16 + r) * 16 + 4 * (dwi % 4)
+                        pos[r, src + np.arange(4)] = base + np.arange(4)
+            pos[r, 192:208] = 3072 + 16 * r + np.arange(16)
+            pos[r, 208:210] = 3328 + 2 * r + np.arange(2)
+        else:
+            pos[r, 0:2] = 2 * r + np.arange(2)
+            for g in range(4):
+                pos[r, 2 + 8 * g + np.arange(8)] = 32 + (16 * g + r) * 8 + np.arange(8)
+    assert np.array_equal(np.sort(pos.reshape(-1)), np.arange(16 * ub))
+    return pos
 
 
 def to_tiles(t, raw, n, k):
-    """Raw GGUF bytes of an [n, k] tensor -> HBM row layout bytes."""
-    block, size = BLOCK[t]
-    nb = k // block
-    raw = np.asarray(raw, np.uint8).reshape(n, nb, size)
-    trb = tile_row_bytes(t, k)
-    out = np.zeros((n, trb), np.uint8)
-    if t == 12:
-        out[:] = raw.reshape(n, -1)
-    elif t == 8:
-        out[:, :k] = raw[:, :, 2:].reshape(n, k)
-        out[:, k:k + 2 * nb] = raw[:, :, :2].reshape(n, 2 * nb)
-    else:
-        out[:, :k // 2] = raw[:, :, :128].reshape(n, -1)
-        out[:, k // 2:k // 2 + k // 4] = raw[:, :, 128:192].reshape(n, -1)
-        o = k // 2 + k // 4
-        out[:, o:o + k // 16] = raw[:, :, 192:208].reshape(n, -1)
-        out[:, o + k // 16:o + k // 16 + 2 * nb] = raw[:, :, 208:210].reshape(n, -1)
+    """Raw GGUF bytes of an [n, k] tensor -> row-tile layout bytes."""
+    block, ub = BLOCK[t]
+    nu = k // block
+    npad = tiled_rows(n)
+    rows = np.zeros((npad, nu, ub), np.uint8)
+    rows[:n] = np.asarray(raw, np.uint8).reshape(n, nu, ub)
+    pos = _unit_maps(t)
+    out = np.zeros((npad // 16, nu, 16 * ub), np.uint8)
+    for r in range(16):
+        out[:, :, pos[r]] = rows[r::16]
     return out.reshape(-1)
 
 
 def from_tiles(t, tiles, n, k):
-    """Inverse of ``to_tiles``."""
-    block, size = BLOCK[t]
-    nb = k // block
-    tiles = np.asarray(tiles, np.uint8).reshape(n, tile_row_bytes(t, k))
-    raw = np.zeros((n, nb, size), np.uint8)
-    if t == 12:
-        raw[:] = tiles[:, :144 * nb].reshape(n, nb, 144)
-    elif t == 8:
-        raw[:, :, 2:] = tiles[:, :k].reshape(n, nb, 32)
-        raw[:, :, :2] = tiles[:, k:k + 2 * nb].reshape(n, nb, 2)
-    else:
-        o = k // 2 + k // 4
-        raw[:, :, :128] = tiles[:, :k // 2].reshape(n, nb, 128)
-        raw[:, :, 128:192] = tiles[:, k // 2:o].reshape(n, nb, 64)
-        raw[:, :, 192:208] = tiles[:, o:o + k // 16].reshape(n, nb, 16)
-        raw[:, :, 208:210] = tiles[:, o + k // 16:o + k // 16 + 2 * nb].reshape(n, nb, 2)
-    return raw.reshape(-1)
+    """Inverse of ``to_tiles`` (drops the padding rows)."""
+    block, ub = BLOCK[t]
+    nu = k // block
+    npad = tiled_rows(n)
+    tl = np.asarray(tiles, np.uint8).reshape(npad // 16, nu, 16 * ub)
+    pos = _unit_maps(t)
+    rows = np.zeros((npad, nu, ub), np.uint8)
+    for r in range(16):
+        rows[r::16] = tl[:, :, pos[r]]
+    return rows[:n].reshape(-1)
 
 
 def random_blocks(t, n, k, seed, specials=False):
