@@ -55,46 +55,77 @@ struct Unit<8> {  // qs bytes 8g..8g+7, d
   uint32_t d;
 };
 
-// Scale group size (elements sharing one scale) and units in flight per wave.
+// Scale group size (elements sharing one scale) and units in flight per wave
+// (P; deepest for a single activation row, whose staged chunk is small).
 #ifndef GGUF_DECODE_P_Q4K
-#define GGUF_DECODE_P_Q4K 6
+#define GGUF_DECODE_P_Q4K 4
 #endif
 #ifndef GGUF_DECODE_P_Q6K
 #define GGUF_DECODE_P_Q6K 2
 #endif
 #ifndef GGUF_DECODE_P_Q8
-#define GGUF_DECODE_P_Q8 16
+#define GGUF_DECODE_P_Q8 8
 #endif
 template <int TYPE>
 struct Dec;
 template <>
 struct Dec<12> {
-  static constexpr int GS = 32, P = GGUF_DECODE_P_Q4K;
+  static constexpr int GS = 32, P1 = GGUF_DECODE_P_Q4K;
 };
 template <>
 struct Dec<14> {
-  static constexpr int GS = 16, P = GGUF_DECODE_P_Q6K;
+  static constexpr int GS = 16, P1 = GGUF_DECODE_P_Q6K;
 };
 template <>
 struct Dec<8> {
-  static constexpr int GS = 32, P = GGUF_DECODE_P_Q8;
+  static constexpr int GS = 32, P1 = GGUF_DECODE_P_Q8;
 };
+template <int TYPE, int MT, int MR>
+constexpr int decode_p() {
+  return MR == 1 ? Dec<TYPE>::P1 : (MT == 1 ? (Dec<TYPE>::P1 + 1) / 2 : (TYPE == 8 ? 4 : 1));
+}
 
-__device__ __forceinline__ void load_unit(const uint8_t *tu, int r, int g, Unit<12> &u) {
-  u.h = ldg16_stream(tu + 16 * r);
-  u.a = ldg16_stream(tu + 256 + (16 * g + r) * 16);
-  u.b = ldg16_stream(tu + 256 + (16 * (4 + g) + r) * 16);
+// Weight loads go through a buffer resource spanning the wave's row tile
+// (base = tile start, num_records = its byte count): the per-unit offset is a
+// scalar (soffset), the lane's offset a loop-invariant VGPR, and a load of a
+// tile that does not exist (num_records = 0) returns zeros instead of
+// touching memory.  Loads are nontemporal (aux bit 1).
+constexpr int kNT = 2;
+constexpr int kRsrcWord3 = 0x00020000;
+
+__device__ __forceinline__ uint4 bload16(__amdgpu_buffer_rsrc_t rs, int voff, int soff) {
+  const auto v = __builtin_amdgcn_raw_buffer_load_b128(rs, voff, soff, kNT);
+  return make_uint4(v[0], v[1], v[2], v[3]);
 }
-__device__ __forceinline__ void load_unit(const uint8_t *tu, int r, int g, Unit<14> &u) {
-  u.p0 = ldg16_stream(tu + (16 * g + r) * 16);
-  u.p1 = ldg16_stream(tu + (16 * (4 + g) + r) * 16);
-  u.p2 = ldg16_stream(tu + (16 * (8 + g) + r) * 16);
-  u.sc = ldg16_stream(tu + 3072 + 16 * r);
-  u.d = *(const uint16_t *)(tu + 3328 + 2 * r);
+__device__ __forceinline__ uint2 bload8(__amdgpu_buffer_rsrc_t rs, int voff, int soff) {
+  const auto v = __builtin_amdgcn_raw_buffer_load_b64(rs, voff, soff, kNT);
+  return make_uint2(v[0], v[1]);
 }
-__device__ __forceinline__ void load_unit(const uint8_t *tu, int r, int g, Unit<8> &u) {
-  u.q = ldg8_stream(tu + 32 + (16 * g + r) * 8);
-  u.d = *(const uint16_t *)(tu + 2 * r);
+__device__ __forceinline__ uint32_t bload2(__amdgpu_buffer_rsrc_t rs, int voff, int soff) {
+  return (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(rs, voff, soff, kNT);
+}
+
+// soff = unit * tile_unit_bytes; r = lane & 15, g = lane >> 4.
+__device__ __forceinline__ void load_unit(__amdgpu_buffer_rsrc_t rs, int soff, int r, int g,
+                                          Unit<12> &u) {
+  const int qa = 256 + (16 * g + r) * 16;
+  u.h = bload16(rs, 16 * r, soff);
+  u.a = bload16(rs, qa, soff);
+  u.b = bload16(rs, qa + 1024, soff);
+}
+__device__ __forceinline__ void load_unit(__amdgpu_buffer_rsrc_t rs, int soff, int r, int g,
+                                          Unit<14> &u) {
+  const int p0 = (16 * g + r) * 16;
+  u.p0 = bload16(rs, p0, soff);
+  u.p1 = bload16(rs, p0 + 1024, soff);
+  u.p2 = bload16(rs, p0 + 2048, soff);
+  u.sc = bload16(rs, 3072 + 16 * r, soff);
+  u.d = bload2(rs, 3328 + 2 * r, soff);
+}
+__device__ __forceinline__ void load_unit(__amdgpu_buffer_rsrc_t rs, int soff, int r, int g,
+                                          Unit<8> &u) {
+  u.q = bload8(rs, 32 + (16 * g + r) * 8, soff);
+  u.d = bload2(rs, 2 * r, soff);
 }
 
 __device__ __forceinline__ half8_t as_h8(uint32_t a, uint32_t b, uint32_t c, uint32_t d) {
@@ -116,6 +147,12 @@ struct Stage {
   int ms;      // 16 * MT
 };
 
+__device__ __forceinline__ half8_t lds_h8b(int byte_off) {
+  return *(const half8_t *)(g_lds + byte_off);
+}
+__device__ __forceinline__ half4_t lds_h4b(int byte_off) {
+  return *(const half4_t *)(g_lds + byte_off);
+}
 __device__ __forceinline__ half8_t lds_h8(int half_off) {
   return *(const half8_t *)((const half_t *)g_lds + half_off);
 }
@@ -159,7 +196,7 @@ __device__ __forceinline__ void apply(float (&acc)[4], const float4_t &D, float 
 }
 
 // Shared-memory view of one staged chunk of activations.
-constexpr int kZeroHalves = 32;
+constexpr int kZeroHalves = 256;  // covers every immediate offset added to a selected address
 
 // ---------------------------------------------------------------------------
 // Single activation row (M = 1).  The 16 A rows of the MFMA are then free to
@@ -178,22 +215,13 @@ __device__ __forceinline__ void unit_m1(const Unit<12> &u, const Stage &st, int 
   const int r = lane & 15, g = lane >> 4;
   const int jo = r >> 1;
   const bool live = PARTS == 2 || (r & 1) == 0;
-  const int own = (st.xh + (r & 1) * (st.xl - st.xh)) + 256 * ul + 8 * g;
-  const uint32_t w[8] = {u.a.x, u.a.y, u.a.z, u.a.w, u.b.x, u.b.y, u.b.z, u.b.w};
-  float4_t D = {0.f, 0.f, 0.f, 0.f};
+  // byte addresses: the lane's own activation row and the zero operand
+  const int own = 2 * (st.xh + (r & 1) * (st.xl - st.xh) + 256 * ul + 8 * g);
+  const int zero = 2 * st.zero;
+  // all eight A fragments first, so their LDS latency overlaps the decode below
+  half8_t a[8];
 #pragma unroll
-  for (int c = 0; c < 4; ++c) {
-    const uint32_t wa = w[2 * c], wb = w[2 * c + 1];
-    const uint32_t wa8 = wa >> 8, wb8 = wb >> 8;
-    const half8_t blo = as_h8(wa & 0x000F000Fu, wa8 & 0x000F000Fu, wb & 0x000F000Fu, wb8 & 0x000F000Fu);
-    const half8_t bhi = as_h8(wa & 0x00F000F0u, wa8 & 0x00F000F0u, wb & 0x00F000F0u, wb8 & 0x00F000F0u);
-    const int pa = (live && jo == 2 * c) ? own + 64 * c : st.zero;
-    const int pb = (live && jo == 2 * c + 1) ? own + 64 * c + 32 : st.zero;
-    D = __builtin_amdgcn_mfma_f32_16x16x32_f16(lds_h8(pa), blo, D, 0, 0, 0);
-    D = __builtin_amdgcn_mfma_f32_16x16x32_f16(lds_h8(pb), bhi, D, 0, 0, 0);
-  }
-  // rows 4g + i: sub-block 2g (i = 0, 1) and 2g + 1 (i = 2, 3), part i & 1
-  const float dlo = D[0] + D[1], dhi = D[2] + D[3];
+  for (int j = 0; j < 8; ++j) a[j] = lds_h8b(((live && jo == j) ? own : zero) + 64 * j);
   uint32_t sc_lo, sc_hi, m_lo, m_hi;
   q4k_scales_packed(u.h.y, u.h.z, u.h.w, sc_lo, sc_hi, m_lo, m_hi);
   const uint32_t scw = g < 2 ? sc_lo : sc_hi, mw = g < 2 ? m_lo : m_hi;
@@ -201,9 +229,21 @@ __device__ __forceinline__ void unit_m1(const Unit<12> &u, const Stage &st, int 
   const float sc0 = (float)((scw >> sh) & 0xFFu), sc1 = (float)((scw >> (sh + 8)) & 0xFFu);
   const float m0 = (float)((mw >> sh) & 0xFFu), m1 = (float)((mw >> (sh + 8)) & 0xFFu);
   const int xs = st.xs + (ul * 8 + 2 * g) * st.ms;
+  const float mx = m0 * lds_f(xs) + m1 * lds_f(xs + st.ms);
   const float d = h2f(u.h.x), dmin = h2f(u.h.x >> 16);
-  acc += (d * kTwo24) * (sc0 * dlo) + (d * kTwo20) * (sc1 * dhi) -
-         dmin * (m0 * lds_f(xs) + m1 * lds_f(xs + st.ms));
+  const uint32_t w[8] = {u.a.x, u.a.y, u.a.z, u.a.w, u.b.x, u.b.y, u.b.z, u.b.w};
+  float4_t D = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {  // codes of chunk c decoded just before its two MFMAs
+    const uint32_t wa = w[2 * c], wb = w[2 * c + 1];
+    const uint32_t wa8 = wa >> 8, wb8 = wb >> 8;
+    const half8_t blo = as_h8(wa & 0x000F000Fu, wa8 & 0x000F000Fu, wb & 0x000F000Fu, wb8 & 0x000F000Fu);
+    const half8_t bhi = as_h8(wa & 0x00F000F0u, wa8 & 0x00F000F0u, wb & 0x00F000F0u, wb8 & 0x00F000F0u);
+    D = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[2 * c], blo, D, 0, 0, 0);
+    D = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[2 * c + 1], bhi, D, 0, 0, 0);
+  }
+  // rows 4g + i: sub-block 2g (i = 0, 1) and 2g + 1 (i = 2, 3), part i & 1
+  acc += (d * kTwo24) * (sc0 * (D[0] + D[1])) + (d * kTwo20) * (sc1 * (D[2] + D[3])) - dmin * mx;
 }
 
 // Q6_K: 16 groups of 16 elements, two chains of 8 (halves hf = 0, 1); lane
@@ -214,7 +254,8 @@ __device__ __forceinline__ void unit_m1(const Unit<14> &u, const Stage &st, int 
   const int r = lane & 15, g = lane >> 4;
   const int so = r >> 1;
   const bool live = PARTS == 2 || (r & 1) == 0;
-  const int own = (st.xh + (r & 1) * (st.xl - st.xh)) + 256 * ul + 4 * g;
+  const int own = 2 * (st.xh + (r & 1) * (st.xl - st.xh) + 256 * ul + 4 * g);
+  const int zero = 2 * st.zero;
   const uint32_t dw[12] = {u.p0.x, u.p0.y, u.p0.z, u.p0.w, u.p1.x, u.p1.y,
                            u.p1.z, u.p1.w, u.p2.x, u.p2.y, u.p2.z, u.p2.w};
   const uint32_t scw[4] = {u.sc.x, u.sc.y, u.sc.z, u.sc.w};
@@ -222,7 +263,14 @@ __device__ __forceinline__ void unit_m1(const Unit<14> &u, const Stage &st, int 
   float sd = 0.f, sx = 0.f;
 #pragma unroll
   for (int hf = 0; hf < 2; ++hf) {
-    float4_t D = {0.f, 0.f, 0.f, 0.f};
+    // the chain's eight A fragments first (LDS latency overlaps the decode)
+    half4_t a[8];
+#pragma unroll
+    for (int sl = 0; sl < 8; ++sl) {
+      const int t = sl >> 1, lh = sl & 1;
+      a[sl] = lds_h4b(((live && so == sl) ? own : zero) + 2 * (128 * hf + 32 * t + 16 * lh));
+    }
+    half4_t b[8];
 #pragma unroll
     for (int lh = 0; lh < 2; ++lh) {
       const int i = 2 * hf + lh;
@@ -232,19 +280,18 @@ __device__ __forceinline__ void unit_m1(const Unit<14> &u, const Stage &st, int 
                              ((qa >> 4) & 0x0F0F0F0Fu) | (qh & 0x30303030u),
                              ((qb >> 4) & 0x0F0F0F0Fu) | ((qh >> 2) & 0x30303030u)};
 #pragma unroll
-      for (int t = 0; t < 4; ++t) {
-        const half4_t b = as_h4(v[t] & 0x00FF00FFu, (v[t] >> 8) & 0x00FF00FFu);
-        const int pa = (live && so == 2 * t + lh) ? own + 128 * hf + 32 * t + 16 * lh : st.zero;
-        D = __builtin_amdgcn_mfma_f32_16x16x16f16(lds_h4(pa), b, D, 0, 0, 0);
-      }
+      for (int t = 0; t < 4; ++t) b[2 * t + lh] = as_h4(v[t] & 0x00FF00FFu, (v[t] >> 8) & 0x00FF00FFu);
     }
     // rows 4g + i: group 8 hf + 2 g + (i >> 1), part i & 1
     const uint32_t sw = scw[2 * hf + (g >> 1)];
     const int sh = 16 * (g & 1);
     const float s0 = (float)(int8_t)((sw >> sh) & 0xFFu), s1 = (float)(int8_t)((sw >> (sh + 8)) & 0xFFu);
     const int xs = st.xs + (ul * 16 + 8 * hf + 2 * g) * st.ms;
-    sd += s0 * (D[0] + D[1]) + s1 * (D[2] + D[3]);
     sx += s0 * lds_f(xs) + s1 * lds_f(xs + st.ms);
+    float4_t D = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int sl = 0; sl < 8; ++sl) D = __builtin_amdgcn_mfma_f32_16x16x16f16(a[sl], b[sl], D, 0, 0, 0);
+    sd += s0 * (D[0] + D[1]) + s1 * (D[2] + D[3]);
   }
   acc += (d * kTwo24) * sd - (d * 32.f) * sx;
 }
@@ -381,55 +428,71 @@ __device__ __forceinline__ void unit_compute(const Unit<8> &u, const Stage &st, 
 }
 
 // Stage activations x[0:M, k0 : k0 + ce) into LDS (zeros past K).
-// Activation staging.  A chunk of M x ce activations is converted quad by
-// quad (4 consecutive elements per thread and step).  When a chunk has at most
-// 256 * kXQ quads, its loads are issued one chunk ahead into registers
-// (XPre) -- before the weight loads they would otherwise queue behind, since
-// the vector-memory counter retires loads in issue order.
-constexpr int kXQ = 4;
+// Activation staging.  A chunk of M x ce activations is converted in items of
+// 16 consecutive elements, one item per thread and step.  When a chunk has at
+// most 256 items its loads are issued one chunk ahead into registers (XPre) --
+// before the weight loads they would otherwise queue behind, since the
+// vector-memory counter retires loads in issue order.
+constexpr int kItem = 16;
 
 struct XPre {
-  float v[kXQ][4];
+  float v[kItem];
 };
 
 template <typename XT>
-__device__ __forceinline__ void load_quad(const XT *__restrict__ x, int64_t ldx, int K, int k0,
-                                          int quads, int total, int q, float (&v)[4]) {
-  v[0] = v[1] = v[2] = v[3] = 0.f;
+__device__ __forceinline__ void load_item(const XT *__restrict__ x, int64_t ldx, int K, int k0,
+                                          int per_row, int total, int q, float (&v)[kItem]) {
+#pragma unroll
+  for (int i = 0; i < kItem; ++i) v[i] = 0.f;
   if (q < total) {
-    const int m = q / quads, e = 4 * (q - m * quads), k = k0 + e;
-    if (k < K) {
+    const int m = q / per_row, e = kItem * (q - m * per_row), k = k0 + e;
+    if (k < K) {  // K is a multiple of 32, so an item is either all in or all out
       if constexpr (sizeof(XT) == 4) {
-        const float4 t = *(const float4 *)(x + (int64_t)m * ldx + k);
-        v[0] = t.x; v[1] = t.y; v[2] = t.z; v[3] = t.w;
+        const float4 *src = (const float4 *)(x + (int64_t)m * ldx + k);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float4 t = src[i];
+          v[4 * i] = t.x; v[4 * i + 1] = t.y; v[4 * i + 2] = t.z; v[4 * i + 3] = t.w;
+        }
       } else {
-        const half4_t t = *(const half4_t *)(x + (int64_t)m * ldx + k);
-        v[0] = (float)t[0]; v[1] = (float)t[1]; v[2] = (float)t[2]; v[3] = (float)t[3];
+        const half8_t *src = (const half8_t *)(x + (int64_t)m * ldx + k);
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+          const half8_t t = src[i];
+#pragma unroll
+          for (int j = 0; j < 8; ++j) v[8 * i + j] = (float)t[j];
+        }
       }
     }
   }
 }
 
-// hi / lo parts (quad stored in (0, 2, 1, 3) order) and the group sums of hi + lo.
-// Groups never straddle a wave, so the shuffle reduction stays within one group.
+// hi / lo parts (each quad stored in (0, 2, 1, 3) order) and group sums of hi + lo.
+// A group (16 or 32 elements) spans one or two consecutive threads of a wave.
 template <int PARTS, int GS>
-__device__ __forceinline__ void store_quad(int quads, int total, int q, const float (&v)[4],
+__device__ __forceinline__ void store_item(int per_row, int total, int q, const float (&v)[kItem],
                                            const Stage &st) {
-  half_t hi[4], lo[4];
+  half8_t hi[2], lo[2];
   float s = 0.f;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    hi[i] = (half_t)v[i];
-    lo[i] = (half_t)(v[i] - (float)hi[i]);
-    s += (float)hi[i] + (PARTS == 2 ? (float)lo[i] : 0.f);
+  for (int i = 0; i < kItem; ++i) {
+    const int pos = (i & ~3) | ((i & 1) << 1) | ((i >> 1) & 1);  // swap 1 <-> 2 in each quad
+    const half_t h = (half_t)v[i];
+    const half_t l = (half_t)(v[i] - (float)h);
+    hi[pos >> 3][pos & 7] = h;
+    lo[pos >> 3][pos & 7] = l;
+    s += (float)h + (PARTS == 2 ? (float)l : 0.f);
   }
-#pragma unroll
-  for (int mask = 1; mask < GS / 4; mask <<= 1) s += __shfl_xor(s, mask);
+  if (GS == 2 * kItem) s += __shfl_xor(s, 1);
   if (q < total) {
-    const int m = q / quads, e = 4 * (q - m * quads);
+    const int m = q / per_row, e = kItem * (q - m * per_row);
     half_t *lh = (half_t *)g_lds;
-    *(half4_t *)(lh + st.xh + m * st.ld + e) = half4_t{hi[0], hi[2], hi[1], hi[3]};
-    if (PARTS == 2) *(half4_t *)(lh + st.xl + m * st.ld + e) = half4_t{lo[0], lo[2], lo[1], lo[3]};
+    *(half8_t *)(lh + st.xh + m * st.ld + e) = hi[0];
+    *(half8_t *)(lh + st.xh + m * st.ld + e + 8) = hi[1];
+    if (PARTS == 2) {
+      *(half8_t *)(lh + st.xl + m * st.ld + e) = lo[0];
+      *(half8_t *)(lh + st.xl + m * st.ld + e + 8) = lo[1];
+    }
     if ((e & (GS - 1)) == 0) ((float *)g_lds)[st.xs + (e / GS) * st.ms + m] = s;
   }
 }
@@ -437,27 +500,24 @@ __device__ __forceinline__ void store_quad(int quads, int total, int q, const fl
 template <typename XT>
 __device__ __forceinline__ void prefetch_x(const XT *__restrict__ x, int64_t ldx, int M, int K,
                                            int k0, int ce, XPre &p) {
-  const int quads = ce >> 2, total = M * quads;
-#pragma unroll
-  for (int it = 0; it < kXQ; ++it) load_quad<XT>(x, ldx, K, k0, quads, total, it * 256 + (int)threadIdx.x, p.v[it]);
+  const int per_row = ce / kItem;
+  load_item<XT>(x, ldx, K, k0, per_row, M * per_row, (int)threadIdx.x, p.v);
 }
 
 // Stage chunk [k0, k0 + ce): from the prefetched registers when the chunk fits
-// them, else with synchronous loads.
+// them (at most 256 items), else with synchronous loads.
 template <typename XT, int PARTS, int GS>
 __device__ __forceinline__ void stage_x(const XT *__restrict__ x, int64_t ldx, int M, int K,
                                         int k0, int ce, const Stage &st, const XPre &p) {
-  const int quads = ce >> 2, total = M * quads;
-  if (total <= 256 * kXQ) {
-#pragma unroll
-    for (int it = 0; it < kXQ; ++it)
-      if (it * 256 < total) store_quad<PARTS, GS>(quads, total, it * 256 + (int)threadIdx.x, p.v[it], st);
+  const int per_row = ce / kItem, total = M * per_row;
+  if (total <= 256) {
+    store_item<PARTS, GS>(per_row, total, (int)threadIdx.x, p.v, st);
     return;
   }
   for (int q0 = 0; q0 < total; q0 += 256) {
-    float v[4];
-    load_quad<XT>(x, ldx, K, k0, quads, total, q0 + (int)threadIdx.x, v);
-    store_quad<PARTS, GS>(quads, total, q0 + (int)threadIdx.x, v, st);
+    float v[kItem];
+    load_item<XT>(x, ldx, K, k0, per_row, total, q0 + (int)threadIdx.x, v);
+    store_item<PARTS, GS>(per_row, total, q0 + (int)threadIdx.x, v, st);
   }
 }
 
@@ -468,8 +528,10 @@ __global__ __launch_bounds__(256) void decode_kernel(const XT *__restrict__ x, i
                                                      int ks_n, int uc) {
   constexpr int PARTS = sizeof(XT) == 4 ? 2 : 1;
   constexpr int UE = Fmt<TYPE>::UE, TU = Fmt<TYPE>::TU, GS = Dec<TYPE>::GS;
-  constexpr int P = Dec<TYPE>::P;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  constexpr int P = decode_p<TYPE, MT, MR>();
+  // the wave index is uniform across a wave; say so, so that the tile, the
+  // unit offsets and the buffer resource live in scalar registers
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int r = lane & 15, g = lane >> 4;
   const int ts_n = 4 / ks_n;
   const int ts = wave / ks_n, ks = wave - ts * ks_n;
@@ -496,7 +558,8 @@ __global__ __launch_bounds__(256) void decode_kernel(const XT *__restrict__ x, i
   for (int i = threadIdx.x; i < (ce / GS) * st.ms; i += 256) ((float *)g_lds)[st.xs + i] = 0.f;
   if (threadIdx.x < kZeroHalves / 2) ((uint32_t *)((half_t *)g_lds + st.zero))[threadIdx.x] = 0u;
 
-  const uint8_t *wtile = W + (int64_t)(active ? tile : 0) * nu * TU;
+  const __amdgpu_buffer_rsrc_t wrs = __builtin_amdgcn_make_buffer_rsrc(
+      (void *)(W + (int64_t)(active ? tile : 0) * nu * TU), 0, active ? nu * TU : 0, kRsrcWord3);
   float acc[MT][4];
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt)
@@ -506,35 +569,38 @@ __global__ __launch_bounds__(256) void decode_kernel(const XT *__restrict__ x, i
   // Trip i handles unit ks + ks_n * i; P units are in flight at any time.
   // The first chunk's activations are requested ahead of the weights.
   XPre xpre;
-  const bool xreg = M * (ce >> 2) <= 256 * kXQ;
+  const bool xreg = M * (ce / kItem) <= 256;
   if (xreg) prefetch_x<XT>(x, ldx, M, K, 0, ce, xpre);
   Unit<TYPE> buf[P];
 #pragma unroll
   for (int j = 0; j < P; ++j) {
     const int u = ks + ks_n * j;
-    if (active && j < iters && u < nu) load_unit(wtile + (int64_t)u * TU, r, g, buf[j]);
+    if (j < iters && u < nu) load_unit(wrs, u * TU, r, g, buf[j]);
   }
-  for (int i0 = 0; i0 < iters; i0 += P) {
+  // uc is a multiple of P, so a chunk starts on buffer slot 0 and the staging
+  // code sits outside the unrolled body.
+  const int nch = (iters + uc - 1) / uc;
+  for (int c = 0; c < nch; ++c) {  // uniform over the workgroup
+    __syncthreads();  // the previous chunk is fully consumed
+    stage_x<XT, PARTS, GS>(x, ldx, M, K, c * ce, ce, st, xpre);
+    __syncthreads();
+    if (xreg && c + 1 < nch) prefetch_x<XT>(x, ldx, M, K, (c + 1) * ce, ce, xpre);
+    const int iend = min((c + 1) * uc, iters);
+    for (int i0 = c * uc; i0 < iend; i0 += P) {
 #pragma unroll
-    for (int j = 0; j < P; ++j) {
-      const int i = i0 + j;
-      if (i < iters) {  // uniform over the workgroup
-        if (i % uc == 0) {
-          const int c = i / uc;
-          __syncthreads();  // the previous chunk is fully consumed
-          stage_x<XT, PARTS, GS>(x, ldx, M, K, c * ce, ce, st, xpre);
-          __syncthreads();
-          if (xreg && (c + 1) * uc < iters) prefetch_x<XT>(x, ldx, M, K, (c + 1) * ce, ce, xpre);
+      for (int j = 0; j < P; ++j) {
+        const int i = i0 + j;
+        if (i < iend) {
+          const int u = ks + ks_n * i;
+          if (active && u < nu) {
+            if constexpr (MT == 1 && MR == 1)
+              unit_m1<PARTS>(buf[j], st, ks + ks_n * (i - c * uc), lane, acc[0][0]);
+            else
+              unit_compute<PARTS, MT, MR>(buf[j], st, ks + ks_n * (i - c * uc), lane, M, acc);
+          }
+          const int un = u + ks_n * P;
+          if (i + P < iters && un < nu) load_unit(wrs, un * TU, r, g, buf[j]);
         }
-        const int u = ks + ks_n * i;
-        if (active && u < nu) {
-          if constexpr (MT == 1 && MR == 1)
-            unit_m1<PARTS>(buf[j], st, ks + ks_n * (i % uc), lane, acc[0][0]);
-          else
-            unit_compute<PARTS, MT, MR>(buf[j], st, ks + ks_n * (i % uc), lane, M, acc);
-        }
-        const int un = u + ks_n * P;
-        if (active && i + P < iters && un < nu) load_unit(wtile + (int64_t)un * TU, r, g, buf[j]);
       }
     }
   }
@@ -584,17 +650,27 @@ hipError_t launch_t(const XT *x, int64_t ldx, const uint8_t *W, int N, int K, fl
   constexpr int UE = Fmt<TYPE>::UE, GS = Dec<TYPE>::GS;
   const int ntiles = (N + 15) / 16;
   const int nu = K / UE;
+  constexpr int P = decode_p<TYPE, MT, MR>();
   // K split: enough waves to fill the chip once, at least two units per wave
   int ks = 1;
   while (ks < 4 && ntiles * ks * 2 <= GGUF_DECODE_WAVES && nu >= 4 * ks) ks <<= 1;
-  // staged activations per chunk stay under 48 KB; for small M a chunk is at
-  // most 256 * kXQ quads so that it can be prefetched into registers
+  // Units per wave per staged chunk: a multiple of P (the unrolled body never
+  // crosses a chunk), staging under 48 KB, and for small M at most 256 items
+  // of 16 activations so that a chunk can be prefetched into registers.
   const int per_unit = M * UE * 2 * PARTS;
-  const int iters = (nu + ks - 1) / ks;
-  int uc = iters;
-  while (uc > 1 && ks * uc * per_unit > 48 * 1024) uc = (uc + 1) / 2;
-  if (M * ks * UE <= 4 * 256 * kXQ)
-    while (uc > 1 && M * ks * uc * UE > 4 * 256 * kXQ) uc = (uc + 1) / 2;
+  auto up = [](int v) { return (v + P - 1) / P * P; };
+  int uc;
+  for (;;) {
+    uc = up((nu + ks - 1) / ks);
+    while (uc > P && ks * uc * per_unit > 48 * 1024) uc = up((uc + 1) / 2);
+    if (M * ks * P * UE <= kItem * 256)
+      while (uc > P && M * ks * uc * UE > kItem * 256) uc = up((uc + 1) / 2);
+    if (ks > 1 && ks * uc * per_unit > 48 * 1024) {
+      ks >>= 1;
+      continue;
+    }
+    break;
+  }
   const int ce = ks * uc * UE;
   const size_t lds = (size_t)M * (ce + kXPad) * 2 * PARTS + (size_t)(ce / GS) * 16 * MT * 4 +
                      (size_t)4 * MT * 4 * 64 * 4 + kZeroHalves * 2;
