@@ -61,8 +61,9 @@ int check_k(int t, int64_t k) {
   if (k <= 0 || k % b != 0)
     return fail(GGUF_HIP_ERR_SHAPE, "[GGUF] ne[0]=%lld not divisible by block size %d for type %d",
                 (long long)k, b, t);
-  if (k > (int64_t)1 << 30)
-    return fail(GGUF_HIP_ERR_SHAPE, "[gguf-hip] K=%lld too large", (long long)k);
+  // kernels address 8 row tiles of one K range with 32-bit byte offsets
+  if (k > (int64_t)1 << 24)
+    return fail(GGUF_HIP_ERR_SHAPE, "[gguf-hip] K=%lld too large (max 2^24)", (long long)k);
   return GGUF_HIP_OK;
 }
 
@@ -210,6 +211,9 @@ int gguf_hip_matmul_variant(const void *x, int x_type, int64_t ldx, const void *
   const hipStream_t s = (hipStream_t)stream;
   if (variant == GGUF_HIP_VARIANT_AUTO)
     variant = m <= GGUF_HIP_DECODE_MAX_M ? GGUF_HIP_VARIANT_DECODE : GGUF_HIP_VARIANT_GEMM;
+  // the GEMM addresses one 128-row activation block with 32-bit byte offsets
+  if (variant == GGUF_HIP_VARIANT_GEMM && (127 * ldx + k) * esize >= ((int64_t)1 << 31))
+    return fail(GGUF_HIP_ERR_SHAPE, "[gguf-hip] ldx too large for the GEMM kernel");
   const hipError_t e =
       variant == GGUF_HIP_VARIANT_DECODE
           ? gguf::launch_decode(x, x_type, ldx, (const uint8_t *)tiles, ggml_type, n, k, y, ldy, m, s)

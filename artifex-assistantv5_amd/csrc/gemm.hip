@@ -1,217 +1,466 @@
 // MFMA dequant-GEMM for prefill: y[m, n] = sum_k x[m, k] * dequant(W)[n, k].
 //
 // The reference has no GEMM for these types: prefill re-runs its GEMV once
-// per activation row (webgpu/src/engine/forward-pass.ts:1536-1539).  Here a
-// workgroup owns a BM x BN output tile; per 64-wide K step it stages the
-// activation tile (fp16) and the weight tile dequantized to fp16 (one
-// rounding of the exact f32 dequant value, RNE) in LDS, and its four waves
-// feed v_mfma_f32_16x16x32_f16 with f32 accumulation.  f32 activations are
-// rounded to fp16 when staged.  Weight tiles are read from the row-tile
-// layout (common.hpp): BN = 128 rows are 8 consecutive row tiles.
+// per activation row (webgpu/src/engine/forward-pass.ts:1536-1539).
+//
+// A workgroup of four waves owns a 128 x 128 output tile; wave w owns all 128
+// rows and the 32 columns [32 w, 32 w + 32) (two row tiles of the weight), so
+// no two waves need the same weight bytes.  K is walked in 64-wide steps:
+//
+//   weights      the row-tile layout (common.hpp) hands lane (r, g) exactly
+//                the 8 consecutive k of row r that form its operand of
+//                v_mfma_f32_16x16x32_f16, so each wave dequantizes its weight
+//                bytes straight into MFMA B registers.  A quant code enters
+//                as an f16 subnormal (code x 2^-24, exact) and one
+//                v_fma_mix computes fp16(d*sc*q - dmin*m) with f32 internals:
+//                the exact f32 dequant value rounded once to fp16.
+//   activations  staged through LDS as fp16 (f32 input is rounded to fp16),
+//                two buffers, rows of 128 B whose 16-byte chunks are rotated
+//                by the row index so that fragment reads and row writes are
+//                free of bank conflicts.  Q6_K's lanes hold k in the order
+//                16 lh + 4 g + b; its activation columns are permuted the same
+//                way when staged, so both MFMA operands agree.
+//
+// Pipeline, one barrier per step: issue the global loads of step s+1, run
+// step s's 32 MFMAs per wave, dequantize step s+1's weights into registers,
+// store its activations into the other LDS buffer, barrier.  All loads are
+// buffer loads; their scalar offsets only ever address bytes inside the
+// weight / activation block, and rows past M or N fall outside the buffer
+// resource by their vector offset and read as zero.  Tiles are assigned XCD
+// by XCD (workgroup b runs on XCD b % 8): each XCD gets a contiguous range of
+// tiles, m fastest, so its workgroups share weight columns in its L2.
 #include "common.hpp"
 
 namespace gguf {
 
 namespace {
 
-constexpr int kBK = 64;
-constexpr int kLd = kBK + 8;  // LDS row stride in halves (144 B, 16-B aligned)
+constexpr int kBM = 128, kBN = 128, kBK = 64;
+constexpr int kThreads = 256;
+constexpr int kTM = kBM / 16;  // 16-row MFMA tiles per wave
+constexpr int kTN = 2;         // 16-column MFMA tiles per wave
+constexpr int kRowB = 2 * kBK;             // LDS bytes per activation row
+constexpr int kStageB = kBM * kRowB;       // LDS bytes per pipeline stage
+constexpr float kTwo24 = 16777216.0f, kTwo20 = 1048576.0f;
 
-template <typename XT, int BM>
-__device__ __forceinline__ void stage_a(const XT *__restrict__ x, int64_t ldx, int M, int K,
-                                        int m0, int k0, half_t *As, int tid) {
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
+
+__device__ __forceinline__ rsrc_t make_rsrc(const void *base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc((void *)base, 0, (int)bytes, 0x00020000);
+}
+__device__ __forceinline__ uint4 bl16(rsrc_t rs, int voff, int soff) {
+  const auto v = __builtin_amdgcn_raw_buffer_load_b128(rs, voff, soff, 0);
+  return make_uint4(v[0], v[1], v[2], v[3]);
+}
+__device__ __forceinline__ uint2 bl8(rsrc_t rs, int voff, int soff) {
+  const auto v = __builtin_amdgcn_raw_buffer_load_b64(rs, voff, soff, 0);
+  return make_uint2(v[0], v[1]);
+}
+__device__ __forceinline__ uint32_t bl4(rsrc_t rs, int voff, int soff) {
+  return __builtin_amdgcn_raw_buffer_load_b32(rs, voff, soff, 0);
+}
+__device__ __forceinline__ uint32_t bl2(rsrc_t rs, int voff, int soff) {
+  return __builtin_amdgcn_raw_buffer_load_b16(rs, voff, soff, 0);
+}
+
+__device__ __forceinline__ half_t lo16(uint32_t w) { return __builtin_bit_cast(half2_t, w)[0]; }
+__device__ __forceinline__ half_t hi16(uint32_t w) { return __builtin_bit_cast(half2_t, w)[1]; }
+// fp16 of s * h + c computed in f32 (v_fma_mix{lo,hi}_f16)
+__device__ __forceinline__ half_t fmix(half_t h, float s, float c) {
+  return (half_t)__builtin_fmaf((float)h, s, c);
+}
+
+// ---------------------------------------------------------------------------
+// Weight operands.  Item j in {0, 1} is the wave's row tile 2 w + j; bf[j][h]
+// is its B operand for k in [k0 + 32 h, k0 + 32 h + 32).
+// ---------------------------------------------------------------------------
+template <int TYPE>
+struct BRaw;
+template <>
+struct BRaw<12> {
+  uint4 hd[kTN];  // d, dmin, 12 scale bytes of row r
+  uint2 q[kTN];   // the lane's 8 code bytes of the 64-wide window
+};
+template <>
+struct BRaw<14> {
+  uint4 pa[kTN], pb[kTN];  // the two pieces holding the window's quant dwords
+  uint32_t d[kTN], sc[kTN];
+};
+template <>
+struct BRaw<8> {
+  uint2 q[kTN][2];  // block b of the step: 8 int8 codes
+  uint32_t d[kTN][2];
+};
+
+struct BOff {       // per-lane vector offsets, fixed for the whole K loop
+  int v0, v1, v2, v3;
+};
+
+template <int TYPE>
+__device__ __forceinline__ BOff b_offsets(int r, int g);
+template <>
+__device__ __forceinline__ BOff b_offsets<12>(int r, int g) {
+  return BOff{16 * r, 256 + (16 * g + r) * 16, 0, 0};
+}
+template <>
+__device__ __forceinline__ BOff b_offsets<14>(int r, int g) {
+  return BOff{(16 * g + r) * 16, 3328 + 2 * r, 3072 + 16 * r, 0};
+}
+template <>
+__device__ __forceinline__ BOff b_offsets<8>(int r, int g) {
+  return BOff{32 + (16 * g + r) * 8, 2 * r, 0, 0};
+}
+
+// Loads for the 64-wide window c (0..3) of unit u (K-quants) or for blocks
+// 2u, 2u + 1 (Q8_0; c unused).  ts = bytes of one row tile.
+template <int C>
+__device__ __forceinline__ void load_b(rsrc_t rs, const BOff &o, int ts, int u, int nu,
+                                       BRaw<12> &b) {
+  constexpr int TU = Fmt<12>::TU;
+  const int su = u * TU;
 #pragma unroll
-  for (int p = tid; p < BM * 8; p += 256) {
-    const int r = p >> 3, cc = p & 7;
-    const int m = m0 + r, k = k0 + 8 * cc;
-    half8_t v;
-    if (m < M && k < K) {
-      if constexpr (sizeof(XT) == 4) {
-        const float4 *src = (const float4 *)(x + (int64_t)m * ldx + k);
-        const float4 a = src[0], b = src[1];
-        v = half8_t{(half_t)a.x, (half_t)a.y, (half_t)a.z, (half_t)a.w,
-                    (half_t)b.x, (half_t)b.y, (half_t)b.z, (half_t)b.w};
-      } else {
-        v = *(const half8_t *)(x + (int64_t)m * ldx + k);
+  for (int j = 0; j < kTN; ++j) {
+    b.hd[j] = bl16(rs, o.v0 + j * ts, su);
+    b.q[j] = bl8(rs, o.v1 + j * ts, su + (C >> 1) * 1024 + 8 * (C & 1));
+  }
+}
+template <int C>
+__device__ __forceinline__ void load_b(rsrc_t rs, const BOff &o, int ts, int u, int nu,
+                                       BRaw<14> &b) {
+  constexpr int TU = Fmt<14>::TU, HF = C >> 1, TP = C & 1;
+  const int su = u * TU;
+#pragma unroll
+  for (int j = 0; j < kTN; ++j) {
+    b.pa[j] = bl16(rs, o.v0 + j * ts, su + HF * 1024);
+    b.pb[j] = bl16(rs, o.v0 + j * ts, su + HF * 1024 + 1024);
+    b.d[j] = bl2(rs, o.v1 + j * ts, su);
+    b.sc[j] = bl4(rs, o.v2 + j * ts, su + 8 * HF + 4 * TP);
+  }
+}
+template <int C>
+__device__ __forceinline__ void load_b(rsrc_t rs, const BOff &o, int ts, int u, int nu,
+                                       BRaw<8> &b) {
+  constexpr int TU = Fmt<8>::TU;
+#pragma unroll
+  for (int blk = 0; blk < 2; ++blk) {
+    const int ub = 2 * u + blk;
+    if (ub < nu) {  // uniform: K may end after the first block of the step
+#pragma unroll
+      for (int j = 0; j < kTN; ++j) {
+        b.q[j][blk] = bl8(rs, o.v0 + j * ts, ub * TU);
+        b.d[j][blk] = bl2(rs, o.v1 + j * ts, ub * TU);
       }
     } else {
-      v = half8_t{0, 0, 0, 0, 0, 0, 0, 0};
+#pragma unroll
+      for (int j = 0; j < kTN; ++j) {
+        b.q[j][blk] = make_uint2(0, 0);
+        b.d[j][blk] = 0;
+      }
     }
-    *(half8_t *)(As + r * kLd + 8 * cc) = v;
   }
 }
 
-__device__ __forceinline__ void put8(half_t *dst, const float *v) {
-  half8_t a;
+// Q4_K: lane (r, g), window c = chunk c of the superblock: low nibbles are
+// sub-block 2c (k = 8 g .. 8 g + 7 of the first 32), high nibbles sub-block 2c + 1.
+template <int C>
+__device__ __forceinline__ void dequant_b(const BRaw<12> &b, half8_t (&bf)[kTN][2]) {
 #pragma unroll
-  for (int i = 0; i < 8; ++i) a[i] = (half_t)v[i];
-  *(half8_t *)dst = a;
-}
-__device__ __forceinline__ void put4(half_t *dst, const float *v) {
-  *(half4_t *)dst = half4_t{(half_t)v[0], (half_t)v[1], (half_t)v[2], (half_t)v[3]};
-}
-__device__ __forceinline__ void zero8(half_t *dst) {
-  *(half8_t *)dst = half8_t{0, 0, 0, 0, 0, 0, 0, 0};
+  for (int j = 0; j < kTN; ++j) {
+    const uint4 hd = b.hd[j];
+    uint32_t sc_lo, sc_hi, m_lo, m_hi;
+    q4k_scales_packed(hd.y, hd.z, hd.w, sc_lo, sc_hi, m_lo, m_hi);
+    const uint32_t scw = C < 2 ? sc_lo : sc_hi, mw = C < 2 ? m_lo : m_hi;
+    constexpr int B0 = (2 * C) & 3;
+    const float d = h2f(hd.x), dmin = h2f(hd.x >> 16);
+    const float s0 = (d * kTwo24) * ubyte(scw, B0), c0 = -(dmin * ubyte(mw, B0));
+    const float s1 = (d * kTwo20) * ubyte(scw, B0 + 1), c1 = -(dmin * ubyte(mw, B0 + 1));
+    half8_t lo, hi;
+#pragma unroll
+    for (int w = 0; w < 2; ++w) {
+      const uint32_t q = w ? b.q[j].y : b.q[j].x, q8 = q >> 8;
+      const uint32_t el = q & 0x000F000Fu, ol = q8 & 0x000F000Fu;  // bytes 0, 2 / 1, 3: low nibble
+      const uint32_t eh = q & 0x00F000F0u, oh = q8 & 0x00F000F0u;  // high nibble (x 16)
+      lo[4 * w + 0] = fmix(lo16(el), s0, c0);
+      lo[4 * w + 1] = fmix(lo16(ol), s0, c0);
+      lo[4 * w + 2] = fmix(hi16(el), s0, c0);
+      lo[4 * w + 3] = fmix(hi16(ol), s0, c0);
+      hi[4 * w + 0] = fmix(lo16(eh), s1, c1);
+      hi[4 * w + 1] = fmix(lo16(oh), s1, c1);
+      hi[4 * w + 2] = fmix(hi16(eh), s1, c1);
+      hi[4 * w + 3] = fmix(hi16(oh), s1, c1);
+    }
+    bf[j][0] = lo;
+    bf[j][1] = hi;
+  }
 }
 
-// Weight tile: BN rows x 64 columns [k0, k0 + 64) dequantized to fp16.
-// Work item = (row tile tt, lane slot (r, g)); rows past N are the zero
-// padding of the last tile or, for tiles past the end, skipped (written 0).
-template <int TYPE, int BN>
-__device__ __forceinline__ void stage_b(const uint8_t *__restrict__ W, int N, int K, int n0, int k0,
-                                        half_t *Bs, int tid) {
-  constexpr int TU = Fmt<TYPE>::TU, UE = Fmt<TYPE>::UE;
-  const int nu = K / UE;
-  const int ntiles = (N + 15) >> 4;
-  if (TYPE == 8) {
-    // two blocks per step: items (tt, b, g, r)
+// Q6_K: window c = quarters 2 (c & 1), 2 (c & 1) + 1 of half c >> 1.  The
+// lane's operand for k-block t2 (32 wide) holds the window columns
+// 32 t2 + 16 lh + 4 g + e at position 4 lh + e.
+template <int C>
+__device__ __forceinline__ void dequant_b(const BRaw<14> &b, half8_t (&bf)[kTN][2]) {
+  constexpr int HF = C >> 1, TP = C & 1;
 #pragma unroll
-    for (int p = tid; p < BN * 8; p += 256) {
-      const int r = p & 15, g = (p >> 4) & 3, b = (p >> 6) & 1, tt = p >> 7;
-      const int tile = (n0 >> 4) + tt, blk = (k0 >> 5) + b;
-      half_t *dst = Bs + (16 * tt + r) * kLd + 32 * b + 8 * g;
-      if (tile < ntiles && blk < nu) {
-        const uint8_t *tu = W + ((int64_t)tile * nu + blk) * TU;
-        const uint2 q = *(const uint2 *)(tu + 32 + (16 * g + r) * 8);
-        const float d = h2f(*(const uint16_t *)(tu + 2 * r));
-        float v[8];
+  for (int j = 0; j < kTN; ++j) {
+    const uint4 pa = b.pa[j], pb = b.pb[j];
+    // quant dwords 3i .. 3i + 2 of i = 2 HF + lh, taken from pieces HF and HF + 1
+    const uint32_t dq[2][3] = {{HF ? pa.z : pa.x, HF ? pa.w : pa.y, HF ? pb.x : pa.z},
+                               {HF ? pb.y : pa.w, HF ? pb.z : pb.x, HF ? pb.w : pb.y}};
+    const float d = h2f(b.d[j]);
 #pragma unroll
-        for (int i = 0; i < 8; ++i) v[i] = d * (float)(int8_t)(((i < 4 ? q.x : q.y) >> (8 * (i & 3))) & 0xFFu);
-        put8(dst, v);
-      } else {
-        zero8(dst);
-      }
-    }
-    return;
-  }
-  const int u = k0 >> 8, wq = (k0 >> 6) & 3;
-#pragma unroll
-  for (int p = tid; p < BN * 4; p += 256) {
-    const int r = p & 15, g = (p >> 4) & 3, tt = p >> 6;
-    const int tile = (n0 >> 4) + tt;
-    half_t *row = Bs + (16 * tt + r) * kLd;
-    if (tile >= ntiles) {
-      if (TYPE == 12) {
-        zero8(row + 8 * g);
-        zero8(row + 32 + 8 * g);
-      } else {
-#pragma unroll
-        for (int j = 0; j < 4; ++j) *(half4_t *)(row + 16 * j + 4 * g) = half4_t{0, 0, 0, 0};
-      }
-      continue;
-    }
-    const uint8_t *tu = W + ((int64_t)tile * nu + u) * TU;
-    if (TYPE == 12) {  // window = chunk c = wq: lo -> [8g, 8g+8), hi -> [32 + 8g, 32 + 8g + 8)
-      const int c = wq, cp = c >> 1, h = c & 1;
-      const uint4 hd = ldg16(tu + 16 * r);
-      const uint4 pc = ldg16(tu + 256 + ((4 * cp + g) * 16 + r) * 16);
-      const uint32_t q0 = h ? pc.z : pc.x, q1 = h ? pc.w : pc.y;
-      const float d = h2f(hd.x), dmin = h2f(hd.x >> 16);
-      uint32_t sc0, m0, sc1, m1;
-      q4k_scale_min(2 * c, hd.y, hd.z, hd.w, sc0, m0);
-      q4k_scale_min(2 * c + 1, hd.y, hd.z, hd.w, sc1, m1);
-      const float d1 = d * (float)sc0, mn1 = dmin * (float)m0;
-      const float d2 = d * (float)sc1, mn2 = dmin * (float)m1;
-      float lo[8], hi[8];
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const uint32_t b = ((i < 4 ? q0 : q1) >> (8 * (i & 3))) & 0xFFu;
-        lo[i] = d1 * (float)(b & 0x0Fu) - mn1;
-        hi[i] = d2 * (float)(b >> 4) - mn2;
-      }
-      put8(row + 8 * g, lo);
-      put8(row + 32 + 8 * g, hi);
-    } else {  // Q6_K: window = half hf, quarters t in {2 tp, 2 tp + 1}
-      const int hf = wq >> 1, tp = wq & 1;
-      const float d = h2f(*(const uint16_t *)(tu + 3328 + 2 * r));
-      const int8_t *sc = (const int8_t *)(tu + 3072 + 16 * r);
+    for (int t2 = 0; t2 < 2; ++t2) {
+      half8_t v;
 #pragma unroll
       for (int lh = 0; lh < 2; ++lh) {
-        const int i = 2 * hf + lh;  // dwords 3i .. 3i + 2 of the lane's 12
-        uint32_t dq[3];
-#pragma unroll
-        for (int j = 0; j < 3; ++j) {
-          const int dwi = 3 * i + j;
-          dq[j] = *(const uint32_t *)(tu + ((4 * (dwi >> 2) + g) * 16 + r) * 16 + 4 * (dwi & 3));
-        }
-#pragma unroll
-        for (int tt2 = 0; tt2 < 2; ++tt2) {
-          const int t = 2 * tp + tt2;
-          const uint32_t ql = (t & 1) ? dq[1] : dq[0];
-          const float s = d * (float)sc[8 * hf + 2 * t + lh];
-          float v[4];
-#pragma unroll
-          for (int b = 0; b < 4; ++b) {
-            const uint32_t qb = (ql >> (8 * b)) & 0xFFu, hb = (dq[2] >> (8 * b)) & 0xFFu;
-            const uint32_t nib = (t >> 1) ? (qb >> 4) : (qb & 0x0Fu);
-            v[b] = s * (float)((int)(nib | (((hb >> (2 * t)) & 3u) << 4)) - 32);
-          }
-          // window-local element 32 * tt2 + 16 lh + 4 g + b
-          put4(row + 32 * tt2 + 16 * lh + 4 * g, v);
-        }
+        const int t = 2 * TP + t2;
+        const uint32_t ql = dq[lh][t & 1], qh = dq[lh][2];
+        const uint32_t n4 = (t >> 1) ? ((ql >> 4) & 0x0F0F0F0Fu) : (ql & 0x0F0F0F0Fu);
+        const uint32_t q6 = n4 | (((qh >> (2 * t)) & 0x03030303u) << 4);
+        const uint32_t ev = q6 & 0x00FF00FFu, od = (q6 >> 8) & 0x00FF00FFu;
+        const float sv = d * (float)(int8_t)((b.sc[j] >> (8 * (2 * t2 + lh))) & 0xFFu);
+        const float s = sv * kTwo24, c = -32.0f * sv;
+        v[4 * lh + 0] = fmix(lo16(ev), s, c);
+        v[4 * lh + 1] = fmix(lo16(od), s, c);
+        v[4 * lh + 2] = fmix(hi16(ev), s, c);
+        v[4 * lh + 3] = fmix(hi16(od), s, c);
       }
+      bf[j][t2] = v;
     }
   }
 }
 
-template <int TYPE, typename XT, int BM, int BN, int WM, int WN>
-__global__ __launch_bounds__(256) void gemm_kernel(const XT *__restrict__ x, int64_t ldx,
-                                                   const uint8_t *__restrict__ W, int M, int N,
-                                                   int K, float *__restrict__ y, int64_t ldy) {
-  static_assert(WM * WN == 4, "four waves");
-  constexpr int TM = BM / WM / 16, TN = BN / WN / 16;
-  __shared__ half_t As[BM * kLd];
-  __shared__ half_t Bs[BN * kLd];
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int wm = wave / WN, wn = wave % WN;
-  const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
-  float4_t acc[TM][TN];
+// Q8_0: block b of the step is k-block b; code + 128 enters as a subnormal.
+template <int C>
+__device__ __forceinline__ void dequant_b(const BRaw<8> &b, half8_t (&bf)[kTN][2]) {
 #pragma unroll
-  for (int i = 0; i < TM; ++i)
+  for (int j = 0; j < kTN; ++j)
 #pragma unroll
-    for (int j = 0; j < TN; ++j) acc[i][j] = float4_t{0.f, 0.f, 0.f, 0.f};
-
-  for (int k0 = 0; k0 < K; k0 += kBK) {
-    stage_a<XT, BM>(x, ldx, M, K, m0, k0, As, tid);
-    stage_b<TYPE, BN>(W, N, K, n0, k0, Bs, tid);
-    __syncthreads();
+    for (int blk = 0; blk < 2; ++blk) {
+      const float d = h2f(b.d[j][blk]);
+      const float s = d * kTwo24, c = -128.0f * d;
+      half8_t v;
 #pragma unroll
-    for (int kk = 0; kk < kBK; kk += 32) {
-      half8_t a[TM], b[TN];
-#pragma unroll
-      for (int i = 0; i < TM; ++i)
-        a[i] = *(const half8_t *)(As + (wm * TM * 16 + i * 16 + (lane & 15)) * kLd + kk + 8 * (lane >> 4));
-#pragma unroll
-      for (int j = 0; j < TN; ++j)
-        b[j] = *(const half8_t *)(Bs + (wn * TN * 16 + j * 16 + (lane & 15)) * kLd + kk + 8 * (lane >> 4));
-#pragma unroll
-      for (int i = 0; i < TM; ++i)
-#pragma unroll
-        for (int j = 0; j < TN; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[i], b[j], acc[i][j], 0, 0, 0);
+      for (int w = 0; w < 2; ++w) {
+        const uint32_t q = (w ? b.q[j][blk].y : b.q[j][blk].x) ^ 0x80808080u;
+        const uint32_t ev = q & 0x00FF00FFu, od = (q >> 8) & 0x00FF00FFu;
+        v[4 * w + 0] = fmix(lo16(ev), s, c);
+        v[4 * w + 1] = fmix(lo16(od), s, c);
+        v[4 * w + 2] = fmix(hi16(ev), s, c);
+        v[4 * w + 3] = fmix(hi16(od), s, c);
+      }
+      bf[j][blk] = v;
     }
-    __syncthreads();
+}
+
+// ---------------------------------------------------------------------------
+// Activations.  Thread t stages rows (t >> 3) + 32 i, i = 0..3, 16-byte
+// column chunk t & 7 of the 64-wide step.
+// ---------------------------------------------------------------------------
+template <typename XT>
+struct ARaw {
+  static constexpr int W = sizeof(XT) / 2;  // 16-byte loads per item
+  uint4 v[4][W];
+};
+
+template <int TYPE, typename XT>
+__device__ __forceinline__ void load_a(rsrc_t rs, int voff, int64_t ldxb, int k0, int K, int cc,
+                                       ARaw<XT> &a) {
+  constexpr int W = ARaw<XT>::W;
+  const int soff = k0 * (int)sizeof(XT);
+  // only Q8_0 weights can end K halfway through a step; chunks past K read as zero
+  const bool ok = TYPE != 8 || k0 + 8 * cc < K;
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int w = 0; w < W; ++w)
+      a.v[i][w] = ok ? bl16(rs, voff + (int)(32 * i * ldxb) + 16 * w, soff) : make_uint4(0, 0, 0, 0);
+}
+
+__device__ __forceinline__ uint4 to_f16x8(const uint4 (&v)[1]) { return v[0]; }
+__device__ __forceinline__ uint4 to_f16x8(const uint4 (&v)[2]) {
+  half8_t h;
+  const uint4 a = v[0], b = v[1];
+  h[0] = (half_t)__uint_as_float(a.x);
+  h[1] = (half_t)__uint_as_float(a.y);
+  h[2] = (half_t)__uint_as_float(a.z);
+  h[3] = (half_t)__uint_as_float(a.w);
+  h[4] = (half_t)__uint_as_float(b.x);
+  h[5] = (half_t)__uint_as_float(b.y);
+  h[6] = (half_t)__uint_as_float(b.z);
+  h[7] = (half_t)__uint_as_float(b.w);
+  return __builtin_bit_cast(uint4, h);
+}
+
+// LDS byte address of (row, 16-byte chunk): chunks rotate by the row index.
+__device__ __forceinline__ int lds_at(int row, int chunk) {
+  return row * kRowB + ((chunk + row) & 7) * 16;
+}
+
+template <int TYPE, typename XT>
+__device__ __forceinline__ void store_a(unsigned char *lds, int stage, int row0, int cc,
+                                        const ARaw<XT> &a) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const uint4 h = to_f16x8(a.v[i]);
+    const int row = row0 + 32 * i;
+    unsigned char *base = lds + stage * kStageB;
+    if constexpr (TYPE == 14) {
+      // columns 8 q + e (q = cc & 3, e = 0..7) of k-block cc >> 2 go to
+      // position 8 g + 4 lh + (e & 3) with g = 2 (q & 1) + (e >> 2), lh = q >> 1
+      const int q = cc & 3, ch = 4 * (cc >> 2) + 2 * (q & 1), half = 8 * (q >> 1);
+      *(uint2 *)(base + lds_at(row, ch) + half) = make_uint2(h.x, h.y);
+      *(uint2 *)(base + lds_at(row, ch + 1) + half) = make_uint2(h.z, h.w);
+    } else {
+      *(uint4 *)(base + lds_at(row, cc)) = h;
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+
+template <int TYPE, typename XT>
+struct Gemm {
+  rsrc_t ars, brs;
+  int avoff, row0, cc;
+  int64_t ldxb;
+  int K, nu, ts;
+  BOff bo;
+  int afrag[2];  // LDS byte address of the lane's A fragment, k-block 0 / 1
+  ARaw<XT> ar[2];     // raw loads of the next two steps, by step parity
+  BRaw<TYPE> br[2];
+  half8_t bf[kTN][2];  // B operands of the current step
+  float4_t acc[kTM][kTN];
+  unsigned char *lds;
+
+  template <int C, int P>
+  __device__ __forceinline__ void load(int u, int k0) {
+    load_a<TYPE, XT>(ars, avoff, ldxb, k0, K, cc, ar[P]);
+    load_b<C>(brs, bo, ts, u, nu, br[P]);
   }
 
+  template <int C, int P>
+  __device__ __forceinline__ void prepare(int stage) {
+    dequant_b<C>(br[P], bf);
+    store_a<TYPE, XT>(lds, stage, row0, cc, ar[P]);
+  }
+
+  __device__ __forceinline__ void mma(int stage) {
+    const unsigned char *base = lds + stage * kStageB;
 #pragma unroll
-  for (int i = 0; i < TM; ++i)
+    for (int h = 0; h < 2; ++h) {
+      half8_t a[kTM];
 #pragma unroll
-    for (int j = 0; j < TN; ++j)
+      for (int i = 0; i < kTM; ++i) a[i] = *(const half8_t *)(base + afrag[h] + i * 16 * kRowB);
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int m = m0 + wm * TM * 16 + i * 16 + 4 * (lane >> 4) + r;
-        const int n = n0 + wn * TN * 16 + j * 16 + (lane & 15);
-        if (m < M && n < N) y[(int64_t)m * ldy + n] = acc[i][j][r];
+      for (int i = 0; i < kTM; ++i)
+#pragma unroll
+        for (int j = 0; j < kTN; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[i], bf[j][h], acc[i][j], 0, 0, 0);
+    }
+  }
+
+  // Step s (parity P = s & 1) from LDS stage P.  Loads step s + 2 (window C2 of
+  // unit u2, k = k2) into raw set P when `load2`; dequantizes / stages step
+  // s + 1 (window C1) from raw set P ^ 1 when `next`.
+  template <int P, int C1, int C2>
+  __device__ __forceinline__ void step(bool next, bool load2, int u2, int k2) {
+    if (load2) load<C2, P>(u2, k2);
+    mma(P);
+    if (next) prepare<C1, P ^ 1>(P ^ 1);
+    __syncthreads();
+  }
+};
+
+template <int TYPE, typename XT>
+__global__ __launch_bounds__(kThreads, 2) void gemm_kernel(const XT *__restrict__ x, int64_t ldx,
+                                                           const uint8_t *__restrict__ W, int M,
+                                                           int N, int K, float *__restrict__ y,
+                                                           int64_t ldy, int tiles_m) {
+  constexpr int TU = Fmt<TYPE>::TU, UE = Fmt<TYPE>::UE;
+  __shared__ __align__(16) unsigned char lds[2 * kStageB];
+
+  int bid = blockIdx.x;
+  if ((gridDim.x & 7) == 0) bid = (bid & 7) * (gridDim.x >> 3) + (bid >> 3);
+  const int m0 = (bid % tiles_m) * kBM, n0 = (bid / tiles_m) * kBN;
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int r = lane & 15, g = lane >> 4;
+
+  Gemm<TYPE, XT> s;
+  s.lds = lds;
+  s.K = K;
+  s.nu = K / UE;
+  s.ts = s.nu * TU;
+  // the wave's two row tiles; tiles past the weight's end are outside the resource
+  const int ntiles = (N + 15) >> 4, t0 = (n0 >> 4) + 2 * wave;
+  const int nt = __builtin_amdgcn_readfirstlane(max(0, min(kTN, ntiles - t0)));
+  s.brs = make_rsrc(W + (int64_t)t0 * s.ts, (uint32_t)__builtin_amdgcn_readfirstlane(nt * s.ts));
+  s.bo = b_offsets<TYPE>(r, g);
+  // activation rows m0 .. m0 + rows - 1; rows past M are outside the resource
+  const int rows = min(kBM, M - m0);
+  s.ldxb = ldx * (int64_t)sizeof(XT);
+  s.ars = make_rsrc(x + (int64_t)m0 * ldx,
+                    (uint32_t)__builtin_amdgcn_readfirstlane(
+                        (int)((int64_t)(rows - 1) * s.ldxb + (int64_t)K * sizeof(XT))));
+  s.row0 = tid >> 3;
+  s.cc = tid & 7;
+  s.avoff = (int)(s.row0 * s.ldxb) + s.cc * 16 * (int)ARaw<XT>::W;
+  s.afrag[0] = lds_at(r, g);
+  s.afrag[1] = lds_at(r, 4 + g);
+#pragma unroll
+  for (int i = 0; i < kTM; ++i)
+#pragma unroll
+    for (int j = 0; j < kTN; ++j) s.acc[i][j] = float4_t{0.f, 0.f, 0.f, 0.f};
+
+  if constexpr (UE == 256) {
+    // step s = 4 u + c covers window c of superblock u; 4 nu >= 4 steps
+    s.template load<0, 0>(0, 0);
+    s.template load<1, 1>(0, 64);
+    s.template prepare<0, 0>(0);
+    __syncthreads();
+    for (int u = 0; u < s.nu; ++u) {
+      const int k = u * 256;
+      const bool more = u + 1 < s.nu;
+      s.template step<0, 1, 2>(true, true, u, k + 128);
+      s.template step<1, 2, 3>(true, true, u, k + 192);
+      s.template step<0, 3, 0>(true, more, u + 1, k + 256);
+      s.template step<1, 0, 1>(more, more, u + 1, k + 320);
+    }
+  } else {
+    // step s covers blocks 2 s, 2 s + 1
+    const int steps = (s.nu + 1) >> 1;
+    s.template load<0, 0>(0, 0);
+    if (steps > 1) s.template load<0, 1>(1, kBK);
+    s.template prepare<0, 0>(0);
+    __syncthreads();
+    for (int st = 0; st < steps; st += 2) {
+      s.template step<0, 0, 0>(st + 1 < steps, st + 2 < steps, st + 2, (st + 2) * kBK);
+      if (st + 1 < steps)
+        s.template step<1, 0, 0>(st + 2 < steps, st + 3 < steps, st + 3, (st + 3) * kBK);
+    }
+  }
+
+  // D layout of the 16x16 MFMA: lane holds rows 4 g + e of column r
+#pragma unroll
+  for (int i = 0; i < kTM; ++i)
+#pragma unroll
+    for (int j = 0; j < kTN; ++j) {
+      const int n = n0 + 32 * wave + 16 * j + r;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int m = m0 + 16 * i + 4 * g + e;
+        if (m < M && n < N) y[(int64_t)m * ldy + n] = s.acc[i][j][e];
       }
+    }
 }
 
 template <int TYPE, typename XT>
 void launch_type(const XT *x, int64_t ldx, const uint8_t *W, int M, int N, int K, float *y,
                  int64_t ldy, hipStream_t s) {
-  constexpr int BM = 128, BN = 128;
-  const dim3 grid((unsigned)((N + BN - 1) / BN), (unsigned)((M + BM - 1) / BM));
-  hipLaunchKernelGGL((gemm_kernel<TYPE, XT, BM, BN, 2, 2>), grid, dim3(256), 0, s, x, ldx, W, M, N,
-                     K, y, ldy);
+  const int tiles_m = (M + kBM - 1) / kBM, tiles_n = (N + kBN - 1) / kBN;
+  hipLaunchKernelGGL((gemm_kernel<TYPE, XT>), dim3((unsigned)(tiles_m * tiles_n)), dim3(kThreads),
+                     0, s, x, ldx, W, M, N, K, y, ldy, tiles_m);
 }
 
 template <typename XT>
@@ -231,7 +480,9 @@ hipError_t launch_x(const XT *x, int64_t ldx, const uint8_t *W, int type, int64_
 hipError_t launch_gemm(const void *x, int x_type, int64_t ldx, const uint8_t *tiles, int type,
                        int64_t n, int64_t k, float *y, int64_t ldy, int64_t m, hipStream_t s) {
   const int esize = x_type == 0 ? 4 : 2;
-  const int64_t chunk = (int64_t)65535 * 128;  // grid.y cap
+  // one launch covers at most 2^30 output tiles; split M beyond that
+  const int64_t tiles_n = (n + kBN - 1) / kBN;
+  const int64_t chunk = ((int64_t)1 << 30) / tiles_n * kBM;
   hipError_t e = hipSuccess;
   for (int64_t m0 = 0; m0 < m && e == hipSuccess; m0 += chunk) {
     const int64_t mc = (m - m0) < chunk ? (m - m0) : chunk;
