@@ -3,9 +3,10 @@
 // The reference has no GEMM for these types: prefill re-runs its GEMV once
 // per activation row (webgpu/src/engine/forward-pass.ts:1536-1539).
 //
-// A workgroup of four waves owns a 128 x 128 output tile; wave w owns all 128
+// A workgroup of eight waves owns a 128 x 256 output tile; wave w owns all 128
 // rows and the 32 columns [32 w, 32 w + 32) (two row tiles of the weight), so
-// no two waves need the same weight bytes.  K is walked in 64-wide steps:
+// no two waves need the same weight bytes and one staged activation tile
+// feeds 256 columns.  K is walked in 64-wide steps:
 //
 //   weights      the row-tile layout (common.hpp) hands lane (r, g) exactly
 //                the 8 consecutive k of row r that form its operand of
@@ -35,10 +36,13 @@ namespace gguf {
 
 namespace {
 
-constexpr int kBM = 128, kBN = 128, kBK = 64;
-constexpr int kThreads = 256;
+constexpr int kWaves = 8;
+constexpr int kBM = 128, kBN = 32 * kWaves, kBK = 64;
+constexpr int kThreads = 64 * kWaves;
 constexpr int kTM = kBM / 16;  // 16-row MFMA tiles per wave
 constexpr int kTN = 2;         // 16-column MFMA tiles per wave
+constexpr int kAI = kBM * 8 / kThreads;  // activation chunks staged per thread
+constexpr int kARows = kThreads / 8;     // row distance between a thread's chunks
 constexpr int kRowB = 2 * kBK;             // LDS bytes per activation row
 constexpr int kStageB = kBM * kRowB;       // LDS bytes per pipeline stage
 constexpr float kTwo24 = 16777216.0f, kTwo20 = 1048576.0f;
@@ -78,18 +82,29 @@ template <int TYPE>
 struct BRaw;
 template <>
 struct BRaw<12> {
-  uint4 hd[kTN];  // d, dmin, 12 scale bytes of row r
-  uint2 q[kTN];   // the lane's 8 code bytes of the 64-wide window
+  uint2 q[kTN];  // the lane's 8 code bytes of the 64-wide window
 };
 template <>
 struct BRaw<14> {
   uint4 pa[kTN], pb[kTN];  // the two pieces holding the window's quant dwords
-  uint32_t d[kTN], sc[kTN];
 };
 template <>
 struct BRaw<8> {
   uint2 q[kTN][2];  // block b of the step: 8 int8 codes
   uint32_t d[kTN][2];
+};
+
+// Per-superblock fields of row r, loaded with the superblock's first window.
+template <int TYPE>
+struct BHdr {};
+template <>
+struct BHdr<12> {
+  uint4 hd[kTN];  // d, dmin, 12 scale bytes
+};
+template <>
+struct BHdr<14> {
+  uint4 sc[kTN];  // 16 int8 scales
+  uint32_t d[kTN];
 };
 
 struct BOff {       // per-lane vector offsets, fixed for the whole K loop
@@ -115,31 +130,33 @@ __device__ __forceinline__ BOff b_offsets<8>(int r, int g) {
 // 2u, 2u + 1 (Q8_0; c unused).  ts = bytes of one row tile.
 template <int C>
 __device__ __forceinline__ void load_b(rsrc_t rs, const BOff &o, int ts, int u, int nu,
-                                       BRaw<12> &b) {
+                                       BRaw<12> &b, BHdr<12> &h) {
   constexpr int TU = Fmt<12>::TU;
   const int su = u * TU;
 #pragma unroll
   for (int j = 0; j < kTN; ++j) {
-    b.hd[j] = bl16(rs, o.v0 + j * ts, su);
+    if (C == 0) h.hd[j] = bl16(rs, o.v0 + j * ts, su);
     b.q[j] = bl8(rs, o.v1 + j * ts, su + (C >> 1) * 1024 + 8 * (C & 1));
   }
 }
 template <int C>
 __device__ __forceinline__ void load_b(rsrc_t rs, const BOff &o, int ts, int u, int nu,
-                                       BRaw<14> &b) {
-  constexpr int TU = Fmt<14>::TU, HF = C >> 1, TP = C & 1;
+                                       BRaw<14> &b, BHdr<14> &h) {
+  constexpr int TU = Fmt<14>::TU, HF = C >> 1;
   const int su = u * TU;
 #pragma unroll
   for (int j = 0; j < kTN; ++j) {
     b.pa[j] = bl16(rs, o.v0 + j * ts, su + HF * 1024);
     b.pb[j] = bl16(rs, o.v0 + j * ts, su + HF * 1024 + 1024);
-    b.d[j] = bl2(rs, o.v1 + j * ts, su);
-    b.sc[j] = bl4(rs, o.v2 + j * ts, su + 8 * HF + 4 * TP);
+    if (C == 0) {
+      h.d[j] = bl2(rs, o.v1 + j * ts, su);
+      h.sc[j] = bl16(rs, o.v2 + j * ts, su);
+    }
   }
 }
 template <int C>
 __device__ __forceinline__ void load_b(rsrc_t rs, const BOff &o, int ts, int u, int nu,
-                                       BRaw<8> &b) {
+                                       BRaw<8> &b, BHdr<8> &) {
   constexpr int TU = Fmt<8>::TU;
 #pragma unroll
   for (int blk = 0; blk < 2; ++blk) {
@@ -163,10 +180,11 @@ __device__ __forceinline__ void load_b(rsrc_t rs, const BOff &o, int ts, int u, 
 // Q4_K: lane (r, g), window c = chunk c of the superblock: low nibbles are
 // sub-block 2c (k = 8 g .. 8 g + 7 of the first 32), high nibbles sub-block 2c + 1.
 template <int C>
-__device__ __forceinline__ void dequant_b(const BRaw<12> &b, half8_t (&bf)[kTN][2]) {
+__device__ __forceinline__ void dequant_b(const BRaw<12> &b, const BHdr<12> &h,
+                                          half8_t (&bf)[kTN][2]) {
 #pragma unroll
   for (int j = 0; j < kTN; ++j) {
-    const uint4 hd = b.hd[j];
+    const uint4 hd = h.hd[j];
     uint32_t sc_lo, sc_hi, m_lo, m_hi;
     q4k_scales_packed(hd.y, hd.z, hd.w, sc_lo, sc_hi, m_lo, m_hi);
     const uint32_t scw = C < 2 ? sc_lo : sc_hi, mw = C < 2 ? m_lo : m_hi;
@@ -198,7 +216,8 @@ __device__ __forceinline__ void dequant_b(const BRaw<12> &b, half8_t (&bf)[kTN][
 // lane's operand for k-block t2 (32 wide) holds the window columns
 // 32 t2 + 16 lh + 4 g + e at position 4 lh + e.
 template <int C>
-__device__ __forceinline__ void dequant_b(const BRaw<14> &b, half8_t (&bf)[kTN][2]) {
+__device__ __forceinline__ void dequant_b(const BRaw<14> &b, const BHdr<14> &h,
+                                          half8_t (&bf)[kTN][2]) {
   constexpr int HF = C >> 1, TP = C & 1;
 #pragma unroll
   for (int j = 0; j < kTN; ++j) {
@@ -206,7 +225,12 @@ __device__ __forceinline__ void dequant_b(const BRaw<14> &b, half8_t (&bf)[kTN][
     // quant dwords 3i .. 3i + 2 of i = 2 HF + lh, taken from pieces HF and HF + 1
     const uint32_t dq[2][3] = {{HF ? pa.z : pa.x, HF ? pa.w : pa.y, HF ? pb.x : pa.z},
                                {HF ? pb.y : pa.w, HF ? pb.z : pb.x, HF ? pb.w : pb.y}};
-    const float d = h2f(b.d[j]);
+    const float d = h2f(h.d[j]);
+    // scale bytes 8 HF + 4 TP .. + 3 of the window
+    const uint32_t scw = (2 * HF + TP) == 0 ? h.sc[j].x
+                         : (2 * HF + TP) == 1 ? h.sc[j].y
+                         : (2 * HF + TP) == 2 ? h.sc[j].z
+                                              : h.sc[j].w;
 #pragma unroll
     for (int t2 = 0; t2 < 2; ++t2) {
       half8_t v;
@@ -217,7 +241,7 @@ __device__ __forceinline__ void dequant_b(const BRaw<14> &b, half8_t (&bf)[kTN][
         const uint32_t n4 = (t >> 1) ? ((ql >> 4) & 0x0F0F0F0Fu) : (ql & 0x0F0F0F0Fu);
         const uint32_t q6 = n4 | (((qh >> (2 * t)) & 0x03030303u) << 4);
         const uint32_t ev = q6 & 0x00FF00FFu, od = (q6 >> 8) & 0x00FF00FFu;
-        const float sv = d * (float)(int8_t)((b.sc[j] >> (8 * (2 * t2 + lh))) & 0xFFu);
+        const float sv = d * (float)(int8_t)((scw >> (8 * (2 * t2 + lh))) & 0xFFu);
         const float s = sv * kTwo24, c = -32.0f * sv;
         v[4 * lh + 0] = fmix(lo16(ev), s, c);
         v[4 * lh + 1] = fmix(lo16(od), s, c);
@@ -231,7 +255,8 @@ __device__ __forceinline__ void dequant_b(const BRaw<14> &b, half8_t (&bf)[kTN][
 
 // Q8_0: block b of the step is k-block b; code + 128 enters as a subnormal.
 template <int C>
-__device__ __forceinline__ void dequant_b(const BRaw<8> &b, half8_t (&bf)[kTN][2]) {
+__device__ __forceinline__ void dequant_b(const BRaw<8> &b, const BHdr<8> &,
+                                          half8_t (&bf)[kTN][2]) {
 #pragma unroll
   for (int j = 0; j < kTN; ++j)
 #pragma unroll
@@ -253,13 +278,13 @@ __device__ __forceinline__ void dequant_b(const BRaw<8> &b, half8_t (&bf)[kTN][2
 }
 
 // ---------------------------------------------------------------------------
-// Activations.  Thread t stages rows (t >> 3) + 32 i, i = 0..3, 16-byte
+// Activations.  Thread t stages rows (t >> 3) + kARows i, i < kAI, 16-byte
 // column chunk t & 7 of the 64-wide step.
 // ---------------------------------------------------------------------------
 template <typename XT>
 struct ARaw {
   static constexpr int W = sizeof(XT) / 2;  // 16-byte loads per item
-  uint4 v[4][W];
+  uint4 v[kAI][W];
 };
 
 template <int TYPE, typename XT>
@@ -270,10 +295,11 @@ __device__ __forceinline__ void load_a(rsrc_t rs, int voff, int64_t ldxb, int k0
   // only Q8_0 weights can end K halfway through a step; chunks past K read as zero
   const bool ok = TYPE != 8 || k0 + 8 * cc < K;
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < kAI; ++i)
 #pragma unroll
     for (int w = 0; w < W; ++w)
-      a.v[i][w] = ok ? bl16(rs, voff + (int)(32 * i * ldxb) + 16 * w, soff) : make_uint4(0, 0, 0, 0);
+      a.v[i][w] =
+          ok ? bl16(rs, voff + (int)(kARows * i * ldxb) + 16 * w, soff) : make_uint4(0, 0, 0, 0);
 }
 
 __device__ __forceinline__ uint4 to_f16x8(const uint4 (&v)[1]) { return v[0]; }
@@ -300,9 +326,9 @@ template <int TYPE, typename XT>
 __device__ __forceinline__ void store_a(unsigned char *lds, int stage, int row0, int cc,
                                         const ARaw<XT> &a) {
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
+  for (int i = 0; i < kAI; ++i) {
     const uint4 h = to_f16x8(a.v[i]);
-    const int row = row0 + 32 * i;
+    const int row = row0 + kARows * i;
     unsigned char *base = lds + stage * kStageB;
     if constexpr (TYPE == 14) {
       // columns 8 q + e (q = cc & 3, e = 0..7) of k-block cc >> 2 go to
@@ -328,6 +354,7 @@ struct Gemm {
   int afrag[2];  // LDS byte address of the lane's A fragment, k-block 0 / 1
   ARaw<XT> ar[2];     // raw loads of the next two steps, by step parity
   BRaw<TYPE> br[2];
+  BHdr<TYPE> hn, hc;   // superblock fields: loaded ahead / in use
   half8_t bf[kTN][2];  // B operands of the current step
   float4_t acc[kTM][kTN];
   unsigned char *lds;
@@ -335,12 +362,13 @@ struct Gemm {
   template <int C, int P>
   __device__ __forceinline__ void load(int u, int k0) {
     load_a<TYPE, XT>(ars, avoff, ldxb, k0, K, cc, ar[P]);
-    load_b<C>(brs, bo, ts, u, nu, br[P]);
+    load_b<C>(brs, bo, ts, u, nu, br[P], hn);
   }
 
   template <int C, int P>
   __device__ __forceinline__ void prepare(int stage) {
-    dequant_b<C>(br[P], bf);
+    if (C == 0) hc = hn;
+    dequant_b<C>(br[P], hc, bf);
     store_a<TYPE, XT>(lds, stage, row0, cc, ar[P]);
   }
 
@@ -372,7 +400,7 @@ struct Gemm {
 };
 
 template <int TYPE, typename XT>
-__global__ __launch_bounds__(kThreads, 2) void gemm_kernel(const XT *__restrict__ x, int64_t ldx,
+__global__ __launch_bounds__(kThreads) void gemm_kernel(const XT *__restrict__ x, int64_t ldx,
                                                            const uint8_t *__restrict__ W, int M,
                                                            int N, int K, float *__restrict__ y,
                                                            int64_t ldy, int tiles_m) {
@@ -392,8 +420,8 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_kernel(const XT *__restrict_
   s.K = K;
   s.nu = K / UE;
   s.ts = s.nu * TU;
-  // the wave's two row tiles; tiles past the weight's end are outside the resource
-  const int ntiles = (N + 15) >> 4, t0 = (n0 >> 4) + 2 * wave;
+  // the wave's kTN row tiles; tiles past the weight's end are outside the resource
+  const int ntiles = (N + 15) >> 4, t0 = (n0 >> 4) + kTN * wave;
   const int nt = __builtin_amdgcn_readfirstlane(max(0, min(kTN, ntiles - t0)));
   s.brs = make_rsrc(W + (int64_t)t0 * s.ts, (uint32_t)__builtin_amdgcn_readfirstlane(nt * s.ts));
   s.bo = b_offsets<TYPE>(r, g);
@@ -446,7 +474,7 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_kernel(const XT *__restrict_
   for (int i = 0; i < kTM; ++i)
 #pragma unroll
     for (int j = 0; j < kTN; ++j) {
-      const int n = n0 + 32 * wave + 16 * j + r;
+      const int n = n0 + 16 * (kTN * wave + j) + r;
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const int m = m0 + 16 * i + 4 * g + e;
