@@ -67,11 +67,27 @@ __device__ __forceinline__ uint32_t bl2(rsrc_t rs, int voff, int soff) {
   return __builtin_amdgcn_raw_buffer_load_b16(rs, voff, soff, 0);
 }
 
-__device__ __forceinline__ half_t lo16(uint32_t w) { return __builtin_bit_cast(half2_t, w)[0]; }
-__device__ __forceinline__ half_t hi16(uint32_t w) { return __builtin_bit_cast(half2_t, w)[1]; }
-// fp16 of s * h + c computed in f32 (v_fma_mix{lo,hi}_f16)
-__device__ __forceinline__ half_t fmix(half_t h, float s, float c) {
-  return (half_t)__builtin_fmaf((float)h, s, c);
+// Two f16 results packed in a word: fp16(s * x + c) for the f16 x taken from
+// the low halves (mix_lo) or the high halves (mix_hi) of a and b, computed in
+// f32 and rounded once (v_fma_mixlo_f16 / v_fma_mixhi_f16).
+__device__ __forceinline__ uint32_t mix_lo(uint32_t a, uint32_t b, float s, float c) {
+  uint32_t r;
+  asm("v_fma_mixlo_f16 %0, %1, %2, %3 op_sel_hi:[1,0,0]\n\t"
+      "v_fma_mixhi_f16 %0, %4, %2, %3 op_sel_hi:[1,0,0]"
+      : "=&v"(r)
+      : "v"(a), "v"(s), "v"(c), "v"(b));
+  return r;
+}
+__device__ __forceinline__ uint32_t mix_hi(uint32_t a, uint32_t b, float s, float c) {
+  uint32_t r;
+  asm("v_fma_mixlo_f16 %0, %1, %2, %3 op_sel:[1,0,0] op_sel_hi:[1,0,0]\n\t"
+      "v_fma_mixhi_f16 %0, %4, %2, %3 op_sel:[1,0,0] op_sel_hi:[1,0,0]"
+      : "=&v"(r)
+      : "v"(a), "v"(s), "v"(c), "v"(b));
+  return r;
+}
+__device__ __forceinline__ half8_t h8(uint32_t a, uint32_t b, uint32_t c, uint32_t d) {
+  return __builtin_bit_cast(half8_t, make_uint4(a, b, c, d));
 }
 
 // ---------------------------------------------------------------------------
@@ -105,6 +121,39 @@ template <>
 struct BHdr<14> {
   uint4 sc[kTN];  // 16 int8 scales
   uint32_t d[kTN];
+};
+
+// The same fields in the form the dequantization uses, derived once per superblock.
+template <int TYPE>
+struct BCur {
+  __device__ __forceinline__ void set(const BHdr<TYPE> &) {}
+};
+template <>
+struct BCur<12> {
+  uint32_t sc[kTN][2], mn[kTN][2];  // 6-bit scales / mins 0-3 and 4-7, one per byte
+  float d24[kTN], d20[kTN], dmin[kTN];
+  __device__ __forceinline__ void set(const BHdr<12> &h) {
+#pragma unroll
+    for (int j = 0; j < kTN; ++j) {
+      q4k_scales_packed(h.hd[j].y, h.hd[j].z, h.hd[j].w, sc[j][0], sc[j][1], mn[j][0], mn[j][1]);
+      const float d = h2f(h.hd[j].x);
+      d24[j] = d * kTwo24;
+      d20[j] = d * kTwo20;
+      dmin[j] = h2f(h.hd[j].x >> 16);
+    }
+  }
+};
+template <>
+struct BCur<14> {
+  uint4 sc[kTN];
+  float d[kTN];
+  __device__ __forceinline__ void set(const BHdr<14> &h) {
+#pragma unroll
+    for (int j = 0; j < kTN; ++j) {
+      sc[j] = h.sc[j];
+      d[j] = h2f(h.d[j]);
+    }
+  }
 };
 
 struct BOff {       // per-lane vector offsets, fixed for the whole K loop
@@ -180,35 +229,27 @@ __device__ __forceinline__ void load_b(rsrc_t rs, const BOff &o, int ts, int u, 
 // Q4_K: lane (r, g), window c = chunk c of the superblock: low nibbles are
 // sub-block 2c (k = 8 g .. 8 g + 7 of the first 32), high nibbles sub-block 2c + 1.
 template <int C>
-__device__ __forceinline__ void dequant_b(const BRaw<12> &b, const BHdr<12> &h,
+__device__ __forceinline__ void dequant_b(const BRaw<12> &b, const BCur<12> &h,
                                           half8_t (&bf)[kTN][2]) {
+  constexpr int W = C >> 1, B0 = (2 * C) & 3;  // scale word, byte of sub-block 2C
 #pragma unroll
   for (int j = 0; j < kTN; ++j) {
-    const uint4 hd = h.hd[j];
-    uint32_t sc_lo, sc_hi, m_lo, m_hi;
-    q4k_scales_packed(hd.y, hd.z, hd.w, sc_lo, sc_hi, m_lo, m_hi);
-    const uint32_t scw = C < 2 ? sc_lo : sc_hi, mw = C < 2 ? m_lo : m_hi;
-    constexpr int B0 = (2 * C) & 3;
-    const float d = h2f(hd.x), dmin = h2f(hd.x >> 16);
-    const float s0 = (d * kTwo24) * ubyte(scw, B0), c0 = -(dmin * ubyte(mw, B0));
-    const float s1 = (d * kTwo20) * ubyte(scw, B0 + 1), c1 = -(dmin * ubyte(mw, B0 + 1));
-    half8_t lo, hi;
+    const float s0 = h.d24[j] * ubyte(h.sc[j][W], B0), c0 = -(h.dmin[j] * ubyte(h.mn[j][W], B0));
+    const float s1 = h.d20[j] * ubyte(h.sc[j][W], B0 + 1),
+                c1 = -(h.dmin[j] * ubyte(h.mn[j][W], B0 + 1));
+    uint32_t lo[4], hi[4];
 #pragma unroll
     for (int w = 0; w < 2; ++w) {
       const uint32_t q = w ? b.q[j].y : b.q[j].x, q8 = q >> 8;
       const uint32_t el = q & 0x000F000Fu, ol = q8 & 0x000F000Fu;  // bytes 0, 2 / 1, 3: low nibble
       const uint32_t eh = q & 0x00F000F0u, oh = q8 & 0x00F000F0u;  // high nibble (x 16)
-      lo[4 * w + 0] = fmix(lo16(el), s0, c0);
-      lo[4 * w + 1] = fmix(lo16(ol), s0, c0);
-      lo[4 * w + 2] = fmix(hi16(el), s0, c0);
-      lo[4 * w + 3] = fmix(hi16(ol), s0, c0);
-      hi[4 * w + 0] = fmix(lo16(eh), s1, c1);
-      hi[4 * w + 1] = fmix(lo16(oh), s1, c1);
-      hi[4 * w + 2] = fmix(hi16(eh), s1, c1);
-      hi[4 * w + 3] = fmix(hi16(oh), s1, c1);
+      lo[2 * w] = mix_lo(el, ol, s0, c0);
+      lo[2 * w + 1] = mix_hi(el, ol, s0, c0);
+      hi[2 * w] = mix_lo(eh, oh, s1, c1);
+      hi[2 * w + 1] = mix_hi(eh, oh, s1, c1);
     }
-    bf[j][0] = lo;
-    bf[j][1] = hi;
+    bf[j][0] = h8(lo[0], lo[1], lo[2], lo[3]);
+    bf[j][1] = h8(hi[0], hi[1], hi[2], hi[3]);
   }
 }
 
@@ -216,7 +257,7 @@ __device__ __forceinline__ void dequant_b(const BRaw<12> &b, const BHdr<12> &h,
 // lane's operand for k-block t2 (32 wide) holds the window columns
 // 32 t2 + 16 lh + 4 g + e at position 4 lh + e.
 template <int C>
-__device__ __forceinline__ void dequant_b(const BRaw<14> &b, const BHdr<14> &h,
+__device__ __forceinline__ void dequant_b(const BRaw<14> &b, const BCur<14> &h,
                                           half8_t (&bf)[kTN][2]) {
   constexpr int HF = C >> 1, TP = C & 1;
 #pragma unroll
@@ -225,7 +266,7 @@ __device__ __forceinline__ void dequant_b(const BRaw<14> &b, const BHdr<14> &h,
     // quant dwords 3i .. 3i + 2 of i = 2 HF + lh, taken from pieces HF and HF + 1
     const uint32_t dq[2][3] = {{HF ? pa.z : pa.x, HF ? pa.w : pa.y, HF ? pb.x : pa.z},
                                {HF ? pb.y : pa.w, HF ? pb.z : pb.x, HF ? pb.w : pb.y}};
-    const float d = h2f(h.d[j]);
+    const float d = h.d[j];
     // scale bytes 8 HF + 4 TP .. + 3 of the window
     const uint32_t scw = (2 * HF + TP) == 0 ? h.sc[j].x
                          : (2 * HF + TP) == 1 ? h.sc[j].y
@@ -233,7 +274,7 @@ __device__ __forceinline__ void dequant_b(const BRaw<14> &b, const BHdr<14> &h,
                                               : h.sc[j].w;
 #pragma unroll
     for (int t2 = 0; t2 < 2; ++t2) {
-      half8_t v;
+      uint32_t v[4];
 #pragma unroll
       for (int lh = 0; lh < 2; ++lh) {
         const int t = 2 * TP + t2;
@@ -243,19 +284,17 @@ __device__ __forceinline__ void dequant_b(const BRaw<14> &b, const BHdr<14> &h,
         const uint32_t ev = q6 & 0x00FF00FFu, od = (q6 >> 8) & 0x00FF00FFu;
         const float sv = d * (float)(int8_t)((scw >> (8 * (2 * t2 + lh))) & 0xFFu);
         const float s = sv * kTwo24, c = -32.0f * sv;
-        v[4 * lh + 0] = fmix(lo16(ev), s, c);
-        v[4 * lh + 1] = fmix(lo16(od), s, c);
-        v[4 * lh + 2] = fmix(hi16(ev), s, c);
-        v[4 * lh + 3] = fmix(hi16(od), s, c);
+        v[2 * lh] = mix_lo(ev, od, s, c);
+        v[2 * lh + 1] = mix_hi(ev, od, s, c);
       }
-      bf[j][t2] = v;
+      bf[j][t2] = h8(v[0], v[1], v[2], v[3]);
     }
   }
 }
 
 // Q8_0: block b of the step is k-block b; code + 128 enters as a subnormal.
 template <int C>
-__device__ __forceinline__ void dequant_b(const BRaw<8> &b, const BHdr<8> &,
+__device__ __forceinline__ void dequant_b(const BRaw<8> &b, const BCur<8> &,
                                           half8_t (&bf)[kTN][2]) {
 #pragma unroll
   for (int j = 0; j < kTN; ++j)
@@ -263,17 +302,15 @@ __device__ __forceinline__ void dequant_b(const BRaw<8> &b, const BHdr<8> &,
     for (int blk = 0; blk < 2; ++blk) {
       const float d = h2f(b.d[j][blk]);
       const float s = d * kTwo24, c = -128.0f * d;
-      half8_t v;
+      uint32_t v[4];
 #pragma unroll
       for (int w = 0; w < 2; ++w) {
         const uint32_t q = (w ? b.q[j][blk].y : b.q[j][blk].x) ^ 0x80808080u;
         const uint32_t ev = q & 0x00FF00FFu, od = (q >> 8) & 0x00FF00FFu;
-        v[4 * w + 0] = fmix(lo16(ev), s, c);
-        v[4 * w + 1] = fmix(lo16(od), s, c);
-        v[4 * w + 2] = fmix(hi16(ev), s, c);
-        v[4 * w + 3] = fmix(hi16(od), s, c);
+        v[2 * w] = mix_lo(ev, od, s, c);
+        v[2 * w + 1] = mix_hi(ev, od, s, c);
       }
-      bf[j][blk] = v;
+      bf[j][blk] = h8(v[0], v[1], v[2], v[3]);
     }
 }
 
@@ -354,7 +391,8 @@ struct Gemm {
   int afrag[2];  // LDS byte address of the lane's A fragment, k-block 0 / 1
   ARaw<XT> ar[2];     // raw loads of the next two steps, by step parity
   BRaw<TYPE> br[2];
-  BHdr<TYPE> hn, hc;   // superblock fields: loaded ahead / in use
+  BHdr<TYPE> hn;       // superblock fields loaded ahead
+  BCur<TYPE> hc;       // superblock fields in use
   half8_t bf[kTN][2];  // B operands of the current step
   float4_t acc[kTM][kTN];
   unsigned char *lds;
@@ -367,34 +405,41 @@ struct Gemm {
 
   template <int C, int P>
   __device__ __forceinline__ void prepare(int stage) {
-    if (C == 0) hc = hn;
+    if (C == 0) hc.set(hn);
     dequant_b<C>(br[P], hc, bf);
     store_a<TYPE, XT>(lds, stage, row0, cc, ar[P]);
   }
 
-  __device__ __forceinline__ void mma(int stage) {
-    const unsigned char *base = lds + stage * kStageB;
+  // Step s (parity P = s & 1) from LDS stage P.  Loads step s + 2 (window C2 of
+  // unit u2, k = k2) into raw set P when `load2`; dequantizes / stages step
+  // s + 1 (window C1) from raw set P ^ 1 when `next`.  The schedule is pinned:
+  // global loads first, then all sixteen A fragment reads, then the 32 MFMAs
+  // with the dequantization of the next step's weights interleaved.
+  template <int P, int C1, int C2>
+  __device__ __forceinline__ void step(bool next, bool load2, int u2, int k2) {
+    if (load2) load<C2, P>(u2, k2);
+    const unsigned char *base = lds + P * kStageB;
+    half8_t a[2][kTM];
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      half8_t a[kTM];
+    for (int h = 0; h < 2; ++h)
 #pragma unroll
-      for (int i = 0; i < kTM; ++i) a[i] = *(const half8_t *)(base + afrag[h] + i * 16 * kRowB);
+      for (int i = 0; i < kTM; ++i) a[h][i] = *(const half8_t *)(base + afrag[h] + i * 16 * kRowB);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
 #pragma unroll
       for (int i = 0; i < kTM; ++i)
 #pragma unroll
         for (int j = 0; j < kTN; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[i], bf[j][h], acc[i][j], 0, 0, 0);
+          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[h][i], bf[j][h], acc[i][j], 0, 0, 0);
+    if (next) {
+      prepare<C1, P ^ 1>(P ^ 1);
+#pragma unroll
+      for (int i = 0; i < 2 * kTM * kTN; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
+        __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);  // four VALU
+      }
     }
-  }
-
-  // Step s (parity P = s & 1) from LDS stage P.  Loads step s + 2 (window C2 of
-  // unit u2, k = k2) into raw set P when `load2`; dequantizes / stages step
-  // s + 1 (window C1) from raw set P ^ 1 when `next`.
-  template <int P, int C1, int C2>
-  __device__ __forceinline__ void step(bool next, bool load2, int u2, int k2) {
-    if (load2) load<C2, P>(u2, k2);
-    mma(P);
-    if (next) prepare<C1, P ^ 1>(P ^ 1);
     __syncthreads();
   }
 };
