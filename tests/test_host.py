@@ -1,5 +1,7 @@
 """Host-side logic (CPU only): type traits, layout math, quantizer, layout model."""
 
+import importlib
+
 import numpy as np
 import pytest
 
@@ -94,3 +96,28 @@ def test_synthetic_inputs_seeded(pkg):
     assert np.array_equal(a, b) and a.dtype == np.float32
     h = pkg.quantize.synthetic_activations(2, 64, seed=5, dtype=np.float16)
     assert h.dtype == np.float16 and np.array_equal(h, a.astype(np.float16))
+
+
+def test_decoder_weight_bytes_per_token():
+    dec = importlib.import_module("artifex-assistantv5_amd.decoder")
+    cfg = dec.DecoderConfig()
+    # 137.82 MB per layer (Q4_K q/k/v/o and gate/up, Q6_K down) + 510.5 MB Q6_K LM head
+    assert cfg.weight_bytes_per_token() == 32 * 137_822_208 + 510_504_960
+    assert cfg.qkv_rows == 6144
+
+
+def test_decoder_rope_tables_and_norm():
+    import torch
+    dec = importlib.import_module("artifex-assistantv5_amd.decoder")
+    cfg = dec.DecoderConfig(head_dim=8, max_seq=4, rope_base=100.0)
+    cos, sin = dec.rope_tables(cfg, "cpu")
+    # theta(pos, i) = pos / base^(2i/d): position 0 is the identity, pairs i and i + d/2
+    x = torch.arange(8, dtype=torch.float32).view(1, 1, 8)
+    y = dec.apply_rope(x, cos[:1], sin[:1])
+    assert torch.equal(x, y)
+    y = dec.apply_rope(x, cos[3:4], sin[3:4])
+    th = 3.0 / 100.0 ** (torch.arange(4, dtype=torch.float64) * 2 / 8)
+    z = torch.complex(x[0, 0, :4].double(), x[0, 0, 4:].double()) * torch.exp(1j * th)
+    assert torch.allclose(y[0, 0].double(), torch.cat([z.real, z.imag]), atol=1e-6)
+    v = torch.tensor([[3.0, 4.0]])
+    assert torch.allclose(dec.rms_norm(v, torch.ones(2), 0.0), v / (12.5 ** 0.5))
