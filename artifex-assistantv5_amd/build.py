@@ -19,7 +19,7 @@ ROOT = os.path.dirname(HERE)
 CSRC = os.path.join(HERE, "csrc")
 BUILD = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libgguf_hip.so")
-SOURCES = ["api.hip", "layout.hip", "decode.hip", "gemm.hip"]
+SOURCES = ["api.hip", "layout.hip", "decode.hip", "gemm.hip", "glue.hip"]
 ARCH = "gfx950"
 
 HIPCC_FLAGS = [

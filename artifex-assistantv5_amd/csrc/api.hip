@@ -221,6 +221,89 @@ int gguf_hip_matmul_variant(const void *x, int x_type, int64_t ldx, const void *
   return hip_status(e, "matmul launch");
 }
 
+int gguf_hip_rmsnorm(const float *x, const float *w, float eps, float *y, int64_t rows,
+                     int64_t n, void *stream) {
+  return gguf_hip_add_rmsnorm(const_cast<float *>(x), nullptr, w, eps, y, rows, n, stream);
+}
+
+int gguf_hip_add_rmsnorm(float *x, const float *res, const float *w, float eps, float *y,
+                         int64_t rows, int64_t n, void *stream) {
+  if (rows < 0 || n <= 0 || n % 4 || n > ((int64_t)1 << 30) || rows > 65535 * 1024)
+    return fail(GGUF_HIP_ERR_SHAPE, "[gguf-hip] rmsnorm: bad shape rows=%lld n=%lld",
+                (long long)rows, (long long)n);
+  if (!(eps >= 0.0f)) return fail(GGUF_HIP_ERR_SHAPE, "[gguf-hip] rmsnorm: eps must be >= 0");
+  if (rows == 0) return ok();
+  if (!x || !w || !y) return fail(GGUF_HIP_ERR_NULL, "[gguf-hip] null pointer");
+  if (!aligned(x, 16) || !aligned(w, 16) || !aligned(y, 16) || (res && !aligned(res, 16)))
+    return fail(GGUF_HIP_ERR_ALIGN, "[gguf-hip] rmsnorm buffers must be 16-byte aligned");
+  if (res && y == x) return fail(GGUF_HIP_ERR_SHAPE, "[gguf-hip] add_rmsnorm: y aliases x");
+  return hip_status(gguf::launch_rmsnorm(x, res, w, eps, y, rows, n, (hipStream_t)stream),
+                    "rmsnorm launch");
+}
+
+int gguf_hip_swiglu(const float *gate_up, float *out, int64_t rows, int64_t ffn, void *stream) {
+  if (rows < 0 || ffn <= 0 || ffn % 4 || ffn > ((int64_t)1 << 30) || rows > 65535)
+    return fail(GGUF_HIP_ERR_SHAPE, "[gguf-hip] swiglu: bad shape rows=%lld ffn=%lld",
+                (long long)rows, (long long)ffn);
+  if (rows == 0) return ok();
+  if (!gate_up || !out) return fail(GGUF_HIP_ERR_NULL, "[gguf-hip] null pointer");
+  if (!aligned(gate_up, 16) || !aligned(out, 16))
+    return fail(GGUF_HIP_ERR_ALIGN, "[gguf-hip] swiglu buffers must be 16-byte aligned");
+  return hip_status(gguf::launch_swiglu(gate_up, out, rows, ffn, (hipStream_t)stream),
+                    "swiglu launch");
+}
+
+int check_attention(int n_heads, int n_kv_heads, int head_dim, int64_t max_seq) {
+  if (n_heads <= 0 || n_kv_heads <= 0 || n_heads % n_kv_heads || n_heads / n_kv_heads > 8)
+    return fail(GGUF_HIP_ERR_SHAPE,
+                "[gguf-hip] attention: n_heads %d must be 1..8 times n_kv_heads %d", n_heads,
+                n_kv_heads);
+  if (head_dim != 64 && head_dim != 128 && head_dim != 256)
+    return fail(GGUF_HIP_ERR_SHAPE, "[gguf-hip] attention: head_dim %d not 64, 128 or 256",
+                head_dim);
+  if (max_seq <= 0 || max_seq > (1 << 20))
+    return fail(GGUF_HIP_ERR_SHAPE, "[gguf-hip] attention: max_seq %lld out of range",
+                (long long)max_seq);
+  if ((int64_t)n_kv_heads * max_seq * head_dim > ((int64_t)1 << 31))
+    return fail(GGUF_HIP_ERR_SHAPE, "[gguf-hip] attention: cache of one layer too large");
+  return GGUF_HIP_OK;
+}
+
+int64_t gguf_hip_attention_workspace(int n_heads, int n_kv_heads, int head_dim, int64_t max_seq) {
+  const int rc = check_attention(n_heads, n_kv_heads, head_dim, max_seq);
+  if (rc) return rc;
+  ok();
+  return gguf::attention_work_bytes(n_heads, n_kv_heads, head_dim, max_seq);
+}
+
+int gguf_hip_attention_decode(const float *qkv, const int64_t *pos, const float *cos_table,
+                              const float *sin_table, float *k_cache, float *v_cache, float *out,
+                              int n_heads, int n_kv_heads, int head_dim, int64_t max_seq,
+                              void *work, void *stream) {
+  int rc = check_attention(n_heads, n_kv_heads, head_dim, max_seq);
+  if (rc) return rc;
+  if (!qkv || !pos || !cos_table || !sin_table || !k_cache || !v_cache || !out || !work)
+    return fail(GGUF_HIP_ERR_NULL, "[gguf-hip] null pointer");
+  if (!aligned(qkv, 16) || !aligned(k_cache, 16) || !aligned(v_cache, 16) || !aligned(out, 4) ||
+      !aligned(pos, 8) || !aligned(cos_table, 4) || !aligned(sin_table, 4) || !aligned(work, 16))
+    return fail(GGUF_HIP_ERR_ALIGN, "[gguf-hip] attention buffers misaligned");
+  return hip_status(gguf::launch_attention_decode(qkv, pos, cos_table, sin_table, k_cache,
+                                                  v_cache, out, (float *)work, n_heads,
+                                                  n_kv_heads, head_dim, max_seq,
+                                                  (hipStream_t)stream),
+                    "attention launch");
+}
+
+int64_t gguf_hip_argmax_workspace(void) { return gguf::argmax_work_bytes(); }
+
+int gguf_hip_argmax(const float *x, int64_t n, int64_t *out, void *work, void *stream) {
+  if (n <= 0) return fail(GGUF_HIP_ERR_SHAPE, "[gguf-hip] argmax: n must be positive");
+  if (!x || !out || !work) return fail(GGUF_HIP_ERR_NULL, "[gguf-hip] null pointer");
+  if (!aligned(x, 4) || !aligned(out, 8) || !aligned(work, 8))
+    return fail(GGUF_HIP_ERR_ALIGN, "[gguf-hip] argmax buffers misaligned");
+  return hip_status(gguf::launch_argmax(x, n, out, work, (hipStream_t)stream), "argmax launch");
+}
+
 int gguf_hip_matmul(const void *x, int x_type, int64_t ldx, const void *tiles, int ggml_type,
                     int64_t n, int64_t k, float *y, int64_t ldy, int64_t m, void *stream) {
   return gguf_hip_matmul_variant(x, x_type, ldx, tiles, ggml_type, n, k, y, ldy, m,

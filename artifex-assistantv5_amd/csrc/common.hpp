@@ -143,5 +143,14 @@ hipError_t launch_decode(const void *x, int x_type, int64_t ldx, const uint8_t *
                          int64_t n, int64_t k, float *y, int64_t ldy, int64_t m, hipStream_t s);
 hipError_t launch_gemm(const void *x, int x_type, int64_t ldx, const uint8_t *tiles, int type,
                        int64_t n, int64_t k, float *y, int64_t ldy, int64_t m, hipStream_t s);
+hipError_t launch_rmsnorm(float *x, const float *r, const float *w, float eps, float *y,
+                          int64_t rows, int64_t n, hipStream_t s);
+hipError_t launch_swiglu(const float *gu, float *out, int64_t rows, int64_t ffn, hipStream_t s);
+int64_t attention_work_bytes(int nh, int nkv, int hd, int64_t max_seq);
+hipError_t launch_attention_decode(const float *qkv, const int64_t *pos, const float *cs,
+                                   const float *sn, float *kc, float *vc, float *out, float *work,
+                                   int nh, int nkv, int hd, int64_t max_seq, hipStream_t s);
+int64_t argmax_work_bytes();
+hipError_t launch_argmax(const float *x, int64_t n, int64_t *out, void *work, hipStream_t s);
 
 }  // namespace gguf

@@ -1,0 +1,376 @@
+// Decode-step glue of a Llama-style layer around the quantized projections:
+// RMSNorm (optionally fused with the residual add that precedes it), SwiGLU,
+// rotate_half RoPE + KV-cache append + GQA attention for one new position,
+// and greedy argmax.  Reference shaders: rmsnorm.wgsl:1-9,58-67,
+// rope.wgsl:1-10, elementwise.wgsl:96-102 (gate_silu), argmax.wgsl; the
+// layer loop is webgpu/src/engine/forward-pass.ts:2925-3297.
+//
+// All kernels are f32, one row (or one KV head) per workgroup; they are small
+// and latency-bound, so the goal is one launch per op with coalesced 16-byte
+// accesses, not occupancy.
+#include "common.hpp"
+
+namespace gguf {
+
+namespace {
+
+constexpr int kGlueThreads = 256;
+
+// Sum over the workgroup; every thread gets the result.  `red` holds one
+// float per wave.
+__device__ __forceinline__ float block_sum(float v, float *red) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  __syncthreads();
+  if (lane == 0) red[wave] = v;
+  __syncthreads();
+  float s = 0.f;
+  for (int w = 0; w < (int)(blockDim.x >> 6); ++w) s += red[w];
+  return s;
+}
+
+__device__ __forceinline__ float block_max(float v, float *red) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  __syncthreads();
+  if (lane == 0) red[wave] = v;
+  __syncthreads();
+  float s = red[0];
+  for (int w = 1; w < (int)(blockDim.x >> 6); ++w) s = fmaxf(s, red[w]);
+  return s;
+}
+
+// y = x * 1/sqrt(mean(x^2) + eps) * w  (rmsnorm.wgsl:58-67, direct weight);
+// with r != null the residual add x += r is applied first and x is updated.
+// Rows of up to 4 * 4 * kNormThreads elements are held in registers (one
+// read of x); longer rows are read twice.
+constexpr int kNormThreads = 1024;
+__global__ __launch_bounds__(kNormThreads) void rmsnorm_kernel(float *__restrict__ x,
+                                                               const float *__restrict__ r,
+                                                               const float *__restrict__ w,
+                                                               float eps, float *__restrict__ y,
+                                                               int n) {
+  __shared__ float red[kNormThreads / 64];
+  float *xr = x + (int64_t)blockIdx.x * n;
+  const float *rr = r ? r + (int64_t)blockIdx.x * n : nullptr;
+  float *yr = y + (int64_t)blockIdx.x * n;
+  constexpr int R = 4;
+  float4 v[R];
+  float ss = 0.f;
+#pragma unroll
+  for (int c = 0; c < R; ++c) {
+    const int i = 4 * (c * kNormThreads + threadIdx.x);
+    v[c] = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (i < n) {
+      v[c] = *(const float4 *)(xr + i);
+      if (rr) {
+        const float4 a = *(const float4 *)(rr + i);
+        v[c].x += a.x;
+        v[c].y += a.y;
+        v[c].z += a.z;
+        v[c].w += a.w;
+        *(float4 *)(xr + i) = v[c];
+      }
+    }
+    ss += v[c].x * v[c].x + v[c].y * v[c].y + v[c].z * v[c].z + v[c].w * v[c].w;
+  }
+  for (int i = 4 * (R * kNormThreads + threadIdx.x); i < n; i += 4 * kNormThreads) {
+    float4 a = *(const float4 *)(xr + i);
+    if (rr) {
+      const float4 b = *(const float4 *)(rr + i);
+      a.x += b.x;
+      a.y += b.y;
+      a.z += b.z;
+      a.w += b.w;
+      *(float4 *)(xr + i) = a;
+    }
+    ss += a.x * a.x + a.y * a.y + a.z * a.z + a.w * a.w;
+  }
+  const float inv = 1.0f / sqrtf(block_sum(ss, red) / (float)n + eps);
+#pragma unroll
+  for (int c = 0; c < R; ++c) {
+    const int i = 4 * (c * kNormThreads + threadIdx.x);
+    if (i < n) {
+      const float4 g = *(const float4 *)(w + i);
+      *(float4 *)(yr + i) = make_float4(v[c].x * inv * g.x, v[c].y * inv * g.y,
+                                        v[c].z * inv * g.z, v[c].w * inv * g.w);
+    }
+  }
+  for (int i = 4 * (R * kNormThreads + threadIdx.x); i < n; i += 4 * kNormThreads) {
+    const float4 a = *(const float4 *)(xr + i), g = *(const float4 *)(w + i);
+    *(float4 *)(yr + i) = make_float4(a.x * inv * g.x, a.y * inv * g.y, a.z * inv * g.z,
+                                      a.w * inv * g.w);
+  }
+}
+
+// out[i] = up[i] * silu(gate[i]) for a row [gate (ffn) | up (ffn)]
+// (elementwise.wgsl:96-102 with a = up, b = gate).
+__global__ __launch_bounds__(kGlueThreads) void swiglu_kernel(const float *__restrict__ gu,
+                                                              float *__restrict__ out, int ffn) {
+  const float *g = gu + (int64_t)blockIdx.y * 2 * ffn, *u = g + ffn;
+  float *o = out + (int64_t)blockIdx.y * ffn;
+  const int i = 4 * (blockIdx.x * kGlueThreads + threadIdx.x);
+  if (i >= ffn) return;
+  const float4 a = *(const float4 *)(g + i), b = *(const float4 *)(u + i);
+  *(float4 *)(o + i) = make_float4(b.x * (a.x / (1.0f + expf(-a.x))), b.y * (a.y / (1.0f + expf(-a.y))),
+                                   b.z * (a.z / (1.0f + expf(-a.z))), b.w * (a.w / (1.0f + expf(-a.w))));
+}
+
+// Decode attention, flash-decoding style.  Pass 1: workgroup (g, sp) takes KV
+// head g and cache slots [64 sp, 64 sp + 64) of the causal range 0..p,
+// p = *pos.  The workgroup whose range holds p first writes slot p (k after
+// rotate_half RoPE, v as is).  Each computes, for the grp query heads of g,
+// the running max m, sum l of exp(s - m) and o = sum exp(s - m) v over its
+// slots, into work[(g * S + sp) * grp + j] records of hd + 2 floats.
+// Pass 2 merges the S records of each query head.
+constexpr int kSplit = 64;
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
+  return v;
+}
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+  return v;
+}
+
+__global__ __launch_bounds__(kGlueThreads) void attention_split_kernel(
+    const float *__restrict__ qkv, const int64_t *__restrict__ pos, const float *__restrict__ cs,
+    const float *__restrict__ sn, float *__restrict__ kc, float *__restrict__ vc,
+    float *__restrict__ work, int nh, int nkv, int hd, int max_seq) {
+  __shared__ __align__(16) float qs[8 * 256];       // grp * hd roped, scaled queries
+  __shared__ float pr[8 * kSplit];                  // grp * kSplit probabilities
+  __shared__ float wred[8 * 4];
+  const int grp = nh / nkv, g = blockIdx.x, sp = blockIdx.y, half = hd / 2, tid = threadIdx.x;
+  const int S = gridDim.y;
+  const int64_t p64 = pos[0];
+  if (p64 < 0 || p64 >= max_seq) return;  // no cache slot: write nothing
+  const int p = (int)p64, T = p + 1, t0 = sp * kSplit;
+  if (t0 >= T) return;  // beyond the causal range: no record (pass 2 reads sp < ceil(T / 64))
+  const int tn = min(kSplit, T - t0);
+  const float *crow = cs + (int64_t)p * half, *srow = sn + (int64_t)p * half;
+  float *kbase = kc + (int64_t)g * max_seq * hd, *vbase = vc + (int64_t)g * max_seq * hd;
+  if (p < t0 + kSplit) {  // this range holds the new slot
+    const float *kin = qkv + (int64_t)nh * hd + g * hd;
+    const float *vin = qkv + (int64_t)(nh + nkv) * hd + g * hd;
+    float *krow = kbase + (int64_t)p * hd, *vrow = vbase + (int64_t)p * hd;
+    for (int i = tid; i < half; i += kGlueThreads) {
+      const float c = crow[i], s = srow[i], a = kin[i], b = kin[i + half];
+      krow[i] = a * c - b * s;
+      krow[i + half] = b * c + a * s;
+    }
+    for (int i = tid; i < hd; i += kGlueThreads) vrow[i] = vin[i];
+  }
+  const float scale = 1.0f / sqrtf((float)hd);
+  for (int e = tid; e < grp * half; e += kGlueThreads) {
+    const int j = e / half, i = e % half;
+    const float *q = qkv + (int64_t)(g * grp + j) * hd;
+    const float c = crow[i], s = srow[i], a = q[i], b = q[i + half];
+    qs[j * hd + i] = (a * c - b * s) * scale;
+    qs[j * hd + i + half] = (b * c + a * s) * scale;
+  }
+  __syncthreads();  // slot p and the queries are visible to the workgroup
+
+  // scores: wave w takes slots t0 + 16 w + (lane & 15); the four lanes of a
+  // slot split hd into quarters and combine with two shuffles
+  const int lane = tid & 63, w = tid >> 6, tl = 16 * w + (lane & 15), qt = lane >> 4;
+  const int qlen = hd / 4;
+  float acc[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) acc[j] = 0.f;
+  if (tl < tn) {
+    const float *kr = kbase + (int64_t)(t0 + tl) * hd + qt * qlen;
+    for (int i = 0; i < qlen; i += 4) {
+      const float4 kv = *(const float4 *)(kr + i);
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+        if (j < grp) {
+          const float4 q = *(const float4 *)(qs + j * hd + qt * qlen + i);
+          acc[j] += q.x * kv.x + q.y * kv.y + q.z * kv.z + q.w * kv.w;
+        }
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    acc[j] += __shfl_xor(acc[j], 16);
+    acc[j] += __shfl_xor(acc[j], 32);
+  }
+  // per query: max and exp-sum over the workgroup's slots
+  float mj[8], lj[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    if (j >= grp) break;
+    const float sv = tl < tn ? acc[j] : -INFINITY;
+    const float m = wave_max(sv);
+    if (lane == 0) wred[j * 4 + w] = m;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    if (j >= grp) break;
+    mj[j] = fmaxf(fmaxf(wred[j * 4], wred[j * 4 + 1]), fmaxf(wred[j * 4 + 2], wred[j * 4 + 3]));
+  }
+  __syncthreads();
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    if (j >= grp) break;
+    const float e = tl < tn ? expf(acc[j] - mj[j]) : 0.f;
+    if (qt == 0 && tl < kSplit) pr[j * kSplit + tl] = e;
+    const float l = wave_sum(qt == 0 ? e : 0.f);
+    if (lane == 0) wred[j * 4 + w] = l;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    if (j >= grp) break;
+    lj[j] = wred[j * 4] + wred[j * 4 + 1] + wred[j * 4 + 2] + wred[j * 4 + 3];
+  }
+  // partial output: thread -> element i = tid % hd, queries j = tid / hd, + 256 / hd, ...
+  float *rec = work + ((int64_t)(g * S + sp) * grp) * (hd + 2);
+  const int step = kGlueThreads / hd;  // hd divides 256 (hd is 64, 128 or 256)
+  const int i = tid % hd;
+  for (int j = tid / hd; j < grp; j += step) {
+    float o = 0.f;
+    for (int t = 0; t < tn; ++t) o += pr[j * kSplit + t] * vbase[(int64_t)(t0 + t) * hd + i];
+    rec[j * (hd + 2) + 2 + i] = o;
+  }
+  if (tid < grp) {
+    rec[tid * (hd + 2)] = mj[0];
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+      if (j == tid) {
+        rec[tid * (hd + 2)] = mj[j];
+        rec[tid * (hd + 2) + 1] = lj[j];
+      }
+  }
+}
+
+// Pass 2: query head h = blockIdx.x merges the records of its KV head.
+__global__ __launch_bounds__(kGlueThreads) void attention_merge_kernel(
+    const int64_t *__restrict__ pos, const float *__restrict__ work, float *__restrict__ out,
+    int nh, int nkv, int hd, int S, int max_seq) {
+  const int grp = nh / nkv, h = blockIdx.x, g = h / grp, j = h % grp;
+  const int64_t p64 = pos[0];
+  if (p64 < 0 || p64 >= max_seq) return;  // pass 1 wrote no records
+  const int n = ((int)p64 + kSplit) / kSplit;  // records written: ceil((p + 1) / 64)
+  const float *base = work + ((int64_t)g * S * grp + j) * (hd + 2);
+  const int64_t stride = (int64_t)grp * (hd + 2);
+  float M = -INFINITY;
+  for (int s = 0; s < n; ++s) M = fmaxf(M, base[s * stride]);
+  float L = 0.f;
+  for (int s = 0; s < n; ++s) L += base[s * stride + 1] * expf(base[s * stride] - M);
+  const float inv = 1.0f / L;
+  for (int i = threadIdx.x; i < hd; i += kGlueThreads) {
+    float o = 0.f;
+    for (int s = 0; s < n; ++s) o += base[s * stride + 2 + i] * expf(base[s * stride] - M);
+    out[(int64_t)h * hd + i] = o * inv;
+  }
+}
+
+// Argmax, pass 1: workgroup b scans a contiguous chunk and writes its (value,
+// index) with the first index on ties and NaN never winning; pass 2 (one
+// workgroup) merges the partials the same way.
+constexpr int kArgBlocks = 256;
+
+__device__ __forceinline__ void better(float &v, int64_t &i, float ov, int64_t oi) {
+  if (ov > v || (ov == v && oi < i)) {
+    v = ov;
+    i = oi;
+  }
+}
+
+__device__ __forceinline__ void block_argmax(float &v, int64_t &idx, float *bv, int64_t *bi) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) better(v, idx, __shfl_xor(v, o), __shfl_xor(idx, o));
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  if (lane == 0) {
+    bv[wave] = v;
+    bi[wave] = idx;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0)
+    for (int w2 = 1; w2 < (int)(blockDim.x >> 6); ++w2) better(v, idx, bv[w2], bi[w2]);
+}
+
+__global__ __launch_bounds__(kGlueThreads) void argmax_partial_kernel(const float *__restrict__ x,
+                                                                      int64_t n,
+                                                                      float *__restrict__ pv,
+                                                                      int64_t *__restrict__ pi) {
+  __shared__ float bv[kGlueThreads / 64];
+  __shared__ int64_t bi[kGlueThreads / 64];
+  const int64_t chunk = (n + kArgBlocks - 1) / kArgBlocks;
+  const int64_t lo = (int64_t)blockIdx.x * chunk, hi = min(n, lo + chunk);
+  float v = -INFINITY;
+  int64_t idx = INT64_MAX;  // no candidate yet
+  for (int64_t i = lo + threadIdx.x; i < hi; i += kGlueThreads) better(v, idx, x[i], i);
+  block_argmax(v, idx, bv, bi);
+  if (threadIdx.x == 0) {
+    pv[blockIdx.x] = v;
+    pi[blockIdx.x] = idx;
+  }
+}
+
+__global__ __launch_bounds__(kGlueThreads) void argmax_merge_kernel(const float *__restrict__ pv,
+                                                                    const int64_t *__restrict__ pi,
+                                                                    int64_t *__restrict__ out) {
+  __shared__ float bv[kGlueThreads / 64];
+  __shared__ int64_t bi[kGlueThreads / 64];
+  float v = -INFINITY;
+  int64_t idx = INT64_MAX;
+  for (int b = threadIdx.x; b < kArgBlocks; b += kGlueThreads) better(v, idx, pv[b], pi[b]);
+  block_argmax(v, idx, bv, bi);
+  if (threadIdx.x == 0) out[0] = idx == INT64_MAX ? 0 : idx;
+}
+
+}  // namespace
+
+hipError_t launch_rmsnorm(float *x, const float *r, const float *w, float eps, float *y,
+                          int64_t rows, int64_t n, hipStream_t s) {
+  hipLaunchKernelGGL(rmsnorm_kernel, dim3((unsigned)rows), dim3(kNormThreads), 0, s, x, r, w, eps,
+                     y, (int)n);
+  return hipGetLastError();
+}
+
+hipError_t launch_swiglu(const float *gu, float *out, int64_t rows, int64_t ffn, hipStream_t s) {
+  const unsigned bx = (unsigned)((ffn / 4 + kGlueThreads - 1) / kGlueThreads);
+  hipLaunchKernelGGL(swiglu_kernel, dim3(bx, (unsigned)rows), dim3(kGlueThreads), 0, s, gu, out,
+                     (int)ffn);
+  return hipGetLastError();
+}
+
+int64_t attention_work_bytes(int nh, int nkv, int hd, int64_t max_seq) {
+  const int64_t S = (max_seq + kSplit - 1) / kSplit;
+  return (int64_t)sizeof(float) * nkv * S * (nh / nkv) * (hd + 2);
+}
+
+hipError_t launch_attention_decode(const float *qkv, const int64_t *pos, const float *cs,
+                                   const float *sn, float *kc, float *vc, float *out, float *work,
+                                   int nh, int nkv, int hd, int64_t max_seq, hipStream_t s) {
+  const int S = (int)((max_seq + kSplit - 1) / kSplit);
+  hipLaunchKernelGGL(attention_split_kernel, dim3((unsigned)nkv, (unsigned)S), dim3(kGlueThreads),
+                     0, s, qkv, pos, cs, sn, kc, vc, work, nh, nkv, hd, (int)max_seq);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL(attention_merge_kernel, dim3((unsigned)nh), dim3(kGlueThreads), 0, s, pos,
+                     work, out, nh, nkv, hd, S, (int)max_seq);
+  return hipGetLastError();
+}
+
+int64_t argmax_work_bytes() { return (int64_t)kArgBlocks * (sizeof(float) + sizeof(int64_t)); }
+
+hipError_t launch_argmax(const float *x, int64_t n, int64_t *out, void *work, hipStream_t s) {
+  int64_t *pi = (int64_t *)work;
+  float *pv = (float *)(pi + kArgBlocks);
+  hipLaunchKernelGGL(argmax_partial_kernel, dim3(kArgBlocks), dim3(kGlueThreads), 0, s, x, n, pv,
+                     pi);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL(argmax_merge_kernel, dim3(1), dim3(kGlueThreads), 0, s, pv, pi, out);
+  return hipGetLastError();
+}
+
+}  // namespace gguf

@@ -17,10 +17,13 @@ Glue semantics follow the reference's shaders:
 Every projection goes through ``dispatch_matmul_gguf`` (libgguf_hip): Q/K/V are
 one row-concatenated weight and gate/up another (the reference's gate+up
 fusion, forward-pass.ts:740-791, applied to Q/K/V too; byte-identical to
-separate dispatches).  The glue ops (norms, RoPE, attention, SwiGLU, argmax)
-run as torch ops in f32 on the same stream.  A decode step keeps the token
-and position in device tensors, so it can be captured once in a HIP graph and
-replayed for every generated token without host synchronization.
+separate dispatches).  A decode step runs the glue as libgguf_hip kernels
+(``glue.py``: RMSNorm fused with the residual add, RoPE + KV append + GQA
+attention in one launch, SwiGLU, argmax) over preallocated buffers: eight
+launches per layer.  Prefill (many positions at once) runs the glue as torch
+f32 ops; ``fused=False`` does the same for decode steps.  A decode step keeps
+the token and position in device tensors, so it can be captured once in a HIP
+graph and replayed for every generated token without host synchronization.
 """
 
 from __future__ import annotations
@@ -33,7 +36,7 @@ from typing import Optional
 import numpy as np
 import torch
 
-from . import quantize
+from . import glue, quantize
 from .ggml import Q4_K, Q6_K
 from .linear import GGUFWeight, LayerWeights, concat_rows, dispatch_matmul_gguf, repack_gguf_for_gpu
 
@@ -158,14 +161,24 @@ def apply_rope(x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor) -> torch.T
 class QuantDecoder:
     """Greedy decoder over ``DecoderWeights`` with an f32 KV cache in HBM."""
 
-    def __init__(self, cfg: DecoderConfig, weights: DecoderWeights, device="cuda"):
-        self.cfg, self.w, self.device = cfg, weights, torch.device(device)
+    def __init__(self, cfg: DecoderConfig, weights: DecoderWeights, device="cuda",
+                 fused: bool = True):
+        self.cfg, self.w, self.device, self.fused = cfg, weights, torch.device(device), fused
         L, kv, T, hd = cfg.n_layers, cfg.n_kv_heads, cfg.max_seq, cfg.head_dim
         self.k_cache = torch.zeros(L, kv, T, hd, device=self.device)
         self.v_cache = torch.zeros(L, kv, T, hd, device=self.device)
         self.cos, self.sin = rope_tables(cfg, self.device)
         self.t_idx = torch.arange(T, device=self.device)
         self._graph = None
+        # static buffers of the fused decode step
+        e = lambda n: torch.empty(1, n, device=self.device)  # noqa: E731
+        d = cfg.d_model
+        self.b_x, self.b_h, self.b_qkv = e(d), e(d), e(cfg.qkv_rows)
+        self.b_att, self.b_o = e(cfg.n_heads * hd), e(d)
+        self.b_gu, self.b_a, self.b_d = e(2 * cfg.ffn), e(cfg.ffn), e(d)
+        self.b_logits = e(cfg.vocab)
+        self.w_att = glue.attention_workspace(cfg.n_heads, cfg.n_kv_heads, hd, T, self.device)
+        self.w_arg = glue.argmax_workspace(self.device)
 
     # -- one pass of all layers over M tokens at positions ``pos`` (device [M]) --
     def _proj(self, x: torch.Tensor, w: GGUFWeight, label: str) -> torch.Tensor:
@@ -220,11 +233,38 @@ class QuantDecoder:
         x = self._layers(x, pos)
         return self._logits(x[-1:])
 
+    def _proj_into(self, x: torch.Tensor, w: GGUFWeight, y: torch.Tensor, label: str) -> None:
+        dispatch_matmul_gguf(x, w, y, 1, w.n, w.k, label)
+
+    def _step_fused(self, tok: torch.Tensor, pos: torch.Tensor) -> torch.Tensor:
+        cfg, W = self.cfg, self.w
+        x, h = self.b_x, self.b_h
+        x.copy_(W.embed.index_select(0, tok))
+        glue.rmsnorm(x, W.layers[0].attn_norm, cfg.eps, h)
+        for l, lw in enumerate(W.layers):
+            self._proj_into(h, lw.qkv_gg, self.b_qkv, f"L{l}-qkv")
+            glue.attention_decode(self.b_qkv, pos, self.cos, self.sin, self.k_cache[l],
+                                  self.v_cache[l], self.b_att, cfg.n_heads, cfg.n_kv_heads,
+                                  cfg.head_dim, self.w_att)
+            self._proj_into(self.b_att, lw.o_gg, self.b_o, f"L{l}-o")
+            glue.add_rmsnorm(x, self.b_o, lw.ffn_norm, cfg.eps, h)
+            self._proj_into(h, lw.gateUp_gg, self.b_gu, f"L{l}-gateUp")
+            glue.swiglu(self.b_gu, self.b_a)
+            self._proj_into(self.b_a, lw.down_gg, self.b_d, f"L{l}-down")
+            nxt = W.layers[l + 1].attn_norm if l + 1 < len(W.layers) else W.final_norm
+            glue.add_rmsnorm(x, self.b_d, nxt, cfg.eps, h)
+        self._proj_into(h, W.lm_head_gg, self.b_logits, "lm_head")
+        glue.argmax(self.b_logits, tok, self.w_arg)
+        pos.add_(1)
+        return self.b_logits
+
     @torch.no_grad()
     def step(self, tok: torch.Tensor, pos: torch.Tensor) -> torch.Tensor:
         """One greedy decode step in place: reads token ``tok`` [1] at position
         ``pos`` [1], writes the next token into ``tok`` and advances ``pos``.
         Touches no host state, so it can be captured in a graph."""
+        if self.fused:
+            return self._step_fused(tok, pos)
         x = self.w.embed.index_select(0, tok).float()
         x = self._layers(x, pos)
         logits = self._logits(x)
@@ -262,6 +302,9 @@ class QuantDecoder:
         """Greedy generation: returns the new token ids and prefill / decode timings.
         tok/s = n_new / decode wall time (prefill excluded, generate.ts:1155-1160)."""
         dev = self.device
+        if prompt.numel() + n_new > self.cfg.max_seq:
+            raise ValueError(f"prompt {prompt.numel()} + {n_new} new tokens exceed max_seq "
+                             f"{self.cfg.max_seq}")
         self.k_cache.zero_()
         self.v_cache.zero_()
         torch.cuda.synchronize(dev)

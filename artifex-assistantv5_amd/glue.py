@@ -1,0 +1,101 @@
+"""Decode-step glue kernels of libgguf_hip (f32 torch tensors on the current HIP stream).
+
+Each function is one launch; shapes are checked here and again by the library.
+Reference shaders: rmsnorm.wgsl:1-9,58-67, rope.wgsl:1-10,
+elementwise.wgsl:96-102 (gate_silu), argmax.wgsl; layer loop
+webgpu/src/engine/forward-pass.ts:2925-3297.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from . import _native
+
+
+def _s(t: torch.Tensor) -> int:
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def _f32(*ts: torch.Tensor) -> None:
+    for t in ts:
+        if t.dtype != torch.float32 or not t.is_cuda or not t.is_contiguous():
+            raise ValueError("glue kernels take contiguous float32 device tensors")
+
+
+def rmsnorm(x: torch.Tensor, w: torch.Tensor, eps: float, out: torch.Tensor) -> torch.Tensor:
+    """out = x / sqrt(mean(x^2) + eps) * w over the last dimension."""
+    _f32(x, w, out)
+    n = x.shape[-1]
+    lib = _native.load_library()
+    _native.check(lib.gguf_hip_rmsnorm(x.data_ptr(), w.data_ptr(), eps, out.data_ptr(),
+                                       x.numel() // n, n, _s(x)), lib)
+    return out
+
+
+def add_rmsnorm(x: torch.Tensor, res: torch.Tensor, w: torch.Tensor, eps: float,
+                out: torch.Tensor) -> torch.Tensor:
+    """x += res (in place), then out = rmsnorm(x) * w."""
+    _f32(x, res, w, out)
+    n = x.shape[-1]
+    lib = _native.load_library()
+    _native.check(lib.gguf_hip_add_rmsnorm(x.data_ptr(), res.data_ptr(), w.data_ptr(), eps,
+                                           out.data_ptr(), x.numel() // n, n, _s(x)), lib)
+    return out
+
+
+def swiglu(gate_up: torch.Tensor, out: torch.Tensor) -> torch.Tensor:
+    """out = up * silu(gate) for rows [gate | up]."""
+    _f32(gate_up, out)
+    ffn = out.shape[-1]
+    lib = _native.load_library()
+    _native.check(lib.gguf_hip_swiglu(gate_up.data_ptr(), out.data_ptr(), out.numel() // ffn, ffn,
+                                      _s(out)), lib)
+    return out
+
+
+def attention_workspace(n_heads: int, n_kv_heads: int, head_dim: int, max_seq: int,
+                        device) -> torch.Tensor:
+    """Device workspace for ``attention_decode`` (allocate once, reuse every step)."""
+    lib = _native.load_library()
+    nbytes = _native.check(lib.gguf_hip_attention_workspace(n_heads, n_kv_heads, head_dim,
+                                                            max_seq), lib)
+    return torch.empty((nbytes + 15) // 16 * 4, dtype=torch.float32, device=device)
+
+
+def attention_decode(qkv: torch.Tensor, pos: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor,
+                     k_cache: torch.Tensor, v_cache: torch.Tensor, out: torch.Tensor,
+                     n_heads: int, n_kv_heads: int, head_dim: int,
+                     work: torch.Tensor) -> torch.Tensor:
+    """RoPE + KV append at slot ``pos`` (device int64 [1]) + causal GQA attention."""
+    _f32(qkv, cos, sin, k_cache, v_cache, out)
+    if pos.dtype != torch.int64 or not pos.is_cuda:
+        raise ValueError("pos must be an int64 device tensor")
+    lib = _native.load_library()
+    need = lib.gguf_hip_attention_workspace(n_heads, n_kv_heads, head_dim, k_cache.shape[-2])
+    if work.numel() * work.element_size() < need:
+        raise ValueError(f"attention workspace holds {work.numel() * work.element_size()} bytes, "
+                         f"needs {need}")
+    _native.check(lib.gguf_hip_attention_decode(
+        qkv.data_ptr(), pos.data_ptr(), cos.data_ptr(), sin.data_ptr(), k_cache.data_ptr(),
+        v_cache.data_ptr(), out.data_ptr(), n_heads, n_kv_heads, head_dim, k_cache.shape[-2],
+        work.data_ptr(), _s(out)), lib)
+    return out
+
+
+def argmax_workspace(device) -> torch.Tensor:
+    lib = _native.load_library()
+    return torch.empty(lib.gguf_hip_argmax_workspace() // 8, dtype=torch.int64, device=device)
+
+
+def argmax(x: torch.Tensor, out: torch.Tensor, work: torch.Tensor) -> torch.Tensor:
+    """out[0] = first index of max(x) (int64 device tensor)."""
+    _f32(x)
+    if out.dtype != torch.int64 or not out.is_cuda:
+        raise ValueError("argmax output must be an int64 device tensor")
+    lib = _native.load_library()
+    if work.numel() * work.element_size() < lib.gguf_hip_argmax_workspace():
+        raise ValueError("argmax workspace too small")
+    _native.check(lib.gguf_hip_argmax(x.data_ptr(), x.numel(), out.data_ptr(), work.data_ptr(),
+                                      _s(x)), lib)
+    return out

@@ -43,7 +43,7 @@ extern "C" {
  * are exported (kernels and helpers cannot be interposed across libraries). */
 #pragma GCC visibility push(default)
 
-#define GGUF_HIP_ABI_VERSION 2
+#define GGUF_HIP_ABI_VERSION 3
 
 /* ggml type ids (gguf.ts:24-35); activation dtypes reuse F32 / F16. */
 #define GGUF_HIP_F32 0
@@ -129,6 +129,53 @@ int gguf_hip_matmul(const void *x, int x_type, int64_t ldx, const void *tiles, i
 int gguf_hip_matmul_variant(const void *x, int x_type, int64_t ldx, const void *tiles,
                             int ggml_type, int64_t n, int64_t k, float *y, int64_t ldy,
                             int64_t m, int variant, void *stream);
+
+/* ---------------------------------------------------------------------------
+ * Decode-step glue around the quantized projections (f32, contiguous rows,
+ * 16-byte aligned pointers, lengths multiple of 4).  The reference runs these
+ * as WGSL shaders inside its layer loop (forward-pass.ts:2925-3297).
+ * ------------------------------------------------------------------------- */
+
+/* y[r] = x[r] / sqrt(mean(x[r]^2) + eps) * w for rows r < rows of n elements
+ * (rmsnorm.wgsl:1-9,58-67 with use_residual_weight = 0). */
+int gguf_hip_rmsnorm(const float *x, const float *w, float eps, float *y, int64_t rows,
+                     int64_t n, void *stream);
+
+/* Residual add then RMSNorm: x[r] += res[r] (x updated in place), then
+ * y[r] = rmsnorm(x[r]) * w.  The reference's separate add and rmsnorm
+ * dispatches of its layer loop, fused.  y must not alias x. */
+int gguf_hip_add_rmsnorm(float *x, const float *res, const float *w, float eps, float *y,
+                         int64_t rows, int64_t n, void *stream);
+
+/* out[r, i] = up[i] * silu(gate[i]) for rows [gate (ffn) | up (ffn)]
+ * (elementwise.wgsl:96-102, gate_silu with a = up, b = gate). */
+int gguf_hip_swiglu(const float *gate_up, float *out, int64_t rows, int64_t ffn, void *stream);
+
+/* One decode position p = *pos (device int64): rotate_half RoPE of q and k
+ * (rope.wgsl:1-10; cos / sin tables [max_seq, head_dim / 2] at row p), k and
+ * v appended to the caches at slot p, then causal GQA attention of each query
+ * head h over slots 0..p of KV head h / (n_heads / n_kv_heads), softmax scaled
+ * by 1/sqrt(head_dim).  qkv = [q (n_heads*head_dim) | k | v (n_kv*head_dim each)];
+ * caches [n_kv, max_seq, head_dim]; out [n_heads * head_dim]; head_dim is 64,
+ * 128 or 256 and n_heads / n_kv_heads at most 8.  `work` (device, 16-byte
+ * aligned, gguf_hip_attention_workspace bytes) holds per-64-slot partial
+ * softmax records between the two launches.  The position is read on the
+ * device, so the call can be captured in a graph. */
+int gguf_hip_attention_decode(const float *qkv, const int64_t *pos, const float *cos_table,
+                              const float *sin_table, float *k_cache, float *v_cache, float *out,
+                              int n_heads, int n_kv_heads, int head_dim, int64_t max_seq,
+                              void *work, void *stream);
+
+/* Bytes of the gguf_hip_attention_decode workspace; negative on bad shapes. */
+int64_t gguf_hip_attention_workspace(int n_heads, int n_kv_heads, int head_dim, int64_t max_seq);
+
+/* *out = first index of the maximum of x[0..n) (NaN never wins); greedy
+ * sampling.  `work`: gguf_hip_argmax_workspace() bytes of device memory
+ * (8-byte aligned) for the per-workgroup partials. */
+int gguf_hip_argmax(const float *x, int64_t n, int64_t *out, void *work, void *stream);
+
+/* Bytes of the gguf_hip_argmax workspace. */
+int64_t gguf_hip_argmax_workspace(void);
 
 #pragma GCC visibility pop
 

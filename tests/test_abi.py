@@ -43,7 +43,7 @@ def native(pkg):
 
 def test_exports_every_declared_symbol(lib, native):
     names = _declared_functions()
-    assert len(names) == 10, names
+    assert len(names) == 17, names
     for n in names:
         assert hasattr(lib, n), n
         assert n in native.SIGNATURES, n
@@ -67,7 +67,7 @@ def test_constants_match_header(native):
 
 
 def test_abi_version(lib):
-    assert lib.gguf_hip_abi_version() == 2
+    assert lib.gguf_hip_abi_version() == 3
 
 
 def test_type_traits(lib, native):
@@ -167,3 +167,33 @@ def test_last_error_is_thread_local(lib, native):
 
 def test_single_hip_runtime_mapped(lib, native):
     assert len(native._hip_runtimes_mapped()) <= 1
+
+
+def test_glue_errors(lib, native):
+    a, b, c = 0x10000, 0x20000, 0x30000
+    assert lib.gguf_hip_rmsnorm(a, b, 1e-6, c, 1, 4094, None) == native.ERR_SHAPE   # n % 4
+    assert lib.gguf_hip_rmsnorm(a, b, -1.0, c, 1, 4096, None) == native.ERR_SHAPE
+    assert lib.gguf_hip_rmsnorm(None, b, 1e-6, c, 1, 4096, None) == native.ERR_NULL
+    assert lib.gguf_hip_rmsnorm(a + 4, b, 1e-6, c, 1, 4096, None) == native.ERR_ALIGN
+    assert lib.gguf_hip_rmsnorm(None, None, 1e-6, None, 0, 4096, None) == 0         # no rows
+    assert lib.gguf_hip_add_rmsnorm(a, b, b, 1e-6, a, 1, 4096, None) == native.ERR_SHAPE
+    assert "aliases" in native.last_error(lib)
+    assert lib.gguf_hip_swiglu(a, b, 1, 14338, None) == native.ERR_SHAPE
+    assert lib.gguf_hip_swiglu(a, b + 8, 1, 14336, None) == native.ERR_ALIGN
+    att = lib.gguf_hip_attention_decode
+    wk = 0x40000
+    assert att(a, b, c, c, a, a, b, 32, 5, 128, 512, wk, None) == native.ERR_SHAPE  # 32 % 5
+    assert att(a, b, c, c, a, a, b, 32, 2, 128, 512, wk, None) == native.ERR_SHAPE  # grp 16 > 8
+    assert att(a, b, c, c, a, a, b, 32, 8, 96, 512, wk, None) == native.ERR_SHAPE   # head_dim
+    assert "head_dim 96" in native.last_error(lib)
+    assert att(a, b, c, c, a, a, b, 32, 8, 128, 0, wk, None) == native.ERR_SHAPE
+    assert att(None, b, c, c, a, a, b, 32, 8, 128, 512, wk, None) == native.ERR_NULL
+    assert att(a, b, c, c, a, a, b, 32, 8, 128, 512, None, None) == native.ERR_NULL
+    assert att(a + 4, b, c, c, a, a, b, 32, 8, 128, 512, wk, None) == native.ERR_ALIGN
+    # workspace: 8 KV heads x 8 slot ranges of 64 x 4 query heads x (128 + 2) floats
+    assert lib.gguf_hip_attention_workspace(32, 8, 128, 512) == 8 * 8 * 4 * 130 * 4
+    assert lib.gguf_hip_attention_workspace(32, 8, 100, 512) == native.ERR_SHAPE
+    assert lib.gguf_hip_argmax_workspace() > 0
+    assert lib.gguf_hip_argmax(a, 0, b, c, None) == native.ERR_SHAPE
+    assert lib.gguf_hip_argmax(a, 10, b + 4, c, None) == native.ERR_ALIGN
+    assert lib.gguf_hip_argmax(a, 10, b, None, None) == native.ERR_NULL

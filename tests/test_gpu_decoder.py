@@ -119,3 +119,19 @@ def test_graph_replay_matches_eager(dec, model):
     d = c.generate(prompt, 8, graph=True)
     assert torch.equal(a["tokens"], d["tokens"])
 
+
+
+def test_fused_glue_matches_torch_glue(dec, model):
+    cfg, w = model
+    prompt = torch.from_numpy(np.random.default_rng(11).integers(0, cfg.vocab, 20)).cuda()
+    a, b = dec.QuantDecoder(cfg, w, fused=True), dec.QuantDecoder(cfg, w, fused=False)
+    la, lb = a.prefill(prompt), b.prefill(prompt)
+    assert torch.equal(la, lb)                       # prefill glue is shared
+    ta, tb = torch.argmax(la).view(1), torch.argmax(lb).view(1)
+    pa = torch.tensor([prompt.numel()], device="cuda")
+    pb = pa.clone()
+    for _ in range(5):
+        ga, gb = a.step(ta, pa).clone(), b.step(tb, pb).clone()
+        assert _rel(ga, gb) < 1e-5
+        assert torch.equal(ta, tb) and torch.equal(pa, pb)
+    assert torch.allclose(a.k_cache, b.k_cache, rtol=1e-5, atol=1e-5)

@@ -1,0 +1,115 @@
+"""Decode glue kernels (libgguf_hip) against torch float32 / float64 references."""
+import ctypes
+import importlib
+import math
+
+import pytest
+
+torch = pytest.importorskip("torch")
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def lib():
+    return importlib.import_module("artifex-assistantv5_amd._native").load_library()
+
+
+def _s():
+    return torch.cuda.current_stream().cuda_stream
+
+
+def _ok(lib, rc):
+    assert rc == 0, importlib.import_module("artifex-assistantv5_amd._native").last_error(lib)
+
+
+@pytest.mark.parametrize("rows,n", [(1, 4096), (3, 256), (2, 14336)])
+def test_rmsnorm_and_add_rmsnorm(lib, rows, n):
+    g = torch.Generator(device="cuda").manual_seed(n + rows)
+    x = torch.randn(rows, n, device="cuda", generator=g) * 3
+    r = torch.randn(rows, n, device="cuda", generator=g)
+    w = 1 + 0.1 * torch.randn(n, device="cuda", generator=g)
+    y = torch.empty_like(x)
+    _ok(lib, lib.gguf_hip_rmsnorm(x.data_ptr(), w.data_ptr(), 1e-6, y.data_ptr(), rows, n, _s()))
+    xd = x.double()
+    ref = xd / torch.sqrt((xd * xd).mean(-1, keepdim=True) + 1e-6) * w.double()
+    assert torch.allclose(y.double(), ref, rtol=2e-6, atol=1e-6)
+    x2 = x.clone()
+    _ok(lib, lib.gguf_hip_add_rmsnorm(x2.data_ptr(), r.data_ptr(), w.data_ptr(), 1e-6, y.data_ptr(),
+                                      rows, n, _s()))
+    assert torch.equal(x2, x + r)                    # the residual add is one f32 add
+    s = (x + r).double()
+    ref = s / torch.sqrt((s * s).mean(-1, keepdim=True) + 1e-6) * w.double()
+    assert torch.allclose(y.double(), ref, rtol=2e-6, atol=1e-6)
+
+
+def test_swiglu(lib):
+    ffn = 14336
+    gu = torch.randn(2, 2 * ffn, device="cuda") * 4
+    out = torch.empty(2, ffn, device="cuda")
+    _ok(lib, lib.gguf_hip_swiglu(gu.data_ptr(), out.data_ptr(), 2, ffn, _s()))
+    g, u = gu[:, :ffn].double(), gu[:, ffn:].double()
+    assert torch.allclose(out.double(), u * g / (1 + torch.exp(-g)), rtol=1e-6, atol=1e-6)
+
+
+@pytest.mark.parametrize("nh,nkv,hd,max_seq,p", [(32, 8, 128, 512, 0), (32, 8, 128, 512, 137),
+                                                  (32, 8, 128, 512, 511), (4, 2, 64, 64, 63),
+                                                  (8, 8, 64, 128, 64), (16, 2, 256, 200, 130)])
+def test_attention_decode(lib, nh, nkv, hd, max_seq, p):
+    g = torch.Generator(device="cuda").manual_seed(p + nh)
+    qkv = torch.randn((nh + 2 * nkv) * hd, device="cuda", generator=g)
+    kc = torch.randn(nkv, max_seq, hd, device="cuda", generator=g)
+    vc = torch.randn(nkv, max_seq, hd, device="cuda", generator=g)
+    kc0, vc0 = kc.clone(), vc.clone()
+    half = hd // 2
+    inv = 1.0 / (10000.0 ** (torch.arange(half, dtype=torch.float64) * 2 / hd))
+    ang = torch.arange(max_seq, dtype=torch.float64)[:, None] * inv[None]
+    cos, sin = ang.cos().float().cuda(), ang.sin().float().cuda()
+    pos = torch.tensor([p], device="cuda")
+    out = torch.empty(nh * hd, device="cuda")
+    work = torch.full(((lib.gguf_hip_attention_workspace(nh, nkv, hd, max_seq) + 3) // 4,),
+                      float("nan"), device="cuda")   # stale records must never be read
+    _ok(lib, lib.gguf_hip_attention_decode(qkv.data_ptr(), pos.data_ptr(), cos.data_ptr(),
+                                           sin.data_ptr(), kc.data_ptr(), vc.data_ptr(),
+                                           out.data_ptr(), nh, nkv, hd, max_seq, work.data_ptr(),
+                                           _s()))
+    # float64 reference: complex-rotation RoPE, explicit softmax
+    th = torch.tensor(float(p), dtype=torch.float64) * inv
+    rot = lambda v: torch.view_as_real(  # noqa: E731
+        torch.complex(v[..., :half], v[..., half:]) * torch.exp(1j * th.cuda())).transpose(-1, -2).reshape(v.shape)
+    q = rot(qkv[:nh * hd].double().view(nh, hd))
+    k = rot(qkv[nh * hd:(nh + nkv) * hd].double().view(nkv, hd))
+    v = qkv[(nh + nkv) * hd:].double().view(nkv, hd)
+    K, V = kc0.double().clone(), vc0.double().clone()
+    K[:, p], V[:, p] = k, v
+    assert torch.allclose(kc[:, p].double(), k, rtol=1e-5, atol=1e-6)   # cache slot p written
+    assert torch.equal(vc[:, p], qkv[(nh + nkv) * hd:].view(nkv, hd))
+    others = [t for t in range(max_seq) if t != p]
+    assert torch.equal(kc[:, others], kc0[:, others]) and torch.equal(vc[:, others], vc0[:, others])
+    ref = torch.empty(nh, hd, dtype=torch.float64, device="cuda")
+    for h in range(nh):
+        kv = h // (nh // nkv)
+        s = K[kv, :p + 1] @ q[h] / math.sqrt(hd)
+        e = torch.exp(s - s.max())
+        ref[h] = (e / e.sum()) @ V[kv, :p + 1]
+    assert torch.allclose(out.double().view(nh, hd), ref, rtol=1e-4, atol=2e-5)
+
+
+def test_argmax_first_index_and_ties(lib):
+    out = torch.empty(1, dtype=torch.long, device="cuda")
+    work = torch.empty(lib.gguf_hip_argmax_workspace() // 8, dtype=torch.long, device="cuda")
+    x = torch.randn(151936, device="cuda")
+    _ok(lib, lib.gguf_hip_argmax(x.data_ptr(), x.numel(), out.data_ptr(), work.data_ptr(), _s()))
+    assert out.item() == torch.argmax(x).item()
+    x[[7, 90000, 151935]] = 100.0                    # ties: the first index wins
+    _ok(lib, lib.gguf_hip_argmax(x.data_ptr(), x.numel(), out.data_ptr(), work.data_ptr(), _s()))
+    assert out.item() == 7
+    y = torch.full((5,), float("-inf"), device="cuda")
+    _ok(lib, lib.gguf_hip_argmax(y.data_ptr(), 5, out.data_ptr(), work.data_ptr(), _s()))
+    assert out.item() == 0
+    z = torch.tensor([1.0, float("nan"), 3.0, 2.0], device="cuda")
+    _ok(lib, lib.gguf_hip_argmax(z.data_ptr(), 4, out.data_ptr(), work.data_ptr(), _s()))
+    assert out.item() == 2                           # NaN never wins
+    x[151935] = 1000.0                               # maximum in the last workgroup's chunk
+    _ok(lib, lib.gguf_hip_argmax(x.data_ptr(), x.numel(), out.data_ptr(), work.data_ptr(), _s()))
+    assert out.item() == 151935
