@@ -14,10 +14,18 @@ kernels, so ``roofline.achieved`` (algorithmic bytes per step / ms_per_step)
 is a lower bound on the kernel's own rate.  The eager (one Python launch per
 step) time is reported under ``secondary``.
 
-Prints ONE JSON line.  ``secondary`` holds the other configurations of the
-path (Q8_0 / Q4_K / Q6_K decode shapes and batch sizes, Q4_K prefill GEMM).
-``cpu_baseline`` = the CPU restatement of the reference path (numpy dequant to
-f32 + torch fp32 matmul) on all host cores, repeated for about 10 s.
+Prints ONE JSON line.  Besides the headline it carries the other two parts of
+the metric: ``prefill_gemm`` (Q4_K dequant-GEMM M=2048 K=4096 N=14336, fp16
+activations, TFLOP/s against the dense fp16 MFMA peak) and ``decode`` (the
+full synthetic Llama-style decoder: 32 layers, d_model 4096, 32/8 heads of
+128, SwiGLU FFN 14336, vocab 151936, Q4_K attention and gate/up, Q6_K down and
+LM head; 128 random prompt tokens then 256 greedy tokens; tok/s = generated
+tokens / decode wall time, prefill excluded).  ``secondary`` holds the other
+configurations of the path (Q8_0 / Q4_K / Q6_K decode shapes and batch sizes,
+more prefill shapes).  ``cpu_baseline`` = the CPU restatement of the reference
+path (numpy dequant to f32 + torch fp32 matmul) on all host cores, repeated
+for about 10 s.  ``roofline.traffic`` is read from the committed rocprofv3
+counter summary of the headline kernel when present.
 """
 
 from __future__ import annotations
@@ -50,6 +58,11 @@ def parse():
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--no-secondary", action="store_true")
     p.add_argument("--only", default="", help="comma list of secondary groups to run")
+    p.add_argument("--no-decoder", action="store_true")
+    p.add_argument("--kernel-only", type=int, default=0, metavar="N",
+                   help="profiling driver: N headline launches over the cold pool, then four "
+                        "64 MiB device copies (counter calibration); prints no JSON")
+    p.add_argument("--decode-tokens", type=int, default=256)
     return p.parse_args()
 
 
@@ -72,6 +85,30 @@ def graph_time(step, steps, warmup):
     end.record()
     torch.cuda.synchronize()
     return start.elapsed_time(end) / steps
+
+
+def graph_time_median(step, steps, warmup, replays=3):
+    """Like graph_time, but the median over ``replays`` timed replays of the graph."""
+    import torch
+    for i in range(warmup):
+        step(i)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for i in range(steps):
+            step(i)
+    g.replay()
+    torch.cuda.synchronize()
+    times = []
+    for _ in range(replays):
+        start = torch.cuda.Event(enable_timing=True)
+        end = torch.cuda.Event(enable_timing=True)
+        start.record()
+        g.replay()
+        end.record()
+        torch.cuda.synchronize()
+        times.append(start.elapsed_time(end) / steps)
+    return float(np.median(times))
 
 
 def eager_time(step, steps, warmup):
@@ -116,7 +153,8 @@ def make_pool(pkg, t, n, k, copies, seed, quantized=True):
     return pool, raw
 
 
-def matmul_case(pkg, t, m, n, k, pool, steps, warmup, xdtype="float32", eager=False):
+def matmul_case(pkg, t, m, n, k, pool, steps, warmup, xdtype="float32", eager=False,
+                replays=1):
     import torch
     x = torch.from_numpy(pkg.quantize.synthetic_activations(m, k, seed=7)).cuda().to(
         getattr(torch, xdtype))
@@ -126,7 +164,8 @@ def matmul_case(pkg, t, m, n, k, pool, steps, warmup, xdtype="float32", eager=Fa
     def step(i):
         pkg.dispatch_matmul_gguf(x, pool[i % P], y, m, n, k, "bench")
 
-    ms = graph_time(step, steps, warmup)
+    ms = graph_time(step, steps, warmup) if replays == 1 else graph_time_median(step, steps, warmup,
+                                                                               replays)
     wbytes = n * pkg.raw_row_bytes(t, k)
     algo = wbytes + m * k * x.element_size() + m * n * 4
     out = {"ms": ms, "bytes": algo, "gbs": algo / (ms * 1e-3) / 1e9,
@@ -175,6 +214,55 @@ def cpu_baseline(pkg, raw, t, n, k, seconds, m=1):
     }
 
 
+def decoder_case(pkg, n_new):
+    """Full synthetic decoder: 128-token random prompt then ``n_new`` greedy tokens."""
+    import torch
+    dec = importlib.import_module("artifex-assistantv5_amd.decoder")
+    cfg = dec.DecoderConfig()
+    t0 = time.perf_counter()
+    w = dec.synthetic_weights(cfg, seed=0, lm_head_unique_rows=16384)
+    torch.cuda.synchronize()
+    t_w = time.perf_counter() - t0
+    m = dec.QuantDecoder(cfg, w)
+    prompt = torch.from_numpy(np.random.default_rng(0).integers(0, cfg.vocab, 128)).cuda()
+    m.generate(prompt, 16)                              # warm-up (kernels, graph capture)
+    r = m.generate(prompt, n_new)
+    bpt = cfg.weight_bytes_per_token()
+    ceiling = HBM_PEAK_GBS * 1e9 / bpt
+    out = {
+        "tok_s": round(r["tok_s"], 1),
+        "ms_per_token": round(1e3 / r["tok_s"], 3),
+        "weight_bytes_per_token": bpt,
+        "weight_gbs": round(bpt * r["tok_s"] / 1e9, 1),
+        "hbm_ceiling_tok_s": round(ceiling, 1),
+        "frac_of_ceiling": round(r["tok_s"] / ceiling, 4),
+        "prefill_ms": round(r["prefill_s"] * 1e3, 2),
+        "prefill_tok_s": round(r["prefill_tok_s"], 1),
+        "decode_steps_timed": r["decode_steps"],
+        "workload": ("32 layers, d 4096, 32/8 heads x 128, SwiGLU 14336, vocab 151936; Q4_K "
+                     "q/k/v/o and gate/up, Q6_K down and LM head; 128 random prompt ids then "
+                     f"{n_new} greedy tokens, batch 1, each decode step one HIP graph replay"),
+        "weights": ("seeded N(0,0.02) quantized with the package quantizer; the 32 layers hold "
+                    "separate device copies of one quantized layer set, the LM head repeats "
+                    "16384 quantized rows (every byte still streamed from HBM)"),
+        "weight_setup_s": round(t_w, 1),
+    }
+    del m, w
+    torch.cuda.empty_cache()
+    return out
+
+
+def traffic_from_profile():
+    """HBM bytes per launch of the headline kernel from the committed rocprofv3
+    FETCH_SIZE / WRITE_SIZE summary (profiles/q4k_decode_m1_k4096_n14336_traffic.json)."""
+    f = os.path.join(ROOT, "profiles", "q4k_decode_m1_k4096_n14336_traffic.json")
+    try:
+        with open(f, encoding="utf-8") as fh:
+            return json.load(fh).get("traffic_bytes_per_launch")
+    except (OSError, ValueError):
+        return None
+
+
 def secondary_cases(pkg, args, pool, secondary):
     only = set(filter(None, args.only.split(",")))
 
@@ -206,7 +294,7 @@ def secondary_cases(pkg, args, pool, secondary):
         secondary["q6k_lm_head_weights"] = "random blocks with finite f16 scales"
         del lpool
     if want("prefill"):
-        for mm, nn in ((512, 4096), (2048, 14336), (8192, 4096)):
+        for mm, nn in ((512, 4096), (512, 14336), (8192, 4096), (8192, 14336)):
             ppool = pool[:2] if nn == 14336 else make_pool(pkg, t, nn, 4096, 2, seed=3)[0]
             r = matmul_case(pkg, t, mm, nn, 4096, ppool, 10, 2, xdtype="float16")
             secondary[f"q4k_gemm_m{mm}_n{nn}_tflops"] = round(r["tflops"], 1)
@@ -227,11 +315,31 @@ def main():
 
     t, m, n, k = 12, 1, 14336, 4096
     pool, raw = make_pool(pkg, t, n, k, args.pool, seed=1)
+    if args.kernel_only:
+        x = torch.from_numpy(pkg.quantize.synthetic_activations(m, k, seed=7)).cuda()
+        y = torch.empty(m, n, device="cuda")
+        a = torch.randn(16 * 2**20, device="cuda")
+        b = torch.empty_like(a)
+        torch.cuda.synchronize()
+        for i in range(args.kernel_only):
+            pkg.dispatch_matmul_gguf(x, pool[i % len(pool)], y, m, n, k, "profile")
+        for _ in range(4):
+            b.copy_(a)
+        torch.cuda.synchronize()
+        print(f"kernel-only: {args.kernel_only} launches + 4 x 64 MiB copies", flush=True)
+        return
     head = matmul_case(pkg, t, m, n, k, pool, args.steps, args.warmup, eager=True)
     warm = matmul_case(pkg, t, m, n, k, pool[:1], args.steps, args.warmup)
     secondary = {"q4k_decode_m1_warm_gbs": round(warm["gbs"], 1),
                  "q4k_decode_m1_eager_ms_per_step": round(head["eager_ms"], 5)}
     secondary_cases(pkg, args, pool, secondary)
+    gemm = matmul_case(pkg, t, 2048, n, k, pool[:2], 20, 2, xdtype="float16", replays=3)
+    prefill = {"tflops": round(gemm["tflops"], 1), "peak": FP16_PEAK_TFLOPS, "unit": "TFLOP/s",
+               "frac": round(gemm["tflops"] / FP16_PEAK_TFLOPS, 4),
+               "ms_per_step": round(gemm["ms"], 4),
+               "workload": "Q4_K dequant-GEMM M=2048 K=4096 N=14336, fp16 activations, f32 out",
+               "timing": "median of 3 graph replays of 20 launches over 2 weight copies"}
+    decode = None if args.no_decoder else decoder_case(pkg, args.decode_tokens)
 
     out = {
         "metric": "Q4_K GEMV weight GB/s (% HBM peak); prefill GEMM TFLOP/s; decode tok/s",
@@ -251,7 +359,9 @@ def main():
                    "bytes_per_step": head["bytes"], "timing": "graph replay of the timed steps"},
         "roofline": {"bound": "hbm", "achieved": round(head["gbs"], 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(head["gbs"] / HBM_PEAK_GBS, 4),
-                     "traffic": None},
+                     "traffic": traffic_from_profile()},
+        "prefill_gemm": prefill,
+        "decode": decode,
         "secondary": secondary,
     }
     if not args.no_cpu_baseline:
