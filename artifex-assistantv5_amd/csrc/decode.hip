@@ -681,10 +681,148 @@ hipError_t launch_t(const XT *x, int64_t ldx, const uint8_t *W, int N, int K, fl
   return hipGetLastError();
 }
 
+// ---------------------------------------------------------------------------
+// M = 1: every weight unit a wave owns is requested at once.
+//
+// A workgroup of NW = max(4, ks_n) waves covers NW / ks_n row tiles; the
+// ks_n waves of a tile split its units (wave ks takes units ks, ks + ks_n,
+// ...), at most U per wave, so one latency round brings a wave's whole share
+// of the weights.  The activation vector is requested before the weights (the
+// memory counter retires in issue order, so staging never waits on weight
+// bytes), staged once for all of K, and each unit is consumed as it arrives.
+// ---------------------------------------------------------------------------
+template <int TYPE, typename XT, int U, int XI>
+__global__ __launch_bounds__(512) void decode_m1_kernel(const XT *__restrict__ x,
+                                                        const uint8_t *__restrict__ W, int N,
+                                                        int K, float *__restrict__ y, int ks_n) {
+  constexpr int PARTS = sizeof(XT) == 4 ? 2 : 1;
+  constexpr int UE = Fmt<TYPE>::UE, TU = Fmt<TYPE>::TU, GS = Dec<TYPE>::GS;
+  const int nthr = blockDim.x;
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int r = lane & 15, g = lane >> 4;
+  const int ts_n = (nthr >> 6) / ks_n;
+  const int ts = wave / ks_n, ks = wave - ts * ks_n;
+  const int ntiles = (N + 15) >> 4;
+  const int tile = blockIdx.x * ts_n + ts;
+  const bool active = tile < ntiles;
+  const int nu = K / UE;
+  const int iters = (nu + ks_n - 1) / ks_n;  // <= U
+
+  Stage st;
+  st.ld = K + kXPad;
+  st.ms = 1;
+  st.xh = 0;
+  st.xl = st.ld;
+  st.xs = (st.xl + (PARTS == 2 ? st.ld : 0)) / 2;
+  const int red_off = st.xs + K / GS;  // floats: [waves][64]
+  st.zero = 2 * (red_off + (nthr >> 6) * 64);
+  float *red = (float *)g_lds + red_off;
+  if (threadIdx.x < kZeroHalves / 2) ((uint32_t *)((half_t *)g_lds + st.zero))[threadIdx.x] = 0u;
+
+  // activations first: item q = threadIdx.x + nthr * i of the K / 16 items
+  const int per_row = K / kItem;
+  float xv[XI][kItem];
+#pragma unroll
+  for (int i = 0; i < XI; ++i)
+    load_item<XT>(x, 0, K, 0, per_row, per_row, (int)threadIdx.x + nthr * i, xv[i]);
+
+  // Branch-free over the U slots, so that the compiler can interleave the
+  // units: a slot past the wave's share loads a valid unit of the tile (the
+  // last one) and contributes zero; a wave past the last tile reads the last
+  // tile and stores nothing.
+  const int tile_c = active ? tile : ntiles - 1;
+  const __amdgpu_buffer_rsrc_t wrs = __builtin_amdgcn_make_buffer_rsrc(
+      (void *)(W + (int64_t)tile_c * nu * TU), 0, nu * TU, kRsrcWord3);
+  Unit<TYPE> buf[U];
+#pragma unroll
+  for (int j = 0; j < U; ++j) {
+    const int u = ks + ks_n * j;
+    const int uc = (j < iters && u < nu) ? u : nu - 1;
+    load_unit(wrs, uc * TU, r, g, buf[j]);
+  }
+
+#pragma unroll
+  for (int i = 0; i < XI; ++i)
+    store_item<PARTS, GS>(per_row, per_row, (int)threadIdx.x + nthr * i, xv[i], st);
+  __syncthreads();
+
+  float acc = 0.f;
+#pragma unroll
+  for (int j = 0; j < U; ++j) {
+    const int u = ks + ks_n * j;
+    const bool valid = j < iters && u < nu;
+    float t = 0.f;
+    unit_m1<PARTS>(buf[j], st, valid ? u : nu - 1, lane, t);
+    acc += valid ? t : 0.f;
+  }
+  acc += __shfl_xor(acc, 16);  // the four lane groups of each row
+  acc += __shfl_xor(acc, 32);
+
+  const int n = 16 * tile + r;
+  if (ks_n > 1) {  // fixed-order sum of the ks_n partial sums of each tile
+    red[wave * 64 + lane] = acc;
+    __syncthreads();
+    if (ks != 0) return;
+    for (int j = 1; j < ks_n; ++j) acc += red[(wave + j) * 64 + lane];
+  }
+  if (active && n < N && g == 0) y[n] = acc;
+}
+
+// Units per wave held in registers: with K <= 4096 the staged activations
+// take one item per thread; longer K needs four and leaves less room.
+template <int TYPE>
+constexpr int m1_umax(bool long_k) {
+  return TYPE == 8 ? (long_k ? 16 : 32) : (TYPE == 14 || long_k ? 8 : 16);
+}
+
+// Returns hipErrorNotSupported (nothing launched) when K is beyond the
+// one-shot staging (16384) or the units per wave exceed the register budget.
+template <int TYPE, typename XT>
+hipError_t launch_m1(const XT *x, const uint8_t *W, int N, int K, float *y, hipStream_t s) {
+  constexpr int UE = Fmt<TYPE>::UE, GS = Dec<TYPE>::GS;
+  constexpr int PARTS = sizeof(XT) == 4 ? 2 : 1;
+  const int ntiles = (N + 15) / 16, nu = K / UE;
+  if (K > 16384) return hipErrorNotSupported;
+  const bool long_k = K > 4096;
+  const int umax = m1_umax<TYPE>(long_k);
+  // K split: units per wave within the budget, and at least ~1024 waves when possible
+  int ks = 1;
+  while (ks < 8 && ks < nu && ((nu + ks - 1) / ks > umax || ntiles * ks < 1024)) ks <<= 1;
+  const int per = (nu + ks - 1) / ks;
+  if (per > umax) return hipErrorNotSupported;
+  const int nw = ks > 4 ? ks : 4, nthr = 64 * nw, ts = nw / ks;
+  const size_t lds = (size_t)(K + kXPad) * 2 * PARTS + (size_t)(K / GS) * 4 +
+                     (size_t)nw * 64 * 4 + kZeroHalves * 2;
+  if (lds > 65536) return hipErrorNotSupported;
+  const dim3 grid((unsigned)((ntiles + ts - 1) / ts)), block(nthr);
+  // template U is clamped to the compile-time budget (runtime per <= umax already)
+#define GGUF_M1(UU, XX)                                                                    \
+  hipLaunchKernelGGL(                                                                      \
+      (decode_m1_kernel<TYPE, XT, ((UU) < m1_umax<TYPE>((XX) > 1) ? (UU) : m1_umax<TYPE>((XX) > 1)), \
+                        XX>),                                                              \
+      grid, block, lds, s, x, W, N, K, y, ks)
+  if (!long_k) {  // K / 16 <= 256 items: one per thread
+    if (per <= 4) GGUF_M1(4, 1);
+    else if (per <= 8) GGUF_M1(8, 1);
+    else if (per <= 16) GGUF_M1(16, 1);
+    else GGUF_M1(32, 1);
+  } else {        // K / 16 <= 1024 items: at most four per thread
+    if (per <= 4) GGUF_M1(4, 4);
+    else if (per <= 8) GGUF_M1(8, 4);
+    else GGUF_M1(16, 4);
+  }
+#undef GGUF_M1
+  return hipGetLastError();
+}
+
 template <int TYPE, typename XT>
 hipError_t launch_m(const XT *x, int64_t ldx, const uint8_t *W, int N, int K, float *y,
                     int64_t ldy, int M, hipStream_t s) {
-  if (M == 1) return launch_t<TYPE, XT, 1, 1>(x, ldx, W, N, K, y, ldy, M, s);
+  if (M == 1) {
+    const hipError_t e = launch_m1<TYPE, XT>(x, W, N, K, y, s);
+    if (e != hipErrorNotSupported) return e;
+    return launch_t<TYPE, XT, 1, 1>(x, ldx, W, N, K, y, ldy, M, s);
+  }
   if (M <= 16) return launch_t<TYPE, XT, 1, 4>(x, ldx, W, N, K, y, ldy, M, s);
   return launch_t<TYPE, XT, 2, 4>(x, ldx, W, N, K, y, ldy, M, s);
 }
