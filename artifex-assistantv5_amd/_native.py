@@ -17,10 +17,11 @@ from .ggml import GGMLTypeError
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libgguf_hip.so")
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 ERR_TYPE, ERR_SHAPE, ERR_NULL, ERR_ALIGN, ERR_DTYPE, ERR_BYTES, ERR_HIP = -1, -2, -3, -4, -5, -6, -7
 VARIANT_AUTO, VARIANT_DECODE, VARIANT_GEMM = 0, 1, 2
+PROLOGUE_NONE, PROLOGUE_RMSNORM, PROLOGUE_SWIGLU = 0, 1, 2
 DECODE_MAX_M = 32
 
 # Every symbol include/gguf_hip.h declares: name -> (restype, argtypes)
@@ -37,6 +38,8 @@ SIGNATURES = {
     "gguf_hip_matmul": (_i32, [_vp, _i32, _i64, _vp, _i32, _i64, _i64, _fp, _i64, _i64, _vp]),
     "gguf_hip_matmul_variant": (_i32, [_vp, _i32, _i64, _vp, _i32, _i64, _i64, _fp, _i64, _i64,
                                        _i32, _vp]),
+    "gguf_hip_matmul_fused": (_i32, [_fp, _vp, _i32, _i64, _i64, _fp, _i32, _fp, ctypes.c_float,
+                                     _i32, _vp]),
     "gguf_hip_rmsnorm": (_i32, [_fp, _fp, ctypes.c_float, _fp, _i64, _i64, _vp]),
     "gguf_hip_add_rmsnorm": (_i32, [_fp, _fp, _fp, ctypes.c_float, _fp, _i64, _i64, _vp]),
     "gguf_hip_swiglu": (_i32, [_fp, _fp, _i64, _i64, _vp]),

@@ -304,6 +304,35 @@ int gguf_hip_argmax(const float *x, int64_t n, int64_t *out, void *work, void *s
   return hip_status(gguf::launch_argmax(x, n, out, work, (hipStream_t)stream), "argmax launch");
 }
 
+int gguf_hip_matmul_fused(const float *x, const void *tiles, int ggml_type, int64_t n, int64_t k,
+                          float *y, int prologue, const float *norm_w, float eps, int accumulate,
+                          void *stream) {
+  int rc = check_type(ggml_type);
+  if (rc) return rc;
+  if ((rc = check_k(ggml_type, k))) return rc;
+  if (prologue < GGUF_HIP_PROLOGUE_NONE || prologue > GGUF_HIP_PROLOGUE_SWIGLU)
+    return fail(GGUF_HIP_ERR_SHAPE, "[gguf-hip] unknown prologue %d", prologue);
+  if (n < 0 || n > ((int64_t)1 << 30)) return fail(GGUF_HIP_ERR_SHAPE, "[gguf-hip] bad N");
+  if (k > 16384)
+    return fail(GGUF_HIP_ERR_SHAPE, "[gguf-hip] fused matmul: K=%lld above 16384", (long long)k);
+  if (k % 16) return fail(GGUF_HIP_ERR_SHAPE, "[gguf-hip] fused matmul: K %% 16 != 0");
+  if (prologue == GGUF_HIP_PROLOGUE_RMSNORM && !(eps >= 0.0f))
+    return fail(GGUF_HIP_ERR_SHAPE, "[gguf-hip] rmsnorm: eps must be >= 0");
+  if (n == 0) return ok();
+  if (!x || !tiles || !y || (prologue == GGUF_HIP_PROLOGUE_RMSNORM && !norm_w))
+    return fail(GGUF_HIP_ERR_NULL, "[gguf-hip] null pointer");
+  if (!aligned(x, 16) || !aligned(tiles, 16) || !aligned(y, 4) ||
+      (norm_w && prologue == GGUF_HIP_PROLOGUE_RMSNORM && !aligned(norm_w, 16)))
+    return fail(GGUF_HIP_ERR_ALIGN, "[gguf-hip] fused matmul buffers misaligned");
+  const hipError_t e = gguf::launch_decode_fused(x, (const uint8_t *)tiles, ggml_type, n, k, y,
+                                                 prologue, norm_w, eps, accumulate ? 1 : 0,
+                                                 (hipStream_t)stream);
+  if (e == hipErrorNotSupported)
+    return fail(GGUF_HIP_ERR_SHAPE, "[gguf-hip] no fused kernel for N=%lld K=%lld type %d",
+                (long long)n, (long long)k, ggml_type);
+  return hip_status(e, "fused matmul launch");
+}
+
 int gguf_hip_matmul(const void *x, int x_type, int64_t ldx, const void *tiles, int ggml_type,
                     int64_t n, int64_t k, float *y, int64_t ldy, int64_t m, void *stream) {
   return gguf_hip_matmul_variant(x, x_type, ldx, tiles, ggml_type, n, k, y, ldy, m,

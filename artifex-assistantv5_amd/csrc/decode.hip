@@ -684,17 +684,29 @@ hipError_t launch_t(const XT *x, int64_t ldx, const uint8_t *W, int N, int K, fl
 // ---------------------------------------------------------------------------
 // M = 1: every weight unit a wave owns is requested at once.
 //
-// A workgroup of NW = max(4, ks_n) waves covers NW / ks_n row tiles; the
-// ks_n waves of a tile split its units (wave ks takes units ks, ks + ks_n,
+// A workgroup of NW waves (4, or 8 when K > 4096 or ks_n = 8) covers NW / ks_n
+// row tiles;
+// the ks_n waves of a tile split its units (wave ks takes units ks, ks + ks_n,
 // ...), at most U per wave, so one latency round brings a wave's whole share
 // of the weights.  The activation vector is requested before the weights (the
 // memory counter retires in issue order, so staging never waits on weight
 // bytes), staged once for all of K, and each unit is consumed as it arrives.
+//
+// Fused variants for a decoder step (PRO, f32 activations only):
+//   PRO = 1  x is replaced by rmsnorm(x) * w before staging (the input norm of
+//            the projection, rmsnorm.wgsl:58-67); every workgroup reduces the
+//            whole row itself, so no extra launch or buffer is needed;
+//   PRO = 2  x is a row [gate (K) | up (K)] and is replaced by up * silu(gate)
+//            (elementwise.wgsl:96-102);
+// and `accumulate` adds the result to y instead of storing it (the residual
+// add that follows the output and down projections).
 // ---------------------------------------------------------------------------
-template <int TYPE, typename XT, int U, int XI>
+template <int TYPE, typename XT, int U, int XI, int PRO>
 __global__ __launch_bounds__(512) void decode_m1_kernel(const XT *__restrict__ x,
                                                         const uint8_t *__restrict__ W, int N,
-                                                        int K, float *__restrict__ y, int ks_n) {
+                                                        int K, float *__restrict__ y, int ks_n,
+                                                        const float *__restrict__ pw, float eps,
+                                                        int accumulate) {
   constexpr int PARTS = sizeof(XT) == 4 ? 2 : 1;
   constexpr int UE = Fmt<TYPE>::UE, TU = Fmt<TYPE>::TU, GS = Dec<TYPE>::GS;
   const int nthr = blockDim.x;
@@ -722,9 +734,14 @@ __global__ __launch_bounds__(512) void decode_m1_kernel(const XT *__restrict__ x
   // activations first: item q = threadIdx.x + nthr * i of the K / 16 items
   const int per_row = K / kItem;
   float xv[XI][kItem];
+  float pv[PRO ? XI : 1][kItem];  // norm weights (PRO 1) or up values (PRO 2)
 #pragma unroll
-  for (int i = 0; i < XI; ++i)
-    load_item<XT>(x, 0, K, 0, per_row, per_row, (int)threadIdx.x + nthr * i, xv[i]);
+  for (int i = 0; i < XI; ++i) {
+    const int q = (int)threadIdx.x + nthr * i;
+    load_item<XT>(x, 0, K, 0, per_row, per_row, q, xv[i]);
+    if constexpr (PRO == 1) load_item<float>(pw, 0, K, 0, per_row, per_row, q, pv[i]);
+    if constexpr (PRO == 2) load_item<float>((const float *)x + K, 0, K, 0, per_row, per_row, q, pv[i]);
+  }
 
   // Branch-free over the U slots, so that the compiler can interleave the
   // units: a slot past the wave's share loads a valid unit of the tile (the
@@ -741,6 +758,33 @@ __global__ __launch_bounds__(512) void decode_m1_kernel(const XT *__restrict__ x
     load_unit(wrs, uc * TU, r, g, buf[j]);
   }
 
+  if constexpr (PRO == 1) {  // 1 / rms over the whole row, reduced by this workgroup
+    float ss = 0.f;
+#pragma unroll
+    for (int i = 0; i < XI; ++i)
+#pragma unroll
+      for (int e = 0; e < kItem; ++e) ss += xv[i][e] * xv[i][e];
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o);
+    if (lane == 0) red[wave] = ss;
+    __syncthreads();
+    float tot = 0.f;
+    for (int w = 0; w < (nthr >> 6); ++w) tot += red[w];
+    const float inv = 1.0f / sqrtf(tot / (float)K + eps);
+#pragma unroll
+    for (int i = 0; i < XI; ++i)
+#pragma unroll
+      for (int e = 0; e < kItem; ++e) xv[i][e] = xv[i][e] * inv * pv[i][e];
+  }
+  if constexpr (PRO == 2) {
+#pragma unroll
+    for (int i = 0; i < XI; ++i)
+#pragma unroll
+      for (int e = 0; e < kItem; ++e) {
+        const float gt = xv[i][e];
+        xv[i][e] = pv[i][e] * (gt / (1.0f + expf(-gt)));
+      }
+  }
 #pragma unroll
   for (int i = 0; i < XI; ++i)
     store_item<PARTS, GS>(per_row, per_row, (int)threadIdx.x + nthr * i, xv[i], st);
@@ -765,51 +809,56 @@ __global__ __launch_bounds__(512) void decode_m1_kernel(const XT *__restrict__ x
     if (ks != 0) return;
     for (int j = 1; j < ks_n; ++j) acc += red[(wave + j) * 64 + lane];
   }
-  if (active && n < N && g == 0) y[n] = acc;
+  if (active && n < N && g == 0) y[n] = accumulate ? y[n] + acc : acc;
 }
 
 // Units per wave held in registers: with K <= 4096 the staged activations
-// take one item per thread; longer K needs four and leaves less room.
+// take one item per thread; longer K (or a fused prologue) leaves less room.
 template <int TYPE>
-constexpr int m1_umax(bool long_k) {
-  return TYPE == 8 ? (long_k ? 16 : 32) : (TYPE == 14 || long_k ? 8 : 16);
+constexpr int m1_umax(bool tight) {
+  return TYPE == 8 ? (tight ? 16 : 32) : (TYPE == 14 || tight ? 8 : 16);
 }
 
 // Returns hipErrorNotSupported (nothing launched) when K is beyond the
 // one-shot staging (16384) or the units per wave exceed the register budget.
-template <int TYPE, typename XT>
-hipError_t launch_m1(const XT *x, const uint8_t *W, int N, int K, float *y, hipStream_t s) {
+template <int TYPE, typename XT, int PRO>
+hipError_t launch_m1(const XT *x, const uint8_t *W, int N, int K, float *y, const float *pw,
+                     float eps, int accumulate, hipStream_t s) {
   constexpr int UE = Fmt<TYPE>::UE, GS = Dec<TYPE>::GS;
   constexpr int PARTS = sizeof(XT) == 4 ? 2 : 1;
   const int ntiles = (N + 15) / 16, nu = K / UE;
   if (K > 16384) return hipErrorNotSupported;
   const bool long_k = K > 4096;
-  const int umax = m1_umax<TYPE>(long_k);
+  const int umax = m1_umax<TYPE>(long_k || PRO != 0);
   // K split: units per wave within the budget, and at least ~1024 waves when possible
   int ks = 1;
   while (ks < 8 && ks < nu && ((nu + ks - 1) / ks > umax || ntiles * ks < 1024)) ks <<= 1;
   const int per = (nu + ks - 1) / ks;
   if (per > umax) return hipErrorNotSupported;
-  const int nw = ks > 4 ? ks : 4, nthr = 64 * nw, ts = nw / ks;
+  const int nw = (long_k || ks > 4) ? 8 : 4, nthr = 64 * nw, ts = nw / ks;
+  const int xi = (K / kItem + nthr - 1) / nthr;  // 1 or 2
   const size_t lds = (size_t)(K + kXPad) * 2 * PARTS + (size_t)(K / GS) * 4 +
                      (size_t)nw * 64 * 4 + kZeroHalves * 2;
   if (lds > 65536) return hipErrorNotSupported;
   const dim3 grid((unsigned)((ntiles + ts - 1) / ts)), block(nthr);
   // template U is clamped to the compile-time budget (runtime per <= umax already)
-#define GGUF_M1(UU, XX)                                                                    \
-  hipLaunchKernelGGL(                                                                      \
-      (decode_m1_kernel<TYPE, XT, ((UU) < m1_umax<TYPE>((XX) > 1) ? (UU) : m1_umax<TYPE>((XX) > 1)), \
-                        XX>),                                                              \
-      grid, block, lds, s, x, W, N, K, y, ks)
-  if (!long_k) {  // K / 16 <= 256 items: one per thread
+#define GGUF_M1(UU, XX)                                                                          \
+  hipLaunchKernelGGL(                                                                            \
+      (decode_m1_kernel<TYPE, XT,                                                                \
+                        ((UU) < m1_umax<TYPE>((XX) > 1 || PRO != 0)                              \
+                             ? (UU)                                                              \
+                             : m1_umax<TYPE>((XX) > 1 || PRO != 0)),                             \
+                        XX, PRO>),                                                               \
+      grid, block, lds, s, x, W, N, K, y, ks, pw, eps, accumulate)
+  if (xi <= 1) {
     if (per <= 4) GGUF_M1(4, 1);
     else if (per <= 8) GGUF_M1(8, 1);
     else if (per <= 16) GGUF_M1(16, 1);
     else GGUF_M1(32, 1);
-  } else {        // K / 16 <= 1024 items: at most four per thread
-    if (per <= 4) GGUF_M1(4, 4);
-    else if (per <= 8) GGUF_M1(8, 4);
-    else GGUF_M1(16, 4);
+  } else {
+    if (per <= 4) GGUF_M1(4, 2);
+    else if (per <= 8) GGUF_M1(8, 2);
+    else GGUF_M1(16, 2);
   }
 #undef GGUF_M1
   return hipGetLastError();
@@ -819,7 +868,7 @@ template <int TYPE, typename XT>
 hipError_t launch_m(const XT *x, int64_t ldx, const uint8_t *W, int N, int K, float *y,
                     int64_t ldy, int M, hipStream_t s) {
   if (M == 1) {
-    const hipError_t e = launch_m1<TYPE, XT>(x, W, N, K, y, s);
+    const hipError_t e = launch_m1<TYPE, XT, 0>(x, W, N, K, y, nullptr, 0.f, 0, s);
     if (e != hipErrorNotSupported) return e;
     return launch_t<TYPE, XT, 1, 1>(x, ldx, W, N, K, y, ldy, M, s);
   }
@@ -836,6 +885,24 @@ hipError_t launch_x(const XT *x, int64_t ldx, const uint8_t *W, int type, int N,
 }
 
 }  // namespace
+
+// One f32 activation row with a fused prologue / accumulate epilogue
+// (decode_m1_kernel).  hipErrorNotSupported: no fused kernel for this shape.
+hipError_t launch_decode_fused(const float *x, const uint8_t *tiles, int type, int64_t n,
+                               int64_t k, float *y, int prologue, const float *pw, float eps,
+                               int accumulate, hipStream_t s) {
+#define GGUF_FUSED(T)                                                                        \
+  return prologue == 1   ? launch_m1<T, float, 1>(x, tiles, (int)n, (int)k, y, pw, eps,     \
+                                                  accumulate, s)                             \
+         : prologue == 2 ? launch_m1<T, float, 2>(x, tiles, (int)n, (int)k, y, pw, eps,     \
+                                                  accumulate, s)                             \
+                         : launch_m1<T, float, 0>(x, tiles, (int)n, (int)k, y, pw, eps,     \
+                                                  accumulate, s)
+  if (type == 12) GGUF_FUSED(12);
+  if (type == 14) GGUF_FUSED(14);
+  GGUF_FUSED(8);
+#undef GGUF_FUSED
+}
 
 // Rows are processed in groups of at most 32 (one pass over the weights each).
 hipError_t launch_decode(const void *x, int x_type, int64_t ldx, const uint8_t *tiles, int type,

@@ -18,9 +18,10 @@ Every projection goes through ``dispatch_matmul_gguf`` (libgguf_hip): Q/K/V are
 one row-concatenated weight and gate/up another (the reference's gate+up
 fusion, forward-pass.ts:740-791, applied to Q/K/V too; byte-identical to
 separate dispatches).  A decode step runs the glue as libgguf_hip kernels
-(``glue.py``: RMSNorm fused with the residual add, RoPE + KV append + GQA
-attention in one launch, SwiGLU, argmax) over preallocated buffers: eight
-launches per layer.  Prefill (many positions at once) runs the glue as torch
+(``glue.py``: the input norms and SwiGLU run as prologues of the projections
+that consume them, the residual adds as accumulate epilogues of the output
+and down projections, RoPE + KV append + GQA attention as one two-pass
+launch, argmax) over preallocated buffers: six launches per layer.  Prefill (many positions at once) runs the glue as torch
 f32 ops; ``fused=False`` does the same for decode steps.  A decode step keeps
 the token and position in device tensors, so it can be captured once in a HIP
 graph and replayed for every generated token without host synchronization.
@@ -237,23 +238,25 @@ class QuantDecoder:
         dispatch_matmul_gguf(x, w, y, 1, w.n, w.k, label)
 
     def _step_fused(self, tok: torch.Tensor, pos: torch.Tensor) -> torch.Tensor:
+        """Six launches per layer: Q/K/V projection with the input RMSNorm as its
+        prologue, attention (two passes), output projection accumulated into the
+        residual, gate/up projection with the FFN RMSNorm prologue, down
+        projection with the SwiGLU prologue accumulated into the residual."""
         cfg, W = self.cfg, self.w
-        x, h = self.b_x, self.b_h
+        x = self.b_x
         x.copy_(W.embed.index_select(0, tok))
-        glue.rmsnorm(x, W.layers[0].attn_norm, cfg.eps, h)
         for l, lw in enumerate(W.layers):
-            self._proj_into(h, lw.qkv_gg, self.b_qkv, f"L{l}-qkv")
+            glue.matmul_fused(x, lw.qkv_gg, self.b_qkv, glue.PROLOGUE_RMSNORM, lw.attn_norm,
+                              cfg.eps)
             glue.attention_decode(self.b_qkv, pos, self.cos, self.sin, self.k_cache[l],
                                   self.v_cache[l], self.b_att, cfg.n_heads, cfg.n_kv_heads,
                                   cfg.head_dim, self.w_att)
-            self._proj_into(self.b_att, lw.o_gg, self.b_o, f"L{l}-o")
-            glue.add_rmsnorm(x, self.b_o, lw.ffn_norm, cfg.eps, h)
-            self._proj_into(h, lw.gateUp_gg, self.b_gu, f"L{l}-gateUp")
-            glue.swiglu(self.b_gu, self.b_a)
-            self._proj_into(self.b_a, lw.down_gg, self.b_d, f"L{l}-down")
-            nxt = W.layers[l + 1].attn_norm if l + 1 < len(W.layers) else W.final_norm
-            glue.add_rmsnorm(x, self.b_d, nxt, cfg.eps, h)
-        self._proj_into(h, W.lm_head_gg, self.b_logits, "lm_head")
+            glue.matmul_fused(self.b_att, lw.o_gg, x, accumulate=True)
+            glue.matmul_fused(x, lw.gateUp_gg, self.b_gu, glue.PROLOGUE_RMSNORM, lw.ffn_norm,
+                              cfg.eps)
+            glue.matmul_fused(self.b_gu, lw.down_gg, x, glue.PROLOGUE_SWIGLU, accumulate=True)
+        glue.matmul_fused(x, W.lm_head_gg, self.b_logits, glue.PROLOGUE_RMSNORM, W.final_norm,
+                          cfg.eps)
         glue.argmax(self.b_logits, tok, self.w_arg)
         pos.add_(1)
         return self.b_logits

@@ -99,3 +99,31 @@ def argmax(x: torch.Tensor, out: torch.Tensor, work: torch.Tensor) -> torch.Tens
     _native.check(lib.gguf_hip_argmax(x.data_ptr(), x.numel(), out.data_ptr(), work.data_ptr(),
                                       _s(x)), lib)
     return out
+
+
+PROLOGUE_NONE, PROLOGUE_RMSNORM, PROLOGUE_SWIGLU = (_native.PROLOGUE_NONE, _native.PROLOGUE_RMSNORM,
+                                                    _native.PROLOGUE_SWIGLU)
+
+
+def matmul_fused(x: torch.Tensor, w, y: torch.Tensor, prologue: int = PROLOGUE_NONE,
+                 norm_w: torch.Tensor | None = None, eps: float = 0.0,
+                 accumulate: bool = False) -> torch.Tensor:
+    """One activation row through a quantized weight with fused neighbours:
+    ``y (=|+=) x' @ dequant(w)^T`` where x' is x, ``rmsnorm(x) * norm_w`` or, for
+    x = [gate | up], ``up * silu(gate)``.  ``w`` is a GGUFWeight."""
+    _f32(x, y)
+    k = w.k
+    want = 2 * k if prologue == PROLOGUE_SWIGLU else k
+    if x.numel() != want or y.numel() != w.n:
+        raise ValueError(f"matmul_fused: x has {x.numel()} elements (needs {want}), "
+                         f"y has {y.numel()} (needs {w.n})")
+    if prologue == PROLOGUE_RMSNORM:
+        if norm_w is None:
+            raise ValueError("matmul_fused: RMSNORM prologue needs norm_w")
+        _f32(norm_w)
+    lib = _native.load_library()
+    _native.check(lib.gguf_hip_matmul_fused(
+        x.data_ptr(), w.ptr(), w.ggml_type, w.n, k, y.data_ptr(), prologue,
+        norm_w.data_ptr() if norm_w is not None else None, float(eps), int(bool(accumulate)),
+        _s(y)), lib)
+    return y

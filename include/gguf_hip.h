@@ -43,7 +43,7 @@ extern "C" {
  * are exported (kernels and helpers cannot be interposed across libraries). */
 #pragma GCC visibility push(default)
 
-#define GGUF_HIP_ABI_VERSION 3
+#define GGUF_HIP_ABI_VERSION 4
 
 /* ggml type ids (gguf.ts:24-35); activation dtypes reuse F32 / F16. */
 #define GGUF_HIP_F32 0
@@ -129,6 +129,22 @@ int gguf_hip_matmul(const void *x, int x_type, int64_t ldx, const void *tiles, i
 int gguf_hip_matmul_variant(const void *x, int x_type, int64_t ldx, const void *tiles,
                             int ggml_type, int64_t n, int64_t k, float *y, int64_t ldy,
                             int64_t m, int variant, void *stream);
+
+/* Prologues of gguf_hip_matmul_fused. */
+#define GGUF_HIP_PROLOGUE_NONE 0
+#define GGUF_HIP_PROLOGUE_RMSNORM 1 /* x' = x / sqrt(mean(x^2) + eps) * norm_w */
+#define GGUF_HIP_PROLOGUE_SWIGLU 2  /* x = [gate (k) | up (k)], x' = up * silu(gate) */
+
+/* One decode-step projection with its neighbours fused in:
+ *   y[n] = sum_k x'[k] * dequant(W)[n, k]     (accumulate = 0)
+ *   y[n] += sum_k x'[k] * dequant(W)[n, k]    (accumulate = 1: the residual add)
+ * for a single f32 activation row x (16-byte aligned), x' given by the
+ * prologue.  The reference dispatches these as separate rmsnorm, gate_silu,
+ * matmul and add shaders in its layer loop (forward-pass.ts:2925-3297).
+ * K <= 16384; shapes without a fused kernel return GGUF_HIP_ERR_SHAPE. */
+int gguf_hip_matmul_fused(const float *x, const void *tiles, int ggml_type, int64_t n, int64_t k,
+                          float *y, int prologue, const float *norm_w, float eps, int accumulate,
+                          void *stream);
 
 /* ---------------------------------------------------------------------------
  * Decode-step glue around the quantized projections (f32, contiguous rows,

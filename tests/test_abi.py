@@ -43,7 +43,7 @@ def native(pkg):
 
 def test_exports_every_declared_symbol(lib, native):
     names = _declared_functions()
-    assert len(names) == 17, names
+    assert len(names) == 18, names
     for n in names:
         assert hasattr(lib, n), n
         assert n in native.SIGNATURES, n
@@ -67,7 +67,7 @@ def test_constants_match_header(native):
 
 
 def test_abi_version(lib):
-    assert lib.gguf_hip_abi_version() == 3
+    assert lib.gguf_hip_abi_version() == 4
 
 
 def test_type_traits(lib, native):
@@ -197,3 +197,20 @@ def test_glue_errors(lib, native):
     assert lib.gguf_hip_argmax(a, 0, b, c, None) == native.ERR_SHAPE
     assert lib.gguf_hip_argmax(a, 10, b + 4, c, None) == native.ERR_ALIGN
     assert lib.gguf_hip_argmax(a, 10, b, None, None) == native.ERR_NULL
+
+
+def test_fused_matmul_errors(lib, native):
+    f = lib.gguf_hip_matmul_fused
+    x, w, y, nw = 0x10000, 0x20000, 0x30000, 0x40000
+    assert f(x, w, 12, 64, 4096, y, 3, nw, 1e-6, 0, None) == native.ERR_SHAPE      # prologue
+    assert f(x, w, 12, 64, 32768, y, 0, None, 0.0, 0, None) == native.ERR_SHAPE    # K > 16384
+    assert "16384" in native.last_error(lib)
+    assert f(x, w, 12, 64, 4096, y, 1, None, 1e-6, 0, None) == native.ERR_NULL     # no norm weight
+    assert f(x, w, 12, 64, 4096, y, 1, nw, -1.0, 0, None) == native.ERR_SHAPE
+    assert f(x + 4, w, 12, 64, 4096, y, 0, None, 0.0, 0, None) == native.ERR_ALIGN
+    assert f(x, w, 11, 64, 4096, y, 0, None, 0.0, 0, None) == native.ERR_TYPE
+    assert f(x, w, 12, 0, 4096, y, 2, None, 0.0, 1, None) == 0                     # N = 0: no-op
+    d = _defines()
+    assert (d["GGUF_HIP_PROLOGUE_NONE"], d["GGUF_HIP_PROLOGUE_RMSNORM"],
+            d["GGUF_HIP_PROLOGUE_SWIGLU"]) == (native.PROLOGUE_NONE, native.PROLOGUE_RMSNORM,
+                                               native.PROLOGUE_SWIGLU)

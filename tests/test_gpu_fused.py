@@ -1,0 +1,81 @@
+"""Fused decode-step projections (gguf_hip_matmul_fused) against a float64 composition."""
+import importlib
+
+import numpy as np
+import pytest
+
+torch = pytest.importorskip("torch")
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def mods():
+    return (importlib.import_module("artifex-assistantv5_amd"),
+            importlib.import_module("artifex-assistantv5_amd.glue"))
+
+
+def _weight(pkg, t, n, k, seed):
+    w = pkg.quantize.synthetic_weight(n, k, seed=seed)
+    return pkg.repack_gguf_for_gpu(t, pkg.quantize.quantize(w, t), n, k, device="cuda")
+
+
+def _rel(a, b):
+    return ((a.double() - b.double()).norm() / b.double().norm()).item()
+
+
+def _elementwise(y, ref, wd, xd):
+    """max_n |y - ref| / sum_k |w[n, k] x[k]|: the per-element criterion of the path,
+    insensitive to cancellation in the dot products."""
+    scale = wd.abs() @ xd.abs()
+    return ((y.double() - ref).abs() / scale).max().item()
+
+
+@pytest.mark.parametrize("t,n,k", [(12, 6144, 4096), (12, 1000, 4096), (14, 4096, 14336),
+                                   (8, 512, 4096), (12, 4096, 14336), (14, 2048, 4096)])
+def test_rmsnorm_prologue(mods, t, n, k):
+    pkg, glue = mods
+    w = _weight(pkg, t, n, k, seed=n + k)
+    g = torch.Generator(device="cuda").manual_seed(k)
+    x = torch.randn(k, device="cuda", generator=g) * 5
+    nw = 1 + 0.1 * torch.randn(k, device="cuda", generator=g)
+    y = torch.empty(n, device="cuda")
+    glue.matmul_fused(x, w, y, glue.PROLOGUE_RMSNORM, nw, 1e-6)
+    xd = x.double()
+    h = xd / torch.sqrt((xd * xd).mean() + 1e-6) * nw.double()
+    wd = w.dequant().double()
+    ref = wd @ h
+    assert _rel(y, ref) < 1e-5
+    assert _elementwise(y, ref, wd, h) < 1e-6
+
+
+@pytest.mark.parametrize("t,n,k", [(14, 4096, 14336), (12, 4096, 14336), (8, 256, 2048)])
+def test_swiglu_prologue_accumulate(mods, t, n, k):
+    pkg, glue = mods
+    w = _weight(pkg, t, n, k, seed=7 * n + k)
+    g = torch.Generator(device="cuda").manual_seed(n)
+    gu = torch.randn(2 * k, device="cuda", generator=g) * 3
+    y0 = torch.randn(n, device="cuda", generator=g)
+    y = y0.clone()
+    glue.matmul_fused(gu, w, y, glue.PROLOGUE_SWIGLU, accumulate=True)
+    gd, ud = gu[:k].double(), gu[k:].double()
+    a = ud * gd / (1 + torch.exp(-gd))
+    wd = w.dequant().double()
+    ref = y0.double() + wd @ a
+    # f32-grade per element (normwise it is ~1e-5: the products cancel heavily)
+    assert _elementwise(y, ref, wd, a) < 1e-6
+
+
+def test_plain_accumulate_matches_matmul(mods):
+    pkg, glue = mods
+    w = _weight(pkg, 12, 4096, 4096, seed=3)
+    x = torch.randn(4096, device="cuda")
+    y0 = torch.randn(4096, device="cuda")
+    y = y0.clone()
+    glue.matmul_fused(x, w, y, accumulate=True)
+    z = torch.empty(1, 4096, device="cuda")
+    pkg.dispatch_matmul_gguf(x.view(1, -1), w, z, 1, 4096, 4096)
+    assert torch.allclose(y, y0 + z[0], rtol=1e-6, atol=1e-6)   # same kernel, plus one add
+    z2 = torch.empty(4096, device="cuda")
+    glue.matmul_fused(x, w, z2)
+    assert torch.equal(z2, z[0])
