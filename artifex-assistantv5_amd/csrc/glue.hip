@@ -138,114 +138,102 @@ __device__ __forceinline__ float wave_sum(float v) {
   return v;
 }
 
+// Pass 1 layout: the workgroup stages its 64 K rows (stride HD + 4 floats,
+// so that lane t reading row t is free of bank conflicts) and 64 V rows in
+// LDS with coalesced loads, then wave w takes query heads w, w + 4, ... of
+// the group: lane t owns slot t0 + t, so a wave computes 64 dot products, one
+// wave-wide softmax reduction, and sum_t p_t v_t reading V rows from LDS.
+template <int HD>
 __global__ __launch_bounds__(kGlueThreads) void attention_split_kernel(
     const float *__restrict__ qkv, const int64_t *__restrict__ pos, const float *__restrict__ cs,
     const float *__restrict__ sn, float *__restrict__ kc, float *__restrict__ vc,
-    float *__restrict__ work, int nh, int nkv, int hd, int max_seq) {
-  __shared__ __align__(16) float qs[8 * 256];       // grp * hd roped, scaled queries
-  __shared__ float pr[8 * kSplit];                  // grp * kSplit probabilities
-  __shared__ float wred[8 * 4];
-  const int grp = nh / nkv, g = blockIdx.x, sp = blockIdx.y, half = hd / 2, tid = threadIdx.x;
+    float *__restrict__ work, int nh, int nkv, int max_seq) {
+  constexpr int hd = HD, half = HD / 2, KLD = HD + 4;
+  constexpr int C4 = HD / 4;  // float4 chunks per row
+  __shared__ __align__(16) float ks[kSplit * KLD];
+  __shared__ __align__(16) float vs[kSplit * HD];
+  __shared__ __align__(16) float qw[4 * HD];       // per wave: roped, scaled query
+  __shared__ float pw[4 * kSplit];                  // per wave: probabilities
+  const int grp = nh / nkv, g = blockIdx.x, sp = blockIdx.y, tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
   const int S = gridDim.y;
   const int64_t p64 = pos[0];
   if (p64 < 0 || p64 >= max_seq) return;  // no cache slot: write nothing
   const int p = (int)p64, T = p + 1, t0 = sp * kSplit;
   if (t0 >= T) return;  // beyond the causal range: no record (pass 2 reads sp < ceil(T / 64))
   const int tn = min(kSplit, T - t0);
-  const float *crow = cs + (int64_t)p * half, *srow = sn + (int64_t)p * half;
+  const bool holds_p = p < t0 + kSplit;
   float *kbase = kc + (int64_t)g * max_seq * hd, *vbase = vc + (int64_t)g * max_seq * hd;
-  if (p < t0 + kSplit) {  // this range holds the new slot
+  const float *crow = cs + (int64_t)p * half, *srow = sn + (int64_t)p * half;
+
+  // the rows of slots t0 .. t0 + tn - 1, coalesced; slot p is read stale here
+  // and replaced below
+  for (int e = tid; e < tn * C4; e += kGlueThreads) {
+    const int t = e / C4, c = e - t * C4;
+    *(float4 *)(ks + t * KLD + 4 * c) = *(const float4 *)(kbase + (int64_t)(t0 + t) * hd + 4 * c);
+    *(float4 *)(vs + t * HD + 4 * c) = *(const float4 *)(vbase + (int64_t)(t0 + t) * hd + 4 * c);
+  }
+  __syncthreads();
+  if (holds_p) {  // rotate_half RoPE of k (rope.wgsl:1-10); slot p into the cache and LDS
     const float *kin = qkv + (int64_t)nh * hd + g * hd;
     const float *vin = qkv + (int64_t)(nh + nkv) * hd + g * hd;
     float *krow = kbase + (int64_t)p * hd, *vrow = vbase + (int64_t)p * hd;
+    const int tp = p - t0;
     for (int i = tid; i < half; i += kGlueThreads) {
-      const float c = crow[i], s = srow[i], a = kin[i], b = kin[i + half];
-      krow[i] = a * c - b * s;
-      krow[i + half] = b * c + a * s;
+      const float c = crow[i], sv = srow[i], a = kin[i], b = kin[i + half];
+      const float k0 = a * c - b * sv, k1 = b * c + a * sv;
+      krow[i] = k0;
+      krow[i + half] = k1;
+      ks[tp * KLD + i] = k0;
+      ks[tp * KLD + i + half] = k1;
     }
-    for (int i = tid; i < hd; i += kGlueThreads) vrow[i] = vin[i];
+    for (int i = tid; i < hd; i += kGlueThreads) {
+      vrow[i] = vin[i];
+      vs[tp * HD + i] = vin[i];
+    }
   }
-  const float scale = 1.0f / sqrtf((float)hd);
-  for (int e = tid; e < grp * half; e += kGlueThreads) {
-    const int j = e / half, i = e % half;
-    const float *q = qkv + (int64_t)(g * grp + j) * hd;
-    const float c = crow[i], s = srow[i], a = q[i], b = q[i + half];
-    qs[j * hd + i] = (a * c - b * s) * scale;
-    qs[j * hd + i + half] = (b * c + a * s) * scale;
-  }
-  __syncthreads();  // slot p and the queries are visible to the workgroup
+  __syncthreads();
 
-  // scores: wave w takes slots t0 + 16 w + (lane & 15); the four lanes of a
-  // slot split hd into quarters and combine with two shuffles
-  const int lane = tid & 63, w = tid >> 6, tl = 16 * w + (lane & 15), qt = lane >> 4;
-  const int qlen = hd / 4;
-  float acc[8];
-#pragma unroll
-  for (int j = 0; j < 8; ++j) acc[j] = 0.f;
-  if (tl < tn) {
-    const float *kr = kbase + (int64_t)(t0 + tl) * hd + qt * qlen;
-    for (int i = 0; i < qlen; i += 4) {
-      const float4 kv = *(const float4 *)(kr + i);
-#pragma unroll
-      for (int j = 0; j < 8; ++j)
-        if (j < grp) {
-          const float4 q = *(const float4 *)(qs + j * hd + qt * qlen + i);
-          acc[j] += q.x * kv.x + q.y * kv.y + q.z * kv.z + q.w * kv.w;
-        }
+  const float scale = 1.0f / sqrtf((float)hd);
+  float *q = qw + wave * HD;
+  float *pr = pw + wave * kSplit;
+  for (int j = wave; j < grp; j += 4) {
+    const float *qin = qkv + (int64_t)(g * grp + j) * hd;
+    for (int i = lane; i < half; i += 64) {
+      const float c = crow[i], sv = srow[i], a = qin[i], b = qin[i + half];
+      q[i] = (a * c - b * sv) * scale;
+      q[i + half] = (b * c + a * sv) * scale;
     }
-  }
+    // the wave's own LDS writes are visible to it in program order
+    float sc = -INFINITY;
+    if (lane < tn) {
+      const float *kr = ks + lane * KLD;
+      float a0 = 0.f, a1 = 0.f;
 #pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    acc[j] += __shfl_xor(acc[j], 16);
-    acc[j] += __shfl_xor(acc[j], 32);
-  }
-  // per query: max and exp-sum over the workgroup's slots
-  float mj[8], lj[8];
-#pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    if (j >= grp) break;
-    const float sv = tl < tn ? acc[j] : -INFINITY;
-    const float m = wave_max(sv);
-    if (lane == 0) wred[j * 4 + w] = m;
-  }
-  __syncthreads();
-#pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    if (j >= grp) break;
-    mj[j] = fmaxf(fmaxf(wred[j * 4], wred[j * 4 + 1]), fmaxf(wred[j * 4 + 2], wred[j * 4 + 3]));
-  }
-  __syncthreads();
-#pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    if (j >= grp) break;
-    const float e = tl < tn ? expf(acc[j] - mj[j]) : 0.f;
-    if (qt == 0 && tl < kSplit) pr[j * kSplit + tl] = e;
-    const float l = wave_sum(qt == 0 ? e : 0.f);
-    if (lane == 0) wred[j * 4 + w] = l;
-  }
-  __syncthreads();
-#pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    if (j >= grp) break;
-    lj[j] = wred[j * 4] + wred[j * 4 + 1] + wred[j * 4 + 2] + wred[j * 4 + 3];
-  }
-  // partial output: thread -> element i = tid % hd, queries j = tid / hd, + 256 / hd, ...
-  float *rec = work + ((int64_t)(g * S + sp) * grp) * (hd + 2);
-  const int step = kGlueThreads / hd;  // hd divides 256 (hd is 64, 128 or 256)
-  const int i = tid % hd;
-  for (int j = tid / hd; j < grp; j += step) {
-    float o = 0.f;
-    for (int t = 0; t < tn; ++t) o += pr[j * kSplit + t] * vbase[(int64_t)(t0 + t) * hd + i];
-    rec[j * (hd + 2) + 2 + i] = o;
-  }
-  if (tid < grp) {
-    rec[tid * (hd + 2)] = mj[0];
-#pragma unroll
-    for (int j = 0; j < 8; ++j)
-      if (j == tid) {
-        rec[tid * (hd + 2)] = mj[j];
-        rec[tid * (hd + 2) + 1] = lj[j];
+      for (int c = 0; c < C4; c += 2) {
+        const float4 k0 = *(const float4 *)(kr + 4 * c), q0 = *(const float4 *)(q + 4 * c);
+        const float4 k1 = *(const float4 *)(kr + 4 * c + 4), q1 = *(const float4 *)(q + 4 * c + 4);
+        a0 += q0.x * k0.x + q0.y * k0.y + q0.z * k0.z + q0.w * k0.w;
+        a1 += q1.x * k1.x + q1.y * k1.y + q1.z * k1.z + q1.w * k1.w;
       }
+      sc = a0 + a1;
+    }
+    const float m = wave_max(sc);
+    const float e = lane < tn ? expf(sc - m) : 0.f;
+    const float l = wave_sum(e);
+    pr[lane] = e;
+    // o[i] for i = lane, lane + 64, ...: sum over the slots of p_t v_t
+    float *rec = work + ((int64_t)(g * S + sp) * grp + j) * (hd + 2);
+    for (int i = lane; i < hd; i += 64) {
+      float o = 0.f;
+#pragma unroll 8
+      for (int t = 0; t < tn; ++t) o += pr[t] * vs[t * HD + i];
+      rec[2 + i] = o;
+    }
+    if (lane == 0) {
+      rec[0] = m;
+      rec[1] = l;
+    }
   }
 }
 
@@ -259,6 +247,8 @@ __global__ __launch_bounds__(kGlueThreads) void attention_merge_kernel(
   const int n = ((int)p64 + kSplit) / kSplit;  // records written: ceil((p + 1) / 64)
   const float *base = work + ((int64_t)g * S * grp + j) * (hd + 2);
   const int64_t stride = (int64_t)grp * (hd + 2);
+  // records are read once into registers (at most 16 splits of 64 slots
+  // per pass; longer caches loop)
   float M = -INFINITY;
   for (int s = 0; s < n; ++s) M = fmaxf(M, base[s * stride]);
   float L = 0.f;
@@ -266,6 +256,7 @@ __global__ __launch_bounds__(kGlueThreads) void attention_merge_kernel(
   const float inv = 1.0f / L;
   for (int i = threadIdx.x; i < hd; i += kGlueThreads) {
     float o = 0.f;
+#pragma unroll 8
     for (int s = 0; s < n; ++s) o += base[s * stride + 2 + i] * expf(base[s * stride] - M);
     out[(int64_t)h * hd + i] = o * inv;
   }
@@ -351,8 +342,16 @@ hipError_t launch_attention_decode(const float *qkv, const int64_t *pos, const f
                                    const float *sn, float *kc, float *vc, float *out, float *work,
                                    int nh, int nkv, int hd, int64_t max_seq, hipStream_t s) {
   const int S = (int)((max_seq + kSplit - 1) / kSplit);
-  hipLaunchKernelGGL(attention_split_kernel, dim3((unsigned)nkv, (unsigned)S), dim3(kGlueThreads),
-                     0, s, qkv, pos, cs, sn, kc, vc, work, nh, nkv, hd, (int)max_seq);
+  const dim3 grid((unsigned)nkv, (unsigned)S), block(kGlueThreads);
+  if (hd == 64)
+    hipLaunchKernelGGL(attention_split_kernel<64>, grid, block, 0, s, qkv, pos, cs, sn, kc, vc,
+                       work, nh, nkv, (int)max_seq);
+  else if (hd == 128)
+    hipLaunchKernelGGL(attention_split_kernel<128>, grid, block, 0, s, qkv, pos, cs, sn, kc, vc,
+                       work, nh, nkv, (int)max_seq);
+  else
+    hipLaunchKernelGGL(attention_split_kernel<256>, grid, block, 0, s, qkv, pos, cs, sn, kc, vc,
+                       work, nh, nkv, (int)max_seq);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   hipLaunchKernelGGL(attention_merge_kernel, dim3((unsigned)nh), dim3(kGlueThreads), 0, s, pos,
