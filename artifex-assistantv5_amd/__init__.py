@@ -10,6 +10,10 @@ reference's WebGPU engine (``webgpu/src/engine/forward-pass.ts``):
 * ``dispatch_projection``   — per-layer projection lookup (forward-pass.ts:1576-1629)
 * ``dequant_ggml``          — dequantize to f32 on the GPU (gguf-dequant.ts:844-868)
 * ``qlinear``               — functional form returning a new tensor
+* ``QuantEmbedding``        — raw GGUF rows in HBM, gathered per token (forward-pass.ts:2171-2186)
+* ``parse_gguf``            — GGUF header / KV / tensor table (gguf.ts:241-299)
+* ``load_gguf_model``       — place a GGUF file's tensors in HBM (gguf-loader.ts:166-460)
+* ``load_decoder``          — a llama-architecture GGUF file as a ``QuantDecoder``
 
 Importing this package does not touch the GPU; the native library is loaded
 on first use and a missing or unbuilt library raises immediately.
@@ -18,14 +22,20 @@ on first use and a missing or unbuilt library raises immediately.
 from . import ggml, quantize  # noqa: F401
 from .ggml import (GGML_TYPES, GGMLTypeError, ggml_tensor_bytes, ggml_type_traits,  # noqa: F401
                    raw_row_bytes, tile_row_bytes, tiled_bytes)
-from .linear import (GGUFWeight, LayerWeights, concat_rows, dequant_ggml,  # noqa: F401
-                     dequant_raw, dispatch_matmul_gguf, dispatch_projection, qlinear,
-                     repack_gguf_for_gpu)
+from .linear import (GGUFWeight, LayerWeights, QuantEmbedding, concat_rows,  # noqa: F401
+                     dequant_ggml, dequant_raw, dispatch_matmul_gguf, dispatch_projection,
+                     qlinear, repack_gguf_for_gpu)
+from .gguf_file import parse_gguf, parse_gguf_path, write_gguf  # noqa: F401
+from .gguf_loader import load_gguf_model  # noqa: F401
+from .gguf_model import load_decoder  # noqa: F401
 from ._native import GGUFHipError, load_library  # noqa: F401
 
 __all__ = [
     "GGML_TYPES", "GGMLTypeError", "GGUFHipError", "GGUFWeight", "LayerWeights",
+    "QuantEmbedding", "load_decoder", "load_gguf_model", "parse_gguf", "parse_gguf_path",
+    "write_gguf",
     "concat_rows", "dequant_ggml", "dequant_raw", "dispatch_matmul_gguf",
     "dispatch_projection", "ggml_tensor_bytes", "ggml_type_traits", "load_library",
     "qlinear", "raw_row_bytes", "repack_gguf_for_gpu", "tile_row_bytes", "tiled_bytes",
 ]
+

@@ -17,7 +17,7 @@ from .ggml import GGMLTypeError
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libgguf_hip.so")
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 ERR_TYPE, ERR_SHAPE, ERR_NULL, ERR_ALIGN, ERR_DTYPE, ERR_BYTES, ERR_HIP = -1, -2, -3, -4, -5, -6, -7
 VARIANT_AUTO, VARIANT_DECODE, VARIANT_GEMM = 0, 1, 2
@@ -35,6 +35,7 @@ SIGNATURES = {
     "gguf_hip_repack": (_i32, [_vp, _i64, _i32, _i64, _i64, _vp, _i64, _vp]),
     "gguf_hip_dequant": (_i32, [_vp, _i32, _i64, _i64, _fp, _i64, _vp]),
     "gguf_hip_dequant_raw": (_i32, [_vp, _i32, _i64, _fp, _vp]),
+    "gguf_hip_get_rows": (_i32, [_vp, _i32, _i64, _i64, _vp, _i64, _fp, _i64, _vp]),
     "gguf_hip_matmul": (_i32, [_vp, _i32, _i64, _vp, _i32, _i64, _i64, _fp, _i64, _i64, _vp]),
     "gguf_hip_matmul_variant": (_i32, [_vp, _i32, _i64, _vp, _i32, _i64, _i64, _fp, _i64, _i64,
                                        _i32, _vp]),

@@ -183,6 +183,22 @@ int gguf_hip_dequant_raw(const void *raw, int ggml_type, int64_t n_elems, float 
       "dequant_raw launch");
 }
 
+int gguf_hip_get_rows(const void *raw, int ggml_type, int64_t n_rows, int64_t k,
+                      const int64_t *ids, int64_t n_ids, float *out, int64_t ldo, void *stream) {
+  int rc = check_type(ggml_type);
+  if (rc) return rc;
+  if ((rc = check_k(ggml_type, k))) return rc;
+  if (n_rows < 0 || n_ids < 0) return fail(GGUF_HIP_ERR_SHAPE, "[gguf-hip] negative row count");
+  if (n_ids > 1 && ldo < k) return fail(GGUF_HIP_ERR_SHAPE, "[gguf-hip] ldo < K");
+  if (n_ids == 0) return ok();
+  if (!raw || !ids || !out) return fail(GGUF_HIP_ERR_NULL, "[gguf-hip] null pointer");
+  if (!aligned(ids, 8)) return fail(GGUF_HIP_ERR_ALIGN, "[gguf-hip] ids must be 8-byte aligned");
+  if (!aligned(out, 4)) return fail(GGUF_HIP_ERR_ALIGN, "[gguf-hip] output must be 4-byte aligned");
+  return hip_status(gguf::launch_get_rows((const uint8_t *)raw, ggml_type, n_rows, k, ids, n_ids,
+                                          out, ldo, (hipStream_t)stream),
+                    "get_rows launch");
+}
+
 int gguf_hip_matmul_variant(const void *x, int x_type, int64_t ldx, const void *tiles,
                             int ggml_type, int64_t n, int64_t k, float *y, int64_t ldy, int64_t m,
                             int variant, void *stream) {

@@ -139,6 +139,9 @@ hipError_t launch_dequant(const uint8_t *tiles, int type, int64_t n_rows, int64_
                           int64_t ldo, hipStream_t s);
 hipError_t launch_dequant_raw(const uint8_t *raw, int type, int64_t n_elems, float *out,
                               hipStream_t s);
+hipError_t launch_get_rows(const uint8_t *raw, int type, int64_t n_rows, int64_t k,
+                           const int64_t *ids, int64_t n_ids, float *out, int64_t ldo,
+                           hipStream_t s);
 hipError_t launch_decode(const void *x, int x_type, int64_t ldx, const uint8_t *tiles, int type,
                          int64_t n, int64_t k, float *y, int64_t ldy, int64_t m, hipStream_t s);
 hipError_t launch_gemm(const void *x, int x_type, int64_t ldx, const uint8_t *tiles, int type,

@@ -36,11 +36,17 @@ namespace gguf {
 
 namespace {
 
-constexpr int kWaves = 8;
-constexpr int kBM = 128, kBN = 32 * kWaves, kBK = 64;
+#ifndef GGUF_GEMM_WAVES
+#define GGUF_GEMM_WAVES 8
+#endif
+#ifndef GGUF_GEMM_TN
+#define GGUF_GEMM_TN 2
+#endif
+constexpr int kWaves = GGUF_GEMM_WAVES;
+constexpr int kTN = GGUF_GEMM_TN;  // 16-column MFMA tiles (row tiles of W) per wave
+constexpr int kBM = 128, kBN = 16 * kTN * kWaves, kBK = 64;
 constexpr int kThreads = 64 * kWaves;
 constexpr int kTM = kBM / 16;  // 16-row MFMA tiles per wave
-constexpr int kTN = 2;         // 16-column MFMA tiles per wave
 constexpr int kAI = kBM * 8 / kThreads;  // activation chunks staged per thread
 constexpr int kARows = kThreads / 8;     // row distance between a thread's chunks
 constexpr int kRowB = 2 * kBK;             // LDS bytes per activation row

@@ -257,33 +257,21 @@ hipError_t launch_dequant(const uint8_t *tiles, int type, int64_t n_rows, int64_
 // Dequantization of raw GGUF bytes (any alignment: byte loads)
 // ---------------------------------------------------------------------------
 
-__global__ __launch_bounds__(256) void dequant_raw_q8_0_kernel(const uint8_t *__restrict__ raw,
-                                                               int64_t nb,
-                                                               float *__restrict__ out) {
-  const int64_t b = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (b >= nb) return;
-  const uint8_t *src = raw + b * 34;
-  const float d = h2f(ld_u16_bytes(src));
-  float *o = out + 32 * b;
+// One piece of a raw GGUF row: a Q8_0 block (32 values), a 64-value chunk c
+// of a Q4_K superblock, or a 128-value half hf of a Q6_K superblock.
+__device__ __forceinline__ void raw_piece_q8_0(const uint8_t *blk, float *o) {
+  const float d = h2f(ld_u16_bytes(blk));
 #pragma unroll
-  for (int i = 0; i < 32; ++i) o[i] = d * (float)(int8_t)src[2 + i];
+  for (int i = 0; i < 32; ++i) o[i] = d * (float)(int8_t)blk[2 + i];
 }
 
-__global__ __launch_bounds__(256) void dequant_raw_q4_k_kernel(const uint8_t *__restrict__ raw,
-                                                               int64_t nsb,
-                                                               float *__restrict__ out) {
-  const int64_t g = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (g >= nsb * 4) return;
-  const int c = (int)(g & 3);
-  const int64_t b = g >> 2;
-  const uint8_t *blk = raw + b * 144;
+__device__ __forceinline__ void raw_piece_q4_k(const uint8_t *blk, int c, float *o) {
   uint32_t q[8];
 #pragma unroll
   for (int i = 0; i < 8; ++i) q[i] = ld_u32_bytes(blk + 16 + 32 * c + 4 * i);
   float lo[32], hi[32];
   q4k_decode_chunk(ld_u32_bytes(blk), ld_u32_bytes(blk + 4), ld_u32_bytes(blk + 8),
                    ld_u32_bytes(blk + 12), c, q, lo, hi);
-  float *o = out + 256 * b + 64 * c;
 #pragma unroll
   for (int i = 0; i < 32; ++i) {
     o[i] = lo[i];
@@ -291,17 +279,9 @@ __global__ __launch_bounds__(256) void dequant_raw_q4_k_kernel(const uint8_t *__
   }
 }
 
-__global__ __launch_bounds__(256) void dequant_raw_q6_k_kernel(const uint8_t *__restrict__ raw,
-                                                               int64_t nsb,
-                                                               float *__restrict__ out) {
-  const int64_t g = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (g >= nsb * 2) return;
-  const int hf = (int)(g & 1);
-  const int64_t b = g >> 1;
-  const uint8_t *blk = raw + b * 210;
+__device__ __forceinline__ void raw_piece_q6_k(const uint8_t *blk, int hf, float *o) {
   const float d = h2f(ld_u16_bytes(blk + 208));
   const int8_t *sc = (const int8_t *)(blk + 192);
-  float *o = out + 256 * b + 128 * hf;
   for (int l = 0; l < 32; ++l) {
     const uint32_t ab = blk[64 * hf + l], bb = blk[64 * hf + 32 + l], hb = blk[128 + 32 * hf + l];
 #pragma unroll
@@ -310,21 +290,97 @@ __global__ __launch_bounds__(256) void dequant_raw_q6_k_kernel(const uint8_t *__
   }
 }
 
+// Pieces per 256-element superblock (per 32-element block for Q8_0) and values per piece.
+template <int TYPE>
+struct RawPiece;
+template <>
+struct RawPiece<8> {
+  static constexpr int PER_UNIT = 1, VALUES = 32;
+  __device__ static void run(const uint8_t *unit, int, float *o) { raw_piece_q8_0(unit, o); }
+};
+template <>
+struct RawPiece<12> {
+  static constexpr int PER_UNIT = 4, VALUES = 64;
+  __device__ static void run(const uint8_t *unit, int p, float *o) { raw_piece_q4_k(unit, p, o); }
+};
+template <>
+struct RawPiece<14> {
+  static constexpr int PER_UNIT = 2, VALUES = 128;
+  __device__ static void run(const uint8_t *unit, int p, float *o) { raw_piece_q6_k(unit, p, o); }
+};
+
+// Contiguous raw bytes: one thread per piece of the whole buffer.
+template <int TYPE>
+__global__ __launch_bounds__(256) void dequant_raw_kernel(const uint8_t *__restrict__ raw,
+                                                          int64_t n_pieces,
+                                                          float *__restrict__ out) {
+  using P = RawPiece<TYPE>;
+  const int64_t g = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (g >= n_pieces) return;
+  const int64_t u = g / P::PER_UNIT;
+  P::run(raw + u * Fmt<TYPE>::UB, (int)(g % P::PER_UNIT), out + g * P::VALUES);
+}
+
+// Row gather: out[i * ldo + j] = dequant(raw row ids[i])[j].  One thread per
+// (output row, piece).  An id outside [0, n_rows) reads nothing and writes a
+// row of NaN, so a bad token id is visible in the output instead of faulting.
+template <int TYPE>
+__global__ __launch_bounds__(256) void get_rows_kernel(const uint8_t *__restrict__ raw,
+                                                       int64_t n_rows, int64_t units_per_row,
+                                                       const int64_t *__restrict__ ids,
+                                                       int64_t n_ids, float *__restrict__ out,
+                                                       int64_t ldo) {
+  using P = RawPiece<TYPE>;
+  const int64_t per_row = units_per_row * P::PER_UNIT;
+  const int64_t g = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (g >= n_ids * per_row) return;
+  const int64_t i = g / per_row, p = g % per_row;
+  const int64_t id = ids[i];
+  float *o = out + i * ldo + p * P::VALUES;
+  if (id < 0 || id >= n_rows) {
+    for (int j = 0; j < P::VALUES; ++j) o[j] = __builtin_nanf("");
+    return;
+  }
+  const uint8_t *unit = raw + (id * units_per_row + p / P::PER_UNIT) * Fmt<TYPE>::UB;
+  P::run(unit, (int)(p % P::PER_UNIT), o);
+}
+
+template <int TYPE>
+static void dequant_raw_type(const uint8_t *raw, int64_t n_elems, float *out, hipStream_t s) {
+  const int64_t pieces = n_elems / RawPiece<TYPE>::VALUES;
+  hipLaunchKernelGGL(dequant_raw_kernel<TYPE>, dim3((unsigned)((pieces + 255) / 256)), dim3(256),
+                     0, s, raw, pieces, out);
+}
+
 hipError_t launch_dequant_raw(const uint8_t *raw, int type, int64_t n_elems, float *out,
                               hipStream_t s) {
-  if (type == 8) {
-    const int64_t nb = n_elems / 32;
-    hipLaunchKernelGGL(dequant_raw_q8_0_kernel, dim3((unsigned)((nb + 255) / 256)), dim3(256), 0,
-                       s, raw, nb, out);
-  } else if (type == 12) {
-    const int64_t nsb = n_elems / 256;
-    hipLaunchKernelGGL(dequant_raw_q4_k_kernel, dim3((unsigned)((nsb * 4 + 255) / 256)), dim3(256),
-                       0, s, raw, nsb, out);
-  } else {
-    const int64_t nsb = n_elems / 256;
-    hipLaunchKernelGGL(dequant_raw_q6_k_kernel, dim3((unsigned)((nsb * 2 + 255) / 256)), dim3(256),
-                       0, s, raw, nsb, out);
-  }
+  if (type == 8)
+    dequant_raw_type<8>(raw, n_elems, out, s);
+  else if (type == 12)
+    dequant_raw_type<12>(raw, n_elems, out, s);
+  else
+    dequant_raw_type<14>(raw, n_elems, out, s);
+  return hipGetLastError();
+}
+
+template <int TYPE>
+static void get_rows_type(const uint8_t *raw, int64_t n_rows, int64_t k, const int64_t *ids,
+                          int64_t n_ids, float *out, int64_t ldo, hipStream_t s) {
+  const int64_t upr = k / Fmt<TYPE>::UE;
+  const int64_t threads = n_ids * upr * RawPiece<TYPE>::PER_UNIT;
+  hipLaunchKernelGGL(get_rows_kernel<TYPE>, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0,
+                     s, raw, n_rows, upr, ids, n_ids, out, ldo);
+}
+
+hipError_t launch_get_rows(const uint8_t *raw, int type, int64_t n_rows, int64_t k,
+                           const int64_t *ids, int64_t n_ids, float *out, int64_t ldo,
+                           hipStream_t s) {
+  if (type == 8)
+    get_rows_type<8>(raw, n_rows, k, ids, n_ids, out, ldo, s);
+  else if (type == 12)
+    get_rows_type<12>(raw, n_rows, k, ids, n_ids, out, ldo, s);
+  else
+    get_rows_type<14>(raw, n_rows, k, ids, n_ids, out, ldo, s);
   return hipGetLastError();
 }
 

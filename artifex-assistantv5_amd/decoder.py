@@ -32,14 +32,15 @@ from __future__ import annotations
 import dataclasses
 import math
 import time
-from typing import Optional
+from typing import Optional, Union
 
 import numpy as np
 import torch
 
 from . import glue, quantize
-from .ggml import Q4_K, Q6_K
-from .linear import GGUFWeight, LayerWeights, concat_rows, dispatch_matmul_gguf, repack_gguf_for_gpu
+from .ggml import Q4_K, Q6_K, raw_row_bytes
+from .linear import (GGUFWeight, LayerWeights, QuantEmbedding, concat_rows, dispatch_matmul_gguf,
+                     repack_gguf_for_gpu)
 
 
 @dataclasses.dataclass
@@ -58,6 +59,7 @@ class DecoderConfig:
     gate_up_type: int = Q4_K
     down_type: int = Q6_K
     lm_head_type: int = Q6_K
+    rope_freq_factors: Optional[tuple] = None   # per-pair divisors of theta (llama rope_freqs)
 
     @property
     def qkv_rows(self) -> int:
@@ -65,7 +67,6 @@ class DecoderConfig:
 
     def weight_bytes_per_token(self) -> int:
         """Quantized weight bytes one decode step streams from HBM."""
-        from .ggml import raw_row_bytes
         d, f = self.d_model, self.ffn
         per_layer = (self.qkv_rows * raw_row_bytes(self.attn_type, d)
                      + d * raw_row_bytes(self.attn_type, self.n_heads * self.head_dim)
@@ -76,10 +77,32 @@ class DecoderConfig:
 
 @dataclasses.dataclass
 class DecoderWeights:
-    layers: list            # LayerWeights: qkv_gg, o_gg, gateUp_gg, down_gg, attn_norm, ffn_norm
+    """Per-layer ``LayerWeights`` slots: ``qkv_gg`` (Q, K, V rows concatenated) or,
+    when the three have different GGUF types, ``qkv_parts = [q, k, v]``; likewise
+    ``gateUp_gg`` or ``gateUp_parts = [gate, up]``; ``o_gg``, ``down_gg`` and the f32
+    norms ``attn_norm`` / ``ffn_norm``.  ``embed`` is a dense ``[vocab, d_model]``
+    table or a ``QuantEmbedding`` of raw GGUF rows."""
+    layers: list
     final_norm: torch.Tensor
     lm_head_gg: GGUFWeight
-    embed: torch.Tensor     # [vocab, d_model] f16, gathered by token id
+    embed: Union[torch.Tensor, QuantEmbedding]
+
+    def weight_bytes_per_token(self) -> int:
+        """Quantized bytes one decode step streams (projections and LM head)."""
+        def nb(w):
+            return w.n * raw_row_bytes(w.ggml_type, w.k)
+        total = nb(self.lm_head_gg)
+        for lw in self.layers:
+            for slot in ("qkv", "gateUp"):
+                total += sum(nb(w) for w in parts(lw, slot))
+            total += nb(lw.o_gg) + nb(lw.down_gg)
+        return total
+
+
+def parts(lw: LayerWeights, slot: str) -> list:
+    """The weights of a row-concatenated slot: ``[<slot>_gg]`` or ``<slot>_parts``."""
+    w = lw.get(f"{slot}_gg")
+    return [w] if w is not None else list(lw.get(f"{slot}_parts"))
 
 
 def _quantized(ggml_type: int, n: int, k: int, seed: int, device) -> GGUFWeight:
@@ -147,6 +170,11 @@ def rms_norm(x: torch.Tensor, w: torch.Tensor, eps: float) -> torch.Tensor:
 def rope_tables(cfg: DecoderConfig, device) -> tuple[torch.Tensor, torch.Tensor]:
     half = cfg.head_dim // 2
     inv = 1.0 / (cfg.rope_base ** (torch.arange(half, dtype=torch.float64) * 2.0 / cfg.head_dim))
+    if cfg.rope_freq_factors is not None:
+        f = torch.tensor(cfg.rope_freq_factors, dtype=torch.float64)
+        if f.numel() != half:
+            raise ValueError(f"rope_freq_factors has {f.numel()} entries, head_dim/2 = {half}")
+        inv = inv / f
     ang = torch.arange(cfg.max_seq, dtype=torch.float64)[:, None] * inv[None, :]
     return ang.cos().float().to(device), ang.sin().float().to(device)
 
@@ -188,6 +216,22 @@ class QuantDecoder:
         dispatch_matmul_gguf(x, w, y, M, w.n, w.k, label)
         return y
 
+    def _proj_slot(self, x: torch.Tensor, lw: LayerWeights, slot: str, label: str) -> torch.Tensor:
+        ws = parts(lw, slot)
+        if len(ws) == 1:
+            return self._proj(x, ws[0], label)
+        return torch.cat([self._proj(x, w, f"{label}{i}") for i, w in enumerate(ws)], dim=1)
+
+    def _embed(self, tok: torch.Tensor, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+        e = self.w.embed
+        if isinstance(e, QuantEmbedding):
+            return e.gather(tok, out)
+        x = e.index_select(0, tok).float()
+        if out is None:
+            return x
+        out.copy_(x)
+        return out
+
     def _layers(self, x: torch.Tensor, pos: torch.Tensor) -> torch.Tensor:
         cfg = self.cfg
         M, nh, nkv, hd = x.shape[0], cfg.n_heads, cfg.n_kv_heads, cfg.head_dim
@@ -199,7 +243,7 @@ class QuantDecoder:
         scale = 1.0 / math.sqrt(hd)
         for l, lw in enumerate(self.w.layers):
             h = rms_norm(x, lw.attn_norm, cfg.eps)
-            qkv = self._proj(h, lw.qkv_gg, f"L{l}-qkv")
+            qkv = self._proj_slot(h, lw, "qkv", f"L{l}-qkv")
             q = qkv[:, :nh * hd].view(M, nh, hd)
             k = qkv[:, nh * hd:(nh + nkv) * hd].view(M, nkv, hd)
             v = qkv[:, (nh + nkv) * hd:].view(M, nkv, hd)
@@ -213,7 +257,7 @@ class QuantDecoder:
             o = o.view(nkv, M, grp, hd).permute(1, 0, 2, 3).reshape(M, nh * hd)
             x = x + self._proj(o, lw.o_gg, f"L{l}-o")
             h = rms_norm(x, lw.ffn_norm, cfg.eps)
-            gu = self._proj(h, lw.gateUp_gg, f"L{l}-gateUp")
+            gu = self._proj_slot(h, lw, "gateUp", f"L{l}-gateUp")
             a = gu[:, cfg.ffn:] * torch.nn.functional.silu(gu[:, :cfg.ffn])
             x = x + self._proj(a, lw.down_gg, f"L{l}-down")
         return x
@@ -230,7 +274,7 @@ class QuantDecoder:
         if pos0 + M > self.cfg.max_seq:
             raise ValueError(f"sequence of {pos0 + M} exceeds max_seq {self.cfg.max_seq}")
         pos = torch.arange(pos0, pos0 + M, device=self.device)
-        x = self.w.embed.index_select(0, tokens).float()
+        x = self._embed(tokens)
         x = self._layers(x, pos)
         return self._logits(x[-1:])
 
@@ -244,22 +288,28 @@ class QuantDecoder:
         projection with the SwiGLU prologue accumulated into the residual."""
         cfg, W = self.cfg, self.w
         x = self.b_x
-        x.copy_(W.embed.index_select(0, tok))
+        self._embed(tok, x)
         for l, lw in enumerate(W.layers):
-            glue.matmul_fused(x, lw.qkv_gg, self.b_qkv, glue.PROLOGUE_RMSNORM, lw.attn_norm,
-                              cfg.eps)
+            self._fused_slot(x, lw, "qkv", self.b_qkv, lw.attn_norm)
             glue.attention_decode(self.b_qkv, pos, self.cos, self.sin, self.k_cache[l],
                                   self.v_cache[l], self.b_att, cfg.n_heads, cfg.n_kv_heads,
                                   cfg.head_dim, self.w_att)
             glue.matmul_fused(self.b_att, lw.o_gg, x, accumulate=True)
-            glue.matmul_fused(x, lw.gateUp_gg, self.b_gu, glue.PROLOGUE_RMSNORM, lw.ffn_norm,
-                              cfg.eps)
+            self._fused_slot(x, lw, "gateUp", self.b_gu, lw.ffn_norm)
             glue.matmul_fused(self.b_gu, lw.down_gg, x, glue.PROLOGUE_SWIGLU, accumulate=True)
         glue.matmul_fused(x, W.lm_head_gg, self.b_logits, glue.PROLOGUE_RMSNORM, W.final_norm,
                           cfg.eps)
         glue.argmax(self.b_logits, tok, self.w_arg)
         pos.add_(1)
         return self.b_logits
+
+    def _fused_slot(self, x, lw, slot, y, norm_w) -> None:
+        """RMSNorm-prologue projection of a concatenated slot into ``y`` (one launch
+        per part; the parts write consecutive column ranges of ``y``)."""
+        c = 0
+        for w in parts(lw, slot):
+            glue.matmul_fused(x, w, y[:, c:c + w.n], glue.PROLOGUE_RMSNORM, norm_w, self.cfg.eps)
+            c += w.n
 
     @torch.no_grad()
     def step(self, tok: torch.Tensor, pos: torch.Tensor) -> torch.Tensor:
@@ -268,7 +318,7 @@ class QuantDecoder:
         Touches no host state, so it can be captured in a graph."""
         if self.fused:
             return self._step_fused(tok, pos)
-        x = self.w.embed.index_select(0, tok).float()
+        x = self._embed(tok)
         x = self._layers(x, pos)
         logits = self._logits(x)
         tok.copy_(torch.argmax(logits, dim=-1))

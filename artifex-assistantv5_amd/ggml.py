@@ -40,6 +40,7 @@ GGML_TYPE_NAMES = {v: k for k, v in GGML_TYPES.items()}
 
 F32 = GGML_TYPES["F32"]
 F16 = GGML_TYPES["F16"]
+BF16 = GGML_TYPES["BF16"]
 Q8_0 = GGML_TYPES["Q8_0"]
 Q4_K = GGML_TYPES["Q4_K"]
 Q6_K = GGML_TYPES["Q6_K"]

@@ -25,7 +25,7 @@ import torch
 
 from . import _native
 from .ggml import (F16, F32, GGML_TYPE_NAMES, TILE_ROWS, check_kernel_type, ggml_type_traits,
-                   tile_row_bytes, tiled_bytes)
+                   raw_row_bytes, tile_row_bytes, tiled_bytes)
 
 _X_TYPES = {torch.float32: F32, torch.float16: F16}
 
@@ -198,6 +198,53 @@ def dequant_raw(ggml_type: int, data, n: int, device=None) -> torch.Tensor:
         _native.check(lib.gguf_hip_dequant_raw(raw.data_ptr(), ggml_type, n, out.data_ptr(),
                                                _stream(dev)), lib)
     return out
+
+
+@dataclasses.dataclass
+class QuantEmbedding:
+    """A table of ``n`` raw GGUF rows of ``k`` elements resident in HBM.
+
+    ``gather(ids)`` dequantizes the rows named by a device int64 tensor with
+    one launch (``gguf_hip_get_rows``).  The reference keeps ``token_embd`` in
+    host RAM as raw blocks and row-gathers + dequantizes each token on the CPU
+    (webgpu/src/model/gguf-loader.ts:177-187, webgpu/src/engine/forward-pass.ts:2171-2186);
+    with 288 GB of HBM the table stays on the device and the token id never
+    leaves it, so a decode step that embeds its token can be graph-captured.
+    An id outside ``[0, n)`` produces a row of NaN."""
+
+    data: torch.Tensor   # uint8, raw GGUF bytes of the n rows
+    ggml_type: int
+    n: int
+    k: int
+
+    def __post_init__(self):
+        check_kernel_type(self.ggml_type)
+        if self.data.dtype != torch.uint8 or not self.data.is_cuda:
+            raise ValueError("QuantEmbedding.data must be a uint8 tensor on a HIP device")
+        need = self.n * raw_row_bytes(self.ggml_type, self.k)
+        if self.data.numel() != need:
+            raise ValueError(f"[GGUF] token table holds {self.data.numel()} B, expected {need}")
+
+    @property
+    def device(self) -> torch.device:
+        return self.data.device
+
+    def gather(self, ids: torch.Tensor, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+        """f32 ``[len(ids), k]`` rows (written into ``out`` when given)."""
+        lib = _native.load_library()
+        if ids.dtype != torch.int64 or ids.device != self.device:
+            raise ValueError("QuantEmbedding.gather: ids must be int64 on the table's device")
+        ids = ids.reshape(-1).contiguous()
+        if out is None:
+            out = torch.empty(ids.numel(), self.k, dtype=torch.float32, device=self.device)
+        ldo = _row_stride(out, ids.numel(), self.k, "out")
+        if out.dtype != torch.float32:
+            raise ValueError("QuantEmbedding.gather: out must be float32")
+        with torch.cuda.device(self.device):
+            _native.check(lib.gguf_hip_get_rows(self.data.data_ptr(), self.ggml_type, self.n,
+                                                self.k, ids.data_ptr(), ids.numel(),
+                                                out.data_ptr(), ldo, _stream(self.device)), lib)
+        return out
 
 
 def _row_stride(t: torch.Tensor, rows: int, cols: int, name: str) -> int:

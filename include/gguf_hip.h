@@ -43,7 +43,7 @@ extern "C" {
  * are exported (kernels and helpers cannot be interposed across libraries). */
 #pragma GCC visibility push(default)
 
-#define GGUF_HIP_ABI_VERSION 4
+#define GGUF_HIP_ABI_VERSION 5
 
 /* ggml type ids (gguf.ts:24-35); activation dtypes reuse F32 / F16. */
 #define GGUF_HIP_F32 0
@@ -113,6 +113,17 @@ int gguf_hip_dequant(const void *tiles, int ggml_type, int64_t n_rows, int64_t k
  * the reference uses it for the CPU embedding row-gather (forward-pass.ts:2171-2186). */
 int gguf_hip_dequant_raw(const void *raw, int ggml_type, int64_t n_elems, float *out,
                          void *stream);
+
+/* Row gather of a raw GGUF table: out[i * ldo + j] = dequant(raw row ids[i])[j]
+ * for i < n_ids, j < k.  raw: n_rows x k elements of raw GGUF rows (device,
+ * any alignment); ids: device int64[n_ids]; out: f32.  Values are those of
+ * dequantGGML on the row's bytes.  Replaces the reference's CPU embedding
+ * row-gather (webgpu/src/engine/forward-pass.ts:2171-2186, token_embd kept in
+ * RAM by webgpu/src/model/gguf-loader.ts:177-187); here the table stays in HBM
+ * and the ids are read on the device, so a decode step that gathers its token
+ * can be captured in a graph.  An id outside [0, n_rows) yields a row of NaN. */
+int gguf_hip_get_rows(const void *raw, int ggml_type, int64_t n_rows, int64_t k,
+                      const int64_t *ids, int64_t n_ids, float *out, int64_t ldo, void *stream);
 
 /* y[m * ldy + n] = sum_k x[m * ldx + k] * dequant(W)[n, k] for m < M, n < N.
  * x: f32 or f16 (x_type = GGUF_HIP_F32 / GGUF_HIP_F16), 16-byte aligned rows

@@ -43,7 +43,7 @@ def native(pkg):
 
 def test_exports_every_declared_symbol(lib, native):
     names = _declared_functions()
-    assert len(names) == 18, names
+    assert len(names) == 19, names
     for n in names:
         assert hasattr(lib, n), n
         assert n in native.SIGNATURES, n
@@ -67,7 +67,7 @@ def test_constants_match_header(native):
 
 
 def test_abi_version(lib):
-    assert lib.gguf_hip_abi_version() == 4
+    assert lib.gguf_hip_abi_version() == 5
 
 
 def test_type_traits(lib, native):
@@ -114,6 +114,19 @@ def test_dequant_errors(lib, native):
     assert lib.gguf_hip_dequant_raw(None, 8, 33, None, None) == native.ERR_SHAPE
     assert lib.gguf_hip_dequant_raw(None, 8, 64, None, None) == native.ERR_NULL
     assert lib.gguf_hip_dequant_raw(None, 8, 0, None, None) == 0
+
+
+def test_get_rows_errors(lib, native):
+    gr = lib.gguf_hip_get_rows
+    raw, ids, out = 0x1000, 0x2000, 0x3000
+    assert gr(raw, 2, 4, 512, ids, 1, out, 512, None) == native.ERR_TYPE
+    assert gr(raw, 12, 4, 300, ids, 1, out, 512, None) == native.ERR_SHAPE
+    assert gr(raw, 12, -1, 512, ids, 1, out, 512, None) == native.ERR_SHAPE
+    assert gr(raw, 12, 4, 512, ids, 2, out, 256, None) == native.ERR_SHAPE     # ldo < K
+    assert gr(None, 12, 4, 512, ids, 1, out, 512, None) == native.ERR_NULL
+    assert gr(raw, 12, 4, 512, ids + 4, 1, out, 512, None) == native.ERR_ALIGN
+    assert gr(raw, 12, 4, 512, ids, 1, out + 2, 512, None) == native.ERR_ALIGN
+    assert gr(None, 12, 4, 512, None, 0, None, 512, None) == 0                 # no ids: no-op
 
 
 def test_matmul_errors(lib, native):

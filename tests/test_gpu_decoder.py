@@ -37,13 +37,21 @@ class Reference:
     """float64 decoder over dequantized weights, one position at a time."""
 
     def __init__(self, cfg, w):
+        dec = importlib.import_module("artifex-assistantv5_amd.decoder")
         self.cfg = cfg
         d = lambda gg: gg.dequant().double()  # noqa: E731
-        self.layers = [dict(qkv=d(l.qkv_gg), o=d(l.o_gg), gu=d(l.gateUp_gg), down=d(l.down_gg),
-                            an=l.attn_norm.double(), fn=l.ffn_norm.double()) for l in w.layers]
+        cat = lambda l, slot: torch.cat([d(p) for p in dec.parts(l, slot)])  # noqa: E731
+        self.layers = [dict(qkv=cat(l, "qkv"), o=d(l.o_gg), gu=cat(l, "gateUp"),
+                            down=d(l.down_gg), an=l.attn_norm.double(),
+                            fn=l.ffn_norm.double()) for l in w.layers]
         self.lm = d(w.lm_head_gg)
         self.fnorm = w.final_norm.double()
-        self.embed = w.embed.double()
+        if isinstance(w.embed, torch.Tensor):
+            self.embed = w.embed.double()
+        else:
+            self.embed = w.embed.gather(torch.arange(w.embed.n, device="cuda")).double()
+        self.freq = (torch.tensor(cfg.rope_freq_factors, dtype=torch.float64, device="cuda")
+                     if cfg.rope_freq_factors is not None else 1.0)
         self.k = [[] for _ in w.layers]
         self.v = [[] for _ in w.layers]
 
@@ -53,7 +61,7 @@ class Reference:
     def rope(self, x, pos):  # x [H, D]
         D = x.shape[-1]
         i = torch.arange(D // 2, dtype=torch.float64, device=x.device)
-        theta = pos / self.cfg.rope_base ** (2 * i / D)
+        theta = pos / self.cfg.rope_base ** (2 * i / D) / self.freq
         z = torch.complex(x[:, :D // 2], x[:, D // 2:]) * torch.exp(1j * theta)
         return torch.cat([z.real, z.imag], dim=-1)
 

@@ -1,0 +1,131 @@
+"""GGUF loader, row-gather kernel and file-loaded decoder on the GPU.
+
+* ``gguf_hip_get_rows`` is bit-exact to the oracle's dequant of the named rows
+  (the reference's CPU embedding row-gather, forward-pass.ts:2171-2186).
+* The loader places each tensor kind as ``gguf-loader.ts`` does: quantized
+  matrices repacked, F32/F16/BF16 as f32, ``token_embd`` as a gather table,
+  experts / vision / ``rope_freqs`` kept off the device.
+* A decoder loaded from a synthetic llama GGUF file (Q/K rows permuted as
+  llama.cpp's converter writes them, Q/K/V of mixed types, a Q8_0 token table)
+  matches a decoder built directly from the same quantized rows bit for bit,
+  and the float64 reference decoder of test_gpu_decoder.py with RoPE
+  frequency factors.
+"""
+import importlib
+
+import numpy as np
+import pytest
+
+torch = pytest.importorskip("torch")
+
+import gguf_models as gm  # noqa: E402
+from test_gpu_decoder import Reference, _rel  # noqa: E402
+
+pytestmark = pytest.mark.gpu
+
+pkg = importlib.import_module("artifex-assistantv5_amd")
+loader = importlib.import_module("artifex-assistantv5_amd.gguf_loader")
+gmodel = importlib.import_module("artifex-assistantv5_amd.gguf_model")
+dec = importlib.import_module("artifex-assistantv5_amd.decoder")
+
+
+@pytest.mark.parametrize("t", [8, 12, 14])
+def test_get_rows_bit_exact(ref, t):
+    n, k = 40, 512
+    raw = pkg.quantize.quantize(pkg.quantize.synthetic_weight(n, k, seed=t, std=1.0), t)
+    table = pkg.QuantEmbedding(torch.from_numpy(raw).cuda(), t, n, k)
+    ids = [3, 0, 39, 3, 17]
+    got = table.gather(torch.tensor(ids, device="cuda")).cpu().numpy()
+    want = ref.dequant_rows(t, raw, n, k)[ids]
+    assert ref.same_bits(got, want)
+    # strided output rows and an out-of-range id (a NaN row, no fault)
+    out = torch.zeros(3, k + 64, device="cuda")
+    table.gather(torch.tensor([1, n, -1], device="cuda"), out[:, :k])
+    o = out.cpu().numpy()
+    assert ref.same_bits(o[0, :k], ref.dequant_rows(t, raw, n, k)[1])
+    assert np.isnan(o[1:, :k]).all() and (o[:, k:] == 0).all()
+
+
+def test_loader_placement(tmp_path, ref):
+    tensors = gm.make_model(seed=1, rope_freqs=True)
+    extra = [("blk.0.ffn_gate_exps.weight", [256, 64, 4], 12,
+              np.zeros(4 * 64 * 144, np.uint8)),
+             ("v.patch_embd.weight", [32, 4], 0, np.zeros(128, np.float32)),
+             ("blk.0.attn_q_norm.weight", [64], 1, np.arange(64, dtype=np.float16)),
+             ("blk.0.bias16.weight", [64], 30,
+              (np.arange(64, dtype=np.float32).view(np.uint32) >> 16).astype(np.uint16))]
+    p = str(tmp_path / "m.gguf")
+    gm.write_model(p, tensors, extra_tensors=extra)
+    m = loader.load_gguf_model(p, "cuda")
+    assert set(m.expert_tensors) == {"blk.0.ffn_gate_exps.weight"}
+    assert m.expert_bytes == 4 * 64 * 144
+    assert "v.patch_embd.weight" not in m.tensors
+    assert "rope_freqs.weight" in m.host_tensors and "rope_freqs.weight" not in m.tensors
+    f16 = m.tensors["blk.0.attn_q_norm.weight"]
+    assert f16.data.dtype == torch.float32 and not f16.is_quantized
+    assert torch.equal(f16.data.cpu(), torch.arange(64, dtype=torch.float32))
+    assert torch.equal(m.tensors["blk.0.bias16.weight"].data.cpu(),
+                       torch.arange(64, dtype=torch.float32))
+    norm = m.tensors["blk.1.ffn_norm.weight"].data.cpu().numpy()
+    assert np.array_equal(norm, tensors["blk.1.ffn_norm.weight"][3])
+    emb = m.row_tables["token_embd.weight"]
+    assert isinstance(emb, pkg.QuantEmbedding) and "token_embd.weight" not in m.tensors
+    down = m.tensors["blk.1.ffn_down.weight"]
+    assert down.is_quantized and down.dtype == "Q6_K"
+    typ, n, k, raw = tensors["blk.1.ffn_down.weight"]
+    assert ref.same_bits(down.data.dequant().cpu().numpy(), ref.dequant_rows(typ, raw, n, k))
+    assert m.total_gpu_bytes >= sum(t.byte_length for t in m.tensors.values())
+
+
+def test_tied_embeddings_feed_the_lm_head(tmp_path, ref):
+    tensors = gm.make_model(seed=2, tied=True)
+    p = str(tmp_path / "tied.gguf")
+    gm.write_model(p, tensors)
+    m = loader.load_gguf_model(p, "cuda")
+    typ, n, k, raw = tensors["token_embd.weight"]
+    w = m.tensors["token_embd.weight"].data
+    assert (w.n, w.k) == (n, k)
+    assert ref.same_bits(w.dequant().cpu().numpy(), ref.dequant_rows(typ, raw, n, k))
+    assert isinstance(m.row_tables["token_embd.weight"], pkg.QuantEmbedding)
+
+
+@pytest.mark.parametrize("variant", ["mixed_qkv", "uniform_tied"])
+def test_decoder_from_gguf_matches_direct_build(tmp_path, variant):
+    types = {} if variant == "mixed_qkv" else {"v": 12, "down": 12, "embd": 14}
+    tensors = gm.make_model(seed=4, types=types, tied=variant == "uniform_tied")
+    p = str(tmp_path / "m.gguf")
+    gm.write_model(p, tensors)
+    model, loaded = gmodel.load_decoder(p, "cuda", max_seq=64)
+    cfg = model.cfg
+    lw = model.w.layers[0]
+    if variant == "mixed_qkv":
+        assert lw.get("qkv_gg") is None and len(lw.qkv_parts) == 3
+    else:
+        assert lw.qkv_gg is not None
+    direct = dec.QuantDecoder(cfg, gm.direct_weights(tensors, gm.TINY))
+    prompt = torch.from_numpy(np.random.default_rng(7).integers(0, cfg.vocab, 24)).cuda()
+    assert torch.equal(model.prefill(prompt), direct.prefill(prompt))
+    a = model.generate(prompt, 10, graph=True)
+    b = direct.generate(prompt, 10, graph=False)
+    assert torch.equal(a["tokens"], b["tokens"])
+
+
+def test_decoder_from_gguf_matches_float64_reference(tmp_path):
+    tensors = gm.make_model(seed=5, rope_freqs=True)
+    p = str(tmp_path / "m.gguf")
+    gm.write_model(p, tensors, extra_kv={"llama.rope.freq_base": 500000.0})
+    model, _ = gmodel.load_decoder(p, "cuda", max_seq=64)
+    cfg = model.cfg
+    assert cfg.rope_base == 500000.0 and len(cfg.rope_freq_factors) == cfg.head_dim // 2
+    r = Reference(cfg, model.w)
+    prompt = torch.from_numpy(np.random.default_rng(8).integers(0, cfg.vocab, 36)).cuda()
+    logits = model.prefill(prompt)[0]
+    for pos, t in enumerate(prompt.tolist()):
+        rl = r.token(t, pos)
+    assert _rel(logits, rl) < 5e-3
+    tok = torch.argmax(logits).view(1)
+    pos = torch.tensor([prompt.numel()], device="cuda")
+    for _ in range(4):
+        t = int(tok.item())
+        lg = model.step(tok, pos)[0]
+        assert _rel(lg, r.token(t, int(pos.item()) - 1)) < 1e-3
