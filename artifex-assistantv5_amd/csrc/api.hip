@@ -45,7 +45,9 @@ bool traits(int t, int *block, int *size) {
   return false;
 }
 
-bool kernel_type(int t) { return t == GGUF_HIP_Q8_0 || t == GGUF_HIP_Q4_K || t == GGUF_HIP_Q6_K; }
+bool kernel_type(int t) {
+  return t == GGUF_HIP_Q8_0 || t == GGUF_HIP_Q4_K || t == GGUF_HIP_Q5_K || t == GGUF_HIP_Q6_K;
+}
 
 int check_type(int t) {
   int b, s;

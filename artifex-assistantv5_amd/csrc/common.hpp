@@ -20,7 +20,7 @@ constexpr int kWave = 64;
 //
 // A weight of N rows x K columns is stored as ceil(N/16) row tiles of 16
 // consecutive rows (rows past N are zero).  A tile holds, for each "unit" of
-// the row (a 256-element superblock for Q4_K / Q6_K, a 32-element block for
+// the row (a 256-element superblock for Q4_K / Q5_K / Q6_K, a 32-element block for
 // Q8_0) in K order, one tile-unit of 16 * (GGUF block bytes): the 16 rows'
 // blocks interleaved at 16-byte (Q8_0 quant bytes: 8-byte) granularity so
 // that one wave-wide load reads contiguous memory and lane (r = lane & 15,
@@ -29,6 +29,8 @@ constexpr int kWave = 64;
 //   Q4_K (2304 B)  [   0,  256) header of row r at 16 r: d, dmin, scales[12]
 //                  [ 256, 2304) piece (cp, g, r) at 256 + ((4 cp + g) * 16 + r) * 16:
 //                               qs[64 cp + 8 g, +8) | qs[64 cp + 32 + 8 g, +8)
+//   Q5_K (2816 B)  [   0, 2304) as Q4_K (headers, then the qs pieces)
+//                  [2304, 2816) piece (g, r) at 2304 + (16 g + r) * 8: qh[8 g, +8)
 //   Q6_K (3360 B)  [   0, 3072) piece (v, g, r) at ((4 v + g) * 16 + r) * 16 holds
 //                               dwords 4v..4v+3 of the lane's 12 quant dwords;
 //                               for i = 2 hf + lh:  dword 3i   = ql[64 hf + 16 lh + 4 g, +4)
@@ -51,6 +53,10 @@ struct Fmt<12> {  // Q4_K
   static constexpr int UE = 256, UB = 144, TU = 16 * 144;
 };
 template <>
+struct Fmt<13> {  // Q5_K
+  static constexpr int UE = 256, UB = 176, TU = 16 * 176;
+};
+template <>
 struct Fmt<14> {  // Q6_K
   static constexpr int UE = 256, UB = 210, TU = 16 * 210;
 };
@@ -61,7 +67,7 @@ struct Fmt<8> {  // Q8_0
 
 __host__ __device__ inline int unit_elems(int type) { return type == 8 ? 32 : 256; }
 __host__ __device__ inline int unit_bytes(int type) {
-  return type == 8 ? 34 : (type == 12 ? 144 : 210);
+  return type == 8 ? 34 : (type == 12 ? 144 : (type == 13 ? 176 : 210));
 }
 
 // IEEE half bits -> f32 with the hardware converter (subnormals, Inf and NaN
@@ -86,6 +92,26 @@ __device__ __forceinline__ void q4k_scale_min(int j, uint32_t s0, uint32_t s1, u
     sc = (b2 & 0x0Fu) | ((b0 >> 6) << 4);
     m = (b2 >> 4) | ((b1 >> 6) << 4);
   }
+}
+
+// The fifth bits of a Q5_K code word.  w holds four code bytes (k = b0..b0+3
+// of a lane's 8), h the qh bytes of the same k; sub-block j's fifth bit is
+// bit j of the qh byte.  Returns the words of 16-bit halves that add
+// 16 * bit to the codes the decoders extract with the masks 0x000F000F
+// (even bytes) and (w >> 8) & 0x000F000F (odd bytes) for the low-nibble
+// sub-block j = 2c, and 256 * bit (16 x the high nibble's 16) for the
+// high-nibble sub-block j = 2c + 1 (masks 0x00F000F0).
+__device__ __forceinline__ uint32_t q5k_lo_even(uint32_t h, int c) {
+  return ((h >> (2 * c)) & 0x00010001u) << 4;
+}
+__device__ __forceinline__ uint32_t q5k_lo_odd(uint32_t h, int c) {
+  return ((h >> (8 + 2 * c)) & 0x00010001u) << 4;
+}
+__device__ __forceinline__ uint32_t q5k_hi_even(uint32_t h, int c) {
+  return ((h >> (2 * c + 1)) & 0x00010001u) << 8;
+}
+__device__ __forceinline__ uint32_t q5k_hi_odd(uint32_t h, int c) {
+  return ((h >> (9 + 2 * c)) & 0x00010001u) << 8;
 }
 
 // All eight 6-bit scales and mins of a Q4_K superblock, one per byte:

@@ -10,8 +10,8 @@
 // Arithmetic.  The reference computes sum_k a_k * (d1 * q_k - min1) per unit
 // in f32.  Here the quantized codes q are fed to the matrix cores *exactly*:
 // a code masked into the low bits of an f16 is the subnormal q * 2^-24
-// (Q4_K high nibbles: 16 q * 2^-24; Q8_0: (q + 128) * 2^-24; Q6_K: the
-// unsigned 6-bit q + 32).  Activations are split into f16 hi + lo parts
+// (Q4_K high nibbles: 16 q * 2^-24; Q5_K: the 5-bit code, its high-nibble
+// sub-blocks as 16 q; Q8_0: (q + 128) * 2^-24; Q6_K: the unsigned 6-bit q + 32).  Activations are split into f16 hi + lo parts
 // (x = hi + lo to 22 significant bits; f16 activations are exact in hi
 // alone).  One v_mfma_f32_16x16x32_f16 (Q6_K: 16x16x16, one 16-element scale
 // group) then yields the exact-product, f32-accumulated dot of one scale
@@ -45,6 +45,11 @@ struct Unit<12> {  // header, qs pieces cp = 0, 1
   uint4 h, a, b;
 };
 template <>
+struct Unit<13> {  // as Q4_K, plus the lane's qh bytes 8g..8g+7
+  uint4 h, a, b;
+  uint2 qh;
+};
+template <>
 struct Unit<14> {  // quant pieces v = 0..2, scales, d
   uint4 p0, p1, p2, sc;
   uint32_t d;
@@ -70,6 +75,10 @@ template <int TYPE>
 struct Dec;
 template <>
 struct Dec<12> {
+  static constexpr int GS = 32, P1 = GGUF_DECODE_P_Q4K;
+};
+template <>
+struct Dec<13> {
   static constexpr int GS = 32, P1 = GGUF_DECODE_P_Q4K;
 };
 template <>
@@ -112,6 +121,14 @@ __device__ __forceinline__ void load_unit(__amdgpu_buffer_rsrc_t rs, int soff, i
   u.h = bload16(rs, 16 * r, soff);
   u.a = bload16(rs, qa, soff);
   u.b = bload16(rs, qa + 1024, soff);
+}
+__device__ __forceinline__ void load_unit(__amdgpu_buffer_rsrc_t rs, int soff, int r, int g,
+                                          Unit<13> &u) {
+  const int qa = 256 + (16 * g + r) * 16;
+  u.h = bload16(rs, 16 * r, soff);
+  u.a = bload16(rs, qa, soff);
+  u.b = bload16(rs, qa + 1024, soff);
+  u.qh = bload8(rs, 2304 + (16 * g + r) * 8, soff);
 }
 __device__ __forceinline__ void load_unit(__amdgpu_buffer_rsrc_t rs, int soff, int r, int g,
                                           Unit<14> &u) {
@@ -207,11 +224,30 @@ constexpr int kZeroHalves = 256;  // covers every immediate offset added to a se
 // applies their scales; a 4-lane sum per row finishes the unit.
 // ---------------------------------------------------------------------------
 
-// Q4_K: 8 sub-blocks, one chain; lane (n, g) keeps sub-blocks 2g (lo nibbles
-// of chunk g) and 2g + 1 (hi nibbles).
-template <int PARTS>
-__device__ __forceinline__ void unit_m1(const Unit<12> &u, const Stage &st, int ul, int lane,
-                                        float &acc) {
+// B operands of chunk c of a Q4_K / Q5_K unit: the lane's 8 codes of
+// sub-block 2c (low nibbles, as q) and 2c + 1 (high nibbles, as 16 q), halves
+// in (0, 2, 1, 3) order per quad.  Q5_K adds the fifth bits.
+template <int TYPE>
+__device__ __forceinline__ void k_codes(const Unit<TYPE> &u, int c, half8_t &blo, half8_t &bhi) {
+  const uint32_t w[8] = {u.a.x, u.a.y, u.a.z, u.a.w, u.b.x, u.b.y, u.b.z, u.b.w};
+  const uint32_t wa = w[2 * c], wb = w[2 * c + 1];
+  const uint32_t wa8 = wa >> 8, wb8 = wb >> 8;
+  uint32_t l0 = wa & 0x000F000Fu, l1 = wa8 & 0x000F000Fu, l2 = wb & 0x000F000Fu, l3 = wb8 & 0x000F000Fu;
+  uint32_t h0 = wa & 0x00F000F0u, h1 = wa8 & 0x00F000F0u, h2 = wb & 0x00F000F0u, h3 = wb8 & 0x00F000F0u;
+  if constexpr (TYPE == 13) {
+    const uint32_t qa = u.qh.x, qb = u.qh.y;
+    l0 |= q5k_lo_even(qa, c); l1 |= q5k_lo_odd(qa, c); l2 |= q5k_lo_even(qb, c); l3 |= q5k_lo_odd(qb, c);
+    h0 |= q5k_hi_even(qa, c); h1 |= q5k_hi_odd(qa, c); h2 |= q5k_hi_even(qb, c); h3 |= q5k_hi_odd(qb, c);
+  }
+  blo = as_h8(l0, l1, l2, l3);
+  bhi = as_h8(h0, h1, h2, h3);
+}
+
+// Q4_K / Q5_K: 8 sub-blocks, one chain; lane (n, g) keeps sub-blocks 2g (lo
+// nibbles of chunk g) and 2g + 1 (hi nibbles).
+template <int PARTS, int TYPE>
+__device__ __forceinline__ void unit_m1_k(const Unit<TYPE> &u, const Stage &st, int ul, int lane,
+                                          float &acc) {
   const int r = lane & 15, g = lane >> 4;
   const int jo = r >> 1;
   const bool live = PARTS == 2 || (r & 1) == 0;
@@ -231,19 +267,26 @@ __device__ __forceinline__ void unit_m1(const Unit<12> &u, const Stage &st, int 
   const int xs = st.xs + (ul * 8 + 2 * g) * st.ms;
   const float mx = m0 * lds_f(xs) + m1 * lds_f(xs + st.ms);
   const float d = h2f(u.h.x), dmin = h2f(u.h.x >> 16);
-  const uint32_t w[8] = {u.a.x, u.a.y, u.a.z, u.a.w, u.b.x, u.b.y, u.b.z, u.b.w};
   float4_t D = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int c = 0; c < 4; ++c) {  // codes of chunk c decoded just before its two MFMAs
-    const uint32_t wa = w[2 * c], wb = w[2 * c + 1];
-    const uint32_t wa8 = wa >> 8, wb8 = wb >> 8;
-    const half8_t blo = as_h8(wa & 0x000F000Fu, wa8 & 0x000F000Fu, wb & 0x000F000Fu, wb8 & 0x000F000Fu);
-    const half8_t bhi = as_h8(wa & 0x00F000F0u, wa8 & 0x00F000F0u, wb & 0x00F000F0u, wb8 & 0x00F000F0u);
+    half8_t blo, bhi;
+    k_codes(u, c, blo, bhi);
     D = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[2 * c], blo, D, 0, 0, 0);
     D = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[2 * c + 1], bhi, D, 0, 0, 0);
   }
   // rows 4g + i: sub-block 2g (i = 0, 1) and 2g + 1 (i = 2, 3), part i & 1
   acc += (d * kTwo24) * (sc0 * (D[0] + D[1])) + (d * kTwo20) * (sc1 * (D[2] + D[3])) - dmin * mx;
+}
+template <int PARTS>
+__device__ __forceinline__ void unit_m1(const Unit<12> &u, const Stage &st, int ul, int lane,
+                                        float &acc) {
+  unit_m1_k<PARTS, 12>(u, st, ul, lane, acc);
+}
+template <int PARTS>
+__device__ __forceinline__ void unit_m1(const Unit<13> &u, const Stage &st, int ul, int lane,
+                                        float &acc) {
+  unit_m1_k<PARTS, 13>(u, st, ul, lane, acc);
 }
 
 // Q6_K: 16 groups of 16 elements, two chains of 8 (halves hf = 0, 1); lane
@@ -314,17 +357,16 @@ __device__ __forceinline__ void unit_m1(const Unit<8> &u, const Stage &st, int u
   acc += g == 0 ? v : 0.f;
 }
 
-// One unit of Q4_K: 8 sub-blocks x MT activation tiles.  Per activation row
-// the sub-block dots are folded as
+// One unit of Q4_K / Q5_K: 8 sub-blocks x MT activation tiles.  Per
+// activation row the sub-block dots are folded as
 //   acc += d 2^24 sum_even sc_j D_j + d 2^20 sum_odd sc_j D_j - dmin sum_j m_j xs_j
 // (odd sub-blocks hold high nibbles, coded as 16 q).
-template <int PARTS, int MT, int MR>
-__device__ __forceinline__ void unit_compute(const Unit<12> &u, const Stage &st, int ul, int lane,
-                                             int M, float (&acc)[MT][4]) {
+template <int PARTS, int MT, int MR, int TYPE>
+__device__ __forceinline__ void unit_compute_k(const Unit<TYPE> &u, const Stage &st, int ul,
+                                               int lane, int M, float (&acc)[MT][4]) {
   const int r = lane & 15, g = lane >> 4;
   uint32_t sc_lo, sc_hi, m_lo, m_hi;
   q4k_scales_packed(u.h.y, u.h.z, u.h.w, sc_lo, sc_hi, m_lo, m_hi);
-  const uint32_t w[8] = {u.a.x, u.a.y, u.a.z, u.a.w, u.b.x, u.b.y, u.b.z, u.b.w};
   float se[MT][4], so[MT][4], sm[MT][4];
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt)
@@ -332,10 +374,8 @@ __device__ __forceinline__ void unit_compute(const Unit<12> &u, const Stage &st,
     for (int i = 0; i < 4; ++i) se[mt][i] = so[mt][i] = sm[mt][i] = 0.f;
 #pragma unroll
   for (int c = 0; c < 4; ++c) {
-    const uint32_t wa = w[2 * c], wb = w[2 * c + 1];
-    const uint32_t wa8 = wa >> 8, wb8 = wb >> 8;
-    const half8_t blo = as_h8(wa & 0x000F000Fu, wa8 & 0x000F000Fu, wb & 0x000F000Fu, wb8 & 0x000F000Fu);
-    const half8_t bhi = as_h8(wa & 0x00F000F0u, wa8 & 0x00F000F0u, wb & 0x00F000F0u, wb8 & 0x00F000F0u);
+    half8_t blo, bhi;
+    k_codes(u, c, blo, bhi);
     const uint32_t scw = c < 2 ? sc_lo : sc_hi, mw = c < 2 ? m_lo : m_hi;
     const int b0 = (2 * c) & 3, b1 = (2 * c + 1) & 3;
     const float sc0 = ubyte(scw, b0), m0 = ubyte(mw, b0);
@@ -371,6 +411,16 @@ __device__ __forceinline__ void unit_compute(const Unit<12> &u, const Stage &st,
 #pragma unroll
     for (int i = 0; i < MR; ++i)
       acc[mt][i] += d24 * se[mt][i] + d20 * so[mt][i] - dmin * sm[mt][i];
+}
+template <int PARTS, int MT, int MR>
+__device__ __forceinline__ void unit_compute(const Unit<12> &u, const Stage &st, int ul, int lane,
+                                             int M, float (&acc)[MT][4]) {
+  unit_compute_k<PARTS, MT, MR, 12>(u, st, ul, lane, M, acc);
+}
+template <int PARTS, int MT, int MR>
+__device__ __forceinline__ void unit_compute(const Unit<13> &u, const Stage &st, int ul, int lane,
+                                             int M, float (&acc)[MT][4]) {
+  unit_compute_k<PARTS, MT, MR, 13>(u, st, ul, lane, M, acc);
 }
 
 // One unit of Q6_K: 16 scale groups of 16 elements.
@@ -816,7 +866,7 @@ __global__ __launch_bounds__(512) void decode_m1_kernel(const XT *__restrict__ x
 // take one item per thread; longer K (or a fused prologue) leaves less room.
 template <int TYPE>
 constexpr int m1_umax(bool tight) {
-  return TYPE == 8 ? (tight ? 16 : 32) : (TYPE == 14 || tight ? 8 : 16);
+  return TYPE == 8 ? (tight ? 16 : 32) : (TYPE == 14 || TYPE == 13 || tight ? 8 : 16);
 }
 
 // Returns hipErrorNotSupported (nothing launched) when K is beyond the
@@ -880,6 +930,7 @@ template <typename XT>
 hipError_t launch_x(const XT *x, int64_t ldx, const uint8_t *W, int type, int N, int K, float *y,
                     int64_t ldy, int M, hipStream_t s) {
   if (type == 12) return launch_m<12, XT>(x, ldx, W, N, K, y, ldy, M, s);
+  if (type == 13) return launch_m<13, XT>(x, ldx, W, N, K, y, ldy, M, s);
   if (type == 14) return launch_m<14, XT>(x, ldx, W, N, K, y, ldy, M, s);
   return launch_m<8, XT>(x, ldx, W, N, K, y, ldy, M, s);
 }
@@ -899,6 +950,7 @@ hipError_t launch_decode_fused(const float *x, const uint8_t *tiles, int type, i
                          : launch_m1<T, float, 0>(x, tiles, (int)n, (int)k, y, pw, eps,     \
                                                   accumulate, s)
   if (type == 12) GGUF_FUSED(12);
+  if (type == 13) GGUF_FUSED(13);
   if (type == 14) GGUF_FUSED(14);
   GGUF_FUSED(8);
 #undef GGUF_FUSED

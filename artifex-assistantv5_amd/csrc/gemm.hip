@@ -107,6 +107,10 @@ struct BRaw<12> {
   uint2 q[kTN];  // the lane's 8 code bytes of the 64-wide window
 };
 template <>
+struct BRaw<13> {
+  uint2 q[kTN];  // the lane's 8 code bytes of the 64-wide window
+};
+template <>
 struct BRaw<14> {
   uint4 pa[kTN], pb[kTN];  // the two pieces holding the window's quant dwords
 };
@@ -124,6 +128,11 @@ struct BHdr<12> {
   uint4 hd[kTN];  // d, dmin, 12 scale bytes
 };
 template <>
+struct BHdr<13> {
+  uint4 hd[kTN];  // d, dmin, 12 scale bytes
+  uint2 qh[kTN];  // qh bytes 8g .. 8g + 7: the fifth bits of every window
+};
+template <>
 struct BHdr<14> {
   uint4 sc[kTN];  // 16 int8 scales
   uint32_t d[kTN];
@@ -138,7 +147,8 @@ template <>
 struct BCur<12> {
   uint32_t sc[kTN][2], mn[kTN][2];  // 6-bit scales / mins 0-3 and 4-7, one per byte
   float d24[kTN], d20[kTN], dmin[kTN];
-  __device__ __forceinline__ void set(const BHdr<12> &h) {
+  template <class H>
+  __device__ __forceinline__ void set(const H &h) {
 #pragma unroll
     for (int j = 0; j < kTN; ++j) {
       q4k_scales_packed(h.hd[j].y, h.hd[j].z, h.hd[j].w, sc[j][0], sc[j][1], mn[j][0], mn[j][1]);
@@ -147,6 +157,15 @@ struct BCur<12> {
       d20[j] = d * kTwo20;
       dmin[j] = h2f(h.hd[j].x >> 16);
     }
+  }
+};
+template <>
+struct BCur<13> : BCur<12> {
+  uint2 qh[kTN];
+  __device__ __forceinline__ void set(const BHdr<13> &h) {
+    BCur<12>::set(h);
+#pragma unroll
+    for (int j = 0; j < kTN; ++j) qh[j] = h.qh[j];
   }
 };
 template <>
@@ -173,6 +192,10 @@ __device__ __forceinline__ BOff b_offsets<12>(int r, int g) {
   return BOff{16 * r, 256 + (16 * g + r) * 16, 0, 0};
 }
 template <>
+__device__ __forceinline__ BOff b_offsets<13>(int r, int g) {
+  return BOff{16 * r, 256 + (16 * g + r) * 16, 2304 + (16 * g + r) * 8, 0};
+}
+template <>
 __device__ __forceinline__ BOff b_offsets<14>(int r, int g) {
   return BOff{(16 * g + r) * 16, 3328 + 2 * r, 3072 + 16 * r, 0};
 }
@@ -191,6 +214,20 @@ __device__ __forceinline__ void load_b(rsrc_t rs, const BOff &o, int ts, int u, 
 #pragma unroll
   for (int j = 0; j < kTN; ++j) {
     if (C == 0) h.hd[j] = bl16(rs, o.v0 + j * ts, su);
+    b.q[j] = bl8(rs, o.v1 + j * ts, su + (C >> 1) * 1024 + 8 * (C & 1));
+  }
+}
+template <int C>
+__device__ __forceinline__ void load_b(rsrc_t rs, const BOff &o, int ts, int u, int nu,
+                                       BRaw<13> &b, BHdr<13> &h) {
+  constexpr int TU = Fmt<13>::TU;
+  const int su = u * TU;
+#pragma unroll
+  for (int j = 0; j < kTN; ++j) {
+    if (C == 0) {
+      h.hd[j] = bl16(rs, o.v0 + j * ts, su);
+      h.qh[j] = bl8(rs, o.v2 + j * ts, su);
+    }
     b.q[j] = bl8(rs, o.v1 + j * ts, su + (C >> 1) * 1024 + 8 * (C & 1));
   }
 }
@@ -232,11 +269,12 @@ __device__ __forceinline__ void load_b(rsrc_t rs, const BOff &o, int ts, int u, 
   }
 }
 
-// Q4_K: lane (r, g), window c = chunk c of the superblock: low nibbles are
-// sub-block 2c (k = 8 g .. 8 g + 7 of the first 32), high nibbles sub-block 2c + 1.
-template <int C>
-__device__ __forceinline__ void dequant_b(const BRaw<12> &b, const BCur<12> &h,
-                                          half8_t (&bf)[kTN][2]) {
+// Q4_K / Q5_K: lane (r, g), window c = chunk c of the superblock: low
+// nibbles are sub-block 2c (k = 8 g .. 8 g + 7 of the first 32), high nibbles
+// sub-block 2c + 1.  Q5_K ORs the fifth bits into the codes first.
+template <int C, int TYPE>
+__device__ __forceinline__ void dequant_b_k(const BRaw<TYPE> &b, const BCur<TYPE> &h,
+                                            half8_t (&bf)[kTN][2]) {
   constexpr int W = C >> 1, B0 = (2 * C) & 3;  // scale word, byte of sub-block 2C
 #pragma unroll
   for (int j = 0; j < kTN; ++j) {
@@ -247,8 +285,15 @@ __device__ __forceinline__ void dequant_b(const BRaw<12> &b, const BCur<12> &h,
 #pragma unroll
     for (int w = 0; w < 2; ++w) {
       const uint32_t q = w ? b.q[j].y : b.q[j].x, q8 = q >> 8;
-      const uint32_t el = q & 0x000F000Fu, ol = q8 & 0x000F000Fu;  // bytes 0, 2 / 1, 3: low nibble
-      const uint32_t eh = q & 0x00F000F0u, oh = q8 & 0x00F000F0u;  // high nibble (x 16)
+      uint32_t el = q & 0x000F000Fu, ol = q8 & 0x000F000Fu;  // bytes 0, 2 / 1, 3: low nibble
+      uint32_t eh = q & 0x00F000F0u, oh = q8 & 0x00F000F0u;  // high nibble (x 16)
+      if constexpr (TYPE == 13) {
+        const uint32_t hb = w ? h.qh[j].y : h.qh[j].x;
+        el |= q5k_lo_even(hb, C);
+        ol |= q5k_lo_odd(hb, C);
+        eh |= q5k_hi_even(hb, C);
+        oh |= q5k_hi_odd(hb, C);
+      }
       lo[2 * w] = mix_lo(el, ol, s0, c0);
       lo[2 * w + 1] = mix_hi(el, ol, s0, c0);
       hi[2 * w] = mix_lo(eh, oh, s1, c1);
@@ -257,6 +302,17 @@ __device__ __forceinline__ void dequant_b(const BRaw<12> &b, const BCur<12> &h,
     bf[j][0] = h8(lo[0], lo[1], lo[2], lo[3]);
     bf[j][1] = h8(hi[0], hi[1], hi[2], hi[3]);
   }
+}
+
+template <int C>
+__device__ __forceinline__ void dequant_b(const BRaw<12> &b, const BCur<12> &h,
+                                          half8_t (&bf)[kTN][2]) {
+  dequant_b_k<C, 12>(b, h, bf);
+}
+template <int C>
+__device__ __forceinline__ void dequant_b(const BRaw<13> &b, const BCur<13> &h,
+                                          half8_t (&bf)[kTN][2]) {
+  dequant_b_k<C, 13>(b, h, bf);
 }
 
 // Q6_K: window c = quarters 2 (c & 1), 2 (c & 1) + 1 of half c >> 1.  The
@@ -547,6 +603,8 @@ hipError_t launch_x(const XT *x, int64_t ldx, const uint8_t *W, int type, int64_
                     float *y, int64_t ldy, int64_t m, hipStream_t s) {
   if (type == 12)
     launch_type<12, XT>(x, ldx, W, (int)m, (int)n, (int)k, y, ldy, s);
+  else if (type == 13)
+    launch_type<13, XT>(x, ldx, W, (int)m, (int)n, (int)k, y, ldy, s);
   else if (type == 8)
     launch_type<8, XT>(x, ldx, W, (int)m, (int)n, (int)k, y, ldy, s);
   else

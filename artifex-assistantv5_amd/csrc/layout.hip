@@ -36,10 +36,13 @@ __global__ __launch_bounds__(256) void repack_kernel(const uint8_t *__restrict__
   uint8_t *tu = tiles + ((n >> 4) * nu + u) * (int64_t)TU;
   if (n >= n_rows) {  // padding row of the last tile: every byte of its slots is zero
     const uint4 z = make_uint4(0, 0, 0, 0);
-    if (TYPE == 12) {
+    if (TYPE == 12 || TYPE == 13) {
       *(uint4 *)(tu + 16 * r) = z;
 #pragma unroll
       for (int p = 0; p < 8; ++p) *(uint4 *)(tu + 256 + (p * 16 + r) * 16) = z;
+      if (TYPE == 13)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) *(uint2 *)(tu + 2304 + (16 * g + r) * 8) = make_uint2(0, 0);
     } else if (TYPE == 14) {
 #pragma unroll
       for (int p = 0; p < 12; ++p) *(uint4 *)(tu + (p * 16 + r) * 16) = z;
@@ -53,10 +56,13 @@ __global__ __launch_bounds__(256) void repack_kernel(const uint8_t *__restrict__
     return;
   }
   const uint8_t *src = raw + (n * nu + u) * UB;
-  if (TYPE == 12) {
+  if (TYPE == 12 || TYPE == 13) {
     *(uint4 *)(tu + 16 * r) = make_uint4(ld_u32_bytes(src), ld_u32_bytes(src + 4),
                                          ld_u32_bytes(src + 8), ld_u32_bytes(src + 12));
-    const uint8_t *qs = src + 16;
+    const uint8_t *qs = src + (TYPE == 13 ? 48 : 16);
+    if (TYPE == 13)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) *(uint2 *)(tu + 2304 + (16 * g + r) * 8) = ld_u64_bytes(src + 16 + 8 * g);
 #pragma unroll
     for (int cp = 0; cp < 2; ++cp)
 #pragma unroll
@@ -101,6 +107,8 @@ hipError_t launch_repack(const uint8_t *raw, int type, int64_t n_rows, int64_t k
   const dim3 grid((unsigned)((total + 255) / 256)), block(256);
   if (type == 12)
     hipLaunchKernelGGL(repack_kernel<12>, grid, block, 0, s, raw, n_rows, nu, n_pad, tiles);
+  else if (type == 13)
+    hipLaunchKernelGGL(repack_kernel<13>, grid, block, 0, s, raw, n_rows, nu, n_pad, tiles);
   else if (type == 14)
     hipLaunchKernelGGL(repack_kernel<14>, grid, block, 0, s, raw, n_rows, nu, n_pad, tiles);
   else
@@ -131,6 +139,26 @@ __device__ __forceinline__ void q4k_decode_chunk(uint32_t hdr0, uint32_t s0, uin
   }
 }
 
+// Q5_K chunk c: as q4k_decode_chunk, with 16 x bit 2c (lo) / 2c + 1 (hi) of
+// qh[l] (bytes of h[0..7]) added to the codes (gguf-dequant.ts:283-314).
+__device__ __forceinline__ void q5k_decode_chunk(uint32_t hdr0, uint32_t s0, uint32_t s1,
+                                                 uint32_t s2, int c, const uint32_t q[8],
+                                                 const uint32_t h[8], float *lo, float *hi) {
+  const float d = h2f(hdr0), dmin = h2f(hdr0 >> 16);
+  uint32_t sc0, m0, sc1, m1;
+  q4k_scale_min(2 * c, s0, s1, s2, sc0, m0);
+  q4k_scale_min(2 * c + 1, s0, s1, s2, sc1, m1);
+  const float d1 = d * (float)sc0, min1 = dmin * (float)m0;
+  const float d2 = d * (float)sc1, min2 = dmin * (float)m1;
+#pragma unroll
+  for (int i = 0; i < 32; ++i) {
+    const uint32_t b = (q[i >> 2] >> (8 * (i & 3))) & 0xFFu;
+    const uint32_t hb = (h[i >> 2] >> (8 * (i & 3))) & 0xFFu;
+    lo[i] = d1 * (float)((b & 0x0Fu) | (((hb >> (2 * c)) & 1u) << 4)) - min1;
+    hi[i] = d2 * (float)((b >> 4) | (((hb >> (2 * c + 1)) & 1u) << 4)) - min2;
+  }
+}
+
 // Q6_K 6-bit value (unsigned, q + 32) of element (hf, t, l) from the ql byte
 // ql[64 hf + 32 (t & 1) + l] and the qh byte qh[32 hf + l] (gguf-dequant.ts:369-399).
 __device__ __forceinline__ int q6k_value(uint32_t qlb, uint32_t qhb, int t) {
@@ -142,7 +170,8 @@ __device__ __forceinline__ int q6k_value(uint32_t qlb, uint32_t qhb, int t) {
 // Dequantization of the row-tile layout: out[n * ldo + k], rows n < N.
 // ---------------------------------------------------------------------------
 
-// Q4_K: one thread per (row, unit, chunk c).
+// Q4_K / Q5_K: one thread per (row, unit, chunk c).
+template <int TYPE>
 __global__ __launch_bounds__(256) void dequant_q4_k_kernel(const uint8_t *__restrict__ tiles,
                                                            int64_t n_rows, int nu,
                                                            float *__restrict__ out, int64_t ldo) {
@@ -153,7 +182,7 @@ __global__ __launch_bounds__(256) void dequant_q4_k_kernel(const uint8_t *__rest
   const int64_t n = nuid / nu;
   const int u = (int)(nuid - n * nu);
   const int r = (int)(n & 15);
-  const uint8_t *tu = tiles + ((n >> 4) * nu + u) * (int64_t)Fmt<12>::TU;
+  const uint8_t *tu = tiles + ((n >> 4) * nu + u) * (int64_t)Fmt<TYPE>::TU;
   const uint4 hd = ldg16(tu + 16 * r);
   const int cp = c >> 1, h = c & 1;
   uint32_t q[8];
@@ -164,7 +193,18 @@ __global__ __launch_bounds__(256) void dequant_q4_k_kernel(const uint8_t *__rest
     q[2 * g + 1] = h ? p.w : p.y;
   }
   float lo[32], hi[32];
-  q4k_decode_chunk(hd.x, hd.y, hd.z, hd.w, c, q, lo, hi);
+  if constexpr (TYPE == 13) {
+    uint32_t h[8];
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const uint2 p = *(const uint2 *)(tu + 2304 + (16 * g + r) * 8);
+      h[2 * g] = p.x;
+      h[2 * g + 1] = p.y;
+    }
+    q5k_decode_chunk(hd.x, hd.y, hd.z, hd.w, c, q, h, lo, hi);
+  } else {
+    q4k_decode_chunk(hd.x, hd.y, hd.z, hd.w, c, q, lo, hi);
+  }
   float *o = out + n * ldo + 256 * (int64_t)u + 64 * c;
 #pragma unroll
   for (int i = 0; i < 32; ++i) {
@@ -241,11 +281,13 @@ __global__ __launch_bounds__(256) void dequant_q8_0_kernel(const uint8_t *__rest
 hipError_t launch_dequant(const uint8_t *tiles, int type, int64_t n_rows, int64_t k, float *out,
                           int64_t ldo, hipStream_t s) {
   const int nu = (int)(k / unit_elems(type));
-  const int parts = type == 12 ? 4 : (type == 14 ? 2 : 1);
+  const int parts = (type == 12 || type == 13) ? 4 : (type == 14 ? 2 : 1);
   const int64_t total = n_rows * nu * parts;
   const dim3 grid((unsigned)((total + 255) / 256)), block(256);
   if (type == 12)
-    hipLaunchKernelGGL(dequant_q4_k_kernel, grid, block, 0, s, tiles, n_rows, nu, out, ldo);
+    hipLaunchKernelGGL(dequant_q4_k_kernel<12>, grid, block, 0, s, tiles, n_rows, nu, out, ldo);
+  else if (type == 13)
+    hipLaunchKernelGGL(dequant_q4_k_kernel<13>, grid, block, 0, s, tiles, n_rows, nu, out, ldo);
   else if (type == 14)
     hipLaunchKernelGGL(dequant_q6_k_kernel, grid, block, 0, s, tiles, n_rows, nu, out, ldo);
   else
@@ -279,6 +321,23 @@ __device__ __forceinline__ void raw_piece_q4_k(const uint8_t *blk, int c, float 
   }
 }
 
+__device__ __forceinline__ void raw_piece_q5_k(const uint8_t *blk, int c, float *o) {
+  uint32_t q[8], h[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    q[i] = ld_u32_bytes(blk + 48 + 32 * c + 4 * i);
+    h[i] = ld_u32_bytes(blk + 16 + 4 * i);
+  }
+  float lo[32], hi[32];
+  q5k_decode_chunk(ld_u32_bytes(blk), ld_u32_bytes(blk + 4), ld_u32_bytes(blk + 8),
+                   ld_u32_bytes(blk + 12), c, q, h, lo, hi);
+#pragma unroll
+  for (int i = 0; i < 32; ++i) {
+    o[i] = lo[i];
+    o[32 + i] = hi[i];
+  }
+}
+
 __device__ __forceinline__ void raw_piece_q6_k(const uint8_t *blk, int hf, float *o) {
   const float d = h2f(ld_u16_bytes(blk + 208));
   const int8_t *sc = (const int8_t *)(blk + 192);
@@ -302,6 +361,11 @@ template <>
 struct RawPiece<12> {
   static constexpr int PER_UNIT = 4, VALUES = 64;
   __device__ static void run(const uint8_t *unit, int p, float *o) { raw_piece_q4_k(unit, p, o); }
+};
+template <>
+struct RawPiece<13> {
+  static constexpr int PER_UNIT = 4, VALUES = 64;
+  __device__ static void run(const uint8_t *unit, int p, float *o) { raw_piece_q5_k(unit, p, o); }
 };
 template <>
 struct RawPiece<14> {
@@ -358,6 +422,8 @@ hipError_t launch_dequant_raw(const uint8_t *raw, int type, int64_t n_elems, flo
     dequant_raw_type<8>(raw, n_elems, out, s);
   else if (type == 12)
     dequant_raw_type<12>(raw, n_elems, out, s);
+  else if (type == 13)
+    dequant_raw_type<13>(raw, n_elems, out, s);
   else
     dequant_raw_type<14>(raw, n_elems, out, s);
   return hipGetLastError();
@@ -379,6 +445,8 @@ hipError_t launch_get_rows(const uint8_t *raw, int type, int64_t n_rows, int64_t
     get_rows_type<8>(raw, n_rows, k, ids, n_ids, out, ldo, s);
   else if (type == 12)
     get_rows_type<12>(raw, n_rows, k, ids, n_ids, out, ldo, s);
+  else if (type == 13)
+    get_rows_type<13>(raw, n_rows, k, ids, n_ids, out, ldo, s);
   else
     get_rows_type<14>(raw, n_rows, k, ids, n_ids, out, ldo, s);
   return hipGetLastError();

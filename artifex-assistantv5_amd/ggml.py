@@ -43,6 +43,7 @@ F16 = GGML_TYPES["F16"]
 BF16 = GGML_TYPES["BF16"]
 Q8_0 = GGML_TYPES["Q8_0"]
 Q4_K = GGML_TYPES["Q4_K"]
+Q5_K = GGML_TYPES["Q5_K"]
 Q6_K = GGML_TYPES["Q6_K"]
 
 # gguf.ts:39-73 — [elements per block, bytes per block]
@@ -57,7 +58,7 @@ _TYPE_TRAITS = {
 }
 
 # Types the HIP kernels of this library decode.
-KERNEL_TYPES = (Q8_0, Q4_K, Q6_K)
+KERNEL_TYPES = (Q8_0, Q4_K, Q5_K, Q6_K)
 
 
 class GGMLTypeError(NotImplementedError):

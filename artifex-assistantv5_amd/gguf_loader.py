@@ -2,7 +2,7 @@
 
 Mirrors ``loadGGUFModel`` (``webgpu/src/model/gguf-loader.ts:166-460``):
 
-* quantized matrices of a type the HIP kernels decode (Q8_0 / Q4_K / Q6_K)
+* quantized matrices of a type the HIP kernels decode (Q8_0 / Q4_K / Q5_K / Q6_K)
   are copied to the device and repacked there into the row-tile layout
   (``repackGGUFForGPU``, ``gguf-loader.ts:422-424``) -> ``GGUFWeight``;
 * F32 tensors are uploaded as they are; F16 / BF16 tensors become f32 at load

@@ -12,6 +12,9 @@ split of Q6_K) with simpler scale searches:
 * Q4_K: per 32-element sub-block ``scale = (max - min(0, min)) / 15`` and
   ``min = -min(0, min)``; per superblock ``d = max scale / 63``,
   ``dmin = max min / 63`` (f16); 6-bit ``sc, m`` then 4-bit ``q``.
+* Q5_K: as Q4_K with ``/ 31`` and 5-bit ``q``: low nibble into ``qs`` as Q4_K
+  does, the fifth bit of sub-block j into bit j of ``qh[l]`` (element l of
+  the sub-block).
 * Q6_K: per 16-element sub-block ``scale = max|w| / 31``; ``d = max|scale| /
   127`` (f16); int8 ``sc`` then ``q - 32`` in [-32, 31].
 
@@ -22,7 +25,7 @@ from __future__ import annotations
 
 import numpy as np
 
-from .ggml import Q4_K, Q6_K, Q8_0
+from .ggml import Q4_K, Q5_K, Q6_K, Q8_0
 
 _CHUNK_ROWS = 4096
 
@@ -84,6 +87,39 @@ def _quantize_q8_0(w: np.ndarray) -> np.ndarray:
     return out.reshape(-1)
 
 
+def _k_scales(w: np.ndarray, levels: int):
+    """Per-sub-block scale / min codes of Q4_K / Q5_K and the integer codes q."""
+    sub = w.reshape(-1, 8, 32)
+    wmin = np.minimum(sub.min(axis=2), np.float32(0))
+    wmax = sub.max(axis=2)
+    scale = (wmax - wmin) / np.float32(levels)
+    mins = -wmin
+    d16 = _f16(scale.max(axis=1) / np.float32(63))
+    dmin16 = _f16(mins.max(axis=1) / np.float32(63))
+    d = d16.astype(np.float32)[:, None]
+    dmin = dmin16.astype(np.float32)[:, None]
+    sc = np.clip(np.rint(_safe_div(scale, d)), 0, 63).astype(np.uint8)
+    m = np.clip(np.rint(_safe_div(mins, dmin)), 0, 63).astype(np.uint8)
+    d1 = (d * sc)[:, :, None]
+    m1 = (dmin * m)[:, :, None]
+    q = np.clip(np.rint(_safe_div(sub + m1, d1)), 0, levels).astype(np.uint8)   # (nb, 8, 32)
+    return d16, dmin16, sc, m, q
+
+
+def _quantize_q5_k(w: np.ndarray) -> np.ndarray:
+    d16, dmin16, sc, m, q = _k_scales(w, 31)
+    nb = q.shape[0]
+    qs = (q[:, 0::2, :] & 0x0F) | ((q[:, 1::2, :] & 0x0F) << 4)          # (nb, 4, 32)
+    qh = ((q >> 4) << np.arange(8, dtype=np.uint8)[None, :, None]).sum(axis=1, dtype=np.uint8)
+    out = np.empty((nb, 176), np.uint8)
+    out[:, 0:2] = d16.view(np.uint8).reshape(-1, 2)
+    out[:, 2:4] = dmin16.view(np.uint8).reshape(-1, 2)
+    out[:, 4:16] = pack_q4_k_scales(sc, m)
+    out[:, 16:48] = qh
+    out[:, 48:176] = qs.reshape(nb, 128)
+    return out.reshape(-1)
+
+
 def _quantize_q4_k(w: np.ndarray) -> np.ndarray:
     sub = w.reshape(-1, 8, 32)
     nb = sub.shape[0]
@@ -128,7 +164,7 @@ def _quantize_q6_k(w: np.ndarray) -> np.ndarray:
 
 
 _QUANTIZERS = {Q8_0: (32, 34, _quantize_q8_0), Q4_K: (256, 144, _quantize_q4_k),
-               Q6_K: (256, 210, _quantize_q6_k)}
+               Q5_K: (256, 176, _quantize_q5_k), Q6_K: (256, 210, _quantize_q6_k)}
 
 
 def quantize(w: np.ndarray, ggml_type: int) -> np.ndarray:

@@ -45,7 +45,7 @@ sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0           # MI355X HBM3E, published
 FP16_PEAK_TFLOPS = 2500.0       # MI355X dense fp16 MFMA, published
-BLOCK = {8: (32, 34), 12: (256, 144), 14: (256, 210)}
+BLOCK = {8: (32, 34), 12: (256, 144), 13: (256, 176), 14: (256, 210)}
 
 
 def parse():
@@ -144,7 +144,7 @@ def make_pool(pkg, t, n, k, copies, seed, quantized=True):
         rawd = torch.randint(0, 256, (n * (k // block) * size,), dtype=torch.uint8, device="cuda",
                              generator=g)
         blocks = rawd.view(-1, size)
-        for o in {8: [0], 12: [0, 2], 14: [208]}[t]:
+        for o in {8: [0], 12: [0, 2], 13: [0, 2], 14: [208]}[t]:
             v = (torch.rand(blocks.shape[0], device="cuda", generator=g) * 0.003 + 0.0005).half()
             blocks[:, o:o + 2] = v.view(torch.uint8).view(-1, 2)
         base = pkg.repack_gguf_for_gpu(t, rawd, n, k)
@@ -286,6 +286,15 @@ def secondary_cases(pkg, args, pool, secondary):
         secondary["q8_0_decode_m1_gbs"] = round(r["gbs"], 1)
         secondary["q8_0_decode_m1_frac_hbm"] = round(r["gbs"] / HBM_PEAK_GBS, 4)
         del qpool
+    if want("q5k"):
+        q5pool, _ = make_pool(pkg, 13, 14336, 4096, 14, seed=6)
+        r = matmul_case(pkg, 13, 1, 14336, 4096, q5pool, 280, 10)
+        secondary["q5k_decode_m1_gbs"] = round(r["gbs"], 1)
+        secondary["q5k_decode_m1_frac_hbm"] = round(r["gbs"] / HBM_PEAK_GBS, 4)
+        r = matmul_case(pkg, 13, 2048, 14336, 4096, q5pool[:2], 10, 2, xdtype="float16")
+        secondary["q5k_gemm_m2048_n14336_tflops"] = round(r["tflops"], 1)
+        secondary["q5k_gemm_m2048_n14336_frac_fp16_peak"] = round(r["tflops"] / FP16_PEAK_TFLOPS, 4)
+        del q5pool
     if want("lm_head"):
         lpool, _ = make_pool(pkg, 14, 151936, 4096, 2, seed=5, quantized=False)
         r = matmul_case(pkg, 14, 1, 151936, 4096, lpool, 40, 3)

@@ -50,6 +50,7 @@ extern "C" {
 #define GGUF_HIP_F16 1
 #define GGUF_HIP_Q8_0 8
 #define GGUF_HIP_Q4_K 12
+#define GGUF_HIP_Q5_K 13
 #define GGUF_HIP_Q6_K 14
 
 /* Error codes.  The Python host maps them onto the reference's throws:

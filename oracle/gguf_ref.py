@@ -1,4 +1,4 @@
-"""CPU oracle for the GGUF Q8_0 / Q4_K / Q6_K dequant-matmul path.
+"""CPU oracle for the GGUF Q8_0 / Q4_K / Q5_K / Q6_K dequant-matmul path.
 
 TEST INFRASTRUCTURE ONLY.  This module is the checker: only ``tests/``,
 ``__graft_entry__.smoke()`` and the ``cpu_baseline`` leg of ``bench.py`` may
@@ -15,14 +15,14 @@ It restates the reference's CPU dequantization
 * the vectorised numpy functions compute in f32.  They are bit-identical to
   the loops because every product in these formats is exact in f32 (Q8_0
   ``d*q`` needs <= 18 significant bits, Q6_K ``d*sc*q`` <= 23, Q4_K
-  ``d*sc*q`` <= 21 and ``dmin*m`` <= 17) and the only rounding left is the
-  final Q4_K subtraction, which f32 and f64-then-f32 both round correctly
-  (the exact difference is a multiple of 2**-24 below 2**27, so it fits in
-  f64's 53 bits).
+  ``d*sc*q`` <= 21, Q5_K ``d*sc*q`` <= 22 and ``dmin*m`` <= 17) and the only
+  rounding left is the final Q4_K / Q5_K subtraction, which f32 and
+  f64-then-f32 both round correctly (the exact difference is a multiple of
+  2**-24 below 2**27, so it fits in f64's 53 bits).
 
 Parity pins (all in ``tests/test_oracle.py``):
 * the reference's gguf-py golden vectors (``webgpu/test-fixtures/gguf-*.json``
-  ``dequant_samples``: 1 Q8_0, 2 Q4_K, 3 Q6_K samples) — bit-exact;
+  ``dequant_samples``: 1 Q8_0, 2 Q4_K, 2 Q5_K, 3 Q6_K samples) — bit-exact;
 * exact rational arithmetic (``fractions.Fraction``) on random blocks;
 * an independently written encoder (the packing side of the 6-bit scale/min
   and the Q6_K ql/qh split, in the package quantizer) round-tripping through
@@ -37,7 +37,7 @@ import math
 
 import numpy as np
 
-T_F32, T_F16, T_Q8_0, T_Q4_K, T_Q6_K, T_BF16 = 0, 1, 8, 12, 14, 30
+T_F32, T_F16, T_Q8_0, T_Q4_K, T_Q5_K, T_Q6_K, T_BF16 = 0, 1, 8, 12, 13, 14, 30
 
 # ---------------------------------------------------------------------------
 # Literal restatement (pure Python, f64 arithmetic, f32 store)
@@ -114,6 +114,37 @@ def dequant_q4_k_loop(data: bytes, n: int) -> np.ndarray:
     return out
 
 
+def dequant_q5_k_loop(data: bytes, n: int) -> np.ndarray:
+    """gguf-dequant.ts:283-314."""
+    if n % 256 != 0:
+        raise ValueError(f"[Q5_K] n={n} not divisible by 256")
+    out = np.zeros(n, np.float32)
+    for b in range(n // 256):
+        base = b * 176
+        d = f16_to_f32(_u16(data, base))
+        dmin = f16_to_f32(_u16(data, base + 2))
+        scales_base, qh_base = base + 4, base + 16
+        y, ql, is_ = b * 256, base + 48, 0
+        u1, u2 = 1, 2
+        for _ in range(0, 256, 64):
+            sc1, m1 = get_scale_min_k4(is_ + 0, data, scales_base)
+            sc2, m2 = get_scale_min_k4(is_ + 1, data, scales_base)
+            d1, min1 = d * sc1, dmin * m1
+            d2, min2 = d * sc2, dmin * m2
+            for l in range(32):
+                out[y + l] = d1 * ((data[ql + l] & 0x0F)
+                                   + (16 if data[qh_base + l] & u1 else 0)) - min1
+            for l in range(32):
+                out[y + 32 + l] = d2 * ((data[ql + l] >> 4)
+                                        + (16 if data[qh_base + l] & u2 else 0)) - min2
+            y += 64
+            ql += 32
+            is_ += 2
+            u1 <<= 2
+            u2 <<= 2
+    return out
+
+
 def dequant_q6_k_loop(data: bytes, n: int) -> np.ndarray:
     """gguf-dequant.ts:369-399."""
     if n % 256 != 0:
@@ -155,6 +186,8 @@ def dequant_ggml_loop(ggml_type: int, data: bytes, n: int) -> np.ndarray:
         return dequant_q8_0_loop(data, n)
     if ggml_type == T_Q4_K:
         return dequant_q4_k_loop(data, n)
+    if ggml_type == T_Q5_K:
+        return dequant_q5_k_loop(data, n)
     if ggml_type == T_Q6_K:
         return dequant_q6_k_loop(data, n)
     raise NotImplementedError(f"[GGUF-dequant] No CPU reference for ggml type {ggml_type}")
@@ -166,8 +199,11 @@ def dequant_ggml_loop(ggml_type: int, data: bytes, n: int) -> np.ndarray:
 
 Q8_0_BLOCK = np.dtype([("d", "<f2"), ("qs", "i1", 32)])
 Q4_K_BLOCK = np.dtype([("d", "<f2"), ("dmin", "<f2"), ("scales", "u1", 12), ("qs", "u1", 128)])
+Q5_K_BLOCK = np.dtype([("d", "<f2"), ("dmin", "<f2"), ("scales", "u1", 12), ("qh", "u1", 32),
+                       ("qs", "u1", 128)])
 Q6_K_BLOCK = np.dtype([("ql", "u1", 128), ("qh", "u1", 64), ("sc", "i1", 16), ("d", "<f2")])
 assert Q8_0_BLOCK.itemsize == 34 and Q4_K_BLOCK.itemsize == 144 and Q6_K_BLOCK.itemsize == 210
+assert Q5_K_BLOCK.itemsize == 176
 
 
 def _blocks(data, dtype: np.dtype, n: int, block: int, name: str) -> np.ndarray:
@@ -211,6 +247,27 @@ def dequant_q4_k(data, n: int) -> np.ndarray:
     return (d1 * q.astype(np.float32) - m1).reshape(-1)
 
 
+def q5_k_values(blk: np.ndarray) -> np.ndarray:
+    """Unsigned 5-bit codes of Q5_K blocks in element order, shape (nb, 8, 32): sub-block
+    2c holds the low nibbles of qs[32c..32c+31] plus 16 x bit 2c of qh[l], sub-block
+    2c + 1 the high nibbles plus 16 x bit 2c + 1."""
+    nb = blk.shape[0]
+    qs = blk["qs"].reshape(nb, 4, 1, 32)
+    nib = np.concatenate([qs & 0x0F, qs >> 4], axis=2).reshape(nb, 8, 32)
+    bits = (blk["qh"][:, None, :] >> np.arange(8, dtype=np.uint8)[None, :, None]) & 1
+    return nib + (bits << 4)
+
+
+def dequant_q5_k(data, n: int) -> np.ndarray:
+    blk = _blocks(data, Q5_K_BLOCK, n, 256, "Q5_K")
+    d = blk["d"].astype(np.float32)[:, None]
+    dmin = blk["dmin"].astype(np.float32)[:, None]
+    sc, m = q4_k_scale_min(blk["scales"])
+    d1 = (d * sc.astype(np.float32))[:, :, None]        # exact
+    m1 = (dmin * m.astype(np.float32))[:, :, None]      # exact
+    return (d1 * q5_k_values(blk).astype(np.float32) - m1).reshape(-1)
+
+
 def q6_k_values(blk: np.ndarray) -> np.ndarray:
     """Signed 6-bit values (q - 32) of Q6_K blocks in element order, shape (nb, 256)."""
     nb = blk.shape[0]
@@ -241,6 +298,8 @@ def dequant_ggml(ggml_type: int, data, n: int) -> np.ndarray:
         return dequant_q8_0(data, n)
     if ggml_type == T_Q4_K:
         return dequant_q4_k(data, n)
+    if ggml_type == T_Q5_K:
+        return dequant_q5_k(data, n)
     if ggml_type == T_Q6_K:
         return dequant_q6_k(data, n)
     if ggml_type in (T_F32, T_F16, T_BF16):

@@ -63,7 +63,8 @@ def test_constants_match_header(native):
     assert d["GGUF_HIP_VARIANT_DECODE"] == native.VARIANT_DECODE
     assert d["GGUF_HIP_VARIANT_GEMM"] == native.VARIANT_GEMM
     assert d["GGUF_HIP_DECODE_MAX_M"] == native.DECODE_MAX_M
-    assert (d["GGUF_HIP_Q8_0"], d["GGUF_HIP_Q4_K"], d["GGUF_HIP_Q6_K"]) == (8, 12, 14)
+    assert (d["GGUF_HIP_Q8_0"], d["GGUF_HIP_Q4_K"], d["GGUF_HIP_Q5_K"],
+            d["GGUF_HIP_Q6_K"]) == (8, 12, 13, 14)
 
 
 def test_abi_version(lib):
@@ -79,12 +80,12 @@ def test_type_traits(lib, native):
 
 
 def test_byte_queries_agree_with_python(lib, pkg):
-    for t in (8, 12, 14):
+    for t in (8, 12, 13, 14):
         for k in (256, 512, 1024, 4096, 14336):
             assert lib.gguf_hip_tile_bytes(t, 7, k) == 16 * pkg.tile_row_bytes(t, k)
             assert lib.gguf_hip_tile_bytes(t, 33, k) == pkg.tiled_bytes(t, 33, k)
             assert lib.gguf_hip_raw_bytes(t, 7, k) == pkg.ggml_tensor_bytes(t, [k, 7])
-    assert lib.gguf_hip_tile_bytes(13, 1, 256) == -1   # Q5_K: known type, no kernel
+    assert lib.gguf_hip_tile_bytes(6, 1, 256) == -1    # Q5_0: known type, no kernel
     assert lib.gguf_hip_tile_bytes(8, 1, 48) == -2
 
 

@@ -10,6 +10,7 @@ pytestmark = pytest.mark.gpu
 
 SHAPES = {8: [(1, 32), (3, 96), (5, 4096), (2, 160)],
           12: [(1, 256), (4, 768), (3, 4096), (2, 14336)],
+          13: [(1, 256), (4, 768), (3, 4096), (2, 14336)],
           14: [(1, 256), (4, 768), (3, 4096), (2, 14336)]}
 
 
@@ -20,7 +21,7 @@ def _dev_u8(a):
 def test_golden_vectors_on_gpu(pkg, ref, golden_samples):
     for s in golden_samples:
         t = s["ggml_type"]
-        if t not in (8, 12, 14):
+        if t not in (8, 12, 13, 14):
             continue
         raw = np.frombuffer(bytes.fromhex(s["bytes_hex"]), np.uint8)
         want = np.array(s["expected_f32"], np.float64).astype(np.float32)
@@ -32,7 +33,7 @@ def test_golden_vectors_on_gpu(pkg, ref, golden_samples):
         assert ref.same_bits(got_raw, want), (s["tensor"], "raw")
 
 
-@pytest.mark.parametrize("t", [8, 12, 14])
+@pytest.mark.parametrize("t", [8, 12, 13, 14])
 @pytest.mark.parametrize("specials", [False, True])
 def test_repack_layout_and_dequant_bit_exact(pkg, ref, t, specials):
     for i, (n, k) in enumerate(SHAPES[t]):
@@ -45,7 +46,7 @@ def test_repack_layout_and_dequant_bit_exact(pkg, ref, t, specials):
         assert ref.same_bits(pkg.dequant_raw(t, raw, n * k).cpu().numpy(), want.reshape(-1))
 
 
-@pytest.mark.parametrize("t", [8, 12, 14])
+@pytest.mark.parametrize("t", [8, 12, 13, 14])
 def test_repack_from_unaligned_raw(pkg, ref, t):
     n, k = 3, 512
     raw = tile_model.random_blocks(t, n, k, seed=77)
@@ -58,7 +59,7 @@ def test_repack_from_unaligned_raw(pkg, ref, t):
                          ref.dequant_rows(t, raw, n, k).reshape(-1))
 
 
-@pytest.mark.parametrize("t", [8, 12, 14])
+@pytest.mark.parametrize("t", [8, 12, 13, 14])
 def test_row_views_and_concat(pkg, ref, t):
     k = 512
     raw = tile_model.random_blocks(t, 40, k, seed=5)
@@ -84,7 +85,7 @@ def test_full_size_dequant(pkg, ref, t, n, k):
     raw_dev = torch.randint(0, 256, (n * rows_bytes,), dtype=torch.uint8, device="cuda")
     # stamp finite scales into every block on the device
     blocks = raw_dev.view(-1, size)
-    offs = {8: [0], 12: [0, 2], 14: [208]}[t]
+    offs = {8: [0], 12: [0, 2], 13: [0, 2], 14: [208]}[t]
     for o in offs:
         vals = torch.empty(blocks.shape[0], device="cuda").uniform_(0.001, 0.01).half()
         blocks[:, o:o + 2] = vals.view(torch.uint8).view(-1, 2)

@@ -15,8 +15,9 @@ from fractions import Fraction
 import numpy as np
 import pytest
 
-IN_SCOPE = (8, 12, 14)
-BLOCK = {8: (32, 34), 12: (256, 144), 14: (256, 210)}
+IN_SCOPE = (8, 12, 13, 14)
+BLOCK = {8: (32, 34), 12: (256, 144), 13: (256, 176), 14: (256, 210)}
+F16_FIELDS = {8: [0], 12: [0, 2], 13: [0, 2], 14: [208]}
 
 
 def _samples(golden_samples, types=IN_SCOPE):
@@ -25,7 +26,7 @@ def _samples(golden_samples, types=IN_SCOPE):
 
 def test_golden_covers_all_types(golden_samples):
     kinds = sorted(s["ggml_type"] for s in _samples(golden_samples))
-    assert kinds == [8, 12, 12, 14, 14, 14]
+    assert kinds == [8, 12, 12, 13, 13, 14, 14, 14]
 
 
 @pytest.mark.parametrize("loop", [False, True])
@@ -97,6 +98,27 @@ def exact_q4_k(raw: bytes) -> list:
     return out
 
 
+def exact_q5_k(raw: bytes) -> list:
+    out = []
+    for b in range(len(raw) // 176):
+        blk = raw[176 * b:176 * (b + 1)]
+        d = f16_fraction(blk[0] | blk[1] << 8)
+        dmin = f16_fraction(blk[2] | blk[3] << 8)
+        sc, qh, q = blk[4:16], blk[16:48], blk[48:]
+        for e in range(256):
+            j, l = divmod(e, 32)               # sub-block j, element l
+            c, hi = divmod(j, 2)               # 64-element chunk c, nibble
+            if j < 4:
+                s, m = sc[j] % 64, sc[j + 4] % 64
+            else:
+                s = sc[j + 4] % 16 + 16 * (sc[j - 4] // 64)
+                m = sc[j + 4] // 16 + 16 * (sc[j] // 64)
+            nib = q[32 * c + l] // 16 if hi else q[32 * c + l] % 16
+            fifth = (qh[l] >> j) % 2           # bit j of qh[l] is the fifth bit of sub-block j
+            out.append(round_f32(d * s * (nib + 16 * fifth) - dmin * m))
+    return out
+
+
 def exact_q6_k(raw: bytes) -> list:
     out = []
     for b in range(len(raw) // 210):
@@ -134,13 +156,14 @@ def _random_blocks(t: int, nblocks: int, seed: int) -> bytes:
     raw = bytearray(rng.randrange(256) for _ in range(nblocks * size))
     for b in range(nblocks):
         base = b * size
-        offs = {8: [0], 12: [0, 2], 14: [208]}[t]
+        offs = F16_FIELDS[t]
         for o in offs:
             struct.pack_into("<H", raw, base + o, random_finite_f16(rng))
     return bytes(raw)
 
 
-@pytest.mark.parametrize("t,exact", [(8, exact_q8_0), (12, exact_q4_k), (14, exact_q6_k)])
+@pytest.mark.parametrize("t,exact", [(8, exact_q8_0), (12, exact_q4_k), (13, exact_q5_k),
+                                     (14, exact_q6_k)])
 def test_exact_rational(ref, t, exact):
     raw = _random_blocks(t, 12, seed=t)
     n = 12 * BLOCK[t][0]
@@ -167,7 +190,7 @@ def test_loop_equals_vectorised_with_special_values(ref, t):
     raw = bytearray(rng.randrange(256) for _ in range(nb * size))
     for b in range(nb):
         h = SPECIAL_F16[b % len(SPECIAL_F16)]
-        for o in {8: [0], 12: [0, 2], 14: [208]}[t]:
+        for o in F16_FIELDS[t]:
             struct.pack_into("<H", raw, b * size + o, h if (b // len(SPECIAL_F16)) != 1 or o == 0 else
                              SPECIAL_F16[(b + 5) % len(SPECIAL_F16)])
     raw = bytes(raw)
@@ -243,6 +266,16 @@ def test_q6_k_pack_roundtrip(ref, pkg):
     assert np.array_equal(ref.q6_k_values(blk) + 32, q)
 
 
+def test_q5_k_pack_roundtrip(ref, pkg):
+    w = pkg.quantize.synthetic_weight(6, 512, seed=9)
+    d16, dmin16, sc, m, q = pkg.quantize._k_scales(w, 31)
+    assert q.max() > 15                                  # the fifth bit is exercised
+    blk = pkg.quantize.quantize(w, 13).view(ref.Q5_K_BLOCK)
+    assert np.array_equal(ref.q5_k_values(blk), q)
+    dsc, dm = ref.q4_k_scale_min(blk["scales"])
+    assert np.array_equal(dsc, sc) and np.array_equal(dm, m)
+
+
 @pytest.mark.parametrize("t", IN_SCOPE)
 def test_quantizer_error_is_bounded(ref, pkg, t):
     w = pkg.quantize.synthetic_weight(4, 512, seed=3)
@@ -250,7 +283,7 @@ def test_quantizer_error_is_bounded(ref, pkg, t):
     assert raw.size == 4 * 512 // BLOCK[t][0] * BLOCK[t][1]
     deq = ref.dequant_rows(t, raw, 4, 512)
     rel = np.linalg.norm(deq - w) / np.linalg.norm(w)
-    assert rel < {8: 0.01, 12: 0.12, 14: 0.05}[t]
+    assert rel < {8: 0.01, 12: 0.12, 13: 0.06, 14: 0.05}[t]
 
 
 # ---------------------------------------------------------------------------
@@ -344,6 +377,24 @@ def test_mutations_are_caught(ref, golden_samples):
         d = blk["d"].astype(np.float32)[:, None]
         return (d * blk["qs"].view(np.uint8).astype(np.float32)).reshape(-1)
 
+    def q5_qh_bit_by_chunk(raw, n):   # fifth bit taken from bit c of qh, not bit 2c + hi
+        blk = ref._blocks(raw, ref.Q5_K_BLOCK, n, 256, "Q5_K")
+        d = blk["d"].astype(np.float32)[:, None, None]
+        dmin = blk["dmin"].astype(np.float32)[:, None, None]
+        sc, m = ref.q4_k_scale_min(blk["scales"])
+        qs = blk["qs"].reshape(-1, 4, 1, 32)
+        nib = np.concatenate([qs & 15, qs >> 4], axis=2).reshape(-1, 8, 32)
+        bit = (blk["qh"][:, None, :] >> (np.arange(8) // 2)[None, :, None].astype(np.uint8)) & 1
+        q = (nib + (bit << 4)).astype(np.float32)
+        return (d * sc[:, :, None] * q - dmin * m[:, :, None]).reshape(-1).astype(np.float32)
+
+    def q5_no_fifth_bit(raw, n):
+        blk = ref._blocks(raw, ref.Q5_K_BLOCK, n, 256, "Q5_K").copy()
+        blk["qh"] = 0
+        return ref.dequant_q5_k(blk.view(np.uint8), n)
+
+    assert _golden_fails(ref, golden_samples, 13, q5_qh_bit_by_chunk)
+    assert _golden_fails(ref, golden_samples, 13, q5_no_fifth_bit)
     assert _golden_fails(ref, golden_samples, 12, q4_no_min)
     assert _golden_fails(ref, golden_samples, 12, q4_swapped_nibbles)
     assert _golden_fails(ref, golden_samples, 14, q6_wrong_qh_shift)

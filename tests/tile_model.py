@@ -6,6 +6,8 @@ block) a tile stores the 16 rows' GGUF blocks interleaved:
 
 * Q4_K: [header of row r at 16 r] then piece (cp, g, r) at 256 + ((4 cp + g) 16 + r) 16
   = qs[64 cp + 8 g, +8) | qs[64 cp + 32 + 8 g, +8)
+* Q5_K: as Q4_K (qs from byte 48 of the block), then piece (g, r) at 2304 + (16 g + r) 8
+  = qh[8 g, +8)
 * Q6_K: piece (v, g, r) at ((4 v + g) 16 + r) 16 = the lane's quant dwords 4v..4v+3,
   dword 3i = ql[64 hf + 16 lh + 4 g, +4), 3i+1 = ql[64 hf + 32 + 16 lh + 4 g, +4),
   3i+2 = qh[32 hf + 16 lh + 4 g, +4) for i = 2 hf + lh; scales at 3072 + 16 r; d at 3328 + 2 r
@@ -14,7 +16,7 @@ block) a tile stores the 16 rows' GGUF blocks interleaved:
 
 import numpy as np
 
-BLOCK = {8: (32, 34), 12: (256, 144), 14: (256, 210)}
+BLOCK = {8: (32, 34), 12: (256, 144), 13: (256, 176), 14: (256, 210)}
 
 
 def tile_row_bytes(t, k):
@@ -36,13 +38,17 @@ def _unit_maps(t):
     block, ub = BLOCK[t]
     pos = np.zeros((16, ub), np.int64)
     for r in range(16):
-        if t == 12:
+        if t in (12, 13):
+            qs = 16 if t == 12 else 48
             pos[r, 0:16] = 16 * r + np.arange(16)
             for cp in range(2):
                 for g in range(4):
                     base = 256 + ((4 * cp + g) * 16 + r) * 16
-                    pos[r, 16 + 64 * cp + 8 * g + np.arange(8)] = base + np.arange(8)
-                    pos[r, 16 + 64 * cp + 32 + 8 * g + np.arange(8)] = base + 8 + np.arange(8)
+                    pos[r, qs + 64 * cp + 8 * g + np.arange(8)] = base + np.arange(8)
+                    pos[r, qs + 64 * cp + 32 + 8 * g + np.arange(8)] = base + 8 + np.arange(8)
+            if t == 13:
+                for g in range(4):
+                    pos[r, 16 + 8 * g + np.arange(8)] = 2304 + (16 * g + r) * 8 + np.arange(8)
         elif t == 14:
             for g in range(4):
                 for i in range(4):
@@ -97,9 +103,10 @@ def random_blocks(t, n, k, seed, specials=False):
     block, size = BLOCK[t]
     nb = n * (k // block)
     raw = rng.integers(0, 256, (nb, size), dtype=np.uint8)
-    offs = {8: [0], 12: [0, 2], 14: [208]}[t]
+    offs = {8: [0], 12: [0, 2], 13: [0, 2], 14: [208]}[t]
     for o in offs:
-        vals = (rng.uniform(-0.01, 0.01, nb) if t != 12 or o == 0 else rng.uniform(0, 0.005, nb))
+        vals = (rng.uniform(-0.01, 0.01, nb) if t not in (12, 13) or o == 0
+                else rng.uniform(0, 0.005, nb))
         h = vals.astype(np.float16)
         if specials:
             pick = rng.random(nb)
