@@ -24,7 +24,7 @@ from .ggml import (GGML_TYPES, GGMLTypeError, ggml_tensor_bytes, ggml_type_trait
                    raw_row_bytes, tile_row_bytes, tiled_bytes)
 from .linear import (GGUFWeight, LayerWeights, QuantEmbedding, concat_rows,  # noqa: F401
                      dequant_ggml, dequant_raw, dispatch_matmul_gguf, dispatch_projection,
-                     qlinear, repack_gguf_for_gpu)
+                     interleave_tiles, qlinear, repack_gguf_for_gpu, split_interleaved)
 from .gguf_file import parse_gguf, parse_gguf_path, write_gguf  # noqa: F401
 from .gguf_loader import load_gguf_model  # noqa: F401
 from .gguf_model import load_decoder  # noqa: F401
@@ -34,7 +34,7 @@ __all__ = [
     "GGML_TYPES", "GGMLTypeError", "GGUFHipError", "GGUFWeight", "LayerWeights",
     "QuantEmbedding", "load_decoder", "load_gguf_model", "parse_gguf", "parse_gguf_path",
     "write_gguf",
-    "concat_rows", "dequant_ggml", "dequant_raw", "dispatch_matmul_gguf",
+    "concat_rows", "interleave_tiles", "split_interleaved", "dequant_ggml", "dequant_raw", "dispatch_matmul_gguf",
     "dispatch_projection", "ggml_tensor_bytes", "ggml_type_traits", "load_library",
     "qlinear", "raw_row_bytes", "repack_gguf_for_gpu", "tile_row_bytes", "tiled_bytes",
 ]

@@ -17,11 +17,12 @@ from .ggml import GGMLTypeError
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libgguf_hip.so")
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 ERR_TYPE, ERR_SHAPE, ERR_NULL, ERR_ALIGN, ERR_DTYPE, ERR_BYTES, ERR_HIP = -1, -2, -3, -4, -5, -6, -7
 VARIANT_AUTO, VARIANT_DECODE, VARIANT_GEMM = 0, 1, 2
 PROLOGUE_NONE, PROLOGUE_RMSNORM, PROLOGUE_SWIGLU = 0, 1, 2
+EPILOGUE_STORE, EPILOGUE_ACCUMULATE, EPILOGUE_SWIGLU = 0, 1, 2
 DECODE_MAX_M = 32
 
 # Every symbol include/gguf_hip.h declares: name -> (restype, argtypes)

@@ -323,13 +323,17 @@ int gguf_hip_argmax(const float *x, int64_t n, int64_t *out, void *work, void *s
 }
 
 int gguf_hip_matmul_fused(const float *x, const void *tiles, int ggml_type, int64_t n, int64_t k,
-                          float *y, int prologue, const float *norm_w, float eps, int accumulate,
+                          float *y, int prologue, const float *norm_w, float eps, int epilogue,
                           void *stream) {
   int rc = check_type(ggml_type);
   if (rc) return rc;
   if ((rc = check_k(ggml_type, k))) return rc;
   if (prologue < GGUF_HIP_PROLOGUE_NONE || prologue > GGUF_HIP_PROLOGUE_SWIGLU)
     return fail(GGUF_HIP_ERR_SHAPE, "[gguf-hip] unknown prologue %d", prologue);
+  if (epilogue < GGUF_HIP_EPILOGUE_STORE || epilogue > GGUF_HIP_EPILOGUE_SWIGLU)
+    return fail(GGUF_HIP_ERR_SHAPE, "[gguf-hip] unknown epilogue %d", epilogue);
+  if (epilogue == GGUF_HIP_EPILOGUE_SWIGLU && n % 32)
+    return fail(GGUF_HIP_ERR_SHAPE, "[gguf-hip] SwiGLU epilogue: N %% 32 != 0");
   if (n < 0 || n > ((int64_t)1 << 30)) return fail(GGUF_HIP_ERR_SHAPE, "[gguf-hip] bad N");
   if (k > 16384)
     return fail(GGUF_HIP_ERR_SHAPE, "[gguf-hip] fused matmul: K=%lld above 16384", (long long)k);
@@ -343,7 +347,7 @@ int gguf_hip_matmul_fused(const float *x, const void *tiles, int ggml_type, int6
       (norm_w && prologue == GGUF_HIP_PROLOGUE_RMSNORM && !aligned(norm_w, 16)))
     return fail(GGUF_HIP_ERR_ALIGN, "[gguf-hip] fused matmul buffers misaligned");
   const hipError_t e = gguf::launch_decode_fused(x, (const uint8_t *)tiles, ggml_type, n, k, y,
-                                                 prologue, norm_w, eps, accumulate ? 1 : 0,
+                                                 prologue, norm_w, eps, epilogue,
                                                  (hipStream_t)stream);
   if (e == hipErrorNotSupported)
     return fail(GGUF_HIP_ERR_SHAPE, "[gguf-hip] no fused kernel for N=%lld K=%lld type %d",

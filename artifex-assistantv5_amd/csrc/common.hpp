@@ -174,7 +174,7 @@ hipError_t launch_gemm(const void *x, int x_type, int64_t ldx, const uint8_t *ti
                        int64_t n, int64_t k, float *y, int64_t ldy, int64_t m, hipStream_t s);
 hipError_t launch_decode_fused(const float *x, const uint8_t *tiles, int type, int64_t n,
                                int64_t k, float *y, int prologue, const float *pw, float eps,
-                               int accumulate, hipStream_t s);
+                               int epilogue, hipStream_t s);
 hipError_t launch_rmsnorm(float *x, const float *r, const float *w, float eps, float *y,
                           int64_t rows, int64_t n, hipStream_t s);
 hipError_t launch_swiglu(const float *gu, float *out, int64_t rows, int64_t ffn, hipStream_t s);

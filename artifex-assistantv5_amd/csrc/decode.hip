@@ -214,6 +214,7 @@ __device__ __forceinline__ void apply(float (&acc)[4], const float4_t &D, float 
 
 // Shared-memory view of one staged chunk of activations.
 constexpr int kZeroHalves = 256;  // covers every immediate offset added to a selected address
+constexpr size_t kMaxLds = 160 * 1024;  // LDS a gfx950 workgroup may use
 
 // ---------------------------------------------------------------------------
 // Single activation row (M = 1).  The 16 A rows of the MFMA are then free to
@@ -527,8 +528,13 @@ __device__ __forceinline__ void store_item(int per_row, int total, int q, const 
 #pragma unroll
   for (int i = 0; i < kItem; ++i) {
     const int pos = (i & ~3) | ((i & 1) << 1) | ((i >> 1) & 1);  // swap 1 <-> 2 in each quad
-    const half_t h = (half_t)v[i];
-    const half_t l = (half_t)(v[i] - (float)h);
+    // Split the f32 value itself: when the compiler folds the multiply that
+    // produced it into the f16 conversions (v_fma_mix), the RMSNorm prologue
+    // measured ~15x the error of the plain kernel on the same products.
+    float vi = v[i];
+    asm volatile("" : "+v"(vi));
+    const half_t h = (half_t)vi;
+    const half_t l = (half_t)(vi - (float)h);
     hi[pos >> 3][pos & 7] = h;
     lo[pos >> 3][pos & 7] = l;
     s += (float)h + (PARTS == 2 ? (float)l : 0.f);
@@ -743,20 +749,29 @@ hipError_t launch_t(const XT *x, int64_t ldx, const uint8_t *W, int N, int K, fl
 // bytes), staged once for all of K, and each unit is consumed as it arrives.
 //
 // Fused variants for a decoder step (PRO, f32 activations only):
-//   PRO = 1  x is replaced by rmsnorm(x) * w before staging (the input norm of
-//            the projection, rmsnorm.wgsl:58-67); every workgroup reduces the
-//            whole row itself, so no extra launch or buffer is needed;
+//   PRO = 1  the input norm of the projection, rmsnorm(x) * w
+//            (rmsnorm.wgsl:58-67).  The scale r = 1 / rms(x) is common to the
+//            whole row, so W (x * w * r) = r (W (x * w)): x * w is staged at
+//            once, every thread publishes its partial sum of x^2 with the
+//            staging barrier that exists anyway, and the sum is reduced and
+//            applied only to the final sums.  No extra launch, buffer or
+//            barrier, and nothing ahead of the staging writes;
 //   PRO = 2  x is a row [gate (K) | up (K)] and is replaced by up * silu(gate)
 //            (elementwise.wgsl:96-102);
-// and `accumulate` adds the result to y instead of storing it (the residual
-// add that follows the output and down projections).
+// and the epilogue `epi`:
+//   0  y = result;
+//   1  y += result (the residual add after the output and down projections);
+//   2  SwiGLU over tile pairs: the weight holds gate and up row tiles
+//      interleaved (tile 2m = gate rows 16m..16m+15, tile 2m + 1 = the same up
+//      rows), and y[16 m + r] = up * silu(gate) (N / 2 outputs), so the FFN
+//      activation never takes a separate pass.
 // ---------------------------------------------------------------------------
 template <int TYPE, typename XT, int U, int XI, int PRO>
 __global__ __launch_bounds__(512) void decode_m1_kernel(const XT *__restrict__ x,
                                                         const uint8_t *__restrict__ W, int N,
                                                         int K, float *__restrict__ y, int ks_n,
                                                         const float *__restrict__ pw, float eps,
-                                                        int accumulate) {
+                                                        int epi) {
   constexpr int PARTS = sizeof(XT) == 4 ? 2 : 1;
   constexpr int UE = Fmt<TYPE>::UE, TU = Fmt<TYPE>::TU, GS = Dec<TYPE>::GS;
   const int nthr = blockDim.x;
@@ -779,6 +794,7 @@ __global__ __launch_bounds__(512) void decode_m1_kernel(const XT *__restrict__ x
   const int red_off = st.xs + K / GS;  // floats: [waves][64]
   st.zero = 2 * (red_off + (nthr >> 6) * 64);
   float *red = (float *)g_lds + red_off;
+  float *ssq = (float *)g_lds + st.zero / 2 + kZeroHalves / 2;  // [threads] partial sums of x^2
   if (threadIdx.x < kZeroHalves / 2) ((uint32_t *)((half_t *)g_lds + st.zero))[threadIdx.x] = 0u;
 
   // activations first: item q = threadIdx.x + nthr * i of the K / 16 items
@@ -808,23 +824,16 @@ __global__ __launch_bounds__(512) void decode_m1_kernel(const XT *__restrict__ x
     load_unit(wrs, uc * TU, r, g, buf[j]);
   }
 
-  if constexpr (PRO == 1) {  // 1 / rms over the whole row, reduced by this workgroup
+  if constexpr (PRO == 1) {  // stage x * w; the row's sum of x^2 rides on the staging barrier
     float ss = 0.f;
 #pragma unroll
     for (int i = 0; i < XI; ++i)
 #pragma unroll
-      for (int e = 0; e < kItem; ++e) ss += xv[i][e] * xv[i][e];
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o);
-    if (lane == 0) red[wave] = ss;
-    __syncthreads();
-    float tot = 0.f;
-    for (int w = 0; w < (nthr >> 6); ++w) tot += red[w];
-    const float inv = 1.0f / sqrtf(tot / (float)K + eps);
-#pragma unroll
-    for (int i = 0; i < XI; ++i)
-#pragma unroll
-      for (int e = 0; e < kItem; ++e) xv[i][e] = xv[i][e] * inv * pv[i][e];
+      for (int e = 0; e < kItem; ++e) {
+        ss += xv[i][e] * xv[i][e];
+        xv[i][e] *= pv[i][e];
+      }
+    ssq[threadIdx.x] = ss;
   }
   if constexpr (PRO == 2) {
 #pragma unroll
@@ -839,6 +848,9 @@ __global__ __launch_bounds__(512) void decode_m1_kernel(const XT *__restrict__ x
   for (int i = 0; i < XI; ++i)
     store_item<PARTS, GS>(per_row, per_row, (int)threadIdx.x + nthr * i, xv[i], st);
   __syncthreads();
+  float ssp = 0.f;  // this lane's share of the row's sum of x^2 (reduced after the units)
+  if constexpr (PRO == 1)
+    for (int t = lane; t < nthr; t += 64) ssp += ssq[t];
 
   float acc = 0.f;
 #pragma unroll
@@ -851,19 +863,45 @@ __global__ __launch_bounds__(512) void decode_m1_kernel(const XT *__restrict__ x
   }
   acc += __shfl_xor(acc, 16);  // the four lane groups of each row
   acc += __shfl_xor(acc, 32);
+  float scale = 1.0f;
+  if constexpr (PRO == 1) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) ssp += __shfl_xor(ssp, o);
+    scale = 1.0f / sqrtf(ssp / (float)K + eps);
+  }
 
   const int n = 16 * tile + r;
   if (ks_n > 1) {  // fixed-order sum of the ks_n partial sums of each tile
     red[wave * 64 + lane] = acc;
     __syncthreads();
-    if (ks != 0) return;
-    for (int j = 1; j < ks_n; ++j) acc += red[(wave + j) * 64 + lane];
+    if (ks == 0)
+      for (int j = 1; j < ks_n; ++j) acc += red[(wave + j) * 64 + lane];
   }
-  if (active && n < N && g == 0) y[n] = accumulate ? y[n] + acc : acc;
+  acc *= scale;
+  if (epi == 2) {  // every wave reaches both barriers
+    __syncthreads();  // the partial sums above are read
+    if (ks == 0 && (ts & 1) && g == 0) red[(ts >> 1) * 16 + r] = acc;  // up rows
+    __syncthreads();
+    if (ks == 0 && !(ts & 1) && g == 0 && active && n < N) {
+      const float up = red[(ts >> 1) * 16 + r];
+      y[16 * (tile >> 1) + r] = up * (acc / (1.0f + expf(-acc)));
+    }
+    return;
+  }
+  if (ks == 0 && active && n < N && g == 0) y[n] = epi == 1 ? y[n] + acc : acc;
 }
 
 // Units per wave held in registers: with K <= 4096 the staged activations
 // take one item per thread; longer K (or a fused prologue) leaves less room.
+#ifndef GGUF_M1_PRO_TIGHT
+#define GGUF_M1_PRO_TIGHT 1  // a fused prologue takes the tight unit budget
+#endif
+#ifndef GGUF_M1_NW_MIN
+#define GGUF_M1_NW_MIN 4     // waves per workgroup, at least
+#endif
+#ifndef GGUF_M1_MIN_WAVES
+#define GGUF_M1_MIN_WAVES 1024  // K split until the grid has this many waves
+#endif
 template <int TYPE>
 constexpr int m1_umax(bool tight) {
   return TYPE == 8 ? (tight ? 16 : 32) : (TYPE == 14 || TYPE == 13 || tight ? 8 : 16);
@@ -873,33 +911,48 @@ constexpr int m1_umax(bool tight) {
 // one-shot staging (16384) or the units per wave exceed the register budget.
 template <int TYPE, typename XT, int PRO>
 hipError_t launch_m1(const XT *x, const uint8_t *W, int N, int K, float *y, const float *pw,
-                     float eps, int accumulate, hipStream_t s) {
+                     float eps, int epi, hipStream_t s) {
   constexpr int UE = Fmt<TYPE>::UE, GS = Dec<TYPE>::GS;
   constexpr int PARTS = sizeof(XT) == 4 ? 2 : 1;
   const int ntiles = (N + 15) / 16, nu = K / UE;
   if (K > 16384) return hipErrorNotSupported;
   const bool long_k = K > 4096;
-  const int umax = m1_umax<TYPE>(long_k || PRO != 0);
-  // K split: units per wave within the budget, and at least ~1024 waves when possible
+  const int umax = m1_umax<TYPE>(long_k || (PRO != 0 && GGUF_M1_PRO_TIGHT));
+  // K split: units per wave within the budget, and at least ~1024 waves when
+  // possible (at most 4 with the SwiGLU epilogue, which needs two tiles per workgroup)
   int ks = 1;
-  while (ks < 8 && ks < nu && ((nu + ks - 1) / ks > umax || ntiles * ks < 1024)) ks <<= 1;
+  const int ks_max = epi == 2 ? 4 : 8;
+  while (ks < ks_max && ks < nu &&
+         ((nu + ks - 1) / ks > umax || ntiles * ks < GGUF_M1_MIN_WAVES))
+    ks <<= 1;
   const int per = (nu + ks - 1) / ks;
   if (per > umax) return hipErrorNotSupported;
-  const int nw = (long_k || ks > 4) ? 8 : 4, nthr = 64 * nw, ts = nw / ks;
+  int nw = (long_k || ks > 4 || GGUF_M1_NW_MIN > 4) ? 8 : 4;
+  if (epi == 2 && nw / ks < 2) nw = 8;  // the SwiGLU epilogue pairs tiles 2m, 2m + 1
+  const int nthr = 64 * nw, ts = nw / ks;
+  if (epi == 2 && (ts < 2 || (ntiles & 1))) return hipErrorNotSupported;
   const int xi = (K / kItem + nthr - 1) / nthr;  // 1 or 2
   const size_t lds = (size_t)(K + kXPad) * 2 * PARTS + (size_t)(K / GS) * 4 +
-                     (size_t)nw * 64 * 4 + kZeroHalves * 2;
-  if (lds > 65536) return hipErrorNotSupported;
+                     (size_t)nw * 64 * 4 + kZeroHalves * 2 + (size_t)nthr * 4;
+  if (lds > kMaxLds) return hipErrorNotSupported;
   const dim3 grid((unsigned)((ntiles + ts - 1) / ts)), block(nthr);
-  // template U is clamped to the compile-time budget (runtime per <= umax already)
+  // template U is clamped to the compile-time budget (runtime per <= umax already);
+  // above 64 KB of dynamic LDS the kernel's limit is raised first (gfx950: 160 KB)
 #define GGUF_M1(UU, XX)                                                                          \
-  hipLaunchKernelGGL(                                                                            \
-      (decode_m1_kernel<TYPE, XT,                                                                \
-                        ((UU) < m1_umax<TYPE>((XX) > 1 || PRO != 0)                              \
-                             ? (UU)                                                              \
-                             : m1_umax<TYPE>((XX) > 1 || PRO != 0)),                             \
-                        XX, PRO>),                                                               \
-      grid, block, lds, s, x, W, N, K, y, ks, pw, eps, accumulate)
+  do {                                                                                           \
+    auto kern = decode_m1_kernel<TYPE, XT,                                                       \
+                                 ((UU) < m1_umax<TYPE>((XX) > 1 || (PRO != 0 && GGUF_M1_PRO_TIGHT)) \
+                                      ? (UU)                                                     \
+                                      : m1_umax<TYPE>((XX) > 1 || (PRO != 0 && GGUF_M1_PRO_TIGHT))), \
+                                 XX, PRO>;                                                       \
+    if (lds > 65536) {                                                                           \
+      const hipError_t ea = hipFuncSetAttribute((const void *)kern,                              \
+                                                hipFuncAttributeMaxDynamicSharedMemorySize,      \
+                                                (int)lds);                                       \
+      if (ea != hipSuccess) return ea;                                                           \
+    }                                                                                            \
+    hipLaunchKernelGGL(kern, grid, block, lds, s, x, W, N, K, y, ks, pw, eps, epi);              \
+  } while (0)
   if (xi <= 1) {
     if (per <= 4) GGUF_M1(4, 1);
     else if (per <= 8) GGUF_M1(8, 1);
@@ -937,18 +990,18 @@ hipError_t launch_x(const XT *x, int64_t ldx, const uint8_t *W, int type, int N,
 
 }  // namespace
 
-// One f32 activation row with a fused prologue / accumulate epilogue
-// (decode_m1_kernel).  hipErrorNotSupported: no fused kernel for this shape.
+// One f32 activation row with a fused prologue / epilogue (decode_m1_kernel).
+// hipErrorNotSupported: no fused kernel for this shape.
 hipError_t launch_decode_fused(const float *x, const uint8_t *tiles, int type, int64_t n,
                                int64_t k, float *y, int prologue, const float *pw, float eps,
-                               int accumulate, hipStream_t s) {
+                               int epi, hipStream_t s) {
 #define GGUF_FUSED(T)                                                                        \
   return prologue == 1   ? launch_m1<T, float, 1>(x, tiles, (int)n, (int)k, y, pw, eps,     \
-                                                  accumulate, s)                             \
+                                                  epi, s)                             \
          : prologue == 2 ? launch_m1<T, float, 2>(x, tiles, (int)n, (int)k, y, pw, eps,     \
-                                                  accumulate, s)                             \
+                                                  epi, s)                             \
                          : launch_m1<T, float, 0>(x, tiles, (int)n, (int)k, y, pw, eps,     \
-                                                  accumulate, s)
+                                                  epi, s)
   if (type == 12) GGUF_FUSED(12);
   if (type == 13) GGUF_FUSED(13);
   if (type == 14) GGUF_FUSED(14);

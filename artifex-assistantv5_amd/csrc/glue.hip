@@ -118,13 +118,25 @@ __global__ __launch_bounds__(kGlueThreads) void swiglu_kernel(const float *__res
                                    b.z * (a.z / (1.0f + expf(-a.z))), b.w * (a.w / (1.0f + expf(-a.w))));
 }
 
-// Decode attention, flash-decoding style.  Pass 1: workgroup (g, sp) takes KV
-// head g and cache slots [64 sp, 64 sp + 64) of the causal range 0..p,
-// p = *pos.  The workgroup whose range holds p first writes slot p (k after
-// rotate_half RoPE, v as is).  Each computes, for the grp query heads of g,
-// the running max m, sum l of exp(s - m) and o = sum exp(s - m) v over its
-// slots, into work[(g * S + sp) * grp + j] records of hd + 2 floats.
-// Pass 2 merges the S records of each query head.
+// Decode attention in one launch, flash-decoding style.  Workgroup (g, sp)
+// takes KV head g and cache slots [64 sp, 64 sp + 64) of the causal range
+// 0..p, p = *pos; the n = ceil((p + 1) / 64) workgroups of the range take
+// part and the others exit.  The workgroup whose range holds p writes slot p
+// (k after rotate_half RoPE, v as is) into the cache.
+//
+// Every global load of a workgroup (its K / V rows, the new k / v, the first
+// query row of each wave, the RoPE rows) is issued before any is consumed,
+// so the whole input arrives in one latency round.  The K / V rows are
+// staged in LDS (K rows at a stride of HD + 4 floats, so that lane t reading
+// row t is free of bank conflicts); wave w takes query heads w, w + 4, ...:
+// lane t owns slot t0 + t, a wave computes 64 dot products, one wave-wide
+// softmax reduction and sum_t p_t v_t reading V rows from LDS.
+//
+// With n = 1 the workgroup writes the output.  Otherwise it writes a record
+// (m, l, o[hd]) per query head to work[(g * S + sp) * grp + j], and the last
+// of the n workgroups to finish -- an atomic counter per KV head, kept in
+// the workspace and left at zero -- merges the n records in slot order, so
+// the result does not depend on which workgroup finishes last.
 constexpr int kSplit = 64;
 
 __device__ __forceinline__ float wave_max(float v) {
@@ -138,81 +150,134 @@ __device__ __forceinline__ float wave_sum(float v) {
   return v;
 }
 
-// Pass 1 layout: the workgroup stages its 64 K rows (stride HD + 4 floats,
-// so that lane t reading row t is free of bank conflicts) and 64 V rows in
-// LDS with coalesced loads, then wave w takes query heads w, w + 4, ... of
-// the group: lane t owns slot t0 + t, so a wave computes 64 dot products, one
-// wave-wide softmax reduction, and sum_t p_t v_t reading V rows from LDS.
 template <int HD>
-__global__ __launch_bounds__(kGlueThreads) void attention_split_kernel(
+__global__ __launch_bounds__(kGlueThreads) void attention_kernel(
     const float *__restrict__ qkv, const int64_t *__restrict__ pos, const float *__restrict__ cs,
     const float *__restrict__ sn, float *__restrict__ kc, float *__restrict__ vc,
-    float *__restrict__ work, int nh, int nkv, int max_seq) {
-  constexpr int hd = HD, half = HD / 2, KLD = HD + 4;
-  constexpr int C4 = HD / 4;  // float4 chunks per row
-  __shared__ __align__(16) float ks[kSplit * KLD];
-  __shared__ __align__(16) float vs[kSplit * HD];
+    float *__restrict__ out, float *__restrict__ work, unsigned *__restrict__ counters, int nh,
+    int nkv, int max_seq) {
+  constexpr int half = HD / 2, KLD = HD + 4, C4 = HD / 4;
+  constexpr int KV4 = kSplit * C4 / kGlueThreads;  // float4 of K (and of V) per thread
+  constexpr int QR = (half + 63) / 64;             // query element pairs per lane
+  // K / V rows; row kSplit is a pad that takes the stores of rows outside the range
+  __shared__ __align__(16) float ks[(kSplit + 1) * KLD];
+  __shared__ __align__(16) float vs[(kSplit + 1) * HD];
   __shared__ __align__(16) float qw[4 * HD];       // per wave: roped, scaled query
   __shared__ float pw[4 * kSplit];                  // per wave: probabilities
+  __shared__ int merge;
   const int grp = nh / nkv, g = blockIdx.x, sp = blockIdx.y, tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
   const int S = gridDim.y;
   const int64_t p64 = pos[0];
   if (p64 < 0 || p64 >= max_seq) return;  // no cache slot: write nothing
   const int p = (int)p64, T = p + 1, t0 = sp * kSplit;
-  if (t0 >= T) return;  // beyond the causal range: no record (pass 2 reads sp < ceil(T / 64))
+  if (t0 >= T) return;                     // beyond the causal range
+  const int n = (T + kSplit - 1) / kSplit;
   const int tn = min(kSplit, T - t0);
-  const bool holds_p = p < t0 + kSplit;
-  float *kbase = kc + (int64_t)g * max_seq * hd, *vbase = vc + (int64_t)g * max_seq * hd;
+  const int tp = p - t0;                   // row of slot p in this block when < kSplit
+  const bool holds_p = tp < kSplit;
+  float *kbase = kc + (int64_t)g * max_seq * HD, *vbase = vc + (int64_t)g * max_seq * HD;
   const float *crow = cs + (int64_t)p * half, *srow = sn + (int64_t)p * half;
 
-  // the rows of slots t0 .. t0 + tn - 1, coalesced; slot p is read stale here
-  // and replaced below
-  for (int e = tid; e < tn * C4; e += kGlueThreads) {
-    const int t = e / C4, c = e - t * C4;
-    *(float4 *)(ks + t * KLD + 4 * c) = *(const float4 *)(kbase + (int64_t)(t0 + t) * hd + 4 * c);
-    *(float4 *)(vs + t * HD + 4 * c) = *(const float4 *)(vbase + (int64_t)(t0 + t) * hd + 4 * c);
+  // 1. all global loads, straight-line: a row outside [t0, t0 + tn) or slot p
+  // (written below) reads row t0 instead (always a valid slot) into the pad
+  float4 kr[KV4], vr[KV4];
+#pragma unroll
+  for (int i = 0; i < KV4; ++i) {
+    const int e = tid + i * kGlueThreads, t = e / C4, c = e - t * C4;
+    const int row = (t < tn && t != tp) ? t0 + t : t0;
+    kr[i] = *(const float4 *)(kbase + (int64_t)row * HD + 4 * c);
+    vr[i] = *(const float4 *)(vbase + (int64_t)row * HD + 4 * c);
   }
-  __syncthreads();
-  if (holds_p) {  // rotate_half RoPE of k (rope.wgsl:1-10); slot p into the cache and LDS
-    const float *kin = qkv + (int64_t)nh * hd + g * hd;
-    const float *vin = qkv + (int64_t)(nh + nkv) * hd + g * hd;
-    float *krow = kbase + (int64_t)p * hd, *vrow = vbase + (int64_t)p * hd;
-    const int tp = p - t0;
-    for (int i = tid; i < half; i += kGlueThreads) {
-      const float c = crow[i], sv = srow[i], a = kin[i], b = kin[i + half];
-      const float k0 = a * c - b * sv, k1 = b * c + a * sv;
-      krow[i] = k0;
-      krow[i + half] = k1;
-      ks[tp * KLD + i] = k0;
-      ks[tp * KLD + i + half] = k1;
+  const int j0 = wave;
+  float qa[QR], qb[QR], qc[QR], qs[QR];
+  if (j0 < grp) {
+    const float *qin = qkv + (int64_t)(g * grp + j0) * HD;
+#pragma unroll
+    for (int r = 0; r < QR; ++r) {
+      const int i = lane + 64 * r;
+      if (i < half) {
+        qa[r] = qin[i];
+        qb[r] = qin[i + half];
+        qc[r] = crow[i];
+        qs[r] = srow[i];
+      }
     }
-    for (int i = tid; i < hd; i += kGlueThreads) {
-      vrow[i] = vin[i];
-      vs[tp * HD + i] = vin[i];
+  }
+  float ka = 0.f, kb = 0.f, kcs = 0.f, ksn = 0.f, vv = 0.f;
+  if (holds_p) {
+    const float *kin = qkv + (int64_t)nh * HD + g * HD;
+    const float *vin = qkv + (int64_t)(nh + nkv) * HD + g * HD;
+    if (tid < half) {
+      ka = kin[tid];
+      kb = kin[tid + half];
+      kcs = crow[tid];
+      ksn = srow[tid];
+    }
+    if (tid < HD) vv = vin[tid];
+  }
+
+  // keep the loads above ahead of every use below (the scheduler would
+  // otherwise sink each load to its store and serialize the round trips)
+  __builtin_amdgcn_sched_barrier(0);
+
+  // 2. LDS: the block's K / V rows, slot p (rotate_half RoPE of k, rope.wgsl:1-10;
+  // also into the caches) and each wave's first roped, scaled query
+#pragma unroll
+  for (int i = 0; i < KV4; ++i) {
+    const int e = tid + i * kGlueThreads, t = e / C4, c = e - t * C4;
+    const int st = (t < tn && t != tp) ? t : kSplit;
+    *(float4 *)(ks + st * KLD + 4 * c) = kr[i];
+    *(float4 *)(vs + st * HD + 4 * c) = vr[i];
+  }
+  if (holds_p) {
+    float *krow = kbase + (int64_t)p * HD, *vrow = vbase + (int64_t)p * HD;
+    if (tid < half) {
+      const float k0 = ka * kcs - kb * ksn, k1 = kb * kcs + ka * ksn;
+      krow[tid] = k0;
+      krow[tid + half] = k1;
+      ks[tp * KLD + tid] = k0;
+      ks[tp * KLD + tid + half] = k1;
+    }
+    if (tid < HD) {
+      vrow[tid] = vv;
+      vs[tp * HD + tid] = vv;
+    }
+  }
+  const float scale = 1.0f / sqrtf((float)HD);
+  float *q = qw + wave * HD;
+  if (j0 < grp) {
+#pragma unroll
+    for (int r = 0; r < QR; ++r) {
+      const int i = lane + 64 * r;
+      if (i < half) {
+        q[i] = (qa[r] * qc[r] - qb[r] * qs[r]) * scale;
+        q[i + half] = (qb[r] * qc[r] + qa[r] * qs[r]) * scale;
+      }
     }
   }
   __syncthreads();
 
-  const float scale = 1.0f / sqrtf((float)hd);
-  float *q = qw + wave * HD;
+  // 3. per query head: scores, softmax, sum p v
   float *pr = pw + wave * kSplit;
-  for (int j = wave; j < grp; j += 4) {
-    const float *qin = qkv + (int64_t)(g * grp + j) * hd;
-    for (int i = lane; i < half; i += 64) {
-      const float c = crow[i], sv = srow[i], a = qin[i], b = qin[i + half];
-      q[i] = (a * c - b * sv) * scale;
-      q[i + half] = (b * c + a * sv) * scale;
+  for (int j = j0; j < grp; j += 4) {
+    if (j != j0) {  // later heads of a group larger than four: rope this query now
+      const float *qin = qkv + (int64_t)(g * grp + j) * HD;
+      for (int i = lane; i < half; i += 64) {
+        const float c = crow[i], sv = srow[i], a = qin[i], b = qin[i + half];
+        q[i] = (a * c - b * sv) * scale;
+        q[i + half] = (b * c + a * sv) * scale;
+      }
     }
     // the wave's own LDS writes are visible to it in program order
     float sc = -INFINITY;
     if (lane < tn) {
-      const float *kr = ks + lane * KLD;
+      const float *kr_ = ks + lane * KLD;
       float a0 = 0.f, a1 = 0.f;
 #pragma unroll
       for (int c = 0; c < C4; c += 2) {
-        const float4 k0 = *(const float4 *)(kr + 4 * c), q0 = *(const float4 *)(q + 4 * c);
-        const float4 k1 = *(const float4 *)(kr + 4 * c + 4), q1 = *(const float4 *)(q + 4 * c + 4);
+        const float4 k0 = *(const float4 *)(kr_ + 4 * c), q0 = *(const float4 *)(q + 4 * c);
+        const float4 k1 = *(const float4 *)(kr_ + 4 * c + 4), q1 = *(const float4 *)(q + 4 * c + 4);
         a0 += q0.x * k0.x + q0.y * k0.y + q0.z * k0.z + q0.w * k0.w;
         a1 += q1.x * k1.x + q1.y * k1.y + q1.z * k1.z + q1.w * k1.w;
       }
@@ -222,44 +287,67 @@ __global__ __launch_bounds__(kGlueThreads) void attention_split_kernel(
     const float e = lane < tn ? expf(sc - m) : 0.f;
     const float l = wave_sum(e);
     pr[lane] = e;
-    // o[i] for i = lane, lane + 64, ...: sum over the slots of p_t v_t
-    float *rec = work + ((int64_t)(g * S + sp) * grp + j) * (hd + 2);
-    for (int i = lane; i < hd; i += 64) {
+    float *rec = work + ((int64_t)(g * S + sp) * grp + j) * (HD + 2);
+    float *o_out = out + (int64_t)(g * grp + j) * HD;
+    for (int i = lane; i < HD; i += 64) {
       float o = 0.f;
 #pragma unroll 8
       for (int t = 0; t < tn; ++t) o += pr[t] * vs[t * HD + i];
-      rec[2 + i] = o;
+      if (n == 1)
+        o_out[i] = o / l;
+      else
+        rec[2 + i] = o;
     }
-    if (lane == 0) {
+    if (n > 1 && lane == 0) {
       rec[0] = m;
       rec[1] = l;
     }
   }
-}
+  if (n == 1) return;
 
-// Pass 2: query head h = blockIdx.x merges the records of its KV head.
-__global__ __launch_bounds__(kGlueThreads) void attention_merge_kernel(
-    const int64_t *__restrict__ pos, const float *__restrict__ work, float *__restrict__ out,
-    int nh, int nkv, int hd, int S, int max_seq) {
-  const int grp = nh / nkv, h = blockIdx.x, g = h / grp, j = h % grp;
-  const int64_t p64 = pos[0];
-  if (p64 < 0 || p64 >= max_seq) return;  // pass 1 wrote no records
-  const int n = ((int)p64 + kSplit) / kSplit;  // records written: ceil((p + 1) / 64)
-  const float *base = work + ((int64_t)g * S * grp + j) * (hd + 2);
-  const int64_t stride = (int64_t)grp * (hd + 2);
-  // records are read once into registers (at most 16 splits of 64 slots
-  // per pass; longer caches loop)
-  float M = -INFINITY;
-  for (int s = 0; s < n; ++s) M = fmaxf(M, base[s * stride]);
-  float L = 0.f;
-  for (int s = 0; s < n; ++s) L += base[s * stride + 1] * expf(base[s * stride] - M);
-  const float inv = 1.0f / L;
-  for (int i = threadIdx.x; i < hd; i += kGlueThreads) {
-    float o = 0.f;
+  // 4. the last of the n workgroups of KV head g merges the records
+  __threadfence();  // this workgroup's records are visible before it is counted
+  __syncthreads();
+  if (tid == 0) merge = atomicAdd(counters + g, 1u) == (unsigned)(n - 1);
+  __syncthreads();
+  if (!merge) return;
+  __threadfence();  // every other workgroup's records are visible to the merge
+  // wave w merges query heads w, w + 4, ...: lane s reads record s's (m, l),
+  // so a chunk of 64 records costs one load round, and the weighted sums of
+  // the outputs issue their loads together
+  constexpr int QO = HD / 64;  // outputs per lane
+  const int64_t stride = (int64_t)grp * (HD + 2);
+  for (int j = wave; j < grp; j += 4) {
+    const float *base = work + ((int64_t)g * S * grp + j) * (HD + 2);
+    float M = -INFINITY;
+    for (int s0 = 0; s0 < n; s0 += 64)
+      if (s0 + lane < n) M = fmaxf(M, base[(s0 + lane) * stride]);
+    M = wave_max(M);
+    float L = 0.f, o[QO];
+#pragma unroll
+    for (int r = 0; r < QO; ++r) o[r] = 0.f;
+    for (int s0 = 0; s0 < n; s0 += 64) {
+      float w = 0.f;
+      if (s0 + lane < n) {
+        const float *rec = base + (s0 + lane) * stride;
+        w = expf(rec[0] - M);
+        L += w * rec[1];
+      }
+      pr[lane] = w;  // wave-local: read back in program order
+      const int cnt = min(64, n - s0);
 #pragma unroll 8
-    for (int s = 0; s < n; ++s) o += base[s * stride + 2 + i] * expf(base[s * stride] - M);
-    out[(int64_t)h * hd + i] = o * inv;
+      for (int u = 0; u < cnt; ++u) {
+        const float wu = pr[u];
+        const float *ro = base + (s0 + u) * stride + 2 + lane;
+#pragma unroll
+        for (int r = 0; r < QO; ++r) o[r] += wu * ro[64 * r];
+      }
+    }
+    const float inv = 1.0f / wave_sum(L);
+#pragma unroll
+    for (int r = 0; r < QO; ++r) out[(int64_t)(g * grp + j) * HD + lane + 64 * r] = o[r] * inv;
   }
+  if (tid == 0) counters[g] = 0u;  // ready for the next call
 }
 
 // Argmax, pass 1: workgroup b scans a contiguous chunk and writes its (value,
@@ -333,29 +421,32 @@ hipError_t launch_swiglu(const float *gu, float *out, int64_t rows, int64_t ffn,
   return hipGetLastError();
 }
 
-int64_t attention_work_bytes(int nh, int nkv, int hd, int64_t max_seq) {
+// Workspace: the records [nkv][S][grp][hd + 2] floats, then nkv counters.
+static int64_t attention_record_bytes(int nh, int nkv, int hd, int64_t max_seq) {
   const int64_t S = (max_seq + kSplit - 1) / kSplit;
-  return (int64_t)sizeof(float) * nkv * S * (nh / nkv) * (hd + 2);
+  return ((int64_t)sizeof(float) * nkv * S * (nh / nkv) * (hd + 2) + 15) / 16 * 16;
+}
+
+int64_t attention_work_bytes(int nh, int nkv, int hd, int64_t max_seq) {
+  return attention_record_bytes(nh, nkv, hd, max_seq) + ((int64_t)nkv * 4 + 15) / 16 * 16;
 }
 
 hipError_t launch_attention_decode(const float *qkv, const int64_t *pos, const float *cs,
                                    const float *sn, float *kc, float *vc, float *out, float *work,
                                    int nh, int nkv, int hd, int64_t max_seq, hipStream_t s) {
   const int S = (int)((max_seq + kSplit - 1) / kSplit);
+  unsigned *counters =
+      (unsigned *)((char *)work + attention_record_bytes(nh, nkv, hd, max_seq));
   const dim3 grid((unsigned)nkv, (unsigned)S), block(kGlueThreads);
   if (hd == 64)
-    hipLaunchKernelGGL(attention_split_kernel<64>, grid, block, 0, s, qkv, pos, cs, sn, kc, vc,
-                       work, nh, nkv, (int)max_seq);
+    hipLaunchKernelGGL(attention_kernel<64>, grid, block, 0, s, qkv, pos, cs, sn, kc, vc, out,
+                       work, counters, nh, nkv, (int)max_seq);
   else if (hd == 128)
-    hipLaunchKernelGGL(attention_split_kernel<128>, grid, block, 0, s, qkv, pos, cs, sn, kc, vc,
-                       work, nh, nkv, (int)max_seq);
+    hipLaunchKernelGGL(attention_kernel<128>, grid, block, 0, s, qkv, pos, cs, sn, kc, vc, out,
+                       work, counters, nh, nkv, (int)max_seq);
   else
-    hipLaunchKernelGGL(attention_split_kernel<256>, grid, block, 0, s, qkv, pos, cs, sn, kc, vc,
-                       work, nh, nkv, (int)max_seq);
-  hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(attention_merge_kernel, dim3((unsigned)nh), dim3(kGlueThreads), 0, s, pos,
-                     work, out, nh, nkv, hd, S, (int)max_seq);
+    hipLaunchKernelGGL(attention_kernel<256>, grid, block, 0, s, qkv, pos, cs, sn, kc, vc, out,
+                       work, counters, nh, nkv, (int)max_seq);
   return hipGetLastError();
 }
 

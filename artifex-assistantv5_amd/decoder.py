@@ -40,7 +40,7 @@ import torch
 from . import glue, quantize
 from .ggml import Q4_K, Q6_K, raw_row_bytes
 from .linear import (GGUFWeight, LayerWeights, QuantEmbedding, concat_rows, dispatch_matmul_gguf,
-                     repack_gguf_for_gpu)
+                     interleave_tiles, repack_gguf_for_gpu, split_interleaved)
 
 
 @dataclasses.dataclass
@@ -78,10 +78,12 @@ class DecoderConfig:
 @dataclasses.dataclass
 class DecoderWeights:
     """Per-layer ``LayerWeights`` slots: ``qkv_gg`` (Q, K, V rows concatenated) or,
-    when the three have different GGUF types, ``qkv_parts = [q, k, v]``; likewise
-    ``gateUp_gg`` or ``gateUp_parts = [gate, up]``; ``o_gg``, ``down_gg`` and the f32
-    norms ``attn_norm`` / ``ffn_norm``.  ``embed`` is a dense ``[vocab, d_model]``
-    table or a ``QuantEmbedding`` of raw GGUF rows."""
+    when the three have different GGUF types, ``qkv_parts = [q, k, v]``; the FFN
+    input as ``gateUpI_gg`` (gate and up tiles interleaved, ``interleave_tiles``:
+    the decode step then applies SwiGLU in the projection's epilogue),
+    ``gateUp_gg`` (rows concatenated) or ``gateUp_parts = [gate, up]``; ``o_gg``,
+    ``down_gg`` and the f32 norms ``attn_norm`` / ``ffn_norm``.  ``embed`` is a
+    dense ``[vocab, d_model]`` table or a ``QuantEmbedding`` of raw GGUF rows."""
     layers: list
     final_norm: torch.Tensor
     lm_head_gg: GGUFWeight
@@ -100,9 +102,13 @@ class DecoderWeights:
 
 
 def parts(lw: LayerWeights, slot: str) -> list:
-    """The weights of a row-concatenated slot: ``[<slot>_gg]`` or ``<slot>_parts``."""
-    w = lw.get(f"{slot}_gg")
-    return [w] if w is not None else list(lw.get(f"{slot}_parts"))
+    """The weights of a slot: ``[<slot>_gg]``, ``[<slot>I_gg]`` (tile-interleaved)
+    or ``<slot>_parts``."""
+    for name in (f"{slot}_gg", f"{slot}I_gg"):
+        w = lw.get(name)
+        if w is not None:
+            return [w]
+    return list(lw.get(f"{slot}_parts"))
 
 
 def _quantized(ggml_type: int, n: int, k: int, seed: int, device) -> GGUFWeight:
@@ -140,7 +146,7 @@ def synthetic_weights(cfg: DecoderConfig, seed: int = 0, device="cuda",
         gate = _quantized(cfg.gate_up_type, cfg.ffn, d, s + 5, device)
         up = _quantized(cfg.gate_up_type, cfg.ffn, d, s + 6, device)
         down = _quantized(cfg.down_type, d, cfg.ffn, s + 7, device)
-        return concat_rows(q, k, v), o, concat_rows(gate, up), down
+        return concat_rows(q, k, v), o, interleave_tiles(gate, up), down
 
     layers = []
     shared = None if distinct_layers else layer_set(seed * 1000)
@@ -150,7 +156,7 @@ def synthetic_weights(cfg: DecoderConfig, seed: int = 0, device="cuda",
             qkv, o, gu, down = (GGUFWeight(w.data[w.byte_offset:w.byte_offset + w.nbytes].clone(),
                                            w.ggml_type, w.n, w.k) for w in shared)
         layers.append(LayerWeights(
-            qkv_gg=qkv, o_gg=o, gateUp_gg=gu, down_gg=down,
+            qkv_gg=qkv, o_gg=o, gateUpI_gg=gu, down_gg=down,
             attn_norm=1.0 + 0.02 * torch.randn(d, device=device, generator=g),
             ffn_norm=1.0 + 0.02 * torch.randn(d, device=device, generator=g)))
     if lm_head_unique_rows:
@@ -222,6 +228,14 @@ class QuantDecoder:
             return self._proj(x, ws[0], label)
         return torch.cat([self._proj(x, w, f"{label}{i}") for i, w in enumerate(ws)], dim=1)
 
+    def _gate_up(self, h: torch.Tensor, lw: LayerWeights, label: str):
+        """(gate, up) projections of the FFN input ``h``."""
+        w = lw.get("gateUpI_gg")
+        if w is not None:
+            return split_interleaved(self._proj(h, w, label))
+        gu = self._proj_slot(h, lw, "gateUp", label)
+        return gu[:, :self.cfg.ffn], gu[:, self.cfg.ffn:]
+
     def _embed(self, tok: torch.Tensor, out: Optional[torch.Tensor] = None) -> torch.Tensor:
         e = self.w.embed
         if isinstance(e, QuantEmbedding):
@@ -257,8 +271,8 @@ class QuantDecoder:
             o = o.view(nkv, M, grp, hd).permute(1, 0, 2, 3).reshape(M, nh * hd)
             x = x + self._proj(o, lw.o_gg, f"L{l}-o")
             h = rms_norm(x, lw.ffn_norm, cfg.eps)
-            gu = self._proj_slot(h, lw, "gateUp", f"L{l}-gateUp")
-            a = gu[:, cfg.ffn:] * torch.nn.functional.silu(gu[:, :cfg.ffn])
+            gate, up = self._gate_up(h, lw, f"L{l}-gateUp")
+            a = up * torch.nn.functional.silu(gate)
             x = x + self._proj(a, lw.down_gg, f"L{l}-down")
         return x
 
@@ -282,10 +296,12 @@ class QuantDecoder:
         dispatch_matmul_gguf(x, w, y, 1, w.n, w.k, label)
 
     def _step_fused(self, tok: torch.Tensor, pos: torch.Tensor) -> torch.Tensor:
-        """Six launches per layer: Q/K/V projection with the input RMSNorm as its
-        prologue, attention (two passes), output projection accumulated into the
-        residual, gate/up projection with the FFN RMSNorm prologue, down
-        projection with the SwiGLU prologue accumulated into the residual."""
+        """Five launches per layer: Q/K/V projection with the input RMSNorm as its
+        prologue, attention, output projection accumulated into the residual,
+        gate/up projection with the FFN RMSNorm prologue and the SwiGLU epilogue
+        (interleaved gate / up tiles), down projection accumulated into the
+        residual.  With concatenated or split gate / up weights, SwiGLU runs as
+        the down projection's prologue instead."""
         cfg, W = self.cfg, self.w
         x = self.b_x
         self._embed(tok, x)
@@ -295,8 +311,15 @@ class QuantDecoder:
                                   self.v_cache[l], self.b_att, cfg.n_heads, cfg.n_kv_heads,
                                   cfg.head_dim, self.w_att)
             glue.matmul_fused(self.b_att, lw.o_gg, x, accumulate=True)
-            self._fused_slot(x, lw, "gateUp", self.b_gu, lw.ffn_norm)
-            glue.matmul_fused(self.b_gu, lw.down_gg, x, glue.PROLOGUE_SWIGLU, accumulate=True)
+            gui = lw.get("gateUpI_gg")
+            if gui is not None:
+                glue.matmul_fused(x, gui, self.b_a, glue.PROLOGUE_RMSNORM, lw.ffn_norm, cfg.eps,
+                                  epilogue=glue.EPILOGUE_SWIGLU)
+                glue.matmul_fused(self.b_a, lw.down_gg, x, accumulate=True)
+            else:
+                self._fused_slot(x, lw, "gateUp", self.b_gu, lw.ffn_norm)
+                glue.matmul_fused(self.b_gu, lw.down_gg, x, glue.PROLOGUE_SWIGLU,
+                                  accumulate=True)
         glue.matmul_fused(x, W.lm_head_gg, self.b_logits, glue.PROLOGUE_RMSNORM, W.final_norm,
                           cfg.eps)
         glue.argmax(self.b_logits, tok, self.w_arg)

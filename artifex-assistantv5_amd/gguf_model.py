@@ -32,7 +32,7 @@ from .decoder import DecoderConfig, DecoderWeights, QuantDecoder
 from .ggml import GGML_TYPE_NAMES
 from .gguf_file import GGUFFile, GGUFTensorInfo, arch_kv, gguf_architecture, parse_gguf_path
 from .gguf_loader import LoadedGGUFModel, load_gguf_model
-from .linear import GGUFWeight, LayerWeights, QuantEmbedding, concat_rows
+from .linear import GGUFWeight, LayerWeights, QuantEmbedding, concat_rows, interleave_tiles
 
 SUPPORTED_ARCHS = ("llama",)
 BLOCK_TENSORS = ("attn_norm", "attn_q", "attn_k", "attn_v", "attn_output", "ffn_norm",
@@ -137,22 +137,27 @@ def load_decoder(path: str, device="cuda", max_seq: int = 2048, fused: bool = Tr
             return {"gg": concat_rows(*ws)}
         return {"parts": list(ws)}
 
+    def fuse_ffn(gate, up):
+        if gate.ggml_type == up.ggml_type and gate.n % 16 == 0:
+            return {"I_gg": interleave_tiles(gate, up)}
+        return {"_parts": [gate, up]}
+
     d, hd, nh, nkv, f = cfg.d_model, cfg.head_dim, cfg.n_heads, cfg.n_kv_heads, cfg.ffn
     layers = []
     for l in range(cfg.n_layers):
         b = f"blk.{l}."
         qkv = fuse([quant(b + "attn_q.weight", nh * hd, d), quant(b + "attn_k.weight", nkv * hd, d),
                     quant(b + "attn_v.weight", nkv * hd, d)])
-        gu = fuse([quant(b + "ffn_gate.weight", f, d), quant(b + "ffn_up.weight", f, d)])
+        gu = fuse_ffn(quant(b + "ffn_gate.weight", f, d), quant(b + "ffn_up.weight", f, d))
         slots = dict(o_gg=quant(b + "attn_output.weight", d, nh * hd),
                      down_gg=quant(b + "ffn_down.weight", d, f),
                      attn_norm=vec(b + "attn_norm.weight", d),
                      ffn_norm=vec(b + "ffn_norm.weight", d))
         slots.update({f"qkv_{k}": v for k, v in qkv.items()})
-        slots.update({f"gateUp_{k}": v for k, v in gu.items()})
+        slots.update({f"gateUp{k}": v for k, v in gu.items()})
         layers.append(LayerWeights(**slots))
         for name in ("attn_q", "attn_k", "attn_v", "ffn_gate", "ffn_up"):
-            if "gg" in (qkv if name.startswith("attn") else gu):
+            if (qkv if name.startswith("attn") else gu).keys() & {"gg", "I_gg"}:
                 T.pop(b + name + ".weight", None)   # the concatenated copy replaces them
     lm_name = "output.weight" if "output.weight" in T else "token_embd.weight"
     lm = quant(lm_name, cfg.vocab, d)

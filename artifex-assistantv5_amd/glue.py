@@ -56,11 +56,13 @@ def swiglu(gate_up: torch.Tensor, out: torch.Tensor) -> torch.Tensor:
 
 def attention_workspace(n_heads: int, n_kv_heads: int, head_dim: int, max_seq: int,
                         device) -> torch.Tensor:
-    """Device workspace for ``attention_decode`` (allocate once, reuse every step)."""
+    """Device workspace for ``attention_decode`` (allocate once, reuse every step).
+    Zero-filled: its per-KV-head counters must start at zero (each call leaves
+    them at zero)."""
     lib = _native.load_library()
     nbytes = _native.check(lib.gguf_hip_attention_workspace(n_heads, n_kv_heads, head_dim,
                                                             max_seq), lib)
-    return torch.empty((nbytes + 15) // 16 * 4, dtype=torch.float32, device=device)
+    return torch.zeros((nbytes + 15) // 16 * 4, dtype=torch.float32, device=device)
 
 
 def attention_decode(qkv: torch.Tensor, pos: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor,
@@ -103,20 +105,28 @@ def argmax(x: torch.Tensor, out: torch.Tensor, work: torch.Tensor) -> torch.Tens
 
 PROLOGUE_NONE, PROLOGUE_RMSNORM, PROLOGUE_SWIGLU = (_native.PROLOGUE_NONE, _native.PROLOGUE_RMSNORM,
                                                     _native.PROLOGUE_SWIGLU)
+EPILOGUE_STORE, EPILOGUE_ACCUMULATE, EPILOGUE_SWIGLU = (
+    _native.EPILOGUE_STORE, _native.EPILOGUE_ACCUMULATE, _native.EPILOGUE_SWIGLU)
 
 
 def matmul_fused(x: torch.Tensor, w, y: torch.Tensor, prologue: int = PROLOGUE_NONE,
                  norm_w: torch.Tensor | None = None, eps: float = 0.0,
-                 accumulate: bool = False) -> torch.Tensor:
+                 accumulate: bool = False, epilogue: int | None = None) -> torch.Tensor:
     """One activation row through a quantized weight with fused neighbours:
-    ``y (=|+=) x' @ dequant(w)^T`` where x' is x, ``rmsnorm(x) * norm_w`` or, for
-    x = [gate | up], ``up * silu(gate)``.  ``w`` is a GGUFWeight."""
+    ``r = x' @ dequant(w)^T`` where x' is x, ``rmsnorm(x) * norm_w`` or, for
+    x = [gate | up], ``up * silu(gate)``; then ``y = r``, ``y += r``
+    (``accumulate`` / EPILOGUE_ACCUMULATE) or, for a weight of interleaved
+    gate / up tiles (``interleave_tiles``), ``y = up * silu(gate)``
+    (EPILOGUE_SWIGLU, ``w.n / 2`` outputs).  ``w`` is a GGUFWeight."""
     _f32(x, y)
     k = w.k
+    epi = epilogue if epilogue is not None else (EPILOGUE_ACCUMULATE if accumulate
+                                                 else EPILOGUE_STORE)
     want = 2 * k if prologue == PROLOGUE_SWIGLU else k
-    if x.numel() != want or y.numel() != w.n:
+    n_out = w.n // 2 if epi == EPILOGUE_SWIGLU else w.n
+    if x.numel() != want or y.numel() != n_out:
         raise ValueError(f"matmul_fused: x has {x.numel()} elements (needs {want}), "
-                         f"y has {y.numel()} (needs {w.n})")
+                         f"y has {y.numel()} (needs {n_out})")
     if prologue == PROLOGUE_RMSNORM:
         if norm_w is None:
             raise ValueError("matmul_fused: RMSNORM prologue needs norm_w")
@@ -124,6 +134,5 @@ def matmul_fused(x: torch.Tensor, w, y: torch.Tensor, prologue: int = PROLOGUE_N
     lib = _native.load_library()
     _native.check(lib.gguf_hip_matmul_fused(
         x.data_ptr(), w.ptr(), w.ggml_type, w.n, k, y.data_ptr(), prologue,
-        norm_w.data_ptr() if norm_w is not None else None, float(eps), int(bool(accumulate)),
-        _s(y)), lib)
+        norm_w.data_ptr() if norm_w is not None else None, float(eps), int(epi), _s(y)), lib)
     return y

@@ -166,6 +166,31 @@ def concat_rows(*weights: GGUFWeight) -> GGUFWeight:
     return GGUFWeight(torch.cat(parts), t, sum(w.n for w in weights), k)
 
 
+def interleave_tiles(gate: GGUFWeight, up: GGUFWeight) -> GGUFWeight:
+    """Gate and up weights with their 16-row tiles interleaved: tile 2m holds gate
+    rows 16m..16m+15, tile 2m + 1 the same up rows.  A matmul over it computes
+    the rows of the reference's gate+up concatenation (forward-pass.ts:740-791)
+    in this order, and the SwiGLU epilogue of the fused decode kernel pairs
+    them in one workgroup.  Both weights need the same type, K and a multiple
+    of 16 rows."""
+    if gate.ggml_type != up.ggml_type or gate.k != up.k or gate.n != up.n:
+        raise ValueError("interleave_tiles: gate and up must share type and shape")
+    if gate.n % TILE_ROWS:
+        raise ValueError(f"interleave_tiles: rows must be a multiple of {TILE_ROWS}")
+    tb = TILE_ROWS * gate.row_bytes
+    nt = gate.n // TILE_ROWS
+    g = gate.data[gate.byte_offset:gate.byte_offset + gate.nbytes].view(nt, tb)
+    u = up.data[up.byte_offset:up.byte_offset + up.nbytes].view(nt, tb)
+    return GGUFWeight(torch.stack([g, u], dim=1).reshape(-1), gate.ggml_type, 2 * gate.n, gate.k)
+
+
+def split_interleaved(y: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """(gate, up) columns of a result ``[M, 2 * ffn]`` computed over ``interleave_tiles``."""
+    m, n2 = y.shape
+    v = y.view(m, n2 // (2 * TILE_ROWS), 2, TILE_ROWS)
+    return v[:, :, 0, :].reshape(m, n2 // 2), v[:, :, 1, :].reshape(m, n2 // 2)
+
+
 def dequant_ggml(ggml_type: int, data, n: int) -> torch.Tensor:
     """Dequantize ``n`` elements to f32 on the GPU (gguf-dequant.ts:844-868).
 

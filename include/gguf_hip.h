@@ -43,7 +43,7 @@ extern "C" {
  * are exported (kernels and helpers cannot be interposed across libraries). */
 #pragma GCC visibility push(default)
 
-#define GGUF_HIP_ABI_VERSION 5
+#define GGUF_HIP_ABI_VERSION 6
 
 /* ggml type ids (gguf.ts:24-35); activation dtypes reuse F32 / F16. */
 #define GGUF_HIP_F32 0
@@ -147,15 +147,23 @@ int gguf_hip_matmul_variant(const void *x, int x_type, int64_t ldx, const void *
 #define GGUF_HIP_PROLOGUE_RMSNORM 1 /* x' = x / sqrt(mean(x^2) + eps) * norm_w */
 #define GGUF_HIP_PROLOGUE_SWIGLU 2  /* x = [gate (k) | up (k)], x' = up * silu(gate) */
 
-/* One decode-step projection with its neighbours fused in:
- *   y[n] = sum_k x'[k] * dequant(W)[n, k]     (accumulate = 0)
- *   y[n] += sum_k x'[k] * dequant(W)[n, k]    (accumulate = 1: the residual add)
- * for a single f32 activation row x (16-byte aligned), x' given by the
- * prologue.  The reference dispatches these as separate rmsnorm, gate_silu,
- * matmul and add shaders in its layer loop (forward-pass.ts:2925-3297).
- * K <= 16384; shapes without a fused kernel return GGUF_HIP_ERR_SHAPE. */
+/* Epilogues of gguf_hip_matmul_fused. */
+#define GGUF_HIP_EPILOGUE_STORE 0      /* y[n] = r[n] */
+#define GGUF_HIP_EPILOGUE_ACCUMULATE 1 /* y[n] += r[n] (the residual add) */
+#define GGUF_HIP_EPILOGUE_SWIGLU 2     /* W holds gate / up row tiles interleaved
+                                        * (tile 2m = gate rows 16m..16m+15, tile
+                                        * 2m + 1 = those up rows; N % 32 == 0):
+                                        * y[16m + i] = r[16(2m+1) + i] * silu(r[32m + i]),
+                                        * N / 2 outputs */
+
+/* One decode-step projection with its neighbours fused in: the row
+ * r[n] = sum_k x'[k] * dequant(W)[n, k] for a single f32 activation row x
+ * (16-byte aligned), x' given by the prologue, written by the epilogue.
+ * The reference dispatches these as separate rmsnorm, gate_silu, matmul and
+ * add shaders in its layer loop (forward-pass.ts:2925-3297).  K <= 16384;
+ * shapes without a fused kernel return GGUF_HIP_ERR_SHAPE. */
 int gguf_hip_matmul_fused(const float *x, const void *tiles, int ggml_type, int64_t n, int64_t k,
-                          float *y, int prologue, const float *norm_w, float eps, int accumulate,
+                          float *y, int prologue, const float *norm_w, float eps, int epilogue,
                           void *stream);
 
 /* ---------------------------------------------------------------------------
@@ -185,10 +193,12 @@ int gguf_hip_swiglu(const float *gate_up, float *out, int64_t rows, int64_t ffn,
  * head h over slots 0..p of KV head h / (n_heads / n_kv_heads), softmax scaled
  * by 1/sqrt(head_dim).  qkv = [q (n_heads*head_dim) | k | v (n_kv*head_dim each)];
  * caches [n_kv, max_seq, head_dim]; out [n_heads * head_dim]; head_dim is 64,
- * 128 or 256 and n_heads / n_kv_heads at most 8.  `work` (device, 16-byte
- * aligned, gguf_hip_attention_workspace bytes) holds per-64-slot partial
- * softmax records between the two launches.  The position is read on the
- * device, so the call can be captured in a graph. */
+ * 128 or 256 and n_heads / n_kv_heads at most 8.  One launch.  `work`
+ * (device, 16-byte aligned, gguf_hip_attention_workspace bytes) holds the
+ * per-64-slot partial softmax records and one counter per KV head; it must be
+ * zero-filled once before its first use, and every call leaves the counters
+ * at zero again.  Calls that share a workspace must not overlap.  The
+ * position is read on the device, so the call can be captured in a graph. */
 int gguf_hip_attention_decode(const float *qkv, const int64_t *pos, const float *cos_table,
                               const float *sin_table, float *k_cache, float *v_cache, float *out,
                               int n_heads, int n_kv_heads, int head_dim, int64_t max_seq,

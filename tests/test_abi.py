@@ -68,7 +68,7 @@ def test_constants_match_header(native):
 
 
 def test_abi_version(lib):
-    assert lib.gguf_hip_abi_version() == 5
+    assert lib.gguf_hip_abi_version() == 6
 
 
 def test_type_traits(lib, native):
@@ -205,7 +205,8 @@ def test_glue_errors(lib, native):
     assert att(a, b, c, c, a, a, b, 32, 8, 128, 512, None, None) == native.ERR_NULL
     assert att(a + 4, b, c, c, a, a, b, 32, 8, 128, 512, wk, None) == native.ERR_ALIGN
     # workspace: 8 KV heads x 8 slot ranges of 64 x 4 query heads x (128 + 2) floats
-    assert lib.gguf_hip_attention_workspace(32, 8, 128, 512) == 8 * 8 * 4 * 130 * 4
+    # records [nkv][S][grp][hd + 2] floats, then nkv counters (16-byte rounded)
+    assert lib.gguf_hip_attention_workspace(32, 8, 128, 512) == 8 * 8 * 4 * 130 * 4 + 32
     assert lib.gguf_hip_attention_workspace(32, 8, 100, 512) == native.ERR_SHAPE
     assert lib.gguf_hip_argmax_workspace() > 0
     assert lib.gguf_hip_argmax(a, 0, b, c, None) == native.ERR_SHAPE
@@ -223,8 +224,13 @@ def test_fused_matmul_errors(lib, native):
     assert f(x, w, 12, 64, 4096, y, 1, nw, -1.0, 0, None) == native.ERR_SHAPE
     assert f(x + 4, w, 12, 64, 4096, y, 0, None, 0.0, 0, None) == native.ERR_ALIGN
     assert f(x, w, 11, 64, 4096, y, 0, None, 0.0, 0, None) == native.ERR_TYPE
+    assert f(x, w, 12, 64, 4096, y, 0, None, 0.0, 3, None) == native.ERR_SHAPE      # epilogue
+    assert f(x, w, 12, 48, 4096, y, 0, None, 0.0, 2, None) == native.ERR_SHAPE      # SwiGLU: N % 32
     assert f(x, w, 12, 0, 4096, y, 2, None, 0.0, 1, None) == 0                     # N = 0: no-op
     d = _defines()
     assert (d["GGUF_HIP_PROLOGUE_NONE"], d["GGUF_HIP_PROLOGUE_RMSNORM"],
             d["GGUF_HIP_PROLOGUE_SWIGLU"]) == (native.PROLOGUE_NONE, native.PROLOGUE_RMSNORM,
                                                native.PROLOGUE_SWIGLU)
+    assert (d["GGUF_HIP_EPILOGUE_STORE"], d["GGUF_HIP_EPILOGUE_ACCUMULATE"],
+            d["GGUF_HIP_EPILOGUE_SWIGLU"]) == (native.EPILOGUE_STORE, native.EPILOGUE_ACCUMULATE,
+                                               native.EPILOGUE_SWIGLU)

@@ -41,7 +41,13 @@ class Reference:
         self.cfg = cfg
         d = lambda gg: gg.dequant().double()  # noqa: E731
         cat = lambda l, slot: torch.cat([d(p) for p in dec.parts(l, slot)])  # noqa: E731
-        self.layers = [dict(qkv=cat(l, "qkv"), o=d(l.o_gg), gu=cat(l, "gateUp"),
+
+        def gate_up(l):  # rows in [gate; up] order whatever the layout
+            w = l.get("gateUpI_gg")
+            if w is None:
+                return cat(l, "gateUp")
+            return d(w).view(-1, 2, 16, w.k).permute(1, 0, 2, 3).reshape(w.n, w.k)
+        self.layers = [dict(qkv=cat(l, "qkv"), o=d(l.o_gg), gu=gate_up(l),
                             down=d(l.down_gg), an=l.attn_norm.double(),
                             fn=l.ffn_norm.double()) for l in w.layers]
         self.lm = d(w.lm_head_gg)

@@ -66,6 +66,45 @@ def test_swiglu_prologue_accumulate(mods, t, n, k):
     assert _elementwise(y, ref, wd, a) < 1e-6
 
 
+@pytest.mark.parametrize("t,ffn,k", [(12, 14336, 4096), (12, 512, 2048), (13, 1024, 4096),
+                                     (14, 256, 4096), (8, 768, 1024)])
+@pytest.mark.parametrize("norm", [False, True])
+def test_swiglu_epilogue(mods, t, ffn, k, norm):
+    """Interleaved gate / up tiles: y = up * silu(gate) straight from the projection,
+    against the float64 composition; the gate / up values themselves equal a plain
+    matmul over the interleaved weight, split back by ``split_interleaved``."""
+    pkg, glue = mods
+    gw, uw = _weight(pkg, t, ffn, k, seed=ffn + k), _weight(pkg, t, ffn, k, seed=ffn + k + 1)
+    w = pkg.interleave_tiles(gw, uw)
+    g = torch.Generator(device="cuda").manual_seed(ffn)
+    x = torch.randn(k, device="cuda", generator=g) * 2
+    nw = 1 + 0.1 * torch.randn(k, device="cuda", generator=g)
+    y = torch.full((ffn,), float("nan"), device="cuda")
+    if norm:
+        glue.matmul_fused(x, w, y, glue.PROLOGUE_RMSNORM, nw, 1e-5, epilogue=glue.EPILOGUE_SWIGLU)
+        xd = x.double()
+        h = xd / torch.sqrt((xd * xd).mean() + 1e-5) * nw.double()
+    else:
+        glue.matmul_fused(x, w, y, epilogue=glue.EPILOGUE_SWIGLU)
+        h = x.double()
+    gd, ud = gw.dequant().double(), uw.dequant().double()
+    gv, uv = gd @ h, ud @ h
+    ref = uv * gv / (1 + torch.exp(-gv))
+    # per element, relative to the magnitudes that enter: |d up| silu(g) + |up| |d silu(g)|
+    sg, su = gd.abs() @ h.abs(), ud.abs() @ h.abs()
+    bound = su * gv.abs() + uv.abs() * sg * 1.1
+    assert torch.isfinite(y).all()
+    assert ((y.double() - ref).abs() / bound).max().item() < 1e-6
+    # the raw rows: the interleaved matmul, split, equals the row-concatenated one
+    # (same number of row tiles, hence the same K split and summation order)
+    r = torch.empty(1, 2 * ffn, device="cuda")
+    pkg.dispatch_matmul_gguf(x.view(1, -1), w, r, 1, 2 * ffn, k)
+    c = torch.empty(1, 2 * ffn, device="cuda")
+    pkg.dispatch_matmul_gguf(x.view(1, -1), pkg.concat_rows(gw, uw), c, 1, 2 * ffn, k)
+    gs, us = pkg.split_interleaved(r)
+    assert torch.equal(gs, c[:, :ffn]) and torch.equal(us, c[:, ffn:])
+
+
 def test_plain_accumulate_matches_matmul(mods):
     pkg, glue = mods
     w = _weight(pkg, 12, 4096, 4096, seed=3)

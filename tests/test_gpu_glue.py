@@ -67,12 +67,18 @@ def test_attention_decode(lib, nh, nkv, hd, max_seq, p):
     cos, sin = ang.cos().float().cuda(), ang.sin().float().cuda()
     pos = torch.tensor([p], device="cuda")
     out = torch.empty(nh * hd, device="cuda")
-    work = torch.full(((lib.gguf_hip_attention_workspace(nh, nkv, hd, max_seq) + 3) // 4,),
-                      float("nan"), device="cuda")   # stale records must never be read
-    _ok(lib, lib.gguf_hip_attention_decode(qkv.data_ptr(), pos.data_ptr(), cos.data_ptr(),
-                                           sin.data_ptr(), kc.data_ptr(), vc.data_ptr(),
-                                           out.data_ptr(), nh, nkv, hd, max_seq, work.data_ptr(),
-                                           _s()))
+    nbytes = lib.gguf_hip_attention_workspace(nh, nkv, hd, max_seq)
+    work = torch.full(((nbytes + 3) // 4,), float("nan"), device="cuda")  # stale records
+    ctr = (nkv * 4 + 15) // 16 * 4           # counter words at the end, zero before first use
+    work.view(torch.int32)[-ctr:] = 0
+
+    def run(out_):
+        _ok(lib, lib.gguf_hip_attention_decode(qkv.data_ptr(), pos.data_ptr(), cos.data_ptr(),
+                                               sin.data_ptr(), kc.data_ptr(), vc.data_ptr(),
+                                               out_.data_ptr(), nh, nkv, hd, max_seq,
+                                               work.data_ptr(), _s()))
+    run(out)
+    assert not work.view(torch.int32)[-ctr:].any()        # every call leaves them at zero
     # float64 reference: complex-rotation RoPE, explicit softmax
     th = torch.tensor(float(p), dtype=torch.float64) * inv
     rot = lambda v: torch.view_as_real(  # noqa: E731
@@ -93,6 +99,10 @@ def test_attention_decode(lib, nh, nkv, hd, max_seq, p):
         e = torch.exp(s - s.max())
         ref[h] = (e / e.sum()) @ V[kv, :p + 1]
     assert torch.allclose(out.double().view(nh, hd), ref, rtol=1e-4, atol=2e-5)
+    # a second call on the same workspace (slot p rewritten with the same k / v) is identical
+    out2 = torch.empty_like(out)
+    run(out2)
+    assert torch.equal(out, out2) and not work.view(torch.int32)[-ctr:].any()
 
 
 def test_argmax_first_index_and_ties(lib):
