@@ -264,6 +264,7 @@ def traffic_from_profile():
 
 
 def secondary_cases(pkg, args, pool, secondary):
+    import torch
     only = set(filter(None, args.only.split(",")))
 
     def want(name):
@@ -303,6 +304,15 @@ def secondary_cases(pkg, args, pool, secondary):
         secondary["q6k_lm_head_weights"] = "random blocks with finite f16 scales"
         del lpool
     if want("prefill"):
+        # the vendor's plain fp16 GEMM (hipBLASLt through torch.matmul, timed eagerly, not in
+        # a graph) on the headline prefill shape: fp16 weights already dequantized, so a
+        # ceiling for reference only
+        xa = torch.randn(2048, 4096, device="cuda", dtype=torch.float16)
+        wa = torch.randn(14336, 4096, device="cuda", dtype=torch.float16) * 0.02
+        ms = min(eager_time(lambda i: torch.matmul(xa, wa.t()), 20, 3) for _ in range(3))
+        secondary["torch_fp16_gemm_m2048_n14336_tflops"] = round(2.0 * 2048 * 14336 * 4096 /
+                                                                 (ms * 1e-3) / 1e12, 1)
+        del xa, wa
         for mm, nn in ((512, 4096), (512, 14336), (8192, 4096), (8192, 14336)):
             ppool = pool[:2] if nn == 14336 else make_pool(pkg, t, nn, 4096, 2, seed=3)[0]
             r = matmul_case(pkg, t, mm, nn, 4096, ppool, 10, 2, xdtype="float16")
