@@ -738,15 +738,21 @@ hipError_t launch_t(const XT *x, int64_t ldx, const uint8_t *W, int N, int K, fl
 }
 
 // ---------------------------------------------------------------------------
-// M = 1: every weight unit a wave owns is requested at once.
+// M = 1: a wave's whole share of the weights sits in registers.
 //
 // A workgroup of NW waves (4, or 8 when K > 4096 or ks_n = 8) covers NW / ks_n
 // row tiles;
 // the ks_n waves of a tile split its units (wave ks takes units ks, ks + ks_n,
-// ...), at most U per wave, so one latency round brings a wave's whole share
-// of the weights.  The activation vector is requested before the weights (the
-// memory counter retires in issue order, so staging never waits on weight
-// bytes), staged once for all of K, and each unit is consumed as it arrives.
+// ...), at most U per wave.  The activation vector is requested before the
+// weights (the memory counter retires in issue order, so staging never waits
+// on weight bytes) and staged once for all of K.  DP units of each wave are in
+// flight at a time (DP = 0: all U at once), and each is consumed as it
+// arrives.  The depth matters when the grid is one round of waves: with every
+// unit of every wave requested at once (48 MB for a 4096 x 14336 Q6_K weight)
+// the memory system returns them in no useful order, a wave's first unit lands
+// as late as its last, and the decode runs after the transfer instead of
+// under it.  A few units per wave (about 12 MB over the chip) keep the
+// transfer at full rate and the arrivals in order.
 //
 // Fused variants for a decoder step (PRO, f32 activations only):
 //   PRO = 1  the input norm of the projection, rmsnorm(x) * w
@@ -766,7 +772,7 @@ hipError_t launch_t(const XT *x, int64_t ldx, const uint8_t *W, int N, int K, fl
 //      rows), and y[16 m + r] = up * silu(gate) (N / 2 outputs), so the FFN
 //      activation never takes a separate pass.
 // ---------------------------------------------------------------------------
-template <int TYPE, typename XT, int U, int XI, int PRO>
+template <int TYPE, typename XT, int U, int XI, int PRO, int DP>
 __global__ __launch_bounds__(512) void decode_m1_kernel(const XT *__restrict__ x,
                                                         const uint8_t *__restrict__ W, int N,
                                                         int K, float *__restrict__ y, int ks_n,
@@ -816,9 +822,13 @@ __global__ __launch_bounds__(512) void decode_m1_kernel(const XT *__restrict__ x
   const int tile_c = active ? tile : ntiles - 1;
   const __amdgpu_buffer_rsrc_t wrs = __builtin_amdgcn_make_buffer_rsrc(
       (void *)(W + (int64_t)tile_c * nu * TU), 0, nu * TU, kRsrcWord3);
-  Unit<TYPE> buf[U];
+  // D units in flight: slot j + D is requested once unit j is consumed.  The
+  // issue order is pinned (sched_barrier) because the memory counter retires
+  // in order.
+  constexpr int D = (DP == 0 || DP >= U) ? U : DP;
+  Unit<TYPE> buf[D];
 #pragma unroll
-  for (int j = 0; j < U; ++j) {
+  for (int j = 0; j < D; ++j) {
     const int u = ks + ks_n * j;
     const int uc = (j < iters && u < nu) ? u : nu - 1;
     load_unit(wrs, uc * TU, r, g, buf[j]);
@@ -858,8 +868,15 @@ __global__ __launch_bounds__(512) void decode_m1_kernel(const XT *__restrict__ x
     const int u = ks + ks_n * j;
     const bool valid = j < iters && u < nu;
     float t = 0.f;
-    unit_m1<PARTS>(buf[j], st, valid ? u : nu - 1, lane, t);
+    unit_m1<PARTS>(buf[j % D], st, valid ? u : nu - 1, lane, t);
     acc += valid ? t : 0.f;
+    if (j + D < U) {
+      const int un = ks + ks_n * (j + D);
+      const int ucn = (j + D < iters && un < nu) ? un : nu - 1;
+      __builtin_amdgcn_sched_barrier(0);
+      load_unit(wrs, ucn * TU, r, g, buf[j % D]);
+      __builtin_amdgcn_sched_barrier(0);
+    }
   }
   acc += __shfl_xor(acc, 16);  // the four lane groups of each row
   acc += __shfl_xor(acc, 32);
@@ -907,6 +924,19 @@ constexpr int m1_umax(bool tight) {
   return TYPE == 8 ? (tight ? 16 : 32) : (TYPE == 14 || TYPE == 13 || tight ? 8 : 16);
 }
 
+// Units in flight per wave for a grid of `waves` waves holding `per` units
+// of `unit_bytes` each: about 12 MB over the chip when the grid is one round
+// (at most 2048 resident waves), one unit when later rounds stream in behind
+// the first anyway.  0 = all of them (the transfer is small enough to issue
+// at once).
+constexpr double kM1Flight = 12.0 * 1024 * 1024;
+inline int m1_depth(int waves, int per, int unit_bytes) {
+  if (waves > 2 * 2048) return 1;
+  const int resident = waves < 2048 ? waves : 2048;
+  const int d = (int)(kM1Flight / ((double)resident * unit_bytes) + 0.5);
+  return d < 1 ? 1 : (d > 3 || d >= per ? 0 : d);
+}
+
 // Returns hipErrorNotSupported (nothing launched) when K is beyond the
 // one-shot staging (16384) or the units per wave exceed the register budget.
 template <int TYPE, typename XT, int PRO>
@@ -936,15 +966,16 @@ hipError_t launch_m1(const XT *x, const uint8_t *W, int N, int K, float *y, cons
                      (size_t)nw * 64 * 4 + kZeroHalves * 2 + (size_t)nthr * 4;
   if (lds > kMaxLds) return hipErrorNotSupported;
   const dim3 grid((unsigned)((ntiles + ts - 1) / ts)), block(nthr);
+  const int dp = m1_depth(grid.x * nw, per, Fmt<TYPE>::TU);
   // template U is clamped to the compile-time budget (runtime per <= umax already);
   // above 64 KB of dynamic LDS the kernel's limit is raised first (gfx950: 160 KB)
-#define GGUF_M1(UU, XX)                                                                          \
+#define GGUF_M1_K(UU, XX, DD)                                                                    \
   do {                                                                                           \
     auto kern = decode_m1_kernel<TYPE, XT,                                                       \
                                  ((UU) < m1_umax<TYPE>((XX) > 1 || (PRO != 0 && GGUF_M1_PRO_TIGHT)) \
                                       ? (UU)                                                     \
                                       : m1_umax<TYPE>((XX) > 1 || (PRO != 0 && GGUF_M1_PRO_TIGHT))), \
-                                 XX, PRO>;                                                       \
+                                 XX, PRO, DD>;                                                   \
     if (lds > 65536) {                                                                           \
       const hipError_t ea = hipFuncSetAttribute((const void *)kern,                              \
                                                 hipFuncAttributeMaxDynamicSharedMemorySize,      \
@@ -952,6 +983,13 @@ hipError_t launch_m1(const XT *x, const uint8_t *W, int N, int K, float *y, cons
       if (ea != hipSuccess) return ea;                                                           \
     }                                                                                            \
     hipLaunchKernelGGL(kern, grid, block, lds, s, x, W, N, K, y, ks, pw, eps, epi);              \
+  } while (0)
+#define GGUF_M1(UU, XX)                                                                          \
+  do {                                                                                           \
+    if (dp == 1) GGUF_M1_K(UU, XX, 1);                                                           \
+    else if (dp == 2) GGUF_M1_K(UU, XX, 2);                                                      \
+    else if (dp == 3) GGUF_M1_K(UU, XX, 3);                                                      \
+    else GGUF_M1_K(UU, XX, 0);                                                                   \
   } while (0)
   if (xi <= 1) {
     if (per <= 4) GGUF_M1(4, 1);
@@ -964,6 +1002,7 @@ hipError_t launch_m1(const XT *x, const uint8_t *W, int N, int K, float *y, cons
     else GGUF_M1(16, 2);
   }
 #undef GGUF_M1
+#undef GGUF_M1_K
   return hipGetLastError();
 }
 
