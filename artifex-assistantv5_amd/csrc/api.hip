@@ -300,7 +300,7 @@ int gguf_hip_attention_decode(const float *qkv, const int64_t *pos, const float 
                               void *work, void *stream) {
   int rc = check_attention(n_heads, n_kv_heads, head_dim, max_seq);
   if (rc) return rc;
-  if (!qkv || !pos || !cos_table || !sin_table || !k_cache || !v_cache || !out || !work)
+  if (!qkv || !pos || !cos_table || !sin_table || !k_cache || !v_cache || !work)
     return fail(GGUF_HIP_ERR_NULL, "[gguf-hip] null pointer");
   if (!aligned(qkv, 16) || !aligned(k_cache, 16) || !aligned(v_cache, 16) || !aligned(out, 4) ||
       !aligned(pos, 8) || !aligned(cos_table, 4) || !aligned(sin_table, 4) || !aligned(work, 16))
@@ -353,6 +353,31 @@ int gguf_hip_matmul_fused(const float *x, const void *tiles, int ggml_type, int6
     return fail(GGUF_HIP_ERR_SHAPE, "[gguf-hip] no fused kernel for N=%lld K=%lld type %d",
                 (long long)n, (long long)k, ggml_type);
   return hip_status(e, "fused matmul launch");
+}
+
+int gguf_hip_matmul_attn_merge(const void *work, const int64_t *pos, int n_heads, int n_kv_heads,
+                               int head_dim, int64_t max_seq, const void *tiles, int ggml_type,
+                               int64_t n, float *y, int epilogue, void *stream) {
+  int rc = check_attention(n_heads, n_kv_heads, head_dim, max_seq);
+  if (rc) return rc;
+  if ((rc = check_type(ggml_type))) return rc;
+  const int64_t k = (int64_t)n_heads * head_dim;
+  if ((rc = check_k(ggml_type, k))) return rc;
+  if (epilogue != GGUF_HIP_EPILOGUE_STORE && epilogue != GGUF_HIP_EPILOGUE_ACCUMULATE)
+    return fail(GGUF_HIP_ERR_SHAPE, "[gguf-hip] attention merge: epilogue %d not store / accumulate",
+                epilogue);
+  if (n < 0 || n > ((int64_t)1 << 30)) return fail(GGUF_HIP_ERR_SHAPE, "[gguf-hip] bad N");
+  if (n == 0) return ok();
+  if (!work || !pos || !tiles || !y) return fail(GGUF_HIP_ERR_NULL, "[gguf-hip] null pointer");
+  if (!aligned(work, 16) || !aligned(pos, 8) || !aligned(tiles, 16) || !aligned(y, 4))
+    return fail(GGUF_HIP_ERR_ALIGN, "[gguf-hip] attention merge buffers misaligned");
+  const gguf::AttnRecords ar{(const float *)work, pos, n_heads, n_kv_heads, head_dim, (int)max_seq};
+  const hipError_t e = gguf::launch_decode_attn_merge(ar, (const uint8_t *)tiles, ggml_type, n, y,
+                                                      epilogue, (hipStream_t)stream);
+  if (e == hipErrorNotSupported)
+    return fail(GGUF_HIP_ERR_SHAPE, "[gguf-hip] no merge kernel for N=%lld K=%lld type %d",
+                (long long)n, (long long)k, ggml_type);
+  return hip_status(e, "attention merge launch");
 }
 
 int gguf_hip_matmul(const void *x, int x_type, int64_t ldx, const void *tiles, int ggml_type,

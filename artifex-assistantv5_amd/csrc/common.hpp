@@ -159,6 +159,24 @@ __device__ __forceinline__ uint2 ldg8_stream(const void *p) {
 // ---------------------------------------------------------------------------
 namespace gguf {
 
+// Decode attention splits the causal range 0..p into workgroups of
+// kAttnSplit cache slots.  Each writes one partial-softmax record per query
+// head: o[hd] (the unnormalized sum_t e_t v_t), then m (the largest score) and
+// l (sum_t e_t, e_t = exp(score_t - m)), at a stride of hd + 4 floats, so
+// every record starts 16-byte aligned.  The record of KV head g, split s and
+// query head j of the group sits at ((g * S + s) * grp + j) * (hd + 4),
+// S = ceil(max_seq / kAttnSplit).  Records are merged in split order:
+//   M = max_s m_s,  w_s = exp(m_s - M),  L = sum_s w_s l_s,
+//   out = (sum_s w_s o_s) * (1 / L).
+constexpr int kAttnSplit = 64;
+constexpr int attn_record_stride(int hd) { return hd + 4; }
+struct AttnRecords {
+  const float *work;     // the records
+  const int64_t *pos;    // device position p; the range holds slots 0..p
+  int nh, nkv, hd;       // query heads, KV heads, head dim
+  int max_seq;
+};
+
 hipError_t launch_repack(const uint8_t *raw, int type, int64_t n_rows, int64_t k, uint8_t *tiles,
                          hipStream_t s);
 hipError_t launch_dequant(const uint8_t *tiles, int type, int64_t n_rows, int64_t k, float *out,
@@ -175,6 +193,8 @@ hipError_t launch_gemm(const void *x, int x_type, int64_t ldx, const uint8_t *ti
 hipError_t launch_decode_fused(const float *x, const uint8_t *tiles, int type, int64_t n,
                                int64_t k, float *y, int prologue, const float *pw, float eps,
                                int epilogue, hipStream_t s);
+hipError_t launch_decode_attn_merge(const AttnRecords &ar, const uint8_t *tiles, int type,
+                                   int64_t n, float *y, int epilogue, hipStream_t s);
 hipError_t launch_rmsnorm(float *x, const float *r, const float *w, float eps, float *y,
                           int64_t rows, int64_t n, hipStream_t s);
 hipError_t launch_swiglu(const float *gu, float *out, int64_t rows, int64_t ffn, hipStream_t s);

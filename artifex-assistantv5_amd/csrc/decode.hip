@@ -485,6 +485,7 @@ __device__ __forceinline__ void unit_compute(const Unit<8> &u, const Stage &st, 
 // before the weight loads they would otherwise queue behind, since the
 // vector-memory counter retires loads in issue order.
 constexpr int kItem = 16;
+constexpr int kMergeChunk = 8;  // attention records per item held in registers (merge prologue)
 
 struct XPre {
   float v[kItem];
@@ -764,6 +765,11 @@ hipError_t launch_t(const XT *x, int64_t ldx, const uint8_t *W, int N, int K, fl
 //            barrier, and nothing ahead of the staging writes;
 //   PRO = 2  x is a row [gate (K) | up (K)] and is replaced by up * silu(gate)
 //            (elementwise.wgsl:96-102);
+//   PRO = 3  x is the attention output, merged here from the partial-softmax
+//            records that the decode attention wrote (no merge pass of its
+//            own): each thread's item is a 16-element slice of one query
+//            head, and the records of the first kMergeChunk splits are
+//            requested with the activations, ahead of the weights;
 // and the epilogue `epi`:
 //   0  y = result;
 //   1  y += result (the residual add after the output and down projections);
@@ -777,7 +783,7 @@ __global__ __launch_bounds__(512) void decode_m1_kernel(const XT *__restrict__ x
                                                         const uint8_t *__restrict__ W, int N,
                                                         int K, float *__restrict__ y, int ks_n,
                                                         const float *__restrict__ pw, float eps,
-                                                        int epi) {
+                                                        int epi, AttnRecords ar) {
   constexpr int PARTS = sizeof(XT) == 4 ? 2 : 1;
   constexpr int UE = Fmt<TYPE>::UE, TU = Fmt<TYPE>::TU, GS = Dec<TYPE>::GS;
   const int nthr = blockDim.x;
@@ -806,13 +812,48 @@ __global__ __launch_bounds__(512) void decode_m1_kernel(const XT *__restrict__ x
   // activations first: item q = threadIdx.x + nthr * i of the K / 16 items
   const int per_row = K / kItem;
   float xv[XI][kItem];
-  float pv[PRO ? XI : 1][kItem];  // norm weights (PRO 1) or up values (PRO 2)
+  float pv[PRO == 1 || PRO == 2 ? XI : 1][kItem];  // norm weights (PRO 1) or up values (PRO 2)
 #pragma unroll
   for (int i = 0; i < XI; ++i) {
     const int q = (int)threadIdx.x + nthr * i;
-    load_item<XT>(x, 0, K, 0, per_row, per_row, q, xv[i]);
+    if constexpr (PRO != 3) load_item<XT>(x, 0, K, 0, per_row, per_row, q, xv[i]);
     if constexpr (PRO == 1) load_item<float>(pw, 0, K, 0, per_row, per_row, q, pv[i]);
     if constexpr (PRO == 2) load_item<float>((const float *)x + K, 0, K, 0, per_row, per_row, q, pv[i]);
+  }
+  // PRO 3: the item's 16-element slice of the first RC attention records of
+  // its query head (the slots past the range are not loaded and get weight
+  // zero), and where the rest would be
+  constexpr int RC = PRO == 3 ? kMergeChunk : 1;
+  float4 ro[PRO == 3 ? XI : 1][RC][4];
+  float2 rml[PRO == 3 ? XI : 1][RC];
+  const float *ro_base[PRO == 3 ? XI : 1], *rml_base[PRO == 3 ? XI : 1];
+  int mn = 0;              // records to merge: ceil((p + 1) / kAttnSplit), 0 for a bad p
+  int64_t rstride = 0;     // floats from one split's record to the next
+  if constexpr (PRO == 3) {
+    const int64_t p = ar.pos[0];
+    mn = (p >= 0 && p < ar.max_seq) ? (int)(p / kAttnSplit) + 1 : 0;
+    const int grp = ar.nh / ar.nkv, S = (ar.max_seq + kAttnSplit - 1) / kAttnSplit;
+    const int rs = attn_record_stride(ar.hd);
+    rstride = (int64_t)grp * rs;
+    const int last = mn > 0 ? mn - 1 : 0;
+#pragma unroll
+    for (int i = 0; i < XI; ++i) {
+      const int q = min((int)threadIdx.x + nthr * i, per_row - 1);
+      const int k0 = kItem * q, h = k0 / ar.hd, i0 = k0 - h * ar.hd;
+      const int gk = h / grp, jh = h - gk * grp;
+      const float *rec = ar.work + ((int64_t)gk * S * grp + jh) * rs;
+      ro_base[i] = rec + i0;
+      rml_base[i] = rec + ar.hd;
+#pragma unroll
+      for (int c = 0; c < RC; ++c) {
+        if (c > last) break;  // uniform: the loads of splits past the range are not issued
+        const int64_t off = (int64_t)c * rstride;
+        const float4 *o4 = (const float4 *)(ro_base[i] + off);
+#pragma unroll
+        for (int v = 0; v < 4; ++v) ro[i][c][v] = o4[v];
+        rml[i][c] = *(const float2 *)(rml_base[i] + off);
+      }
+    }
   }
 
   // Branch-free over the U slots, so that the compiler can interleave the
@@ -853,6 +894,42 @@ __global__ __launch_bounds__(512) void decode_m1_kernel(const XT *__restrict__ x
         const float gt = xv[i][e];
         xv[i][e] = pv[i][e] * (gt / (1.0f + expf(-gt)));
       }
+  }
+  if constexpr (PRO == 3) {  // merge in split order (attention_kernel's merge, same arithmetic)
+#pragma unroll
+    for (int i = 0; i < XI; ++i) {
+      float M = -INFINITY;
+#pragma unroll
+      for (int c = 0; c < RC; ++c)
+        if (c < mn) M = fmaxf(M, rml[i][c].x);
+      for (int s2 = RC; s2 < mn; ++s2) M = fmaxf(M, rml_base[i][s2 * rstride]);
+      float L = 0.f, a[kItem];
+#pragma unroll
+      for (int e = 0; e < kItem; ++e) a[e] = 0.f;
+#pragma unroll
+      for (int c = 0; c < RC; ++c) {
+        if (c >= mn) break;  // uniform; the slots past the range were never loaded
+        const float w = expf(rml[i][c].x - M);
+        L = fmaf(w, rml[i][c].y, L);
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          a[4 * v] = fmaf(w, ro[i][c][v].x, a[4 * v]);
+          a[4 * v + 1] = fmaf(w, ro[i][c][v].y, a[4 * v + 1]);
+          a[4 * v + 2] = fmaf(w, ro[i][c][v].z, a[4 * v + 2]);
+          a[4 * v + 3] = fmaf(w, ro[i][c][v].w, a[4 * v + 3]);
+        }
+      }
+      for (int s2 = RC; s2 < mn; ++s2) {  // ranges beyond RC splits: one record at a time
+        const float *rp = ro_base[i] + s2 * rstride, *ml = rml_base[i] + s2 * rstride;
+        const float w = expf(ml[0] - M);
+        L = fmaf(w, ml[1], L);
+#pragma unroll
+        for (int e = 0; e < kItem; ++e) a[e] = fmaf(w, rp[e], a[e]);
+      }
+      const float inv = 1.0f / L;  // no records (bad position): 0 * inf = NaN
+#pragma unroll
+      for (int e = 0; e < kItem; ++e) xv[i][e] = a[e] * inv;
+    }
   }
 #pragma unroll
   for (int i = 0; i < XI; ++i)
@@ -941,7 +1018,7 @@ inline int m1_depth(int waves, int per, int unit_bytes) {
 // one-shot staging (16384) or the units per wave exceed the register budget.
 template <int TYPE, typename XT, int PRO>
 hipError_t launch_m1(const XT *x, const uint8_t *W, int N, int K, float *y, const float *pw,
-                     float eps, int epi, hipStream_t s) {
+                     float eps, int epi, const AttnRecords &ar, hipStream_t s) {
   constexpr int UE = Fmt<TYPE>::UE, GS = Dec<TYPE>::GS;
   constexpr int PARTS = sizeof(XT) == 4 ? 2 : 1;
   const int ntiles = (N + 15) / 16, nu = K / UE;
@@ -982,7 +1059,7 @@ hipError_t launch_m1(const XT *x, const uint8_t *W, int N, int K, float *y, cons
                                                 (int)lds);                                       \
       if (ea != hipSuccess) return ea;                                                           \
     }                                                                                            \
-    hipLaunchKernelGGL(kern, grid, block, lds, s, x, W, N, K, y, ks, pw, eps, epi);              \
+    hipLaunchKernelGGL(kern, grid, block, lds, s, x, W, N, K, y, ks, pw, eps, epi, ar);          \
   } while (0)
 #define GGUF_M1(UU, XX)                                                                          \
   do {                                                                                           \
@@ -996,10 +1073,12 @@ hipError_t launch_m1(const XT *x, const uint8_t *W, int N, int K, float *y, cons
     else if (per <= 8) GGUF_M1(8, 1);
     else if (per <= 16) GGUF_M1(16, 1);
     else GGUF_M1(32, 1);
-  } else {
+  } else if constexpr (PRO != 3) {
     if (per <= 4) GGUF_M1(4, 2);
     else if (per <= 8) GGUF_M1(8, 2);
     else GGUF_M1(16, 2);
+  } else {
+    return hipErrorNotSupported;  // the merge prologue holds one item per thread
   }
 #undef GGUF_M1
 #undef GGUF_M1_K
@@ -1010,7 +1089,7 @@ template <int TYPE, typename XT>
 hipError_t launch_m(const XT *x, int64_t ldx, const uint8_t *W, int N, int K, float *y,
                     int64_t ldy, int M, hipStream_t s) {
   if (M == 1) {
-    const hipError_t e = launch_m1<TYPE, XT, 0>(x, W, N, K, y, nullptr, 0.f, 0, s);
+    const hipError_t e = launch_m1<TYPE, XT, 0>(x, W, N, K, y, nullptr, 0.f, 0, AttnRecords{}, s);
     if (e != hipErrorNotSupported) return e;
     return launch_t<TYPE, XT, 1, 1>(x, ldx, W, N, K, y, ldy, M, s);
   }
@@ -1036,16 +1115,30 @@ hipError_t launch_decode_fused(const float *x, const uint8_t *tiles, int type, i
                                int epi, hipStream_t s) {
 #define GGUF_FUSED(T)                                                                        \
   return prologue == 1   ? launch_m1<T, float, 1>(x, tiles, (int)n, (int)k, y, pw, eps,     \
-                                                  epi, s)                             \
+                                                  epi, AttnRecords{}, s)              \
          : prologue == 2 ? launch_m1<T, float, 2>(x, tiles, (int)n, (int)k, y, pw, eps,     \
-                                                  epi, s)                             \
+                                                  epi, AttnRecords{}, s)              \
                          : launch_m1<T, float, 0>(x, tiles, (int)n, (int)k, y, pw, eps,     \
-                                                  epi, s)
+                                                  epi, AttnRecords{}, s)
   if (type == 12) GGUF_FUSED(12);
   if (type == 13) GGUF_FUSED(13);
   if (type == 14) GGUF_FUSED(14);
   GGUF_FUSED(8);
 #undef GGUF_FUSED
+}
+
+// The attention output projection with the record merge as its prologue
+// (decode_m1_kernel, PRO 3): K = nh * hd.
+hipError_t launch_decode_attn_merge(const AttnRecords &ar, const uint8_t *tiles, int type,
+                                    int64_t n, float *y, int epi, hipStream_t s) {
+  const int k = ar.nh * ar.hd;
+#define GGUF_MERGE(T) \
+  return launch_m1<T, float, 3>(nullptr, tiles, (int)n, k, y, nullptr, 0.f, epi, ar, s)
+  if (type == 12) GGUF_MERGE(12);
+  if (type == 13) GGUF_MERGE(13);
+  if (type == 14) GGUF_MERGE(14);
+  GGUF_MERGE(8);
+#undef GGUF_MERGE
 }
 
 // Rows are processed in groups of at most 32 (one pass over the weights each).

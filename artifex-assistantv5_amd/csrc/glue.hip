@@ -132,12 +132,15 @@ __global__ __launch_bounds__(kGlueThreads) void swiglu_kernel(const float *__res
 // lane t owns slot t0 + t, a wave computes 64 dot products, one wave-wide
 // softmax reduction and sum_t p_t v_t reading V rows from LDS.
 //
-// With n = 1 the workgroup writes the output.  Otherwise it writes a record
-// (m, l, o[hd]) per query head to work[(g * S + sp) * grp + j], and the last
-// of the n workgroups to finish -- an atomic counter per KV head, kept in
-// the workspace and left at zero -- merges the n records in slot order, so
-// the result does not depend on which workgroup finishes last.
-constexpr int kSplit = 64;
+// With n = 1 the workgroup writes the output.  Otherwise it writes its
+// partial-softmax record per query head (layout and merge rule next to
+// kAttnSplit), and the last of the n workgroups to finish -- an atomic
+// counter per KV head, kept in the workspace and left at zero -- merges the n
+// records in split order, so the result does not depend on which workgroup
+// finishes last.  With out == nullptr every workgroup writes its records and
+// nothing is merged: the consumer (the output projection's merge prologue)
+// merges them with the same arithmetic.
+constexpr int kSplit = kAttnSplit;
 
 __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll
@@ -176,6 +179,8 @@ __global__ __launch_bounds__(kGlueThreads) void attention_kernel(
   const int tn = min(kSplit, T - t0);
   const int tp = p - t0;                   // row of slot p in this block when < kSplit
   const bool holds_p = tp < kSplit;
+  const bool rec_only = out == nullptr;
+  constexpr int RS = attn_record_stride(HD);
   float *kbase = kc + (int64_t)g * max_seq * HD, *vbase = vc + (int64_t)g * max_seq * HD;
   const float *crow = cs + (int64_t)p * half, *srow = sn + (int64_t)p * half;
 
@@ -287,23 +292,22 @@ __global__ __launch_bounds__(kGlueThreads) void attention_kernel(
     const float e = lane < tn ? expf(sc - m) : 0.f;
     const float l = wave_sum(e);
     pr[lane] = e;
-    float *rec = work + ((int64_t)(g * S + sp) * grp + j) * (HD + 2);
-    float *o_out = out + (int64_t)(g * grp + j) * HD;
+    const bool direct = n == 1 && !rec_only;
+    float *rec = work + ((int64_t)(g * S + sp) * grp + j) * RS;
+    float *o_out = direct ? out + (int64_t)(g * grp + j) * HD : rec;
+    const float inv = direct ? 1.0f / l : 1.0f;
     for (int i = lane; i < HD; i += 64) {
       float o = 0.f;
 #pragma unroll 8
       for (int t = 0; t < tn; ++t) o += pr[t] * vs[t * HD + i];
-      if (n == 1)
-        o_out[i] = o / l;
-      else
-        rec[2 + i] = o;
+      o_out[i] = o * inv;
     }
-    if (n > 1 && lane == 0) {
-      rec[0] = m;
-      rec[1] = l;
+    if (!direct && lane == 0) {
+      rec[HD] = m;
+      rec[HD + 1] = l;
     }
   }
-  if (n == 1) return;
+  if (n == 1 || rec_only) return;
 
   // 4. the last of the n workgroups of KV head g merges the records
   __threadfence();  // this workgroup's records are visible before it is counted
@@ -314,36 +318,40 @@ __global__ __launch_bounds__(kGlueThreads) void attention_kernel(
   __threadfence();  // every other workgroup's records are visible to the merge
   // wave w merges query heads w, w + 4, ...: lane s reads record s's (m, l),
   // so a chunk of 64 records costs one load round, and the weighted sums of
-  // the outputs issue their loads together
+  // the outputs issue their loads together.  L and the outputs accumulate in
+  // split order, as the merge prologue of the output projection does.
   constexpr int QO = HD / 64;  // outputs per lane
-  const int64_t stride = (int64_t)grp * (HD + 2);
+  const int64_t stride = (int64_t)grp * RS;
+  float *pl = ks;  // the K rows are consumed: per wave, the 64 (w_s, l_s) of a chunk
   for (int j = wave; j < grp; j += 4) {
-    const float *base = work + ((int64_t)g * S * grp + j) * (HD + 2);
+    const float *base = work + ((int64_t)g * S * grp + j) * RS;
     float M = -INFINITY;
     for (int s0 = 0; s0 < n; s0 += 64)
-      if (s0 + lane < n) M = fmaxf(M, base[(s0 + lane) * stride]);
+      if (s0 + lane < n) M = fmaxf(M, base[(s0 + lane) * stride + HD]);
     M = wave_max(M);
     float L = 0.f, o[QO];
 #pragma unroll
     for (int r = 0; r < QO; ++r) o[r] = 0.f;
     for (int s0 = 0; s0 < n; s0 += 64) {
-      float w = 0.f;
+      float w = 0.f, lv = 0.f;
       if (s0 + lane < n) {
         const float *rec = base + (s0 + lane) * stride;
-        w = expf(rec[0] - M);
-        L += w * rec[1];
+        w = expf(rec[HD] - M);
+        lv = rec[HD + 1];
       }
       pr[lane] = w;  // wave-local: read back in program order
+      pl[wave * 64 + lane] = lv;
       const int cnt = min(64, n - s0);
 #pragma unroll 8
       for (int u = 0; u < cnt; ++u) {
         const float wu = pr[u];
-        const float *ro = base + (s0 + u) * stride + 2 + lane;
+        L = fmaf(wu, pl[wave * 64 + u], L);
+        const float *ro = base + (s0 + u) * stride + lane;
 #pragma unroll
-        for (int r = 0; r < QO; ++r) o[r] += wu * ro[64 * r];
+        for (int r = 0; r < QO; ++r) o[r] = fmaf(wu, ro[64 * r], o[r]);
       }
     }
-    const float inv = 1.0f / wave_sum(L);
+    const float inv = 1.0f / L;
 #pragma unroll
     for (int r = 0; r < QO; ++r) out[(int64_t)(g * grp + j) * HD + lane + 64 * r] = o[r] * inv;
   }
@@ -421,10 +429,10 @@ hipError_t launch_swiglu(const float *gu, float *out, int64_t rows, int64_t ffn,
   return hipGetLastError();
 }
 
-// Workspace: the records [nkv][S][grp][hd + 2] floats, then nkv counters.
+// Workspace: the records [nkv][S][grp][hd + 4] floats, then nkv counters.
 static int64_t attention_record_bytes(int nh, int nkv, int hd, int64_t max_seq) {
   const int64_t S = (max_seq + kSplit - 1) / kSplit;
-  return ((int64_t)sizeof(float) * nkv * S * (nh / nkv) * (hd + 2) + 15) / 16 * 16;
+  return (int64_t)sizeof(float) * nkv * S * (nh / nkv) * attn_record_stride(hd);
 }
 
 int64_t attention_work_bytes(int nh, int nkv, int hd, int64_t max_seq) {

@@ -297,20 +297,27 @@ class QuantDecoder:
 
     def _step_fused(self, tok: torch.Tensor, pos: torch.Tensor) -> torch.Tensor:
         """Five launches per layer: Q/K/V projection with the input RMSNorm as its
-        prologue, attention, output projection accumulated into the residual,
-        gate/up projection with the FFN RMSNorm prologue and the SwiGLU epilogue
-        (interleaved gate / up tiles), down projection accumulated into the
-        residual.  With concatenated or split gate / up weights, SwiGLU runs as
-        the down projection's prologue instead."""
+        prologue, attention (partial-softmax records only), output projection
+        that merges the records as its prologue and accumulates into the
+        residual, gate/up projection with the FFN RMSNorm prologue and the
+        SwiGLU epilogue (interleaved gate / up tiles), down projection
+        accumulated into the residual.  With concatenated or split gate / up
+        weights, SwiGLU runs as the down projection's prologue instead; with
+        n_heads * head_dim above 8192 the attention merges its own records."""
         cfg, W = self.cfg, self.w
         x = self.b_x
+        merge = cfg.n_heads * cfg.head_dim <= 8192
         self._embed(tok, x)
         for l, lw in enumerate(W.layers):
             self._fused_slot(x, lw, "qkv", self.b_qkv, lw.attn_norm)
             glue.attention_decode(self.b_qkv, pos, self.cos, self.sin, self.k_cache[l],
-                                  self.v_cache[l], self.b_att, cfg.n_heads, cfg.n_kv_heads,
-                                  cfg.head_dim, self.w_att)
-            glue.matmul_fused(self.b_att, lw.o_gg, x, accumulate=True)
+                                  self.v_cache[l], None if merge else self.b_att, cfg.n_heads,
+                                  cfg.n_kv_heads, cfg.head_dim, self.w_att)
+            if merge:
+                glue.matmul_attn_merge(self.w_att, pos, lw.o_gg, x, cfg.n_heads, cfg.n_kv_heads,
+                                       cfg.head_dim, cfg.max_seq, accumulate=True)
+            else:
+                glue.matmul_fused(self.b_att, lw.o_gg, x, accumulate=True)
             gui = lw.get("gateUpI_gg")
             if gui is not None:
                 glue.matmul_fused(x, gui, self.b_a, glue.PROLOGUE_RMSNORM, lw.ffn_norm, cfg.eps,

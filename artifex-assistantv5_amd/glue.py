@@ -65,24 +65,54 @@ def attention_workspace(n_heads: int, n_kv_heads: int, head_dim: int, max_seq: i
     return torch.zeros((nbytes + 15) // 16 * 4, dtype=torch.float32, device=device)
 
 
-def attention_decode(qkv: torch.Tensor, pos: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor,
-                     k_cache: torch.Tensor, v_cache: torch.Tensor, out: torch.Tensor,
-                     n_heads: int, n_kv_heads: int, head_dim: int,
-                     work: torch.Tensor) -> torch.Tensor:
-    """RoPE + KV append at slot ``pos`` (device int64 [1]) + causal GQA attention."""
-    _f32(qkv, cos, sin, k_cache, v_cache, out)
-    if pos.dtype != torch.int64 or not pos.is_cuda:
-        raise ValueError("pos must be an int64 device tensor")
-    lib = _native.load_library()
-    need = lib.gguf_hip_attention_workspace(n_heads, n_kv_heads, head_dim, k_cache.shape[-2])
+def _check_attention_work(lib, work: torch.Tensor, n_heads: int, n_kv_heads: int,
+                          head_dim: int, max_seq: int) -> None:
+    need = _native.check(lib.gguf_hip_attention_workspace(n_heads, n_kv_heads, head_dim,
+                                                          max_seq), lib)
     if work.numel() * work.element_size() < need:
         raise ValueError(f"attention workspace holds {work.numel() * work.element_size()} bytes, "
                          f"needs {need}")
+
+
+def attention_decode(qkv: torch.Tensor, pos: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor,
+                     k_cache: torch.Tensor, v_cache: torch.Tensor, out: torch.Tensor | None,
+                     n_heads: int, n_kv_heads: int, head_dim: int,
+                     work: torch.Tensor) -> torch.Tensor | None:
+    """RoPE + KV append at slot ``pos`` (device int64 [1]) + causal GQA attention.
+    ``out=None`` writes only the partial-softmax records into ``work``, for
+    ``matmul_attn_merge`` to merge inside the output projection."""
+    _f32(qkv, cos, sin, k_cache, v_cache, *(() if out is None else (out,)))
+    if pos.dtype != torch.int64 or not pos.is_cuda:
+        raise ValueError("pos must be an int64 device tensor")
+    lib = _native.load_library()
+    _check_attention_work(lib, work, n_heads, n_kv_heads, head_dim, k_cache.shape[-2])
     _native.check(lib.gguf_hip_attention_decode(
         qkv.data_ptr(), pos.data_ptr(), cos.data_ptr(), sin.data_ptr(), k_cache.data_ptr(),
-        v_cache.data_ptr(), out.data_ptr(), n_heads, n_kv_heads, head_dim, k_cache.shape[-2],
-        work.data_ptr(), _s(out)), lib)
+        v_cache.data_ptr(), None if out is None else out.data_ptr(), n_heads, n_kv_heads,
+        head_dim, k_cache.shape[-2], work.data_ptr(), _s(qkv)), lib)
     return out
+
+
+def matmul_attn_merge(work: torch.Tensor, pos: torch.Tensor, w, y: torch.Tensor, n_heads: int,
+                      n_kv_heads: int, head_dim: int, max_seq: int,
+                      accumulate: bool = False) -> torch.Tensor:
+    """The attention output projection with the merge fused in: ``y = a @ dequant(w)^T``
+    (``y +=`` with ``accumulate``), a = the attention output merged from the
+    records that ``attention_decode(..., out=None, work=work)`` wrote for ``pos``.
+    ``w`` is a GGUFWeight with k = n_heads * head_dim."""
+    _f32(y)
+    if pos.dtype != torch.int64 or not pos.is_cuda:
+        raise ValueError("pos must be an int64 device tensor")
+    if w.k != n_heads * head_dim or y.numel() != w.n:
+        raise ValueError(f"matmul_attn_merge: weight {w.n}x{w.k} for {n_heads}x{head_dim} heads, "
+                         f"y has {y.numel()} elements")
+    lib = _native.load_library()
+    _check_attention_work(lib, work, n_heads, n_kv_heads, head_dim, max_seq)
+    _native.check(lib.gguf_hip_matmul_attn_merge(
+        work.data_ptr(), pos.data_ptr(), n_heads, n_kv_heads, head_dim, max_seq, w.ptr(),
+        w.ggml_type, w.n, y.data_ptr(), EPILOGUE_ACCUMULATE if accumulate else EPILOGUE_STORE,
+        _s(y)), lib)
+    return y
 
 
 def argmax_workspace(device) -> torch.Tensor:

@@ -43,7 +43,7 @@ extern "C" {
  * are exported (kernels and helpers cannot be interposed across libraries). */
 #pragma GCC visibility push(default)
 
-#define GGUF_HIP_ABI_VERSION 6
+#define GGUF_HIP_ABI_VERSION 7
 
 /* ggml type ids (gguf.ts:24-35); activation dtypes reuse F32 / F16. */
 #define GGUF_HIP_F32 0
@@ -198,7 +198,9 @@ int gguf_hip_swiglu(const float *gate_up, float *out, int64_t rows, int64_t ffn,
  * per-64-slot partial softmax records and one counter per KV head; it must be
  * zero-filled once before its first use, and every call leaves the counters
  * at zero again.  Calls that share a workspace must not overlap.  The
- * position is read on the device, so the call can be captured in a graph. */
+ * position is read on the device, so the call can be captured in a graph.
+ * out == NULL: only the records are written (no merge, counters untouched),
+ * for gguf_hip_matmul_attn_merge to merge inside the output projection. */
 int gguf_hip_attention_decode(const float *qkv, const int64_t *pos, const float *cos_table,
                               const float *sin_table, float *k_cache, float *v_cache, float *out,
                               int n_heads, int n_kv_heads, int head_dim, int64_t max_seq,
@@ -206,6 +208,20 @@ int gguf_hip_attention_decode(const float *qkv, const int64_t *pos, const float 
 
 /* Bytes of the gguf_hip_attention_decode workspace; negative on bad shapes. */
 int64_t gguf_hip_attention_workspace(int n_heads, int n_kv_heads, int head_dim, int64_t max_seq);
+
+/* The attention output projection of one decode position with the attention
+ * merge fused in: y (= or +=, epilogue STORE / ACCUMULATE) W . a, where a
+ * [n_heads * head_dim] is the attention output merged on the fly from the
+ * records that gguf_hip_attention_decode(..., out = NULL, work) wrote for
+ * position *pos -- the same arithmetic as that call's own merge, so y equals
+ * gguf_hip_matmul_fused(a, W, ..., PROLOGUE_NONE, ...) on its output.  Replaces
+ * the reference's attention-output and o-projection dispatches
+ * (forward-pass.ts:2925-3297) by one.  The shapes are those of the attention
+ * call; K = n_heads * head_dim <= 8192.  A position outside 0..max_seq - 1
+ * gives NaN outputs. */
+int gguf_hip_matmul_attn_merge(const void *work, const int64_t *pos, int n_heads, int n_kv_heads,
+                               int head_dim, int64_t max_seq, const void *tiles, int ggml_type,
+                               int64_t n, float *y, int epilogue, void *stream);
 
 /* *out = first index of the maximum of x[0..n) (NaN never wins); greedy
  * sampling.  `work`: gguf_hip_argmax_workspace() bytes of device memory

@@ -43,7 +43,7 @@ def native(pkg):
 
 def test_exports_every_declared_symbol(lib, native):
     names = _declared_functions()
-    assert len(names) == 19, names
+    assert len(names) == 20, names
     for n in names:
         assert hasattr(lib, n), n
         assert n in native.SIGNATURES, n
@@ -68,7 +68,7 @@ def test_constants_match_header(native):
 
 
 def test_abi_version(lib):
-    assert lib.gguf_hip_abi_version() == 6
+    assert lib.gguf_hip_abi_version() == 7
 
 
 def test_type_traits(lib, native):
@@ -204,14 +204,34 @@ def test_glue_errors(lib, native):
     assert att(None, b, c, c, a, a, b, 32, 8, 128, 512, wk, None) == native.ERR_NULL
     assert att(a, b, c, c, a, a, b, 32, 8, 128, 512, None, None) == native.ERR_NULL
     assert att(a + 4, b, c, c, a, a, b, 32, 8, 128, 512, wk, None) == native.ERR_ALIGN
-    # workspace: 8 KV heads x 8 slot ranges of 64 x 4 query heads x (128 + 2) floats
-    # records [nkv][S][grp][hd + 2] floats, then nkv counters (16-byte rounded)
-    assert lib.gguf_hip_attention_workspace(32, 8, 128, 512) == 8 * 8 * 4 * 130 * 4 + 32
+    # workspace: 8 KV heads x 8 slot ranges of 64 x 4 query heads x (128 + 4) floats
+    # records [nkv][S][grp][hd + 4] floats, then nkv counters (16-byte rounded)
+    assert lib.gguf_hip_attention_workspace(32, 8, 128, 512) == 8 * 8 * 4 * 132 * 4 + 32
+    assert lib.gguf_hip_attention_workspace(4, 2, 64, 65) == 2 * 2 * 2 * 68 * 4 + 16
     assert lib.gguf_hip_attention_workspace(32, 8, 100, 512) == native.ERR_SHAPE
     assert lib.gguf_hip_argmax_workspace() > 0
     assert lib.gguf_hip_argmax(a, 0, b, c, None) == native.ERR_SHAPE
     assert lib.gguf_hip_argmax(a, 10, b + 4, c, None) == native.ERR_ALIGN
     assert lib.gguf_hip_argmax(a, 10, b, None, None) == native.ERR_NULL
+
+
+def test_attn_merge_errors(lib, native):
+    f = lib.gguf_hip_matmul_attn_merge
+    wk, pos, w, y = 0x10000, 0x20000, 0x30000, 0x40000
+    assert f(wk, pos, 32, 5, 128, 512, w, 12, 64, y, 1, None) == native.ERR_SHAPE   # 32 % 5
+    assert f(wk, pos, 32, 8, 96, 512, w, 12, 64, y, 1, None) == native.ERR_SHAPE    # head_dim
+    assert f(wk, pos, 32, 8, 128, 0, w, 12, 64, y, 1, None) == native.ERR_SHAPE     # max_seq
+    assert f(wk, pos, 32, 8, 128, 512, w, 11, 64, y, 1, None) == native.ERR_TYPE
+    assert f(wk, pos, 3, 1, 64, 512, w, 12, 64, y, 1, None) == native.ERR_SHAPE     # K=192 % 256
+    assert f(wk, pos, 32, 8, 128, 512, w, 12, 64, y, 2, None) == native.ERR_SHAPE   # SwiGLU epi
+    assert "epilogue 2" in native.last_error(lib)
+    assert f(wk, pos, 64, 8, 256, 512, w, 12, 64, y, 1, None) == native.ERR_SHAPE   # K=16384
+    assert "no merge kernel" in native.last_error(lib)
+    assert f(None, pos, 32, 8, 128, 512, w, 12, 64, y, 1, None) == native.ERR_NULL
+    assert f(wk, None, 32, 8, 128, 512, w, 12, 64, y, 1, None) == native.ERR_NULL
+    assert f(wk + 4, pos, 32, 8, 128, 512, w, 12, 64, y, 1, None) == native.ERR_ALIGN
+    assert f(wk, pos + 4, 32, 8, 128, 512, w, 12, 64, y, 1, None) == native.ERR_ALIGN
+    assert f(None, None, 32, 8, 128, 512, None, 12, 0, None, 0, None) == 0          # N = 0
 
 
 def test_fused_matmul_errors(lib, native):
