@@ -741,7 +741,8 @@ hipError_t launch_t(const XT *x, int64_t ldx, const uint8_t *W, int N, int K, fl
 // ---------------------------------------------------------------------------
 // M = 1: a wave's whole share of the weights sits in registers.
 //
-// A workgroup of NW waves (4, or 8 when K > 4096 or ks_n = 8) covers NW / ks_n
+// A workgroup of NW waves (8 when K > 4096, ks_n = 8 or the grid has at least
+// 1536 waves, else 4) covers NW / ks_n
 // row tiles;
 // the ks_n waves of a tile split its units (wave ks takes units ks, ks + ks_n,
 // ...), at most U per wave.  The activation vector is requested before the
@@ -1034,7 +1035,10 @@ hipError_t launch_m1(const XT *x, const uint8_t *W, int N, int K, float *y, cons
     ks <<= 1;
   const int per = (nu + ks - 1) / ks;
   if (per > umax) return hipErrorNotSupported;
-  int nw = (long_k || ks > 4 || GGUF_M1_NW_MIN > 4) ? 8 : 4;
+  // 8 waves per workgroup (half as many workgroups staging the activations)
+  // once the grid keeps at least 192 of them; smaller grids keep 4 so that
+  // every CU gets a workgroup
+  int nw = (long_k || ks > 4 || GGUF_M1_NW_MIN > 4 || ntiles * ks >= 1536) ? 8 : 4;
   if (epi == 2 && nw / ks < 2) nw = 8;  // the SwiGLU epilogue pairs tiles 2m, 2m + 1
   const int nthr = 64 * nw, ts = nw / ks;
   if (epi == 2 && (ts < 2 || (ntiles & 1))) return hipErrorNotSupported;
