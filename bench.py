@@ -273,23 +273,23 @@ def secondary_cases(pkg, args, pool, secondary):
     t = 12
     if want("gemv_batch"):
         for mm in (8, 32):
-            r = matmul_case(pkg, t, mm, 14336, 4096, pool, 170, 5)
+            r = matmul_case(pkg, t, mm, 14336, 4096, pool, 170, 5, replays=3)
             secondary[f"q4k_decode_m{mm}_gate_up_gbs"] = round(r["gbs"], 1)
     if want("down"):
         dpool, _ = make_pool(pkg, t, 4096, 14336, args.pool, seed=2)
         for mm in (1, 8, 32):
-            r = matmul_case(pkg, t, mm, 4096, 14336, dpool, 170, 5)
+            r = matmul_case(pkg, t, mm, 4096, 14336, dpool, 170, 5, replays=3)
             secondary[f"q4k_decode_m{mm}_down_gbs"] = round(r["gbs"], 1)
         del dpool
     if want("q8"):
         qpool, _ = make_pool(pkg, 8, 4096, 4096, 32, seed=4)
-        r = matmul_case(pkg, 8, 1, 4096, 4096, qpool, 320, 10)
+        r = matmul_case(pkg, 8, 1, 4096, 4096, qpool, 320, 10, replays=3)
         secondary["q8_0_decode_m1_gbs"] = round(r["gbs"], 1)
         secondary["q8_0_decode_m1_frac_hbm"] = round(r["gbs"] / HBM_PEAK_GBS, 4)
         del qpool
     if want("q5k"):
         q5pool, _ = make_pool(pkg, 13, 14336, 4096, 14, seed=6)
-        r = matmul_case(pkg, 13, 1, 14336, 4096, q5pool, 280, 10)
+        r = matmul_case(pkg, 13, 1, 14336, 4096, q5pool, 280, 10, replays=3)
         secondary["q5k_decode_m1_gbs"] = round(r["gbs"], 1)
         secondary["q5k_decode_m1_frac_hbm"] = round(r["gbs"] / HBM_PEAK_GBS, 4)
         r = matmul_case(pkg, 13, 2048, 14336, 4096, q5pool[:2], 10, 2, xdtype="float16")
@@ -298,7 +298,7 @@ def secondary_cases(pkg, args, pool, secondary):
         del q5pool
     if want("lm_head"):
         lpool, _ = make_pool(pkg, 14, 151936, 4096, 2, seed=5, quantized=False)
-        r = matmul_case(pkg, 14, 1, 151936, 4096, lpool, 40, 3)
+        r = matmul_case(pkg, 14, 1, 151936, 4096, lpool, 40, 3, replays=3)
         secondary["q6k_lm_head_m1_gbs"] = round(r["gbs"], 1)
         secondary["q6k_lm_head_m1_frac_hbm"] = round(r["gbs"] / HBM_PEAK_GBS, 4)
         secondary["q6k_lm_head_weights"] = "random blocks with finite f16 scales"
