@@ -40,6 +40,18 @@ constexpr int kWave = 64;
 //                  [3328, 3360) d of row r at 3328 + 2 r
 //   Q8_0 ( 544 B)  [   0,   32) d of row r at 2 r
 //                  [  32,  544) piece (g, r) at 32 + (16 g + r) * 8: qs[8 g, +8)
+//   Q4_0, IQ4_NL (288 B)  [0, 32) d of row r at 2 r
+//                  [  32,  288) word (g, r) at 32 + (16 g + r) * 4: byte i holds the
+//                               4-bit codes of elements 8 g + i (low nibble) and
+//                               8 g + 4 + i (high nibble) of the block
+//   Q5_0 ( 352 B)  [   0,   32) d of row r at 2 r
+//                  [  32,   96) qh of row r at 32 + 4 r (bit k: fifth bit of element k)
+//                  [  96,  352) word (g, r) at 96 + (16 g + r) * 4, as Q4_0
+//
+// The 32-element block types (Q4_0, Q5_0, IQ4_NL; element k of a GGUF block
+// is the low nibble of qs[k] for k < 16, the high nibble of qs[k - 16] above)
+// are the only ones whose bytes are reordered inside a row's block: each lane's
+// eight codes sit in one word, in the order b32_codes unpacks.
 //
 // Byte offset of (tile t, unit u) = (t * units_per_row + u) * tile_unit_bytes.
 // No bytes are added: a tile is exactly 16 rows of GGUF blocks.
@@ -64,10 +76,90 @@ template <>
 struct Fmt<8> {  // Q8_0
   static constexpr int UE = 32, UB = 34, TU = 16 * 34;
 };
+template <>
+struct Fmt<2> {  // Q4_0
+  static constexpr int UE = 32, UB = 18, TU = 16 * 18;
+};
+template <>
+struct Fmt<6> {  // Q5_0
+  static constexpr int UE = 32, UB = 22, TU = 16 * 22;
+};
+template <>
+struct Fmt<20> {  // IQ4_NL
+  static constexpr int UE = 32, UB = 18, TU = 16 * 18;
+};
 
-__host__ __device__ inline int unit_elems(int type) { return type == 8 ? 32 : 256; }
+// 32-element block types whose codes are nibbles (b32_codes below).
+__host__ __device__ constexpr bool is_b32(int type) { return type == 2 || type == 6 || type == 20; }
+
+__host__ __device__ inline int unit_elems(int type) {
+  return (type == 8 || is_b32(type)) ? 32 : 256;
+}
 __host__ __device__ inline int unit_bytes(int type) {
-  return type == 8 ? 34 : (type == 12 ? 144 : (type == 13 ? 176 : 210));
+  return type == 8    ? 34
+         : type == 2  ? 18
+         : type == 6  ? 22
+         : type == 20 ? 18
+         : (type == 12 ? 144 : (type == 13 ? 176 : 210));
+}
+
+// Byte offset of the code words in a 32-element-block tile-unit.
+template <int TYPE>
+constexpr int b32_code_off() {
+  return TYPE == 6 ? 96 : 32;
+}
+// The unsigned code a block stores for value d * (code - offset): Q4_0
+// d * (q - 8), Q5_0 d * (q5 - 16), IQ4_NL d * kvalues[q] coded as
+// kvalues[q] + 128 (a table lookup in b32_codes), Q8_0 d * q coded as q + 128.
+template <int TYPE>
+constexpr float code_offset() {
+  return TYPE == 2 ? 8.f : (TYPE == 6 ? 16.f : 128.f);
+}
+
+// IQ4_NL's 16-entry codebook (kvalues_iq4nl, gguf-dequant.ts:29) plus 128,
+// four entries per little-endian word: entries 0-3, 4-7, 8-11, 12-15.
+constexpr uint32_t kIq4Tab0 = 0x3F2D1801u;  //   1,  24,  45,  63
+constexpr uint32_t kIq4Tab1 = 0x766A5D4Fu;  //  79,  93, 106, 118
+constexpr uint32_t kIq4Tab2 = 0xA6998D81u;  // 129, 141, 153, 166
+constexpr uint32_t kIq4Tab3 = 0xF1D9C5B5u;  // 181, 197, 217, 241
+
+// Four 4-bit indices (one per byte of s) -> their codebook codes (one per byte).
+__device__ __forceinline__ uint32_t iq4nl_lookup(uint32_t s) {
+  const uint32_t lo3 = s & 0x07070707u;
+  const uint32_t ra = __builtin_amdgcn_perm(kIq4Tab1, kIq4Tab0, lo3);  // entries 0-7
+  const uint32_t rb = __builtin_amdgcn_perm(kIq4Tab3, kIq4Tab2, lo3);  // entries 8-15
+  const uint32_t m8 = s & 0x08080808u;
+  const uint32_t sel = (m8 << 5) - (m8 >> 3);  // 0xFF in the bytes whose index is >= 8
+  return (rb & sel) | (ra & ~sel);
+}
+
+// The eight codes of a lane in a 32-element-block unit, from its code word q
+// (and, for Q5_0, its qh byte: bit i = fifth bit of the lane's element i), as
+// four words of 16-bit halves: w[0] = (e0, e2), w[1] = (e1, e3),
+// w[2] = (e4, e6), w[3] = (e5, e7) for the lane's elements e0..e7.
+template <int TYPE>
+__device__ __forceinline__ void b32_codes(uint32_t q, uint32_t qhb, uint32_t (&w)[4]) {
+  if constexpr (TYPE == 20) {
+    const uint32_t lo = iq4nl_lookup(q & 0x0F0F0F0Fu), hi = iq4nl_lookup((q >> 4) & 0x0F0F0F0Fu);
+    w[0] = lo & 0x00FF00FFu;
+    w[1] = (lo >> 8) & 0x00FF00FFu;
+    w[2] = hi & 0x00FF00FFu;
+    w[3] = (hi >> 8) & 0x00FF00FFu;
+  } else {
+    w[0] = q & 0x000F000Fu;
+    w[1] = (q >> 8) & 0x000F000Fu;
+    w[2] = (q >> 4) & 0x000F000Fu;
+    w[3] = (q >> 12) & 0x000F000Fu;
+    if constexpr (TYPE == 6) {
+      // bit i of qhb to bit 4 of the half holding element i: e0 / e2 sit at
+      // bits 4 / 20 of t, and the other words read t shifted by 1, 4 and 5
+      const uint32_t t = qhb * 0x00040010u;
+      w[0] |= t & 0x00100010u;
+      w[1] |= (t >> 1) & 0x00100010u;
+      w[2] |= (t >> 4) & 0x00100010u;
+      w[3] |= (t >> 5) & 0x00100010u;
+    }
+  }
 }
 
 // IEEE half bits -> f32 with the hardware converter (subnormals, Inf and NaN

@@ -59,6 +59,19 @@ struct Unit<8> {  // qs bytes 8g..8g+7, d
   uint2 q;
   uint32_t d;
 };
+// Q4_0 / Q5_0 / IQ4_NL: the lane's code word, d, and (Q5_0) the row's qh
+template <>
+struct Unit<2> {
+  uint32_t q, d;
+};
+template <>
+struct Unit<6> {
+  uint32_t q, d, qh;
+};
+template <>
+struct Unit<20> {
+  uint32_t q, d;
+};
 
 // Scale group size (elements sharing one scale) and units in flight per wave
 // (P; deepest for a single activation row, whose staged chunk is small).
@@ -89,9 +102,22 @@ template <>
 struct Dec<8> {
   static constexpr int GS = 32, P1 = GGUF_DECODE_P_Q8;
 };
+template <>
+struct Dec<2> {
+  static constexpr int GS = 32, P1 = GGUF_DECODE_P_Q8;
+};
+template <>
+struct Dec<6> {
+  static constexpr int GS = 32, P1 = GGUF_DECODE_P_Q8;
+};
+template <>
+struct Dec<20> {
+  static constexpr int GS = 32, P1 = GGUF_DECODE_P_Q8;
+};
 template <int TYPE, int MT, int MR>
 constexpr int decode_p() {
-  return MR == 1 ? Dec<TYPE>::P1 : (MT == 1 ? (Dec<TYPE>::P1 + 1) / 2 : (TYPE == 8 ? 4 : 1));
+  return MR == 1 ? Dec<TYPE>::P1
+                 : (MT == 1 ? (Dec<TYPE>::P1 + 1) / 2 : ((TYPE == 8 || is_b32(TYPE)) ? 4 : 1));
 }
 
 // Weight loads go through a buffer resource spanning the wave's row tile
@@ -144,12 +170,42 @@ __device__ __forceinline__ void load_unit(__amdgpu_buffer_rsrc_t rs, int soff, i
   u.q = bload8(rs, 32 + (16 * g + r) * 8, soff);
   u.d = bload2(rs, 2 * r, soff);
 }
+__device__ __forceinline__ uint32_t bload4(__amdgpu_buffer_rsrc_t rs, int voff, int soff) {
+  return (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(rs, voff, soff, kNT);
+}
+__device__ __forceinline__ void load_unit(__amdgpu_buffer_rsrc_t rs, int soff, int r, int g,
+                                          Unit<2> &u) {
+  u.q = bload4(rs, 32 + (16 * g + r) * 4, soff);
+  u.d = bload2(rs, 2 * r, soff);
+}
+__device__ __forceinline__ void load_unit(__amdgpu_buffer_rsrc_t rs, int soff, int r, int g,
+                                          Unit<6> &u) {
+  u.q = bload4(rs, 96 + (16 * g + r) * 4, soff);
+  u.d = bload2(rs, 2 * r, soff);
+  u.qh = bload4(rs, 32 + 4 * r, soff);
+}
+__device__ __forceinline__ void load_unit(__amdgpu_buffer_rsrc_t rs, int soff, int r, int g,
+                                          Unit<20> &u) {
+  u.q = bload4(rs, 32 + (16 * g + r) * 4, soff);
+  u.d = bload2(rs, 2 * r, soff);
+}
 
 __device__ __forceinline__ half8_t as_h8(uint32_t a, uint32_t b, uint32_t c, uint32_t d) {
   return __builtin_bit_cast(half8_t, make_uint4(a, b, c, d));
 }
 __device__ __forceinline__ half4_t as_h4(uint32_t a, uint32_t b) {
   return __builtin_bit_cast(half4_t, make_uint2(a, b));
+}
+
+// The B operand (codes, halves in the staged (0, 2, 1, 3) quad order) of a
+// 32-element-block unit for lane group g.
+template <int TYPE>
+__device__ __forceinline__ half8_t b32_operand(const Unit<TYPE> &u, int g) {
+  uint32_t qhb = 0;
+  if constexpr (TYPE == 6) qhb = (u.qh >> (8 * g)) & 0xFFu;
+  uint32_t w[4];
+  b32_codes<TYPE>(u.q, qhb, w);
+  return as_h8(w[0], w[1], w[2], w[3]);
 }
 
 // Dynamic LDS of the decode kernel.  Stage records offsets into it (not
@@ -358,6 +414,38 @@ __device__ __forceinline__ void unit_m1(const Unit<8> &u, const Stage &st, int u
   acc += g == 0 ? v : 0.f;
 }
 
+// Q4_0 / Q5_0 / IQ4_NL: as Q8_0, with the codes from the lane's word and the
+// type's code offset.
+template <int PARTS, int TYPE>
+__device__ __forceinline__ void unit_m1_b32(const Unit<TYPE> &u, const Stage &st, int ul, int lane,
+                                            float &acc) {
+  const int r = lane & 15, g = lane >> 4;
+  const bool live = r == 0 || (PARTS == 2 && r == 1);
+  const int pa = live ? st.xh + r * (st.xl - st.xh) + 32 * ul + 8 * g : st.zero;
+  const half8_t b = b32_operand<TYPE>(u, g);
+  float4_t D = {0.f, 0.f, 0.f, 0.f};
+  D = __builtin_amdgcn_mfma_f32_16x16x32_f16(lds_h8(pa), b, D, 0, 0, 0);
+  const float d = h2f(u.d);
+  const float v = (d * kTwo24) * (D[0] + D[1]) -
+                  (d * code_offset<TYPE>()) * lds_f(st.xs + ul * st.ms);
+  acc += g == 0 ? v : 0.f;
+}
+template <int PARTS>
+__device__ __forceinline__ void unit_m1(const Unit<2> &u, const Stage &st, int ul, int lane,
+                                        float &acc) {
+  unit_m1_b32<PARTS, 2>(u, st, ul, lane, acc);
+}
+template <int PARTS>
+__device__ __forceinline__ void unit_m1(const Unit<6> &u, const Stage &st, int ul, int lane,
+                                        float &acc) {
+  unit_m1_b32<PARTS, 6>(u, st, ul, lane, acc);
+}
+template <int PARTS>
+__device__ __forceinline__ void unit_m1(const Unit<20> &u, const Stage &st, int ul, int lane,
+                                        float &acc) {
+  unit_m1_b32<PARTS, 20>(u, st, ul, lane, acc);
+}
+
 // One unit of Q4_K / Q5_K: 8 sub-blocks x MT activation tiles.  Per
 // activation row the sub-block dots are folded as
 //   acc += d 2^24 sum_even sc_j D_j + d 2^20 sum_odd sc_j D_j - dmin sum_j m_j xs_j
@@ -476,6 +564,38 @@ __device__ __forceinline__ void unit_compute(const Unit<8> &u, const Stage &st, 
     const float4_t D = mfma32<PARTS>(st.xh + off, st.xl + off, st.zero, b, m < M);
     apply<MR>(acc[mt], D, sd, so, st.xs + ul * st.ms + 16 * mt + 4 * g);
   }
+}
+
+// One Q4_0 / Q5_0 / IQ4_NL block.
+template <int PARTS, int MT, int MR, int TYPE>
+__device__ __forceinline__ void unit_compute_b32(const Unit<TYPE> &u, const Stage &st, int ul,
+                                                 int lane, int M, float (&acc)[MT][4]) {
+  const int r = lane & 15, g = lane >> 4;
+  const half8_t b = b32_operand<TYPE>(u, g);
+  const float d = h2f(u.d);
+  const float sd = d * kTwo24, so = d * code_offset<TYPE>();
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) {
+    const int m = 16 * mt + r;
+    const int off = m * st.ld + 32 * ul + 8 * g;
+    const float4_t D = mfma32<PARTS>(st.xh + off, st.xl + off, st.zero, b, m < M);
+    apply<MR>(acc[mt], D, sd, so, st.xs + ul * st.ms + 16 * mt + 4 * g);
+  }
+}
+template <int PARTS, int MT, int MR>
+__device__ __forceinline__ void unit_compute(const Unit<2> &u, const Stage &st, int ul, int lane,
+                                             int M, float (&acc)[MT][4]) {
+  unit_compute_b32<PARTS, MT, MR, 2>(u, st, ul, lane, M, acc);
+}
+template <int PARTS, int MT, int MR>
+__device__ __forceinline__ void unit_compute(const Unit<6> &u, const Stage &st, int ul, int lane,
+                                             int M, float (&acc)[MT][4]) {
+  unit_compute_b32<PARTS, MT, MR, 6>(u, st, ul, lane, M, acc);
+}
+template <int PARTS, int MT, int MR>
+__device__ __forceinline__ void unit_compute(const Unit<20> &u, const Stage &st, int ul, int lane,
+                                             int M, float (&acc)[MT][4]) {
+  unit_compute_b32<PARTS, MT, MR, 20>(u, st, ul, lane, M, acc);
 }
 
 // Stage activations x[0:M, k0 : k0 + ce) into LDS (zeros past K).
@@ -986,8 +1106,8 @@ __global__ __launch_bounds__(512) void decode_m1_kernel(const XT *__restrict__ x
   if (ks == 0 && active && n < N && g == 0) y[n] = epi == 1 ? y[n] + acc : acc;
 }
 
-// Units per wave held in registers: with K <= 4096 the staged activations
-// take one item per thread; longer K (or a fused prologue) leaves less room.
+// Units per wave a kernel may own (K-quant units stay in registers whole; a
+// fused prologue or long K leaves less room for them).
 #ifndef GGUF_M1_PRO_TIGHT
 #define GGUF_M1_PRO_TIGHT 1  // a fused prologue takes the tight unit budget
 #endif
@@ -999,7 +1119,9 @@ __global__ __launch_bounds__(512) void decode_m1_kernel(const XT *__restrict__ x
 #endif
 template <int TYPE>
 constexpr int m1_umax(bool tight) {
-  return TYPE == 8 ? (tight ? 16 : 32) : (TYPE == 14 || TYPE == 13 || tight ? 8 : 16);
+  // 32-element blocks: up to 64 per wave (K = 16384 over 8 waves); past 32 at
+  // most 3 are in flight (m1_depth), so the register cost stays small
+  return (TYPE == 8 || is_b32(TYPE)) ? 64 : (TYPE == 14 || TYPE == 13 || tight ? 8 : 16);
 }
 
 // Units in flight per wave for a grid of `waves` waves holding `per` units
@@ -1012,7 +1134,9 @@ inline int m1_depth(int waves, int per, int unit_bytes) {
   if (waves > 2 * 2048) return 1;
   const int resident = waves < 2048 ? waves : 2048;
   const int d = (int)(kM1Flight / ((double)resident * unit_bytes) + 0.5);
-  return d < 1 ? 1 : (d > 3 || d >= per ? 0 : d);
+  if (d < 1) return 1;
+  if (d > 3 || d >= per) return per > 32 ? 3 : 0;  // more than 32 units never all in registers
+  return d;
 }
 
 // Returns hipErrorNotSupported (nothing launched) when K is beyond the
@@ -1076,11 +1200,14 @@ hipError_t launch_m1(const XT *x, const uint8_t *W, int N, int K, float *y, cons
     if (per <= 4) GGUF_M1(4, 1);
     else if (per <= 8) GGUF_M1(8, 1);
     else if (per <= 16) GGUF_M1(16, 1);
-    else GGUF_M1(32, 1);
+    else if (per <= 32) GGUF_M1(32, 1);
+    else GGUF_M1(64, 1);
   } else if constexpr (PRO != 3) {
     if (per <= 4) GGUF_M1(4, 2);
     else if (per <= 8) GGUF_M1(8, 2);
-    else GGUF_M1(16, 2);
+    else if (per <= 16) GGUF_M1(16, 2);
+    else if (per <= 32) GGUF_M1(32, 2);
+    else GGUF_M1(64, 2);
   } else {
     return hipErrorNotSupported;  // the merge prologue holds one item per thread
   }
@@ -1107,6 +1234,9 @@ hipError_t launch_x(const XT *x, int64_t ldx, const uint8_t *W, int type, int N,
   if (type == 12) return launch_m<12, XT>(x, ldx, W, N, K, y, ldy, M, s);
   if (type == 13) return launch_m<13, XT>(x, ldx, W, N, K, y, ldy, M, s);
   if (type == 14) return launch_m<14, XT>(x, ldx, W, N, K, y, ldy, M, s);
+  if (type == 2) return launch_m<2, XT>(x, ldx, W, N, K, y, ldy, M, s);
+  if (type == 6) return launch_m<6, XT>(x, ldx, W, N, K, y, ldy, M, s);
+  if (type == 20) return launch_m<20, XT>(x, ldx, W, N, K, y, ldy, M, s);
   return launch_m<8, XT>(x, ldx, W, N, K, y, ldy, M, s);
 }
 
@@ -1127,6 +1257,9 @@ hipError_t launch_decode_fused(const float *x, const uint8_t *tiles, int type, i
   if (type == 12) GGUF_FUSED(12);
   if (type == 13) GGUF_FUSED(13);
   if (type == 14) GGUF_FUSED(14);
+  if (type == 2) GGUF_FUSED(2);
+  if (type == 6) GGUF_FUSED(6);
+  if (type == 20) GGUF_FUSED(20);
   GGUF_FUSED(8);
 #undef GGUF_FUSED
 }
@@ -1141,6 +1274,9 @@ hipError_t launch_decode_attn_merge(const AttnRecords &ar, const uint8_t *tiles,
   if (type == 12) GGUF_MERGE(12);
   if (type == 13) GGUF_MERGE(13);
   if (type == 14) GGUF_MERGE(14);
+  if (type == 2) GGUF_MERGE(2);
+  if (type == 6) GGUF_MERGE(6);
+  if (type == 20) GGUF_MERGE(20);
   GGUF_MERGE(8);
 #undef GGUF_MERGE
 }

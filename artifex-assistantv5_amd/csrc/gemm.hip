@@ -119,6 +119,22 @@ struct BRaw<8> {
   uint2 q[kTN][2];  // block b of the step: 8 int8 codes
   uint32_t d[kTN][2];
 };
+template <>
+struct BRaw<2> {
+  uint32_t q[kTN][2];  // block b of the step: the lane's code word
+  uint32_t d[kTN][2];
+};
+template <>
+struct BRaw<20> {
+  uint32_t q[kTN][2];
+  uint32_t d[kTN][2];
+};
+template <>
+struct BRaw<6> {
+  uint32_t q[kTN][2];
+  uint32_t d[kTN][2];
+  uint32_t qh[kTN][2];  // the row's fifth bits of block b
+};
 
 // Per-superblock fields of row r, loaded with the superblock's first window.
 template <int TYPE>
@@ -203,6 +219,18 @@ template <>
 __device__ __forceinline__ BOff b_offsets<8>(int r, int g) {
   return BOff{32 + (16 * g + r) * 8, 2 * r, 0, 0};
 }
+template <>
+__device__ __forceinline__ BOff b_offsets<2>(int r, int g) {
+  return BOff{32 + (16 * g + r) * 4, 2 * r, 0, 0};
+}
+template <>
+__device__ __forceinline__ BOff b_offsets<20>(int r, int g) {
+  return BOff{32 + (16 * g + r) * 4, 2 * r, 0, 0};
+}
+template <>
+__device__ __forceinline__ BOff b_offsets<6>(int r, int g) {
+  return BOff{96 + (16 * g + r) * 4, 2 * r, 32 + 4 * r, 0};
+}
 
 // Loads for the 64-wide window c (0..3) of unit u (K-quants) or for blocks
 // 2u, 2u + 1 (Q8_0; c unused).  ts = bytes of one row tile.
@@ -269,6 +297,47 @@ __device__ __forceinline__ void load_b(rsrc_t rs, const BOff &o, int ts, int u, 
   }
 }
 
+// Q4_0 / Q5_0 / IQ4_NL: blocks 2u, 2u + 1 (as Q8_0).
+template <int C, int TYPE>
+__device__ __forceinline__ void load_b_b32(rsrc_t rs, const BOff &o, int ts, int u, int nu,
+                                           BRaw<TYPE> &b) {
+  constexpr int TU = Fmt<TYPE>::TU;
+#pragma unroll
+  for (int blk = 0; blk < 2; ++blk) {
+    const int ub = 2 * u + blk;
+    if (ub < nu) {  // uniform: K may end after the first block of the step
+#pragma unroll
+      for (int j = 0; j < kTN; ++j) {
+        b.q[j][blk] = bl4(rs, o.v0 + j * ts, ub * TU);
+        b.d[j][blk] = bl2(rs, o.v1 + j * ts, ub * TU);
+        if constexpr (TYPE == 6) b.qh[j][blk] = bl4(rs, o.v2 + j * ts, ub * TU);
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < kTN; ++j) {
+        b.q[j][blk] = 0;
+        b.d[j][blk] = 0;
+        if constexpr (TYPE == 6) b.qh[j][blk] = 0;
+      }
+    }
+  }
+}
+template <int C>
+__device__ __forceinline__ void load_b(rsrc_t rs, const BOff &o, int ts, int u, int nu,
+                                       BRaw<2> &b, BHdr<2> &) {
+  load_b_b32<C, 2>(rs, o, ts, u, nu, b);
+}
+template <int C>
+__device__ __forceinline__ void load_b(rsrc_t rs, const BOff &o, int ts, int u, int nu,
+                                       BRaw<6> &b, BHdr<6> &) {
+  load_b_b32<C, 6>(rs, o, ts, u, nu, b);
+}
+template <int C>
+__device__ __forceinline__ void load_b(rsrc_t rs, const BOff &o, int ts, int u, int nu,
+                                       BRaw<20> &b, BHdr<20> &) {
+  load_b_b32<C, 20>(rs, o, ts, u, nu, b);
+}
+
 // Q4_K / Q5_K: lane (r, g), window c = chunk c of the superblock: low
 // nibbles are sub-block 2c (k = 8 g .. 8 g + 7 of the first 32), high nibbles
 // sub-block 2c + 1.  Q5_K ORs the fifth bits into the codes first.
@@ -306,12 +375,12 @@ __device__ __forceinline__ void dequant_b_k(const BRaw<TYPE> &b, const BCur<TYPE
 
 template <int C>
 __device__ __forceinline__ void dequant_b(const BRaw<12> &b, const BCur<12> &h,
-                                          half8_t (&bf)[kTN][2]) {
+                                          half8_t (&bf)[kTN][2], int) {
   dequant_b_k<C, 12>(b, h, bf);
 }
 template <int C>
 __device__ __forceinline__ void dequant_b(const BRaw<13> &b, const BCur<13> &h,
-                                          half8_t (&bf)[kTN][2]) {
+                                          half8_t (&bf)[kTN][2], int) {
   dequant_b_k<C, 13>(b, h, bf);
 }
 
@@ -320,7 +389,7 @@ __device__ __forceinline__ void dequant_b(const BRaw<13> &b, const BCur<13> &h,
 // 32 t2 + 16 lh + 4 g + e at position 4 lh + e.
 template <int C>
 __device__ __forceinline__ void dequant_b(const BRaw<14> &b, const BCur<14> &h,
-                                          half8_t (&bf)[kTN][2]) {
+                                          half8_t (&bf)[kTN][2], int) {
   constexpr int HF = C >> 1, TP = C & 1;
 #pragma unroll
   for (int j = 0; j < kTN; ++j) {
@@ -357,7 +426,7 @@ __device__ __forceinline__ void dequant_b(const BRaw<14> &b, const BCur<14> &h,
 // Q8_0: block b of the step is k-block b; code + 128 enters as a subnormal.
 template <int C>
 __device__ __forceinline__ void dequant_b(const BRaw<8> &b, const BCur<8> &,
-                                          half8_t (&bf)[kTN][2]) {
+                                          half8_t (&bf)[kTN][2], int) {
 #pragma unroll
   for (int j = 0; j < kTN; ++j)
 #pragma unroll
@@ -376,6 +445,40 @@ __device__ __forceinline__ void dequant_b(const BRaw<8> &b, const BCur<8> &,
     }
 }
 
+// Q4_0 / Q5_0 / IQ4_NL: block b of the step is k-block b; the code (minus the
+// type's offset, times d) is dequantized in f32 and rounded once to fp16.
+template <int TYPE>
+__device__ __forceinline__ void dequant_b_b32(const BRaw<TYPE> &b, half8_t (&bf)[kTN][2], int g) {
+#pragma unroll
+  for (int j = 0; j < kTN; ++j)
+#pragma unroll
+    for (int blk = 0; blk < 2; ++blk) {
+      const float d = h2f(b.d[j][blk]);
+      const float s = d * kTwo24, c = -code_offset<TYPE>() * d;
+      uint32_t qhb = 0;
+      if constexpr (TYPE == 6) qhb = (b.qh[j][blk] >> (8 * g)) & 0xFFu;
+      uint32_t w[4];
+      b32_codes<TYPE>(b.q[j][blk], qhb, w);
+      bf[j][blk] = h8(mix_lo(w[0], w[1], s, c), mix_hi(w[0], w[1], s, c), mix_lo(w[2], w[3], s, c),
+                      mix_hi(w[2], w[3], s, c));
+    }
+}
+template <int C>
+__device__ __forceinline__ void dequant_b(const BRaw<2> &b, const BCur<2> &, half8_t (&bf)[kTN][2],
+                                          int g) {
+  dequant_b_b32<2>(b, bf, g);
+}
+template <int C>
+__device__ __forceinline__ void dequant_b(const BRaw<6> &b, const BCur<6> &, half8_t (&bf)[kTN][2],
+                                          int g) {
+  dequant_b_b32<6>(b, bf, g);
+}
+template <int C>
+__device__ __forceinline__ void dequant_b(const BRaw<20> &b, const BCur<20> &,
+                                          half8_t (&bf)[kTN][2], int g) {
+  dequant_b_b32<20>(b, bf, g);
+}
+
 // ---------------------------------------------------------------------------
 // Activations.  Thread t stages rows (t >> 3) + kARows i, i < kAI, 16-byte
 // column chunk t & 7 of the 64-wide step.
@@ -391,8 +494,8 @@ __device__ __forceinline__ void load_a(rsrc_t rs, int voff, int64_t ldxb, int k0
                                        ARaw<XT> &a) {
   constexpr int W = ARaw<XT>::W;
   const int soff = k0 * (int)sizeof(XT);
-  // only Q8_0 weights can end K halfway through a step; chunks past K read as zero
-  const bool ok = TYPE != 8 || k0 + 8 * cc < K;
+  // only 32-element-block weights can end K halfway through a step; chunks past K read as zero
+  const bool ok = (TYPE != 8 && !is_b32(TYPE)) || k0 + 8 * cc < K;
 #pragma unroll
   for (int i = 0; i < kAI; ++i)
 #pragma unroll
@@ -446,7 +549,7 @@ __device__ __forceinline__ void store_a(unsigned char *lds, int stage, int row0,
 template <int TYPE, typename XT>
 struct Gemm {
   rsrc_t ars, brs;
-  int avoff, row0, cc;
+  int avoff, row0, cc, lg;  // lg: the lane's group (lane >> 4)
   int64_t ldxb;
   int K, nu, ts;
   BOff bo;
@@ -468,7 +571,7 @@ struct Gemm {
   template <int C, int P>
   __device__ __forceinline__ void prepare(int stage) {
     if (C == 0) hc.set(hn);
-    dequant_b<C>(br[P], hc, bf);
+    dequant_b<C>(br[P], hc, bf, lg);
     store_a<TYPE, XT>(lds, stage, row0, cc, ar[P]);
   }
 
@@ -532,6 +635,7 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(const XT *__restrict__ x
   const int nt = __builtin_amdgcn_readfirstlane(max(0, min(kTN, ntiles - t0)));
   s.brs = make_rsrc(W + (int64_t)t0 * s.ts, (uint32_t)__builtin_amdgcn_readfirstlane(nt * s.ts));
   s.bo = b_offsets<TYPE>(r, g);
+  s.lg = g;
   // activation rows m0 .. m0 + rows - 1; rows past M are outside the resource
   const int rows = min(kBM, M - m0);
   s.ldxb = ldx * (int64_t)sizeof(XT);
@@ -607,6 +711,12 @@ hipError_t launch_x(const XT *x, int64_t ldx, const uint8_t *W, int type, int64_
     launch_type<13, XT>(x, ldx, W, (int)m, (int)n, (int)k, y, ldy, s);
   else if (type == 8)
     launch_type<8, XT>(x, ldx, W, (int)m, (int)n, (int)k, y, ldy, s);
+  else if (type == 2)
+    launch_type<2, XT>(x, ldx, W, (int)m, (int)n, (int)k, y, ldy, s);
+  else if (type == 6)
+    launch_type<6, XT>(x, ldx, W, (int)m, (int)n, (int)k, y, ldy, s);
+  else if (type == 20)
+    launch_type<20, XT>(x, ldx, W, (int)m, (int)n, (int)k, y, ldy, s);
   else
     launch_type<14, XT>(x, ldx, W, (int)m, (int)n, (int)k, y, ldy, s);
   return hipGetLastError();

@@ -1,8 +1,9 @@
 // Repack (raw GGUF bytes -> HBM row-tile layout) and dequantization to f32.
 //
 // Dequantization is bit-exact to the reference CPU dequant
-// (webgpu/src/model/gguf-dequant.ts:152-166 Q8_0, :255-281 Q4_K,
-// :369-399 Q6_K): every product in these formats is exact in f32, so the
+// (webgpu/src/model/gguf-dequant.ts:110-127 Q4_0, :130-149 Q5_0, :152-166 Q8_0,
+// :255-281 Q4_K, :283-314 Q5_K, :321-341 IQ4_NL, :369-399 Q6_K): every
+// product in these formats is exact in f32, so the
 // only rounding is the final Q4_K subtraction, which f32 arithmetic (fused
 // or not) rounds exactly once, as the reference's f64-then-Float32Array does.
 // The row-tile layout itself is described in common.hpp.
@@ -18,6 +19,26 @@ __device__ __forceinline__ uint32_t ld_u16_bytes(const uint8_t *p) {
 }
 __device__ __forceinline__ uint2 ld_u64_bytes(const uint8_t *p) {
   return make_uint2(ld_u32_bytes(p), ld_u32_bytes(p + 4));
+}
+
+// 4-bit code of element k (0..31) of a 32-element GGUF block: the low nibble
+// of qs[k] for k < 16, the high nibble of qs[k - 16] above
+// (gguf-dequant.ts:110-127, :130-149, :321-341).
+__device__ __forceinline__ uint32_t b32_code_of(const uint8_t *qs, int k) {
+  return k < 16 ? (qs[k] & 0x0Fu) : (qs[k - 16] >> 4);
+}
+
+// IQ4_NL codebook (kvalues_iq4nl, gguf-dequant.ts:29).
+__constant__ int8_t kIq4nl[16] = {-127, -104, -83, -65, -49, -35, -22, -10,
+                                  1,    13,   25,  38,  53,  69,  89,  113};
+
+// Value of element k of a Q4_0 / Q5_0 / IQ4_NL block with scale d, code q (4 bits) and
+// fifth bit h (Q5_0).  d * an integer of at most 8 bits: exact in f32.
+template <int TYPE>
+__device__ __forceinline__ float b32_value(float d, uint32_t q, uint32_t h) {
+  if constexpr (TYPE == 2) return d * (float)((int)q - 8);
+  if constexpr (TYPE == 6) return d * (float)((int)(q | (h << 4)) - 16);
+  return d * (float)kIq4nl[q];
 }
 
 // ---------------------------------------------------------------------------
@@ -48,6 +69,11 @@ __global__ __launch_bounds__(256) void repack_kernel(const uint8_t *__restrict__
       for (int p = 0; p < 12; ++p) *(uint4 *)(tu + (p * 16 + r) * 16) = z;
       *(uint4 *)(tu + 3072 + 16 * r) = z;
       *(uint16_t *)(tu + 3328 + 2 * r) = 0;
+    } else if (is_b32(TYPE)) {
+      *(uint16_t *)(tu + 2 * r) = 0;
+      if (TYPE == 6) *(uint32_t *)(tu + 32 + 4 * r) = 0u;
+#pragma unroll
+      for (int g = 0; g < 4; ++g) *(uint32_t *)(tu + b32_code_off<TYPE>() + (16 * g + r) * 4) = 0u;
     } else {
       *(uint16_t *)(tu + 2 * r) = 0;
 #pragma unroll
@@ -92,6 +118,18 @@ __global__ __launch_bounds__(256) void repack_kernel(const uint8_t *__restrict__
     *(uint4 *)(tu + 3072 + 16 * r) = make_uint4(ld_u32_bytes(sc), ld_u32_bytes(sc + 4),
                                                 ld_u32_bytes(sc + 8), ld_u32_bytes(sc + 12));
     *(uint16_t *)(tu + 3328 + 2 * r) = (uint16_t)ld_u16_bytes(src + 208);
+  } else if (is_b32(TYPE)) {  // Q4_0 / Q5_0 / IQ4_NL: codes regrouped per lane
+    *(uint16_t *)(tu + 2 * r) = (uint16_t)ld_u16_bytes(src);
+    if (TYPE == 6) *(uint32_t *)(tu + 32 + 4 * r) = ld_u32_bytes(src + 2);
+    const uint8_t *qs = src + (TYPE == 6 ? 6 : 2);
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      uint32_t w = 0;
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        w |= (b32_code_of(qs, 8 * g + i) | (b32_code_of(qs, 8 * g + 4 + i) << 4)) << (8 * i);
+      *(uint32_t *)(tu + b32_code_off<TYPE>() + (16 * g + r) * 4) = w;
+    }
   } else {  // Q8_0
     *(uint16_t *)(tu + 2 * r) = (uint16_t)ld_u16_bytes(src);
 #pragma unroll
@@ -111,6 +149,12 @@ hipError_t launch_repack(const uint8_t *raw, int type, int64_t n_rows, int64_t k
     hipLaunchKernelGGL(repack_kernel<13>, grid, block, 0, s, raw, n_rows, nu, n_pad, tiles);
   else if (type == 14)
     hipLaunchKernelGGL(repack_kernel<14>, grid, block, 0, s, raw, n_rows, nu, n_pad, tiles);
+  else if (type == 2)
+    hipLaunchKernelGGL(repack_kernel<2>, grid, block, 0, s, raw, n_rows, nu, n_pad, tiles);
+  else if (type == 6)
+    hipLaunchKernelGGL(repack_kernel<6>, grid, block, 0, s, raw, n_rows, nu, n_pad, tiles);
+  else if (type == 20)
+    hipLaunchKernelGGL(repack_kernel<20>, grid, block, 0, s, raw, n_rows, nu, n_pad, tiles);
   else
     hipLaunchKernelGGL(repack_kernel<8>, grid, block, 0, s, raw, n_rows, nu, n_pad, tiles);
   return hipGetLastError();
@@ -278,6 +322,32 @@ __global__ __launch_bounds__(256) void dequant_q8_0_kernel(const uint8_t *__rest
   }
 }
 
+// Q4_0 / Q5_0 / IQ4_NL: one thread per (row, block).
+template <int TYPE>
+__global__ __launch_bounds__(256) void dequant_b32_kernel(const uint8_t *__restrict__ tiles,
+                                                          int64_t n_rows, int nu,
+                                                          float *__restrict__ out, int64_t ldo) {
+  const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (gid >= n_rows * nu) return;
+  const int64_t n = gid / nu;
+  const int u = (int)(gid - n * nu);
+  const int r = (int)(n & 15);
+  const uint8_t *tu = tiles + ((n >> 4) * nu + u) * (int64_t)Fmt<TYPE>::TU;
+  const float d = h2f(*(const uint16_t *)(tu + 2 * r));
+  const uint32_t qh = TYPE == 6 ? *(const uint32_t *)(tu + 32 + 4 * r) : 0u;
+  float *o = out + n * ldo + 32 * (int64_t)u;
+#pragma unroll
+  for (int g = 0; g < 4; ++g) {
+    const uint32_t w = *(const uint32_t *)(tu + b32_code_off<TYPE>() + (16 * g + r) * 4);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int k = 8 * g + i;
+      const uint32_t q = (w >> (8 * (i & 3) + 4 * (i >> 2))) & 0x0Fu;
+      o[k] = b32_value<TYPE>(d, q, (qh >> k) & 1u);
+    }
+  }
+}
+
 hipError_t launch_dequant(const uint8_t *tiles, int type, int64_t n_rows, int64_t k, float *out,
                           int64_t ldo, hipStream_t s) {
   const int nu = (int)(k / unit_elems(type));
@@ -290,6 +360,12 @@ hipError_t launch_dequant(const uint8_t *tiles, int type, int64_t n_rows, int64_
     hipLaunchKernelGGL(dequant_q4_k_kernel<13>, grid, block, 0, s, tiles, n_rows, nu, out, ldo);
   else if (type == 14)
     hipLaunchKernelGGL(dequant_q6_k_kernel, grid, block, 0, s, tiles, n_rows, nu, out, ldo);
+  else if (type == 2)
+    hipLaunchKernelGGL(dequant_b32_kernel<2>, grid, block, 0, s, tiles, n_rows, nu, out, ldo);
+  else if (type == 6)
+    hipLaunchKernelGGL(dequant_b32_kernel<6>, grid, block, 0, s, tiles, n_rows, nu, out, ldo);
+  else if (type == 20)
+    hipLaunchKernelGGL(dequant_b32_kernel<20>, grid, block, 0, s, tiles, n_rows, nu, out, ldo);
   else
     hipLaunchKernelGGL(dequant_q8_0_kernel, grid, block, 0, s, tiles, n_rows, nu, out, ldo);
   return hipGetLastError();
@@ -349,9 +425,34 @@ __device__ __forceinline__ void raw_piece_q6_k(const uint8_t *blk, int hf, float
   }
 }
 
+// Q4_0 / Q5_0 / IQ4_NL block (32 values) from raw GGUF bytes.
+template <int TYPE>
+__device__ __forceinline__ void raw_piece_b32(const uint8_t *blk, float *o) {
+  const float d = h2f(ld_u16_bytes(blk));
+  const uint32_t qh = TYPE == 6 ? ld_u32_bytes(blk + 2) : 0u;
+  const uint8_t *qs = blk + (TYPE == 6 ? 6 : 2);
+#pragma unroll
+  for (int k = 0; k < 32; ++k) o[k] = b32_value<TYPE>(d, b32_code_of(qs, k), (qh >> k) & 1u);
+}
+
 // Pieces per 256-element superblock (per 32-element block for Q8_0) and values per piece.
 template <int TYPE>
 struct RawPiece;
+template <>
+struct RawPiece<2> {
+  static constexpr int PER_UNIT = 1, VALUES = 32;
+  __device__ static void run(const uint8_t *unit, int, float *o) { raw_piece_b32<2>(unit, o); }
+};
+template <>
+struct RawPiece<6> {
+  static constexpr int PER_UNIT = 1, VALUES = 32;
+  __device__ static void run(const uint8_t *unit, int, float *o) { raw_piece_b32<6>(unit, o); }
+};
+template <>
+struct RawPiece<20> {
+  static constexpr int PER_UNIT = 1, VALUES = 32;
+  __device__ static void run(const uint8_t *unit, int, float *o) { raw_piece_b32<20>(unit, o); }
+};
 template <>
 struct RawPiece<8> {
   static constexpr int PER_UNIT = 1, VALUES = 32;
@@ -420,6 +521,12 @@ hipError_t launch_dequant_raw(const uint8_t *raw, int type, int64_t n_elems, flo
                               hipStream_t s) {
   if (type == 8)
     dequant_raw_type<8>(raw, n_elems, out, s);
+  else if (type == 2)
+    dequant_raw_type<2>(raw, n_elems, out, s);
+  else if (type == 6)
+    dequant_raw_type<6>(raw, n_elems, out, s);
+  else if (type == 20)
+    dequant_raw_type<20>(raw, n_elems, out, s);
   else if (type == 12)
     dequant_raw_type<12>(raw, n_elems, out, s);
   else if (type == 13)
@@ -443,6 +550,12 @@ hipError_t launch_get_rows(const uint8_t *raw, int type, int64_t n_rows, int64_t
                            hipStream_t s) {
   if (type == 8)
     get_rows_type<8>(raw, n_rows, k, ids, n_ids, out, ldo, s);
+  else if (type == 2)
+    get_rows_type<2>(raw, n_rows, k, ids, n_ids, out, ldo, s);
+  else if (type == 6)
+    get_rows_type<6>(raw, n_rows, k, ids, n_ids, out, ldo, s);
+  else if (type == 20)
+    get_rows_type<20>(raw, n_rows, k, ids, n_ids, out, ldo, s);
   else if (type == 12)
     get_rows_type<12>(raw, n_rows, k, ids, n_ids, out, ldo, s);
   else if (type == 13)

@@ -9,10 +9,11 @@ The row-tile layout is this library's own (the reference pads blocks to
 4-byte strides for WGSL, ``gguf-dequant.ts:655-672``).  Rows are grouped in
 tiles of 16 consecutive rows (row-major weight, ``matmul_gguf.wgsl:5-8``;
 the last tile is zero-padded).  For each unit of K -- a 256-element
-superblock (Q4_K, Q6_K) or a 32-element block (Q8_0) -- a tile stores the 16
-rows' GGUF blocks interleaved at 16-byte granularity (8 bytes for Q8_0
-quants), so that one wave-wide load of a matrix-core operand reads
-contiguous HBM.  No bytes are added: a weight of ``N`` rows takes
+superblock (Q4_K, Q5_K, Q6_K) or a 32-element block (Q4_0, Q5_0, Q8_0,
+IQ4_NL) -- a tile stores the 16 rows' GGUF blocks interleaved at 16-byte
+granularity (8 bytes for Q8_0 quants, 4 for the nibble codes of the other
+32-element types, regrouped per lane), so that one wave-wide load of a
+matrix-core operand reads contiguous HBM.  No bytes are added: a weight of ``N`` rows takes
 ``round_up(N, 16) * raw_row_bytes(type, K)`` bytes.  The byte order inside a
 tile-unit is defined in ``csrc/common.hpp`` (and modelled in
 ``tests/tile_model.py``).
@@ -41,10 +42,13 @@ GGML_TYPE_NAMES = {v: k for k, v in GGML_TYPES.items()}
 F32 = GGML_TYPES["F32"]
 F16 = GGML_TYPES["F16"]
 BF16 = GGML_TYPES["BF16"]
+Q4_0 = GGML_TYPES["Q4_0"]
+Q5_0 = GGML_TYPES["Q5_0"]
 Q8_0 = GGML_TYPES["Q8_0"]
 Q4_K = GGML_TYPES["Q4_K"]
 Q5_K = GGML_TYPES["Q5_K"]
 Q6_K = GGML_TYPES["Q6_K"]
+IQ4_NL = GGML_TYPES["IQ4_NL"]
 
 # gguf.ts:39-73 — [elements per block, bytes per block]
 _TYPE_TRAITS = {
@@ -58,7 +62,7 @@ _TYPE_TRAITS = {
 }
 
 # Types the HIP kernels of this library decode.
-KERNEL_TYPES = (Q8_0, Q4_K, Q5_K, Q6_K)
+KERNEL_TYPES = (Q4_0, Q5_0, Q8_0, Q4_K, Q5_K, Q6_K, IQ4_NL)
 
 
 class GGMLTypeError(NotImplementedError):

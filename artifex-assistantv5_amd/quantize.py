@@ -17,6 +17,13 @@ split of Q6_K) with simpler scale searches:
   the sub-block).
 * Q6_K: per 16-element sub-block ``scale = max|w| / 31``; ``d = max|scale| /
   127`` (f16); int8 ``sc`` then ``q - 32`` in [-32, 31].
+* Q4_0 / Q5_0: ``d = v / -8`` (``/ -16``) per 32 elements, ``v`` the element
+  of largest magnitude (so that it maps to code 0); ``q = rint(w / d) + 8``
+  (``+ 16``) clipped to 4 (5) bits; element ``j`` of the block goes to the low
+  nibble of ``qs[j]`` for ``j < 16`` and to the high nibble of ``qs[j - 16]``
+  above, Q5_0's fifth bit of element ``j`` to bit ``j`` of ``qh``.
+* IQ4_NL: ``d = v / -127`` per 32 elements; each element takes the nearest
+  entry of the 16-value codebook (ties to the lower index); packed as Q4_0.
 
 All arithmetic is numpy f32; results depend only on the input values.
 """
@@ -25,7 +32,7 @@ from __future__ import annotations
 
 import numpy as np
 
-from .ggml import Q4_K, Q5_K, Q6_K, Q8_0
+from .ggml import IQ4_NL, Q4_0, Q4_K, Q5_0, Q5_K, Q6_K, Q8_0
 
 _CHUNK_ROWS = 4096
 
@@ -163,8 +170,64 @@ def _quantize_q6_k(w: np.ndarray) -> np.ndarray:
     return out.reshape(-1)
 
 
+# IQ4_NL codebook (kvalues_iq4nl; gguf-dequant.ts:29).
+IQ4NL_VALUES = np.array([-127, -104, -83, -65, -49, -35, -22, -10, 1, 13, 25, 38, 53, 69, 89, 113],
+                        np.int8)
+
+
+def _signed_absmax(b: np.ndarray) -> np.ndarray:
+    """The element of largest magnitude of each row (first on ties), keeping its sign."""
+    idx = np.abs(b).argmax(axis=1)
+    return b[np.arange(b.shape[0]), idx]
+
+
+def pack_nibbles32(q: np.ndarray) -> np.ndarray:
+    """4-bit codes (nb, 32) -> qs (nb, 16): element j < 16 in the low nibble of byte j,
+    element j + 16 in its high nibble."""
+    q = np.asarray(q, np.uint8)
+    return (q[:, :16] & 0x0F) | ((q[:, 16:] & 0x0F) << 4)
+
+
+def _quantize_q4_0(w: np.ndarray) -> np.ndarray:
+    b = w.reshape(-1, 32)
+    d16 = _f16(_signed_absmax(b) / np.float32(-8))
+    d = d16.astype(np.float32)[:, None]
+    q = np.clip(np.rint(_safe_div(b, d)) + 8, 0, 15).astype(np.uint8)
+    out = np.empty((b.shape[0], 18), np.uint8)
+    out[:, 0:2] = d16.view(np.uint8).reshape(-1, 2)
+    out[:, 2:18] = pack_nibbles32(q)
+    return out.reshape(-1)
+
+
+def _quantize_q5_0(w: np.ndarray) -> np.ndarray:
+    b = w.reshape(-1, 32)
+    d16 = _f16(_signed_absmax(b) / np.float32(-16))
+    d = d16.astype(np.float32)[:, None]
+    q = np.clip(np.rint(_safe_div(b, d)) + 16, 0, 31).astype(np.uint32)
+    qh = ((q >> 4) << np.arange(32, dtype=np.uint32)[None, :]).sum(axis=1, dtype=np.uint64)
+    out = np.empty((b.shape[0], 22), np.uint8)
+    out[:, 0:2] = d16.view(np.uint8).reshape(-1, 2)
+    out[:, 2:6] = qh.astype("<u4").view(np.uint8).reshape(-1, 4)
+    out[:, 6:22] = pack_nibbles32(q & 0x0F)
+    return out.reshape(-1)
+
+
+def _quantize_iq4_nl(w: np.ndarray) -> np.ndarray:
+    b = w.reshape(-1, 32)
+    d16 = _f16(_signed_absmax(b) / np.float32(-127))
+    d = d16.astype(np.float32)[:, None]
+    t = _safe_div(b, d)
+    q = np.abs(t[:, :, None] - IQ4NL_VALUES.astype(np.float32)[None, None, :]).argmin(axis=2)
+    out = np.empty((b.shape[0], 18), np.uint8)
+    out[:, 0:2] = d16.view(np.uint8).reshape(-1, 2)
+    out[:, 2:18] = pack_nibbles32(q)
+    return out.reshape(-1)
+
+
 _QUANTIZERS = {Q8_0: (32, 34, _quantize_q8_0), Q4_K: (256, 144, _quantize_q4_k),
-               Q5_K: (256, 176, _quantize_q5_k), Q6_K: (256, 210, _quantize_q6_k)}
+               Q5_K: (256, 176, _quantize_q5_k), Q6_K: (256, 210, _quantize_q6_k),
+               Q4_0: (32, 18, _quantize_q4_0), Q5_0: (32, 22, _quantize_q5_0),
+               IQ4_NL: (32, 18, _quantize_iq4_nl)}
 
 
 def quantize(w: np.ndarray, ggml_type: int) -> np.ndarray:

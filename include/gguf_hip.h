@@ -43,15 +43,18 @@ extern "C" {
  * are exported (kernels and helpers cannot be interposed across libraries). */
 #pragma GCC visibility push(default)
 
-#define GGUF_HIP_ABI_VERSION 7
+#define GGUF_HIP_ABI_VERSION 8
 
 /* ggml type ids (gguf.ts:24-35); activation dtypes reuse F32 / F16. */
 #define GGUF_HIP_F32 0
 #define GGUF_HIP_F16 1
+#define GGUF_HIP_Q4_0 2
+#define GGUF_HIP_Q5_0 6
 #define GGUF_HIP_Q8_0 8
 #define GGUF_HIP_Q4_K 12
 #define GGUF_HIP_Q5_K 13
 #define GGUF_HIP_Q6_K 14
+#define GGUF_HIP_IQ4_NL 20
 
 /* Error codes.  The Python host maps them onto the reference's throws:
  * TYPE -> NotImplementedError ("no pipeline for ggml type", forward-pass.ts:1524;

@@ -1,4 +1,4 @@
-"""CPU oracle for the GGUF Q8_0 / Q4_K / Q5_K / Q6_K dequant-matmul path.
+"""CPU oracle for the GGUF Q4_0 / Q5_0 / Q8_0 / IQ4_NL / Q4_K / Q5_K / Q6_K dequant-matmul path.
 
 TEST INFRASTRUCTURE ONLY.  This module is the checker: only ``tests/``,
 ``__graft_entry__.smoke()`` and the ``cpu_baseline`` leg of ``bench.py`` may
@@ -14,7 +14,8 @@ It restates the reference's CPU dequantization
   use them on small inputs only.
 * the vectorised numpy functions compute in f32.  They are bit-identical to
   the loops because every product in these formats is exact in f32 (Q8_0
-  ``d*q`` needs <= 18 significant bits, Q6_K ``d*sc*q`` <= 23, Q4_K
+  ``d*q`` needs <= 18 significant bits, Q4_0 / Q5_0 ``d*(q-8)`` / ``d*(q-16)``
+  <= 15 / 16, IQ4_NL ``d*kvalues[q]`` <= 18, Q6_K ``d*sc*q`` <= 23, Q4_K
   ``d*sc*q`` <= 21, Q5_K ``d*sc*q`` <= 22 and ``dmin*m`` <= 17) and the only
   rounding left is the final Q4_K / Q5_K subtraction, which f32 and
   f64-then-f32 both round correctly (the exact difference is a multiple of
@@ -28,6 +29,14 @@ Parity pins (all in ``tests/test_oracle.py``):
   and the Q6_K ql/qh split, in the package quantizer) round-tripping through
   the decoders, exhaustively over each scale slot;
 * special values: d = 0, f16 subnormal and Inf/NaN scales, Q6_K sc = -128.
+Q4_0, Q5_0 and IQ4_NL have no reference fixture: they are pinned by exact
+rational arithmetic over every code value, closed-form blocks (each element
+equal to d times a known integer), the nibble order checked element by
+element against the reference's documented rule (element j in the low
+nibble of ``qs[j]``, element j + 16 in its high nibble; Q5_0's fifth bit of
+element j in bit j of ``qh``), the package quantizer's round trip, and
+IQ4_NL's codebook cross-checked as the 16 values Q4_0-style code points take
+(kvalues_iq4nl, ``gguf-dequant.ts:29``).
 ``matmul_bt`` is pinned against numpy float64 products and linearity.
 """
 
@@ -38,6 +47,10 @@ import math
 import numpy as np
 
 T_F32, T_F16, T_Q8_0, T_Q4_K, T_Q5_K, T_Q6_K, T_BF16 = 0, 1, 8, 12, 13, 14, 30
+T_Q4_0, T_Q5_0, T_IQ4_NL = 2, 6, 20
+
+# kvalues_iq4nl, gguf-dequant.ts:29 (shared by IQ4_NL and IQ4_XS)
+KVALUES_IQ4NL = (-127, -104, -83, -65, -49, -35, -22, -10, 1, 13, 25, 38, 53, 69, 89, 113)
 
 # ---------------------------------------------------------------------------
 # Literal restatement (pure Python, f64 arithmetic, f32 store)
@@ -83,6 +96,54 @@ def dequant_q8_0_loop(data: bytes, n: int) -> np.ndarray:
         d = f16_to_f32(_u16(data, base))
         for i in range(32):
             out[b * 32 + i] = d * _i8(data[base + 2 + i])
+    return out
+
+
+def dequant_q4_0_loop(data: bytes, n: int) -> np.ndarray:
+    """gguf-dequant.ts:110-127."""
+    if n % 32 != 0:
+        raise ValueError(f"[Q4_0] n={n} not divisible by 32")
+    out = np.zeros(n, np.float32)
+    for b in range(n // 32):
+        base = b * 18
+        d = f16_to_f32(_u16(data, base))
+        for j in range(16):
+            q = data[base + 2 + j]
+            out[b * 32 + j] = d * ((q & 0xF) - 8)
+            out[b * 32 + j + 16] = d * ((q >> 4) - 8)
+    return out
+
+
+def dequant_q5_0_loop(data: bytes, n: int) -> np.ndarray:
+    """gguf-dequant.ts:130-149."""
+    if n % 32 != 0:
+        raise ValueError(f"[Q5_0] n={n} not divisible by 32")
+    out = np.zeros(n, np.float32)
+    for b in range(n // 32):
+        base = b * 22
+        d = f16_to_f32(_u16(data, base))
+        qh = _u16(data, base + 2) | (_u16(data, base + 4) << 16)
+        for j in range(16):
+            q = data[base + 6 + j]
+            lo = (q & 0xF) | (((qh >> j) & 1) << 4)
+            hi = (q >> 4) | (((qh >> (j + 16)) & 1) << 4)
+            out[b * 32 + j] = d * (lo - 16)
+            out[b * 32 + j + 16] = d * (hi - 16)
+    return out
+
+
+def dequant_iq4_nl_loop(data: bytes, n: int) -> np.ndarray:
+    """gguf-dequant.ts:321-341."""
+    if n % 32 != 0:
+        raise ValueError(f"[IQ4_NL] n={n} not divisible by 32")
+    out = np.zeros(n, np.float32)
+    for b in range(n // 32):
+        base = b * 18
+        d = f16_to_f32(_u16(data, base))
+        for j in range(16):
+            q = data[base + 2 + j]
+            out[b * 32 + j] = d * KVALUES_IQ4NL[q & 0xF]
+            out[b * 32 + j + 16] = d * KVALUES_IQ4NL[q >> 4]
     return out
 
 
@@ -184,6 +245,12 @@ def dequant_ggml_loop(ggml_type: int, data: bytes, n: int) -> np.ndarray:
         return u.view(np.float32).copy()
     if ggml_type == T_Q8_0:
         return dequant_q8_0_loop(data, n)
+    if ggml_type == T_Q4_0:
+        return dequant_q4_0_loop(data, n)
+    if ggml_type == T_Q5_0:
+        return dequant_q5_0_loop(data, n)
+    if ggml_type == T_IQ4_NL:
+        return dequant_iq4_nl_loop(data, n)
     if ggml_type == T_Q4_K:
         return dequant_q4_k_loop(data, n)
     if ggml_type == T_Q5_K:
@@ -204,6 +271,9 @@ Q5_K_BLOCK = np.dtype([("d", "<f2"), ("dmin", "<f2"), ("scales", "u1", 12), ("qh
 Q6_K_BLOCK = np.dtype([("ql", "u1", 128), ("qh", "u1", 64), ("sc", "i1", 16), ("d", "<f2")])
 assert Q8_0_BLOCK.itemsize == 34 and Q4_K_BLOCK.itemsize == 144 and Q6_K_BLOCK.itemsize == 210
 assert Q5_K_BLOCK.itemsize == 176
+Q4_0_BLOCK = np.dtype([("d", "<f2"), ("qs", "u1", 16)])           # also IQ4_NL
+Q5_0_BLOCK = np.dtype([("d", "<f2"), ("qh", "<u4"), ("qs", "u1", 16)])
+assert Q4_0_BLOCK.itemsize == 18 and Q5_0_BLOCK.itemsize == 22
 
 
 def _blocks(data, dtype: np.dtype, n: int, block: int, name: str) -> np.ndarray:
@@ -232,6 +302,37 @@ def dequant_q8_0(data, n: int) -> np.ndarray:
     blk = _blocks(data, Q8_0_BLOCK, n, 32, "Q8_0")
     d = blk["d"].astype(np.float32)[:, None]
     return (d * blk["qs"].astype(np.float32)).reshape(-1)
+
+
+def nibbles32(qs: np.ndarray) -> np.ndarray:
+    """4-bit codes of 32-element blocks in element order, (nb, 32): element j < 16 is the
+    low nibble of qs[j], element j + 16 the high nibble."""
+    return np.concatenate([qs & 0x0F, qs >> 4], axis=1)
+
+
+def dequant_q4_0(data, n: int) -> np.ndarray:
+    blk = _blocks(data, Q4_0_BLOCK, n, 32, "Q4_0")
+    d = blk["d"].astype(np.float32)[:, None]
+    return (d * (nibbles32(blk["qs"]).astype(np.float32) - 8)).reshape(-1)
+
+
+def q5_0_values(blk: np.ndarray) -> np.ndarray:
+    """Unsigned 5-bit codes of Q5_0 blocks in element order, (nb, 32)."""
+    bits = (blk["qh"][:, None] >> np.arange(32, dtype=np.uint32)[None, :]) & 1
+    return nibbles32(blk["qs"]).astype(np.uint32) | (bits << 4)
+
+
+def dequant_q5_0(data, n: int) -> np.ndarray:
+    blk = _blocks(data, Q5_0_BLOCK, n, 32, "Q5_0")
+    d = blk["d"].astype(np.float32)[:, None]
+    return (d * (q5_0_values(blk).astype(np.float32) - 16)).reshape(-1)
+
+
+def dequant_iq4_nl(data, n: int) -> np.ndarray:
+    blk = _blocks(data, Q4_0_BLOCK, n, 32, "IQ4_NL")
+    d = blk["d"].astype(np.float32)[:, None]
+    table = np.array(KVALUES_IQ4NL, np.float32)
+    return (d * table[nibbles32(blk["qs"])]).reshape(-1)
 
 
 def dequant_q4_k(data, n: int) -> np.ndarray:
@@ -296,6 +397,12 @@ def dequant_ggml(ggml_type: int, data, n: int) -> np.ndarray:
     """Vectorised dequantization of raw GGUF bytes to f32 (gguf-dequant.ts:844-868)."""
     if ggml_type == T_Q8_0:
         return dequant_q8_0(data, n)
+    if ggml_type == T_Q4_0:
+        return dequant_q4_0(data, n)
+    if ggml_type == T_Q5_0:
+        return dequant_q5_0(data, n)
+    if ggml_type == T_IQ4_NL:
+        return dequant_iq4_nl(data, n)
     if ggml_type == T_Q4_K:
         return dequant_q4_k(data, n)
     if ggml_type == T_Q5_K:

@@ -12,6 +12,9 @@
 3. ``synthetic_small.npz`` — seeded synthetic blocks for each type, with the
    oracle's dequantized values and f64 matmul results, so a change to the
    oracle or to the quantizer shows up as a fixture mismatch.
+4. ``iq4nl_codebook.json`` — the 16 entries of the IQ4_NL / IQ4_XS codebook
+   as the reference's CPU dequant declares them (``KVALUES_IQ4NL``,
+   ``webgpu/src/model/gguf-dequant.ts``).  Data only.
 
 Run from the repository root:  python tests/golden/make_golden.py [reference_root]
 """
@@ -74,13 +77,31 @@ def write_tensor_tables(ref_root: str) -> None:
     print(f"wrote tensor tables of {len(out)} files")
 
 
+def write_codebook(ref_root: str) -> None:
+    import re
+    path = os.path.join(ref_root, "webgpu", "src", "model", "gguf-dequant.ts")
+    with open(path, encoding="utf-8") as f:
+        lines = f.read().splitlines()
+    for no, line in enumerate(lines, 1):
+        m = re.search(r"KVALUES_IQ4NL\s*=\s*new Int8Array\(\[([^\]]*)\]\)", line)
+        if m:
+            vals = [int(v) for v in m.group(1).split(",")]
+            with open(os.path.join(HERE, "iq4nl_codebook.json"), "w", encoding="utf-8") as f:
+                json.dump({"source": f"webgpu/src/model/gguf-dequant.ts:{no}",
+                           "kvalues_iq4nl": vals}, f)
+            print(f"wrote the IQ4_NL codebook ({len(vals)} entries)")
+            return
+    raise RuntimeError("KVALUES_IQ4NL not found")
+
+
 def write_synthetic() -> None:
     sys.path.insert(0, ROOT)
     pkg = importlib.import_module("artifex-assistantv5_amd")
     from oracle import gguf_ref
 
     arrays = {}
-    for t, (n, k) in {8: (5, 96), 12: (3, 512), 13: (3, 512), 14: (3, 512)}.items():
+    for t, (n, k) in {8: (5, 96), 12: (3, 512), 13: (3, 512), 14: (3, 512), 2: (5, 96),
+                      6: (5, 96), 20: (5, 96)}.items():
         w = pkg.quantize.synthetic_weight(n, k, seed=1000 + t)
         raw = pkg.quantize.quantize(w, t)
         deq = gguf_ref.dequant_rows(t, raw, n, k)
@@ -99,4 +120,5 @@ if __name__ == "__main__":
     if os.path.isdir(ref):
         write_reference_samples(ref)
         write_tensor_tables(ref)
+        write_codebook(ref)
     write_synthetic()

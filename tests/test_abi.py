@@ -65,10 +65,11 @@ def test_constants_match_header(native):
     assert d["GGUF_HIP_DECODE_MAX_M"] == native.DECODE_MAX_M
     assert (d["GGUF_HIP_Q8_0"], d["GGUF_HIP_Q4_K"], d["GGUF_HIP_Q5_K"],
             d["GGUF_HIP_Q6_K"]) == (8, 12, 13, 14)
+    assert (d["GGUF_HIP_Q4_0"], d["GGUF_HIP_Q5_0"], d["GGUF_HIP_IQ4_NL"]) == (2, 6, 20)
 
 
 def test_abi_version(lib):
-    assert lib.gguf_hip_abi_version() == 7
+    assert lib.gguf_hip_abi_version() == 8
 
 
 def test_type_traits(lib, native):
@@ -80,12 +81,12 @@ def test_type_traits(lib, native):
 
 
 def test_byte_queries_agree_with_python(lib, pkg):
-    for t in (8, 12, 13, 14):
+    for t in (2, 6, 8, 12, 13, 14, 20):
         for k in (256, 512, 1024, 4096, 14336):
             assert lib.gguf_hip_tile_bytes(t, 7, k) == 16 * pkg.tile_row_bytes(t, k)
             assert lib.gguf_hip_tile_bytes(t, 33, k) == pkg.tiled_bytes(t, 33, k)
             assert lib.gguf_hip_raw_bytes(t, 7, k) == pkg.ggml_tensor_bytes(t, [k, 7])
-    assert lib.gguf_hip_tile_bytes(6, 1, 256) == -1    # Q5_0: known type, no kernel
+    assert lib.gguf_hip_tile_bytes(3, 1, 256) == -1    # Q4_1: known type, no kernel
     assert lib.gguf_hip_tile_bytes(8, 1, 48) == -2
 
 
@@ -108,8 +109,8 @@ def test_dequant_errors(lib, native):
     assert lib.gguf_hip_dequant(0x1004, 12, 1, 512, 0x2000, 512, None) == native.ERR_ALIGN
     assert lib.gguf_hip_dequant(0x1000, 12, 1, 512, 0x2002, 512, None) == native.ERR_ALIGN
     assert lib.gguf_hip_dequant(0x1000, 12, 2, 512, 0x2000, 256, None) == native.ERR_SHAPE
-    assert lib.gguf_hip_dequant(0x1000, 2, 1, 512, 0x2000, 512, None) == native.ERR_TYPE
-    assert "no kernel for ggml type 2" in native.last_error(lib)
+    assert lib.gguf_hip_dequant(0x1000, 3, 1, 512, 0x2000, 512, None) == native.ERR_TYPE
+    assert "no kernel for ggml type 3" in native.last_error(lib)
     assert lib.gguf_hip_dequant(0x1000, 14, 1, 100, 0x2000, 512, None) == native.ERR_SHAPE
     assert "not divisible by block size 256" in native.last_error(lib)
     assert lib.gguf_hip_dequant_raw(None, 8, 33, None, None) == native.ERR_SHAPE
@@ -120,7 +121,7 @@ def test_dequant_errors(lib, native):
 def test_get_rows_errors(lib, native):
     gr = lib.gguf_hip_get_rows
     raw, ids, out = 0x1000, 0x2000, 0x3000
-    assert gr(raw, 2, 4, 512, ids, 1, out, 512, None) == native.ERR_TYPE
+    assert gr(raw, 3, 4, 512, ids, 1, out, 512, None) == native.ERR_TYPE
     assert gr(raw, 12, 4, 300, ids, 1, out, 512, None) == native.ERR_SHAPE
     assert gr(raw, 12, -1, 512, ids, 1, out, 512, None) == native.ERR_SHAPE
     assert gr(raw, 12, 4, 512, ids, 2, out, 256, None) == native.ERR_SHAPE     # ldo < K

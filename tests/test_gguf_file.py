@@ -202,11 +202,11 @@ def test_loader_preflight_runs_before_any_device_work(tmp_path):
     loader = importlib.import_module("artifex-assistantv5_amd.gguf_loader")
     gmodel = importlib.import_module("artifex-assistantv5_amd.gguf_model")
     tensors = gm.make_model(seed=1)
-    p = str(tmp_path / "q50.gguf")
+    p = str(tmp_path / "q41.gguf")
     gm.write_model(p, tensors, extra_tensors=[
-        ("blk.0.odd.weight", [32, 2], 6, np.zeros(44, np.uint8)),
-        ("blk.1.odd.weight", [32, 2], 6, np.zeros(44, np.uint8))])
-    with pytest.raises(ValueError, match=r"can't run yet: Q5_0 \(2 tensors\)"):
+        ("blk.0.odd.weight", [32, 2], 3, np.zeros(40, np.uint8)),
+        ("blk.1.odd.weight", [32, 2], 3, np.zeros(40, np.uint8))])
+    with pytest.raises(ValueError, match=r"can't run yet: Q4_1 \(2 tensors\)"):
         loader.load_gguf_model(p, "cuda")
     p2 = str(tmp_path / "ok.gguf")
     gm.write_model(p2, tensors)

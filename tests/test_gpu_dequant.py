@@ -11,7 +11,11 @@ pytestmark = pytest.mark.gpu
 SHAPES = {8: [(1, 32), (3, 96), (5, 4096), (2, 160)],
           12: [(1, 256), (4, 768), (3, 4096), (2, 14336)],
           13: [(1, 256), (4, 768), (3, 4096), (2, 14336)],
-          14: [(1, 256), (4, 768), (3, 4096), (2, 14336)]}
+          14: [(1, 256), (4, 768), (3, 4096), (2, 14336)],
+          2: [(1, 32), (3, 96), (5, 4096), (2, 160)],
+          6: [(1, 32), (3, 96), (5, 4096), (2, 160)],
+          20: [(1, 32), (3, 96), (5, 4096), (2, 160)]}
+ALL = [2, 6, 8, 12, 13, 14, 20]
 
 
 def _dev_u8(a):
@@ -33,7 +37,7 @@ def test_golden_vectors_on_gpu(pkg, ref, golden_samples):
         assert ref.same_bits(got_raw, want), (s["tensor"], "raw")
 
 
-@pytest.mark.parametrize("t", [8, 12, 13, 14])
+@pytest.mark.parametrize("t", ALL)
 @pytest.mark.parametrize("specials", [False, True])
 def test_repack_layout_and_dequant_bit_exact(pkg, ref, t, specials):
     for i, (n, k) in enumerate(SHAPES[t]):
@@ -46,7 +50,7 @@ def test_repack_layout_and_dequant_bit_exact(pkg, ref, t, specials):
         assert ref.same_bits(pkg.dequant_raw(t, raw, n * k).cpu().numpy(), want.reshape(-1))
 
 
-@pytest.mark.parametrize("t", [8, 12, 13, 14])
+@pytest.mark.parametrize("t", ALL)
 def test_repack_from_unaligned_raw(pkg, ref, t):
     n, k = 3, 512
     raw = tile_model.random_blocks(t, n, k, seed=77)
@@ -59,7 +63,7 @@ def test_repack_from_unaligned_raw(pkg, ref, t):
                          ref.dequant_rows(t, raw, n, k).reshape(-1))
 
 
-@pytest.mark.parametrize("t", [8, 12, 13, 14])
+@pytest.mark.parametrize("t", ALL)
 def test_row_views_and_concat(pkg, ref, t):
     k = 512
     raw = tile_model.random_blocks(t, 40, k, seed=5)
@@ -75,7 +79,8 @@ def test_row_views_and_concat(pkg, ref, t):
 
 
 @pytest.mark.parametrize("t,n,k", [(12, 14336, 4096), (12, 4096, 14336), (14, 4096, 14336),
-                                   (8, 4096, 4096), (14, 151936, 4096)])
+                                   (8, 4096, 4096), (14, 151936, 4096), (2, 14336, 4096),
+                                   (6, 4096, 14336), (20, 4096, 4096)])
 def test_full_size_dequant(pkg, ref, t, n, k):
     """Full configuration sizes: repack+dequant equals raw dequant everywhere (GPU vs
     GPU, size independent) and equals the oracle on a sample of rows."""
@@ -85,7 +90,7 @@ def test_full_size_dequant(pkg, ref, t, n, k):
     raw_dev = torch.randint(0, 256, (n * rows_bytes,), dtype=torch.uint8, device="cuda")
     # stamp finite scales into every block on the device
     blocks = raw_dev.view(-1, size)
-    offs = {8: [0], 12: [0, 2], 13: [0, 2], 14: [208]}[t]
+    offs = {8: [0], 12: [0, 2], 13: [0, 2], 14: [208], 2: [0], 6: [0], 20: [0]}[t]
     for o in offs:
         vals = torch.empty(blocks.shape[0], device="cuda").uniform_(0.001, 0.01).half()
         blocks[:, o:o + 2] = vals.view(torch.uint8).view(-1, 2)

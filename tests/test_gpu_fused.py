@@ -32,7 +32,8 @@ def _elementwise(y, ref, wd, xd):
 
 
 @pytest.mark.parametrize("t,n,k", [(12, 6144, 4096), (12, 1000, 4096), (14, 4096, 14336),
-                                   (8, 512, 4096), (12, 4096, 14336), (14, 2048, 4096)])
+                                   (8, 512, 4096), (12, 4096, 14336), (14, 2048, 4096),
+                                   (2, 1000, 4096), (6, 512, 14336), (20, 2048, 4096)])
 def test_rmsnorm_prologue(mods, t, n, k):
     pkg, glue = mods
     w = _weight(pkg, t, n, k, seed=n + k)

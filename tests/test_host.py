@@ -30,7 +30,7 @@ def test_tensor_bytes(pkg):
         g.ggml_tensor_bytes(12, [100, 3])
 
 
-@pytest.mark.parametrize("t", [8, 12, 13, 14])
+@pytest.mark.parametrize("t", [2, 6, 8, 12, 13, 14, 20])
 @pytest.mark.parametrize("k", [256, 512, 768, 1280, 4096, 14336])
 def test_tile_row_bytes(pkg, t, k):
     trb = pkg.tile_row_bytes(t, k)
@@ -45,7 +45,7 @@ def test_tile_row_bytes_rejects(pkg):
     with pytest.raises(ValueError):
         pkg.tile_row_bytes(12, 100)
     with pytest.raises(NotImplementedError):
-        pkg.tile_row_bytes(6, 256)             # Q5_0: known type, no kernel
+        pkg.tile_row_bytes(3, 256)             # Q4_1: known type, no kernel
 
 
 def test_layout_model_is_a_permutation_of_each_tile_unit():
@@ -59,7 +59,8 @@ def test_layout_model_is_a_permutation_of_each_tile_unit():
     assert tile_model._unit_maps(8)[7, 0] == 14
 
 
-@pytest.mark.parametrize("t,k", [(8, 96), (8, 4096), (12, 512), (13, 1024), (14, 768), (14, 4096)])
+@pytest.mark.parametrize("t,k", [(8, 96), (8, 4096), (12, 512), (13, 1024), (14, 768), (14, 4096),
+                                 (2, 96), (6, 160), (20, 4096)])
 @pytest.mark.parametrize("n", [5, 16, 37])
 def test_layout_model_roundtrip(ref, t, k, n):
     raw = tile_model.random_blocks(t, n, k, seed=t + k)
@@ -74,7 +75,7 @@ def test_layout_model_roundtrip(ref, t, k, n):
     assert ref.same_bits(ref.dequant_rows(t, back, 5, k), ref.dequant_rows(t, raw, 5, k))
 
 
-@pytest.mark.parametrize("t", [8, 12, 13, 14])
+@pytest.mark.parametrize("t", [2, 6, 8, 12, 13, 14, 20])
 def test_quantize_deterministic_and_sized(pkg, t):
     w = pkg.quantize.synthetic_weight(3, 512, seed=11)
     a = pkg.quantize.quantize(w, t)
@@ -87,7 +88,7 @@ def test_quantize_rejects(pkg):
     with pytest.raises(ValueError):
         pkg.quantize.quantize(np.zeros((2, 100), np.float32), 12)
     with pytest.raises(NotImplementedError):
-        pkg.quantize.quantize(np.zeros((2, 256), np.float32), 6)
+        pkg.quantize.quantize(np.zeros((2, 256), np.float32), 3)       # Q4_1
 
 
 def test_synthetic_inputs_seeded(pkg):

@@ -15,12 +15,14 @@ from fractions import Fraction
 import numpy as np
 import pytest
 
-IN_SCOPE = (8, 12, 13, 14)
-BLOCK = {8: (32, 34), 12: (256, 144), 13: (256, 176), 14: (256, 210)}
-F16_FIELDS = {8: [0], 12: [0, 2], 13: [0, 2], 14: [208]}
+IN_SCOPE = (2, 6, 8, 12, 13, 14, 20)
+GOLDEN_TYPES = (8, 12, 13, 14)                 # the types the reference's gguf-py fixtures cover
+BLOCK = {8: (32, 34), 12: (256, 144), 13: (256, 176), 14: (256, 210), 2: (32, 18), 6: (32, 22),
+         20: (32, 18)}
+F16_FIELDS = {8: [0], 12: [0, 2], 13: [0, 2], 14: [208], 2: [0], 6: [0], 20: [0]}
 
 
-def _samples(golden_samples, types=IN_SCOPE):
+def _samples(golden_samples, types=GOLDEN_TYPES):
     return [s for s in golden_samples if s["ggml_type"] in types]
 
 
@@ -139,6 +141,52 @@ def exact_q6_k(raw: bytes) -> list:
     return out
 
 
+# Q4_0 / Q5_0 / IQ4_NL, from the documented element rule (gguf-dequant.ts:108-109,
+# :128-129, :318-320): element j < 16 is the low nibble of qs[j], element j + 16 its
+# high nibble; Q5_0's fifth bit of element j is bit j of the 32-bit qh.
+def _nib(qs: bytes, j: int) -> int:
+    return qs[j] & 15 if j < 16 else qs[j - 16] >> 4
+
+
+def exact_q4_0(raw: bytes) -> list:
+    out = []
+    for b in range(len(raw) // 18):
+        blk = raw[18 * b:18 * (b + 1)]
+        d = f16_fraction(blk[0] | blk[1] << 8)
+        out += [round_f32(d * (_nib(blk[2:], j) - 8)) for j in range(32)]
+    return out
+
+
+def exact_q5_0(raw: bytes) -> list:
+    out = []
+    for b in range(len(raw) // 22):
+        blk = raw[22 * b:22 * (b + 1)]
+        d = f16_fraction(blk[0] | blk[1] << 8)
+        qh = int.from_bytes(blk[2:6], "little")
+        out += [round_f32(d * ((_nib(blk[6:], j) | ((qh >> j) & 1) << 4) - 16)) for j in range(32)]
+    return out
+
+
+def exact_iq4_nl(raw: bytes, table=None) -> list:
+    table = table or IQ4NL_GOLDEN
+    out = []
+    for b in range(len(raw) // 18):
+        blk = raw[18 * b:18 * (b + 1)]
+        d = f16_fraction(blk[0] | blk[1] << 8)
+        out += [round_f32(d * table[_nib(blk[2:], j)]) for j in range(32)]
+    return out
+
+
+def _load_codebook():
+    import json
+    import os
+    with open(os.path.join(os.path.dirname(__file__), "golden", "iq4nl_codebook.json")) as f:
+        return json.load(f)["kvalues_iq4nl"]
+
+
+IQ4NL_GOLDEN = _load_codebook()
+
+
 def exact_q8_0(raw: bytes) -> list:
     out = []
     for b in range(len(raw) // 34):
@@ -163,7 +211,8 @@ def _random_blocks(t: int, nblocks: int, seed: int) -> bytes:
 
 
 @pytest.mark.parametrize("t,exact", [(8, exact_q8_0), (12, exact_q4_k), (13, exact_q5_k),
-                                     (14, exact_q6_k)])
+                                     (14, exact_q6_k), (2, exact_q4_0), (6, exact_q5_0),
+                                     (20, exact_iq4_nl)])
 def test_exact_rational(ref, t, exact):
     raw = _random_blocks(t, 12, seed=t)
     n = 12 * BLOCK[t][0]
@@ -283,7 +332,7 @@ def test_quantizer_error_is_bounded(ref, pkg, t):
     assert raw.size == 4 * 512 // BLOCK[t][0] * BLOCK[t][1]
     deq = ref.dequant_rows(t, raw, 4, 512)
     rel = np.linalg.norm(deq - w) / np.linalg.norm(w)
-    assert rel < {8: 0.01, 12: 0.12, 13: 0.06, 14: 0.05}[t]
+    assert rel < {8: 0.01, 12: 0.12, 13: 0.06, 14: 0.05, 2: 0.12, 6: 0.06, 20: 0.1}[t]
 
 
 # ---------------------------------------------------------------------------
@@ -400,3 +449,119 @@ def test_mutations_are_caught(ref, golden_samples):
     assert _golden_fails(ref, golden_samples, 14, q6_wrong_qh_shift)
     assert _golden_fails(ref, golden_samples, 14, q6_unsigned_scale)
     assert _golden_fails(ref, golden_samples, 8, q8_unsigned)
+
+
+# ---------------------------------------------------------------------------
+# Q4_0 / Q5_0 / IQ4_NL: no reference fixture; pinned by the element rule,
+# closed forms, the reference's codebook and the quantizer round trip
+# ---------------------------------------------------------------------------
+
+def test_iq4nl_codebook_matches_reference(ref):
+    # the fixture is read out of the reference's gguf-dequant.ts by make_golden.py
+    assert list(ref.KVALUES_IQ4NL) == IQ4NL_GOLDEN
+    assert len(set(IQ4NL_GOLDEN)) == 16 and IQ4NL_GOLDEN == sorted(IQ4NL_GOLDEN)
+
+
+def _block_with_codes(t, d_bits, codes, fifth=None):
+    """One raw block whose element j has 4-bit code codes[j] (and fifth bit fifth[j])."""
+    qs = bytes((codes[j] & 15) | ((codes[j + 16] & 15) << 4) for j in range(16))
+    head = struct.pack("<H", d_bits)
+    if t == 6:
+        qh = sum(int(b) << j for j, b in enumerate(fifth))
+        return head + struct.pack("<I", qh) + qs
+    return head + qs
+
+
+@pytest.mark.parametrize("t", [2, 6, 20])
+def test_small_block_element_order_closed_form(ref, t):
+    """Every element position with every code: value = d * (code - offset) (Q4_0, Q5_0) or
+    d * kvalues[code] (IQ4_NL), d = 0.5 -- so a swapped nibble, a shifted fifth bit or an
+    off-by-one offset moves at least one element."""
+    rng = random.Random(t)
+    for rep in range(20):
+        codes = [rng.randrange(16) for _ in range(32)]
+        fifth = [rng.randrange(2) for _ in range(32)]
+        raw = _block_with_codes(t, 0x3800, codes, fifth)
+        want = []
+        for j in range(32):
+            if t == 2:
+                want.append(0.5 * (codes[j] - 8))
+            elif t == 6:
+                want.append(0.5 * ((codes[j] | fifth[j] << 4) - 16))
+            else:
+                want.append(0.5 * IQ4NL_GOLDEN[codes[j]])
+        got = ref.dequant_ggml(t, raw, 32)
+        assert np.array_equal(got, np.array(want, np.float32)), (t, rep)
+        assert np.array_equal(ref.dequant_ggml_loop(t, raw, 32), got)
+
+
+def test_small_block_extremes(ref):
+    # Q4_0 code 0 -> -8 d, code 15 -> 7 d; Q5_0 31 -> 15 d, 0 -> -16 d; IQ4_NL 0 -> -127 d
+    one = 0x3C00
+    assert np.all(ref.dequant_ggml(2, _block_with_codes(2, one, [0] * 32), 32) == -8)
+    assert np.all(ref.dequant_ggml(2, _block_with_codes(2, one, [15] * 32), 32) == 7)
+    assert np.all(ref.dequant_ggml(6, _block_with_codes(6, one, [15] * 32, [1] * 32), 32) == 15)
+    assert np.all(ref.dequant_ggml(6, _block_with_codes(6, one, [0] * 32, [0] * 32), 32) == -16)
+    assert np.all(ref.dequant_ggml(20, _block_with_codes(20, one, [0] * 32), 32) == -127)
+    assert np.all(ref.dequant_ggml(20, _block_with_codes(20, one, [15] * 32), 32) == 113)
+    # subnormal d times the largest magnitude code is exact
+    v = ref.dequant_ggml(20, _block_with_codes(20, 0x0001, [0] * 32), 32)
+    assert np.all(v == np.float32(-127 * 2.0 ** -24))
+
+
+@pytest.mark.parametrize("t", [2, 6, 20])
+def test_small_block_quantizer_roundtrip(ref, pkg, t):
+    """The package quantizer (an independent encoder: own nibble packing, own qh
+    assembly, own codebook search) decodes to d times its chosen integers."""
+    w = pkg.quantize.synthetic_weight(3, 256, seed=21 + t)
+    raw = pkg.quantize.quantize(w, t)
+    b = w.reshape(-1, 32)
+    idx = np.abs(b).argmax(axis=1)
+    vmax = b[np.arange(b.shape[0]), idx]
+    div = {2: -8.0, 6: -16.0, 20: -127.0}[t]
+    d = (vmax / np.float32(div)).astype(np.float16).astype(np.float32)[:, None]
+    if t == 20:
+        tab = np.array(IQ4NL_GOLDEN, np.float32)
+        q = np.abs((b / d)[:, :, None] - tab[None, None, :]).argmin(axis=2)
+        want = d * tab[q]
+    else:
+        off = 8 if t == 2 else 16
+        q = np.clip(np.rint(b / d) + off, 0, 2 * off - 1)
+        want = d * (q - off)
+    assert np.array_equal(ref.dequant_rows(t, raw, 3, 256), want.reshape(3, 256).astype(np.float32))
+
+
+def test_small_block_mutations_are_caught(ref):
+    """Plausible oracle mistakes each fail the closed-form element pin."""
+    rng = random.Random(7)
+    codes = [rng.randrange(16) for _ in range(32)]
+    fifth = [rng.randrange(2) for _ in range(32)]
+
+    def fails(t, fn):
+        raw = _block_with_codes(t, 0x3800, codes, fifth)
+        return not np.array_equal(fn(raw), ref.dequant_ggml(t, raw, 32))
+
+    def q4_interleaved(raw):       # element 2j / 2j + 1 from byte j (llama.cpp-style misread)
+        qs = np.frombuffer(raw[2:], np.uint8)
+        q = np.stack([qs & 15, qs >> 4], axis=1).reshape(-1).astype(np.float32)
+        return np.float32(0.5) * (q - 8)
+
+    def q4_offset_7(raw):
+        qs = np.frombuffer(raw[2:], np.uint8)
+        return np.float32(0.5) * (ref.nibbles32(qs[None]).reshape(-1).astype(np.float32) - 7)
+
+    def q5_fifth_from_byte(raw):   # fifth bit of element j taken from bit j % 8 of qh byte j // 16
+        qh = raw[2:6]
+        qs = np.frombuffer(raw[6:], np.uint8)
+        nib = ref.nibbles32(qs[None]).reshape(-1)
+        bits = np.array([(qh[j // 16] >> (j % 8)) & 1 for j in range(32)])
+        return np.float32(0.5) * ((nib | (bits << 4)).astype(np.float32) - 16)
+
+    def iq4_reversed_table(raw):
+        qs = np.frombuffer(raw[2:], np.uint8)
+        tab = np.array(IQ4NL_GOLDEN[::-1], np.float32)
+        return np.float32(0.5) * tab[ref.nibbles32(qs[None]).reshape(-1)]
+
+    assert fails(2, q4_interleaved) and fails(2, q4_offset_7)
+    assert fails(6, q5_fifth_from_byte)
+    assert fails(20, iq4_reversed_table)

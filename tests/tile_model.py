@@ -12,11 +12,17 @@ block) a tile stores the 16 rows' GGUF blocks interleaved:
   dword 3i = ql[64 hf + 16 lh + 4 g, +4), 3i+1 = ql[64 hf + 32 + 16 lh + 4 g, +4),
   3i+2 = qh[32 hf + 16 lh + 4 g, +4) for i = 2 hf + lh; scales at 3072 + 16 r; d at 3328 + 2 r
 * Q8_0: d at 2 r, then piece (g, r) at 32 + (16 g + r) 8 = qs[8 g, +8)
+* Q4_0 / IQ4_NL: d at 2 r, then word (g, r) at 32 + (16 g + r) 4 whose byte i holds the
+  codes of block elements 8 g + i (low nibble) and 8 g + 4 + i (high nibble); element j
+  of a GGUF block is the low nibble of qs[j] (j < 16) or the high nibble of qs[j - 16]
+* Q5_0: d at 2 r, qh at 32 + 4 r, then the code words at 96 + (16 g + r) 4 as Q4_0
 """
 
 import numpy as np
 
-BLOCK = {8: (32, 34), 12: (256, 144), 13: (256, 176), 14: (256, 210)}
+BLOCK = {8: (32, 34), 12: (256, 144), 13: (256, 176), 14: (256, 210), 2: (32, 18), 6: (32, 22),
+         20: (32, 18)}
+SMALL = (2, 6, 20)          # nibble codes regrouped per lane (not a byte permutation)
 
 
 def tile_row_bytes(t, k):
@@ -69,9 +75,56 @@ def _unit_maps(t):
     return pos
 
 
+def _small_to_unit(t, blk):
+    """(..., 16 rows, UB) raw blocks -> (..., 16 * UB) tile-unit bytes."""
+    sh = blk.shape[:-2]
+    out = np.zeros(sh + (16 * BLOCK[t][1],), np.uint8)
+    qs = blk[..., 6:] if t == 6 else blk[..., 2:]
+    codes = np.concatenate([qs & 15, qs >> 4], axis=-1)          # (..., 16, 32) element order
+    off = 96 if t == 6 else 32
+    for r in range(16):
+        out[..., 2 * r:2 * r + 2] = blk[..., r, 0:2]
+        if t == 6:
+            out[..., 32 + 4 * r:36 + 4 * r] = blk[..., r, 2:6]
+        for g in range(4):
+            base = off + (16 * g + r) * 4
+            for i in range(4):
+                out[..., base + i] = codes[..., r, 8 * g + i] | (codes[..., r, 8 * g + 4 + i] << 4)
+    return out
+
+
+def _small_from_unit(t, tu):
+    """Inverse of _small_to_unit: (..., 16 * UB) -> (..., 16, UB)."""
+    sh = tu.shape[:-1]
+    ub = BLOCK[t][1]
+    blk = np.zeros(sh + (16, ub), np.uint8)
+    off = 96 if t == 6 else 32
+    for r in range(16):
+        blk[..., r, 0:2] = tu[..., 2 * r:2 * r + 2]
+        if t == 6:
+            blk[..., r, 2:6] = tu[..., 32 + 4 * r:36 + 4 * r]
+        codes = np.zeros(sh + (32,), np.uint8)
+        for g in range(4):
+            base = off + (16 * g + r) * 4
+            for i in range(4):
+                b = tu[..., base + i]
+                codes[..., 8 * g + i] = b & 15
+                codes[..., 8 * g + 4 + i] = b >> 4
+        q0 = 6 if t == 6 else 2
+        blk[..., r, q0:q0 + 16] = codes[..., :16] | (codes[..., 16:] << 4)
+    return blk
+
+
 def to_tiles(t, raw, n, k):
     """Raw GGUF bytes of an [n, k] tensor -> row-tile layout bytes."""
     block, ub = BLOCK[t]
+    if t in SMALL:
+        nu = k // block
+        npad = tiled_rows(n)
+        rows = np.zeros((npad, nu, ub), np.uint8)
+        rows[:n] = np.asarray(raw, np.uint8).reshape(n, nu, ub)
+        grp = rows.reshape(npad // 16, 16, nu, ub).transpose(0, 2, 1, 3)   # (tiles, nu, 16, ub)
+        return _small_to_unit(t, grp).reshape(-1)
     nu = k // block
     npad = tiled_rows(n)
     rows = np.zeros((npad, nu, ub), np.uint8)
@@ -86,6 +139,12 @@ def to_tiles(t, raw, n, k):
 def from_tiles(t, tiles, n, k):
     """Inverse of ``to_tiles`` (drops the padding rows)."""
     block, ub = BLOCK[t]
+    if t in SMALL:
+        nu = k // block
+        npad = tiled_rows(n)
+        tl = np.asarray(tiles, np.uint8).reshape(npad // 16, nu, 16 * ub)
+        rows = _small_from_unit(t, tl).transpose(0, 2, 1, 3).reshape(npad, nu, ub)
+        return rows[:n].reshape(-1)
     nu = k // block
     npad = tiled_rows(n)
     tl = np.asarray(tiles, np.uint8).reshape(npad // 16, nu, 16 * ub)
@@ -103,7 +162,7 @@ def random_blocks(t, n, k, seed, specials=False):
     block, size = BLOCK[t]
     nb = n * (k // block)
     raw = rng.integers(0, 256, (nb, size), dtype=np.uint8)
-    offs = {8: [0], 12: [0, 2], 13: [0, 2], 14: [208]}[t]
+    offs = {8: [0], 12: [0, 2], 13: [0, 2], 14: [208], 2: [0], 6: [0], 20: [0]}[t]
     for o in offs:
         vals = (rng.uniform(-0.01, 0.01, nb) if t not in (12, 13) or o == 0
                 else rng.uniform(0, 0.005, nb))
