@@ -1120,10 +1120,13 @@ __global__ __launch_bounds__(512) void decode_m1_kernel(const XT *__restrict__ x
 template <int TYPE>
 constexpr int m1_umax(bool tight) {
   // 32-element blocks: up to 64 per wave (K = 16384 over 8 waves); past 32 at
-  // most 3 are in flight (m1_depth), so the register cost stays small
+  // most GGUF_M1_DEEP are in flight (m1_depth), so the register cost stays small
   return (TYPE == 8 || is_b32(TYPE)) ? 64 : (TYPE == 14 || TYPE == 13 || tight ? 8 : 16);
 }
 
+#ifndef GGUF_M1_DEEP
+#define GGUF_M1_DEEP 8  // units in flight of a wave holding more than 32 small blocks
+#endif
 // Units in flight per wave for a grid of `waves` waves holding `per` units
 // of `unit_bytes` each: about 12 MB over the chip when the grid is one round
 // (at most 2048 resident waves), one unit when later rounds stream in behind
@@ -1135,7 +1138,9 @@ inline int m1_depth(int waves, int per, int unit_bytes) {
   const int resident = waves < 2048 ? waves : 2048;
   const int d = (int)(kM1Flight / ((double)resident * unit_bytes) + 0.5);
   if (d < 1) return 1;
-  if (d > 3 || d >= per) return per > 32 ? 3 : 0;  // more than 32 units never all in registers
+  if (per > 32)  // 32-element blocks only: never all in registers, a deep window instead
+    return d > 3 ? GGUF_M1_DEEP : d;
+  if (d > 3 || d >= per) return 0;
   return d;
 }
 
@@ -1194,6 +1199,8 @@ hipError_t launch_m1(const XT *x, const uint8_t *W, int N, int K, float *y, cons
     if (dp == 1) GGUF_M1_K(UU, XX, 1);                                                           \
     else if (dp == 2) GGUF_M1_K(UU, XX, 2);                                                      \
     else if (dp == 3) GGUF_M1_K(UU, XX, 3);                                                      \
+    else if (dp == GGUF_M1_DEEP)                                                                 \
+      GGUF_M1_K(UU, XX, ((UU) == 64 && Fmt<TYPE>::UE == 32 ? GGUF_M1_DEEP : 0));                 \
     else GGUF_M1_K(UU, XX, 0);                                                                   \
   } while (0)
   if (xi <= 1) {

@@ -20,10 +20,12 @@
  *  - No call allocates device memory: weights, activations and outputs are
  *    owned by the caller, as in the reference (forward-pass.ts:1140-1163).
  *  - Weights live in the "row-tile layout": rows are grouped in tiles of 16
- *    (the last tile zero-padded); for each 256-element superblock (Q4_K, Q6_K)
- *    or 32-element block (Q8_0) of K, a tile stores the 16 rows' GGUF blocks
- *    interleaved at 16-byte granularity (8 bytes for Q8_0 quants), so that
- *    one wave-wide load of a matrix-core operand reads contiguous HBM.  The
+ *    (the last tile zero-padded); for each 256-element superblock (Q4_K,
+ *    Q5_K, Q6_K) or 32-element block (Q8_0, Q4_0, Q5_0, IQ4_NL) of K, a tile
+ *    stores the 16 rows' GGUF blocks interleaved at 16-byte granularity (8
+ *    bytes for Q8_0 quants; the 4-bit codes of Q4_0 / Q5_0 / IQ4_NL regrouped
+ *    into one 4-byte word per lane), so that one wave-wide load of a
+ *    matrix-core operand reads contiguous HBM.  The
  *    byte count is exactly round_up(N, 16) rows of GGUF blocks
  *    (gguf_hip_tile_bytes); the interleave is defined in csrc/common.hpp of
  *    the library.  gguf_hip_repack converts raw GGUF bytes.  Row ranges that
