@@ -47,11 +47,15 @@ constexpr int kWave = 64;
 //   Q5_0 ( 352 B)  [   0,   32) d of row r at 2 r
 //                  [  32,   96) qh of row r at 32 + 4 r (bit k: fifth bit of element k)
 //                  [  96,  352) word (g, r) at 96 + (16 g + r) * 4, as Q4_0
+//   IQ4_XS (2176 B) [   0,  128) header of row r at 8 r: d, scales_h, scales_l[4]
+//                  [ 128, 2176) piece (g, r) at 128 + (16 g + r) * 32: word j (j = 0..7)
+//                               holds sub-block j's codes 8 g .. 8 g + 7, as Q4_0
 //
 // The 32-element block types (Q4_0, Q5_0, IQ4_NL; element k of a GGUF block
 // is the low nibble of qs[k] for k < 16, the high nibble of qs[k - 16] above)
-// are the only ones whose bytes are reordered inside a row's block: each lane's
-// eight codes sit in one word, in the order b32_codes unpacks.
+// and IQ4_XS (whose 32-element sub-blocks store their codes the same way) are
+// the only ones whose bytes are reordered inside a row's block: each lane's
+// eight codes of a (sub-)block sit in one word, in the order b32_codes unpacks.
 //
 // Byte offset of (tile t, unit u) = (t * units_per_row + u) * tile_unit_bytes.
 // No bytes are added: a tile is exactly 16 rows of GGUF blocks.
@@ -88,6 +92,17 @@ template <>
 struct Fmt<20> {  // IQ4_NL
   static constexpr int UE = 32, UB = 18, TU = 16 * 18;
 };
+template <>
+struct Fmt<23> {  // IQ4_XS
+  static constexpr int UE = 256, UB = 136, TU = 16 * 136;
+};
+
+// IQ4_XS: the 6-bit scale of sub-block j, from nibble j of scales_l (bits
+// 4j..4j+3 of the little-endian word sl) and bits 2j, 2j + 1 of scales_h
+// (gguf-dequant.ts:354-356); the sub-block's values are d * (ls - 32) * kvalues[q].
+__host__ __device__ __forceinline__ uint32_t iq4xs_ls(uint32_t sh, uint32_t sl, int j) {
+  return ((sl >> (4 * j)) & 0xFu) | (((sh >> (2 * j)) & 3u) << 4);
+}
 
 // 32-element block types whose codes are nibbles (b32_codes below).
 __host__ __device__ constexpr bool is_b32(int type) { return type == 2 || type == 6 || type == 20; }
@@ -100,6 +115,7 @@ __host__ __device__ inline int unit_bytes(int type) {
          : type == 2  ? 18
          : type == 6  ? 22
          : type == 20 ? 18
+         : type == 23 ? 136
          : (type == 12 ? 144 : (type == 13 ? 176 : 210));
 }
 

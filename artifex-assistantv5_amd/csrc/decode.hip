@@ -72,6 +72,11 @@ template <>
 struct Unit<20> {
   uint32_t q, d;
 };
+template <>
+struct Unit<23> {  // IQ4_XS: the row's header; the lane's code words of sub-blocks 0-3, 4-7
+  uint2 h;
+  uint4 a, b;
+};
 
 // Scale group size (elements sharing one scale) and units in flight per wave
 // (P; deepest for a single activation row, whose staged chunk is small).
@@ -113,6 +118,10 @@ struct Dec<6> {
 template <>
 struct Dec<20> {
   static constexpr int GS = 32, P1 = GGUF_DECODE_P_Q8;
+};
+template <>
+struct Dec<23> {
+  static constexpr int GS = 32, P1 = GGUF_DECODE_P_Q4K;
 };
 template <int TYPE, int MT, int MR>
 constexpr int decode_p() {
@@ -188,6 +197,13 @@ __device__ __forceinline__ void load_unit(__amdgpu_buffer_rsrc_t rs, int soff, i
                                           Unit<20> &u) {
   u.q = bload4(rs, 32 + (16 * g + r) * 4, soff);
   u.d = bload2(rs, 2 * r, soff);
+}
+__device__ __forceinline__ void load_unit(__amdgpu_buffer_rsrc_t rs, int soff, int r, int g,
+                                          Unit<23> &u) {
+  const int qa = 128 + (16 * g + r) * 32;
+  u.h = bload8(rs, 8 * r, soff);
+  u.a = bload16(rs, qa, soff);
+  u.b = bload16(rs, qa + 16, soff);
 }
 
 __device__ __forceinline__ half8_t as_h8(uint32_t a, uint32_t b, uint32_t c, uint32_t d) {
@@ -446,6 +462,39 @@ __device__ __forceinline__ void unit_m1(const Unit<20> &u, const Stage &st, int 
   unit_m1_b32<PARTS, 20>(u, st, ul, lane, acc);
 }
 
+// IQ4_XS: the B operand of sub-block j (codebook + 128 as f16 subnormals).
+__device__ __forceinline__ half8_t xs_codes(const Unit<23> &u, int j) {
+  const uint32_t w[8] = {u.a.x, u.a.y, u.a.z, u.a.w, u.b.x, u.b.y, u.b.z, u.b.w};
+  uint32_t c[4];
+  b32_codes<20>(w[j], 0u, c);
+  return as_h8(c[0], c[1], c[2], c[3]);
+}
+
+// IQ4_XS: 8 sub-blocks, one chain as Q4_K; lane (n, g) keeps sub-blocks 2g
+// and 2g + 1, whose scales are d * (ls - 32), with the code offset 128 taken
+// off through the group sums.
+template <int PARTS>
+__device__ __forceinline__ void unit_m1(const Unit<23> &u, const Stage &st, int ul, int lane,
+                                        float &acc) {
+  const int r = lane & 15, g = lane >> 4;
+  const int jo = r >> 1;
+  const bool live = PARTS == 2 || (r & 1) == 0;
+  const int own = 2 * (st.xh + (r & 1) * (st.xl - st.xh) + 256 * ul + 8 * g);
+  const int zero = 2 * st.zero;
+  half8_t a[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) a[j] = lds_h8b(((live && jo == j) ? own : zero) + 64 * j);
+  float4_t D = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int j = 0; j < 8; ++j) D = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[j], xs_codes(u, j), D, 0, 0, 0);
+  const float d = h2f(u.h.x);
+  const float l0 = (float)((int)iq4xs_ls(u.h.x >> 16, u.h.y, 2 * g) - 32);
+  const float l1 = (float)((int)iq4xs_ls(u.h.x >> 16, u.h.y, 2 * g + 1) - 32);
+  const int xs = st.xs + (ul * 8 + 2 * g) * st.ms;
+  acc += (d * kTwo24) * (l0 * (D[0] + D[1]) + l1 * (D[2] + D[3])) -
+         (d * 128.f) * (l0 * lds_f(xs) + l1 * lds_f(xs + st.ms));
+}
+
 // One unit of Q4_K / Q5_K: 8 sub-blocks x MT activation tiles.  Per
 // activation row the sub-block dots are folded as
 //   acc += d 2^24 sum_even sc_j D_j + d 2^20 sum_odd sc_j D_j - dmin sum_j m_j xs_j
@@ -596,6 +645,26 @@ template <int PARTS, int MT, int MR>
 __device__ __forceinline__ void unit_compute(const Unit<20> &u, const Stage &st, int ul, int lane,
                                              int M, float (&acc)[MT][4]) {
   unit_compute_b32<PARTS, MT, MR, 20>(u, st, ul, lane, M, acc);
+}
+// IQ4_XS: sub-block j as an IQ4_NL block with scale d * (ls_j - 32).
+template <int PARTS, int MT, int MR>
+__device__ __forceinline__ void unit_compute(const Unit<23> &u, const Stage &st, int ul, int lane,
+                                             int M, float (&acc)[MT][4]) {
+  const int r = lane & 15, g = lane >> 4;
+  const float d = h2f(u.h.x);
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const half8_t b = xs_codes(u, j);
+    const float dl = d * (float)((int)iq4xs_ls(u.h.x >> 16, u.h.y, j) - 32);
+    const float sd = dl * kTwo24, so = dl * 128.f;
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      const int m = 16 * mt + r;
+      const int off = m * st.ld + 256 * ul + 32 * j + 8 * g;
+      const float4_t D = mfma32<PARTS>(st.xh + off, st.xl + off, st.zero, b, m < M);
+      apply<MR>(acc[mt], D, sd, so, st.xs + (ul * 8 + j) * st.ms + 16 * mt + 4 * g);
+    }
+  }
 }
 
 // Stage activations x[0:M, k0 : k0 + ce) into LDS (zeros past K).
@@ -1244,6 +1313,7 @@ hipError_t launch_x(const XT *x, int64_t ldx, const uint8_t *W, int type, int N,
   if (type == 2) return launch_m<2, XT>(x, ldx, W, N, K, y, ldy, M, s);
   if (type == 6) return launch_m<6, XT>(x, ldx, W, N, K, y, ldy, M, s);
   if (type == 20) return launch_m<20, XT>(x, ldx, W, N, K, y, ldy, M, s);
+  if (type == 23) return launch_m<23, XT>(x, ldx, W, N, K, y, ldy, M, s);
   return launch_m<8, XT>(x, ldx, W, N, K, y, ldy, M, s);
 }
 
@@ -1267,6 +1337,7 @@ hipError_t launch_decode_fused(const float *x, const uint8_t *tiles, int type, i
   if (type == 2) GGUF_FUSED(2);
   if (type == 6) GGUF_FUSED(6);
   if (type == 20) GGUF_FUSED(20);
+  if (type == 23) GGUF_FUSED(23);
   GGUF_FUSED(8);
 #undef GGUF_FUSED
 }
@@ -1284,6 +1355,7 @@ hipError_t launch_decode_attn_merge(const AttnRecords &ar, const uint8_t *tiles,
   if (type == 2) GGUF_MERGE(2);
   if (type == 6) GGUF_MERGE(6);
   if (type == 20) GGUF_MERGE(20);
+  if (type == 23) GGUF_MERGE(23);
   GGUF_MERGE(8);
 #undef GGUF_MERGE
 }

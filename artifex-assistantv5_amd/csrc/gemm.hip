@@ -136,6 +136,11 @@ struct BRaw<6> {
   uint32_t qh[kTN][2];  // the row's fifth bits of block b
 };
 
+template <>
+struct BRaw<23> {
+  uint2 q[kTN];  // the lane's code words of sub-blocks 2c, 2c + 1 (window c)
+};
+
 // Per-superblock fields of row r, loaded with the superblock's first window.
 template <int TYPE>
 struct BHdr {};
@@ -152,6 +157,11 @@ template <>
 struct BHdr<14> {
   uint4 sc[kTN];  // 16 int8 scales
   uint32_t d[kTN];
+};
+
+template <>
+struct BHdr<23> {
+  uint2 hd[kTN];  // d | scales_h << 16, scales_l[4]
 };
 
 // The same fields in the form the dequantization uses, derived once per superblock.
@@ -197,6 +207,19 @@ struct BCur<14> {
   }
 };
 
+template <>
+struct BCur<23> {
+  uint2 hd[kTN];
+  float d[kTN];
+  __device__ __forceinline__ void set(const BHdr<23> &h) {
+#pragma unroll
+    for (int j = 0; j < kTN; ++j) {
+      hd[j] = h.hd[j];
+      d[j] = h2f(h.hd[j].x);
+    }
+  }
+};
+
 struct BOff {       // per-lane vector offsets, fixed for the whole K loop
   int v0, v1, v2, v3;
 };
@@ -226,6 +249,10 @@ __device__ __forceinline__ BOff b_offsets<2>(int r, int g) {
 template <>
 __device__ __forceinline__ BOff b_offsets<20>(int r, int g) {
   return BOff{32 + (16 * g + r) * 4, 2 * r, 0, 0};
+}
+template <>
+__device__ __forceinline__ BOff b_offsets<23>(int r, int g) {
+  return BOff{8 * r, 128 + (16 * g + r) * 32, 0, 0};
 }
 template <>
 __device__ __forceinline__ BOff b_offsets<6>(int r, int g) {
@@ -336,6 +363,18 @@ template <int C>
 __device__ __forceinline__ void load_b(rsrc_t rs, const BOff &o, int ts, int u, int nu,
                                        BRaw<20> &b, BHdr<20> &) {
   load_b_b32<C, 20>(rs, o, ts, u, nu, b);
+}
+
+template <int C>
+__device__ __forceinline__ void load_b(rsrc_t rs, const BOff &o, int ts, int u, int nu,
+                                       BRaw<23> &b, BHdr<23> &h) {
+  constexpr int TU = Fmt<23>::TU;
+  const int su = u * TU;
+#pragma unroll
+  for (int j = 0; j < kTN; ++j) {
+    if (C == 0) h.hd[j] = bl8(rs, o.v0 + j * ts, su);
+    b.q[j] = bl8(rs, o.v1 + j * ts, su + 8 * C);
+  }
 }
 
 // Q4_K / Q5_K: lane (r, g), window c = chunk c of the superblock: low
@@ -477,6 +516,24 @@ template <int C>
 __device__ __forceinline__ void dequant_b(const BRaw<20> &b, const BCur<20> &,
                                           half8_t (&bf)[kTN][2], int g) {
   dequant_b_b32<20>(b, bf, g);
+}
+
+// IQ4_XS: window c = sub-blocks 2c, 2c + 1, each an IQ4_NL block with scale
+// d * (ls - 32) (exact in f32), rounded once to fp16.
+template <int C>
+__device__ __forceinline__ void dequant_b(const BRaw<23> &b, const BCur<23> &h,
+                                          half8_t (&bf)[kTN][2], int) {
+#pragma unroll
+  for (int j = 0; j < kTN; ++j)
+#pragma unroll
+    for (int hb = 0; hb < 2; ++hb) {
+      const float dl = h.d[j] * (float)((int)iq4xs_ls(h.hd[j].x >> 16, h.hd[j].y, 2 * C + hb) - 32);
+      const float s = dl * kTwo24, c = -128.0f * dl;
+      uint32_t w[4];
+      b32_codes<20>(hb ? b.q[j].y : b.q[j].x, 0u, w);
+      bf[j][hb] = h8(mix_lo(w[0], w[1], s, c), mix_hi(w[0], w[1], s, c), mix_lo(w[2], w[3], s, c),
+                     mix_hi(w[2], w[3], s, c));
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -717,6 +774,8 @@ hipError_t launch_x(const XT *x, int64_t ldx, const uint8_t *W, int type, int64_
     launch_type<6, XT>(x, ldx, W, (int)m, (int)n, (int)k, y, ldy, s);
   else if (type == 20)
     launch_type<20, XT>(x, ldx, W, (int)m, (int)n, (int)k, y, ldy, s);
+  else if (type == 23)
+    launch_type<23, XT>(x, ldx, W, (int)m, (int)n, (int)k, y, ldy, s);
   else
     launch_type<14, XT>(x, ldx, W, (int)m, (int)n, (int)k, y, ldy, s);
   return hipGetLastError();

@@ -2,7 +2,7 @@
 //
 // Dequantization is bit-exact to the reference CPU dequant
 // (webgpu/src/model/gguf-dequant.ts:110-127 Q4_0, :130-149 Q5_0, :152-166 Q8_0,
-// :255-281 Q4_K, :283-314 Q5_K, :321-341 IQ4_NL, :369-399 Q6_K): every
+// :255-281 Q4_K, :283-314 Q5_K, :321-341 IQ4_NL, :344-366 IQ4_XS, :369-399 Q6_K): every
 // product in these formats is exact in f32, so the
 // only rounding is the final Q4_K subtraction, which f32 arithmetic (fused
 // or not) rounds exactly once, as the reference's f64-then-Float32Array does.
@@ -69,6 +69,13 @@ __global__ __launch_bounds__(256) void repack_kernel(const uint8_t *__restrict__
       for (int p = 0; p < 12; ++p) *(uint4 *)(tu + (p * 16 + r) * 16) = z;
       *(uint4 *)(tu + 3072 + 16 * r) = z;
       *(uint16_t *)(tu + 3328 + 2 * r) = 0;
+    } else if (TYPE == 23) {
+      *(uint2 *)(tu + 8 * r) = make_uint2(0, 0);
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        *(uint4 *)(tu + 128 + (16 * g + r) * 32) = z;
+        *(uint4 *)(tu + 128 + (16 * g + r) * 32 + 16) = z;
+      }
     } else if (is_b32(TYPE)) {
       *(uint16_t *)(tu + 2 * r) = 0;
       if (TYPE == 6) *(uint32_t *)(tu + 32 + 4 * r) = 0u;
@@ -118,6 +125,23 @@ __global__ __launch_bounds__(256) void repack_kernel(const uint8_t *__restrict__
     *(uint4 *)(tu + 3072 + 16 * r) = make_uint4(ld_u32_bytes(sc), ld_u32_bytes(sc + 4),
                                                 ld_u32_bytes(sc + 8), ld_u32_bytes(sc + 12));
     *(uint16_t *)(tu + 3328 + 2 * r) = (uint16_t)ld_u16_bytes(src + 208);
+  } else if (TYPE == 23) {  // IQ4_XS: header, then each sub-block's codes regrouped per lane
+    *(uint2 *)(tu + 8 * r) = ld_u64_bytes(src);
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      uint32_t w[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const uint8_t *qs = src + 8 + 16 * j;
+        w[j] = 0;
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          w[j] |= (b32_code_of(qs, 8 * g + i) | (b32_code_of(qs, 8 * g + 4 + i) << 4)) << (8 * i);
+      }
+      uint8_t *p = tu + 128 + (16 * g + r) * 32;
+      *(uint4 *)p = make_uint4(w[0], w[1], w[2], w[3]);
+      *(uint4 *)(p + 16) = make_uint4(w[4], w[5], w[6], w[7]);
+    }
   } else if (is_b32(TYPE)) {  // Q4_0 / Q5_0 / IQ4_NL: codes regrouped per lane
     *(uint16_t *)(tu + 2 * r) = (uint16_t)ld_u16_bytes(src);
     if (TYPE == 6) *(uint32_t *)(tu + 32 + 4 * r) = ld_u32_bytes(src + 2);
@@ -155,6 +179,8 @@ hipError_t launch_repack(const uint8_t *raw, int type, int64_t n_rows, int64_t k
     hipLaunchKernelGGL(repack_kernel<6>, grid, block, 0, s, raw, n_rows, nu, n_pad, tiles);
   else if (type == 20)
     hipLaunchKernelGGL(repack_kernel<20>, grid, block, 0, s, raw, n_rows, nu, n_pad, tiles);
+  else if (type == 23)
+    hipLaunchKernelGGL(repack_kernel<23>, grid, block, 0, s, raw, n_rows, nu, n_pad, tiles);
   else
     hipLaunchKernelGGL(repack_kernel<8>, grid, block, 0, s, raw, n_rows, nu, n_pad, tiles);
   return hipGetLastError();
@@ -348,10 +374,35 @@ __global__ __launch_bounds__(256) void dequant_b32_kernel(const uint8_t *__restr
   }
 }
 
+// IQ4_XS: one thread per (row, unit, sub-block j).  d * (ls - 32) has at most
+// 16 significant bits and times a codebook entry at most 23: exact in f32.
+__global__ __launch_bounds__(256) void dequant_iq4_xs_kernel(const uint8_t *__restrict__ tiles,
+                                                             int64_t n_rows, int nu,
+                                                             float *__restrict__ out, int64_t ldo) {
+  const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (gid >= n_rows * nu * 8) return;
+  const int j = (int)(gid & 7);
+  const int64_t nuid = gid >> 3;
+  const int64_t n = nuid / nu;
+  const int u = (int)(nuid - n * nu);
+  const int r = (int)(n & 15);
+  const uint8_t *tu = tiles + ((n >> 4) * nu + u) * (int64_t)Fmt<23>::TU;
+  const uint2 h = *(const uint2 *)(tu + 8 * r);
+  const float dl = h2f(h.x) * (float)((int)iq4xs_ls(h.x >> 16, h.y, j) - 32);
+  float *o = out + n * ldo + 256 * (int64_t)u + 32 * j;
+#pragma unroll
+  for (int g = 0; g < 4; ++g) {
+    const uint32_t w = *(const uint32_t *)(tu + 128 + (16 * g + r) * 32 + 4 * j);
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+      o[8 * g + i] = dl * (float)kIq4nl[(w >> (8 * (i & 3) + 4 * (i >> 2))) & 0x0Fu];
+  }
+}
+
 hipError_t launch_dequant(const uint8_t *tiles, int type, int64_t n_rows, int64_t k, float *out,
                           int64_t ldo, hipStream_t s) {
   const int nu = (int)(k / unit_elems(type));
-  const int parts = (type == 12 || type == 13) ? 4 : (type == 14 ? 2 : 1);
+  const int parts = (type == 12 || type == 13) ? 4 : (type == 14 ? 2 : (type == 23 ? 8 : 1));
   const int64_t total = n_rows * nu * parts;
   const dim3 grid((unsigned)((total + 255) / 256)), block(256);
   if (type == 12)
@@ -366,6 +417,8 @@ hipError_t launch_dequant(const uint8_t *tiles, int type, int64_t n_rows, int64_
     hipLaunchKernelGGL(dequant_b32_kernel<6>, grid, block, 0, s, tiles, n_rows, nu, out, ldo);
   else if (type == 20)
     hipLaunchKernelGGL(dequant_b32_kernel<20>, grid, block, 0, s, tiles, n_rows, nu, out, ldo);
+  else if (type == 23)
+    hipLaunchKernelGGL(dequant_iq4_xs_kernel, grid, block, 0, s, tiles, n_rows, nu, out, ldo);
   else
     hipLaunchKernelGGL(dequant_q8_0_kernel, grid, block, 0, s, tiles, n_rows, nu, out, ldo);
   return hipGetLastError();
@@ -435,6 +488,15 @@ __device__ __forceinline__ void raw_piece_b32(const uint8_t *blk, float *o) {
   for (int k = 0; k < 32; ++k) o[k] = b32_value<TYPE>(d, b32_code_of(qs, k), (qh >> k) & 1u);
 }
 
+// Sub-block j (32 values) of an IQ4_XS superblock from raw GGUF bytes.
+__device__ __forceinline__ void raw_piece_iq4_xs(const uint8_t *blk, int j, float *o) {
+  const float dl = h2f(ld_u16_bytes(blk)) *
+                   (float)((int)iq4xs_ls(ld_u16_bytes(blk + 2), ld_u32_bytes(blk + 4), j) - 32);
+  const uint8_t *qs = blk + 8 + 16 * j;
+#pragma unroll
+  for (int k = 0; k < 32; ++k) o[k] = dl * (float)kIq4nl[b32_code_of(qs, k)];
+}
+
 // Pieces per 256-element superblock (per 32-element block for Q8_0) and values per piece.
 template <int TYPE>
 struct RawPiece;
@@ -452,6 +514,11 @@ template <>
 struct RawPiece<20> {
   static constexpr int PER_UNIT = 1, VALUES = 32;
   __device__ static void run(const uint8_t *unit, int, float *o) { raw_piece_b32<20>(unit, o); }
+};
+template <>
+struct RawPiece<23> {
+  static constexpr int PER_UNIT = 8, VALUES = 32;
+  __device__ static void run(const uint8_t *unit, int p, float *o) { raw_piece_iq4_xs(unit, p, o); }
 };
 template <>
 struct RawPiece<8> {
@@ -527,6 +594,8 @@ hipError_t launch_dequant_raw(const uint8_t *raw, int type, int64_t n_elems, flo
     dequant_raw_type<6>(raw, n_elems, out, s);
   else if (type == 20)
     dequant_raw_type<20>(raw, n_elems, out, s);
+  else if (type == 23)
+    dequant_raw_type<23>(raw, n_elems, out, s);
   else if (type == 12)
     dequant_raw_type<12>(raw, n_elems, out, s);
   else if (type == 13)
@@ -556,6 +625,8 @@ hipError_t launch_get_rows(const uint8_t *raw, int type, int64_t n_rows, int64_t
     get_rows_type<6>(raw, n_rows, k, ids, n_ids, out, ldo, s);
   else if (type == 20)
     get_rows_type<20>(raw, n_rows, k, ids, n_ids, out, ldo, s);
+  else if (type == 23)
+    get_rows_type<23>(raw, n_rows, k, ids, n_ids, out, ldo, s);
   else if (type == 12)
     get_rows_type<12>(raw, n_rows, k, ids, n_ids, out, ldo, s);
   else if (type == 13)

@@ -24,6 +24,11 @@ split of Q6_K) with simpler scale searches:
   above, Q5_0's fifth bit of element ``j`` to bit ``j`` of ``qh``.
 * IQ4_NL: ``d = v / -127`` per 32 elements; each element takes the nearest
   entry of the 16-value codebook (ties to the lower index); packed as Q4_0.
+* IQ4_XS: per 32-element sub-block the IQ4_NL scale ``s = v / -127``; per
+  superblock ``d = max|s| / 31`` (f16) and ``ls - 32 = rint(s / d)``; each
+  element takes the nearest codebook entry of ``w / (d (ls - 32))``; ``ls``
+  packed as nibble ``j`` of ``scales_l`` and bits ``2j, 2j + 1`` of
+  ``scales_h``, each sub-block's codes as a Q4_0 block.
 
 All arithmetic is numpy f32; results depend only on the input values.
 """
@@ -32,7 +37,7 @@ from __future__ import annotations
 
 import numpy as np
 
-from .ggml import IQ4_NL, Q4_0, Q4_K, Q5_0, Q5_K, Q6_K, Q8_0
+from .ggml import IQ4_NL, IQ4_XS, Q4_0, Q4_K, Q5_0, Q5_K, Q6_K, Q8_0
 
 _CHUNK_ROWS = 4096
 
@@ -224,10 +229,30 @@ def _quantize_iq4_nl(w: np.ndarray) -> np.ndarray:
     return out.reshape(-1)
 
 
+def _quantize_iq4_xs(w: np.ndarray) -> np.ndarray:
+    sb = w.reshape(-1, 8, 32)
+    nb = sb.shape[0]
+    s = _signed_absmax(sb.reshape(-1, 32)).reshape(nb, 8) / np.float32(-127)   # per sub-block
+    d16 = _f16(np.abs(s).max(axis=1) / np.float32(31))
+    d = d16.astype(np.float32)[:, None]
+    l = np.clip(np.rint(_safe_div(s, d)), -32, 31).astype(np.int32)            # ls - 32
+    ls = (l + 32).astype(np.uint32)
+    dl = (d * l.astype(np.float32))[:, :, None]
+    t = _safe_div(sb, dl)
+    q = np.abs(t[..., None] - IQ4NL_VALUES.astype(np.float32)).argmin(axis=-1)
+    out = np.empty((nb, 136), np.uint8)
+    out[:, 0:2] = d16.view(np.uint8).reshape(-1, 2)
+    sh = (((ls >> 4) & 3) << (2 * np.arange(8, dtype=np.uint32))).sum(axis=1, dtype=np.uint32)
+    out[:, 2:4] = sh.astype("<u2").view(np.uint8).reshape(-1, 2)
+    out[:, 4:8] = ((ls[:, 0::2] & 0xF) | ((ls[:, 1::2] & 0xF) << 4)).astype(np.uint8)
+    out[:, 8:136] = pack_nibbles32(q.reshape(-1, 32)).reshape(nb, 128)
+    return out.reshape(-1)
+
+
 _QUANTIZERS = {Q8_0: (32, 34, _quantize_q8_0), Q4_K: (256, 144, _quantize_q4_k),
                Q5_K: (256, 176, _quantize_q5_k), Q6_K: (256, 210, _quantize_q6_k),
                Q4_0: (32, 18, _quantize_q4_0), Q5_0: (32, 22, _quantize_q5_0),
-               IQ4_NL: (32, 18, _quantize_iq4_nl)}
+               IQ4_NL: (32, 18, _quantize_iq4_nl), IQ4_XS: (256, 136, _quantize_iq4_xs)}
 
 
 def quantize(w: np.ndarray, ggml_type: int) -> np.ndarray:

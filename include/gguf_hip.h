@@ -21,11 +21,12 @@
  *    owned by the caller, as in the reference (forward-pass.ts:1140-1163).
  *  - Weights live in the "row-tile layout": rows are grouped in tiles of 16
  *    (the last tile zero-padded); for each 256-element superblock (Q4_K,
- *    Q5_K, Q6_K) or 32-element block (Q8_0, Q4_0, Q5_0, IQ4_NL) of K, a tile
- *    stores the 16 rows' GGUF blocks interleaved at 16-byte granularity (8
- *    bytes for Q8_0 quants; the 4-bit codes of Q4_0 / Q5_0 / IQ4_NL regrouped
- *    into one 4-byte word per lane), so that one wave-wide load of a
- *    matrix-core operand reads contiguous HBM.  The
+ *    Q5_K, Q6_K, IQ4_XS) or 32-element block (Q8_0, Q4_0, Q5_0, IQ4_NL) of
+ *    K, a tile stores the 16 rows' GGUF blocks interleaved at 16-byte
+ *    granularity (8 bytes for Q8_0 quants; the 4-bit codes of Q4_0 / Q5_0 /
+ *    IQ4_NL and of each IQ4_XS sub-block regrouped into one 4-byte word per
+ *    lane), so that one wave-wide load of a matrix-core operand reads
+ *    contiguous HBM.  The
  *    byte count is exactly round_up(N, 16) rows of GGUF blocks
  *    (gguf_hip_tile_bytes); the interleave is defined in csrc/common.hpp of
  *    the library.  gguf_hip_repack converts raw GGUF bytes.  Row ranges that
@@ -45,7 +46,7 @@ extern "C" {
  * are exported (kernels and helpers cannot be interposed across libraries). */
 #pragma GCC visibility push(default)
 
-#define GGUF_HIP_ABI_VERSION 8
+#define GGUF_HIP_ABI_VERSION 9
 
 /* ggml type ids (gguf.ts:24-35); activation dtypes reuse F32 / F16. */
 #define GGUF_HIP_F32 0
@@ -57,6 +58,7 @@ extern "C" {
 #define GGUF_HIP_Q5_K 13
 #define GGUF_HIP_Q6_K 14
 #define GGUF_HIP_IQ4_NL 20
+#define GGUF_HIP_IQ4_XS 23
 
 /* Error codes.  The Python host maps them onto the reference's throws:
  * TYPE -> NotImplementedError ("no pipeline for ggml type", forward-pass.ts:1524;

@@ -1,4 +1,4 @@
-"""CPU oracle for the GGUF Q4_0 / Q5_0 / Q8_0 / IQ4_NL / Q4_K / Q5_K / Q6_K dequant-matmul path.
+"""CPU oracle for the GGUF Q4_0 / Q5_0 / Q8_0 / IQ4_NL / IQ4_XS / Q4_K / Q5_K / Q6_K dequant-matmul path.
 
 TEST INFRASTRUCTURE ONLY.  This module is the checker: only ``tests/``,
 ``__graft_entry__.smoke()`` and the ``cpu_baseline`` leg of ``bench.py`` may
@@ -15,7 +15,8 @@ It restates the reference's CPU dequantization
 * the vectorised numpy functions compute in f32.  They are bit-identical to
   the loops because every product in these formats is exact in f32 (Q8_0
   ``d*q`` needs <= 18 significant bits, Q4_0 / Q5_0 ``d*(q-8)`` / ``d*(q-16)``
-  <= 15 / 16, IQ4_NL ``d*kvalues[q]`` <= 18, Q6_K ``d*sc*q`` <= 23, Q4_K
+  <= 15 / 16, IQ4_NL ``d*kvalues[q]`` <= 18, IQ4_XS ``d*(ls-32)*kvalues[q]``
+  <= 23, Q6_K ``d*sc*q`` <= 23, Q4_K
   ``d*sc*q`` <= 21, Q5_K ``d*sc*q`` <= 22 and ``dmin*m`` <= 17) and the only
   rounding left is the final Q4_K / Q5_K subtraction, which f32 and
   f64-then-f32 both round correctly (the exact difference is a multiple of
@@ -36,7 +37,11 @@ element against the reference's documented rule (element j in the low
 nibble of ``qs[j]``, element j + 16 in its high nibble; Q5_0's fifth bit of
 element j in bit j of ``qh``), the package quantizer's round trip, and
 IQ4_NL's codebook cross-checked as the 16 values Q4_0-style code points take
-(kvalues_iq4nl, ``gguf-dequant.ts:29``).
+(kvalues_iq4nl, ``gguf-dequant.ts:29``).  IQ4_XS (no fixture either) is pinned
+by exact rational arithmetic, a closed-form superblock that sets each 6-bit
+sub-block scale through its scales_l nibble and scales_h bit pair
+separately, its equality with eight IQ4_NL blocks of scale d * (ls - 32)
+where that scale is an f16, and the quantizer's round trip.
 ``matmul_bt`` is pinned against numpy float64 products and linearity.
 """
 
@@ -47,7 +52,7 @@ import math
 import numpy as np
 
 T_F32, T_F16, T_Q8_0, T_Q4_K, T_Q5_K, T_Q6_K, T_BF16 = 0, 1, 8, 12, 13, 14, 30
-T_Q4_0, T_Q5_0, T_IQ4_NL = 2, 6, 20
+T_Q4_0, T_Q5_0, T_IQ4_NL, T_IQ4_XS = 2, 6, 20, 23
 
 # kvalues_iq4nl, gguf-dequant.ts:29 (shared by IQ4_NL and IQ4_XS)
 KVALUES_IQ4NL = (-127, -104, -83, -65, -49, -35, -22, -10, 1, 13, 25, 38, 53, 69, 89, 113)
@@ -144,6 +149,27 @@ def dequant_iq4_nl_loop(data: bytes, n: int) -> np.ndarray:
             q = data[base + 2 + j]
             out[b * 32 + j] = d * KVALUES_IQ4NL[q & 0xF]
             out[b * 32 + j + 16] = d * KVALUES_IQ4NL[q >> 4]
+    return out
+
+
+def dequant_iq4_xs_loop(data: bytes, n: int) -> np.ndarray:
+    """gguf-dequant.ts:344-366."""
+    if n % 256 != 0:
+        raise ValueError(f"[IQ4_XS] n={n} not divisible by 256")
+    out = np.zeros(n, np.float32)
+    for b in range(n // 256):
+        base = b * 136
+        d = f16_to_f32(_u16(data, base))
+        sh = _u16(data, base + 2)
+        y, qs = b * 256, base + 8
+        for ib in range(8):
+            ls = ((data[base + 4 + (ib >> 1)] >> (4 * (ib & 1))) & 0xF) | (((sh >> (2 * ib)) & 3) << 4)
+            dl = d * (ls - 32)
+            for j in range(16):
+                out[y + j] = dl * KVALUES_IQ4NL[data[qs + j] & 0xF]
+                out[y + j + 16] = dl * KVALUES_IQ4NL[data[qs + j] >> 4]
+            y += 32
+            qs += 16
     return out
 
 
@@ -251,6 +277,8 @@ def dequant_ggml_loop(ggml_type: int, data: bytes, n: int) -> np.ndarray:
         return dequant_q5_0_loop(data, n)
     if ggml_type == T_IQ4_NL:
         return dequant_iq4_nl_loop(data, n)
+    if ggml_type == T_IQ4_XS:
+        return dequant_iq4_xs_loop(data, n)
     if ggml_type == T_Q4_K:
         return dequant_q4_k_loop(data, n)
     if ggml_type == T_Q5_K:
@@ -273,6 +301,7 @@ assert Q8_0_BLOCK.itemsize == 34 and Q4_K_BLOCK.itemsize == 144 and Q6_K_BLOCK.i
 assert Q5_K_BLOCK.itemsize == 176
 Q4_0_BLOCK = np.dtype([("d", "<f2"), ("qs", "u1", 16)])           # also IQ4_NL
 Q5_0_BLOCK = np.dtype([("d", "<f2"), ("qh", "<u4"), ("qs", "u1", 16)])
+IQ4_XS_BLOCK = np.dtype([("d", "<f2"), ("scales_h", "<u2"), ("scales_l", "u1", 4), ("qs", "u1", 128)])
 assert Q4_0_BLOCK.itemsize == 18 and Q5_0_BLOCK.itemsize == 22
 
 
@@ -333,6 +362,23 @@ def dequant_iq4_nl(data, n: int) -> np.ndarray:
     d = blk["d"].astype(np.float32)[:, None]
     table = np.array(KVALUES_IQ4NL, np.float32)
     return (d * table[nibbles32(blk["qs"])]).reshape(-1)
+
+
+def iq4_xs_scales(blk: np.ndarray) -> np.ndarray:
+    """The eight 6-bit sub-block scales ``ls`` of IQ4_XS superblocks, (nb, 8)."""
+    ib = np.arange(8)
+    lo = (blk["scales_l"][:, ib >> 1] >> (4 * (ib & 1))) & 0xF
+    hi = (blk["scales_h"][:, None].astype(np.uint32) >> (2 * ib)) & 3
+    return lo.astype(np.int32) | (hi.astype(np.int32) << 4)
+
+
+def dequant_iq4_xs(data, n: int) -> np.ndarray:
+    blk = _blocks(data, IQ4_XS_BLOCK, n, 256, "IQ4_XS")
+    nb = blk.shape[0]
+    dl = blk["d"].astype(np.float32)[:, None] * (iq4_xs_scales(blk) - 32).astype(np.float32)
+    codes = nibbles32(blk["qs"].reshape(nb * 8, 16)).reshape(nb, 8, 32)
+    table = np.array(KVALUES_IQ4NL, np.float32)
+    return (dl[:, :, None] * table[codes]).reshape(-1)
 
 
 def dequant_q4_k(data, n: int) -> np.ndarray:
@@ -403,6 +449,8 @@ def dequant_ggml(ggml_type: int, data, n: int) -> np.ndarray:
         return dequant_q5_0(data, n)
     if ggml_type == T_IQ4_NL:
         return dequant_iq4_nl(data, n)
+    if ggml_type == T_IQ4_XS:
+        return dequant_iq4_xs(data, n)
     if ggml_type == T_Q4_K:
         return dequant_q4_k(data, n)
     if ggml_type == T_Q5_K:

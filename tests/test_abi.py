@@ -65,11 +65,12 @@ def test_constants_match_header(native):
     assert d["GGUF_HIP_DECODE_MAX_M"] == native.DECODE_MAX_M
     assert (d["GGUF_HIP_Q8_0"], d["GGUF_HIP_Q4_K"], d["GGUF_HIP_Q5_K"],
             d["GGUF_HIP_Q6_K"]) == (8, 12, 13, 14)
-    assert (d["GGUF_HIP_Q4_0"], d["GGUF_HIP_Q5_0"], d["GGUF_HIP_IQ4_NL"]) == (2, 6, 20)
+    assert (d["GGUF_HIP_Q4_0"], d["GGUF_HIP_Q5_0"], d["GGUF_HIP_IQ4_NL"],
+            d["GGUF_HIP_IQ4_XS"]) == (2, 6, 20, 23)
 
 
 def test_abi_version(lib):
-    assert lib.gguf_hip_abi_version() == 8
+    assert lib.gguf_hip_abi_version() == 9
 
 
 def test_type_traits(lib, native):
@@ -81,7 +82,7 @@ def test_type_traits(lib, native):
 
 
 def test_byte_queries_agree_with_python(lib, pkg):
-    for t in (2, 6, 8, 12, 13, 14, 20):
+    for t in (2, 6, 8, 12, 13, 14, 20, 23):
         for k in (256, 512, 1024, 4096, 14336):
             assert lib.gguf_hip_tile_bytes(t, 7, k) == 16 * pkg.tile_row_bytes(t, k)
             assert lib.gguf_hip_tile_bytes(t, 33, k) == pkg.tiled_bytes(t, 33, k)

@@ -15,11 +15,11 @@ from fractions import Fraction
 import numpy as np
 import pytest
 
-IN_SCOPE = (2, 6, 8, 12, 13, 14, 20)
+IN_SCOPE = (2, 6, 8, 12, 13, 14, 20, 23)
 GOLDEN_TYPES = (8, 12, 13, 14)                 # the types the reference's gguf-py fixtures cover
 BLOCK = {8: (32, 34), 12: (256, 144), 13: (256, 176), 14: (256, 210), 2: (32, 18), 6: (32, 22),
-         20: (32, 18)}
-F16_FIELDS = {8: [0], 12: [0, 2], 13: [0, 2], 14: [208], 2: [0], 6: [0], 20: [0]}
+         20: (32, 18), 23: (256, 136)}
+F16_FIELDS = {8: [0], 12: [0, 2], 13: [0, 2], 14: [208], 2: [0], 6: [0], 20: [0], 23: [0]}
 
 
 def _samples(golden_samples, types=GOLDEN_TYPES):
@@ -187,6 +187,22 @@ def _load_codebook():
 IQ4NL_GOLDEN = _load_codebook()
 
 
+def exact_iq4_xs(raw: bytes) -> list:
+    """IQ4_XS (gguf-dequant.ts:339-343 layout note): the 6-bit scale of sub-block i is
+    digit i (base 16) of the 32-bit scales_l plus 16 x digit i (base 4) of the 16-bit
+    scales_h; sub-block i's codes are a Q4_0-style nibble block at byte 8 + 16 i."""
+    out = []
+    for b in range(len(raw) // 136):
+        blk = raw[136 * b:136 * (b + 1)]
+        d = f16_fraction(blk[0] | blk[1] << 8)
+        sh, sl = int.from_bytes(blk[2:4], "little"), int.from_bytes(blk[4:8], "little")
+        for i in range(8):
+            scale = (sl // 16 ** i) % 16 + 16 * ((sh // 4 ** i) % 4) - 32
+            qs = blk[8 + 16 * i:24 + 16 * i]
+            out += [round_f32(d * scale * IQ4NL_GOLDEN[_nib(qs, j)]) for j in range(32)]
+    return out
+
+
 def exact_q8_0(raw: bytes) -> list:
     out = []
     for b in range(len(raw) // 34):
@@ -212,7 +228,7 @@ def _random_blocks(t: int, nblocks: int, seed: int) -> bytes:
 
 @pytest.mark.parametrize("t,exact", [(8, exact_q8_0), (12, exact_q4_k), (13, exact_q5_k),
                                      (14, exact_q6_k), (2, exact_q4_0), (6, exact_q5_0),
-                                     (20, exact_iq4_nl)])
+                                     (20, exact_iq4_nl), (23, exact_iq4_xs)])
 def test_exact_rational(ref, t, exact):
     raw = _random_blocks(t, 12, seed=t)
     n = 12 * BLOCK[t][0]
@@ -332,7 +348,7 @@ def test_quantizer_error_is_bounded(ref, pkg, t):
     assert raw.size == 4 * 512 // BLOCK[t][0] * BLOCK[t][1]
     deq = ref.dequant_rows(t, raw, 4, 512)
     rel = np.linalg.norm(deq - w) / np.linalg.norm(w)
-    assert rel < {8: 0.01, 12: 0.12, 13: 0.06, 14: 0.05, 2: 0.12, 6: 0.06, 20: 0.1}[t]
+    assert rel < {8: 0.01, 12: 0.12, 13: 0.06, 14: 0.05, 2: 0.12, 6: 0.06, 20: 0.1, 23: 0.1}[t]
 
 
 # ---------------------------------------------------------------------------
@@ -565,3 +581,81 @@ def test_small_block_mutations_are_caught(ref):
     assert fails(2, q4_interleaved) and fails(2, q4_offset_7)
     assert fails(6, q5_fifth_from_byte)
     assert fails(20, iq4_reversed_table)
+
+
+def _iq4_xs_block(d_bits, ls, codes):
+    """One raw IQ4_XS superblock with sub-block scales ls[0..7] and element codes codes[0..255]."""
+    sh = sum((l >> 4) << (2 * i) for i, l in enumerate(ls))
+    sl = bytes((ls[2 * i] & 15) | ((ls[2 * i + 1] & 15) << 4) for i in range(4))
+    qs = b"".join(bytes((codes[32 * i + j] & 15) | ((codes[32 * i + j + 16] & 15) << 4)
+                        for j in range(16)) for i in range(8))
+    return struct.pack("<HH", d_bits, sh) + sl + qs
+
+
+def test_iq4_xs_scales_closed_form(ref):
+    """Each sub-block scale changed through its scales_l nibble alone, then its scales_h
+    bit pair alone: every element is d * (ls - 32) * kvalues[code] with d = 1."""
+    rng = random.Random(23)
+    codes = [rng.randrange(16) for _ in range(256)]
+    for i in range(8):
+        # the other sub-blocks keep ls = 32 (bit pair 10, nibble 0: scale 0)
+        for ls in ([32] * i + [37] + [32] * (7 - i),                # nibble 5, bit pair kept
+                   [32] * i + [48] + [32] * (7 - i),                 # bit pair 11, nibble kept
+                   [32] * i + [0] + [32] * (7 - i),                  # bit pair 00, nibble 0
+                   [32] * i + [63] + [32] * (7 - i)):                # both at their maximum
+            raw = _iq4_xs_block(0x3C00, ls, codes)
+            want = [(ls[e // 32] - 32) * IQ4NL_GOLDEN[codes[e]] for e in range(256)]
+            got = ref.dequant_ggml(23, raw, 256)
+            assert np.array_equal(got, np.array(want, np.float32)), (i, ls)
+            assert np.array_equal(ref.dequant_ggml_loop(23, raw, 256), got)
+
+
+def test_iq4_xs_is_eight_iq4_nl_blocks(ref):
+    """Where d * (ls - 32) is an f16, an IQ4_XS superblock decodes like eight IQ4_NL
+    blocks carrying that scale and the same code bytes."""
+    rng = random.Random(5)
+    for rep_ in range(10):
+        ls = [rng.randrange(64) for _ in range(8)]
+        codes = [rng.randrange(16) for _ in range(256)]
+        raw = _iq4_xs_block(0x3400, ls, codes)                       # d = 0.25
+        nl = b"".join(struct.pack("<e", 0.25 * (ls[i] - 32)) + raw[8 + 16 * i:24 + 16 * i]
+                      for i in range(8))
+        assert np.array_equal(ref.dequant_ggml(23, raw, 256), ref.dequant_ggml(20, nl, 256))
+
+
+def test_iq4_xs_quantizer_roundtrip(ref, pkg):
+    """The package quantizer's IQ4_XS bytes decode to d * (ls - 32) * table[q] for the
+    integers it chose (recomputed here from the weights)."""
+    w = pkg.quantize.synthetic_weight(2, 512, seed=77)
+    raw = pkg.quantize.quantize(w, 23)
+    sb = w.reshape(-1, 8, 32)
+    b = sb.reshape(-1, 32)
+    s = (b[np.arange(b.shape[0]), np.abs(b).argmax(axis=1)] / np.float32(-127)).reshape(-1, 8)
+    d = (np.abs(s).max(axis=1) / np.float32(31)).astype(np.float16).astype(np.float32)[:, None]
+    l = np.clip(np.rint(s / d), -32, 31)
+    dl = (d * l.astype(np.float32))[:, :, None]
+    tab = np.array(IQ4NL_GOLDEN, np.float32)
+    q = np.abs((sb / dl)[..., None] - tab).argmin(axis=-1)
+    want = (dl * tab[q]).reshape(2, 512).astype(np.float32)
+    assert np.array_equal(ref.dequant_rows(23, raw, 2, 512), want)
+
+
+def test_iq4_xs_mutations_are_caught(ref):
+    """Plausible misreadings of the scale bits fail the closed-form pin."""
+    rng = random.Random(9)
+    ls = [rng.randrange(64) for _ in range(8)]
+    codes = [rng.randrange(16) for _ in range(256)]
+    raw = _iq4_xs_block(0x3C00, ls, codes)
+    good = ref.dequant_ggml(23, raw, 256)
+    sh = raw[2] | raw[3] << 8
+    tab = np.array(IQ4NL_GOLDEN, np.float32)
+    cod = np.array(codes).reshape(8, 32)
+
+    def decode(scale_of):
+        return np.concatenate([np.float32(scale_of(i) - 32) * tab[cod[i]] for i in range(8)])
+
+    nib_swapped = decode(lambda i: ((raw[4 + i // 2] >> (4 * (1 - i % 2))) & 15) | (((sh >> 2 * i) & 3) << 4))
+    h_one_bit = decode(lambda i: ((raw[4 + i // 2] >> (4 * (i % 2))) & 15) | (((sh >> i) & 3) << 4))
+    no_bias = decode(lambda i: ls[i] + 32)
+    for bad in (nib_swapped, h_one_bit, no_bias):
+        assert not np.array_equal(bad, good)

@@ -16,13 +16,16 @@ block) a tile stores the 16 rows' GGUF blocks interleaved:
   codes of block elements 8 g + i (low nibble) and 8 g + 4 + i (high nibble); element j
   of a GGUF block is the low nibble of qs[j] (j < 16) or the high nibble of qs[j - 16]
 * Q5_0: d at 2 r, qh at 32 + 4 r, then the code words at 96 + (16 g + r) 4 as Q4_0
+* IQ4_XS: header (d, scales_h, scales_l) at 8 r, then piece (g, r) at 128 + (16 g + r) 32
+  whose word j holds sub-block j's codes 8 g .. 8 g + 7 as Q4_0 (sub-block j's 16 code
+  bytes start at byte 8 + 16 j of the GGUF block)
 """
 
 import numpy as np
 
 BLOCK = {8: (32, 34), 12: (256, 144), 13: (256, 176), 14: (256, 210), 2: (32, 18), 6: (32, 22),
-         20: (32, 18)}
-SMALL = (2, 6, 20)          # nibble codes regrouped per lane (not a byte permutation)
+         20: (32, 18), 23: (256, 136)}
+SMALL = (2, 6, 20, 23)      # nibble codes regrouped per lane (not a byte permutation)
 
 
 def tile_row_bytes(t, k):
@@ -75,10 +78,26 @@ def _unit_maps(t):
     return pos
 
 
+def _word(codes, g):
+    """Byte i of lane group g's word: codes 8 g + i (low nibble), 8 g + 4 + i (high)."""
+    return [codes[..., 8 * g + i] | (codes[..., 8 * g + 4 + i] << 4) for i in range(4)]
+
+
 def _small_to_unit(t, blk):
     """(..., 16 rows, UB) raw blocks -> (..., 16 * UB) tile-unit bytes."""
     sh = blk.shape[:-2]
     out = np.zeros(sh + (16 * BLOCK[t][1],), np.uint8)
+    if t == 23:
+        for r in range(16):
+            out[..., 8 * r:8 * r + 8] = blk[..., r, 0:8]
+            for j in range(8):
+                qs = blk[..., r, 8 + 16 * j:24 + 16 * j]
+                codes = np.concatenate([qs & 15, qs >> 4], axis=-1)
+                for g in range(4):
+                    base = 128 + (16 * g + r) * 32 + 4 * j
+                    for i, b in enumerate(_word(codes, g)):
+                        out[..., base + i] = b
+        return out
     qs = blk[..., 6:] if t == 6 else blk[..., 2:]
     codes = np.concatenate([qs & 15, qs >> 4], axis=-1)          # (..., 16, 32) element order
     off = 96 if t == 6 else 32
@@ -98,6 +117,19 @@ def _small_from_unit(t, tu):
     sh = tu.shape[:-1]
     ub = BLOCK[t][1]
     blk = np.zeros(sh + (16, ub), np.uint8)
+    if t == 23:
+        for r in range(16):
+            blk[..., r, 0:8] = tu[..., 8 * r:8 * r + 8]
+            for j in range(8):
+                codes = np.zeros(sh + (32,), np.uint8)
+                for g in range(4):
+                    base = 128 + (16 * g + r) * 32 + 4 * j
+                    for i in range(4):
+                        b = tu[..., base + i]
+                        codes[..., 8 * g + i] = b & 15
+                        codes[..., 8 * g + 4 + i] = b >> 4
+                blk[..., r, 8 + 16 * j:24 + 16 * j] = codes[..., :16] | (codes[..., 16:] << 4)
+        return blk
     off = 96 if t == 6 else 32
     for r in range(16):
         blk[..., r, 0:2] = tu[..., 2 * r:2 * r + 2]
@@ -162,7 +194,7 @@ def random_blocks(t, n, k, seed, specials=False):
     block, size = BLOCK[t]
     nb = n * (k // block)
     raw = rng.integers(0, 256, (nb, size), dtype=np.uint8)
-    offs = {8: [0], 12: [0, 2], 13: [0, 2], 14: [208], 2: [0], 6: [0], 20: [0]}[t]
+    offs = {8: [0], 12: [0, 2], 13: [0, 2], 14: [208], 2: [0], 6: [0], 20: [0], 23: [0]}[t]
     for o in offs:
         vals = (rng.uniform(-0.01, 0.01, nb) if t not in (12, 13) or o == 0
                 else rng.uniform(0, 0.005, nb))
