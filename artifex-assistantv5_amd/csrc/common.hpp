@@ -47,6 +47,10 @@ constexpr int kWave = 64;
 //   Q5_0 ( 352 B)  [   0,   32) d of row r at 2 r
 //                  [  32,   96) qh of row r at 32 + 4 r (bit k: fifth bit of element k)
 //                  [  96,  352) word (g, r) at 96 + (16 g + r) * 4, as Q4_0
+//   Q2_K (1344 B)  [   0,  256) scales[16] of row r at 16 r
+//                  [ 256,  320) d | dmin << 16 of row r at 256 + 4 r
+//                  [ 320, 1344) piece (g, r) at 320 + (16 g + r) * 16:
+//                               qs[8 g, +8) | qs[32 + 8 g, +8)
 //   IQ4_XS (2176 B) [   0,  128) header of row r at 8 r: d, scales_h, scales_l[4]
 //                  [ 128, 2176) piece (g, r) at 128 + (16 g + r) * 32: word j (j = 0..7)
 //                               holds sub-block j's codes 8 g .. 8 g + 7, as Q4_0
@@ -93,6 +97,10 @@ struct Fmt<20> {  // IQ4_NL
   static constexpr int UE = 32, UB = 18, TU = 16 * 18;
 };
 template <>
+struct Fmt<10> {  // Q2_K
+  static constexpr int UE = 256, UB = 84, TU = 16 * 84;
+};
+template <>
 struct Fmt<23> {  // IQ4_XS
   static constexpr int UE = 256, UB = 136, TU = 16 * 136;
 };
@@ -116,6 +124,7 @@ __host__ __device__ inline int unit_bytes(int type) {
          : type == 6  ? 22
          : type == 20 ? 18
          : type == 23 ? 136
+         : type == 10 ? 84
          : (type == 12 ? 144 : (type == 13 ? 176 : 210));
 }
 

@@ -73,6 +73,11 @@ struct Unit<20> {
   uint32_t q, d;
 };
 template <>
+struct Unit<10> {  // Q2_K: the lane's qs pieces, the row's 16 scale bytes, d | dmin << 16
+  uint4 q, sc;
+  uint32_t dm;
+};
+template <>
 struct Unit<23> {  // IQ4_XS: the row's header; the lane's code words of sub-blocks 0-3, 4-7
   uint2 h;
   uint4 a, b;
@@ -118,6 +123,10 @@ struct Dec<6> {
 template <>
 struct Dec<20> {
   static constexpr int GS = 32, P1 = GGUF_DECODE_P_Q8;
+};
+template <>
+struct Dec<10> {
+  static constexpr int GS = 16, P1 = GGUF_DECODE_P_Q4K;
 };
 template <>
 struct Dec<23> {
@@ -197,6 +206,12 @@ __device__ __forceinline__ void load_unit(__amdgpu_buffer_rsrc_t rs, int soff, i
                                           Unit<20> &u) {
   u.q = bload4(rs, 32 + (16 * g + r) * 4, soff);
   u.d = bload2(rs, 2 * r, soff);
+}
+__device__ __forceinline__ void load_unit(__amdgpu_buffer_rsrc_t rs, int soff, int r, int g,
+                                          Unit<10> &u) {
+  u.q = bload16(rs, 320 + (16 * g + r) * 16, soff);
+  u.sc = bload16(rs, 16 * r, soff);
+  u.dm = bload4(rs, 256 + 4 * r, soff);
 }
 __device__ __forceinline__ void load_unit(__amdgpu_buffer_rsrc_t rs, int soff, int r, int g,
                                           Unit<23> &u) {
@@ -462,6 +477,52 @@ __device__ __forceinline__ void unit_m1(const Unit<20> &u, const Stage &st, int 
   unit_m1_b32<PARTS, 20>(u, st, ul, lane, acc);
 }
 
+// Q2_K: the B operand of 32-element window w = 4 h + j: the lane's 8 codes
+// (k = 8 g .. 8 g + 7 of the window), bits 2 j of its qs bytes 32 h + 8 g + i,
+// as 256 q (subnormal, exact) so that the products keep the magnitude of the
+// other types' codes; halves in the staged (0, 2, 1, 3) quad order.
+constexpr float kTwo16 = 65536.0f;  // 2^24 / 256
+__device__ __forceinline__ half8_t q2k_codes(const Unit<10> &u, int w) {
+  const uint32_t qw[4] = {u.q.x, u.q.y, u.q.z, u.q.w};
+  const int h = w >> 2, sh = 2 * (w & 3);
+  const uint32_t t0 = (qw[2 * h] >> sh) & 0x03030303u, t1 = (qw[2 * h + 1] >> sh) & 0x03030303u;
+  return as_h8((t0 << 8) & 0x03000300u, t0 & 0x03000300u, (t1 << 8) & 0x03000300u,
+               t1 & 0x03000300u);
+}
+
+// Q2_K: 16 scale groups of 16.  Two chains (h = 0, 1) of four MFMAs, one per
+// window j; selector row 2 i + p of chain h carries group 8 h + i, whose k-half
+// (i & 1) of window i >> 1 only the lanes g >> 1 == (i & 1) supply.  Lane
+// (n, g) keeps groups 8 h + 2 g and 8 h + 2 g + 1 of each chain.
+template <int PARTS>
+__device__ __forceinline__ void unit_m1(const Unit<10> &u, const Stage &st, int ul, int lane,
+                                        float &acc) {
+  const int r = lane & 15, g = lane >> 4;
+  const int gi = r >> 1;
+  const bool on = (PARTS == 2 || (r & 1) == 0) && (gi & 1) == (g >> 1);
+  const int own = 2 * (st.xh + (r & 1) * (st.xl - st.xh) + 256 * ul + 8 * g);
+  const int zero = 2 * st.zero;
+  half8_t a[8];
+#pragma unroll
+  for (int w = 0; w < 8; ++w) a[w] = lds_h8b((on && (gi >> 1) == (w & 3)) ? own + 64 * w : zero);
+  float4_t D0 = {0.f, 0.f, 0.f, 0.f}, D1 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    D0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[j], q2k_codes(u, j), D0, 0, 0, 0);
+    D1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[4 + j], q2k_codes(u, 4 + j), D1, 0, 0, 0);
+  }
+  const int sh = 16 * (g & 1);
+  const uint32_t w0 = (g >> 1) ? u.sc.y : u.sc.x, w1 = (g >> 1) ? u.sc.w : u.sc.z;  // groups 2g.., 8+2g..
+  const uint32_t a0 = (w0 >> sh) & 0xFFu, a1 = (w0 >> (sh + 8)) & 0xFFu;
+  const uint32_t b0 = (w1 >> sh) & 0xFFu, b1 = (w1 >> (sh + 8)) & 0xFFu;
+  const float s = (float)(a0 & 15u) * (D0[0] + D0[1]) + (float)(a1 & 15u) * (D0[2] + D0[3]) +
+                  (float)(b0 & 15u) * (D1[0] + D1[1]) + (float)(b1 & 15u) * (D1[2] + D1[3]);
+  const int xs = st.xs + (ul * 16 + 2 * g) * st.ms;
+  const float m = (float)(a0 >> 4) * lds_f(xs) + (float)(a1 >> 4) * lds_f(xs + st.ms) +
+                  (float)(b0 >> 4) * lds_f(xs + 8 * st.ms) + (float)(b1 >> 4) * lds_f(xs + 9 * st.ms);
+  acc += (h2f(u.dm) * kTwo16) * s - h2f(u.dm >> 16) * m;
+}
+
 // IQ4_XS: the B operand of sub-block j (codebook + 128 as f16 subnormals).
 __device__ __forceinline__ half8_t xs_codes(const Unit<23> &u, int j) {
   const uint32_t w[8] = {u.a.x, u.a.y, u.a.z, u.a.w, u.b.x, u.b.y, u.b.z, u.b.w};
@@ -645,6 +706,33 @@ template <int PARTS, int MT, int MR>
 __device__ __forceinline__ void unit_compute(const Unit<20> &u, const Stage &st, int ul, int lane,
                                              int M, float (&acc)[MT][4]) {
   unit_compute_b32<PARTS, MT, MR, 20>(u, st, ul, lane, M, acc);
+}
+// Q2_K: each window twice, once per 16-element group (the other k-half reads
+// the zero operand), with that group's d * sc and dmin * m.
+template <int PARTS, int MT, int MR>
+__device__ __forceinline__ void unit_compute(const Unit<10> &u, const Stage &st, int ul, int lane,
+                                             int M, float (&acc)[MT][4]) {
+  const int r = lane & 15, g = lane >> 4;
+  const float d = h2f(u.dm), dmin = h2f(u.dm >> 16);
+  const uint32_t scw[4] = {u.sc.x, u.sc.y, u.sc.z, u.sc.w};
+#pragma unroll
+  for (int w = 0; w < 8; ++w) {
+    const half8_t b = q2k_codes(u, w);
+#pragma unroll
+    for (int sub = 0; sub < 2; ++sub) {
+      const int grp = 2 * w + sub;
+      const uint32_t sb = (scw[grp >> 2] >> (8 * (grp & 3))) & 0xFFu;
+      const float sd = d * (float)(sb & 15u) * kTwo16, so = dmin * (float)(sb >> 4);
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        const int m = 16 * mt + r;
+        const int off = m * st.ld + 256 * ul + 32 * w + 8 * g;
+        const float4_t Dv = mfma32<PARTS>(st.xh + off, st.xl + off, st.zero, b,
+                                          m < M && (g >> 1) == sub);
+        apply<MR>(acc[mt], Dv, sd, so, st.xs + (ul * 16 + grp) * st.ms + 16 * mt + 4 * g);
+      }
+    }
+  }
 }
 // IQ4_XS: sub-block j as an IQ4_NL block with scale d * (ls_j - 32).
 template <int PARTS, int MT, int MR>
@@ -1314,6 +1402,7 @@ hipError_t launch_x(const XT *x, int64_t ldx, const uint8_t *W, int type, int N,
   if (type == 6) return launch_m<6, XT>(x, ldx, W, N, K, y, ldy, M, s);
   if (type == 20) return launch_m<20, XT>(x, ldx, W, N, K, y, ldy, M, s);
   if (type == 23) return launch_m<23, XT>(x, ldx, W, N, K, y, ldy, M, s);
+  if (type == 10) return launch_m<10, XT>(x, ldx, W, N, K, y, ldy, M, s);
   return launch_m<8, XT>(x, ldx, W, N, K, y, ldy, M, s);
 }
 
@@ -1338,6 +1427,7 @@ hipError_t launch_decode_fused(const float *x, const uint8_t *tiles, int type, i
   if (type == 6) GGUF_FUSED(6);
   if (type == 20) GGUF_FUSED(20);
   if (type == 23) GGUF_FUSED(23);
+  if (type == 10) GGUF_FUSED(10);
   GGUF_FUSED(8);
 #undef GGUF_FUSED
 }
@@ -1356,6 +1446,7 @@ hipError_t launch_decode_attn_merge(const AttnRecords &ar, const uint8_t *tiles,
   if (type == 6) GGUF_MERGE(6);
   if (type == 20) GGUF_MERGE(20);
   if (type == 23) GGUF_MERGE(23);
+  if (type == 10) GGUF_MERGE(10);
   GGUF_MERGE(8);
 #undef GGUF_MERGE
 }

@@ -137,6 +137,10 @@ struct BRaw<6> {
 };
 
 template <>
+struct BRaw<10> {
+  uint2 q[kTN];  // the lane's 8 qs bytes of half c >> 1 (windows 2c, 2c + 1 share them)
+};
+template <>
 struct BRaw<23> {
   uint2 q[kTN];  // the lane's code words of sub-blocks 2c, 2c + 1 (window c)
 };
@@ -159,6 +163,11 @@ struct BHdr<14> {
   uint32_t d[kTN];
 };
 
+template <>
+struct BHdr<10> {
+  uint4 sc[kTN];  // the row's 16 scale bytes
+  uint32_t dm[kTN];  // d | dmin << 16
+};
 template <>
 struct BHdr<23> {
   uint2 hd[kTN];  // d | scales_h << 16, scales_l[4]
@@ -208,6 +217,19 @@ struct BCur<14> {
 };
 
 template <>
+struct BCur<10> {
+  uint4 sc[kTN];
+  float d24[kTN], dmin[kTN];
+  __device__ __forceinline__ void set(const BHdr<10> &h) {
+#pragma unroll
+    for (int j = 0; j < kTN; ++j) {
+      sc[j] = h.sc[j];
+      d24[j] = h2f(h.dm[j]) * kTwo24;
+      dmin[j] = h2f(h.dm[j] >> 16);
+    }
+  }
+};
+template <>
 struct BCur<23> {
   uint2 hd[kTN];
   float d[kTN];
@@ -249,6 +271,10 @@ __device__ __forceinline__ BOff b_offsets<2>(int r, int g) {
 template <>
 __device__ __forceinline__ BOff b_offsets<20>(int r, int g) {
   return BOff{32 + (16 * g + r) * 4, 2 * r, 0, 0};
+}
+template <>
+__device__ __forceinline__ BOff b_offsets<10>(int r, int g) {
+  return BOff{320 + (16 * g + r) * 16, 16 * r, 256 + 4 * r, 0};
 }
 template <>
 __device__ __forceinline__ BOff b_offsets<23>(int r, int g) {
@@ -365,6 +391,20 @@ __device__ __forceinline__ void load_b(rsrc_t rs, const BOff &o, int ts, int u, 
   load_b_b32<C, 20>(rs, o, ts, u, nu, b);
 }
 
+template <int C>
+__device__ __forceinline__ void load_b(rsrc_t rs, const BOff &o, int ts, int u, int nu,
+                                       BRaw<10> &b, BHdr<10> &h) {
+  constexpr int TU = Fmt<10>::TU;
+  const int su = u * TU;
+#pragma unroll
+  for (int j = 0; j < kTN; ++j) {
+    if (C == 0) {
+      h.sc[j] = bl16(rs, o.v1 + j * ts, su);
+      h.dm[j] = bl4(rs, o.v2 + j * ts, su);
+    }
+    b.q[j] = bl8(rs, o.v0 + j * ts, su + 8 * (C >> 1));
+  }
+}
 template <int C>
 __device__ __forceinline__ void load_b(rsrc_t rs, const BOff &o, int ts, int u, int nu,
                                        BRaw<23> &b, BHdr<23> &h) {
@@ -516,6 +556,31 @@ template <int C>
 __device__ __forceinline__ void dequant_b(const BRaw<20> &b, const BCur<20> &,
                                           half8_t (&bf)[kTN][2], int g) {
   dequant_b_b32<20>(b, bf, g);
+}
+
+// Q2_K: the 64-wide step c holds 32-element windows w = 2c, 2c + 1 (bits 2 (w & 3)
+// of the lane's qs bytes of half c >> 1); the lane's 8 k of a window lie in scale
+// group 2 w + (g >> 1), dequantized as fp16(d sc q - dmin m).
+template <int C>
+__device__ __forceinline__ void dequant_b(const BRaw<10> &b, const BCur<10> &h,
+                                          half8_t (&bf)[kTN][2], int g) {
+#pragma unroll
+  for (int j = 0; j < kTN; ++j)
+#pragma unroll
+    for (int hb = 0; hb < 2; ++hb) {
+      const int w = 2 * C + hb, sh = 2 * (w & 3);
+      const uint32_t scw = (w >> 1) == 0 ? h.sc[j].x
+                           : (w >> 1) == 1 ? h.sc[j].y
+                           : (w >> 1) == 2 ? h.sc[j].z
+                                           : h.sc[j].w;
+      const uint32_t sb = (scw >> (8 * (2 * (w & 1) + (g >> 1)))) & 0xFFu;
+      const float s = h.d24[j] * (float)(sb & 15u), c = -(h.dmin[j] * (float)(sb >> 4));
+      const uint32_t t0 = (b.q[j].x >> sh) & 0x03030303u, t1 = (b.q[j].y >> sh) & 0x03030303u;
+      const uint32_t e0 = t0 & 0x00FF00FFu, o0 = (t0 >> 8) & 0x00FF00FFu;
+      const uint32_t e1 = t1 & 0x00FF00FFu, o1 = (t1 >> 8) & 0x00FF00FFu;
+      bf[j][hb] = h8(mix_lo(e0, o0, s, c), mix_hi(e0, o0, s, c), mix_lo(e1, o1, s, c),
+                     mix_hi(e1, o1, s, c));
+    }
 }
 
 // IQ4_XS: window c = sub-blocks 2c, 2c + 1, each an IQ4_NL block with scale
@@ -776,6 +841,8 @@ hipError_t launch_x(const XT *x, int64_t ldx, const uint8_t *W, int type, int64_
     launch_type<20, XT>(x, ldx, W, (int)m, (int)n, (int)k, y, ldy, s);
   else if (type == 23)
     launch_type<23, XT>(x, ldx, W, (int)m, (int)n, (int)k, y, ldy, s);
+  else if (type == 10)
+    launch_type<10, XT>(x, ldx, W, (int)m, (int)n, (int)k, y, ldy, s);
   else
     launch_type<14, XT>(x, ldx, W, (int)m, (int)n, (int)k, y, ldy, s);
   return hipGetLastError();

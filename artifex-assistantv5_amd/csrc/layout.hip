@@ -2,7 +2,7 @@
 //
 // Dequantization is bit-exact to the reference CPU dequant
 // (webgpu/src/model/gguf-dequant.ts:110-127 Q4_0, :130-149 Q5_0, :152-166 Q8_0,
-// :255-281 Q4_K, :283-314 Q5_K, :321-341 IQ4_NL, :344-366 IQ4_XS, :369-399 Q6_K): every
+// :181-206 Q2_K, :255-281 Q4_K, :283-314 Q5_K, :321-341 IQ4_NL, :344-366 IQ4_XS, :369-399 Q6_K): every
 // product in these formats is exact in f32, so the
 // only rounding is the final Q4_K subtraction, which f32 arithmetic (fused
 // or not) rounds exactly once, as the reference's f64-then-Float32Array does.
@@ -69,6 +69,11 @@ __global__ __launch_bounds__(256) void repack_kernel(const uint8_t *__restrict__
       for (int p = 0; p < 12; ++p) *(uint4 *)(tu + (p * 16 + r) * 16) = z;
       *(uint4 *)(tu + 3072 + 16 * r) = z;
       *(uint16_t *)(tu + 3328 + 2 * r) = 0;
+    } else if (TYPE == 10) {
+      *(uint4 *)(tu + 16 * r) = z;
+      *(uint32_t *)(tu + 256 + 4 * r) = 0u;
+#pragma unroll
+      for (int g = 0; g < 4; ++g) *(uint4 *)(tu + 320 + (16 * g + r) * 16) = z;
     } else if (TYPE == 23) {
       *(uint2 *)(tu + 8 * r) = make_uint2(0, 0);
 #pragma unroll
@@ -125,6 +130,16 @@ __global__ __launch_bounds__(256) void repack_kernel(const uint8_t *__restrict__
     *(uint4 *)(tu + 3072 + 16 * r) = make_uint4(ld_u32_bytes(sc), ld_u32_bytes(sc + 4),
                                                 ld_u32_bytes(sc + 8), ld_u32_bytes(sc + 12));
     *(uint16_t *)(tu + 3328 + 2 * r) = (uint16_t)ld_u16_bytes(src + 208);
+  } else if (TYPE == 10) {  // Q2_K: scales, d | dmin, then the lane's two 8-byte qs pieces
+    *(uint4 *)(tu + 16 * r) = make_uint4(ld_u32_bytes(src), ld_u32_bytes(src + 4),
+                                         ld_u32_bytes(src + 8), ld_u32_bytes(src + 12));
+    *(uint32_t *)(tu + 256 + 4 * r) = ld_u32_bytes(src + 80);
+    const uint8_t *qs = src + 16;
+#pragma unroll
+    for (int g = 0; g < 4; ++g)
+      *(uint4 *)(tu + 320 + (16 * g + r) * 16) =
+          make_uint4(ld_u32_bytes(qs + 8 * g), ld_u32_bytes(qs + 8 * g + 4),
+                     ld_u32_bytes(qs + 32 + 8 * g), ld_u32_bytes(qs + 32 + 8 * g + 4));
   } else if (TYPE == 23) {  // IQ4_XS: header, then each sub-block's codes regrouped per lane
     *(uint2 *)(tu + 8 * r) = ld_u64_bytes(src);
 #pragma unroll
@@ -181,6 +196,8 @@ hipError_t launch_repack(const uint8_t *raw, int type, int64_t n_rows, int64_t k
     hipLaunchKernelGGL(repack_kernel<20>, grid, block, 0, s, raw, n_rows, nu, n_pad, tiles);
   else if (type == 23)
     hipLaunchKernelGGL(repack_kernel<23>, grid, block, 0, s, raw, n_rows, nu, n_pad, tiles);
+  else if (type == 10)
+    hipLaunchKernelGGL(repack_kernel<10>, grid, block, 0, s, raw, n_rows, nu, n_pad, tiles);
   else
     hipLaunchKernelGGL(repack_kernel<8>, grid, block, 0, s, raw, n_rows, nu, n_pad, tiles);
   return hipGetLastError();
@@ -374,6 +391,38 @@ __global__ __launch_bounds__(256) void dequant_b32_kernel(const uint8_t *__restr
   }
 }
 
+// Q2_K: one thread per (row, unit, half h).  Element 128 h + 32 j + 8 g + i
+// has code (qs[32 h + 8 g + i] >> 2 j) & 3 and scale group 8 h + 2 j + (g >> 1);
+// d * sc * q (at most 17 bits) and dmin * m are exact, the difference is
+// rounded once.
+__global__ __launch_bounds__(256) void dequant_q2_k_kernel(const uint8_t *__restrict__ tiles,
+                                                           int64_t n_rows, int nu,
+                                                           float *__restrict__ out, int64_t ldo) {
+  const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (gid >= n_rows * nu * 2) return;
+  const int h = (int)(gid & 1);
+  const int64_t nuid = gid >> 1;
+  const int64_t n = nuid / nu;
+  const int u = (int)(nuid - n * nu);
+  const int r = (int)(n & 15);
+  const uint8_t *tu = tiles + ((n >> 4) * nu + u) * (int64_t)Fmt<10>::TU;
+  const uint8_t *sc = tu + 16 * r;
+  const uint32_t dm = *(const uint32_t *)(tu + 256 + 4 * r);
+  const float d = h2f(dm), dmin = h2f(dm >> 16);
+  float *o = out + n * ldo + 256 * (int64_t)u + 128 * h;
+#pragma unroll
+  for (int g = 0; g < 4; ++g) {
+    const uint8_t *q = tu + 320 + (16 * g + r) * 16 + 8 * h;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const uint32_t s = sc[8 * h + 2 * j + (g >> 1)];
+      const float dl = d * (float)(s & 15u), ml = dmin * (float)(s >> 4);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) o[32 * j + 8 * g + i] = dl * (float)((q[i] >> (2 * j)) & 3u) - ml;
+    }
+  }
+}
+
 // IQ4_XS: one thread per (row, unit, sub-block j).  d * (ls - 32) has at most
 // 16 significant bits and times a codebook entry at most 23: exact in f32.
 __global__ __launch_bounds__(256) void dequant_iq4_xs_kernel(const uint8_t *__restrict__ tiles,
@@ -402,7 +451,9 @@ __global__ __launch_bounds__(256) void dequant_iq4_xs_kernel(const uint8_t *__re
 hipError_t launch_dequant(const uint8_t *tiles, int type, int64_t n_rows, int64_t k, float *out,
                           int64_t ldo, hipStream_t s) {
   const int nu = (int)(k / unit_elems(type));
-  const int parts = (type == 12 || type == 13) ? 4 : (type == 14 ? 2 : (type == 23 ? 8 : 1));
+  const int parts = (type == 12 || type == 13) ? 4
+                    : (type == 14 || type == 10) ? 2
+                    : (type == 23 ? 8 : 1);
   const int64_t total = n_rows * nu * parts;
   const dim3 grid((unsigned)((total + 255) / 256)), block(256);
   if (type == 12)
@@ -419,6 +470,8 @@ hipError_t launch_dequant(const uint8_t *tiles, int type, int64_t n_rows, int64_
     hipLaunchKernelGGL(dequant_b32_kernel<20>, grid, block, 0, s, tiles, n_rows, nu, out, ldo);
   else if (type == 23)
     hipLaunchKernelGGL(dequant_iq4_xs_kernel, grid, block, 0, s, tiles, n_rows, nu, out, ldo);
+  else if (type == 10)
+    hipLaunchKernelGGL(dequant_q2_k_kernel, grid, block, 0, s, tiles, n_rows, nu, out, ldo);
   else
     hipLaunchKernelGGL(dequant_q8_0_kernel, grid, block, 0, s, tiles, n_rows, nu, out, ldo);
   return hipGetLastError();
@@ -488,6 +541,21 @@ __device__ __forceinline__ void raw_piece_b32(const uint8_t *blk, float *o) {
   for (int k = 0; k < 32; ++k) o[k] = b32_value<TYPE>(d, b32_code_of(qs, k), (qh >> k) & 1u);
 }
 
+// Half h (128 values) of a Q2_K superblock from raw GGUF bytes (gguf-dequant.ts:191-203).
+__device__ __forceinline__ void raw_piece_q2_k(const uint8_t *blk, int h, float *o) {
+  const float d = h2f(ld_u16_bytes(blk + 80)), dmin = h2f(ld_u16_bytes(blk + 82));
+  const uint8_t *q = blk + 16 + 32 * h;
+  for (int j = 0; j < 4; ++j)
+#pragma unroll
+    for (int sub = 0; sub < 2; ++sub) {
+      const uint32_t s = blk[8 * h + 2 * j + sub];
+      const float dl = d * (float)(s & 15u), ml = dmin * (float)(s >> 4);
+#pragma unroll
+      for (int l = 0; l < 16; ++l)
+        o[32 * j + 16 * sub + l] = dl * (float)((q[16 * sub + l] >> (2 * j)) & 3u) - ml;
+    }
+}
+
 // Sub-block j (32 values) of an IQ4_XS superblock from raw GGUF bytes.
 __device__ __forceinline__ void raw_piece_iq4_xs(const uint8_t *blk, int j, float *o) {
   const float dl = h2f(ld_u16_bytes(blk)) *
@@ -514,6 +582,11 @@ template <>
 struct RawPiece<20> {
   static constexpr int PER_UNIT = 1, VALUES = 32;
   __device__ static void run(const uint8_t *unit, int, float *o) { raw_piece_b32<20>(unit, o); }
+};
+template <>
+struct RawPiece<10> {
+  static constexpr int PER_UNIT = 2, VALUES = 128;
+  __device__ static void run(const uint8_t *unit, int p, float *o) { raw_piece_q2_k(unit, p, o); }
 };
 template <>
 struct RawPiece<23> {
@@ -596,6 +669,8 @@ hipError_t launch_dequant_raw(const uint8_t *raw, int type, int64_t n_elems, flo
     dequant_raw_type<20>(raw, n_elems, out, s);
   else if (type == 23)
     dequant_raw_type<23>(raw, n_elems, out, s);
+  else if (type == 10)
+    dequant_raw_type<10>(raw, n_elems, out, s);
   else if (type == 12)
     dequant_raw_type<12>(raw, n_elems, out, s);
   else if (type == 13)
@@ -627,6 +702,8 @@ hipError_t launch_get_rows(const uint8_t *raw, int type, int64_t n_rows, int64_t
     get_rows_type<20>(raw, n_rows, k, ids, n_ids, out, ldo, s);
   else if (type == 23)
     get_rows_type<23>(raw, n_rows, k, ids, n_ids, out, ldo, s);
+  else if (type == 10)
+    get_rows_type<10>(raw, n_rows, k, ids, n_ids, out, ldo, s);
   else if (type == 12)
     get_rows_type<12>(raw, n_rows, k, ids, n_ids, out, ldo, s);
   else if (type == 13)

@@ -29,6 +29,11 @@ split of Q6_K) with simpler scale searches:
   element takes the nearest codebook entry of ``w / (d (ls - 32))``; ``ls``
   packed as nibble ``j`` of ``scales_l`` and bits ``2j, 2j + 1`` of
   ``scales_h``, each sub-block's codes as a Q4_0 block.
+* Q2_K: per 16-element group ``m = -min(0, min)`` and ``s = (max + m) / 3``;
+  per superblock ``d = max s / 15``, ``dmin = max m / 15`` (f16); 4-bit
+  ``sc, mn`` packed as ``sc | mn << 4``; ``q = rint((w + dmin mn) / (d sc))``
+  clipped to 2 bits; element ``128 h + 32 j + 16 s + l`` goes to bits ``2 j``
+  of ``qs[32 h + 16 s + l]``.
 
 All arithmetic is numpy f32; results depend only on the input values.
 """
@@ -37,7 +42,7 @@ from __future__ import annotations
 
 import numpy as np
 
-from .ggml import IQ4_NL, IQ4_XS, Q4_0, Q4_K, Q5_0, Q5_K, Q6_K, Q8_0
+from .ggml import IQ4_NL, IQ4_XS, Q2_K, Q4_0, Q4_K, Q5_0, Q5_K, Q6_K, Q8_0
 
 _CHUNK_ROWS = 4096
 
@@ -249,10 +254,37 @@ def _quantize_iq4_xs(w: np.ndarray) -> np.ndarray:
     return out.reshape(-1)
 
 
+def _quantize_q2_k(w: np.ndarray) -> np.ndarray:
+    g = w.reshape(-1, 16, 16)                                   # (nb, group, element)
+    nb = g.shape[0]
+    mn = -np.minimum(g.min(axis=2), 0)
+    sc = (g.max(axis=2) + mn) / np.float32(3)
+    d16 = _f16(sc.max(axis=1) / np.float32(15))
+    m16 = _f16(mn.max(axis=1) / np.float32(15))
+    d, dm = d16.astype(np.float32)[:, None], m16.astype(np.float32)[:, None]
+    isc = np.clip(np.rint(_safe_div(sc, d)), 0, 15).astype(np.uint8)
+    imn = np.clip(np.rint(_safe_div(mn, dm)), 0, 15).astype(np.uint8)
+    dl = (d * isc.astype(np.float32))[:, :, None]
+    ml = (dm * imn.astype(np.float32))[:, :, None]
+    q = np.clip(np.rint(_safe_div(g + ml, dl)), 0, 3).astype(np.uint8)
+    # element e = 128 h + 32 j + 16 s + l = group 8 h + 2 j + s, index l
+    q = q.reshape(nb, 2, 4, 2, 16)                              # (nb, h, j, s, l)
+    qs = np.zeros((nb, 2, 2, 16), np.uint8)                     # (nb, h, s, l)
+    for j in range(4):
+        qs |= q[:, :, j] << (2 * j)
+    out = np.empty((nb, 84), np.uint8)
+    out[:, 0:16] = isc | (imn << 4)
+    out[:, 16:80] = qs.reshape(nb, 64)
+    out[:, 80:82] = d16.view(np.uint8).reshape(-1, 2)
+    out[:, 82:84] = m16.view(np.uint8).reshape(-1, 2)
+    return out.reshape(-1)
+
+
 _QUANTIZERS = {Q8_0: (32, 34, _quantize_q8_0), Q4_K: (256, 144, _quantize_q4_k),
                Q5_K: (256, 176, _quantize_q5_k), Q6_K: (256, 210, _quantize_q6_k),
                Q4_0: (32, 18, _quantize_q4_0), Q5_0: (32, 22, _quantize_q5_0),
-               IQ4_NL: (32, 18, _quantize_iq4_nl), IQ4_XS: (256, 136, _quantize_iq4_xs)}
+               IQ4_NL: (32, 18, _quantize_iq4_nl), IQ4_XS: (256, 136, _quantize_iq4_xs),
+               Q2_K: (256, 84, _quantize_q2_k)}
 
 
 def quantize(w: np.ndarray, ggml_type: int) -> np.ndarray:

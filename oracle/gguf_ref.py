@@ -1,4 +1,5 @@
-"""CPU oracle for the GGUF Q4_0 / Q5_0 / Q8_0 / IQ4_NL / IQ4_XS / Q4_K / Q5_K / Q6_K dequant-matmul path.
+"""CPU oracle for the GGUF Q4_0 / Q5_0 / Q8_0 / IQ4_NL / IQ4_XS / Q2_K / Q4_K / Q5_K / Q6_K
+dequant-matmul path.
 
 TEST INFRASTRUCTURE ONLY.  This module is the checker: only ``tests/``,
 ``__graft_entry__.smoke()`` and the ``cpu_baseline`` leg of ``bench.py`` may
@@ -16,9 +17,9 @@ It restates the reference's CPU dequantization
   the loops because every product in these formats is exact in f32 (Q8_0
   ``d*q`` needs <= 18 significant bits, Q4_0 / Q5_0 ``d*(q-8)`` / ``d*(q-16)``
   <= 15 / 16, IQ4_NL ``d*kvalues[q]`` <= 18, IQ4_XS ``d*(ls-32)*kvalues[q]``
-  <= 23, Q6_K ``d*sc*q`` <= 23, Q4_K
+  <= 23, Q2_K ``d*sc*q`` <= 17 and ``dmin*m`` <= 15, Q6_K ``d*sc*q`` <= 23, Q4_K
   ``d*sc*q`` <= 21, Q5_K ``d*sc*q`` <= 22 and ``dmin*m`` <= 17) and the only
-  rounding left is the final Q4_K / Q5_K subtraction, which f32 and
+  rounding left is the final Q2_K / Q4_K / Q5_K subtraction, which f32 and
   f64-then-f32 both round correctly (the exact difference is a multiple of
   2**-24 below 2**27, so it fits in f64's 53 bits).
 
@@ -41,7 +42,10 @@ IQ4_NL's codebook cross-checked as the 16 values Q4_0-style code points take
 by exact rational arithmetic, a closed-form superblock that sets each 6-bit
 sub-block scale through its scales_l nibble and scales_h bit pair
 separately, its equality with eight IQ4_NL blocks of scale d * (ls - 32)
-where that scale is an f16, and the quantizer's round trip.
+where that scale is an f16, and the quantizer's round trip.  Q2_K (no
+fixture) is pinned by exact rational arithmetic, a closed-form superblock
+whose every element sits in its own (group, code) cell, and the quantizer's
+round trip.
 ``matmul_bt`` is pinned against numpy float64 products and linearity.
 """
 
@@ -52,7 +56,7 @@ import math
 import numpy as np
 
 T_F32, T_F16, T_Q8_0, T_Q4_K, T_Q5_K, T_Q6_K, T_BF16 = 0, 1, 8, 12, 13, 14, 30
-T_Q4_0, T_Q5_0, T_IQ4_NL, T_IQ4_XS = 2, 6, 20, 23
+T_Q4_0, T_Q5_0, T_IQ4_NL, T_IQ4_XS, T_Q2_K = 2, 6, 20, 23, 10
 
 # kvalues_iq4nl, gguf-dequant.ts:29 (shared by IQ4_NL and IQ4_XS)
 KVALUES_IQ4NL = (-127, -104, -83, -65, -49, -35, -22, -10, 1, 13, 25, 38, 53, 69, 89, 113)
@@ -149,6 +153,31 @@ def dequant_iq4_nl_loop(data: bytes, n: int) -> np.ndarray:
             q = data[base + 2 + j]
             out[b * 32 + j] = d * KVALUES_IQ4NL[q & 0xF]
             out[b * 32 + j + 16] = d * KVALUES_IQ4NL[q >> 4]
+    return out
+
+
+def dequant_q2_k_loop(data: bytes, n: int) -> np.ndarray:
+    """gguf-dequant.ts:181-206."""
+    if n % 256 != 0:
+        raise ValueError(f"[Q2_K] n={n} not divisible by 256")
+    out = np.zeros(n, np.float32)
+    for b in range(n // 256):
+        base = b * 84
+        d = f16_to_f32(_u16(data, base + 80))
+        mn = f16_to_f32(_u16(data, base + 82))
+        oi, is_ = b * 256, 0
+        for nn in (0, 128):
+            q_base = base + 16 + (nn // 128) * 32
+            shift = 0
+            for _j in range(4):
+                for half in (0, 16):
+                    sc = data[base + is_]
+                    is_ += 1
+                    dl, ml = d * (sc & 0xF), mn * (sc >> 4)
+                    for l in range(16):
+                        out[oi] = dl * ((data[q_base + half + l] >> shift) & 3) - ml
+                        oi += 1
+                shift += 2
     return out
 
 
@@ -279,6 +308,8 @@ def dequant_ggml_loop(ggml_type: int, data: bytes, n: int) -> np.ndarray:
         return dequant_iq4_nl_loop(data, n)
     if ggml_type == T_IQ4_XS:
         return dequant_iq4_xs_loop(data, n)
+    if ggml_type == T_Q2_K:
+        return dequant_q2_k_loop(data, n)
     if ggml_type == T_Q4_K:
         return dequant_q4_k_loop(data, n)
     if ggml_type == T_Q5_K:
@@ -301,6 +332,7 @@ assert Q8_0_BLOCK.itemsize == 34 and Q4_K_BLOCK.itemsize == 144 and Q6_K_BLOCK.i
 assert Q5_K_BLOCK.itemsize == 176
 Q4_0_BLOCK = np.dtype([("d", "<f2"), ("qs", "u1", 16)])           # also IQ4_NL
 Q5_0_BLOCK = np.dtype([("d", "<f2"), ("qh", "<u4"), ("qs", "u1", 16)])
+Q2_K_BLOCK = np.dtype([("scales", "u1", 16), ("qs", "u1", 64), ("d", "<f2"), ("dmin", "<f2")])
 IQ4_XS_BLOCK = np.dtype([("d", "<f2"), ("scales_h", "<u2"), ("scales_l", "u1", 4), ("qs", "u1", 128)])
 assert Q4_0_BLOCK.itemsize == 18 and Q5_0_BLOCK.itemsize == 22
 
@@ -362,6 +394,24 @@ def dequant_iq4_nl(data, n: int) -> np.ndarray:
     d = blk["d"].astype(np.float32)[:, None]
     table = np.array(KVALUES_IQ4NL, np.float32)
     return (d * table[nibbles32(blk["qs"])]).reshape(-1)
+
+
+def q2_k_codes(blk: np.ndarray) -> np.ndarray:
+    """2-bit codes of Q2_K superblocks in element order, (nb, 256): element
+    128 h + 32 j + 16 s + l is bits 2 j of qs[32 h + 16 s + l]."""
+    qs = blk["qs"].reshape(-1, 2, 1, 32)                          # (nb, h, 1, 16 s + l)
+    shifts = (2 * np.arange(4, dtype=np.uint8)).reshape(1, 1, 4, 1)
+    return ((qs >> shifts) & 3).reshape(-1, 256)
+
+
+def dequant_q2_k(data, n: int) -> np.ndarray:
+    blk = _blocks(data, Q2_K_BLOCK, n, 256, "Q2_K")
+    d = blk["d"].astype(np.float32)[:, None]
+    dmin = blk["dmin"].astype(np.float32)[:, None]
+    sc = blk["scales"]
+    dl = np.repeat(d * (sc & 0xF).astype(np.float32), 16, axis=1)   # group e // 16
+    ml = np.repeat(dmin * (sc >> 4).astype(np.float32), 16, axis=1)
+    return (dl * q2_k_codes(blk).astype(np.float32) - ml).reshape(-1)
 
 
 def iq4_xs_scales(blk: np.ndarray) -> np.ndarray:
@@ -451,6 +501,8 @@ def dequant_ggml(ggml_type: int, data, n: int) -> np.ndarray:
         return dequant_iq4_nl(data, n)
     if ggml_type == T_IQ4_XS:
         return dequant_iq4_xs(data, n)
+    if ggml_type == T_Q2_K:
+        return dequant_q2_k(data, n)
     if ggml_type == T_Q4_K:
         return dequant_q4_k(data, n)
     if ggml_type == T_Q5_K:

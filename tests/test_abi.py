@@ -70,7 +70,7 @@ def test_constants_match_header(native):
 
 
 def test_abi_version(lib):
-    assert lib.gguf_hip_abi_version() == 9
+    assert lib.gguf_hip_abi_version() == 10
 
 
 def test_type_traits(lib, native):
@@ -82,7 +82,7 @@ def test_type_traits(lib, native):
 
 
 def test_byte_queries_agree_with_python(lib, pkg):
-    for t in (2, 6, 8, 12, 13, 14, 20, 23):
+    for t in (2, 6, 8, 10, 12, 13, 14, 20, 23):
         for k in (256, 512, 1024, 4096, 14336):
             assert lib.gguf_hip_tile_bytes(t, 7, k) == 16 * pkg.tile_row_bytes(t, k)
             assert lib.gguf_hip_tile_bytes(t, 33, k) == pkg.tiled_bytes(t, 33, k)

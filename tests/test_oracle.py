@@ -15,11 +15,12 @@ from fractions import Fraction
 import numpy as np
 import pytest
 
-IN_SCOPE = (2, 6, 8, 12, 13, 14, 20, 23)
+IN_SCOPE = (2, 6, 8, 10, 12, 13, 14, 20, 23)
 GOLDEN_TYPES = (8, 12, 13, 14)                 # the types the reference's gguf-py fixtures cover
 BLOCK = {8: (32, 34), 12: (256, 144), 13: (256, 176), 14: (256, 210), 2: (32, 18), 6: (32, 22),
-         20: (32, 18), 23: (256, 136)}
-F16_FIELDS = {8: [0], 12: [0, 2], 13: [0, 2], 14: [208], 2: [0], 6: [0], 20: [0], 23: [0]}
+         20: (32, 18), 23: (256, 136), 10: (256, 84)}
+F16_FIELDS = {8: [0], 12: [0, 2], 13: [0, 2], 14: [208], 2: [0], 6: [0], 20: [0], 23: [0],
+              10: [80, 82]}
 
 
 def _samples(golden_samples, types=GOLDEN_TYPES):
@@ -203,6 +204,22 @@ def exact_iq4_xs(raw: bytes) -> list:
     return out
 
 
+def exact_q2_k(raw: bytes) -> list:
+    """Q2_K from the element rule (gguf-dequant.ts:186-203 read as a formula): element
+    e = 128 h + 32 j + 16 s + l has code floor(qs[32 h + 16 s + l] / 4^j) mod 4 and
+    scale byte 8 h + 2 j + s = sc + 16 mn; value d sc q - dmin mn."""
+    out = []
+    for b in range(len(raw) // 84):
+        blk = raw[84 * b:84 * (b + 1)]
+        d, dmin = f16_fraction(blk[80] | blk[81] << 8), f16_fraction(blk[82] | blk[83] << 8)
+        for e in range(256):
+            h, j, s, l = e // 128, (e // 32) % 4, (e // 16) % 2, e % 16
+            q = (blk[16 + 32 * h + 16 * s + l] // 4 ** j) % 4
+            sb = blk[8 * h + 2 * j + s]
+            out.append(round_f32(d * (sb % 16) * q - dmin * (sb // 16)))
+    return out
+
+
 def exact_q8_0(raw: bytes) -> list:
     out = []
     for b in range(len(raw) // 34):
@@ -228,7 +245,7 @@ def _random_blocks(t: int, nblocks: int, seed: int) -> bytes:
 
 @pytest.mark.parametrize("t,exact", [(8, exact_q8_0), (12, exact_q4_k), (13, exact_q5_k),
                                      (14, exact_q6_k), (2, exact_q4_0), (6, exact_q5_0),
-                                     (20, exact_iq4_nl), (23, exact_iq4_xs)])
+                                     (20, exact_iq4_nl), (23, exact_iq4_xs), (10, exact_q2_k)])
 def test_exact_rational(ref, t, exact):
     raw = _random_blocks(t, 12, seed=t)
     n = 12 * BLOCK[t][0]
@@ -256,7 +273,7 @@ def test_loop_equals_vectorised_with_special_values(ref, t):
     for b in range(nb):
         h = SPECIAL_F16[b % len(SPECIAL_F16)]
         for o in F16_FIELDS[t]:
-            struct.pack_into("<H", raw, b * size + o, h if (b // len(SPECIAL_F16)) != 1 or o == 0 else
+            struct.pack_into("<H", raw, b * size + o, h if (b // len(SPECIAL_F16)) != 1 or o == F16_FIELDS[t][0] else
                              SPECIAL_F16[(b + 5) % len(SPECIAL_F16)])
     raw = bytes(raw)
     n = nb * block
@@ -348,7 +365,7 @@ def test_quantizer_error_is_bounded(ref, pkg, t):
     assert raw.size == 4 * 512 // BLOCK[t][0] * BLOCK[t][1]
     deq = ref.dequant_rows(t, raw, 4, 512)
     rel = np.linalg.norm(deq - w) / np.linalg.norm(w)
-    assert rel < {8: 0.01, 12: 0.12, 13: 0.06, 14: 0.05, 2: 0.12, 6: 0.06, 20: 0.1, 23: 0.1}[t]
+    assert rel < {8: 0.01, 12: 0.12, 13: 0.06, 14: 0.05, 2: 0.12, 6: 0.06, 20: 0.1, 23: 0.1, 10: 0.35}[t]
 
 
 # ---------------------------------------------------------------------------
@@ -659,3 +676,64 @@ def test_iq4_xs_mutations_are_caught(ref):
     no_bias = decode(lambda i: ls[i] + 32)
     for bad in (nib_swapped, h_one_bit, no_bias):
         assert not np.array_equal(bad, good)
+
+
+def test_q2_k_closed_form(ref):
+    """Scale byte i = (i % 16) + 16 (i // 8) with d = 1, dmin = 1/2, and code bits chosen so
+    that element e holds code (e // 16 + e) % 4: each element's value names its group
+    and code, so a shifted group, code plane or byte moves at least one element."""
+    sc = bytes((i % 16) | ((i // 8) << 4) for i in range(16))
+    qs = bytearray(64)
+    for e in range(256):
+        h, j, s, l = e // 128, (e // 32) % 4, (e // 16) % 2, e % 16
+        qs[32 * h + 16 * s + l] |= ((e // 16 + e) % 4) << (2 * j)
+    raw = sc + bytes(qs) + struct.pack("<ee", 1.0, 0.5)
+    want = [(e // 16 % 16) * ((e // 16 + e) % 4) - 0.5 * (e // 16 // 8) for e in range(256)]
+    got = ref.dequant_ggml(10, raw, 256)
+    assert np.array_equal(got, np.array(want, np.float32))
+    assert np.array_equal(ref.dequant_ggml_loop(10, raw, 256), got)
+
+
+def test_q2_k_quantizer_roundtrip(ref, pkg):
+    """The package quantizer's Q2_K bytes decode to d sc q - dmin mn for the integers it
+    chose (recomputed here from the weights)."""
+    w = pkg.quantize.synthetic_weight(2, 512, seed=78)
+    raw = pkg.quantize.quantize(w, 10)
+    g = w.reshape(-1, 16, 16)
+    mn = -np.minimum(g.min(axis=2), 0)
+    sc = (g.max(axis=2) + mn) / np.float32(3)
+    d = (sc.max(axis=1) / np.float32(15)).astype(np.float16).astype(np.float32)[:, None]
+    dm = (mn.max(axis=1) / np.float32(15)).astype(np.float16).astype(np.float32)[:, None]
+    isc = np.clip(np.rint(sc / d), 0, 15)
+    imn = np.clip(np.rint(mn / dm), 0, 15)
+    dl, ml = (d * isc)[:, :, None], (dm * imn)[:, :, None]
+    q = np.clip(np.rint((g + ml) / dl), 0, 3)
+    want = (dl * q - ml).reshape(2, 512).astype(np.float32)
+    assert np.array_equal(ref.dequant_rows(10, raw, 2, 512), want)
+
+
+def test_q2_k_mutations_are_caught(ref):
+    """Misreadings of the Q2_K element order fail the exact-rational pin."""
+    raw = _random_blocks(10, 2, seed=101)
+    good = np.array(exact_q2_k(raw), np.float32) + np.float32(0)
+
+    def decode(code_of, scale_of):
+        out = []
+        for b in range(2):
+            blk = raw[84 * b:84 * (b + 1)]
+            d = np.float32(np.frombuffer(blk[80:82], "<f2")[0])
+            dm = np.float32(np.frombuffer(blk[82:84], "<f2")[0])
+            for e in range(256):
+                sb = blk[scale_of(e)]
+                out.append(d * np.float32(sb & 15) * np.float32(code_of(blk, e)) - dm * np.float32(sb >> 4))
+        return np.array(out, np.float32) + np.float32(0)
+
+    right_code = lambda blk, e: (blk[16 + 32 * (e // 128) + e % 32] >> (2 * ((e // 32) % 4))) & 3
+    right_scale = lambda e: e // 16
+    assert np.array_equal(decode(right_code, right_scale), good, equal_nan=True)
+    planes_swapped = lambda blk, e: (blk[16 + 32 * (e // 128) + e % 32] >> (2 * (3 - (e // 32) % 4))) & 3
+    by_64 = lambda blk, e: (blk[16 + (e % 64)] >> (2 * (e // 64))) & 3      # llama-style misread
+    scale_per_32 = lambda e: e // 32
+    for bad in (decode(planes_swapped, right_scale), decode(by_64, right_scale),
+                decode(right_code, scale_per_32)):
+        assert not np.array_equal(bad, good, equal_nan=True)
