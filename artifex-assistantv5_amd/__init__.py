@@ -1,5 +1,5 @@
-"""MI355X-native GGUF Q8_0 / Q4_K / Q5_K / Q6_K / Q2_K / Q4_0 / Q5_0 / IQ4_NL /
-IQ4_XS dequant-matmul.
+"""MI355X-native GGUF Q8_0 / Q4_K / Q5_K / Q6_K / Q2_K / Q3_K / Q4_0 / Q5_0 /
+IQ4_NL / IQ4_XS dequant-matmul.
 
 Python host side of ``libgguf_hip.so`` (hand-written HIP kernels for gfx950
 behind a C ABI, ``include/gguf_hip.h``).  The per-layer API mirrors the

@@ -47,7 +47,8 @@ bool traits(int t, int *block, int *size) {
 
 bool kernel_type(int t) {
   return t == GGUF_HIP_Q8_0 || t == GGUF_HIP_Q4_K || t == GGUF_HIP_Q5_K || t == GGUF_HIP_Q6_K ||
-         t == GGUF_HIP_Q4_0 || t == GGUF_HIP_Q5_0 || t == GGUF_HIP_IQ4_NL || t == GGUF_HIP_IQ4_XS || t == GGUF_HIP_Q2_K;
+         t == GGUF_HIP_Q4_0 || t == GGUF_HIP_Q5_0 || t == GGUF_HIP_IQ4_NL || t == GGUF_HIP_IQ4_XS || t == GGUF_HIP_Q2_K ||
+         t == GGUF_HIP_Q3_K;
 }
 
 int check_type(int t) {

@@ -51,6 +51,11 @@ constexpr int kWave = 64;
 //                  [ 256,  320) d | dmin << 16 of row r at 256 + 4 r
 //                  [ 320, 1344) piece (g, r) at 320 + (16 g + r) * 16:
 //                               qs[8 g, +8) | qs[32 + 8 g, +8)
+//   Q3_K (1760 B)  [   0,  192) scales[12] of row r at 12 r
+//                  [ 192,  224) d of row r at 192 + 2 r
+//                  [ 224,  736) piece (g, r) at 224 + (16 g + r) * 8: hmask[8 g, +8)
+//                  [ 736, 1760) piece (g, r) at 736 + (16 g + r) * 16:
+//                               qs[8 g, +8) | qs[32 + 8 g, +8)
 //   IQ4_XS (2176 B) [   0,  128) header of row r at 8 r: d, scales_h, scales_l[4]
 //                  [ 128, 2176) piece (g, r) at 128 + (16 g + r) * 32: word j (j = 0..7)
 //                               holds sub-block j's codes 8 g .. 8 g + 7, as Q4_0
@@ -101,9 +106,25 @@ struct Fmt<10> {  // Q2_K
   static constexpr int UE = 256, UB = 84, TU = 16 * 84;
 };
 template <>
+struct Fmt<11> {  // Q3_K
+  static constexpr int UE = 256, UB = 110, TU = 16 * 110;
+};
+template <>
 struct Fmt<23> {  // IQ4_XS
   static constexpr int UE = 256, UB = 136, TU = 16 * 136;
 };
+
+// Q3_K: the 16 6-bit scales (stored + 32) from the 12 scale bytes (words a0,
+// a1, a2), one per byte of S[0..3]: low nibbles from a0 / a1 (scales 0-7) and
+// their high nibbles (8-15), bits 4-5 from the 2-bit fields of a2
+// (gguf-dequant.ts:227-231).
+__host__ __device__ __forceinline__ void q3k_scales(uint32_t a0, uint32_t a1, uint32_t a2,
+                                                    uint32_t (&S)[4]) {
+  S[0] = (a0 & 0x0F0F0F0Fu) | ((a2 & 0x03030303u) << 4);
+  S[1] = (a1 & 0x0F0F0F0Fu) | (((a2 >> 2) & 0x03030303u) << 4);
+  S[2] = ((a0 >> 4) & 0x0F0F0F0Fu) | (((a2 >> 4) & 0x03030303u) << 4);
+  S[3] = ((a1 >> 4) & 0x0F0F0F0Fu) | (((a2 >> 6) & 0x03030303u) << 4);
+}
 
 // IQ4_XS: the 6-bit scale of sub-block j, from nibble j of scales_l (bits
 // 4j..4j+3 of the little-endian word sl) and bits 2j, 2j + 1 of scales_h
@@ -125,6 +146,7 @@ __host__ __device__ inline int unit_bytes(int type) {
          : type == 20 ? 18
          : type == 23 ? 136
          : type == 10 ? 84
+         : type == 11 ? 110
          : (type == 12 ? 144 : (type == 13 ? 176 : 210));
 }
 

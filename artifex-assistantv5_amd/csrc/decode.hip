@@ -78,6 +78,12 @@ struct Unit<10> {  // Q2_K: the lane's qs pieces, the row's 16 scale bytes, d | 
   uint32_t dm;
 };
 template <>
+struct Unit<11> {  // Q3_K: the lane's qs and hmask pieces, the row's scale words and d
+  uint4 q;
+  uint2 hm;
+  uint32_t s0, s1, s2, d;
+};
+template <>
 struct Unit<23> {  // IQ4_XS: the row's header; the lane's code words of sub-blocks 0-3, 4-7
   uint2 h;
   uint4 a, b;
@@ -126,6 +132,10 @@ struct Dec<20> {
 };
 template <>
 struct Dec<10> {
+  static constexpr int GS = 16, P1 = GGUF_DECODE_P_Q4K;
+};
+template <>
+struct Dec<11> {
   static constexpr int GS = 16, P1 = GGUF_DECODE_P_Q4K;
 };
 template <>
@@ -212,6 +222,15 @@ __device__ __forceinline__ void load_unit(__amdgpu_buffer_rsrc_t rs, int soff, i
   u.q = bload16(rs, 320 + (16 * g + r) * 16, soff);
   u.sc = bload16(rs, 16 * r, soff);
   u.dm = bload4(rs, 256 + 4 * r, soff);
+}
+__device__ __forceinline__ void load_unit(__amdgpu_buffer_rsrc_t rs, int soff, int r, int g,
+                                          Unit<11> &u) {
+  u.q = bload16(rs, 736 + (16 * g + r) * 16, soff);
+  u.hm = bload8(rs, 224 + (16 * g + r) * 8, soff);
+  u.s0 = bload4(rs, 12 * r, soff);
+  u.s1 = bload4(rs, 12 * r + 4, soff);
+  u.s2 = bload4(rs, 12 * r + 8, soff);
+  u.d = bload2(rs, 192 + 2 * r, soff);
 }
 __device__ __forceinline__ void load_unit(__amdgpu_buffer_rsrc_t rs, int soff, int r, int g,
                                           Unit<23> &u) {
@@ -523,6 +542,57 @@ __device__ __forceinline__ void unit_m1(const Unit<10> &u, const Stage &st, int 
   acc += (h2f(u.dm) * kTwo16) * s - h2f(u.dm >> 16) * m;
 }
 
+// Q3_K: the B operand of window w = 4 h + j as 128 q3 (q3 = low bits | high
+// bit << 2 <= 7: at most 896, subnormal and exact), halves in the staged (0, 2,
+// 1, 3) quad order; the lane's codes as in Q2_K plus bit 4 h + j of its hmask
+// bytes 8 g + i.
+constexpr float kTwo17 = 131072.0f;  // 2^24 / 128
+__device__ __forceinline__ half8_t q3k_codes(const Unit<11> &u, int w) {
+  const uint32_t qw[4] = {u.q.x, u.q.y, u.q.z, u.q.w};
+  const int h = w >> 2, j = w & 3;
+  const uint32_t t0 = ((qw[2 * h] >> (2 * j)) & 0x03030303u) |
+                      (((u.hm.x >> (4 * h + j)) & 0x01010101u) << 2);
+  const uint32_t t1 = ((qw[2 * h + 1] >> (2 * j)) & 0x03030303u) |
+                      (((u.hm.y >> (4 * h + j)) & 0x01010101u) << 2);
+  return as_h8((t0 << 7) & 0x03800380u, (t0 >> 1) & 0x03800380u, (t1 << 7) & 0x03800380u,
+               (t1 >> 1) & 0x03800380u);
+}
+__device__ __forceinline__ float q3k_scale(const uint32_t (&S)[4], int grp) {
+  return (float)((int)((S[grp >> 2] >> (8 * (grp & 3))) & 0xFFu) - 32);
+}
+
+// Q3_K: the Q2_K scheme (two chains, two groups per MFMA) with signed 6-bit
+// scales and the code offset 4 taken off through the group sums.
+template <int PARTS>
+__device__ __forceinline__ void unit_m1(const Unit<11> &u, const Stage &st, int ul, int lane,
+                                        float &acc) {
+  const int r = lane & 15, g = lane >> 4;
+  const int gi = r >> 1;
+  const bool on = (PARTS == 2 || (r & 1) == 0) && (gi & 1) == (g >> 1);
+  const int own = 2 * (st.xh + (r & 1) * (st.xl - st.xh) + 256 * ul + 8 * g);
+  const int zero = 2 * st.zero;
+  half8_t a[8];
+#pragma unroll
+  for (int w = 0; w < 8; ++w) a[w] = lds_h8b((on && (gi >> 1) == (w & 3)) ? own + 64 * w : zero);
+  float4_t D0 = {0.f, 0.f, 0.f, 0.f}, D1 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    D0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[j], q3k_codes(u, j), D0, 0, 0, 0);
+    D1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[4 + j], q3k_codes(u, 4 + j), D1, 0, 0, 0);
+  }
+  uint32_t S[4];
+  q3k_scales(u.s0, u.s1, u.s2, S);
+  const float a0 = q3k_scale(S, 2 * g), a1 = q3k_scale(S, 2 * g + 1);
+  const float b0 = q3k_scale(S, 8 + 2 * g), b1 = q3k_scale(S, 9 + 2 * g);
+  const float s = a0 * (D0[0] + D0[1]) + a1 * (D0[2] + D0[3]) + b0 * (D1[0] + D1[1]) +
+                  b1 * (D1[2] + D1[3]);
+  const int xs = st.xs + (ul * 16 + 2 * g) * st.ms;
+  const float m = a0 * lds_f(xs) + a1 * lds_f(xs + st.ms) + b0 * lds_f(xs + 8 * st.ms) +
+                  b1 * lds_f(xs + 9 * st.ms);
+  const float d = h2f(u.d);
+  acc += (d * kTwo17) * s - (4.f * d) * m;
+}
+
 // IQ4_XS: the B operand of sub-block j (codebook + 128 as f16 subnormals).
 __device__ __forceinline__ half8_t xs_codes(const Unit<23> &u, int j) {
   const uint32_t w[8] = {u.a.x, u.a.y, u.a.z, u.a.w, u.b.x, u.b.y, u.b.z, u.b.w};
@@ -723,6 +793,33 @@ __device__ __forceinline__ void unit_compute(const Unit<10> &u, const Stage &st,
       const int grp = 2 * w + sub;
       const uint32_t sb = (scw[grp >> 2] >> (8 * (grp & 3))) & 0xFFu;
       const float sd = d * (float)(sb & 15u) * kTwo16, so = dmin * (float)(sb >> 4);
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        const int m = 16 * mt + r;
+        const int off = m * st.ld + 256 * ul + 32 * w + 8 * g;
+        const float4_t Dv = mfma32<PARTS>(st.xh + off, st.xl + off, st.zero, b,
+                                          m < M && (g >> 1) == sub);
+        apply<MR>(acc[mt], Dv, sd, so, st.xs + (ul * 16 + grp) * st.ms + 16 * mt + 4 * g);
+      }
+    }
+  }
+}
+// Q3_K: as Q2_K, with the group's d * (sc - 32) and the code offset 4.
+template <int PARTS, int MT, int MR>
+__device__ __forceinline__ void unit_compute(const Unit<11> &u, const Stage &st, int ul, int lane,
+                                             int M, float (&acc)[MT][4]) {
+  const int r = lane & 15, g = lane >> 4;
+  const float d = h2f(u.d);
+  uint32_t S[4];
+  q3k_scales(u.s0, u.s1, u.s2, S);
+#pragma unroll
+  for (int w = 0; w < 8; ++w) {
+    const half8_t b = q3k_codes(u, w);
+#pragma unroll
+    for (int sub = 0; sub < 2; ++sub) {
+      const int grp = 2 * w + sub;
+      const float dl = d * q3k_scale(S, grp);
+      const float sd = dl * kTwo17, so = 4.f * dl;
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) {
         const int m = 16 * mt + r;
@@ -1403,6 +1500,7 @@ hipError_t launch_x(const XT *x, int64_t ldx, const uint8_t *W, int type, int N,
   if (type == 20) return launch_m<20, XT>(x, ldx, W, N, K, y, ldy, M, s);
   if (type == 23) return launch_m<23, XT>(x, ldx, W, N, K, y, ldy, M, s);
   if (type == 10) return launch_m<10, XT>(x, ldx, W, N, K, y, ldy, M, s);
+  if (type == 11) return launch_m<11, XT>(x, ldx, W, N, K, y, ldy, M, s);
   return launch_m<8, XT>(x, ldx, W, N, K, y, ldy, M, s);
 }
 
@@ -1428,6 +1526,7 @@ hipError_t launch_decode_fused(const float *x, const uint8_t *tiles, int type, i
   if (type == 20) GGUF_FUSED(20);
   if (type == 23) GGUF_FUSED(23);
   if (type == 10) GGUF_FUSED(10);
+  if (type == 11) GGUF_FUSED(11);
   GGUF_FUSED(8);
 #undef GGUF_FUSED
 }
@@ -1447,6 +1546,7 @@ hipError_t launch_decode_attn_merge(const AttnRecords &ar, const uint8_t *tiles,
   if (type == 20) GGUF_MERGE(20);
   if (type == 23) GGUF_MERGE(23);
   if (type == 10) GGUF_MERGE(10);
+  if (type == 11) GGUF_MERGE(11);
   GGUF_MERGE(8);
 #undef GGUF_MERGE
 }

@@ -141,6 +141,10 @@ struct BRaw<10> {
   uint2 q[kTN];  // the lane's 8 qs bytes of half c >> 1 (windows 2c, 2c + 1 share them)
 };
 template <>
+struct BRaw<11> {
+  uint2 q[kTN];  // as Q2_K
+};
+template <>
 struct BRaw<23> {
   uint2 q[kTN];  // the lane's code words of sub-blocks 2c, 2c + 1 (window c)
 };
@@ -167,6 +171,12 @@ template <>
 struct BHdr<10> {
   uint4 sc[kTN];  // the row's 16 scale bytes
   uint32_t dm[kTN];  // d | dmin << 16
+};
+template <>
+struct BHdr<11> {
+  uint32_t s[kTN][3];  // the row's 12 scale bytes
+  uint32_t d[kTN];
+  uint2 hm[kTN];       // the lane's hmask bytes 8 g .. 8 g + 7
 };
 template <>
 struct BHdr<23> {
@@ -230,6 +240,20 @@ struct BCur<10> {
   }
 };
 template <>
+struct BCur<11> {
+  uint32_t S[kTN][4];  // the 16 scales (+ 32), one per byte
+  float d[kTN];
+  uint2 hm[kTN];
+  __device__ __forceinline__ void set(const BHdr<11> &h) {
+#pragma unroll
+    for (int j = 0; j < kTN; ++j) {
+      q3k_scales(h.s[j][0], h.s[j][1], h.s[j][2], S[j]);
+      d[j] = h2f(h.d[j]);
+      hm[j] = h.hm[j];
+    }
+  }
+};
+template <>
 struct BCur<23> {
   uint2 hd[kTN];
   float d[kTN];
@@ -275,6 +299,10 @@ __device__ __forceinline__ BOff b_offsets<20>(int r, int g) {
 template <>
 __device__ __forceinline__ BOff b_offsets<10>(int r, int g) {
   return BOff{320 + (16 * g + r) * 16, 16 * r, 256 + 4 * r, 0};
+}
+template <>
+__device__ __forceinline__ BOff b_offsets<11>(int r, int g) {
+  return BOff{736 + (16 * g + r) * 16, 12 * r, 192 + 2 * r, 224 + (16 * g + r) * 8};
 }
 template <>
 __device__ __forceinline__ BOff b_offsets<23>(int r, int g) {
@@ -401,6 +429,23 @@ __device__ __forceinline__ void load_b(rsrc_t rs, const BOff &o, int ts, int u, 
     if (C == 0) {
       h.sc[j] = bl16(rs, o.v1 + j * ts, su);
       h.dm[j] = bl4(rs, o.v2 + j * ts, su);
+    }
+    b.q[j] = bl8(rs, o.v0 + j * ts, su + 8 * (C >> 1));
+  }
+}
+template <int C>
+__device__ __forceinline__ void load_b(rsrc_t rs, const BOff &o, int ts, int u, int nu,
+                                       BRaw<11> &b, BHdr<11> &h) {
+  constexpr int TU = Fmt<11>::TU;
+  const int su = u * TU;
+#pragma unroll
+  for (int j = 0; j < kTN; ++j) {
+    if (C == 0) {
+      h.s[j][0] = bl4(rs, o.v1 + j * ts, su);
+      h.s[j][1] = bl4(rs, o.v1 + 4 + j * ts, su);
+      h.s[j][2] = bl4(rs, o.v1 + 8 + j * ts, su);
+      h.d[j] = bl2(rs, o.v2 + j * ts, su);
+      h.hm[j] = bl8(rs, o.v3 + j * ts, su);
     }
     b.q[j] = bl8(rs, o.v0 + j * ts, su + 8 * (C >> 1));
   }
@@ -576,6 +621,30 @@ __device__ __forceinline__ void dequant_b(const BRaw<10> &b, const BCur<10> &h,
       const uint32_t sb = (scw >> (8 * (2 * (w & 1) + (g >> 1)))) & 0xFFu;
       const float s = h.d24[j] * (float)(sb & 15u), c = -(h.dmin[j] * (float)(sb >> 4));
       const uint32_t t0 = (b.q[j].x >> sh) & 0x03030303u, t1 = (b.q[j].y >> sh) & 0x03030303u;
+      const uint32_t e0 = t0 & 0x00FF00FFu, o0 = (t0 >> 8) & 0x00FF00FFu;
+      const uint32_t e1 = t1 & 0x00FF00FFu, o1 = (t1 >> 8) & 0x00FF00FFu;
+      bf[j][hb] = h8(mix_lo(e0, o0, s, c), mix_hi(e0, o0, s, c), mix_lo(e1, o1, s, c),
+                     mix_hi(e1, o1, s, c));
+    }
+}
+
+// Q3_K: as Q2_K, codes q3 = low bits | hmask bit 4 (c >> 1) + (w & 3) << 2,
+// dequantized as fp16(d (sc - 32) (q3 - 4)) (exact in f32, rounded once).
+template <int C>
+__device__ __forceinline__ void dequant_b(const BRaw<11> &b, const BCur<11> &h,
+                                          half8_t (&bf)[kTN][2], int g) {
+#pragma unroll
+  for (int j = 0; j < kTN; ++j)
+#pragma unroll
+    for (int hb = 0; hb < 2; ++hb) {
+      const int w = 2 * C + hb, jj = w & 3, hh = w >> 2;
+      const uint32_t sb = (h.S[j][w >> 1] >> (8 * (2 * (w & 1) + (g >> 1)))) & 0xFFu;
+      const float dl = h.d[j] * (float)((int)sb - 32);
+      const float s = dl * kTwo24, c = -4.0f * dl;
+      const uint32_t t0 = ((b.q[j].x >> (2 * jj)) & 0x03030303u) |
+                          (((h.hm[j].x >> (4 * hh + jj)) & 0x01010101u) << 2);
+      const uint32_t t1 = ((b.q[j].y >> (2 * jj)) & 0x03030303u) |
+                          (((h.hm[j].y >> (4 * hh + jj)) & 0x01010101u) << 2);
       const uint32_t e0 = t0 & 0x00FF00FFu, o0 = (t0 >> 8) & 0x00FF00FFu;
       const uint32_t e1 = t1 & 0x00FF00FFu, o1 = (t1 >> 8) & 0x00FF00FFu;
       bf[j][hb] = h8(mix_lo(e0, o0, s, c), mix_hi(e0, o0, s, c), mix_lo(e1, o1, s, c),
@@ -843,6 +912,8 @@ hipError_t launch_x(const XT *x, int64_t ldx, const uint8_t *W, int type, int64_
     launch_type<23, XT>(x, ldx, W, (int)m, (int)n, (int)k, y, ldy, s);
   else if (type == 10)
     launch_type<10, XT>(x, ldx, W, (int)m, (int)n, (int)k, y, ldy, s);
+  else if (type == 11)
+    launch_type<11, XT>(x, ldx, W, (int)m, (int)n, (int)k, y, ldy, s);
   else
     launch_type<14, XT>(x, ldx, W, (int)m, (int)n, (int)k, y, ldy, s);
   return hipGetLastError();

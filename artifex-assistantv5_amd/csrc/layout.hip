@@ -2,7 +2,7 @@
 //
 // Dequantization is bit-exact to the reference CPU dequant
 // (webgpu/src/model/gguf-dequant.ts:110-127 Q4_0, :130-149 Q5_0, :152-166 Q8_0,
-// :181-206 Q2_K, :255-281 Q4_K, :283-314 Q5_K, :321-341 IQ4_NL, :344-366 IQ4_XS, :369-399 Q6_K): every
+// :181-206 Q2_K, :217-252 Q3_K, :255-281 Q4_K, :283-314 Q5_K, :321-341 IQ4_NL, :344-366 IQ4_XS, :369-399 Q6_K): every
 // product in these formats is exact in f32, so the
 // only rounding is the final Q4_K subtraction, which f32 arithmetic (fused
 // or not) rounds exactly once, as the reference's f64-then-Float32Array does.
@@ -69,6 +69,16 @@ __global__ __launch_bounds__(256) void repack_kernel(const uint8_t *__restrict__
       for (int p = 0; p < 12; ++p) *(uint4 *)(tu + (p * 16 + r) * 16) = z;
       *(uint4 *)(tu + 3072 + 16 * r) = z;
       *(uint16_t *)(tu + 3328 + 2 * r) = 0;
+    } else if (TYPE == 11) {
+      *(uint32_t *)(tu + 12 * r) = 0u;
+      *(uint32_t *)(tu + 12 * r + 4) = 0u;
+      *(uint32_t *)(tu + 12 * r + 8) = 0u;
+      *(uint16_t *)(tu + 192 + 2 * r) = 0;
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        *(uint2 *)(tu + 224 + (16 * g + r) * 8) = make_uint2(0, 0);
+        *(uint4 *)(tu + 736 + (16 * g + r) * 16) = z;
+      }
     } else if (TYPE == 10) {
       *(uint4 *)(tu + 16 * r) = z;
       *(uint32_t *)(tu + 256 + 4 * r) = 0u;
@@ -130,6 +140,19 @@ __global__ __launch_bounds__(256) void repack_kernel(const uint8_t *__restrict__
     *(uint4 *)(tu + 3072 + 16 * r) = make_uint4(ld_u32_bytes(sc), ld_u32_bytes(sc + 4),
                                                 ld_u32_bytes(sc + 8), ld_u32_bytes(sc + 12));
     *(uint16_t *)(tu + 3328 + 2 * r) = (uint16_t)ld_u16_bytes(src + 208);
+  } else if (TYPE == 11) {  // Q3_K: scales, d, then the lane's hmask and qs pieces
+    *(uint32_t *)(tu + 12 * r) = ld_u32_bytes(src + 96);
+    *(uint32_t *)(tu + 12 * r + 4) = ld_u32_bytes(src + 100);
+    *(uint32_t *)(tu + 12 * r + 8) = ld_u32_bytes(src + 104);
+    *(uint16_t *)(tu + 192 + 2 * r) = (uint16_t)ld_u16_bytes(src + 108);
+    const uint8_t *qs = src + 32;
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      *(uint2 *)(tu + 224 + (16 * g + r) * 8) = ld_u64_bytes(src + 8 * g);
+      *(uint4 *)(tu + 736 + (16 * g + r) * 16) =
+          make_uint4(ld_u32_bytes(qs + 8 * g), ld_u32_bytes(qs + 8 * g + 4),
+                     ld_u32_bytes(qs + 32 + 8 * g), ld_u32_bytes(qs + 32 + 8 * g + 4));
+    }
   } else if (TYPE == 10) {  // Q2_K: scales, d | dmin, then the lane's two 8-byte qs pieces
     *(uint4 *)(tu + 16 * r) = make_uint4(ld_u32_bytes(src), ld_u32_bytes(src + 4),
                                          ld_u32_bytes(src + 8), ld_u32_bytes(src + 12));
@@ -198,6 +221,8 @@ hipError_t launch_repack(const uint8_t *raw, int type, int64_t n_rows, int64_t k
     hipLaunchKernelGGL(repack_kernel<23>, grid, block, 0, s, raw, n_rows, nu, n_pad, tiles);
   else if (type == 10)
     hipLaunchKernelGGL(repack_kernel<10>, grid, block, 0, s, raw, n_rows, nu, n_pad, tiles);
+  else if (type == 11)
+    hipLaunchKernelGGL(repack_kernel<11>, grid, block, 0, s, raw, n_rows, nu, n_pad, tiles);
   else
     hipLaunchKernelGGL(repack_kernel<8>, grid, block, 0, s, raw, n_rows, nu, n_pad, tiles);
   return hipGetLastError();
@@ -423,6 +448,43 @@ __global__ __launch_bounds__(256) void dequant_q2_k_kernel(const uint8_t *__rest
   }
 }
 
+// Q3_K: one thread per (row, unit, half h).  Element 128 h + 32 j + 8 g + i
+// has low bits (qs[32 h + 8 g + i] >> 2 j) & 3, high bit (hmask[8 g + i] >> (4 h
+// + j)) & 1 and scale group 8 h + 2 j + (g >> 1); d * (sc - 32) * (q3 - 4) is
+// exact in f32 (at most 20 significant bits).
+__global__ __launch_bounds__(256) void dequant_q3_k_kernel(const uint8_t *__restrict__ tiles,
+                                                           int64_t n_rows, int nu,
+                                                           float *__restrict__ out, int64_t ldo) {
+  const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (gid >= n_rows * nu * 2) return;
+  const int h = (int)(gid & 1);
+  const int64_t nuid = gid >> 1;
+  const int64_t n = nuid / nu;
+  const int u = (int)(nuid - n * nu);
+  const int r = (int)(n & 15);
+  const uint8_t *tu = tiles + ((n >> 4) * nu + u) * (int64_t)Fmt<11>::TU;
+  uint32_t S[4];
+  q3k_scales(*(const uint32_t *)(tu + 12 * r), *(const uint32_t *)(tu + 12 * r + 4),
+             *(const uint32_t *)(tu + 12 * r + 8), S);
+  const float d = h2f(*(const uint16_t *)(tu + 192 + 2 * r));
+  float *o = out + n * ldo + 256 * (int64_t)u + 128 * h;
+#pragma unroll
+  for (int g = 0; g < 4; ++g) {
+    const uint8_t *q = tu + 736 + (16 * g + r) * 16 + 8 * h;
+    const uint8_t *hm = tu + 224 + (16 * g + r) * 8;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int grp = 8 * h + 2 * j + (g >> 1);
+      const float dl = d * (float)((int)((S[grp >> 2] >> (8 * (grp & 3))) & 0xFFu) - 32);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const int q3 = (int)(((q[i] >> (2 * j)) & 3u) | (((hm[i] >> (4 * h + j)) & 1u) << 2));
+        o[32 * j + 8 * g + i] = dl * (float)(q3 - 4);
+      }
+    }
+  }
+}
+
 // IQ4_XS: one thread per (row, unit, sub-block j).  d * (ls - 32) has at most
 // 16 significant bits and times a codebook entry at most 23: exact in f32.
 __global__ __launch_bounds__(256) void dequant_iq4_xs_kernel(const uint8_t *__restrict__ tiles,
@@ -452,7 +514,7 @@ hipError_t launch_dequant(const uint8_t *tiles, int type, int64_t n_rows, int64_
                           int64_t ldo, hipStream_t s) {
   const int nu = (int)(k / unit_elems(type));
   const int parts = (type == 12 || type == 13) ? 4
-                    : (type == 14 || type == 10) ? 2
+                    : (type == 14 || type == 10 || type == 11) ? 2
                     : (type == 23 ? 8 : 1);
   const int64_t total = n_rows * nu * parts;
   const dim3 grid((unsigned)((total + 255) / 256)), block(256);
@@ -472,6 +534,8 @@ hipError_t launch_dequant(const uint8_t *tiles, int type, int64_t n_rows, int64_
     hipLaunchKernelGGL(dequant_iq4_xs_kernel, grid, block, 0, s, tiles, n_rows, nu, out, ldo);
   else if (type == 10)
     hipLaunchKernelGGL(dequant_q2_k_kernel, grid, block, 0, s, tiles, n_rows, nu, out, ldo);
+  else if (type == 11)
+    hipLaunchKernelGGL(dequant_q3_k_kernel, grid, block, 0, s, tiles, n_rows, nu, out, ldo);
   else
     hipLaunchKernelGGL(dequant_q8_0_kernel, grid, block, 0, s, tiles, n_rows, nu, out, ldo);
   return hipGetLastError();
@@ -556,6 +620,26 @@ __device__ __forceinline__ void raw_piece_q2_k(const uint8_t *blk, int h, float 
     }
 }
 
+// Half h (128 values) of a Q3_K superblock from raw GGUF bytes (gguf-dequant.ts:232-249).
+__device__ __forceinline__ void raw_piece_q3_k(const uint8_t *blk, int h, float *o) {
+  uint32_t S[4];
+  q3k_scales(ld_u32_bytes(blk + 96), ld_u32_bytes(blk + 100), ld_u32_bytes(blk + 104), S);
+  const float d = h2f(ld_u16_bytes(blk + 108));
+  const uint8_t *q = blk + 32 + 32 * h;
+  for (int j = 0; j < 4; ++j)
+#pragma unroll
+    for (int sub = 0; sub < 2; ++sub) {
+      const int grp = 8 * h + 2 * j + sub;
+      const float dl = d * (float)((int)((S[grp >> 2] >> (8 * (grp & 3))) & 0xFFu) - 32);
+#pragma unroll
+      for (int l = 0; l < 16; ++l) {
+        const int q3 = (int)(((q[16 * sub + l] >> (2 * j)) & 3u) |
+                             (((blk[16 * sub + l] >> (4 * h + j)) & 1u) << 2));
+        o[32 * j + 16 * sub + l] = dl * (float)(q3 - 4);
+      }
+    }
+}
+
 // Sub-block j (32 values) of an IQ4_XS superblock from raw GGUF bytes.
 __device__ __forceinline__ void raw_piece_iq4_xs(const uint8_t *blk, int j, float *o) {
   const float dl = h2f(ld_u16_bytes(blk)) *
@@ -587,6 +671,11 @@ template <>
 struct RawPiece<10> {
   static constexpr int PER_UNIT = 2, VALUES = 128;
   __device__ static void run(const uint8_t *unit, int p, float *o) { raw_piece_q2_k(unit, p, o); }
+};
+template <>
+struct RawPiece<11> {
+  static constexpr int PER_UNIT = 2, VALUES = 128;
+  __device__ static void run(const uint8_t *unit, int p, float *o) { raw_piece_q3_k(unit, p, o); }
 };
 template <>
 struct RawPiece<23> {
@@ -671,6 +760,8 @@ hipError_t launch_dequant_raw(const uint8_t *raw, int type, int64_t n_elems, flo
     dequant_raw_type<23>(raw, n_elems, out, s);
   else if (type == 10)
     dequant_raw_type<10>(raw, n_elems, out, s);
+  else if (type == 11)
+    dequant_raw_type<11>(raw, n_elems, out, s);
   else if (type == 12)
     dequant_raw_type<12>(raw, n_elems, out, s);
   else if (type == 13)
@@ -704,6 +795,8 @@ hipError_t launch_get_rows(const uint8_t *raw, int type, int64_t n_rows, int64_t
     get_rows_type<23>(raw, n_rows, k, ids, n_ids, out, ldo, s);
   else if (type == 10)
     get_rows_type<10>(raw, n_rows, k, ids, n_ids, out, ldo, s);
+  else if (type == 11)
+    get_rows_type<11>(raw, n_rows, k, ids, n_ids, out, ldo, s);
   else if (type == 12)
     get_rows_type<12>(raw, n_rows, k, ids, n_ids, out, ldo, s);
   else if (type == 13)

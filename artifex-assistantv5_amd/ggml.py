@@ -9,7 +9,7 @@ The row-tile layout is this library's own (the reference pads blocks to
 4-byte strides for WGSL, ``gguf-dequant.ts:655-672``).  Rows are grouped in
 tiles of 16 consecutive rows (row-major weight, ``matmul_gguf.wgsl:5-8``;
 the last tile is zero-padded).  For each unit of K -- a 256-element
-superblock (Q2_K, Q4_K, Q5_K, Q6_K, IQ4_XS) or a 32-element block (Q4_0, Q5_0,
+superblock (Q2_K, Q3_K, Q4_K, Q5_K, Q6_K, IQ4_XS) or a 32-element block (Q4_0, Q5_0,
 Q8_0, IQ4_NL) -- a tile stores the 16 rows' GGUF blocks interleaved at 16-byte
 granularity (8 bytes for Q8_0 quants, 4 for the nibble codes of the other
 32-element types and of each IQ4_XS sub-block, regrouped per lane), so that one wave-wide load of a
@@ -51,6 +51,7 @@ Q6_K = GGML_TYPES["Q6_K"]
 IQ4_NL = GGML_TYPES["IQ4_NL"]
 IQ4_XS = GGML_TYPES["IQ4_XS"]
 Q2_K = GGML_TYPES["Q2_K"]
+Q3_K = GGML_TYPES["Q3_K"]
 
 # gguf.ts:39-73 — [elements per block, bytes per block]
 _TYPE_TRAITS = {
@@ -64,7 +65,7 @@ _TYPE_TRAITS = {
 }
 
 # Types the HIP kernels of this library decode.
-KERNEL_TYPES = (Q4_0, Q5_0, Q8_0, Q2_K, Q4_K, Q5_K, Q6_K, IQ4_NL, IQ4_XS)
+KERNEL_TYPES = (Q4_0, Q5_0, Q8_0, Q2_K, Q3_K, Q4_K, Q5_K, Q6_K, IQ4_NL, IQ4_XS)
 
 
 class GGMLTypeError(NotImplementedError):

@@ -34,6 +34,12 @@ split of Q6_K) with simpler scale searches:
   ``sc, mn`` packed as ``sc | mn << 4``; ``q = rint((w + dmin mn) / (d sc))``
   clipped to 2 bits; element ``128 h + 32 j + 16 s + l`` goes to bits ``2 j``
   of ``qs[32 h + 16 s + l]``.
+* Q3_K: per 16-element group ``s = v / -4``; per superblock ``d = max|s| / 31``
+  (f16), ``sc - 32 = rint(s / d)``; ``q3 = rint(w / (d (sc - 32))) + 4`` clipped
+  to 3 bits: bits 0-1 into ``qs`` as Q2_K, bit 2 into bit ``4 h + j`` of
+  ``hmask[16 s + l]``; the 6-bit ``sc`` packed as low nibbles (scales 0-7 in the
+  low, 8-15 in the high nibbles of bytes 0-7) and 2-bit fields (scale ``i`` in
+  bits ``2 (i // 4)`` of byte ``8 + i % 4``).
 
 All arithmetic is numpy f32; results depend only on the input values.
 """
@@ -42,7 +48,7 @@ from __future__ import annotations
 
 import numpy as np
 
-from .ggml import IQ4_NL, IQ4_XS, Q2_K, Q4_0, Q4_K, Q5_0, Q5_K, Q6_K, Q8_0
+from .ggml import IQ4_NL, IQ4_XS, Q2_K, Q3_K, Q4_0, Q4_K, Q5_0, Q5_K, Q6_K, Q8_0
 
 _CHUNK_ROWS = 4096
 
@@ -280,11 +286,40 @@ def _quantize_q2_k(w: np.ndarray) -> np.ndarray:
     return out.reshape(-1)
 
 
+def _quantize_q3_k(w: np.ndarray) -> np.ndarray:
+    g = w.reshape(-1, 16, 16)
+    nb = g.shape[0]
+    s = _signed_absmax(g.reshape(-1, 16)).reshape(nb, 16) / np.float32(-4)
+    d16 = _f16(np.abs(s).max(axis=1) / np.float32(31))
+    d = d16.astype(np.float32)[:, None]
+    l = np.clip(np.rint(_safe_div(s, d)), -32, 31).astype(np.int32)
+    dl = (d * l.astype(np.float32))[:, :, None]
+    q = (np.clip(np.rint(_safe_div(g, dl)) + 4, 0, 7)).astype(np.uint8)
+    q = q.reshape(nb, 2, 4, 2, 16)                              # (nb, h, j, s, l)
+    qs = np.zeros((nb, 2, 2, 16), np.uint8)
+    hm = np.zeros((nb, 2, 16), np.uint8)                        # (nb, s, l)
+    for h in range(2):
+        for j in range(4):
+            qs[:, h] |= (q[:, h, j] & 3) << (2 * j)
+            hm |= ((q[:, h, j] >> 2) & 1) << (4 * h + j)
+    sc = (l + 32).astype(np.uint8)                              # (nb, 16), 6 bits
+    sb = np.zeros((nb, 12), np.uint8)
+    sb[:, 0:8] = (sc[:, 0:8] & 15) | ((sc[:, 8:16] & 15) << 4)
+    for i in range(16):
+        sb[:, 8 + i % 4] |= ((sc[:, i] >> 4) & 3) << (2 * (i // 4))
+    out = np.empty((nb, 110), np.uint8)
+    out[:, 0:32] = hm.reshape(nb, 32)
+    out[:, 32:96] = qs.reshape(nb, 64)
+    out[:, 96:108] = sb
+    out[:, 108:110] = d16.view(np.uint8).reshape(-1, 2)
+    return out.reshape(-1)
+
+
 _QUANTIZERS = {Q8_0: (32, 34, _quantize_q8_0), Q4_K: (256, 144, _quantize_q4_k),
                Q5_K: (256, 176, _quantize_q5_k), Q6_K: (256, 210, _quantize_q6_k),
                Q4_0: (32, 18, _quantize_q4_0), Q5_0: (32, 22, _quantize_q5_0),
                IQ4_NL: (32, 18, _quantize_iq4_nl), IQ4_XS: (256, 136, _quantize_iq4_xs),
-               Q2_K: (256, 84, _quantize_q2_k)}
+               Q2_K: (256, 84, _quantize_q2_k), Q3_K: (256, 110, _quantize_q3_k)}
 
 
 def quantize(w: np.ndarray, ggml_type: int) -> np.ndarray:

@@ -46,7 +46,7 @@ sys.path.insert(0, ROOT)
 HBM_PEAK_GBS = 8000.0           # MI355X HBM3E, published
 FP16_PEAK_TFLOPS = 2500.0       # MI355X dense fp16 MFMA, published
 BLOCK = {8: (32, 34), 12: (256, 144), 13: (256, 176), 14: (256, 210), 2: (32, 18), 6: (32, 22),
-         20: (32, 18), 23: (256, 136), 10: (256, 84)}
+         20: (32, 18), 23: (256, 136), 10: (256, 84), 11: (256, 110)}
 
 
 def parse():
@@ -289,12 +289,12 @@ def secondary_cases(pkg, args, pool, secondary):
         secondary["q8_0_decode_m1_frac_hbm"] = round(r["gbs"] / HBM_PEAK_GBS, 4)
         del qpool
     if want("small_blocks"):
-        for tt, name in ((2, "q4_0"), (6, "q5_0"), (20, "iq4_nl"), (23, "iq4_xs"), (10, "q2_k")):
+        for tt, name in ((2, "q4_0"), (6, "q5_0"), (20, "iq4_nl"), (23, "iq4_xs"), (10, "q2_k"), (11, "q3_k")):
             spool, _ = make_pool(pkg, tt, 14336, 4096, 20, seed=8 + tt)
             r = matmul_case(pkg, tt, 1, 14336, 4096, spool, 280, 10, replays=3)
             secondary[f"{name}_decode_m1_gbs"] = round(r["gbs"], 1)
             secondary[f"{name}_decode_m1_frac_hbm"] = round(r["gbs"] / HBM_PEAK_GBS, 4)
-            if tt in (23, 10):
+            if tt in (23, 10, 11):
                 r = matmul_case(pkg, tt, 2048, 14336, 4096, spool[:2], 10, 2, xdtype="float16")
                 secondary[f"{name}_gemm_m2048_n14336_tflops"] = round(r["tflops"], 1)
                 secondary[f"{name}_gemm_m2048_n14336_frac_fp16_peak"] = round(

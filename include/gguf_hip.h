@@ -21,7 +21,7 @@
  *    owned by the caller, as in the reference (forward-pass.ts:1140-1163).
  *  - Weights live in the "row-tile layout": rows are grouped in tiles of 16
  *    (the last tile zero-padded); for each 256-element superblock (Q2_K,
- *    Q4_K, Q5_K, Q6_K, IQ4_XS) or 32-element block (Q8_0, Q4_0, Q5_0, IQ4_NL) of
+ *    Q3_K, Q4_K, Q5_K, Q6_K, IQ4_XS) or 32-element block (Q8_0, Q4_0, Q5_0, IQ4_NL) of
  *    K, a tile stores the 16 rows' GGUF blocks interleaved at 16-byte
  *    granularity (8 bytes for Q8_0 quants; the 4-bit codes of Q4_0 / Q5_0 /
  *    IQ4_NL and of each IQ4_XS sub-block regrouped into one 4-byte word per
@@ -46,7 +46,7 @@ extern "C" {
  * are exported (kernels and helpers cannot be interposed across libraries). */
 #pragma GCC visibility push(default)
 
-#define GGUF_HIP_ABI_VERSION 10
+#define GGUF_HIP_ABI_VERSION 11
 
 /* ggml type ids (gguf.ts:24-35); activation dtypes reuse F32 / F16. */
 #define GGUF_HIP_F32 0
@@ -55,6 +55,7 @@ extern "C" {
 #define GGUF_HIP_Q5_0 6
 #define GGUF_HIP_Q8_0 8
 #define GGUF_HIP_Q2_K 10
+#define GGUF_HIP_Q3_K 11
 #define GGUF_HIP_Q4_K 12
 #define GGUF_HIP_Q5_K 13
 #define GGUF_HIP_Q6_K 14

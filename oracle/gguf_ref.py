@@ -1,5 +1,5 @@
-"""CPU oracle for the GGUF Q4_0 / Q5_0 / Q8_0 / IQ4_NL / IQ4_XS / Q2_K / Q4_K / Q5_K / Q6_K
-dequant-matmul path.
+"""CPU oracle for the GGUF Q4_0 / Q5_0 / Q8_0 / IQ4_NL / IQ4_XS / Q2_K / Q3_K / Q4_K / Q5_K /
+Q6_K dequant-matmul path.
 
 TEST INFRASTRUCTURE ONLY.  This module is the checker: only ``tests/``,
 ``__graft_entry__.smoke()`` and the ``cpu_baseline`` leg of ``bench.py`` may
@@ -17,7 +17,7 @@ It restates the reference's CPU dequantization
   the loops because every product in these formats is exact in f32 (Q8_0
   ``d*q`` needs <= 18 significant bits, Q4_0 / Q5_0 ``d*(q-8)`` / ``d*(q-16)``
   <= 15 / 16, IQ4_NL ``d*kvalues[q]`` <= 18, IQ4_XS ``d*(ls-32)*kvalues[q]``
-  <= 23, Q2_K ``d*sc*q`` <= 17 and ``dmin*m`` <= 15, Q6_K ``d*sc*q`` <= 23, Q4_K
+  <= 23, Q2_K ``d*sc*q`` <= 17 and ``dmin*m`` <= 15, Q3_K ``d*(sc-32)*(q-4)`` <= 20, Q6_K ``d*sc*q`` <= 23, Q4_K
   ``d*sc*q`` <= 21, Q5_K ``d*sc*q`` <= 22 and ``dmin*m`` <= 17) and the only
   rounding left is the final Q2_K / Q4_K / Q5_K subtraction, which f32 and
   f64-then-f32 both round correctly (the exact difference is a multiple of
@@ -45,7 +45,9 @@ separately, its equality with eight IQ4_NL blocks of scale d * (ls - 32)
 where that scale is an f16, and the quantizer's round trip.  Q2_K (no
 fixture) is pinned by exact rational arithmetic, a closed-form superblock
 whose every element sits in its own (group, code) cell, and the quantizer's
-round trip.
+round trip.  Q3_K likewise (exact rationals with the scale bits read as
+fields of a 96-bit integer, a closed-form superblock, the quantizer's round
+trip).
 ``matmul_bt`` is pinned against numpy float64 products and linearity.
 """
 
@@ -56,7 +58,7 @@ import math
 import numpy as np
 
 T_F32, T_F16, T_Q8_0, T_Q4_K, T_Q5_K, T_Q6_K, T_BF16 = 0, 1, 8, 12, 13, 14, 30
-T_Q4_0, T_Q5_0, T_IQ4_NL, T_IQ4_XS, T_Q2_K = 2, 6, 20, 23, 10
+T_Q4_0, T_Q5_0, T_IQ4_NL, T_IQ4_XS, T_Q2_K, T_Q3_K = 2, 6, 20, 23, 10, 11
 
 # kvalues_iq4nl, gguf-dequant.ts:29 (shared by IQ4_NL and IQ4_XS)
 KVALUES_IQ4NL = (-127, -104, -83, -65, -49, -35, -22, -10, 1, 13, 25, 38, 53, 69, 89, 113)
@@ -178,6 +180,40 @@ def dequant_q2_k_loop(data: bytes, n: int) -> np.ndarray:
                         out[oi] = dl * ((data[q_base + half + l] >> shift) & 3) - ml
                         oi += 1
                 shift += 2
+    return out
+
+
+def dequant_q3_k_loop(data: bytes, n: int) -> np.ndarray:
+    """gguf-dequant.ts:213-252."""
+    if n % 256 != 0:
+        raise ValueError(f"[Q3_K] n={n} not divisible by 256")
+    km1, km2 = 0x03030303, 0x0F0F0F0F
+    out = np.zeros(n, np.float32)
+    for b in range(n // 256):
+        base = b * 110
+        d_all = f16_to_f32(_u16(data, base + 108))
+        s0 = int.from_bytes(data[base + 96:base + 100], "little")
+        s1 = int.from_bytes(data[base + 100:base + 104], "little")
+        tmp = int.from_bytes(data[base + 104:base + 108], "little")
+        aux2 = ((s0 >> 4) & km2) | (((tmp >> 4) & km1) << 4)
+        aux3 = ((s1 >> 4) & km2) | (((tmp >> 6) & km1) << 4)
+        aux0 = (s0 & km2) | (((tmp >> 0) & km1) << 4)
+        aux1 = (s1 & km2) | (((tmp >> 2) & km1) << 4)
+        aux = b"".join(v.to_bytes(4, "little") for v in (aux0, aux1, aux2, aux3))
+        oi, is_, m = b * 256, 0, 1
+        for nn in (0, 128):
+            q_base = base + 32 + (nn // 128) * 32
+            shift = 0
+            for _j in range(4):
+                for half in (0, 16):
+                    dl = d_all * (aux[is_] - 32)
+                    is_ += 1
+                    for l in range(16):
+                        q3 = (data[q_base + half + l] >> shift) & 3
+                        out[oi] = dl * (q3 - (0 if data[base + half + l] & m else 4))
+                        oi += 1
+                shift += 2
+                m <<= 1
     return out
 
 
@@ -310,6 +346,8 @@ def dequant_ggml_loop(ggml_type: int, data: bytes, n: int) -> np.ndarray:
         return dequant_iq4_xs_loop(data, n)
     if ggml_type == T_Q2_K:
         return dequant_q2_k_loop(data, n)
+    if ggml_type == T_Q3_K:
+        return dequant_q3_k_loop(data, n)
     if ggml_type == T_Q4_K:
         return dequant_q4_k_loop(data, n)
     if ggml_type == T_Q5_K:
@@ -333,6 +371,7 @@ assert Q5_K_BLOCK.itemsize == 176
 Q4_0_BLOCK = np.dtype([("d", "<f2"), ("qs", "u1", 16)])           # also IQ4_NL
 Q5_0_BLOCK = np.dtype([("d", "<f2"), ("qh", "<u4"), ("qs", "u1", 16)])
 Q2_K_BLOCK = np.dtype([("scales", "u1", 16), ("qs", "u1", 64), ("d", "<f2"), ("dmin", "<f2")])
+Q3_K_BLOCK = np.dtype([("hmask", "u1", 32), ("qs", "u1", 64), ("scales", "u1", 12), ("d", "<f2")])
 IQ4_XS_BLOCK = np.dtype([("d", "<f2"), ("scales_h", "<u2"), ("scales_l", "u1", 4), ("qs", "u1", 128)])
 assert Q4_0_BLOCK.itemsize == 18 and Q5_0_BLOCK.itemsize == 22
 
@@ -412,6 +451,29 @@ def dequant_q2_k(data, n: int) -> np.ndarray:
     dl = np.repeat(d * (sc & 0xF).astype(np.float32), 16, axis=1)   # group e // 16
     ml = np.repeat(dmin * (sc >> 4).astype(np.float32), 16, axis=1)
     return (dl * q2_k_codes(blk).astype(np.float32) - ml).reshape(-1)
+
+
+def q3_k_scales(blk: np.ndarray) -> np.ndarray:
+    """The 16 6-bit scales (stored + 32) of Q3_K superblocks, (nb, 16): low nibbles
+    are the low / high nibbles of bytes 0-7 (scales 0-7 / 8-15), bits 4-5 of scale i
+    are bits 2 (i // 4) of byte 8 + i % 4."""
+    a = blk["scales"]
+    lo = np.concatenate([a[:, :8] & 15, a[:, :8] >> 4], axis=1)
+    i = np.arange(16)
+    hi = (a[:, 8 + i % 4] >> (2 * (i // 4))) & 3
+    return lo.astype(np.int32) | (hi.astype(np.int32) << 4)
+
+
+def dequant_q3_k(data, n: int) -> np.ndarray:
+    blk = _blocks(data, Q3_K_BLOCK, n, 256, "Q3_K")
+    d = blk["d"].astype(np.float32)[:, None]
+    dl = np.repeat(d * (q3_k_scales(blk) - 32).astype(np.float32), 16, axis=1)
+    low = q2_k_codes(blk)
+    hb = (blk["hmask"].reshape(-1, 1, 1, 32) >>
+          (4 * np.arange(2, dtype=np.uint8).reshape(1, 2, 1, 1) +
+           np.arange(4, dtype=np.uint8).reshape(1, 1, 4, 1))) & 1
+    q3 = low.astype(np.int32) + 4 * hb.reshape(-1, 256).astype(np.int32) - 4
+    return (dl * q3.astype(np.float32)).reshape(-1)
 
 
 def iq4_xs_scales(blk: np.ndarray) -> np.ndarray:
@@ -503,6 +565,8 @@ def dequant_ggml(ggml_type: int, data, n: int) -> np.ndarray:
         return dequant_iq4_xs(data, n)
     if ggml_type == T_Q2_K:
         return dequant_q2_k(data, n)
+    if ggml_type == T_Q3_K:
+        return dequant_q3_k(data, n)
     if ggml_type == T_Q4_K:
         return dequant_q4_k(data, n)
     if ggml_type == T_Q5_K:

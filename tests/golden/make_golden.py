@@ -101,7 +101,7 @@ def write_synthetic() -> None:
 
     arrays = {}
     for t, (n, k) in {8: (5, 96), 12: (3, 512), 13: (3, 512), 14: (3, 512), 2: (5, 96),
-                      6: (5, 96), 20: (5, 96), 23: (3, 512), 10: (3, 512)}.items():
+                      6: (5, 96), 20: (5, 96), 23: (3, 512), 10: (3, 512), 11: (3, 512)}.items():
         w = pkg.quantize.synthetic_weight(n, k, seed=1000 + t)
         raw = pkg.quantize.quantize(w, t)
         deq = gguf_ref.dequant_rows(t, raw, n, k)

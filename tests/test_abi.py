@@ -70,7 +70,7 @@ def test_constants_match_header(native):
 
 
 def test_abi_version(lib):
-    assert lib.gguf_hip_abi_version() == 10
+    assert lib.gguf_hip_abi_version() == 11
 
 
 def test_type_traits(lib, native):
@@ -82,7 +82,7 @@ def test_type_traits(lib, native):
 
 
 def test_byte_queries_agree_with_python(lib, pkg):
-    for t in (2, 6, 8, 10, 12, 13, 14, 20, 23):
+    for t in (2, 6, 8, 10, 11, 12, 13, 14, 20, 23):
         for k in (256, 512, 1024, 4096, 14336):
             assert lib.gguf_hip_tile_bytes(t, 7, k) == 16 * pkg.tile_row_bytes(t, k)
             assert lib.gguf_hip_tile_bytes(t, 33, k) == pkg.tiled_bytes(t, 33, k)
@@ -139,7 +139,7 @@ def test_matmul_errors(lib, native):
     assert mm(x, 0, 512, w, 12, 8, 512, y, 8, 1, 9, None) == native.ERR_SHAPE    # bad variant
     assert "unknown kernel variant 9" in native.last_error(lib)
     assert mm(x, 0, 512, w, 12, 8, 512, y, 8, 1, -1, None) == native.ERR_SHAPE
-    assert mm(x, 0, 512, w, 11, 8, 512, y, 8, 1, 0, None) == native.ERR_TYPE     # Q3_K
+    assert mm(x, 0, 512, w, 3, 8, 512, y, 8, 1, 0, None) == native.ERR_TYPE      # Q4_1
     assert mm(x, 0, 512, w, 12, 8, 500, y, 8, 1, 0, None) == native.ERR_SHAPE
     assert mm(None, 0, 512, w, 12, 8, 512, y, 8, 1, 0, None) == native.ERR_NULL
     assert mm(x + 4, 0, 512, w, 12, 8, 512, y, 8, 1, 0, None) == native.ERR_ALIGN
@@ -223,7 +223,7 @@ def test_attn_merge_errors(lib, native):
     assert f(wk, pos, 32, 5, 128, 512, w, 12, 64, y, 1, None) == native.ERR_SHAPE   # 32 % 5
     assert f(wk, pos, 32, 8, 96, 512, w, 12, 64, y, 1, None) == native.ERR_SHAPE    # head_dim
     assert f(wk, pos, 32, 8, 128, 0, w, 12, 64, y, 1, None) == native.ERR_SHAPE     # max_seq
-    assert f(wk, pos, 32, 8, 128, 512, w, 11, 64, y, 1, None) == native.ERR_TYPE
+    assert f(wk, pos, 32, 8, 128, 512, w, 3, 64, y, 1, None) == native.ERR_TYPE
     assert f(wk, pos, 3, 1, 64, 512, w, 12, 64, y, 1, None) == native.ERR_SHAPE     # K=192 % 256
     assert f(wk, pos, 32, 8, 128, 512, w, 12, 64, y, 2, None) == native.ERR_SHAPE   # SwiGLU epi
     assert "epilogue 2" in native.last_error(lib)
@@ -245,7 +245,7 @@ def test_fused_matmul_errors(lib, native):
     assert f(x, w, 12, 64, 4096, y, 1, None, 1e-6, 0, None) == native.ERR_NULL     # no norm weight
     assert f(x, w, 12, 64, 4096, y, 1, nw, -1.0, 0, None) == native.ERR_SHAPE
     assert f(x + 4, w, 12, 64, 4096, y, 0, None, 0.0, 0, None) == native.ERR_ALIGN
-    assert f(x, w, 11, 64, 4096, y, 0, None, 0.0, 0, None) == native.ERR_TYPE
+    assert f(x, w, 3, 64, 4096, y, 0, None, 0.0, 0, None) == native.ERR_TYPE
     assert f(x, w, 12, 64, 4096, y, 0, None, 0.0, 3, None) == native.ERR_SHAPE      # epilogue
     assert f(x, w, 12, 48, 4096, y, 0, None, 0.0, 2, None) == native.ERR_SHAPE      # SwiGLU: N % 32
     assert f(x, w, 12, 0, 4096, y, 2, None, 0.0, 1, None) == 0                     # N = 0: no-op

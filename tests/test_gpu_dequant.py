@@ -15,8 +15,9 @@ SHAPES = {8: [(1, 32), (3, 96), (5, 4096), (2, 160)],
           2: [(1, 32), (3, 96), (5, 4096), (2, 160)],
           6: [(1, 32), (3, 96), (5, 4096), (2, 160)],
           20: [(1, 32), (3, 96), (5, 4096), (2, 160)], 23: [(1, 256), (3, 512), (17, 4096)],
-          10: [(1, 256), (4, 768), (17, 4096), (2, 14336)]}
-ALL = [2, 6, 8, 10, 12, 13, 14, 20, 23]
+          10: [(1, 256), (4, 768), (17, 4096), (2, 14336)],
+          11: [(1, 256), (4, 768), (17, 4096)]}
+ALL = [2, 6, 8, 10, 11, 12, 13, 14, 20, 23]
 
 
 def _dev_u8(a):
@@ -91,7 +92,7 @@ def test_full_size_dequant(pkg, ref, t, n, k):
     raw_dev = torch.randint(0, 256, (n * rows_bytes,), dtype=torch.uint8, device="cuda")
     # stamp finite scales into every block on the device
     blocks = raw_dev.view(-1, size)
-    offs = {8: [0], 12: [0, 2], 13: [0, 2], 14: [208], 2: [0], 6: [0], 20: [0], 23: [0], 10: [80, 82]}[t]
+    offs = {8: [0], 12: [0, 2], 13: [0, 2], 14: [208], 2: [0], 6: [0], 20: [0], 23: [0], 10: [80, 82], 11: [108]}[t]
     for o in offs:
         vals = torch.empty(blocks.shape[0], device="cuda").uniform_(0.001, 0.01).half()
         blocks[:, o:o + 2] = vals.view(torch.uint8).view(-1, 2)

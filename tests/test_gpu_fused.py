@@ -35,7 +35,7 @@ def _elementwise(y, ref, wd, xd):
                                    (8, 512, 4096), (12, 4096, 14336), (14, 2048, 4096),
                                    (2, 1000, 4096), (6, 512, 14336), (20, 2048, 4096),
                                    (23, 1000, 4096), (23, 4096, 14336), (10, 1000, 4096),
-                                   (10, 4096, 14336)])
+                                   (10, 4096, 14336), (11, 1000, 4096), (11, 4096, 14336)])
 def test_rmsnorm_prologue(mods, t, n, k):
     pkg, glue = mods
     w = _weight(pkg, t, n, k, seed=n + k)
@@ -71,7 +71,7 @@ def test_swiglu_prologue_accumulate(mods, t, n, k):
 
 @pytest.mark.parametrize("t,ffn,k", [(12, 14336, 4096), (12, 512, 2048), (13, 1024, 4096),
                                      (14, 256, 4096), (8, 768, 1024), (23, 1024, 4096),
-                                     (10, 1024, 4096)])
+                                     (10, 1024, 4096), (11, 1024, 4096)])
 @pytest.mark.parametrize("norm", [False, True])
 def test_swiglu_epilogue(mods, t, ffn, k, norm):
     """Interleaved gate / up tiles: y = up * silu(gate) straight from the projection,
@@ -141,7 +141,8 @@ def _attention_inputs(nh, nkv, hd, max_seq, p):
     (12, 32, 8, 128, 1200, 0), (12, 32, 8, 128, 1200, 63), (12, 32, 8, 128, 1200, 64),
     (12, 32, 8, 128, 1200, 300), (12, 32, 8, 128, 1200, 511), (12, 32, 8, 128, 1200, 1199),
     (14, 32, 8, 128, 640, 383), (8, 8, 8, 64, 128, 100), (12, 16, 2, 256, 700, 650),
-    (13, 64, 8, 128, 256, 200), (23, 32, 8, 128, 300, 130), (10, 32, 8, 128, 300, 77)])
+    (13, 64, 8, 128, 256, 200), (23, 32, 8, 128, 300, 130), (10, 32, 8, 128, 300, 77),
+    (11, 32, 8, 128, 300, 200)])
 def test_attention_merge_projection(mods, t, nh, nkv, hd, max_seq, p):
     """Records-only attention + the merge prologue equal, bit for bit, attention
     with its own merge followed by the plain fused projection (same arithmetic

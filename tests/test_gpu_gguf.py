@@ -29,7 +29,7 @@ gmodel = importlib.import_module("artifex-assistantv5_amd.gguf_model")
 dec = importlib.import_module("artifex-assistantv5_amd.decoder")
 
 
-@pytest.mark.parametrize("t", [2, 6, 8, 10, 12, 13, 14, 20, 23])
+@pytest.mark.parametrize("t", [2, 6, 8, 10, 11, 12, 13, 14, 20, 23])
 def test_get_rows_bit_exact(ref, t):
     n, k = 40, 512
     raw = pkg.quantize.quantize(pkg.quantize.synthetic_weight(n, k, seed=t, std=1.0), t)

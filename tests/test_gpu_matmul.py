@@ -43,7 +43,7 @@ SMALL = [(1, 1, 256), (1, 70, 512), (3, 70, 512), (1, 257, 1280), (7, 9, 768), (
          (32, 64, 1024), (33, 129, 512), (130, 200, 768)]
 
 
-@pytest.mark.parametrize("t", [2, 6, 8, 10, 12, 13, 14, 20, 23])
+@pytest.mark.parametrize("t", [2, 6, 8, 10, 11, 12, 13, 14, 20, 23])
 @pytest.mark.parametrize("variant", [DECODE, GEMM, AUTO])
 @pytest.mark.parametrize("xdt", ["f32", "f16"])
 def test_small_shapes(pkg, ref, t, variant, xdt):
@@ -72,7 +72,7 @@ def test_q8_0_k_not_multiple_of_64(pkg, ref, t):
 DECODE_TOL = 2e-5
 
 
-@pytest.mark.parametrize("t", [2, 6, 8, 10, 12, 13, 14, 20, 23])
+@pytest.mark.parametrize("t", [2, 6, 8, 10, 11, 12, 13, 14, 20, 23])
 def test_decode_is_f32_grade(pkg, ref, t):
     """The decode path feeds exact quant codes and hi/lo-split f32 activations to
     the matrix cores: per element |y - y_ref| <= 2e-5 * sum_k |x_k w_nk| (a
@@ -91,7 +91,7 @@ def test_decode_is_f32_grade(pkg, ref, t):
 
 def test_reference_kernel_test_shapes(pkg, ref):
     """kernel-tests.ts:910-927: M=3, N=70, K=512 per type, and N > 65535 (Q8_0, M=1, K=64)."""
-    for t in (2, 6, 8, 10, 12, 13, 14, 20, 23):
+    for t in (2, 6, 8, 10, 11, 12, 13, 14, 20, 23):
         raw = tile_model.random_blocks(t, 70, 512, seed=t)
         w = pkg.repack_gguf_for_gpu(t, raw, 70, 512)
         a = (np.random.default_rng(t).random((3, 512), dtype=np.float32) * 0.5 - 0.25)
@@ -204,6 +204,8 @@ FULL = [  # (type, M, N, K, x dtype)
     (23, 2048, 4096, 4096, torch.float16),
     (10, 1, 14336, 4096, torch.float32), (10, 8, 4096, 14336, torch.float32),
     (10, 32, 4096, 4096, torch.float32), (10, 2048, 4096, 4096, torch.float16),
+    (11, 1, 14336, 4096, torch.float32), (11, 8, 4096, 14336, torch.float32),
+    (11, 2048, 4096, 4096, torch.float16),
 ]
 
 
@@ -219,7 +221,7 @@ def test_full_size_configs(pkg, t, m, n, k, xdt):
         rawd = torch.randint(0, 256, (n * k // block * size,), dtype=torch.uint8, device="cuda",
                              generator=g)
         blocks = rawd.view(-1, size)
-        for o in {8: [0], 12: [0, 2], 13: [0, 2], 14: [208], 2: [0], 6: [0], 20: [0], 23: [0], 10: [80, 82]}[t]:
+        for o in {8: [0], 12: [0, 2], 13: [0, 2], 14: [208], 2: [0], 6: [0], 20: [0], 23: [0], 10: [80, 82], 11: [108]}[t]:
             v = (torch.rand(blocks.shape[0], device="cuda", generator=g) * 0.003 + 0.0005).half()
             blocks[:, o:o + 2] = v.view(torch.uint8).view(-1, 2)
         w = pkg.repack_gguf_for_gpu(t, rawd, n, k)

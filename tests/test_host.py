@@ -30,7 +30,7 @@ def test_tensor_bytes(pkg):
         g.ggml_tensor_bytes(12, [100, 3])
 
 
-@pytest.mark.parametrize("t", [2, 6, 8, 10, 12, 13, 14, 20, 23])
+@pytest.mark.parametrize("t", [2, 6, 8, 10, 11, 12, 13, 14, 20, 23])
 @pytest.mark.parametrize("k", [256, 512, 768, 1280, 4096, 14336])
 def test_tile_row_bytes(pkg, t, k):
     trb = pkg.tile_row_bytes(t, k)
@@ -75,7 +75,7 @@ def test_layout_model_roundtrip(ref, t, k, n):
     assert ref.same_bits(ref.dequant_rows(t, back, 5, k), ref.dequant_rows(t, raw, 5, k))
 
 
-@pytest.mark.parametrize("t", [2, 6, 8, 10, 12, 13, 14, 20, 23])
+@pytest.mark.parametrize("t", [2, 6, 8, 10, 11, 12, 13, 14, 20, 23])
 def test_quantize_deterministic_and_sized(pkg, t):
     w = pkg.quantize.synthetic_weight(3, 512, seed=11)
     a = pkg.quantize.quantize(w, t)

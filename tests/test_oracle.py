@@ -15,12 +15,12 @@ from fractions import Fraction
 import numpy as np
 import pytest
 
-IN_SCOPE = (2, 6, 8, 10, 12, 13, 14, 20, 23)
+IN_SCOPE = (2, 6, 8, 10, 11, 12, 13, 14, 20, 23)
 GOLDEN_TYPES = (8, 12, 13, 14)                 # the types the reference's gguf-py fixtures cover
 BLOCK = {8: (32, 34), 12: (256, 144), 13: (256, 176), 14: (256, 210), 2: (32, 18), 6: (32, 22),
-         20: (32, 18), 23: (256, 136), 10: (256, 84)}
+         20: (32, 18), 23: (256, 136), 10: (256, 84), 11: (256, 110)}
 F16_FIELDS = {8: [0], 12: [0, 2], 13: [0, 2], 14: [208], 2: [0], 6: [0], 20: [0], 23: [0],
-              10: [80, 82]}
+              10: [80, 82], 11: [108]}
 
 
 def _samples(golden_samples, types=GOLDEN_TYPES):
@@ -220,6 +220,29 @@ def exact_q2_k(raw: bytes) -> list:
     return out
 
 
+def exact_q3_k(raw: bytes) -> list:
+    """Q3_K from the element rule read as a formula: the 12 scale bytes as one 96-bit
+    integer S; the low nibble of scale i (0..15) is bits 8 (i % 8) + 4 (i // 8) of S,
+    its bits 4-5 are bits 64 + 8 (i % 4) + 2 (i // 4); element e = 128 h + 32 j + 16 s
+    + l has code digit j (base 4) of qs[32 h + 16 s + l] plus 4 x bit 4 h + j of
+    hmask[16 s + l], value d (scale - 32) (code - 4)."""
+    out = []
+    for b in range(len(raw) // 110):
+        blk = raw[110 * b:110 * (b + 1)]
+        d = f16_fraction(blk[108] | blk[109] << 8)
+        S = int.from_bytes(blk[96:108], "little")
+        sc = []
+        for i in range(16):
+            lo = (S >> (8 * (i % 8) + 4 * (i // 8))) % 16
+            hi = (S >> (64 + 8 * (i % 4) + 2 * (i // 4))) % 4
+            sc.append(lo + 16 * hi - 32)
+        for e in range(256):
+            h, j, s, l = e // 128, (e // 32) % 4, (e // 16) % 2, e % 16
+            code = (blk[32 + 32 * h + 16 * s + l] // 4 ** j) % 4 + 4 * ((blk[16 * s + l] >> (4 * h + j)) % 2)
+            out.append(round_f32(d * sc[e // 16] * (code - 4)))
+    return out
+
+
 def exact_q8_0(raw: bytes) -> list:
     out = []
     for b in range(len(raw) // 34):
@@ -245,7 +268,8 @@ def _random_blocks(t: int, nblocks: int, seed: int) -> bytes:
 
 @pytest.mark.parametrize("t,exact", [(8, exact_q8_0), (12, exact_q4_k), (13, exact_q5_k),
                                      (14, exact_q6_k), (2, exact_q4_0), (6, exact_q5_0),
-                                     (20, exact_iq4_nl), (23, exact_iq4_xs), (10, exact_q2_k)])
+                                     (20, exact_iq4_nl), (23, exact_iq4_xs), (10, exact_q2_k),
+                                     (11, exact_q3_k)])
 def test_exact_rational(ref, t, exact):
     raw = _random_blocks(t, 12, seed=t)
     n = 12 * BLOCK[t][0]
@@ -365,7 +389,7 @@ def test_quantizer_error_is_bounded(ref, pkg, t):
     assert raw.size == 4 * 512 // BLOCK[t][0] * BLOCK[t][1]
     deq = ref.dequant_rows(t, raw, 4, 512)
     rel = np.linalg.norm(deq - w) / np.linalg.norm(w)
-    assert rel < {8: 0.01, 12: 0.12, 13: 0.06, 14: 0.05, 2: 0.12, 6: 0.06, 20: 0.1, 23: 0.1, 10: 0.35}[t]
+    assert rel < {8: 0.01, 12: 0.12, 13: 0.06, 14: 0.05, 2: 0.12, 6: 0.06, 20: 0.1, 23: 0.1, 10: 0.35, 11: 0.2}[t]
 
 
 # ---------------------------------------------------------------------------
@@ -737,3 +761,39 @@ def test_q2_k_mutations_are_caught(ref):
     for bad in (decode(planes_swapped, right_scale), decode(by_64, right_scale),
                 decode(right_code, scale_per_32)):
         assert not np.array_equal(bad, good, equal_nan=True)
+
+
+def test_q3_k_closed_form(ref):
+    """Scale i = 32 + (i - 8) (signed -8..7) and code (e // 16 + 3 e) % 8 per element,
+    with d = 1: every value names its group and code, and the high bit comes from hmask."""
+    sc = [32 + i - 8 for i in range(16)]
+    sb = bytearray(12)
+    for i in range(8):
+        sb[i] = (sc[i] & 15) | ((sc[8 + i] & 15) << 4)
+    for i in range(16):
+        sb[8 + i % 4] |= ((sc[i] >> 4) & 3) << (2 * (i // 4))
+    hm, qs = bytearray(32), bytearray(64)
+    code = [(e // 16 + 3 * e) % 8 for e in range(256)]
+    for e in range(256):
+        h, j, s, l = e // 128, (e // 32) % 4, (e // 16) % 2, e % 16
+        qs[32 * h + 16 * s + l] |= (code[e] & 3) << (2 * j)
+        hm[16 * s + l] |= (code[e] >> 2) << (4 * h + j)
+    raw = bytes(hm) + bytes(qs) + bytes(sb) + struct.pack("<e", 1.0)
+    want = [(e // 16 - 8) * (code[e] - 4) for e in range(256)]
+    got = ref.dequant_ggml(11, raw, 256)
+    assert np.array_equal(got, np.array(want, np.float32))
+    assert np.array_equal(ref.dequant_ggml_loop(11, raw, 256), got)
+
+
+def test_q3_k_quantizer_roundtrip(ref, pkg):
+    w = pkg.quantize.synthetic_weight(2, 512, seed=79)
+    raw = pkg.quantize.quantize(w, 11)
+    g = w.reshape(-1, 16, 16)
+    b = g.reshape(-1, 16)
+    s = (b[np.arange(b.shape[0]), np.abs(b).argmax(axis=1)] / np.float32(-4)).reshape(-1, 16)
+    d = (np.abs(s).max(axis=1) / np.float32(31)).astype(np.float16).astype(np.float32)[:, None]
+    l = np.clip(np.rint(s / d), -32, 31)
+    dl = (d * l.astype(np.float32))[:, :, None]
+    q = np.clip(np.rint(g / dl) + 4, 0, 7)
+    want = (dl * (q - 4)).reshape(2, 512).astype(np.float32)
+    assert np.array_equal(ref.dequant_rows(11, raw, 2, 512), want)

@@ -18,6 +18,8 @@ block) a tile stores the 16 rows' GGUF blocks interleaved:
 * Q5_0: d at 2 r, qh at 32 + 4 r, then the code words at 96 + (16 g + r) 4 as Q4_0
 * Q2_K: scales[16] at 16 r, d | dmin at 256 + 4 r, then piece (g, r) at 320 + (16 g + r) 16
   = qs[8 g, +8) | qs[32 + 8 g, +8)
+* Q3_K: scales[12] at 12 r, d at 192 + 2 r, hmask piece (g, r) at 224 + (16 g + r) 8 =
+  hmask[8 g, +8), qs piece (g, r) at 736 + (16 g + r) 16 as Q2_K
 * IQ4_XS: header (d, scales_h, scales_l) at 8 r, then piece (g, r) at 128 + (16 g + r) 32
   whose word j holds sub-block j's codes 8 g .. 8 g + 7 as Q4_0 (sub-block j's 16 code
   bytes start at byte 8 + 16 j of the GGUF block)
@@ -26,7 +28,7 @@ block) a tile stores the 16 rows' GGUF blocks interleaved:
 import numpy as np
 
 BLOCK = {8: (32, 34), 12: (256, 144), 13: (256, 176), 14: (256, 210), 2: (32, 18), 6: (32, 22),
-         20: (32, 18), 23: (256, 136), 10: (256, 84)}
+         20: (32, 18), 23: (256, 136), 10: (256, 84), 11: (256, 110)}
 SMALL = (2, 6, 20, 23)      # nibble codes regrouped per lane (not a byte permutation)
 
 
@@ -60,6 +62,14 @@ def _unit_maps(t):
             if t == 13:
                 for g in range(4):
                     pos[r, 16 + 8 * g + np.arange(8)] = 2304 + (16 * g + r) * 8 + np.arange(8)
+        elif t == 11:
+            pos[r, 96:108] = 12 * r + np.arange(12)                     # scales
+            pos[r, 108:110] = 192 + 2 * r + np.arange(2)                # d
+            for g in range(4):
+                pos[r, 8 * g + np.arange(8)] = 224 + (16 * g + r) * 8 + np.arange(8)   # hmask
+                base = 736 + (16 * g + r) * 16
+                pos[r, 32 + 8 * g + np.arange(8)] = base + np.arange(8)
+                pos[r, 32 + 32 + 8 * g + np.arange(8)] = base + 8 + np.arange(8)
         elif t == 10:
             pos[r, 0:16] = 16 * r + np.arange(16)                       # scales
             pos[r, 80:84] = 256 + 4 * r + np.arange(4)                  # d, dmin
@@ -204,7 +214,7 @@ def random_blocks(t, n, k, seed, specials=False):
     nb = n * (k // block)
     raw = rng.integers(0, 256, (nb, size), dtype=np.uint8)
     offs = {8: [0], 12: [0, 2], 13: [0, 2], 14: [208], 2: [0], 6: [0], 20: [0], 23: [0],
-            10: [80, 82]}[t]
+            10: [80, 82], 11: [108]}[t]
     for o in offs:
         vals = (rng.uniform(-0.01, 0.01, nb) if t not in (12, 13) or o == 0
                 else rng.uniform(0, 0.005, nb))
