@@ -89,16 +89,21 @@ def test_tied_embeddings_feed_the_lm_head(tmp_path, ref):
     assert isinstance(m.row_tables["token_embd.weight"], pkg.QuantEmbedding)
 
 
-@pytest.mark.parametrize("variant", ["mixed_qkv", "uniform_tied"])
+LOW_BIT = {"q": 11, "k": 10, "v": 23, "o": 2, "gate": 6, "up": 6, "down": 20, "embd": 11,
+           "out": 10}          # Q3_K, Q2_K, IQ4_XS, Q4_0, Q5_0, IQ4_NL, Q3_K table, Q2_K head
+
+
+@pytest.mark.parametrize("variant", ["mixed_qkv", "uniform_tied", "low_bit"])
 def test_decoder_from_gguf_matches_direct_build(tmp_path, variant):
-    types = {} if variant == "mixed_qkv" else {"v": 12, "down": 12, "embd": 14}
+    types = {"mixed_qkv": {}, "uniform_tied": {"v": 12, "down": 12, "embd": 14},
+             "low_bit": LOW_BIT}[variant]
     tensors = gm.make_model(seed=4, types=types, tied=variant == "uniform_tied")
     p = str(tmp_path / "m.gguf")
     gm.write_model(p, tensors)
     model, loaded = gmodel.load_decoder(p, "cuda", max_seq=64)
     cfg = model.cfg
     lw = model.w.layers[0]
-    if variant == "mixed_qkv":
+    if variant != "uniform_tied":
         assert lw.get("qkv_gg") is None and len(lw.qkv_parts) == 3
     else:
         assert lw.qkv_gg is not None
