@@ -21,8 +21,8 @@ full synthetic Llama-style decoder: 32 layers, d_model 4096, 32/8 heads of
 128, SwiGLU FFN 14336, vocab 151936, Q4_K attention and gate/up, Q6_K down and
 LM head; 128 random prompt tokens then 256 greedy tokens; tok/s = generated
 tokens / decode wall time, prefill excluded).  ``secondary`` holds the other
-configurations of the path (Q8_0 / Q4_K / Q6_K decode shapes and batch sizes,
-more prefill shapes).  ``cpu_baseline`` = the CPU restatement of the reference
+configurations of the path (Q4_K / Q5_K / Q6_K decode shapes and batch sizes,
+the other GGML types at the headline shape, more prefill shapes).  ``cpu_baseline`` = the CPU restatement of the reference
 path (numpy dequant to f32 + torch fp32 matmul) on all host cores, repeated
 for about 10 s.  ``roofline.traffic`` is read from the committed rocprofv3
 counter summary of the headline kernel when present.
