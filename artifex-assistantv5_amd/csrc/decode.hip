@@ -1371,6 +1371,9 @@ __global__ __launch_bounds__(512) void decode_m1_kernel(const XT *__restrict__ x
 #ifndef GGUF_M1_MIN_WAVES
 #define GGUF_M1_MIN_WAVES 1024  // K split until the grid has this many waves
 #endif
+#ifndef GGUF_M1_ROUND_WAVES
+#define GGUF_M1_ROUND_WAVES 2048  // waves resident at once (256 CUs x 8)
+#endif
 template <int TYPE>
 constexpr int m1_umax(bool tight) {
   // 32-element blocks: up to 64 per wave (K = 16384 over 8 waves); past 32 at
@@ -1410,11 +1413,14 @@ hipError_t launch_m1(const XT *x, const uint8_t *W, int N, int K, float *y, cons
   const bool long_k = K > 4096;
   const int umax = m1_umax<TYPE>(long_k || (PRO != 0 && GGUF_M1_PRO_TIGHT));
   // K split: units per wave within the budget, and at least ~1024 waves when
-  // possible (at most 4 with the SwiGLU epilogue, which needs two tiles per workgroup)
+  // possible (at most 4 with the SwiGLU epilogue, which needs two tiles per workgroup);
+  // 32-element blocks (one MFMA per unit, latency-bound) split further while the
+  // grid stays one round of resident waves (Q8_0 4096 x 4096: 7.5 -> 6.4 us)
   int ks = 1;
   const int ks_max = epi == 2 ? 4 : 8;
   while (ks < ks_max && ks < nu &&
-         ((nu + ks - 1) / ks > umax || ntiles * ks < GGUF_M1_MIN_WAVES))
+         ((nu + ks - 1) / ks > umax || ntiles * ks < GGUF_M1_MIN_WAVES ||
+          (UE == 32 && 2 * ntiles * ks <= GGUF_M1_ROUND_WAVES)))
     ks <<= 1;
   const int per = (nu + ks - 1) / ks;
   if (per > umax) return hipErrorNotSupported;
