@@ -19,7 +19,9 @@ ROOT = os.path.dirname(HERE)
 CSRC = os.path.join(HERE, "csrc")
 BUILD = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libgguf_hip.so")
-SOURCES = ["api.hip", "layout.hip", "decode.hip", "gemm.hip", "glue.hip"]
+# every .hip file of csrc/ (the decode kernels are one translation unit per
+# ggml type, decode_<type>.hip, so that they compile in parallel)
+SOURCES = sorted(f for f in os.listdir(CSRC) if f.endswith(".hip"))
 ARCH = "gfx950"
 
 HIPCC_FLAGS = [
@@ -55,7 +57,8 @@ def _compile(src: str, verbose: bool) -> str:
 def build(verbose: bool = False) -> str:
     """Compile every HIP source and link ``libgguf_hip.so``; returns its path."""
     os.makedirs(BUILD, exist_ok=True)
-    with concurrent.futures.ThreadPoolExecutor(max_workers=len(SOURCES)) as ex:
+    workers = max(1, min(len(SOURCES), len(os.sched_getaffinity(0))))
+    with concurrent.futures.ThreadPoolExecutor(max_workers=workers) as ex:
         objs = list(ex.map(lambda s: _compile(s, verbose), SOURCES))
     tmp = LIB + ".tmp"
     # Export the C ABI only: kernel stubs and helpers bind locally, so two

@@ -229,8 +229,14 @@ int gguf_hip_matmul_variant(const void *x, int x_type, int64_t ldx, const void *
   if (!aligned(y, 4)) return fail(GGUF_HIP_ERR_ALIGN, "[gguf-hip] output must be 4-byte aligned");
 
   const hipStream_t s = (hipStream_t)stream;
+  // f16 activations: the decode path up to 32 rows, the fp16 GEMM above; f32
+  // activations keep the f32-grade decode path below GGUF_HIP_F32_GEMM_MIN_M
+  // rows (the reference computes in f32) and take the row-scaled fp16 GEMM
+  // from there on (prefill)
   if (variant == GGUF_HIP_VARIANT_AUTO)
-    variant = m <= GGUF_HIP_DECODE_MAX_M ? GGUF_HIP_VARIANT_DECODE : GGUF_HIP_VARIANT_GEMM;
+    variant = m <= (x_type == GGUF_HIP_F32 ? GGUF_HIP_F32_GEMM_MIN_M - 1 : GGUF_HIP_DECODE_MAX_M)
+                  ? GGUF_HIP_VARIANT_DECODE
+                  : GGUF_HIP_VARIANT_GEMM;
   // the GEMM addresses one 128-row activation block with 32-bit byte offsets
   if (variant == GGUF_HIP_VARIANT_GEMM && (127 * ldx + k) * esize >= ((int64_t)1 << 31))
     return fail(GGUF_HIP_ERR_SHAPE, "[gguf-hip] ldx too large for the GEMM kernel");

@@ -268,6 +268,61 @@ __device__ __forceinline__ float ubyte(uint32_t w, int i) {
   return (float)((w >> (8 * i)) & 0xFFu);
 }
 
+// Range of f32 activations on the f16 matrix-core paths.  A block of
+// activations whose largest magnitude is mx is multiplied by 2^e with
+// e = stage_exp(mx), which puts mx in [2^14, 2^15): no f16 overflow (65504),
+// and the hi / lo split keeps 22 significant bits of the block's large
+// values whatever the f32 range of the input.  Products with 2^e are exact;
+// the inverse 2^-e is applied to the block's dot products in f32.  e is
+// clamped to [-126, 126] so that both 2^e and 2^-e are normal floats (a zero
+// or subnormal block gets 2^126; an Inf / NaN block stays non-finite).
+__device__ __forceinline__ int stage_exp(float mx) {
+  // biased exponent E of mx: mx in [2^(E-127), 2^(E-126)) for normal mx
+  const int E = (int)((__float_as_uint(mx) >> 23) & 0xFFu);
+  const int e = 141 - E;  // 15 - (E - 126)
+  return e < -126 ? -126 : (e > 126 ? 126 : e);
+}
+__device__ __forceinline__ float pow2f(int e) {  // 2^e for e in [-126, 127]
+  return __uint_as_float((uint32_t)(e + 127) << 23);
+}
+
+// Cross-lane reductions on the VALU (DPP and gfx950 permlane swaps) rather than
+// through the LDS crossbar (ds_bpermute, tens of cycles each).  Every lane of
+// the wave must be active.
+template <int CTRL>
+__device__ __forceinline__ float dpp(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+constexpr int kDppXor1 = 0xB1;         // quad_perm [1, 0, 3, 2]
+constexpr int kDppXor2 = 0x4E;         // quad_perm [2, 3, 0, 1]
+constexpr int kDppHalfMirror = 0x141;  // lane i <-> 7 - i within each 8
+constexpr int kDppMirror = 0x140;      // lane i <-> 15 - i within each 16
+__device__ __forceinline__ float max_lanes2(float v) { return fmaxf(v, dpp<kDppXor1>(v)); }
+// max over each aligned group of 16 lanes, in every lane of the group
+__device__ __forceinline__ float max_lanes16(float v) {
+  v = fmaxf(v, dpp<kDppXor1>(v));
+  v = fmaxf(v, dpp<kDppXor2>(v));
+  v = fmaxf(v, dpp<kDppHalfMirror>(v));
+  return fmaxf(v, dpp<kDppMirror>(v));
+}
+// v + v of lane ^ 16 / lane ^ 32
+__device__ __forceinline__ float sum_xor16(float v) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float sum_xor32(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+// (a & m) | c.  Plain code on purpose: an inline-asm v_and_or_b32 whose input
+// was a buffer-load destination read the register before the load had landed
+// in a deeply pipelined kernel (results varied run to run); the compiler's
+// wait-count insertion is only trusted for instructions it selects itself.
+__device__ __forceinline__ uint32_t and_or(uint32_t a, uint32_t m, uint32_t c) {
+  return (a & m) | c;
+}
+
 __device__ __forceinline__ uint4 ldg16(const void *p) { return *(const uint4 *)p; }
 
 // Streaming (read-once) 16-byte load of weight data: nontemporal, so the

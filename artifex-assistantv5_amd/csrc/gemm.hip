@@ -15,10 +15,13 @@
 //                as an f16 subnormal (code x 2^-24, exact) and one
 //                v_fma_mix computes fp16(d*sc*q - dmin*m) with f32 internals:
 //                the exact f32 dequant value rounded once to fp16.
-//   activations  staged through LDS as fp16 (f32 input is rounded to fp16),
-//                two buffers, rows of 128 B whose 16-byte chunks are rotated
-//                by the row index so that fragment reads and row writes are
-//                free of bank conflicts.  Q6_K's lanes hold k in the order
+//   activations  staged through LDS as fp16, two buffers, rows of 128 B whose
+//                16-byte chunks are rotated by the row index so that fragment
+//                reads and row writes are free of bank conflicts.  f32 input
+//                is scaled per row by the power of two 2^e that puts the row's
+//                largest magnitude in [2^14, 2^15) (a pass over the block's
+//                rows before the K loop), rounded to fp16, and the row's
+//                outputs take 2^-e: any f32 range, 11 significant bits.  Q6_K's lanes hold k in the order
 //                16 lh + 4 g + b; its activation columns are permuted the same
 //                way when staged, so both MFMA operands agree.
 //
@@ -695,19 +698,29 @@ __device__ __forceinline__ void load_a(rsrc_t rs, int voff, int64_t ldxb, int k0
           ok ? bl16(rs, voff + (int)(kARows * i * ldxb) + 16 * w, soff) : make_uint4(0, 0, 0, 0);
 }
 
-__device__ __forceinline__ uint4 to_f16x8(const uint4 (&v)[1]) { return v[0]; }
-__device__ __forceinline__ uint4 to_f16x8(const uint4 (&v)[2]) {
+__device__ __forceinline__ uint4 to_f16x8(const uint4 (&v)[1], float) { return v[0]; }
+// eight f32 values times the row's power-of-two scale (exact), rounded to fp16
+__device__ __forceinline__ uint4 to_f16x8(const uint4 (&v)[2], float sc) {
   half8_t h;
   const uint4 a = v[0], b = v[1];
-  h[0] = (half_t)__uint_as_float(a.x);
-  h[1] = (half_t)__uint_as_float(a.y);
-  h[2] = (half_t)__uint_as_float(a.z);
-  h[3] = (half_t)__uint_as_float(a.w);
-  h[4] = (half_t)__uint_as_float(b.x);
-  h[5] = (half_t)__uint_as_float(b.y);
-  h[6] = (half_t)__uint_as_float(b.z);
-  h[7] = (half_t)__uint_as_float(b.w);
+  h[0] = (half_t)(__uint_as_float(a.x) * sc);
+  h[1] = (half_t)(__uint_as_float(a.y) * sc);
+  h[2] = (half_t)(__uint_as_float(a.z) * sc);
+  h[3] = (half_t)(__uint_as_float(a.w) * sc);
+  h[4] = (half_t)(__uint_as_float(b.x) * sc);
+  h[5] = (half_t)(__uint_as_float(b.y) * sc);
+  h[6] = (half_t)(__uint_as_float(b.z) * sc);
+  h[7] = (half_t)(__uint_as_float(b.w) * sc);
   return __builtin_bit_cast(uint4, h);
+}
+
+// Largest magnitude of the f32 values of a raw activation item.
+__device__ __forceinline__ float absmax(const uint4 (&v)[2], float m) {
+  const uint4 a = v[0], b = v[1];
+  m = fmaxf(m, fmaxf(fabsf(__uint_as_float(a.x)), fabsf(__uint_as_float(a.y))));
+  m = fmaxf(m, fmaxf(fabsf(__uint_as_float(a.z)), fabsf(__uint_as_float(a.w))));
+  m = fmaxf(m, fmaxf(fabsf(__uint_as_float(b.x)), fabsf(__uint_as_float(b.y))));
+  return fmaxf(m, fmaxf(fabsf(__uint_as_float(b.z)), fabsf(__uint_as_float(b.w))));
 }
 
 // LDS byte address of (row, 16-byte chunk): chunks rotate by the row index.
@@ -717,10 +730,10 @@ __device__ __forceinline__ int lds_at(int row, int chunk) {
 
 template <int TYPE, typename XT>
 __device__ __forceinline__ void store_a(unsigned char *lds, int stage, int row0, int cc,
-                                        const ARaw<XT> &a) {
+                                        const ARaw<XT> &a, const float (&rsc)[kAI]) {
 #pragma unroll
   for (int i = 0; i < kAI; ++i) {
-    const uint4 h = to_f16x8(a.v[i]);
+    const uint4 h = to_f16x8(a.v[i], rsc[i]);
     const int row = row0 + kARows * i;
     unsigned char *base = lds + stage * kStageB;
     if constexpr (TYPE == 14) {
@@ -745,6 +758,7 @@ struct Gemm {
   int K, nu, ts;
   BOff bo;
   int afrag[2];  // LDS byte address of the lane's A fragment, k-block 0 / 1
+  float rsc[kAI];     // power-of-two scales of the staged rows (f32 input)
   ARaw<XT> ar[2];     // raw loads of the next two steps, by step parity
   BRaw<TYPE> br[2];
   BHdr<TYPE> hn;       // superblock fields loaded ahead
@@ -763,7 +777,7 @@ struct Gemm {
   __device__ __forceinline__ void prepare(int stage) {
     if (C == 0) hc.set(hn);
     dequant_b<C>(br[P], hc, bf, lg);
-    store_a<TYPE, XT>(lds, stage, row0, cc, ar[P]);
+    store_a<TYPE, XT>(lds, stage, row0, cc, ar[P], rsc);
   }
 
   // Step s (parity P = s & 1) from LDS stage P.  Loads step s + 2 (window C2 of
@@ -807,6 +821,7 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(const XT *__restrict__ x
                                                            int64_t ldy, int tiles_m) {
   constexpr int TU = Fmt<TYPE>::TU, UE = Fmt<TYPE>::UE;
   __shared__ __align__(16) unsigned char lds[2 * kStageB];
+  __shared__ __align__(16) float rowf[kBM];  // f32 input: the rows' inverse scales 2^-e
 
   int bid = blockIdx.x;
   if ((gridDim.x & 7) == 0) bid = (bid & 7) * (gridDim.x >> 3) + (bid >> 3);
@@ -842,6 +857,30 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(const XT *__restrict__ x
   for (int i = 0; i < kTM; ++i)
 #pragma unroll
     for (int j = 0; j < kTN; ++j) s.acc[i][j] = float4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int i = 0; i < kAI; ++i) s.rsc[i] = 1.0f;
+  if constexpr (sizeof(XT) == 4) {
+    // row scales: each thread reads its staged rows' column chunk of every
+    // step; the 8 threads of a row are lanes 8 j .. 8 j + 7 of a wave
+    float mx[kAI];
+#pragma unroll
+    for (int i = 0; i < kAI; ++i) mx[i] = 0.f;
+#pragma unroll 4
+    for (int k0 = 0; k0 < K; k0 += kBK) {
+      ARaw<XT> a;
+      load_a<TYPE, XT>(s.ars, s.avoff, s.ldxb, k0, K, s.cc, a);
+#pragma unroll
+      for (int i = 0; i < kAI; ++i) mx[i] = absmax(a.v[i], mx[i]);
+    }
+#pragma unroll
+    for (int i = 0; i < kAI; ++i) {
+#pragma unroll
+      for (int o = 1; o < 8; o <<= 1) mx[i] = fmaxf(mx[i], __shfl_xor(mx[i], o));
+      const int e = stage_exp(mx[i]);
+      s.rsc[i] = pow2f(e);
+      if (s.cc == 0) rowf[s.row0 + kARows * i] = pow2f(-e);
+    }
+  }
 
   if constexpr (UE == 256) {
     // step s = 4 u + c covers window c of superblock u; 4 nu >= 4 steps
@@ -873,16 +912,25 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(const XT *__restrict__ x
 
   // D layout of the 16x16 MFMA: lane holds rows 4 g + e of column r
 #pragma unroll
-  for (int i = 0; i < kTM; ++i)
+  for (int i = 0; i < kTM; ++i) {
+    float f[4] = {1.f, 1.f, 1.f, 1.f};
+    if constexpr (sizeof(XT) == 4) {
+      const float4 v = *(const float4 *)(rowf + 16 * i + 4 * g);
+      f[0] = v.x;
+      f[1] = v.y;
+      f[2] = v.z;
+      f[3] = v.w;
+    }
 #pragma unroll
     for (int j = 0; j < kTN; ++j) {
       const int n = n0 + 16 * (kTN * wave + j) + r;
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const int m = m0 + 16 * i + 4 * g + e;
-        if (m < M && n < N) y[(int64_t)m * ldy + n] = s.acc[i][j][e];
+        if (m < M && n < N) y[(int64_t)m * ldy + n] = s.acc[i][j][e] * f[e];
       }
     }
+  }
 }
 
 template <int TYPE, typename XT>

@@ -80,13 +80,17 @@ extern "C" {
 #define GGUF_HIP_ERR_HIP (-7)
 
 /* Kernel family for gguf_hip_matmul_variant. */
-#define GGUF_HIP_VARIANT_AUTO 0   /* DECODE for M <= GGUF_HIP_DECODE_MAX_M, GEMM above */
-#define GGUF_HIP_VARIANT_DECODE 1 /* matrix-core decode: exact quant codes x split f16
-                                     activations, f32 scales; one pass over the weights
-                                     per 32 activation rows (any M) */
+#define GGUF_HIP_VARIANT_AUTO 0   /* DECODE for f16 x with M <= GGUF_HIP_DECODE_MAX_M and
+                                     for f32 x with M < GGUF_HIP_F32_GEMM_MIN_M, GEMM above */
+#define GGUF_HIP_VARIANT_DECODE 1 /* matrix-core decode: exact quant codes x f16 hi + lo
+                                     parts of the activations scaled by a power of two
+                                     per 256- or 32-element unit, f32 scales; one pass
+                                     over the weights per 32 activation rows (any M) */
 #define GGUF_HIP_VARIANT_GEMM 2   /* MFMA GEMM with dequantized fp16 weight tiles and fp16
-                                     activations staged in LDS (prefill) */
+                                     activations staged in LDS (prefill); f32 activation
+                                     rows are scaled by a power of two each first */
 #define GGUF_HIP_DECODE_MAX_M 32
+#define GGUF_HIP_F32_GEMM_MIN_M 512
 
 /* ABI version of the loaded library (GGUF_HIP_ABI_VERSION). */
 int gguf_hip_abi_version(void);
@@ -137,7 +141,9 @@ int gguf_hip_get_rows(const void *raw, int ggml_type, int64_t n_rows, int64_t k,
 
 /* y[m * ldy + n] = sum_k x[m * ldx + k] * dequant(W)[n, k] for m < M, n < N.
  * x: f32 or f16 (x_type = GGUF_HIP_F32 / GGUF_HIP_F16), 16-byte aligned rows
- * (ldx * sizeof(x) % 16 == 0), finite and within the f16 range (|x| < 65504).
+ * (ldx * sizeof(x) % 16 == 0), any finite values: the kernels scale blocks of
+ * activations by powers of two before they enter the f16 matrix cores, so
+ * there is no range limit beyond f32's own (non-finite x gives non-finite y).
  * W: row-tile layout, 16-byte aligned.
  * y: f32, 4-byte aligned.  Accumulation in f32.  Replaces dispatchMatmulGGUF
  * (forward-pass.ts:1496-1544); its io.aOffset / io.cOffset windows are plain

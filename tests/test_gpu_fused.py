@@ -190,3 +190,25 @@ def test_attention_merge_bad_position(mods):
     for p in (max_seq, -1):
         glue.matmul_attn_merge(work, torch.tensor([p], device="cuda"), w, y, nh, nkv, hd, max_seq)
         assert torch.isnan(y).all()
+
+
+def test_fused_lm_head_full_vocab(mods):
+    """The decode step's LM head: RMSNorm prologue over a Q6_K weight of 151936 x 4096."""
+    pkg, glue = mods
+    dec = importlib.import_module("artifex-assistantv5_amd.decoder")
+    n, k = 151936, 4096
+    w = dec._tiled_rows(14, 2048, n, k, seed=11, device="cuda")
+    g = torch.Generator(device="cuda").manual_seed(5)
+    x = torch.randn(k, device="cuda", generator=g) * 3
+    nw = 1 + 0.02 * torch.randn(k, device="cuda", generator=g)
+    y = torch.empty(n, device="cuda")
+    glue.matmul_fused(x, w, y, glue.PROLOGUE_RMSNORM, nw, 1e-6)
+    xd = x.double()
+    h = xd / torch.sqrt((xd * xd).mean() + 1e-6) * nw.double()
+    wd = w.dequant().double()
+    ref = wd @ h
+    assert torch.isfinite(y).all()
+    assert _rel(y, ref) < 1e-5
+    assert _elementwise(y, ref, wd, h) < 1e-6
+    del wd
+    torch.cuda.empty_cache()

@@ -193,7 +193,12 @@ FULL = [  # (type, M, N, K, x dtype)
     (12, 1, 4096, 14336, torch.float32), (12, 8, 4096, 14336, torch.float32),
     (12, 32, 4096, 14336, torch.float32),
     (14, 1, 151936, 4096, torch.float32),
-    (12, 512, 4096, 4096, torch.float16), (12, 2048, 14336, 4096, torch.float16),
+    # the prefill GEMM at every (M, N) of the Q4_K prefill configuration
+    (12, 512, 4096, 4096, torch.float16), (12, 512, 14336, 4096, torch.float16),
+    (12, 2048, 4096, 4096, torch.float16), (12, 2048, 14336, 4096, torch.float16),
+    (12, 8192, 4096, 4096, torch.float16), (12, 8192, 14336, 4096, torch.float16),
+    # f32 activations: below 512 rows the decode path, from 512 on the row-scaled GEMM
+    (12, 100, 4096, 4096, torch.float32), (12, 512, 4096, 4096, torch.float32),
     (13, 1, 4096, 14336, torch.float32), (13, 8, 1024, 4096, torch.float32),
     (13, 512, 4096, 4096, torch.float16),
     (2, 1, 14336, 4096, torch.float32), (2, 8, 4096, 14336, torch.float32),
