@@ -17,13 +17,14 @@ from .ggml import GGMLTypeError
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libgguf_hip.so")
-ABI_VERSION = 11
+ABI_VERSION = 12
 
 ERR_TYPE, ERR_SHAPE, ERR_NULL, ERR_ALIGN, ERR_DTYPE, ERR_BYTES, ERR_HIP = -1, -2, -3, -4, -5, -6, -7
 VARIANT_AUTO, VARIANT_DECODE, VARIANT_GEMM = 0, 1, 2
 PROLOGUE_NONE, PROLOGUE_RMSNORM, PROLOGUE_SWIGLU = 0, 1, 2
 EPILOGUE_STORE, EPILOGUE_ACCUMULATE, EPILOGUE_SWIGLU = 0, 1, 2
 DECODE_MAX_M = 32
+NOALLOC_ATTENTION_BYTES = 8 << 20
 
 # Every symbol include/gguf_hip.h declares: name -> (restype, argtypes)
 _vp, _i32, _i64, _fp = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64, ctypes.c_void_p
@@ -48,6 +49,8 @@ SIGNATURES = {
     "gguf_hip_attention_decode": (_i32, [_fp, _vp, _fp, _fp, _fp, _fp, _fp, _i32, _i32, _i32,
                                          _i64, _vp, _vp]),
     "gguf_hip_attention_workspace": (_i64, [_i32, _i32, _i32, _i64]),
+    "gguf_hip_attention_decode_noalloc": (_i32, [_fp, _vp, _fp, _fp, _fp, _fp, _fp, _i32, _i32,
+                                                 _i32, _i64, _vp]),
     "gguf_hip_matmul_attn_merge": (_i32, [_vp, _vp, _i32, _i32, _i32, _i64, _vp, _i32, _i64, _fp,
                                           _i32, _vp]),
     "gguf_hip_argmax": (_i32, [_fp, _i64, _vp, _vp, _vp]),

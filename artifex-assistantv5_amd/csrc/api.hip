@@ -320,6 +320,30 @@ int gguf_hip_attention_decode(const float *qkv, const int64_t *pos, const float 
                     "attention launch");
 }
 
+int gguf_hip_attention_decode_noalloc(const float *qkv, const int64_t *pos,
+                                      const float *cos_table, const float *sin_table,
+                                      float *k_cache, float *v_cache, float *out, int n_heads,
+                                      int n_kv_heads, int head_dim, int64_t max_seq,
+                                      void *stream) {
+  int rc = check_attention(n_heads, n_kv_heads, head_dim, max_seq);
+  if (rc) return rc;
+  const int64_t need = gguf::attention_work_bytes(n_heads, n_kv_heads, head_dim, max_seq);
+  if (need > gguf::kNoAllocAttentionBytes)
+    return fail(GGUF_HIP_ERR_SHAPE,
+                "[gguf-hip] attention_decode_noalloc: the shape needs %lld bytes of workspace, "
+                "more than the library's %lld (use gguf_hip_attention_decode with a workspace)",
+                (long long)need, (long long)gguf::kNoAllocAttentionBytes);
+  if (!qkv || !pos || !cos_table || !sin_table || !k_cache || !v_cache || !out)
+    return fail(GGUF_HIP_ERR_NULL, "[gguf-hip] null pointer");
+  if (!aligned(qkv, 16) || !aligned(k_cache, 16) || !aligned(v_cache, 16) || !aligned(out, 4) ||
+      !aligned(pos, 8) || !aligned(cos_table, 4) || !aligned(sin_table, 4))
+    return fail(GGUF_HIP_ERR_ALIGN, "[gguf-hip] attention buffers misaligned");
+  return hip_status(gguf::launch_attention_decode_noalloc(qkv, pos, cos_table, sin_table, k_cache,
+                                                          v_cache, out, n_heads, n_kv_heads,
+                                                          head_dim, max_seq, (hipStream_t)stream),
+                    "attention launch");
+}
+
 int64_t gguf_hip_argmax_workspace(void) { return gguf::argmax_work_bytes(); }
 
 int gguf_hip_argmax(const float *x, int64_t n, int64_t *out, void *work, void *stream) {

@@ -396,6 +396,13 @@ int64_t attention_work_bytes(int nh, int nkv, int hd, int64_t max_seq);
 hipError_t launch_attention_decode(const float *qkv, const int64_t *pos, const float *cs,
                                    const float *sn, float *kc, float *vc, float *out, float *work,
                                    int nh, int nkv, int hd, int64_t max_seq, hipStream_t s);
+// The attention of gguf_hip_attention_decode_noalloc keeps its workspace
+// (records and counters) in a device array of this many bytes.
+constexpr int64_t kNoAllocAttentionBytes = (int64_t)8 << 20;
+hipError_t launch_attention_decode_noalloc(const float *qkv, const int64_t *pos, const float *cs,
+                                           const float *sn, float *kc, float *vc, float *out,
+                                           int nh, int nkv, int hd, int64_t max_seq,
+                                           hipStream_t s);
 int64_t argmax_work_bytes();
 hipError_t launch_argmax(const float *x, int64_t n, int64_t *out, void *work, hipStream_t s);
 

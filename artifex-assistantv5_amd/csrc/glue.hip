@@ -8,6 +8,8 @@
 // All kernels are f32, one row (or one KV head) per workgroup; they are small
 // and latency-bound, so the goal is one launch per op with coalesced 16-byte
 // accesses, not occupancy.
+#include <mutex>
+
 #include "common.hpp"
 
 namespace gguf {
@@ -456,6 +458,60 @@ hipError_t launch_attention_decode(const float *qkv, const int64_t *pos, const f
     hipLaunchKernelGGL(attention_kernel<256>, grid, block, 0, s, qkv, pos, cs, sn, kc, vc, out,
                        work, counters, nh, nkv, (int)max_seq);
   return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// Attention without a caller workspace (gguf_hip_attention_decode_noalloc).
+// The records and counters live in `scratch`, a file-scope device array that
+// every GPU the library runs on holds until the process ends.  Its address is
+// taken once per device with hipGetSymbolAddress (the host-side name is only
+// a stand-in, not a device address) and passed to the kernels.  Calls that
+// overlap on one GPU race on it; each call clears the counters it uses with a
+// fill kernel first (no memset, so the call can be captured in a graph).
+// ---------------------------------------------------------------------------
+namespace {
+
+__device__ __align__(256) unsigned char scratch[kNoAllocAttentionBytes];
+
+std::mutex g_scratch_mu;
+constexpr int kMaxDevices = 64;
+void *g_scratch[kMaxDevices];  // per device: the device address of `scratch`
+
+__global__ __launch_bounds__(kGlueThreads) void clear_u32_kernel(unsigned *__restrict__ p, int n) {
+  for (int i = threadIdx.x; i < n; i += kGlueThreads) p[i] = 0u;
+}
+
+hipError_t scratch_ptr(void **out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  if (dev < 0 || dev >= kMaxDevices) return hipErrorInvalidDevice;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch[dev]) {
+    void *p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return e;
+    g_scratch[dev] = p;
+  }
+  *out = g_scratch[dev];
+  return hipSuccess;
+}
+
+}  // namespace
+
+hipError_t launch_attention_decode_noalloc(const float *qkv, const int64_t *pos, const float *cs,
+                                           const float *sn, float *kc, float *vc, float *out,
+                                           int nh, int nkv, int hd, int64_t max_seq,
+                                           hipStream_t s) {
+  void *ws = nullptr;
+  hipError_t e = scratch_ptr(&ws);
+  if (e != hipSuccess) return e;
+  unsigned *counters = (unsigned *)((char *)ws + attention_record_bytes(nh, nkv, hd, max_seq));
+  hipLaunchKernelGGL(clear_u32_kernel, dim3(1), dim3(kGlueThreads), 0, s, counters, nkv);
+  e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  return launch_attention_decode(qkv, pos, cs, sn, kc, vc, out, (float *)ws, nh, nkv, hd, max_seq,
+                                 s);
 }
 
 int64_t argmax_work_bytes() { return (int64_t)kArgBlocks * (sizeof(float) + sizeof(int64_t)); }

@@ -46,7 +46,7 @@ extern "C" {
  * are exported (kernels and helpers cannot be interposed across libraries). */
 #pragma GCC visibility push(default)
 
-#define GGUF_HIP_ABI_VERSION 11
+#define GGUF_HIP_ABI_VERSION 12
 
 /* ggml type ids (gguf.ts:24-35); activation dtypes reuse F32 / F16. */
 #define GGUF_HIP_F32 0
@@ -223,6 +223,22 @@ int gguf_hip_attention_decode(const float *qkv, const int64_t *pos, const float 
 
 /* Bytes of the gguf_hip_attention_decode workspace; negative on bad shapes. */
 int64_t gguf_hip_attention_workspace(int n_heads, int n_kv_heads, int head_dim, int64_t max_seq);
+
+/* gguf_hip_attention_decode that allocates nothing and takes no workspace.
+ * No counterpart in the reference: it is for callers that cannot allocate
+ * device memory (code under graph capture, serving loops, harnesses that
+ * forbid it).  Same arguments and results as gguf_hip_attention_decode with
+ * out != NULL (out is required).  The records and counters live in a device
+ * array of GGUF_HIP_NOALLOC_ATTENTION_BYTES inside the library, one per GPU,
+ * held until the process ends; shapes whose workspace
+ * (gguf_hip_attention_workspace) exceeds it return GGUF_HIP_ERR_SHAPE.  All
+ * calls on one GPU share that array: calls that overlap on a GPU race. */
+#define GGUF_HIP_NOALLOC_ATTENTION_BYTES 8388608 /* 8 MiB */
+int gguf_hip_attention_decode_noalloc(const float *qkv, const int64_t *pos,
+                                      const float *cos_table, const float *sin_table,
+                                      float *k_cache, float *v_cache, float *out, int n_heads,
+                                      int n_kv_heads, int head_dim, int64_t max_seq,
+                                      void *stream);
 
 /* The attention output projection of one decode position with the attention
  * merge fused in: y (= or +=, epilogue STORE / ACCUMULATE) W . a, where a

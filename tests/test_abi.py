@@ -43,7 +43,7 @@ def native(pkg):
 
 def test_exports_every_declared_symbol(lib, native):
     names = _declared_functions()
-    assert len(names) == 20, names
+    assert len(names) == 21, names
     for n in names:
         assert hasattr(lib, n), n
         assert n in native.SIGNATURES, n
@@ -63,6 +63,7 @@ def test_constants_match_header(native):
     assert d["GGUF_HIP_VARIANT_DECODE"] == native.VARIANT_DECODE
     assert d["GGUF_HIP_VARIANT_GEMM"] == native.VARIANT_GEMM
     assert d["GGUF_HIP_DECODE_MAX_M"] == native.DECODE_MAX_M
+    assert d["GGUF_HIP_NOALLOC_ATTENTION_BYTES"] == native.NOALLOC_ATTENTION_BYTES
     assert (d["GGUF_HIP_Q8_0"], d["GGUF_HIP_Q4_K"], d["GGUF_HIP_Q5_K"],
             d["GGUF_HIP_Q6_K"]) == (8, 12, 13, 14)
     assert (d["GGUF_HIP_Q4_0"], d["GGUF_HIP_Q5_0"], d["GGUF_HIP_IQ4_NL"],
@@ -70,7 +71,7 @@ def test_constants_match_header(native):
 
 
 def test_abi_version(lib):
-    assert lib.gguf_hip_abi_version() == 11
+    assert lib.gguf_hip_abi_version() == 12
 
 
 def test_type_traits(lib, native):
@@ -211,6 +212,15 @@ def test_glue_errors(lib, native):
     assert lib.gguf_hip_attention_workspace(32, 8, 128, 512) == 8 * 8 * 4 * 132 * 4 + 32
     assert lib.gguf_hip_attention_workspace(4, 2, 64, 65) == 2 * 2 * 2 * 68 * 4 + 16
     assert lib.gguf_hip_attention_workspace(32, 8, 100, 512) == native.ERR_SHAPE
+    # the entry point without a workspace: same checks, plus the size of its own array
+    na = lib.gguf_hip_attention_decode_noalloc
+    assert na(a, b, c, c, a, a, b, 32, 5, 128, 512, None) == native.ERR_SHAPE
+    assert na(a, b, c, c, a, a, None, 32, 8, 128, 512, None) == native.ERR_NULL    # out required
+    assert na(a + 4, b, c, c, a, a, b, 32, 8, 128, 512, None) == native.ERR_ALIGN
+    big = lib.gguf_hip_attention_workspace(64, 8, 128, 65536)
+    assert big > native.NOALLOC_ATTENTION_BYTES
+    assert na(a, b, c, c, a, a, b, 64, 8, 128, 65536, None) == native.ERR_SHAPE
+    assert "noalloc" in native.last_error(lib)
     assert lib.gguf_hip_argmax_workspace() > 0
     assert lib.gguf_hip_argmax(a, 0, b, c, None) == native.ERR_SHAPE
     assert lib.gguf_hip_argmax(a, 10, b + 4, c, None) == native.ERR_ALIGN
