@@ -17,7 +17,7 @@ from .ggml import GGMLTypeError
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libgguf_hip.so")
-ABI_VERSION = 12
+ABI_VERSION = 13
 
 ERR_TYPE, ERR_SHAPE, ERR_NULL, ERR_ALIGN, ERR_DTYPE, ERR_BYTES, ERR_HIP = -1, -2, -3, -4, -5, -6, -7
 VARIANT_AUTO, VARIANT_DECODE, VARIANT_GEMM = 0, 1, 2
@@ -41,6 +41,9 @@ SIGNATURES = {
     "gguf_hip_matmul": (_i32, [_vp, _i32, _i64, _vp, _i32, _i64, _i64, _fp, _i64, _i64, _vp]),
     "gguf_hip_matmul_variant": (_i32, [_vp, _i32, _i64, _vp, _i32, _i64, _i64, _fp, _i64, _i64,
                                        _i32, _vp]),
+    "gguf_hip_matmul_ws": (_i32, [_vp, _i32, _i64, _vp, _i32, _i64, _i64, _fp, _i64, _i64, _i32,
+                                  _vp, _i64, _vp]),
+    "gguf_hip_matmul_workspace": (_i64, [_i32, _i32, _i64, _i64, _i64]),
     "gguf_hip_matmul_fused": (_i32, [_fp, _vp, _i32, _i64, _i64, _fp, _i32, _fp, ctypes.c_float,
                                      _i32, _vp]),
     "gguf_hip_rmsnorm": (_i32, [_fp, _fp, ctypes.c_float, _fp, _i64, _i64, _vp]),

@@ -203,9 +203,9 @@ int gguf_hip_get_rows(const void *raw, int ggml_type, int64_t n_rows, int64_t k,
                     "get_rows launch");
 }
 
-int gguf_hip_matmul_variant(const void *x, int x_type, int64_t ldx, const void *tiles,
-                            int ggml_type, int64_t n, int64_t k, float *y, int64_t ldy, int64_t m,
-                            int variant, void *stream) {
+int gguf_hip_matmul_ws(const void *x, int x_type, int64_t ldx, const void *tiles, int ggml_type,
+                       int64_t n, int64_t k, float *y, int64_t ldy, int64_t m, int variant,
+                       void *work, int64_t work_bytes, void *stream) {
   int rc = check_type(ggml_type);
   if (rc) return rc;
   if ((rc = check_k(ggml_type, k))) return rc;
@@ -227,6 +227,9 @@ int gguf_hip_matmul_variant(const void *x, int x_type, int64_t ldx, const void *
   if (!aligned(x, 16) || (m > 1 && (ldx * esize) % 16 != 0))
     return fail(GGUF_HIP_ERR_ALIGN, "[gguf-hip] activation rows must be 16-byte aligned");
   if (!aligned(y, 4)) return fail(GGUF_HIP_ERR_ALIGN, "[gguf-hip] output must be 4-byte aligned");
+  if (work_bytes < 0) return fail(GGUF_HIP_ERR_SHAPE, "[gguf-hip] negative workspace size");
+  if (work && !aligned(work, 16))
+    return fail(GGUF_HIP_ERR_ALIGN, "[gguf-hip] workspace must be 16-byte aligned");
 
   const hipStream_t s = (hipStream_t)stream;
   // f16 activations: the decode path up to 32 rows, the fp16 GEMM above; f32
@@ -242,9 +245,31 @@ int gguf_hip_matmul_variant(const void *x, int x_type, int64_t ldx, const void *
     return fail(GGUF_HIP_ERR_SHAPE, "[gguf-hip] ldx too large for the GEMM kernel");
   const hipError_t e =
       variant == GGUF_HIP_VARIANT_DECODE
-          ? gguf::launch_decode(x, x_type, ldx, (const uint8_t *)tiles, ggml_type, n, k, y, ldy, m, s)
+          ? gguf::launch_decode(x, x_type, ldx, (const uint8_t *)tiles, ggml_type, n, k, y, ldy, m,
+                                (float *)work, work ? work_bytes / 4 : 0, s)
           : gguf::launch_gemm(x, x_type, ldx, (const uint8_t *)tiles, ggml_type, n, k, y, ldy, m, s);
   return hip_status(e, "matmul launch");
+}
+
+int gguf_hip_matmul_variant(const void *x, int x_type, int64_t ldx, const void *tiles,
+                            int ggml_type, int64_t n, int64_t k, float *y, int64_t ldy, int64_t m,
+                            int variant, void *stream) {
+  return gguf_hip_matmul_ws(x, x_type, ldx, tiles, ggml_type, n, k, y, ldy, m, variant, nullptr, 0,
+                            stream);
+}
+
+int64_t gguf_hip_matmul_workspace(int ggml_type, int x_type, int64_t n, int64_t k, int64_t m) {
+  int rc = check_type(ggml_type);
+  if (rc) return rc;
+  if ((rc = check_k(ggml_type, k))) return rc;
+  if (x_type != GGUF_HIP_F32 && x_type != GGUF_HIP_F16)
+    return fail(GGUF_HIP_ERR_DTYPE, "[gguf-hip] activations must be f32 (0) or f16 (1), got %d",
+                x_type);
+  if (m < 0 || n < 0 || n > ((int64_t)1 << 30) || m > ((int64_t)1 << 30))
+    return fail(GGUF_HIP_ERR_SHAPE, "[gguf-hip] bad M or N");
+  ok();
+  if (m < 2 || n == 0) return 0;
+  return 4 * gguf::launch_decode_work(ggml_type, x_type, n, k, m);
 }
 
 int gguf_hip_rmsnorm(const float *x, const float *w, float eps, float *y, int64_t rows,

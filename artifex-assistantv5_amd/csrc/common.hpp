@@ -381,7 +381,10 @@ hipError_t launch_get_rows(const uint8_t *raw, int type, int64_t n_rows, int64_t
                            const int64_t *ids, int64_t n_ids, float *out, int64_t ldo,
                            hipStream_t s);
 hipError_t launch_decode(const void *x, int x_type, int64_t ldx, const uint8_t *tiles, int type,
-                         int64_t n, int64_t k, float *y, int64_t ldy, int64_t m, hipStream_t s);
+                         int64_t n, int64_t k, float *y, int64_t ldy, int64_t m, float *work,
+                         int64_t work_floats, hipStream_t s);
+// Workspace floats launch_decode uses for these shapes (0: it needs none).
+int64_t launch_decode_work(int type, int x_type, int64_t n, int64_t k, int64_t m);
 hipError_t launch_gemm(const void *x, int x_type, int64_t ldx, const uint8_t *tiles, int type,
                        int64_t n, int64_t k, float *y, int64_t ldy, int64_t m, hipStream_t s);
 hipError_t launch_decode_fused(const float *x, const uint8_t *tiles, int type, int64_t n,

@@ -43,9 +43,37 @@ hipError_t launch_decode_attn_merge(const AttnRecords &ar, const uint8_t *tiles,
   }
 }
 
+// Workspace floats of one pass of mc <= 32 rows.
+static int64_t pass_work(int type, int x_type, int n, int k, int mc) {
+  switch (type) {
+    case 2: return decode_work_q4_0(x_type, n, k, mc);
+    case 6: return decode_work_q5_0(x_type, n, k, mc);
+    case 8: return decode_work_q8_0(x_type, n, k, mc);
+    case 10: return decode_work_q2_k(x_type, n, k, mc);
+    case 11: return decode_work_q3_k(x_type, n, k, mc);
+    case 12: return decode_work_q4_k(x_type, n, k, mc);
+    case 13: return decode_work_q5_k(x_type, n, k, mc);
+    case 14: return decode_work_q6_k(x_type, n, k, mc);
+    case 20: return decode_work_iq4_nl(x_type, n, k, mc);
+    case 23: return decode_work_iq4_xs(x_type, n, k, mc);
+    default: return 0;
+  }
+}
+
+int64_t launch_decode_work(int type, int x_type, int64_t n, int64_t k, int64_t m) {
+  int64_t w = 0;
+  if (m >= 32) w = pass_work(type, x_type, (int)n, (int)k, 32);
+  if (m % 32) {
+    const int64_t v = pass_work(type, x_type, (int)n, (int)k, (int)(m % 32));
+    w = v > w ? v : w;
+  }
+  return w;
+}
+
 // Rows are processed in groups of at most 32 (one pass over the weights each).
 hipError_t launch_decode(const void *x, int x_type, int64_t ldx, const uint8_t *tiles, int type,
-                         int64_t n, int64_t k, float *y, int64_t ldy, int64_t m, hipStream_t s) {
+                         int64_t n, int64_t k, float *y, int64_t ldy, int64_t m, float *work,
+                         int64_t work_floats, hipStream_t s) {
   const int esize = x_type == 0 ? 4 : 2;
   hipError_t e = hipSuccess;
   for (int64_t m0 = 0; m0 < m && e == hipSuccess; m0 += 32) {
@@ -53,16 +81,16 @@ hipError_t launch_decode(const void *x, int x_type, int64_t ldx, const uint8_t *
     const char *xb = (const char *)x + m0 * ldx * esize;
     float *yb = y + m0 * ldy;
     switch (type) {
-      case 2: e = decode_q4_0(xb, x_type, ldx, tiles, (int)n, (int)k, yb, ldy, mc, s); break;
-      case 6: e = decode_q5_0(xb, x_type, ldx, tiles, (int)n, (int)k, yb, ldy, mc, s); break;
-      case 8: e = decode_q8_0(xb, x_type, ldx, tiles, (int)n, (int)k, yb, ldy, mc, s); break;
-      case 10: e = decode_q2_k(xb, x_type, ldx, tiles, (int)n, (int)k, yb, ldy, mc, s); break;
-      case 11: e = decode_q3_k(xb, x_type, ldx, tiles, (int)n, (int)k, yb, ldy, mc, s); break;
-      case 12: e = decode_q4_k(xb, x_type, ldx, tiles, (int)n, (int)k, yb, ldy, mc, s); break;
-      case 13: e = decode_q5_k(xb, x_type, ldx, tiles, (int)n, (int)k, yb, ldy, mc, s); break;
-      case 14: e = decode_q6_k(xb, x_type, ldx, tiles, (int)n, (int)k, yb, ldy, mc, s); break;
-      case 20: e = decode_iq4_nl(xb, x_type, ldx, tiles, (int)n, (int)k, yb, ldy, mc, s); break;
-      case 23: e = decode_iq4_xs(xb, x_type, ldx, tiles, (int)n, (int)k, yb, ldy, mc, s); break;
+      case 2: e = decode_q4_0(xb, x_type, ldx, tiles, (int)n, (int)k, yb, ldy, mc, work, work_floats, s); break;
+      case 6: e = decode_q5_0(xb, x_type, ldx, tiles, (int)n, (int)k, yb, ldy, mc, work, work_floats, s); break;
+      case 8: e = decode_q8_0(xb, x_type, ldx, tiles, (int)n, (int)k, yb, ldy, mc, work, work_floats, s); break;
+      case 10: e = decode_q2_k(xb, x_type, ldx, tiles, (int)n, (int)k, yb, ldy, mc, work, work_floats, s); break;
+      case 11: e = decode_q3_k(xb, x_type, ldx, tiles, (int)n, (int)k, yb, ldy, mc, work, work_floats, s); break;
+      case 12: e = decode_q4_k(xb, x_type, ldx, tiles, (int)n, (int)k, yb, ldy, mc, work, work_floats, s); break;
+      case 13: e = decode_q5_k(xb, x_type, ldx, tiles, (int)n, (int)k, yb, ldy, mc, work, work_floats, s); break;
+      case 14: e = decode_q6_k(xb, x_type, ldx, tiles, (int)n, (int)k, yb, ldy, mc, work, work_floats, s); break;
+      case 20: e = decode_iq4_nl(xb, x_type, ldx, tiles, (int)n, (int)k, yb, ldy, mc, work, work_floats, s); break;
+      case 23: e = decode_iq4_xs(xb, x_type, ldx, tiles, (int)n, (int)k, yb, ldy, mc, work, work_floats, s); break;
       default: e = hipErrorNotSupported;
     }
   }

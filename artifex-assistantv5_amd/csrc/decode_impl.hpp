@@ -407,17 +407,23 @@ __device__ __forceinline__ float4_t mfma16(int ah, int al, int zero, half4_t b, 
 
 // acc[i] += f[i] (s D[i] - o xs[i]) for the MR activation rows a lane holds
 // (f: the rows' inverse unit scales 2^-e).
+// The batched kernels keep two row tiles per wave (two inlined copies of the
+// unit arithmetic): every accumulation is an explicit fmaf with contraction
+// off, so that a row's rounding never depends on which copy computed it (the
+// compiler may otherwise fuse the products of a * b + c * d differently in
+// the two copies, and rows would differ in the last bit by tile position).
 template <int MR>
 __device__ __forceinline__ void apply(float (&acc)[4], const float4_t &D, float s, float o, int xs,
                                       const float (&f)[4]) {
+#pragma clang fp contract(off)
   if (MR == 1) {
-    acc[0] += f[0] * (s * D[0] - o * lds_f(xs));
+    acc[0] = fmaf(f[0], fmaf(s, D[0], -(o * lds_f(xs))), acc[0]);
   } else {
     const float4 v = lds_f4(xs);
-    acc[0] += f[0] * (s * D[0] - o * v.x);
-    acc[1] += f[1] * (s * D[1] - o * v.y);
-    acc[2] += f[2] * (s * D[2] - o * v.z);
-    acc[3] += f[3] * (s * D[3] - o * v.w);
+    acc[0] = fmaf(f[0], fmaf(s, D[0], -(o * v.x)), acc[0]);
+    acc[1] = fmaf(f[1], fmaf(s, D[1], -(o * v.y)), acc[1]);
+    acc[2] = fmaf(f[2], fmaf(s, D[2], -(o * v.z)), acc[2]);
+    acc[3] = fmaf(f[3], fmaf(s, D[3], -(o * v.w)), acc[3]);
   }
 }
 
@@ -425,8 +431,9 @@ __device__ __forceinline__ void apply(float (&acc)[4], const float4_t &D, float 
 template <int MR>
 __device__ __forceinline__ void apply_s(float (&acc)[4], const float4_t &D, float s,
                                         const float (&f)[4]) {
+#pragma clang fp contract(off)
 #pragma unroll
-  for (int i = 0; i < MR; ++i) acc[i] += f[i] * (s * D[i]);
+  for (int i = 0; i < MR; ++i) acc[i] = fmaf(f[i], s * D[i], acc[i]);
 }
 
 // The inverse unit scales of unit ul for the MR rows of each activation tile a lane holds.
@@ -754,6 +761,7 @@ __device__ __forceinline__ void unit_m1(const Unit<23> &u, const Stage &st, int 
 template <int PARTS, int MT, int MR, int TYPE>
 __device__ __forceinline__ void unit_compute_k(const Unit<TYPE> &u, const Stage &st, int ul,
                                                int lane, int M, float (&acc)[MT][4]) {
+#pragma clang fp contract(off)
   const int r = lane & 15, g = lane >> 4;
   uint32_t sc_lo, sc_hi, m_lo, m_hi;
   q4k_scales_packed(u.h.y, u.h.z, u.h.w, sc_lo, sc_hi, m_lo, m_hi);
@@ -779,17 +787,17 @@ __device__ __forceinline__ void unit_compute_k(const Unit<TYPE> &u, const Stage 
       const float4_t D1 = mfma32<PARTS>(st.xh + off + 32, st.xl + off + 32, st.zero, bhi, on);
       const int xs = st.xs + (ul * 8 + 2 * c) * st.ms + 16 * mt + 4 * g;
       if (MR == 1) {
-        se[mt][0] += sc0 * D0[0];
-        so[mt][0] += sc1 * D1[0];
-        sm[mt][0] += m0 * lds_f(xs) + m1 * lds_f(xs + st.ms);
+        se[mt][0] = fmaf(sc0, D0[0], se[mt][0]);
+        so[mt][0] = fmaf(sc1, D1[0], so[mt][0]);
+        sm[mt][0] = fmaf(m0, lds_f(xs), fmaf(m1, lds_f(xs + st.ms), sm[mt][0]));
       } else {
         const float4 x0 = lds_f4(xs), x1 = lds_f4(xs + st.ms);
         const float xv0[4] = {x0.x, x0.y, x0.z, x0.w}, xv1[4] = {x1.x, x1.y, x1.z, x1.w};
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          se[mt][i] += sc0 * D0[i];
-          so[mt][i] += sc1 * D1[i];
-          sm[mt][i] += m0 * xv0[i] + m1 * xv1[i];
+          se[mt][i] = fmaf(sc0, D0[i], se[mt][i]);
+          so[mt][i] = fmaf(sc1, D1[i], so[mt][i]);
+          sm[mt][i] = fmaf(m0, xv0[i], fmaf(m1, xv1[i], sm[mt][i]));
         }
       }
     }
@@ -802,7 +810,8 @@ __device__ __forceinline__ void unit_compute_k(const Unit<TYPE> &u, const Stage 
   for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
     for (int i = 0; i < MR; ++i)
-      acc[mt][i] += f[mt][i] * (d24 * se[mt][i] + d20 * so[mt][i] - dmin * sm[mt][i]);
+      acc[mt][i] = fmaf(f[mt][i], fmaf(d24, se[mt][i], fmaf(d20, so[mt][i], -(dmin * sm[mt][i]))),
+                        acc[mt][i]);
 }
 template <int PARTS, int MT, int MR>
 __device__ __forceinline__ void unit_compute(const Unit<12> &u, const Stage &st, int ul, int lane,
@@ -982,18 +991,10 @@ __device__ __forceinline__ void unit_compute(const Unit<23> &u, const Stage &st,
   }
 }
 
-// Stage activations x[0:M, k0 : k0 + ce) into LDS (zeros past K).
-// Activation staging.  A chunk of M x ce activations is converted in items of
-// 16 consecutive elements, one item per thread and step.  When a chunk has at
-// most 256 items its loads are issued one chunk ahead into registers (XPre) --
-// before the weight loads they would otherwise queue behind, since the
-// vector-memory counter retires loads in issue order.
+// Activation staging.  Activations are converted in items of 16 consecutive
+// elements of one row, one item per thread and step.
 constexpr int kItem = 16;
 constexpr int kMergeChunk = 8;  // attention records per item held in registers (merge prologue)
-
-struct XPre {
-  float v[kItem];
-};
 
 template <typename XT>
 __device__ __forceinline__ void load_item(const XT *__restrict__ x, int64_t ldx, int K, int k0,
@@ -1069,53 +1070,62 @@ __device__ __forceinline__ void store_item(int per_row, int total, int q, const 
   }
 }
 
-template <typename XT>
-__device__ __forceinline__ void prefetch_x(const XT *__restrict__ x, int64_t ldx, int M, int K,
-                                           int k0, int ce, XPre &p) {
-  const int per_row = ce / kItem;
-  load_item<XT>(x, ldx, K, k0, per_row, M * per_row, (int)threadIdx.x, p.v);
+// ---------------------------------------------------------------------------
+// Batched decode: 2 <= M <= 32 activation rows in one pass over the weights
+// (and M = 1 beyond the one-shot kernel's K).
+//
+// The reference re-reads the weights once per activation row
+// (forward-pass.ts:1536-1539).  Here a workgroup of 8 waves owns 4 row tiles
+// (two pairs) and one or more K slices of `us` units.  A slice's activations
+// (M rows: scaled hi / lo parts, group sums, unit scales) are staged in LDS at
+// once; wave (pair p, lane kl) takes tile pair p and every 4th unit of the
+// slice, so every A fragment read from LDS feeds the MFMAs of two row tiles.
+// The 4 waves of a pair add their partial sums in a fixed order.
+//
+// Split K.  With a workspace the slices are spread over the grid (grid.y =
+// number of slices): a workgroup stages one slice and writes its partial sums
+// to the workspace, and mb_reduce_kernel adds the slices in a fixed order.
+// For a small N (the FFN down projection: 256 row tiles for 256 CUs) this is
+// what keeps the per-CU activation staging small: without it every CU would
+// convert and stage all M x K activations for its one tile.  Without a
+// workspace each workgroup walks all slices (spw of them) itself.  Either way
+// the sums are deterministic.
+// ---------------------------------------------------------------------------
+#ifndef GGUF_MB_MIN_WGS
+#define GGUF_MB_MIN_WGS 512  // split K further while the grid has fewer workgroups
+#endif
+#ifndef GGUF_MB_DEPTH_K
+#define GGUF_MB_DEPTH_K 2    // units in flight per tile per wave, 256-element units
+#endif
+#ifndef GGUF_MB_DEPTH_K2
+#define GGUF_MB_DEPTH_K2 2   // the same, two 16-row activation tiles
+#endif
+#ifndef GGUF_MB_DEPTH_B
+#define GGUF_MB_DEPTH_B 4    // the same, 32-element blocks
+#endif
+constexpr int kMbThreads = 512;
+constexpr int kMbTiles = 4;  // row tiles per workgroup
+template <int TYPE, int MT>
+constexpr int mb_depth() {  // units in flight per tile per wave
+  return (TYPE == 8 || is_b32(TYPE)) ? GGUF_MB_DEPTH_B : (MT == 2 ? GGUF_MB_DEPTH_K2 : GGUF_MB_DEPTH_K);
 }
 
-// Stage chunk [k0, k0 + ce): from the prefetched registers when the chunk fits
-// them (at most 256 items), else with synchronous loads.
-template <typename XT, int PARTS, int GS, int UE, bool SUMS, bool NAT>
-__device__ __forceinline__ void stage_x(const XT *__restrict__ x, int64_t ldx, int M, int K,
-                                        int k0, int ce, const Stage &st, const XPre &p) {
-  const int per_row = ce / kItem, total = M * per_row;
-  if (total <= 256) {
-    store_item<PARTS, GS, UE, SUMS, NAT>(per_row, total, (int)threadIdx.x, p.v, st);
-    return;
-  }
-  for (int q0 = 0; q0 < total; q0 += 256) {
-    float v[kItem];
-    load_item<XT>(x, ldx, K, k0, per_row, total, q0 + (int)threadIdx.x, v);
-    store_item<PARTS, GS, UE, SUMS, NAT>(per_row, total, q0 + (int)threadIdx.x, v, st);
-  }
-}
-
-template <int TYPE, typename XT, int MT, int MR>
-__global__ __launch_bounds__(256) void decode_kernel(const XT *__restrict__ x, int64_t ldx,
-                                                     const uint8_t *__restrict__ W, int N, int K,
-                                                     float *__restrict__ y, int64_t ldy, int M,
-                                                     int ks_n, int uc) {
+template <int TYPE, typename XT, int MT>
+__global__ __launch_bounds__(kMbThreads) void mb_kernel(const XT *__restrict__ x, int64_t ldx,
+                                                        const uint8_t *__restrict__ W, int N,
+                                                        int K, int M, int us, int spw,
+                                                        float *__restrict__ out, int64_t ldo) {
   constexpr int PARTS = sizeof(XT) == 4 ? 2 : 1;
   constexpr int UE = Fmt<TYPE>::UE, TU = Fmt<TYPE>::TU, GS = Dec<TYPE>::GS;
-  constexpr int P = decode_p<TYPE, MT, MR>();
-  // the wave index is uniform across a wave; say so, so that the tile, the
-  // unit offsets and the buffer resource live in scalar registers
+  constexpr int P = mb_depth<TYPE, MT>();
   const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int r = lane & 15, g = lane >> 4;
-  const int ts_n = 4 / ks_n;
-  const int ts = wave / ks_n, ks = wave - ts * ks_n;
-  const int ntiles = (N + 15) >> 4;
-  const int tile = blockIdx.x * ts_n + ts;
-  const bool active = tile < ntiles;
-  const int nu = K / UE;
-  const int cu = ks_n * uc;                    // units per staged chunk
-  const int ce = cu * UE;                      // elements per staged chunk
-  const int iters = (nu + ks_n - 1) / ks_n;    // loop trips, equal for every wave
+  const int pr = wave & 1, kl = wave >> 1;
+  const int ntiles = (N + 15) >> 4, nu = K / UE;
+  const int nsl = (nu + us - 1) / us;
+  const int tt = kMbTiles * blockIdx.x + 2 * pr;  // the wave's first tile
+  const int ce = us * UE;
 
-  // LDS: [hi][lo][group sums][reduction][zero]; hi/lo row blocks are multiples of 16 bytes
   Stage st;
   st.ld = ce + kXPad;
   st.ms = 16 * MT;
@@ -1123,133 +1133,176 @@ __global__ __launch_bounds__(256) void decode_kernel(const XT *__restrict__ x, i
   st.xl = M * st.ld;
   st.xs = (st.xl + (PARTS == 2 ? M * st.ld : 0)) / 2;
   st.xf = st.xs + (ce / GS) * st.ms;
-  const int red_off = st.xf + (ce / UE) * st.ms;   // floats: [4 waves][MT * 4][64]
-  st.zero = 2 * (red_off + 4 * MT * 4 * 64);
-  float *red = (float *)g_lds + red_off;
-
-  // rows M..ms-1 of the group sums / unit scales and the zero operand stay zero throughout
-  for (int i = threadIdx.x; i < (ce / GS + ce / UE) * st.ms; i += 256) ((float *)g_lds)[st.xs + i] = 0.f;
+  st.zero = 2 * (st.xf + (ce / UE) * st.ms);
+  // rows M..ms-1 of the group sums / unit scales and the zero operand stay zero
+  // throughout (only those rows: the staging below writes rows < M without a
+  // barrier in between)
+  for (int i = threadIdx.x; i < (ce / GS + ce / UE) * st.ms; i += kMbThreads)
+    if (i % st.ms >= M) ((float *)g_lds)[st.xs + i] = 0.f;
   if (threadIdx.x < kZeroHalves / 2) ((uint32_t *)((half_t *)g_lds + st.zero))[threadIdx.x] = 0u;
 
-  const __amdgpu_buffer_rsrc_t wrs = __builtin_amdgcn_make_buffer_rsrc(
-      (void *)(W + (int64_t)(active ? tile : 0) * nu * TU), 0, active ? nu * TU : 0, kRsrcWord3);
-  float acc[MT][4];
+  // one buffer resource per tile; a tile past the weight's end has no records (loads read 0)
+  const int tb = nu * TU;
+  const __amdgpu_buffer_rsrc_t rs0 = __builtin_amdgcn_make_buffer_rsrc(
+      (void *)(W + (int64_t)min(tt, ntiles - 1) * tb), 0, tt < ntiles ? tb : 0, kRsrcWord3);
+  const __amdgpu_buffer_rsrc_t rs1 = __builtin_amdgcn_make_buffer_rsrc(
+      (void *)(W + (int64_t)min(tt + 1, ntiles - 1) * tb), 0, tt + 1 < ntiles ? tb : 0,
+      kRsrcWord3);
+  float acc[2][MT][4];
 #pragma unroll
-  for (int mt = 0; mt < MT; ++mt)
+  for (int t = 0; t < 2; ++t)
 #pragma unroll
-    for (int i = 0; i < 4; ++i) acc[mt][i] = 0.f;
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) acc[t][mt][i] = 0.f;
 
-  // Trip i handles unit ks + ks_n * i; P units are in flight at any time.
-  // The first chunk's activations are requested ahead of the weights.
-  XPre xpre;
-  const bool xreg = M * (ce / kItem) <= 256;
-  if (xreg) prefetch_x<XT>(x, ldx, M, K, 0, ce, xpre);
-  Unit<TYPE> buf[P];
+  const int sl0 = blockIdx.y * spw, sl1 = min(sl0 + spw, nsl);
+  for (int sl = sl0; sl < sl1; ++sl) {  // uniform over the workgroup
+    const int u0 = sl * us, nus = min(us, nu - u0);
+    const int cnt = (nus - kl + 3) >> 2;  // the wave's units: u0 + kl + 4 j, j < cnt
+    // weights first (the staging below overlaps their latency)
+    Unit<TYPE> b0[P], b1[P];
 #pragma unroll
-  for (int j = 0; j < P; ++j) {
-    const int u = ks + ks_n * j;
-    if (j < iters && u < nu) load_unit(wrs, u * TU, r, g, buf[j]);
-  }
-  // uc is a multiple of P, so a chunk starts on buffer slot 0 and the staging
-  // code sits outside the unrolled body.
-  const int nch = (iters + uc - 1) / uc;
-  for (int c = 0; c < nch; ++c) {  // uniform over the workgroup
-    __syncthreads();  // the previous chunk is fully consumed
-    stage_x<XT, PARTS, GS, UE, Dec<TYPE>::SUMS, Dec<TYPE>::NAT>(x, ldx, M, K, c * ce, ce, st, xpre);
+    for (int j = 0; j < P; ++j)
+      if (j < cnt) {
+        const int soff = (u0 + kl + 4 * j) * TU;
+        load_unit(rs0, soff, r, g, b0[j]);
+        load_unit(rs1, soff, r, g, b1[j]);
+      }
+    if (sl > sl0) __syncthreads();  // the previous slice is consumed
+    const int per_row = ce / kItem, total = M * per_row;
+    for (int q0 = 0; q0 < total; q0 += kMbThreads) {
+      float v[kItem];
+      load_item<XT>(x, ldx, K, u0 * UE, per_row, total, q0 + (int)threadIdx.x, v);
+      store_item<PARTS, GS, UE, Dec<TYPE>::SUMS, Dec<TYPE>::NAT>(per_row, total,
+                                                                 q0 + (int)threadIdx.x, v, st);
+    }
     __syncthreads();
-    if (xreg && c + 1 < nch) prefetch_x<XT>(x, ldx, M, K, (c + 1) * ce, ce, xpre);
-    const int iend = min((c + 1) * uc, iters);
-    for (int i0 = c * uc; i0 < iend; i0 += P) {
+    for (int j0 = 0; j0 < cnt; j0 += P) {
 #pragma unroll
-      for (int j = 0; j < P; ++j) {
-        const int i = i0 + j;
-        if (i < iend) {
-          const int u = ks + ks_n * i;
-          if (active && u < nu) {
-            if constexpr (MT == 1 && MR == 1)
-              unit_m1<PARTS>(buf[j], st, ks + ks_n * (i - c * uc), lane, acc[0][0]);
-            else
-              unit_compute<PARTS, MT, MR>(buf[j], st, ks + ks_n * (i - c * uc), lane, M, acc);
+      for (int jj = 0; jj < P; ++jj) {
+        const int j = j0 + jj;
+        if (j < cnt) {
+          const int ul = kl + 4 * j;  // unit within the slice
+          unit_compute<PARTS, MT, 4>(b0[jj], st, ul, lane, M, acc[0]);
+          unit_compute<PARTS, MT, 4>(b1[jj], st, ul, lane, M, acc[1]);
+          if (j + P < cnt) {
+            const int soff = (u0 + kl + 4 * (j + P)) * TU;
+            load_unit(rs0, soff, r, g, b0[jj]);
+            load_unit(rs1, soff, r, g, b1[jj]);
           }
-          const int un = u + ks_n * P;
-          if (i + P < iters && un < nu) load_unit(wrs, un * TU, r, g, buf[j]);
         }
       }
     }
   }
 
-  if constexpr (MT == 1 && MR == 1) acc[0][0] = sum_xor32(sum_xor16(acc[0][0]));  // the four lane groups of each row
-
-  // fixed-order reduction of the ks_n partial sums of each tile
-  const int n = 16 * tile + r;
-  if (ks_n > 1) {
-    __syncthreads();
+  // fixed-order sum of the 4 waves of each pair (kl = 0, 1, 2, 3), through LDS
+  __syncthreads();  // the staged activations are consumed
+  float *red = (float *)g_lds;  // [8 waves][2][MT][4][64]
+#pragma unroll
+  for (int t = 0; t < 2; ++t)
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-      for (int i = 0; i < MR; ++i) red[(wave * MT * 4 + mt * 4 + i) * 64 + lane] = acc[mt][i];
-    __syncthreads();
-    if (ks != 0) return;
+      for (int i = 0; i < 4; ++i) red[(((wave * 2 + t) * MT + mt) * 4 + i) * 64 + lane] = acc[t][mt][i];
+  __syncthreads();
+  if (kl != 0) return;
+  float *o = out + (int64_t)blockIdx.y * (gridDim.y > 1 ? (int64_t)M * N : 0);
+#pragma unroll
+  for (int t = 0; t < 2; ++t) {
+    const int n = 16 * (tt + t) + r;
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-      for (int i = 0; i < MR; ++i) {
-        float s = acc[mt][i];
-        for (int j = 1; j < ks_n; ++j) s += red[((wave + j) * MT * 4 + mt * 4 + i) * 64 + lane];
-        acc[mt][i] = s;
+      for (int i = 0; i < 4; ++i) {
+        float v = acc[t][mt][i];
+#pragma unroll
+        for (int w2 = 1; w2 < 4; ++w2) v += red[((((pr + 2 * w2) * 2 + t) * MT + mt) * 4 + i) * 64 + lane];
+        const int m = 16 * mt + 4 * g + i;
+        if (m < M && n < N) o[(int64_t)m * ldo + n] = v;
       }
   }
-  if (!active || n >= N) return;
-#pragma unroll
-  for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-    for (int i = 0; i < MR; ++i) {
-      const int m = 16 * mt + 4 * g + i;
-      if (m < M) y[(int64_t)m * ldy + n] = acc[mt][i];
-    }
 }
 
-#ifndef GGUF_DECODE_WAVES
-#define GGUF_DECODE_WAVES 2048  // target resident waves: 2 per SIMD on 256 CUs
-#endif
+// y[m, n] = sum over the S slices of part[s][m][n], in slice order.
+__global__ __launch_bounds__(256) void mb_reduce_kernel(const float *__restrict__ part, int S, int M,
+                                                        int N, float *__restrict__ y, int64_t ldy) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x, mn = (int64_t)M * N;
+  if (i >= mn) return;
+  float v = part[i];
+  for (int s = 1; s < S; ++s) v += part[(int64_t)s * mn + i];
+  y[(i / N) * ldy + i % N] = v;
+}
 
-template <int TYPE, typename XT, int MT, int MR>
-hipError_t launch_t(const XT *x, int64_t ldx, const uint8_t *W, int N, int K, float *y,
-                    int64_t ldy, int M, hipStream_t s) {
+// Staged slice width: the units whose staged activations (hi / lo parts of M
+// rows, group sums and unit scales of the MT * 16 padded rows) fit in
+// kMbStageBytes of LDS next to the row padding and the zero operand.
+constexpr size_t kMbStageBytes = 150 * 1024;
+template <int TYPE, typename XT>
+int mb_units_per_slice(int M, int K) {
+  constexpr int UE = Fmt<TYPE>::UE, GS = Dec<TYPE>::GS, PARTS = sizeof(XT) == 4 ? 2 : 1;
+  const int MT = M <= 16 ? 1 : 2;
+  const size_t per_unit = (size_t)M * UE * 2 * PARTS + (size_t)(UE / GS + 1) * 16 * MT * 4;
+  const size_t fixed = (size_t)M * kXPad * 2 * PARTS + kZeroHalves * 2;
+  int us = (int)((kMbStageBytes - fixed) / per_unit);
+  us = us < 1 ? 1 : us;
+  const int nu = K / UE;
+  return us < nu ? us : nu;
+}
+// Slices and workspace: at least ~2 workgroups per CU, split K further while
+// the grid is smaller; the workspace holds the slices' partial sums.
+template <int TYPE, typename XT>
+void mb_plan(int M, int N, int K, int *us, int *nsl) {
+  constexpr int UE = Fmt<TYPE>::UE;
+  const int nu = K / UE, groups = ((N + 15) / 16 + kMbTiles - 1) / kMbTiles;
+  int u = mb_units_per_slice<TYPE, XT>(M, K);
+  while (u > 1 && (int64_t)groups * ((nu + u - 1) / u) < GGUF_MB_MIN_WGS) u = (u + 1) / 2;
+  *us = u;
+  *nsl = (nu + u - 1) / u;
+}
+
+template <int TYPE, typename XT, int MT>
+hipError_t launch_mb(const XT *x, int64_t ldx, const uint8_t *W, int N, int K, float *y,
+                     int64_t ldy, int M, float *work, int64_t work_floats, hipStream_t s) {
   constexpr int PARTS = sizeof(XT) == 4 ? 2 : 1;
   constexpr int UE = Fmt<TYPE>::UE, GS = Dec<TYPE>::GS;
-  const int ntiles = (N + 15) / 16;
-  const int nu = K / UE;
-  constexpr int P = decode_p<TYPE, MT, MR>();
-  // K split: enough waves to fill the chip once, at least two units per wave
-  int ks = 1;
-  while (ks < 4 && ntiles * ks * 2 <= GGUF_DECODE_WAVES && nu >= 4 * ks) ks <<= 1;
-  // Units per wave per staged chunk: a multiple of P (the unrolled body never
-  // crosses a chunk), staging under 48 KB, and for small M at most 256 items
-  // of 16 activations so that a chunk can be prefetched into registers.
-  const int per_unit = M * UE * 2 * PARTS;
-  auto up = [](int v) { return (v + P - 1) / P * P; };
-  int uc;
-  for (;;) {
-    uc = up((nu + ks - 1) / ks);
-    while (uc > P && ks * uc * per_unit > 48 * 1024) uc = up((uc + 1) / 2);
-    if (M * ks * P * UE <= kItem * 256)
-      while (uc > P && M * ks * uc * UE > kItem * 256) uc = up((uc + 1) / 2);
-    if (ks > 1 && ks * uc * per_unit > 48 * 1024) {
-      ks >>= 1;
-      continue;
-    }
-    break;
+  int us, nsl;
+  mb_plan<TYPE, XT>(M, N, K, &us, &nsl);
+  const bool split = nsl > 1 && work && work_floats >= (int64_t)nsl * M * N;
+  if (!split) {  // every workgroup walks all of K, in the widest slices that fit
+    us = mb_units_per_slice<TYPE, XT>(M, K);
+    nsl = (K / UE + us - 1) / us;
   }
-  const int ce = ks * uc * UE;
-  const size_t lds = (size_t)M * (ce + kXPad) * 2 * PARTS +
-                     (size_t)(ce / GS + ce / UE) * 16 * MT * 4 + (size_t)4 * MT * 4 * 64 * 4 +
-                     kZeroHalves * 2;
-  const int ts = 4 / ks;
-  const dim3 grid((unsigned)((ntiles + ts - 1) / ts)), block(256);
-  hipLaunchKernelGGL((decode_kernel<TYPE, XT, MT, MR>), grid, block, lds, s, x, ldx, W, N, K, y,
-                     ldy, M, ks, uc);
+  const int ce = us * UE;
+  size_t lds = (size_t)M * (ce + kXPad) * 2 * PARTS + (size_t)(ce / GS + ce / UE) * 16 * MT * 4 +
+               kZeroHalves * 2;
+  const size_t red = (size_t)8 * 2 * MT * 4 * 64 * 4;
+  lds = lds > red ? lds : red;
+  auto kern = mb_kernel<TYPE, XT, MT>;
+  if (lds > 65536) {
+    const hipError_t ea =
+        hipFuncSetAttribute((const void *)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    if (ea != hipSuccess) return ea;
+  }
+  const unsigned groups = (unsigned)(((N + 15) / 16 + kMbTiles - 1) / kMbTiles);
+  const dim3 grid(groups, split ? (unsigned)nsl : 1u), block(kMbThreads);
+  hipLaunchKernelGGL(kern, grid, block, lds, s, x, ldx, W, N, K, M, us, split ? 1 : nsl,
+                     split ? work : y, split ? (int64_t)N : ldy);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess || !split) return e;
+  const int64_t mn = (int64_t)M * N;
+  hipLaunchKernelGGL(mb_reduce_kernel, dim3((unsigned)((mn + 255) / 256)), dim3(256), 0, s, work,
+                     nsl, M, N, y, ldy);
   return hipGetLastError();
+}
+
+// Workspace floats the split-K batched decode uses for M rows (0: none).
+template <int TYPE, typename XT>
+int64_t mb_work_floats(int M, int N, int K) {
+  if (M < 2) return 0;
+  int us, nsl;
+  mb_plan<TYPE, XT>(M, N, K, &us, &nsl);
+  return nsl > 1 ? (int64_t)nsl * M * N : 0;
 }
 
 // ---------------------------------------------------------------------------
@@ -1629,14 +1682,13 @@ hipError_t launch_m1(const XT *x, const uint8_t *W, int N, int K, float *y, cons
 
 template <int TYPE, typename XT>
 hipError_t launch_m(const XT *x, int64_t ldx, const uint8_t *W, int N, int K, float *y,
-                    int64_t ldy, int M, hipStream_t s) {
+                    int64_t ldy, int M, float *work, int64_t work_floats, hipStream_t s) {
   if (M == 1) {
     const hipError_t e = launch_m1<TYPE, XT, 0>(x, W, N, K, y, nullptr, 0.f, 0, AttnRecords{}, s);
     if (e != hipErrorNotSupported) return e;
-    return launch_t<TYPE, XT, 1, 1>(x, ldx, W, N, K, y, ldy, M, s);
   }
-  if (M <= 16) return launch_t<TYPE, XT, 1, 4>(x, ldx, W, N, K, y, ldy, M, s);
-  return launch_t<TYPE, XT, 2, 4>(x, ldx, W, N, K, y, ldy, M, s);
+  if (M <= 16) return launch_mb<TYPE, XT, 1>(x, ldx, W, N, K, y, ldy, M, work, work_floats, s);
+  return launch_mb<TYPE, XT, 2>(x, ldx, W, N, K, y, ldy, M, work, work_floats, s);
 }
 
 }  // namespace
@@ -1645,9 +1697,15 @@ hipError_t launch_m(const XT *x, int64_t ldx, const uint8_t *W, int N, int K, fl
 // a translation unit of its own (decode_<type>.hip) that expands this macro.
 #define GGUF_DECODE_DEFINE(T, NAME)                                                              \
   hipError_t decode_##NAME(const void *x, int x_type, int64_t ldx, const uint8_t *tiles, int n,  \
-                           int k, float *y, int64_t ldy, int m, hipStream_t s) {                 \
-    return x_type == 0 ? launch_m<T, float>((const float *)x, ldx, tiles, n, k, y, ldy, m, s)    \
-                       : launch_m<T, half_t>((const half_t *)x, ldx, tiles, n, k, y, ldy, m, s); \
+                           int k, float *y, int64_t ldy, int m, float *work, int64_t work_floats, \
+                           hipStream_t s) {                                                      \
+    return x_type == 0 ? launch_m<T, float>((const float *)x, ldx, tiles, n, k, y, ldy, m, work, \
+                                            work_floats, s)                                      \
+                       : launch_m<T, half_t>((const half_t *)x, ldx, tiles, n, k, y, ldy, m,     \
+                                             work, work_floats, s);                              \
+  }                                                                                              \
+  int64_t decode_work_##NAME(int x_type, int n, int k, int m) {                                  \
+    return x_type == 0 ? mb_work_floats<T, float>(m, n, k) : mb_work_floats<T, half_t>(m, n, k); \
   }                                                                                              \
   hipError_t decode_fused_##NAME(const float *x, const uint8_t *tiles, int n, int k, float *y,   \
                                  int prologue, const float *pw, float eps, int epi,              \

@@ -8,7 +8,9 @@ namespace gguf {
 
 #define GGUF_DECODE_DECLARE(NAME)                                                               \
   hipError_t decode_##NAME(const void *x, int x_type, int64_t ldx, const uint8_t *tiles, int n, \
-                           int k, float *y, int64_t ldy, int m, hipStream_t s);                 \
+                           int k, float *y, int64_t ldy, int m, float *work,                    \
+                           int64_t work_floats, hipStream_t s);                                 \
+  int64_t decode_work_##NAME(int x_type, int n, int k, int m);                                  \
   hipError_t decode_fused_##NAME(const float *x, const uint8_t *tiles, int n, int k, float *y,  \
                                  int prologue, const float *pw, float eps, int epi,             \
                                  hipStream_t s);                                                \

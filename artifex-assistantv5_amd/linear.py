@@ -314,10 +314,17 @@ def dispatch_matmul_gguf(a: torch.Tensor, gg: GGUFWeight, c: torch.Tensor, M: in
     if c_off and c.numel() * 4 < c_off + M * N * 4:
         raise ValueError(f'matmul_gguf "{label}": C window out of range')
     dev = gg.device
+    x_type = _X_TYPES[a.dtype]
+    # the split-K batched decode's workspace (partial sums of the K slices), taken
+    # from torch's caching allocator: stream-ordered, and from the graph's pool
+    # under capture
+    need = _native.check(lib.gguf_hip_matmul_workspace(gg.ggml_type, x_type, N, K, M), lib)
+    work = torch.empty(need, dtype=torch.uint8, device=dev) if need > 0 else None
     with torch.cuda.device(dev):
-        _native.check(lib.gguf_hip_matmul_variant(
-            a.data_ptr() + a_off, _X_TYPES[a.dtype], ldx, gg.ptr(), gg.ggml_type, N, K,
-            c.data_ptr() + c_off, ldy, M, variant, _stream(dev)), lib)
+        _native.check(lib.gguf_hip_matmul_ws(
+            a.data_ptr() + a_off, x_type, ldx, gg.ptr(), gg.ggml_type, N, K,
+            c.data_ptr() + c_off, ldy, M, variant, work.data_ptr() if work is not None else None,
+            need, _stream(dev)), lib)
 
 
 def dispatch_projection(input_buf: torch.Tensor, lw: LayerWeights, proj: str,

@@ -46,7 +46,7 @@ extern "C" {
  * are exported (kernels and helpers cannot be interposed across libraries). */
 #pragma GCC visibility push(default)
 
-#define GGUF_HIP_ABI_VERSION 12
+#define GGUF_HIP_ABI_VERSION 13
 
 /* ggml type ids (gguf.ts:24-35); activation dtypes reuse F32 / F16. */
 #define GGUF_HIP_F32 0
@@ -156,6 +156,22 @@ int gguf_hip_matmul(const void *x, int x_type, int64_t ldx, const void *tiles, i
 int gguf_hip_matmul_variant(const void *x, int x_type, int64_t ldx, const void *tiles,
                             int ggml_type, int64_t n, int64_t k, float *y, int64_t ldy,
                             int64_t m, int variant, void *stream);
+
+/* gguf_hip_matmul_variant with a caller workspace (device, 16-byte aligned,
+ * work_bytes long; NULL / 0 = none).  With at least gguf_hip_matmul_workspace
+ * bytes, a decode pass of 2..32 activation rows splits K over the grid and
+ * adds the slices' partial sums in a fixed order (a second launch): the same
+ * results as without a workspace up to f32 rounding of the sums, deterministic
+ * either way, and much faster for weights of few rows (the FFN down projection).
+ * The reference engine likewise preallocates its scratch (forward-pass.ts:1140-1163).
+ * Calls that share a workspace must not overlap. */
+int gguf_hip_matmul_ws(const void *x, int x_type, int64_t ldx, const void *tiles, int ggml_type,
+                       int64_t n, int64_t k, float *y, int64_t ldy, int64_t m, int variant,
+                       void *work, int64_t work_bytes, void *stream);
+
+/* Bytes of workspace gguf_hip_matmul_ws uses for these shapes (0: none);
+ * negative on bad arguments. */
+int64_t gguf_hip_matmul_workspace(int ggml_type, int x_type, int64_t n, int64_t k, int64_t m);
 
 /* Prologues of gguf_hip_matmul_fused. */
 #define GGUF_HIP_PROLOGUE_NONE 0

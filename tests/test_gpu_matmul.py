@@ -233,3 +233,39 @@ def test_full_size_configs(pkg, t, m, n, k, xdt):
     x = torch.randn(m, k, device="cuda", generator=g).to(xdt)
     y = pkg.qlinear(x, w)
     _gpu_check(y, x.float(), w.dequant().view(n, k), (t, m, n, k))
+
+
+@pytest.mark.parametrize("t,m,n,k", [(12, 8, 14336, 4096), (12, 32, 4096, 14336), (14, 17, 4096, 14336),
+                                     (2, 32, 4096, 4096), (8, 5, 1000, 2048), (10, 32, 512, 8192),
+                                     (13, 2, 300, 4096)])
+def test_batched_split_k_and_whole_k_agree(pkg, ref, t, m, n, k):
+    """The batched decode with a workspace (K split over the grid, slices added in
+    a fixed order by a second kernel) and without (each workgroup walks all of K)
+    both meet the decode gate against the oracle, and each is deterministic."""
+    raw, w = _case(pkg, t, n, k, seed=m + n)
+    wdeq = ref.dequant_rows(t, raw, n, k)
+    x = pkg.quantize.synthetic_activations(m, k, seed=k + m)
+    xt = torch.from_numpy(x).cuda()
+    lib = pkg.load_library()
+    need = lib.gguf_hip_matmul_workspace(t, 0, n, k, m)
+    assert need >= 0
+    s = torch.cuda.current_stream().cuda_stream
+    outs = []
+    for use_ws in (True, False):
+        y = torch.full((m, n), float("nan"), device="cuda")
+        work = torch.empty(max(need, 16), dtype=torch.uint8, device="cuda") if use_ws else None
+        rc = lib.gguf_hip_matmul_ws(xt.data_ptr(), 0, k, w.ptr(), t, n, k, y.data_ptr(), n, m, DECODE,
+                                    work.data_ptr() if use_ws else None, need if use_ws else 0, s)
+        assert rc == 0, lib.gguf_hip_last_error()
+        y2 = torch.empty_like(y)
+        lib.gguf_hip_matmul_ws(xt.data_ptr(), 0, k, w.ptr(), t, n, k, y2.data_ptr(), n, m, DECODE,
+                               work.data_ptr() if use_ws else None, need if use_ws else 0, s)
+        assert torch.equal(y, y2)
+        met = _metrics_decode(ref, y.cpu().numpy(), x, wdeq)
+        assert met["finite"] and met["elemwise"] <= DECODE_TOL, ((t, m, n, k, use_ws), met)
+        outs.append(y)
+
+
+def _metrics_decode(ref, y, x, wdeq):
+    x64 = x.astype(np.float64)
+    return ref.parity_metrics(y, ref.matmul_bt(x64, wdeq), ref.matmul_bt_abs(x64, wdeq))
