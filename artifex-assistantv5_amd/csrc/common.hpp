@@ -305,6 +305,15 @@ __device__ __forceinline__ float max_lanes16(float v) {
   v = fmaxf(v, dpp<kDppHalfMirror>(v));
   return fmaxf(v, dpp<kDppMirror>(v));
 }
+// max(v, v of lane ^ 16 / lane ^ 32)
+__device__ __forceinline__ float max_xor16(float v) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float max_xor32(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
 // v + v of lane ^ 16 / lane ^ 32
 __device__ __forceinline__ float sum_xor16(float v) {
   const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);

@@ -1296,10 +1296,13 @@ hipError_t launch_mb(const XT *x, int64_t ldx, const uint8_t *W, int N, int K, f
   return hipGetLastError();
 }
 
+#include "decode_mk.hpp"
+
 // Workspace floats the split-K batched decode uses for M rows (0: none).
 template <int TYPE, typename XT>
 int64_t mb_work_floats(int M, int N, int K) {
   if (M < 2) return 0;
+  if constexpr (TYPE == 12) return (int64_t)((mk_work_bytes<XT>(M, N, K) + 3) / 4);
   int us, nsl;
   mb_plan<TYPE, XT>(M, N, K, &us, &nsl);
   return nsl > 1 ? (int64_t)nsl * M * N : 0;
@@ -1685,6 +1688,10 @@ hipError_t launch_m(const XT *x, int64_t ldx, const uint8_t *W, int N, int K, fl
                     int64_t ldy, int M, float *work, int64_t work_floats, hipStream_t s) {
   if (M == 1) {
     const hipError_t e = launch_m1<TYPE, XT, 0>(x, W, N, K, y, nullptr, 0.f, 0, AttnRecords{}, s);
+    if (e != hipErrorNotSupported) return e;
+  }
+  if constexpr (TYPE == 12) {
+    const hipError_t e = launch_mk<XT>(x, ldx, W, N, K, y, ldy, M, work, work_floats, s);
     if (e != hipErrorNotSupported) return e;
   }
   if (M <= 16) return launch_mb<TYPE, XT, 1>(x, ldx, W, N, K, y, ldy, M, work, work_floats, s);

@@ -1,0 +1,502 @@
+// Batched decode of Q4_K weights (2 <= M <= 32 activation rows, and M = 1
+// beyond the one-shot kernel's K).
+//
+// Replaces the reference's batched decode, which runs its Q4_K GEMV once per
+// activation row (grid.y = M, webgpu/src/engine/forward-pass.ts:1536-1539;
+// kernel webgpu/src/shaders/matmul_gguf.wgsl:3191-3245): here the weights are
+// read once for all M rows.
+//
+// mk_prep_kernel converts the activations once per call into an image in the
+// workspace, laid out exactly as a workgroup's shared memory holds them (so
+// staging a K range is a flat copy), one block of mk_unit_bytes<MA>() per
+// 256-element unit (MA activation tiles of 16 MFMA rows each); mk_kernel
+// streams the weights; mk_reduce_kernel adds the partial sums when K is
+// split over workgroups.
+//   A [16 MA][kMkLd] f16  MFMA row 2m + p holds part p (hi, lo) of activation
+//                         row m for f32 inputs (8 rows per tile); row m holds
+//                         row m for 16-bit inputs (16 rows per tile).  The
+//                         elements are x * 2^e(m, unit), with e putting the
+//                         unit's largest magnitude in [2^14, 2^15) (stage_exp),
+//                         each quad in (0, 2, 1, 3) order.
+//   S [16 MA][16] f16     the unit's 8 group sums sum(hi + lo) / 32, as hi and
+//                         lo f16 parts, on the row of part 0 (zeros on the row
+//                         of part 1): the A operand of the mins MFMA.
+//   F [16 MA] f32         2^-e(m, unit) on every row of m.
+//
+// Arithmetic per unit, weight row n, activation row m.  The B operand is the
+// sub-block's codes times its 6-bit scale, exact f16 integers (q sc <= 945,
+// one v_pk_fma_f16 per two codes, mk_scaled), so the 8 sub-block
+// MFMAs of a unit chain into one f32 accumulator D[m, n] = sum_j sc_j sum_k q x;
+// one 16x16x16 MFMA gives the mins' dot M[m, n] = sum_j m_j S_j[m]; then
+//     acc[m, n] += F[m] (d D[m, n] - 32 dmin M[m, n])
+// in f32, and the parts are added at the end.
+#pragma once
+
+constexpr int kMkLd = 256 + 8;  // halves per staged row: a 16-byte pad (bank spread)
+template <int MA>
+constexpr int mk_unit_bytes() {
+  return 16 * MA * (kMkLd * 2 + 32 + 4);
+}
+template <int MA>
+constexpr int mk_s_off() {
+  return 16 * MA * kMkLd * 2;
+}
+template <int MA>
+constexpr int mk_f_off() {
+  return 16 * MA * (kMkLd * 2 + 32);
+}
+
+#ifndef GGUF_MK_LDS
+#define GGUF_MK_LDS (150 * 1024)  // shared memory a workgroup's staged range may take
+#endif
+#ifndef GGUF_MK_MIN_WGS
+#define GGUF_MK_MIN_WGS 224  // split K further while the grid has fewer workgroups
+#endif
+#ifndef GGUF_MK_DEPTH
+#define GGUF_MK_DEPTH 2  // units in flight per wave, 1 or 2 activation tiles
+#endif
+#ifndef GGUF_MK_DEPTH_WIDE
+#define GGUF_MK_DEPTH_WIDE 2  // the same, 3 or 4 activation tiles
+#endif
+#ifndef GGUF_MK_WIDE_T
+#define GGUF_MK_WIDE_T 1  // row tiles per wave for 3 or 4 activation tiles (16 T tiles per workgroup)
+#endif
+template <int MA>
+constexpr int mk_kw_max() {  // units a workgroup can stage
+  return (GGUF_MK_LDS - 1024) / mk_unit_bytes<MA>();
+}
+
+// Convert one (unit, activation row) into the unit's image block at blk;
+// lane l holds elements 4l .. 4l + 3 in v (zeros for a padding row).  Every
+// lane of the wave takes part.
+template <int PARTS, int MA>
+__device__ __forceinline__ void mk_stage(const float (&v)[4], int m, int l, uint8_t *blk) {
+  float mx = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
+  mx = max_xor32(max_xor16(max_lanes16(mx)));
+  const int ex = stage_exp(mx);
+  const float sc = pow2f(ex);
+  half4_t h, lo;
+  float s = 0.f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int pos = (i & 1) << 1 | (i >> 1);  // quad order (0, 2, 1, 3)
+    float vi = v[i];
+    asm volatile("" : "+v"(vi));  // keep the product out of the f16 conversions (no v_fma_mix)
+    const float t = vi * sc;      // exact: a power of two
+    const half_t hh = (half_t)t;
+    const half_t ll = (half_t)(t - (float)hh);
+    h[pos] = hh;
+    lo[pos] = ll;
+    s += (float)hh + (PARTS == 2 ? (float)ll : 0.f);
+  }
+  s += dpp<kDppXor1>(s);  // the 8 lanes of a 32-element group
+  s += dpp<kDppXor2>(s);
+  s += dpp<kDppHalfMirror>(s);
+  const int row = PARTS == 2 ? 2 * m : m;
+  half_t *A = (half_t *)blk + row * kMkLd + 4 * l;
+  *(half4_t *)A = h;
+  if (PARTS == 2) *(half4_t *)(A + kMkLd) = lo;
+  if ((l & 7) == 0) {
+    // group j's sum at K position 4 (j >> 2) + e (hi) and 8 + that (lo), with e
+    // the position of j & 3 in the (0, 2, 1, 3) order of the mins operand
+    const int j = l >> 3, e = ((j & 1) << 1) | ((j >> 1) & 1), k = 4 * (j >> 2) + e;
+    const float xs = s * 0.03125f;
+    const half_t xh = (half_t)xs, xl = (half_t)(xs - (float)xh);
+    half_t *S = (half_t *)(blk + mk_s_off<MA>()) + row * 16;
+    S[k] = xh;
+    S[8 + k] = xl;
+    if (PARTS == 2) {
+      S[16 + k] = (half_t)0.f;
+      S[24 + k] = (half_t)0.f;
+    }
+  }
+  if (l == 0) {
+    float *F = (float *)(blk + mk_f_off<MA>());
+    F[row] = pow2f(-ex);
+    if (PARTS == 2) F[row + 1] = pow2f(-ex);
+  }
+}
+
+// The activations' image, once per call: one wave per (unit, activation
+// row), four per block; rows M .. ROWS - 1 are written as zeros.
+template <typename XT, int MA>
+__global__ __launch_bounds__(256) void mk_prep_kernel(const XT *__restrict__ x, int64_t ldx, int M,
+                                                      uint8_t *__restrict__ img) {
+  constexpr int PARTS = sizeof(XT) == 4 ? 2 : 1;
+  const int u = blockIdx.x, m = 4 * blockIdx.y + (threadIdx.x >> 6), l = threadIdx.x & 63;
+  float v[4] = {0.f, 0.f, 0.f, 0.f};
+  if (m < M) {
+    const XT *src = x + (int64_t)m * ldx + 256 * u + 4 * l;
+    if constexpr (sizeof(XT) == 4) {
+      const float4 t = *(const float4 *)src;
+      v[0] = t.x; v[1] = t.y; v[2] = t.z; v[3] = t.w;
+    } else {
+      const half4_t t = *(const half4_t *)src;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) v[e] = (float)t[e];
+    }
+  }
+  mk_stage<PARTS, MA>(v, m, l, img + (size_t)u * mk_unit_bytes<MA>());
+}
+
+// The mins operand of lane group g: m_j for j = 4 (g & 1) + (0, 2, 1, 3).
+__device__ __forceinline__ half4_t mk_mins_operand(uint32_t mw) {
+  constexpr uint32_t nb = neg_base(0);
+  return as_h4(f16_codes(mw, 0x00FF00FFu, nb), f16_codes(mw >> 8, 0x00FF00FFu, nb));
+}
+
+// sc q for the two codes masked (m) into the halves of w: (base + c) sc' - 1024 sc'
+// with base = 1024.0 in both halves, c = q (low nibbles, sc' = sc) or 16 q
+// (high nibbles, sc' = sc / 16); scp holds sc' in both halves, nsp -1024 sc'.
+// Exact: every product and the result q sc <= 945 are f16 integers.
+__device__ __forceinline__ uint32_t mk_scaled(uint32_t w, uint32_t m, uint32_t base, half2_t scp,
+                                              half2_t nsp) {
+  const half2_t c = __builtin_bit_cast(half2_t, and_or(w, m, base));
+  return __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(c, scp, nsp));
+}
+
+template <int MA, int T>
+__device__ __forceinline__ void mk_unit(const Unit<12> (&w)[T], int bo, int lane, bool valid,
+                                        float (&acc)[T][MA][4]) {
+#pragma clang fp contract(off)
+  const int r = lane & 15, g = lane >> 4;
+  // 1024.0 x 2 in a register: with both the mask and this as literals the
+  // compiler splits every and-or into two instructions
+  uint32_t base = kF16Base;
+  asm volatile("" : "+v"(base));
+  // SC[t][i]: scales (sc0, sc2), (sc1, sc3) / 16, (sc4, sc6), (sc5, sc7) / 16
+  // (odd sub-blocks hold high nibbles); NS = -1024 SC
+  half2_t SC[T][4], NS[T][4];
+  uint32_t ml[T], mh[T];
+#pragma unroll
+  for (int t = 0; t < T; ++t) {
+    uint32_t scl, sch;
+    q4k_scales_packed(w[t].h.y, w[t].h.z, w[t].h.w, scl, sch, ml[t], mh[t]);
+    constexpr uint32_t nb = neg_base(0);
+    const half2_t h16 = {(half_t)0.0625f, (half_t)0.0625f}, hn = {(half_t)-1024.f, (half_t)-1024.f};
+    SC[t][0] = __builtin_bit_cast(half2_t, f16_codes(scl, 0x00FF00FFu, nb));
+    SC[t][1] = __builtin_bit_cast(half2_t, f16_codes(scl >> 8, 0x00FF00FFu, nb)) * h16;
+    SC[t][2] = __builtin_bit_cast(half2_t, f16_codes(sch, 0x00FF00FFu, nb));
+    SC[t][3] = __builtin_bit_cast(half2_t, f16_codes(sch >> 8, 0x00FF00FFu, nb)) * h16;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) NS[t][i] = SC[t][i] * hn;
+  }
+  float4_t D[T][MA];
+#pragma unroll
+  for (int t = 0; t < T; ++t)
+#pragma unroll
+    for (int a = 0; a < MA; ++a) D[t][a] = (float4_t){0.f, 0.f, 0.f, 0.f};
+  const int arow = bo + r * (kMkLd * 2) + 16 * g;  // byte offset of the lane's A fragment
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+    uint32_t wq[T][4];  // the lane's chunk-c words and their bytes 1, 3 moved down
+#pragma unroll
+    for (int t = 0; t < T; ++t) {
+      const uint32_t q[8] = {w[t].a.x, w[t].a.y, w[t].a.z, w[t].a.w,
+                             w[t].b.x, w[t].b.y, w[t].b.z, w[t].b.w};
+      wq[t][0] = q[2 * c];
+      wq[t][1] = q[2 * c] >> 8;
+      wq[t][2] = q[2 * c + 1];
+      wq[t][3] = q[2 * c + 1] >> 8;
+    }
+#pragma unroll
+    for (int hb = 0; hb < 2; ++hb) {  // sub-block j = 2c + hb: low (hb 0) / high nibbles
+      const int j = 2 * c + hb;
+      const uint32_t m = hb ? 0x00F000F0u : 0x000F000Fu;
+      half8_t A[MA];
+#pragma unroll
+      for (int a = 0; a < MA; ++a) A[a] = lds_h8b(arow + a * 16 * (kMkLd * 2) + 2 * (64 * c + 32 * hb));
+#pragma unroll
+      for (int t = 0; t < T; ++t) {
+        const int si = (j >> 2) * 2 + hb, sh = (j >> 1) & 1;
+        const half2_t scp = {SC[t][si][sh], SC[t][si][sh]}, nsp = {NS[t][si][sh], NS[t][si][sh]};
+        const half8_t B = as_h8(mk_scaled(wq[t][0], m, base, scp, nsp), mk_scaled(wq[t][1], m, base, scp, nsp),
+                                mk_scaled(wq[t][2], m, base, scp, nsp), mk_scaled(wq[t][3], m, base, scp, nsp));
+#pragma unroll
+        for (int a = 0; a < MA; ++a)
+          D[t][a] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[a], B, D[t][a], 0, 0, 0);
+      }
+      // wide tiles: one sub-block's operands at a time (unconstrained, the
+      // scheduler loads every A fragment of the unit up front and spills)
+      if constexpr (MA * T >= 4) __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+  // mins: one 16x16x16 MFMA per activation tile (K = 8 group sums x hi / lo)
+  half4_t B2[T];
+  float d[T], dm[T];
+#pragma unroll
+  for (int t = 0; t < T; ++t) {
+    B2[t] = mk_mins_operand((g & 1) ? mh[t] : ml[t]);
+    // a slot past the wave's units (valid false) adds exactly zero
+    d[t] = valid ? h2f(w[t].h.x) : 0.f;
+    dm[t] = valid ? -32.f * h2f(w[t].h.x >> 16) : 0.f;
+  }
+#pragma unroll
+  for (int a = 0; a < MA; ++a) {
+    const half4_t A2 = lds_h4b(bo + mk_s_off<MA>() + (16 * a + r) * 32 + 8 * g);
+    const float4 F = *(const float4 *)(g_lds + bo + mk_f_off<MA>() + (16 * a + 4 * g) * 4);
+    const float f[4] = {F.x, F.y, F.z, F.w};
+#pragma unroll
+    for (int t = 0; t < T; ++t) {
+      const float4_t zero = {0.f, 0.f, 0.f, 0.f};
+      const float4_t D2 = __builtin_amdgcn_mfma_f32_16x16x16f16(A2, B2[t], zero, 0, 0, 0);
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        acc[t][a][i] = fmaf(f[i], fmaf(d[t], D[t][a][i], dm[t] * D2[i]), acc[t][a][i]);
+    }
+    if constexpr (MA * T >= 4) __builtin_amdgcn_sched_barrier(0);  // one tile at a time
+  }
+  // The sums are used only under the output's conditions: without this the
+  // compiler sinks every unit's update there and keeps all the units'
+  // products alive until the end (spilling them).
+#pragma unroll
+  for (int t = 0; t < T; ++t)
+#pragma unroll
+    for (int a = 0; a < MA; ++a)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) asm volatile("" : "+v"(acc[t][a][i]));
+}
+
+// Workgroup (blockIdx.x, blockIdx.y) of TS x KL waves: row tiles
+// TS T blockIdx.x .. + TS T - 1 (T per wave; wave w takes tile slot w % TS and
+// K-lane w / TS), units blockIdx.y kw .. + kw - 1 of K, of which K-lane kl
+// takes every KL-th from kl.
+//
+// Order of work: every thread requests its share of the range's image, then
+// all of its tiles' units (at most U per tile); it writes the image to shared
+// memory as it lands (the weights still in flight); after the one barrier
+// each wave consumes its units in order as they arrive.  The K-lanes of a
+// tile slot are added in a fixed order through shared memory.
+template <typename XT, int MA, int T, int TS, int KL>
+__global__ __launch_bounds__(64 * TS * KL) void mk_kernel(const uint8_t *__restrict__ img,
+                                                          const uint8_t *__restrict__ W, int N,
+                                                          int K, int M, int kw,
+                                                          float *__restrict__ out, int64_t ldo) {
+  constexpr int PARTS = sizeof(XT) == 4 ? 2 : 1, NW = TS * KL;
+  constexpr int UB = mk_unit_bytes<MA>(), TU = Fmt<12>::TU;
+  constexpr int CP = (mk_kw_max<MA>() * UB / 16 + 64 * NW - 1) / (64 * NW);  // 16 B pieces per thread
+  constexpr int U = (mk_kw_max<MA>() + KL - 1) / KL;                          // unit slots per wave
+  // slots in flight per tile: a few MB over the chip keep the transfer at full
+  // rate and the arrivals in order (all at once, they land in no useful order
+  // and the decode runs after the transfer instead of under it)
+  constexpr int P = (MA > 2 ? GGUF_MK_DEPTH_WIDE : GGUF_MK_DEPTH) < U
+                        ? (MA > 2 ? GGUF_MK_DEPTH_WIDE : GGUF_MK_DEPTH) : U;
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int r = lane & 15, g = lane >> 4;
+  const int ts = wave % TS, kl = wave / TS;
+  const int ntiles = (N + 15) >> 4, nu = K >> 8;
+  const int t0 = (blockIdx.x * TS + ts) * T;
+  const int u0 = blockIdx.y * kw, nun = min(kw, nu - u0);
+  const int cnt = (nun - kl + KL - 1) / KL;  // the wave's units: kl + KL i, i < cnt
+  const int tb = nu * TU;
+  const int nq = nun * (UB / 16);  // 16-byte pieces of the range's image
+
+  // the range's image.  Narrow tiles (MA <= 2): through registers, requested
+  // ahead of the weights and written as it lands (pieces past the range repeat
+  // the last one and are not stored).  Wide tiles: LDS-direct loads in 1 KB
+  // pieces (the workspace holds 1 KB of slack past the image), no registers,
+  // before the weights are requested (the barrier waits for every load).
+  constexpr bool DMA = MA > 2;
+  typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));  // a value type: no memcpy copies
+  const uint8_t *src = img + (size_t)u0 * UB;
+  u32x4 R[DMA ? 1 : CP];
+  if constexpr (DMA) {
+    const int kb = (nun * UB + 1023) >> 10;
+    for (int i = wave; i < kb; i += NW)
+      __builtin_amdgcn_global_load_lds((const void *)(src + 1024 * i + 16 * lane),
+                                       (__attribute__((address_space(3))) void *)(g_lds + 1024 * i),
+                                       16, 0, 0);
+    __syncthreads();
+  } else {
+#pragma unroll
+    for (int c = 0; c < CP; ++c)
+      R[c] = *(const u32x4 *)(src + 16 * min((int)threadIdx.x + 64 * NW * c, nq - 1));
+  }
+  __amdgpu_buffer_rsrc_t rs[T];
+#pragma unroll
+  for (int t = 0; t < T; ++t)  // a tile past the weight's end has no records (loads read 0)
+    rs[t] = __builtin_amdgcn_make_buffer_rsrc((void *)(W + (int64_t)min(t0 + t, ntiles - 1) * tb), 0,
+                                              t0 + t < ntiles ? tb : 0, kRsrcWord3);
+  // The wave's U unit slots in straight-line code, P in flight (slot i + P
+  // requested once slot i is consumed), branch-free: a slot past the wave's
+  // units loads its last unit (an L2 hit) and adds zero.  Under a branch or in
+  // a loop the memory-counter waits lose track of the requests and wait for
+  // all of them at every unit.
+  const int ulast = cnt > 0 ? kl + KL * (cnt - 1) : 0;  // a unit of the range
+  Unit<12> wb[P][T];
+#pragma unroll
+  for (int i = 0; i < P; ++i)
+#pragma unroll
+    for (int t = 0; t < T; ++t) load_unit(rs[t], (u0 + min(kl + KL * i, ulast)) * TU, r, g, wb[i][t]);
+  if constexpr (!DMA) {
+#pragma unroll
+    for (int c = 0; c < CP; ++c) {
+      const int q = (int)threadIdx.x + 64 * NW * c;
+      if (q < nq) *(u32x4 *)(g_lds + 16 * q) = R[c];
+    }
+    __syncthreads();
+  }
+  float acc[T][MA][4];
+#pragma unroll
+  for (int t = 0; t < T; ++t)
+#pragma unroll
+    for (int a = 0; a < MA; ++a)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) acc[t][a][i] = 0.f;
+#pragma unroll
+  for (int i = 0; i < U; ++i) {
+    mk_unit<MA, T>(wb[i % P], min(kl + KL * i, ulast) * UB, lane, i < cnt, acc);
+    if (i + P < U)  // compile-time
+#pragma unroll
+      for (int t = 0; t < T; ++t)
+        load_unit(rs[t], (u0 + min(kl + KL * (i + P), ulast)) * TU, r, g, wb[i % P][t]);
+  }
+  if constexpr (KL > 1) {  // K-lanes 1 .. KL - 1 hand their sums to lane 0, added in order
+    __syncthreads();  // the staged activations are consumed
+    float *red = (float *)g_lds;  // [KL - 1][TS][T][MA][4][64]
+    if (kl > 0) {
+#pragma unroll
+      for (int t = 0; t < T; ++t)
+#pragma unroll
+        for (int a = 0; a < MA; ++a)
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            red[(((((kl - 1) * TS + ts) * T + t) * MA + a) * 4 + i) * 64 + lane] = acc[t][a][i];
+    }
+    __syncthreads();
+    if (kl > 0) return;
+#pragma unroll
+    for (int k2 = 1; k2 < KL; ++k2)
+#pragma unroll
+      for (int t = 0; t < T; ++t)
+#pragma unroll
+        for (int a = 0; a < MA; ++a)
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            acc[t][a][i] += red[(((((k2 - 1) * TS + ts) * T + t) * MA + a) * 4 + i) * 64 + lane];
+  }
+  float *o = out + (int64_t)blockIdx.y * (gridDim.y > 1 ? (int64_t)M * ldo : 0);
+#pragma unroll
+  for (int t = 0; t < T; ++t) {
+    const int n = 16 * (t0 + t) + r;
+    if (n >= N) continue;
+#pragma unroll
+    for (int a = 0; a < MA; ++a) {
+      if (PARTS == 2) {
+        const int m = 8 * a + 2 * g;
+        if (m < M) o[(int64_t)m * ldo + n] = acc[t][a][0] + acc[t][a][1];
+        if (m + 1 < M) o[(int64_t)(m + 1) * ldo + n] = acc[t][a][2] + acc[t][a][3];
+      } else {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int m = 16 * a + 4 * g + i;
+          if (m < M) o[(int64_t)m * ldo + n] = acc[t][a][i];
+        }
+      }
+    }
+  }
+}
+
+// y[m, n] = sum over the S ranges of part[s][m][n] (row stride np), in
+// order.  One output element per thread; the S partials are requested at
+// once (up to kMkMaxRanges), then added.
+constexpr int kMkMaxRanges = 32;
+__global__ __launch_bounds__(256) void mk_reduce_kernel(const float *__restrict__ part, int S, int M,
+                                                        int np, int N, float *__restrict__ y,
+                                                        int64_t ldy) {
+  const int m = blockIdx.y, n = blockIdx.x * 256 + (int)threadIdx.x;
+  if (n >= N) return;
+  const float *p = part + (int64_t)m * np + n;
+  const int64_t st = (int64_t)M * np;
+  float v[kMkMaxRanges];
+#pragma unroll
+  for (int s = 0; s < kMkMaxRanges; ++s) v[s] = s < S ? p[s * st] : 0.f;
+  float a = v[0];
+#pragma unroll
+  for (int s = 1; s < kMkMaxRanges; ++s)
+    if (s < S) a += v[s];
+  y[(int64_t)m * ldy + n] = a;
+}
+
+// Launch shape: MA activation tiles; TS tile slots x KL K-lanes of T tiles
+// per workgroup (more tiles share each staged unit when the staging is
+// large); K split into `ranges` of kw units, as few as the shared memory
+// allows, more while the grid has fewer than GGUF_MK_MIN_WGS workgroups.
+struct MkPlan {
+  int ma, ts, kl, t, groups, kw, ranges;
+  size_t lds, part_off, bytes;  // workspace: the image, then the ranges' partial sums
+};
+template <typename XT>
+MkPlan mk_plan(int M, int N, int K) {
+  constexpr int PARTS = sizeof(XT) == 4 ? 2 : 1;
+  MkPlan p;
+  p.ma = (M * PARTS + 15) / 16;
+  const bool wide = p.ma > 2;
+  p.ts = wide ? 16 / GGUF_MK_WIDE_T : 4;
+  p.kl = wide ? 1 : 4;
+  p.t = wide ? GGUF_MK_WIDE_T : 1;
+  const size_t ub = p.ma == 1 ? mk_unit_bytes<1>() : p.ma == 2 ? mk_unit_bytes<2>()
+                  : p.ma == 3 ? mk_unit_bytes<3>() : mk_unit_bytes<4>();
+  const int kw_max = p.ma == 1 ? mk_kw_max<1>() : p.ma == 2 ? mk_kw_max<2>()
+                   : p.ma == 3 ? mk_kw_max<3>() : mk_kw_max<4>();
+  const int ntiles = (N + 15) / 16, nu = K / 256;
+  p.groups = (ntiles + p.ts * p.t - 1) / (p.ts * p.t);
+  int ranges = (nu + kw_max - 1) / kw_max;
+  while (ranges < nu && (int64_t)p.groups * ranges < GGUF_MK_MIN_WGS) ++ranges;
+  p.kw = (nu + ranges - 1) / ranges;
+  p.ranges = (nu + p.kw - 1) / p.kw;
+  const size_t stage = ((size_t)p.kw * ub + 1023) & ~(size_t)1023;
+  const size_t red = (size_t)(p.kl - 1) * p.ts * p.t * p.ma * 4 * 64 * 4;
+  p.lds = stage > red ? stage : red;
+  p.part_off = ((size_t)nu * ub + 1024 + 255) & ~(size_t)255;  // 1 KB slack for 1 KB copy pieces
+  p.bytes = p.part_off + (p.ranges > 1 ? (size_t)p.ranges * M * ntiles * 16 * 4 : 0);
+  return p;
+}
+
+template <typename XT, int MA, int T, int TS, int KL>
+hipError_t launch_mk_ma(const XT *x, int64_t ldx, const uint8_t *W, int N, int K, float *y,
+                        int64_t ldy, int M, float *work, const MkPlan &p, hipStream_t s) {
+  constexpr int PARTS = sizeof(XT) == 4 ? 2 : 1;
+  const int np = (N + 15) / 16 * 16;
+  uint8_t *img = (uint8_t *)work;
+  float *part = (float *)(img + p.part_off);
+  hipLaunchKernelGGL((mk_prep_kernel<XT, MA>), dim3((unsigned)(K / 256), (unsigned)(16 * MA / PARTS / 4)),
+                     dim3(256), 0, s, x, ldx, M, img);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  auto kern = mk_kernel<XT, MA, T, TS, KL>;
+  if (p.lds > 65536) {
+    e = hipFuncSetAttribute((const void *)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)p.lds);
+    if (e != hipSuccess) return e;
+  }
+  hipLaunchKernelGGL(kern, dim3((unsigned)p.groups, (unsigned)p.ranges), dim3(64 * TS * KL), p.lds, s,
+                     img, W, N, K, M, p.kw, p.ranges > 1 ? part : y, p.ranges > 1 ? (int64_t)np : ldy);
+  e = hipGetLastError();
+  if (e != hipSuccess || p.ranges == 1) return e;
+  hipLaunchKernelGGL(mk_reduce_kernel, dim3((unsigned)((N + 255) / 256), (unsigned)M), dim3(256), 0, s,
+                     part, p.ranges, M, np, N, y, ldy);
+  return hipGetLastError();
+}
+
+// Workspace bytes of the batched path for M rows of XT activations.
+template <typename XT>
+size_t mk_work_bytes(int M, int N, int K) {
+  return mk_plan<XT>(M, N, K).bytes;
+}
+
+// hipErrorNotSupported (nothing launched) when the workspace is missing or
+// too small, or K needs more ranges than the reduction takes: the caller then
+// takes the kernel that stages in every workgroup.
+template <typename XT>
+hipError_t launch_mk(const XT *x, int64_t ldx, const uint8_t *W, int N, int K, float *y,
+                     int64_t ldy, int M, float *work, int64_t work_floats, hipStream_t s) {
+  const MkPlan p = mk_plan<XT>(M, N, K);
+  if (M > 32 || p.ranges > kMkMaxRanges || !work || (size_t)work_floats * 4 < p.bytes)
+    return hipErrorNotSupported;
+  switch (p.ma) {  // the shapes mk_plan assumes for each MA
+    case 1: return launch_mk_ma<XT, 1, 1, 4, 4>(x, ldx, W, N, K, y, ldy, M, work, p, s);
+    case 2: return launch_mk_ma<XT, 2, 1, 4, 4>(x, ldx, W, N, K, y, ldy, M, work, p, s);
+    case 3: return launch_mk_ma<XT, 3, GGUF_MK_WIDE_T, 16 / GGUF_MK_WIDE_T, 1>(x, ldx, W, N, K, y, ldy, M, work, p, s);
+    default: return launch_mk_ma<XT, 4, GGUF_MK_WIDE_T, 16 / GGUF_MK_WIDE_T, 1>(x, ldx, W, N, K, y, ldy, M, work, p, s);
+  }
+}
