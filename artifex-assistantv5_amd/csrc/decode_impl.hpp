@@ -278,9 +278,19 @@ __device__ __forceinline__ half4_t as_h4(uint32_t a, uint32_t b) {
 // with such a span) for normal operands.
 constexpr uint32_t kF16Base = 0x64006400u;  // 1024.0 in both halves
 constexpr uint32_t neg_base(uint32_t off) { return (0xE400u + off) * 0x00010001u; }  // -(1024 + off) x 2
+// kF16Base in a vector register.  With the mask and the base both literals
+// the compiler splits every (w & m) | base into a v_and and a v_or (a VOP3
+// v_and_or_b32 takes at most one constant from the scalar side); with the base
+// in a register it is one v_and_or_b32.  The asm has no inputs and no side
+// effects, so identical copies fold into one per kernel.
+__device__ __forceinline__ uint32_t f16_base() {
+  uint32_t v;
+  asm("v_mov_b32 %0, %1" : "=v"(v) : "i"(kF16Base));
+  return v;
+}
 // the two codes (w & m) (each < 1024, one per half) minus off, as f16
 __device__ __forceinline__ uint32_t f16_codes(uint32_t w, uint32_t m, uint32_t nb) {
-  const half2_t v = __builtin_bit_cast(half2_t, and_or(w, m, kF16Base)) + __builtin_bit_cast(half2_t, nb);
+  const half2_t v = __builtin_bit_cast(half2_t, and_or(w, m, f16_base())) + __builtin_bit_cast(half2_t, nb);
   return __builtin_bit_cast(uint32_t, v);
 }
 // the same for codes already masked into the low bits of their halves
