@@ -24,7 +24,10 @@ tokens / decode wall time, prefill excluded).  ``secondary`` holds the other
 configurations of the path (Q4_K / Q5_K / Q6_K decode shapes and batch sizes,
 the other GGML types at the headline shape, more prefill shapes).  ``cpu_baseline`` = the CPU restatement of the reference
 path (numpy dequant to f32 + torch fp32 matmul) on all host cores, repeated
-for about 10 s.  ``roofline.traffic`` is read from the committed rocprofv3
+for about 10 s, with two more entries: ``prefill`` (the Q4_K GEMM shape at
+M=256) and ``decoder`` (the bench decoder in f32 on the host, ms/token over 8
+greedy tokens).  Each carries the host CPU model string, the cores used and the
+torch version.  ``roofline.traffic`` is read from the committed rocprofv3
 counter summary of the headline kernel when present.
 """
 
@@ -33,6 +36,7 @@ from __future__ import annotations
 import argparse
 import importlib
 import json
+import math
 import os
 import platform
 import sys
@@ -210,7 +214,165 @@ def cpu_baseline(pkg, raw, t, n, k, seconds, m=1):
                    f"torch.matmul f32; median dequant {np.median(t_deq) * 1e3:.1f} ms, matmul "
                    f"{np.median(t_mm) * 1e3:.1f} ms, total {tot * 1e3:.1f} ms per step"),
         "ms_per_step": round(tot * 1e3, 3),
-        "cpu": platform.processor() or platform.machine(),
+        "cpu": cpu_model(),
+        "torch": torch.__version__,
+    }
+
+
+def cpu_model():
+    """The host CPU's model string (/proc/cpuinfo), else what platform reports."""
+    try:
+        with open("/proc/cpuinfo", encoding="utf-8") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or platform.machine()
+
+
+def cpu_prefill_baseline(pkg, raw, t, n, k, m, reps=5):
+    """The prefill path on the host: oracle dequant (blocks -> f32 [N, K]) + torch
+    fp32 matmul of M fp16 activations upcast to f32; median of ``reps`` after 2
+    warm-ups."""
+    import torch
+    from oracle import gguf_ref as ref
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    x = torch.from_numpy(pkg.quantize.synthetic_activations(m, k, seed=7)).half().float()
+    t_deq, t_mm = [], []
+    for it in range(reps + 2):
+        t0 = time.perf_counter()
+        w = torch.from_numpy(ref.dequant_rows(t, raw, n, k))
+        t1 = time.perf_counter()
+        torch.matmul(x, w.T)
+        t2 = time.perf_counter()
+        if it >= 2:
+            t_deq.append(t1 - t0)
+            t_mm.append(t2 - t1)
+    deq, mm = float(np.median(t_deq)), float(np.median(t_mm))
+    flop = 2.0 * m * n * k
+    return {
+        "value": round(flop / (deq + mm) / 1e12, 4),
+        "unit": "TFLOP/s",
+        "cores": cores,
+        "kind": "port",
+        "sample": (f"Q4_K dequant-GEMM M={m} (the GPU line is M=2048) K={k} N={n}, fp16 "
+                   f"activations upcast to f32: {reps} runs after 2 warm-ups; median dequant "
+                   f"{deq * 1e3:.1f} ms + f32 matmul {mm * 1e3:.1f} ms "
+                   f"({flop / mm / 1e12:.3f} TFLOP/s for the matmul alone)"),
+        "ms_per_step": round((deq + mm) * 1e3, 3),
+        "cpu": cpu_model(),
+        "torch": torch.__version__,
+    }
+
+
+class CpuDecoder:
+    """The bench decoder on the host in f32: weights dequantized once by the
+    oracle (the CPU restatement of the reference dequant), projections as
+    torch fp32 matmuls, norm / RoPE / attention / SwiGLU as plain torch ops
+    (the same functions as the GPU decoder's prefill path).  Layers share one
+    dequantized layer set, as the GPU run's layers share one quantized set;
+    each layer's 0.9 GB still streams from DRAM (far beyond the caches)."""
+
+    def __init__(self, cfg, w, norms, final_norm):
+        import torch
+        dec = importlib.import_module("artifex-assistantv5_amd.decoder")
+        self.cfg, self.w, self.dec = cfg, w, dec
+        self.norms, self.final_norm = norms, final_norm
+        self.cos, self.sin = dec.rope_tables(cfg, "cpu")
+        self.k = [[] for _ in range(cfg.n_layers)]
+        self.v = [[] for _ in range(cfg.n_layers)]
+        self.torch = torch
+
+    def forward(self, tokens, pos0):
+        """Run token ids ``tokens`` at positions pos0.. and return the last
+        position's logits."""
+        torch, cfg, dec, w = self.torch, self.cfg, self.dec, self.w
+        M, nh, nkv, hd = len(tokens), cfg.n_heads, cfg.n_kv_heads, cfg.head_dim
+        grp = nh // nkv
+        pos = torch.arange(pos0, pos0 + M)
+        cos, sin = self.cos[pos], self.sin[pos]
+        x = w["embed"][torch.as_tensor(tokens)]
+        for l in range(cfg.n_layers):
+            an, fn = self.norms[l]
+            qkv = dec.rms_norm(x, an, cfg.eps) @ w["qkv"].T
+            q = dec.apply_rope(qkv[:, :nh * hd].view(M, nh, hd), cos, sin)
+            k = dec.apply_rope(qkv[:, nh * hd:(nh + nkv) * hd].view(M, nkv, hd), cos, sin)
+            self.k[l].append(k)
+            self.v[l].append(qkv[:, (nh + nkv) * hd:].view(M, nkv, hd))
+            K, V = torch.cat(self.k[l]), torch.cat(self.v[l])          # [T, nkv, hd]
+            T = K.shape[0]
+            qg = q.view(M, nkv, grp, hd).permute(1, 0, 2, 3).reshape(nkv, M * grp, hd)
+            s = torch.matmul(qg, K.permute(1, 2, 0)) / math.sqrt(hd)   # [nkv, M*grp, T]
+            mask = torch.arange(T)[None, :] > pos[:, None]              # [M, T]
+            s = s.masked_fill(mask.repeat_interleave(grp, dim=0)[None], float("-inf"))
+            o = torch.matmul(torch.softmax(s, dim=-1), V.permute(1, 0, 2))
+            o = o.view(nkv, M, grp, hd).permute(1, 0, 2, 3).reshape(M, nh * hd)
+            x = x + o @ w["o"].T
+            h = dec.rms_norm(x, fn, cfg.eps)
+            g, u = h @ w["gate"].T, h @ w["up"].T
+            x = x + (u * torch.nn.functional.silu(g)) @ w["down"].T
+        return dec.rms_norm(x[-1:], self.final_norm, cfg.eps) @ w["lm"].T
+
+
+def cpu_decoder_baseline(pkg, prompt_len=16, n_new=8, lm_head_unique_rows=16384):
+    """The bench decoder (``decoder_case``) on the host: the same configuration
+    and quantized layer set (same seeds), dequantized once at load by the
+    oracle; ``prompt_len`` prompt tokens, then ``n_new`` greedy tokens timed one
+    by one (ms/token = median)."""
+    import torch
+    from oracle import gguf_ref as ref
+    dec = importlib.import_module("artifex-assistantv5_amd.decoder")
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    cfg = dec.DecoderConfig()
+    d, hd, q = cfg.d_model, cfg.head_dim, pkg.quantize
+    t0 = time.perf_counter()
+
+    def deq(t, n, k, seed):  # decoder.synthetic_weights' blocks for the same seed
+        raw = q.quantize(q.synthetic_weight(n, k, seed=seed), t)
+        return torch.from_numpy(ref.dequant_rows(t, raw, n, k))
+
+    w = {"qkv": torch.cat([deq(cfg.attn_type, cfg.n_heads * hd, d, 1),
+                           deq(cfg.attn_type, cfg.n_kv_heads * hd, d, 2),
+                           deq(cfg.attn_type, cfg.n_kv_heads * hd, d, 3)]),
+         "o": deq(cfg.attn_type, d, cfg.n_heads * hd, 4),
+         "gate": deq(cfg.gate_up_type, cfg.ffn, d, 5),
+         "up": deq(cfg.gate_up_type, cfg.ffn, d, 6),
+         "down": deq(cfg.down_type, d, cfg.ffn, 7)}
+    lm = deq(cfg.lm_head_type, lm_head_unique_rows, d, 99)
+    w["lm"] = lm.repeat(-(-cfg.vocab // lm_head_unique_rows), 1)[:cfg.vocab].contiguous()
+    w["embed"] = w["lm"]                                   # tied embedding table
+    g = torch.Generator().manual_seed(0)
+    norms = [(1.0 + 0.02 * torch.randn(d, generator=g), 1.0 + 0.02 * torch.randn(d, generator=g))
+             for _ in range(cfg.n_layers)]
+    final_norm = 1.0 + 0.02 * torch.randn(d, generator=g)
+    t_load = time.perf_counter() - t0
+    m = CpuDecoder(cfg, w, norms, final_norm)
+    prompt = np.random.default_rng(0).integers(0, cfg.vocab, prompt_len).tolist()
+    with torch.no_grad():
+        t1 = time.perf_counter()
+        tok = int(m.forward(prompt, 0).argmax())
+        t_pre = time.perf_counter() - t1
+        steps = []
+        for i in range(n_new):
+            t2 = time.perf_counter()
+            tok = int(m.forward([tok], prompt_len + i).argmax())
+            steps.append(time.perf_counter() - t2)
+    ms = float(np.median(steps)) * 1e3
+    return {
+        "value": round(1e3 / ms, 3),
+        "unit": "tok/s",
+        "cores": cores,
+        "kind": "port",
+        "sample": (f"the bench decoder (32 layers, d 4096, 32/8 x 128, FFN 14336, vocab 151936, "
+                   f"Q4_K attention and gate/up, Q6_K down and LM head) in f32 on the host: "
+                   f"weights dequantized once at load ({t_load:.1f} s, one shared layer set), "
+                   f"{prompt_len}-token prompt ({t_pre * 1e3:.0f} ms), then {n_new} greedy tokens "
+                   f"(the GPU line decodes 256); median {ms:.1f} ms per token"),
+        "ms_per_token": round(ms, 2),
+        "cpu": cpu_model(),
         "torch": torch.__version__,
     }
 
@@ -397,7 +559,11 @@ def main():
         "secondary": secondary,
     }
     if not args.no_cpu_baseline:
-        out["cpu_baseline"] = cpu_baseline(pkg, raw, t, n, k, args.cpu_seconds)
+        cpu = cpu_baseline(pkg, raw, t, n, k, args.cpu_seconds)
+        cpu["prefill"] = cpu_prefill_baseline(pkg, raw, t, n, k, m=256)
+        if not args.no_decoder:
+            cpu["decoder"] = cpu_decoder_baseline(pkg)
+        out["cpu_baseline"] = cpu
     print(json.dumps(out), flush=True)
 
 
