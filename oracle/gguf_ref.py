@@ -1,5 +1,6 @@
 """CPU oracle for the GGUF Q4_0 / Q5_0 / Q8_0 / IQ4_NL / IQ4_XS / Q2_K / Q3_K / Q4_K / Q5_K /
-Q6_K dequant-matmul path.
+Q6_K dequant-matmul path (and, through ``oracle/gguf_iq.py``, the grid-codebook
+IQ types IQ2_XXS / IQ2_XS / IQ2_S / IQ3_XXS / IQ3_S / IQ1_M).
 
 TEST INFRASTRUCTURE ONLY.  This module is the checker: only ``tests/``,
 ``__graft_entry__.smoke()`` and the ``cpu_baseline`` leg of ``bench.py`` may
@@ -59,6 +60,8 @@ import numpy as np
 
 T_F32, T_F16, T_Q8_0, T_Q4_K, T_Q5_K, T_Q6_K, T_BF16 = 0, 1, 8, 12, 13, 14, 30
 T_Q4_0, T_Q5_0, T_IQ4_NL, T_IQ4_XS, T_Q2_K, T_Q3_K = 2, 6, 20, 23, 10, 11
+# the grid-codebook IQ types, restated in oracle/gguf_iq.py
+_IQ_TYPES = (16, 17, 18, 21, 22, 29)
 
 # kvalues_iq4nl, gguf-dequant.ts:29 (shared by IQ4_NL and IQ4_XS)
 KVALUES_IQ4NL = (-127, -104, -83, -65, -49, -35, -22, -10, 1, 13, 25, 38, 53, 69, 89, 113)
@@ -354,6 +357,9 @@ def dequant_ggml_loop(ggml_type: int, data: bytes, n: int) -> np.ndarray:
         return dequant_q5_k_loop(data, n)
     if ggml_type == T_Q6_K:
         return dequant_q6_k_loop(data, n)
+    if ggml_type in _IQ_TYPES:
+        from oracle import gguf_iq
+        return gguf_iq.LOOPS[ggml_type](data, n)
     raise NotImplementedError(f"[GGUF-dequant] No CPU reference for ggml type {ggml_type}")
 
 
@@ -573,6 +579,9 @@ def dequant_ggml(ggml_type: int, data, n: int) -> np.ndarray:
         return dequant_q5_k(data, n)
     if ggml_type == T_Q6_K:
         return dequant_q6_k(data, n)
+    if ggml_type in _IQ_TYPES:
+        from oracle import gguf_iq
+        return gguf_iq.VECTORISED[ggml_type](data, n)
     if ggml_type in (T_F32, T_F16, T_BF16):
         return dequant_ggml_loop(ggml_type, bytes(np.frombuffer(data, np.uint8)), n)
     raise NotImplementedError(f"[GGUF-dequant] No CPU reference for ggml type {ggml_type}")

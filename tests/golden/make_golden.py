@@ -16,6 +16,8 @@
    as the reference's CPU dequant declares them (``KVALUES_IQ4NL``,
    ``webgpu/src/model/gguf-dequant.ts``).  Data only.
 
+5. ``iq_grids.json`` and 6. ``iq_parity_samples.json`` — see write_iq_fixtures.
+
 Run from the repository root:  python tests/golden/make_golden.py [reference_root]
 """
 
@@ -94,6 +96,45 @@ def write_codebook(ref_root: str) -> None:
     raise RuntimeError("KVALUES_IQ4NL not found")
 
 
+IQ_GRIDS = {  # array name in gguf-dequant.ts -> key (ggml-common.h table it restates)
+    "IQ2XXS_GRID": "iq2xxs_grid", "KSIGNS_IQ2XS": "ksigns_iq2xs", "IQ3XXS_GRID": "iq3xxs_grid",
+    "IQ3S_GRID": "iq3s_grid", "IQ2S_GRID": "iq2s_grid", "IQ2XS_GRID": "iq2xs_grid",
+    "IQ1S_GRID": "iq1s_grid",
+}
+
+
+def write_iq_fixtures(ref_root: str) -> None:
+    """5. ``iq_grids.json`` — the IQ grid codebooks and the ksigns table as the
+    reference's CPU dequant declares them (byte arrays, gguf-dequant.ts), data
+    only.  6. ``iq_parity_samples.json`` — the reference's IQ dequant parity
+    fixture (``webgpu/scripts/iq_parity_fixture.json``: gguf-py output on random
+    blocks of IQ2_XXS / IQ2_XS / IQ2_S / IQ3_XXS / IQ3_S / IQ1_M), copied as is."""
+    import re
+    path = os.path.join(ref_root, "webgpu", "src", "model", "gguf-dequant.ts")
+    with open(path, encoding="utf-8") as f:
+        lines = f.read().splitlines()
+    grids = {}
+    for no, line in enumerate(lines, 1):
+        m = re.match(r"const (\w+) = new (Uint8Array|Int8Array)\(\[([^\]]*)\]\)", line)
+        if m and m.group(1) in IQ_GRIDS:
+            grids[IQ_GRIDS[m.group(1)]] = {
+                "source": f"webgpu/src/model/gguf-dequant.ts:{no}", "signed": m.group(2) == "Int8Array",
+                "values": [int(v) for v in m.group(3).split(",")]}
+    missing = set(IQ_GRIDS.values()) - set(grids)
+    if missing:
+        raise RuntimeError(f"grids not found: {sorted(missing)}")
+    with open(os.path.join(HERE, "iq_grids.json"), "w", encoding="utf-8") as f:
+        json.dump({"iq1_delta": 0.125, "grids": grids}, f, separators=(",", ":"))
+    print("wrote the IQ grids: " + ", ".join(f"{k} {len(v['values'])}" for k, v in grids.items()))
+    src = os.path.join(ref_root, "webgpu", "scripts", "iq_parity_fixture.json")
+    with open(src, encoding="utf-8") as f:
+        fx = json.load(f)
+    with open(os.path.join(HERE, "iq_parity_samples.json"), "w", encoding="utf-8") as f:
+        json.dump({"source": "webgpu/scripts/iq_parity_fixture.json",
+                   "samples": fx["dequant_samples"]}, f, indent=0)
+    print(f"wrote {len(fx['dequant_samples'])} IQ parity samples")
+
+
 def write_synthetic() -> None:
     sys.path.insert(0, ROOT)
     pkg = importlib.import_module("artifex-assistantv5_amd")
@@ -121,4 +162,5 @@ if __name__ == "__main__":
         write_reference_samples(ref)
         write_tensor_tables(ref)
         write_codebook(ref)
+        write_iq_fixtures(ref)
     write_synthetic()
