@@ -45,10 +45,17 @@ bool traits(int t, int *block, int *size) {
   return false;
 }
 
+// the grid-codebook IQ types: decode kernels only (every M in passes of 32
+// rows), always with a workspace
+bool grid_type(int t) {
+  return t == GGUF_HIP_IQ2_XXS || t == GGUF_HIP_IQ2_XS || t == GGUF_HIP_IQ2_S ||
+         t == GGUF_HIP_IQ3_XXS || t == GGUF_HIP_IQ3_S || t == GGUF_HIP_IQ1_M;
+}
+
 bool kernel_type(int t) {
   return t == GGUF_HIP_Q8_0 || t == GGUF_HIP_Q4_K || t == GGUF_HIP_Q5_K || t == GGUF_HIP_Q6_K ||
-         t == GGUF_HIP_Q4_0 || t == GGUF_HIP_Q5_0 || t == GGUF_HIP_IQ4_NL || t == GGUF_HIP_IQ4_XS || t == GGUF_HIP_Q2_K ||
-         t == GGUF_HIP_Q3_K;
+         t == GGUF_HIP_Q4_0 || t == GGUF_HIP_Q5_0 || t == GGUF_HIP_IQ4_NL || t == GGUF_HIP_IQ4_XS ||
+         t == GGUF_HIP_Q2_K || t == GGUF_HIP_Q3_K || grid_type(t);
 }
 
 int check_type(int t) {
@@ -237,9 +244,20 @@ int gguf_hip_matmul_ws(const void *x, int x_type, int64_t ldx, const void *tiles
   // rows (the reference computes in f32) and take the row-scaled fp16 GEMM
   // from there on (prefill)
   if (variant == GGUF_HIP_VARIANT_AUTO)
-    variant = m <= (x_type == GGUF_HIP_F32 ? GGUF_HIP_F32_GEMM_MIN_M - 1 : GGUF_HIP_DECODE_MAX_M)
+    variant = grid_type(ggml_type) ||
+                      m <= (x_type == GGUF_HIP_F32 ? GGUF_HIP_F32_GEMM_MIN_M - 1 : GGUF_HIP_DECODE_MAX_M)
                   ? GGUF_HIP_VARIANT_DECODE
                   : GGUF_HIP_VARIANT_GEMM;
+  if (grid_type(ggml_type)) {
+    if (variant == GGUF_HIP_VARIANT_GEMM)
+      return fail(GGUF_HIP_ERR_TYPE, "[gguf-hip] no GEMM kernel for ggml type %d (use the decode variant)",
+                  ggml_type);
+    const int64_t need = 4 * gguf::launch_decode_work(ggml_type, x_type, n, k, m);
+    if (!work || work_bytes < need)
+      return fail(GGUF_HIP_ERR_SHAPE,
+                  "[gguf-hip] ggml type %d needs a workspace of %lld bytes (gguf_hip_matmul_workspace), "
+                  "got %lld", ggml_type, (long long)need, (long long)(work ? work_bytes : 0));
+  }
   // the GEMM addresses one 128-row activation block with 32-bit byte offsets
   if (variant == GGUF_HIP_VARIANT_GEMM && (127 * ldx + k) * esize >= ((int64_t)1 << 31))
     return fail(GGUF_HIP_ERR_SHAPE, "[gguf-hip] ldx too large for the GEMM kernel");
@@ -268,7 +286,7 @@ int64_t gguf_hip_matmul_workspace(int ggml_type, int x_type, int64_t n, int64_t 
   if (m < 0 || n < 0 || n > ((int64_t)1 << 30) || m > ((int64_t)1 << 30))
     return fail(GGUF_HIP_ERR_SHAPE, "[gguf-hip] bad M or N");
   ok();
-  if (m < 2 || n == 0) return 0;
+  if (n == 0 || m == 0 || (m < 2 && !grid_type(ggml_type))) return 0;
   return 4 * gguf::launch_decode_work(ggml_type, x_type, n, k, m);
 }
 

@@ -113,6 +113,31 @@ template <>
 struct Fmt<23> {  // IQ4_XS
   static constexpr int UE = 256, UB = 136, TU = 16 * 136;
 };
+// the grid-codebook IQ types (layout in iq.hpp)
+template <>
+struct Fmt<16> {  // IQ2_XXS
+  static constexpr int UE = 256, UB = 66, TU = 16 * 66;
+};
+template <>
+struct Fmt<17> {  // IQ2_XS
+  static constexpr int UE = 256, UB = 74, TU = 16 * 74;
+};
+template <>
+struct Fmt<18> {  // IQ3_XXS
+  static constexpr int UE = 256, UB = 98, TU = 16 * 98;
+};
+template <>
+struct Fmt<21> {  // IQ3_S
+  static constexpr int UE = 256, UB = 110, TU = 16 * 110;
+};
+template <>
+struct Fmt<22> {  // IQ2_S
+  static constexpr int UE = 256, UB = 82, TU = 16 * 82;
+};
+template <>
+struct Fmt<29> {  // IQ1_M
+  static constexpr int UE = 256, UB = 56, TU = 16 * 56;
+};
 
 // Q3_K: the 16 6-bit scales (stored + 32) from the 12 scale bytes (words a0,
 // a1, a2), one per byte of S[0..3]: low nibbles from a0 / a1 (scales 0-7) and
@@ -147,6 +172,12 @@ __host__ __device__ inline int unit_bytes(int type) {
          : type == 23 ? 136
          : type == 10 ? 84
          : type == 11 ? 110
+         : type == 16 ? 66
+         : type == 17 ? 74
+         : type == 18 ? 98
+         : type == 21 ? 110
+         : type == 22 ? 82
+         : type == 29 ? 56
          : (type == 12 ? 144 : (type == 13 ? 176 : 210));
 }
 

@@ -56,6 +56,12 @@ static int64_t pass_work(int type, int x_type, int n, int k, int mc) {
     case 14: return decode_work_q6_k(x_type, n, k, mc);
     case 20: return decode_work_iq4_nl(x_type, n, k, mc);
     case 23: return decode_work_iq4_xs(x_type, n, k, mc);
+    case 16: return decode_work_iq2_xxs(x_type, n, k, mc);
+    case 17: return decode_work_iq2_xs(x_type, n, k, mc);
+    case 22: return decode_work_iq2_s(x_type, n, k, mc);
+    case 18: return decode_work_iq3_xxs(x_type, n, k, mc);
+    case 21: return decode_work_iq3_s(x_type, n, k, mc);
+    case 29: return decode_work_iq1_m(x_type, n, k, mc);
     default: return 0;
   }
 }
@@ -91,6 +97,12 @@ hipError_t launch_decode(const void *x, int x_type, int64_t ldx, const uint8_t *
       case 14: e = decode_q6_k(xb, x_type, ldx, tiles, (int)n, (int)k, yb, ldy, mc, work, work_floats, s); break;
       case 20: e = decode_iq4_nl(xb, x_type, ldx, tiles, (int)n, (int)k, yb, ldy, mc, work, work_floats, s); break;
       case 23: e = decode_iq4_xs(xb, x_type, ldx, tiles, (int)n, (int)k, yb, ldy, mc, work, work_floats, s); break;
+      case 16: e = decode_iq2_xxs(xb, x_type, ldx, tiles, (int)n, (int)k, yb, ldy, mc, work, work_floats, s); break;
+      case 17: e = decode_iq2_xs(xb, x_type, ldx, tiles, (int)n, (int)k, yb, ldy, mc, work, work_floats, s); break;
+      case 22: e = decode_iq2_s(xb, x_type, ldx, tiles, (int)n, (int)k, yb, ldy, mc, work, work_floats, s); break;
+      case 18: e = decode_iq3_xxs(xb, x_type, ldx, tiles, (int)n, (int)k, yb, ldy, mc, work, work_floats, s); break;
+      case 21: e = decode_iq3_s(xb, x_type, ldx, tiles, (int)n, (int)k, yb, ldy, mc, work, work_floats, s); break;
+      case 29: e = decode_iq1_m(xb, x_type, ldx, tiles, (int)n, (int)k, yb, ldy, mc, work, work_floats, s); break;
       default: e = hipErrorNotSupported;
     }
   }

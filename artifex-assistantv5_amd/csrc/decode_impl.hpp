@@ -38,6 +38,7 @@
 
 #include "common.hpp"
 #include "decode_types.hpp"
+#include "iq.hpp"
 
 namespace gguf {
 
@@ -1312,7 +1313,7 @@ hipError_t launch_mb(const XT *x, int64_t ldx, const uint8_t *W, int N, int K, f
 template <int TYPE, typename XT>
 int64_t mb_work_floats(int M, int N, int K) {
   if (M < 2) return 0;
-  if constexpr (TYPE == 12) return (int64_t)((mk_work_bytes<XT>(M, N, K) + 3) / 4);
+  if constexpr (TYPE == 12) return (int64_t)((mk_work_bytes<12, XT>(M, N, K) + 3) / 4);
   int us, nsl;
   mb_plan<TYPE, XT>(M, N, K, &us, &nsl);
   return nsl > 1 ? (int64_t)nsl * M * N : 0;
@@ -1701,7 +1702,7 @@ hipError_t launch_m(const XT *x, int64_t ldx, const uint8_t *W, int N, int K, fl
     if (e != hipErrorNotSupported) return e;
   }
   if constexpr (TYPE == 12) {
-    const hipError_t e = launch_mk<XT>(x, ldx, W, N, K, y, ldy, M, work, work_floats, s);
+    const hipError_t e = launch_mk<12, XT>(x, ldx, W, N, K, y, ldy, M, work, work_floats, s);
     if (e != hipErrorNotSupported) return e;
   }
   if (M <= 16) return launch_mb<TYPE, XT, 1>(x, ldx, W, N, K, y, ldy, M, work, work_floats, s);
@@ -1737,6 +1738,31 @@ hipError_t launch_m(const XT *x, int64_t ldx, const uint8_t *W, int N, int K, fl
   hipError_t decode_merge_##NAME(const AttnRecords &ar, const uint8_t *tiles, int n, float *y,   \
                                  int epi, hipStream_t s) {                                       \
     return launch_m1<T, float, 3>(nullptr, tiles, n, ar.nh * ar.hd, y, nullptr, 0.f, epi, ar, s); \
+  }
+
+// The grid-codebook IQ types take the batched kernel (decode_mk.hpp) for every
+// M up to 32, M = 1 included, so they always need its workspace; they have no
+// fused prologue / epilogue or merge kernels.
+#define GGUF_DECODE_DEFINE_IQ(T, NAME)                                                           \
+  hipError_t decode_##NAME(const void *x, int x_type, int64_t ldx, const uint8_t *tiles, int n,  \
+                           int k, float *y, int64_t ldy, int m, float *work, int64_t work_floats, \
+                           hipStream_t s) {                                                      \
+    return x_type == 0 ? launch_mk<T, float>((const float *)x, ldx, tiles, n, k, y, ldy, m, work, \
+                                             work_floats, s)                                     \
+                       : launch_mk<T, half_t>((const half_t *)x, ldx, tiles, n, k, y, ldy, m,    \
+                                              work, work_floats, s);                             \
+  }                                                                                              \
+  int64_t decode_work_##NAME(int x_type, int n, int k, int m) {                                  \
+    const size_t b = x_type == 0 ? mk_work_bytes<T, float>(m, n, k) : mk_work_bytes<T, half_t>(m, n, k); \
+    return (int64_t)((b + 3) / 4);                                                               \
+  }                                                                                              \
+  hipError_t decode_fused_##NAME(const float *, const uint8_t *, int, int, float *, int,         \
+                                 const float *, float, int, hipStream_t) {                       \
+    return hipErrorNotSupported;                                                                 \
+  }                                                                                              \
+  hipError_t decode_merge_##NAME(const AttnRecords &, const uint8_t *, int, float *, int,        \
+                                 hipStream_t) {                                                  \
+    return hipErrorNotSupported;                                                                 \
   }
 
 }  // namespace gguf

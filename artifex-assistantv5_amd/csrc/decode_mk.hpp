@@ -61,15 +61,33 @@ constexpr int mk_f_off() {
 #ifndef GGUF_MK_WIDE_T
 #define GGUF_MK_WIDE_T 1  // row tiles per wave for 3 or 4 activation tiles (16 T tiles per workgroup)
 #endif
-template <int MA>
+// IQ grid types: the shared-memory tables of the B-operand decode, behind the
+// staged range: the grid as f16 (NG entries of W values; IQ1_M as 8 g) and,
+// for the types with sign bits, NS sign masks of 8 f16 sign bits (indexed by
+// the 7-bit ksigns index, KS, or by the raw sign byte).
+template <int TYPE>
+struct IqTab {
+  static constexpr int NG = TYPE == 16 ? 256 : TYPE == 17 ? 512 : TYPE == 22 ? 1024
+                          : TYPE == 18 ? 256 : TYPE == 21 ? 512 : 2048;
+  static constexpr int W = (TYPE == 18 || TYPE == 21) ? 4 : 8;
+  static constexpr int NS = TYPE == 29 ? 0 : (TYPE == 22 || TYPE == 21) ? 256 : 128;
+  static constexpr bool KS = TYPE == 16 || TYPE == 17 || TYPE == 18;
+  static constexpr int GB = NG * W * 2;  // grid bytes (the masks follow)
+};
+template <int TYPE>
+constexpr int mk_tbl_bytes() {
+  if constexpr (is_iq(TYPE)) return IqTab<TYPE>::GB + IqTab<TYPE>::NS * 16;
+  return 0;
+}
+template <int TYPE, int MA>
 constexpr int mk_kw_max() {  // units a workgroup can stage
-  return (GGUF_MK_LDS - 1024) / mk_unit_bytes<MA>();
+  return (GGUF_MK_LDS - 1024 - mk_tbl_bytes<TYPE>()) / mk_unit_bytes<MA>();
 }
 
 // Convert one (unit, activation row) into the unit's image block at blk;
 // lane l holds elements 4l .. 4l + 3 in v (zeros for a padding row).  Every
 // lane of the wave takes part.
-template <int PARTS, int MA>
+template <int PARTS, int MA, bool QUAD, bool SUMS>
 __device__ __forceinline__ void mk_stage(const float (&v)[4], int m, int l, uint8_t *blk) {
   float mx = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
   mx = max_xor32(max_xor16(max_lanes16(mx)));
@@ -79,7 +97,7 @@ __device__ __forceinline__ void mk_stage(const float (&v)[4], int m, int l, uint
   float s = 0.f;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    const int pos = (i & 1) << 1 | (i >> 1);  // quad order (0, 2, 1, 3)
+    const int pos = QUAD ? ((i & 1) << 1 | (i >> 1)) : i;  // quad order (0, 2, 1, 3) or natural
     float vi = v[i];
     asm volatile("" : "+v"(vi));  // keep the product out of the f16 conversions (no v_fma_mix)
     const float t = vi * sc;      // exact: a power of two
@@ -96,7 +114,7 @@ __device__ __forceinline__ void mk_stage(const float (&v)[4], int m, int l, uint
   half_t *A = (half_t *)blk + row * kMkLd + 4 * l;
   *(half4_t *)A = h;
   if (PARTS == 2) *(half4_t *)(A + kMkLd) = lo;
-  if ((l & 7) == 0) {
+  if (SUMS && (l & 7) == 0) {
     // group j's sum at K position 4 (j >> 2) + e (hi) and 8 + that (lo), with e
     // the position of j & 3 in the (0, 2, 1, 3) order of the mins operand
     const int j = l >> 3, e = ((j & 1) << 1) | ((j >> 1) & 1), k = 4 * (j >> 2) + e;
@@ -119,7 +137,7 @@ __device__ __forceinline__ void mk_stage(const float (&v)[4], int m, int l, uint
 
 // The activations' image, once per call: one wave per (unit, activation
 // row), four per block; rows M .. ROWS - 1 are written as zeros.
-template <typename XT, int MA>
+template <typename XT, int MA, bool QUAD, bool SUMS>
 __global__ __launch_bounds__(256) void mk_prep_kernel(const XT *__restrict__ x, int64_t ldx, int M,
                                                       uint8_t *__restrict__ img) {
   constexpr int PARTS = sizeof(XT) == 4 ? 2 : 1;
@@ -136,7 +154,7 @@ __global__ __launch_bounds__(256) void mk_prep_kernel(const XT *__restrict__ x, 
       for (int e = 0; e < 4; ++e) v[e] = (float)t[e];
     }
   }
-  mk_stage<PARTS, MA>(v, m, l, img + (size_t)u * mk_unit_bytes<MA>());
+  mk_stage<PARTS, MA, QUAD, SUMS>(v, m, l, img + (size_t)u * mk_unit_bytes<MA>());
 }
 
 // The mins operand of lane group g: m_j for j = 4 (g & 1) + (0, 2, 1, 3).
@@ -257,6 +275,234 @@ __device__ __forceinline__ void mk_unit(const Unit<12> (&w)[T], int bo, int lane
       for (int i = 0; i < 4; ++i) asm volatile("" : "+v"(acc[t][a][i]));
 }
 
+// ---------------------------------------------------------------------------
+// IQ grid types (iq.hpp).  The B operand of sub-block ib for lane group g
+// (elements 8 g .. 8 g + 7, group l = g of the format) is the grid entry's
+// magnitudes with the signs applied (an XOR of f16 sign bits) times the
+// group's odd sub-block factor f (2 ls + 1, 2 s + 1): exact f16 integers
+// (at most 43 x 31, 62 x 31, 15 x 31, 9 x 15).  The unit scale (d / 8, d / 4
+// or d) is applied to the f32 result.
+// ---------------------------------------------------------------------------
+template <int TYPE>
+struct IqUnit {
+  uint32_t w[iq_rd<TYPE>()];  // the row's record (the block without its d)
+  uint32_t d;                 // the f16 d (types that have one)
+};
+template <int TYPE>
+__device__ __forceinline__ void load_iq(__amdgpu_buffer_rsrc_t rs, int soff, int r, IqUnit<TYPE> &u) {
+  constexpr int RD = iq_rd<TYPE>();
+  const int base = iq_rec_off<TYPE>(r);
+#pragma unroll
+  for (int c = 0; c < RD / 4; ++c) {
+    const uint4 v = bload16(rs, base + 16 * c, soff);
+    u.w[4 * c] = v.x; u.w[4 * c + 1] = v.y; u.w[4 * c + 2] = v.z; u.w[4 * c + 3] = v.w;
+  }
+  if constexpr (RD % 4 >= 2) {
+    const uint2 v = bload8(rs, base + 16 * (RD / 4), soff);
+    u.w[RD / 4 * 4] = v.x;
+    u.w[RD / 4 * 4 + 1] = v.y;
+  }
+  if constexpr (RD % 2 == 1) u.w[RD - 1] = bload4(rs, base + 4 * (RD - 1), soff);
+  u.d = IqFmt<TYPE>::HASD ? bload2(rs, 2 * r, soff) : 0u;
+}
+// the type's grid bytes, as 16-byte chunks
+template <int TYPE>
+__device__ __forceinline__ const void *iq_grid() {
+  if constexpr (TYPE == 16) return kIq2xxsGrid;
+  if constexpr (TYPE == 17) return kIq2xsGrid;
+  if constexpr (TYPE == 22) return kIq2sGrid;
+  if constexpr (TYPE == 18) return kIq3xxsGrid;
+  if constexpr (TYPE == 21) return kIq3sGrid;
+  return kIq1sGrid;
+}
+// Table loads (16 grid bytes per chunk, at most CH chunks per thread), requested
+// with the other loads; written to shared memory by iq_put_tables.
+template <int TYPE, int NT>
+struct IqTabRegs {
+  static constexpr int CHUNKS = is_iq(TYPE) ? IqTab<TYPE>::NG * IqTab<TYPE>::W / 16 : 0;
+  static constexpr int CH = (CHUNKS + NT - 1) / NT;
+  uint4 v[CH > 0 ? CH : 1];
+};
+template <int TYPE, int NT>
+__device__ __forceinline__ void iq_get_tables(IqTabRegs<TYPE, NT> &t) {
+  using R = IqTabRegs<TYPE, NT>;
+  const uint4 *src = (const uint4 *)iq_grid<TYPE>();
+#pragma unroll
+  for (int c = 0; c < R::CH; ++c) t.v[c] = src[min((int)threadIdx.x + NT * c, R::CHUNKS - 1)];
+}
+template <int TYPE, int NT>
+__device__ __forceinline__ void iq_put_tables(const IqTabRegs<TYPE, NT> &t, int tbl) {
+  using R = IqTabRegs<TYPE, NT>;
+  using Q = IqTab<TYPE>;
+#pragma unroll
+  for (int c = 0; c < R::CH; ++c) {
+    const int q = (int)threadIdx.x + NT * c;
+    if (q < R::CHUNKS) {
+      const uint32_t b[4] = {t.v[c].x, t.v[c].y, t.v[c].z, t.v[c].w};
+      half8_t h[2];
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const uint32_t byte = (b[i >> 2] >> (8 * (i & 3))) & 0xFFu;
+        h[i >> 3][i & 7] = TYPE == 29 ? (half_t)(8.f * (float)(int8_t)byte) : (half_t)(float)byte;
+      }
+      *(half8_t *)(g_lds + tbl + 32 * q) = h[0];
+      *(half8_t *)(g_lds + tbl + 32 * q + 16) = h[1];
+    }
+  }
+  // sign masks: entry e, bit j of its sign byte (ksigns[e] = e with bit 7 making
+  // the popcount even, or e itself) -> 0x8000 in half j
+  for (int q = threadIdx.x; q < Q::NS; q += NT) {
+    const uint32_t sb = Q::KS ? (uint32_t)q | ((__builtin_popcount(q) & 1u) << 7) : (uint32_t)q;
+    uint32_t m[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) m[i] = (((sb >> (2 * i)) & 1u) << 15) | (((sb >> (2 * i + 1)) & 1u) << 31);
+    *(uint4 *)(g_lds + tbl + Q::GB + 16 * q) = make_uint4(m[0], m[1], m[2], m[3]);
+  }
+}
+
+__device__ __forceinline__ uint32_t iq_byte(uint32_t w, int i) { return (w >> (8 * i)) & 0xFFu; }
+
+// The B operand of sub-block ib for lane group g, and (scale) the f32 factor
+// of the unit.
+template <int TYPE>
+__device__ __forceinline__ half8_t iq_b(const IqUnit<TYPE> &u, int ib, int g, int tbl) {
+  using Q = IqTab<TYPE>;
+  uint32_t idx0, idx1 = 0, sidx = 0, f;
+  half2_t delta = {(half_t)0.f, (half_t)0.f};
+  if constexpr (TYPE == 16) {  // IQ2_XXS: (4 index bytes, u32 7-bit sign indices | ls << 28)
+    const uint32_t aux1 = u.w[2 * ib + 1];
+    idx0 = iq_byte(u.w[2 * ib], g);
+    sidx = (aux1 >> (7 * g)) & 127u;
+    f = 2u * (aux1 >> 28) + 1u;
+  } else if constexpr (TYPE == 17) {  // IQ2_XS: u16 (9-bit index | 7-bit sign index); scales
+    const uint32_t q = (((g & 2) ? u.w[2 * ib + 1] : u.w[2 * ib]) >> (16 * (g & 1))) & 0xFFFFu;
+    const uint32_t sc = iq_byte(u.w[16 + (ib >> 2)], ib & 3);
+    idx0 = q & 511u;
+    sidx = q >> 9;
+    f = 2u * (g < 2 ? sc & 15u : sc >> 4) + 1u;
+  } else if constexpr (TYPE == 22) {  // IQ2_S: qs[32] | signs[32] | qh[8] | scales[8]
+    const uint32_t qh = iq_byte(u.w[16 + (ib >> 2)], ib & 3), sc = iq_byte(u.w[18 + (ib >> 2)], ib & 3);
+    idx0 = iq_byte(u.w[ib], g) | ((qh << (8 - 2 * g)) & 0x300u);
+    sidx = iq_byte(u.w[8 + ib], g);
+    f = 2u * (g < 2 ? sc & 15u : sc >> 4) + 1u;
+  } else if constexpr (TYPE == 18) {  // IQ3_XXS: qs[64] | u32 (7-bit sign indices | ls << 28)
+    const uint32_t q = ((g & 2) ? u.w[2 * ib + 1] : u.w[2 * ib]) >> (16 * (g & 1)), aux = u.w[16 + ib];
+    idx0 = q & 0xFFu;
+    idx1 = (q >> 8) & 0xFFu;
+    sidx = (aux >> (7 * g)) & 127u;
+    f = 2u * (aux >> 28) + 1u;
+  } else if constexpr (TYPE == 21) {  // IQ3_S: qs[64] | qh[8] | signs[32] | scales[4]
+    const uint32_t q = ((g & 2) ? u.w[2 * ib + 1] : u.w[2 * ib]) >> (16 * (g & 1));
+    const uint32_t qh = iq_byte(u.w[16 + (ib >> 2)], ib & 3), sc = iq_byte(u.w[26], ib >> 1);
+    idx0 = (q & 0xFFu) | ((qh << (8 - 2 * g)) & 256u);
+    idx1 = ((q >> 8) & 0xFFu) | ((qh << (7 - 2 * g)) & 256u);
+    sidx = iq_byte(u.w[18 + ib], g);
+    f = 2u * ((ib & 1) ? sc >> 4 : sc & 15u) + 1u;
+  } else {  // IQ1_M: qs[32] | qh[16] | scales[4] u16
+    const uint32_t qh = iq_byte(u.w[8 + (ib >> 1)], 2 * (ib & 1) + (g >> 1));
+    const uint32_t wk = (u.w[12 + (ib >> 2)] >> (16 * ((ib >> 1) & 1))) & 0xFFFFu;
+    const int sh = 6 * (ib & 1) + (g < 2 ? 0 : 3);
+    idx0 = iq_byte(u.w[ib], g) | ((qh << ((g & 1) ? 4 : 8)) & 0x700u);
+    f = 2u * ((wk >> sh) & 7u) + 1u;
+    const half_t dl = (qh & ((g & 1) ? 0x80u : 0x08u)) ? (half_t)-1.f : (half_t)1.f;  // 8 x (+-1/8)
+    delta = {dl, dl};
+  }
+  const half_t fh = (half_t)(float)f;
+  const half2_t fp = {fh, fh};
+  uint32_t v[4];
+  if constexpr (Q::W == 8) {
+    const uint4 gr = *(const uint4 *)(g_lds + tbl + 16 * idx0);
+    v[0] = gr.x; v[1] = gr.y; v[2] = gr.z; v[3] = gr.w;
+  } else {
+    const uint2 g1 = *(const uint2 *)(g_lds + tbl + 8 * idx0), g2 = *(const uint2 *)(g_lds + tbl + 8 * idx1);
+    v[0] = g1.x; v[1] = g1.y; v[2] = g2.x; v[3] = g2.y;
+  }
+  if constexpr (Q::NS > 0) {
+    const uint4 m = *(const uint4 *)(g_lds + tbl + Q::GB + 16 * sidx);
+    v[0] ^= m.x; v[1] ^= m.y; v[2] ^= m.z; v[3] ^= m.w;
+  }
+  half8_t b;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const half2_t h = __builtin_bit_cast(half2_t, v[i]);
+    const half2_t r = TYPE == 29 ? __builtin_elementwise_fma(h, fp, delta * fp) : h * fp;
+    b[2 * i] = r[0];
+    b[2 * i + 1] = r[1];
+  }
+  return b;
+}
+template <int TYPE>
+__device__ __forceinline__ float iq_unit_scale(const IqUnit<TYPE> &u) {
+  if constexpr (TYPE == 29) {
+    const uint32_t s01 = u.w[12], s23 = u.w[13];
+    const uint32_t bits = ((s01 >> 12) & 0x000Fu) | ((s01 >> 24) & 0x00F0u) | ((s23 >> 4) & 0x0F00u) |
+                          ((s23 >> 16) & 0xF000u);
+    return h2f(bits) * 0.125f;
+  }
+  return h2f(u.d) * (TYPE == 18 ? 0.25f : TYPE == 21 ? 1.f : 0.125f);
+}
+
+template <int TYPE, int MA, int T>
+__device__ __forceinline__ void mk_unit_iq(const IqUnit<TYPE> (&w)[T], int bo, int lane, bool valid,
+                                           int tbl, float (&acc)[T][MA][4]) {
+#pragma clang fp contract(off)
+  const int r = lane & 15, g = lane >> 4;
+  float4_t D[T][MA];
+#pragma unroll
+  for (int t = 0; t < T; ++t)
+#pragma unroll
+    for (int a = 0; a < MA; ++a) D[t][a] = (float4_t){0.f, 0.f, 0.f, 0.f};
+  const int arow = bo + r * (kMkLd * 2) + 16 * g;  // byte offset of the lane's A fragment
+#pragma unroll
+  for (int ib = 0; ib < 8; ++ib) {
+    half8_t A[MA];
+#pragma unroll
+    for (int a = 0; a < MA; ++a) A[a] = lds_h8b(arow + a * 16 * (kMkLd * 2) + 64 * ib);
+#pragma unroll
+    for (int t = 0; t < T; ++t) {
+      const half8_t B = iq_b<TYPE>(w[t], ib, g, tbl);
+#pragma unroll
+      for (int a = 0; a < MA; ++a) D[t][a] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[a], B, D[t][a], 0, 0, 0);
+    }
+    if constexpr (MA * T >= 4) __builtin_amdgcn_sched_barrier(0);
+  }
+#pragma unroll
+  for (int a = 0; a < MA; ++a) {
+    const float4 F = *(const float4 *)(g_lds + bo + mk_f_off<MA>() + (16 * a + 4 * g) * 4);
+    const float f[4] = {F.x, F.y, F.z, F.w};
+#pragma unroll
+    for (int t = 0; t < T; ++t) {
+      const float us = valid ? iq_unit_scale<TYPE>(w[t]) : 0.f;  // a slot past the units adds zero
+#pragma unroll
+      for (int i = 0; i < 4; ++i) acc[t][a][i] = fmaf(f[i], us * D[t][a][i], acc[t][a][i]);
+    }
+  }
+#pragma unroll
+  for (int t = 0; t < T; ++t)
+#pragma unroll
+    for (int a = 0; a < MA; ++a)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) asm volatile("" : "+v"(acc[t][a][i]));
+}
+
+// The per-lane weight unit of a type and its load.
+template <int TYPE, bool IQ = is_iq(TYPE)>
+struct MkW {
+  using U = Unit<TYPE>;
+};
+template <int TYPE>
+struct MkW<TYPE, true> {
+  using U = IqUnit<TYPE>;
+};
+template <int TYPE>
+__device__ __forceinline__ void mk_load(__amdgpu_buffer_rsrc_t rs, int soff, int r, int g,
+                                        typename MkW<TYPE>::U &u) {
+  if constexpr (is_iq(TYPE))
+    load_iq<TYPE>(rs, soff, r, u);
+  else
+    load_unit(rs, soff, r, g, u);
+}
+
 // Workgroup (blockIdx.x, blockIdx.y) of TS x KL waves: row tiles
 // TS T blockIdx.x .. + TS T - 1 (T per wave; wave w takes tile slot w % TS and
 // K-lane w / TS), units blockIdx.y kw .. + kw - 1 of K, of which K-lane kl
@@ -267,15 +513,16 @@ __device__ __forceinline__ void mk_unit(const Unit<12> (&w)[T], int bo, int lane
 // memory as it lands (the weights still in flight); after the one barrier
 // each wave consumes its units in order as they arrive.  The K-lanes of a
 // tile slot are added in a fixed order through shared memory.
-template <typename XT, int MA, int T, int TS, int KL>
+template <int TYPE, typename XT, int MA, int T, int TS, int KL>
 __global__ __launch_bounds__(64 * TS * KL) void mk_kernel(const uint8_t *__restrict__ img,
                                                           const uint8_t *__restrict__ W, int N,
                                                           int K, int M, int kw,
                                                           float *__restrict__ out, int64_t ldo) {
   constexpr int PARTS = sizeof(XT) == 4 ? 2 : 1, NW = TS * KL;
-  constexpr int UB = mk_unit_bytes<MA>(), TU = Fmt<12>::TU;
-  constexpr int CP = (mk_kw_max<MA>() * UB / 16 + 64 * NW - 1) / (64 * NW);  // 16 B pieces per thread
-  constexpr int U = (mk_kw_max<MA>() + KL - 1) / KL;                          // unit slots per wave
+  constexpr int UB = mk_unit_bytes<MA>(), TU = Fmt<TYPE>::TU;
+  constexpr int CP = (mk_kw_max<TYPE, MA>() * UB / 16 + 64 * NW - 1) / (64 * NW);  // 16 B pieces per thread
+  constexpr int U = (mk_kw_max<TYPE, MA>() + KL - 1) / KL;                          // unit slots per wave
+  constexpr bool IQ = is_iq(TYPE);
   // slots in flight per tile: a few MB over the chip keep the transfer at full
   // rate and the arrivals in order (all at once, they land in no useful order
   // and the decode runs after the transfer instead of under it)
@@ -290,6 +537,7 @@ __global__ __launch_bounds__(64 * TS * KL) void mk_kernel(const uint8_t *__restr
   const int cnt = (nun - kl + KL - 1) / KL;  // the wave's units: kl + KL i, i < cnt
   const int tb = nu * TU;
   const int nq = nun * (UB / 16);  // 16-byte pieces of the range's image
+  const int tbl = (kw * UB + 1023) & ~1023;  // IQ types: the decode tables, behind the range
 
   // the range's image.  Narrow tiles (MA <= 2): through registers, requested
   // ahead of the weights and written as it lands (pieces past the range repeat
@@ -300,12 +548,15 @@ __global__ __launch_bounds__(64 * TS * KL) void mk_kernel(const uint8_t *__restr
   typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));  // a value type: no memcpy copies
   const uint8_t *src = img + (size_t)u0 * UB;
   u32x4 R[DMA ? 1 : CP];
+  IqTabRegs<TYPE, 64 * NW> tab;
+  if constexpr (IQ) iq_get_tables<TYPE, 64 * NW>(tab);
   if constexpr (DMA) {
     const int kb = (nun * UB + 1023) >> 10;
     for (int i = wave; i < kb; i += NW)
       __builtin_amdgcn_global_load_lds((const void *)(src + 1024 * i + 16 * lane),
                                        (__attribute__((address_space(3))) void *)(g_lds + 1024 * i),
                                        16, 0, 0);
+    if constexpr (IQ) iq_put_tables<TYPE, 64 * NW>(tab, tbl);
     __syncthreads();
   } else {
 #pragma unroll
@@ -323,17 +574,18 @@ __global__ __launch_bounds__(64 * TS * KL) void mk_kernel(const uint8_t *__restr
   // a loop the memory-counter waits lose track of the requests and wait for
   // all of them at every unit.
   const int ulast = cnt > 0 ? kl + KL * (cnt - 1) : 0;  // a unit of the range
-  Unit<12> wb[P][T];
+  typename MkW<TYPE>::U wb[P][T];
 #pragma unroll
   for (int i = 0; i < P; ++i)
 #pragma unroll
-    for (int t = 0; t < T; ++t) load_unit(rs[t], (u0 + min(kl + KL * i, ulast)) * TU, r, g, wb[i][t]);
+    for (int t = 0; t < T; ++t) mk_load<TYPE>(rs[t], (u0 + min(kl + KL * i, ulast)) * TU, r, g, wb[i][t]);
   if constexpr (!DMA) {
 #pragma unroll
     for (int c = 0; c < CP; ++c) {
       const int q = (int)threadIdx.x + 64 * NW * c;
       if (q < nq) *(u32x4 *)(g_lds + 16 * q) = R[c];
     }
+    if constexpr (IQ) iq_put_tables<TYPE, 64 * NW>(tab, tbl);
     __syncthreads();
   }
   float acc[T][MA][4];
@@ -345,11 +597,14 @@ __global__ __launch_bounds__(64 * TS * KL) void mk_kernel(const uint8_t *__restr
       for (int i = 0; i < 4; ++i) acc[t][a][i] = 0.f;
 #pragma unroll
   for (int i = 0; i < U; ++i) {
-    mk_unit<MA, T>(wb[i % P], min(kl + KL * i, ulast) * UB, lane, i < cnt, acc);
+    if constexpr (IQ)
+      mk_unit_iq<TYPE, MA, T>(wb[i % P], min(kl + KL * i, ulast) * UB, lane, i < cnt, tbl, acc);
+    else
+      mk_unit<MA, T>(wb[i % P], min(kl + KL * i, ulast) * UB, lane, i < cnt, acc);
     if (i + P < U)  // compile-time
 #pragma unroll
       for (int t = 0; t < T; ++t)
-        load_unit(rs[t], (u0 + min(kl + KL * (i + P), ulast)) * TU, r, g, wb[i % P][t]);
+        mk_load<TYPE>(rs[t], (u0 + min(kl + KL * (i + P), ulast)) * TU, r, g, wb[i % P][t]);
   }
   if constexpr (KL > 1) {  // K-lanes 1 .. KL - 1 hand their sums to lane 0, added in order
     __syncthreads();  // the staged activations are consumed
@@ -398,9 +653,9 @@ __global__ __launch_bounds__(64 * TS * KL) void mk_kernel(const uint8_t *__restr
 }
 
 // y[m, n] = sum over the S ranges of part[s][m][n] (row stride np), in
-// order.  One output element per thread; the S partials are requested at
-// once (up to kMkMaxRanges), then added.
-constexpr int kMkMaxRanges = 32;
+// order.  One output element per thread; the partials are requested
+// kMkBatch at a time, then added.
+constexpr int kMkBatch = 32;
 __global__ __launch_bounds__(256) void mk_reduce_kernel(const float *__restrict__ part, int S, int M,
                                                         int np, int N, float *__restrict__ y,
                                                         int64_t ldy) {
@@ -408,13 +663,15 @@ __global__ __launch_bounds__(256) void mk_reduce_kernel(const float *__restrict_
   if (n >= N) return;
   const float *p = part + (int64_t)m * np + n;
   const int64_t st = (int64_t)M * np;
-  float v[kMkMaxRanges];
+  float a = p[0];
+  for (int s0 = 0; s0 < S; s0 += kMkBatch) {
+    float v[kMkBatch];
 #pragma unroll
-  for (int s = 0; s < kMkMaxRanges; ++s) v[s] = s < S ? p[s * st] : 0.f;
-  float a = v[0];
+    for (int s = 0; s < kMkBatch; ++s) v[s] = s0 + s < S ? p[(s0 + s) * st] : 0.f;
 #pragma unroll
-  for (int s = 1; s < kMkMaxRanges; ++s)
-    if (s < S) a += v[s];
+    for (int s = 0; s < kMkBatch; ++s)
+      if (s0 + s > 0 && s0 + s < S) a += v[s];
+  }
   y[(int64_t)m * ldy + n] = a;
 }
 
@@ -426,7 +683,7 @@ struct MkPlan {
   int ma, ts, kl, t, groups, kw, ranges;
   size_t lds, part_off, bytes;  // workspace: the image, then the ranges' partial sums
 };
-template <typename XT>
+template <int TYPE, typename XT>
 MkPlan mk_plan(int M, int N, int K) {
   constexpr int PARTS = sizeof(XT) == 4 ? 2 : 1;
   MkPlan p;
@@ -437,8 +694,8 @@ MkPlan mk_plan(int M, int N, int K) {
   p.t = wide ? GGUF_MK_WIDE_T : 1;
   const size_t ub = p.ma == 1 ? mk_unit_bytes<1>() : p.ma == 2 ? mk_unit_bytes<2>()
                   : p.ma == 3 ? mk_unit_bytes<3>() : mk_unit_bytes<4>();
-  const int kw_max = p.ma == 1 ? mk_kw_max<1>() : p.ma == 2 ? mk_kw_max<2>()
-                   : p.ma == 3 ? mk_kw_max<3>() : mk_kw_max<4>();
+  const int kw_max = p.ma == 1 ? mk_kw_max<TYPE, 1>() : p.ma == 2 ? mk_kw_max<TYPE, 2>()
+                   : p.ma == 3 ? mk_kw_max<TYPE, 3>() : mk_kw_max<TYPE, 4>();
   const int ntiles = (N + 15) / 16, nu = K / 256;
   p.groups = (ntiles + p.ts * p.t - 1) / (p.ts * p.t);
   int ranges = (nu + kw_max - 1) / kw_max;
@@ -447,24 +704,25 @@ MkPlan mk_plan(int M, int N, int K) {
   p.ranges = (nu + p.kw - 1) / p.kw;
   const size_t stage = ((size_t)p.kw * ub + 1023) & ~(size_t)1023;
   const size_t red = (size_t)(p.kl - 1) * p.ts * p.t * p.ma * 4 * 64 * 4;
-  p.lds = stage > red ? stage : red;
+  const size_t used = stage + mk_tbl_bytes<TYPE>();  // the tables sit behind the range
+  p.lds = used > red ? used : red;
   p.part_off = ((size_t)nu * ub + 1024 + 255) & ~(size_t)255;  // 1 KB slack for 1 KB copy pieces
   p.bytes = p.part_off + (p.ranges > 1 ? (size_t)p.ranges * M * ntiles * 16 * 4 : 0);
   return p;
 }
 
-template <typename XT, int MA, int T, int TS, int KL>
+template <int TYPE, typename XT, int MA, int T, int TS, int KL>
 hipError_t launch_mk_ma(const XT *x, int64_t ldx, const uint8_t *W, int N, int K, float *y,
                         int64_t ldy, int M, float *work, const MkPlan &p, hipStream_t s) {
   constexpr int PARTS = sizeof(XT) == 4 ? 2 : 1;
   const int np = (N + 15) / 16 * 16;
   uint8_t *img = (uint8_t *)work;
   float *part = (float *)(img + p.part_off);
-  hipLaunchKernelGGL((mk_prep_kernel<XT, MA>), dim3((unsigned)(K / 256), (unsigned)(16 * MA / PARTS / 4)),
+  hipLaunchKernelGGL((mk_prep_kernel<XT, MA, TYPE == 12, TYPE == 12>), dim3((unsigned)(K / 256), (unsigned)(16 * MA / PARTS / 4)),
                      dim3(256), 0, s, x, ldx, M, img);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  auto kern = mk_kernel<XT, MA, T, TS, KL>;
+  auto kern = mk_kernel<TYPE, XT, MA, T, TS, KL>;
   if (p.lds > 65536) {
     e = hipFuncSetAttribute((const void *)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)p.lds);
     if (e != hipSuccess) return e;
@@ -479,24 +737,23 @@ hipError_t launch_mk_ma(const XT *x, int64_t ldx, const uint8_t *W, int N, int K
 }
 
 // Workspace bytes of the batched path for M rows of XT activations.
-template <typename XT>
+template <int TYPE, typename XT>
 size_t mk_work_bytes(int M, int N, int K) {
-  return mk_plan<XT>(M, N, K).bytes;
+  return mk_plan<TYPE, XT>(M, N, K).bytes;
 }
 
 // hipErrorNotSupported (nothing launched) when the workspace is missing or
-// too small, or K needs more ranges than the reduction takes: the caller then
-// takes the kernel that stages in every workgroup.
-template <typename XT>
+// too small: the caller then takes the kernel that stages in every workgroup.
+template <int TYPE, typename XT>
 hipError_t launch_mk(const XT *x, int64_t ldx, const uint8_t *W, int N, int K, float *y,
                      int64_t ldy, int M, float *work, int64_t work_floats, hipStream_t s) {
-  const MkPlan p = mk_plan<XT>(M, N, K);
-  if (M > 32 || p.ranges > kMkMaxRanges || !work || (size_t)work_floats * 4 < p.bytes)
+  const MkPlan p = mk_plan<TYPE, XT>(M, N, K);
+  if (M > 32 || !work || (size_t)work_floats * 4 < p.bytes)
     return hipErrorNotSupported;
   switch (p.ma) {  // the shapes mk_plan assumes for each MA
-    case 1: return launch_mk_ma<XT, 1, 1, 4, 4>(x, ldx, W, N, K, y, ldy, M, work, p, s);
-    case 2: return launch_mk_ma<XT, 2, 1, 4, 4>(x, ldx, W, N, K, y, ldy, M, work, p, s);
-    case 3: return launch_mk_ma<XT, 3, GGUF_MK_WIDE_T, 16 / GGUF_MK_WIDE_T, 1>(x, ldx, W, N, K, y, ldy, M, work, p, s);
-    default: return launch_mk_ma<XT, 4, GGUF_MK_WIDE_T, 16 / GGUF_MK_WIDE_T, 1>(x, ldx, W, N, K, y, ldy, M, work, p, s);
+    case 1: return launch_mk_ma<TYPE, XT, 1, 1, 4, 4>(x, ldx, W, N, K, y, ldy, M, work, p, s);
+    case 2: return launch_mk_ma<TYPE, XT, 2, 1, 4, 4>(x, ldx, W, N, K, y, ldy, M, work, p, s);
+    case 3: return launch_mk_ma<TYPE, XT, 3, GGUF_MK_WIDE_T, 16 / GGUF_MK_WIDE_T, 1>(x, ldx, W, N, K, y, ldy, M, work, p, s);
+    default: return launch_mk_ma<TYPE, XT, 4, GGUF_MK_WIDE_T, 16 / GGUF_MK_WIDE_T, 1>(x, ldx, W, N, K, y, ldy, M, work, p, s);
   }
 }

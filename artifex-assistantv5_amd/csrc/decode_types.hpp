@@ -26,6 +26,12 @@ GGUF_DECODE_DECLARE(q5_k)
 GGUF_DECODE_DECLARE(q6_k)
 GGUF_DECODE_DECLARE(iq4_nl)
 GGUF_DECODE_DECLARE(iq4_xs)
+GGUF_DECODE_DECLARE(iq2_xxs)
+GGUF_DECODE_DECLARE(iq2_xs)
+GGUF_DECODE_DECLARE(iq2_s)
+GGUF_DECODE_DECLARE(iq3_xxs)
+GGUF_DECODE_DECLARE(iq3_s)
+GGUF_DECODE_DECLARE(iq1_m)
 
 #undef GGUF_DECODE_DECLARE
 

@@ -8,6 +8,7 @@
 // or not) rounds exactly once, as the reference's f64-then-Float32Array does.
 // The row-tile layout itself is described in common.hpp.
 #include "common.hpp"
+#include "iq.hpp"
 
 namespace gguf {
 
@@ -199,13 +200,45 @@ __global__ __launch_bounds__(256) void repack_kernel(const uint8_t *__restrict__
   }
 }
 
+// IQ grid types: one thread per (row, unit); d and the rest of the block to
+// their places in the tile unit (iq.hpp), zeros for the padding rows.
+template <int TYPE>
+__global__ __launch_bounds__(256) void repack_iq_kernel(const uint8_t *__restrict__ raw, int64_t n_rows,
+                                                        int nu, int64_t n_pad,
+                                                        uint8_t *__restrict__ tiles) {
+  constexpr int BS = IqFmt<TYPE>::BS, HASD = IqFmt<TYPE>::HASD;
+  const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (gid >= n_pad * nu) return;
+  const int64_t n = gid / nu;
+  const int u = (int)(gid - n * nu);
+  const int r = (int)(n & 15);
+  uint8_t *tu = tiles + ((n >> 4) * nu + u) * (int64_t)Fmt<TYPE>::TU;
+  const bool pad = n >= n_rows;
+  const uint8_t *src = raw + (n * nu + u) * BS;
+  if (HASD) *(uint16_t *)(tu + 2 * r) = pad ? 0 : (uint16_t)ld_u16_bytes(src);
+  uint32_t *rec = (uint32_t *)(tu + iq_rec_off<TYPE>(r));
+  for (int i = 0; i < iq_rd<TYPE>(); ++i) rec[i] = pad ? 0u : ld_u32_bytes(src + 2 * HASD + 4 * i);
+}
+
 hipError_t launch_repack(const uint8_t *raw, int type, int64_t n_rows, int64_t k, uint8_t *tiles,
                          hipStream_t s) {
   const int nu = (int)(k / unit_elems(type));
   const int64_t n_pad = (n_rows + 15) & ~(int64_t)15;
   const int64_t total = n_pad * nu;
   const dim3 grid((unsigned)((total + 255) / 256)), block(256);
-  if (type == 12)
+  if (type == 16)
+    hipLaunchKernelGGL(repack_iq_kernel<16>, grid, block, 0, s, raw, n_rows, nu, n_pad, tiles);
+  else if (type == 17)
+    hipLaunchKernelGGL(repack_iq_kernel<17>, grid, block, 0, s, raw, n_rows, nu, n_pad, tiles);
+  else if (type == 18)
+    hipLaunchKernelGGL(repack_iq_kernel<18>, grid, block, 0, s, raw, n_rows, nu, n_pad, tiles);
+  else if (type == 21)
+    hipLaunchKernelGGL(repack_iq_kernel<21>, grid, block, 0, s, raw, n_rows, nu, n_pad, tiles);
+  else if (type == 22)
+    hipLaunchKernelGGL(repack_iq_kernel<22>, grid, block, 0, s, raw, n_rows, nu, n_pad, tiles);
+  else if (type == 29)
+    hipLaunchKernelGGL(repack_iq_kernel<29>, grid, block, 0, s, raw, n_rows, nu, n_pad, tiles);
+  else if (type == 12)
     hipLaunchKernelGGL(repack_kernel<12>, grid, block, 0, s, raw, n_rows, nu, n_pad, tiles);
   else if (type == 13)
     hipLaunchKernelGGL(repack_kernel<13>, grid, block, 0, s, raw, n_rows, nu, n_pad, tiles);
@@ -510,15 +543,44 @@ __global__ __launch_bounds__(256) void dequant_iq4_xs_kernel(const uint8_t *__re
   }
 }
 
+// IQ grid types: one thread per (row, unit, sub-block ib).
+template <int TYPE>
+__global__ __launch_bounds__(256) void dequant_iq_kernel(const uint8_t *__restrict__ tiles,
+                                                         int64_t n_rows, int nu,
+                                                         float *__restrict__ out, int64_t ldo) {
+  const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (gid >= n_rows * nu * 8) return;
+  const int ib = (int)(gid & 7);
+  const int64_t nuid = gid >> 3;
+  const int64_t n = nuid / nu;
+  const int u = (int)(nuid - n * nu);
+  const int r = (int)(n & 15);
+  const uint8_t *tu = tiles + ((n >> 4) * nu + u) * (int64_t)Fmt<TYPE>::TU;
+  iq_piece<TYPE>([&](int o) { return iq_tile_byte<TYPE>(tu, r, o); }, ib,
+                 out + n * ldo + 256 * (int64_t)u + 32 * ib);
+}
+
 hipError_t launch_dequant(const uint8_t *tiles, int type, int64_t n_rows, int64_t k, float *out,
                           int64_t ldo, hipStream_t s) {
   const int nu = (int)(k / unit_elems(type));
   const int parts = (type == 12 || type == 13) ? 4
                     : (type == 14 || type == 10 || type == 11) ? 2
-                    : (type == 23 ? 8 : 1);
+                    : (type == 23 || is_iq(type) ? 8 : 1);
   const int64_t total = n_rows * nu * parts;
   const dim3 grid((unsigned)((total + 255) / 256)), block(256);
-  if (type == 12)
+  if (type == 16)
+    hipLaunchKernelGGL(dequant_iq_kernel<16>, grid, block, 0, s, tiles, n_rows, nu, out, ldo);
+  else if (type == 17)
+    hipLaunchKernelGGL(dequant_iq_kernel<17>, grid, block, 0, s, tiles, n_rows, nu, out, ldo);
+  else if (type == 18)
+    hipLaunchKernelGGL(dequant_iq_kernel<18>, grid, block, 0, s, tiles, n_rows, nu, out, ldo);
+  else if (type == 21)
+    hipLaunchKernelGGL(dequant_iq_kernel<21>, grid, block, 0, s, tiles, n_rows, nu, out, ldo);
+  else if (type == 22)
+    hipLaunchKernelGGL(dequant_iq_kernel<22>, grid, block, 0, s, tiles, n_rows, nu, out, ldo);
+  else if (type == 29)
+    hipLaunchKernelGGL(dequant_iq_kernel<29>, grid, block, 0, s, tiles, n_rows, nu, out, ldo);
+  else if (type == 12)
     hipLaunchKernelGGL(dequant_q4_k_kernel<12>, grid, block, 0, s, tiles, n_rows, nu, out, ldo);
   else if (type == 13)
     hipLaunchKernelGGL(dequant_q4_k_kernel<13>, grid, block, 0, s, tiles, n_rows, nu, out, ldo);
@@ -703,6 +765,26 @@ struct RawPiece<14> {
   __device__ static void run(const uint8_t *unit, int p, float *o) { raw_piece_q6_k(unit, p, o); }
 };
 
+template <int TYPE>
+struct RawPieceIq {
+  static constexpr int PER_UNIT = 8, VALUES = 32;
+  __device__ static void run(const uint8_t *unit, int p, float *o) {
+    iq_piece<TYPE>([&](int off) { return (uint32_t)unit[off]; }, p, o);
+  }
+};
+template <>
+struct RawPiece<16> : RawPieceIq<16> {};
+template <>
+struct RawPiece<17> : RawPieceIq<17> {};
+template <>
+struct RawPiece<18> : RawPieceIq<18> {};
+template <>
+struct RawPiece<21> : RawPieceIq<21> {};
+template <>
+struct RawPiece<22> : RawPieceIq<22> {};
+template <>
+struct RawPiece<29> : RawPieceIq<29> {};
+
 // Contiguous raw bytes: one thread per piece of the whole buffer.
 template <int TYPE>
 __global__ __launch_bounds__(256) void dequant_raw_kernel(const uint8_t *__restrict__ raw,
@@ -748,7 +830,19 @@ static void dequant_raw_type(const uint8_t *raw, int64_t n_elems, float *out, hi
 
 hipError_t launch_dequant_raw(const uint8_t *raw, int type, int64_t n_elems, float *out,
                               hipStream_t s) {
-  if (type == 8)
+  if (type == 16)
+    dequant_raw_type<16>(raw, n_elems, out, s);
+  else if (type == 17)
+    dequant_raw_type<17>(raw, n_elems, out, s);
+  else if (type == 18)
+    dequant_raw_type<18>(raw, n_elems, out, s);
+  else if (type == 21)
+    dequant_raw_type<21>(raw, n_elems, out, s);
+  else if (type == 22)
+    dequant_raw_type<22>(raw, n_elems, out, s);
+  else if (type == 29)
+    dequant_raw_type<29>(raw, n_elems, out, s);
+  else if (type == 8)
     dequant_raw_type<8>(raw, n_elems, out, s);
   else if (type == 2)
     dequant_raw_type<2>(raw, n_elems, out, s);
@@ -783,7 +877,19 @@ static void get_rows_type(const uint8_t *raw, int64_t n_rows, int64_t k, const i
 hipError_t launch_get_rows(const uint8_t *raw, int type, int64_t n_rows, int64_t k,
                            const int64_t *ids, int64_t n_ids, float *out, int64_t ldo,
                            hipStream_t s) {
-  if (type == 8)
+  if (type == 16)
+    get_rows_type<16>(raw, n_rows, k, ids, n_ids, out, ldo, s);
+  else if (type == 17)
+    get_rows_type<17>(raw, n_rows, k, ids, n_ids, out, ldo, s);
+  else if (type == 18)
+    get_rows_type<18>(raw, n_rows, k, ids, n_ids, out, ldo, s);
+  else if (type == 21)
+    get_rows_type<21>(raw, n_rows, k, ids, n_ids, out, ldo, s);
+  else if (type == 22)
+    get_rows_type<22>(raw, n_rows, k, ids, n_ids, out, ldo, s);
+  else if (type == 29)
+    get_rows_type<29>(raw, n_rows, k, ids, n_ids, out, ldo, s);
+  else if (type == 8)
     get_rows_type<8>(raw, n_rows, k, ids, n_ids, out, ldo, s);
   else if (type == 2)
     get_rows_type<2>(raw, n_rows, k, ids, n_ids, out, ldo, s);

@@ -38,7 +38,7 @@ import numpy as np
 import torch
 
 from . import glue, quantize
-from .ggml import Q4_K, Q6_K, raw_row_bytes
+from .ggml import FUSED_TYPES, Q4_K, Q6_K, raw_row_bytes
 from .linear import (GGUFWeight, LayerWeights, QuantEmbedding, concat_rows, dispatch_matmul_gguf,
                      interleave_tiles, repack_gguf_for_gpu, split_interleaved)
 
@@ -99,6 +99,16 @@ class DecoderWeights:
                 total += sum(nb(w) for w in parts(lw, slot))
             total += nb(lw.o_gg) + nb(lw.down_gg)
         return total
+
+
+def all_weights(w: DecoderWeights) -> list:
+    """Every quantized projection of the model, the LM head included."""
+    out = [w.lm_head_gg]
+    for lw in w.layers:
+        for slot in ("qkv", "gateUp"):
+            out += parts(lw, slot)
+        out += [lw.o_gg, lw.down_gg]
+    return out
 
 
 def parts(lw: LayerWeights, slot: str) -> list:
@@ -198,7 +208,11 @@ class QuantDecoder:
 
     def __init__(self, cfg: DecoderConfig, weights: DecoderWeights, device="cuda",
                  fused: bool = True):
-        self.cfg, self.w, self.device, self.fused = cfg, weights, torch.device(device), fused
+        # the grid-codebook IQ types have no fused decode-step kernels: a model
+        # holding one runs its decode steps unfused
+        grid = any(w.ggml_type not in FUSED_TYPES for w in all_weights(weights))
+        self.cfg, self.w, self.device = cfg, weights, torch.device(device)
+        self.fused = fused and not grid
         L, kv, T, hd = cfg.n_layers, cfg.n_kv_heads, cfg.max_seq, cfg.head_dim
         self.k_cache = torch.zeros(L, kv, T, hd, device=self.device)
         self.v_cache = torch.zeros(L, kv, T, hd, device=self.device)

@@ -3,7 +3,8 @@
 Mirrors ``loadGGUFModel`` (``webgpu/src/model/gguf-loader.ts:166-460``):
 
 * quantized matrices of a type the HIP kernels decode (``ggml.KERNEL_TYPES``:
-  Q8_0, Q2_K - Q6_K, Q4_0, Q5_0, IQ4_NL, IQ4_XS) are copied to the device and repacked there into the row-tile layout
+  Q8_0, Q2_K - Q6_K, Q4_0, Q5_0, IQ4_NL, IQ4_XS, IQ2_XXS, IQ2_XS, IQ2_S,
+  IQ3_XXS, IQ3_S, IQ1_M) are copied to the device and repacked there into the row-tile layout
   (``repackGGUFForGPU``, ``gguf-loader.ts:422-424``) -> ``GGUFWeight``;
 * F32 tensors are uploaded as they are; F16 / BF16 tensors become f32 at load
   (``gguf-loader.ts:401-421``);

@@ -26,7 +26,10 @@
  *    granularity (8 bytes for Q8_0 quants; the 4-bit codes of Q4_0 / Q5_0 /
  *    IQ4_NL and of each IQ4_XS sub-block regrouped into one 4-byte word per
  *    lane), so that one wave-wide load of a matrix-core operand reads
- *    contiguous HBM.  The
+ *    contiguous HBM.  The grid-codebook types (IQ2_XXS, IQ2_XS, IQ2_S, IQ3_XXS,
+ *    IQ3_S, IQ1_M; 256-element superblocks) store per tile and superblock the
+ *    16 f16 d fields first (32 bytes), then each row's remaining block bytes
+ *    as they are (IQ1_M, which has no d field: the 16 blocks as they are).  The
  *    byte count is exactly round_up(N, 16) rows of GGUF blocks
  *    (gguf_hip_tile_bytes); the interleave is defined in csrc/common.hpp of
  *    the library.  gguf_hip_repack converts raw GGUF bytes.  Row ranges that
@@ -46,7 +49,7 @@ extern "C" {
  * are exported (kernels and helpers cannot be interposed across libraries). */
 #pragma GCC visibility push(default)
 
-#define GGUF_HIP_ABI_VERSION 13
+#define GGUF_HIP_ABI_VERSION 14
 
 /* ggml type ids (gguf.ts:24-35); activation dtypes reuse F32 / F16. */
 #define GGUF_HIP_F32 0
@@ -61,6 +64,13 @@ extern "C" {
 #define GGUF_HIP_Q6_K 14
 #define GGUF_HIP_IQ4_NL 20
 #define GGUF_HIP_IQ4_XS 23
+/* grid-codebook types: decode variant only, always with a workspace */
+#define GGUF_HIP_IQ2_XXS 16
+#define GGUF_HIP_IQ2_XS 17
+#define GGUF_HIP_IQ3_XXS 18
+#define GGUF_HIP_IQ3_S 21
+#define GGUF_HIP_IQ2_S 22
+#define GGUF_HIP_IQ1_M 29
 
 /* Error codes.  The Python host maps them onto the reference's throws:
  * TYPE -> NotImplementedError ("no pipeline for ggml type", forward-pass.ts:1524;
@@ -164,7 +174,11 @@ int gguf_hip_matmul_variant(const void *x, int x_type, int64_t ldx, const void *
  * results as without a workspace up to f32 rounding of the sums, deterministic
  * either way, and much faster for weights of few rows (the FFN down projection).
  * The reference engine likewise preallocates its scratch (forward-pass.ts:1140-1163).
- * Calls that share a workspace must not overlap. */
+ * Calls that share a workspace must not overlap.
+ * The grid-codebook IQ types run only the decode variant (AUTO picks it for
+ * every M; GEMM returns GGUF_HIP_ERR_TYPE) and need the workspace for every M,
+ * M = 1 included: without one they return GGUF_HIP_ERR_SHAPE, so
+ * gguf_hip_matmul and gguf_hip_matmul_variant reject them. */
 int gguf_hip_matmul_ws(const void *x, int x_type, int64_t ldx, const void *tiles, int ggml_type,
                        int64_t n, int64_t k, float *y, int64_t ldy, int64_t m, int variant,
                        void *work, int64_t work_bytes, void *stream);

@@ -68,10 +68,36 @@ def test_constants_match_header(native):
             d["GGUF_HIP_Q6_K"]) == (8, 12, 13, 14)
     assert (d["GGUF_HIP_Q4_0"], d["GGUF_HIP_Q5_0"], d["GGUF_HIP_IQ4_NL"],
             d["GGUF_HIP_IQ4_XS"]) == (2, 6, 20, 23)
+    assert (d["GGUF_HIP_IQ2_XXS"], d["GGUF_HIP_IQ2_XS"], d["GGUF_HIP_IQ3_XXS"], d["GGUF_HIP_IQ3_S"],
+            d["GGUF_HIP_IQ2_S"], d["GGUF_HIP_IQ1_M"]) == (16, 17, 18, 21, 22, 29)
+
+
+def test_grid_types_contract(lib, native):
+    """IQ2_XXS .. IQ1_M: decode variant only, a workspace for every M, no fused
+    kernels.  Fake (aligned, never dereferenced) pointers: every check fails
+    before any HIP call."""
+    x, w, y = 0x10000, 0x20000, 0x30000
+    for t in (16, 17, 18, 21, 22, 29):
+        for m in (1, 5, 40):
+            for xt in (0, 1):
+                assert lib.gguf_hip_matmul_workspace(t, xt, 64, 512, m) > 0
+        assert lib.gguf_hip_matmul(x, 0, 512, w, t, 64, 512, y, 64, 1, None) == native.ERR_SHAPE
+        assert "needs a workspace" in native.last_error(lib)
+        need = lib.gguf_hip_matmul_workspace(t, 0, 64, 512, 3)
+        assert lib.gguf_hip_matmul_ws(x, 0, 512, w, t, 64, 512, y, 64, 3, 0, 0x40000, need - 16,
+                                      None) == native.ERR_SHAPE
+        assert lib.gguf_hip_matmul_variant(x, 0, 512, w, t, 64, 512, y, 64, 3, 2,
+                                           None) == native.ERR_TYPE
+        assert "no GEMM kernel" in native.last_error(lib)
+        assert lib.gguf_hip_matmul_fused(x, w, t, 64, 512, y, 0, None, ctypes.c_float(0.0), 0,
+                                         None) == native.ERR_SHAPE
+        assert "no fused kernel" in native.last_error(lib)
+    assert (lib.gguf_hip_matmul_workspace(12, 0, 64, 512, 1), lib.gguf_hip_matmul_workspace(
+        20, 0, 64, 512, 1)) == (0, 0)
 
 
 def test_abi_version(lib):
-    assert lib.gguf_hip_abi_version() == 13
+    assert lib.gguf_hip_abi_version() == 14
 
 
 def test_type_traits(lib, native):
@@ -83,7 +109,7 @@ def test_type_traits(lib, native):
 
 
 def test_byte_queries_agree_with_python(lib, pkg):
-    for t in (2, 6, 8, 10, 11, 12, 13, 14, 20, 23):
+    for t in (2, 6, 8, 10, 11, 12, 13, 14, 20, 23, 16, 17, 18, 21, 22, 29):
         for k in (256, 512, 1024, 4096, 14336):
             assert lib.gguf_hip_tile_bytes(t, 7, k) == 16 * pkg.tile_row_bytes(t, k)
             assert lib.gguf_hip_tile_bytes(t, 33, k) == pkg.tiled_bytes(t, 33, k)

@@ -1,0 +1,124 @@
+"""GPU: the grid-codebook IQ types (IQ2_XXS, IQ2_XS, IQ2_S, IQ3_XXS, IQ3_S, IQ1_M).
+
+* repack into the row-tile layout (byte-exact against the numpy tile model),
+  tile dequant, raw dequant and the row gather: bit-exact to the oracle, whose
+  dequant is pinned to the reference's IQ parity fixture
+  (webgpu/tests/fixtures/iq_parity_fixture.json, tests/test_oracle_iq.py);
+* the decode matmul for M = 1 .. 40 (two passes of at most 32 rows above 32),
+  f32 and f16 activations: per element |y - y_ref| <= 2e-5 sum_k |x_k w_nk|
+  against the f64 product of the oracle's dequantized weights (the same
+  f32-grade gate as the other types' decode path);
+* the API contract: no GEMM variant, and a workspace for every M.
+"""
+
+import ctypes
+
+import numpy as np
+import pytest
+import torch
+
+import tile_model
+
+pytestmark = pytest.mark.gpu
+
+GRID = (16, 17, 22, 18, 21, 29)
+NAMES = {16: "IQ2_XXS", 17: "IQ2_XS", 22: "IQ2_S", 18: "IQ3_XXS", 21: "IQ3_S", 29: "IQ1_M"}
+DECODE_TOL = 2e-5
+DECODE, GEMM, AUTO = 1, 2, 0
+
+
+@pytest.fixture(scope="module")
+def native(pkg):
+    from importlib import import_module
+    return import_module("artifex-assistantv5_amd._native")
+
+
+def _weight(pkg, t, n, k, seed):
+    raw = tile_model.random_blocks(t, n, k, seed=seed)
+    return raw, pkg.repack_gguf_for_gpu(t, raw, n, k)
+
+
+@pytest.mark.parametrize("t", GRID)
+@pytest.mark.parametrize("specials", [False, True])
+def test_repack_layout_and_dequant_bit_exact(pkg, ref, t, specials):
+    for i, (n, k) in enumerate([(1, 256), (3, 512), (17, 4096), (2, 14336)]):
+        raw = tile_model.random_blocks(t, n, k, seed=41 * t + i, specials=specials)
+        w = pkg.repack_gguf_for_gpu(t, raw, n, k)
+        assert np.array_equal(w.data.cpu().numpy(), tile_model.to_tiles(t, raw, n, k)), (n, k)
+        want = ref.dequant_rows(t, raw, n, k)
+        assert ref.same_bits(w.dequant().cpu().numpy(), want), (NAMES[t], n, k, "tiles")
+        got = pkg.dequant_raw(t, raw, n * k).cpu().numpy()
+        assert ref.same_bits(got, want.reshape(-1)), (NAMES[t], n, k, "raw")
+
+
+@pytest.mark.parametrize("t", GRID)
+def test_get_rows_bit_exact(pkg, ref, t):
+    n, k = 37, 512
+    raw = tile_model.random_blocks(t, n, k, seed=7 * t)
+    table = pkg.QuantEmbedding(torch.from_numpy(raw).cuda(), t, n, k)
+    ids = torch.tensor([0, 36, 5, 5, 17], dtype=torch.int64, device="cuda")
+    got = table.gather(ids).cpu().numpy()
+    want = ref.dequant_rows(t, raw, n, k)[[0, 36, 5, 5, 17]]
+    assert ref.same_bits(got, want)
+
+
+@pytest.mark.parametrize("t", GRID)
+@pytest.mark.parametrize("xdt", ["f32", "f16"])
+def test_decode_matmul_f32_grade(pkg, ref, t, xdt):
+    shapes = [(1, 1, 256), (1, 300, 1024), (4, 37, 512), (8, 64, 768), (17, 40, 512),
+              (32, 130, 1280), (40, 33, 512), (1, 48, 14336), (32, 16, 14336)]
+    for i, (m, n, k) in enumerate(shapes):
+        raw, w = _weight(pkg, t, n, k, seed=300 * t + i)
+        wdeq = ref.dequant_rows(t, raw, n, k)
+        x = pkg.quantize.synthetic_activations(m, k, seed=800 + i,
+                                               dtype=np.float32 if xdt == "f32" else np.float16)
+        y = pkg.qlinear(torch.from_numpy(x).cuda(), w).cpu().numpy()
+        x64 = x.astype(np.float64)
+        met = ref.parity_metrics(y, ref.matmul_bt(x64, wdeq), ref.matmul_bt_abs(x64, wdeq))
+        assert met["finite"] and met["elemwise"] <= DECODE_TOL, ((NAMES[t], xdt, m, n, k), met)
+
+
+@pytest.mark.parametrize("t", GRID)
+def test_decode_matmul_wide_range_activations(pkg, ref, t):
+    """Activations spanning 2^-60 .. 2^60 across units and rows: every unit is
+    scaled by its own power of two before it enters the matrix cores."""
+    m, n, k = 5, 48, 1024
+    raw, w = _weight(pkg, t, n, k, seed=11 * t)
+    rng = np.random.default_rng(t)
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    x *= np.exp2(rng.integers(-60, 61, size=(m, k // 256, 1))).repeat(256, axis=2).reshape(m, k)
+    y = pkg.qlinear(torch.from_numpy(x).cuda(), w).cpu().numpy()
+    wdeq = ref.dequant_rows(t, raw, n, k)
+    x64 = x.astype(np.float64)
+    met = ref.parity_metrics(y, ref.matmul_bt(x64, wdeq), ref.matmul_bt_abs(x64, wdeq))
+    assert met["finite"] and met["elemwise"] <= DECODE_TOL, (NAMES[t], met)
+
+
+def test_api_contract(pkg, native):
+    lib = native.load_library()
+    t, m, n, k = 16, 3, 32, 512
+    raw, w = _weight(pkg, t, n, k, seed=5)
+    x = torch.from_numpy(pkg.quantize.synthetic_activations(m, k, seed=6)).cuda()
+    y = torch.zeros(m, n, device="cuda")
+    # no GEMM kernel for the grid types
+    rc = lib.gguf_hip_matmul_variant(x.data_ptr(), 0, k, w.ptr(), t, n, k, y.data_ptr(), n, m,
+                                     GEMM, None)
+    assert rc == native.ERR_TYPE and "no GEMM kernel" in native.last_error(lib)
+    # a workspace for every M, M = 1 included
+    for mm in (1, m):
+        need = lib.gguf_hip_matmul_workspace(t, 0, n, k, mm)
+        assert need > 0
+        rc = lib.gguf_hip_matmul(x.data_ptr(), 0, k, w.ptr(), t, n, k, y.data_ptr(), n, mm, None)
+        assert rc == native.ERR_SHAPE and "workspace" in native.last_error(lib)
+        ws = torch.empty(need, dtype=torch.uint8, device="cuda")
+        rc = lib.gguf_hip_matmul_ws(x.data_ptr(), 0, k, w.ptr(), t, n, k, y.data_ptr(), n, mm,
+                                    AUTO, ws.data_ptr(), need - 1, None)
+        assert rc == native.ERR_SHAPE
+        rc = lib.gguf_hip_matmul_ws(x.data_ptr(), 0, k, w.ptr(), t, n, k, y.data_ptr(), n, mm,
+                                    AUTO, ws.data_ptr(), need, None)
+        assert rc == 0, native.last_error(lib)
+    torch.cuda.synchronize()
+    # fused decode-step kernels do not exist for these types
+    rc = lib.gguf_hip_matmul_fused(x.data_ptr(), w.ptr(), t, n, k, y.data_ptr(), 0, None,
+                                   ctypes.c_float(0.0), 0, None)
+    assert rc == native.ERR_SHAPE and "no fused kernel" in native.last_error(lib)

@@ -116,3 +116,33 @@ def test_iq1_m_scale_and_delta():
     want = np.concatenate([d * (2 * sc[l] + 1) * (G["iq1s"][idx[l]].astype(np.float64) + dlt[l])
                            for l in range(4)])
     assert np.array_equal(got, want)
+
+
+def test_device_tables_match_the_grids():
+    """csrc/iq_tables.hpp is what gen_iq_tables.py writes from the grid fixture."""
+    import subprocess
+    import sys
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    gen = os.path.join(root, "artifex-assistantv5_amd", "gen_iq_tables.py")
+    assert subprocess.run([sys.executable, gen, "--check"]).returncode == 0
+
+
+def test_tile_model_layout_round_trip():
+    """The IQ row-tile layout of the numpy model is a byte permutation of the
+    raw rows (d of row r at 2 r, the rest of its block at 32 + r (BS - 2);
+    IQ1_M blocks whole at 56 r) and inverts exactly."""
+    import tile_model
+    for t in (16, 17, 22, 18, 21, 29):
+        raw = tile_model.random_blocks(t, 19, 768, seed=t, specials=True)
+        tiles = tile_model.to_tiles(t, raw, 19, 768)
+        assert tiles.size == tile_model.tiled_bytes(t, 19, 768)
+        assert np.array_equal(tile_model.from_tiles(t, tiles, 19, 768), raw)
+        bs = tile_model.BLOCK[t][1]
+        tu = tiles[:16 * bs]                       # tile 0, superblock 0
+        blk = raw.reshape(19, 3, bs)[:, 0]
+        for r in (0, 7, 15):
+            if t == 29:
+                assert np.array_equal(tu[56 * r:56 * r + 56], blk[r])
+            else:
+                assert np.array_equal(tu[2 * r:2 * r + 2], blk[r, :2])
+                assert np.array_equal(tu[32 + r * (bs - 2):32 + (r + 1) * (bs - 2)], blk[r, 2:])

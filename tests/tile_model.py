@@ -23,12 +23,18 @@ block) a tile stores the 16 rows' GGUF blocks interleaved:
 * IQ4_XS: header (d, scales_h, scales_l) at 8 r, then piece (g, r) at 128 + (16 g + r) 32
   whose word j holds sub-block j's codes 8 g .. 8 g + 7 as Q4_0 (sub-block j's 16 code
   bytes start at byte 8 + 16 j of the GGUF block)
+* IQ2_XXS, IQ2_XS, IQ2_S, IQ3_XXS, IQ3_S (block bytes BS, f16 d first): d at 2 r, then
+  the block's bytes 2 .. BS - 1 at 32 + r (BS - 2)
+* IQ1_M (no d field): row r's block at 56 r
 """
 
 import numpy as np
 
 BLOCK = {8: (32, 34), 12: (256, 144), 13: (256, 176), 14: (256, 210), 2: (32, 18), 6: (32, 22),
-         20: (32, 18), 23: (256, 136), 10: (256, 84), 11: (256, 110)}
+         20: (32, 18), 23: (256, 136), 10: (256, 84), 11: (256, 110),
+         16: (256, 66), 17: (256, 74), 22: (256, 82), 18: (256, 98), 21: (256, 110),
+         29: (256, 56)}
+GRID = (16, 17, 22, 18, 21, 29)
 SMALL = (2, 6, 20, 23)      # nibble codes regrouped per lane (not a byte permutation)
 
 
@@ -51,7 +57,12 @@ def _unit_maps(t):
     block, ub = BLOCK[t]
     pos = np.zeros((16, ub), np.int64)
     for r in range(16):
-        if t in (12, 13):
+        if t == 29:
+            pos[r] = ub * r + np.arange(ub)
+        elif t in GRID:
+            pos[r, 0:2] = 2 * r + np.arange(2)
+            pos[r, 2:] = 32 + r * (ub - 2) + np.arange(ub - 2)
+        elif t in (12, 13):
             qs = 16 if t == 12 else 48
             pos[r, 0:16] = 16 * r + np.arange(16)
             for cp in range(2):
@@ -214,7 +225,7 @@ def random_blocks(t, n, k, seed, specials=False):
     nb = n * (k // block)
     raw = rng.integers(0, 256, (nb, size), dtype=np.uint8)
     offs = {8: [0], 12: [0, 2], 13: [0, 2], 14: [208], 2: [0], 6: [0], 20: [0], 23: [0],
-            10: [80, 82], 11: [108]}[t]
+            10: [80, 82], 11: [108], 16: [0], 17: [0], 22: [0], 18: [0], 21: [0], 29: [None]}[t]
     for o in offs:
         vals = (rng.uniform(-0.01, 0.01, nb) if t not in (12, 13) or o == 0
                 else rng.uniform(0, 0.005, nb))
@@ -226,5 +237,12 @@ def random_blocks(t, n, k, seed, specials=False):
             h = np.where((pick >= 0.06) & (pick < 0.07), np.float16(np.inf), h)
             h = np.where((pick >= 0.07) & (pick < 0.08), np.float16(np.nan), h)
             h = np.where((pick >= 0.08) & (pick < 0.10), np.float16(-3.0e4), h)
-        raw[:, o:o + 2] = h.astype(np.float16).view(np.uint8).reshape(nb, 2)
+        if o is None:  # IQ1_M: the f16 d in the top nibbles of the four scale words
+            dh = h.astype(np.float16).view(np.uint16).astype(np.int64)
+            w = raw[:, 48:56].copy().view("<u2").astype(np.int64)
+            for i in range(4):
+                w[:, i] = (w[:, i] & 0x0FFF) | (((dh >> (4 * i)) & 0xF) << 12)
+            raw[:, 48:56] = w.astype("<u2").view(np.uint8).reshape(nb, 8)
+        else:
+            raw[:, o:o + 2] = h.astype(np.float16).view(np.uint8).reshape(nb, 2)
     return raw.reshape(-1)
