@@ -50,7 +50,8 @@ sys.path.insert(0, ROOT)
 HBM_PEAK_GBS = 8000.0           # MI355X HBM3E, published
 FP16_PEAK_TFLOPS = 2500.0       # MI355X dense fp16 MFMA, published
 BLOCK = {8: (32, 34), 12: (256, 144), 13: (256, 176), 14: (256, 210), 2: (32, 18), 6: (32, 22),
-         20: (32, 18), 23: (256, 136), 10: (256, 84), 11: (256, 110)}
+         20: (32, 18), 23: (256, 136), 10: (256, 84), 11: (256, 110), 16: (256, 66),
+         17: (256, 74), 22: (256, 82), 18: (256, 98), 21: (256, 110), 29: (256, 56)}
 
 
 def parse():
@@ -156,6 +157,30 @@ def make_pool(pkg, t, n, k, copies, seed, quantized=True):
         del rawd
     pool = [base] + [pkg.GGUFWeight(base.data.clone(), t, n, k) for _ in range(copies - 1)]
     return pool, raw
+
+
+IQ_GRID = ((16, "iq2_xxs"), (17, "iq2_xs"), (22, "iq2_s"), (18, "iq3_xxs"), (21, "iq3_s"),
+           (29, "iq1_m"))
+
+
+def iq_pool(pkg, t, n, k, copies, seed):
+    """``copies`` device copies of random IQ blocks (every bit pattern is a legal
+    code) whose f16 d is 2^-8 (IQ1_M: spread over its scale words' top nibbles):
+    the package has no quantizer for the grid types."""
+    import torch
+    block, size = BLOCK[t]
+    rng = np.random.default_rng(seed)
+    raw = rng.integers(0, 256, (n * (k // block), size), dtype=np.uint8)
+    dh = int(np.array([2.0 ** -8], np.float16).view(np.uint16)[0])
+    if t == 29:
+        w = raw[:, 48:56].copy().view("<u2").astype(np.int64)
+        for i in range(4):
+            w[:, i] = (w[:, i] & 0x0FFF) | (((dh >> (4 * i)) & 0xF) << 12)
+        raw[:, 48:56] = w.astype("<u2").view(np.uint8).reshape(-1, 8)
+    else:
+        raw[:, 0], raw[:, 1] = dh & 0xFF, dh >> 8
+    base = pkg.repack_gguf_for_gpu(t, raw.reshape(-1), n, k, device="cuda")
+    return [base] + [pkg.GGUFWeight(base.data.clone(), t, n, k) for _ in range(copies - 1)]
 
 
 def matmul_case(pkg, t, m, n, k, pool, steps, warmup, xdtype="float32", eager=False,
@@ -462,6 +487,13 @@ def secondary_cases(pkg, args, pool, secondary):
                 secondary[f"{name}_gemm_m2048_n14336_frac_fp16_peak"] = round(
                     r["tflops"] / FP16_PEAK_TFLOPS, 4)
             del spool
+    if want("iq"):
+        for tt, name in IQ_GRID:
+            ipool = iq_pool(pkg, tt, 14336, 4096, 24, seed=20 + tt)
+            for mm in (1, 8, 32):
+                r = matmul_case(pkg, tt, mm, 14336, 4096, ipool, 240, 10, replays=3)
+                secondary[f"{name}_decode_m{mm}_gbs"] = round(r["gbs"], 1)
+            del ipool
     if want("q5k"):
         q5pool, _ = make_pool(pkg, 13, 14336, 4096, 14, seed=6)
         r = matmul_case(pkg, 13, 1, 14336, 4096, q5pool, 280, 10, replays=3)
