@@ -1365,7 +1365,7 @@ __global__ __launch_bounds__(512) void decode_m1_kernel(const XT *__restrict__ x
                                                         const uint8_t *__restrict__ W, int N,
                                                         int K, float *__restrict__ y, int ks_n,
                                                         const float *__restrict__ pw, float eps,
-                                                        int epi, AttnRecords ar) {
+                                                        int epi, AttnRecords ar, int rows_wg) {
   constexpr int PARTS = sizeof(XT) == 4 ? 2 : 1;
   constexpr int UE = Fmt<TYPE>::UE, TU = Fmt<TYPE>::TU, GS = Dec<TYPE>::GS;
   const int nthr = blockDim.x;
@@ -1374,8 +1374,24 @@ __global__ __launch_bounds__(512) void decode_m1_kernel(const XT *__restrict__ x
   const int ts_n = (nthr >> 6) / ks_n;
   const int ts = wave / ks_n, ks = wave - ts * ks_n;
   const int ntiles = (N + 15) >> 4;
-  const int tile = blockIdx.x * ts_n + ts;
-  const bool active = tile < ntiles;
+  // rows_wg > 0: the workgroup owns rows [rows_wg b, rows_wg b + rows_wg) (a
+  // multiple of 8, so that every CU gets the same share of a weight whose tiles
+  // do not divide evenly over the grid); tile slot ts is the ts-th tile they
+  // touch, and lanes of rows outside the range load nothing (their offsets are
+  // past the buffer's end, which reads as zero) and store nothing
+  int tile, lo, hi;
+  if (rows_wg > 0) {
+    const int row0 = blockIdx.x * rows_wg;
+    tile = (row0 >> 4) + ts;
+    lo = max(row0, 16 * tile);
+    hi = min(min(row0 + rows_wg, N), 16 * tile + 16);
+  } else {
+    tile = blockIdx.x * ts_n + ts;
+    lo = 16 * tile;
+    hi = min(N, 16 * tile + 16);
+  }
+  const bool active = tile < ntiles && lo < hi;
+  const int rl = (16 * tile + r >= lo && 16 * tile + r < hi) ? r : r + (1 << 20);  // row of the loads
   const int nu = K / UE;
   const int iters = (nu + ks_n - 1) / ks_n;  // <= U
 
@@ -1455,7 +1471,7 @@ __global__ __launch_bounds__(512) void decode_m1_kernel(const XT *__restrict__ x
   for (int j = 0; j < D; ++j) {
     const int u = ks + ks_n * j;
     const int uc = u < nu ? u : nu - 1;
-    load_unit(wrs, uc * TU, r, g, buf[j]);
+    load_unit(wrs, uc * TU, rl, g, buf[j]);
   }
 
   if constexpr (PRO == 1) {  // stage x * w; the row's sum of x^2 rides on the staging barrier
@@ -1535,7 +1551,7 @@ __global__ __launch_bounds__(512) void decode_m1_kernel(const XT *__restrict__ x
       const int un = ks + ks_n * (j + D);
       const int ucn = un < nu ? un : nu - 1;
       __builtin_amdgcn_sched_barrier(0);
-      load_unit(wrs, ucn * TU, r, g, buf[j % D]);
+      load_unit(wrs, ucn * TU, rl, g, buf[j % D]);
       __builtin_amdgcn_sched_barrier(0);
     }
   }
@@ -1568,7 +1584,7 @@ __global__ __launch_bounds__(512) void decode_m1_kernel(const XT *__restrict__ x
     }
     return;
   }
-  if (ks == 0 && active && n < N && g == 0) y[n] = epi == 1 ? y[n] + acc : acc;
+  if (ks == 0 && active && n >= lo && n < hi && g == 0) y[n] = epi == 1 ? y[n] + acc : acc;
 }
 
 // Units per wave a kernel may own (K-quant units stay in registers whole; a
@@ -1582,6 +1598,14 @@ __global__ __launch_bounds__(512) void decode_m1_kernel(const XT *__restrict__ x
 #ifndef GGUF_M1_MIN_WAVES
 #define GGUF_M1_MIN_WAVES 1024  // K split until the grid has this many waves
 #endif
+#ifndef GGUF_M1_FILL
+#define GGUF_M1_FILL 1  // K-quants too: split K while the doubled grid fits one round of waves
+                        // and keeps 4 units per wave (16384 x 4096: 11.7 -> 9.1 us)
+#endif
+#ifndef GGUF_M1_ROWS
+#define GGUF_M1_ROWS 1  // spread rows evenly over the CUs when the tiles do not divide
+#endif
+constexpr int kM1Cus = 256;  // compute units of the MI355X
 #ifndef GGUF_M1_ROUND_WAVES
 #define GGUF_M1_ROUND_WAVES 2048  // waves resident at once (256 CUs x 8)
 #endif
@@ -1626,12 +1650,14 @@ hipError_t launch_m1(const XT *x, const uint8_t *W, int N, int K, float *y, cons
   // K split: units per wave within the budget, and at least ~1024 waves when
   // possible (at most 4 with the SwiGLU epilogue, which needs two tiles per workgroup);
   // 32-element blocks (one MFMA per unit, latency-bound) split further while the
-  // grid stays one round of resident waves (Q8_0 4096 x 4096: 7.5 -> 6.4 us)
+  // grid stays one round of resident waves (Q8_0 4096 x 4096: 7.5 -> 6.4 us), and
+  // so do the K-quants while each wave keeps at least 4 units
   int ks = 1;
   const int ks_max = epi == 2 ? 4 : 8;
   while (ks < ks_max && ks < nu &&
          ((nu + ks - 1) / ks > umax || ntiles * ks < GGUF_M1_MIN_WAVES ||
-          (UE == 32 && 2 * ntiles * ks <= GGUF_M1_ROUND_WAVES)))
+          (UE == 32 && 2 * ntiles * ks <= GGUF_M1_ROUND_WAVES) ||
+          (GGUF_M1_FILL && 2 * ntiles * ks <= GGUF_M1_ROUND_WAVES && nu >= 8 * ks)))
     ks <<= 1;
   const int per = (nu + ks - 1) / ks;
   if (per > umax) return hipErrorNotSupported;
@@ -1646,7 +1672,20 @@ hipError_t launch_m1(const XT *x, const uint8_t *W, int N, int K, float *y, cons
   const size_t lds = (size_t)(K + kXPad) * 2 * PARTS + (size_t)(K / GS + K / UE) * 4 +
                      (size_t)nw * 64 * 4 + kZeroHalves * 2 + (size_t)nthr * 4;
   if (lds > kMaxLds) return hipErrorNotSupported;
-  const dim3 grid((unsigned)((ntiles + ts - 1) / ts)), block(nthr);
+  // Rows per workgroup instead of whole tiles when the tiles leave CUs without
+  // a workgroup (14336 rows: 224 workgroups of 4 tiles on 256 CUs): a
+  // multiple of 8 rows each, so that the bytes per CU are even (the kernel is
+  // bound by the data each CU keeps in flight, not by the chip's bandwidth).
+  unsigned groups = (unsigned)((ntiles + ts - 1) / ts);
+  int rows_wg = 0;
+  if (GGUF_M1_ROWS && epi != 2 && groups < (unsigned)kM1Cus) {
+    const int R = 8 * ((N + 8 * kM1Cus - 1) / (8 * kM1Cus));
+    if ((R + 15) / 16 <= ts) {
+      rows_wg = R;
+      groups = (unsigned)((N + R - 1) / R);
+    }
+  }
+  const dim3 grid(groups), block(nthr);
   const int dp = m1_depth(grid.x * nw, per, Fmt<TYPE>::TU);
   // template U is clamped to the compile-time budget (runtime per <= umax already);
   // above 64 KB of dynamic LDS the kernel's limit is raised first (gfx950: 160 KB)
@@ -1663,7 +1702,7 @@ hipError_t launch_m1(const XT *x, const uint8_t *W, int N, int K, float *y, cons
                                                 (int)lds);                                       \
       if (ea != hipSuccess) return ea;                                                           \
     }                                                                                            \
-    hipLaunchKernelGGL(kern, grid, block, lds, s, x, W, N, K, y, ks, pw, eps, epi, ar);          \
+    hipLaunchKernelGGL(kern, grid, block, lds, s, x, W, N, K, y, ks, pw, eps, epi, ar, rows_wg); \
   } while (0)
 #define GGUF_M1(UU, XX)                                                                          \
   do {                                                                                           \
