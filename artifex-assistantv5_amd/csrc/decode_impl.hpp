@@ -380,6 +380,7 @@ struct Stage {
   int zero;    // half offset of kZeroHalves zeros: the A operand of lanes that contribute nothing
   int ld;      // ce + kXPad
   int ms;      // 16 * MT
+  int tbl;     // byte offset of the IQ decode tables (grid-codebook types)
 };
 
 __device__ __forceinline__ half8_t lds_h8b(int byte_off) {
@@ -398,6 +399,8 @@ __device__ __forceinline__ float lds_f(int float_off) { return ((const float *)g
 __device__ __forceinline__ float4 lds_f4(int float_off) {
   return *(const float4 *)((const float *)g_lds + float_off);
 }
+
+#include "iq_decode.hpp"
 
 // D = (hi + lo parts of A) x B; lanes with on == false read the zero operand.
 template <int PARTS>
@@ -551,6 +554,42 @@ __device__ __forceinline__ void unit_m1(const Unit<13> &u, const Stage &st, int 
                                         float &acc) {
   unit_m1_k<PARTS, 13>(u, st, ul, lane, acc);
 }
+
+// IQ grid types: the B operand of sub-block j is the lane's grid entries with
+// signs and odd factor (exact f16 integers, iq_b); one chain over the 8
+// sub-blocks leaves sub-block j in rows 2j, 2j + 1, and every row takes the
+// same unit scale.
+template <int PARTS, int TYPE>
+__device__ __forceinline__ void unit_m1_iq(const Unit<TYPE> &u, const Stage &st, int ul, int lane,
+                                           float &acc) {
+  const int r = lane & 15, g = lane >> 4;
+  const int jo = r >> 1;
+  const bool live = PARTS == 2 || (r & 1) == 0;
+  const int own = 2 * (st.xh + (r & 1) * (st.xl - st.xh) + 256 * ul + 8 * g);
+  const int zero = 2 * st.zero;
+  half8_t a[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) a[j] = lds_h8b(((live && jo == j) ? own : zero) + 64 * j);
+  float4_t D = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int j = 0; j < 8; ++j)
+    D = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[j], iq_b<TYPE>(u, j, g, st.tbl), D, 0, 0, 0);
+  const float fu = lds_f(st.xf + ul * st.ms);
+  acc += fu * (iq_unit_scale<TYPE>(u) * ((D[0] + D[1]) + (D[2] + D[3])));
+}
+#define GGUF_IQ_M1(T)                                                                        \
+  template <int PARTS>                                                                       \
+  __device__ __forceinline__ void unit_m1(const Unit<T> &u, const Stage &st, int ul, int lane, \
+                                          float &acc) {                                      \
+    unit_m1_iq<PARTS, T>(u, st, ul, lane, acc);                                              \
+  }
+GGUF_IQ_M1(16)
+GGUF_IQ_M1(17)
+GGUF_IQ_M1(18)
+GGUF_IQ_M1(21)
+GGUF_IQ_M1(22)
+GGUF_IQ_M1(29)
+#undef GGUF_IQ_M1
 
 // Q6_K: 16 groups of 16 elements, two chains of 8 (halves hf = 0, 1); lane
 // (n, g) keeps groups 8 hf + 2 g + lh, lh = 0, 1.
@@ -1407,6 +1446,10 @@ __global__ __launch_bounds__(512) void decode_m1_kernel(const XT *__restrict__ x
   float *red = (float *)g_lds + red_off;
   float *ssq = (float *)g_lds + st.zero / 2 + kZeroHalves / 2;  // [threads] partial sums of x^2
   if (threadIdx.x < kZeroHalves / 2) ((uint32_t *)((half_t *)g_lds + st.zero))[threadIdx.x] = 0u;
+  // IQ types: the decode tables behind the rest, requested first, written with the staging
+  st.tbl = (4 * (st.zero / 2 + kZeroHalves / 2 + nthr) + 15) & ~15;
+  IqTabRegs<TYPE, 256> tab;
+  if constexpr (is_iq(TYPE)) iq_get_tables<TYPE, 256>(tab);
 
   // activations first: item q = threadIdx.x + nthr * i of the K / 16 items
   const int per_row = K / kItem;
@@ -1534,6 +1577,7 @@ __global__ __launch_bounds__(512) void decode_m1_kernel(const XT *__restrict__ x
   for (int i = 0; i < XI; ++i)
     store_item<PARTS, GS, UE, Dec<TYPE>::SUMS, Dec<TYPE>::NAT>(per_row, per_row,
                                                                (int)threadIdx.x + nthr * i, xv[i], st);
+  if constexpr (is_iq(TYPE)) iq_put_tables<TYPE, 256>(tab, st.tbl);
   __syncthreads();
   float ssp = 0.f;  // this lane's share of the row's sum of x^2 (reduced after the units)
   if constexpr (PRO == 1)
@@ -1613,7 +1657,7 @@ template <int TYPE>
 constexpr int m1_umax(bool tight) {
   // 32-element blocks: up to 64 per wave (K = 16384 over 8 waves); past 32 at
   // most GGUF_M1_DEEP are in flight (m1_depth), so the register cost stays small
-  return (TYPE == 8 || is_b32(TYPE)) ? 64 : (TYPE == 14 || TYPE == 13 || tight ? 8 : 16);
+  return (TYPE == 8 || is_b32(TYPE)) ? 64 : (TYPE == 14 || TYPE == 13 || is_iq(TYPE) || tight ? 8 : 16);
 }
 
 #ifndef GGUF_M1_DEEP
@@ -1669,16 +1713,18 @@ hipError_t launch_m1(const XT *x, const uint8_t *W, int N, int K, float *y, cons
   const int nthr = 64 * nw, ts = nw / ks;
   if (epi == 2 && (ts < 2 || (ntiles & 1))) return hipErrorNotSupported;
   const int xi = (K / kItem + nthr - 1) / nthr;  // 1 or 2
-  const size_t lds = (size_t)(K + kXPad) * 2 * PARTS + (size_t)(K / GS + K / UE) * 4 +
-                     (size_t)nw * 64 * 4 + kZeroHalves * 2 + (size_t)nthr * 4;
+  size_t lds = (size_t)(K + kXPad) * 2 * PARTS + (size_t)(K / GS + K / UE) * 4 +
+               (size_t)nw * 64 * 4 + kZeroHalves * 2 + (size_t)nthr * 4;
+  if constexpr (is_iq(TYPE)) lds = ((lds + 15) & ~(size_t)15) + iq_tbl_bytes<TYPE>();
   if (lds > kMaxLds) return hipErrorNotSupported;
-  // Rows per workgroup instead of whole tiles when the tiles leave CUs without
-  // a workgroup (14336 rows: 224 workgroups of 4 tiles on 256 CUs): a
-  // multiple of 8 rows each, so that the bytes per CU are even (the kernel is
-  // bound by the data each CU keeps in flight, not by the chip's bandwidth).
+  // Rows per workgroup instead of whole tiles when the tiles leave more than a
+  // fifth of the CUs without a workgroup (6144 or 12288 rows: 192 workgroups
+  // on 256 CUs): a multiple of 8 rows each, so that the bytes per CU are even
+  // (6144 x 4096: 6.02 -> 5.55 us, 12288 x 4096: 9.60 -> 7.97 us).  At 224 of
+  // 256 (14336 rows) it measured no faster, and the tile layout stays.
   unsigned groups = (unsigned)((ntiles + ts - 1) / ts);
   int rows_wg = 0;
-  if (GGUF_M1_ROWS && epi != 2 && groups < (unsigned)kM1Cus) {
+  if (GGUF_M1_ROWS && epi != 2 && 5 * groups < 4u * kM1Cus) {
     const int R = 8 * ((N + 8 * kM1Cus - 1) / (8 * kM1Cus));
     if ((R + 15) / 16 <= ts) {
       rows_wg = R;
@@ -1686,7 +1732,8 @@ hipError_t launch_m1(const XT *x, const uint8_t *W, int N, int K, float *y, cons
     }
   }
   const dim3 grid(groups), block(nthr);
-  const int dp = m1_depth(grid.x * nw, per, Fmt<TYPE>::TU);
+  int dp = m1_depth(grid.x * nw, per, Fmt<TYPE>::TU);
+  if (is_iq(TYPE) && (dp == 0 || dp > 3)) dp = 3;  // the IQ records are large: 3 in flight at most
   // template U is clamped to the compile-time budget (runtime per <= umax already);
   // above 64 KB of dynamic LDS the kernel's limit is raised first (gfx950: 160 KB)
 #define GGUF_M1_K(UU, XX, DD)                                                                    \
@@ -1779,13 +1826,22 @@ hipError_t launch_m(const XT *x, int64_t ldx, const uint8_t *W, int N, int K, fl
     return launch_m1<T, float, 3>(nullptr, tiles, n, ar.nh * ar.hd, y, nullptr, 0.f, epi, ar, s); \
   }
 
-// The grid-codebook IQ types take the batched kernel (decode_mk.hpp) for every
-// M up to 32, M = 1 included, so they always need its workspace; they have no
-// fused prologue / epilogue or merge kernels.
+// The grid-codebook IQ types: the one-shot kernel for M = 1 (K <= 16384), the
+// batched kernel (decode_mk.hpp) otherwise; the API asks for the workspace for
+// every M so that the batched kernel is always available.  No fused prologue /
+// epilogue or merge kernels.
 #define GGUF_DECODE_DEFINE_IQ(T, NAME)                                                           \
   hipError_t decode_##NAME(const void *x, int x_type, int64_t ldx, const uint8_t *tiles, int n,  \
                            int k, float *y, int64_t ldy, int m, float *work, int64_t work_floats, \
                            hipStream_t s) {                                                      \
+    if (m == 1) {                                                                                \
+      const hipError_t e =                                                                       \
+          x_type == 0 ? launch_m1<T, float, 0>((const float *)x, tiles, n, k, y, nullptr, 0.f, 0, \
+                                               AttnRecords{}, s)                                 \
+                      : launch_m1<T, half_t, 0>((const half_t *)x, tiles, n, k, y, nullptr, 0.f, \
+                                                0, AttnRecords{}, s);                            \
+      if (e != hipErrorNotSupported) return e;                                                   \
+    }                                                                                            \
     return x_type == 0 ? launch_mk<T, float>((const float *)x, ldx, tiles, n, k, y, ldy, m, work, \
                                              work_floats, s)                                     \
                        : launch_mk<T, half_t>((const half_t *)x, ldx, tiles, n, k, y, ldy, m,    \

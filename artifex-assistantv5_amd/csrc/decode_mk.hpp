@@ -61,27 +61,9 @@ constexpr int mk_f_off() {
 #ifndef GGUF_MK_WIDE_T
 #define GGUF_MK_WIDE_T 1  // row tiles per wave for 3 or 4 activation tiles (16 T tiles per workgroup)
 #endif
-// IQ grid types: the shared-memory tables of the B-operand decode, behind the
-// staged range: the grid as f16 (NG entries of W values; IQ1_M as 8 g) and,
-// for the types with sign bits, NS sign masks of 8 f16 sign bits (indexed by
-// the 7-bit ksigns index, KS, or by the raw sign byte).
-template <int TYPE>
-struct IqTab {
-  static constexpr int NG = TYPE == 16 ? 256 : TYPE == 17 ? 512 : TYPE == 22 ? 1024
-                          : TYPE == 18 ? 256 : TYPE == 21 ? 512 : 2048;
-  static constexpr int W = (TYPE == 18 || TYPE == 21) ? 4 : 8;
-  static constexpr int NS = TYPE == 29 ? 0 : (TYPE == 22 || TYPE == 21) ? 256 : 128;
-  static constexpr bool KS = TYPE == 16 || TYPE == 17 || TYPE == 18;
-  static constexpr int GB = NG * W * 2;  // grid bytes (the masks follow)
-};
-template <int TYPE>
-constexpr int mk_tbl_bytes() {
-  if constexpr (is_iq(TYPE)) return IqTab<TYPE>::GB + IqTab<TYPE>::NS * 16;
-  return 0;
-}
 template <int TYPE, int MA>
 constexpr int mk_kw_max() {  // units a workgroup can stage
-  return (GGUF_MK_LDS - 1024 - mk_tbl_bytes<TYPE>()) / mk_unit_bytes<MA>();
+  return (GGUF_MK_LDS - 1024 - iq_tbl_bytes<TYPE>()) / mk_unit_bytes<MA>();
 }
 
 // Convert one (unit, activation row) into the unit's image block at blk;
@@ -275,175 +257,8 @@ __device__ __forceinline__ void mk_unit(const Unit<12> (&w)[T], int bo, int lane
       for (int i = 0; i < 4; ++i) asm volatile("" : "+v"(acc[t][a][i]));
 }
 
-// ---------------------------------------------------------------------------
-// IQ grid types (iq.hpp).  The B operand of sub-block ib for lane group g
-// (elements 8 g .. 8 g + 7, group l = g of the format) is the grid entry's
-// magnitudes with the signs applied (an XOR of f16 sign bits) times the
-// group's odd sub-block factor f (2 ls + 1, 2 s + 1): exact f16 integers
-// (at most 43 x 31, 62 x 31, 15 x 31, 9 x 15).  The unit scale (d / 8, d / 4
-// or d) is applied to the f32 result.
-// ---------------------------------------------------------------------------
-template <int TYPE>
-struct IqUnit {
-  uint32_t w[iq_rd<TYPE>()];  // the row's record (the block without its d)
-  uint32_t d;                 // the f16 d (types that have one)
-};
-template <int TYPE>
-__device__ __forceinline__ void load_iq(__amdgpu_buffer_rsrc_t rs, int soff, int r, IqUnit<TYPE> &u) {
-  constexpr int RD = iq_rd<TYPE>();
-  const int base = iq_rec_off<TYPE>(r);
-#pragma unroll
-  for (int c = 0; c < RD / 4; ++c) {
-    const uint4 v = bload16(rs, base + 16 * c, soff);
-    u.w[4 * c] = v.x; u.w[4 * c + 1] = v.y; u.w[4 * c + 2] = v.z; u.w[4 * c + 3] = v.w;
-  }
-  if constexpr (RD % 4 >= 2) {
-    const uint2 v = bload8(rs, base + 16 * (RD / 4), soff);
-    u.w[RD / 4 * 4] = v.x;
-    u.w[RD / 4 * 4 + 1] = v.y;
-  }
-  if constexpr (RD % 2 == 1) u.w[RD - 1] = bload4(rs, base + 4 * (RD - 1), soff);
-  u.d = IqFmt<TYPE>::HASD ? bload2(rs, 2 * r, soff) : 0u;
-}
-// the type's grid bytes, as 16-byte chunks
-template <int TYPE>
-__device__ __forceinline__ const void *iq_grid() {
-  if constexpr (TYPE == 16) return kIq2xxsGrid;
-  if constexpr (TYPE == 17) return kIq2xsGrid;
-  if constexpr (TYPE == 22) return kIq2sGrid;
-  if constexpr (TYPE == 18) return kIq3xxsGrid;
-  if constexpr (TYPE == 21) return kIq3sGrid;
-  return kIq1sGrid;
-}
-// Table loads (16 grid bytes per chunk, at most CH chunks per thread), requested
-// with the other loads; written to shared memory by iq_put_tables.
-template <int TYPE, int NT>
-struct IqTabRegs {
-  static constexpr int CHUNKS = is_iq(TYPE) ? IqTab<TYPE>::NG * IqTab<TYPE>::W / 16 : 0;
-  static constexpr int CH = (CHUNKS + NT - 1) / NT;
-  uint4 v[CH > 0 ? CH : 1];
-};
-template <int TYPE, int NT>
-__device__ __forceinline__ void iq_get_tables(IqTabRegs<TYPE, NT> &t) {
-  using R = IqTabRegs<TYPE, NT>;
-  const uint4 *src = (const uint4 *)iq_grid<TYPE>();
-#pragma unroll
-  for (int c = 0; c < R::CH; ++c) t.v[c] = src[min((int)threadIdx.x + NT * c, R::CHUNKS - 1)];
-}
-template <int TYPE, int NT>
-__device__ __forceinline__ void iq_put_tables(const IqTabRegs<TYPE, NT> &t, int tbl) {
-  using R = IqTabRegs<TYPE, NT>;
-  using Q = IqTab<TYPE>;
-#pragma unroll
-  for (int c = 0; c < R::CH; ++c) {
-    const int q = (int)threadIdx.x + NT * c;
-    if (q < R::CHUNKS) {
-      const uint32_t b[4] = {t.v[c].x, t.v[c].y, t.v[c].z, t.v[c].w};
-      half8_t h[2];
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const uint32_t byte = (b[i >> 2] >> (8 * (i & 3))) & 0xFFu;
-        h[i >> 3][i & 7] = TYPE == 29 ? (half_t)(8.f * (float)(int8_t)byte) : (half_t)(float)byte;
-      }
-      *(half8_t *)(g_lds + tbl + 32 * q) = h[0];
-      *(half8_t *)(g_lds + tbl + 32 * q + 16) = h[1];
-    }
-  }
-  // sign masks: entry e, bit j of its sign byte (ksigns[e] = e with bit 7 making
-  // the popcount even, or e itself) -> 0x8000 in half j
-  for (int q = threadIdx.x; q < Q::NS; q += NT) {
-    const uint32_t sb = Q::KS ? (uint32_t)q | ((__builtin_popcount(q) & 1u) << 7) : (uint32_t)q;
-    uint32_t m[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) m[i] = (((sb >> (2 * i)) & 1u) << 15) | (((sb >> (2 * i + 1)) & 1u) << 31);
-    *(uint4 *)(g_lds + tbl + Q::GB + 16 * q) = make_uint4(m[0], m[1], m[2], m[3]);
-  }
-}
-
-__device__ __forceinline__ uint32_t iq_byte(uint32_t w, int i) { return (w >> (8 * i)) & 0xFFu; }
-
-// The B operand of sub-block ib for lane group g, and (scale) the f32 factor
-// of the unit.
-template <int TYPE>
-__device__ __forceinline__ half8_t iq_b(const IqUnit<TYPE> &u, int ib, int g, int tbl) {
-  using Q = IqTab<TYPE>;
-  uint32_t idx0, idx1 = 0, sidx = 0, f;
-  half2_t delta = {(half_t)0.f, (half_t)0.f};
-  if constexpr (TYPE == 16) {  // IQ2_XXS: (4 index bytes, u32 7-bit sign indices | ls << 28)
-    const uint32_t aux1 = u.w[2 * ib + 1];
-    idx0 = iq_byte(u.w[2 * ib], g);
-    sidx = (aux1 >> (7 * g)) & 127u;
-    f = 2u * (aux1 >> 28) + 1u;
-  } else if constexpr (TYPE == 17) {  // IQ2_XS: u16 (9-bit index | 7-bit sign index); scales
-    const uint32_t q = (((g & 2) ? u.w[2 * ib + 1] : u.w[2 * ib]) >> (16 * (g & 1))) & 0xFFFFu;
-    const uint32_t sc = iq_byte(u.w[16 + (ib >> 2)], ib & 3);
-    idx0 = q & 511u;
-    sidx = q >> 9;
-    f = 2u * (g < 2 ? sc & 15u : sc >> 4) + 1u;
-  } else if constexpr (TYPE == 22) {  // IQ2_S: qs[32] | signs[32] | qh[8] | scales[8]
-    const uint32_t qh = iq_byte(u.w[16 + (ib >> 2)], ib & 3), sc = iq_byte(u.w[18 + (ib >> 2)], ib & 3);
-    idx0 = iq_byte(u.w[ib], g) | ((qh << (8 - 2 * g)) & 0x300u);
-    sidx = iq_byte(u.w[8 + ib], g);
-    f = 2u * (g < 2 ? sc & 15u : sc >> 4) + 1u;
-  } else if constexpr (TYPE == 18) {  // IQ3_XXS: qs[64] | u32 (7-bit sign indices | ls << 28)
-    const uint32_t q = ((g & 2) ? u.w[2 * ib + 1] : u.w[2 * ib]) >> (16 * (g & 1)), aux = u.w[16 + ib];
-    idx0 = q & 0xFFu;
-    idx1 = (q >> 8) & 0xFFu;
-    sidx = (aux >> (7 * g)) & 127u;
-    f = 2u * (aux >> 28) + 1u;
-  } else if constexpr (TYPE == 21) {  // IQ3_S: qs[64] | qh[8] | signs[32] | scales[4]
-    const uint32_t q = ((g & 2) ? u.w[2 * ib + 1] : u.w[2 * ib]) >> (16 * (g & 1));
-    const uint32_t qh = iq_byte(u.w[16 + (ib >> 2)], ib & 3), sc = iq_byte(u.w[26], ib >> 1);
-    idx0 = (q & 0xFFu) | ((qh << (8 - 2 * g)) & 256u);
-    idx1 = ((q >> 8) & 0xFFu) | ((qh << (7 - 2 * g)) & 256u);
-    sidx = iq_byte(u.w[18 + ib], g);
-    f = 2u * ((ib & 1) ? sc >> 4 : sc & 15u) + 1u;
-  } else {  // IQ1_M: qs[32] | qh[16] | scales[4] u16
-    const uint32_t qh = iq_byte(u.w[8 + (ib >> 1)], 2 * (ib & 1) + (g >> 1));
-    const uint32_t wk = (u.w[12 + (ib >> 2)] >> (16 * ((ib >> 1) & 1))) & 0xFFFFu;
-    const int sh = 6 * (ib & 1) + (g < 2 ? 0 : 3);
-    idx0 = iq_byte(u.w[ib], g) | ((qh << ((g & 1) ? 4 : 8)) & 0x700u);
-    f = 2u * ((wk >> sh) & 7u) + 1u;
-    const half_t dl = (qh & ((g & 1) ? 0x80u : 0x08u)) ? (half_t)-1.f : (half_t)1.f;  // 8 x (+-1/8)
-    delta = {dl, dl};
-  }
-  const half_t fh = (half_t)(float)f;
-  const half2_t fp = {fh, fh};
-  uint32_t v[4];
-  if constexpr (Q::W == 8) {
-    const uint4 gr = *(const uint4 *)(g_lds + tbl + 16 * idx0);
-    v[0] = gr.x; v[1] = gr.y; v[2] = gr.z; v[3] = gr.w;
-  } else {
-    const uint2 g1 = *(const uint2 *)(g_lds + tbl + 8 * idx0), g2 = *(const uint2 *)(g_lds + tbl + 8 * idx1);
-    v[0] = g1.x; v[1] = g1.y; v[2] = g2.x; v[3] = g2.y;
-  }
-  if constexpr (Q::NS > 0) {
-    const uint4 m = *(const uint4 *)(g_lds + tbl + Q::GB + 16 * sidx);
-    v[0] ^= m.x; v[1] ^= m.y; v[2] ^= m.z; v[3] ^= m.w;
-  }
-  half8_t b;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const half2_t h = __builtin_bit_cast(half2_t, v[i]);
-    const half2_t r = TYPE == 29 ? __builtin_elementwise_fma(h, fp, delta * fp) : h * fp;
-    b[2 * i] = r[0];
-    b[2 * i + 1] = r[1];
-  }
-  return b;
-}
-template <int TYPE>
-__device__ __forceinline__ float iq_unit_scale(const IqUnit<TYPE> &u) {
-  if constexpr (TYPE == 29) {
-    const uint32_t s01 = u.w[12], s23 = u.w[13];
-    const uint32_t bits = ((s01 >> 12) & 0x000Fu) | ((s01 >> 24) & 0x00F0u) | ((s23 >> 4) & 0x0F00u) |
-                          ((s23 >> 16) & 0xF000u);
-    return h2f(bits) * 0.125f;
-  }
-  return h2f(u.d) * (TYPE == 18 ? 0.25f : TYPE == 21 ? 1.f : 0.125f);
-}
-
 template <int TYPE, int MA, int T>
-__device__ __forceinline__ void mk_unit_iq(const IqUnit<TYPE> (&w)[T], int bo, int lane, bool valid,
+__device__ __forceinline__ void mk_unit_iq(const Unit<TYPE> (&w)[T], int bo, int lane, bool valid,
                                            int tbl, float (&acc)[T][MA][4]) {
 #pragma clang fp contract(off)
   const int r = lane & 15, g = lane >> 4;
@@ -483,24 +298,6 @@ __device__ __forceinline__ void mk_unit_iq(const IqUnit<TYPE> (&w)[T], int bo, i
     for (int a = 0; a < MA; ++a)
 #pragma unroll
       for (int i = 0; i < 4; ++i) asm volatile("" : "+v"(acc[t][a][i]));
-}
-
-// The per-lane weight unit of a type and its load.
-template <int TYPE, bool IQ = is_iq(TYPE)>
-struct MkW {
-  using U = Unit<TYPE>;
-};
-template <int TYPE>
-struct MkW<TYPE, true> {
-  using U = IqUnit<TYPE>;
-};
-template <int TYPE>
-__device__ __forceinline__ void mk_load(__amdgpu_buffer_rsrc_t rs, int soff, int r, int g,
-                                        typename MkW<TYPE>::U &u) {
-  if constexpr (is_iq(TYPE))
-    load_iq<TYPE>(rs, soff, r, u);
-  else
-    load_unit(rs, soff, r, g, u);
 }
 
 // Workgroup (blockIdx.x, blockIdx.y) of TS x KL waves: row tiles
@@ -574,11 +371,11 @@ __global__ __launch_bounds__(64 * TS * KL) void mk_kernel(const uint8_t *__restr
   // a loop the memory-counter waits lose track of the requests and wait for
   // all of them at every unit.
   const int ulast = cnt > 0 ? kl + KL * (cnt - 1) : 0;  // a unit of the range
-  typename MkW<TYPE>::U wb[P][T];
+  Unit<TYPE> wb[P][T];
 #pragma unroll
   for (int i = 0; i < P; ++i)
 #pragma unroll
-    for (int t = 0; t < T; ++t) mk_load<TYPE>(rs[t], (u0 + min(kl + KL * i, ulast)) * TU, r, g, wb[i][t]);
+    for (int t = 0; t < T; ++t) load_unit(rs[t], (u0 + min(kl + KL * i, ulast)) * TU, r, g, wb[i][t]);
   if constexpr (!DMA) {
 #pragma unroll
     for (int c = 0; c < CP; ++c) {
@@ -604,7 +401,7 @@ __global__ __launch_bounds__(64 * TS * KL) void mk_kernel(const uint8_t *__restr
     if (i + P < U)  // compile-time
 #pragma unroll
       for (int t = 0; t < T; ++t)
-        mk_load<TYPE>(rs[t], (u0 + min(kl + KL * (i + P), ulast)) * TU, r, g, wb[i % P][t]);
+        load_unit(rs[t], (u0 + min(kl + KL * (i + P), ulast)) * TU, r, g, wb[i % P][t]);
   }
   if constexpr (KL > 1) {  // K-lanes 1 .. KL - 1 hand their sums to lane 0, added in order
     __syncthreads();  // the staged activations are consumed
@@ -704,7 +501,7 @@ MkPlan mk_plan(int M, int N, int K) {
   p.ranges = (nu + p.kw - 1) / p.kw;
   const size_t stage = ((size_t)p.kw * ub + 1023) & ~(size_t)1023;
   const size_t red = (size_t)(p.kl - 1) * p.ts * p.t * p.ma * 4 * 64 * 4;
-  const size_t used = stage + mk_tbl_bytes<TYPE>();  // the tables sit behind the range
+  const size_t used = stage + iq_tbl_bytes<TYPE>();  // the tables sit behind the range
   p.lds = used > red ? used : red;
   p.part_off = ((size_t)nu * ub + 1024 + 255) & ~(size_t)255;  // 1 KB slack for 1 KB copy pieces
   p.bytes = p.part_off + (p.ranges > 1 ? (size_t)p.ranges * M * ntiles * 16 * 4 : 0);
