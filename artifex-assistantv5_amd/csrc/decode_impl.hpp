@@ -558,7 +558,9 @@ __device__ __forceinline__ void unit_m1(const Unit<13> &u, const Stage &st, int 
 // IQ grid types: the B operand of sub-block j is the lane's grid entries with
 // signs and odd factor (exact f16 integers, iq_b); one chain over the 8
 // sub-blocks leaves sub-block j in rows 2j, 2j + 1, and every row takes the
-// same unit scale.
+// same unit scale.  Types with one factor per sub-block leave it out of the
+// operand and apply it to the two rows of the sub-block (four packed
+// multiplies per sub-block fewer).
 template <int PARTS, int TYPE>
 __device__ __forceinline__ void unit_m1_iq(const Unit<TYPE> &u, const Stage &st, int ul, int lane,
                                            float &acc) {
@@ -570,12 +572,17 @@ __device__ __forceinline__ void unit_m1_iq(const Unit<TYPE> &u, const Stage &st,
   half8_t a[8];
 #pragma unroll
   for (int j = 0; j < 8; ++j) a[j] = lds_h8b(((live && jo == j) ? own : zero) + 64 * j);
+  constexpr bool BF = iq_block_factor<TYPE>();
   float4_t D = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int j = 0; j < 8; ++j)
-    D = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[j], iq_b<TYPE>(u, j, g, st.tbl), D, 0, 0, 0);
+    D = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[j], iq_b<TYPE, !BF>(u, j, g, st.tbl), D, 0, 0, 0);
   const float fu = lds_f(st.xf + ul * st.ms);
-  acc += fu * (iq_unit_scale<TYPE>(u) * ((D[0] + D[1]) + (D[2] + D[3])));
+  // rows 4g + i: sub-block 2g (i = 0, 1) and 2g + 1 (i = 2, 3)
+  float f0 = 1.f, f1 = 1.f;
+  if constexpr (BF) iq_factors<TYPE>(u, g, f0, f1);
+  const float s = f0 * (D[0] + D[1]) + f1 * (D[2] + D[3]);
+  acc += fu * (iq_unit_scale<TYPE>(u) * s);
 }
 #define GGUF_IQ_M1(T)                                                                        \
   template <int PARTS>                                                                       \
@@ -1757,8 +1764,8 @@ hipError_t launch_m1(const XT *x, const uint8_t *W, int N, int K, float *y, cons
     else if (dp == 2) GGUF_M1_K(UU, XX, 2);                                                      \
     else if (dp == 3) GGUF_M1_K(UU, XX, 3);                                                      \
     else if (dp == GGUF_M1_DEEP)                                                                 \
-      GGUF_M1_K(UU, XX, ((UU) == 64 && Fmt<TYPE>::UE == 32 ? GGUF_M1_DEEP : 0));                 \
-    else GGUF_M1_K(UU, XX, 0);                                                                   \
+      GGUF_M1_K(UU, XX, ((UU) == 64 && Fmt<TYPE>::UE == 32 ? GGUF_M1_DEEP : is_iq(TYPE) ? 3 : 0)); \
+    else GGUF_M1_K(UU, XX, (is_iq(TYPE) ? 3 : 0));  /* IQ: never all units at once */          \
   } while (0)
   if (xi <= 1) {
     if (per <= 4) GGUF_M1(4, 1);

@@ -110,7 +110,37 @@ __device__ __forceinline__ uint32_t iq_byte(uint32_t w, int i) { return (w >> (8
 
 // The B operand of sub-block ib for lane group g, and (scale) the f32 factor
 // of the unit.
+// Types whose odd factor is one per sub-block (not per pair of groups).
 template <int TYPE>
+constexpr bool iq_block_factor() {
+  return TYPE == 16 || TYPE == 18 || TYPE == 21;
+}
+// Those factors of sub-blocks 2g and 2g + 1 (the rows lane group g holds), as
+// f32 integers; the words are picked with selects (no indexing by g).
+__device__ __forceinline__ uint32_t sel4(uint32_t a0, uint32_t a1, uint32_t a2, uint32_t a3, int g) {
+  return (g & 2) ? ((g & 1) ? a3 : a2) : ((g & 1) ? a1 : a0);
+}
+template <int TYPE>
+__device__ __forceinline__ void iq_factors(const IqUnit<TYPE> &u, int g, float &f0, float &f1) {
+  uint32_t l0, l1;
+  if constexpr (TYPE == 16) {  // ls in the top nibble of word 2 ib + 1
+    l0 = sel4(u.w[1], u.w[5], u.w[9], u.w[13], g) >> 28;
+    l1 = sel4(u.w[3], u.w[7], u.w[11], u.w[15], g) >> 28;
+  } else if constexpr (TYPE == 18) {  // ls in the top nibble of word 16 + ib
+    l0 = sel4(u.w[16], u.w[18], u.w[20], u.w[22], g) >> 28;
+    l1 = sel4(u.w[17], u.w[19], u.w[21], u.w[23], g) >> 28;
+  } else {  // IQ3_S: scale byte g, low nibble for the even sub-block
+    const uint32_t sc = iq_byte(u.w[26], g);
+    l0 = sc & 15u;
+    l1 = sc >> 4;
+  }
+  f0 = (float)(2u * l0 + 1u);
+  f1 = (float)(2u * l1 + 1u);
+}
+
+// FACTOR false (iq_block_factor types only): the operand without the odd
+// factor, which the caller applies to the sub-block's f32 result.
+template <int TYPE, bool FACTOR = true>
 __device__ __forceinline__ half8_t iq_b(const IqUnit<TYPE> &u, int ib, int g, int tbl) {
   using Q = IqTab<TYPE>;
   uint32_t idx0, idx1 = 0, sidx = 0, f;
@@ -171,7 +201,7 @@ __device__ __forceinline__ half8_t iq_b(const IqUnit<TYPE> &u, int ib, int g, in
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const half2_t h = __builtin_bit_cast(half2_t, v[i]);
-    const half2_t r = TYPE == 29 ? __builtin_elementwise_fma(h, fp, delta * fp) : h * fp;
+    const half2_t r = TYPE == 29 ? __builtin_elementwise_fma(h, fp, delta * fp) : FACTOR ? h * fp : h;
     b[2 * i] = r[0];
     b[2 * i + 1] = r[1];
   }
