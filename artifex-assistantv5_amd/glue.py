@@ -1,6 +1,9 @@
 """Decode-step glue kernels of libgguf_hip (f32 torch tensors on the current HIP stream).
 
-Each function is one launch; shapes are checked here and again by the library.
+Each function is one launch.  Every buffer's element count is checked against
+the launch shape here, before the dtype / device checks and before the C ABI
+(which cannot see tensor sizes): a mismatch raises ValueError instead of
+reading or writing past a buffer on the device.
 Reference shaders: rmsnorm.wgsl:1-9,58-67, rope.wgsl:1-10,
 elementwise.wgsl:96-102 (gate_silu), argmax.wgsl; layer loop
 webgpu/src/engine/forward-pass.ts:2925-3297.
@@ -23,10 +26,17 @@ def _f32(*ts: torch.Tensor) -> None:
             raise ValueError("glue kernels take contiguous float32 device tensors")
 
 
+def _numel(what: str, t: torch.Tensor, want: int) -> None:
+    if t.numel() != want:
+        raise ValueError(f"{what} has {t.numel()} elements, the launch needs {want}")
+
+
 def rmsnorm(x: torch.Tensor, w: torch.Tensor, eps: float, out: torch.Tensor) -> torch.Tensor:
     """out = x / sqrt(mean(x^2) + eps) * w over the last dimension."""
-    _f32(x, w, out)
     n = x.shape[-1]
+    _numel("rmsnorm: w", w, n)
+    _numel("rmsnorm: out", out, x.numel())
+    _f32(x, w, out)
     lib = _native.load_library()
     _native.check(lib.gguf_hip_rmsnorm(x.data_ptr(), w.data_ptr(), eps, out.data_ptr(),
                                        x.numel() // n, n, _s(x)), lib)
@@ -36,8 +46,11 @@ def rmsnorm(x: torch.Tensor, w: torch.Tensor, eps: float, out: torch.Tensor) -> 
 def add_rmsnorm(x: torch.Tensor, res: torch.Tensor, w: torch.Tensor, eps: float,
                 out: torch.Tensor) -> torch.Tensor:
     """x += res (in place), then out = rmsnorm(x) * w."""
-    _f32(x, res, w, out)
     n = x.shape[-1]
+    _numel("add_rmsnorm: res", res, x.numel())
+    _numel("add_rmsnorm: w", w, n)
+    _numel("add_rmsnorm: out", out, x.numel())
+    _f32(x, res, w, out)
     lib = _native.load_library()
     _native.check(lib.gguf_hip_add_rmsnorm(x.data_ptr(), res.data_ptr(), w.data_ptr(), eps,
                                            out.data_ptr(), x.numel() // n, n, _s(x)), lib)
@@ -46,8 +59,11 @@ def add_rmsnorm(x: torch.Tensor, res: torch.Tensor, w: torch.Tensor, eps: float,
 
 def swiglu(gate_up: torch.Tensor, out: torch.Tensor) -> torch.Tensor:
     """out = up * silu(gate) for rows [gate | up]."""
-    _f32(gate_up, out)
     ffn = out.shape[-1]
+    _numel("swiglu: gate_up", gate_up, 2 * out.numel())
+    if gate_up.dim() > 1 and gate_up.shape[-1] != 2 * ffn:
+        raise ValueError(f"swiglu: gate_up rows hold {gate_up.shape[-1]} values, need {2 * ffn}")
+    _f32(gate_up, out)
     lib = _native.load_library()
     _native.check(lib.gguf_hip_swiglu(gate_up.data_ptr(), out.data_ptr(), out.numel() // ffn, ffn,
                                       _s(out)), lib)
@@ -80,7 +96,23 @@ def attention_decode(qkv: torch.Tensor, pos: torch.Tensor, cos: torch.Tensor, si
                      work: torch.Tensor) -> torch.Tensor | None:
     """RoPE + KV append at slot ``pos`` (device int64 [1]) + causal GQA attention.
     ``out=None`` writes only the partial-softmax records into ``work``, for
-    ``matmul_attn_merge`` to merge inside the output projection."""
+    ``matmul_attn_merge`` to merge inside the output projection.  Caches are
+    ``[n_kv_heads, max_seq, head_dim]``, cos / sin ``[max_seq, head_dim / 2]``."""
+    if k_cache.dim() < 2:
+        raise ValueError("attention_decode: k_cache must be [n_kv_heads, max_seq, head_dim]")
+    max_seq = k_cache.shape[-2]
+    if k_cache.shape[-1] != head_dim:
+        raise ValueError(f"attention_decode: k_cache rows hold {k_cache.shape[-1]} values, "
+                         f"head_dim is {head_dim}")
+    _numel("attention_decode: k_cache", k_cache, n_kv_heads * max_seq * head_dim)
+    _numel("attention_decode: v_cache", v_cache, n_kv_heads * max_seq * head_dim)
+    _numel("attention_decode: qkv", qkv, (n_heads + 2 * n_kv_heads) * head_dim)
+    _numel("attention_decode: cos", cos, max_seq * (head_dim // 2))
+    _numel("attention_decode: sin", sin, max_seq * (head_dim // 2))
+    if out is not None:
+        _numel("attention_decode: out", out, n_heads * head_dim)
+    if pos.numel() != 1:
+        raise ValueError("attention_decode: pos must hold one position")
     _f32(qkv, cos, sin, k_cache, v_cache, *(() if out is None else (out,)))
     if pos.dtype != torch.int64 or not pos.is_cuda:
         raise ValueError("pos must be an int64 device tensor")
@@ -100,6 +132,8 @@ def matmul_attn_merge(work: torch.Tensor, pos: torch.Tensor, w, y: torch.Tensor,
     (``y +=`` with ``accumulate``), a = the attention output merged from the
     records that ``attention_decode(..., out=None, work=work)`` wrote for ``pos``.
     ``w`` is a GGUFWeight with k = n_heads * head_dim."""
+    if pos.numel() != 1:
+        raise ValueError("matmul_attn_merge: pos must hold one position")
     _f32(y)
     if pos.dtype != torch.int64 or not pos.is_cuda:
         raise ValueError("pos must be an int64 device tensor")
@@ -122,6 +156,8 @@ def argmax_workspace(device) -> torch.Tensor:
 
 def argmax(x: torch.Tensor, out: torch.Tensor, work: torch.Tensor) -> torch.Tensor:
     """out[0] = first index of max(x) (int64 device tensor)."""
+    if x.numel() == 0 or out.numel() < 1:
+        raise ValueError("argmax: x must be non-empty and out must hold one index")
     _f32(x)
     if out.dtype != torch.int64 or not out.is_cuda:
         raise ValueError("argmax output must be an int64 device tensor")
@@ -148,7 +184,6 @@ def matmul_fused(x: torch.Tensor, w, y: torch.Tensor, prologue: int = PROLOGUE_N
     (``accumulate`` / EPILOGUE_ACCUMULATE) or, for a weight of interleaved
     gate / up tiles (``interleave_tiles``), ``y = up * silu(gate)``
     (EPILOGUE_SWIGLU, ``w.n / 2`` outputs).  ``w`` is a GGUFWeight."""
-    _f32(x, y)
     k = w.k
     epi = epilogue if epilogue is not None else (EPILOGUE_ACCUMULATE if accumulate
                                                  else EPILOGUE_STORE)
@@ -160,7 +195,8 @@ def matmul_fused(x: torch.Tensor, w, y: torch.Tensor, prologue: int = PROLOGUE_N
     if prologue == PROLOGUE_RMSNORM:
         if norm_w is None:
             raise ValueError("matmul_fused: RMSNORM prologue needs norm_w")
-        _f32(norm_w)
+        _numel("matmul_fused: norm_w", norm_w, k)
+    _f32(x, y, *((norm_w,) if prologue == PROLOGUE_RMSNORM else ()))
     lib = _native.load_library()
     _native.check(lib.gguf_hip_matmul_fused(
         x.data_ptr(), w.ptr(), w.ggml_type, w.n, k, y.data_ptr(), prologue,

@@ -147,8 +147,20 @@ def test_attention_merge_projection(mods, t, nh, nkv, hd, max_seq, p):
     """Records-only attention + the merge prologue equal, bit for bit, attention
     with its own merge followed by the plain fused projection (same arithmetic
     in the same order), for STORE and ACCUMULATE."""
+    _merge_case(mods, t, nh, nkv, hd, max_seq, p, 1024)
+
+
+# the 32-element-block types at the decoder's output-projection shape (32 x 128
+# heads, N = 4096), whose K split and waves per workgroup differ from N = 1024
+@pytest.mark.parametrize("t", [2, 6, 8, 20])
+@pytest.mark.parametrize("p", [130, 511])
+def test_attention_merge_projection_n4096_small_blocks(mods, t, p):
+    _merge_case(mods, t, 32, 8, 128, 600, p, 4096)
+
+
+def _merge_case(mods, t, nh, nkv, hd, max_seq, p, n):
     pkg, glue = mods
-    k, n = nh * hd, 1024
+    k = nh * hd
     w = _weight(pkg, t, n, k, seed=k + p)
     qkv, kc, vc, cos, sin = _attention_inputs(nh, nkv, hd, max_seq, p)
     kc2, vc2 = kc.clone(), vc.clone()

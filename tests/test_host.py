@@ -122,3 +122,51 @@ def test_decoder_rope_tables_and_norm():
     assert torch.allclose(y[0, 0].double(), torch.cat([z.real, z.imag]), atol=1e-6)
     v = torch.tensor([[3.0, 4.0]])
     assert torch.allclose(dec.rms_norm(v, torch.ones(2), 0.0), v / (12.5 ** 0.5))
+
+
+def test_glue_rejects_mismatched_buffers(pkg):
+    """Every glue wrapper checks element counts against the launch shape before
+    anything reaches the C ABI (CPU tensors: the size check comes first)."""
+    import types
+    import torch
+    from importlib import import_module
+    glue = import_module("artifex-assistantv5_amd.glue")
+    z = lambda *s: torch.zeros(*s)  # noqa: E731
+    cases = [
+        (lambda: glue.rmsnorm(z(2, 8), z(7), 1e-5, z(2, 8)), "rmsnorm: w"),
+        (lambda: glue.rmsnorm(z(2, 8), z(8), 1e-5, z(8)), "rmsnorm: out"),
+        (lambda: glue.add_rmsnorm(z(2, 8), z(8), z(8), 1e-5, z(2, 8)), "add_rmsnorm: res"),
+        (lambda: glue.add_rmsnorm(z(2, 8), z(2, 8), z(4), 1e-5, z(2, 8)), "add_rmsnorm: w"),
+        (lambda: glue.add_rmsnorm(z(2, 8), z(2, 8), z(8), 1e-5, z(1, 8)), "add_rmsnorm: out"),
+        (lambda: glue.swiglu(z(2, 15), z(2, 8)), "swiglu: gate_up"),
+        (lambda: glue.swiglu(z(4, 8), z(2, 8)), "swiglu: gate_up rows"),
+        (lambda: glue.attention_decode(z(6 * 64), z(1), z(16, 32), z(16, 32), z(2, 16, 32), z(2, 16, 64),
+                                       None, 4, 1, 64, z(1)), "k_cache rows"),
+        (lambda: glue.attention_decode(z(6 * 64), z(1), z(16, 32), z(16, 32), z(2, 16, 64), z(2, 16, 64),
+                                       None, 4, 1, 64, z(1)), "attention_decode: k_cache"),
+        (lambda: glue.attention_decode(z(6 * 64), z(1), z(16, 32), z(16, 32), z(1, 16, 64), z(2, 16, 64),
+                                       None, 4, 1, 64, z(1)), "attention_decode: v_cache"),
+        (lambda: glue.attention_decode(z(5 * 64), z(1), z(16, 32), z(16, 32), z(1, 16, 64), z(1, 16, 64),
+                                       None, 4, 1, 64, z(1)), "attention_decode: qkv"),
+        (lambda: glue.attention_decode(z(6 * 64), z(1), z(15, 32), z(16, 32), z(1, 16, 64), z(1, 16, 64),
+                                       None, 4, 1, 64, z(1)), "attention_decode: cos"),
+        (lambda: glue.attention_decode(z(6 * 64), z(1), z(16, 32), z(16, 31), z(1, 16, 64), z(1, 16, 64),
+                                       None, 4, 1, 64, z(1)), "attention_decode: sin"),
+        (lambda: glue.attention_decode(z(6 * 64), z(1), z(16, 32), z(16, 32), z(1, 16, 64), z(1, 16, 64),
+                                       z(255), 4, 1, 64, z(1)), "attention_decode: out"),
+        (lambda: glue.attention_decode(z(6 * 64), z(2), z(16, 32), z(16, 32), z(1, 16, 64), z(1, 16, 64),
+                                       None, 4, 1, 64, z(1)), "pos must hold one"),
+        (lambda: glue.argmax(z(0), z(1), z(1)), "argmax"),
+    ]
+    w = types.SimpleNamespace(k=256, n=64, ggml_type=12)
+    cases += [
+        (lambda: glue.matmul_fused(z(255), w, z(64)), "matmul_fused: x"),
+        (lambda: glue.matmul_fused(z(256), w, z(63)), "matmul_fused: x"),
+        (lambda: glue.matmul_fused(z(256), w, z(64), glue.PROLOGUE_RMSNORM, z(255)), "norm_w"),
+        (lambda: glue.matmul_fused(z(512), w, z(64), glue.PROLOGUE_SWIGLU, None,
+                                   epilogue=glue.EPILOGUE_SWIGLU), "matmul_fused: x"),
+        (lambda: glue.matmul_attn_merge(z(1), z(2), w, z(64), 4, 1, 64, 16), "pos must hold one"),
+    ]
+    for fn, msg in cases:
+        with pytest.raises(ValueError, match=msg):
+            fn()
