@@ -45,8 +45,7 @@ bool traits(int t, int *block, int *size) {
   return false;
 }
 
-// the grid-codebook IQ types: decode kernels only (every M in passes of 32
-// rows), always with a workspace
+// the grid-codebook IQ types: their decode kernel always takes a workspace
 bool grid_type(int t) {
   return t == GGUF_HIP_IQ2_XXS || t == GGUF_HIP_IQ2_XS || t == GGUF_HIP_IQ2_S ||
          t == GGUF_HIP_IQ3_XXS || t == GGUF_HIP_IQ3_S || t == GGUF_HIP_IQ1_M;
@@ -244,14 +243,10 @@ int gguf_hip_matmul_ws(const void *x, int x_type, int64_t ldx, const void *tiles
   // rows (the reference computes in f32) and take the row-scaled fp16 GEMM
   // from there on (prefill)
   if (variant == GGUF_HIP_VARIANT_AUTO)
-    variant = grid_type(ggml_type) ||
-                      m <= (x_type == GGUF_HIP_F32 ? GGUF_HIP_F32_GEMM_MIN_M - 1 : GGUF_HIP_DECODE_MAX_M)
+    variant = m <= (x_type == GGUF_HIP_F32 ? GGUF_HIP_F32_GEMM_MIN_M - 1 : GGUF_HIP_DECODE_MAX_M)
                   ? GGUF_HIP_VARIANT_DECODE
                   : GGUF_HIP_VARIANT_GEMM;
-  if (grid_type(ggml_type)) {
-    if (variant == GGUF_HIP_VARIANT_GEMM)
-      return fail(GGUF_HIP_ERR_TYPE, "[gguf-hip] no GEMM kernel for ggml type %d (use the decode variant)",
-                  ggml_type);
+  if (grid_type(ggml_type) && variant == GGUF_HIP_VARIANT_DECODE) {
     const int64_t need = 4 * gguf::launch_decode_work(ggml_type, x_type, n, k, m);
     if (!work || work_bytes < need)
       return fail(GGUF_HIP_ERR_SHAPE,

@@ -39,6 +39,7 @@
 #include "common.hpp"
 #include "decode_types.hpp"
 #include "iq.hpp"
+#include "iq_ops.hpp"
 
 namespace gguf {
 
@@ -576,7 +577,7 @@ __device__ __forceinline__ void unit_m1_iq(const Unit<TYPE> &u, const Stage &st,
   float4_t D = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int j = 0; j < 8; ++j)
-    D = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[j], iq_b<TYPE, !BF>(u, j, g, st.tbl), D, 0, 0, 0);
+    D = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[j], iq_b<TYPE, !BF>(u, j, g, g_lds + st.tbl), D, 0, 0, 0);
   const float fu = lds_f(st.xf + ul * st.ms);
   // rows 4g + i: sub-block 2g (i = 0, 1) and 2g + 1 (i = 2, 3)
   float f0 = 1.f, f1 = 1.f;
@@ -1584,7 +1585,7 @@ __global__ __launch_bounds__(512) void decode_m1_kernel(const XT *__restrict__ x
   for (int i = 0; i < XI; ++i)
     store_item<PARTS, GS, UE, Dec<TYPE>::SUMS, Dec<TYPE>::NAT>(per_row, per_row,
                                                                (int)threadIdx.x + nthr * i, xv[i], st);
-  if constexpr (is_iq(TYPE)) iq_put_tables<TYPE, 256>(tab, st.tbl);
+  if constexpr (is_iq(TYPE)) iq_put_tables<TYPE, 256>(tab, g_lds + st.tbl);
   __syncthreads();
   float ssp = 0.f;  // this lane's share of the row's sum of x^2 (reduced after the units)
   if constexpr (PRO == 1)

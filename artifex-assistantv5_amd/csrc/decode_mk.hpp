@@ -275,7 +275,7 @@ __device__ __forceinline__ void mk_unit_iq(const Unit<TYPE> (&w)[T], int bo, int
     for (int a = 0; a < MA; ++a) A[a] = lds_h8b(arow + a * 16 * (kMkLd * 2) + 64 * ib);
 #pragma unroll
     for (int t = 0; t < T; ++t) {
-      const half8_t B = iq_b<TYPE>(w[t], ib, g, tbl);
+      const half8_t B = iq_b<TYPE>(w[t], ib, g, g_lds + tbl);
 #pragma unroll
       for (int a = 0; a < MA; ++a) D[t][a] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[a], B, D[t][a], 0, 0, 0);
     }
@@ -353,7 +353,7 @@ __global__ __launch_bounds__(64 * TS * KL) void mk_kernel(const uint8_t *__restr
       __builtin_amdgcn_global_load_lds((const void *)(src + 1024 * i + 16 * lane),
                                        (__attribute__((address_space(3))) void *)(g_lds + 1024 * i),
                                        16, 0, 0);
-    if constexpr (IQ) iq_put_tables<TYPE, 64 * NW>(tab, tbl);
+    if constexpr (IQ) iq_put_tables<TYPE, 64 * NW>(tab, g_lds + tbl);
     __syncthreads();
   } else {
 #pragma unroll
@@ -382,7 +382,7 @@ __global__ __launch_bounds__(64 * TS * KL) void mk_kernel(const uint8_t *__restr
       const int q = (int)threadIdx.x + 64 * NW * c;
       if (q < nq) *(u32x4 *)(g_lds + 16 * q) = R[c];
     }
-    if constexpr (IQ) iq_put_tables<TYPE, 64 * NW>(tab, tbl);
+    if constexpr (IQ) iq_put_tables<TYPE, 64 * NW>(tab, g_lds + tbl);
     __syncthreads();
   }
   float acc[T][MA][4];

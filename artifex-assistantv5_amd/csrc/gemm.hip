@@ -34,6 +34,7 @@
 // by XCD (workgroup b runs on XCD b % 8): each XCD gets a contiguous range of
 // tiles, m fastest, so its workgroups share weight columns in its L2.
 #include "common.hpp"
+#include "iq_ops.hpp"
 
 namespace gguf {
 
@@ -674,6 +675,129 @@ __device__ __forceinline__ void dequant_b(const BRaw<23> &b, const BCur<23> &h,
 }
 
 // ---------------------------------------------------------------------------
+// Grid-codebook IQ types (iq_ops.hpp).  Window c is sub-blocks 2c, 2c + 1; the
+// lane (r, g) loads the words of its row's record those two sub-blocks use
+// (indices as in the record: the block without its d, 4-byte words) into a
+// sparse IqUnit, builds the exact f16 operand of grid entry, signs and odd
+// factor (iq_b, tables in shared memory) and rounds unit scale x operand to
+// fp16 once (v_fma_mix).
+// ---------------------------------------------------------------------------
+#define GGUF_GEMM_IQ(T)                                                                          \
+  template <>                                                                                    \
+  struct BRaw<T> {                                                                               \
+    IqUnit<T> u[kTN];                                                                            \
+  };                                                                                             \
+  template <>                                                                                    \
+  struct BHdr<T> {                                                                               \
+    uint32_t d[kTN];                                                                             \
+  };                                                                                             \
+  template <>                                                                                    \
+  struct BCur<T> {                                                                               \
+    float us[kTN];                                                                               \
+    const unsigned char *tb;                                                                     \
+    __device__ __forceinline__ void set(const BHdr<T> &h) {                                      \
+      _Pragma("unroll") for (int j = 0; j < kTN; ++j) us[j] = h2f(h.d[j]) * iq_d_factor<T>();    \
+    }                                                                                            \
+  };                                                                                             \
+  template <>                                                                                    \
+  __device__ __forceinline__ BOff b_offsets<T>(int r, int) {                                     \
+    return BOff{iq_rec_off<T>(r), 2 * r, 0, 0};                                                  \
+  }                                                                                              \
+  template <int C>                                                                               \
+  __device__ __forceinline__ void load_b(rsrc_t rs, const BOff &o, int ts, int u, int,           \
+                                         BRaw<T> &b, BHdr<T> &h) {                               \
+    load_b_iq<C, T>(rs, o, ts, u, b, h);                                                         \
+  }                                                                                              \
+  template <int C>                                                                               \
+  __device__ __forceinline__ void dequant_b(const BRaw<T> &b, const BCur<T> &h,                  \
+                                            half8_t (&bf)[kTN][2], int g) {                      \
+    dequant_b_iq<C, T>(b, h, bf, g);                                                             \
+  }
+
+// the unit scale over the f16 d (IQ1_M: d assembled from its scale words)
+template <int T>
+constexpr float iq_d_factor() {
+  return T == 18 ? 0.25f : T == 21 ? 1.f : 0.125f;
+}
+template <int T>
+struct BRaw;
+template <int T>
+struct BHdr;
+template <int T>
+struct BCur;
+
+// fp16(s * x) of both f16 halves of w, computed in f32 and rounded once
+__device__ __forceinline__ uint32_t mix_w(uint32_t w, float s) {
+  uint32_t r;
+  asm("v_fma_mixlo_f16 %0, %1, %2, 0 op_sel_hi:[1,0,0]\n\t"
+      "v_fma_mixhi_f16 %0, %1, %2, 0 op_sel:[1,0,0] op_sel_hi:[1,0,0]"
+      : "=&v"(r)
+      : "v"(w), "v"(s));
+  return r;
+}
+
+template <int C, int T>
+__device__ __forceinline__ void load_b_iq(rsrc_t rs, const BOff &o, int ts, int u, BRaw<T> &b,
+                                          BHdr<T> &h) {
+  const int su = u * Fmt<T>::TU;
+#pragma unroll
+  for (int j = 0; j < kTN; ++j) {
+    uint32_t *w = b.u[j].w;
+    const int v = o.v0 + j * ts;  // the record of the lane's row in tile j
+    if constexpr (T == 16 || T == 17 || T == 18 || T == 21) {  // index words 4C .. 4C + 3
+      const uint4 q = bl16(rs, v + 16 * C, su);
+      w[4 * C] = q.x; w[4 * C + 1] = q.y; w[4 * C + 2] = q.z; w[4 * C + 3] = q.w;
+    }
+    if constexpr (T == 17) w[16 + (C >> 1)] = bl4(rs, v + 4 * (16 + (C >> 1)), su);
+    if constexpr (T == 18) {
+      const uint2 a = bl8(rs, v + 4 * (16 + 2 * C), su);
+      w[16 + 2 * C] = a.x; w[17 + 2 * C] = a.y;
+    }
+    if constexpr (T == 21) {
+      w[16 + (C >> 1)] = bl4(rs, v + 4 * (16 + (C >> 1)), su);
+      const uint2 sg = bl8(rs, v + 4 * (18 + 2 * C), su);
+      w[18 + 2 * C] = sg.x; w[19 + 2 * C] = sg.y;
+      w[26] = bl4(rs, v + 4 * 26, su);
+    }
+    if constexpr (T == 22) {
+      const uint2 q = bl8(rs, v + 8 * C, su), sg = bl8(rs, v + 4 * (8 + 2 * C), su);
+      w[2 * C] = q.x; w[2 * C + 1] = q.y; w[8 + 2 * C] = sg.x; w[9 + 2 * C] = sg.y;
+      w[16 + (C >> 1)] = bl4(rs, v + 4 * (16 + (C >> 1)), su);
+      w[18 + (C >> 1)] = bl4(rs, v + 4 * (18 + (C >> 1)), su);
+    }
+    if constexpr (T == 29) {
+      const uint2 q = bl8(rs, v + 8 * C, su), sw = bl8(rs, v + 48, su);
+      w[2 * C] = q.x; w[2 * C + 1] = q.y; w[12] = sw.x; w[13] = sw.y;
+      w[8 + C] = bl4(rs, v + 4 * (8 + C), su);
+    }
+    if constexpr (T != 29)
+      if (C == 0) h.d[j] = bl2(rs, o.v1 + j * ts, su);
+  }
+}
+
+template <int C, int T>
+__device__ __forceinline__ void dequant_b_iq(const BRaw<T> &b, const BCur<T> &h,
+                                             half8_t (&bf)[kTN][2], int g) {
+#pragma unroll
+  for (int j = 0; j < kTN; ++j) {
+    const float us = T == 29 ? iq_unit_scale<T>(b.u[j]) : h.us[j];
+#pragma unroll
+    for (int hb = 0; hb < 2; ++hb) {
+      const uint4 v = __builtin_bit_cast(uint4, iq_b<T>(b.u[j], 2 * C + hb, g, h.tb));
+      bf[j][hb] = h8(mix_w(v.x, us), mix_w(v.y, us), mix_w(v.z, us), mix_w(v.w, us));
+    }
+  }
+}
+
+GGUF_GEMM_IQ(16)
+GGUF_GEMM_IQ(17)
+GGUF_GEMM_IQ(18)
+GGUF_GEMM_IQ(21)
+GGUF_GEMM_IQ(22)
+GGUF_GEMM_IQ(29)
+#undef GGUF_GEMM_IQ
+
+// ---------------------------------------------------------------------------
 // Activations.  Thread t stages rows (t >> 3) + kARows i, i < kAI, 16-byte
 // column chunk t & 7 of the 64-wide step.
 // ---------------------------------------------------------------------------
@@ -822,6 +946,10 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(const XT *__restrict__ x
   constexpr int TU = Fmt<TYPE>::TU, UE = Fmt<TYPE>::UE;
   __shared__ __align__(16) unsigned char lds[2 * kStageB];
   __shared__ __align__(16) float rowf[kBM];  // f32 input: the rows' inverse scales 2^-e
+  // IQ types: the decode tables, requested first and written before the first dequantization
+  __shared__ __align__(16) unsigned char iqtbl[is_iq(TYPE) ? iq_tbl_bytes<TYPE>() : 16];
+  IqTabRegs<TYPE, kThreads> tab;
+  if constexpr (is_iq(TYPE)) iq_get_tables<TYPE, kThreads>(tab);
 
   int bid = blockIdx.x;
   if ((gridDim.x & 7) == 0) bid = (bid & 7) * (gridDim.x >> 3) + (bid >> 3);
@@ -886,6 +1014,11 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(const XT *__restrict__ x
     // step s = 4 u + c covers window c of superblock u; 4 nu >= 4 steps
     s.template load<0, 0>(0, 0);
     s.template load<1, 1>(0, 64);
+    if constexpr (is_iq(TYPE)) {
+      iq_put_tables<TYPE, kThreads>(tab, iqtbl);
+      s.hc.tb = iqtbl;
+      __syncthreads();
+    }
     s.template prepare<0, 0>(0);
     __syncthreads();
     for (int u = 0; u < s.nu; ++u) {
@@ -958,6 +1091,18 @@ hipError_t launch_x(const XT *x, int64_t ldx, const uint8_t *W, int type, int64_
     launch_type<20, XT>(x, ldx, W, (int)m, (int)n, (int)k, y, ldy, s);
   else if (type == 23)
     launch_type<23, XT>(x, ldx, W, (int)m, (int)n, (int)k, y, ldy, s);
+  else if (type == 16)
+    launch_type<16, XT>(x, ldx, W, (int)m, (int)n, (int)k, y, ldy, s);
+  else if (type == 17)
+    launch_type<17, XT>(x, ldx, W, (int)m, (int)n, (int)k, y, ldy, s);
+  else if (type == 18)
+    launch_type<18, XT>(x, ldx, W, (int)m, (int)n, (int)k, y, ldy, s);
+  else if (type == 21)
+    launch_type<21, XT>(x, ldx, W, (int)m, (int)n, (int)k, y, ldy, s);
+  else if (type == 22)
+    launch_type<22, XT>(x, ldx, W, (int)m, (int)n, (int)k, y, ldy, s);
+  else if (type == 29)
+    launch_type<29, XT>(x, ldx, W, (int)m, (int)n, (int)k, y, ldy, s);
   else if (type == 10)
     launch_type<10, XT>(x, ldx, W, (int)m, (int)n, (int)k, y, ldy, s);
   else if (type == 11)

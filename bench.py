@@ -493,6 +493,8 @@ def secondary_cases(pkg, args, pool, secondary):
             for mm in (1, 8, 32):
                 r = matmul_case(pkg, tt, mm, 14336, 4096, ipool, 240, 10, replays=3)
                 secondary[f"{name}_decode_m{mm}_gbs"] = round(r["gbs"], 1)
+            r = matmul_case(pkg, tt, 2048, 14336, 4096, ipool[:2], 10, 2, xdtype="float16")
+            secondary[f"{name}_gemm_m2048_n14336_tflops"] = round(r["tflops"], 1)
             del ipool
     if want("q5k"):
         q5pool, _ = make_pool(pkg, 13, 14336, 4096, 14, seed=6)

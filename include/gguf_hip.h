@@ -64,7 +64,7 @@ extern "C" {
 #define GGUF_HIP_Q6_K 14
 #define GGUF_HIP_IQ4_NL 20
 #define GGUF_HIP_IQ4_XS 23
-/* grid-codebook types: decode variant only, always with a workspace */
+/* grid-codebook types: the decode variant always with a workspace */
 #define GGUF_HIP_IQ2_XXS 16
 #define GGUF_HIP_IQ2_XS 17
 #define GGUF_HIP_IQ3_XXS 18
@@ -175,10 +175,10 @@ int gguf_hip_matmul_variant(const void *x, int x_type, int64_t ldx, const void *
  * either way, and much faster for weights of few rows (the FFN down projection).
  * The reference engine likewise preallocates its scratch (forward-pass.ts:1140-1163).
  * Calls that share a workspace must not overlap.
- * The grid-codebook IQ types run only the decode variant (AUTO picks it for
- * every M; GEMM returns GGUF_HIP_ERR_TYPE) and need the workspace for every M,
- * M = 1 included: without one they return GGUF_HIP_ERR_SHAPE, so
- * gguf_hip_matmul and gguf_hip_matmul_variant reject them. */
+ * The grid-codebook IQ types need the workspace whenever the decode variant
+ * runs (AUTO picks it as for the other types), M = 1 included: without one it
+ * returns GGUF_HIP_ERR_SHAPE, so gguf_hip_matmul and gguf_hip_matmul_variant
+ * take them only where AUTO / GEMM choose the GEMM. */
 int gguf_hip_matmul_ws(const void *x, int x_type, int64_t ldx, const void *tiles, int ggml_type,
                        int64_t n, int64_t k, float *y, int64_t ldy, int64_t m, int variant,
                        void *work, int64_t work_bytes, void *stream);

@@ -8,7 +8,8 @@
   f32 and f16 activations: per element |y - y_ref| <= 2e-5 sum_k |x_k w_nk|
   against the f64 product of the oracle's dequantized weights (the same
   f32-grade gate as the other types' decode path);
-* the API contract: no GEMM variant, and a workspace for every M.
+* the GEMM (M > 32): the gate of the other types' fp16 GEMM;
+* the API contract: a workspace for the decode variant at every M.
 """
 
 import ctypes
@@ -72,7 +73,7 @@ def test_decode_matmul_f32_grade(pkg, ref, t, xdt):
         wdeq = ref.dequant_rows(t, raw, n, k)
         x = pkg.quantize.synthetic_activations(m, k, seed=800 + i,
                                                dtype=np.float32 if xdt == "f32" else np.float16)
-        y = pkg.qlinear(torch.from_numpy(x).cuda(), w).cpu().numpy()
+        y = pkg.qlinear(torch.from_numpy(x).cuda(), w, variant=DECODE).cpu().numpy()
         x64 = x.astype(np.float64)
         met = ref.parity_metrics(y, ref.matmul_bt(x64, wdeq), ref.matmul_bt_abs(x64, wdeq))
         assert met["finite"] and met["elemwise"] <= DECODE_TOL, ((NAMES[t], xdt, m, n, k), met)
@@ -100,11 +101,11 @@ def test_api_contract(pkg, native):
     raw, w = _weight(pkg, t, n, k, seed=5)
     x = torch.from_numpy(pkg.quantize.synthetic_activations(m, k, seed=6)).cuda()
     y = torch.zeros(m, n, device="cuda")
-    # no GEMM kernel for the grid types
+    # the GEMM variant needs no workspace
     rc = lib.gguf_hip_matmul_variant(x.data_ptr(), 0, k, w.ptr(), t, n, k, y.data_ptr(), n, m,
                                      GEMM, None)
-    assert rc == native.ERR_TYPE and "no GEMM kernel" in native.last_error(lib)
-    # a workspace for every M, M = 1 included
+    assert rc == 0, native.last_error(lib)
+    # the decode variant needs a workspace for every M, M = 1 included
     for mm in (1, m):
         need = lib.gguf_hip_matmul_workspace(t, 0, n, k, mm)
         assert need > 0
@@ -122,3 +123,37 @@ def test_api_contract(pkg, native):
     rc = lib.gguf_hip_matmul_fused(x.data_ptr(), w.ptr(), t, n, k, y.data_ptr(), 0, None,
                                    ctypes.c_float(0.0), 0, None)
     assert rc == native.ERR_SHAPE and "no fused kernel" in native.last_error(lib)
+
+
+GEMM_TOL = 1e-3
+
+
+@pytest.mark.parametrize("t", GRID)
+@pytest.mark.parametrize("xdt", ["f16", "f32"])
+def test_gemm_matches_oracle(pkg, ref, t, xdt):
+    """The MFMA GEMM with fp16 operands (weights rounded once from the exact f32
+    dequant value): normwise and elementwise within 1e-3 of the f64 product, as
+    for the other types (tests/test_gpu_matmul.py)."""
+    for i, (m, n, k) in enumerate([(40, 70, 512), (130, 200, 768), (300, 64, 1024),
+                                   (64, 33, 4096)]):
+        raw, w = _weight(pkg, t, n, k, seed=900 * t + i)
+        wdeq = ref.dequant_rows(t, raw, n, k)
+        x = pkg.quantize.synthetic_activations(m, k, seed=40 + i,
+                                               dtype=np.float32 if xdt == "f32" else np.float16)
+        y = pkg.qlinear(torch.from_numpy(x).cuda(), w, variant=GEMM).cpu().numpy()
+        x64 = x.astype(np.float64)
+        met = ref.parity_metrics(y, ref.matmul_bt(x64, wdeq), ref.matmul_bt_abs(x64, wdeq))
+        assert met["ok"], ((NAMES[t], xdt, m, n, k), met)
+
+
+@pytest.mark.parametrize("t", GRID)
+def test_auto_takes_the_gemm_for_prefill(pkg, ref, t):
+    """f16 activations above 32 rows take the GEMM under AUTO, no workspace needed."""
+    m, n, k = 96, 48, 512
+    raw, w = _weight(pkg, t, n, k, seed=77 * t)
+    x = pkg.quantize.synthetic_activations(m, k, seed=3, dtype=np.float16)
+    y = pkg.qlinear(torch.from_numpy(x).cuda(), w).cpu().numpy()
+    wdeq = ref.dequant_rows(t, raw, n, k)
+    x64 = x.astype(np.float64)
+    met = ref.parity_metrics(y, ref.matmul_bt(x64, wdeq), ref.matmul_bt_abs(x64, wdeq))
+    assert met["ok"], (NAMES[t], met)
