@@ -1,7 +1,8 @@
 """Synthetic llama-architecture GGUF files for the loader tests.
 
 Weights are drawn in the usual [out, in] order, quantized row by row with the
-package quantizer, and written the way llama.cpp's converter lays a llama
+package quantizer (the grid-codebook IQ types, which it does not produce: random
+valid blocks), and written the way llama.cpp's converter lays a llama
 model out: Q and K rows permuted for interleaved-pair RoPE (stored row
 ``h*hd + 2j + p`` holds original row ``h*hd + p*hd/2 + j``), tensor names
 ``blk.N.attn_q.weight`` ..., ``ne = [in, out]``.  ``direct_weights`` builds the
@@ -18,6 +19,7 @@ pkg = importlib.import_module("artifex-assistantv5_amd")
 gf = importlib.import_module("artifex-assistantv5_amd.gguf_file")
 
 Q8_0, Q4_K, Q5_K, Q6_K, F32, F16, BF16 = 8, 12, 13, 14, 0, 1, 30
+GRID = (16, 17, 18, 21, 22, 29)  # IQ2_XXS, IQ2_XS, IQ3_XXS, IQ3_S, IQ2_S, IQ1_M
 
 TINY = dict(n_layers=2, d_model=256, n_heads=4, n_kv_heads=2, head_dim=64, ffn=512, vocab=384)
 
@@ -40,6 +42,12 @@ def make_model(seed=0, types=None, rope_freqs=False, tied=False, cfg=TINY):
     tensors = {}
 
     def quant(name, typ, n, k, scale=0.02):
+        if typ in GRID:  # no quantizer for the grid-codebook types: random valid blocks
+            from oracle import gguf_iq
+            raw = gguf_iq.random_blocks(typ, n * k // 256, seed=int(rng.integers(1 << 30)),
+                                        d=2.0 ** -10 if scale < 0.5 else 2.0 ** -5)
+            tensors[name] = (typ, n, k, raw)
+            return
         w = (rng.standard_normal((n, k)) * scale).astype(np.float32)
         tensors[name] = (typ, n, k, pkg.quantize.quantize(w, typ))
 

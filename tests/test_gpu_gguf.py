@@ -93,10 +93,14 @@ LOW_BIT = {"q": 11, "k": 10, "v": 23, "o": 2, "gate": 6, "up": 6, "down": 20, "e
            "out": 10}          # Q3_K, Q2_K, IQ4_XS, Q4_0, Q5_0, IQ4_NL, Q3_K table, Q2_K head
 
 
-@pytest.mark.parametrize("variant", ["mixed_qkv", "uniform_tied", "low_bit"])
+GRID_MIX = {"q": 16, "k": 17, "v": 18, "o": 21, "gate": 22, "up": 29, "down": 16, "embd": 21,
+            "out": 22}         # IQ2_XXS, IQ2_XS, IQ3_XXS, IQ3_S, IQ2_S, IQ1_M (unfused decode)
+
+
+@pytest.mark.parametrize("variant", ["mixed_qkv", "uniform_tied", "low_bit", "grid"])
 def test_decoder_from_gguf_matches_direct_build(tmp_path, variant):
     types = {"mixed_qkv": {}, "uniform_tied": {"v": 12, "down": 12, "embd": 14},
-             "low_bit": LOW_BIT}[variant]
+             "low_bit": LOW_BIT, "grid": GRID_MIX}[variant]
     tensors = gm.make_model(seed=4, types=types, tied=variant == "uniform_tied")
     p = str(tmp_path / "m.gguf")
     gm.write_model(p, tensors)
