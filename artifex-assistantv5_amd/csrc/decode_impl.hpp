@@ -1676,7 +1676,10 @@ constexpr int m1_umax(bool tight) {
 // (at most 2048 resident waves), one unit when later rounds stream in behind
 // the first anyway.  0 = all of them (the transfer is small enough to issue
 // at once).
-constexpr double kM1Flight = 12.0 * 1024 * 1024;
+#ifndef GGUF_M1_FLIGHT_MB
+#define GGUF_M1_FLIGHT_MB 12.0
+#endif
+constexpr double kM1Flight = GGUF_M1_FLIGHT_MB * 1024 * 1024;
 inline int m1_depth(int waves, int per, int unit_bytes) {
   if (waves > 2 * 2048) return 1;
   const int resident = waves < 2048 ? waves : 2048;

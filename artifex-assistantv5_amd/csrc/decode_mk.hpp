@@ -33,21 +33,22 @@
 #pragma once
 
 constexpr int kMkLd = 256 + 8;  // halves per staged row: a 16-byte pad (bank spread)
-template <int MA>
+// S: the image carries the group sums (Q4_K's mins; the IQ types have none)
+template <int MA, bool S = true>
 constexpr int mk_unit_bytes() {
-  return 16 * MA * (kMkLd * 2 + 32 + 4);
+  return 16 * MA * (kMkLd * 2 + (S ? 32 : 0) + 4);
 }
 template <int MA>
 constexpr int mk_s_off() {
   return 16 * MA * kMkLd * 2;
 }
-template <int MA>
+template <int MA, bool S = true>
 constexpr int mk_f_off() {
-  return 16 * MA * (kMkLd * 2 + 32);
+  return 16 * MA * (kMkLd * 2 + (S ? 32 : 0));
 }
 
 #ifndef GGUF_MK_LDS
-#define GGUF_MK_LDS (150 * 1024)  // shared memory a workgroup's staged range may take
+#define GGUF_MK_LDS (159 * 1024)  // shared memory a workgroup's staged range may take
 #endif
 #ifndef GGUF_MK_MIN_WGS
 #define GGUF_MK_MIN_WGS 224  // split K further while the grid has fewer workgroups
@@ -63,7 +64,7 @@ constexpr int mk_f_off() {
 #endif
 template <int TYPE, int MA>
 constexpr int mk_kw_max() {  // units a workgroup can stage
-  return (GGUF_MK_LDS - 1024 - iq_tbl_bytes<TYPE>()) / mk_unit_bytes<MA>();
+  return (GGUF_MK_LDS - 1024 - iq_tbl_bytes<TYPE>()) / mk_unit_bytes<MA, TYPE == 12>();
 }
 
 // Convert one (unit, activation row) into the unit's image block at blk;
@@ -111,7 +112,7 @@ __device__ __forceinline__ void mk_stage(const float (&v)[4], int m, int l, uint
     }
   }
   if (l == 0) {
-    float *F = (float *)(blk + mk_f_off<MA>());
+    float *F = (float *)(blk + mk_f_off<MA, SUMS>());
     F[row] = pow2f(-ex);
     if (PARTS == 2) F[row + 1] = pow2f(-ex);
   }
@@ -136,7 +137,7 @@ __global__ __launch_bounds__(256) void mk_prep_kernel(const XT *__restrict__ x, 
       for (int e = 0; e < 4; ++e) v[e] = (float)t[e];
     }
   }
-  mk_stage<PARTS, MA, QUAD, SUMS>(v, m, l, img + (size_t)u * mk_unit_bytes<MA>());
+  mk_stage<PARTS, MA, QUAD, SUMS>(v, m, l, img + (size_t)u * mk_unit_bytes<MA, SUMS>());
 }
 
 // The mins operand of lane group g: m_j for j = 4 (g & 1) + (0, 2, 1, 3).
@@ -283,7 +284,7 @@ __device__ __forceinline__ void mk_unit_iq(const Unit<TYPE> (&w)[T], int bo, int
   }
 #pragma unroll
   for (int a = 0; a < MA; ++a) {
-    const float4 F = *(const float4 *)(g_lds + bo + mk_f_off<MA>() + (16 * a + 4 * g) * 4);
+    const float4 F = *(const float4 *)(g_lds + bo + mk_f_off<MA, false>() + (16 * a + 4 * g) * 4);
     const float f[4] = {F.x, F.y, F.z, F.w};
 #pragma unroll
     for (int t = 0; t < T; ++t) {
@@ -316,7 +317,7 @@ __global__ __launch_bounds__(64 * TS * KL) void mk_kernel(const uint8_t *__restr
                                                           int K, int M, int kw,
                                                           float *__restrict__ out, int64_t ldo) {
   constexpr int PARTS = sizeof(XT) == 4 ? 2 : 1, NW = TS * KL;
-  constexpr int UB = mk_unit_bytes<MA>(), TU = Fmt<TYPE>::TU;
+  constexpr int UB = mk_unit_bytes<MA, TYPE == 12>(), TU = Fmt<TYPE>::TU;
   constexpr int CP = (mk_kw_max<TYPE, MA>() * UB / 16 + 64 * NW - 1) / (64 * NW);  // 16 B pieces per thread
   constexpr int U = (mk_kw_max<TYPE, MA>() + KL - 1) / KL;                          // unit slots per wave
   constexpr bool IQ = is_iq(TYPE);
@@ -489,8 +490,9 @@ MkPlan mk_plan(int M, int N, int K) {
   p.ts = wide ? 16 / GGUF_MK_WIDE_T : 4;
   p.kl = wide ? 1 : 4;
   p.t = wide ? GGUF_MK_WIDE_T : 1;
-  const size_t ub = p.ma == 1 ? mk_unit_bytes<1>() : p.ma == 2 ? mk_unit_bytes<2>()
-                  : p.ma == 3 ? mk_unit_bytes<3>() : mk_unit_bytes<4>();
+  constexpr bool S = TYPE == 12;
+  const size_t ub = p.ma == 1 ? mk_unit_bytes<1, S>() : p.ma == 2 ? mk_unit_bytes<2, S>()
+                  : p.ma == 3 ? mk_unit_bytes<3, S>() : mk_unit_bytes<4, S>();
   const int kw_max = p.ma == 1 ? mk_kw_max<TYPE, 1>() : p.ma == 2 ? mk_kw_max<TYPE, 2>()
                    : p.ma == 3 ? mk_kw_max<TYPE, 3>() : mk_kw_max<TYPE, 4>();
   const int ntiles = (N + 15) / 16, nu = K / 256;
