@@ -260,7 +260,8 @@ int gguf_hip_matmul_ws(const void *x, int x_type, int64_t ldx, const void *tiles
       variant == GGUF_HIP_VARIANT_DECODE
           ? gguf::launch_decode(x, x_type, ldx, (const uint8_t *)tiles, ggml_type, n, k, y, ldy, m,
                                 (float *)work, work ? work_bytes / 4 : 0, s)
-          : gguf::launch_gemm(x, x_type, ldx, (const uint8_t *)tiles, ggml_type, n, k, y, ldy, m, s);
+          : gguf::launch_gemm(x, x_type, ldx, (const uint8_t *)tiles, ggml_type, n, k, y, ldy, m,
+                              (float *)work, work ? work_bytes / 4 : 0, s);
   return hip_status(e, "matmul launch");
 }
 
@@ -281,8 +282,11 @@ int64_t gguf_hip_matmul_workspace(int ggml_type, int x_type, int64_t n, int64_t 
   if (m < 0 || n < 0 || n > ((int64_t)1 << 30) || m > ((int64_t)1 << 30))
     return fail(GGUF_HIP_ERR_SHAPE, "[gguf-hip] bad M or N");
   ok();
-  if (n == 0 || m == 0 || (m < 2 && !grid_type(ggml_type))) return 0;
-  return 4 * gguf::launch_decode_work(ggml_type, x_type, n, k, m);
+  if (n == 0 || m == 0) return 0;
+  // the larger of the decode path's and the GEMM's (AUTO may take either)
+  const int64_t dec = (m < 2 && !grid_type(ggml_type)) ? 0 : gguf::launch_decode_work(ggml_type, x_type, n, k, m);
+  const int64_t gem = m > 32 ? gguf::launch_gemm_work(ggml_type, n, k, m) : 0;
+  return 4 * (dec > gem ? dec : gem);
 }
 
 int gguf_hip_rmsnorm(const float *x, const float *w, float eps, float *y, int64_t rows,

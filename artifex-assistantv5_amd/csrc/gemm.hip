@@ -942,7 +942,7 @@ template <int TYPE, typename XT>
 __global__ __launch_bounds__(kThreads) void gemm_kernel(const XT *__restrict__ x, int64_t ldx,
                                                            const uint8_t *__restrict__ W, int M,
                                                            int N, int K, float *__restrict__ y,
-                                                           int64_t ldy, int tiles_m) {
+                                                           int64_t ldy, int tiles_m, int kunits) {
   constexpr int TU = Fmt<TYPE>::TU, UE = Fmt<TYPE>::UE;
   __shared__ __align__(16) unsigned char lds[2 * kStageB];
   __shared__ __align__(16) float rowf[kBM];  // f32 input: the rows' inverse scales 2^-e
@@ -1012,8 +1012,11 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(const XT *__restrict__ x
 
   if constexpr (UE == 256) {
     // step s = 4 u + c covers window c of superblock u; 4 nu >= 4 steps
-    s.template load<0, 0>(0, 0);
-    s.template load<1, 1>(0, 64);
+    // split K (gridDim.y > 1): units blockIdx.y kunits .. + kunits - 1, partial
+    // sums written to y + blockIdx.y M ldy
+    const int ub = blockIdx.y * kunits, ue = min(s.nu, ub + kunits);
+    s.template load<0, 0>(ub, ub * 256);
+    s.template load<1, 1>(ub, ub * 256 + 64);
     if constexpr (is_iq(TYPE)) {
       iq_put_tables<TYPE, kThreads>(tab, iqtbl);
       s.hc.tb = iqtbl;
@@ -1021,9 +1024,9 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(const XT *__restrict__ x
     }
     s.template prepare<0, 0>(0);
     __syncthreads();
-    for (int u = 0; u < s.nu; ++u) {
+    for (int u = ub; u < ue; ++u) {
       const int k = u * 256;
-      const bool more = u + 1 < s.nu;
+      const bool more = u + 1 < ue;
       s.template step<0, 1, 2>(true, true, u, k + 128);
       s.template step<1, 2, 3>(true, true, u, k + 192);
       s.template step<0, 3, 0>(true, more, u + 1, k + 256);
@@ -1043,6 +1046,7 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(const XT *__restrict__ x
     }
   }
 
+  y += (int64_t)blockIdx.y * M * ldy;  // this split's partial sums
   // D layout of the 16x16 MFMA: lane holds rows 4 g + e of column r
 #pragma unroll
   for (int i = 0; i < kTM; ++i) {
@@ -1066,56 +1070,108 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(const XT *__restrict__ x
   }
 }
 
+// y[m, n] = sum over the S splits of part[s][m][n] (M x N each), in split order.
+__global__ __launch_bounds__(256) void gemm_reduce_kernel(const float *__restrict__ part, int S,
+                                                          int M, int N, float *__restrict__ y,
+                                                          int64_t ldy) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= (int64_t)M * N) return;
+  const int64_t st = (int64_t)M * N;
+  float a = part[i];
+  for (int t = 1; t < S; ++t) a += part[i + t * st];
+  y[(i / N) * ldy + i % N] = a;
+}
+
+// Splits of K for a grid of `tiles` workgroups: while the grid leaves most CUs
+// idle (fewer than 192 tiles) and each split keeps at least 4 superblocks,
+// double the splits up to 256 workgroups (M=512, N=4096: 64 tiles, 4 splits).
+#ifndef GGUF_GEMM_SPLIT_WGS
+#define GGUF_GEMM_SPLIT_WGS 256  // the split grid stays within this many workgroups
+#endif
+#ifndef GGUF_GEMM_SPLIT_MIN
+#define GGUF_GEMM_SPLIT_MIN 4  // doubling the splits keeps at least half this many superblocks each
+#endif
+inline int gemm_splits(int type, int64_t tiles, int nu) {
+  if (unit_elems(type) != 256) return 1;
+  int sp = 1;
+  while (tiles * sp < 192 && tiles * 2 * sp <= GGUF_GEMM_SPLIT_WGS && nu >= GGUF_GEMM_SPLIT_MIN * sp) sp <<= 1;
+  return sp;
+}
+
 template <int TYPE, typename XT>
-void launch_type(const XT *x, int64_t ldx, const uint8_t *W, int M, int N, int K, float *y,
-                 int64_t ldy, hipStream_t s) {
-  const int tiles_m = (M + kBM - 1) / kBM, tiles_n = (N + kBN - 1) / kBN;
-  hipLaunchKernelGGL((gemm_kernel<TYPE, XT>), dim3((unsigned)(tiles_m * tiles_n)), dim3(kThreads),
-                     0, s, x, ldx, W, M, N, K, y, ldy, tiles_m);
+hipError_t launch_type(const XT *x, int64_t ldx, const uint8_t *W, int M, int N, int K, float *y,
+                       int64_t ldy, float *work, int64_t work_floats, hipStream_t s) {
+  const int tiles_m = (M + kBM - 1) / kBM, tiles_n = (N + kBN - 1) / kBN, nu = K / Fmt<TYPE>::UE;
+  int sp = gemm_splits(TYPE, (int64_t)tiles_m * tiles_n, nu);
+  if (!work || work_floats < (int64_t)sp * M * N) sp = 1;
+  const int kunits = (nu + sp - 1) / sp;
+  sp = (nu + kunits - 1) / kunits;
+  hipLaunchKernelGGL((gemm_kernel<TYPE, XT>), dim3((unsigned)(tiles_m * tiles_n), (unsigned)sp),
+                     dim3(kThreads), 0, s, x, ldx, W, M, N, K, sp > 1 ? work : y,
+                     sp > 1 ? (int64_t)N : ldy, tiles_m, kunits);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess || sp == 1) return e;
+  const int64_t mn = (int64_t)M * N;
+  hipLaunchKernelGGL(gemm_reduce_kernel, dim3((unsigned)((mn + 255) / 256)), dim3(256), 0, s, work,
+                     sp, M, N, y, ldy);
+  return hipGetLastError();
 }
 
 template <typename XT>
 hipError_t launch_x(const XT *x, int64_t ldx, const uint8_t *W, int type, int64_t n, int64_t k,
-                    float *y, int64_t ldy, int64_t m, hipStream_t s) {
+                    float *y, int64_t ldy, int64_t m, float *work, int64_t work_floats,
+                    hipStream_t s) {
+  hipError_t e;
   if (type == 12)
-    launch_type<12, XT>(x, ldx, W, (int)m, (int)n, (int)k, y, ldy, s);
+    e = launch_type<12, XT>(x, ldx, W, (int)m, (int)n, (int)k, y, ldy, work, work_floats, s);
   else if (type == 13)
-    launch_type<13, XT>(x, ldx, W, (int)m, (int)n, (int)k, y, ldy, s);
+    e = launch_type<13, XT>(x, ldx, W, (int)m, (int)n, (int)k, y, ldy, work, work_floats, s);
   else if (type == 8)
-    launch_type<8, XT>(x, ldx, W, (int)m, (int)n, (int)k, y, ldy, s);
+    e = launch_type<8, XT>(x, ldx, W, (int)m, (int)n, (int)k, y, ldy, work, work_floats, s);
   else if (type == 2)
-    launch_type<2, XT>(x, ldx, W, (int)m, (int)n, (int)k, y, ldy, s);
+    e = launch_type<2, XT>(x, ldx, W, (int)m, (int)n, (int)k, y, ldy, work, work_floats, s);
   else if (type == 6)
-    launch_type<6, XT>(x, ldx, W, (int)m, (int)n, (int)k, y, ldy, s);
+    e = launch_type<6, XT>(x, ldx, W, (int)m, (int)n, (int)k, y, ldy, work, work_floats, s);
   else if (type == 20)
-    launch_type<20, XT>(x, ldx, W, (int)m, (int)n, (int)k, y, ldy, s);
+    e = launch_type<20, XT>(x, ldx, W, (int)m, (int)n, (int)k, y, ldy, work, work_floats, s);
   else if (type == 23)
-    launch_type<23, XT>(x, ldx, W, (int)m, (int)n, (int)k, y, ldy, s);
+    e = launch_type<23, XT>(x, ldx, W, (int)m, (int)n, (int)k, y, ldy, work, work_floats, s);
   else if (type == 16)
-    launch_type<16, XT>(x, ldx, W, (int)m, (int)n, (int)k, y, ldy, s);
+    e = launch_type<16, XT>(x, ldx, W, (int)m, (int)n, (int)k, y, ldy, work, work_floats, s);
   else if (type == 17)
-    launch_type<17, XT>(x, ldx, W, (int)m, (int)n, (int)k, y, ldy, s);
+    e = launch_type<17, XT>(x, ldx, W, (int)m, (int)n, (int)k, y, ldy, work, work_floats, s);
   else if (type == 18)
-    launch_type<18, XT>(x, ldx, W, (int)m, (int)n, (int)k, y, ldy, s);
+    e = launch_type<18, XT>(x, ldx, W, (int)m, (int)n, (int)k, y, ldy, work, work_floats, s);
   else if (type == 21)
-    launch_type<21, XT>(x, ldx, W, (int)m, (int)n, (int)k, y, ldy, s);
+    e = launch_type<21, XT>(x, ldx, W, (int)m, (int)n, (int)k, y, ldy, work, work_floats, s);
   else if (type == 22)
-    launch_type<22, XT>(x, ldx, W, (int)m, (int)n, (int)k, y, ldy, s);
+    e = launch_type<22, XT>(x, ldx, W, (int)m, (int)n, (int)k, y, ldy, work, work_floats, s);
   else if (type == 29)
-    launch_type<29, XT>(x, ldx, W, (int)m, (int)n, (int)k, y, ldy, s);
+    e = launch_type<29, XT>(x, ldx, W, (int)m, (int)n, (int)k, y, ldy, work, work_floats, s);
   else if (type == 10)
-    launch_type<10, XT>(x, ldx, W, (int)m, (int)n, (int)k, y, ldy, s);
+    e = launch_type<10, XT>(x, ldx, W, (int)m, (int)n, (int)k, y, ldy, work, work_floats, s);
   else if (type == 11)
-    launch_type<11, XT>(x, ldx, W, (int)m, (int)n, (int)k, y, ldy, s);
+    e = launch_type<11, XT>(x, ldx, W, (int)m, (int)n, (int)k, y, ldy, work, work_floats, s);
   else
-    launch_type<14, XT>(x, ldx, W, (int)m, (int)n, (int)k, y, ldy, s);
-  return hipGetLastError();
+    e = launch_type<14, XT>(x, ldx, W, (int)m, (int)n, (int)k, y, ldy, work, work_floats, s);
+  return e;
 }
 
 }  // namespace
 
+// Workspace floats of the GEMM's K split for these shapes (0: none).
+int64_t launch_gemm_work(int type, int64_t n, int64_t k, int64_t m) {
+  const int64_t tiles = ((m + kBM - 1) / kBM) * ((n + kBN - 1) / kBN);
+  const int nu = (int)(k / unit_elems(type));
+  const int sp = m <= ((int64_t)1 << 30) / ((n + kBN - 1) / kBN) * kBM ? gemm_splits(type, tiles, nu) : 1;
+  if (sp == 1) return 0;
+  const int kunits = (nu + sp - 1) / sp;
+  return (int64_t)((nu + kunits - 1) / kunits) * m * n;
+}
+
 hipError_t launch_gemm(const void *x, int x_type, int64_t ldx, const uint8_t *tiles, int type,
-                       int64_t n, int64_t k, float *y, int64_t ldy, int64_t m, hipStream_t s) {
+                       int64_t n, int64_t k, float *y, int64_t ldy, int64_t m, float *work,
+                       int64_t work_floats, hipStream_t s) {
   const int esize = x_type == 0 ? 4 : 2;
   // one launch covers at most 2^30 output tiles; split M beyond that
   const int64_t tiles_n = (n + kBN - 1) / kBN;
@@ -1125,9 +1181,9 @@ hipError_t launch_gemm(const void *x, int x_type, int64_t ldx, const uint8_t *ti
     const int64_t mc = (m - m0) < chunk ? (m - m0) : chunk;
     const char *xb = (const char *)x + m0 * ldx * esize;
     e = x_type == 0 ? launch_x<float>((const float *)xb, ldx, tiles, type, n, k, y + m0 * ldy, ldy,
-                                      mc, s)
+                                      mc, work, work_floats, s)
                     : launch_x<half_t>((const half_t *)xb, ldx, tiles, type, n, k, y + m0 * ldy,
-                                       ldy, mc, s);
+                                       ldy, mc, work, work_floats, s);
   }
   return e;
 }

@@ -269,3 +269,33 @@ def test_batched_split_k_and_whole_k_agree(pkg, ref, t, m, n, k):
 def _metrics_decode(ref, y, x, wdeq):
     x64 = x.astype(np.float64)
     return ref.parity_metrics(y, ref.matmul_bt(x64, wdeq), ref.matmul_bt_abs(x64, wdeq))
+
+
+@pytest.mark.parametrize("t,m,n,k", [(12, 200, 300, 4096), (14, 64, 256, 2048), (23, 130, 256, 4096),
+                                     (10, 100, 512, 4096), (13, 40, 200, 4096), (11, 96, 64, 8192),
+                                     (12, 512, 4096, 4096)])
+@pytest.mark.parametrize("xdt", [np.float16, np.float32])
+def test_gemm_split_k(pkg, ref, t, m, n, k, xdt):
+    """Grids of fewer than 192 workgroups split K when given the workspace
+    (gguf_hip_matmul_workspace), adding the splits' partial sums in split order:
+    within the GEMM gate of the oracle, and within f32 rounding of the same
+    GEMM without a workspace (one K range)."""
+    lib = pkg.load_library()
+    raw, w = _case(pkg, t, n, k, seed=t * 7 + m)
+    wdeq = ref.dequant_rows(t, raw, n, k)
+    x = pkg.quantize.synthetic_activations(m, k, seed=m + k, dtype=xdt)
+    xt = torch.from_numpy(x).cuda()
+    x_type = 0 if xdt == np.float32 else 1
+    need = lib.gguf_hip_matmul_workspace(t, x_type, n, k, m)
+    assert need > 0, "this shape should split K"
+    work = torch.empty(need, dtype=torch.uint8, device="cuda")
+    y = torch.full((m, n), float("nan"), device="cuda")
+    y1 = torch.full((m, n), float("nan"), device="cuda")
+    assert lib.gguf_hip_matmul_ws(xt.data_ptr(), x_type, k, w.ptr(), t, n, k, y.data_ptr(), n, m,
+                                  GEMM, work.data_ptr(), need, None) == 0
+    assert lib.gguf_hip_matmul_variant(xt.data_ptr(), x_type, k, w.ptr(), t, n, k, y1.data_ptr(), n,
+                                       m, GEMM, None) == 0
+    torch.cuda.synchronize()
+    ys, y1s = y.cpu().numpy(), y1.cpu().numpy()
+    _check(ref, ys, x.astype(np.float32), wdeq, (t, m, n, k, "split"))
+    assert np.abs(ys - y1s).max() <= 1e-5 * np.abs(y1s).max(), (t, m, n, k)
