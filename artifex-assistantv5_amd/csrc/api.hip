@@ -248,7 +248,7 @@ int gguf_hip_matmul_ws(const void *x, int x_type, int64_t ldx, const void *tiles
                   : GGUF_HIP_VARIANT_GEMM;
   if (grid_type(ggml_type) && variant == GGUF_HIP_VARIANT_DECODE) {
     const int64_t need = 4 * gguf::launch_decode_work(ggml_type, x_type, n, k, m);
-    if (!work || work_bytes < need)
+    if (need > 0 && (!work || work_bytes < need))
       return fail(GGUF_HIP_ERR_SHAPE,
                   "[gguf-hip] ggml type %d needs a workspace of %lld bytes (gguf_hip_matmul_workspace), "
                   "got %lld", ggml_type, (long long)need, (long long)(work ? work_bytes : 0));
@@ -261,7 +261,10 @@ int gguf_hip_matmul_ws(const void *x, int x_type, int64_t ldx, const void *tiles
           ? gguf::launch_decode(x, x_type, ldx, (const uint8_t *)tiles, ggml_type, n, k, y, ldy, m,
                                 (float *)work, work ? work_bytes / 4 : 0, s)
           : gguf::launch_gemm(x, x_type, ldx, (const uint8_t *)tiles, ggml_type, n, k, y, ldy, m,
-                              (float *)work, work ? work_bytes / 4 : 0, s);
+                              work && work_bytes > gguf::kWsPrefix
+                                  ? (float *)((char *)work + gguf::kWsPrefix) : nullptr,
+                              work && work_bytes > gguf::kWsPrefix
+                                  ? (work_bytes - gguf::kWsPrefix) / 4 : 0, s);
   return hip_status(e, "matmul launch");
 }
 
@@ -285,7 +288,8 @@ int64_t gguf_hip_matmul_workspace(int ggml_type, int x_type, int64_t n, int64_t 
   if (n == 0 || m == 0) return 0;
   // the larger of the decode path's and the GEMM's (AUTO may take either)
   const int64_t dec = (m < 2 && !grid_type(ggml_type)) ? 0 : gguf::launch_decode_work(ggml_type, x_type, n, k, m);
-  const int64_t gem = m > 32 ? gguf::launch_gemm_work(ggml_type, n, k, m) : 0;
+  int64_t gem = m > 32 ? gguf::launch_gemm_work(ggml_type, n, k, m) : 0;
+  if (gem > 0) gem += gguf::kWsPrefix / 4;  // the GEMM's partial sums follow the counter prefix
   return 4 * (dec > gem ? dec : gem);
 }
 

@@ -420,6 +420,11 @@ hipError_t launch_dequant_raw(const uint8_t *raw, int type, int64_t n_elems, flo
 hipError_t launch_get_rows(const uint8_t *raw, int type, int64_t n_rows, int64_t k,
                            const int64_t *ids, int64_t n_ids, float *out, int64_t ldo,
                            hipStream_t s);
+// A matmul workspace starts with kWsPrefix bytes of counters (zero before the
+// workspace's first use; every call leaves them zero); the kernels' data
+// follows.  Only the batched decode's range reduction uses the counters, so
+// a workspace can be shared by calls of any shape and path.
+constexpr int64_t kWsPrefix = 65536;
 hipError_t launch_decode(const void *x, int x_type, int64_t ldx, const uint8_t *tiles, int type,
                          int64_t n, int64_t k, float *y, int64_t ldy, int64_t m, float *work,
                          int64_t work_floats, hipStream_t s);

@@ -1326,7 +1326,9 @@ hipError_t launch_mb(const XT *x, int64_t ldx, const uint8_t *W, int N, int K, f
   constexpr int UE = Fmt<TYPE>::UE, GS = Dec<TYPE>::GS;
   int us, nsl;
   mb_plan<TYPE, XT>(M, N, K, &us, &nsl);
-  const bool split = nsl > 1 && work && work_floats >= (int64_t)nsl * M * N;
+  // the partial sums follow the workspace's counter prefix
+  const bool split = nsl > 1 && work && work_floats >= kWsPrefix / 4 + (int64_t)nsl * M * N;
+  float *part = split ? work + kWsPrefix / 4 : nullptr;
   if (!split) {  // every workgroup walks all of K, in the widest slices that fit
     us = mb_units_per_slice<TYPE, XT>(M, K);
     nsl = (K / UE + us - 1) / us;
@@ -1345,11 +1347,11 @@ hipError_t launch_mb(const XT *x, int64_t ldx, const uint8_t *W, int N, int K, f
   const unsigned groups = (unsigned)(((N + 15) / 16 + kMbTiles - 1) / kMbTiles);
   const dim3 grid(groups, split ? (unsigned)nsl : 1u), block(kMbThreads);
   hipLaunchKernelGGL(kern, grid, block, lds, s, x, ldx, W, N, K, M, us, split ? 1 : nsl,
-                     split ? work : y, split ? (int64_t)N : ldy);
+                     split ? part : y, split ? (int64_t)N : ldy);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || !split) return e;
   const int64_t mn = (int64_t)M * N;
-  hipLaunchKernelGGL(mb_reduce_kernel, dim3((unsigned)((mn + 255) / 256)), dim3(256), 0, s, work,
+  hipLaunchKernelGGL(mb_reduce_kernel, dim3((unsigned)((mn + 255) / 256)), dim3(256), 0, s, part,
                      nsl, M, N, y, ldy);
   return hipGetLastError();
 }
@@ -1363,7 +1365,7 @@ int64_t mb_work_floats(int M, int N, int K) {
   if constexpr (TYPE == 12) return (int64_t)((mk_work_bytes<12, XT>(M, N, K) + 3) / 4);
   int us, nsl;
   mb_plan<TYPE, XT>(M, N, K, &us, &nsl);
-  return nsl > 1 ? (int64_t)nsl * M * N : 0;
+  return nsl > 1 ? kWsPrefix / 4 + (int64_t)nsl * M * N : 0;
 }
 
 // ---------------------------------------------------------------------------

@@ -6,12 +6,14 @@
 // kernel webgpu/src/shaders/matmul_gguf.wgsl:3191-3245): here the weights are
 // read once for all M rows.
 //
-// mk_prep_kernel converts the activations once per call into an image in the
-// workspace, laid out exactly as a workgroup's shared memory holds them (so
-// staging a K range is a flat copy), one block of mk_unit_bytes<MA>() per
-// 256-element unit (MA activation tiles of 16 MFMA rows each); mk_kernel
-// streams the weights; mk_reduce_kernel adds the partial sums when K is
-// split over workgroups.
+// The activations are converted into an image laid out exactly as a
+// workgroup's shared memory holds them, one block of mk_unit_bytes<MA>() per
+// 256-element unit (MA activation tiles of 16 MFMA rows each).  Up to 16 rows
+// of f32 (32 of f16, MA <= 2) each workgroup of mk_kernel converts its own K
+// range, so a call is one launch; wider batches convert once per call into
+// the workspace (mk_prep_kernel), and the workgroups copy their range.  K is
+// split over workgroups (ranges); the last range of a tile group to finish
+// adds the ranges' partial sums in range order.
 //   A [16 MA][kMkLd] f16  MFMA row 2m + p holds part p (hi, lo) of activation
 //                         row m for f32 inputs (8 rows per tile); row m holds
 //                         row m for 16-bit inputs (16 rows per tile).  The
@@ -58,6 +60,15 @@ constexpr int mk_f_off() {
 #endif
 #ifndef GGUF_MK_DEPTH_WIDE
 #define GGUF_MK_DEPTH_WIDE 2  // the same, 3 or 4 activation tiles
+#endif
+#ifndef GGUF_MK_FUSE
+#define GGUF_MK_FUSE 1  // MA <= 2: each workgroup converts its own range of x (one launch)
+#endif
+constexpr int kMkFuseKw = 4;  // units per K range when the workgroups convert their own range
+constexpr int kMkBatch = 8;  // ranges whose partial sums are requested at a time by the reduction
+constexpr int kMkOuts = 4;   // outputs a thread of the in-kernel reduction takes at a time
+#ifndef GGUF_MK_FOLD_MAX
+#define GGUF_MK_FOLD_MAX 32768  // partial sums one workgroup may add (rows x M x ranges) in-kernel
 #endif
 #ifndef GGUF_MK_WIDE_T
 #define GGUF_MK_WIDE_T 1  // row tiles per wave for 3 or 4 activation tiles (16 T tiles per workgroup)
@@ -306,20 +317,38 @@ __device__ __forceinline__ void mk_unit_iq(const Unit<TYPE> (&w)[T], int bo, int
 // K-lane w / TS), units blockIdx.y kw .. + kw - 1 of K, of which K-lane kl
 // takes every KL-th from kl.
 //
-// Order of work: every thread requests its share of the range's image, then
-// all of its tiles' units (at most U per tile); it writes the image to shared
-// memory as it lands (the weights still in flight); after the one barrier
-// each wave consumes its units in order as they arrive.  The K-lanes of a
-// tile slot are added in a fixed order through shared memory.
-template <int TYPE, typename XT, int MA, int T, int TS, int KL>
+// Order of work: every thread requests its share of the range's activations,
+// then all of its tiles' units (at most U per tile); it writes the range's
+// image to shared memory as the activations land (the weights still in
+// flight); after the one barrier each wave consumes its units in order as
+// they arrive.  The K-lanes of a tile slot are added in a fixed order through
+// shared memory.
+//
+// SX (narrow tiles, MA <= 2): the workgroup converts its own range of x into
+// the image (mk_stage, one wave per (unit, activation row)), so the call is
+// one launch.  Otherwise the image comes from the workspace (mk_prep_kernel):
+// through registers for MA <= 2, LDS-direct loads for MA 3, 4.
+//
+// K split over gridDim.y > 1 ranges: each range's partial sums go to `part`
+// ([range][M][np]); the last of a tile group's ranges to finish (an atomic
+// counter per group, cnt[blockIdx.x], zero before the call and left zero)
+// adds them in range order and writes y, so the result does not depend on
+// which range finishes last.
+template <int TYPE, typename XT, int MA, int T, int TS, int KL, bool SX>
 __global__ __launch_bounds__(64 * TS * KL) void mk_kernel(const uint8_t *__restrict__ img,
+                                                          const XT *__restrict__ x, int64_t ldx,
                                                           const uint8_t *__restrict__ W, int N,
                                                           int K, int M, int kw,
-                                                          float *__restrict__ out, int64_t ldo) {
+                                                          float *__restrict__ y, int64_t ldy,
+                                                          float *__restrict__ part,
+                                                          unsigned *__restrict__ cnt, int fold) {
   constexpr int PARTS = sizeof(XT) == 4 ? 2 : 1, NW = TS * KL;
   constexpr int UB = mk_unit_bytes<MA, TYPE == 12>(), TU = Fmt<TYPE>::TU;
-  constexpr int CP = (mk_kw_max<TYPE, MA>() * UB / 16 + 64 * NW - 1) / (64 * NW);  // 16 B pieces per thread
-  constexpr int U = (mk_kw_max<TYPE, MA>() + KL - 1) / KL;                          // unit slots per wave
+  constexpr int KWM = SX ? kMkFuseKw : mk_kw_max<TYPE, MA>();  // units a range may hold
+  constexpr int CP = SX ? 1 : (KWM * UB / 16 + 64 * NW - 1) / (64 * NW);  // 16 B pieces per thread
+  constexpr int U = (KWM + KL - 1) / KL;                                    // unit slots per wave
+  constexpr int RW = 16 * MA / PARTS;                  // activation rows of an image block
+  constexpr int SP = SX ? (KWM * RW + NW - 1) / NW : 1;  // (unit, row) pairs a wave stages
   constexpr bool IQ = is_iq(TYPE);
   // slots in flight per tile: a few MB over the chip keep the transfer at full
   // rate and the arrivals in order (all at once, they land in no useful order
@@ -332,23 +361,47 @@ __global__ __launch_bounds__(64 * TS * KL) void mk_kernel(const uint8_t *__restr
   const int ntiles = (N + 15) >> 4, nu = K >> 8;
   const int t0 = (blockIdx.x * TS + ts) * T;
   const int u0 = blockIdx.y * kw, nun = min(kw, nu - u0);
-  const int cnt = (nun - kl + KL - 1) / KL;  // the wave's units: kl + KL i, i < cnt
+  const int cnt_u = (nun - kl + KL - 1) / KL;  // the wave's units: kl + KL i, i < cnt_u
   const int tb = nu * TU;
   const int nq = nun * (UB / 16);  // 16-byte pieces of the range's image
   const int tbl = (kw * UB + 1023) & ~1023;  // IQ types: the decode tables, behind the range
 
-  // the range's image.  Narrow tiles (MA <= 2): through registers, requested
-  // ahead of the weights and written as it lands (pieces past the range repeat
-  // the last one and are not stored).  Wide tiles: LDS-direct loads in 1 KB
-  // pieces (the workspace holds 1 KB of slack past the image), no registers,
-  // before the weights are requested (the barrier waits for every load).
-  constexpr bool DMA = MA > 2;
+  // the range's activations.  SX: x itself, 4 values per lane of each
+  // (unit, row) pair the wave converts (rows past M are zeros).  Otherwise the
+  // image: narrow tiles (MA <= 2) through registers, requested ahead of the
+  // weights and written as it lands (pieces past the range repeat the last
+  // one and are not stored); wide tiles by LDS-direct loads in 1 KB pieces
+  // (the workspace holds 1 KB of slack past the image), no registers, before
+  // the weights are requested (the barrier waits for every load).
+  constexpr bool DMA = !SX && MA > 2;
   typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));  // a value type: no memcpy copies
-  const uint8_t *src = img + (size_t)u0 * UB;
-  u32x4 R[DMA ? 1 : CP];
+  const uint8_t *src = SX ? img : img + (size_t)u0 * UB;
+  u32x4 R[DMA || SX ? 1 : CP];
+  float xv[SP][4];
   IqTabRegs<TYPE, 64 * NW> tab;
   if constexpr (IQ) iq_get_tables<TYPE, 64 * NW>(tab);
-  if constexpr (DMA) {
+  if constexpr (SX) {
+#pragma unroll
+    for (int i = 0; i < SP; ++i) {
+      const int q = wave + NW * i, ul = q / RW, m = q - ul * RW;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) xv[i][e] = 0.f;
+      if (ul < nun && m < M) {  // uniform
+        const XT *p = x + (int64_t)m * ldx + 256 * (u0 + ul) + 4 * lane;
+        if constexpr (sizeof(XT) == 4) {
+          const float4 t = *(const float4 *)p;
+          xv[i][0] = t.x;
+          xv[i][1] = t.y;
+          xv[i][2] = t.z;
+          xv[i][3] = t.w;
+        } else {
+          const half4_t t = *(const half4_t *)p;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) xv[i][e] = (float)t[e];
+        }
+      }
+    }
+  } else if constexpr (DMA) {
     const int kb = (nun * UB + 1023) >> 10;
     for (int i = wave; i < kb; i += NW)
       __builtin_amdgcn_global_load_lds((const void *)(src + 1024 * i + 16 * lane),
@@ -371,13 +424,22 @@ __global__ __launch_bounds__(64 * TS * KL) void mk_kernel(const uint8_t *__restr
   // units loads its last unit (an L2 hit) and adds zero.  Under a branch or in
   // a loop the memory-counter waits lose track of the requests and wait for
   // all of them at every unit.
-  const int ulast = cnt > 0 ? kl + KL * (cnt - 1) : 0;  // a unit of the range
+  const int ulast = cnt_u > 0 ? kl + KL * (cnt_u - 1) : 0;  // a unit of the range
   Unit<TYPE> wb[P][T];
 #pragma unroll
   for (int i = 0; i < P; ++i)
 #pragma unroll
     for (int t = 0; t < T; ++t) load_unit(rs[t], (u0 + min(kl + KL * i, ulast)) * TU, r, g, wb[i][t]);
-  if constexpr (!DMA) {
+  if constexpr (SX) {
+#pragma unroll
+    for (int i = 0; i < SP; ++i) {
+      const int q = wave + NW * i, ul = q / RW, m = q - ul * RW;
+      if (ul < nun)  // uniform
+        mk_stage<PARTS, MA, TYPE == 12, TYPE == 12>(xv[i], m, lane, g_lds + ul * UB);
+    }
+    if constexpr (IQ) iq_put_tables<TYPE, 64 * NW>(tab, g_lds + tbl);
+    __syncthreads();
+  } else if constexpr (!DMA) {
 #pragma unroll
     for (int c = 0; c < CP; ++c) {
       const int q = (int)threadIdx.x + 64 * NW * c;
@@ -396,9 +458,9 @@ __global__ __launch_bounds__(64 * TS * KL) void mk_kernel(const uint8_t *__restr
 #pragma unroll
   for (int i = 0; i < U; ++i) {
     if constexpr (IQ)
-      mk_unit_iq<TYPE, MA, T>(wb[i % P], min(kl + KL * i, ulast) * UB, lane, i < cnt, tbl, acc);
+      mk_unit_iq<TYPE, MA, T>(wb[i % P], min(kl + KL * i, ulast) * UB, lane, i < cnt_u, tbl, acc);
     else
-      mk_unit<MA, T>(wb[i % P], min(kl + KL * i, ulast) * UB, lane, i < cnt, acc);
+      mk_unit<MA, T>(wb[i % P], min(kl + KL * i, ulast) * UB, lane, i < cnt_u, acc);
     if (i + P < U)  // compile-time
 #pragma unroll
       for (int t = 0; t < T; ++t)
@@ -417,43 +479,111 @@ __global__ __launch_bounds__(64 * TS * KL) void mk_kernel(const uint8_t *__restr
             red[(((((kl - 1) * TS + ts) * T + t) * MA + a) * 4 + i) * 64 + lane] = acc[t][a][i];
     }
     __syncthreads();
-    if (kl > 0) return;
+    if (kl == 0) {
 #pragma unroll
-    for (int k2 = 1; k2 < KL; ++k2)
+      for (int k2 = 1; k2 < KL; ++k2)
 #pragma unroll
-      for (int t = 0; t < T; ++t)
+        for (int t = 0; t < T; ++t)
 #pragma unroll
-        for (int a = 0; a < MA; ++a)
+          for (int a = 0; a < MA; ++a)
 #pragma unroll
-          for (int i = 0; i < 4; ++i)
-            acc[t][a][i] += red[(((((k2 - 1) * TS + ts) * T + t) * MA + a) * 4 + i) * 64 + lane];
+            for (int i = 0; i < 4; ++i)
+              acc[t][a][i] += red[(((((k2 - 1) * TS + ts) * T + t) * MA + a) * 4 + i) * 64 + lane];
+    }
   }
-  float *o = out + (int64_t)blockIdx.y * (gridDim.y > 1 ? (int64_t)M * ldo : 0);
+  // this range's sums: to y when K is not split, else to the range's partials.
+  // Partials the kernel adds itself (fold) are agent-scope atomic stores
+  // (written through to the level that every XCD sees), so publishing them
+  // needs no L2 write-back: each wave
+  // waits for its stores to complete, and after the barrier one thread counts
+  // the range.  The last range reads the partials with agent-scope atomic
+  // loads (no stale L2 copies), so it needs no L2 invalidation either.
+  const bool split = gridDim.y > 1;
+  const int np = ntiles * 16;
+  float *o = split ? part + (int64_t)blockIdx.y * M * np : y;
+  const int64_t ldo = split ? (int64_t)np : ldy;
+  auto put = [&](int m, int n, float v) {
+    if (split && fold)
+      __hip_atomic_store(o + (int64_t)m * ldo + n, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    else
+      o[(int64_t)m * ldo + n] = v;
+  };
+  if (kl == 0) {
 #pragma unroll
-  for (int t = 0; t < T; ++t) {
-    const int n = 16 * (t0 + t) + r;
-    if (n >= N) continue;
+    for (int t = 0; t < T; ++t) {
+      const int n = 16 * (t0 + t) + r;
+      if (n >= N) continue;
 #pragma unroll
-    for (int a = 0; a < MA; ++a) {
-      if (PARTS == 2) {
-        const int m = 8 * a + 2 * g;
-        if (m < M) o[(int64_t)m * ldo + n] = acc[t][a][0] + acc[t][a][1];
-        if (m + 1 < M) o[(int64_t)(m + 1) * ldo + n] = acc[t][a][2] + acc[t][a][3];
-      } else {
+      for (int a = 0; a < MA; ++a) {
+        if (PARTS == 2) {
+          const int m = 8 * a + 2 * g;
+          if (m < M) put(m, n, acc[t][a][0] + acc[t][a][1]);
+          if (m + 1 < M) put(m + 1, n, acc[t][a][2] + acc[t][a][3]);
+        } else {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int m = 16 * a + 4 * g + i;
-          if (m < M) o[(int64_t)m * ldo + n] = acc[t][a][i];
+          for (int i = 0; i < 4; ++i) {
+            const int m = 16 * a + 4 * g + i;
+            if (m < M) put(m, n, acc[t][a][i]);
+          }
         }
       }
     }
   }
+  if (!split || !fold) return;  // (not fold: mk_reduce_kernel adds the partials)
+  // the last range of the tile group to finish adds the partials in range order
+  __shared__ unsigned last;
+  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wave's partials are stored
+  __syncthreads();
+  if (threadIdx.x == 0)
+    last = __hip_atomic_fetch_add(cnt + blockIdx.x, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+                   gridDim.y - 1 ? 1u : 0u;
+  __syncthreads();
+  if (!last) return;
+  // kMkOuts outputs per thread at a time, their partials requested kMkBatch
+  // ranges at a time
+  constexpr int RG = 16 * TS * T;  // rows of the tile group
+  const int n0 = RG * blockIdx.x, S = gridDim.y;
+  const int64_t st = (int64_t)M * np;
+  for (int e0 = threadIdx.x; e0 < M * RG; e0 += 64 * NW * kMkOuts) {
+    float *p[kMkOuts];
+    bool ok[kMkOuts];
+    float a[kMkOuts];
+#pragma unroll
+    for (int j = 0; j < kMkOuts; ++j) {
+      const int e = e0 + 64 * NW * j, m = e / RG, n = n0 + (e - m * RG);
+      ok[j] = e < M * RG && n < N;
+      p[j] = part + (ok[j] ? (int64_t)m * np + n : 0);
+      a[j] = __hip_atomic_load(p[j], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    for (int s0 = 1; s0 < S; s0 += kMkBatch) {
+      float v[kMkOuts][kMkBatch];
+#pragma unroll
+      for (int j = 0; j < kMkOuts; ++j)
+#pragma unroll
+        for (int s = 0; s < kMkBatch; ++s)
+          v[j][s] = s0 + s < S ? __hip_atomic_load(p[j] + (s0 + s) * st, __ATOMIC_RELAXED,
+                                                   __HIP_MEMORY_SCOPE_AGENT)
+                               : 0.f;
+#pragma unroll
+      for (int j = 0; j < kMkOuts; ++j)
+#pragma unroll
+        for (int s = 0; s < kMkBatch; ++s)
+          if (s0 + s < S) a[j] += v[j][s];
+    }
+#pragma unroll
+    for (int j = 0; j < kMkOuts; ++j) {
+      if (!ok[j]) continue;
+      const int e = e0 + 64 * NW * j, m = e / RG, n = n0 + (e - m * RG);
+      y[(int64_t)m * ldy + n] = a[j];
+    }
+  }
+  if (threadIdx.x == 0)  // ready for the next call
+    __hip_atomic_store(cnt + blockIdx.x, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// y[m, n] = sum over the S ranges of part[s][m][n] (row stride np), in
-// order.  One output element per thread; the partials are requested
-// kMkBatch at a time, then added.
-constexpr int kMkBatch = 32;
+// y[m, n] = sum over the S ranges of part[s][m][n] (row stride np), in range
+// order: the reduction of K ranges too many for the in-kernel one.  One
+// output element per thread; the partials are requested kMkBatch at a time.
 __global__ __launch_bounds__(256) void mk_reduce_kernel(const float *__restrict__ part, int S, int M,
                                                         int np, int N, float *__restrict__ y,
                                                         int64_t ldy) {
@@ -462,38 +592,50 @@ __global__ __launch_bounds__(256) void mk_reduce_kernel(const float *__restrict_
   const float *p = part + (int64_t)m * np + n;
   const int64_t st = (int64_t)M * np;
   float a = p[0];
-  for (int s0 = 0; s0 < S; s0 += kMkBatch) {
+  for (int s0 = 1; s0 < S; s0 += kMkBatch) {
     float v[kMkBatch];
 #pragma unroll
     for (int s = 0; s < kMkBatch; ++s) v[s] = s0 + s < S ? p[(s0 + s) * st] : 0.f;
 #pragma unroll
     for (int s = 0; s < kMkBatch; ++s)
-      if (s0 + s > 0 && s0 + s < S) a += v[s];
+      if (s0 + s < S) a += v[s];
   }
   y[(int64_t)m * ldy + n] = a;
 }
 
 // Launch shape: MA activation tiles; TS tile slots x KL K-lanes of T tiles
-// per workgroup (more tiles share each staged unit when the staging is
-// large); K split into `ranges` of kw units, as few as the shared memory
-// allows, more while the grid has fewer than GGUF_MK_MIN_WGS workgroups.
+// per workgroup; K split into `ranges` of kw units.
+//   SX (MA <= 2): 16 tiles per workgroup, one per wave; ranges of at most
+//     kMkFuseKw units (the conversion each workgroup does stays small), more
+//     while the grid has fewer than GGUF_MK_MIN_WGS workgroups.
+//   Otherwise: as few ranges as the shared memory allows (the image comes
+//     from the prep launch), more while the grid has fewer than
+//     GGUF_MK_MIN_WGS workgroups.
+// Workspace: the tile groups' counters in the counter prefix (split K only),
+// then, from kWsPrefix on, the image (not SX) and the ranges' partial sums
+// (split K only).  mk_plan takes at most kMkMaxGroups tile groups (the
+// counters the prefix holds); launch_mk runs wider weights in row blocks.
+constexpr int kMkMaxGroups = (int)(kWsPrefix / 4);
 struct MkPlan {
   int ma, ts, kl, t, groups, kw, ranges;
-  size_t lds, part_off, bytes;  // workspace: the image, then the ranges' partial sums
+  bool sx, fold;  // fold: the last range of a tile group adds the partials
+  size_t lds, part_off, bytes;  // part_off: from the start of the workspace
 };
 template <int TYPE, typename XT>
 MkPlan mk_plan(int M, int N, int K) {
   constexpr int PARTS = sizeof(XT) == 4 ? 2 : 1;
   MkPlan p;
   p.ma = (M * PARTS + 15) / 16;
+  p.sx = GGUF_MK_FUSE && p.ma <= 2;
   const bool wide = p.ma > 2;
-  p.ts = wide ? 16 / GGUF_MK_WIDE_T : 4;
-  p.kl = wide ? 1 : 4;
-  p.t = wide ? GGUF_MK_WIDE_T : 1;
+  p.ts = p.sx ? 16 : wide ? 16 / GGUF_MK_WIDE_T : 4;
+  p.kl = p.sx || wide ? 1 : 4;
+  p.t = !p.sx && wide ? GGUF_MK_WIDE_T : 1;
   constexpr bool S = TYPE == 12;
   const size_t ub = p.ma == 1 ? mk_unit_bytes<1, S>() : p.ma == 2 ? mk_unit_bytes<2, S>()
                   : p.ma == 3 ? mk_unit_bytes<3, S>() : mk_unit_bytes<4, S>();
-  const int kw_max = p.ma == 1 ? mk_kw_max<TYPE, 1>() : p.ma == 2 ? mk_kw_max<TYPE, 2>()
+  const int kw_max = p.sx ? kMkFuseKw
+                   : p.ma == 1 ? mk_kw_max<TYPE, 1>() : p.ma == 2 ? mk_kw_max<TYPE, 2>()
                    : p.ma == 3 ? mk_kw_max<TYPE, 3>() : mk_kw_max<TYPE, 4>();
   const int ntiles = (N + 15) / 16, nu = K / 256;
   p.groups = (ntiles + p.ts * p.t - 1) / (p.ts * p.t);
@@ -501,37 +643,46 @@ MkPlan mk_plan(int M, int N, int K) {
   while (ranges < nu && (int64_t)p.groups * ranges < GGUF_MK_MIN_WGS) ++ranges;
   p.kw = (nu + ranges - 1) / ranges;
   p.ranges = (nu + p.kw - 1) / p.kw;
+  p.fold = p.ranges > 1 && (int64_t)p.ts * p.t * 16 * M * p.ranges <= GGUF_MK_FOLD_MAX;
   const size_t stage = ((size_t)p.kw * ub + 1023) & ~(size_t)1023;
   const size_t red = (size_t)(p.kl - 1) * p.ts * p.t * p.ma * 4 * 64 * 4;
   const size_t used = stage + iq_tbl_bytes<TYPE>();  // the tables sit behind the range
   p.lds = used > red ? used : red;
-  p.part_off = ((size_t)nu * ub + 1024 + 255) & ~(size_t)255;  // 1 KB slack for 1 KB copy pieces
-  p.bytes = p.part_off + (p.ranges > 1 ? (size_t)p.ranges * M * ntiles * 16 * 4 : 0);
+  // 1 KB slack past the image for the 1 KB copy pieces
+  const size_t img = p.sx ? 0 : ((size_t)nu * ub + 1024 + 255) & ~(size_t)255;
+  const size_t parts = p.ranges > 1 ? (size_t)p.ranges * M * ntiles * 16 * 4 : 0;
+  p.part_off = (size_t)kWsPrefix + img;
+  p.bytes = img + parts > 0 ? p.part_off + parts : 0;
   return p;
 }
 
-template <int TYPE, typename XT, int MA, int T, int TS, int KL>
+template <int TYPE, typename XT, int MA, int T, int TS, int KL, bool SX>
 hipError_t launch_mk_ma(const XT *x, int64_t ldx, const uint8_t *W, int N, int K, float *y,
                         int64_t ldy, int M, float *work, const MkPlan &p, hipStream_t s) {
   constexpr int PARTS = sizeof(XT) == 4 ? 2 : 1;
-  const int np = (N + 15) / 16 * 16;
-  uint8_t *img = (uint8_t *)work;
-  float *part = (float *)(img + p.part_off);
-  hipLaunchKernelGGL((mk_prep_kernel<XT, MA, TYPE == 12, TYPE == 12>), dim3((unsigned)(K / 256), (unsigned)(16 * MA / PARTS / 4)),
-                     dim3(256), 0, s, x, ldx, M, img);
-  hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return e;
-  auto kern = mk_kernel<TYPE, XT, MA, T, TS, KL>;
+  uint8_t *ws = (uint8_t *)work, *img = ws + kWsPrefix;
+  hipError_t e = hipSuccess;
+  if constexpr (!SX) {
+    hipLaunchKernelGGL((mk_prep_kernel<XT, MA, TYPE == 12, TYPE == 12>),
+                       dim3((unsigned)(K / 256), (unsigned)(16 * MA / PARTS / 4)), dim3(256), 0, s,
+                       x, ldx, M, img);
+    e = hipGetLastError();
+    if (e != hipSuccess) return e;
+  }
+  auto kern = mk_kernel<TYPE, XT, MA, T, TS, KL, SX>;
   if (p.lds > 65536) {
     e = hipFuncSetAttribute((const void *)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)p.lds);
     if (e != hipSuccess) return e;
   }
   hipLaunchKernelGGL(kern, dim3((unsigned)p.groups, (unsigned)p.ranges), dim3(64 * TS * KL), p.lds, s,
-                     img, W, N, K, M, p.kw, p.ranges > 1 ? part : y, p.ranges > 1 ? (int64_t)np : ldy);
+                     img, x, ldx, W, N, K, M, p.kw, y, ldy,
+                     p.ranges > 1 ? (float *)(ws + p.part_off) : nullptr,
+                     p.ranges > 1 ? (unsigned *)ws : nullptr, p.fold ? 1 : 0);
   e = hipGetLastError();
-  if (e != hipSuccess || p.ranges == 1) return e;
+  if (e != hipSuccess || p.ranges == 1 || p.fold) return e;
+  const int np = (N + 15) / 16 * 16;
   hipLaunchKernelGGL(mk_reduce_kernel, dim3((unsigned)((N + 255) / 256), (unsigned)M), dim3(256), 0, s,
-                     part, p.ranges, M, np, N, y, ldy);
+                     (const float *)(ws + p.part_off), p.ranges, M, np, N, y, ldy);
   return hipGetLastError();
 }
 
@@ -547,12 +698,28 @@ template <int TYPE, typename XT>
 hipError_t launch_mk(const XT *x, int64_t ldx, const uint8_t *W, int N, int K, float *y,
                      int64_t ldy, int M, float *work, int64_t work_floats, hipStream_t s) {
   const MkPlan p = mk_plan<TYPE, XT>(M, N, K);
-  if (M > 32 || !work || (size_t)work_floats * 4 < p.bytes)
+  if (M > 32 || (p.bytes > 0 && (!work || (size_t)work_floats * 4 < p.bytes)))
     return hipErrorNotSupported;
+  if (p.ranges > 1 && p.groups > kMkMaxGroups) {
+    // more tile groups than counters: blocks of rows, one launch each (in
+    // stream order, so each block finds the counters zero again)
+    const int rb = kMkMaxGroups * p.ts * p.t * 16;
+    const int64_t tb = (int64_t)(K / 256) * Fmt<TYPE>::TU;
+    for (int n0 = 0; n0 < N; n0 += rb) {
+      const hipError_t e = launch_mk<TYPE, XT>(x, ldx, W + (int64_t)(n0 / 16) * tb, min(rb, N - n0),
+                                               K, y + n0, ldy, M, work, work_floats, s);
+      if (e != hipSuccess) return e;
+    }
+    return hipSuccess;
+  }
+  if (p.sx) {
+    if (p.ma == 1) return launch_mk_ma<TYPE, XT, 1, 1, 16, 1, true>(x, ldx, W, N, K, y, ldy, M, work, p, s);
+    return launch_mk_ma<TYPE, XT, 2, 1, 16, 1, true>(x, ldx, W, N, K, y, ldy, M, work, p, s);
+  }
   switch (p.ma) {  // the shapes mk_plan assumes for each MA
-    case 1: return launch_mk_ma<TYPE, XT, 1, 1, 4, 4>(x, ldx, W, N, K, y, ldy, M, work, p, s);
-    case 2: return launch_mk_ma<TYPE, XT, 2, 1, 4, 4>(x, ldx, W, N, K, y, ldy, M, work, p, s);
-    case 3: return launch_mk_ma<TYPE, XT, 3, GGUF_MK_WIDE_T, 16 / GGUF_MK_WIDE_T, 1>(x, ldx, W, N, K, y, ldy, M, work, p, s);
-    default: return launch_mk_ma<TYPE, XT, 4, GGUF_MK_WIDE_T, 16 / GGUF_MK_WIDE_T, 1>(x, ldx, W, N, K, y, ldy, M, work, p, s);
+    case 1: return launch_mk_ma<TYPE, XT, 1, 1, 4, 4, false>(x, ldx, W, N, K, y, ldy, M, work, p, s);
+    case 2: return launch_mk_ma<TYPE, XT, 2, 1, 4, 4, false>(x, ldx, W, N, K, y, ldy, M, work, p, s);
+    case 3: return launch_mk_ma<TYPE, XT, 3, GGUF_MK_WIDE_T, 16 / GGUF_MK_WIDE_T, 1, false>(x, ldx, W, N, K, y, ldy, M, work, p, s);
+    default: return launch_mk_ma<TYPE, XT, 4, GGUF_MK_WIDE_T, 16 / GGUF_MK_WIDE_T, 1, false>(x, ldx, W, N, K, y, ldy, M, work, p, s);
   }
 }

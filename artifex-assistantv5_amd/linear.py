@@ -284,6 +284,27 @@ def _row_stride(t: torch.Tensor, rows: int, cols: int, name: str) -> int:
     return t.stride(0) if rows > 1 else max(t.stride(0), cols)
 
 
+# One matmul workspace per device, grown on demand.  Its counter prefix must
+# be zero before first use and every call leaves it zero, so it is allocated
+# zero-filled once and shared by every call on the device (calls on one device
+# run in stream order here).  A workspace that is outgrown stays allocated:
+# a captured graph may still address it.
+_WORKSPACES: dict = {}
+_OUTGROWN: list = []
+
+
+def matmul_workspace(dev: torch.device, nbytes: int) -> torch.Tensor:
+    """The device's shared, zero-initialised matmul workspace of at least ``nbytes``."""
+    key = dev.index if dev.index is not None else torch.cuda.current_device()
+    ws = _WORKSPACES.get(key)
+    if ws is None or ws.numel() < nbytes:
+        if ws is not None:
+            _OUTGROWN.append(ws)
+        ws = torch.zeros(max(nbytes, 1 << 20), dtype=torch.uint8, device=dev)
+        _WORKSPACES[key] = ws
+    return ws
+
+
 def dispatch_matmul_gguf(a: torch.Tensor, gg: GGUFWeight, c: torch.Tensor, M: int, N: int,
                          K: int, label: str = "", io: Optional[dict] = None,
                          variant: int = _native.VARIANT_AUTO) -> None:
@@ -315,11 +336,9 @@ def dispatch_matmul_gguf(a: torch.Tensor, gg: GGUFWeight, c: torch.Tensor, M: in
         raise ValueError(f'matmul_gguf "{label}": C window out of range')
     dev = gg.device
     x_type = _X_TYPES[a.dtype]
-    # the split-K batched decode's workspace (partial sums of the K slices), taken
-    # from torch's caching allocator: stream-ordered, and from the graph's pool
-    # under capture
+    # the split-K paths' workspace (counters, partial sums of the K slices)
     need = _native.check(lib.gguf_hip_matmul_workspace(gg.ggml_type, x_type, N, K, M), lib)
-    work = torch.empty(need, dtype=torch.uint8, device=dev) if need > 0 else None
+    work = matmul_workspace(dev, need) if need > 0 else None
     with torch.cuda.device(dev):
         _native.check(lib.gguf_hip_matmul_ws(
             a.data_ptr() + a_off, x_type, ldx, gg.ptr(), gg.ggml_type, N, K,

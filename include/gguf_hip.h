@@ -49,7 +49,7 @@ extern "C" {
  * are exported (kernels and helpers cannot be interposed across libraries). */
 #pragma GCC visibility push(default)
 
-#define GGUF_HIP_ABI_VERSION 14
+#define GGUF_HIP_ABI_VERSION 15
 
 /* ggml type ids (gguf.ts:24-35); activation dtypes reuse F32 / F16. */
 #define GGUF_HIP_F32 0
@@ -171,16 +171,24 @@ int gguf_hip_matmul_variant(const void *x, int x_type, int64_t ldx, const void *
  * work_bytes long; NULL / 0 = none).  With at least gguf_hip_matmul_workspace
  * bytes, a decode pass of 2..32 activation rows, and a GEMM whose output tiles
  * leave most CUs idle (fewer than 192 of 128 x 256; superblock types), split K
- * over the grid and add the slices' partial sums in a fixed order (a second
- * launch): the same results as without a workspace up to f32 rounding of the
- * sums, deterministic either way, and much faster for weights of few rows (the
- * FFN down projection) and short prefills (M = 512, N = 4096: 258 -> 476 TFLOP/s).
+ * over the grid and add the slices' partial sums in a fixed order: the same
+ * results as without a workspace up to f32 rounding of the sums,
+ * deterministic either way, and much faster for weights of few rows (the FFN
+ * down projection) and short prefills (M = 512, N = 4096: 258 -> 476
+ * TFLOP/s).  The batched decode of Q4_K and the grid-codebook types is then
+ * one launch up to 16 f32 (32 f16) rows: each workgroup converts its own K
+ * range of the activations, and the last K range of a row block to finish
+ * adds the ranges' sums (counted in the workspace).
+ * The workspace's first 65536 bytes are those counters: they must be zero
+ * before the workspace's first use (allocate it zero-filled), and every call
+ * leaves them zero, so one workspace serves calls of any shape and type.
  * The reference engine likewise preallocates its scratch (forward-pass.ts:1140-1163).
  * Calls that share a workspace must not overlap.
  * The grid-codebook IQ types need the workspace whenever the decode variant
- * runs (AUTO picks it as for the other types), M = 1 included: without one it
- * returns GGUF_HIP_ERR_SHAPE, so gguf_hip_matmul and gguf_hip_matmul_variant
- * take them only where AUTO / GEMM choose the GEMM. */
+ * runs (AUTO picks it as for the other types) and gguf_hip_matmul_workspace
+ * reports a nonzero size, M = 1 included: without one they return
+ * GGUF_HIP_ERR_SHAPE, so gguf_hip_matmul and gguf_hip_matmul_variant take them
+ * only where AUTO / GEMM choose the GEMM. */
 int gguf_hip_matmul_ws(const void *x, int x_type, int64_t ldx, const void *tiles, int ggml_type,
                        int64_t n, int64_t k, float *y, int64_t ldy, int64_t m, int variant,
                        void *work, int64_t work_bytes, void *stream);

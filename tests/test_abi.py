@@ -94,7 +94,7 @@ def test_grid_types_contract(lib, native):
 
 
 def test_abi_version(lib):
-    assert lib.gguf_hip_abi_version() == 14
+    assert lib.gguf_hip_abi_version() == 15
 
 
 def test_type_traits(lib, native):

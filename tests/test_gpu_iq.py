@@ -111,7 +111,7 @@ def test_api_contract(pkg, native):
         assert need > 0
         rc = lib.gguf_hip_matmul(x.data_ptr(), 0, k, w.ptr(), t, n, k, y.data_ptr(), n, mm, None)
         assert rc == native.ERR_SHAPE and "workspace" in native.last_error(lib)
-        ws = torch.empty(need, dtype=torch.uint8, device="cuda")
+        ws = torch.zeros(need, dtype=torch.uint8, device="cuda")  # counters start at zero
         rc = lib.gguf_hip_matmul_ws(x.data_ptr(), 0, k, w.ptr(), t, n, k, y.data_ptr(), n, mm,
                                     AUTO, ws.data_ptr(), need - 1, None)
         assert rc == native.ERR_SHAPE

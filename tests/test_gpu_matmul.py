@@ -253,7 +253,7 @@ def test_batched_split_k_and_whole_k_agree(pkg, ref, t, m, n, k):
     outs = []
     for use_ws in (True, False):
         y = torch.full((m, n), float("nan"), device="cuda")
-        work = torch.empty(max(need, 16), dtype=torch.uint8, device="cuda") if use_ws else None
+        work = torch.zeros(max(need, 16), dtype=torch.uint8, device="cuda") if use_ws else None
         rc = lib.gguf_hip_matmul_ws(xt.data_ptr(), 0, k, w.ptr(), t, n, k, y.data_ptr(), n, m, DECODE,
                                     work.data_ptr() if use_ws else None, need if use_ws else 0, s)
         assert rc == 0, lib.gguf_hip_last_error()
@@ -288,7 +288,7 @@ def test_gemm_split_k(pkg, ref, t, m, n, k, xdt):
     x_type = 0 if xdt == np.float32 else 1
     need = lib.gguf_hip_matmul_workspace(t, x_type, n, k, m)
     assert need > 0, "this shape should split K"
-    work = torch.empty(need, dtype=torch.uint8, device="cuda")
+    work = torch.zeros(need, dtype=torch.uint8, device="cuda")
     y = torch.full((m, n), float("nan"), device="cuda")
     y1 = torch.full((m, n), float("nan"), device="cuda")
     assert lib.gguf_hip_matmul_ws(xt.data_ptr(), x_type, k, w.ptr(), t, n, k, y.data_ptr(), n, m,
@@ -299,3 +299,45 @@ def test_gemm_split_k(pkg, ref, t, m, n, k, xdt):
     ys, y1s = y.cpu().numpy(), y1.cpu().numpy()
     _check(ref, ys, x.astype(np.float32), wdeq, (t, m, n, k, "split"))
     assert np.abs(ys - y1s).max() <= 1e-5 * np.abs(y1s).max(), (t, m, n, k)
+
+
+@pytest.mark.gpu
+def test_shared_workspace_counters_stay_zero(pkg, ref):
+    """One workspace serves, in turn, the batched decode with K split over the
+    grid (one launch: the last K range of each tile group adds the partials,
+    counted in the workspace's counter prefix), the split-K GEMM and the
+    other types' split decode; up to 16 f32 rows the batched decode converts
+    the activations in every workgroup, 32 f32 rows go through the prep
+    launch.  The counter prefix reads zero after every call, and each call
+    repeats its first result exactly."""
+    lib = pkg.load_library()
+    cases = [(12, 8, 4096, 4096, 0, DECODE), (12, 3, 1024, 2048, 1, DECODE),
+             (12, 512, 4096, 4096, 1, GEMM), (14, 8, 512, 4096, 0, DECODE),
+             (12, 16, 2048, 14336, 0, DECODE), (12, 32, 4096, 4096, 1, DECODE),
+             (12, 32, 1024, 4096, 0, DECODE)]
+    need = max(lib.gguf_hip_matmul_workspace(t, xt_, n, k, m) for t, m, n, k, xt_, _ in cases)
+    work = torch.zeros(need, dtype=torch.uint8, device="cuda")
+    s = torch.cuda.current_stream().cuda_stream
+    runs = []
+    for t, m, n, k, x_type, var in cases:
+        raw, w = _case(pkg, t, n, k, seed=t + m)
+        x = pkg.quantize.synthetic_activations(m, k, seed=m + n,
+                                               dtype=np.float16 if x_type else np.float32)
+        runs.append((t, m, n, k, x_type, var, w, torch.from_numpy(x).cuda(), raw, x))
+    first = []
+    for rep in range(2):
+        for i, (t, m, n, k, x_type, var, w, xt, raw, x) in enumerate(runs):
+            y = torch.full((m, n), float("nan"), device="cuda")
+            rc = lib.gguf_hip_matmul_ws(xt.data_ptr(), x_type, k, w.ptr(), t, n, k, y.data_ptr(), n,
+                                        m, var, work.data_ptr(), need, s)
+            assert rc == 0, lib.gguf_hip_last_error()
+            torch.cuda.synchronize()
+            assert int(work[:65536].count_nonzero()) == 0, ("counter prefix", t, m, n, k)
+            if rep == 0:
+                first.append(y)
+                if var == DECODE and x_type == 0:
+                    wdeq = ref.dequant_rows(t, raw, n, k)
+                    met = _metrics_decode(ref, y.cpu().numpy(), x, wdeq)
+                    assert met["finite"] and met["elemwise"] <= DECODE_TOL, ((t, m, n, k), met)
+            else:
+                assert torch.equal(y, first[i]), ("repeat", t, m, n, k)
