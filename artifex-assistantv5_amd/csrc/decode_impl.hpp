@@ -1409,6 +1409,9 @@ int64_t mb_work_floats(int M, int N, int K) {
 //      rows), and y[16 m + r] = up * silu(gate) (N / 2 outputs), so the FFN
 //      activation never takes a separate pass.
 // ---------------------------------------------------------------------------
+#ifndef GGUF_M1_PRIO
+#define GGUF_M1_PRIO 1  // wave priority from the units still to do
+#endif
 template <int TYPE, typename XT, int U, int XI, int PRO, int DP>
 __global__ __launch_bounds__(512) void decode_m1_kernel(const XT *__restrict__ x,
                                                         const uint8_t *__restrict__ W, int N,
@@ -1596,6 +1599,18 @@ __global__ __launch_bounds__(512) void decode_m1_kernel(const XT *__restrict__ x
   float acc = 0.f;
 #pragma unroll
   for (int j = 0; j < U; ++j) {
+    // Wave priority from the units still to do (3 while at least 6 remain,
+    // down to 0 for the last): the two waves of a SIMD otherwise issue oldest
+    // first, and the younger one finished its units ~1 us after the older one
+    // at the headline shape (per-wave timestamps), which set the kernel's
+    // length.  The wave that is behind now issues first.
+    if (GGUF_M1_PRIO) {
+      const int rem = U - j;
+      if (rem >= 6) __builtin_amdgcn_s_setprio(3);
+      else if (rem >= 4) __builtin_amdgcn_s_setprio(2);
+      else if (rem >= 2) __builtin_amdgcn_s_setprio(1);
+      else __builtin_amdgcn_s_setprio(0);
+    }
     const int u = ks + ks_n * j;
     const bool valid = u < nu;  // implies j < iters
     float t = 0.f;
@@ -1609,6 +1624,7 @@ __global__ __launch_bounds__(512) void decode_m1_kernel(const XT *__restrict__ x
       __builtin_amdgcn_sched_barrier(0);
     }
   }
+  if (GGUF_M1_PRIO) __builtin_amdgcn_s_setprio(0);
   acc = sum_xor32(sum_xor16(acc));  // the four lane groups of each row
   float scale = 1.0f;
   if constexpr (PRO == 1) {
