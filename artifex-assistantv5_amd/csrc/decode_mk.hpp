@@ -457,6 +457,15 @@ __global__ __launch_bounds__(64 * TS * KL) void mk_kernel(const uint8_t *__restr
       for (int i = 0; i < 4; ++i) acc[t][a][i] = 0.f;
 #pragma unroll
   for (int i = 0; i < U; ++i) {
+    // wave priority from the units still to do: the waves of a SIMD otherwise
+    // issue oldest first and the youngest finishes last
+    {
+      const int rem = U - i;
+      if (rem >= 4) __builtin_amdgcn_s_setprio(3);
+      else if (rem == 3) __builtin_amdgcn_s_setprio(2);
+      else if (rem == 2) __builtin_amdgcn_s_setprio(1);
+      else __builtin_amdgcn_s_setprio(0);
+    }
     if constexpr (IQ)
       mk_unit_iq<TYPE, MA, T>(wb[i % P], min(kl + KL * i, ulast) * UB, lane, i < cnt_u, tbl, acc);
     else
@@ -466,6 +475,7 @@ __global__ __launch_bounds__(64 * TS * KL) void mk_kernel(const uint8_t *__restr
       for (int t = 0; t < T; ++t)
         load_unit(rs[t], (u0 + min(kl + KL * (i + P), ulast)) * TU, r, g, wb[i % P][t]);
   }
+  __builtin_amdgcn_s_setprio(0);
   if constexpr (KL > 1) {  // K-lanes 1 .. KL - 1 hand their sums to lane 0, added in order
     __syncthreads();  // the staged activations are consumed
     float *red = (float *)g_lds;  // [KL - 1][TS][T][MA][4][64]
