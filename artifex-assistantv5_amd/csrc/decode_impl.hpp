@@ -1732,6 +1732,13 @@ hipError_t launch_m1(const XT *x, const uint8_t *W, int N, int K, float *y, cons
           (UE == 32 && 2 * ntiles * ks <= GGUF_M1_ROUND_WAVES) ||
           (GGUF_M1_FILL && 2 * ntiles * ks <= GGUF_M1_ROUND_WAVES && nu >= 8 * ks)))
     ks <<= 1;
+  // 2- and 3-bit K-quants: the most VALU per byte, and a wave's units decode
+  // one after another on its own dependency chain, so one more K split while
+  // the grid stays under 4096 waves and every wave keeps 4 units (14336 x
+  // 4096: Q2_K 2193 -> 2384 GB/s, Q3_K 2432 -> 2646; IQ4_XS lost 4% with it,
+  // and 2 units per wave lost a third)
+  if (TYPE == 10 || TYPE == 11)
+    while (ks < ks_max && ks < nu && ntiles * ks < 4096 && nu >= 8 * ks) ks <<= 1;
   const int per = (nu + ks - 1) / ks;
   if (per > umax) return hipErrorNotSupported;
   // 8 waves per workgroup (half as many workgroups staging the activations)
