@@ -1101,6 +1101,33 @@ __global__ __launch_bounds__(256) void gemm_reduce_kernel(const float *__restric
   y[(i / N) * ldy + i % N] = a;
 }
 
+// The same, four outputs per thread (N and ldy multiples of 4, y 16-byte
+// aligned), the splits' partials requested four at a time; the same order of
+// additions.
+__global__ __launch_bounds__(256) void gemm_reduce4_kernel(const float4 *__restrict__ part, int S,
+                                                           int M, int N4, float *__restrict__ y,
+                                                           int64_t ldy) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= (int64_t)M * N4) return;
+  const int64_t st = (int64_t)M * N4;
+  float4 a = part[i];
+  for (int t0 = 1; t0 < S; t0 += 4) {
+    float4 v[4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) v[t] = t0 + t < S ? part[i + (t0 + t) * st] : make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+      if (t0 + t < S) {
+        a.x += v[t].x;
+        a.y += v[t].y;
+        a.z += v[t].z;
+        a.w += v[t].w;
+      }
+  }
+  const int64_t m = i / N4;
+  *(float4 *)(y + m * ldy + 4 * (i - m * N4)) = a;
+}
+
 // Splits of K for a grid of `tiles` workgroups: while the grid leaves most CUs
 // idle (fewer than 192 tiles) and each split keeps at least 4 superblocks,
 // double the splits up to 256 workgroups (M=512, N=4096: 64 tiles, 4 splits).
@@ -1131,8 +1158,12 @@ hipError_t launch_type(const XT *x, int64_t ldx, const uint8_t *W, int M, int N,
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || sp == 1) return e;
   const int64_t mn = (int64_t)M * N;
-  hipLaunchKernelGGL(gemm_reduce_kernel, dim3((unsigned)((mn + 255) / 256)), dim3(256), 0, s, work,
-                     sp, M, N, y, ldy);
+  if (N % 4 == 0 && ldy % 4 == 0 && ((uintptr_t)y & 15) == 0 && ((uintptr_t)work & 15) == 0)
+    hipLaunchKernelGGL(gemm_reduce4_kernel, dim3((unsigned)((mn / 4 + 255) / 256)), dim3(256), 0, s,
+                       (const float4 *)work, sp, M, N / 4, y, ldy);
+  else
+    hipLaunchKernelGGL(gemm_reduce_kernel, dim3((unsigned)((mn + 255) / 256)), dim3(256), 0, s, work,
+                       sp, M, N, y, ldy);
   return hipGetLastError();
 }
 

@@ -273,11 +273,12 @@ def _metrics_decode(ref, y, x, wdeq):
 
 @pytest.mark.parametrize("t,m,n,k", [(12, 200, 300, 4096), (14, 64, 256, 2048), (23, 130, 256, 4096),
                                      (10, 100, 512, 4096), (13, 40, 200, 4096), (11, 96, 64, 8192),
-                                     (12, 512, 4096, 4096)])
+                                     (12, 512, 4096, 4096), (13, 40, 202, 4096)])
 @pytest.mark.parametrize("xdt", [np.float16, np.float32])
 def test_gemm_split_k(pkg, ref, t, m, n, k, xdt):
     """Grids of fewer than 192 workgroups split K when given the workspace
-    (gguf_hip_matmul_workspace), adding the splits' partial sums in split order:
+    (gguf_hip_matmul_workspace), adding the splits' partial sums in split order
+    (four outputs per thread when N is a multiple of 4, N = 202 one per thread):
     within the GEMM gate of the oracle, and within f32 rounding of the same
     GEMM without a workspace (one K range)."""
     lib = pkg.load_library()
