@@ -23,8 +23,9 @@ LM head; 128 random prompt tokens then 256 greedy tokens; tok/s = generated
 tokens / decode wall time, prefill excluded).  ``secondary`` holds the other
 configurations of the path (Q4_K / Q5_K / Q6_K decode shapes and batch sizes,
 the other GGML types at the headline shape, more prefill shapes).  ``cpu_baseline`` = the CPU restatement of the reference
-path (numpy dequant to f32 + torch fp32 matmul) on all host cores, repeated
-for about 10 s, with two more entries: ``prefill`` (the Q4_K GEMM shape at
+path (the compiled C oracle, oracle/gguf_ref_c.c: Q4_K dequant fused with the
+GEMV, OpenMP; numpy dequant + torch fp32 matmul when it is not built) on the
+host threads, repeated for about 10 s, with two more entries: ``prefill`` (the Q4_K GEMM shape at
 M=256) and ``decoder`` (the bench decoder in f32 on the host, ms/token over 8
 greedy tokens).  Each carries the host CPU model string, the cores used and the
 torch version.  ``roofline.traffic`` is read from the committed rocprofv3
@@ -205,23 +206,54 @@ def matmul_case(pkg, t, m, n, k, pool, steps, warmup, xdtype="float32", eager=Fa
     return out
 
 
+def _cpu_threads():
+    """Host threads for the CPU baseline: the process's CPUs, capped by
+    OMP_NUM_THREADS where that is set."""
+    cores = len(os.sched_getaffinity(0))
+    try:
+        cap = int(os.environ.get("OMP_NUM_THREADS", "0"))
+    except ValueError:
+        cap = 0
+    return min(cores, cap) if cap > 0 else cores
+
+
+def _oracle_c():
+    """The compiled C restatement of the oracle (oracle/liboracle.so), or None."""
+    from oracle import build_oracle
+    return build_oracle.load()
+
+
 def cpu_baseline(pkg, raw, t, n, k, seconds, m=1):
-    """CPU restatement of the reference path: numpy dequant (bit-exact to
-    gguf-dequant.ts) + torch fp32 matmul, all host cores, repeated ~``seconds``."""
+    """CPU restatement of the reference path, repeated ~``seconds``: the compiled
+    C oracle (Q4_K dequant fused with the GEMV, gcc -O3 AVX2, OpenMP over weight
+    rows) on every host thread; without it, the numpy oracle's dequant + a torch
+    fp32 matmul."""
     import torch
     from oracle import gguf_ref as ref
-    cores = len(os.sched_getaffinity(0))
+    cores = _cpu_threads()
     torch.set_num_threads(cores)
-    x = torch.from_numpy(pkg.quantize.synthetic_activations(m, k, seed=7))
+    x = pkg.quantize.synthetic_activations(m, k, seed=7).astype(np.float32)
+    clib = _oracle_c() if t == 12 else None
+    # distinct weight copies in turn (8 x 33 MB, beyond the host's last-level
+    # caches), as the GPU line cycles through its cold pool
+    pool = [np.array(raw, dtype=np.uint8, copy=True) for _ in range(8)] if clib is not None else []
+    y = np.empty((m, n), np.float32)
+    xt = torch.from_numpy(x)
     times, t_deq, t_mm = [], [], []
     t_start = time.perf_counter()
     it = 0
-    while it < 4 or (time.perf_counter() - t_start < seconds and it < 1000):
+    while it < 4 or (time.perf_counter() - t_start < seconds and it < 100000):
         t0 = time.perf_counter()
-        w = torch.from_numpy(ref.dequant_rows(t, raw, n, k))
-        t1 = time.perf_counter()
-        torch.matmul(x, w.T)
-        t2 = time.perf_counter()
+        if clib is not None:
+            w8 = pool[it % len(pool)]
+            assert clib.oracle_matmul_q4_k(w8.ctypes.data, n, k, x.ctypes.data, m, y.ctypes.data,
+                                           cores) > 0
+            t1 = t2 = time.perf_counter()
+        else:
+            w = torch.from_numpy(ref.dequant_rows(t, raw, n, k))
+            t1 = time.perf_counter()
+            torch.matmul(xt, w.T)
+            t2 = time.perf_counter()
         if it >= 2:                                    # two warm-ups
             times.append(t2 - t0)
             t_deq.append(t1 - t0)
@@ -229,15 +261,23 @@ def cpu_baseline(pkg, raw, t, n, k, seconds, m=1):
         it += 1
     tot = float(np.median(times))
     wbytes = n * pkg.raw_row_bytes(t, k)
+    head = (f"the headline workload (Q4_K M={m} K={k} N={n}) {len(times)} times after 2 warm-ups "
+            f"({time.perf_counter() - t_start:.1f} s): ")
+    if clib is not None:
+        how = (f"compiled C restatement of the oracle (oracle/gguf_ref_c.c: gcc -O3 "
+               f"-march=x86-64-v3, OpenMP, {cores} threads), each weight superblock dequantized "
+               f"and dotted with x at once, over {len(pool)} weight copies in turn; median "
+               f"{tot * 1e3:.2f} ms per step")
+    else:
+        how = (f"numpy dequant to f32 + torch.matmul f32; median dequant "
+               f"{np.median(t_deq) * 1e3:.1f} ms, matmul {np.median(t_mm) * 1e3:.1f} ms, total "
+               f"{tot * 1e3:.1f} ms per step")
     return {
         "value": round(wbytes / tot / 1e9, 3),
         "unit": "GB/s",
         "cores": cores,
         "kind": "port",
-        "sample": (f"the headline workload (Q4_K M={m} K={k} N={n}) {len(times)} times after 2 "
-                   f"warm-ups ({time.perf_counter() - t_start:.1f} s): numpy dequant to f32 + "
-                   f"torch.matmul f32; median dequant {np.median(t_deq) * 1e3:.1f} ms, matmul "
-                   f"{np.median(t_mm) * 1e3:.1f} ms, total {tot * 1e3:.1f} ms per step"),
+        "sample": head + how,
         "ms_per_step": round(tot * 1e3, 3),
         "cpu": cpu_model(),
         "torch": torch.__version__,
@@ -257,18 +297,26 @@ def cpu_model():
 
 
 def cpu_prefill_baseline(pkg, raw, t, n, k, m, reps=5):
-    """The prefill path on the host: oracle dequant (blocks -> f32 [N, K]) + torch
+    """The prefill path on the host: oracle dequant (blocks -> f32 [N, K]; the
+    compiled C restatement on every host thread when built, else numpy) + torch
     fp32 matmul of M fp16 activations upcast to f32; median of ``reps`` after 2
     warm-ups."""
     import torch
     from oracle import gguf_ref as ref
-    cores = len(os.sched_getaffinity(0))
+    cores = _cpu_threads()
     torch.set_num_threads(cores)
     x = torch.from_numpy(pkg.quantize.synthetic_activations(m, k, seed=7)).half().float()
+    clib = _oracle_c() if t == 12 else None
+    rawc = np.ascontiguousarray(raw, dtype=np.uint8)
+    wbuf = np.empty((n, k), np.float32)
     t_deq, t_mm = [], []
     for it in range(reps + 2):
         t0 = time.perf_counter()
-        w = torch.from_numpy(ref.dequant_rows(t, raw, n, k))
+        if clib is not None:
+            assert clib.oracle_dequant_rows_q4_k(rawc.ctypes.data, n, k, wbuf.ctypes.data, cores) > 0
+            w = torch.from_numpy(wbuf)
+        else:
+            w = torch.from_numpy(ref.dequant_rows(t, raw, n, k))
         t1 = time.perf_counter()
         torch.matmul(x, w.T)
         t2 = time.perf_counter()
@@ -283,7 +331,9 @@ def cpu_prefill_baseline(pkg, raw, t, n, k, m, reps=5):
         "cores": cores,
         "kind": "port",
         "sample": (f"Q4_K dequant-GEMM M={m} (the GPU line is M=2048) K={k} N={n}, fp16 "
-                   f"activations upcast to f32: {reps} runs after 2 warm-ups; median dequant "
+                   f"activations upcast to f32: {reps} runs after 2 warm-ups; "
+                   f"{'compiled C oracle dequant (OpenMP)' if clib is not None else 'numpy oracle dequant'}"
+                   f" + torch f32 matmul; median dequant "
                    f"{deq * 1e3:.1f} ms + f32 matmul {mm * 1e3:.1f} ms "
                    f"({flop / mm / 1e12:.3f} TFLOP/s for the matmul alone)"),
         "ms_per_step": round((deq + mm) * 1e3, 3),
