@@ -202,13 +202,14 @@ constexpr uint32_t kIq4Tab2 = 0xA6998D81u;  // 129, 141, 153, 166
 constexpr uint32_t kIq4Tab3 = 0xF1D9C5B5u;  // 181, 197, 217, 241
 
 // Four 4-bit indices (one per byte of s) -> their codebook codes (one per byte).
+// A third byte permute picks each byte from the upper half's lookup (selector
+// 4 + j) where the index is >= 8, else from the lower half's (selector j).
 __device__ __forceinline__ uint32_t iq4nl_lookup(uint32_t s) {
   const uint32_t lo3 = s & 0x07070707u;
   const uint32_t ra = __builtin_amdgcn_perm(kIq4Tab1, kIq4Tab0, lo3);  // entries 0-7
   const uint32_t rb = __builtin_amdgcn_perm(kIq4Tab3, kIq4Tab2, lo3);  // entries 8-15
-  const uint32_t m8 = s & 0x08080808u;
-  const uint32_t sel = (m8 << 5) - (m8 >> 3);  // 0xFF in the bytes whose index is >= 8
-  return (rb & sel) | (ra & ~sel);
+  const uint32_t sel = ((s >> 1) & 0x04040404u) | 0x03020100u;        // bit 3 -> +4
+  return __builtin_amdgcn_perm(rb, ra, sel);
 }
 
 // The eight codes of a lane in a 32-element-block unit, from its code word q
