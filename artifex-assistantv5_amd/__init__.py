@@ -1,5 +1,7 @@
-"""MI355X-native GGUF Q8_0 / Q4_K / Q5_K / Q6_K / Q2_K / Q3_K / Q4_0 / Q5_0 /
-IQ4_NL / IQ4_XS dequant-matmul.
+"""MI355X-native GGUF dequant-matmul for the 16 quantized types of the
+reference's ``dequantGGML``: Q8_0 / Q4_K / Q5_K / Q6_K / Q2_K / Q3_K / Q4_0 /
+Q5_0 / IQ4_NL / IQ4_XS and the grid-codebook types IQ2_XXS / IQ2_XS / IQ2_S /
+IQ3_XXS / IQ3_S / IQ1_M.
 
 Python host side of ``libgguf_hip.so`` (hand-written HIP kernels for gfx950
 behind a C ABI, ``include/gguf_hip.h``).  The per-layer API mirrors the

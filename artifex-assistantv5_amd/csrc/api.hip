@@ -45,7 +45,9 @@ bool traits(int t, int *block, int *size) {
   return false;
 }
 
-// the grid-codebook IQ types: their decode kernel always takes a workspace
+// The grid-codebook IQ types.  Their decode variant needs a workspace only
+// beyond K = kIqOneShotMaxK (the one-shot kernel's staging limit).
+constexpr int64_t kIqOneShotMaxK = 16384;
 bool grid_type(int t) {
   return t == GGUF_HIP_IQ2_XXS || t == GGUF_HIP_IQ2_XS || t == GGUF_HIP_IQ2_S ||
          t == GGUF_HIP_IQ3_XXS || t == GGUF_HIP_IQ3_S || t == GGUF_HIP_IQ1_M;
@@ -246,7 +248,10 @@ int gguf_hip_matmul_ws(const void *x, int x_type, int64_t ldx, const void *tiles
     variant = m <= (x_type == GGUF_HIP_F32 ? GGUF_HIP_F32_GEMM_MIN_M - 1 : GGUF_HIP_DECODE_MAX_M)
                   ? GGUF_HIP_VARIANT_DECODE
                   : GGUF_HIP_VARIANT_GEMM;
-  if (grid_type(ggml_type) && variant == GGUF_HIP_VARIANT_DECODE) {
+  // grid types: up to K = 16384 the decode variant runs without a workspace
+  // (the one-shot kernel, once per row when the workspace is missing); beyond
+  // it only the batched kernel serves them, and that needs one
+  if (grid_type(ggml_type) && variant == GGUF_HIP_VARIANT_DECODE && k > kIqOneShotMaxK) {
     const int64_t need = 4 * gguf::launch_decode_work(ggml_type, x_type, n, k, m);
     if (need > 0 && (!work || work_bytes < need))
       return fail(GGUF_HIP_ERR_SHAPE,
@@ -287,7 +292,9 @@ int64_t gguf_hip_matmul_workspace(int ggml_type, int x_type, int64_t n, int64_t 
   ok();
   if (n == 0 || m == 0) return 0;
   // the larger of the decode path's and the GEMM's (AUTO may take either)
-  const int64_t dec = (m < 2 && !grid_type(ggml_type)) ? 0 : gguf::launch_decode_work(ggml_type, x_type, n, k, m);
+  // (M = 1: the one-shot kernel needs none; grid types above K = 16384 still do)
+  const int64_t dec = (m < 2 && (!grid_type(ggml_type) || k <= kIqOneShotMaxK))
+                          ? 0 : gguf::launch_decode_work(ggml_type, x_type, n, k, m);
   int64_t gem = m > 32 ? gguf::launch_gemm_work(ggml_type, n, k, m) : 0;
   if (gem > 0) gem += gguf::kWsPrefix / 4;  // the GEMM's partial sums follow the counter prefix
   return 4 * (dec > gem ? dec : gem);

@@ -1863,24 +1863,34 @@ hipError_t launch_m(const XT *x, int64_t ldx, const uint8_t *W, int N, int K, fl
   }
 
 // The grid-codebook IQ types: the one-shot kernel for M = 1 (K <= 16384), the
-// batched kernel (decode_mk.hpp) otherwise; the API asks for the workspace for
-// every M so that the batched kernel is always available.  No fused prologue /
-// epilogue or merge kernels.
+// batched kernel (decode_mk.hpp) for M >= 2 when the caller's workspace holds
+// its image and partial sums; without one (K <= 16384) the one-shot kernel
+// runs once per activation row, which needs no workspace.  K > 16384 always
+// takes the batched kernel (hipErrorNotSupported without a workspace, before
+// anything is launched).  No fused prologue / epilogue or merge kernels.
+template <int TYPE, typename XT>
+hipError_t launch_iq(const XT *x, int64_t ldx, const uint8_t *W, int N, int K, float *y,
+                     int64_t ldy, int M, float *work, int64_t work_floats, hipStream_t s) {
+  if (M == 1) {
+    const hipError_t e = launch_m1<TYPE, XT, 0>(x, W, N, K, y, nullptr, 0.f, 0, AttnRecords{}, s);
+    if (e != hipErrorNotSupported) return e;
+  }
+  hipError_t e = launch_mk<TYPE, XT>(x, ldx, W, N, K, y, ldy, M, work, work_floats, s);
+  if (e != hipErrorNotSupported) return e;
+  for (int m = 0; m < M; ++m) {  // row 0 answers NotSupported before anything is launched
+    e = launch_m1<TYPE, XT, 0>(x + (int64_t)m * ldx, W, N, K, y + (int64_t)m * ldy, nullptr, 0.f, 0,
+                               AttnRecords{}, s);
+    if (e != hipSuccess) return e;
+  }
+  return hipSuccess;
+}
 #define GGUF_DECODE_DEFINE_IQ(T, NAME)                                                           \
   hipError_t decode_##NAME(const void *x, int x_type, int64_t ldx, const uint8_t *tiles, int n,  \
                            int k, float *y, int64_t ldy, int m, float *work, int64_t work_floats, \
                            hipStream_t s) {                                                      \
-    if (m == 1) {                                                                                \
-      const hipError_t e =                                                                       \
-          x_type == 0 ? launch_m1<T, float, 0>((const float *)x, tiles, n, k, y, nullptr, 0.f, 0, \
-                                               AttnRecords{}, s)                                 \
-                      : launch_m1<T, half_t, 0>((const half_t *)x, tiles, n, k, y, nullptr, 0.f, \
-                                                0, AttnRecords{}, s);                            \
-      if (e != hipErrorNotSupported) return e;                                                   \
-    }                                                                                            \
-    return x_type == 0 ? launch_mk<T, float>((const float *)x, ldx, tiles, n, k, y, ldy, m, work, \
+    return x_type == 0 ? launch_iq<T, float>((const float *)x, ldx, tiles, n, k, y, ldy, m, work, \
                                              work_floats, s)                                     \
-                       : launch_mk<T, half_t>((const half_t *)x, ldx, tiles, n, k, y, ldy, m,    \
+                       : launch_iq<T, half_t>((const half_t *)x, ldx, tiles, n, k, y, ldy, m,    \
                                               work, work_floats, s);                             \
   }                                                                                              \
   int64_t decode_work_##NAME(int x_type, int n, int k, int m) {                                  \

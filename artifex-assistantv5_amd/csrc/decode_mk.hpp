@@ -503,11 +503,8 @@ __global__ __launch_bounds__(64 * TS * KL) void mk_kernel(const uint8_t *__restr
   }
   // this range's sums: to y when K is not split, else to the range's partials.
   // Partials the kernel adds itself (fold) are agent-scope atomic stores
-  // (written through to the level that every XCD sees), so publishing them
-  // needs no L2 write-back: each wave
-  // waits for its stores to complete, and after the barrier one thread counts
-  // the range.  The last range reads the partials with agent-scope atomic
-  // loads (no stale L2 copies), so it needs no L2 invalidation either.
+  // (written through to the level that every XCD sees) and are read back with
+  // agent-scope atomic loads.
   const bool split = gridDim.y > 1;
   const int np = ntiles * 16;
   float *o = split ? part + (int64_t)blockIdx.y * M * np : y;
@@ -540,13 +537,19 @@ __global__ __launch_bounds__(64 * TS * KL) void mk_kernel(const uint8_t *__restr
     }
   }
   if (!split || !fold) return;  // (not fold: mk_reduce_kernel adds the partials)
-  // the last range of the tile group to finish adds the partials in range order
+  // The last range of the tile group to finish adds the partials in range
+  // order.  Ordering: the barrier makes every wave's partial stores happen
+  // before thread 0's count, which is a release at agent scope (so they are
+  // visible device-wide before the count is); the range that sees the final
+  // count takes an agent-scope acquire fence before the barrier that releases
+  // its waves to read the partials.
   __shared__ unsigned last;
-  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wave's partials are stored
   __syncthreads();
-  if (threadIdx.x == 0)
-    last = __hip_atomic_fetch_add(cnt + blockIdx.x, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+  if (threadIdx.x == 0) {
+    last = __hip_atomic_fetch_add(cnt + blockIdx.x, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT) ==
                    gridDim.y - 1 ? 1u : 0u;
+    if (last) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+  }
   __syncthreads();
   if (!last) return;
   // kMkOuts outputs per thread at a time, their partials requested kMkBatch

@@ -85,7 +85,13 @@ __device__ __forceinline__ uint32_t bl2(rsrc_t rs, int voff, int soff) {
 
 // Two f16 results packed in a word: fp16(s * x + c) for the f16 x taken from
 // the low halves (mix_lo) or the high halves (mix_hi) of a and b, computed in
-// f32 and rounded once (v_fma_mixlo_f16 / v_fma_mixhi_f16).
+// f32 and rounded once (v_fma_mixlo_f16 / v_fma_mixhi_f16).  Plain code
+// (fmaf of the widened halves, then a conversion) compiles to cvt + fma +
+// cvt_pk and rounds twice, hence the asm.  Every operand passed here is the
+// result of ordinary arithmetic (masks, shifts, products), never a load's
+// destination register, so the compiler's memory-counter waits precede the
+// instructions that produce them; the compiled assembly has no v_fma_mix
+// whose source register was last written by a load.
 __device__ __forceinline__ uint32_t mix_lo(uint32_t a, uint32_t b, float s, float c) {
   uint32_t r;
   asm("v_fma_mixlo_f16 %0, %1, %2, %3 op_sel_hi:[1,0,0]\n\t"

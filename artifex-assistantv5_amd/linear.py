@@ -284,23 +284,47 @@ def _row_stride(t: torch.Tensor, rows: int, cols: int, name: str) -> int:
     return t.stride(0) if rows > 1 else max(t.stride(0), cols)
 
 
-# One matmul workspace per device, grown on demand.  Its counter prefix must
-# be zero before first use and every call leaves it zero, so it is allocated
-# zero-filled once and shared by every call on the device (calls on one device
-# run in stream order here).  A workspace that is outgrown stays allocated:
-# a captured graph may still address it.
+# Matmul workspaces.  Calls that share a workspace must not overlap (the
+# split-K partial sums and the 64 KB counter prefix), and calls on one stream
+# are ordered, so there is one workspace per (device, stream): two streams of
+# one device never share one.  Its counter prefix must be zero before first
+# use and every call leaves it zero, so it is allocated zero-filled once.
+# Under graph capture the key also carries the capture: the graph's workspace
+# is allocated inside the capture (its zero fill is a kernel the graph replays
+# ahead of the first use) and is never handed to eager calls, so replays and
+# eager calls on the capturing stream do not share one; two graphs captured on
+# one stream share theirs and must not be replayed concurrently.  Workspaces
+# grow to the next power of two; an outgrown eager workspace is freed (its
+# stream's later work is ordered after the calls that used it), an outgrown
+# graph workspace is kept, since the graph still addresses it.
 _WORKSPACES: dict = {}
-_OUTGROWN: list = []
+_GRAPH_KEPT: list = []
+_MIN_WORKSPACE = 1 << 20
+
+
+def workspace_key(device_index: int, stream_handle: int, capturing: bool) -> tuple:
+    """Key of the workspace a call uses: one per (device, stream), separate for
+    calls made under graph capture."""
+    return (int(device_index), int(stream_handle), bool(capturing))
+
+
+def workspace_size(nbytes: int) -> int:
+    """Bytes allocated for a request of ``nbytes``: the next power of two, at least 1 MiB."""
+    return max(_MIN_WORKSPACE, 1 << max(0, int(nbytes) - 1).bit_length())
 
 
 def matmul_workspace(dev: torch.device, nbytes: int) -> torch.Tensor:
-    """The device's shared, zero-initialised matmul workspace of at least ``nbytes``."""
-    key = dev.index if dev.index is not None else torch.cuda.current_device()
+    """The zero-initialised matmul workspace of the current stream of ``dev``
+    (at least ``nbytes``)."""
+    idx = dev.index if dev.index is not None else torch.cuda.current_device()
+    stream = torch.cuda.current_stream(idx)
+    capturing = torch.cuda.is_current_stream_capturing()
+    key = workspace_key(idx, stream.cuda_stream, capturing)
     ws = _WORKSPACES.get(key)
     if ws is None or ws.numel() < nbytes:
-        if ws is not None:
-            _OUTGROWN.append(ws)
-        ws = torch.zeros(max(nbytes, 1 << 20), dtype=torch.uint8, device=dev)
+        if ws is not None and capturing:
+            _GRAPH_KEPT.append(ws)
+        ws = torch.zeros(workspace_size(nbytes), dtype=torch.uint8, device=dev)
         _WORKSPACES[key] = ws
     return ws
 

@@ -49,7 +49,7 @@ extern "C" {
  * are exported (kernels and helpers cannot be interposed across libraries). */
 #pragma GCC visibility push(default)
 
-#define GGUF_HIP_ABI_VERSION 15
+#define GGUF_HIP_ABI_VERSION 16
 
 /* ggml type ids (gguf.ts:24-35); activation dtypes reuse F32 / F16. */
 #define GGUF_HIP_F32 0
@@ -64,7 +64,7 @@ extern "C" {
 #define GGUF_HIP_Q6_K 14
 #define GGUF_HIP_IQ4_NL 20
 #define GGUF_HIP_IQ4_XS 23
-/* grid-codebook types: the decode variant always with a workspace */
+/* grid-codebook types: the decode variant needs a workspace only for K > 16384 */
 #define GGUF_HIP_IQ2_XXS 16
 #define GGUF_HIP_IQ2_XS 17
 #define GGUF_HIP_IQ3_XXS 18
@@ -184,11 +184,13 @@ int gguf_hip_matmul_variant(const void *x, int x_type, int64_t ldx, const void *
  * leaves them zero, so one workspace serves calls of any shape and type.
  * The reference engine likewise preallocates its scratch (forward-pass.ts:1140-1163).
  * Calls that share a workspace must not overlap.
- * The grid-codebook IQ types need the workspace whenever the decode variant
- * runs (AUTO picks it as for the other types) and gguf_hip_matmul_workspace
- * reports a nonzero size, M = 1 included: without one they return
- * GGUF_HIP_ERR_SHAPE, so gguf_hip_matmul and gguf_hip_matmul_variant take them
- * only where AUTO / GEMM choose the GEMM. */
+ * The grid-codebook IQ types run the decode variant without a workspace up
+ * to K = 16384, as every other type does: M = 1 is one launch, and M >= 2
+ * without a workspace (or with one smaller than gguf_hip_matmul_workspace)
+ * runs the M = 1 kernel once per row; with the workspace the batched kernel
+ * reads the weights once for all rows.  Beyond K = 16384 only the batched
+ * kernel serves them: without the workspace the call returns
+ * GGUF_HIP_ERR_SHAPE before launching anything. */
 int gguf_hip_matmul_ws(const void *x, int x_type, int64_t ldx, const void *tiles, int ggml_type,
                        int64_t n, int64_t k, float *y, int64_t ldy, int64_t m, int variant,
                        void *work, int64_t work_bytes, void *stream);

@@ -18,7 +18,7 @@ LIB = os.path.join(HERE, "liboracle.so")
 def build() -> str:
     tmp = LIB + ".tmp"
     subprocess.run(["gcc", "-O3", "-march=x86-64-v3", "-fopenmp", "-shared", "-fPIC", "-Wall",
-                    "-Werror", SRC, "-o", tmp, "-lm"], check=True)
+                    SRC, "-o", tmp, "-lm"], check=True)
     os.replace(tmp, LIB)
     return LIB
 

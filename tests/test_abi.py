@@ -73,19 +73,23 @@ def test_constants_match_header(native):
 
 
 def test_grid_types_contract(lib, native):
-    """IQ2_XXS .. IQ1_M: a workspace for the decode variant at every M, no fused
-    kernels.  Fake (aligned, never dereferenced) pointers: every check fails
-    before any HIP call."""
+    """IQ2_XXS .. IQ1_M: no workspace needed for the decode variant up to
+    K = 16384 (M = 1 asks for none, M >= 2 for an optional one); beyond it a
+    workspace is required.  No fused kernels.  Fake (aligned, never
+    dereferenced) pointers: every check below fails before any HIP call."""
     x, w, y = 0x10000, 0x20000, 0x30000
     for t in (16, 17, 18, 21, 22, 29):
-        for m in (1, 5, 40):
-            for xt in (0, 1):
+        for xt in (0, 1):
+            assert lib.gguf_hip_matmul_workspace(t, xt, 64, 512, 1) == 0
+            assert lib.gguf_hip_matmul_workspace(t, xt, 64, 16384, 1) == 0
+            for m in (5, 40):
                 assert lib.gguf_hip_matmul_workspace(t, xt, 64, 512, m) > 0
-        assert lib.gguf_hip_matmul(x, 0, 512, w, t, 64, 512, y, 64, 1, None) == native.ERR_SHAPE
+            assert lib.gguf_hip_matmul_workspace(t, xt, 64, 16640, 1) > 0
+        assert lib.gguf_hip_matmul(x, 0, 16640, w, t, 64, 16640, y, 64, 1, None) == native.ERR_SHAPE
         assert "needs a workspace" in native.last_error(lib)
-        need = lib.gguf_hip_matmul_workspace(t, 0, 64, 512, 3)
-        assert lib.gguf_hip_matmul_ws(x, 0, 512, w, t, 64, 512, y, 64, 3, 0, 0x40000, need - 16,
-                                      None) == native.ERR_SHAPE
+        need = lib.gguf_hip_matmul_workspace(t, 0, 64, 16640, 3)
+        assert lib.gguf_hip_matmul_ws(x, 0, 16640, w, t, 64, 16640, y, 64, 3, 0, 0x40000,
+                                      need - 16, None) == native.ERR_SHAPE
         assert lib.gguf_hip_matmul_fused(x, w, t, 64, 512, y, 0, None, ctypes.c_float(0.0), 0,
                                          None) == native.ERR_SHAPE
         assert "no fused kernel" in native.last_error(lib)
@@ -94,7 +98,7 @@ def test_grid_types_contract(lib, native):
 
 
 def test_abi_version(lib):
-    assert lib.gguf_hip_abi_version() == 15
+    assert lib.gguf_hip_abi_version() == 16
 
 
 def test_type_traits(lib, native):

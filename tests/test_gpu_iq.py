@@ -9,7 +9,8 @@
   against the f64 product of the oracle's dequantized weights (the same
   f32-grade gate as the other types' decode path);
 * the GEMM (M > 32): the gate of the other types' fp16 GEMM;
-* the API contract: a workspace for the decode variant at every M.
+* the API contract: no workspace needed up to K = 16384 (the one-shot kernel,
+  once per row without one), a workspace required beyond it.
 """
 
 import ctypes
@@ -105,24 +106,56 @@ def test_api_contract(pkg, native):
     rc = lib.gguf_hip_matmul_variant(x.data_ptr(), 0, k, w.ptr(), t, n, k, y.data_ptr(), n, m,
                                      GEMM, None)
     assert rc == 0, native.last_error(lib)
-    # the decode variant needs a workspace for every M, M = 1 included
-    for mm in (1, m):
-        need = lib.gguf_hip_matmul_workspace(t, 0, n, k, mm)
-        assert need > 0
-        rc = lib.gguf_hip_matmul(x.data_ptr(), 0, k, w.ptr(), t, n, k, y.data_ptr(), n, mm, None)
-        assert rc == native.ERR_SHAPE and "workspace" in native.last_error(lib)
-        ws = torch.zeros(need, dtype=torch.uint8, device="cuda")  # counters start at zero
-        rc = lib.gguf_hip_matmul_ws(x.data_ptr(), 0, k, w.ptr(), t, n, k, y.data_ptr(), n, mm,
-                                    AUTO, ws.data_ptr(), need - 1, None)
-        assert rc == native.ERR_SHAPE
-        rc = lib.gguf_hip_matmul_ws(x.data_ptr(), 0, k, w.ptr(), t, n, k, y.data_ptr(), n, mm,
-                                    AUTO, ws.data_ptr(), need, None)
+    # M = 1 needs no workspace; M >= 2 asks for one (the batched kernel) but
+    # runs without it too, and a workspace one byte short is taken as none
+    assert lib.gguf_hip_matmul_workspace(t, 0, n, k, 1) == 0
+    need = lib.gguf_hip_matmul_workspace(t, 0, n, k, m)
+    assert need > 0
+    ws = torch.zeros(need, dtype=torch.uint8, device="cuda")  # counters start at zero
+    outs = []
+    for work, nb in ((None, 0), (ws.data_ptr(), need - 1), (ws.data_ptr(), need)):
+        y.zero_()
+        rc = lib.gguf_hip_matmul_ws(x.data_ptr(), 0, k, w.ptr(), t, n, k, y.data_ptr(), n, m,
+                                    AUTO, work, nb, None)
         assert rc == 0, native.last_error(lib)
+        outs.append(y.cpu().numpy().copy())
+    assert np.array_equal(outs[0], outs[1])
+    assert np.count_nonzero(ws.cpu().numpy()[:65536]) == 0  # counters left zero
+    # beyond K = 16384 only the batched kernel serves the grid types: a workspace is required
+    kb = 16640
+    assert lib.gguf_hip_matmul_workspace(t, 0, n, kb, 1) > 0
+    rc = lib.gguf_hip_matmul(x.data_ptr(), 0, kb, w.ptr(), t, n, kb, y.data_ptr(), n, 1, None)
+    assert rc == native.ERR_SHAPE and "workspace" in native.last_error(lib)
     torch.cuda.synchronize()
     # fused decode-step kernels do not exist for these types
     rc = lib.gguf_hip_matmul_fused(x.data_ptr(), w.ptr(), t, n, k, y.data_ptr(), 0, None,
                                    ctypes.c_float(0.0), 0, None)
     assert rc == native.ERR_SHAPE and "no fused kernel" in native.last_error(lib)
+
+
+@pytest.mark.parametrize("t", GRID)
+def test_plain_matmul_entry_without_workspace(pkg, ref, native, t):
+    """gguf_hip_matmul (dispatchMatmulGGUF's counterpart, forward-pass.ts:1496-1544)
+    serves the grid types with no workspace: M = 1, 8 and 32 with f32 activations
+    (the decode path: per element within 2e-5 sum_k |x_k w_nk|) and M = 64 with
+    f16 activations (AUTO takes the GEMM: its 1e-3 gates), against the oracle."""
+    lib = native.load_library()
+    n, k = 80, 1024
+    raw, w = _weight(pkg, t, n, k, seed=61 * t)
+    wdeq = ref.dequant_rows(t, raw, n, k)
+    for m, xdt, tol in ((1, np.float32, DECODE_TOL), (8, np.float32, DECODE_TOL),
+                        (32, np.float32, DECODE_TOL), (64, np.float16, None)):
+        x = pkg.quantize.synthetic_activations(m, k, seed=m + t, dtype=xdt)
+        xd = torch.from_numpy(x).cuda()
+        y = torch.full((m, n), float("nan"), device="cuda")
+        rc = lib.gguf_hip_matmul(xd.data_ptr(), 0 if xdt == np.float32 else 1, k, w.ptr(), t, n,
+                                 k, y.data_ptr(), n, m, None)
+        assert rc == 0, (NAMES[t], m, native.last_error(lib))
+        x64 = x.astype(np.float64)
+        met = ref.parity_metrics(y.cpu().numpy(), ref.matmul_bt(x64, wdeq),
+                                 ref.matmul_bt_abs(x64, wdeq))
+        ok = met["ok"] if tol is None else met["finite"] and met["elemwise"] <= tol
+        assert ok, (NAMES[t], m, met)
 
 
 GEMM_TOL = 1e-3

@@ -7,6 +7,8 @@ y_ref is the f64 product of the oracle's dequantized weights (bit-exact to
 gguf-dequant.ts) with the same activations.
 """
 
+import importlib
+
 import numpy as np
 import pytest
 import torch
@@ -167,6 +169,26 @@ def test_deterministic(pkg):
     for m in (1, 8, 100):
         x = torch.from_numpy(pkg.quantize.synthetic_activations(m, 4096, seed=m)).cuda()
         assert torch.equal(pkg.qlinear(x, w), pkg.qlinear(x, w))
+
+
+@pytest.mark.parametrize("t", [12, 14, 8])
+def test_gemm_deterministic(pkg, t):
+    """The prefill GEMM gives bit-identical results call after call: f16
+    activations at M = 2048 (AUTO: the GEMM), f32 at M = 600 with the GEMM
+    variant forced, and a split-K shape (M = 128, N = 512: few output tiles,
+    partial sums added by the reduction in split order).  Each is run five
+    times, with other launches in between."""
+    w14 = _case(pkg, t, 14336, 4096, seed=5)[1]
+    w5 = _case(pkg, t, 512, 4096, seed=6)[1]
+    cases = [(w14, 2048, np.float16, AUTO), (w14, 600, np.float32, GEMM),
+             (w5, 128, np.float16, AUTO)]
+    for w, m, xdt, variant in cases:
+        x = torch.from_numpy(pkg.quantize.synthetic_activations(m, 4096, seed=m, dtype=xdt)).cuda()
+        first = pkg.qlinear(x, w, variant=variant)
+        for _ in range(4):
+            pkg.qlinear(x[:1].float(), w14)  # another shape in between (decode path)
+            assert torch.equal(pkg.qlinear(x, w, variant=variant), first), (t, m, xdt)
+        assert torch.isfinite(first).all()
 
 
 # ---------------------------------------------------------------------------
@@ -342,3 +364,32 @@ def test_shared_workspace_counters_stay_zero(pkg, ref):
                     assert met["finite"] and met["elemwise"] <= DECODE_TOL, ((t, m, n, k), met)
             else:
                 assert torch.equal(y, first[i]), ("repeat", t, m, n, k)
+
+
+def test_workspace_per_stream(pkg):
+    """Batched decode (Q4_K, M = 8: split K, the last range adds the partials,
+    counted in the workspace) alternating between two streams of one device:
+    each stream gets its own workspace, the results equal the single-stream
+    ones bit for bit, and both counter prefixes are zero afterwards."""
+    lin = importlib.import_module("artifex-assistantv5_amd.linear")
+    raw, w = _case(pkg, 12, 14336, 4096, seed=9)
+    xs = [torch.from_numpy(pkg.quantize.synthetic_activations(8, 4096, seed=s)).cuda()
+          for s in range(4)]
+    want = [pkg.qlinear(x, w) for x in xs]
+    torch.cuda.synchronize()
+    streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+    outs = []
+    for rep in range(3):
+        for i, x in enumerate(xs):
+            s = streams[i % 2]
+            s.wait_stream(torch.cuda.current_stream())
+            with torch.cuda.stream(s):
+                outs.append((i, pkg.qlinear(x, w)))
+    torch.cuda.synchronize()
+    for i, y in outs:
+        assert torch.equal(y, want[i]), i
+    keys = [lin.workspace_key(torch.cuda.current_device(), s.cuda_stream, False) for s in streams]
+    wss = [lin._WORKSPACES[k] for k in keys]
+    assert wss[0].data_ptr() != wss[1].data_ptr()
+    for ws in wss:
+        assert int(torch.count_nonzero(ws[:65536])) == 0

@@ -170,3 +170,21 @@ def test_glue_rejects_mismatched_buffers(pkg):
     for fn, msg in cases:
         with pytest.raises(ValueError, match=msg):
             fn()
+
+
+def test_matmul_workspace_keying_and_growth():
+    """One matmul workspace per (device, stream), a separate one under graph
+    capture; sizes grow to the next power of two (at least 1 MiB)."""
+    lin = importlib.import_module("artifex-assistantv5_amd.linear")
+    k = lin.workspace_key
+    assert k(0, 111, False) != k(0, 222, False)      # two streams of one device
+    assert k(0, 111, False) != k(1, 111, False)      # two devices
+    assert k(0, 111, False) != k(0, 111, True)       # eager vs captured on one stream
+    assert k(0, 111, False) == k(0, 111, False)
+    size = lin.workspace_size
+    assert size(1) == 1 << 20 and size(1 << 20) == 1 << 20
+    assert size((1 << 20) + 1) == 1 << 21
+    assert size(33_000_000) == 1 << 25 and size(1 << 25) == 1 << 25
+    # growth is geometric: a run of slowly growing requests reallocates O(log) times
+    sizes = {size(n) for n in range(1 << 20, 1 << 26, 1 << 18)}
+    assert sizes == {1 << e for e in range(20, 27)}

@@ -3,6 +3,7 @@ reference's IQ parity fixture and the mathematics of the formats."""
 
 import json
 import os
+import re
 
 import numpy as np
 import pytest
@@ -119,12 +120,24 @@ def test_iq1_m_scale_and_delta():
 
 
 def test_device_tables_match_the_grids():
-    """csrc/iq_tables.hpp is what gen_iq_tables.py writes from the grid fixture."""
-    import subprocess
-    import sys
+    """The product's device tables (csrc/iq_tables.hpp) hold, value for value,
+    the grids and ksigns table of the fixture the oracle reads."""
     root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
-    gen = os.path.join(root, "artifex-assistantv5_amd", "gen_iq_tables.py")
-    assert subprocess.run([sys.executable, gen, "--check"]).returncode == 0
+    hdr = open(os.path.join(root, "artifex-assistantv5_amd", "csrc", "iq_tables.hpp"),
+               encoding="utf-8").read()
+    with open(os.path.join(root, "tests", "golden", "iq_grids.json"), encoding="utf-8") as f:
+        grids = json.load(f)["grids"]
+    names = {"iq2xxs_grid": "kIq2xxsGrid", "iq2xs_grid": "kIq2xsGrid", "iq2s_grid": "kIq2sGrid",
+             "iq3xxs_grid": "kIq3xxsGrid", "iq3s_grid": "kIq3sGrid", "iq1s_grid": "kIq1sGrid",
+             "ksigns_iq2xs": "kKsigns"}
+    arrays = dict(re.findall(r"const \w+ (k\w+)\[\d+\] = \{([^}]*)\}", hdr))
+    assert sorted(arrays) == sorted(names.values())
+    for key, cname in names.items():
+        vals = [int(v) for v in arrays[cname].replace("\n", "").split(",") if v.strip()]
+        assert vals == list(grids[key]["values"]), key
+    # a planted mismatch is caught: one grid value changed
+    planted = arrays["kIq2sGrid"].replace("8,", "25,", 1)
+    assert [int(v) for v in planted.split(",") if v.strip()] != list(grids["iq2s_grid"]["values"])
 
 
 def test_tile_model_layout_round_trip():
