@@ -1362,7 +1362,8 @@ hipError_t launch_mb(const XT *x, int64_t ldx, const uint8_t *W, int N, int K, f
 template <int TYPE, typename XT>
 int64_t mb_work_floats(int M, int N, int K) {
   if (M < 2) return 0;
-  if constexpr (TYPE == 12) return (int64_t)((mk_work_bytes<12, XT>(M, N, K) + 3) / 4);
+  if constexpr (TYPE == 12 || TYPE == 14 || TYPE == 8)
+    if (K % 256 == 0) return (int64_t)((mk_work_bytes<TYPE, XT>(M, N, K) + 3) / 4);
   int us, nsl;
   mb_plan<TYPE, XT>(M, N, K, &us, &nsl);
   return nsl > 1 ? kWsPrefix / 4 + (int64_t)nsl * M * N : 0;
@@ -1823,8 +1824,8 @@ hipError_t launch_m(const XT *x, int64_t ldx, const uint8_t *W, int N, int K, fl
     const hipError_t e = launch_m1<TYPE, XT, 0>(x, W, N, K, y, nullptr, 0.f, 0, AttnRecords{}, s);
     if (e != hipErrorNotSupported) return e;
   }
-  if constexpr (TYPE == 12) {
-    const hipError_t e = launch_mk<12, XT>(x, ldx, W, N, K, y, ldy, M, work, work_floats, s);
+  if constexpr (TYPE == 12 || TYPE == 14 || TYPE == 8) {  // the batched kernel (decode_mk.hpp)
+    const hipError_t e = launch_mk<TYPE, XT>(x, ldx, W, N, K, y, ldy, M, work, work_floats, s);
     if (e != hipErrorNotSupported) return e;
   }
   if (M <= 16) return launch_mb<TYPE, XT, 1>(x, ldx, W, N, K, y, ldy, M, work, work_floats, s);

@@ -1,5 +1,5 @@
-// Batched decode of Q4_K weights (2 <= M <= 32 activation rows, and M = 1
-// beyond the one-shot kernel's K).
+// Batched decode of Q4_K, Q6_K, Q8_0 and the grid-codebook IQ weights
+// (2 <= M <= 32 activation rows, and M = 1 beyond the one-shot kernel's K).
 //
 // Replaces the reference's batched decode, which runs its Q4_K GEMV once per
 // activation row (grid.y = M, webgpu/src/engine/forward-pass.ts:1536-1539;
@@ -35,10 +35,12 @@
 #pragma once
 
 constexpr int kMkLd = 256 + 8;  // halves per staged row: a 16-byte pad (bank spread)
-// S: the image carries the group sums (Q4_K's mins; the IQ types have none)
-template <int MA, bool S = true>
+// The image of one 256-element unit: A, then (Q4_K) the group sums S, then F,
+// NF inverse scales per row (one per unit, or one per 32-element block for
+// Q8_0, whose blocks carry independent scales).
+template <int MA, bool S = true, int NF = 1>
 constexpr int mk_unit_bytes() {
-  return 16 * MA * (kMkLd * 2 + (S ? 32 : 0) + 4);
+  return 16 * MA * (kMkLd * 2 + (S ? 32 : 0) + 4 * NF);
 }
 template <int MA>
 constexpr int mk_s_off() {
@@ -47,6 +49,55 @@ constexpr int mk_s_off() {
 template <int MA, bool S = true>
 constexpr int mk_f_off() {
   return 16 * MA * (kMkLd * 2 + (S ? 32 : 0));
+}
+
+// Per-type traits of the batched kernel.  A unit is 256 elements of K: one
+// superblock, or eight Q8_0 blocks (a super-unit of eight tile-units).
+//   ORDER  0: natural k order (the IQ grid types); 1: each quad in (0, 2, 1, 3)
+//          order (codes masked into the halves of a word: Q4_K, Q8_0);
+//          2: as 1, and within each 32-element window the quads of its two
+//          16-element groups interleaved (Q6_K: lane group g's 8 k are quad g
+//          of group 2t, then quad g of group 2t + 1)
+//   NF     inverse scales per unit and row (Q8_0: one per block)
+template <int TYPE>
+struct MkFmt {
+  static constexpr int ORDER = TYPE == 12 ? 1 : 0, NF = 1;
+  static constexpr bool SUMS = TYPE == 12;
+  static constexpr int TU = Fmt<TYPE>::TU;  // bytes of a row tile's unit
+};
+template <>
+struct MkFmt<14> {
+  static constexpr int ORDER = 2, NF = 1;
+  static constexpr bool SUMS = false;
+  static constexpr int TU = Fmt<14>::TU;
+};
+template <>
+struct MkFmt<8> {
+  static constexpr int ORDER = 1, NF = 8;
+  static constexpr bool SUMS = false;
+  static constexpr int TU = 8 * Fmt<8>::TU;
+};
+template <int TYPE, int MA>
+constexpr int mk_ub() {
+  return mk_unit_bytes<MA, MkFmt<TYPE>::SUMS, MkFmt<TYPE>::NF>();
+}
+
+// The weight unit a lane holds: Unit<TYPE>, or eight Q8_0 blocks.
+struct Q8Super {
+  Unit<8> b[8];
+};
+template <int TYPE>
+struct MkUnitOf {
+  using type = Unit<TYPE>;
+};
+template <>
+struct MkUnitOf<8> {
+  using type = Q8Super;
+};
+__device__ __forceinline__ void load_unit(__amdgpu_buffer_rsrc_t rs, int soff, int r, int g,
+                                          Q8Super &u) {
+#pragma unroll
+  for (int b = 0; b < 8; ++b) load_unit(rs, soff + b * Fmt<8>::TU, r, g, u.b[b]);
 }
 
 #ifndef GGUF_MK_LDS
@@ -75,23 +126,30 @@ constexpr int kMkOuts = 4;   // outputs a thread of the in-kernel reduction take
 #endif
 template <int TYPE, int MA>
 constexpr int mk_kw_max() {  // units a workgroup can stage
-  return (GGUF_MK_LDS - 1024 - iq_tbl_bytes<TYPE>()) / mk_unit_bytes<MA, TYPE == 12>();
+  return (GGUF_MK_LDS - 1024 - iq_tbl_bytes<TYPE>()) / mk_ub<TYPE, MA>();
 }
 
 // Convert one (unit, activation row) into the unit's image block at blk;
 // lane l holds elements 4l .. 4l + 3 in v (zeros for a padding row).  Every
-// lane of the wave takes part.
-template <int PARTS, int MA, bool QUAD, bool SUMS>
+// lane of the wave takes part.  NF = 1: one power of two for the unit (its
+// 64 lanes); NF = 8: one per 32-element block (8 lanes).
+template <int PARTS, int MA, int ORDER, bool SUMS, int NF>
 __device__ __forceinline__ void mk_stage(const float (&v)[4], int m, int l, uint8_t *blk) {
   float mx = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
-  mx = max_xor32(max_xor16(max_lanes16(mx)));
+  if constexpr (NF == 8) {
+    mx = fmaxf(mx, dpp<kDppXor1>(mx));
+    mx = fmaxf(mx, dpp<kDppXor2>(mx));
+    mx = fmaxf(mx, dpp<kDppHalfMirror>(mx));
+  } else {
+    mx = max_xor32(max_xor16(max_lanes16(mx)));
+  }
   const int ex = stage_exp(mx);
   const float sc = pow2f(ex);
   half4_t h, lo;
   float s = 0.f;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    const int pos = QUAD ? ((i & 1) << 1 | (i >> 1)) : i;  // quad order (0, 2, 1, 3) or natural
+    const int pos = ORDER ? ((i & 1) << 1 | (i >> 1)) : i;  // quad order (0, 2, 1, 3) or natural
     float vi = v[i];
     asm volatile("" : "+v"(vi));  // keep the product out of the f16 conversions (no v_fma_mix)
     const float t = vi * sc;      // exact: a power of two
@@ -101,29 +159,33 @@ __device__ __forceinline__ void mk_stage(const float (&v)[4], int m, int l, uint
     lo[pos] = ll;
     s += (float)hh + (PARTS == 2 ? (float)ll : 0.f);
   }
-  s += dpp<kDppXor1>(s);  // the 8 lanes of a 32-element group
-  s += dpp<kDppXor2>(s);
-  s += dpp<kDppHalfMirror>(s);
   const int row = PARTS == 2 ? 2 * m : m;
-  half_t *A = (half_t *)blk + row * kMkLd + 4 * l;
+  // ORDER 2: quad l = 8 w + 4 lh + g of window w goes to quad 8 w + 2 g + lh
+  const int dq = ORDER == 2 ? (l & ~7) | ((l & 3) << 1) | ((l >> 2) & 1) : l;
+  half_t *A = (half_t *)blk + row * kMkLd + 4 * dq;
   *(half4_t *)A = h;
   if (PARTS == 2) *(half4_t *)(A + kMkLd) = lo;
-  if (SUMS && (l & 7) == 0) {
-    // group j's sum at K position 4 (j >> 2) + e (hi) and 8 + that (lo), with e
-    // the position of j & 3 in the (0, 2, 1, 3) order of the mins operand
-    const int j = l >> 3, e = ((j & 1) << 1) | ((j >> 1) & 1), k = 4 * (j >> 2) + e;
-    const float xs = s * 0.03125f;
-    const half_t xh = (half_t)xs, xl = (half_t)(xs - (float)xh);
-    half_t *S = (half_t *)(blk + mk_s_off<MA>()) + row * 16;
-    S[k] = xh;
-    S[8 + k] = xl;
-    if (PARTS == 2) {
-      S[16 + k] = (half_t)0.f;
-      S[24 + k] = (half_t)0.f;
+  if constexpr (SUMS) {
+    s += dpp<kDppXor1>(s);  // the 8 lanes of a 32-element group
+    s += dpp<kDppXor2>(s);
+    s += dpp<kDppHalfMirror>(s);
+    if ((l & 7) == 0) {
+      // group j's sum at K position 4 (j >> 2) + e (hi) and 8 + that (lo), with e
+      // the position of j & 3 in the (0, 2, 1, 3) order of the mins operand
+      const int j = l >> 3, e = ((j & 1) << 1) | ((j >> 1) & 1), k = 4 * (j >> 2) + e;
+      const float xs = s * 0.03125f;
+      const half_t xh = (half_t)xs, xl = (half_t)(xs - (float)xh);
+      half_t *S = (half_t *)(blk + mk_s_off<MA>()) + row * 16;
+      S[k] = xh;
+      S[8 + k] = xl;
+      if (PARTS == 2) {
+        S[16 + k] = (half_t)0.f;
+        S[24 + k] = (half_t)0.f;
+      }
     }
   }
-  if (l == 0) {
-    float *F = (float *)(blk + mk_f_off<MA, SUMS>());
+  if ((NF == 8 && (l & 7) == 0) || l == 0) {
+    float *F = (float *)(blk + mk_f_off<MA, SUMS>()) + (NF == 8 ? (l >> 3) * 16 * MA : 0);
     F[row] = pow2f(-ex);
     if (PARTS == 2) F[row + 1] = pow2f(-ex);
   }
@@ -131,7 +193,7 @@ __device__ __forceinline__ void mk_stage(const float (&v)[4], int m, int l, uint
 
 // The activations' image, once per call: one wave per (unit, activation
 // row), four per block; rows M .. ROWS - 1 are written as zeros.
-template <typename XT, int MA, bool QUAD, bool SUMS>
+template <typename XT, int MA, int TYPE>
 __global__ __launch_bounds__(256) void mk_prep_kernel(const XT *__restrict__ x, int64_t ldx, int M,
                                                       uint8_t *__restrict__ img) {
   constexpr int PARTS = sizeof(XT) == 4 ? 2 : 1;
@@ -148,7 +210,8 @@ __global__ __launch_bounds__(256) void mk_prep_kernel(const XT *__restrict__ x, 
       for (int e = 0; e < 4; ++e) v[e] = (float)t[e];
     }
   }
-  mk_stage<PARTS, MA, QUAD, SUMS>(v, m, l, img + (size_t)u * mk_unit_bytes<MA, SUMS>());
+  mk_stage<PARTS, MA, MkFmt<TYPE>::ORDER, MkFmt<TYPE>::SUMS, MkFmt<TYPE>::NF>(
+      v, m, l, img + (size_t)u * mk_ub<TYPE, MA>());
 }
 
 // The mins operand of lane group g: m_j for j = 4 (g & 1) + (0, 2, 1, 3).
@@ -312,6 +375,150 @@ __device__ __forceinline__ void mk_unit_iq(const Unit<TYPE> (&w)[T], int bo, int
       for (int i = 0; i < 4; ++i) asm volatile("" : "+v"(acc[t][a][i]));
 }
 
+// Q6_K: each int8 group scale is split as sc = 16 sh + sl (sl in [0, 15], sh
+// in [-8, 7]), so that the B operands sl (q - 32) and sh (q - 32) are exact
+// f16 integers (|.| <= 480), made as (1024 + q) s - 1056 s by one
+// v_pk_fma_f16 per two codes.  Window w = 4 hf + t (32 elements of K) holds
+// the groups 8 hf + 2 t + lh, lh = 0, 1 (the image interleaves their quads,
+// ORDER 2), so one 16x16x32 MFMA per part covers both groups and the unit's
+// 16 MFMAs chain into two accumulators per activation tile:
+//     D = Dl + 16 Dh = sum_s sc_s sum_k x (q - 32),  acc += F d D.
+template <int MA, int T>
+__device__ __forceinline__ void mk_unit_q6k(const Unit<14> (&w)[T], int bo, int lane, bool valid,
+                                            float (&acc)[T][MA][4]) {
+#pragma clang fp contract(off)
+  const int r = lane & 15, g = lane >> 4;
+  uint32_t base = kF16Base;  // in a register: one v_and_or_b32 per masked pair
+  asm volatile("" : "+v"(base));
+  float4_t Dl[T][MA], Dh[T][MA];
+#pragma unroll
+  for (int t = 0; t < T; ++t)
+#pragma unroll
+    for (int a = 0; a < MA; ++a) Dl[t][a] = Dh[t][a] = (float4_t){0.f, 0.f, 0.f, 0.f};
+  const int arow = bo + r * (kMkLd * 2) + 16 * g;  // byte offset of the lane's A fragment
+  const half2_t n1056 = {(half_t)-1056.f, (half_t)-1056.f};
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {  // scale word q: groups 4q .. 4q + 3, windows 2q, 2q + 1
+    // SL[t][e] = (sl of group 4q + e, and of 4q + e + 2), SH likewise; NL, NH = -1056 x them
+    half2_t SL[T][2], SH[T][2], NL[T][2], NH[T][2];
+#pragma unroll
+    for (int t = 0; t < T; ++t) {
+      const uint32_t sw = q == 0 ? w[t].sc.x : q == 1 ? w[t].sc.y : q == 2 ? w[t].sc.z : w[t].sc.w;
+      constexpr uint32_t nb0 = neg_base(0), nb8 = neg_base(8);
+      SL[t][0] = __builtin_bit_cast(half2_t, f16_codes(sw, 0x000F000Fu, nb0));
+      SL[t][1] = __builtin_bit_cast(half2_t, f16_codes(sw >> 8, 0x000F000Fu, nb0));
+      // the high nibble, signed: (nibble ^ 8) = sh + 8
+      SH[t][0] = __builtin_bit_cast(half2_t, f16_codes((sw >> 4) ^ 0x00080008u, 0x000F000Fu, nb8));
+      SH[t][1] = __builtin_bit_cast(half2_t, f16_codes((sw >> 12) ^ 0x00080008u, 0x000F000Fu, nb8));
+#pragma unroll
+      for (int e = 0; e < 2; ++e) {
+        NL[t][e] = SL[t][e] * n1056;
+        NH[t][e] = SH[t][e] * n1056;
+      }
+    }
+#pragma unroll
+    for (int tp = 0; tp < 2; ++tp) {  // window 2q + tp: hf = q >> 1, quarter tt = 2 (q & 1) + tp
+      const int hf = q >> 1, tt = 2 * (q & 1) + tp;
+      half8_t A[MA];
+#pragma unroll
+      for (int a = 0; a < MA; ++a) A[a] = lds_h8b(arow + a * 16 * (kMkLd * 2) + 64 * (4 * hf + tt));
+#pragma unroll
+      for (int t = 0; t < T; ++t) {
+        const uint32_t dw[12] = {w[t].p0.x, w[t].p0.y, w[t].p0.z, w[t].p0.w, w[t].p1.x, w[t].p1.y,
+                                 w[t].p1.z, w[t].p1.w, w[t].p2.x, w[t].p2.y, w[t].p2.z, w[t].p2.w};
+        uint32_t bl[4], bh[4];
+#pragma unroll
+        for (int lh = 0; lh < 2; ++lh) {
+          const int i = 2 * hf + lh;
+          const uint32_t qa = dw[3 * i], qb = dw[3 * i + 1], qh = dw[3 * i + 2];
+          // the lane's 4 codes of group 8 hf + 2 tt + lh (k = 4 g .. 4 g + 3)
+          const uint32_t v = tt == 0   ? (qa & 0x0F0F0F0Fu) | ((qh << 4) & 0x30303030u)
+                             : tt == 1 ? (qb & 0x0F0F0F0Fu) | ((qh << 2) & 0x30303030u)
+                             : tt == 2 ? ((qa >> 4) & 0x0F0F0F0Fu) | (qh & 0x30303030u)
+                                       : ((qb >> 4) & 0x0F0F0F0Fu) | ((qh >> 2) & 0x30303030u);
+          // scale of the group: byte 2 tp + lh of word q (SL[.][lh] holds bytes lh, lh + 2)
+          const half_t sl = SL[t][lh][tp], sh = SH[t][lh][tp];
+          const half_t nl = NL[t][lh][tp], nh = NH[t][lh][tp];
+          const half2_t c02 = __builtin_bit_cast(half2_t, and_or(v, 0x00FF00FFu, base));
+          const half2_t c13 = __builtin_bit_cast(half2_t, and_or(v >> 8, 0x00FF00FFu, base));
+          const half2_t sl2 = {sl, sl}, sh2 = {sh, sh}, nl2 = {nl, nl}, nh2 = {nh, nh};
+          bl[2 * lh] = __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(c02, sl2, nl2));
+          bl[2 * lh + 1] = __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(c13, sl2, nl2));
+          bh[2 * lh] = __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(c02, sh2, nh2));
+          bh[2 * lh + 1] = __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(c13, sh2, nh2));
+        }
+        const half8_t Bl = as_h8(bl[0], bl[1], bl[2], bl[3]), Bh = as_h8(bh[0], bh[1], bh[2], bh[3]);
+#pragma unroll
+        for (int a = 0; a < MA; ++a) {
+          Dl[t][a] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[a], Bl, Dl[t][a], 0, 0, 0);
+          Dh[t][a] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[a], Bh, Dh[t][a], 0, 0, 0);
+        }
+      }
+      if constexpr (MA * T >= 4) __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+  float d[T];
+#pragma unroll
+  for (int t = 0; t < T; ++t) d[t] = valid ? h2f(w[t].d) : 0.f;  // a slot past the units adds zero
+#pragma unroll
+  for (int a = 0; a < MA; ++a) {
+    const float4 F = *(const float4 *)(g_lds + bo + mk_f_off<MA, false>() + (16 * a + 4 * g) * 4);
+    const float f[4] = {F.x, F.y, F.z, F.w};
+#pragma unroll
+    for (int t = 0; t < T; ++t)
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        acc[t][a][i] = fmaf(f[i], d[t] * fmaf(16.f, Dh[t][a][i], Dl[t][a][i]), acc[t][a][i]);
+  }
+#pragma unroll
+  for (int t = 0; t < T; ++t)
+#pragma unroll
+    for (int a = 0; a < MA; ++a)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) asm volatile("" : "+v"(acc[t][a][i]));
+}
+
+// Q8_0: eight 32-element blocks per unit, each with its own scale d_b and its
+// own inverse activation scale F_b (NF = 8): one MFMA of the exact int8 codes
+// per block and activation tile, acc += (F_b d_b) D_b.
+template <int MA, int T>
+__device__ __forceinline__ void mk_unit_q8(const Q8Super (&w)[T], int bo, int lane, bool valid,
+                                           float (&acc)[T][MA][4]) {
+#pragma clang fp contract(off)
+  const int r = lane & 15, g = lane >> 4;
+  const int arow = bo + r * (kMkLd * 2) + 16 * g;  // byte offset of the lane's A fragment
+#pragma unroll
+  for (int b = 0; b < 8; ++b) {
+    half8_t A[MA];
+    float4 F[MA];
+#pragma unroll
+    for (int a = 0; a < MA; ++a) {
+      A[a] = lds_h8b(arow + a * 16 * (kMkLd * 2) + 64 * b);
+      F[a] = *(const float4 *)(g_lds + bo + mk_f_off<MA, false>() + (16 * MA * b + 16 * a + 4 * g) * 4);
+    }
+#pragma unroll
+    for (int t = 0; t < T; ++t) {
+      const half8_t B = q8_operand(w[t].b[b]);
+      const float d = valid ? h2f(w[t].b[b].d) : 0.f;  // a slot past the units adds zero
+#pragma unroll
+      for (int a = 0; a < MA; ++a) {
+        const float4_t zero = {0.f, 0.f, 0.f, 0.f};
+        const float4_t D = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[a], B, zero, 0, 0, 0);
+        const float f[4] = {F[a].x, F[a].y, F[a].z, F[a].w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[t][a][i] = fmaf(f[i] * d, D[i], acc[t][a][i]);
+      }
+    }
+    if constexpr (MA * T >= 4) __builtin_amdgcn_sched_barrier(0);
+  }
+#pragma unroll
+  for (int t = 0; t < T; ++t)
+#pragma unroll
+    for (int a = 0; a < MA; ++a)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) asm volatile("" : "+v"(acc[t][a][i]));
+}
+
 // Workgroup (blockIdx.x, blockIdx.y) of TS x KL waves: row tiles
 // TS T blockIdx.x .. + TS T - 1 (T per wave; wave w takes tile slot w % TS and
 // K-lane w / TS), units blockIdx.y kw .. + kw - 1 of K, of which K-lane kl
@@ -343,7 +550,7 @@ __global__ __launch_bounds__(64 * TS * KL) void mk_kernel(const uint8_t *__restr
                                                           float *__restrict__ part,
                                                           unsigned *__restrict__ cnt, int fold) {
   constexpr int PARTS = sizeof(XT) == 4 ? 2 : 1, NW = TS * KL;
-  constexpr int UB = mk_unit_bytes<MA, TYPE == 12>(), TU = Fmt<TYPE>::TU;
+  constexpr int UB = mk_ub<TYPE, MA>(), TU = MkFmt<TYPE>::TU;
   constexpr int KWM = SX ? kMkFuseKw : mk_kw_max<TYPE, MA>();  // units a range may hold
   constexpr int CP = SX ? 1 : (KWM * UB / 16 + 64 * NW - 1) / (64 * NW);  // 16 B pieces per thread
   constexpr int U = (KWM + KL - 1) / KL;                                    // unit slots per wave
@@ -425,7 +632,7 @@ __global__ __launch_bounds__(64 * TS * KL) void mk_kernel(const uint8_t *__restr
   // a loop the memory-counter waits lose track of the requests and wait for
   // all of them at every unit.
   const int ulast = cnt_u > 0 ? kl + KL * (cnt_u - 1) : 0;  // a unit of the range
-  Unit<TYPE> wb[P][T];
+  typename MkUnitOf<TYPE>::type wb[P][T];
 #pragma unroll
   for (int i = 0; i < P; ++i)
 #pragma unroll
@@ -435,7 +642,8 @@ __global__ __launch_bounds__(64 * TS * KL) void mk_kernel(const uint8_t *__restr
     for (int i = 0; i < SP; ++i) {
       const int q = wave + NW * i, ul = q / RW, m = q - ul * RW;
       if (ul < nun)  // uniform
-        mk_stage<PARTS, MA, TYPE == 12, TYPE == 12>(xv[i], m, lane, g_lds + ul * UB);
+        mk_stage<PARTS, MA, MkFmt<TYPE>::ORDER, MkFmt<TYPE>::SUMS, MkFmt<TYPE>::NF>(
+            xv[i], m, lane, g_lds + ul * UB);
     }
     if constexpr (IQ) iq_put_tables<TYPE, 64 * NW>(tab, g_lds + tbl);
     __syncthreads();
@@ -468,6 +676,10 @@ __global__ __launch_bounds__(64 * TS * KL) void mk_kernel(const uint8_t *__restr
     }
     if constexpr (IQ)
       mk_unit_iq<TYPE, MA, T>(wb[i % P], min(kl + KL * i, ulast) * UB, lane, i < cnt_u, tbl, acc);
+    else if constexpr (TYPE == 14)
+      mk_unit_q6k<MA, T>(wb[i % P], min(kl + KL * i, ulast) * UB, lane, i < cnt_u, acc);
+    else if constexpr (TYPE == 8)
+      mk_unit_q8<MA, T>(wb[i % P], min(kl + KL * i, ulast) * UB, lane, i < cnt_u, acc);
     else
       mk_unit<MA, T>(wb[i % P], min(kl + KL * i, ulast) * UB, lane, i < cnt_u, acc);
     if (i + P < U)  // compile-time
@@ -644,9 +856,8 @@ MkPlan mk_plan(int M, int N, int K) {
   p.ts = p.sx ? 16 : wide ? 16 / GGUF_MK_WIDE_T : 4;
   p.kl = p.sx || wide ? 1 : 4;
   p.t = !p.sx && wide ? GGUF_MK_WIDE_T : 1;
-  constexpr bool S = TYPE == 12;
-  const size_t ub = p.ma == 1 ? mk_unit_bytes<1, S>() : p.ma == 2 ? mk_unit_bytes<2, S>()
-                  : p.ma == 3 ? mk_unit_bytes<3, S>() : mk_unit_bytes<4, S>();
+  const size_t ub = p.ma == 1 ? mk_ub<TYPE, 1>() : p.ma == 2 ? mk_ub<TYPE, 2>()
+                  : p.ma == 3 ? mk_ub<TYPE, 3>() : mk_ub<TYPE, 4>();
   const int kw_max = p.sx ? kMkFuseKw
                    : p.ma == 1 ? mk_kw_max<TYPE, 1>() : p.ma == 2 ? mk_kw_max<TYPE, 2>()
                    : p.ma == 3 ? mk_kw_max<TYPE, 3>() : mk_kw_max<TYPE, 4>();
@@ -676,7 +887,7 @@ hipError_t launch_mk_ma(const XT *x, int64_t ldx, const uint8_t *W, int N, int K
   uint8_t *ws = (uint8_t *)work, *img = ws + kWsPrefix;
   hipError_t e = hipSuccess;
   if constexpr (!SX) {
-    hipLaunchKernelGGL((mk_prep_kernel<XT, MA, TYPE == 12, TYPE == 12>),
+    hipLaunchKernelGGL((mk_prep_kernel<XT, MA, TYPE>),
                        dim3((unsigned)(K / 256), (unsigned)(16 * MA / PARTS / 4)), dim3(256), 0, s,
                        x, ldx, M, img);
     e = hipGetLastError();
@@ -710,6 +921,7 @@ size_t mk_work_bytes(int M, int N, int K) {
 template <int TYPE, typename XT>
 hipError_t launch_mk(const XT *x, int64_t ldx, const uint8_t *W, int N, int K, float *y,
                      int64_t ldy, int M, float *work, int64_t work_floats, hipStream_t s) {
+  if (K % 256) return hipErrorNotSupported;  // units of 256 elements (Q8_0: eight blocks)
   const MkPlan p = mk_plan<TYPE, XT>(M, N, K);
   if (M > 32 || (p.bytes > 0 && (!work || (size_t)work_floats * 4 < p.bytes)))
     return hipErrorNotSupported;
@@ -717,7 +929,7 @@ hipError_t launch_mk(const XT *x, int64_t ldx, const uint8_t *W, int N, int K, f
     // more tile groups than counters: blocks of rows, one launch each (in
     // stream order, so each block finds the counters zero again)
     const int rb = kMkMaxGroups * p.ts * p.t * 16;
-    const int64_t tb = (int64_t)(K / 256) * Fmt<TYPE>::TU;
+    const int64_t tb = (int64_t)(K / 256) * MkFmt<TYPE>::TU;
     for (int n0 = 0; n0 < N; n0 += rb) {
       const hipError_t e = launch_mk<TYPE, XT>(x, ldx, W + (int64_t)(n0 / 16) * tb, min(rb, N - n0),
                                                K, y + n0, ldy, M, work, work_floats, s);

@@ -519,6 +519,15 @@ def secondary_cases(pkg, args, pool, secondary):
             r = matmul_case(pkg, t, mm, 4096, 14336, dpool, 170, 5, replays=3)
             secondary[f"q4k_decode_m{mm}_down_gbs"] = round(r["gbs"], 1)
         del dpool
+    if want("batch_q6q8"):
+        # batched decode of the other two north-star types at the FFN shapes
+        for tt, name in ((14, "q6k"), (8, "q8_0")):
+            for (nn, kk), shape in (((14336, 4096), "gate_up"), ((4096, 14336), "down")):
+                bpool, _ = make_pool(pkg, tt, nn, kk, 10, seed=40 + tt)
+                for mm in (8, 32):
+                    r = matmul_case(pkg, tt, mm, nn, kk, bpool, 170, 5, replays=3)
+                    secondary[f"{name}_decode_m{mm}_{shape}_gbs"] = round(r["gbs"], 1)
+                del bpool
     if want("q8"):
         qpool, _ = make_pool(pkg, 8, 4096, 4096, 32, seed=4)
         r = matmul_case(pkg, 8, 1, 4096, 4096, qpool, 320, 10, replays=3)

@@ -91,6 +91,56 @@ def test_decode_is_f32_grade(pkg, ref, t):
         assert met["finite"] and met["elemwise"] <= DECODE_TOL, ((t, m, n, k), met)
 
 
+@pytest.mark.parametrize("t", [14, 8, 12])
+@pytest.mark.parametrize("xdt", [np.float32, np.float16])
+def test_batched_decode_random_blocks(pkg, ref, t, xdt):
+    """The batched decode (M = 2 .. 32) on random blocks: every code and every
+    scale value (Q6_K's int8 group scales include -128 and the negative high
+    nibbles that the kernel splits off; Q8_0 blocks of one unit carry unrelated
+    scales, each block its own activation exponent), with and without a
+    workspace, per element within 2e-5 sum_k |x_k w_nk| of the oracle's f64
+    product.  K = 4128 (Q8_0: not a multiple of 256) takes the other batched
+    kernel."""
+    lib = pkg.load_library()
+    s = torch.cuda.current_stream().cuda_stream
+    x_type = 0 if xdt == np.float32 else 1
+    shapes = [(2, 48, 512), (8, 100, 1024), (16, 64, 768), (17, 33, 1280), (32, 130, 2048)]
+    if t == 8:
+        shapes.append((9, 40, 4128))
+    for i, (m, n, k) in enumerate(shapes):
+        raw = tile_model.random_blocks(t, n, k, seed=70 * t + i, specials=False)
+        rng = np.random.default_rng(i)
+        x = rng.standard_normal((m, k)).astype(np.float32)
+        if t == 8 and xdt == np.float32:
+            # one block per 256 elements holds activations 2^30 larger but all-zero
+            # codes: the other blocks carry the whole result, at full precision
+            # only if each block has its own exponent
+            b0 = i % 8
+            raw.reshape(n, k // 32, 34)[:, b0::8, 2:] = 0
+            xb = x.reshape(m, k // 32, 32)
+            xb[:, b0::8, :] *= 2.0 ** 30
+        w = pkg.repack_gguf_for_gpu(t, raw, n, k)
+        wdeq = ref.dequant_rows(t, raw, n, k)
+        x = x.astype(xdt)
+        xd = torch.from_numpy(x).cuda()
+        need = lib.gguf_hip_matmul_workspace(t, x_type, n, k, m)
+        outs = []
+        for use_ws in (True, False):
+            work = torch.zeros(max(need, 16), dtype=torch.uint8, device="cuda") if use_ws else None
+            y = torch.full((m, n), float("nan"), device="cuda")
+            rc = lib.gguf_hip_matmul_ws(xd.data_ptr(), x_type, k, w.ptr(), t, n, k, y.data_ptr(), n,
+                                        m, DECODE, work.data_ptr() if use_ws else None,
+                                        need if use_ws else 0, s)
+            assert rc == 0, lib.gguf_hip_last_error()
+            x64 = x.astype(np.float64)
+            met = ref.parity_metrics(y.cpu().numpy(), ref.matmul_bt(x64, wdeq),
+                                     ref.matmul_bt_abs(x64, wdeq))
+            assert met["finite"] and met["elemwise"] <= DECODE_TOL, ((t, xdt, m, n, k, use_ws), met)
+            if use_ws:
+                assert int(torch.count_nonzero(work[:65536])) == 0
+            outs.append(y)
+
+
 def test_reference_kernel_test_shapes(pkg, ref):
     """kernel-tests.ts:910-927: M=3, N=70, K=512 per type, and N > 65535 (Q8_0, M=1, K=64)."""
     for t in (2, 6, 8, 10, 11, 12, 13, 14, 20, 23):
