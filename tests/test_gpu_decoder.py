@@ -73,7 +73,7 @@ class Reference:
         z = torch.complex(x[:, :D // 2], x[:, D // 2:]) * torch.exp(1j * theta)
         return torch.cat([z.real, z.imag], dim=-1)
 
-    def token(self, tok, pos):
+    def token(self, tok, pos, logits=True):
         c = self.cfg
         x = self.embed[tok]
         nh, nkv, hd = c.n_heads, c.n_kv_heads, c.head_dim
@@ -95,7 +95,7 @@ class Reference:
             gu = L["gu"] @ self.norm(x, L["fn"])
             g, u = gu[:c.ffn], gu[c.ffn:]
             x = x + L["down"] @ (u * g / (1 + torch.exp(-g)))
-        return self.lm @ self.norm(x, self.fnorm)
+        return self.lm @ self.norm(x, self.fnorm) if logits else None
 
 
 def _rel(a, b):
@@ -205,5 +205,78 @@ def test_32_layer_fused_matches_unfused(dec):
             assert torch.equal(ta, tb)
         tok = tb
     assert torch.equal(pa, pb)
+    del a, b, w
+    torch.cuda.empty_cache()
+
+
+BENCH_PROMPT, BENCH_LATE = 128, 376  # the bench decodes positions 128 .. 383
+
+
+def _teacher_forced(models, tokens, pos0):
+    """Decode steps at positions pos0, pos0 + 1, ... feeding ``tokens`` to every
+    model in ``models``; returns each step's logits per model."""
+    out = []
+    pos = [torch.tensor([pos0], device="cuda") for _ in models]
+    for t in tokens:
+        row = []
+        for m, p in zip(models, pos):
+            tok = torch.tensor([t], device="cuda")
+            row.append(m.step(tok, p).clone()[0])
+        out.append(row)
+    return out
+
+
+def test_bench_length_full_width_matches_float64_reference(dec):
+    """The bench's sequence at 2 layers of the full width: a 128-token prompt,
+    teacher-forced decode steps at positions 128-135, the positions up to 375
+    filled by a prefill, then steps at 376-383 (six 64-slot attention ranges
+    merged inside the output projection), against the float64 restatement."""
+    cfg = dec.DecoderConfig(**dict(FULL_WIDTH, max_seq=512))
+    w = dec.synthetic_weights(cfg, seed=6, device="cuda", lm_head_unique_rows=2048)
+    m = dec.QuantDecoder(cfg, w)
+    ref = Reference(cfg, w)
+    rng = np.random.default_rng(8)
+    toks = rng.integers(0, cfg.vocab, BENCH_LATE + 8).tolist()
+    logits = m.prefill(torch.tensor(toks[:BENCH_PROMPT], device="cuda"), 0)[0]
+    for p in range(BENCH_PROMPT):
+        rl = ref.token(toks[p], p, logits=p == BENCH_PROMPT - 1)
+    assert _rel(logits, rl) < 1e-4
+    for i, (lg,) in enumerate(_teacher_forced([m], toks[BENCH_PROMPT:BENCH_PROMPT + 8],
+                                              BENCH_PROMPT)):
+        rl = ref.token(toks[BENCH_PROMPT + i], BENCH_PROMPT + i)
+        assert _rel(lg, rl) < 1e-4, BENCH_PROMPT + i
+    mid = toks[BENCH_PROMPT + 8:BENCH_LATE]
+    m.prefill(torch.tensor(mid, device="cuda"), BENCH_PROMPT + 8)
+    for p in range(BENCH_PROMPT + 8, BENCH_LATE):
+        ref.token(toks[p], p, logits=False)
+    for i, (lg,) in enumerate(_teacher_forced([m], toks[BENCH_LATE:BENCH_LATE + 8], BENCH_LATE)):
+        rl = ref.token(toks[BENCH_LATE + i], BENCH_LATE + i)
+        assert _rel(lg, rl) < 1e-4, BENCH_LATE + i
+    del ref, m, w
+    torch.cuda.empty_cache()
+
+
+def test_bench_length_32_layer_fused_matches_unfused(dec):
+    """The bench decoder (32 layers) over the bench's sequence: a 128-token
+    prompt, then teacher-forced decode steps at positions 128-135 and, after the
+    positions up to 375 are filled by a prefill, 376-383: the fused step (five
+    launches per layer, the attention merge in the output projection) against
+    the torch-glue step over plain projections."""
+    cfg = dec.DecoderConfig()
+    w = dec.synthetic_weights(cfg, seed=0, device="cuda", lm_head_unique_rows=16384)
+    a, b = dec.QuantDecoder(cfg, w, fused=True), dec.QuantDecoder(cfg, w, fused=False)
+    toks = np.random.default_rng(10).integers(0, cfg.vocab, BENCH_LATE + 8).tolist()
+    for m in (a, b):
+        m.prefill(torch.tensor(toks[:BENCH_PROMPT], device="cuda"), 0)
+    for i, (ga, gb) in enumerate(_teacher_forced((a, b), toks[BENCH_PROMPT:BENCH_PROMPT + 8],
+                                                 BENCH_PROMPT)):
+        assert _rel(ga, gb) < 1e-4, BENCH_PROMPT + i
+    for m in (a, b):
+        m.prefill(torch.tensor(toks[BENCH_PROMPT + 8:BENCH_LATE], device="cuda"), BENCH_PROMPT + 8)
+    for i, (ga, gb) in enumerate(_teacher_forced((a, b), toks[BENCH_LATE:BENCH_LATE + 8],
+                                                 BENCH_LATE)):
+        assert _rel(ga, gb) < 1e-4, BENCH_LATE + i
+    assert torch.allclose(a.k_cache[:, :, :BENCH_LATE + 8], b.k_cache[:, :, :BENCH_LATE + 8],
+                          rtol=1e-4, atol=1e-4)
     del a, b, w
     torch.cuda.empty_cache()
