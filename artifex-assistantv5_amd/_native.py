@@ -17,7 +17,7 @@ from .ggml import GGMLTypeError
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libgguf_hip.so")
-ABI_VERSION = 16
+ABI_VERSION = 17
 
 ERR_TYPE, ERR_SHAPE, ERR_NULL, ERR_ALIGN, ERR_DTYPE, ERR_BYTES, ERR_HIP = -1, -2, -3, -4, -5, -6, -7
 VARIANT_AUTO, VARIANT_DECODE, VARIANT_GEMM = 0, 1, 2

@@ -10,10 +10,10 @@
 // workgroup's shared memory holds them, one block of mk_unit_bytes<MA>() per
 // 256-element unit (MA activation tiles of 16 MFMA rows each).  Up to 16 rows
 // of f32 (32 of f16, MA <= 2) each workgroup of mk_kernel converts its own K
-// range, so a call is one launch; wider batches convert once per call into
-// the workspace (mk_prep_kernel), and the workgroups copy their range.  K is
-// split over workgroups (ranges); the last range of a tile group to finish
-// adds the ranges' partial sums in range order.
+// range; wider batches convert once per call into the workspace
+// (mk_prep_kernel), and the workgroups copy their range.  K is split over
+// workgroups (ranges); each range writes its partial sums and
+// mk_reduce_kernel adds them in range order.
 //   A [16 MA][kMkLd] f16  MFMA row 2m + p holds part p (hi, lo) of activation
 //                         row m for f32 inputs (8 rows per tile); row m holds
 //                         row m for 16-bit inputs (16 rows per tile).  The
@@ -117,10 +117,6 @@ __device__ __forceinline__ void load_unit(__amdgpu_buffer_rsrc_t rs, int soff, i
 #endif
 constexpr int kMkFuseKw = 4;  // units per K range when the workgroups convert their own range
 constexpr int kMkBatch = 8;  // ranges whose partial sums are requested at a time by the reduction
-constexpr int kMkOuts = 4;   // outputs a thread of the in-kernel reduction takes at a time
-#ifndef GGUF_MK_FOLD_MAX
-#define GGUF_MK_FOLD_MAX 32768  // partial sums one workgroup may add (rows x M x ranges) in-kernel
-#endif
 #ifndef GGUF_MK_WIDE_T
 #define GGUF_MK_WIDE_T 1  // row tiles per wave for 3 or 4 activation tiles (16 T tiles per workgroup)
 #endif
@@ -532,23 +528,24 @@ __device__ __forceinline__ void mk_unit_q8(const Q8Super (&w)[T], int bo, int la
 // shared memory.
 //
 // SX (narrow tiles, MA <= 2): the workgroup converts its own range of x into
-// the image (mk_stage, one wave per (unit, activation row)), so the call is
-// one launch.  Otherwise the image comes from the workspace (mk_prep_kernel):
-// through registers for MA <= 2, LDS-direct loads for MA 3, 4.
+// the image (mk_stage, one wave per (unit, activation row)).  Otherwise the
+// image comes from the workspace (mk_prep_kernel): through registers for
+// MA <= 2, LDS-direct loads for MA 3, 4.
 //
 // K split over gridDim.y > 1 ranges: each range's partial sums go to `part`
-// ([range][M][np]); the last of a tile group's ranges to finish (an atomic
-// counter per group, cnt[blockIdx.x], zero before the call and left zero)
-// adds them in range order and writes y, so the result does not depend on
-// which range finishes last.
+// ([range][M][np]) and mk_reduce_kernel adds them in range order, so the
+// result does not depend on which range finishes first.  (The last range of
+// a tile group adding the partials itself, behind an agent-scope release /
+// acquire counter, measured 1.5-3 us slower per call than the second launch:
+// the partial stores, the count and the reads are three dependent memory
+// round trips under the weight stream.)
 template <int TYPE, typename XT, int MA, int T, int TS, int KL, bool SX>
 __global__ __launch_bounds__(64 * TS * KL) void mk_kernel(const uint8_t *__restrict__ img,
                                                           const XT *__restrict__ x, int64_t ldx,
                                                           const uint8_t *__restrict__ W, int N,
                                                           int K, int M, int kw,
                                                           float *__restrict__ y, int64_t ldy,
-                                                          float *__restrict__ part,
-                                                          unsigned *__restrict__ cnt, int fold) {
+                                                          float *__restrict__ part) {
   constexpr int PARTS = sizeof(XT) == 4 ? 2 : 1, NW = TS * KL;
   constexpr int UB = mk_ub<TYPE, MA>(), TU = MkFmt<TYPE>::TU;
   constexpr int KWM = SX ? kMkFuseKw : mk_kw_max<TYPE, MA>();  // units a range may hold
@@ -713,20 +710,11 @@ __global__ __launch_bounds__(64 * TS * KL) void mk_kernel(const uint8_t *__restr
               acc[t][a][i] += red[(((((k2 - 1) * TS + ts) * T + t) * MA + a) * 4 + i) * 64 + lane];
     }
   }
-  // this range's sums: to y when K is not split, else to the range's partials.
-  // Partials the kernel adds itself (fold) are agent-scope atomic stores
-  // (written through to the level that every XCD sees) and are read back with
-  // agent-scope atomic loads.
+  // this range's sums: to y when K is not split, else to the range's partials
   const bool split = gridDim.y > 1;
   const int np = ntiles * 16;
   float *o = split ? part + (int64_t)blockIdx.y * M * np : y;
   const int64_t ldo = split ? (int64_t)np : ldy;
-  auto put = [&](int m, int n, float v) {
-    if (split && fold)
-      __hip_atomic_store(o + (int64_t)m * ldo + n, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    else
-      o[(int64_t)m * ldo + n] = v;
-  };
   if (kl == 0) {
 #pragma unroll
     for (int t = 0; t < T; ++t) {
@@ -736,74 +724,18 @@ __global__ __launch_bounds__(64 * TS * KL) void mk_kernel(const uint8_t *__restr
       for (int a = 0; a < MA; ++a) {
         if (PARTS == 2) {
           const int m = 8 * a + 2 * g;
-          if (m < M) put(m, n, acc[t][a][0] + acc[t][a][1]);
-          if (m + 1 < M) put(m + 1, n, acc[t][a][2] + acc[t][a][3]);
+          if (m < M) o[(int64_t)m * ldo + n] = acc[t][a][0] + acc[t][a][1];
+          if (m + 1 < M) o[(int64_t)(m + 1) * ldo + n] = acc[t][a][2] + acc[t][a][3];
         } else {
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
             const int m = 16 * a + 4 * g + i;
-            if (m < M) put(m, n, acc[t][a][i]);
+            if (m < M) o[(int64_t)m * ldo + n] = acc[t][a][i];
           }
         }
       }
     }
   }
-  if (!split || !fold) return;  // (not fold: mk_reduce_kernel adds the partials)
-  // The last range of the tile group to finish adds the partials in range
-  // order.  Ordering: the barrier makes every wave's partial stores happen
-  // before thread 0's count, which is a release at agent scope (so they are
-  // visible device-wide before the count is); the range that sees the final
-  // count takes an agent-scope acquire fence before the barrier that releases
-  // its waves to read the partials.
-  __shared__ unsigned last;
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    last = __hip_atomic_fetch_add(cnt + blockIdx.x, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT) ==
-                   gridDim.y - 1 ? 1u : 0u;
-    if (last) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-  }
-  __syncthreads();
-  if (!last) return;
-  // kMkOuts outputs per thread at a time, their partials requested kMkBatch
-  // ranges at a time
-  constexpr int RG = 16 * TS * T;  // rows of the tile group
-  const int n0 = RG * blockIdx.x, S = gridDim.y;
-  const int64_t st = (int64_t)M * np;
-  for (int e0 = threadIdx.x; e0 < M * RG; e0 += 64 * NW * kMkOuts) {
-    float *p[kMkOuts];
-    bool ok[kMkOuts];
-    float a[kMkOuts];
-#pragma unroll
-    for (int j = 0; j < kMkOuts; ++j) {
-      const int e = e0 + 64 * NW * j, m = e / RG, n = n0 + (e - m * RG);
-      ok[j] = e < M * RG && n < N;
-      p[j] = part + (ok[j] ? (int64_t)m * np + n : 0);
-      a[j] = __hip_atomic_load(p[j], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
-    for (int s0 = 1; s0 < S; s0 += kMkBatch) {
-      float v[kMkOuts][kMkBatch];
-#pragma unroll
-      for (int j = 0; j < kMkOuts; ++j)
-#pragma unroll
-        for (int s = 0; s < kMkBatch; ++s)
-          v[j][s] = s0 + s < S ? __hip_atomic_load(p[j] + (s0 + s) * st, __ATOMIC_RELAXED,
-                                                   __HIP_MEMORY_SCOPE_AGENT)
-                               : 0.f;
-#pragma unroll
-      for (int j = 0; j < kMkOuts; ++j)
-#pragma unroll
-        for (int s = 0; s < kMkBatch; ++s)
-          if (s0 + s < S) a[j] += v[j][s];
-    }
-#pragma unroll
-    for (int j = 0; j < kMkOuts; ++j) {
-      if (!ok[j]) continue;
-      const int e = e0 + 64 * NW * j, m = e / RG, n = n0 + (e - m * RG);
-      y[(int64_t)m * ldy + n] = a[j];
-    }
-  }
-  if (threadIdx.x == 0)  // ready for the next call
-    __hip_atomic_store(cnt + blockIdx.x, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // y[m, n] = sum over the S ranges of part[s][m][n] (row stride np), in range
@@ -836,14 +768,11 @@ __global__ __launch_bounds__(256) void mk_reduce_kernel(const float *__restrict_
 //   Otherwise: as few ranges as the shared memory allows (the image comes
 //     from the prep launch), more while the grid has fewer than
 //     GGUF_MK_MIN_WGS workgroups.
-// Workspace: the tile groups' counters in the counter prefix (split K only),
-// then, from kWsPrefix on, the image (not SX) and the ranges' partial sums
-// (split K only).  mk_plan takes at most kMkMaxGroups tile groups (the
-// counters the prefix holds); launch_mk runs wider weights in row blocks.
-constexpr int kMkMaxGroups = (int)(kWsPrefix / 4);
+// Workspace: from kWsPrefix on (the prefix is not used here), the image (not
+// SX) and the ranges' partial sums (split K only).
 struct MkPlan {
   int ma, ts, kl, t, groups, kw, ranges;
-  bool sx, fold;  // fold: the last range of a tile group adds the partials
+  bool sx;
   size_t lds, part_off, bytes;  // part_off: from the start of the workspace
 };
 template <int TYPE, typename XT>
@@ -867,7 +796,6 @@ MkPlan mk_plan(int M, int N, int K) {
   while (ranges < nu && (int64_t)p.groups * ranges < GGUF_MK_MIN_WGS) ++ranges;
   p.kw = (nu + ranges - 1) / ranges;
   p.ranges = (nu + p.kw - 1) / p.kw;
-  p.fold = p.ranges > 1 && (int64_t)p.ts * p.t * 16 * M * p.ranges <= GGUF_MK_FOLD_MAX;
   const size_t stage = ((size_t)p.kw * ub + 1023) & ~(size_t)1023;
   const size_t red = (size_t)(p.kl - 1) * p.ts * p.t * p.ma * 4 * 64 * 4;
   const size_t used = stage + iq_tbl_bytes<TYPE>();  // the tables sit behind the range
@@ -900,10 +828,9 @@ hipError_t launch_mk_ma(const XT *x, int64_t ldx, const uint8_t *W, int N, int K
   }
   hipLaunchKernelGGL(kern, dim3((unsigned)p.groups, (unsigned)p.ranges), dim3(64 * TS * KL), p.lds, s,
                      img, x, ldx, W, N, K, M, p.kw, y, ldy,
-                     p.ranges > 1 ? (float *)(ws + p.part_off) : nullptr,
-                     p.ranges > 1 ? (unsigned *)ws : nullptr, p.fold ? 1 : 0);
+                     p.ranges > 1 ? (float *)(ws + p.part_off) : nullptr);
   e = hipGetLastError();
-  if (e != hipSuccess || p.ranges == 1 || p.fold) return e;
+  if (e != hipSuccess || p.ranges == 1) return e;
   const int np = (N + 15) / 16 * 16;
   hipLaunchKernelGGL(mk_reduce_kernel, dim3((unsigned)((N + 255) / 256), (unsigned)M), dim3(256), 0, s,
                      (const float *)(ws + p.part_off), p.ranges, M, np, N, y, ldy);
@@ -925,18 +852,6 @@ hipError_t launch_mk(const XT *x, int64_t ldx, const uint8_t *W, int N, int K, f
   const MkPlan p = mk_plan<TYPE, XT>(M, N, K);
   if (M > 32 || (p.bytes > 0 && (!work || (size_t)work_floats * 4 < p.bytes)))
     return hipErrorNotSupported;
-  if (p.ranges > 1 && p.groups > kMkMaxGroups) {
-    // more tile groups than counters: blocks of rows, one launch each (in
-    // stream order, so each block finds the counters zero again)
-    const int rb = kMkMaxGroups * p.ts * p.t * 16;
-    const int64_t tb = (int64_t)(K / 256) * MkFmt<TYPE>::TU;
-    for (int n0 = 0; n0 < N; n0 += rb) {
-      const hipError_t e = launch_mk<TYPE, XT>(x, ldx, W + (int64_t)(n0 / 16) * tb, min(rb, N - n0),
-                                               K, y + n0, ldy, M, work, work_floats, s);
-      if (e != hipSuccess) return e;
-    }
-    return hipSuccess;
-  }
   if (p.sx) {
     if (p.ma == 1) return launch_mk_ma<TYPE, XT, 1, 1, 16, 1, true>(x, ldx, W, N, K, y, ldy, M, work, p, s);
     return launch_mk_ma<TYPE, XT, 2, 1, 16, 1, true>(x, ldx, W, N, K, y, ldy, M, work, p, s);

@@ -285,10 +285,10 @@ def _row_stride(t: torch.Tensor, rows: int, cols: int, name: str) -> int:
 
 
 # Matmul workspaces.  Calls that share a workspace must not overlap (the
-# split-K partial sums and the 64 KB counter prefix), and calls on one stream
+# split-K partial sums and the activation image), and calls on one stream
 # are ordered, so there is one workspace per (device, stream): two streams of
-# one device never share one.  Its counter prefix must be zero before first
-# use and every call leaves it zero, so it is allocated zero-filled once.
+# one device never share one.  It is allocated zero-filled once (its first
+# 64 KB are reserved and stay zero).
 # Under graph capture the key also carries the capture: the graph's workspace
 # is allocated inside the capture (its zero fill is a kernel the graph replays
 # ahead of the first use) and is never handed to eager calls, so replays and
@@ -360,7 +360,7 @@ def dispatch_matmul_gguf(a: torch.Tensor, gg: GGUFWeight, c: torch.Tensor, M: in
         raise ValueError(f'matmul_gguf "{label}": C window out of range')
     dev = gg.device
     x_type = _X_TYPES[a.dtype]
-    # the split-K paths' workspace (counters, partial sums of the K slices)
+    # the split-K paths' workspace (activation image, partial sums of the K slices)
     need = _native.check(lib.gguf_hip_matmul_workspace(gg.ggml_type, x_type, N, K, M), lib)
     work = matmul_workspace(dev, need) if need > 0 else None
     with torch.cuda.device(dev):

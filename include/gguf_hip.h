@@ -49,7 +49,7 @@ extern "C" {
  * are exported (kernels and helpers cannot be interposed across libraries). */
 #pragma GCC visibility push(default)
 
-#define GGUF_HIP_ABI_VERSION 16
+#define GGUF_HIP_ABI_VERSION 17
 
 /* ggml type ids (gguf.ts:24-35); activation dtypes reuse F32 / F16. */
 #define GGUF_HIP_F32 0
@@ -175,13 +175,11 @@ int gguf_hip_matmul_variant(const void *x, int x_type, int64_t ldx, const void *
  * results as without a workspace up to f32 rounding of the sums,
  * deterministic either way, and much faster for weights of few rows (the FFN
  * down projection) and short prefills (M = 512, N = 4096: 258 -> 476
- * TFLOP/s).  The batched decode of Q4_K and the grid-codebook types is then
- * one launch up to 16 f32 (32 f16) rows: each workgroup converts its own K
- * range of the activations, and the last K range of a row block to finish
- * adds the ranges' sums (counted in the workspace).
- * The workspace's first 65536 bytes are those counters: they must be zero
- * before the workspace's first use (allocate it zero-filled), and every call
- * leaves them zero, so one workspace serves calls of any shape and type.
+ * TFLOP/s).  Up to 16 f32 (32 f16) rows the batched decode converts the
+ * activations in every workgroup (its own K range); a second launch adds the
+ * K ranges' sums in range order.
+ * The workspace's first 65536 bytes are reserved: no call reads or writes
+ * them, and one workspace serves calls of any shape and type.
  * The reference engine likewise preallocates its scratch (forward-pass.ts:1140-1163).
  * Calls that share a workspace must not overlap.
  * The grid-codebook IQ types run the decode variant without a workspace up

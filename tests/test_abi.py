@@ -98,7 +98,7 @@ def test_grid_types_contract(lib, native):
 
 
 def test_abi_version(lib):
-    assert lib.gguf_hip_abi_version() == 16
+    assert lib.gguf_hip_abi_version() == 17
 
 
 def test_type_traits(lib, native):

@@ -111,7 +111,7 @@ def test_api_contract(pkg, native):
     assert lib.gguf_hip_matmul_workspace(t, 0, n, k, 1) == 0
     need = lib.gguf_hip_matmul_workspace(t, 0, n, k, m)
     assert need > 0
-    ws = torch.zeros(need, dtype=torch.uint8, device="cuda")  # counters start at zero
+    ws = torch.zeros(need, dtype=torch.uint8, device="cuda")  # zero-filled
     outs = []
     for work, nb in ((None, 0), (ws.data_ptr(), need - 1), (ws.data_ptr(), need)):
         y.zero_()
@@ -120,7 +120,7 @@ def test_api_contract(pkg, native):
         assert rc == 0, native.last_error(lib)
         outs.append(y.cpu().numpy().copy())
     assert np.array_equal(outs[0], outs[1])
-    assert np.count_nonzero(ws.cpu().numpy()[:65536]) == 0  # counters left zero
+    assert np.count_nonzero(ws.cpu().numpy()[:65536]) == 0  # the reserved prefix is never written
     # beyond K = 16384 only the batched kernel serves the grid types: a workspace is required
     kb = 16640
     assert lib.gguf_hip_matmul_workspace(t, 0, n, kb, 1) > 0

@@ -375,14 +375,13 @@ def test_gemm_split_k(pkg, ref, t, m, n, k, xdt):
 
 
 @pytest.mark.gpu
-def test_shared_workspace_counters_stay_zero(pkg, ref):
+def test_shared_workspace_prefix_stays_zero(pkg, ref):
     """One workspace serves, in turn, the batched decode with K split over the
-    grid (one launch: the last K range of each tile group adds the partials,
-    counted in the workspace's counter prefix), the split-K GEMM and the
-    other types' split decode; up to 16 f32 rows the batched decode converts
-    the activations in every workgroup, 32 f32 rows go through the prep
-    launch.  The counter prefix reads zero after every call, and each call
-    repeats its first result exactly."""
+    grid (the K ranges' partial sums added in range order by a second
+    launch), the split-K GEMM and the other types' split decode; up to 16 f32
+    rows the batched decode converts the activations in every workgroup, 32
+    f32 rows go through the prep launch.  The reserved 64 KB prefix reads zero
+    after every call, and each call repeats its first result exactly."""
     lib = pkg.load_library()
     cases = [(12, 8, 4096, 4096, 0, DECODE), (12, 3, 1024, 2048, 1, DECODE),
              (12, 512, 4096, 4096, 1, GEMM), (14, 8, 512, 4096, 0, DECODE),
@@ -405,7 +404,7 @@ def test_shared_workspace_counters_stay_zero(pkg, ref):
                                         m, var, work.data_ptr(), need, s)
             assert rc == 0, lib.gguf_hip_last_error()
             torch.cuda.synchronize()
-            assert int(work[:65536].count_nonzero()) == 0, ("counter prefix", t, m, n, k)
+            assert int(work[:65536].count_nonzero()) == 0, ("reserved prefix", t, m, n, k)
             if rep == 0:
                 first.append(y)
                 if var == DECODE and x_type == 0:
@@ -417,10 +416,10 @@ def test_shared_workspace_counters_stay_zero(pkg, ref):
 
 
 def test_workspace_per_stream(pkg):
-    """Batched decode (Q4_K, M = 8: split K, the last range adds the partials,
-    counted in the workspace) alternating between two streams of one device:
-    each stream gets its own workspace, the results equal the single-stream
-    ones bit for bit, and both counter prefixes are zero afterwards."""
+    """Batched decode (Q4_K, M = 8: split K, the K ranges' partial sums in the
+    workspace) alternating between two streams of one device: each stream
+    gets its own workspace and the results equal the single-stream ones bit
+    for bit."""
     lin = importlib.import_module("artifex-assistantv5_amd.linear")
     raw, w = _case(pkg, 12, 14336, 4096, seed=9)
     xs = [torch.from_numpy(pkg.quantize.synthetic_activations(8, 4096, seed=s)).cuda()
