@@ -58,6 +58,9 @@ constexpr int kAI = kBM * 8 / kThreads;  // activation chunks staged per thread
 constexpr int kARows = kThreads / 8;     // row distance between a thread's chunks
 constexpr int kRowB = 2 * kBK;             // LDS bytes per activation row
 constexpr int kStageB = kBM * kRowB;       // LDS bytes per pipeline stage
+#ifndef GGUF_GEMM_WIDE_MIN
+#define GGUF_GEMM_WIDE_MIN 192  // Q4_K fp16: the wide tile once it gives this many workgroups
+#endif
 #ifndef GGUF_GEMM_GN
 #define GGUF_GEMM_GN 4  // tile order: column bands of this many tiles (0: row tiles fastest)
 #endif
@@ -1150,9 +1153,219 @@ inline int gemm_splits(int type, int64_t tiles, int nu) {
   return sp;
 }
 
+// ---------------------------------------------------------------------------
+// Wide-tile Q4_K GEMM for large grids (fp16 activations).  A workgroup of 8
+// waves owns a 128 x 512 output tile; wave w owns all 128 rows and the 64
+// columns [64 w, 64 w + 64) (four row tiles of the weight): 32 accumulator
+// tiles, 254 VGPRs, two waves per SIMD.  Against gemm_kernel's 128 x 32 per
+// wave, each activation fragment read from LDS feeds twice the MFMAs and a
+// step holds twice the MFMA work per barrier; each dequantized B operand
+// still feeds 8 MFMAs.
+//   Per 64-wide step: the activations of the next step go from registers to
+//   the other LDS stage and the step after that is requested; then k-half by
+//   k-half the 8 fragments of the half are read and each tile's B operand is
+//   dequantized (fp16(d sc q - dmin m), one rounding, as gemm_kernel) just
+//   before its 8 MFMAs; a tile's codes for two steps ahead are requested once
+//   both its operands of this step are built; one barrier.  The step is
+//   branch-free: past the end of K the loads stay inside their buffer
+//   resources and their data is never used.
+// The MFMAs of an output element run in the same k order as gemm_kernel's,
+// so the results are the same bit for bit.
+// Measured (one box, fp16, K = 4096 unless noted), TFLOP/s against
+// gemm_kernel: M = 2048, N = 14336 778 -> 864; M = 8192, N = 14336
+// 968 -> 1053; M = 8192, N = 4096, K = 14336 970 -> 1092.
+//   - One wave per SIMD with 128 x 128 per wave (256 accumulators) spills
+//     (136-164 dwords: the allocator copies accumulators between AGPRs and
+//     VGPRs).
+//   - Pinning an MFMA / VALU interleave (sched_group_barrier, 2-3 VALU per
+//     MFMA) forces 55-89 dwords of spill and runs at 410-626.
+//   - Reading the A fragments a few ahead of their MFMAs instead of all at
+//     the start of a half (gemm_kernel, 2-8 ahead): 734-770 against 786.
+// ---------------------------------------------------------------------------
+constexpr int kWW = 8, kWTN = 4, kWTM = 8;
+constexpr int kWBM = 16 * kWTM, kWBN = 16 * kWTN * kWW;
+constexpr int kWThr = 64 * kWW;
+constexpr int kWAI = kWBM * 8 / kWThr;  // 16-byte activation chunks a thread stages per step
+constexpr int kWAR = kWThr / 8;         // row distance between them
+constexpr int kWStB = kWBM * kRowB;
+
+struct WideQ4K {
+  rsrc_t ars, brs;
+  int avoff, row0, cc, ts, nu, af0, af1;
+  int64_t ldxb;
+  BOff bo;
+  uint4 ar[kWAI];
+  uint2 cq[2][kWTN];
+  uint4 hd[kWTN];
+  uint32_t sc[kWTN][2], mn[kWTN][2];
+  float d24[kWTN], dmin[kWTN];
+  float4_t acc[kWTM][kWTN];
+  unsigned char *lds;
+
+  __device__ __forceinline__ void load_a(int k0) {
+#pragma unroll
+    for (int i = 0; i < kWAI; ++i) ar[i] = bl16(ars, avoff, (int)(kWAR * i * ldxb) + 2 * k0);
+  }
+  __device__ __forceinline__ void store_a(int stage) {
+#pragma unroll
+    for (int i = 0; i < kWAI; ++i)
+      *(uint4 *)(lds + stage * kWStB + lds_at(row0 + kWAR * i, cc)) = ar[i];
+  }
+  __device__ __forceinline__ void load_codes(int set, int j, int u, int c) {
+    cq[set][j] = bl8(brs, bo.v1, j * ts + u * Fmt<12>::TU + (c >> 1) * 1024 + 8 * (c & 1));
+  }
+  __device__ __forceinline__ void load_hdr(int u) {
+#pragma unroll
+    for (int j = 0; j < kWTN; ++j) hd[j] = bl16(brs, bo.v0, j * ts + u * Fmt<12>::TU);
+  }
+  __device__ __forceinline__ void set_cur() {
+#pragma unroll
+    for (int j = 0; j < kWTN; ++j) {
+      q4k_scales_packed(hd[j].y, hd[j].z, hd[j].w, sc[j][0], sc[j][1], mn[j][0], mn[j][1]);
+      const float d = h2f(hd[j].x);
+      d24[j] = d * kTwo24;
+      dmin[j] = h2f(hd[j].x >> 16);
+    }
+  }
+  // B operand of tile j, k-half h (sub-block 2c + h) of window c
+  template <int C, int H>
+  __device__ __forceinline__ half8_t bfrag(uint2 q2, int j) const {
+    constexpr int Wd = C >> 1, B0 = ((2 * C) & 3) + H;
+    // the high nibble enters as 16 q: its scale carries 1/16 (exact)
+    const float s = (H ? d24[j] * 0.0625f : d24[j]) * ubyte(sc[j][Wd], B0),
+                c = -(dmin[j] * ubyte(mn[j][Wd], B0));
+    constexpr uint32_t m = H ? 0x00F000F0u : 0x000F000Fu;
+    uint32_t v[4];
+#pragma unroll
+    for (int w = 0; w < 2; ++w) {
+      const uint32_t q = w ? q2.y : q2.x, q8 = q >> 8;
+      const uint32_t e = q & m, o = q8 & m;
+      v[2 * w] = mix_lo(e, o, s, c);
+      v[2 * w + 1] = mix_hi(e, o, s, c);
+    }
+    return h8(v[0], v[1], v[2], v[3]);
+  }
+
+  // step s = 4 u + C: A from stage C & 1, codes from set C & 1.  First the A
+  // of step s + 1 (loaded during step s - 1) goes to the other stage (read by
+  // step s - 1, which every wave has left) and step s + 2's A is requested;
+  // then k-half by k-half the fragments of this step, each tile's B operand
+  // dequantized before its 8 MFMAs and its codes of step s + 2 requested once
+  // both halves are built.
+  template <int C>
+  __device__ __forceinline__ void step(int u) {
+    constexpr int P = C & 1;
+    // branch-free: past the end of K these loads are bounded by the buffer
+    // resources (in-range bytes or zeros) and their data is never used
+    const int s = 4 * u + C;
+    store_a(P ^ 1);
+    load_a(64 * (s + 2));
+    if (C == 2) load_hdr(u + 1);
+    const unsigned char *base = lds + P * kWStB;
+    const int u2 = (s + 2) >> 2;
+    constexpr int C2 = (C + 2) & 3;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      half8_t a[kWTM];
+#pragma unroll
+      for (int i = 0; i < kWTM; ++i) a[i] = *(const half8_t *)(base + (h ? af1 : af0) + i * 16 * kRowB);
+#pragma unroll
+      for (int j = 0; j < kWTN; ++j) {
+        const half8_t b = h ? bfrag<C, 1>(cq[P][j], j) : bfrag<C, 0>(cq[P][j], j);
+        if (h == 1) load_codes(P, j, u2, C2);
+#pragma unroll
+        for (int i = 0; i < kWTM; ++i) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[i], b, acc[i][j], 0, 0, 0);
+      }
+      __builtin_amdgcn_sched_barrier(0);  // one half's fragments live at a time
+    }
+    __syncthreads();
+  }
+};
+
+template <typename XT>
+__global__ __launch_bounds__(kWThr) void gemm_wide_q4k(const XT *__restrict__ x, int64_t ldx,
+                                                      const uint8_t *__restrict__ W, int M, int N,
+                                                      int K, float *__restrict__ y, int64_t ldy,
+                                                      int tiles_m) {
+  __shared__ __align__(16) unsigned char lds[2 * kWStB];
+  int bid = blockIdx.x;
+  if ((gridDim.x & 7) == 0) bid = (bid & 7) * (gridDim.x >> 3) + (bid >> 3);
+  int m0, n0;
+  {
+    const int band = bid / (tiles_m * GGUF_GEMM_GN), in = bid - band * tiles_m * GGUF_GEMM_GN;
+    const int tiles_n = (int)gridDim.x / tiles_m;
+    const int gn = min(GGUF_GEMM_GN, tiles_n - band * GGUF_GEMM_GN);
+    m0 = (in / gn) * kWBM;
+    n0 = (band * GGUF_GEMM_GN + in % gn) * kWBN;
+  }
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int r = lane & 15, g = lane >> 4;
+  WideQ4K s;
+  s.lds = lds;
+  s.nu = K / 256;
+  s.ts = s.nu * Fmt<12>::TU;
+  const int ntiles = (N + 15) >> 4, t0 = (n0 >> 4) + kWTN * wave;
+  const int nt = __builtin_amdgcn_readfirstlane(max(0, min(kWTN, ntiles - t0)));
+  s.brs = make_rsrc(W + (int64_t)min(t0, ntiles - 1) * s.ts, (uint32_t)__builtin_amdgcn_readfirstlane(nt * s.ts));
+  s.bo = b_offsets<12>(r, g);
+  const int rows = min(kWBM, M - m0);
+  s.ldxb = ldx * (int64_t)sizeof(XT);
+  s.ars = make_rsrc(x + (int64_t)m0 * ldx,
+                    (uint32_t)__builtin_amdgcn_readfirstlane(
+                        (int)((int64_t)(rows - 1) * s.ldxb + (int64_t)K * sizeof(XT))));
+  s.row0 = tid >> 3;
+  s.cc = tid & 7;
+  s.avoff = (int)(s.row0 * s.ldxb) + s.cc * 16;
+  s.af0 = lds_at(r, g);
+  s.af1 = lds_at(r, 4 + g);
+#pragma unroll
+  for (int i = 0; i < kWTM; ++i)
+#pragma unroll
+    for (int j = 0; j < kWTN; ++j) s.acc[i][j] = float4_t{0.f, 0.f, 0.f, 0.f};
+  // prologue: header of superblock 0, A of steps 0 and 1, codes of steps 0 and 1
+  s.load_hdr(0);
+  s.load_a(0);
+#pragma unroll
+  for (int j = 0; j < kWTN; ++j) {
+    s.load_codes(0, j, 0, 0);
+    s.load_codes(1, j, 0, 1);
+  }
+  s.store_a(0);
+  s.load_a(64);
+  __syncthreads();
+  for (int u = 0; u < s.nu; ++u) {
+    s.set_cur();
+    s.template step<0>(u);
+    s.template step<1>(u);
+    s.template step<2>(u);
+    s.template step<3>(u);
+  }
+#pragma unroll
+  for (int i = 0; i < kWTM; ++i)
+#pragma unroll
+    for (int j = 0; j < kWTN; ++j) {
+      const int n = n0 + 16 * (kWTN * wave + j) + r;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int m = m0 + 16 * i + 4 * g + e;
+        if (m < M && n < N) y[(int64_t)m * ldy + n] = s.acc[i][j][e];
+      }
+    }
+}
+
 template <int TYPE, typename XT>
 hipError_t launch_type(const XT *x, int64_t ldx, const uint8_t *W, int M, int N, int K, float *y,
                        int64_t ldy, float *work, int64_t work_floats, hipStream_t s) {
+  if constexpr (TYPE == 12 && sizeof(XT) == 2) {
+    // Q4_K with fp16 activations on a grid that fills the chip: the wide tile
+    const int wm = (M + kWBM - 1) / kWBM, wn = (N + kWBN - 1) / kWBN;
+    if ((int64_t)wm * wn >= GGUF_GEMM_WIDE_MIN) {
+      hipLaunchKernelGGL((gemm_wide_q4k<XT>), dim3((unsigned)(wm * wn)), dim3(kWThr), 0, s, x, ldx, W,
+                         M, N, K, y, ldy, wm);
+      return hipGetLastError();
+    }
+  }
   const int tiles_m = (M + kBM - 1) / kBM, tiles_n = (N + kBN - 1) / kBN, nu = K / Fmt<TYPE>::UE;
   int sp = gemm_splits(TYPE, (int64_t)tiles_m * tiles_n, nu);
   if (!work || work_floats < (int64_t)sp * M * N) sp = 1;

@@ -307,6 +307,23 @@ def test_full_size_configs(pkg, t, m, n, k, xdt):
     _gpu_check(y, x.float(), w.dequant().view(n, k), (t, m, n, k))
 
 
+@pytest.mark.parametrize("m,n,k", [(1000, 14000, 4096), (777, 29000, 1536), (2100, 8200, 4096)])
+def test_wide_gemm_ragged(pkg, m, n, k):
+    """Q4_K prefill with fp16 activations on grids of at least 192 128 x 512
+    tiles takes the wide-tile GEMM: rows past M in the last row tile, a last
+    workgroup with fewer than 32 weight row tiles, N not a multiple of 16 and
+    a K of 6 superblocks, against the f64 product of the dequantized weights;
+    a second call gives the same bits."""
+    g = torch.Generator(device="cuda").manual_seed(m + n + k)
+    wf = torch.randn(n, k, device="cuda", generator=g) * 0.02
+    raw = pkg.quantize.quantize(wf.cpu().numpy(), 12)
+    w = pkg.repack_gguf_for_gpu(12, raw, n, k)
+    x = torch.randn(m, k, device="cuda", generator=g).half()
+    y = pkg.qlinear(x, w)
+    _gpu_check(y, x.float(), w.dequant().view(n, k), (m, n, k))
+    assert torch.equal(pkg.qlinear(x, w), y)
+
+
 @pytest.mark.parametrize("t,m,n,k", [(12, 8, 14336, 4096), (12, 32, 4096, 14336), (14, 17, 4096, 14336),
                                      (2, 32, 4096, 4096), (8, 5, 1000, 2048), (10, 32, 512, 8192),
                                      (13, 2, 300, 4096)])
