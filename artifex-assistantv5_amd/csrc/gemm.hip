@@ -1161,19 +1161,23 @@ inline int gemm_splits(int type, int64_t tiles, int nu) {
 // wave, each activation fragment read from LDS feeds twice the MFMAs and a
 // step holds twice the MFMA work per barrier; each dequantized B operand
 // still feeds 8 MFMAs.
-//   Per 64-wide step: the activations of the next step go from registers to
-//   the other LDS stage and the step after that is requested; then k-half by
-//   k-half the 8 fragments of the half are read and each tile's B operand is
-//   dequantized (fp16(d sc q - dmin m), one rounding, as gemm_kernel) just
-//   before its 8 MFMAs; a tile's codes for two steps ahead are requested once
-//   both its operands of this step are built; one barrier.  The step is
-//   branch-free: past the end of K the loads stay inside their buffer
-//   resources and their data is never used.
+//   Per 64-wide step: the activations of the step after next go from
+//   registers to their LDS stage (four stages) and the following step's are
+//   requested; then k-half by k-half the 8 fragments of the half are read and
+//   each tile's B operand is dequantized (fp16(d sc q - dmin m), one rounding,
+//   as gemm_kernel) just before its 8 MFMAs; a tile's codes for two steps
+//   ahead are requested once both its operands of this step are built; a
+//   barrier after every second step.  The step is branch-free: past the end
+//   of K the loads stay inside their buffer resources and their data is never
+//   used.
 // The MFMAs of an output element run in the same k order as gemm_kernel's,
 // so the results are the same bit for bit.
 // Measured (one box, fp16, K = 4096 unless noted), TFLOP/s against
 // gemm_kernel: M = 2048, N = 14336 778 -> 864; M = 8192, N = 14336
-// 968 -> 1053; M = 8192, N = 4096, K = 14336 970 -> 1092.
+// 968 -> 1053; M = 8192, N = 4096, K = 14336 970 -> 1092.  Four stages and a
+// barrier every second step instead of two stages and one per step: another
+// +3% (852 -> 877, 1048 -> 1071); eight stages and one barrier per
+// superblock measured level with four (868 / 1056).
 //   - One wave per SIMD with 128 x 128 per wave (256 accumulators) spills
 //     (136-164 dwords: the allocator copies accumulators between AGPRs and
 //     VGPRs).
@@ -1181,6 +1185,10 @@ inline int gemm_splits(int type, int64_t tiles, int nu) {
 //     MFMA) forces 55-89 dwords of spill and runs at 410-626.
 //   - Reading the A fragments a few ahead of their MFMAs instead of all at
 //     the start of a half (gemm_kernel, 2-8 ahead): 734-770 against 786.
+//   - The same wave tile on v_mfma_f32_32x32x16_f16 (each lane dequantizes
+//     its own weight row per 32-column block, so the sub-block scales are
+//     derived once per row; 217 VGPRs): bit-identical results, 868-875
+//     against 865-869 at M = 2048, 1-2% slower at M = 8192.
 // ---------------------------------------------------------------------------
 constexpr int kWW = 8, kWTN = 4, kWTM = 8;
 constexpr int kWBM = 16 * kWTM, kWBN = 16 * kWTN * kWW;
@@ -1246,22 +1254,24 @@ struct WideQ4K {
     return h8(v[0], v[1], v[2], v[3]);
   }
 
-  // step s = 4 u + C: A from stage C & 1, codes from set C & 1.  First the A
-  // of step s + 1 (loaded during step s - 1) goes to the other stage (read by
-  // step s - 1, which every wave has left) and step s + 2's A is requested;
-  // then k-half by k-half the fragments of this step, each tile's B operand
-  // dequantized before its 8 MFMAs and its codes of step s + 2 requested once
-  // both halves are built.
+  // step s = 4 u + C: A from stage s & 3 (= C), codes from set C & 1.  First
+  // the A of step s + 2 (loaded during step s - 1) goes to stage (s + 2) & 3
+  // and step s + 3's A is requested; then k-half by k-half the fragments of
+  // this step, each tile's B operand dequantized before its 8 MFMAs and its
+  // codes of step s + 2 requested once both halves are built.  A barrier
+  // after odd steps only: stage (s + 2) & 3 was last read at step s - 2 and is
+  // next read at step s + 2, and a barrier at the end of an odd step lies
+  // between each pair.
   template <int C>
   __device__ __forceinline__ void step(int u) {
     constexpr int P = C & 1;
     // branch-free: past the end of K these loads are bounded by the buffer
     // resources (in-range bytes or zeros) and their data is never used
     const int s = 4 * u + C;
-    store_a(P ^ 1);
-    load_a(64 * (s + 2));
+    store_a((C + 2) & 3);
+    load_a(64 * (s + 3));
     if (C == 2) load_hdr(u + 1);
-    const unsigned char *base = lds + P * kWStB;
+    const unsigned char *base = lds + C * kWStB;
     const int u2 = (s + 2) >> 2;
     constexpr int C2 = (C + 2) & 3;
 #pragma unroll
@@ -1278,7 +1288,7 @@ struct WideQ4K {
       }
       __builtin_amdgcn_sched_barrier(0);  // one half's fragments live at a time
     }
-    __syncthreads();
+    if (C & 1) __syncthreads();
   }
 };
 
@@ -1287,7 +1297,7 @@ __global__ __launch_bounds__(kWThr) void gemm_wide_q4k(const XT *__restrict__ x,
                                                       const uint8_t *__restrict__ W, int M, int N,
                                                       int K, float *__restrict__ y, int64_t ldy,
                                                       int tiles_m) {
-  __shared__ __align__(16) unsigned char lds[2 * kWStB];
+  __shared__ __align__(16) unsigned char lds[4 * kWStB];
   int bid = blockIdx.x;
   if ((gridDim.x & 7) == 0) bid = (bid & 7) * (gridDim.x >> 3) + (bid >> 3);
   int m0, n0;
@@ -1323,7 +1333,8 @@ __global__ __launch_bounds__(kWThr) void gemm_wide_q4k(const XT *__restrict__ x,
   for (int i = 0; i < kWTM; ++i)
 #pragma unroll
     for (int j = 0; j < kWTN; ++j) s.acc[i][j] = float4_t{0.f, 0.f, 0.f, 0.f};
-  // prologue: header of superblock 0, A of steps 0 and 1, codes of steps 0 and 1
+  // prologue: header of superblock 0, codes of steps 0 and 1, A of steps 0
+  // and 1 into stages 0 and 1, A of step 2 requested
   s.load_hdr(0);
   s.load_a(0);
 #pragma unroll
@@ -1333,6 +1344,8 @@ __global__ __launch_bounds__(kWThr) void gemm_wide_q4k(const XT *__restrict__ x,
   }
   s.store_a(0);
   s.load_a(64);
+  s.store_a(1);
+  s.load_a(128);
   __syncthreads();
   for (int u = 0; u < s.nu; ++u) {
     s.set_cur();
