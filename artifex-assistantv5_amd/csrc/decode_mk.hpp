@@ -8,10 +8,11 @@
 //
 // The activations are converted into an image laid out exactly as a
 // workgroup's shared memory holds them, one block of mk_unit_bytes<MA>() per
-// 256-element unit (MA activation tiles of 16 MFMA rows each).  Up to 16 rows
-// of f32 (32 of f16, MA <= 2) each workgroup of mk_kernel converts its own K
-// range; wider batches convert once per call into the workspace
-// (mk_prep_kernel), and the workgroups copy their range.  K is split over
+// 256-element unit (MA activation tiles of 16 MFMA rows each).  Up to 24 rows
+// of f32 (48 of f16, MA <= 3), and 32 when K >= 8192, each workgroup of
+// mk_kernel converts its own K range; otherwise the batch is converted once
+// per call into the workspace (mk_prep_kernel), and the workgroups copy their
+// range.  K is split over
 // workgroups (ranges); each range writes its partial sums and
 // mk_reduce_kernel adds them in range order.
 //   A [16 MA][kMkLd] f16  MFMA row 2m + p holds part p (hi, lo) of activation
@@ -113,7 +114,7 @@ __device__ __forceinline__ void load_unit(__amdgpu_buffer_rsrc_t rs, int soff, i
 #define GGUF_MK_DEPTH_WIDE 2  // the same, 3 or 4 activation tiles
 #endif
 #ifndef GGUF_MK_FUSE
-#define GGUF_MK_FUSE 1  // MA <= 2: each workgroup converts its own range of x (one launch)
+#define GGUF_MK_FUSE 1  // each workgroup converts its own range of x (no prep launch)
 #endif
 constexpr int kMkFuseKw = 4;  // units per K range when the workgroups convert their own range
 constexpr int kMkBatch = 8;  // ranges whose partial sums are requested at a time by the reduction
@@ -527,7 +528,7 @@ __device__ __forceinline__ void mk_unit_q8(const Q8Super (&w)[T], int bo, int la
 // they arrive.  The K-lanes of a tile slot are added in a fixed order through
 // shared memory.
 //
-// SX (narrow tiles, MA <= 2): the workgroup converts its own range of x into
+// SX (MA <= 3, or 4 with K >= 8192): the workgroup converts its own range of x into
 // the image (mk_stage, one wave per (unit, activation row)).  Otherwise the
 // image comes from the workspace (mk_prep_kernel): through registers for
 // MA <= 2, LDS-direct loads for MA 3, 4.
@@ -762,7 +763,7 @@ __global__ __launch_bounds__(256) void mk_reduce_kernel(const float *__restrict_
 
 // Launch shape: MA activation tiles; TS tile slots x KL K-lanes of T tiles
 // per workgroup; K split into `ranges` of kw units.
-//   SX (MA <= 2): 16 tiles per workgroup, one per wave; ranges of at most
+//   SX (MA <= 3, or 4 with K >= 8192): 16 tiles per workgroup, one per wave; ranges of at most
 //     kMkFuseKw units (the conversion each workgroup does stays small), more
 //     while the grid has fewer than GGUF_MK_MIN_WGS workgroups.
 //   Otherwise: as few ranges as the shared memory allows (the image comes
@@ -780,7 +781,11 @@ MkPlan mk_plan(int M, int N, int K) {
   constexpr int PARTS = sizeof(XT) == 4 ? 2 : 1;
   MkPlan p;
   p.ma = (M * PARTS + 15) / 16;
-  p.sx = GGUF_MK_FUSE && p.ma <= 2;
+  // each workgroup converts its own K range up to 3 activation tiles, and at 4
+  // when K has at least 32 units (measured: 32 f32 rows at K = 14336 gain 1-2 us
+  // per call against the prep launch + image copy, at K = 4096 they lose 1.5 us;
+  // 24 rows gain at K = 4096 too)
+  p.sx = GGUF_MK_FUSE && (p.ma <= 3 || (p.ma == 4 && K / 256 >= 32));
   const bool wide = p.ma > 2;
   p.ts = p.sx ? 16 : wide ? 16 / GGUF_MK_WIDE_T : 4;
   p.kl = p.sx || wide ? 1 : 4;
@@ -854,7 +859,9 @@ hipError_t launch_mk(const XT *x, int64_t ldx, const uint8_t *W, int N, int K, f
     return hipErrorNotSupported;
   if (p.sx) {
     if (p.ma == 1) return launch_mk_ma<TYPE, XT, 1, 1, 16, 1, true>(x, ldx, W, N, K, y, ldy, M, work, p, s);
-    return launch_mk_ma<TYPE, XT, 2, 1, 16, 1, true>(x, ldx, W, N, K, y, ldy, M, work, p, s);
+    if (p.ma == 2) return launch_mk_ma<TYPE, XT, 2, 1, 16, 1, true>(x, ldx, W, N, K, y, ldy, M, work, p, s);
+    if (p.ma == 3) return launch_mk_ma<TYPE, XT, 3, 1, 16, 1, true>(x, ldx, W, N, K, y, ldy, M, work, p, s);
+    return launch_mk_ma<TYPE, XT, 4, 1, 16, 1, true>(x, ldx, W, N, K, y, ldy, M, work, p, s);
   }
   switch (p.ma) {  // the shapes mk_plan assumes for each MA
     case 1: return launch_mk_ma<TYPE, XT, 1, 1, 4, 4, false>(x, ldx, W, N, K, y, ldy, M, work, p, s);

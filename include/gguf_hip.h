@@ -175,9 +175,10 @@ int gguf_hip_matmul_variant(const void *x, int x_type, int64_t ldx, const void *
  * results as without a workspace up to f32 rounding of the sums,
  * deterministic either way, and much faster for weights of few rows (the FFN
  * down projection) and short prefills (M = 512, N = 4096: 258 -> 476
- * TFLOP/s).  Up to 16 f32 (32 f16) rows the batched decode converts the
- * activations in every workgroup (its own K range); a second launch adds the
- * K ranges' sums in range order.
+ * TFLOP/s).  Up to 24 f32 (48 f16) rows, and 32 when K >= 8192, the batched
+ * decode converts the activations in every workgroup (its own K range);
+ * otherwise a first launch converts them once.  A last launch adds the K
+ * ranges' sums in range order.
  * The workspace's first 65536 bytes are reserved: no call reads or writes
  * them, and one workspace serves calls of any shape and type.
  * The reference engine likewise preallocates its scratch (forward-pass.ts:1140-1163).
