@@ -1197,38 +1197,29 @@ constexpr int kWAI = kWBM * 8 / kWThr;  // 16-byte activation chunks a thread st
 constexpr int kWAR = kWThr / 8;         // row distance between them
 constexpr int kWStB = kWBM * kRowB;
 
-struct WideQ4K {
-  rsrc_t ars, brs;
-  int avoff, row0, cc, ts, nu, af0, af1;
-  int64_t ldxb;
+// The B side of a Q4_K wave tile: NT row tiles of 16 weight rows in the
+// repacked row-tile layout, the headers of the current superblock and two
+// sets of code words (steps of even and odd parity).
+template <int NT>
+struct Q4KB {
+  rsrc_t brs;
+  int ts;
   BOff bo;
-  uint4 ar[kWAI];
-  uint2 cq[2][kWTN];
-  uint4 hd[kWTN];
-  uint32_t sc[kWTN][2], mn[kWTN][2];
-  float d24[kWTN], dmin[kWTN];
-  float4_t acc[kWTM][kWTN];
-  unsigned char *lds;
+  uint2 cq[2][NT];
+  uint4 hd[NT];
+  uint32_t sc[NT][2], mn[NT][2];
+  float d24[NT], dmin[NT];
 
-  __device__ __forceinline__ void load_a(int k0) {
-#pragma unroll
-    for (int i = 0; i < kWAI; ++i) ar[i] = bl16(ars, avoff, (int)(kWAR * i * ldxb) + 2 * k0);
-  }
-  __device__ __forceinline__ void store_a(int stage) {
-#pragma unroll
-    for (int i = 0; i < kWAI; ++i)
-      *(uint4 *)(lds + stage * kWStB + lds_at(row0 + kWAR * i, cc)) = ar[i];
-  }
   __device__ __forceinline__ void load_codes(int set, int j, int u, int c) {
     cq[set][j] = bl8(brs, bo.v1, j * ts + u * Fmt<12>::TU + (c >> 1) * 1024 + 8 * (c & 1));
   }
   __device__ __forceinline__ void load_hdr(int u) {
 #pragma unroll
-    for (int j = 0; j < kWTN; ++j) hd[j] = bl16(brs, bo.v0, j * ts + u * Fmt<12>::TU);
+    for (int j = 0; j < NT; ++j) hd[j] = bl16(brs, bo.v0, j * ts + u * Fmt<12>::TU);
   }
   __device__ __forceinline__ void set_cur() {
 #pragma unroll
-    for (int j = 0; j < kWTN; ++j) {
+    for (int j = 0; j < NT; ++j) {
       q4k_scales_packed(hd[j].y, hd[j].z, hd[j].w, sc[j][0], sc[j][1], mn[j][0], mn[j][1]);
       const float d = h2f(hd[j].x);
       d24[j] = d * kTwo24;
@@ -1252,6 +1243,25 @@ struct WideQ4K {
       v[2 * w + 1] = mix_hi(e, o, s, c);
     }
     return h8(v[0], v[1], v[2], v[3]);
+  }
+};
+
+struct WideQ4K : Q4KB<kWTN> {
+  rsrc_t ars;
+  int avoff, row0, cc, nu, af0, af1;
+  int64_t ldxb;
+  uint4 ar[kWAI];
+  float4_t acc[kWTM][kWTN];
+  unsigned char *lds;
+
+  __device__ __forceinline__ void load_a(int k0) {
+#pragma unroll
+    for (int i = 0; i < kWAI; ++i) ar[i] = bl16(ars, avoff, (int)(kWAR * i * ldxb) + 2 * k0);
+  }
+  __device__ __forceinline__ void store_a(int stage) {
+#pragma unroll
+    for (int i = 0; i < kWAI; ++i)
+      *(uint4 *)(lds + stage * kWStB + lds_at(row0 + kWAR * i, cc)) = ar[i];
   }
 
   // step s = 4 u + C: A from stage s & 3 (= C), codes from set C & 1.  First
