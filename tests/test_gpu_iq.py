@@ -81,6 +81,25 @@ def test_decode_matmul_f32_grade(pkg, ref, t, xdt):
 
 
 @pytest.mark.parametrize("t", GRID)
+@pytest.mark.parametrize("m,xdt", [(8, torch.float32), (16, torch.float16), (3, torch.float32)])
+def test_decode_full_width(pkg, t, m, xdt):
+    """Batched decode at the FFN width (N = 14336, K = 4096; the K ranges'
+    sums added by the second launch) against the f64 product of the
+    GPU-dequantized weights (pinned to the oracle by the dequant tests), and
+    deterministic."""
+    n, k = 14336, 4096
+    raw, w = _weight(pkg, t, n, k, seed=31 * t + m)
+    g = torch.Generator(device="cuda").manual_seed(t * 100 + m)
+    x = torch.randn(m, k, device="cuda", generator=g).to(xdt)
+    y = pkg.qlinear(x, w, variant=DECODE)
+    x64, w64 = x.double(), w.dequant().view(n, k).double()
+    err = (y.double() - x64 @ w64.T).abs()
+    elem = (err / (x64.abs() @ w64.abs().T)).max().item()
+    assert torch.isfinite(y).all() and elem <= DECODE_TOL, (NAMES[t], m, xdt, elem)
+    assert torch.equal(pkg.qlinear(x, w, variant=DECODE), y)
+
+
+@pytest.mark.parametrize("t", GRID)
 def test_decode_matmul_wide_range_activations(pkg, ref, t):
     """Activations spanning 2^-60 .. 2^60 across units and rows: every unit is
     scaled by its own power of two before it enters the matrix cores."""

@@ -262,6 +262,9 @@ FULL = [  # (type, M, N, K, x dtype)
     (8, 1, 4096, 4096, torch.float32),
     (12, 1, 14336, 4096, torch.float32), (12, 8, 14336, 4096, torch.float32),
     (12, 32, 14336, 4096, torch.float32),
+    # the batched decode at the FFN width: Q6_K, Q8_0, 16 f16 rows, a ragged N
+    (14, 8, 14336, 4096, torch.float32), (8, 8, 14336, 4096, torch.float32),
+    (12, 16, 14336, 4096, torch.float16), (12, 5, 14400, 3072, torch.float32),
     (12, 1, 4096, 14336, torch.float32), (12, 8, 4096, 14336, torch.float32),
     (12, 32, 4096, 14336, torch.float32),
     (14, 1, 151936, 4096, torch.float32),
@@ -433,13 +436,13 @@ def test_shared_workspace_prefix_stays_zero(pkg, ref):
 
 
 def test_workspace_per_stream(pkg):
-    """Batched decode (Q4_K, M = 8: split K, the K ranges' partial sums in the
-    workspace) alternating between two streams of one device: each stream
-    gets its own workspace and the results equal the single-stream ones bit
-    for bit."""
+    """Batched decode (Q4_K, M = 8, K = 14336: split K, the K ranges' partial
+    sums in the workspace) alternating between two streams of one device:
+    each stream gets its own workspace and the results equal the
+    single-stream ones bit for bit."""
     lin = importlib.import_module("artifex-assistantv5_amd.linear")
-    raw, w = _case(pkg, 12, 14336, 4096, seed=9)
-    xs = [torch.from_numpy(pkg.quantize.synthetic_activations(8, 4096, seed=s)).cuda()
+    raw, w = _case(pkg, 12, 4096, 14336, seed=9)
+    xs = [torch.from_numpy(pkg.quantize.synthetic_activations(8, 14336, seed=s)).cuda()
           for s in range(4)]
     want = [pkg.qlinear(x, w) for x in xs]
     torch.cuda.synchronize()
