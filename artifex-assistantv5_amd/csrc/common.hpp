@@ -15,6 +15,19 @@ typedef float float4_t __attribute__((ext_vector_type(4)));
 
 constexpr int kWave = 64;
 
+// Shared-memory addressing by 32-bit LDS address.  A pointer into shared
+// memory becomes its LDS address once (an address-space cast), and loads
+// through such addresses fold constant offsets into the instruction, where
+// offsets from the dynamic array's symbol each cost an add.
+__device__ __forceinline__ uint32_t lds_addr32(const void *p) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) unsigned char *)p;
+}
+template <typename T>
+__device__ __forceinline__ T lds_ld(uint32_t a) {
+  typedef uint32_t words_t __attribute__((ext_vector_type(sizeof(T) / 4)));
+  return __builtin_bit_cast(T, *(const __attribute__((address_space(3))) words_t *)a);
+}
+
 // ---------------------------------------------------------------------------
 // HBM row-tile layout.
 //

@@ -401,6 +401,20 @@ __device__ __forceinline__ float4 lds_f4(int float_off) {
   return *(const float4 *)((const float *)g_lds + float_off);
 }
 
+// The eight selector-row A fragments of an IQ unit (M = 1): fragment j holds
+// the lane's activations (LDS address own + 64 j) where its row belongs to
+// sub-block j (jo == j), and zeros elsewhere.  The lane reads its one
+// fragment and selects the other seven to zero, where the K-quant units read
+// all eight (seven from the zero block): the IQ units' table lookups keep the
+// LDS busy (IQ2_XXS M = 1 10.5 -> 10.0 us), while Q4_K, whose VALU sets the
+// pace, measured slower with the selects (7.9-8.2 -> 8.5-8.8 us).
+__device__ __forceinline__ void iq_frags(uint32_t own, uint32_t zero, bool live, int jo,
+                                         half8_t (&a)[8]) {
+  const half8_t mine = lds_ld<half8_t>(live ? own + 64 * jo : zero), z = {};
+#pragma unroll
+  for (int j = 0; j < 8; ++j) a[j] = jo == j ? mine : z;
+}
+
 #include "iq_decode.hpp"
 
 // D = (hi + lo parts of A) x B; lanes with on == false read the zero operand.
@@ -568,11 +582,10 @@ __device__ __forceinline__ void unit_m1_iq(const Unit<TYPE> &u, const Stage &st,
   const int r = lane & 15, g = lane >> 4;
   const int jo = r >> 1;
   const bool live = PARTS == 2 || (r & 1) == 0;
-  const int own = 2 * (st.xh + (r & 1) * (st.xl - st.xh) + 256 * ul + 8 * g);
-  const int zero = 2 * st.zero;
+  const uint32_t own = lds_addr32(g_lds) + 2 * (st.xh + (r & 1) * (st.xl - st.xh) + 256 * ul + 8 * g);
+  const uint32_t zero = lds_addr32(g_lds) + 2 * st.zero;
   half8_t a[8];
-#pragma unroll
-  for (int j = 0; j < 8; ++j) a[j] = lds_h8b(((live && jo == j) ? own : zero) + 64 * j);
+  iq_frags(own, zero, live, jo, a);
   constexpr bool BF = iq_block_factor<TYPE>();
   float4_t D = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll

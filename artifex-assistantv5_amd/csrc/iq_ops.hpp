@@ -91,7 +91,7 @@ __device__ __forceinline__ void iq_put_tables(const IqTabRegs<TYPE, NT> &t, unsi
   }
 }
 
-__device__ __forceinline__ uint32_t iq_byte(uint32_t w, int i) { return (w >> (8 * i)) & 0xFFu; }
+__device__ __forceinline__ uint32_t iq_byte(uint32_t w, int i) { return __builtin_amdgcn_ubfe(w, 8 * i, 8); }
 // a0 for lane groups 0, 1 and a1 for 2, 3, selected as values (a select of the
 // two array elements' addresses keeps the record out of registers)
 __device__ __forceinline__ uint32_t pick2(uint32_t a0, uint32_t a1, int g) { return (g & 2) ? a1 : a0; }
@@ -136,7 +136,7 @@ __device__ __forceinline__ half8_t iq_b(const IqUnit<TYPE> &u, int ib, int g, co
   if constexpr (TYPE == 16) {  // IQ2_XXS: (4 index bytes, u32 7-bit sign indices | ls << 28)
     const uint32_t aux1 = u.w[2 * ib + 1];
     idx0 = iq_byte(u.w[2 * ib], g);
-    sidx = (aux1 >> (7 * g)) & 127u;
+    sidx = __builtin_amdgcn_ubfe(aux1, 7 * g, 7);
     f = 2u * (aux1 >> 28) + 1u;
   } else if constexpr (TYPE == 17) {  // IQ2_XS: u16 (9-bit index | 7-bit sign index); scales
     const uint32_t q = (pick2(u.w[2 * ib], u.w[2 * ib + 1], g) >> (16 * (g & 1))) & 0xFFFFu;
@@ -153,7 +153,7 @@ __device__ __forceinline__ half8_t iq_b(const IqUnit<TYPE> &u, int ib, int g, co
     const uint32_t q = pick2(u.w[2 * ib], u.w[2 * ib + 1], g) >> (16 * (g & 1)), aux = u.w[16 + ib];
     idx0 = q & 0xFFu;
     idx1 = (q >> 8) & 0xFFu;
-    sidx = (aux >> (7 * g)) & 127u;
+    sidx = __builtin_amdgcn_ubfe(aux, 7 * g, 7);
     f = 2u * (aux >> 28) + 1u;
   } else if constexpr (TYPE == 21) {  // IQ3_S: qs[64] | qh[8] | signs[32] | scales[4]
     const uint32_t q = pick2(u.w[2 * ib], u.w[2 * ib + 1], g) >> (16 * (g & 1));
@@ -174,15 +174,16 @@ __device__ __forceinline__ half8_t iq_b(const IqUnit<TYPE> &u, int ib, int g, co
   const half_t fh = (half_t)(float)f;
   const half2_t fp = {fh, fh};
   uint32_t v[4];
+  const uint32_t ta = lds_addr32(tb);  // entry i at ta + entry bytes * i: one shift-add each
   if constexpr (Q::W == 8) {
-    const uint4 gr = *(const uint4 *)(tb + 16 * idx0);
+    const uint4 gr = lds_ld<uint4>(ta + 16 * idx0);
     v[0] = gr.x; v[1] = gr.y; v[2] = gr.z; v[3] = gr.w;
   } else {
-    const uint2 g1 = *(const uint2 *)(tb + 8 * idx0), g2 = *(const uint2 *)(tb + 8 * idx1);
+    const uint2 g1 = lds_ld<uint2>(ta + 8 * idx0), g2 = lds_ld<uint2>(ta + 8 * idx1);
     v[0] = g1.x; v[1] = g1.y; v[2] = g2.x; v[3] = g2.y;
   }
   if constexpr (Q::NS > 0) {
-    const uint4 m = *(const uint4 *)(tb + Q::GB + 16 * sidx);
+    const uint4 m = lds_ld<uint4>(ta + Q::GB + 16 * sidx);
     v[0] ^= m.x; v[1] ^= m.y; v[2] ^= m.z; v[3] ^= m.w;
   }
   half8_t b;
