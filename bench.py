@@ -520,7 +520,7 @@ def secondary_cases(pkg, args, pool, secondary):
             secondary[f"q4k_decode_m{mm}_down_gbs"] = round(r["gbs"], 1)
         del dpool
     if want("batch_q6q8"):
-        # batched decode of the other two north-star types at the FFN shapes
+        # batched decode of the path's other two types (Q6_K, Q8_0) at the FFN shapes
         for tt, name in ((14, "q6k"), (8, "q8_0")):
             for (nn, kk), shape in (((14336, 4096), "gate_up"), ((4096, 14336), "down")):
                 bpool, _ = make_pool(pkg, tt, nn, kk, 10, seed=40 + tt)
@@ -591,7 +591,7 @@ def secondary_cases(pkg, args, pool, secondary):
 def main():
     args = parse()
     if args.gpus != 1:
-        print(json.dumps({"error": "this build runs on one GPU only; use --gpus 1 (the "
+        print(json.dumps({"error": "this library runs on one GPU only; use --gpus 1 (the "
                                    "multi-GPU sharding of this path is a design note, not code)",
                           "n_gpus": args.gpus}))
         sys.exit(2)

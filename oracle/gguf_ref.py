@@ -2,7 +2,7 @@
 Q6_K dequant-matmul path (and, through ``oracle/gguf_iq.py``, the grid-codebook
 IQ types IQ2_XXS / IQ2_XS / IQ2_S / IQ3_XXS / IQ3_S / IQ1_M).
 
-TEST INFRASTRUCTURE ONLY.  This module is the checker: only ``tests/``,
+TEST INFRASTRUCTURE ONLY.  This module is the oracle: only ``tests/``,
 ``__graft_entry__.smoke()`` and the ``cpu_baseline`` leg of ``bench.py`` may
 import it, and only to check or to time the CPU baseline.  The product path
 (the HIP library and its Python host code) never calls it.

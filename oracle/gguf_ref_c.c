@@ -1,8 +1,8 @@
 /* Compiled CPU restatement of the reference's Q4_K dequantization, for the CPU
  * baseline of the dequant-matmul path.
  *
- * TEST INFRASTRUCTURE ONLY.  Like oracle/gguf_ref.py this is the checker's
- * side: only tests/ and the cpu_baseline leg of bench.py load it (through
+ * TEST INFRASTRUCTURE ONLY.  Like oracle/gguf_ref.py this is part of the
+ * oracle: only tests/ and the cpu_baseline leg of bench.py load it (through
  * ctypes), to pin it against the numpy oracle and to time the host.  The
  * product path (the HIP library and its Python host code) never calls it.
  *
