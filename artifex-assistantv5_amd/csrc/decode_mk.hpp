@@ -9,7 +9,7 @@
 // The activations are converted into an image laid out exactly as a
 // workgroup's shared memory holds them, one block of mk_unit_bytes<MA>() per
 // 256-element unit (MA activation tiles of 16 MFMA rows each).  Up to 24 rows
-// of f32 (48 of f16, MA <= 3), and 32 when K >= 8192, each workgroup of
+// of f32 (48 of f16, MA <= 3), and 32 when K >= 8192 or for Q6_K, each workgroup of
 // mk_kernel converts its own K range; otherwise the batch is converted once
 // per call into the workspace (mk_prep_kernel), and the workgroups copy their
 // range.  K is split over
@@ -794,8 +794,9 @@ MkPlan mk_plan(int M, int N, int K) {
   // each workgroup converts its own K range up to 3 activation tiles, and at 4
   // when K has at least 32 units (measured: 32 f32 rows at K = 14336 gain 1-2 us
   // per call against the prep launch + image copy, at K = 4096 they lose 1.5 us;
-  // 24 rows gain at K = 4096 too)
-  p.sx = GGUF_MK_FUSE && (p.ma <= 3 || (p.ma == 4 && K / 256 >= 32));
+  // 24 rows gain at K = 4096 too), or for Q6_K at any K (32 rows at K = 4096:
+  // 28.59 -> 27.13 us; Q8_0 level, the IQ types 2% slower)
+  p.sx = GGUF_MK_FUSE && (p.ma <= 3 || (p.ma == 4 && (K / 256 >= 32 || TYPE == 14)));
   const bool wide = p.ma > 2;
   p.ts = p.sx ? 16 : wide ? 16 / GGUF_MK_WIDE_T : 4;
   p.kl = p.sx || wide ? 1 : 4;

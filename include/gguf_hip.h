@@ -175,7 +175,8 @@ int gguf_hip_matmul_variant(const void *x, int x_type, int64_t ldx, const void *
  * results as without a workspace up to f32 rounding of the sums,
  * deterministic either way, and much faster for weights of few rows (the FFN
  * down projection) and short prefills (M = 512, N = 4096: 258 -> 476
- * TFLOP/s).  Up to 24 f32 (48 f16) rows, and 32 when K >= 8192, the batched
+ * TFLOP/s).  Up to 24 f32 (48 f16) rows, and 32 when K >= 8192 or the
+ * weight is Q6_K, the batched
  * decode converts the activations in every workgroup (its own K range);
  * otherwise a first launch converts them once.  A last launch adds the K
  * ranges' sums in range order.
