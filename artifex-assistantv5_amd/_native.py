@@ -17,7 +17,7 @@ from .ggml import GGMLTypeError
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libgguf_hip.so")
-ABI_VERSION = 17
+ABI_VERSION = 18
 
 ERR_TYPE, ERR_SHAPE, ERR_NULL, ERR_ALIGN, ERR_DTYPE, ERR_BYTES, ERR_HIP = -1, -2, -3, -4, -5, -6, -7
 VARIANT_AUTO, VARIANT_DECODE, VARIANT_GEMM = 0, 1, 2
@@ -54,6 +54,8 @@ SIGNATURES = {
     "gguf_hip_attention_workspace": (_i64, [_i32, _i32, _i32, _i64]),
     "gguf_hip_attention_decode_noalloc": (_i32, [_fp, _vp, _fp, _fp, _fp, _fp, _fp, _i32, _i32,
                                                  _i32, _i64, _vp]),
+    "gguf_hip_attention_prefill": (_i32, [_fp, _i64, _vp, _i64, _fp, _fp, _fp, _fp, _fp, _i64,
+                                          _i32, _i32, _i32, _i64, _vp]),
     "gguf_hip_matmul_attn_merge": (_i32, [_vp, _vp, _i32, _i32, _i32, _i64, _vp, _i32, _i64, _fp,
                                           _i32, _vp]),
     "gguf_hip_argmax": (_i32, [_fp, _i64, _vp, _vp, _vp]),

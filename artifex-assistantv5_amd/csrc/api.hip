@@ -397,6 +397,35 @@ int gguf_hip_attention_decode_noalloc(const float *qkv, const int64_t *pos,
                     "attention launch");
 }
 
+int gguf_hip_attention_prefill(const float *qkv, int64_t ldqkv, const int64_t *pos, int64_t m,
+                               const float *cos_table, const float *sin_table, float *k_cache,
+                               float *v_cache, float *out, int64_t ldo, int n_heads,
+                               int n_kv_heads, int head_dim, int64_t max_seq, void *stream) {
+  int rc = check_attention(n_heads, n_kv_heads, head_dim, max_seq);
+  if (rc) return rc;
+  if (m < 0 || m > ((int64_t)1 << 30))
+    return fail(GGUF_HIP_ERR_SHAPE, "[gguf-hip] attention_prefill: M %lld out of range",
+                (long long)m);
+  const int64_t row = (int64_t)(n_heads + 2 * n_kv_heads) * head_dim;
+  if (ldqkv < row || ldqkv % 4 || ldo < (int64_t)n_heads * head_dim || ldo % 4)
+    return fail(GGUF_HIP_ERR_SHAPE,
+                "[gguf-hip] attention_prefill: ldqkv %lld (row %lld) / ldo %lld (row %lld) must "
+                "hold a row and be multiples of 4",
+                (long long)ldqkv, (long long)row, (long long)ldo,
+                (long long)n_heads * head_dim);
+  if (m == 0) return ok();
+  if (!qkv || !pos || !cos_table || !sin_table || !k_cache || !v_cache || !out)
+    return fail(GGUF_HIP_ERR_NULL, "[gguf-hip] null pointer");
+  if (!aligned(qkv, 16) || !aligned(k_cache, 16) || !aligned(v_cache, 16) || !aligned(out, 16) ||
+      !aligned(pos, 8) || !aligned(cos_table, 16) || !aligned(sin_table, 16))
+    return fail(GGUF_HIP_ERR_ALIGN, "[gguf-hip] attention_prefill buffers misaligned");
+  return hip_status(gguf::launch_attention_prefill(qkv, ldqkv, pos, m, cos_table, sin_table,
+                                                   k_cache, v_cache, out, ldo, n_heads,
+                                                   n_kv_heads, head_dim, max_seq,
+                                                   (hipStream_t)stream),
+                    "attention_prefill launch");
+}
+
 int64_t gguf_hip_argmax_workspace(void) { return gguf::argmax_work_bytes(); }
 
 int gguf_hip_argmax(const float *x, int64_t n, int64_t *out, void *work, void *stream) {

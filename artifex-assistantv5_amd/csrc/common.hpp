@@ -462,6 +462,10 @@ int64_t attention_work_bytes(int nh, int nkv, int hd, int64_t max_seq);
 hipError_t launch_attention_decode(const float *qkv, const int64_t *pos, const float *cs,
                                    const float *sn, float *kc, float *vc, float *out, float *work,
                                    int nh, int nkv, int hd, int64_t max_seq, hipStream_t s);
+hipError_t launch_attention_prefill(const float *qkv, int64_t ldq, const int64_t *pos, int64_t m,
+                                    const float *cs, const float *sn, float *kc, float *vc,
+                                    float *out, int64_t ldo, int nh, int nkv, int hd,
+                                    int64_t max_seq, hipStream_t s);
 // The attention of gguf_hip_attention_decode_noalloc keeps its workspace
 // (records and counters) in a device array of this many bytes.
 constexpr int64_t kNoAllocAttentionBytes = (int64_t)8 << 20;

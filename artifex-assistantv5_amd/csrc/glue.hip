@@ -360,6 +360,235 @@ __global__ __launch_bounds__(kGlueThreads) void attention_kernel(
   if (tid == 0) counters[g] = 0u;  // ready for the next call
 }
 
+// ---------------------------------------------------------------------------
+// Prefill attention: M new positions, two launches.
+//
+// rope_append_kernel: one workgroup per row m.  It applies rotate_half RoPE
+// (rope.wgsl:1-10, the same products as the decode kernel) to the row's k
+// heads and stores k and v at slot pos[m] of the caches.  A row whose position
+// lies outside 0..max_seq-1 writes nothing.
+//
+// attention_prefill_kernel: causal GQA attention of each row over slots
+// 0..pos[m] (attention.wgsl:60-234 with new_seq_len = M), flash-style on the
+// f32 matrix cores.
+// - A workgroup takes 16 rows and one KV head.  Wave w takes query heads
+//   w, w + 4, ... of the group, one per pass over the keys.
+// - Keys come in tiles of KT slots: K rows [KT][HD + 4] and V transposed
+//   [HD][KT + 4] in LDS.  The next tile's loads are in flight while the
+//   current tile is used.
+// - Per 16 keys, v_mfma_f32_16x16x4f32 computes S^T = K . Q^T (keys x rows).
+//   Its accumulator layout (lane l: keys 4(l/16) + r of row l%16) is exactly
+//   the B-operand layout of O^T += V^T . P^T when k-step r takes keys
+//   4(l/16) + r.  So the probabilities never leave their registers.
+// - Every lane holds one row's running max, running sum and output column,
+//   so the online-softmax rescale is lane-local.
+// - The head_dim reduction of S^T runs over elements 16a + 4(l/16) + b, a
+//   bijection onto 0..HD-1, so each lane's K and Q operands are float4 reads.
+// A row whose position lies outside 0..max_seq-1, or past M, attends to
+// nothing and is not written.
+constexpr int kPfRows = 16;  // rows (positions) per workgroup
+
+template <int HD>
+struct PfShape {
+  static constexpr int KT = HD <= 128 ? 64 : 32;          // key slots per tile
+  static constexpr int KLD = HD + 4, VLD = KT + 4;         // LDS row strides (floats)
+  static constexpr int NF = KT * HD / 4 / kGlueThreads;    // float4 of K (and of V) per thread
+};
+
+template <int HD>
+__global__ __launch_bounds__(kGlueThreads) void rope_append_kernel(
+    const float *__restrict__ qkv, int64_t ldq, const int64_t *__restrict__ pos,
+    const float *__restrict__ cs, const float *__restrict__ sn, float *__restrict__ kc,
+    float *__restrict__ vc, int nh, int nkv, int max_seq) {
+  constexpr int half = HD / 2;
+  const int64_t m = blockIdx.x;
+  const int64_t p = pos[m];
+  if (p < 0 || p >= max_seq) return;
+  const float *kin = qkv + m * ldq + (int64_t)nh * HD, *vin = kin + (int64_t)nkv * HD;
+  const float *crow = cs + p * half, *srow = sn + p * half;
+  for (int e = threadIdx.x; e < nkv * half; e += kGlueThreads) {
+    const int h = e / half, i = e - h * half;
+    const float a = kin[h * HD + i], b = kin[h * HD + i + half], c = crow[i], s = srow[i];
+    float *krow = kc + ((int64_t)h * max_seq + p) * HD;
+    krow[i] = a * c - b * s;
+    krow[i + half] = b * c + a * s;
+  }
+  for (int e = threadIdx.x; e < nkv * HD; e += kGlueThreads) {
+    const int h = e / HD, i = e - h * HD;
+    vc[((int64_t)h * max_seq + p) * HD + i] = vin[h * HD + i];
+  }
+}
+
+__device__ __forceinline__ float4_t mfma_f32(float a, float b, float4_t c) {
+  return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+
+template <int HD>
+__global__ __launch_bounds__(kGlueThreads) void attention_prefill_kernel(
+    const float *__restrict__ qkv, int64_t ldq, const int64_t *__restrict__ pos, int64_t M,
+    const float *__restrict__ cs, const float *__restrict__ sn, const float *__restrict__ kc,
+    const float *__restrict__ vc, float *__restrict__ out, int64_t ldo, int nh, int nkv,
+    int max_seq) {
+  using Sh = PfShape<HD>;
+  constexpr int KT = Sh::KT, KLD = Sh::KLD, VLD = Sh::VLD, NF = Sh::NF, half = HD / 2;
+  constexpr int QA = HD / 16;  // float4 of q per lane, and 16-element output tiles
+  constexpr int NT = KT / 16;  // 16-key tiles per key tile
+  __shared__ __align__(16) float ks[KT * KLD];
+  __shared__ __align__(16) float vt[HD * VLD];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int col = lane & 15, g4 = lane >> 4;  // MFMA column (row of the block), k group
+  const int grp = nh / nkv, kvh = blockIdx.y;
+  const int64_t m = (int64_t)blockIdx.x * kPfRows + col;
+  int my = -1;  // the row's position; -1: attends to nothing, not written
+  if (m < M) {
+    const int64_t p = pos[m];
+    if (p >= 0 && p < max_seq) my = (int)p;
+  }
+  // slots 0 .. kend - 1 hold every key of the block's rows (same in every wave)
+  int kend = my + 1;
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) kend = max(kend, __shfl_xor(kend, o));
+  const int ntile = (kend + KT - 1) / KT;
+  const float *kbase = kc + (int64_t)kvh * max_seq * HD;
+  const float *vbase = vc + (int64_t)kvh * max_seq * HD;
+  const float scale = 1.0f / sqrtf((float)HD);
+
+  // float4 f = i * 256 + tid of a tile: 64-float4 block f / 64 = (16-slot block,
+  // 4-chunk block); within it slot f % 16, chunk (f / 16) % 4.  A wave's LDS
+  // stores (K rows, V transposed) are then free of bank conflicts.
+  float4 kr[NF], vr[NF];
+  auto load_tile = [&](int t0) {
+#pragma unroll
+    for (int i = 0; i < NF; ++i) {
+      const int f = i * kGlueThreads + tid, blk = f >> 6;
+      const int t = (blk / (HD / 16)) * 16 + (f & 15), c = (blk % (HD / 16)) * 4 + ((f >> 4) & 3);
+      const int row = t0 + t;  // < kend <= max_seq when read
+      kr[i] = row < kend ? *(const float4 *)(kbase + (int64_t)row * HD + 4 * c)
+                         : make_float4(0.f, 0.f, 0.f, 0.f);
+      vr[i] = row < kend ? *(const float4 *)(vbase + (int64_t)row * HD + 4 * c)
+                         : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+  };
+  auto store_tile = [&]() {
+#pragma unroll
+    for (int i = 0; i < NF; ++i) {
+      const int f = i * kGlueThreads + tid, blk = f >> 6;
+      const int t = (blk / (HD / 16)) * 16 + (f & 15), c = (blk % (HD / 16)) * 4 + ((f >> 4) & 3);
+      *(float4 *)(ks + t * KLD + 4 * c) = kr[i];
+      vt[(4 * c + 0) * VLD + t] = vr[i].x;
+      vt[(4 * c + 1) * VLD + t] = vr[i].y;
+      vt[(4 * c + 2) * VLD + t] = vr[i].z;
+      vt[(4 * c + 3) * VLD + t] = vr[i].w;
+    }
+  };
+
+  for (int hp = 0; hp * 4 < grp; ++hp) {
+    const int jh = hp * 4 + wave;  // query head within the group
+    const bool act = jh < grp;     // wave-uniform
+    const int64_t qcol = (int64_t)(kvh * grp + jh) * HD + 4 * g4;
+    // the row's query, roped and scaled: q[a] = elements 16a + 4 g4 + 0..3
+    float4 q[QA];
+#pragma unroll
+    for (int a = 0; a < QA; ++a) q[a] = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (act && my >= 0) {
+      const float *qin = qkv + m * ldq + qcol;
+#pragma unroll
+      for (int a = 0; a < QA; ++a) q[a] = *(const float4 *)(qin + 16 * a);
+      const float *crow = cs + (int64_t)my * half + 4 * g4, *srow = sn + (int64_t)my * half + 4 * g4;
+#pragma unroll
+      for (int a = 0; a < QA / 2; ++a) {
+        const float4 c = *(const float4 *)(crow + 16 * a), s = *(const float4 *)(srow + 16 * a);
+        const float4 x = q[a], y = q[a + QA / 2];
+        q[a] = make_float4((x.x * c.x - y.x * s.x) * scale, (x.y * c.y - y.y * s.y) * scale,
+                           (x.z * c.z - y.z * s.z) * scale, (x.w * c.w - y.w * s.w) * scale);
+        q[a + QA / 2] =
+            make_float4((y.x * c.x + x.x * s.x) * scale, (y.y * c.y + x.y * s.y) * scale,
+                        (y.z * c.z + x.z * s.z) * scale, (y.w * c.w + x.w * s.w) * scale);
+      }
+    }
+    float4_t o[QA];
+#pragma unroll
+    for (int a = 0; a < QA; ++a) o[a] = float4_t{0.f, 0.f, 0.f, 0.f};
+    float mrun = -INFINITY, lrun = 0.f;
+
+    if (ntile > 0) load_tile(0);
+    for (int it = 0; it < ntile; ++it) {
+      __syncthreads();  // every wave is done with the previous tile
+      store_tile();
+      __syncthreads();
+      if (it + 1 < ntile) load_tile((it + 1) * KT);
+      if (!act) continue;
+      // S^T for the tile's keys: s[j][r] = score of key it*KT + 16j + 4 g4 + r
+      float4_t s[NT];
+#pragma unroll
+      for (int j = 0; j < NT; ++j) {
+        s[j] = float4_t{0.f, 0.f, 0.f, 0.f};
+        const float *kp = ks + (16 * j + col) * KLD + 4 * g4;
+#pragma unroll
+        for (int a = 0; a < QA; ++a) {
+          const float4 kf = *(const float4 *)(kp + 16 * a);
+          s[j] = mfma_f32(kf.x, q[a].x, s[j]);
+          s[j] = mfma_f32(kf.y, q[a].y, s[j]);
+          s[j] = mfma_f32(kf.z, q[a].z, s[j]);
+          s[j] = mfma_f32(kf.w, q[a].w, s[j]);
+        }
+      }
+      // causal mask, the block's max over the row (4 lanes share a row)
+      const int tb = it * KT + 4 * g4;
+      float bm = -INFINITY;
+#pragma unroll
+      for (int j = 0; j < NT; ++j)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const float v = tb + 16 * j + r <= my ? s[j][r] : -INFINITY;
+          s[j][r] = v;
+          bm = fmaxf(bm, v);
+        }
+      bm = fmaxf(bm, __shfl_xor(bm, 16));
+      bm = fmaxf(bm, __shfl_xor(bm, 32));
+      const float mnew = fmaxf(mrun, bm);
+      const float alpha = mnew == -INFINITY ? 1.f : expf(mrun - mnew);
+      mrun = mnew;
+      float ls = 0.f;
+#pragma unroll
+      for (int j = 0; j < NT; ++j)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const float e = s[j][r] == -INFINITY ? 0.f : expf(s[j][r] - mnew);
+          s[j][r] = e;
+          ls += e;
+        }
+      lrun = lrun * alpha + ls;
+#pragma unroll
+      for (int a = 0; a < QA; ++a) o[a] *= alpha;
+      // O^T[d][row] += sum over the tile's keys of V[key][d] P[row][key]
+#pragma unroll
+      for (int j = 0; j < NT; ++j) {
+        const float *vp = vt + col * VLD + 16 * j + 4 * g4;
+#pragma unroll
+        for (int a = 0; a < QA; ++a) {
+          const float4 vf = *(const float4 *)(vp + 16 * a * VLD);
+          o[a] = mfma_f32(vf.x, s[j][0], o[a]);
+          o[a] = mfma_f32(vf.y, s[j][1], o[a]);
+          o[a] = mfma_f32(vf.z, s[j][2], o[a]);
+          o[a] = mfma_f32(vf.w, s[j][3], o[a]);
+        }
+      }
+    }
+    if (!act) continue;
+    float l = lrun + __shfl_xor(lrun, 16);
+    l += __shfl_xor(l, 32);
+    if (my >= 0) {
+      const float inv = 1.0f / l;
+      float *orow = out + m * ldo + qcol;
+#pragma unroll
+      for (int a = 0; a < QA; ++a)
+        *(float4 *)(orow + 16 * a) = make_float4(o[a][0] * inv, o[a][1] * inv, o[a][2] * inv,
+                                                 o[a][3] * inv);
+    }
+  }
+}
+
 // Argmax, pass 1: workgroup b scans a contiguous chunk and writes its (value,
 // index) with the first index on ties and NaN never winning; pass 2 (one
 // workgroup) merges the partials the same way.
@@ -458,6 +687,35 @@ hipError_t launch_attention_decode(const float *qkv, const int64_t *pos, const f
     hipLaunchKernelGGL(attention_kernel<256>, grid, block, 0, s, qkv, pos, cs, sn, kc, vc, out,
                        work, counters, nh, nkv, (int)max_seq);
   return hipGetLastError();
+}
+
+template <int HD>
+static hipError_t launch_prefill_hd(const float *qkv, int64_t ldq, const int64_t *pos, int64_t m,
+                                    const float *cs, const float *sn, float *kc, float *vc,
+                                    float *out, int64_t ldo, int nh, int nkv, int max_seq,
+                                    hipStream_t s) {
+  hipLaunchKernelGGL(rope_append_kernel<HD>, dim3((unsigned)m), dim3(kGlueThreads), 0, s, qkv,
+                     ldq, pos, cs, sn, kc, vc, nh, nkv, max_seq);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  const dim3 grid((unsigned)((m + kPfRows - 1) / kPfRows), (unsigned)nkv);
+  hipLaunchKernelGGL(attention_prefill_kernel<HD>, grid, dim3(kGlueThreads), 0, s, qkv, ldq, pos,
+                     m, cs, sn, kc, vc, out, ldo, nh, nkv, max_seq);
+  return hipGetLastError();
+}
+
+hipError_t launch_attention_prefill(const float *qkv, int64_t ldq, const int64_t *pos, int64_t m,
+                                    const float *cs, const float *sn, float *kc, float *vc,
+                                    float *out, int64_t ldo, int nh, int nkv, int hd,
+                                    int64_t max_seq, hipStream_t s) {
+  if (hd == 64)
+    return launch_prefill_hd<64>(qkv, ldq, pos, m, cs, sn, kc, vc, out, ldo, nh, nkv,
+                                 (int)max_seq, s);
+  if (hd == 128)
+    return launch_prefill_hd<128>(qkv, ldq, pos, m, cs, sn, kc, vc, out, ldo, nh, nkv,
+                                  (int)max_seq, s);
+  return launch_prefill_hd<256>(qkv, ldq, pos, m, cs, sn, kc, vc, out, ldo, nh, nkv,
+                                (int)max_seq, s);
 }
 
 // ---------------------------------------------------------------------------

@@ -20,9 +20,15 @@ fusion, forward-pass.ts:740-791, applied to Q/K/V too; byte-identical to
 separate dispatches).  A decode step runs the glue as libgguf_hip kernels
 (``glue.py``: the input norms and SwiGLU run as prologues of the projections
 that consume them, the residual adds as accumulate epilogues of the output
-and down projections, RoPE + KV append + GQA attention as one two-pass
-launch, argmax) over preallocated buffers: six launches per layer.  Prefill (many positions at once) runs the glue as torch
-f32 ops; ``fused=False`` does the same for decode steps.  A decode step keeps
+and down projections, RoPE + KV append + GQA attention as one launch whose
+records the output projection merges, argmax) over preallocated buffers: five
+launches per layer.  Prefill (many positions at once) runs the glue as
+libgguf_hip kernels too: RMSNorm rows, each residual add fused with the
+RMSNorm after it, RoPE + KV append + causal GQA attention of all rows
+(``glue.attention_prefill``, the reference's attention.wgsl with
+new_seq_len > 1), SwiGLU rows.  ``hip_glue=False`` runs the prefill glue as
+torch f32 ops instead, and ``fused=False`` does the same for decode steps.
+A decode step keeps
 the token and position in device tensors, so it can be captured once in a HIP
 graph and replayed for every generated token without host synchronization.
 """
@@ -203,16 +209,25 @@ def apply_rope(x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor) -> torch.T
     return torch.cat([x1 * c - x2 * s, x2 * c + x1 * s], dim=-1)
 
 
+def glue_shapes(cfg: DecoderConfig) -> bool:
+    """Whether the glue kernels take the configuration: head_dim 64, 128 or 256,
+    at most 8 query heads per KV head, rows of a multiple of 4 values."""
+    return (cfg.head_dim in (64, 128, 256) and cfg.n_heads % cfg.n_kv_heads == 0
+            and cfg.n_heads // cfg.n_kv_heads <= 8 and cfg.d_model % 4 == 0
+            and cfg.ffn % 4 == 0)
+
+
 class QuantDecoder:
     """Greedy decoder over ``DecoderWeights`` with an f32 KV cache in HBM."""
 
     def __init__(self, cfg: DecoderConfig, weights: DecoderWeights, device="cuda",
-                 fused: bool = True):
+                 fused: bool = True, hip_glue: bool = True):
         # the grid-codebook IQ types have no fused decode-step kernels: a model
         # holding one runs its decode steps unfused
         grid = any(w.ggml_type not in FUSED_TYPES for w in all_weights(weights))
         self.cfg, self.w, self.device = cfg, weights, torch.device(device)
         self.fused = fused and not grid
+        self.hip_glue = hip_glue and glue_shapes(cfg)
         L, kv, T, hd = cfg.n_layers, cfg.n_kv_heads, cfg.max_seq, cfg.head_dim
         self.k_cache = torch.zeros(L, kv, T, hd, device=self.device)
         self.v_cache = torch.zeros(L, kv, T, hd, device=self.device)
@@ -290,6 +305,31 @@ class QuantDecoder:
             x = x + self._proj(a, lw.down_gg, f"L{l}-down")
         return x
 
+    def _layers_glue(self, x: torch.Tensor, pos: torch.Tensor) -> torch.Tensor:
+        """All layers over the M rows of ``x`` (updated in place) with the glue as
+        libgguf_hip kernels; returns the rows after the final RMSNorm."""
+        cfg, layers = self.cfg, self.w.layers
+        M = x.shape[0]
+        h = torch.empty_like(x)
+        att = torch.empty(M, cfg.n_heads * cfg.head_dim, device=self.device)
+        a = torch.empty(M, cfg.ffn, device=self.device)
+        glue.rmsnorm(x, layers[0].attn_norm, cfg.eps, h)
+        for l, lw in enumerate(layers):
+            qkv = self._proj_slot(h, lw, "qkv", f"L{l}-qkv")
+            glue.attention_prefill(qkv, pos, self.cos, self.sin, self.k_cache[l],
+                                   self.v_cache[l], att, cfg.n_heads, cfg.n_kv_heads,
+                                   cfg.head_dim)
+            glue.add_rmsnorm(x, self._proj(att, lw.o_gg, f"L{l}-o"), lw.ffn_norm, cfg.eps, h)
+            w = lw.get("gateUpI_gg")
+            if w is not None:  # tile-interleaved gate / up columns -> [gate | up] rows
+                gu = torch.cat(split_interleaved(self._proj(h, w, f"L{l}-gateUp")), dim=1)
+            else:
+                gu = self._proj_slot(h, lw, "gateUp", f"L{l}-gateUp")
+            glue.swiglu(gu, a)
+            nxt = layers[l + 1].attn_norm if l + 1 < len(layers) else self.w.final_norm
+            glue.add_rmsnorm(x, self._proj(a, lw.down_gg, f"L{l}-down"), nxt, cfg.eps, h)
+        return h
+
     def _logits(self, x_last: torch.Tensor) -> torch.Tensor:
         h = rms_norm(x_last, self.w.final_norm, self.cfg.eps)
         return self._proj(h, self.w.lm_head_gg, "lm_head")
@@ -303,6 +343,9 @@ class QuantDecoder:
             raise ValueError(f"sequence of {pos0 + M} exceeds max_seq {self.cfg.max_seq}")
         pos = torch.arange(pos0, pos0 + M, device=self.device)
         x = self._embed(tokens)
+        if self.hip_glue:
+            h = self._layers_glue(x, pos)
+            return self._proj(h[-1:], self.w.lm_head_gg, "lm_head")
         x = self._layers(x, pos)
         return self._logits(x[-1:])
 

@@ -125,6 +125,46 @@ def attention_decode(qkv: torch.Tensor, pos: torch.Tensor, cos: torch.Tensor, si
     return out
 
 
+def attention_prefill(qkv: torch.Tensor, pos: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor,
+                      k_cache: torch.Tensor, v_cache: torch.Tensor, out: torch.Tensor,
+                      n_heads: int, n_kv_heads: int, head_dim: int) -> torch.Tensor:
+    """RoPE + KV append + causal GQA attention of M rows at once (prefill).
+    ``qkv`` [M, >= (n_heads + 2 n_kv_heads) head_dim] and ``out`` [M, >= n_heads
+    head_dim] may have a row stride (unit column stride); ``pos`` device int64
+    [M] holds distinct positions.  Row r attends over cache slots 0..pos[r]:
+    the slots this call does not write must already hold keys.  Two launches."""
+    if qkv.dim() != 2 or out.dim() != 2 or qkv.shape[0] != out.shape[0]:
+        raise ValueError("attention_prefill: qkv and out must be [M, ...] with the same M")
+    m = qkv.shape[0]
+    if pos.numel() != m:
+        raise ValueError(f"attention_prefill: pos holds {pos.numel()} positions, M = {m}")
+    if k_cache.dim() < 2 or k_cache.shape[-1] != head_dim:
+        raise ValueError("attention_prefill: k_cache must be [n_kv_heads, max_seq, head_dim]")
+    max_seq = k_cache.shape[-2]
+    _numel("attention_prefill: k_cache", k_cache, n_kv_heads * max_seq * head_dim)
+    _numel("attention_prefill: v_cache", v_cache, n_kv_heads * max_seq * head_dim)
+    _numel("attention_prefill: cos", cos, max_seq * (head_dim // 2))
+    _numel("attention_prefill: sin", sin, max_seq * (head_dim // 2))
+    row, orow = (n_heads + 2 * n_kv_heads) * head_dim, n_heads * head_dim
+    if qkv.shape[1] < row or out.shape[1] < orow:
+        raise ValueError(f"attention_prefill: qkv rows hold {qkv.shape[1]} values (need {row}), "
+                         f"out rows {out.shape[1]} (need {orow})")
+    for name, t in (("qkv", qkv), ("out", out)):
+        if t.dtype != torch.float32 or not t.is_cuda or (m > 1 and t.stride(1) != 1) \
+                or t.stride(0) < t.shape[1]:
+            raise ValueError(f"attention_prefill: {name} must be float32 device rows "
+                             "with unit column stride")
+    _f32(cos, sin, k_cache, v_cache)
+    if pos.dtype != torch.int64 or not pos.is_cuda:
+        raise ValueError("pos must be an int64 device tensor")
+    lib = _native.load_library()
+    _native.check(lib.gguf_hip_attention_prefill(
+        qkv.data_ptr(), qkv.stride(0), pos.data_ptr(), m, cos.data_ptr(), sin.data_ptr(),
+        k_cache.data_ptr(), v_cache.data_ptr(), out.data_ptr(), out.stride(0), n_heads,
+        n_kv_heads, head_dim, max_seq, _s(qkv)), lib)
+    return out
+
+
 def matmul_attn_merge(work: torch.Tensor, pos: torch.Tensor, w, y: torch.Tensor, n_heads: int,
                       n_kv_heads: int, head_dim: int, max_seq: int,
                       accumulate: bool = False) -> torch.Tensor:

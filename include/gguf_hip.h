@@ -49,7 +49,7 @@ extern "C" {
  * are exported (kernels and helpers cannot be interposed across libraries). */
 #pragma GCC visibility push(default)
 
-#define GGUF_HIP_ABI_VERSION 17
+#define GGUF_HIP_ABI_VERSION 18
 
 /* ggml type ids (gguf.ts:24-35); activation dtypes reuse F32 / F16. */
 #define GGUF_HIP_F32 0
@@ -281,6 +281,26 @@ int gguf_hip_attention_decode_noalloc(const float *qkv, const int64_t *pos,
                                       float *k_cache, float *v_cache, float *out, int n_heads,
                                       int n_kv_heads, int head_dim, int64_t max_seq,
                                       void *stream);
+
+/* Prefill attention over m new rows (attention.wgsl:60-234 with new_seq_len =
+ * m, causal, and rope.wgsl:1-10 before it; forward-pass.ts:2925-3297).  For
+ * each row r at position pos[r] (device int64 [m]): rotate_half RoPE of q and
+ * k with the tables' row pos[r], k and v stored at slot pos[r] of the caches,
+ * then causal GQA attention of each query head h over slots 0..pos[r] of KV
+ * head h / (n_heads / n_kv_heads), softmax scaled by 1/sqrt(head_dim).
+ * qkv rows (stride ldqkv floats) = [q (n_heads*head_dim) | k | v
+ * (n_kv*head_dim each)]; out rows (stride ldo) = n_heads*head_dim.  Slots
+ * below a row's position that the call does not write must hold keys already
+ * (an earlier prefill or decode call).  Positions within a call must be
+ * distinct; a position outside 0..max_seq-1 leaves its row's cache slot and
+ * output untouched.  out must not overlap qkv or the caches.  Shapes as
+ * gguf_hip_attention_decode; ldqkv and ldo multiples of 4; qkv, out, caches
+ * and tables 16-byte aligned.  Two launches, no workspace.  m == 0 is a
+ * no-op. */
+int gguf_hip_attention_prefill(const float *qkv, int64_t ldqkv, const int64_t *pos, int64_t m,
+                               const float *cos_table, const float *sin_table, float *k_cache,
+                               float *v_cache, float *out, int64_t ldo, int n_heads,
+                               int n_kv_heads, int head_dim, int64_t max_seq, void *stream);
 
 /* The attention output projection of one decode position with the attention
  * merge fused in: y (= or +=, epilogue STORE / ACCUMULATE) W . a, where a

@@ -43,7 +43,7 @@ def native(pkg):
 
 def test_exports_every_declared_symbol(lib, native):
     names = _declared_functions()
-    assert len(names) == 23, names
+    assert len(names) == 24, names
     for n in names:
         assert hasattr(lib, n), n
         assert n in native.SIGNATURES, n
@@ -98,7 +98,7 @@ def test_grid_types_contract(lib, native):
 
 
 def test_abi_version(lib):
-    assert lib.gguf_hip_abi_version() == 17
+    assert lib.gguf_hip_abi_version() == 18
 
 
 def test_type_traits(lib, native):
@@ -248,6 +248,21 @@ def test_glue_errors(lib, native):
     assert big > native.NOALLOC_ATTENTION_BYTES
     assert na(a, b, c, c, a, a, b, 64, 8, 128, 65536, None) == native.ERR_SHAPE
     assert "noalloc" in native.last_error(lib)
+    # prefill attention: qkv row 32*128 + 2*8*128 = 6144 floats, out row 4096
+    pf = lib.gguf_hip_attention_prefill
+    assert pf(a, 6144, b, 128, c, c, a, a, b, 4096, 32, 5, 128, 512, None) == native.ERR_SHAPE
+    assert pf(a, 6144, b, 128, c, c, a, a, b, 4096, 32, 8, 96, 512, None) == native.ERR_SHAPE
+    assert pf(a, 6140, b, 128, c, c, a, a, b, 4096, 32, 8, 128, 512, None) == native.ERR_SHAPE
+    assert pf(a, 6146, b, 128, c, c, a, a, b, 4096, 32, 8, 128, 512, None) == native.ERR_SHAPE
+    assert pf(a, 6144, b, 128, c, c, a, a, b, 4092, 32, 8, 128, 512, None) == native.ERR_SHAPE
+    assert "ldqkv" in native.last_error(lib)
+    assert pf(a, 6144, b, -1, c, c, a, a, b, 4096, 32, 8, 128, 512, None) == native.ERR_SHAPE
+    assert pf(None, 6144, None, 0, None, None, None, None, None, 4096, 32, 8, 128, 512,
+              None) == 0                                                      # no rows
+    assert pf(a, 6144, b, 4, c, c, a, a, None, 4096, 32, 8, 128, 512, None) == native.ERR_NULL
+    assert pf(a, 6144, b + 4, 4, c, c, a, a, b, 4096, 32, 8, 128, 512, None) == native.ERR_ALIGN
+    assert pf(a, 6144, b, 4, c + 4, c, a, a, b, 4096, 32, 8, 128, 512, None) == native.ERR_ALIGN
+    assert pf(a, 6144, b, 4, c, c, a, a, b + 4, 4096, 32, 8, 128, 512, None) == native.ERR_ALIGN
     assert lib.gguf_hip_argmax_workspace() > 0
     assert lib.gguf_hip_argmax(a, 0, b, c, None) == native.ERR_SHAPE
     assert lib.gguf_hip_argmax(a, 10, b + 4, c, None) == native.ERR_ALIGN

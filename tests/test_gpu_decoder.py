@@ -153,6 +153,23 @@ def test_fused_glue_matches_torch_glue(dec, model):
     assert torch.allclose(a.k_cache, b.k_cache, rtol=1e-5, atol=1e-5)
 
 
+def test_prefill_glue_kernels_match_torch_glue(dec, model):
+    """Prefill with its glue as HIP kernels (RMSNorm rows, residual add fused
+    with the next RMSNorm, RoPE + KV append + causal attention of all rows,
+    SwiGLU rows) against the same prefill with the glue as torch f32 ops: a
+    40-row prompt (three blocks of 16 rows, the last ragged), then a second
+    prefill of 20 rows at position 40 over the cached keys."""
+    cfg, w = model
+    a, b = dec.QuantDecoder(cfg, w), dec.QuantDecoder(cfg, w, hip_glue=False)
+    assert a.hip_glue and not b.hip_glue
+    toks = torch.from_numpy(np.random.default_rng(12).integers(0, cfg.vocab, 60)).cuda()
+    assert _rel(a.prefill(toks[:40], 0), b.prefill(toks[:40], 0)) < 2e-5
+    assert _rel(a.prefill(toks[40:], 40), b.prefill(toks[40:], 40)) < 2e-5
+    for ca, cb in ((a.k_cache, b.k_cache), (a.v_cache, b.v_cache)):
+        assert torch.allclose(ca[:, :, :60], cb[:, :, :60], rtol=1e-4, atol=1e-5)
+        assert not ca[:, :, 60:].any()                  # no slot past the prompt written
+
+
 FULL_WIDTH = dict(n_layers=2, d_model=4096, n_heads=32, n_kv_heads=8, head_dim=128, ffn=14336,
                   vocab=151936, max_seq=64)
 

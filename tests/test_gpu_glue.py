@@ -123,3 +123,83 @@ def test_argmax_first_index_and_ties(lib):
     x[151935] = 1000.0                               # maximum in the last workgroup's chunk
     _ok(lib, lib.gguf_hip_argmax(x.data_ptr(), x.numel(), out.data_ptr(), work.data_ptr(), _s()))
     assert out.item() == 151935
+
+
+def _rope_inv(hd, max_seq):
+    half = hd // 2
+    inv = 1.0 / (10000.0 ** (torch.arange(half, dtype=torch.float64) * 2 / hd))
+    ang = torch.arange(max_seq, dtype=torch.float64)[:, None] * inv[None]
+    return inv.cuda(), ang.cos().float().cuda(), ang.sin().float().cuda()
+
+
+@pytest.mark.parametrize("nh,nkv,hd,max_seq,m,pos0,order", [
+    (32, 8, 128, 512, 128, 0, "seq"),     # the decoder's 128-token prompt
+    (32, 8, 128, 512, 248, 128, "seq"),   # a second prefill over 128 cached slots
+    (4, 2, 64, 64, 17, 0, "seq"),         # a ragged block of rows
+    (8, 8, 64, 128, 1, 100, "seq"),       # one row, one query head per KV head
+    (12, 4, 128, 96, 40, 20, "perm"),     # groups of 3 (an idle wave), rows out of order
+    (16, 2, 256, 200, 70, 130, "seq"),    # head_dim 256, groups of 8 (two passes), last slot
+    (32, 8, 128, 300, 50, 7, "bad"),      # rows at positions -1 and max_seq
+])
+def test_attention_prefill(lib, nh, nkv, hd, max_seq, m, pos0, order):
+    """RoPE, KV append and causal GQA attention of m rows against float64:
+    RoPE as a complex rotation, attention as an explicit masked softmax over the
+    whole cache (slots below the call's rows hold earlier keys)."""
+    g = torch.Generator(device="cuda").manual_seed(m + pos0 + hd)
+    row, orow, grp, half = (nh + 2 * nkv) * hd, nh * hd, nh // nkv, hd // 2
+    qkv = torch.randn(m, row + 8, device="cuda", generator=g)[:, :row]   # row stride > row
+    kc = torch.randn(nkv, max_seq, hd, device="cuda", generator=g)
+    vc = torch.randn(nkv, max_seq, hd, device="cuda", generator=g)
+    kc0, vc0 = kc.clone(), vc.clone()
+    inv, cos, sin = _rope_inv(hd, max_seq)
+    p = torch.arange(pos0, pos0 + m)
+    if order == "perm":
+        p = p[torch.randperm(m, generator=torch.Generator().manual_seed(1))]
+    if order == "bad":
+        p[3], p[m - 2] = -1, max_seq
+    pos = p.cuda()
+    obuf = torch.full((m, orow + 4), float("nan"), device="cuda")
+    out = obuf[:, :orow]
+
+    def run(o):
+        _ok(lib, lib.gguf_hip_attention_prefill(qkv.data_ptr(), qkv.stride(0), pos.data_ptr(), m,
+                                                cos.data_ptr(), sin.data_ptr(), kc.data_ptr(),
+                                                vc.data_ptr(), o.data_ptr(), o.stride(0), nh, nkv,
+                                                hd, max_seq, _s()))
+    run(out)
+    valid = (p >= 0) & (p < max_seq)
+    vr = valid.nonzero().flatten().tolist()
+    pv = p[valid].tolist()
+    th = p.clamp(0, max_seq - 1).cuda().double()[:, None, None] * inv   # [m, 1, half]
+
+    def rot(x):
+        z = torch.complex(x[..., :half], x[..., half:]) * torch.exp(1j * th)
+        return torch.cat([z.real, z.imag], dim=-1)
+    q = rot(qkv[:, :orow].double().view(m, nh, hd))
+    k = rot(qkv[:, orow:orow + nkv * hd].double().view(m, nkv, hd))
+    v = qkv[:, orow + nkv * hd:].double().view(m, nkv, hd)
+    K, V = kc0.double().clone(), vc0.double().clone()
+    K[:, pv], V[:, pv] = k[vr].transpose(0, 1), v[vr].transpose(0, 1)
+    # the caches: the valid rows' slots written (v copied as is), every other slot untouched
+    assert torch.allclose(kc[:, pv].double(), K[:, pv], rtol=1e-5, atol=1e-6)
+    assert torch.equal(vc[:, pv], qkv[vr, orow + nkv * hd:].view(-1, nkv, hd).transpose(0, 1))
+    others = [t for t in range(max_seq) if t not in set(pv)]
+    assert torch.equal(kc[:, others], kc0[:, others]) and torch.equal(vc[:, others], vc0[:, others])
+    # attention of the valid rows
+    T = torch.arange(max_seq, device="cuda")
+    masked = T[None, :] > p.cuda()[:, None]                               # [m, max_seq]
+    ref = torch.empty(m, nh, hd, dtype=torch.float64, device="cuda")
+    for h in range(nh):
+        s = (q[:, h] @ K[h // grp].T) / math.sqrt(hd)
+        s = s.masked_fill(masked, float("-inf"))
+        e = torch.exp(s - s.max(dim=1, keepdim=True).values)
+        ref[:, h] = (e / e.sum(dim=1, keepdim=True)) @ V[h // grp]
+    got = out.double().view(m, nh, hd)
+    assert torch.allclose(got[vr], ref[vr], rtol=1e-4, atol=2e-5)
+    bad = [r for r in range(m) if r not in set(vr)]
+    assert torch.isnan(out[bad]).all()                 # rows without a slot are not written
+    assert torch.isnan(obuf[:, orow:]).all()           # nothing past a row
+    # a second call (the same slots rewritten with the same k / v) is bit-identical
+    out2 = torch.full_like(out, float("nan"))
+    run(out2)
+    assert torch.equal(out[vr], out2[vr])
