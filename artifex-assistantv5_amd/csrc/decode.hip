@@ -20,6 +20,12 @@ hipError_t launch_decode_fused(const float *x, const uint8_t *tiles, int type, i
     case 14: return decode_fused_q6_k(x, tiles, (int)n, (int)k, y, prologue, pw, eps, epi, s);
     case 20: return decode_fused_iq4_nl(x, tiles, (int)n, (int)k, y, prologue, pw, eps, epi, s);
     case 23: return decode_fused_iq4_xs(x, tiles, (int)n, (int)k, y, prologue, pw, eps, epi, s);
+    case 16: return decode_fused_iq2_xxs(x, tiles, (int)n, (int)k, y, prologue, pw, eps, epi, s);
+    case 17: return decode_fused_iq2_xs(x, tiles, (int)n, (int)k, y, prologue, pw, eps, epi, s);
+    case 22: return decode_fused_iq2_s(x, tiles, (int)n, (int)k, y, prologue, pw, eps, epi, s);
+    case 18: return decode_fused_iq3_xxs(x, tiles, (int)n, (int)k, y, prologue, pw, eps, epi, s);
+    case 21: return decode_fused_iq3_s(x, tiles, (int)n, (int)k, y, prologue, pw, eps, epi, s);
+    case 29: return decode_fused_iq1_m(x, tiles, (int)n, (int)k, y, prologue, pw, eps, epi, s);
     default: return hipErrorNotSupported;
   }
 }
@@ -39,6 +45,12 @@ hipError_t launch_decode_attn_merge(const AttnRecords &ar, const uint8_t *tiles,
     case 14: return decode_merge_q6_k(ar, tiles, (int)n, y, epi, s);
     case 20: return decode_merge_iq4_nl(ar, tiles, (int)n, y, epi, s);
     case 23: return decode_merge_iq4_xs(ar, tiles, (int)n, y, epi, s);
+    case 16: return decode_merge_iq2_xxs(ar, tiles, (int)n, y, epi, s);
+    case 17: return decode_merge_iq2_xs(ar, tiles, (int)n, y, epi, s);
+    case 22: return decode_merge_iq2_s(ar, tiles, (int)n, y, epi, s);
+    case 18: return decode_merge_iq3_xxs(ar, tiles, (int)n, y, epi, s);
+    case 21: return decode_merge_iq3_s(ar, tiles, (int)n, y, epi, s);
+    case 29: return decode_merge_iq1_m(ar, tiles, (int)n, y, epi, s);
     default: return hipErrorNotSupported;
   }
 }

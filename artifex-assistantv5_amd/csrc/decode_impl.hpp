@@ -1895,7 +1895,8 @@ hipError_t launch_m(const XT *x, int64_t ldx, const uint8_t *W, int N, int K, fl
 // its image and partial sums; without one (K <= 16384) the one-shot kernel
 // runs once per activation row, which needs no workspace.  K > 16384 always
 // takes the batched kernel (hipErrorNotSupported without a workspace, before
-// anything is launched).  No fused prologue / epilogue or merge kernels.
+// anything is launched).  The fused prologue / epilogue and merge kernels are
+// the one-shot kernel's, as for the other types.
 template <int TYPE, typename XT>
 hipError_t launch_iq(const XT *x, int64_t ldx, const uint8_t *W, int N, int K, float *y,
                      int64_t ldy, int M, float *work, int64_t work_floats, hipStream_t s) {
@@ -1925,13 +1926,19 @@ hipError_t launch_iq(const XT *x, int64_t ldx, const uint8_t *W, int N, int K, f
     const size_t b = x_type == 0 ? mk_work_bytes<T, float>(m, n, k) : mk_work_bytes<T, half_t>(m, n, k); \
     return (int64_t)((b + 3) / 4);                                                               \
   }                                                                                              \
-  hipError_t decode_fused_##NAME(const float *, const uint8_t *, int, int, float *, int,         \
-                                 const float *, float, int, hipStream_t) {                       \
-    return hipErrorNotSupported;                                                                 \
+  hipError_t decode_fused_##NAME(const float *x, const uint8_t *tiles, int n, int k, float *y,   \
+                                 int prologue, const float *pw, float eps, int epi,              \
+                                 hipStream_t s) {                                                \
+    return prologue == 1   ? launch_m1<T, float, 1>(x, tiles, n, k, y, pw, eps, epi,             \
+                                                    AttnRecords{}, s)                            \
+           : prologue == 2 ? launch_m1<T, float, 2>(x, tiles, n, k, y, pw, eps, epi,             \
+                                                    AttnRecords{}, s)                            \
+                           : launch_m1<T, float, 0>(x, tiles, n, k, y, pw, eps, epi,             \
+                                                    AttnRecords{}, s);                           \
   }                                                                                              \
-  hipError_t decode_merge_##NAME(const AttnRecords &, const uint8_t *, int, float *, int,        \
-                                 hipStream_t) {                                                  \
-    return hipErrorNotSupported;                                                                 \
+  hipError_t decode_merge_##NAME(const AttnRecords &ar, const uint8_t *tiles, int n, float *y,   \
+                                 int epi, hipStream_t s) {                                       \
+    return launch_m1<T, float, 3>(nullptr, tiles, n, ar.nh * ar.hd, y, nullptr, 0.f, epi, ar, s); \
   }
 
 }  // namespace gguf

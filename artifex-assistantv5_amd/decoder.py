@@ -222,8 +222,7 @@ class QuantDecoder:
 
     def __init__(self, cfg: DecoderConfig, weights: DecoderWeights, device="cuda",
                  fused: bool = True, hip_glue: bool = True):
-        # the grid-codebook IQ types have no fused decode-step kernels: a model
-        # holding one runs its decode steps unfused
+        # a weight of a type without fused decode-step kernels runs the step unfused
         grid = any(w.ggml_type not in FUSED_TYPES for w in all_weights(weights))
         self.cfg, self.w, self.device = cfg, weights, torch.device(device)
         self.fused = fused and not grid

@@ -71,15 +71,15 @@ IQ3_XXS = GGML_TYPES["IQ3_XXS"]
 IQ3_S = GGML_TYPES["IQ3_S"]
 IQ1_M = GGML_TYPES["IQ1_M"]
 
-# The grid-codebook types: decode kernels only (any M, in passes of 32 rows),
-# always with a workspace, no fused prologue / epilogue kernels.
+# The grid-codebook types (codebook entries, sign patterns and odd scale factors
+# per 8 values).
 GRID_TYPES = (IQ2_XXS, IQ2_XS, IQ2_S, IQ3_XXS, IQ3_S, IQ1_M)
 
 # Types the HIP kernels of this library decode.
 KERNEL_TYPES = (Q4_0, Q5_0, Q8_0, Q2_K, Q3_K, Q4_K, Q5_K, Q6_K, IQ4_NL, IQ4_XS) + GRID_TYPES
 
-# Types with fused decode-step kernels (gguf_hip_matmul_fused / _attn_merge).
-FUSED_TYPES = tuple(t for t in KERNEL_TYPES if t not in GRID_TYPES)
+# Types with fused decode-step kernels (gguf_hip_matmul_fused / _attn_merge): all.
+FUSED_TYPES = KERNEL_TYPES
 
 
 class GGMLTypeError(NotImplementedError):

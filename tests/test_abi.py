@@ -75,8 +75,9 @@ def test_constants_match_header(native):
 def test_grid_types_contract(lib, native):
     """IQ2_XXS .. IQ1_M: no workspace needed for the decode variant up to
     K = 16384 (M = 1 asks for none, M >= 2 for an optional one); beyond it a
-    workspace is required.  No fused kernels.  Fake (aligned, never
-    dereferenced) pointers: every check below fails before any HIP call."""
+    workspace is required, and the fused kernels stop there as for the other
+    types.  Fake (aligned, never dereferenced) pointers: every check below
+    fails before any HIP call."""
     x, w, y = 0x10000, 0x20000, 0x30000
     for t in (16, 17, 18, 21, 22, 29):
         for xt in (0, 1):
@@ -90,9 +91,10 @@ def test_grid_types_contract(lib, native):
         need = lib.gguf_hip_matmul_workspace(t, 0, 64, 16640, 3)
         assert lib.gguf_hip_matmul_ws(x, 0, 16640, w, t, 64, 16640, y, 64, 3, 0, 0x40000,
                                       need - 16, None) == native.ERR_SHAPE
-        assert lib.gguf_hip_matmul_fused(x, w, t, 64, 512, y, 0, None, ctypes.c_float(0.0), 0,
+        # fused kernels exist for these types too, up to K = 16384 like the others
+        assert lib.gguf_hip_matmul_fused(x, w, t, 64, 16640, y, 0, None, ctypes.c_float(0.0), 0,
                                          None) == native.ERR_SHAPE
-        assert "no fused kernel" in native.last_error(lib)
+        assert "above 16384" in native.last_error(lib)
     assert (lib.gguf_hip_matmul_workspace(12, 0, 64, 512, 1), lib.gguf_hip_matmul_workspace(
         20, 0, 64, 512, 1)) == (0, 0)
 

@@ -1,12 +1,20 @@
-"""Fused decode-step projections (gguf_hip_matmul_fused) against a float64 composition."""
+"""Fused decode-step projections (gguf_hip_matmul_fused) against a float64 composition.
+
+The K-quant and 32-element types use the package quantizer's weights; the
+grid-codebook IQ types (IQ2_XXS .. IQ1_M) use random valid blocks (every bit
+pattern decodes), whose dequantization is pinned to the oracle elsewhere."""
 import importlib
 
 import numpy as np
 import pytest
 
+import tile_model
+
 torch = pytest.importorskip("torch")
 
 pytestmark = pytest.mark.gpu
+
+GRID = (16, 17, 22, 18, 21, 29)
 
 
 @pytest.fixture(scope="module")
@@ -16,8 +24,11 @@ def mods():
 
 
 def _weight(pkg, t, n, k, seed):
-    w = pkg.quantize.synthetic_weight(n, k, seed=seed)
-    return pkg.repack_gguf_for_gpu(t, pkg.quantize.quantize(w, t), n, k, device="cuda")
+    if t in GRID:
+        raw = tile_model.random_blocks(t, n, k, seed=seed)
+    else:
+        raw = pkg.quantize.quantize(pkg.quantize.synthetic_weight(n, k, seed=seed), t)
+    return pkg.repack_gguf_for_gpu(t, raw, n, k, device="cuda")
 
 
 def _rel(a, b):
@@ -35,7 +46,10 @@ def _elementwise(y, ref, wd, xd):
                                    (8, 512, 4096), (12, 4096, 14336), (14, 2048, 4096),
                                    (2, 1000, 4096), (6, 512, 14336), (20, 2048, 4096),
                                    (23, 1000, 4096), (23, 4096, 14336), (10, 1000, 4096),
-                                   (10, 4096, 14336), (11, 1000, 4096), (11, 4096, 14336)])
+                                   (10, 4096, 14336), (11, 1000, 4096), (11, 4096, 14336),
+                                   (16, 1000, 4096), (17, 1000, 4096), (22, 1000, 4096),
+                                   (18, 1000, 4096), (21, 1000, 4096), (29, 1000, 4096),
+                                   (16, 4096, 14336), (21, 6144, 4096)])
 def test_rmsnorm_prologue(mods, t, n, k):
     pkg, glue = mods
     w = _weight(pkg, t, n, k, seed=n + k)
@@ -52,7 +66,8 @@ def test_rmsnorm_prologue(mods, t, n, k):
     assert _elementwise(y, ref, wd, h) < 1e-6
 
 
-@pytest.mark.parametrize("t,n,k", [(14, 4096, 14336), (12, 4096, 14336), (8, 256, 2048)])
+@pytest.mark.parametrize("t,n,k", [(14, 4096, 14336), (12, 4096, 14336), (8, 256, 2048),
+                                   (18, 4096, 14336), (29, 1024, 2048), (17, 512, 4096)])
 def test_swiglu_prologue_accumulate(mods, t, n, k):
     pkg, glue = mods
     w = _weight(pkg, t, n, k, seed=7 * n + k)
@@ -71,7 +86,8 @@ def test_swiglu_prologue_accumulate(mods, t, n, k):
 
 @pytest.mark.parametrize("t,ffn,k", [(12, 14336, 4096), (12, 512, 2048), (13, 1024, 4096),
                                      (14, 256, 4096), (8, 768, 1024), (23, 1024, 4096),
-                                     (10, 1024, 4096), (11, 1024, 4096)])
+                                     (10, 1024, 4096), (11, 1024, 4096), (16, 14336, 4096),
+                                     (22, 1024, 4096), (21, 512, 2048), (29, 1024, 4096)])
 @pytest.mark.parametrize("norm", [False, True])
 def test_swiglu_epilogue(mods, t, ffn, k, norm):
     """Interleaved gate / up tiles: y = up * silu(gate) straight from the projection,
@@ -142,7 +158,9 @@ def _attention_inputs(nh, nkv, hd, max_seq, p):
     (12, 32, 8, 128, 1200, 300), (12, 32, 8, 128, 1200, 511), (12, 32, 8, 128, 1200, 1199),
     (14, 32, 8, 128, 640, 383), (8, 8, 8, 64, 128, 100), (12, 16, 2, 256, 700, 650),
     (13, 64, 8, 128, 256, 200), (23, 32, 8, 128, 300, 130), (10, 32, 8, 128, 300, 77),
-    (11, 32, 8, 128, 300, 200)])
+    (11, 32, 8, 128, 300, 200), (16, 32, 8, 128, 640, 383), (17, 32, 8, 128, 300, 64),
+    (22, 32, 8, 128, 300, 130), (18, 16, 2, 256, 700, 650), (21, 32, 8, 128, 1200, 1199),
+    (29, 32, 8, 128, 300, 0)])
 def test_attention_merge_projection(mods, t, nh, nkv, hd, max_seq, p):
     """Records-only attention + the merge prologue equal, bit for bit, attention
     with its own merge followed by the plain fused projection (same arithmetic

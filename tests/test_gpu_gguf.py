@@ -94,7 +94,7 @@ LOW_BIT = {"q": 11, "k": 10, "v": 23, "o": 2, "gate": 6, "up": 6, "down": 20, "e
 
 
 GRID_MIX = {"q": 16, "k": 17, "v": 18, "o": 21, "gate": 22, "up": 29, "down": 16, "embd": 21,
-            "out": 22}         # IQ2_XXS, IQ2_XS, IQ3_XXS, IQ3_S, IQ2_S, IQ1_M (unfused decode)
+            "out": 22}         # IQ2_XXS, IQ2_XS, IQ3_XXS, IQ3_S, IQ2_S, IQ1_M (fused decode step)
 
 
 @pytest.mark.parametrize("variant", ["mixed_qkv", "uniform_tied", "low_bit", "grid"])
@@ -112,11 +112,35 @@ def test_decoder_from_gguf_matches_direct_build(tmp_path, variant):
     else:
         assert lw.qkv_gg is not None
     direct = dec.QuantDecoder(cfg, gm.direct_weights(tensors, gm.TINY))
+    assert model.fused and direct.fused           # every type has the fused step kernels
     prompt = torch.from_numpy(np.random.default_rng(7).integers(0, cfg.vocab, 24)).cuda()
     assert torch.equal(model.prefill(prompt), direct.prefill(prompt))
     a = model.generate(prompt, 10, graph=True)
     b = direct.generate(prompt, 10, graph=False)
     assert torch.equal(a["tokens"], b["tokens"])
+
+
+def test_grid_model_fused_step_matches_unfused(tmp_path):
+    """A model of the six grid-codebook types: the fused decode step (RMSNorm
+    prologues, the attention merge inside the output projection, SwiGLU as the
+    down projection's prologue, residual-accumulate epilogues) against the
+    torch-glue step over plain projections, teacher-forced on the same tokens."""
+    tensors = gm.make_model(seed=4, types=GRID_MIX)
+    p = str(tmp_path / "g.gguf")
+    gm.write_model(p, tensors)
+    model, _ = gmodel.load_decoder(p, "cuda", max_seq=64)
+    w = gm.direct_weights(tensors, gm.TINY)
+    a, b = dec.QuantDecoder(model.cfg, w, fused=True), dec.QuantDecoder(model.cfg, w, fused=False)
+    assert a.fused and not b.fused
+    toks = np.random.default_rng(9).integers(0, model.cfg.vocab, 30).tolist()
+    for m in (a, b):
+        m.prefill(torch.tensor(toks[:20], device="cuda"), 0)
+    pa, pb = torch.tensor([20], device="cuda"), torch.tensor([20], device="cuda")
+    for t in toks[20:]:
+        ga = a.step(torch.tensor([t], device="cuda"), pa).clone()[0]
+        gb = b.step(torch.tensor([t], device="cuda"), pb).clone()[0]
+        assert ((ga.double() - gb.double()).norm() / gb.double().norm()).item() < 1e-5
+    assert torch.allclose(a.k_cache[:, :, :30], b.k_cache[:, :, :30], rtol=1e-5, atol=1e-5)
 
 
 def test_decoder_from_gguf_matches_float64_reference(tmp_path):

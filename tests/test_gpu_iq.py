@@ -146,10 +146,15 @@ def test_api_contract(pkg, native):
     rc = lib.gguf_hip_matmul(x.data_ptr(), 0, kb, w.ptr(), t, n, kb, y.data_ptr(), n, 1, None)
     assert rc == native.ERR_SHAPE and "workspace" in native.last_error(lib)
     torch.cuda.synchronize()
-    # fused decode-step kernels do not exist for these types
+    # the fused decode-step kernel without prologue or epilogue is the plain M = 1 kernel
     rc = lib.gguf_hip_matmul_fused(x.data_ptr(), w.ptr(), t, n, k, y.data_ptr(), 0, None,
                                    ctypes.c_float(0.0), 0, None)
-    assert rc == native.ERR_SHAPE and "no fused kernel" in native.last_error(lib)
+    assert rc == 0, native.last_error(lib)
+    z = torch.empty(1, n, device="cuda")
+    assert lib.gguf_hip_matmul(x.data_ptr(), 0, k, w.ptr(), t, n, k, z.data_ptr(), n, 1,
+                               None) == 0
+    torch.cuda.synchronize()
+    assert torch.equal(y.view(-1)[:n], z[0])
 
 
 @pytest.mark.parametrize("t", GRID)
