@@ -133,29 +133,13 @@ def eager_time(step, steps, warmup):
     return start.elapsed_time(end) / steps
 
 
-def make_pool(pkg, t, n, k, copies, seed, quantized=True):
-    """``copies`` distinct device copies of one quantized weight (row-tile layout).
-
-    ``quantized``: seeded N(0, 0.02) weights through the package quantizer (the
-    raw bytes are returned for the CPU baseline); otherwise random block bytes
-    with finite f16 scales drawn on the device (for the 510 MB LM head)."""
-    import torch
-    raw = None
-    if quantized:
-        w = pkg.quantize.synthetic_weight(n, k, seed=seed)
-        raw = pkg.quantize.quantize(w, t)
-        base = pkg.repack_gguf_for_gpu(t, raw, n, k, device="cuda")
-    else:
-        block, size = BLOCK[t]
-        g = torch.Generator(device="cuda").manual_seed(seed)
-        rawd = torch.randint(0, 256, (n * (k // block) * size,), dtype=torch.uint8, device="cuda",
-                             generator=g)
-        blocks = rawd.view(-1, size)
-        for o in {8: [0], 12: [0, 2], 13: [0, 2], 14: [208]}[t]:
-            v = (torch.rand(blocks.shape[0], device="cuda", generator=g) * 0.003 + 0.0005).half()
-            blocks[:, o:o + 2] = v.view(torch.uint8).view(-1, 2)
-        base = pkg.repack_gguf_for_gpu(t, rawd, n, k)
-        del rawd
+def make_pool(pkg, t, n, k, copies, seed):
+    """``copies`` distinct device copies of one quantized weight (row-tile layout):
+    seeded N(0, 0.02) weights through the package quantizer; the raw bytes are
+    returned for the CPU baseline."""
+    w = pkg.quantize.synthetic_weight(n, k, seed=seed)
+    raw = pkg.quantize.quantize(w, t)
+    base = pkg.repack_gguf_for_gpu(t, raw, n, k, device="cuda")
     pool = [base] + [pkg.GGUFWeight(base.data.clone(), t, n, k) for _ in range(copies - 1)]
     return pool, raw
 
@@ -565,12 +549,16 @@ def secondary_cases(pkg, args, pool, secondary):
         secondary["q5k_gemm_m2048_n14336_frac_fp16_peak"] = round(r["tflops"] / FP16_PEAK_TFLOPS, 4)
         del q5pool
     if want("lm_head"):
-        lpool, _ = make_pool(pkg, 14, 151936, 4096, 2, seed=5, quantized=False)
+        dec = importlib.import_module("artifex-assistantv5_amd.decoder")
+        lm = dec._tiled_rows(14, 16384, 151936, 4096, seed=5, device="cuda")
+        lpool = [lm, pkg.GGUFWeight(lm.data.clone(), 14, 151936, 4096)]
         r = matmul_case(pkg, 14, 1, 151936, 4096, lpool, 40, 3, replays=3)
         secondary["q6k_lm_head_m1_gbs"] = round(r["gbs"], 1)
         secondary["q6k_lm_head_m1_frac_hbm"] = round(r["gbs"] / HBM_PEAK_GBS, 4)
-        secondary["q6k_lm_head_weights"] = "random blocks with finite f16 scales"
-        del lpool
+        secondary["q6k_lm_head_weights"] = ("seeded N(0,0.02) weights quantized to Q6_K: 16384 "
+                                            "rows repeated to 151936, each row's own bytes "
+                                            "in HBM, 2 copies")
+        del lpool, lm
     if want("prefill"):
         # the vendor's plain fp16 GEMM (hipBLASLt through torch.matmul, timed eagerly, not in
         # a graph) on the headline prefill shape: fp16 weights already dequantized, so a
@@ -639,7 +627,9 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "q4_k weights (exact codes) x f32 activations, f32 accumulate",
+        "dtype": ("q4_k weights (exact codes) x f32 activations entering the matrix cores as "
+                  "f16 hi + lo parts of each power-of-two-scaled 256-element unit (22 "
+                  "significant bits), f32 accumulate"),
         "data": "synthetic (seeded N(0,0.02) weights quantized to Q4_K, N(0,1) activations)",
         "config": {"workload": "Q4_K decode GEMV M=1 K=4096 N=14336 (FFN gate/up), cold weights",
                    "M": m, "K": k, "N": n, "weight_copies": args.pool,
