@@ -1154,10 +1154,10 @@ inline int gemm_splits(int type, int64_t tiles, int nu) {
 }
 
 // ---------------------------------------------------------------------------
-// Wide-tile Q4_K GEMM for large grids (fp16 activations).  A workgroup of 8
-// waves owns a 128 x 512 output tile; wave w owns all 128 rows and the 64
-// columns [64 w, 64 w + 64) (four row tiles of the weight): 32 accumulator
-// tiles, 254 VGPRs, two waves per SIMD.  Against gemm_kernel's 128 x 32 per
+// Wide-tile GEMM for large grids (Q4_K and Q8_0, fp16 activations, K a
+// multiple of 256).  A workgroup of 8 waves owns a 128 x 512 output tile; wave
+// w owns all 128 rows and the 64 columns [64 w, 64 w + 64) (four row tiles of
+// the weight): 32 accumulator tiles, 255 VGPRs, two waves per SIMD.  Against gemm_kernel's 128 x 32 per
 // wave, each activation fragment read from LDS feeds twice the MFMAs and a
 // step holds twice the MFMA work per barrier; each dequantized B operand
 // still feeds 8 MFMAs.
@@ -1189,6 +1189,11 @@ inline int gemm_splits(int type, int64_t tiles, int nu) {
 //     its own weight row per 32-column block, so the sub-block scales are
 //     derived once per row; 217 VGPRs): bit-identical results, 868-875
 //     against 865-869 at M = 2048, 1-2% slower at M = 8192.
+//   - Q8_0 on it (bit-identical to gemm_kernel): 702 -> 820 TFLOP/s at
+//     M = 2048, N = 14336; 803 -> 1025 at M = 8192, N = 4096, K = 14336.
+//   - Q6_K on it was bit-identical and slower (678 -> 624, 811 -> 729): its 6
+//     quant dwords per tile and half superblock leave no room for a second
+//     set (one step ahead instead of two) and still spill 31 dwords.
 // ---------------------------------------------------------------------------
 constexpr int kWW = 8, kWTN = 4, kWTM = 8;
 constexpr int kWBM = 16 * kWTM, kWBN = 16 * kWTN * kWW;
@@ -1197,43 +1202,73 @@ constexpr int kWAI = kWBM * 8 / kWThr;  // 16-byte activation chunks a thread st
 constexpr int kWAR = kWThr / 8;         // row distance between them
 constexpr int kWStB = kWBM * kRowB;
 
-// The B side of a Q4_K wave tile: NT row tiles of 16 weight rows in the
-// repacked row-tile layout, the headers of the current superblock and two
-// sets of code words (steps of even and odd parity).
-template <int NT>
-struct Q4KB {
-  rsrc_t brs;
-  int ts;
+// The B side of a wide wave tile: kWTN row tiles of 16 weight rows in the
+// row-tile layout.  Per type: the code words of the steps ahead (two sets),
+// the fields of the current superblock, and the operand build, with the
+// arithmetic of gemm_kernel's dequant_b.  Each tile has its own buffer
+// resource (none past the weight's end: its loads read zero), and every load
+// addresses bytes inside its tile: a request for a unit past the end of K
+// re-reads the last unit (its data is never used).
+//   begin<C>(u)    at the start of step C of unit u
+//   done<C>(j, u)  once both operands of tile j at step C are built
+//   bop<C, H>(j)   the B operand of tile j, k-half H of step C
+template <int TYPE>
+struct WB;
+
+// Q4_K: set P holds the 8 code bytes of the steps of parity P, requested two
+// steps ahead; the header of unit u + 1 is requested at step 2 of unit u.
+template <>
+struct WB<12> {
+  rsrc_t brs[kWTN];
+  int ts, nu;
   BOff bo;
-  uint2 cq[2][NT];
-  uint4 hd[NT];
-  uint32_t sc[NT][2], mn[NT][2];
-  float d24[NT], dmin[NT];
+  uint2 cq[2][kWTN];
+  uint4 hd[kWTN];
+  uint32_t sc[kWTN][2], mn[kWTN][2];
+  float d24[kWTN], dmin[kWTN];
 
   __device__ __forceinline__ void load_codes(int set, int j, int u, int c) {
-    cq[set][j] = bl8(brs, bo.v1, j * ts + u * Fmt<12>::TU + (c >> 1) * 1024 + 8 * (c & 1));
+    cq[set][j] = bl8(brs[j], bo.v1, u * Fmt<12>::TU + (c >> 1) * 1024 + 8 * (c & 1));
   }
   __device__ __forceinline__ void load_hdr(int u) {
 #pragma unroll
-    for (int j = 0; j < NT; ++j) hd[j] = bl16(brs, bo.v0, j * ts + u * Fmt<12>::TU);
+    for (int j = 0; j < kWTN; ++j) hd[j] = bl16(brs[j], bo.v0, u * Fmt<12>::TU);
+  }
+  __device__ __forceinline__ void prologue() {
+    load_hdr(0);
+#pragma unroll
+    for (int j = 0; j < kWTN; ++j) {
+      load_codes(0, j, 0, 0);
+      load_codes(1, j, 0, 1);
+    }
+  }
+  template <int C>
+  __device__ __forceinline__ void begin(int u) {
+    if (C == 2) load_hdr(min(u + 1, nu - 1));
+  }
+  template <int C>
+  __device__ __forceinline__ void done(int j, int u) {
+    const int s2 = 4 * u + C + 2;
+    load_codes(C & 1, j, min(s2 >> 2, nu - 1), (C + 2) & 3);
   }
   __device__ __forceinline__ void set_cur() {
 #pragma unroll
-    for (int j = 0; j < NT; ++j) {
+    for (int j = 0; j < kWTN; ++j) {
       q4k_scales_packed(hd[j].y, hd[j].z, hd[j].w, sc[j][0], sc[j][1], mn[j][0], mn[j][1]);
       const float d = h2f(hd[j].x);
       d24[j] = d * kTwo24;
       dmin[j] = h2f(hd[j].x >> 16);
     }
   }
-  // B operand of tile j, k-half h (sub-block 2c + h) of window c
+  // sub-block 2C + H: low (H = 0) or high nibbles of the step's codes
   template <int C, int H>
-  __device__ __forceinline__ half8_t bfrag(uint2 q2, int j) const {
+  __device__ __forceinline__ half8_t bop(int j) const {
     constexpr int Wd = C >> 1, B0 = ((2 * C) & 3) + H;
     // the high nibble enters as 16 q: its scale carries 1/16 (exact)
     const float s = (H ? d24[j] * 0.0625f : d24[j]) * ubyte(sc[j][Wd], B0),
                 c = -(dmin[j] * ubyte(mn[j][Wd], B0));
     constexpr uint32_t m = H ? 0x00F000F0u : 0x000F000Fu;
+    const uint2 q2 = cq[C & 1][j];
     uint32_t v[4];
 #pragma unroll
     for (int w = 0; w < 2; ++w) {
@@ -1246,44 +1281,92 @@ struct Q4KB {
   }
 };
 
-struct WideQ4K : Q4KB<kWTN> {
-  rsrc_t ars;
-  int avoff, row0, cc, nu, af0, af1;
-  int64_t ldxb;
+// Q8_0: step c of unit u (256 elements) is blocks 8 u + 2 c + H; set P holds
+// their codes and d for the steps of parity P, requested two steps ahead.
+template <>
+struct WB<8> {
+  rsrc_t brs[kWTN];
+  int ts, nu;
+  BOff bo;
+  uint2 cq[2][kWTN][2];
+  uint32_t dq[2][kWTN][2];
+
+  __device__ __forceinline__ void load_codes(int set, int j, int u, int c) {
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int so = (8 * u + 2 * c + h) * Fmt<8>::TU;
+      cq[set][j][h] = bl8(brs[j], bo.v0, so);
+      dq[set][j][h] = bl2(brs[j], bo.v1, so);
+    }
+  }
+  __device__ __forceinline__ void prologue() {
+#pragma unroll
+    for (int j = 0; j < kWTN; ++j) {
+      load_codes(0, j, 0, 0);
+      load_codes(1, j, 0, 1);
+    }
+  }
+  template <int C>
+  __device__ __forceinline__ void begin(int) {}
+  template <int C>
+  __device__ __forceinline__ void done(int j, int u) {
+    const int s2 = 4 * u + C + 2;
+    load_codes(C & 1, j, min(s2 >> 2, nu - 1), (C + 2) & 3);
+  }
+  __device__ __forceinline__ void set_cur() {}
+  // code + 128 enters as a subnormal: fp16(d q) rounded once
+  template <int C, int H>
+  __device__ __forceinline__ half8_t bop(int j) const {
+    const float d = h2f(dq[C & 1][j][H]);
+    const float s = d * kTwo24, c = -128.0f * d;
+    const uint2 q2 = cq[C & 1][j][H];
+    uint32_t v[4];
+#pragma unroll
+    for (int w = 0; w < 2; ++w) {
+      const uint32_t q = (w ? q2.y : q2.x) ^ 0x80808080u;
+      const uint32_t ev = q & 0x00FF00FFu, od = (q >> 8) & 0x00FF00FFu;
+      v[2 * w] = mix_lo(ev, od, s, c);
+      v[2 * w + 1] = mix_hi(ev, od, s, c);
+    }
+    return h8(v[0], v[1], v[2], v[3]);
+  }
+};
+
+template <int TYPE>
+struct Wide : WB<TYPE> {
+  rsrc_t ars[kWAI];  // rows m0 + kWAR i + (0 .. kWAR - 1)
+  int av, row0, cc, K, af0, af1;
   uint4 ar[kWAI];
   float4_t acc[kWTM][kWTN];
   unsigned char *lds;
 
+  // the row within its resource is in the vector offset (rows past M read as
+  // zero); the k offset stops at the last step (steps past K are never staged)
   __device__ __forceinline__ void load_a(int k0) {
+    const int so = 2 * min(k0, K - 64);
 #pragma unroll
-    for (int i = 0; i < kWAI; ++i) ar[i] = bl16(ars, avoff, (int)(kWAR * i * ldxb) + 2 * k0);
+    for (int i = 0; i < kWAI; ++i) ar[i] = bl16(ars[i], av, so);
   }
   __device__ __forceinline__ void store_a(int stage) {
+    unsigned char *base = lds + stage * kWStB;
 #pragma unroll
-    for (int i = 0; i < kWAI; ++i)
-      *(uint4 *)(lds + stage * kWStB + lds_at(row0 + kWAR * i, cc)) = ar[i];
+    for (int i = 0; i < kWAI; ++i) *(uint4 *)(base + lds_at(row0 + kWAR * i, cc)) = ar[i];
   }
 
-  // step s = 4 u + C: A from stage s & 3 (= C), codes from set C & 1.  First
-  // the A of step s + 2 (loaded during step s - 1) goes to stage (s + 2) & 3
-  // and step s + 3's A is requested; then k-half by k-half the fragments of
-  // this step, each tile's B operand dequantized before its 8 MFMAs and its
-  // codes of step s + 2 requested once both halves are built.  A barrier
-  // after odd steps only: stage (s + 2) & 3 was last read at step s - 2 and is
-  // next read at step s + 2, and a barrier at the end of an odd step lies
-  // between each pair.
+  // step s = 4 u + C: A from stage s & 3 (= C).  First the A of step s + 2
+  // (loaded during step s - 1) goes to stage (s + 2) & 3 and step s + 3's A is
+  // requested; then k-half by k-half the fragments of this step, each tile's B
+  // operand built before its 8 MFMAs and the tile's codes ahead requested once
+  // both halves are built.  A barrier after odd steps only: stage (s + 2) & 3
+  // was last read at step s - 2 and is next read at step s + 2, and a barrier
+  // at the end of an odd step lies between each pair.
   template <int C>
   __device__ __forceinline__ void step(int u) {
-    constexpr int P = C & 1;
-    // branch-free: past the end of K these loads are bounded by the buffer
-    // resources (in-range bytes or zeros) and their data is never used
     const int s = 4 * u + C;
     store_a((C + 2) & 3);
     load_a(64 * (s + 3));
-    if (C == 2) load_hdr(u + 1);
+    this->template begin<C>(u);
     const unsigned char *base = lds + C * kWStB;
-    const int u2 = (s + 2) >> 2;
-    constexpr int C2 = (C + 2) & 3;
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
       half8_t a[kWTM];
@@ -1291,8 +1374,8 @@ struct WideQ4K : Q4KB<kWTN> {
       for (int i = 0; i < kWTM; ++i) a[i] = *(const half8_t *)(base + (h ? af1 : af0) + i * 16 * kRowB);
 #pragma unroll
       for (int j = 0; j < kWTN; ++j) {
-        const half8_t b = h ? bfrag<C, 1>(cq[P][j], j) : bfrag<C, 0>(cq[P][j], j);
-        if (h == 1) load_codes(P, j, u2, C2);
+        const half8_t b = h ? this->template bop<C, 1>(j) : this->template bop<C, 0>(j);
+        if (h == 1) this->template done<C>(j, u);
 #pragma unroll
         for (int i = 0; i < kWTM; ++i) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[i], b, acc[i][j], 0, 0, 0);
       }
@@ -1302,11 +1385,12 @@ struct WideQ4K : Q4KB<kWTN> {
   }
 };
 
-template <typename XT>
-__global__ __launch_bounds__(kWThr) void gemm_wide_q4k(const XT *__restrict__ x, int64_t ldx,
-                                                      const uint8_t *__restrict__ W, int M, int N,
-                                                      int K, float *__restrict__ y, int64_t ldy,
-                                                      int tiles_m) {
+// K a multiple of 256.
+template <int TYPE, typename XT>
+__global__ __launch_bounds__(kWThr) void gemm_wide(const XT *__restrict__ x, int64_t ldx,
+                                                  const uint8_t *__restrict__ W, int M, int N,
+                                                  int K, float *__restrict__ y, int64_t ldy,
+                                                  int tiles_m) {
   __shared__ __align__(16) unsigned char lds[4 * kWStB];
   int bid = blockIdx.x;
   if ((gridDim.x & 7) == 0) bid = (bid & 7) * (gridDim.x >> 3) + (bid >> 3);
@@ -1321,37 +1405,37 @@ __global__ __launch_bounds__(kWThr) void gemm_wide_q4k(const XT *__restrict__ x,
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int r = lane & 15, g = lane >> 4;
-  WideQ4K s;
+  Wide<TYPE> s;
   s.lds = lds;
+  s.K = K;
   s.nu = K / 256;
-  s.ts = s.nu * Fmt<12>::TU;
-  const int ntiles = (N + 15) >> 4, t0 = (n0 >> 4) + kWTN * wave;
-  const int nt = __builtin_amdgcn_readfirstlane(max(0, min(kWTN, ntiles - t0)));
-  s.brs = make_rsrc(W + (int64_t)min(t0, ntiles - 1) * s.ts, (uint32_t)__builtin_amdgcn_readfirstlane(nt * s.ts));
-  s.bo = b_offsets<12>(r, g);
+  s.ts = (K / Fmt<TYPE>::UE) * Fmt<TYPE>::TU;
+  const int ntiles = (N + 15) >> 4, t0 = __builtin_amdgcn_readfirstlane((n0 >> 4) + kWTN * wave);
+#pragma unroll
+  for (int j = 0; j < kWTN; ++j)  // tile t0 + j, or none past the weight's end
+    s.brs[j] = make_rsrc(W + (int64_t)min(t0 + j, ntiles - 1) * s.ts, t0 + j < ntiles ? s.ts : 0);
+  s.bo = b_offsets<TYPE>(r, g);
   const int rows = min(kWBM, M - m0);
-  s.ldxb = ldx * (int64_t)sizeof(XT);
-  s.ars = make_rsrc(x + (int64_t)m0 * ldx,
-                    (uint32_t)__builtin_amdgcn_readfirstlane(
-                        (int)((int64_t)(rows - 1) * s.ldxb + (int64_t)K * sizeof(XT))));
+  const int64_t ldxb = ldx * (int64_t)sizeof(XT);
+#pragma unroll
+  for (int i = 0; i < kWAI; ++i) {  // rows m0 + kWAR i .. of which ri exist
+    const int ri = rows - kWAR * i;
+    s.ars[i] = make_rsrc(x + (int64_t)(m0 + min(kWAR * i, rows - 1)) * ldx,
+                         ri > 0 ? (int)((int64_t)(ri - 1) * ldxb + (int64_t)K * sizeof(XT)) : 0);
+  }
   s.row0 = tid >> 3;
   s.cc = tid & 7;
-  s.avoff = (int)(s.row0 * s.ldxb) + s.cc * 16;
+  s.av = (int)(s.row0 * ldxb) + s.cc * 16;
   s.af0 = lds_at(r, g);
   s.af1 = lds_at(r, 4 + g);
 #pragma unroll
   for (int i = 0; i < kWTM; ++i)
 #pragma unroll
     for (int j = 0; j < kWTN; ++j) s.acc[i][j] = float4_t{0.f, 0.f, 0.f, 0.f};
-  // prologue: header of superblock 0, codes of steps 0 and 1, A of steps 0
+  // prologue: header of unit 0 and the codes of its first steps, A of steps 0
   // and 1 into stages 0 and 1, A of step 2 requested
-  s.load_hdr(0);
+  s.prologue();
   s.load_a(0);
-#pragma unroll
-  for (int j = 0; j < kWTN; ++j) {
-    s.load_codes(0, j, 0, 0);
-    s.load_codes(1, j, 0, 1);
-  }
   s.store_a(0);
   s.load_a(64);
   s.store_a(1);
@@ -1380,12 +1464,12 @@ __global__ __launch_bounds__(kWThr) void gemm_wide_q4k(const XT *__restrict__ x,
 template <int TYPE, typename XT>
 hipError_t launch_type(const XT *x, int64_t ldx, const uint8_t *W, int M, int N, int K, float *y,
                        int64_t ldy, float *work, int64_t work_floats, hipStream_t s) {
-  if constexpr (TYPE == 12 && sizeof(XT) == 2) {
-    // Q4_K with fp16 activations on a grid that fills the chip: the wide tile
+  if constexpr ((TYPE == 12 || TYPE == 8) && sizeof(XT) == 2) {
+    // Q4_K / Q8_0 with fp16 activations on a grid that fills the chip: the wide tile
     const int wm = (M + kWBM - 1) / kWBM, wn = (N + kWBN - 1) / kWBN;
-    if ((int64_t)wm * wn >= GGUF_GEMM_WIDE_MIN) {
-      hipLaunchKernelGGL((gemm_wide_q4k<XT>), dim3((unsigned)(wm * wn)), dim3(kWThr), 0, s, x, ldx, W,
-                         M, N, K, y, ldy, wm);
+    if ((int64_t)wm * wn >= GGUF_GEMM_WIDE_MIN && K % 256 == 0) {
+      hipLaunchKernelGGL((gemm_wide<TYPE, XT>), dim3((unsigned)(wm * wn)), dim3(kWThr), 0, s, x,
+                         ldx, W, M, N, K, y, ldy, wm);
       return hipGetLastError();
     }
   }

@@ -504,13 +504,19 @@ def secondary_cases(pkg, args, pool, secondary):
             secondary[f"q4k_decode_m{mm}_down_gbs"] = round(r["gbs"], 1)
         del dpool
     if want("batch_q6q8"):
-        # batched decode of the path's other two types (Q6_K, Q8_0) at the FFN shapes
+        # decode (M = 1, 8, 32) and prefill (M = 2048, f16) of the path's other two types
+        # (Q6_K, Q8_0) at the FFN shapes
         for tt, name in ((14, "q6k"), (8, "q8_0")):
             for (nn, kk), shape in (((14336, 4096), "gate_up"), ((4096, 14336), "down")):
                 bpool, _ = make_pool(pkg, tt, nn, kk, 10, seed=40 + tt)
-                for mm in (8, 32):
+                for mm in (1, 8, 32):
                     r = matmul_case(pkg, tt, mm, nn, kk, bpool, 170, 5, replays=3)
                     secondary[f"{name}_decode_m{mm}_{shape}_gbs"] = round(r["gbs"], 1)
+                if shape == "gate_up":
+                    r = matmul_case(pkg, tt, 2048, nn, kk, bpool[:2], 10, 2, xdtype="float16")
+                    secondary[f"{name}_gemm_m2048_n14336_tflops"] = round(r["tflops"], 1)
+                    secondary[f"{name}_gemm_m2048_n14336_frac_fp16_peak"] = round(
+                        r["tflops"] / FP16_PEAK_TFLOPS, 4)
                 del bpool
     if want("q8"):
         qpool, _ = make_pool(pkg, 8, 4096, 4096, 32, seed=4)
