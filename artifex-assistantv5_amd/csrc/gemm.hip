@@ -1154,10 +1154,11 @@ inline int gemm_splits(int type, int64_t tiles, int nu) {
 }
 
 // ---------------------------------------------------------------------------
-// Wide-tile GEMM for large grids (Q4_K and Q8_0, fp16 activations, K a
-// multiple of 256).  A workgroup of 8 waves owns a 128 x 512 output tile; wave
-// w owns all 128 rows and the 64 columns [64 w, 64 w + 64) (four row tiles of
-// the weight): 32 accumulator tiles, 255 VGPRs, two waves per SIMD.  Against gemm_kernel's 128 x 32 per
+// Wide-tile GEMM for large grids (Q4_K, Q8_0 and Q6_K, fp16 activations, K a
+// multiple of 256).  A workgroup of 8 waves owns a 128 x 512 output tile (Q6_K
+// 128 x 384); wave w owns all 128 rows and the 64 columns [64 w, 64 w + 64)
+// (four row tiles of the weight; Q6_K three): 32 accumulator tiles, 255
+// VGPRs, two waves per SIMD.  Against gemm_kernel's 128 x 32 per
 // wave, each activation fragment read from LDS feeds twice the MFMAs and a
 // step holds twice the MFMA work per barrier; each dequantized B operand
 // still feeds 8 MFMAs.
@@ -1191,12 +1192,31 @@ inline int gemm_splits(int type, int64_t tiles, int nu) {
 //     against 865-869 at M = 2048, 1-2% slower at M = 8192.
 //   - Q8_0 on it (bit-identical to gemm_kernel): 702 -> 820 TFLOP/s at
 //     M = 2048, N = 14336; 803 -> 1025 at M = 8192, N = 4096, K = 14336.
-//   - Q6_K on it was bit-identical and slower (678 -> 624, 811 -> 729): its 6
-//     quant dwords per tile and half superblock leave no room for a second
-//     set (one step ahead instead of two) and still spill 31 dwords.
+//   - Q6_K runs 3 tiles per wave (128 x 384 per workgroup, 242 VGPRs, two code
+//     sets three steps ahead): 676 -> 699 TFLOP/s at M = 2048, N = 14336;
+//     809 -> 877 at M = 8192, N = 4096, K = 14336; 800 -> 882 at M = 8192,
+//     N = 14336 (bit-identical to gemm_kernel).  At 4 tiles per wave its 6
+//     quant dwords per tile and half superblock left room for one set only
+//     (one step ahead) and still spilled 31 dwords: 678 -> 624, 811 -> 729.
 // ---------------------------------------------------------------------------
-constexpr int kWW = 8, kWTN = 4, kWTM = 8;
-constexpr int kWBM = 16 * kWTM, kWBN = 16 * kWTN * kWW;
+constexpr int kWW = 8, kWTM = 8;
+// weight row tiles per wave: 4 (a 128 x 512 workgroup tile); Q6_K 3 (128 x 384), whose
+// quant words need the registers of a fourth tile's accumulators
+template <int TYPE>
+constexpr int wide_tn() {
+  return TYPE == 14 ? 3 : 4;
+}
+template <int TYPE>
+constexpr int wide_bn() {
+  return 16 * wide_tn<TYPE>() * kWW;
+}
+// the grid (in workgroups) from which the wide tile runs: Q6_K from two full
+// rounds of the chip (M = 1024, N = 14336: 304 workgroups, 611 -> 551 TFLOP/s)
+template <int TYPE>
+constexpr int wide_min() {
+  return TYPE == 14 ? 512 : GGUF_GEMM_WIDE_MIN;
+}
+constexpr int kWBM = 16 * kWTM;
 constexpr int kWThr = 64 * kWW;
 constexpr int kWAI = kWBM * 8 / kWThr;  // 16-byte activation chunks a thread stages per step
 constexpr int kWAR = kWThr / 8;         // row distance between them
@@ -1219,6 +1239,7 @@ struct WB;
 // steps ahead; the header of unit u + 1 is requested at step 2 of unit u.
 template <>
 struct WB<12> {
+  static constexpr int kWTN = wide_tn<12>();
   rsrc_t brs[kWTN];
   int ts, nu;
   BOff bo;
@@ -1285,6 +1306,7 @@ struct WB<12> {
 // their codes and d for the steps of parity P, requested two steps ahead.
 template <>
 struct WB<8> {
+  static constexpr int kWTN = wide_tn<8>();
   rsrc_t brs[kWTN];
   int ts, nu;
   BOff bo;
@@ -1332,8 +1354,93 @@ struct WB<8> {
   }
 };
 
+// Q6_K: steps 2 HF and 2 HF + 1 of a unit use the same 6 quant dwords of half
+// HF (set HF), requested for unit u + 1 once step 2 HF + 1 of unit u has built
+// the tile's operands (three steps ahead).  The step's scale dword (4 of the 16
+// int8 scales) is requested two steps ahead with set P of the steps of parity
+// P, the d of unit u + 1 at step 2 of unit u.  The lane's operand for k-half t2
+// holds the window columns 32 t2 + 16 lh + 4 g + e at position 4 lh + e (the
+// activations are staged in that order).
+template <>
+struct WB<14> {
+  static constexpr int kWTN = wide_tn<14>();
+  rsrc_t brs[kWTN];
+  int ts, nu;
+  BOff bo;
+  uint32_t dq[2][kWTN][6];  // half HF: dwords 3 lh + i (i = 0, 1 low bits, 2 high bits)
+  uint32_t scq[2][kWTN];    // scale dword of the steps of parity P
+  uint32_t hd[kWTN];        // d of the next unit
+  float d[kWTN];            // d of the current unit
+
+  // half HF's dwords 6 HF .. 6 HF + 5 of the lane's 12, from pieces of 16 bytes
+  __device__ __forceinline__ void load_half(int hf, int j, int u) {
+    const int su = u * Fmt<14>::TU;
+    if (hf == 0) {
+      const uint4 a = bl16(brs[j], bo.v0, su);
+      const uint2 b = bl8(brs[j], bo.v0, su + 1024);
+      dq[0][j][0] = a.x; dq[0][j][1] = a.y; dq[0][j][2] = a.z;
+      dq[0][j][3] = a.w; dq[0][j][4] = b.x; dq[0][j][5] = b.y;
+    } else {
+      const uint2 a = bl8(brs[j], bo.v0, su + 1024 + 8);
+      const uint4 b = bl16(brs[j], bo.v0, su + 2048);
+      dq[1][j][0] = a.x; dq[1][j][1] = a.y; dq[1][j][2] = b.x;
+      dq[1][j][3] = b.y; dq[1][j][4] = b.z; dq[1][j][5] = b.w;
+    }
+  }
+  __device__ __forceinline__ void load_scale(int set, int j, int u, int c) {
+    scq[set][j] = bl4(brs[j], bo.v2, u * Fmt<14>::TU + 4 * c);
+  }
+  __device__ __forceinline__ void load_d(int u) {
+#pragma unroll
+    for (int j = 0; j < kWTN; ++j) hd[j] = bl2(brs[j], bo.v1, u * Fmt<14>::TU);
+  }
+  __device__ __forceinline__ void prologue() {
+    load_d(0);
+#pragma unroll
+    for (int j = 0; j < kWTN; ++j) {
+      load_half(0, j, 0);
+      load_half(1, j, 0);
+      load_scale(0, j, 0, 0);
+      load_scale(1, j, 0, 1);
+    }
+  }
+  template <int C>
+  __device__ __forceinline__ void begin(int u) {
+    if (C == 2) load_d(min(u + 1, nu - 1));
+  }
+  template <int C>
+  __device__ __forceinline__ void done(int j, int u) {
+    const int s2 = 4 * u + C + 2;
+    load_scale(C & 1, j, min(s2 >> 2, nu - 1), (C + 2) & 3);
+    if (C & 1) load_half(C >> 1, j, min(u + 1, nu - 1));
+  }
+  __device__ __forceinline__ void set_cur() {
+#pragma unroll
+    for (int j = 0; j < kWTN; ++j) d[j] = h2f(hd[j]);
+  }
+  template <int C, int H>
+  __device__ __forceinline__ half8_t bop(int j) const {
+    constexpr int HF = C >> 1, TP = C & 1, t = 2 * TP + H;
+    const uint32_t scw = scq[C & 1][j];
+    uint32_t v[4];
+#pragma unroll
+    for (int lh = 0; lh < 2; ++lh) {
+      const uint32_t ql = dq[HF][j][3 * lh + (t & 1)], qh = dq[HF][j][3 * lh + 2];
+      const uint32_t n4 = (t >> 1) ? ((ql >> 4) & 0x0F0F0F0Fu) : (ql & 0x0F0F0F0Fu);
+      const uint32_t q6 = n4 | (((qh >> (2 * t)) & 0x03030303u) << 4);
+      const uint32_t ev = q6 & 0x00FF00FFu, od = (q6 >> 8) & 0x00FF00FFu;
+      const float sv = d[j] * (float)(int8_t)((scw >> (8 * (2 * H + lh))) & 0xFFu);
+      const float s = sv * kTwo24, c = -32.0f * sv;
+      v[2 * lh] = mix_lo(ev, od, s, c);
+      v[2 * lh + 1] = mix_hi(ev, od, s, c);
+    }
+    return h8(v[0], v[1], v[2], v[3]);
+  }
+};
+
 template <int TYPE>
 struct Wide : WB<TYPE> {
+  static constexpr int kWTN = wide_tn<TYPE>();
   rsrc_t ars[kWAI];  // rows m0 + kWAR i + (0 .. kWAR - 1)
   int av, row0, cc, K, af0, af1;
   uint4 ar[kWAI];
@@ -1350,7 +1457,18 @@ struct Wide : WB<TYPE> {
   __device__ __forceinline__ void store_a(int stage) {
     unsigned char *base = lds + stage * kWStB;
 #pragma unroll
-    for (int i = 0; i < kWAI; ++i) *(uint4 *)(base + lds_at(row0 + kWAR * i, cc)) = ar[i];
+    for (int i = 0; i < kWAI; ++i) {
+      const int row = row0 + kWAR * i;
+      if constexpr (TYPE == 14) {
+        // columns 8 q + e (q = cc & 3) of k-block cc >> 2 go to position
+        // 8 g + 4 lh + (e & 3) with g = 2 (q & 1) + (e >> 2), lh = q >> 1
+        const int q = cc & 3, ch = 4 * (cc >> 2) + 2 * (q & 1), half = 8 * (q >> 1);
+        *(uint2 *)(base + lds_at(row, ch) + half) = make_uint2(ar[i].x, ar[i].y);
+        *(uint2 *)(base + lds_at(row, ch + 1) + half) = make_uint2(ar[i].z, ar[i].w);
+      } else {
+        *(uint4 *)(base + lds_at(row, cc)) = ar[i];
+      }
+    }
   }
 
   // step s = 4 u + C: A from stage s & 3 (= C).  First the A of step s + 2
@@ -1391,6 +1509,7 @@ __global__ __launch_bounds__(kWThr) void gemm_wide(const XT *__restrict__ x, int
                                                   const uint8_t *__restrict__ W, int M, int N,
                                                   int K, float *__restrict__ y, int64_t ldy,
                                                   int tiles_m) {
+  constexpr int kWTN = wide_tn<TYPE>();
   __shared__ __align__(16) unsigned char lds[4 * kWStB];
   int bid = blockIdx.x;
   if ((gridDim.x & 7) == 0) bid = (bid & 7) * (gridDim.x >> 3) + (bid >> 3);
@@ -1400,7 +1519,7 @@ __global__ __launch_bounds__(kWThr) void gemm_wide(const XT *__restrict__ x, int
     const int tiles_n = (int)gridDim.x / tiles_m;
     const int gn = min(GGUF_GEMM_GN, tiles_n - band * GGUF_GEMM_GN);
     m0 = (in / gn) * kWBM;
-    n0 = (band * GGUF_GEMM_GN + in % gn) * kWBN;
+    n0 = (band * GGUF_GEMM_GN + in % gn) * wide_bn<TYPE>();
   }
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -1464,10 +1583,10 @@ __global__ __launch_bounds__(kWThr) void gemm_wide(const XT *__restrict__ x, int
 template <int TYPE, typename XT>
 hipError_t launch_type(const XT *x, int64_t ldx, const uint8_t *W, int M, int N, int K, float *y,
                        int64_t ldy, float *work, int64_t work_floats, hipStream_t s) {
-  if constexpr ((TYPE == 12 || TYPE == 8) && sizeof(XT) == 2) {
-    // Q4_K / Q8_0 with fp16 activations on a grid that fills the chip: the wide tile
-    const int wm = (M + kWBM - 1) / kWBM, wn = (N + kWBN - 1) / kWBN;
-    if ((int64_t)wm * wn >= GGUF_GEMM_WIDE_MIN && K % 256 == 0) {
+  if constexpr ((TYPE == 12 || TYPE == 8 || TYPE == 14) && sizeof(XT) == 2) {
+    // Q4_K / Q8_0 / Q6_K with fp16 activations on a grid that fills the chip: the wide tile
+    const int wm = (M + kWBM - 1) / kWBM, wn = (N + wide_bn<TYPE>() - 1) / wide_bn<TYPE>();
+    if ((int64_t)wm * wn >= wide_min<TYPE>() && K % 256 == 0) {
       hipLaunchKernelGGL((gemm_wide<TYPE, XT>), dim3((unsigned)(wm * wn)), dim3(kWThr), 0, s, x,
                          ldx, W, M, N, K, y, ldy, wm);
       return hipGetLastError();

@@ -310,14 +310,17 @@ def test_full_size_configs(pkg, t, m, n, k, xdt):
     _gpu_check(y, x.float(), w.dequant().view(n, k), (t, m, n, k))
 
 
-@pytest.mark.parametrize("t", [12, 8])
-@pytest.mark.parametrize("m,n,k", [(1000, 14000, 4096), (777, 29000, 1536), (2100, 8200, 4096)])
+@pytest.mark.parametrize("t,m,n,k", [(12, 1000, 14000, 4096), (12, 777, 29000, 1536),
+                                     (12, 2100, 8200, 4096), (8, 1000, 14000, 4096),
+                                     (8, 777, 29000, 1536), (8, 2100, 8200, 4096),
+                                     (14, 2100, 14000, 1536), (14, 1500, 29000, 1536)])
 def test_wide_gemm_ragged(pkg, t, m, n, k):
-    """Q4_K and Q8_0 prefill with fp16 activations on grids of at least 192
-    128 x 512 tiles takes the wide-tile GEMM: rows past M in the last row tile,
-    a last workgroup with fewer than 32 weight row tiles, N not a multiple of 16
-    and a K of 6 superblocks, against the f64 product of the dequantized
-    weights; a second call gives the same bits."""
+    """Q4_K, Q8_0 and Q6_K prefill with fp16 activations on grids large enough
+    for the wide-tile GEMM (192 tiles of 128 x 512; Q6_K 512 of 128 x 384):
+    rows past M in the last row tile, a last workgroup with fewer weight row
+    tiles than the others, N not a multiple of 16 and a K of 6 superblocks,
+    against the f64 product of the dequantized weights; a second call gives
+    the same bits."""
     g = torch.Generator(device="cuda").manual_seed(m + n + k + t)
     wf = torch.randn(n, k, device="cuda", generator=g) * 0.02
     raw = pkg.quantize.quantize(wf.cpu().numpy(), t)
@@ -328,14 +331,15 @@ def test_wide_gemm_ragged(pkg, t, m, n, k):
     assert torch.equal(pkg.qlinear(x, w), y)
 
 
-@pytest.mark.parametrize("t,k", [(12, 4096), (8, 4096), (8, 1568)])
-def test_wide_gemm_equals_gemm_kernel_rows(pkg, t, k):
-    """The wide-tile GEMM (1280 rows: 280 tiles of 128 x 512) and gemm_kernel
-    (a slice of 128 rows: 56 tiles of 128 x 256, no workspace, so no K split)
-    run each output element's MFMAs in the same k order: the same bits.  A
-    Q8_0 K that is not a multiple of 256 keeps gemm_kernel for the whole
-    call."""
-    m, n = 1280, 14336
+@pytest.mark.parametrize("t,m,k", [(12, 1280, 4096), (8, 1280, 4096), (8, 1280, 1568),
+                                   (14, 2048, 4096)])
+def test_wide_gemm_equals_gemm_kernel_rows(pkg, t, m, k):
+    """The wide-tile GEMM (1280 rows: 280 tiles of 128 x 512; Q6_K 2048 rows:
+    608 tiles of 128 x 384) and gemm_kernel (a slice of 128 rows: 56 tiles of
+    128 x 256, no workspace, so no K split) run each output element's MFMAs in
+    the same k order: the same bits.  A Q8_0 K that is not a multiple of 256
+    keeps gemm_kernel for the whole call."""
+    n = 14336
     raw, w = _case(pkg, t, n, k, seed=t + k)
     g = torch.Generator(device="cuda").manual_seed(k)
     x = torch.randn(m, k, device="cuda", generator=g).half()
@@ -349,7 +353,7 @@ def test_wide_gemm_equals_gemm_kernel_rows(pkg, t, k):
         assert rc == 0, lib.gguf_hip_last_error()
         return y
     y = gemm(x)
-    for m0 in (0, 640, 1152):
+    for m0 in (0, 640, m - 128):
         assert torch.equal(gemm(x[m0:m0 + 128].contiguous()), y[m0:m0 + 128]), m0
 
 
