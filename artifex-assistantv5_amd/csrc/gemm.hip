@@ -1154,11 +1154,11 @@ inline int gemm_splits(int type, int64_t tiles, int nu) {
 }
 
 // ---------------------------------------------------------------------------
-// Wide-tile GEMM for large grids (Q4_K, Q8_0 and Q6_K, fp16 activations, K a
-// multiple of 256).  A workgroup of 8 waves owns a 128 x 512 output tile (Q6_K
-// 128 x 384); wave w owns all 128 rows and the 64 columns [64 w, 64 w + 64)
-// (four row tiles of the weight; Q6_K three): 32 accumulator tiles, 255
-// VGPRs, two waves per SIMD.  Against gemm_kernel's 128 x 32 per
+// Wide-tile GEMM for large grids (Q4_K, Q8_0, Q6_K and Q5_K, fp16 activations,
+// K a multiple of 256).  A workgroup of 8 waves owns a 128 x 512 output tile
+// (Q6_K, Q5_K 128 x 384); wave w owns all 128 rows and the 64 columns
+// [64 w, 64 w + 64) (four row tiles of the weight; Q6_K, Q5_K three): 32
+// accumulator tiles, 255 VGPRs, two waves per SIMD.  Against gemm_kernel's 128 x 32 per
 // wave, each activation fragment read from LDS feeds twice the MFMAs and a
 // step holds twice the MFMA work per barrier; each dequantized B operand
 // still feeds 8 MFMAs.
@@ -1198,13 +1198,15 @@ inline int gemm_splits(int type, int64_t tiles, int nu) {
 //     N = 14336 (bit-identical to gemm_kernel).  At 4 tiles per wave its 6
 //     quant dwords per tile and half superblock left room for one set only
 //     (one step ahead) and still spilled 31 dwords: 678 -> 624, 811 -> 729.
+//   - Q5_K at 3 tiles per wave (222 VGPRs; 4 spilled 30 dwords): 703 -> 737
+//     at M = 2048, 844 -> 920 at M = 8192 (bit-identical to gemm_kernel).
 // ---------------------------------------------------------------------------
 constexpr int kWW = 8, kWTM = 8;
 // weight row tiles per wave: 4 (a 128 x 512 workgroup tile); Q6_K 3 (128 x 384), whose
 // quant words need the registers of a fourth tile's accumulators
 template <int TYPE>
 constexpr int wide_tn() {
-  return TYPE == 14 ? 3 : 4;
+  return TYPE == 14 || TYPE == 13 ? 3 : 4;
 }
 template <int TYPE>
 constexpr int wide_bn() {
@@ -1214,7 +1216,7 @@ constexpr int wide_bn() {
 // rounds of the chip (M = 1024, N = 14336: 304 workgroups, 611 -> 551 TFLOP/s)
 template <int TYPE>
 constexpr int wide_min() {
-  return TYPE == 14 ? 512 : GGUF_GEMM_WIDE_MIN;
+  return TYPE == 14 || TYPE == 13 ? 512 : GGUF_GEMM_WIDE_MIN;
 }
 constexpr int kWBM = 16 * kWTM;
 constexpr int kWThr = 64 * kWW;
@@ -1295,6 +1297,77 @@ struct WB<12> {
     for (int w = 0; w < 2; ++w) {
       const uint32_t q = w ? q2.y : q2.x, q8 = q >> 8;
       const uint32_t e = q & m, o = q8 & m;
+      v[2 * w] = mix_lo(e, o, s, c);
+      v[2 * w + 1] = mix_hi(e, o, s, c);
+    }
+    return h8(v[0], v[1], v[2], v[3]);
+  }
+};
+
+// Q5_K: Q4_K's codes and header, and the lane's 8 bytes of fifth bits (every
+// window's) with the header; they are ORed into the nibbles as gemm_kernel does.
+template <>
+struct WB<13> {
+  static constexpr int kWTN = wide_tn<13>();
+  rsrc_t brs[kWTN];
+  int ts, nu;
+  BOff bo;
+  uint2 cq[2][kWTN];
+  uint4 hd[kWTN];
+  uint2 hqh[kWTN], qh[kWTN];
+  uint32_t sc[kWTN][2], mn[kWTN][2];
+  float d24[kWTN], dmin[kWTN];
+
+  __device__ __forceinline__ void load_codes(int set, int j, int u, int c) {
+    cq[set][j] = bl8(brs[j], bo.v1, u * Fmt<13>::TU + (c >> 1) * 1024 + 8 * (c & 1));
+  }
+  __device__ __forceinline__ void load_hdr(int u) {
+#pragma unroll
+    for (int j = 0; j < kWTN; ++j) {
+      hd[j] = bl16(brs[j], bo.v0, u * Fmt<13>::TU);
+      hqh[j] = bl8(brs[j], bo.v2, u * Fmt<13>::TU);
+    }
+  }
+  __device__ __forceinline__ void prologue() {
+    load_hdr(0);
+#pragma unroll
+    for (int j = 0; j < kWTN; ++j) {
+      load_codes(0, j, 0, 0);
+      load_codes(1, j, 0, 1);
+    }
+  }
+  template <int C>
+  __device__ __forceinline__ void begin(int u) {
+    if (C == 2) load_hdr(min(u + 1, nu - 1));
+  }
+  template <int C>
+  __device__ __forceinline__ void done(int j, int u) {
+    const int s2 = 4 * u + C + 2;
+    load_codes(C & 1, j, min(s2 >> 2, nu - 1), (C + 2) & 3);
+  }
+  __device__ __forceinline__ void set_cur() {
+#pragma unroll
+    for (int j = 0; j < kWTN; ++j) {
+      q4k_scales_packed(hd[j].y, hd[j].z, hd[j].w, sc[j][0], sc[j][1], mn[j][0], mn[j][1]);
+      const float d = h2f(hd[j].x);
+      d24[j] = d * kTwo24;
+      dmin[j] = h2f(hd[j].x >> 16);
+      qh[j] = hqh[j];
+    }
+  }
+  template <int C, int H>
+  __device__ __forceinline__ half8_t bop(int j) const {
+    constexpr int Wd = C >> 1, B0 = ((2 * C) & 3) + H;
+    const float s = (H ? d24[j] * 0.0625f : d24[j]) * ubyte(sc[j][Wd], B0),
+                c = -(dmin[j] * ubyte(mn[j][Wd], B0));
+    constexpr uint32_t m = H ? 0x00F000F0u : 0x000F000Fu;
+    const uint2 q2 = cq[C & 1][j];
+    uint32_t v[4];
+#pragma unroll
+    for (int w = 0; w < 2; ++w) {
+      const uint32_t q = w ? q2.y : q2.x, q8 = q >> 8, hb = w ? qh[j].y : qh[j].x;
+      const uint32_t e = (q & m) | (H ? q5k_hi_even(hb, C) : q5k_lo_even(hb, C));
+      const uint32_t o = (q8 & m) | (H ? q5k_hi_odd(hb, C) : q5k_lo_odd(hb, C));
       v[2 * w] = mix_lo(e, o, s, c);
       v[2 * w + 1] = mix_hi(e, o, s, c);
     }
@@ -1583,8 +1656,8 @@ __global__ __launch_bounds__(kWThr) void gemm_wide(const XT *__restrict__ x, int
 template <int TYPE, typename XT>
 hipError_t launch_type(const XT *x, int64_t ldx, const uint8_t *W, int M, int N, int K, float *y,
                        int64_t ldy, float *work, int64_t work_floats, hipStream_t s) {
-  if constexpr ((TYPE == 12 || TYPE == 8 || TYPE == 14) && sizeof(XT) == 2) {
-    // Q4_K / Q8_0 / Q6_K with fp16 activations on a grid that fills the chip: the wide tile
+  if constexpr ((TYPE == 12 || TYPE == 8 || TYPE == 14 || TYPE == 13) && sizeof(XT) == 2) {
+    // Q4_K / Q8_0 / Q6_K / Q5_K with fp16 activations on a grid that fills the chip: the wide tile
     const int wm = (M + kWBM - 1) / kWBM, wn = (N + wide_bn<TYPE>() - 1) / wide_bn<TYPE>();
     if ((int64_t)wm * wn >= wide_min<TYPE>() && K % 256 == 0) {
       hipLaunchKernelGGL((gemm_wide<TYPE, XT>), dim3((unsigned)(wm * wn)), dim3(kWThr), 0, s, x,
