@@ -1154,11 +1154,11 @@ inline int gemm_splits(int type, int64_t tiles, int nu) {
 }
 
 // ---------------------------------------------------------------------------
-// Wide-tile GEMM for large grids (Q4_K, Q8_0, Q6_K and Q5_K, fp16 activations,
-// K a multiple of 256).  A workgroup of 8 waves owns a 128 x 512 output tile
-// (Q6_K, Q5_K 128 x 384); wave w owns all 128 rows and the 64 columns
-// [64 w, 64 w + 64) (four row tiles of the weight; Q6_K, Q5_K three): 32
-// accumulator tiles, 255 VGPRs, two waves per SIMD.  Against gemm_kernel's 128 x 32 per
+// Wide-tile GEMM for large grids (Q4_K, Q8_0, Q6_K, Q5_K, Q3_K, Q2_K and
+// IQ4_XS, fp16 activations, K a multiple of 256).  A workgroup of 8 waves owns a
+// 128 x 512 output tile (Q6_K, Q5_K, Q3_K 128 x 384); wave w owns all 128 rows
+// and the 64 columns [64 w, 64 w + 64) (four row tiles of the weight; Q6_K,
+// Q5_K, Q3_K three): 32 accumulator tiles, 255 VGPRs, two waves per SIMD.  Against gemm_kernel's 128 x 32 per
 // wave, each activation fragment read from LDS feeds twice the MFMAs and a
 // step holds twice the MFMA work per barrier; each dequantized B operand
 // still feeds 8 MFMAs.
@@ -1200,13 +1200,18 @@ inline int gemm_splits(int type, int64_t tiles, int nu) {
 //     (one step ahead) and still spilled 31 dwords: 678 -> 624, 811 -> 729.
 //   - Q5_K at 3 tiles per wave (222 VGPRs; 4 spilled 30 dwords): 703 -> 737
 //     at M = 2048, 844 -> 920 at M = 8192 (bit-identical to gemm_kernel).
+//   - Q2_K (4 tiles, 256 VGPRs): 751 -> 848 at M = 2048, 897 -> 1032 at
+//     M = 8192 (3 tiles: 785 / 973).  Q3_K (3 tiles, 226 VGPRs): 681 -> 715,
+//     829 -> 896.  IQ4_XS (4 tiles, 254 VGPRs): 671 -> 742, 797 -> 896.  All
+//     bit-identical to gemm_kernel.
 // ---------------------------------------------------------------------------
 constexpr int kWW = 8, kWTM = 8;
-// weight row tiles per wave: 4 (a 128 x 512 workgroup tile); Q6_K 3 (128 x 384), whose
-// quant words need the registers of a fourth tile's accumulators
+// weight row tiles per wave: 4 (a 128 x 512 workgroup tile); Q6_K, Q5_K and Q3_K 3
+// (128 x 384), whose quant and header words need the registers of a fourth tile's
+// accumulators
 template <int TYPE>
 constexpr int wide_tn() {
-  return TYPE == 14 || TYPE == 13 ? 3 : 4;
+  return TYPE == 14 || TYPE == 13 || TYPE == 11 ? 3 : 4;
 }
 template <int TYPE>
 constexpr int wide_bn() {
@@ -1216,7 +1221,12 @@ constexpr int wide_bn() {
 // rounds of the chip (M = 1024, N = 14336: 304 workgroups, 611 -> 551 TFLOP/s)
 template <int TYPE>
 constexpr int wide_min() {
-  return TYPE == 14 || TYPE == 13 ? 512 : GGUF_GEMM_WIDE_MIN;
+  return wide_tn<TYPE>() == 3 ? 512 : GGUF_GEMM_WIDE_MIN;
+}
+template <int TYPE>
+constexpr bool has_wide() {
+  return TYPE == 12 || TYPE == 8 || TYPE == 14 || TYPE == 13 || TYPE == 10 || TYPE == 11 ||
+         TYPE == 23;
 }
 constexpr int kWBM = 16 * kWTM;
 constexpr int kWThr = 64 * kWW;
@@ -1372,6 +1382,194 @@ struct WB<13> {
       v[2 * w + 1] = mix_hi(e, o, s, c);
     }
     return h8(v[0], v[1], v[2], v[3]);
+  }
+};
+
+// Q2_K: the step's 8 qs bytes of half c >> 1 (windows 2c, 2c + 1 take bit
+// pairs 2 (w & 3) of them); the header (16 scale bytes, d | dmin << 16).  The
+// lane's 8 k of a window lie in scale group 2 w + (g >> 1).
+template <>
+struct WB<10> {
+  static constexpr int kWTN = wide_tn<10>();
+  rsrc_t brs[kWTN];
+  int ts, nu, lg;
+  BOff bo;
+  uint2 cq[2][kWTN];
+  uint4 hsc[kWTN], sc[kWTN];
+  uint32_t hdm[kWTN];
+  float d24[kWTN], dmin[kWTN];
+
+  __device__ __forceinline__ void load_codes(int set, int j, int u, int c) {
+    cq[set][j] = bl8(brs[j], bo.v0, u * Fmt<10>::TU + 8 * (c >> 1));
+  }
+  __device__ __forceinline__ void load_hdr(int u) {
+#pragma unroll
+    for (int j = 0; j < kWTN; ++j) {
+      hsc[j] = bl16(brs[j], bo.v1, u * Fmt<10>::TU);
+      hdm[j] = bl4(brs[j], bo.v2, u * Fmt<10>::TU);
+    }
+  }
+  __device__ __forceinline__ void prologue() {
+    load_hdr(0);
+#pragma unroll
+    for (int j = 0; j < kWTN; ++j) {
+      load_codes(0, j, 0, 0);
+      load_codes(1, j, 0, 1);
+    }
+  }
+  template <int C>
+  __device__ __forceinline__ void begin(int u) {
+    if (C == 2) load_hdr(min(u + 1, nu - 1));
+  }
+  template <int C>
+  __device__ __forceinline__ void done(int j, int u) {
+    const int s2 = 4 * u + C + 2;
+    load_codes(C & 1, j, min(s2 >> 2, nu - 1), (C + 2) & 3);
+  }
+  __device__ __forceinline__ void set_cur() {
+#pragma unroll
+    for (int j = 0; j < kWTN; ++j) {
+      sc[j] = hsc[j];
+      d24[j] = h2f(hdm[j]) * kTwo24;
+      dmin[j] = h2f(hdm[j] >> 16);
+    }
+  }
+  template <int C, int H>
+  __device__ __forceinline__ half8_t bop(int j) const {
+    constexpr int w = 2 * C + H, sh = 2 * (w & 3);
+    const uint32_t scw = (w >> 1) == 0 ? sc[j].x : (w >> 1) == 1 ? sc[j].y : (w >> 1) == 2 ? sc[j].z : sc[j].w;
+    const uint32_t sb = (scw >> (8 * (2 * (w & 1) + (lg >> 1)))) & 0xFFu;
+    const float s = d24[j] * (float)(sb & 15u), c = -(dmin[j] * (float)(sb >> 4));
+    const uint2 q2 = cq[C & 1][j];
+    const uint32_t t0 = (q2.x >> sh) & 0x03030303u, t1 = (q2.y >> sh) & 0x03030303u;
+    const uint32_t e0 = t0 & 0x00FF00FFu, o0 = (t0 >> 8) & 0x00FF00FFu;
+    const uint32_t e1 = t1 & 0x00FF00FFu, o1 = (t1 >> 8) & 0x00FF00FFu;
+    return h8(mix_lo(e0, o0, s, c), mix_hi(e0, o0, s, c), mix_lo(e1, o1, s, c), mix_hi(e1, o1, s, c));
+  }
+};
+
+// Q3_K: as Q2_K, codes q3 = low bits | hmask bit 4 (c >> 1) + (w & 3) << 2,
+// value d (sc - 32) (q3 - 4); the header (12 scale bytes, d, the lane's hmask
+// bytes 8 g .. 8 g + 7).
+template <>
+struct WB<11> {
+  static constexpr int kWTN = wide_tn<11>();
+  rsrc_t brs[kWTN];
+  int ts, nu, lg;
+  BOff bo;
+  uint2 cq[2][kWTN];
+  uint32_t hs[kWTN][3], hd[kWTN];
+  uint2 hhm[kWTN], hm[kWTN];
+  uint32_t S[kWTN][4];
+  float d[kWTN];
+
+  __device__ __forceinline__ void load_codes(int set, int j, int u, int c) {
+    cq[set][j] = bl8(brs[j], bo.v0, u * Fmt<11>::TU + 8 * (c >> 1));
+  }
+  __device__ __forceinline__ void load_hdr(int u) {
+#pragma unroll
+    for (int j = 0; j < kWTN; ++j) {
+      const int su = u * Fmt<11>::TU;
+      hs[j][0] = bl4(brs[j], bo.v1, su);
+      hs[j][1] = bl4(brs[j], bo.v1 + 4, su);
+      hs[j][2] = bl4(brs[j], bo.v1 + 8, su);
+      hd[j] = bl2(brs[j], bo.v2, su);
+      hhm[j] = bl8(brs[j], bo.v3, su);
+    }
+  }
+  __device__ __forceinline__ void prologue() {
+    load_hdr(0);
+#pragma unroll
+    for (int j = 0; j < kWTN; ++j) {
+      load_codes(0, j, 0, 0);
+      load_codes(1, j, 0, 1);
+    }
+  }
+  template <int C>
+  __device__ __forceinline__ void begin(int u) {
+    if (C == 2) load_hdr(min(u + 1, nu - 1));
+  }
+  template <int C>
+  __device__ __forceinline__ void done(int j, int u) {
+    const int s2 = 4 * u + C + 2;
+    load_codes(C & 1, j, min(s2 >> 2, nu - 1), (C + 2) & 3);
+  }
+  __device__ __forceinline__ void set_cur() {
+#pragma unroll
+    for (int j = 0; j < kWTN; ++j) {
+      q3k_scales(hs[j][0], hs[j][1], hs[j][2], S[j]);
+      d[j] = h2f(hd[j]);
+      hm[j] = hhm[j];
+    }
+  }
+  template <int C, int H>
+  __device__ __forceinline__ half8_t bop(int j) const {
+    constexpr int w = 2 * C + H, jj = w & 3, hh = w >> 2;
+    const uint32_t sb = (S[j][w >> 1] >> (8 * (2 * (w & 1) + (lg >> 1)))) & 0xFFu;
+    const float dl = d[j] * (float)((int)sb - 32);
+    const float s = dl * kTwo24, c = -4.0f * dl;
+    const uint2 q2 = cq[C & 1][j];
+    const uint32_t t0 = ((q2.x >> (2 * jj)) & 0x03030303u) | (((hm[j].x >> (4 * hh + jj)) & 0x01010101u) << 2);
+    const uint32_t t1 = ((q2.y >> (2 * jj)) & 0x03030303u) | (((hm[j].y >> (4 * hh + jj)) & 0x01010101u) << 2);
+    const uint32_t e0 = t0 & 0x00FF00FFu, o0 = (t0 >> 8) & 0x00FF00FFu;
+    const uint32_t e1 = t1 & 0x00FF00FFu, o1 = (t1 >> 8) & 0x00FF00FFu;
+    return h8(mix_lo(e0, o0, s, c), mix_hi(e0, o0, s, c), mix_lo(e1, o1, s, c), mix_hi(e1, o1, s, c));
+  }
+};
+
+// IQ4_XS: step c is sub-blocks 2c, 2c + 1 (the lane's code words, one each),
+// each an IQ4_NL block with scale d (ls - 32); the header (d | scales_h << 16,
+// scales_l[4]).
+template <>
+struct WB<23> {
+  static constexpr int kWTN = wide_tn<23>();
+  rsrc_t brs[kWTN];
+  int ts, nu;
+  BOff bo;
+  uint2 cq[2][kWTN];
+  uint2 hhd[kWTN], hd[kWTN];
+  float d[kWTN];
+
+  __device__ __forceinline__ void load_codes(int set, int j, int u, int c) {
+    cq[set][j] = bl8(brs[j], bo.v1, u * Fmt<23>::TU + 8 * c);
+  }
+  __device__ __forceinline__ void load_hdr(int u) {
+#pragma unroll
+    for (int j = 0; j < kWTN; ++j) hhd[j] = bl8(brs[j], bo.v0, u * Fmt<23>::TU);
+  }
+  __device__ __forceinline__ void prologue() {
+    load_hdr(0);
+#pragma unroll
+    for (int j = 0; j < kWTN; ++j) {
+      load_codes(0, j, 0, 0);
+      load_codes(1, j, 0, 1);
+    }
+  }
+  template <int C>
+  __device__ __forceinline__ void begin(int u) {
+    if (C == 2) load_hdr(min(u + 1, nu - 1));
+  }
+  template <int C>
+  __device__ __forceinline__ void done(int j, int u) {
+    const int s2 = 4 * u + C + 2;
+    load_codes(C & 1, j, min(s2 >> 2, nu - 1), (C + 2) & 3);
+  }
+  __device__ __forceinline__ void set_cur() {
+#pragma unroll
+    for (int j = 0; j < kWTN; ++j) {
+      hd[j] = hhd[j];
+      d[j] = h2f(hhd[j].x);
+    }
+  }
+  template <int C, int H>
+  __device__ __forceinline__ half8_t bop(int j) const {
+    const float dl = d[j] * (float)((int)iq4xs_ls(hd[j].x >> 16, hd[j].y, 2 * C + H) - 32);
+    const float s = dl * kTwo24, c = -128.0f * dl;
+    const uint2 q2 = cq[C & 1][j];
+    uint32_t w[4];
+    b32_codes<20>(H ? q2.y : q2.x, 0u, w);
+    return h8(mix_lo(w[0], w[1], s, c), mix_hi(w[0], w[1], s, c), mix_lo(w[2], w[3], s, c),
+              mix_hi(w[2], w[3], s, c));
   }
 };
 
@@ -1607,6 +1805,7 @@ __global__ __launch_bounds__(kWThr) void gemm_wide(const XT *__restrict__ x, int
   for (int j = 0; j < kWTN; ++j)  // tile t0 + j, or none past the weight's end
     s.brs[j] = make_rsrc(W + (int64_t)min(t0 + j, ntiles - 1) * s.ts, t0 + j < ntiles ? s.ts : 0);
   s.bo = b_offsets<TYPE>(r, g);
+  if constexpr (TYPE == 10 || TYPE == 11) s.lg = g;
   const int rows = min(kWBM, M - m0);
   const int64_t ldxb = ldx * (int64_t)sizeof(XT);
 #pragma unroll
@@ -1656,8 +1855,8 @@ __global__ __launch_bounds__(kWThr) void gemm_wide(const XT *__restrict__ x, int
 template <int TYPE, typename XT>
 hipError_t launch_type(const XT *x, int64_t ldx, const uint8_t *W, int M, int N, int K, float *y,
                        int64_t ldy, float *work, int64_t work_floats, hipStream_t s) {
-  if constexpr ((TYPE == 12 || TYPE == 8 || TYPE == 14 || TYPE == 13) && sizeof(XT) == 2) {
-    // Q4_K / Q8_0 / Q6_K / Q5_K with fp16 activations on a grid that fills the chip: the wide tile
+  if constexpr (has_wide<TYPE>() && sizeof(XT) == 2) {
+    // fp16 activations on a grid that fills the chip: the wide tile
     const int wm = (M + kWBM - 1) / kWBM, wn = (N + wide_bn<TYPE>() - 1) / wide_bn<TYPE>();
     if ((int64_t)wm * wn >= wide_min<TYPE>() && K % 256 == 0) {
       hipLaunchKernelGGL((gemm_wide<TYPE, XT>), dim3((unsigned)(wm * wn)), dim3(kWThr), 0, s, x,
