@@ -1154,8 +1154,8 @@ inline int gemm_splits(int type, int64_t tiles, int nu) {
 }
 
 // ---------------------------------------------------------------------------
-// Wide-tile GEMM for large grids (Q4_K, Q8_0, Q6_K, Q5_K, Q3_K, Q2_K and
-// IQ4_XS, fp16 activations, K a multiple of 256).  A workgroup of 8 waves owns a
+// Wide-tile GEMM for large grids (every type but the grid-codebook IQ types,
+// fp16 activations, K a multiple of 256).  A workgroup of 8 waves owns a
 // 128 x 512 output tile (Q6_K, Q5_K, Q3_K 128 x 384); wave w owns all 128 rows
 // and the 64 columns [64 w, 64 w + 64) (four row tiles of the weight; Q6_K,
 // Q5_K, Q3_K three): 32 accumulator tiles, 255 VGPRs, two waves per SIMD.  Against gemm_kernel's 128 x 32 per
@@ -1204,6 +1204,8 @@ inline int gemm_splits(int type, int64_t tiles, int nu) {
 //     M = 8192 (3 tiles: 785 / 973).  Q3_K (3 tiles, 226 VGPRs): 681 -> 715,
 //     829 -> 896.  IQ4_XS (4 tiles, 254 VGPRs): 671 -> 742, 797 -> 896.  All
 //     bit-identical to gemm_kernel.
+//   - Q4_0 / Q5_0 / IQ4_NL (4 tiles): 736 -> 873, 642 -> 744, 641 -> 749 at
+//     M = 2048; 915 -> 1061, 791 -> 928, 793 -> 914 at M = 8192.
 // ---------------------------------------------------------------------------
 constexpr int kWW = 8, kWTM = 8;
 // weight row tiles per wave: 4 (a 128 x 512 workgroup tile); Q6_K, Q5_K and Q3_K 3
@@ -1226,7 +1228,7 @@ constexpr int wide_min() {
 template <int TYPE>
 constexpr bool has_wide() {
   return TYPE == 12 || TYPE == 8 || TYPE == 14 || TYPE == 13 || TYPE == 10 || TYPE == 11 ||
-         TYPE == 23;
+         TYPE == 23 || TYPE == 2 || TYPE == 6 || TYPE == 20;
 }
 constexpr int kWBM = 16 * kWTM;
 constexpr int kWThr = 64 * kWW;
@@ -1709,6 +1711,60 @@ struct WB<14> {
   }
 };
 
+// Q4_0 / Q5_0 / IQ4_NL: as Q8_0, the step's blocks 8 u + 2 c + H; per block
+// the lane's code word, the f16 d and (Q5_0) the row's fifth-bit word.
+template <int T>
+struct WB32 {
+  static constexpr int kWTN = wide_tn<T>();
+  rsrc_t brs[kWTN];
+  int ts, nu, lg;
+  BOff bo;
+  uint32_t cq[2][kWTN][2], dq[2][kWTN][2], hq[2][kWTN][T == 6 ? 2 : 1];
+
+  __device__ __forceinline__ void load_codes(int set, int j, int u, int c) {
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int so = (8 * u + 2 * c + h) * Fmt<T>::TU;
+      cq[set][j][h] = bl4(brs[j], bo.v0, so);
+      dq[set][j][h] = bl2(brs[j], bo.v1, so);
+      if constexpr (T == 6) hq[set][j][h] = bl4(brs[j], bo.v2, so);
+    }
+  }
+  __device__ __forceinline__ void prologue() {
+#pragma unroll
+    for (int j = 0; j < kWTN; ++j) {
+      load_codes(0, j, 0, 0);
+      load_codes(1, j, 0, 1);
+    }
+  }
+  template <int C>
+  __device__ __forceinline__ void begin(int) {}
+  template <int C>
+  __device__ __forceinline__ void done(int j, int u) {
+    const int s2 = 4 * u + C + 2;
+    load_codes(C & 1, j, min(s2 >> 2, nu - 1), (C + 2) & 3);
+  }
+  __device__ __forceinline__ void set_cur() {}
+  // the code minus the type's offset, times d, rounded once to fp16
+  template <int C, int H>
+  __device__ __forceinline__ half8_t bop(int j) const {
+    const float d = h2f(dq[C & 1][j][H]);
+    const float s = d * kTwo24, c = -code_offset<T>() * d;
+    uint32_t qhb = 0;
+    if constexpr (T == 6) qhb = (hq[C & 1][j][H] >> (8 * lg)) & 0xFFu;
+    uint32_t w[4];
+    b32_codes<T>(cq[C & 1][j][H], qhb, w);
+    return h8(mix_lo(w[0], w[1], s, c), mix_hi(w[0], w[1], s, c), mix_lo(w[2], w[3], s, c),
+              mix_hi(w[2], w[3], s, c));
+  }
+};
+template <>
+struct WB<2> : WB32<2> {};
+template <>
+struct WB<6> : WB32<6> {};
+template <>
+struct WB<20> : WB32<20> {};
+
 template <int TYPE>
 struct Wide : WB<TYPE> {
   static constexpr int kWTN = wide_tn<TYPE>();
@@ -1805,7 +1861,7 @@ __global__ __launch_bounds__(kWThr) void gemm_wide(const XT *__restrict__ x, int
   for (int j = 0; j < kWTN; ++j)  // tile t0 + j, or none past the weight's end
     s.brs[j] = make_rsrc(W + (int64_t)min(t0 + j, ntiles - 1) * s.ts, t0 + j < ntiles ? s.ts : 0);
   s.bo = b_offsets<TYPE>(r, g);
-  if constexpr (TYPE == 10 || TYPE == 11) s.lg = g;
+  if constexpr (TYPE == 10 || TYPE == 11 || TYPE == 6) s.lg = g;
   const int rows = min(kWBM, M - m0);
   const int64_t ldxb = ldx * (int64_t)sizeof(XT);
 #pragma unroll

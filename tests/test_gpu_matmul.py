@@ -315,11 +315,13 @@ def test_full_size_configs(pkg, t, m, n, k, xdt):
                                      (8, 777, 29000, 1536), (8, 2100, 8200, 4096),
                                      (14, 2100, 14000, 1536), (14, 1500, 29000, 1536),
                                      (13, 2100, 14000, 1536), (11, 2100, 14000, 1536),
-                                     (10, 1000, 14000, 4096), (23, 1000, 14000, 1536)])
+                                     (10, 1000, 14000, 4096), (23, 1000, 14000, 1536),
+                                     (2, 1000, 14000, 4096), (6, 777, 29000, 1536),
+                                     (20, 1000, 14000, 1536)])
 def test_wide_gemm_ragged(pkg, t, m, n, k):
-    """Q4_K, Q8_0, Q6_K, Q5_K, Q3_K, Q2_K and IQ4_XS prefill with fp16
-    activations on grids large enough for the wide-tile GEMM (192 tiles of
-    128 x 512; Q6_K, Q5_K and Q3_K 512 of 128 x 384):
+    """Every type but the grid-codebook IQ types: prefill with fp16 activations
+    on grids large enough for the wide-tile GEMM (192 tiles of 128 x 512; Q6_K,
+    Q5_K and Q3_K 512 of 128 x 384):
     rows past M in the last row tile, a last workgroup with fewer weight row
     tiles than the others, N not a multiple of 16 and a K of 6 superblocks,
     against the f64 product of the dequantized weights; a second call gives
@@ -336,7 +338,8 @@ def test_wide_gemm_ragged(pkg, t, m, n, k):
 
 @pytest.mark.parametrize("t,m,k", [(12, 1280, 4096), (8, 1280, 4096), (8, 1280, 1568),
                                    (14, 2048, 4096), (13, 2048, 4096), (11, 2048, 4096),
-                                   (10, 1280, 4096), (23, 1280, 4096)])
+                                   (10, 1280, 4096), (23, 1280, 4096), (2, 1280, 4096),
+                                   (6, 1280, 4096), (20, 1280, 4096)])
 def test_wide_gemm_equals_gemm_kernel_rows(pkg, t, m, k):
     """The wide-tile GEMM (1280 rows: 280 tiles of 128 x 512; Q6_K 2048 rows:
     608 tiles of 128 x 384) and gemm_kernel (a slice of 128 rows: 56 tiles of
