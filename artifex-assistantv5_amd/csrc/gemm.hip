@@ -751,14 +751,10 @@ __device__ __forceinline__ uint32_t mix_w(uint32_t w, float s) {
   return r;
 }
 
+// The record words of window C (sub-blocks 2C, 2C + 1) of the lane's row: v =
+// the record's offset in the resource, su = the unit's.
 template <int C, int T>
-__device__ __forceinline__ void load_b_iq(rsrc_t rs, const BOff &o, int ts, int u, BRaw<T> &b,
-                                          BHdr<T> &h) {
-  const int su = u * Fmt<T>::TU;
-#pragma unroll
-  for (int j = 0; j < kTN; ++j) {
-    uint32_t *w = b.u[j].w;
-    const int v = o.v0 + j * ts;  // the record of the lane's row in tile j
+__device__ __forceinline__ void iq_load_window(rsrc_t rs, int v, int su, uint32_t *w) {
     if constexpr (T == 16 || T == 17 || T == 18 || T == 21) {  // index words 4C .. 4C + 3
       const uint4 q = bl16(rs, v + 16 * C, su);
       w[4 * C] = q.x; w[4 * C + 1] = q.y; w[4 * C + 2] = q.z; w[4 * C + 3] = q.w;
@@ -785,6 +781,15 @@ __device__ __forceinline__ void load_b_iq(rsrc_t rs, const BOff &o, int ts, int 
       w[2 * C] = q.x; w[2 * C + 1] = q.y; w[12] = sw.x; w[13] = sw.y;
       w[8 + C] = bl4(rs, v + 4 * (8 + C), su);
     }
+}
+
+template <int C, int T>
+__device__ __forceinline__ void load_b_iq(rsrc_t rs, const BOff &o, int ts, int u, BRaw<T> &b,
+                                          BHdr<T> &h) {
+  const int su = u * Fmt<T>::TU;
+#pragma unroll
+  for (int j = 0; j < kTN; ++j) {
+    iq_load_window<C, T>(rs, o.v0 + j * ts, su, b.u[j].w);  // the record of the lane's row in tile j
     if constexpr (T != 29)
       if (C == 0) h.d[j] = bl2(rs, o.v1 + j * ts, su);
   }
@@ -1154,8 +1159,8 @@ inline int gemm_splits(int type, int64_t tiles, int nu) {
 }
 
 // ---------------------------------------------------------------------------
-// Wide-tile GEMM for large grids (every type but the grid-codebook IQ types,
-// fp16 activations, K a multiple of 256).  A workgroup of 8 waves owns a
+// Wide-tile GEMM for large grids (every type but IQ3_XXS, fp16 activations, K a
+// multiple of 256).  A workgroup of 8 waves owns a
 // 128 x 512 output tile (Q6_K, Q5_K, Q3_K 128 x 384); wave w owns all 128 rows
 // and the 64 columns [64 w, 64 w + 64) (four row tiles of the weight; Q6_K,
 // Q5_K, Q3_K three): 32 accumulator tiles, 255 VGPRs, two waves per SIMD.  Against gemm_kernel's 128 x 32 per
@@ -1206,14 +1211,20 @@ inline int gemm_splits(int type, int64_t tiles, int nu) {
 //     bit-identical to gemm_kernel.
 //   - Q4_0 / Q5_0 / IQ4_NL (4 tiles): 736 -> 873, 642 -> 744, 641 -> 749 at
 //     M = 2048; 915 -> 1061, 791 -> 928, 793 -> 914 at M = 8192.
+//   - Grid-codebook IQ types (tables in shared memory beside the stages, up to
+//     96 KB): IQ2_XXS, IQ2_XS (4 tiles) 723 -> 804, 668 -> 746; IQ3_S, IQ2_S,
+//     IQ1_M (3 tiles) 530 -> 573, 553 -> 613, 648 -> 679.  IQ3_XXS (3 tiles)
+//     measured 685 -> 671 and keeps gemm_kernel.
 // ---------------------------------------------------------------------------
 constexpr int kWW = 8, kWTM = 8;
-// weight row tiles per wave: 4 (a 128 x 512 workgroup tile); Q6_K, Q5_K and Q3_K 3
-// (128 x 384), whose quant and header words need the registers of a fourth tile's
-// accumulators
+// weight row tiles per wave: 4 (a 128 x 512 workgroup tile); Q6_K, Q5_K, Q3_K, IQ3_S,
+// IQ2_S and IQ1_M 3 (128 x 384), whose quant and header words need the registers of a
+// fourth tile's accumulators.  No configuration may spill inside the main loop: IQ1_M
+// at 4 tiles reloaded one spilled dword there, into a register the allocator also used
+// for an accumulator, and one accumulator tile per wave came out wrong.
 template <int TYPE>
 constexpr int wide_tn() {
-  return TYPE == 14 || TYPE == 13 || TYPE == 11 ? 3 : 4;
+  return TYPE == 14 || TYPE == 13 || TYPE == 11 || TYPE == 21 || TYPE == 22 || TYPE == 29 ? 3 : 4;
 }
 template <int TYPE>
 constexpr int wide_bn() {
@@ -1225,10 +1236,12 @@ template <int TYPE>
 constexpr int wide_min() {
   return wide_tn<TYPE>() == 3 ? 512 : GGUF_GEMM_WIDE_MIN;
 }
+// every type but IQ3_XXS (685 -> 671 TFLOP/s on the wide tile at M = 2048)
 template <int TYPE>
 constexpr bool has_wide() {
   return TYPE == 12 || TYPE == 8 || TYPE == 14 || TYPE == 13 || TYPE == 10 || TYPE == 11 ||
-         TYPE == 23 || TYPE == 2 || TYPE == 6 || TYPE == 20;
+         TYPE == 23 || TYPE == 2 || TYPE == 6 || TYPE == 20 || TYPE == 16 || TYPE == 17 ||
+         TYPE == 21 || TYPE == 22 || TYPE == 29;
 }
 constexpr int kWBM = 16 * kWTM;
 constexpr int kWThr = 64 * kWW;
@@ -1758,6 +1771,71 @@ struct WB32 {
               mix_hi(w[2], w[3], s, c));
   }
 };
+// The grid-codebook IQ types: set P holds, per tile, the record words of the
+// window of the steps of parity P (iq_load_window), requested two steps
+// ahead; the operand is built from the workgroup's tables in shared memory
+// (iq_b) and rounded once with the unit scale, as in gemm_kernel.
+template <int T>
+struct WBIq {
+  static constexpr int kWTN = wide_tn<T>();
+  rsrc_t brs[kWTN];
+  int ts, nu, lg;
+  BOff bo;
+  const unsigned char *tb;
+  IqUnit<T> cu[2][kWTN];
+  uint32_t hd[kWTN];
+  float us[kWTN];
+
+  template <int C>
+  __device__ __forceinline__ void load_win(int j, int u) {
+    iq_load_window<C, T>(brs[j], bo.v0, u * Fmt<T>::TU, cu[C & 1][j].w);
+  }
+  __device__ __forceinline__ void load_hdr(int u) {
+    if constexpr (T != 29)
+#pragma unroll
+      for (int j = 0; j < kWTN; ++j) hd[j] = bl2(brs[j], bo.v1, u * Fmt<T>::TU);
+  }
+  __device__ __forceinline__ void prologue() {
+    load_hdr(0);
+#pragma unroll
+    for (int j = 0; j < kWTN; ++j) {
+      load_win<0>(j, 0);
+      load_win<1>(j, 0);
+    }
+  }
+  template <int C>
+  __device__ __forceinline__ void begin(int u) {
+    if (C == 2) load_hdr(min(u + 1, nu - 1));
+  }
+  template <int C>
+  __device__ __forceinline__ void done(int j, int u) {
+    load_win<(C + 2) & 3>(j, min((4 * u + C + 2) >> 2, nu - 1));
+  }
+  __device__ __forceinline__ void set_cur() {
+    if constexpr (T != 29)
+#pragma unroll
+      for (int j = 0; j < kWTN; ++j) us[j] = h2f(hd[j]) * iq_d_factor<T>();
+  }
+  template <int C, int H>
+  __device__ __forceinline__ half8_t bop(int j) const {
+    const float s = T == 29 ? iq_unit_scale<T>(cu[C & 1][j]) : us[j];
+    const uint4 v = __builtin_bit_cast(uint4, iq_b<T>(cu[C & 1][j], 2 * C + H, lg, tb));
+    return h8(mix_w(v.x, s), mix_w(v.y, s), mix_w(v.z, s), mix_w(v.w, s));
+  }
+};
+template <>
+struct WB<16> : WBIq<16> {};
+template <>
+struct WB<17> : WBIq<17> {};
+template <>
+struct WB<18> : WBIq<18> {};
+template <>
+struct WB<21> : WBIq<21> {};
+template <>
+struct WB<22> : WBIq<22> {};
+template <>
+struct WB<29> : WBIq<29> {};
+
 template <>
 struct WB<2> : WB32<2> {};
 template <>
@@ -1838,6 +1916,10 @@ __global__ __launch_bounds__(kWThr) void gemm_wide(const XT *__restrict__ x, int
                                                   int tiles_m) {
   constexpr int kWTN = wide_tn<TYPE>();
   __shared__ __align__(16) unsigned char lds[4 * kWStB];
+  // IQ types: the decode tables, requested first and written before the first barrier
+  __shared__ __align__(16) unsigned char iqtbl[is_iq(TYPE) ? iq_tbl_bytes<TYPE>() : 16];
+  IqTabRegs<TYPE, kWThr> tab;
+  if constexpr (is_iq(TYPE)) iq_get_tables<TYPE, kWThr>(tab);
   int bid = blockIdx.x;
   if ((gridDim.x & 7) == 0) bid = (bid & 7) * (gridDim.x >> 3) + (bid >> 3);
   int m0, n0;
@@ -1861,7 +1943,7 @@ __global__ __launch_bounds__(kWThr) void gemm_wide(const XT *__restrict__ x, int
   for (int j = 0; j < kWTN; ++j)  // tile t0 + j, or none past the weight's end
     s.brs[j] = make_rsrc(W + (int64_t)min(t0 + j, ntiles - 1) * s.ts, t0 + j < ntiles ? s.ts : 0);
   s.bo = b_offsets<TYPE>(r, g);
-  if constexpr (TYPE == 10 || TYPE == 11 || TYPE == 6) s.lg = g;
+  if constexpr (TYPE == 10 || TYPE == 11 || TYPE == 6 || is_iq(TYPE)) s.lg = g;
   const int rows = min(kWBM, M - m0);
   const int64_t ldxb = ldx * (int64_t)sizeof(XT);
 #pragma unroll
@@ -1887,6 +1969,10 @@ __global__ __launch_bounds__(kWThr) void gemm_wide(const XT *__restrict__ x, int
   s.load_a(64);
   s.store_a(1);
   s.load_a(128);
+  if constexpr (is_iq(TYPE)) {
+    iq_put_tables<TYPE, kWThr>(tab, iqtbl);
+    s.tb = iqtbl;
+  }
   __syncthreads();
   for (int u = 0; u < s.nu; ++u) {
     s.set_cur();

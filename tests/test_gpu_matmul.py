@@ -339,7 +339,9 @@ def test_wide_gemm_ragged(pkg, t, m, n, k):
 @pytest.mark.parametrize("t,m,k", [(12, 1280, 4096), (8, 1280, 4096), (8, 1280, 1568),
                                    (14, 2048, 4096), (13, 2048, 4096), (11, 2048, 4096),
                                    (10, 1280, 4096), (23, 1280, 4096), (2, 1280, 4096),
-                                   (6, 1280, 4096), (20, 1280, 4096)])
+                                   (6, 1280, 4096), (20, 1280, 4096), (16, 1280, 4096),
+                                   (17, 1280, 4096), (21, 2048, 4096), (22, 2048, 4096),
+                                   (29, 2048, 4096), (29, 2048, 1536)])
 def test_wide_gemm_equals_gemm_kernel_rows(pkg, t, m, k):
     """The wide-tile GEMM (1280 rows: 280 tiles of 128 x 512; Q6_K 2048 rows:
     608 tiles of 128 x 384) and gemm_kernel (a slice of 128 rows: 56 tiles of
@@ -347,7 +349,11 @@ def test_wide_gemm_equals_gemm_kernel_rows(pkg, t, m, k):
     the same k order: the same bits.  A Q8_0 K that is not a multiple of 256
     keeps gemm_kernel for the whole call."""
     n = 14336
-    raw, w = _case(pkg, t, n, k, seed=t + k)
+    if t in (16, 17, 18, 21, 22, 29):  # random valid blocks: every bit pattern decodes
+        raw = tile_model.random_blocks(t, n, k, seed=t + k)
+        w = pkg.repack_gguf_for_gpu(t, raw, n, k)
+    else:
+        raw, w = _case(pkg, t, n, k, seed=t + k)
     g = torch.Generator(device="cuda").manual_seed(k)
     x = torch.randn(m, k, device="cuda", generator=g).half()
     lib = pkg.load_library()
