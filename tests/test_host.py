@@ -157,6 +157,23 @@ def test_glue_rejects_mismatched_buffers(pkg):
         (lambda: glue.attention_decode(z(6 * 64), z(2), z(16, 32), z(16, 32), z(1, 16, 64), z(1, 16, 64),
                                        None, 4, 1, 64, z(1)), "pos must hold one"),
         (lambda: glue.argmax(z(0), z(1), z(1)), "argmax"),
+        # prefill attention: 4 / 1 heads of 64, max_seq 16, rows of 384 (qkv) and 256 (out)
+        (lambda: glue.attention_prefill(z(3 * 384), z(3), z(16, 32), z(16, 32), z(1, 16, 64),
+                                        z(1, 16, 64), z(3, 256), 4, 1, 64), "same M"),
+        (lambda: glue.attention_prefill(z(3, 384), z(2), z(16, 32), z(16, 32), z(1, 16, 64),
+                                        z(1, 16, 64), z(3, 256), 4, 1, 64), "pos holds 2"),
+        (lambda: glue.attention_prefill(z(3, 384), z(3), z(16, 32), z(16, 32), z(1, 16, 32),
+                                        z(1, 16, 64), z(3, 256), 4, 1, 64), "k_cache must be"),
+        (lambda: glue.attention_prefill(z(3, 384), z(3), z(16, 32), z(16, 32), z(1, 16, 64),
+                                        z(2, 16, 64), z(3, 256), 4, 1, 64), "prefill: v_cache"),
+        (lambda: glue.attention_prefill(z(3, 384), z(3), z(15, 32), z(16, 32), z(1, 16, 64),
+                                        z(1, 16, 64), z(3, 256), 4, 1, 64), "prefill: cos"),
+        (lambda: glue.attention_prefill(z(3, 383), z(3), z(16, 32), z(16, 32), z(1, 16, 64),
+                                        z(1, 16, 64), z(3, 256), 4, 1, 64), "qkv rows hold 383"),
+        (lambda: glue.attention_prefill(z(3, 384), z(3), z(16, 32), z(16, 32), z(1, 16, 64),
+                                        z(1, 16, 64), z(3, 250), 4, 1, 64), "out rows 250"),
+        (lambda: glue.attention_prefill(z(3, 384), z(3), z(16, 32), z(16, 32), z(1, 16, 64),
+                                        z(1, 16, 64), z(3, 256), 4, 1, 64), "float32 device rows"),
     ]
     w = types.SimpleNamespace(k=256, n=64, ggml_type=12)
     cases += [
@@ -188,3 +205,28 @@ def test_matmul_workspace_keying_and_growth():
     # growth is geometric: a run of slowly growing requests reallocates O(log) times
     sizes = {size(n) for n in range(1 << 20, 1 << 26, 1 << 18)}
     assert sizes == {1 << e for e in range(20, 27)}
+
+
+def test_missing_library_raises(pkg):
+    """No CPU fallback: a missing shared library is an error, not a silent path."""
+    from importlib import import_module
+    native = import_module("artifex-assistantv5_amd._native")
+    with pytest.raises(RuntimeError, match="no CPU fallback"):
+        native.load_library("/nonexistent/libgguf_hip.so")
+
+
+def test_package_never_imports_the_oracle():
+    """The oracle is test infrastructure: no module of the package imports or
+    reads anything under oracle/ (the product path is the HIP library)."""
+    import os
+    import re
+    root = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))),
+                        "artifex-assistantv5_amd")
+    bad = []
+    for dirpath, _, files in os.walk(root):
+        for f in files:
+            if f.endswith((".py", ".hip", ".hpp", ".h", ".c")):
+                text = open(os.path.join(dirpath, f), encoding="utf-8").read()
+                if re.search(r"^\s*(import|from)\s+oracle|gguf_ref|gguf_iq|liboracle", text, re.M):
+                    bad.append(f)
+    assert not bad, bad
