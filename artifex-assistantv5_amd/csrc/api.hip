@@ -295,7 +295,7 @@ int64_t gguf_hip_matmul_workspace(int ggml_type, int x_type, int64_t n, int64_t 
   // (M = 1: the one-shot kernel needs none; grid types above K = 16384 still do)
   const int64_t dec = (m < 2 && (!grid_type(ggml_type) || k <= kIqOneShotMaxK))
                           ? 0 : gguf::launch_decode_work(ggml_type, x_type, n, k, m);
-  int64_t gem = m > 32 ? gguf::launch_gemm_work(ggml_type, n, k, m) : 0;
+  int64_t gem = m > 32 ? gguf::launch_gemm_work(ggml_type, x_type, n, k, m) : 0;
   if (gem > 0) gem += gguf::kWsPrefix / 4;  // the GEMM's partial sums follow the counter prefix
   return 4 * (dec > gem ? dec : gem);
 }

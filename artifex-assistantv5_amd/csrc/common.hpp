@@ -445,11 +445,12 @@ hipError_t launch_decode(const void *x, int x_type, int64_t ldx, const uint8_t *
 // Workspace floats launch_decode uses for these shapes (0: it needs none).
 int64_t launch_decode_work(int type, int x_type, int64_t n, int64_t k, int64_t m);
 // The GEMM (gemm.hip); with a workspace of launch_gemm_work floats, small grids
-// split K over the chip and add the partial sums in a second launch.
+// split K over the chip and add the partial sums in a second launch, and f32
+// activations on large grids are staged once as an fp16 image for the wide tile.
 hipError_t launch_gemm(const void *x, int x_type, int64_t ldx, const uint8_t *tiles, int type,
                        int64_t n, int64_t k, float *y, int64_t ldy, int64_t m, float *work,
                        int64_t work_floats, hipStream_t s);
-int64_t launch_gemm_work(int type, int64_t n, int64_t k, int64_t m);
+int64_t launch_gemm_work(int type, int x_type, int64_t n, int64_t k, int64_t m);
 hipError_t launch_decode_fused(const float *x, const uint8_t *tiles, int type, int64_t n,
                                int64_t k, float *y, int prologue, const float *pw, float eps,
                                int epilogue, hipStream_t s);

@@ -962,7 +962,8 @@ template <int TYPE, typename XT>
 __global__ __launch_bounds__(kThreads) void gemm_kernel(const XT *__restrict__ x, int64_t ldx,
                                                            const uint8_t *__restrict__ W, int M,
                                                            int N, int K, float *__restrict__ y,
-                                                           int64_t ldy, int tiles_m, int kunits) {
+                                                           int64_t ldy, int tiles_m, int kunits,
+                                                           const float *__restrict__ rowf_g) {
   constexpr int TU = Fmt<TYPE>::TU, UE = Fmt<TYPE>::UE;
   __shared__ __align__(16) unsigned char lds[2 * kStageB];
   __shared__ __align__(16) float rowf[kBM];  // f32 input: the rows' inverse scales 2^-e
@@ -1084,8 +1085,12 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(const XT *__restrict__ x
 #pragma unroll
   for (int i = 0; i < kTM; ++i) {
     float f[4] = {1.f, 1.f, 1.f, 1.f};
-    if constexpr (sizeof(XT) == 4) {
-      const float4 v = *(const float4 *)(rowf + 16 * i + 4 * g);
+    // the rows' inverse scales: staged here (f32 input) or by stage_rows_kernel
+    // (rowf_g, kBM of them per row tile; entries past M are read, not used)
+    const float *rf = sizeof(XT) == 4 ? rowf + 16 * i + 4 * g
+                                      : (rowf_g ? rowf_g + m0 + 16 * i + 4 * g : nullptr);
+    if (rf) {
+      const float4 v = *(const float4 *)rf;
       f[0] = v.x;
       f[1] = v.y;
       f[2] = v.z;
@@ -1222,9 +1227,12 @@ constexpr int kWW = 8, kWTM = 8;
 // fourth tile's accumulators.  No configuration may spill inside the main loop: IQ1_M
 // at 4 tiles reloaded one spilled dword there, into a register the allocator also used
 // for an accumulator, and one accumulator tile per wave came out wrong.
+constexpr int wide_tn(int type) {
+  return type == 14 || type == 13 || type == 11 || type == 21 || type == 22 || type == 29 ? 3 : 4;
+}
 template <int TYPE>
 constexpr int wide_tn() {
-  return TYPE == 14 || TYPE == 13 || TYPE == 11 || TYPE == 21 || TYPE == 22 || TYPE == 29 ? 3 : 4;
+  return wide_tn(TYPE);
 }
 template <int TYPE>
 constexpr int wide_bn() {
@@ -1232,16 +1240,20 @@ constexpr int wide_bn() {
 }
 // the grid (in workgroups) from which the wide tile runs: Q6_K from two full
 // rounds of the chip (M = 1024, N = 14336: 304 workgroups, 611 -> 551 TFLOP/s)
+constexpr int wide_min(int type) { return wide_tn(type) == 3 ? 512 : GGUF_GEMM_WIDE_MIN; }
 template <int TYPE>
 constexpr int wide_min() {
-  return wide_tn<TYPE>() == 3 ? 512 : GGUF_GEMM_WIDE_MIN;
+  return wide_min(TYPE);
 }
 // every type but IQ3_XXS (685 -> 671 TFLOP/s on the wide tile at M = 2048)
+constexpr bool has_wide(int type) {
+  return type == 12 || type == 8 || type == 14 || type == 13 || type == 10 || type == 11 ||
+         type == 23 || type == 2 || type == 6 || type == 20 || type == 16 || type == 17 ||
+         type == 21 || type == 22 || type == 29;
+}
 template <int TYPE>
 constexpr bool has_wide() {
-  return TYPE == 12 || TYPE == 8 || TYPE == 14 || TYPE == 13 || TYPE == 10 || TYPE == 11 ||
-         TYPE == 23 || TYPE == 2 || TYPE == 6 || TYPE == 20 || TYPE == 16 || TYPE == 17 ||
-         TYPE == 21 || TYPE == 22 || TYPE == 29;
+  return has_wide(TYPE);
 }
 constexpr int kWBM = 16 * kWTM;
 constexpr int kWThr = 64 * kWW;
@@ -1913,7 +1925,7 @@ template <int TYPE, typename XT>
 __global__ __launch_bounds__(kWThr) void gemm_wide(const XT *__restrict__ x, int64_t ldx,
                                                   const uint8_t *__restrict__ W, int M, int N,
                                                   int K, float *__restrict__ y, int64_t ldy,
-                                                  int tiles_m) {
+                                                  int tiles_m, const float *__restrict__ rowf) {
   constexpr int kWTN = wide_tn<TYPE>();
   __shared__ __align__(16) unsigned char lds[4 * kWStB];
   // IQ types: the decode tables, requested first and written before the first barrier
@@ -1981,28 +1993,132 @@ __global__ __launch_bounds__(kWThr) void gemm_wide(const XT *__restrict__ x, int
     s.template step<2>(u);
     s.template step<3>(u);
   }
+  // rowf (staged f32 rows): the rows' inverse scales 2^-e, kWBM of them per
+  // row tile (entries past M are read, not used)
 #pragma unroll
-  for (int i = 0; i < kWTM; ++i)
+  for (int i = 0; i < kWTM; ++i) {
+    float4 f = make_float4(1.f, 1.f, 1.f, 1.f);
+    if (rowf) f = *(const float4 *)(rowf + m0 + 16 * i + 4 * g);
+    const float fe[4] = {f.x, f.y, f.z, f.w};
 #pragma unroll
     for (int j = 0; j < kWTN; ++j) {
       const int n = n0 + 16 * (kWTN * wave + j) + r;
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const int m = m0 + 16 * i + 4 * g + e;
-        if (m < M && n < N) y[(int64_t)m * ldy + n] = s.acc[i][j][e];
+        if (m < M && n < N) y[(int64_t)m * ldy + n] = s.acc[i][j][e] * fe[e];
       }
     }
+  }
 }
 
+// f32 activation rows -> the fp16 image the GEMM kernels read: row m times
+// 2^e, e = stage_exp of the row's largest magnitude, rounded to fp16, and
+// rowf[m] = 2^-e.  The same values gemm_kernel stages in LDS for f32 input
+// (the row maximum, exact, does not depend on the reduction order), so both
+// paths give the same result bit for bit.  One workgroup of NT threads per
+// row; with NC > 0 the row (K <= 4 NT NC) is loaded once into registers, all
+// loads in flight together, otherwise it is read twice.  K % 8 == 0, x rows
+// 16-byte aligned.
+template <int NT, int NC>
+__global__ __launch_bounds__(NT) void stage_rows_kernel(const float *__restrict__ x, int64_t ldx,
+                                                        int K, half_t *__restrict__ img,
+                                                        float *__restrict__ rowf) {
+  __shared__ float wmx[NT / 64];
+  const int m = blockIdx.x, tid = threadIdx.x, K4 = K / 4;
+  const float4 *xr = (const float4 *)(x + (int64_t)m * ldx);
+  uint2 *ir = (uint2 *)(img + (int64_t)m * K);  // four fp16 values per float4 of x
+  float4 v[NC > 0 ? NC : 1];
+  float mx = 0.f;
+  if constexpr (NC > 0) {
+#pragma unroll
+    for (int i = 0; i < NC; ++i) {
+      const int c = tid + NT * i;
+      v[i] = c < K4 ? xr[c] : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+#pragma unroll
+    for (int i = 0; i < NC; ++i)
+      mx = fmaxf(mx, fmaxf(fmaxf(fabsf(v[i].x), fabsf(v[i].y)), fmaxf(fabsf(v[i].z), fabsf(v[i].w))));
+  } else {
+    for (int c = tid; c < K4; c += NT) {
+      const float4 a = xr[c];
+      mx = fmaxf(mx, fmaxf(fmaxf(fabsf(a.x), fabsf(a.y)), fmaxf(fabsf(a.z), fabsf(a.w))));
+    }
+  }
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+  if ((tid & 63) == 0) wmx[tid >> 6] = mx;
+  __syncthreads();
+  mx = wmx[0];
+#pragma unroll
+  for (int w = 1; w < NT / 64; ++w) mx = fmaxf(mx, wmx[w]);
+  const int e = stage_exp(mx);
+  const float sc = pow2f(e);
+  if (tid == 0) rowf[m] = pow2f(-e);
+  auto put = [&](int c, const float4 &a) {
+    half4_t h;
+    h[0] = (half_t)(a.x * sc);
+    h[1] = (half_t)(a.y * sc);
+    h[2] = (half_t)(a.z * sc);
+    h[3] = (half_t)(a.w * sc);
+    ir[c] = __builtin_bit_cast(uint2, h);
+  };
+  if constexpr (NC > 0) {
+#pragma unroll
+    for (int i = 0; i < NC; ++i)
+      if (tid + NT * i < K4) put(tid + NT * i, v[i]);
+  } else {
+    for (int c = tid; c < K4; c += NT) put(c, xr[c]);
+  }
+}
+
+hipError_t launch_stage_rows(const float *x, int64_t ldx, int M, int K, half_t *img, float *rowf,
+                             hipStream_t s) {
+  const dim3 g((unsigned)M);
+  if (K <= 2048)
+    hipLaunchKernelGGL((stage_rows_kernel<256, 2>), g, dim3(256), 0, s, x, ldx, K, img, rowf);
+  else if (K <= 4096)
+    hipLaunchKernelGGL((stage_rows_kernel<256, 4>), g, dim3(256), 0, s, x, ldx, K, img, rowf);
+  else if (K <= 8192)
+    hipLaunchKernelGGL((stage_rows_kernel<256, 8>), g, dim3(256), 0, s, x, ldx, K, img, rowf);
+  else if (K <= 16384)
+    hipLaunchKernelGGL((stage_rows_kernel<1024, 4>), g, dim3(1024), 0, s, x, ldx, K, img, rowf);
+  else if (K <= 32768)
+    hipLaunchKernelGGL((stage_rows_kernel<1024, 8>), g, dim3(1024), 0, s, x, ldx, K, img, rowf);
+  else
+    hipLaunchKernelGGL((stage_rows_kernel<1024, 0>), g, dim3(1024), 0, s, x, ldx, K, img, rowf);
+  return hipGetLastError();
+}
+
+// Workspace floats of the staged f32 rows: M inverse row scales, padded to
+// whole 128-row tiles, then the M x K fp16 image.
+static_assert(kWBM == kBM, "both GEMM kernels read kBM row scales per row tile");
+int64_t stage_floats(int64_t m, int64_t k) { return (m + kBM - 1) / kBM * kBM + m * k / 2; }
+
+// rowf: the rows' inverse scales when x is the fp16 image of f32 rows.
 template <int TYPE, typename XT>
 hipError_t launch_type(const XT *x, int64_t ldx, const uint8_t *W, int M, int N, int K, float *y,
-                       int64_t ldy, float *work, int64_t work_floats, hipStream_t s) {
+                       int64_t ldy, float *work, int64_t work_floats, hipStream_t s,
+                       const float *rowf = nullptr) {
+  if constexpr (sizeof(XT) == 4) {
+    // f32 activations with room for their fp16 image: stage the rows once,
+    // then the fp16 kernels run on the image (the K split's partial sums, if
+    // any, follow it in the workspace)
+    const int64_t sf = stage_floats(M, K);
+    if (work && work_floats >= sf) {
+      half_t *img = (half_t *)(work + (sf - (int64_t)M * K / 2));
+      const hipError_t e = launch_stage_rows(x, ldx, M, K, img, work, s);
+      if (e != hipSuccess) return e;
+      return launch_type<TYPE, half_t>(img, (int64_t)K, W, M, N, K, y, ldy, work + sf,
+                                       work_floats - sf, s, work);
+    }
+  }
   if constexpr (has_wide<TYPE>() && sizeof(XT) == 2) {
     // fp16 activations on a grid that fills the chip: the wide tile
     const int wm = (M + kWBM - 1) / kWBM, wn = (N + wide_bn<TYPE>() - 1) / wide_bn<TYPE>();
     if ((int64_t)wm * wn >= wide_min<TYPE>() && K % 256 == 0) {
       hipLaunchKernelGGL((gemm_wide<TYPE, XT>), dim3((unsigned)(wm * wn)), dim3(kWThr), 0, s, x,
-                         ldx, W, M, N, K, y, ldy, wm);
+                         ldx, W, M, N, K, y, ldy, wm, rowf);
       return hipGetLastError();
     }
   }
@@ -2013,7 +2129,7 @@ hipError_t launch_type(const XT *x, int64_t ldx, const uint8_t *W, int M, int N,
   sp = (nu + kunits - 1) / kunits;
   hipLaunchKernelGGL((gemm_kernel<TYPE, XT>), dim3((unsigned)(tiles_m * tiles_n), (unsigned)sp),
                      dim3(kThreads), 0, s, x, ldx, W, M, N, K, sp > 1 ? work : y,
-                     sp > 1 ? (int64_t)N : ldy, tiles_m, kunits);
+                     sp > 1 ? (int64_t)N : ldy, tiles_m, kunits, rowf);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || sp == 1) return e;
   const int64_t mn = (int64_t)M * N;
@@ -2068,14 +2184,18 @@ hipError_t launch_x(const XT *x, int64_t ldx, const uint8_t *W, int type, int64_
 
 }  // namespace
 
-// Workspace floats of the GEMM's K split for these shapes (0: none).
-int64_t launch_gemm_work(int type, int64_t n, int64_t k, int64_t m) {
+// Workspace floats of the GEMM for these shapes (0: none): for f32
+// activations their fp16 image (of the largest launch_gemm chunk of rows),
+// then the K split's partial sums.
+int64_t launch_gemm_work(int type, int x_type, int64_t n, int64_t k, int64_t m) {
+  const int64_t chunk = ((int64_t)1 << 30) / ((n + kBN - 1) / kBN) * kBM;
+  const int64_t img = x_type == 0 ? stage_floats(m < chunk ? m : chunk, k) : 0;
   const int64_t tiles = ((m + kBM - 1) / kBM) * ((n + kBN - 1) / kBN);
   const int nu = (int)(k / unit_elems(type));
-  const int sp = m <= ((int64_t)1 << 30) / ((n + kBN - 1) / kBN) * kBM ? gemm_splits(type, tiles, nu) : 1;
-  if (sp == 1) return 0;
+  const int sp = m <= chunk ? gemm_splits(type, tiles, nu) : 1;
+  if (sp == 1) return img;
   const int kunits = (nu + sp - 1) / sp;
-  return (int64_t)((nu + kunits - 1) / kunits) * m * n;
+  return img + (int64_t)((nu + kunits - 1) / kunits) * m * n;
 }
 
 hipError_t launch_gemm(const void *x, int x_type, int64_t ldx, const uint8_t *tiles, int type,

@@ -190,7 +190,14 @@ int gguf_hip_matmul_variant(const void *x, int x_type, int64_t ldx, const void *
  * runs the M = 1 kernel once per row; with the workspace the batched kernel
  * reads the weights once for all rows.  Beyond K = 16384 only the batched
  * kernel serves them: without the workspace the call returns
- * GGUF_HIP_ERR_SHAPE before launching anything. */
+ * GGUF_HIP_ERR_SHAPE before launching anything.
+ * The GEMM variant with f32 activations and a workspace of
+ * gguf_hip_matmul_workspace bytes stages the rows once: a first launch writes
+ * each row times its power of two as an fp16 image (M x K halves after M
+ * row scales) and the fp16 kernels run on it, the same bits as without the
+ * workspace (where every workgroup scales its rows itself) and 1.2-1.45x
+ * faster (Q4_K, N = 14336, K = 4096: M = 512 500 -> 658, M = 2048 567 -> 829
+ * TFLOP/s). */
 int gguf_hip_matmul_ws(const void *x, int x_type, int64_t ldx, const void *tiles, int ggml_type,
                        int64_t n, int64_t k, float *y, int64_t ldy, int64_t m, int variant,
                        void *work, int64_t work_bytes, void *stream);

@@ -370,6 +370,95 @@ def test_wide_gemm_equals_gemm_kernel_rows(pkg, t, m, k):
         assert torch.equal(gemm(x[m0:m0 + 128].contiguous()), y[m0:m0 + 128]), m0
 
 
+@pytest.mark.parametrize("t,m,n,k", [(12, 1300, 14336, 1024), (14, 2000, 14000, 768),
+                                     (8, 1500, 14336, 512), (29, 2000, 14336, 512),
+                                     (10, 1100, 14336, 1024), (2, 1100, 14000, 512)])
+def test_f32_wide_gemm_stages_rows_exactly(pkg, t, m, n, k):
+    """f32 activations with a workspace on a wide-tile grid: a first launch
+    writes each row times 2^e (e puts the row's largest magnitude in
+    [2^14, 2^15), clamped to [-126, 126]) as an fp16 image, the wide tile
+    multiplies it and scales its sums by 2^-e.  The result equals bit for bit
+    (a) the fp16 GEMM of that image, computed here from the rows' maxima, times
+    2^-e and (b) the call without a workspace (gemm_kernel, which stages the
+    same fp16 values in LDS).  Rows of zeros and of magnitudes 1e-30 .. 1e30,
+    a row with one large entry, ragged M, ldx > K, and a workspace filled with
+    NaN (the padding of the row scales is read, never used)."""
+    if t in (16, 17, 18, 21, 22, 29):
+        w = pkg.repack_gguf_for_gpu(t, tile_model.random_blocks(t, n, k, seed=t + m), n, k)
+    else:
+        _, w = _case(pkg, t, n, k, seed=t + m)
+    g = torch.Generator(device="cuda").manual_seed(m + k)
+    xs = torch.empty(m, k + 64, device="cuda")
+    x = xs[:, :k]
+    x.copy_(torch.randn(m, k, device="cuda", generator=g))
+    x *= 10.0 ** (torch.rand(m, 1, device="cuda", generator=g) * 60 - 30)
+    x[3] = 0
+    x[5] = 1.0
+    x[5, 7] = 3e4
+    lib = pkg.load_library()
+    s = torch.cuda.current_stream().cuda_stream
+    need = lib.gguf_hip_matmul_workspace(t, 0, n, k, m)
+    assert need >= 65536 + 4 * (m * k // 2 + m), need
+    work = torch.full((need,), 255, dtype=torch.uint8, device="cuda")
+
+    def call(xp, x_type, ldx, ws):
+        y = torch.full((m, n), float("nan"), device="cuda")
+        rc = lib.gguf_hip_matmul_ws(xp, x_type, ldx, w.ptr(), t, n, k, y.data_ptr(), n, m, GEMM,
+                                    ws.data_ptr() if ws is not None else None,
+                                    need if ws is not None else 0, s)
+        assert rc == 0, lib.gguf_hip_last_error()
+        return y
+
+    y = call(xs.data_ptr(), 0, k + 64, work)
+    mx = x.abs().amax(1)
+    e = (141 - ((mx.view(torch.int32) >> 23) & 0xFF)).clamp(-126, 126)
+    up = ((e + 127) << 23).to(torch.int32).view(torch.float32)
+    down = ((127 - e) << 23).to(torch.int32).view(torch.float32)
+    img = (x * up[:, None]).half().contiguous()
+    y16 = call(img.data_ptr(), 1, k, None)
+    assert torch.equal(y, y16 * down[:, None])
+    assert torch.equal(y, call(xs.data_ptr(), 0, k + 64, None))
+    assert torch.isfinite(y).all() and (y[3] == 0).all()
+
+
+@pytest.mark.parametrize("k", [2048, 4096, 4352, 8192, 12288, 16384, 32768, 33024])
+def test_f32_staging_every_row_length(pkg, k):
+    """The row-staging launch holds a row of up to 2048 / 4096 / 8192 (256
+    threads) or 16384 / 32768 (1024 threads) values in registers and reads
+    longer rows twice: at and past each bound, 70 f32 rows through a small
+    GEMM grid (gemm_kernel on the image, K split over the workspace after it)
+    give the same bits as without a workspace, up to the split's order of
+    addition, and as the fp16 GEMM of the image times 2^-e bit for bit."""
+    t, m, n = 12, 70, 256
+    w = pkg.repack_gguf_for_gpu(t, tile_model.random_blocks(t, n, k, seed=k), n, k)
+    g = torch.Generator(device="cuda").manual_seed(k)
+    x = torch.randn(m, k, device="cuda", generator=g)
+    x *= 10.0 ** (torch.rand(m, 1, device="cuda", generator=g) * 20 - 10)
+    lib = pkg.load_library()
+    s = torch.cuda.current_stream().cuda_stream
+    need = lib.gguf_hip_matmul_workspace(t, 0, n, k, m)
+    need16 = lib.gguf_hip_matmul_workspace(t, 1, n, k, m)
+    assert need >= 65536 + 4 * (128 + m * k // 2), need
+    work = torch.full((need,), 255, dtype=torch.uint8, device="cuda")
+
+    def call(xt, x_type, nbytes):
+        y = torch.full((m, n), float("nan"), device="cuda")
+        rc = lib.gguf_hip_matmul_ws(xt.data_ptr(), x_type, k, w.ptr(), t, n, k, y.data_ptr(), n, m,
+                                    GEMM, work.data_ptr() if nbytes else None, nbytes, s)
+        assert rc == 0, lib.gguf_hip_last_error()
+        return y
+
+    y = call(x, 0, need)
+    mx = x.abs().amax(1)
+    e = (141 - ((mx.view(torch.int32) >> 23) & 0xFF)).clamp(-126, 126)
+    up = ((e + 127) << 23).to(torch.int32).view(torch.float32)
+    down = ((127 - e) << 23).to(torch.int32).view(torch.float32)
+    img = (x * up[:, None]).half()
+    assert torch.equal(y, call(img, 1, need16) * down[:, None])
+    y0 = call(x, 0, 0)
+    assert torch.allclose(y, y0, rtol=1e-5, atol=1e-6 * float(y0.abs().max()))
+
+
 @pytest.mark.parametrize("t,m,n,k", [(12, 8, 14336, 4096), (12, 32, 4096, 14336), (14, 17, 4096, 14336),
                                      (2, 32, 4096, 4096), (8, 5, 1000, 2048), (10, 32, 512, 8192),
                                      (13, 2, 300, 4096)])
