@@ -2123,10 +2123,16 @@ hipError_t launch_type(const XT *x, int64_t ldx, const uint8_t *W, int M, int N,
     }
   }
   const int tiles_m = (M + kBM - 1) / kBM, tiles_n = (N + kBN - 1) / kBN, nu = K / Fmt<TYPE>::UE;
+  // sp ranges of kunits superblocks each (the last one shorter); the
+  // workspace is checked against the rounded count, the one
+  // launch_gemm_work sizes it for
   int sp = gemm_splits(TYPE, (int64_t)tiles_m * tiles_n, nu);
-  if (!work || work_floats < (int64_t)sp * M * N) sp = 1;
-  const int kunits = (nu + sp - 1) / sp;
+  int kunits = (nu + sp - 1) / sp;
   sp = (nu + kunits - 1) / kunits;
+  if (!work || work_floats < (int64_t)sp * M * N) {
+    sp = 1;
+    kunits = nu;
+  }
   hipLaunchKernelGGL((gemm_kernel<TYPE, XT>), dim3((unsigned)(tiles_m * tiles_n), (unsigned)sp),
                      dim3(kThreads), 0, s, x, ldx, W, M, N, K, sp > 1 ? work : y,
                      sp > 1 ? (int64_t)N : ldy, tiles_m, kunits, rowf);

@@ -526,6 +526,32 @@ def test_gemm_split_k(pkg, ref, t, m, n, k, xdt):
     assert np.abs(ys - y1s).max() <= 1e-5 * np.abs(y1s).max(), (t, m, n, k)
 
 
+@pytest.mark.parametrize("m,k", [(64, 14336), (128, 14336), (100, 4864)])
+def test_gemm_split_k_with_uneven_ranges(pkg, m, k):
+    """K = 14336 is 56 superblocks: 16 splits round to 14 ranges of 4, and the
+    workspace gguf_hip_matmul_workspace sizes for 14 must be enough for the
+    launch to split (it once compared it with 16 and ran one K range on 16
+    workgroups, 4x slower).  The partial sums land in the workspace past its
+    reserved prefix; the result is within f32 rounding of the unsplit call."""
+    t, n = 14, 4096
+    lib = pkg.load_library()
+    w = pkg.repack_gguf_for_gpu(t, tile_model.random_blocks(t, n, k, seed=m), n, k)
+    x = torch.randn(m, k, device="cuda").half()
+    need = lib.gguf_hip_matmul_workspace(t, 1, n, k, m)
+    work = torch.full((need,), 255, dtype=torch.uint8, device="cuda")
+    y = torch.full((m, n), float("nan"), device="cuda")
+    y1 = torch.full((m, n), float("nan"), device="cuda")
+    assert lib.gguf_hip_matmul_ws(x.data_ptr(), 1, k, w.ptr(), t, n, k, y.data_ptr(), n, m, GEMM,
+                                  work.data_ptr(), need, None) == 0
+    assert lib.gguf_hip_matmul_variant(x.data_ptr(), 1, k, w.ptr(), t, n, k, y1.data_ptr(), n, m,
+                                       GEMM, None) == 0
+    torch.cuda.synchronize()
+    assert bool((work[:65536] == 255).all())
+    assert int((work[65536:65536 + 4 * m * n] != 255).sum()) > 0, "the call did not split K"
+    assert torch.isfinite(y).all()
+    assert float((y - y1).abs().max()) <= 1e-5 * float(y1.abs().max())
+
+
 @pytest.mark.gpu
 def test_shared_workspace_prefix_stays_zero(pkg, ref):
     """One workspace serves, in turn, the batched decode with K split over the
