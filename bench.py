@@ -22,7 +22,8 @@ full synthetic Llama-style decoder: 32 layers, d_model 4096, 32/8 heads of
 LM head; 128 random prompt tokens then 256 greedy tokens; tok/s = generated
 tokens / decode wall time, prefill excluded).  ``secondary`` holds the other
 configurations of the path (Q4_K / Q5_K / Q6_K decode shapes and batch sizes,
-the other GGML types at the headline shape, more prefill shapes).  ``cpu_baseline`` = the CPU restatement of the reference
+the other GGML types at the headline shape, more prefill shapes, f32 prefill
+activations).  ``cpu_baseline`` = the CPU restatement of the reference
 path (the compiled C oracle, oracle/gguf_ref_c.c: Q4_K dequant fused with the
 GEMV, OpenMP; numpy dequant + torch fp32 matmul when it is not built) on the
 host threads, repeated for about 10 s, with two more entries: ``prefill`` (the Q4_K GEMM shape at
@@ -580,6 +581,11 @@ def secondary_cases(pkg, args, pool, secondary):
             r = matmul_case(pkg, t, mm, nn, 4096, ppool, 10, 2, xdtype="float16")
             secondary[f"q4k_gemm_m{mm}_n{nn}_tflops"] = round(r["tflops"], 1)
             secondary[f"q4k_gemm_m{mm}_n{nn}_frac_fp16_peak"] = round(r["tflops"] / FP16_PEAK_TFLOPS, 4)
+        # f32 activations (the decoder's prefill rows): staged once as an fp16 image in the
+        # workspace, then the same GEMM
+        for mm in (512, 2048):
+            r = matmul_case(pkg, t, mm, 14336, 4096, pool[:2], 10, 2, xdtype="float32")
+            secondary[f"q4k_gemm_m{mm}_n14336_f32x_tflops"] = round(r["tflops"], 1)
 
 
 def main():
