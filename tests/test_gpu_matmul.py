@@ -526,6 +526,40 @@ def test_gemm_split_k(pkg, ref, t, m, n, k, xdt):
     assert np.abs(ys - y1s).max() <= 1e-5 * np.abs(y1s).max(), (t, m, n, k)
 
 
+@pytest.mark.parametrize("t,m,n,k,xdt", [(12, 1300, 14336, 1024, torch.float32),
+                                         (14, 64, 4096, 14336, torch.float16),
+                                         (12, 200, 302, 4096, torch.float32),
+                                         (8, 600, 4096, 4096, torch.float32)])
+def test_gemm_paths_replay_in_graphs(pkg, t, m, n, k, xdt):
+    """The GEMM's launch sequences captured in a HIP graph (the staged f32 rows
+    on the wide tile; a K split with the four-wide and the scalar reduction;
+    the staged rows with gemm_kernel): three replays, each after eager calls
+    of other shapes on the same stream and an output poisoned with NaN, give
+    the eager result bit for bit."""
+    if t == 14:
+        w = pkg.repack_gguf_for_gpu(t, tile_model.random_blocks(t, n, k, seed=5), n, k)
+    else:
+        _, w = _case(pkg, t, n, k, seed=5)
+    g = torch.Generator(device="cuda").manual_seed(m)
+    x = torch.randn(m, k, device="cuda", generator=g).to(xdt)
+    y_eager = pkg.qlinear(x, w, variant=GEMM)
+    out = torch.empty(m, n, device="cuda")
+    pkg.qlinear(x, w, out=out, variant=GEMM)  # warm-up outside the capture
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        pkg.qlinear(x, w, out=out, variant=GEMM)
+    other = torch.randn(70, k, device="cuda", generator=g)
+    for rep in range(3):
+        pkg.qlinear(other, w)  # eager work between the replays
+        pkg.qlinear(x[: m // 2 + 1], w)
+        out.fill_(float("nan"))
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, y_eager), rep
+
+
 @pytest.mark.parametrize("m,k", [(64, 14336), (128, 14336), (100, 4864)])
 def test_gemm_split_k_with_uneven_ranges(pkg, m, k):
     """K = 14336 is 56 superblocks: 16 splits round to 14 ranges of 4, and the
