@@ -2095,6 +2095,45 @@ hipError_t launch_stage_rows(const float *x, int64_t ldx, int M, int K, half_t *
 static_assert(kWBM == kBM, "both GEMM kernels read kBM row scales per row tile");
 int64_t stage_floats(int64_t m, int64_t k) { return (m + kBM - 1) / kBM * kBM + m * k / 2; }
 
+// Compute units of the current device (256 on MI355X), read once per device.
+int device_cus() {
+  static int cus[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cus[dev] <= 0) {
+    int v = 0;
+    if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || v <= 0)
+      v = 256;
+    cus[dev] = v;
+  }
+  return cus[dev];
+}
+
+// Column tiles of the wide tile's launch (of wn).  Its workgroups hold a CU
+// each for about the same time, so a grid of wm x wn runs in
+// ceil(wm wn / CUs) rounds; when the last round is partly empty and handing
+// the columns past the whole rounds to gemm_kernel (128 x 256 tiles, one K
+// range) ends sooner, the wide tile keeps only those whole rounds.  A
+// gemm_kernel round takes rho of a wide round (from the measured rates:
+// Q4_K 134 against 69 us, Q6_K 121 against 98 us per round).  Q6_K at
+// M = 2048, N = 14336: 608 workgroups (3 rounds, the last 37.5% full) ->
+// 512 + 128 of gemm_kernel.
+#ifndef GGUF_GEMM_WIDE_SPLIT
+#define GGUF_GEMM_WIDE_SPLIT 1  // 0: the wide tile covers every column
+#endif
+int wide_columns(int wm, int wn, int M, int N, int bn, int tn) {
+  if (!GGUF_GEMM_WIDE_SPLIT) return wn;
+  const int64_t cus = device_cus(), g = (int64_t)wm * wn;
+  const int64_t r = g / cus, rounds = (g + cus - 1) / cus;
+  if (r < 1 || g % cus == 0) return wn;
+  const int w1 = (int)(r * cus / wm);
+  if (w1 < 1 || w1 >= wn) return wn;
+  const int64_t left = N - (int64_t)w1 * bn;
+  const int64_t gk = (int64_t)((M + kBM - 1) / kBM) * ((left + kBN - 1) / kBN);
+  const double rho = tn == 3 ? 0.81 : 0.52;
+  return (double)r + (double)((gk + cus - 1) / cus) * rho < (double)rounds - 0.1 ? w1 : wn;
+}
+
 // rowf: the rows' inverse scales when x is the fp16 image of f32 rows.
 template <int TYPE, typename XT>
 hipError_t launch_type(const XT *x, int64_t ldx, const uint8_t *W, int M, int N, int K, float *y,
@@ -2115,10 +2154,22 @@ hipError_t launch_type(const XT *x, int64_t ldx, const uint8_t *W, int M, int N,
   }
   if constexpr (has_wide<TYPE>() && sizeof(XT) == 2) {
     // fp16 activations on a grid that fills the chip: the wide tile
-    const int wm = (M + kWBM - 1) / kWBM, wn = (N + wide_bn<TYPE>() - 1) / wide_bn<TYPE>();
+    constexpr int bn = wide_bn<TYPE>();
+    const int wm = (M + kWBM - 1) / kWBM, wn = (N + bn - 1) / bn;
     if ((int64_t)wm * wn >= wide_min<TYPE>() && K % 256 == 0) {
-      hipLaunchKernelGGL((gemm_wide<TYPE, XT>), dim3((unsigned)(wm * wn)), dim3(kWThr), 0, s, x,
-                         ldx, W, M, N, K, y, ldy, wm, rowf);
+      const int wn1 = wide_columns(wm, wn, M, N, bn, wide_tn<TYPE>());
+      const int n1 = min(N, wn1 * bn);
+      hipLaunchKernelGGL((gemm_wide<TYPE, XT>), dim3((unsigned)(wm * wn1)), dim3(kWThr), 0, s, x,
+                         ldx, W, M, n1, K, y, ldy, wm, rowf);
+      hipError_t e = hipGetLastError();
+      if (e != hipSuccess || n1 == N) return e;
+      // the columns past the wide tile's whole rounds: gemm_kernel, one K range
+      // (the same bits per element as the wide tile)
+      const int64_t ts = (int64_t)(K / Fmt<TYPE>::UE) * Fmt<TYPE>::TU;
+      const int tm = (M + kBM - 1) / kBM, tn = (N - n1 + kBN - 1) / kBN;
+      hipLaunchKernelGGL((gemm_kernel<TYPE, XT>), dim3((unsigned)(tm * tn), 1u), dim3(kThreads), 0,
+                         s, x, ldx, W + (int64_t)(n1 / 16) * ts, M, N - n1, K, y + n1, ldy, tm,
+                         K / Fmt<TYPE>::UE, rowf);
       return hipGetLastError();
     }
   }
