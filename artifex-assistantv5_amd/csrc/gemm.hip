@@ -2117,7 +2117,10 @@ int device_cus() {
 // gemm_kernel round takes rho of a wide round (from the measured rates:
 // Q4_K 134 against 69 us, Q6_K 121 against 98 us per round).  Q6_K at
 // M = 2048, N = 14336: 608 workgroups (3 rounds, the last 37.5% full) ->
-// 512 + 128 of gemm_kernel.
+// 512 + 128 of gemm_kernel, 656-663 -> 684-696 TFLOP/s; Q4_K M = 4096 896-906
+// -> 933-945, M = 1536 685 -> 761-785.  Q4_K at M = 2048, N = 14336 (448:
+// 1 + 2 rho = 2.04 rounds against 2) keeps the wide tile: split there it
+// measured 802-808 against 853.
 #ifndef GGUF_GEMM_WIDE_SPLIT
 #define GGUF_GEMM_WIDE_SPLIT 1  // 0: the wide tile covers every column
 #endif
