@@ -1271,14 +1271,14 @@ constexpr int kWStB = kWBM * kRowB;
 //   begin<C>(u)    at the start of step C of unit u
 //   done<C>(j, u)  once both operands of tile j at step C are built
 //   bop<C, H>(j)   the B operand of tile j, k-half H of step C
-template <int TYPE>
+template <int TYPE, int TN>
 struct WB;
 
 // Q4_K: set P holds the 8 code bytes of the steps of parity P, requested two
 // steps ahead; the header of unit u + 1 is requested at step 2 of unit u.
-template <>
-struct WB<12> {
-  static constexpr int kWTN = wide_tn<12>();
+template <int TN>
+struct WB<12, TN> {
+  static constexpr int kWTN = TN;
   rsrc_t brs[kWTN];
   int ts, nu;
   BOff bo;
@@ -1343,9 +1343,9 @@ struct WB<12> {
 
 // Q5_K: Q4_K's codes and header, and the lane's 8 bytes of fifth bits (every
 // window's) with the header; they are ORed into the nibbles as gemm_kernel does.
-template <>
-struct WB<13> {
-  static constexpr int kWTN = wide_tn<13>();
+template <int TN>
+struct WB<13, TN> {
+  static constexpr int kWTN = TN;
   rsrc_t brs[kWTN];
   int ts, nu;
   BOff bo;
@@ -1415,9 +1415,9 @@ struct WB<13> {
 // Q2_K: the step's 8 qs bytes of half c >> 1 (windows 2c, 2c + 1 take bit
 // pairs 2 (w & 3) of them); the header (16 scale bytes, d | dmin << 16).  The
 // lane's 8 k of a window lie in scale group 2 w + (g >> 1).
-template <>
-struct WB<10> {
-  static constexpr int kWTN = wide_tn<10>();
+template <int TN>
+struct WB<10, TN> {
+  static constexpr int kWTN = TN;
   rsrc_t brs[kWTN];
   int ts, nu, lg;
   BOff bo;
@@ -1478,9 +1478,9 @@ struct WB<10> {
 // Q3_K: as Q2_K, codes q3 = low bits | hmask bit 4 (c >> 1) + (w & 3) << 2,
 // value d (sc - 32) (q3 - 4); the header (12 scale bytes, d, the lane's hmask
 // bytes 8 g .. 8 g + 7).
-template <>
-struct WB<11> {
-  static constexpr int kWTN = wide_tn<11>();
+template <int TN>
+struct WB<11, TN> {
+  static constexpr int kWTN = TN;
   rsrc_t brs[kWTN];
   int ts, nu, lg;
   BOff bo;
@@ -1547,9 +1547,9 @@ struct WB<11> {
 // IQ4_XS: step c is sub-blocks 2c, 2c + 1 (the lane's code words, one each),
 // each an IQ4_NL block with scale d (ls - 32); the header (d | scales_h << 16,
 // scales_l[4]).
-template <>
-struct WB<23> {
-  static constexpr int kWTN = wide_tn<23>();
+template <int TN>
+struct WB<23, TN> {
+  static constexpr int kWTN = TN;
   rsrc_t brs[kWTN];
   int ts, nu;
   BOff bo;
@@ -1602,9 +1602,9 @@ struct WB<23> {
 
 // Q8_0: step c of unit u (256 elements) is blocks 8 u + 2 c + H; set P holds
 // their codes and d for the steps of parity P, requested two steps ahead.
-template <>
-struct WB<8> {
-  static constexpr int kWTN = wide_tn<8>();
+template <int TN>
+struct WB<8, TN> {
+  static constexpr int kWTN = TN;
   rsrc_t brs[kWTN];
   int ts, nu;
   BOff bo;
@@ -1659,9 +1659,9 @@ struct WB<8> {
 // P, the d of unit u + 1 at step 2 of unit u.  The lane's operand for k-half t2
 // holds the window columns 32 t2 + 16 lh + 4 g + e at position 4 lh + e (the
 // activations are staged in that order).
-template <>
-struct WB<14> {
-  static constexpr int kWTN = wide_tn<14>();
+template <int TN>
+struct WB<14, TN> {
+  static constexpr int kWTN = TN;
   rsrc_t brs[kWTN];
   int ts, nu;
   BOff bo;
@@ -1738,9 +1738,9 @@ struct WB<14> {
 
 // Q4_0 / Q5_0 / IQ4_NL: as Q8_0, the step's blocks 8 u + 2 c + H; per block
 // the lane's code word, the f16 d and (Q5_0) the row's fifth-bit word.
-template <int T>
+template <int T, int TN>
 struct WB32 {
-  static constexpr int kWTN = wide_tn<T>();
+  static constexpr int kWTN = TN;
   rsrc_t brs[kWTN];
   int ts, nu, lg;
   BOff bo;
@@ -1787,9 +1787,9 @@ struct WB32 {
 // window of the steps of parity P (iq_load_window), requested two steps
 // ahead; the operand is built from the workgroup's tables in shared memory
 // (iq_b) and rounded once with the unit scale, as in gemm_kernel.
-template <int T>
+template <int T, int TN>
 struct WBIq {
-  static constexpr int kWTN = wide_tn<T>();
+  static constexpr int kWTN = TN;
   rsrc_t brs[kWTN];
   int ts, nu, lg;
   BOff bo;
@@ -1835,29 +1835,29 @@ struct WBIq {
     return h8(mix_w(v.x, s), mix_w(v.y, s), mix_w(v.z, s), mix_w(v.w, s));
   }
 };
-template <>
-struct WB<16> : WBIq<16> {};
-template <>
-struct WB<17> : WBIq<17> {};
-template <>
-struct WB<18> : WBIq<18> {};
-template <>
-struct WB<21> : WBIq<21> {};
-template <>
-struct WB<22> : WBIq<22> {};
-template <>
-struct WB<29> : WBIq<29> {};
+template <int TN>
+struct WB<16, TN> : WBIq<16, TN> {};
+template <int TN>
+struct WB<17, TN> : WBIq<17, TN> {};
+template <int TN>
+struct WB<18, TN> : WBIq<18, TN> {};
+template <int TN>
+struct WB<21, TN> : WBIq<21, TN> {};
+template <int TN>
+struct WB<22, TN> : WBIq<22, TN> {};
+template <int TN>
+struct WB<29, TN> : WBIq<29, TN> {};
 
-template <>
-struct WB<2> : WB32<2> {};
-template <>
-struct WB<6> : WB32<6> {};
-template <>
-struct WB<20> : WB32<20> {};
+template <int TN>
+struct WB<2, TN> : WB32<2, TN> {};
+template <int TN>
+struct WB<6, TN> : WB32<6, TN> {};
+template <int TN>
+struct WB<20, TN> : WB32<20, TN> {};
 
-template <int TYPE>
-struct Wide : WB<TYPE> {
-  static constexpr int kWTN = wide_tn<TYPE>();
+template <int TYPE, int TN>
+struct Wide : WB<TYPE, TN> {
+  static constexpr int kWTN = TN;
   rsrc_t ars[kWAI];  // rows m0 + kWAR i + (0 .. kWAR - 1)
   int av, row0, cc, K, af0, af1;
   uint4 ar[kWAI];
@@ -1920,13 +1920,14 @@ struct Wide : WB<TYPE> {
   }
 };
 
-// K a multiple of 256.
-template <int TYPE, typename XT>
+// K a multiple of 256; TN weight row tiles per wave (a workgroup tile of
+// 128 x 128 TN).
+template <int TYPE, typename XT, int TN>
 __global__ __launch_bounds__(kWThr) void gemm_wide(const XT *__restrict__ x, int64_t ldx,
                                                   const uint8_t *__restrict__ W, int M, int N,
                                                   int K, float *__restrict__ y, int64_t ldy,
                                                   int tiles_m, const float *__restrict__ rowf) {
-  constexpr int kWTN = wide_tn<TYPE>();
+  constexpr int kWTN = TN;
   __shared__ __align__(16) unsigned char lds[4 * kWStB];
   // IQ types: the decode tables, requested first and written before the first barrier
   __shared__ __align__(16) unsigned char iqtbl[is_iq(TYPE) ? iq_tbl_bytes<TYPE>() : 16];
@@ -1940,12 +1941,12 @@ __global__ __launch_bounds__(kWThr) void gemm_wide(const XT *__restrict__ x, int
     const int tiles_n = (int)gridDim.x / tiles_m;
     const int gn = min(GGUF_GEMM_GN, tiles_n - band * GGUF_GEMM_GN);
     m0 = (in / gn) * kWBM;
-    n0 = (band * GGUF_GEMM_GN + in % gn) * wide_bn<TYPE>();
+    n0 = (band * GGUF_GEMM_GN + in % gn) * (16 * TN * kWW);
   }
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int r = lane & 15, g = lane >> 4;
-  Wide<TYPE> s;
+  Wide<TYPE, TN> s;
   s.lds = lds;
   s.K = K;
   s.nu = K / 256;
@@ -2109,32 +2110,64 @@ int device_cus() {
   return cus[dev];
 }
 
-// Column tiles of the wide tile's launch (of wn).  Its workgroups hold a CU
-// each for about the same time, so a grid of wm x wn runs in
-// ceil(wm wn / CUs) rounds; when the last round is partly empty and handing
-// the columns past the whole rounds to gemm_kernel (128 x 256 tiles, one K
-// range) ends sooner, the wide tile keeps only those whole rounds.  A
-// gemm_kernel round takes rho of a wide round (from the measured rates:
-// Q4_K 134 against 69 us, Q6_K 121 against 98 us per round).  Q6_K at
-// M = 2048, N = 14336: 608 workgroups (3 rounds, the last 37.5% full) ->
-// 512 + 128 of gemm_kernel, 656-663 -> 684-696 TFLOP/s; Q4_K M = 4096 896-906
-// -> 933-945, M = 1536 685 -> 761-785.  Q4_K at M = 2048, N = 14336 (448:
-// 1 + 2 rho = 2.04 rounds against 2) keeps the wide tile: split there it
-// measured 802-808 against 853.
+// The wide tile's launch plan over wn column tiles.  Its workgroups hold a
+// CU each for about the same time, so a grid of wm x wn runs in
+// ceil(wm wn / CUs) rounds.  When the last round is partly empty, the wide
+// launch keeps the columns of its whole rounds and the rest goes to
+// gemm_kernel (128 x 256 tiles, one K range) or, for Q4_K and Q8_0, to
+// their three-tile wide tile, whichever the round estimate says ends sooner by a
+// twentieth of a round.  A round of gemm_kernel takes 0.52 of a four-tile
+// wide round and 0.81 of a three-tile one, a three-tile round 0.91 of a
+// four-tile one (measured: Q4_K 134 against 69 us, Q6_K 121 against 98 us,
+// Q4_K 145 against 132 us).  Q6_K at M = 2048, N = 14336: 608 workgroups (3
+// rounds, the last 37.5% full) -> 512 + 128 of gemm_kernel, 656-663 ->
+// 684-696 TFLOP/s; Q4_K M = 4096 896-906 -> 933-945, M = 1536 685 -> 761-785
+// (gemm_kernel); Q4_K M = 2048 (448: 2 rounds) -> 256 + 256 three-tile
+// workgroups, 826-831 -> 866 (with gemm_kernel for the rest: 802-808).
 #ifndef GGUF_GEMM_WIDE_SPLIT
 #define GGUF_GEMM_WIDE_SPLIT 1  // 0: the wide tile covers every column
 #endif
-int wide_columns(int wm, int wn, int M, int N, int bn, int tn) {
-  if (!GGUF_GEMM_WIDE_SPLIT) return wn;
+#ifndef GGUF_GEMM_RHO3
+#define GGUF_GEMM_RHO3 0.91  // a round of three-tile workgroups against one of four-tile ones
+#endif
+// Q4_K and Q8_0 also have a three-tile wide tile for the columns past the
+// whole rounds (exact against gemm_kernel and repeatable at M = 2048, N =
+// 14336).  The other four-tile types do not use theirs: the three-tile builds
+// of IQ4_NL and IQ2_XS gave wrong values in a few percent of the elements,
+// different from call to call (M = 2048, N = 14336, K = 4096), while those of
+// Q4_0, Q5_0, Q2_K, IQ4_XS and IQ2_XXS matched.  The compiled loop of the
+// IQ4_NL build shows no read of, or write to, a register with a load
+// outstanding; the cause is not known.
+template <int TYPE>
+constexpr bool has_wide3() {
+  return TYPE == 12 || TYPE == 8;
+}
+struct WidePlan {
+  int wn1;   // column tiles of the wide launch
+  int rest;  // the columns past them: 0 none, 1 gemm_kernel, 2 the three-tile wide tile
+};
+WidePlan wide_plan(int wm, int wn, int M, int N, int tn, bool three) {
+  WidePlan p{wn, 0};
+  if (!GGUF_GEMM_WIDE_SPLIT) return p;
   const int64_t cus = device_cus(), g = (int64_t)wm * wn;
   const int64_t r = g / cus, rounds = (g + cus - 1) / cus;
-  if (r < 1 || g % cus == 0) return wn;
+  if (r < 1 || g % cus == 0) return p;
   const int w1 = (int)(r * cus / wm);
-  if (w1 < 1 || w1 >= wn) return wn;
-  const int64_t left = N - (int64_t)w1 * bn;
+  if (w1 < 1 || w1 >= wn) return p;
+  const int64_t left = N - (int64_t)w1 * 16 * tn * kWW;
+  double best = (double)rounds - 0.05;
   const int64_t gk = (int64_t)((M + kBM - 1) / kBM) * ((left + kBN - 1) / kBN);
-  const double rho = tn == 3 ? 0.81 : 0.52;
-  return (double)r + (double)((gk + cus - 1) / cus) * rho < (double)rounds - 0.1 ? w1 : wn;
+  const double ck = (double)r + (double)((gk + cus - 1) / cus) * (tn == 3 ? 0.81 : 0.52);
+  if (ck < best) {
+    best = ck - 0.05;
+    p = WidePlan{w1, 1};
+  }
+  if (three) {
+    const int64_t g3 = (int64_t)wm * ((left + 16 * 3 * kWW - 1) / (16 * 3 * kWW));
+    const double c3 = (double)r + (double)((g3 + cus - 1) / cus) * GGUF_GEMM_RHO3;
+    if (c3 < best) p = WidePlan{w1, 2};
+  }
+  return p;
 }
 
 // rowf: the rows' inverse scales when x is the fp16 image of f32 rows.
@@ -2160,15 +2193,24 @@ hipError_t launch_type(const XT *x, int64_t ldx, const uint8_t *W, int M, int N,
     constexpr int bn = wide_bn<TYPE>();
     const int wm = (M + kWBM - 1) / kWBM, wn = (N + bn - 1) / bn;
     if ((int64_t)wm * wn >= wide_min<TYPE>() && K % 256 == 0) {
-      const int wn1 = wide_columns(wm, wn, M, N, bn, wide_tn<TYPE>());
-      const int n1 = min(N, wn1 * bn);
-      hipLaunchKernelGGL((gemm_wide<TYPE, XT>), dim3((unsigned)(wm * wn1)), dim3(kWThr), 0, s, x,
-                         ldx, W, M, n1, K, y, ldy, wm, rowf);
+      const WidePlan pl = wide_plan(wm, wn, M, N, wide_tn<TYPE>(), has_wide3<TYPE>());
+      const int n1 = min(N, pl.wn1 * bn);
+      hipLaunchKernelGGL((gemm_wide<TYPE, XT, wide_tn<TYPE>()>), dim3((unsigned)(wm * pl.wn1)),
+                         dim3(kWThr), 0, s, x, ldx, W, M, n1, K, y, ldy, wm, rowf);
       hipError_t e = hipGetLastError();
       if (e != hipSuccess || n1 == N) return e;
-      // the columns past the wide tile's whole rounds: gemm_kernel, one K range
-      // (the same bits per element as the wide tile)
+      // the columns past the wide tile's whole rounds: the three-tile wide tile
+      // or gemm_kernel with one K range (the same bits per element either way)
       const int64_t ts = (int64_t)(K / Fmt<TYPE>::UE) * Fmt<TYPE>::TU;
+      if constexpr (has_wide3<TYPE>()) {
+        if (pl.rest == 2) {
+          const int wn3 = (N - n1 + 16 * 3 * kWW - 1) / (16 * 3 * kWW);
+          hipLaunchKernelGGL((gemm_wide<TYPE, XT, 3>), dim3((unsigned)(wm * wn3)), dim3(kWThr), 0,
+                             s, x, ldx, W + (int64_t)(n1 / 16) * ts, M, N - n1, K, y + n1, ldy, wm,
+                             rowf);
+          return hipGetLastError();
+        }
+      }
       const int tm = (M + kBM - 1) / kBM, tn = (N - n1 + kBN - 1) / kBN;
       hipLaunchKernelGGL((gemm_kernel<TYPE, XT>), dim3((unsigned)(tm * tn), 1u), dim3(kThreads), 0,
                          s, x, ldx, W + (int64_t)(n1 / 16) * ts, M, N - n1, K, y + n1, ldy, tm,

@@ -317,7 +317,8 @@ def test_full_size_configs(pkg, t, m, n, k, xdt):
                                      (13, 2100, 14000, 1536), (11, 2100, 14000, 1536),
                                      (10, 1000, 14000, 4096), (23, 1000, 14000, 1536),
                                      (2, 1000, 14000, 4096), (6, 777, 29000, 1536),
-                                     (20, 1000, 14000, 1536)])
+                                     (20, 1000, 14000, 1536), (12, 2048, 14000, 1024),
+                                     (8, 2000, 14000, 1024)])
 def test_wide_gemm_ragged(pkg, t, m, n, k):
     """Every type but the grid-codebook IQ types: prefill with fp16 activations
     on grids large enough for the wide-tile GEMM (192 tiles of 128 x 512; Q6_K,
@@ -337,6 +338,10 @@ def test_wide_gemm_ragged(pkg, t, m, n, k):
 
 
 @pytest.mark.parametrize("t,m,k", [(12, 1280, 4096), (8, 1280, 4096), (8, 1280, 1568),
+                                   (12, 2048, 4096), (8, 2048, 4096), (12, 4096, 1024),
+                                   (10, 2048, 4096), (23, 2048, 4096), (2, 2048, 4096),
+                                   (6, 2048, 4096), (20, 2048, 4096), (16, 2048, 4096),
+                                   (17, 2048, 4096),
                                    (14, 2048, 4096), (13, 2048, 4096), (11, 2048, 4096),
                                    (10, 1280, 4096), (23, 1280, 4096), (2, 1280, 4096),
                                    (6, 1280, 4096), (20, 1280, 4096), (16, 1280, 4096),
@@ -346,8 +351,12 @@ def test_wide_gemm_equals_gemm_kernel_rows(pkg, t, m, k):
     """The wide-tile GEMM (1280 rows: 280 tiles of 128 x 512; Q6_K 2048 rows:
     608 tiles of 128 x 384) and gemm_kernel (a slice of 128 rows: 56 tiles of
     128 x 256, no workspace, so no K split) run each output element's MFMAs in
-    the same k order: the same bits.  A Q8_0 K that is not a multiple of 256
-    keeps gemm_kernel for the whole call."""
+    the same k order: the same bits, and a second call the same bits again.  A
+    Q8_0 K that is not a multiple of 256 keeps gemm_kernel for the whole call.
+    Q4_K and Q8_0 at 2048 rows run the wide tile over 8192 columns and its
+    three-tile form over the rest (the other four-tile types the wide tile over
+    every column); Q4_K at 4096 rows the wide tile over 12288 and gemm_kernel
+    over the rest."""
     n = 14336
     if t in (16, 17, 18, 21, 22, 29):  # random valid blocks: every bit pattern decodes
         raw = tile_model.random_blocks(t, n, k, seed=t + k)
@@ -366,6 +375,7 @@ def test_wide_gemm_equals_gemm_kernel_rows(pkg, t, m, k):
         assert rc == 0, lib.gguf_hip_last_error()
         return y
     y = gemm(x)
+    assert torch.equal(gemm(x), y), "a second call gave other bits"
     for m0 in (0, 640, m - 128):
         assert torch.equal(gemm(x[m0:m0 + 128].contiguous()), y[m0:m0 + 128]), m0
 
