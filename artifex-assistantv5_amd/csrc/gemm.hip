@@ -2142,11 +2142,19 @@ template <int TYPE>
 constexpr bool has_wide3() {
   return TYPE == 12 || TYPE == 8;
 }
+// Q6_K (three tiles per wave) has a two-tile wide tile for those columns.
+template <int TYPE>
+constexpr bool has_wide2() {
+  return TYPE == 14;
+}
+#ifndef GGUF_GEMM_RHO2
+#define GGUF_GEMM_RHO2 0.7  // a round of two-tile workgroups against one of three-tile ones
+#endif
 struct WidePlan {
   int wn1;   // column tiles of the wide launch
-  int rest;  // the columns past them: 0 none, 1 gemm_kernel, 2 the three-tile wide tile
+  int rest;  // the columns past them: 0 none, 1 gemm_kernel, 2 / 3 the three- / two-tile wide tile
 };
-WidePlan wide_plan(int wm, int wn, int M, int N, int tn, bool three) {
+WidePlan wide_plan(int wm, int wn, int M, int N, int tn, bool three, bool two) {
   WidePlan p{wn, 0};
   if (!GGUF_GEMM_WIDE_SPLIT) return p;
   const int64_t cus = device_cus(), g = (int64_t)wm * wn;
@@ -2166,6 +2174,11 @@ WidePlan wide_plan(int wm, int wn, int M, int N, int tn, bool three) {
     const int64_t g3 = (int64_t)wm * ((left + 16 * 3 * kWW - 1) / (16 * 3 * kWW));
     const double c3 = (double)r + (double)((g3 + cus - 1) / cus) * GGUF_GEMM_RHO3;
     if (c3 < best) p = WidePlan{w1, 2};
+  }
+  if (two) {
+    const int64_t g2 = (int64_t)wm * ((left + 16 * 2 * kWW - 1) / (16 * 2 * kWW));
+    const double c2 = (double)r + (double)((g2 + cus - 1) / cus) * GGUF_GEMM_RHO2;
+    if (c2 < best) p = WidePlan{w1, 3};
   }
   return p;
 }
@@ -2193,7 +2206,8 @@ hipError_t launch_type(const XT *x, int64_t ldx, const uint8_t *W, int M, int N,
     constexpr int bn = wide_bn<TYPE>();
     const int wm = (M + kWBM - 1) / kWBM, wn = (N + bn - 1) / bn;
     if ((int64_t)wm * wn >= wide_min<TYPE>() && K % 256 == 0) {
-      const WidePlan pl = wide_plan(wm, wn, M, N, wide_tn<TYPE>(), has_wide3<TYPE>());
+      const WidePlan pl =
+          wide_plan(wm, wn, M, N, wide_tn<TYPE>(), has_wide3<TYPE>(), has_wide2<TYPE>());
       const int n1 = min(N, pl.wn1 * bn);
       hipLaunchKernelGGL((gemm_wide<TYPE, XT, wide_tn<TYPE>()>), dim3((unsigned)(wm * pl.wn1)),
                          dim3(kWThr), 0, s, x, ldx, W, M, n1, K, y, ldy, wm, rowf);
@@ -2206,6 +2220,15 @@ hipError_t launch_type(const XT *x, int64_t ldx, const uint8_t *W, int M, int N,
         if (pl.rest == 2) {
           const int wn3 = (N - n1 + 16 * 3 * kWW - 1) / (16 * 3 * kWW);
           hipLaunchKernelGGL((gemm_wide<TYPE, XT, 3>), dim3((unsigned)(wm * wn3)), dim3(kWThr), 0,
+                             s, x, ldx, W + (int64_t)(n1 / 16) * ts, M, N - n1, K, y + n1, ldy, wm,
+                             rowf);
+          return hipGetLastError();
+        }
+      }
+      if constexpr (has_wide2<TYPE>()) {
+        if (pl.rest == 3) {
+          const int wn2 = (N - n1 + 16 * 2 * kWW - 1) / (16 * 2 * kWW);
+          hipLaunchKernelGGL((gemm_wide<TYPE, XT, 2>), dim3((unsigned)(wm * wn2)), dim3(kWThr), 0,
                              s, x, ldx, W + (int64_t)(n1 / 16) * ts, M, N - n1, K, y + n1, ldy, wm,
                              rowf);
           return hipGetLastError();
