@@ -2142,10 +2142,11 @@ template <int TYPE>
 constexpr bool has_wide3() {
   return TYPE == 12 || TYPE == 8;
 }
-// Q6_K (three tiles per wave) has a two-tile wide tile for those columns.
+// Q6_K, Q5_K and Q3_K (three tiles per wave) have a two-tile wide tile for
+// those columns.
 template <int TYPE>
 constexpr bool has_wide2() {
-  return TYPE == 14;
+  return TYPE == 14 || TYPE == 13 || TYPE == 11;
 }
 #ifndef GGUF_GEMM_RHO2
 #define GGUF_GEMM_RHO2 0.7  // a round of two-tile workgroups against one of three-tile ones
